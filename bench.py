@@ -1,0 +1,231 @@
+"""Benchmark of the GRPO logprob + ClippedPG-loss forward/backward step on one MI355X.
+
+Workload (one "step" = one pass of the hot path over one batch):
+  bf16 logits [B=8, S=2048, V=151936] ~ N(0, 1.5^2), one prompt x 8 generations,
+  512-token prompt (mask 0), responses U{256..1536} (mask 1), right padding;
+  GRPO advantages (rewards ~ Bernoulli(0.5), group mean/std, no leave-one-out);
+  prev = generation = current logprobs + N(0, 0.05^2); ClippedPG with clip
+  0.2/0.2, token-level masked mean, no KL term.
+  step = advantages -> next-token logprobs (fwd) -> loss fwd+bwd -> logprob bwd
+  through the drop-in API (torch autograd), inputs resident in HBM.
+
+Prints one JSON line.  `value` is next-token rows (tokens) per second for the
+whole step; `roofline` is the dominant kernel (the logprob backward) measured
+with HIP events around each of its launches inside the timed region;
+`cpu_baseline` times the CPU oracle (a restatement of the reference's PyTorch
+op sequence) on a bounded sample of the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "logprob+PG-loss fwd/bwd tokens/s and HBM GB/s (% peak) at V=151936 bf16"
+PEAK_HBM_GBPS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--cpu-sample-rows", type=int, default=1024)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy-gib", type=float, default=0.0,
+                    help="also run a plain device copy of this many GiB (HBM counter calibration)")
+    return ap.parse_args()
+
+
+def cpu_baseline(data_cpu_rows: dict, n_rows: int) -> dict:
+    """The CPU oracle (reference op sequence in PyTorch) on `n_rows` rows of the workload."""
+    import torch
+
+    from oracle.logprob import selected_logprobs, selected_logprobs_grad
+    from oracle.loss import clipped_pg_loss
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or len(os.sched_getaffinity(0))
+    threads = min(threads, len(os.sched_getaffinity(0)))
+    torch.set_num_threads(threads)
+    x = data_cpu_rows["logits"]  # [1, n, V] bf16
+    tgt = data_cpu_rows["target"]  # [1, n]
+    V = x.shape[-1]
+    d = data_cpu_rows["data"]
+    t0 = time.perf_counter()
+    lp = selected_logprobs(x, tgt, 0, V, chunk_size=n_rows)
+    lpr = lp.clone().requires_grad_(True)
+    loss, _ = clipped_pg_loss(lpr, d, d["sample_mask"].sum(), d["gvt"], reference_policy_kl_penalty=0.0)
+    (g,) = torch.autograd.grad(loss, [lpr])
+    grad = selected_logprobs_grad(x, tgt, 0, V, g, chunk_size=n_rows)
+    dt = time.perf_counter() - t0
+    del grad
+    return {
+        "value": n_rows / dt,
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{n_rows} consecutive response rows of sequence 0 (V={V}, bf16): "
+                  f"chunked fwd + ClippedPG loss + bwd, {dt:.2f} s",
+    }
+
+
+def main() -> None:
+    args = parse()
+    if args.gpus != 1:
+        sys.exit(f"bench.py runs on one GPU only (got --gpus {args.gpus}); this build has no "
+                 "multi-GPU path: the workload shards by rows with no exchange, see DESIGN.md")
+    import torch
+
+    from rl_amd import _C, workloads
+    from rl_amd.algorithms.advantage_estimator import AdvEstimatorConfig, GRPOAdvantageEstimator
+    from rl_amd.algorithms.loss import ClippedPGLossConfig, ClippedPGLossFn
+    from rl_amd.distributed.model_utils import from_parallel_logits_to_logprobs
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    print(f"[bench] device {torch.cuda.get_device_name(dev)}; building inputs", file=sys.stderr, flush=True)
+    data = workloads.grpo_step_bf16(device=dev)
+    logits = data["logits"].requires_grad_(True)
+    ids = data["input_ids"]
+    B, S, V = logits.shape
+    with torch.no_grad():
+        cur = from_parallel_logits_to_logprobs(logits, ids, 0, V, None, inference_only=True)
+    data = workloads.finish_grpo_step(data, cur)
+    loss_cfg = ClippedPGLossConfig(reference_policy_kl_penalty=0.0)
+    loss_fn = ClippedPGLossFn(loss_cfg)
+    est = GRPOAdvantageEstimator(AdvEstimatorConfig(use_leave_one_out_baseline=False), loss_cfg)
+    gvs = data["sample_mask"].sum()
+    gvt = (data["token_mask"][:, 1:] * data["sample_mask"][:, None]).sum()
+    batch = {k: data[k] for k in ("token_mask", "sample_mask", "prev_logprobs",
+                                   "generation_logprobs", "reference_policy_logprobs")}
+
+    def step():
+        adv = est.compute_advantage(data["prompt_ids"], data["rewards"], data["token_mask"])
+        batch["advantages"] = adv
+        lp = from_parallel_logits_to_logprobs(logits, ids, 0, V, None)
+        loss, metrics = loss_fn(lp, batch, gvs, gvt)
+        (grad,) = torch.autograd.grad(loss, [logits])
+        return grad, lp, metrics
+
+    # active rows: rows whose upstream gradient is non-zero (the bwd reads only those)
+    grad, lp, metrics = step()
+    lp2 = lp.detach().requires_grad_(True)
+    l2, _ = loss_fn(lp2, batch, gvs, gvt)
+    (glp,) = torch.autograd.grad(l2, [lp2])
+    active_rows = int((glp != 0).sum().item())
+    del grad, lp, lp2, l2, glp
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    timer = _C.enable_launch_timing()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    _C.disable_launch_timing()
+
+    def avg_ms(name):
+        evs = timer.get(name, [])
+        return sum(a.elapsed_time(b) for a, b in evs) / max(1, len(evs))
+
+    ms_step = (t1 - t0) * 1e3 / args.steps
+    rows = B * (S - 1)
+    esz = logits.element_size()
+    fwd_bytes = rows * V * esz
+    bwd_bytes = active_rows * V * esz + B * S * V * esz
+    fwd_ms, bwd_ms = avg_ms("mirl_logprob_fwd"), avg_ms("mirl_logprob_bwd")
+    loss_ms, adv_ms = avg_ms("mirl_clipped_pg"), avg_ms("mirl_grpo_advantage")
+    bwd_gbps = bwd_bytes / (bwd_ms * 1e-3) / 1e9
+    fwd_gbps = fwd_bytes / (fwd_ms * 1e-3) / 1e9
+    step_gbps = (fwd_bytes + bwd_bytes) / (ms_step * 1e-3) / 1e9
+
+    traffic = None
+    tf = ROOT / "profiles" / "traffic_logprob_bwd_grpo_bf16.json"
+    if tf.exists():
+        try:
+            traffic = json.loads(tf.read_text()).get("hbm_bytes_per_launch")
+        except Exception:
+            traffic = None
+
+    if args.calibrate_copy_gib > 0:
+        n = int(args.calibrate_copy_gib * (1 << 30)) // 4
+        a = torch.empty(n, dtype=torch.float32, device=dev).fill_(1.0)
+        b = torch.empty_like(a)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        del a, b
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        n = min(args.cpu_sample_rows, int(data["response_lengths"][0].item()))
+        r0 = 511  # first response row: row r predicts token r + 1
+        x_rows = logits.detach()[0:1, r0:r0 + n].cpu()
+        tgt_rows = ids[0:1, r0 + 1:r0 + 1 + n].cpu()
+        sl = slice(r0, r0 + n + 1)
+        d = {
+            "token_mask": data["token_mask"][0:1, sl].cpu(),
+            "sample_mask": torch.ones(1),
+            "advantages": batch["advantages"][0:1, sl].cpu().contiguous(),
+            "prev_logprobs": data["prev_logprobs"][0:1, sl].cpu(),
+            "generation_logprobs": data["generation_logprobs"][0:1, sl].cpu(),
+            "reference_policy_logprobs": data["reference_policy_logprobs"][0:1, sl].cpu(),
+            "gvt": gvt.cpu(),
+        }
+        print(f"[bench] timing CPU oracle on {n} rows", file=sys.stderr, flush=True)
+        cpu = cpu_baseline({"logits": x_rows, "target": tgt_rows, "data": d}, n)
+
+    out = {
+        "metric": METRIC,
+        "value": rows / (ms_step * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "grpo_clipped_pg_logprob_fwd_bwd",
+            "logits": [B, S, V],
+            "next_token_rows": rows,
+            "active_rows": active_rows,
+            "loss": "ClippedPG clip 0.2/0.2 token-level, no KL; GRPO adv (no LOO)",
+            "parallelism": "single-gpu",
+        },
+        "hbm_gbps_step": step_gbps,
+        "hbm_frac_step": step_gbps / PEAK_HBM_GBPS,
+        "kernels_ms": {"logprob_fwd": fwd_ms, "logprob_bwd": bwd_ms, "clipped_pg": loss_ms,
+                       "grpo_advantage": adv_ms},
+        "logprob_fwd_gbps": fwd_gbps,
+        "roofline": {
+            "kernel": "mirl_logprob_bwd",
+            "bound": "hbm",
+            "achieved": bwd_gbps,
+            "peak": PEAK_HBM_GBPS,
+            "unit": "GB/s",
+            "frac": bwd_gbps / PEAK_HBM_GBPS,
+            "traffic": traffic,
+            "algorithmic_bytes": bwd_bytes,
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,238 @@
+/*
+ * mirl.h — C ABI of libmirl.so, the MI355X (gfx950) token-logprob and
+ * clipped-policy-gradient hot path.
+ *
+ * Conventions shared by every entry point:
+ *   - All tensor arguments are raw device pointers plus element strides.  The
+ *     vocabulary (last) dimension of a logits tensor must be unit-stride; the
+ *     Python layer calls .contiguous() when it is not.
+ *   - `stream` is a hipStream_t (NULL = the null stream).  Every call only
+ *     enqueues work on that stream: no device synchronisation, no host copies,
+ *     and no device memory allocation.  Scratch memory, when a kernel needs it,
+ *     is passed in by the caller.
+ *   - Every function returns MIRL_OK (0) or a non-zero status.  The message of
+ *     the last failure on the calling thread is available from
+ *     mirl_last_error().  No entry point aborts or exits.
+ *   - Row r of a [B, R, V] logits tensor is the logits of sequence position r.
+ *     Row (b, r) is paired with target (b, r); callers that want next-token
+ *     logprobs pass a target view shifted by one position (ids[:, 1:]).
+ *
+ * The reference implementation this replaces is pure PyTorch; each function
+ * below names the reference code (path:line inside the NeMo-RL tree) whose
+ * semantics it reproduces.
+ */
+#ifndef MIRL_H
+#define MIRL_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes */
+#define MIRL_OK 0
+#define MIRL_ERR_INVALID_ARGUMENT 1
+#define MIRL_ERR_HIP 2
+#define MIRL_ERR_UNSUPPORTED 3
+
+/* element types of logits / gradient tensors */
+#define MIRL_DTYPE_F32 0
+#define MIRL_DTYPE_BF16 1
+#define MIRL_DTYPE_F16 2
+/* element type of the per-token loss tensors (ClippedPG) */
+#define MIRL_DTYPE_F64 3
+
+/* Last error message on the calling thread ("" when none). */
+const char* mirl_last_error(void);
+
+/* Library version string, e.g. "mirl 0.1.0 gfx950". */
+const char* mirl_version(void);
+
+/*
+ * Selected-token log-probabilities, one row per (b, r):
+ *   m        = max_v x[v]
+ *   logsum   = log(sum_v exp(x[v] - m))
+ *   out[b,r] = (x[t'] - m) - logsum      where t' = target - vocab_start,
+ *   out[b,r] = 0                          when target < vocab_start or >= vocab_end.
+ * Arithmetic is fp32 for every input dtype; one read of the logits row.
+ * If `row_stats` is non-NULL it receives {m, logsum} per row (2 floats, row
+ * major [B, R, 2]) for mirl_logprob_bwd.
+ *
+ * Replaces: nemo_rl/distributed/model_utils.py:87-135
+ * (_compute_distributed_selected_logprobs), the per-chunk forward of
+ * ChunkedDistributedLogprob (model_utils.py:240-290) and the forward of
+ * DistributedLogprob (model_utils.py:145-182) with a vocab group of size 1.
+ */
+int mirl_logprob_fwd(const void* logits, int dtype, int64_t B, int64_t R,
+                     int64_t V, int64_t stride_b, int64_t stride_r,
+                     const int64_t* target, int64_t t_stride_b,
+                     int64_t t_stride_r, int64_t vocab_start,
+                     int64_t vocab_end, float* out, float* row_stats,
+                     void* stream);
+
+/*
+ * Gradient of the selected-token log-probabilities with respect to the logits:
+ *   grad[b,r,v] = (onehot(t')[v] - exp((x[v] - m) - logsum)) * g[b,r]
+ * written in the logits dtype (round to nearest even).  Rows with r >= R
+ * (positions the forward did not compute, up to R_total) and rows whose
+ * upstream gradient is exactly zero are written as zeros without reading the
+ * logits.  `grad_in` may alias `logits` (in-place, each element is read before
+ * it is overwritten by the same thread).
+ *
+ * Replaces: ChunkedDistributedLogprob.backward (model_utils.py:293-349) and
+ * DistributedLogprob.backward (model_utils.py:185-225).
+ */
+int mirl_logprob_bwd(const void* logits, int dtype, int64_t B, int64_t R,
+                     int64_t R_total, int64_t V, int64_t stride_b,
+                     int64_t stride_r, const int64_t* target,
+                     int64_t t_stride_b, int64_t t_stride_r,
+                     int64_t vocab_start, int64_t vocab_end,
+                     const float* row_stats, const float* grad_out,
+                     int64_t g_stride_b, int64_t g_stride_r, void* grad_in,
+                     int64_t gi_stride_b, int64_t gi_stride_r, void* stream);
+
+/* ---------------------------------------------------------------------- */
+/* ClippedPG loss epilogue                                                  */
+/* ---------------------------------------------------------------------- */
+
+/* KL estimator types (nemo_rl/algorithms/utils.py:56-115) */
+#define MIRL_KL_K1 1
+#define MIRL_KL_K2 2
+#define MIRL_KL_K3 3
+
+/* truncated importance sampling types (loss_functions.py:897-1013) */
+#define MIRL_TIS_NONE 0
+#define MIRL_TIS_TIS 1
+#define MIRL_TIS_ICEPOP 2
+#define MIRL_TIS_ADAPTIVE 3
+#define MIRL_TIS_SEQ_MASK 4
+
+/* Scalar configuration of one ClippedPGLossFn call.  Field meanings follow
+ * ClippedPGLossConfig (nemo_rl/algorithms/loss/loss_functions.py:173-260). */
+typedef struct mirl_pg_config {
+  double ratio_clip_min;
+  double ratio_clip_max;
+  double ratio_clip_c;          /* <= 0 disables dual clipping */
+  double kl_penalty;            /* beta; 0 disables the KL term */
+  double kl_input_clamp;        /* used when has_kl_input_clamp */
+  double kl_output_clamp;       /* used when has_kl_output_clamp */
+  double tis_ratio;             /* truncated IS upper bound */
+  double tis_ratio_min;         /* truncated IS lower bound (tis: 0 default) */
+  double adaptive_hi;           /* adaptive-ppo-clip upper bound incl. k */
+  double adaptive_outer;        /* adaptive-ppo-clip outer bound */
+  double nll_weight;            /* VAPO positive-example NLL weight */
+  int32_t kl_type;              /* MIRL_KL_K1/K2/K3 */
+  int32_t tis_type;             /* MIRL_TIS_* */
+  int32_t has_kl_input_clamp;
+  int32_t has_kl_output_clamp;
+  int32_t disable_ppo_ratio;
+  int32_t token_level_loss;
+  int32_t sequence_level_is;
+  int32_t use_is_correction;
+  int32_t use_on_policy_kl;
+  int32_t force_on_policy;
+  int32_t use_cispo;
+  int32_t full_metrics;
+  int32_t need_is;              /* full_metrics || use_is_correction */
+  int32_t has_rewards;          /* rewards tensor present (VAPO) */
+  int32_t has_support_mask;     /* policy_support_mask present */
+  int32_t has_unfiltered;       /* curr_logprobs_unfiltered is a separate tensor */
+} mirl_pg_config;
+
+/* A [B, L] strided view: element (b, l) is ptr[b*sb + l*sl]. */
+typedef struct mirl_view2d {
+  const void* ptr;
+  int64_t sb;
+  int64_t sl;
+} mirl_view2d;
+
+/* Index of each metric in the metrics output array. */
+#define MIRL_M_LOSS 0
+#define MIRL_M_TOKEN_MULT_PROB_ERROR 1
+#define MIRL_M_PROBS_RATIO 2
+#define MIRL_M_PROBS_RATIO_CLAMPED 3
+#define MIRL_M_PROBS_RATIO_MIN 4
+#define MIRL_M_PROBS_RATIO_MAX 5
+#define MIRL_M_PROBS_RATIO_CLAMPED_MIN 6
+#define MIRL_M_PROBS_RATIO_CLAMPED_MAX 7
+#define MIRL_M_GEN_KL_ERROR 8
+#define MIRL_M_POLICY_KL_ERROR 9
+#define MIRL_M_JS_DIVERGENCE_ERROR 10
+#define MIRL_M_APPROX_ENTROPY 11
+#define MIRL_M_SAMPLING_IMPORTANCE_RATIO 12
+#define MIRL_M_KL_PENALTY 13
+#define MIRL_M_NUM_VALID_SAMPLES 14
+#define MIRL_M_POSITIVE_NLL_LOSS 15
+#define MIRL_M_IS_OOB_RATIO 16
+#define MIRL_M_POLICY_SUPPORT_EXCLUDED_TOKENS 17
+#define MIRL_NUM_METRICS 18
+
+/* Number of scratch elements (of the loss dtype) mirl_clipped_pg needs. */
+int64_t mirl_clipped_pg_workspace_elems(int64_t B);
+
+/*
+ * Fused ClippedPG loss forward + closed-form backward over [B, L] tokens
+ * (L = S - 1; the caller passes the [:, 1:] views of the [B, S] data).
+ * Writes: metrics[MIRL_NUM_METRICS] (metrics[MIRL_M_LOSS] is the loss),
+ * grad_curr[B, L] = dloss/dnext_token_logprobs, and, when
+ * cfg->has_unfiltered, grad_unfiltered[B, L] = dloss/dcurr_logprobs_unfiltered.
+ * `dtype` is MIRL_DTYPE_F32 or MIRL_DTYPE_F64 for every float tensor;
+ * support_mask is uint8 (bool); sample_mask and rewards are [B] vectors;
+ * global_valid_seqs / global_valid_toks are device scalars of `dtype`.
+ * `workspace` holds mirl_clipped_pg_workspace_elems(B) elements of `dtype`.
+ *
+ * Replaces: ClippedPGLossFn.__call__ (loss_functions.py:698-1183) with
+ * clipped_pg_actor_objective / clipped_pg_diagnostic_metrics
+ * (clipped_pg.py:53-194), calculate_kl and masked_mean
+ * (algorithms/utils.py:56-115, 294-306), and the autograd backward of all of
+ * them.
+ */
+int mirl_clipped_pg(const mirl_pg_config* cfg, int dtype, int64_t B, int64_t L,
+                    mirl_view2d curr, mirl_view2d unfiltered,
+                    mirl_view2d token_mask, mirl_view2d advantages,
+                    mirl_view2d prev, mirl_view2d generation,
+                    mirl_view2d reference, mirl_view2d support_mask,
+                    const void* sample_mask, const void* rewards,
+                    const void* global_valid_seqs,
+                    const void* global_valid_toks, void* metrics,
+                    void* grad_curr, void* grad_unfiltered, void* workspace,
+                    void* stream);
+
+/* ---------------------------------------------------------------------- */
+/* GRPO group-normalised advantages                                         */
+/* ---------------------------------------------------------------------- */
+
+/*
+ * Per sample i of B (fp32 rewards, int64 prompt keys [B, K] with row stride
+ * `prompt_stride`, fp32 valid mask or NULL for all-valid, fp32 std_rewards or
+ * NULL to use the rewards themselves for the spread statistics):
+ *   group(i) = { j : prompts[j, :] == prompts[i, :] }
+ *   n = sum_{j in group} valid[j]
+ *   n <= 1 : baseline = r_i, std = 0
+ *   else   : baseline = sum_{j in group, j != i if loo} r_j v_j / (n - loo)
+ *            std = sqrt((sum q_j^2 v_j / (n - loo) - qbar^2)
+ *                       * (n - loo) / (n - loo - 1)), NaN -> 0, inf -> FLT_MAX
+ *            with q = std_rewards (or r) and qbar its group mean like baseline
+ *   adv_i = r_i - baseline; when normalize and std > 0 and the comparison set
+ *   (of q) is not all-equal: adv_i /= (std + 1e-6).
+ * Writes adv[B] (fp32) and, when non-NULL, baseline[B], std[B] (fp32) and
+ * trivial[B] (uint8: 1 when the group has <= 1 valid sample or its comparison
+ * set is all-equal).
+ *
+ * Replaces: GRPOAdvantageEstimator.compute_advantage
+ * (nemo_rl/algorithms/advantage_estimator.py:106-145) with
+ * calculate_baseline_and_std_per_prompt (nemo_rl/algorithms/utils.py:118-234).
+ */
+int mirl_grpo_advantage(const int64_t* prompts, int64_t B, int64_t K,
+                        int64_t prompt_stride, const float* rewards,
+                        const float* std_rewards, const float* valid_mask,
+                        int leave_one_out,
+                        int normalize, float* adv, float* baseline, float* std,
+                        uint8_t* trivial, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MIRL_H */

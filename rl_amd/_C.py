@@ -1,0 +1,361 @@
+"""ctypes binding of libmirl.so (the gfx950 kernels behind include/mirl.h).
+
+Every wrapper takes torch tensors that already live on a ROCm device, passes
+raw pointers, element strides and the current HIP stream, and raises
+:class:`MirlError` when the library reports a failure.  The library is loaded
+lazily; a missing or unloadable library raises immediately — there is no
+fallback implementation.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+from typing import Optional
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().with_name("libmirl.so")
+
+DTYPE_CODES = {
+    torch.float32: 0,
+    torch.bfloat16: 1,
+    torch.float16: 2,
+    torch.float64: 3,
+}
+
+KL_TYPES = {"k1": 1, "k2": 2, "k3": 3}
+TIS_TYPES = {None: 0, "tis": 1, "icepop": 2, "adaptive-ppo-clip": 3, "seq-mask-tis": 4}
+
+# metric slots of the ClippedPG kernel (MIRL_M_* in include/mirl.h)
+PG_METRIC_SLOTS = {
+    "loss": 0,
+    "token_mult_prob_error": 1,
+    "probs_ratio": 2,
+    "probs_ratio_clamped": 3,
+    "probs_ratio_min": 4,
+    "probs_ratio_max": 5,
+    "probs_ratio_clamped_min": 6,
+    "probs_ratio_clamped_max": 7,
+    "gen_kl_error": 8,
+    "policy_kl_error": 9,
+    "js_divergence_error": 10,
+    "approx_entropy": 11,
+    "sampling_importance_ratio": 12,
+    "kl_penalty": 13,
+    "num_valid_samples": 14,
+    "positive_nll_loss": 15,
+    "is_oob_ratio": 16,
+    "policy_support_excluded_tokens": 17,
+}
+PG_NUM_METRICS = 18
+
+
+class MirlError(RuntimeError):
+    """A libmirl entry point returned a non-zero status."""
+
+
+class PgConfig(ctypes.Structure):
+    _fields_ = [
+        ("ratio_clip_min", ctypes.c_double),
+        ("ratio_clip_max", ctypes.c_double),
+        ("ratio_clip_c", ctypes.c_double),
+        ("kl_penalty", ctypes.c_double),
+        ("kl_input_clamp", ctypes.c_double),
+        ("kl_output_clamp", ctypes.c_double),
+        ("tis_ratio", ctypes.c_double),
+        ("tis_ratio_min", ctypes.c_double),
+        ("adaptive_hi", ctypes.c_double),
+        ("adaptive_outer", ctypes.c_double),
+        ("nll_weight", ctypes.c_double),
+        ("kl_type", ctypes.c_int32),
+        ("tis_type", ctypes.c_int32),
+        ("has_kl_input_clamp", ctypes.c_int32),
+        ("has_kl_output_clamp", ctypes.c_int32),
+        ("disable_ppo_ratio", ctypes.c_int32),
+        ("token_level_loss", ctypes.c_int32),
+        ("sequence_level_is", ctypes.c_int32),
+        ("use_is_correction", ctypes.c_int32),
+        ("use_on_policy_kl", ctypes.c_int32),
+        ("force_on_policy", ctypes.c_int32),
+        ("use_cispo", ctypes.c_int32),
+        ("full_metrics", ctypes.c_int32),
+        ("need_is", ctypes.c_int32),
+        ("has_rewards", ctypes.c_int32),
+        ("has_support_mask", ctypes.c_int32),
+        ("has_unfiltered", ctypes.c_int32),
+    ]
+
+
+class View2D(ctypes.Structure):
+    _fields_ = [("ptr", ctypes.c_void_p), ("sb", ctypes.c_int64), ("sl", ctypes.c_int64)]
+
+
+# exported symbol -> (restype, argtypes)
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I = ctypes.c_int
+SIGNATURES = {
+    "mirl_last_error": (ctypes.c_char_p, []),
+    "mirl_version": (ctypes.c_char_p, []),
+    "mirl_logprob_fwd": (
+        _I,
+        [_P, _I, _I64, _I64, _I64, _I64, _I64, _P, _I64, _I64, _I64, _I64, _P, _P, _P],
+    ),
+    "mirl_logprob_bwd": (
+        _I,
+        [_P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I64, _I64, _I64, _I64, _P, _P, _I64,
+         _I64, _P, _I64, _I64, _P],
+    ),
+    "mirl_clipped_pg_workspace_elems": (_I64, [_I64]),
+    "mirl_clipped_pg": (
+        _I,
+        [ctypes.POINTER(PgConfig), _I, _I64, _I64] + [View2D] * 8 + [_P] * 9,
+    ),
+    "mirl_grpo_advantage": (
+        _I,
+        [_P, _I64, _I64, _I64, _P, _P, _P, _I, _I, _P, _P, _P, _P, _P],
+    ),
+}
+
+_lib: Optional[ctypes.CDLL] = None
+_lock = threading.Lock()
+
+# Optional per-launch timing: when set, wrapped entry points record a pair of
+# events on the launch stream around each call, keyed by entry-point name.
+_timer: Optional[dict] = None
+
+
+def enable_launch_timing() -> dict:
+    """Start recording (start, end) torch.cuda.Event pairs per entry point; returns the dict."""
+    global _timer
+    _timer = {}
+    return _timer
+
+
+def disable_launch_timing() -> None:
+    global _timer
+    _timer = None
+
+
+class _Timed:
+    def __init__(self, name: str, dev: torch.device):
+        self.name, self.dev = name, dev
+
+    def __enter__(self):
+        if _timer is not None:
+            self.ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            self.ev[0].record(torch.cuda.current_stream(self.dev))
+        return self
+
+    def __exit__(self, *exc):
+        if _timer is not None and exc[0] is None:
+            self.ev[1].record(torch.cuda.current_stream(self.dev))
+            _timer.setdefault(self.name, []).append(self.ev)
+        return False
+
+
+def load() -> ctypes.CDLL:
+    """Load libmirl.so (once) and declare the C signatures."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise MirlError(
+                    f"{LIB_PATH} is not built; run `python -m rl_amd.csrc.build` "
+                    "(or __graft_entry__.build()) first"
+                )
+            lib = ctypes.CDLL(str(LIB_PATH))
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = lib
+    return _lib
+
+
+def version() -> str:
+    return load().mirl_version().decode()
+
+
+def _check(status: int, what: str) -> None:
+    if status != 0:
+        msg = load().mirl_last_error().decode()
+        raise MirlError(f"{what} failed (status {status}): {msg}")
+
+
+def _require_gpu(*tensors: Optional[torch.Tensor]) -> torch.device:
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise MirlError(
+                "rl_amd kernels run on a ROCm GPU; got a tensor on "
+                f"{t.device} (move inputs to a cuda device)"
+            )
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise MirlError(f"tensors on different devices: {dev} and {t.device}")
+    if dev is None:
+        raise MirlError("no device tensor given")
+    return dev
+
+
+def _stream(dev: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    try:
+        return DTYPE_CODES[t.dtype]
+    except KeyError:
+        raise MirlError(f"unsupported dtype {t.dtype}") from None
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+# ---------------------------------------------------------------------------
+# logprob forward / backward
+# ---------------------------------------------------------------------------
+def logprob_fwd(
+    logits: torch.Tensor,
+    target: torch.Tensor,
+    vocab_start: int,
+    vocab_end: int,
+    out: torch.Tensor,
+    stats: Optional[torch.Tensor],
+) -> None:
+    """out[b, r] = log_softmax(logits[b, r])[target[b, r] - vocab_start] (0 when out of range).
+
+    logits: [B, >=R, V] (unit stride on V); target: [B, R] int64; out: [B, R]
+    fp32 contiguous; stats: [B, R, 2] fp32 contiguous or None.
+    """
+    dev = _require_gpu(logits, target, out, stats)
+    B, R = target.shape
+    V = logits.shape[-1]
+    assert logits.stride(-1) == 1 and out.is_contiguous()
+    assert stats is None or stats.is_contiguous()
+    with torch.cuda.device(dev), _Timed("mirl_logprob_fwd", dev):
+        st = load().mirl_logprob_fwd(
+            logits.data_ptr(), _dtype_code(logits), B, R, V, logits.stride(0), logits.stride(1),
+            target.data_ptr(), target.stride(0), target.stride(1), int(vocab_start),
+            int(vocab_end), out.data_ptr(), _ptr(stats), _stream(dev),
+        )
+    _check(st, "mirl_logprob_fwd")
+
+
+def logprob_bwd(
+    logits: torch.Tensor,
+    target: torch.Tensor,
+    vocab_start: int,
+    vocab_end: int,
+    stats: torch.Tensor,
+    grad_out: torch.Tensor,
+    grad_in: torch.Tensor,
+) -> None:
+    """grad_in[b, r, :] = (onehot(target) - softmax(logits[b, r])) * grad_out[b, r].
+
+    Rows r >= R (= target.shape[1]) of grad_in are zeroed.  grad_in may be logits itself.
+    """
+    dev = _require_gpu(logits, target, stats, grad_out, grad_in)
+    B, R = target.shape
+    Rt = grad_in.shape[1]
+    V = logits.shape[-1]
+    assert grad_in.stride(-1) == 1 and logits.stride(-1) == 1
+    assert grad_in.dtype == logits.dtype and grad_out.dtype == torch.float32
+    with torch.cuda.device(dev), _Timed("mirl_logprob_bwd", dev):
+        st = load().mirl_logprob_bwd(
+            logits.data_ptr(), _dtype_code(logits), B, R, Rt, V, logits.stride(0),
+            logits.stride(1), target.data_ptr(), target.stride(0), target.stride(1),
+            int(vocab_start), int(vocab_end), stats.data_ptr(), grad_out.data_ptr(),
+            grad_out.stride(0), grad_out.stride(1), grad_in.data_ptr(), grad_in.stride(0),
+            grad_in.stride(1), _stream(dev),
+        )
+    _check(st, "mirl_logprob_bwd")
+
+
+# ---------------------------------------------------------------------------
+# ClippedPG loss
+# ---------------------------------------------------------------------------
+def _view(t: Optional[torch.Tensor]) -> View2D:
+    if t is None:
+        return View2D(None, 0, 0)
+    return View2D(t.data_ptr(), t.stride(0), t.stride(1))
+
+
+def clipped_pg(
+    cfg: PgConfig,
+    curr: torch.Tensor,
+    unfiltered: Optional[torch.Tensor],
+    token_mask: torch.Tensor,
+    advantages: torch.Tensor,
+    prev: Optional[torch.Tensor],
+    generation: torch.Tensor,
+    reference: Optional[torch.Tensor],
+    support_mask: Optional[torch.Tensor],
+    sample_mask: torch.Tensor,
+    rewards: Optional[torch.Tensor],
+    global_valid_seqs: torch.Tensor,
+    global_valid_toks: torch.Tensor,
+) -> tuple[torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
+    """Run the fused ClippedPG kernel; returns (metrics[18], grad_curr, grad_unfiltered)."""
+    dev = _require_gpu(curr, token_mask, advantages, generation, sample_mask)
+    B, L = curr.shape
+    dtype = curr.dtype
+    metrics = torch.empty(PG_NUM_METRICS, dtype=dtype, device=dev)
+    grad_curr = torch.empty((B, L), dtype=dtype, device=dev)
+    grad_unf = torch.empty((B, L), dtype=dtype, device=dev) if unfiltered is not None else None
+    lib = load()
+    ws = torch.empty(int(lib.mirl_clipped_pg_workspace_elems(B)), dtype=dtype, device=dev)
+    with torch.cuda.device(dev), _Timed("mirl_clipped_pg", dev):
+        st = lib.mirl_clipped_pg(
+            ctypes.byref(cfg), _dtype_code(curr), B, L, _view(curr), _view(unfiltered),
+            _view(token_mask), _view(advantages), _view(prev), _view(generation),
+            _view(reference), _view(support_mask), sample_mask.data_ptr(), _ptr(rewards),
+            global_valid_seqs.data_ptr(), global_valid_toks.data_ptr(), metrics.data_ptr(),
+            grad_curr.data_ptr(), _ptr(grad_unf), ws.data_ptr(), _stream(dev),
+        )
+    _check(st, "mirl_clipped_pg")
+    return metrics, grad_curr, grad_unf
+
+
+# ---------------------------------------------------------------------------
+# GRPO advantages
+# ---------------------------------------------------------------------------
+def grpo_advantage(
+    prompts: torch.Tensor,
+    rewards: torch.Tensor,
+    valid_mask: Optional[torch.Tensor],
+    leave_one_out: bool,
+    normalize: bool,
+    want_stats: bool = False,
+    std_rewards: Optional[torch.Tensor] = None,
+) -> tuple[
+    torch.Tensor, Optional[torch.Tensor], Optional[torch.Tensor], Optional[torch.Tensor]
+]:
+    """GRPO advantages [B]; with want_stats also (baseline, std, trivial) per sample."""
+    dev = _require_gpu(prompts, rewards, valid_mask)
+    B = rewards.shape[0]
+    K = prompts.shape[1]
+    assert prompts.dtype == torch.int64 and prompts.stride(1) == 1
+    assert rewards.dtype == torch.float32 and rewards.is_contiguous()
+    adv = torch.empty(B, dtype=torch.float32, device=dev)
+    base = torch.empty_like(adv) if want_stats else None
+    std = torch.empty_like(adv) if want_stats else None
+    trivial = torch.empty(B, dtype=torch.bool, device=dev) if want_stats else None
+    with torch.cuda.device(dev), _Timed("mirl_grpo_advantage", dev):
+        st = load().mirl_grpo_advantage(
+            prompts.data_ptr(), B, K, prompts.stride(0), rewards.data_ptr(), _ptr(std_rewards),
+            _ptr(valid_mask),
+            int(bool(leave_one_out)), int(bool(normalize)), adv.data_ptr(), _ptr(base), _ptr(std),
+            _ptr(trivial), _stream(dev),
+        )
+    _check(st, "mirl_grpo_advantage")
+    return adv, base, std, trivial

@@ -1,0 +1,80 @@
+"""Training-side top-k / top-p filtering: drop-in for ``nemo_rl.algorithms.logits_sampling_utils``.
+
+``TrainingSamplingParams`` and the predicates keep the reference's semantics
+(reference logits_sampling_utils.py:29-66).  ``apply_top_k_top_p`` runs the
+gfx950 selection kernel (``rl_amd.distributed.sampling``) and keeps the
+reference's autograd contract: gradients outside the kept set are zero.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+# Rows per chunk of the reference's sort-based filter (reference :26).  The
+# kernels here do not sort the vocabulary, so the value is accepted and ignored.
+TOP_K_TOP_P_CHUNK_SIZE: int = 256
+
+
+@dataclass
+class TrainingSamplingParams:
+    """Sampling parameters mirrored from generation (reference :29-44).
+
+    top_k: None or <= 0 disables top-k; top_p: 1.0 disables top-p;
+    temperature is applied by the caller (see ``apply_temperature_scaling``).
+    """
+
+    top_k: int | None = None
+    top_p: float = 1.0
+    temperature: float = 1.0
+
+
+def _need_top_k_filtering(top_k: int | None) -> bool:
+    return top_k is not None and top_k > 0
+
+
+def _need_top_p_filtering(top_p: float | None) -> bool:
+    return top_p is not None and top_p != 1.0
+
+
+def need_top_k_or_top_p_filtering(sampling_params: Optional[TrainingSamplingParams]) -> bool:
+    """True iff top-k (k > 0) or top-p (p != 1) filtering is requested (reference :57-66)."""
+    if sampling_params is None:
+        return False
+    return _need_top_k_filtering(sampling_params.top_k) or _need_top_p_filtering(
+        sampling_params.top_p
+    )
+
+
+def apply_top_k_top_p(
+    logits: torch.Tensor,
+    top_k: int | None,
+    top_p: float,
+    chunk_size: int | None = TOP_K_TOP_P_CHUNK_SIZE,
+) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """Mask logits outside the top-k / top-p set to -inf (reference :256-287).
+
+    Returns ``(filtered_logits, keep_mask)``, or ``(logits, None)`` when no
+    filtering is requested.  Ties at the k-th value are all kept; top-p keeps
+    the shortest suffix of the ascending (stable) order whose cumulative
+    probability exceeds ``1 - top_p``, and always the maximum.
+    """
+    if not _need_top_k_filtering(top_k) and not _need_top_p_filtering(top_p):
+        return logits, None
+    from rl_amd.distributed.sampling import apply_top_k_top_p_kernel
+
+    return apply_top_k_top_p_kernel(logits, top_k, top_p)
+
+
+def apply_temperature_scaling(logits: torch.Tensor, temperature: float) -> torch.Tensor:
+    """In-place ``logits.div_(temperature)`` in the logits dtype (reference automodel/train.py:248-262).
+
+    Kept as the reference's plain tensor op: a single elementwise pass whose
+    rounding (fp32 quotient rounded to the logits dtype) the filtered kernels
+    reproduce when they fuse the temperature instead.
+    """
+    if temperature != 1.0:
+        logits.div_(temperature)
+    return logits

@@ -1,0 +1,107 @@
+"""Loss math helpers: drop-in for the hot-path subset of ``nemo_rl.algorithms.utils``.
+
+``calculate_kl`` and ``masked_mean`` are the reference's one-line tensor
+formulas (reference utils.py:56-115, :294-306), kept as plain tensor code for
+callers that use them directly; ``ClippedPGLossFn`` does not call them — its
+kernel fuses the same arithmetic.  ``calculate_baseline_and_std_per_prompt``
+runs the GRPO group-statistics kernel.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from rl_amd import _C
+
+
+def calculate_kl(
+    logprobs: torch.Tensor,
+    logprobs_reference: torch.Tensor,
+    kl_type: str = "k3",
+    input_clamp_value: float | None = 20.0,
+    output_clamp_value: float | None = 10.0,
+    importance_sampling_weights: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Per-token KL estimate (k1 / k2 / k3, Schulman 2020) with optional clamps and IS weights."""
+    logr = logprobs_reference - logprobs
+    if input_clamp_value is not None:
+        logr_clamped = logr.clamp(min=-input_clamp_value, max=input_clamp_value)
+        if importance_sampling_weights is not None:
+            importance_sampling_weights = torch.where(
+                logr == logr_clamped,
+                importance_sampling_weights,
+                importance_sampling_weights.detach(),
+            )
+        logr = logr_clamped
+    if kl_type == "k1":
+        kl = -logr
+    elif kl_type == "k2":
+        kl = torch.square(logr) / 2
+    elif kl_type == "k3":
+        kl = torch.exp(logr) - 1 - logr
+    else:
+        raise ValueError(f"Invalid KL type: {kl_type}")
+    if importance_sampling_weights is not None:
+        kl = importance_sampling_weights * kl
+    if output_clamp_value is not None:
+        kl = kl.clamp(min=-output_clamp_value, max=output_clamp_value)
+    return kl
+
+
+def masked_mean(
+    values: torch.Tensor,
+    mask: torch.Tensor,
+    dim: Optional[int] = None,
+    global_normalization_factor: Optional[torch.Tensor | float] = None,
+):
+    """``sum(values * mask, dim) / (N + 1e-8)`` with N = sum(mask) or the global factor."""
+    normalization_factor = (
+        torch.sum(mask, dim=dim) if global_normalization_factor is None else global_normalization_factor
+    )
+    return torch.sum(values * mask, dim=dim) / (normalization_factor + 1e-8)
+
+
+def _to_device_inputs(prompts, rewards, valid_mask):
+    if rewards.is_cuda:
+        dev = rewards.device
+    elif torch.cuda.is_available():
+        dev = torch.device("cuda", torch.cuda.current_device())
+    else:
+        raise _C.MirlError("the GRPO advantage kernel needs a ROCm GPU; none is available")
+    p = prompts
+    if p.dim() == 1:
+        p = p.unsqueeze(1)
+    p = p.to(device=dev, dtype=torch.int64).contiguous()
+    r = rewards.to(device=dev, dtype=torch.float32).contiguous()
+    v = None if valid_mask is None else valid_mask.to(device=dev, dtype=torch.float32).contiguous()
+    return p, r, v
+
+
+def calculate_baseline_and_std_per_prompt(
+    prompts: torch.Tensor,
+    rewards: torch.Tensor,
+    valid_mask: torch.Tensor,
+    leave_one_out_baseline: bool = True,
+    std_rewards: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Per-sample group baseline, std and trivial-group flag (reference utils.py:118-234).
+
+    Runs on the GPU; CPU inputs are copied to the current device and the
+    results copied back.  ``std_rewards`` (DAPO) replaces the rewards in the
+    spread statistics and the trivial-group test only.
+    """
+    p, r, v = _to_device_inputs(prompts, rewards, valid_mask)
+    q = None
+    if std_rewards is not None and std_rewards is not rewards:
+        q = std_rewards.to(device=r.device, dtype=torch.float32).contiguous()
+    _, base, std, trivial = _C.grpo_advantage(
+        p, r, v, leave_one_out_baseline, True, want_stats=True, std_rewards=q
+    )
+    out_dev = rewards.device
+    return (
+        base.to(device=out_dev, dtype=rewards.dtype),
+        std.to(device=out_dev, dtype=rewards.dtype),
+        trivial.to(out_dev),
+    )

@@ -1,0 +1,636 @@
+// Fused ClippedPG loss: forward value, every metric of the reference's metric
+// dictionary, and the closed-form gradient with respect to the token
+// log-probabilities, in two launches over [B, L] tokens:
+//
+//   pg_rows_kernel   one workgroup per sequence b: row masks, sequence-level
+//                    ratios / IS weights, per-token loss terms and gradients,
+//                    and the row's partial sums for the loss and metrics;
+//   pg_final_kernel  one workgroup: reduces the row partials in row order
+//                    (deterministic), writes the loss and metrics, and adds
+//                    the one cross-row gradient term (VAPO NLL, whose
+//                    normaliser is the batch's correct-token count).
+//
+// Semantics: nemo_rl/algorithms/loss/loss_functions.py:698-1183 (__call__),
+// nemo_rl/algorithms/loss/clipped_pg.py:38-194 (objective, diagnostics),
+// nemo_rl/algorithms/utils.py:56-115 (calculate_kl), :294-306 (masked_mean).
+// Gradient rules are PyTorch's autograd rules for the same op sequence:
+// maximum/minimum split the gradient 50/50 on exact ties, clamp passes it on
+// the closed interval, where() passes it to the selected branch, nan_to_num
+// passes it where the input was finite.
+
+#include "common.h"
+
+namespace mirl {
+namespace {
+
+constexpr int kRowThreads = 256;
+constexpr int kFinalThreads = 1024;
+
+// row partial-sum slots
+enum Slot {
+  P_ACTOR = 0,
+  P_KL,
+  P_TMPE,
+  P_RATIO,
+  P_RATIO_C,
+  P_RATIO_MIN,
+  P_RATIO_MAX,
+  P_RATIO_C_MIN,
+  P_RATIO_C_MAX,
+  P_GEN_KL,
+  P_POL_KL,
+  P_JS,
+  P_ENT,
+  P_SIR,
+  P_NVS,
+  P_CVT,
+  P_NLL,
+  P_OOB,
+  P_EXCL,
+  NUM_SLOTS
+};
+
+template <class T>
+struct View {
+  const T* p;
+  int64_t sb, sl;
+  __device__ __forceinline__ T operator()(int64_t b, int64_t l) const { return p[b * sb + l * sl]; }
+};
+
+struct MaskView {
+  const uint8_t* p;
+  int64_t sb, sl;
+  __device__ __forceinline__ bool operator()(int64_t b, int64_t l) const {
+    return p[b * sb + l * sl] != 0;
+  }
+};
+
+template <class T>
+__device__ __forceinline__ T dexp(T x) {
+  if constexpr (sizeof(T) == 8) return exp(x); else return expf(x);
+}
+template <class T>
+__device__ __forceinline__ T dlog(T x) {
+  if constexpr (sizeof(T) == 8) return log(x); else return logf(x);
+}
+template <class T>
+__device__ __forceinline__ T dabs(T x) {
+  if constexpr (sizeof(T) == 8) return fabs(x); else return fabsf(x);
+}
+template <class T>
+__device__ __forceinline__ T nan_to_zero_all(T x) {
+  // nan_to_num(x, nan=0, posinf=0, neginf=0)
+  return isfinite(x) ? x : T(0);
+}
+template <class T>
+__device__ __forceinline__ T dclamp(T x, T lo, T hi) {
+  // torch.clamp: min then max, NaN propagates
+  if (isnan(x)) return x;
+  return x < lo ? lo : (x > hi ? hi : x);
+}
+
+// maximum(a, b) gradient share of a (PyTorch: ties split evenly)
+template <class T>
+__device__ __forceinline__ T max_share_a(T a, T b) {
+  return a > b ? T(1) : (a < b ? T(0) : T(0.5));
+}
+
+// Per-token KL estimate k(logr) and its derivative dk/dlogr.
+template <class T>
+__device__ __forceinline__ T kl_value(int type, T lr) {
+  if (type == MIRL_KL_K1) return -lr;
+  if (type == MIRL_KL_K2) return (lr * lr) / T(2);
+  return (dexp(lr) - T(1)) - lr;
+}
+template <class T>
+__device__ __forceinline__ T kl_deriv(int type, T lr) {
+  if (type == MIRL_KL_K1) return T(-1);
+  if (type == MIRL_KL_K2) return lr;
+  return dexp(lr) - T(1);
+}
+
+// Block-wide reductions over kRowThreads / kFinalThreads threads.
+template <class T, int NT>
+__device__ T block_sum(T v, T* scratch) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x % 64, wv = threadIdx.x / 64;
+  __syncthreads();
+  if (lane == 0) scratch[wv] = v;
+  __syncthreads();
+  T r = T(0);
+#pragma unroll
+  for (int k = 0; k < NT / 64; ++k) r += scratch[k];
+  return r;
+}
+
+template <class T>
+__device__ __forceinline__ T wave_min_t(T v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const T o = __shfl_xor(v, off, 64);
+    v = (o < v || isnan(o)) ? o : v;
+  }
+  return v;
+}
+template <class T>
+__device__ __forceinline__ T wave_max_t(T v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const T o = __shfl_xor(v, off, 64);
+    v = (o > v || isnan(o)) ? o : v;
+  }
+  return v;
+}
+template <class T, int NT>
+__device__ T block_min(T v, T* scratch) {
+  v = wave_min_t(v);
+  const int lane = threadIdx.x % 64, wv = threadIdx.x / 64;
+  __syncthreads();
+  if (lane == 0) scratch[wv] = v;
+  __syncthreads();
+  T r = scratch[0];
+  for (int k = 1; k < NT / 64; ++k) r = (scratch[k] < r || isnan(scratch[k])) ? scratch[k] : r;
+  return r;
+}
+template <class T, int NT>
+__device__ T block_max(T v, T* scratch) {
+  v = wave_max_t(v);
+  const int lane = threadIdx.x % 64, wv = threadIdx.x / 64;
+  __syncthreads();
+  if (lane == 0) scratch[wv] = v;
+  __syncthreads();
+  T r = scratch[0];
+  for (int k = 1; k < NT / 64; ++k) r = (scratch[k] > r || isnan(scratch[k])) ? scratch[k] : r;
+  return r;
+}
+
+// Truncated importance sampling applied to one weight (loss_functions.py:921-1013).
+// `oob` reports whether the weight fell outside the truncation bounds.
+template <class T>
+__device__ __forceinline__ T truncate_is(const mirl_pg_config& cfg, T w, T A, T seq_kept, bool* oob) {
+  if (cfg.tis_type == MIRL_TIS_TIS) {
+    const T tmin = T(cfg.tis_ratio_min), tmax = T(cfg.tis_ratio);
+    *oob = (w > tmax) || (w < tmin);
+    return dclamp(w, tmin, tmax);
+  }
+  if (cfg.tis_type == MIRL_TIS_ICEPOP) {
+    const bool kept = (w >= T(cfg.tis_ratio_min)) && (w <= T(cfg.tis_ratio));
+    *oob = !kept;
+    return kept ? w : T(0);
+  }
+  if (cfg.tis_type == MIRL_TIS_ADAPTIVE) {
+    const bool kept = (w <= T(cfg.adaptive_outer)) && ((A >= T(0)) || (w >= T(cfg.tis_ratio_min))) &&
+                      ((A <= T(0)) || (w <= T(cfg.adaptive_hi)));
+    *oob = !kept;
+    return kept ? w : T(0);
+  }
+  if (cfg.tis_type == MIRL_TIS_SEQ_MASK) {
+    *oob = false;
+    return w * seq_kept;
+  }
+  *oob = false;
+  return w;
+}
+
+template <class T>
+struct Inputs {
+  View<T> curr, unf, tm, adv, prev, gen, ref;
+  MaskView psm;
+  const T* sample_mask;
+  const T* rewards;
+  const T* gvs;
+  const T* gvt;
+};
+
+template <class T>
+__global__ __launch_bounds__(kRowThreads) void pg_rows_kernel(mirl_pg_config cfg, int64_t L,
+                                                              Inputs<T> in, T* __restrict__ gcurr,
+                                                              T* __restrict__ gunf,
+                                                              T* __restrict__ part) {
+  __shared__ T scratch[kRowThreads / 64];
+  const int64_t b = blockIdx.x;
+  const int tid = threadIdx.x;
+  const T eps = T(1e-8);
+  const T gvt = *in.gvt + eps;
+  const T gvs = *in.gvs + eps;
+  const bool has_kl = cfg.kl_penalty != 0.0;
+  const T beta = T(cfg.kl_penalty);
+
+  // ---- pass A: row masks --------------------------------------------------
+  // support'(l) = psm & ~isneginf(prev) & ~isneginf(gen)
+  auto support = [&](int64_t l) -> bool {
+    if (!cfg.has_support_mask) return true;
+    const T pv = cfg.force_on_policy ? in.curr(b, l) : in.prev(b, l);
+    return in.psm(b, l) && !(isinf(pv) && pv < 0) && !(isinf(in.gen(b, l)) && in.gen(b, l) < 0);
+  };
+  T any_tm = 0, any_tm2 = 0, sum_tm = 0, sum_tm2 = 0;
+  for (int64_t l = tid; l < L; l += kRowThreads) {
+    const T tmv = in.tm(b, l);
+    const T tm2 = tmv * (support(l) ? T(1) : T(0));
+    any_tm += (tmv != T(0)) ? T(1) : T(0);
+    any_tm2 += (tm2 != T(0)) ? T(1) : T(0);
+    sum_tm += tmv;
+    sum_tm2 += tm2;
+  }
+  any_tm = block_sum<T, kRowThreads>(any_tm, scratch);
+  any_tm2 = block_sum<T, kRowThreads>(any_tm2, scratch);
+  sum_tm = block_sum<T, kRowThreads>(sum_tm, scratch);
+  sum_tm2 = block_sum<T, kRowThreads>(sum_tm2, scratch);
+  const T sm = in.sample_mask[b] * (any_tm > T(0) ? T(1) : T(0));
+  const T sm2 = cfg.has_support_mask ? sm * (any_tm2 > T(0) ? T(1) : T(0)) : sm;
+  // tokens of this row after the support adjustment (token_mask in the objective)
+  auto tm2_at = [&](int64_t l) -> T {
+    const T tmv = in.tm(b, l);
+    return cfg.has_support_mask ? tmv * (support(l) ? T(1) : T(0)) : tmv;
+  };
+  // sanitised operands: where(mask2 != 0, x, 0)
+  auto prev_of = [&](int64_t l) -> T { return cfg.force_on_policy ? in.curr(b, l) : in.prev(b, l); };
+
+  // ---- pass B: sequence-level quantities ----------------------------------
+  T seq_lr = 0, seq_is = 0, seq_lir = 0;
+  {
+    for (int64_t l = tid; l < L; l += kRowThreads) {
+      const T tm2 = tm2_at(l);
+      const T mask2 = tm2 * sm2;
+      const bool on = mask2 != T(0);
+      const T c = on ? in.curr(b, l) : T(0);
+      const T pv = on ? prev_of(l) : T(0);
+      const T gv = on ? in.gen(b, l) : T(0);
+      seq_lr += (c - pv) * tm2;
+      seq_is += (pv - gv) * mask2;
+      seq_lir += nan_to_zero_all(pv - gv) * tm2;
+    }
+    seq_lr = block_sum<T, kRowThreads>(seq_lr, scratch);
+    seq_is = block_sum<T, kRowThreads>(seq_is, scratch);
+    seq_lir = block_sum<T, kRowThreads>(seq_lir, scratch);
+  }
+  // clamp bounds are formed in double, as Python does, then rounded once
+  const T lo = T(1.0 - cfg.ratio_clip_min);
+  const T hi = T(1.0 + cfg.ratio_clip_max);
+  const bool seq_ratio = cfg.sequence_level_is && !cfg.disable_ppo_ratio && !cfg.force_on_policy;
+  const T r_seq = seq_ratio ? dexp(seq_lr / (sum_tm2 + eps)) : T(0);
+  const T w_seq = nan_to_zero_all(dexp(seq_is));
+  T seq_kept = T(1);
+  if (cfg.tis_type == MIRL_TIS_SEQ_MASK) {
+    const T g = dexp(seq_lir / (sum_tm2 + eps));
+    seq_kept = (g >= T(cfg.tis_ratio_min) && g <= T(cfg.tis_ratio)) ? T(1) : T(0);
+  }
+
+  // ---- pass C: per-token terms -------------------------------------------
+  T acc[NUM_SLOTS];
+#pragma unroll
+  for (int k = 0; k < NUM_SLOTS; ++k) acc[k] = T(0);
+  acc[P_RATIO_MIN] = T(INFINITY);
+  acc[P_RATIO_C_MIN] = T(INFINITY);
+  acc[P_RATIO_MAX] = T(-INFINITY);
+  acc[P_RATIO_C_MAX] = T(-INFINITY);
+  T gspo_sum = 0;  // sum_t alpha_t * w_t * dcl_t/dr_seq  (sequence-level ratio)
+  const T actor_row_norm = sum_tm2 + eps;
+  const T kl_row_norm = sum_tm + eps;
+  const bool correct = cfg.has_rewards && cfg.nll_weight > 0.0 && in.rewards[b] > T(0);
+
+  for (int64_t l = tid; l < L; l += kRowThreads) {
+    const T tmv = in.tm(b, l);
+    const T tm2 = tm2_at(l);
+    const T mask2 = tm2 * sm2;
+    const T kl_mask = tmv * sm;
+    const bool on = mask2 != T(0);
+    const T craw = in.curr(b, l);
+    const T c = on ? craw : T(0);
+    const T pv = on ? prev_of(l) : T(0);
+    const T gv = on ? in.gen(b, l) : T(0);
+    const T A = in.adv(b, l);
+    T gc = T(0);  // dloss/dcurr (this token)
+    T gu = T(0);  // dloss/dunfiltered
+
+    // KL term ------------------------------------------------------------
+    if (has_kl) {
+      const bool kon = kl_mask != T(0);
+      const T cu = kon ? (cfg.has_unfiltered ? in.unf(b, l) : craw) : T(0);
+      const T rf = kon ? in.ref(b, l) : T(0);
+      const T kgen = kon ? in.gen(b, l) : T(0);
+      // importance weight exp(cu - X), X detached
+      const T e = cfg.use_on_policy_kl ? dexp(cu - kgen) : dexp(cu - cu);
+      const T w = nan_to_zero_all(e);
+      const T dw = isfinite(e) ? e : T(0);
+      T lr = rf - cu;
+      T dlr_pass = T(1);  // d(clamped logr)/d(logr)
+      bool w_grad = true;
+      if (cfg.has_kl_input_clamp) {
+        const T ic = T(cfg.kl_input_clamp);
+        const T lc = dclamp(lr, -ic, ic);
+        w_grad = (lr == lc);
+        dlr_pass = (lr >= -ic && lr <= ic) ? T(1) : T(0);
+        lr = lc;
+      }
+      const T k = kl_value<T>(cfg.kl_type, lr);
+      T kw = w * k;
+      T out_pass = T(1);
+      if (cfg.has_kl_output_clamp) {
+        const T oc = T(cfg.kl_output_clamp);
+        out_pass = (kw >= -oc && kw <= oc) ? T(1) : T(0);
+        kw = dclamp(kw, -oc, oc);
+      }
+      const T klt = beta * kw;
+      T kappa;
+      if (cfg.token_level_loss) {
+        kappa = kl_mask / gvt;
+        acc[P_KL] += klt * kl_mask;
+      } else {
+        kappa = sm * tmv / (kl_row_norm * gvs);
+        acc[P_KL] += klt * tmv;  // scaled per row below
+      }
+      // d kl_t / d cu
+      const T dk = kl_deriv<T>(cfg.kl_type, lr) * dlr_pass * T(-1);
+      const T dkl = beta * out_pass * ((w_grad ? dw : T(0)) * k + w * dk);
+      const T g = kon ? kappa * dkl : T(0);
+      if (cfg.has_unfiltered) gu = g; else gc += g;
+    }
+
+    // importance weights -------------------------------------------------
+    T w = T(1);
+    bool has_w = false;
+    if (cfg.need_is) {
+      has_w = true;
+      w = cfg.sequence_level_is ? w_seq : nan_to_zero_all(dexp(pv - gv));
+      bool oob = false;
+      w = truncate_is(cfg, w, A, seq_kept, &oob);
+      acc[P_OOB] += (oob ? T(1) : T(0)) * mask2;
+    }
+    const bool use_w = cfg.use_is_correction != 0;
+
+    // actor objective ------------------------------------------------------
+    T r, rc, dr_dc, drc_dr;
+    if (cfg.force_on_policy) {
+      r = dexp(c - c);
+      rc = r;
+      dr_dc = r;
+      drc_dr = T(1);
+    } else if (!cfg.disable_ppo_ratio) {
+      if (cfg.sequence_level_is) {
+        r = r_seq;
+        dr_dc = T(0);  // handled through gspo_sum
+      } else {
+        r = dexp(c - pv);
+        dr_dc = r;
+      }
+      rc = dclamp(r, lo, hi);
+      drc_dr = (r >= lo && r <= hi) ? T(1) : T(0);
+    } else {
+      r = c;
+      rc = c;
+      dr_dc = T(1);
+      drc_dr = T(1);
+    }
+    const T na = -A;
+    T cl, dcl_dr = T(0), dcl_dc_direct = T(0);
+    if (cfg.use_cispo) {
+      cl = (na * rc) * c;
+      dcl_dc_direct = na * rc;
+    } else {
+      const T a1 = na * r, a2 = na * rc;
+      cl = a1 > a2 ? a1 : (a1 < a2 ? a2 : a1);
+      if (isnan(a1) || isnan(a2)) cl = a1 + a2;
+      const T sa = max_share_a(a1, a2);
+      dcl_dr = sa * na + (T(1) - sa) * na * drc_dr;
+      if (cfg.ratio_clip_c > 0.0 && A < T(0)) {
+        const T z = na * T(cfg.ratio_clip_c);
+        const T s = cl < z ? T(1) : (cl > z ? T(0) : T(0.5));
+        cl = cl < z ? cl : z;
+        dcl_dr *= s;
+      }
+    }
+    const T wv = (has_w && use_w) ? w : T(1);
+    const T v = wv * cl;
+    T alpha;
+    if (cfg.token_level_loss) {
+      alpha = mask2 / gvt;
+      acc[P_ACTOR] += v * mask2;
+    } else {
+      alpha = sm2 * tm2 / (actor_row_norm * gvs);
+      acc[P_ACTOR] += v * tm2;  // scaled per row below
+    }
+    if (cfg.use_cispo) {
+      gc += on ? alpha * wv * dcl_dc_direct : T(0);
+    } else if (seq_ratio) {
+      gspo_sum += alpha * wv * dcl_dr;
+    } else {
+      gc += on ? alpha * wv * dcl_dr * dr_dc : T(0);
+    }
+
+    // NLL bookkeeping (gradient added by the final kernel)
+    if (correct) {
+      acc[P_CVT] += mask2;
+      acc[P_NLL] += (-c) * mask2;
+    }
+
+    // metrics ---------------------------------------------------------------
+    acc[P_TMPE] += dexp(dabs(gv - pv) * mask2) * mask2;
+    if (cfg.full_metrics) {
+      acc[P_RATIO] += r * mask2;
+      acc[P_RATIO_C] += rc * mask2;
+      if (on) {
+        acc[P_RATIO_MIN] = (r < acc[P_RATIO_MIN] || isnan(r)) ? r : acc[P_RATIO_MIN];
+        acc[P_RATIO_MAX] = (r > acc[P_RATIO_MAX] || isnan(r)) ? r : acc[P_RATIO_MAX];
+        acc[P_RATIO_C_MIN] = (rc < acc[P_RATIO_C_MIN] || isnan(rc)) ? rc : acc[P_RATIO_C_MIN];
+        acc[P_RATIO_C_MAX] = (rc > acc[P_RATIO_C_MAX] || isnan(rc)) ? rc : acc[P_RATIO_C_MAX];
+      }
+      acc[P_GEN_KL] += kl_value<T>(cfg.kl_type, pv - gv) * mask2;
+      acc[P_POL_KL] += kl_value<T>(cfg.kl_type, gv - pv) * mask2;
+      const T lm = dlog(T(0.5) * dexp(pv) + T(0.5) * dexp(gv));
+      const T a = pv - lm, bb = gv - lm;
+      const T js = T(0.5) * ((dexp(a) - a) - T(1)) + T(0.5) * ((dexp(bb) - bb) - T(1));
+      acc[P_JS] += js * mask2;
+      acc[P_ENT] += (dexp(c - gv) * c) * mask2;
+    }
+    if (cfg.need_is && !cfg.sequence_level_is) acc[P_SIR] += w * mask2;
+    acc[P_EXCL] += kl_mask - mask2;
+
+    gcurr[b * L + l] = gc;
+    if (cfg.has_unfiltered) gunf[b * L + l] = gu;
+  }
+
+  // sequence-level ratio gradient: every token of the row shares r_seq
+  if (seq_ratio) {
+    gspo_sum = block_sum<T, kRowThreads>(gspo_sum, scratch);
+    const T coef = gspo_sum * r_seq / (sum_tm2 + eps);
+    for (int64_t l = tid; l < L; l += kRowThreads) {
+      const T tm2 = tm2_at(l);
+      if (tm2 * sm2 != T(0)) gcurr[b * L + l] += coef * tm2;
+    }
+  }
+
+  // ---- row partials ------------------------------------------------------
+  T* out = part + b * NUM_SLOTS;
+#pragma unroll
+  for (int k = 0; k < NUM_SLOTS; ++k) {
+    T v;
+    if (k == P_RATIO_MIN || k == P_RATIO_C_MIN) v = block_min<T, kRowThreads>(acc[k], scratch);
+    else if (k == P_RATIO_MAX || k == P_RATIO_C_MAX) v = block_max<T, kRowThreads>(acc[k], scratch);
+    else v = block_sum<T, kRowThreads>(acc[k], scratch);
+    if (tid == 0) {
+      if (k == P_ACTOR && !cfg.token_level_loss) v = sm2 * (v / actor_row_norm);
+      if (k == P_KL && !cfg.token_level_loss) v = sm * (v / kl_row_norm);
+      if (k == P_SIR && cfg.sequence_level_is) {
+        bool oob = false;
+        v = truncate_is(cfg, w_seq, T(0), seq_kept, &oob) * sm2;
+      }
+      if (k == P_NVS) v = sm2;
+      if (k == P_OOB && cfg.tis_type == MIRL_TIS_SEQ_MASK) v = (T(1) - seq_kept) * sm2;
+      out[k] = v;
+    }
+  }
+}
+
+template <class T>
+__global__ __launch_bounds__(kFinalThreads) void pg_final_kernel(mirl_pg_config cfg, int64_t B,
+                                                                 int64_t L, Inputs<T> in,
+                                                                 const T* __restrict__ part,
+                                                                 T* __restrict__ metrics,
+                                                                 T* __restrict__ gcurr) {
+  __shared__ T tot[NUM_SLOTS];
+  const int tid = threadIdx.x;
+  if (tid < NUM_SLOTS) {
+    const int k = tid;
+    T v;
+    if (k == P_RATIO_MIN || k == P_RATIO_C_MIN) {
+      v = T(INFINITY);
+      for (int64_t b = 0; b < B; ++b) {
+        const T x = part[b * NUM_SLOTS + k];
+        v = (x < v || isnan(x)) ? x : v;
+      }
+    } else if (k == P_RATIO_MAX || k == P_RATIO_C_MAX) {
+      v = T(-INFINITY);
+      for (int64_t b = 0; b < B; ++b) {
+        const T x = part[b * NUM_SLOTS + k];
+        v = (x > v || isnan(x)) ? x : v;
+      }
+    } else {
+      v = T(0);
+      for (int64_t b = 0; b < B; ++b) v += part[b * NUM_SLOTS + k];
+    }
+    tot[k] = v;
+  }
+  __syncthreads();
+  const T eps = T(1e-8);
+  const T gvt = *in.gvt + eps;
+  const T gvs = *in.gvs + eps;
+  const T cvt = tot[P_CVT];
+  const bool nll_on = cfg.has_rewards && cfg.nll_weight > 0.0;
+  if (tid == 0) {
+    const T actor = tot[P_ACTOR] / (cfg.token_level_loss ? gvt : gvs);
+    const T kl = cfg.kl_penalty != 0.0 ? tot[P_KL] / (cfg.token_level_loss ? gvt : gvs) : T(0);
+    const T nll = (nll_on && cvt > T(0)) ? tot[P_NLL] / (cvt + eps) : T(0);
+    const T loss = (actor + kl) + T(cfg.nll_weight) * nll;
+    T* m = metrics;
+    m[MIRL_M_LOSS] = loss;
+    m[MIRL_M_TOKEN_MULT_PROB_ERROR] = tot[P_TMPE] / gvt;
+    m[MIRL_M_PROBS_RATIO] = tot[P_RATIO] / gvt;
+    m[MIRL_M_PROBS_RATIO_CLAMPED] = tot[P_RATIO_C] / gvt;
+    m[MIRL_M_PROBS_RATIO_MIN] = tot[P_RATIO_MIN];
+    m[MIRL_M_PROBS_RATIO_MAX] = tot[P_RATIO_MAX];
+    m[MIRL_M_PROBS_RATIO_CLAMPED_MIN] = tot[P_RATIO_C_MIN];
+    m[MIRL_M_PROBS_RATIO_CLAMPED_MAX] = tot[P_RATIO_C_MAX];
+    m[MIRL_M_GEN_KL_ERROR] = tot[P_GEN_KL] / gvt;
+    m[MIRL_M_POLICY_KL_ERROR] = tot[P_POL_KL] / gvt;
+    m[MIRL_M_JS_DIVERGENCE_ERROR] = tot[P_JS] / gvt;
+    m[MIRL_M_APPROX_ENTROPY] = -(tot[P_ENT] / gvt);
+    m[MIRL_M_SAMPLING_IMPORTANCE_RATIO] = tot[P_SIR] / (cfg.sequence_level_is ? gvs : gvt);
+    m[MIRL_M_KL_PENALTY] = cfg.kl_penalty != 0.0 ? kl / T(cfg.kl_penalty) : T(0);
+    m[MIRL_M_NUM_VALID_SAMPLES] = tot[P_NVS];
+    m[MIRL_M_POSITIVE_NLL_LOSS] = nll;
+    m[MIRL_M_IS_OOB_RATIO] = tot[P_OOB] / (cfg.tis_type == MIRL_TIS_SEQ_MASK ? gvs : gvt);
+    m[MIRL_M_POLICY_SUPPORT_EXCLUDED_TOKENS] = tot[P_EXCL];
+  }
+  if (nll_on && cvt > T(0)) {
+    // d(mu * nll)/dcurr = -mu * correct_mask / (cvt + 1e-8)
+    const T coef = -T(cfg.nll_weight) / (cvt + eps);
+    for (int64_t i = tid; i < B * L; i += kFinalThreads) {
+      const int64_t b = i / L, l = i - b * L;
+      if (!(in.rewards[b] > T(0))) continue;
+      const T tmv = in.tm(b, l);
+      T tm2 = tmv;
+      if (cfg.has_support_mask) {
+        const T pv = cfg.force_on_policy ? in.curr(b, l) : in.prev(b, l);
+        const bool sup = in.psm(b, l) && !(isinf(pv) && pv < 0) && !(isinf(in.gen(b, l)) && in.gen(b, l) < 0);
+        tm2 = sup ? tmv : T(0);
+      }
+      // sm2 for row b: recover from the row partial (num valid samples slot)
+      const T sm2 = part[b * NUM_SLOTS + P_NVS];
+      const T mask2 = tm2 * sm2;
+      if (mask2 != T(0)) gcurr[i] += coef * mask2;
+    }
+  }
+}
+
+template <class T>
+int run(const mirl_pg_config* cfg, int64_t B, int64_t L, const mirl_view2d* v,
+        const void* sample_mask, const void* rewards, const void* gvs, const void* gvt,
+        void* metrics, void* gcurr, void* gunf, void* ws, hipStream_t st) {
+  Inputs<T> in;
+  auto mk = [](const mirl_view2d& x) { return View<T>{static_cast<const T*>(x.ptr), x.sb, x.sl}; };
+  in.curr = mk(v[0]);
+  in.unf = mk(v[1]);
+  in.tm = mk(v[2]);
+  in.adv = mk(v[3]);
+  in.prev = mk(v[4]);
+  in.gen = mk(v[5]);
+  in.ref = mk(v[6]);
+  in.psm = MaskView{static_cast<const uint8_t*>(v[7].ptr), v[7].sb, v[7].sl};
+  in.sample_mask = static_cast<const T*>(sample_mask);
+  in.rewards = static_cast<const T*>(rewards);
+  in.gvs = static_cast<const T*>(gvs);
+  in.gvt = static_cast<const T*>(gvt);
+  T* part = static_cast<T*>(ws);
+  hipLaunchKernelGGL((pg_rows_kernel<T>), dim3((unsigned)B), dim3(kRowThreads), 0, st, *cfg, L, in,
+                     static_cast<T*>(gcurr), static_cast<T*>(gunf), part);
+  if (int e = check_launch("mirl_clipped_pg(rows)")) return e;
+  hipLaunchKernelGGL((pg_final_kernel<T>), dim3(1), dim3(kFinalThreads), 0, st, *cfg, B, L, in,
+                     static_cast<const T*>(part), static_cast<T*>(metrics), static_cast<T*>(gcurr));
+  return check_launch("mirl_clipped_pg(final)");
+}
+
+}  // namespace
+}  // namespace mirl
+
+using namespace mirl;
+
+extern "C" int64_t mirl_clipped_pg_workspace_elems(int64_t B) { return B * NUM_SLOTS; }
+
+extern "C" int mirl_clipped_pg(const mirl_pg_config* cfg, int dtype, int64_t B, int64_t L,
+                               mirl_view2d curr, mirl_view2d unfiltered, mirl_view2d token_mask,
+                               mirl_view2d advantages, mirl_view2d prev, mirl_view2d generation,
+                               mirl_view2d reference, mirl_view2d support_mask,
+                               const void* sample_mask, const void* rewards,
+                               const void* global_valid_seqs, const void* global_valid_toks,
+                               void* metrics, void* grad_curr, void* grad_unfiltered,
+                               void* workspace, void* stream) {
+  clear_error();
+  MIRL_REQUIRE(cfg != nullptr, "null config");
+  MIRL_REQUIRE(B > 0 && L >= 0, "invalid shape B=%lld L=%lld", (long long)B, (long long)L);
+  MIRL_REQUIRE(B < (int64_t(1) << 31), "batch too large");
+  MIRL_REQUIRE(curr.ptr && token_mask.ptr && advantages.ptr && generation.ptr && sample_mask &&
+                   global_valid_seqs && global_valid_toks && metrics && grad_curr && workspace,
+               "null pointer argument");
+  MIRL_REQUIRE(cfg->force_on_policy || prev.ptr, "prev_logprobs required");
+  MIRL_REQUIRE(cfg->kl_penalty == 0.0 || reference.ptr, "reference_policy_logprobs required");
+  MIRL_REQUIRE(!cfg->has_unfiltered || (unfiltered.ptr && grad_unfiltered),
+               "curr_logprobs_unfiltered and its gradient buffer required");
+  MIRL_REQUIRE(!cfg->has_support_mask || support_mask.ptr, "policy_support_mask required");
+  MIRL_REQUIRE(!cfg->has_rewards || rewards, "rewards required");
+  MIRL_REQUIRE(cfg->kl_type >= MIRL_KL_K1 && cfg->kl_type <= MIRL_KL_K3, "invalid KL type %d",
+               cfg->kl_type);
+  MIRL_REQUIRE(cfg->tis_type >= MIRL_TIS_NONE && cfg->tis_type <= MIRL_TIS_SEQ_MASK,
+               "invalid truncated IS type %d", cfg->tis_type);
+  const mirl_view2d views[8] = {curr, unfiltered, token_mask, advantages,
+                                prev, generation, reference, support_mask};
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == MIRL_DTYPE_F32)
+    return run<float>(cfg, B, L, views, sample_mask, rewards, global_valid_seqs, global_valid_toks,
+                      metrics, grad_curr, grad_unfiltered, workspace, st);
+  if (dtype == MIRL_DTYPE_F64)
+    return run<double>(cfg, B, L, views, sample_mask, rewards, global_valid_seqs,
+                       global_valid_toks, metrics, grad_curr, grad_unfiltered, workspace, st);
+  set_error("mirl_clipped_pg: dtype must be f32 or f64 (got %d)", dtype);
+  return MIRL_ERR_UNSUPPORTED;
+}

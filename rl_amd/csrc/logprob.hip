@@ -1,0 +1,398 @@
+// Selected-token log-probabilities over the vocabulary: forward (online
+// log-sum-exp with the target gather fused in) and backward (softmax
+// recomputed from the saved row statistics, one read + one write).
+//
+// Semantics follow nemo_rl/distributed/model_utils.py:87-135 and :228-349
+// (ChunkedDistributedLogprob with a vocab group of size 1).  Chunking along
+// the sequence only changes how the reference schedules work; every row here
+// is independent, so the result does not depend on any chunk size.
+//
+// Layout: one workgroup of W waves owns one row of V logits.  Each lane
+// streams 16-byte vectors (8 bf16 / 4 fp32) at stride 64*W vectors, U vectors
+// in flight per lane, and keeps a private (offset, sum) pair; lanes and waves
+// are merged once at the end of the row.  Nothing of size V is ever written
+// in the forward.
+
+#include "common.h"
+
+// Offsets and rescale factors below rely on exact fp32 rounding of each
+// product; contractions are written out explicitly with fmaf where wanted.
+#pragma clang fp contract(off)
+
+namespace mirl {
+namespace {
+
+template <class E>
+struct RowSpan {
+  // Splits a row at `p` into a scalar head (to reach 16-byte alignment), a
+  // body of aligned 16-byte vectors and a scalar tail.
+  int64_t head, nvec, tail0;
+  __device__ __forceinline__ RowSpan(const void* p, int64_t V) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    head = (int64_t)(((16u - (a & 15u)) & 15u) / sizeof(typename E::raw));
+    if (head > V) head = V;
+    nvec = (V - head) / E::kVec;
+    tail0 = head + nvec * E::kVec;
+  }
+};
+
+// Per-lane log-sum-exp state kept in base-2 "offset" form: the running sum is
+// sum_i 2^(x_i*log2e - off) with off = fl(m*log2e), m the running max.
+// Four partial sums break the add dependency chain.
+struct LseState {
+  float m = -INFINITY;
+  float off = 0.f;
+  float s[4] = {0.f, 0.f, 0.f, 0.f};
+
+  template <int N>
+  __device__ __forceinline__ void add(const float (&v)[N]) {
+    float bm = v[0];
+#pragma unroll
+    for (int i = 1; i < N; ++i) bm = fmaxf(bm, v[i]);
+    const float mn = fmaxf(m, bm);
+    if (mn == -INFINITY) return;  // nothing finite yet on this lane
+    if (mn != m) {
+      const float noff = mn * kLog2e;
+      // m == -inf gives 2^-inf = 0, which is the correct (empty) rescale.
+      const float sc = (m == -INFINITY) ? 0.f : fast_exp2(off - noff);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) s[k] *= sc;
+      m = mn;
+      off = noff;
+    }
+#pragma unroll
+    for (int i = 0; i < N; ++i) s[i & 3] += fast_exp2(fmaf(v[i], kLog2e, -off));
+  }
+};
+
+template <class E, int W, int U>
+__global__ __launch_bounds__(64 * W) void logprob_fwd_kernel(
+    const typename E::raw* __restrict__ logits, int64_t R, int64_t V, int64_t sb, int64_t sr,
+    const int64_t* __restrict__ target, int64_t tsb, int64_t tsr, int64_t vs, int64_t ve,
+    float* __restrict__ out, float* __restrict__ stats) {
+  constexpr int NT = 64 * W;
+  constexpr int VEC = E::kVec;
+  const int64_t row = blockIdx.x;
+  const int64_t b = row / R;
+  const int64_t r = row - b * R;
+  const typename E::raw* x = logits + b * sb + r * sr;
+  const int tid = threadIdx.x;
+
+  const int64_t t = target[b * tsb + r * tsr];
+  // targets outside the vocabulary slice (or past this row) carry no one-hot
+  const bool tmask = (t < vs) || (t >= ve) || (t - vs >= V);
+  const int64_t tl = tmask ? 0 : (t - vs);
+  float xt = 0.f;
+  if (tid == 0) xt = E::load(x + tl);
+
+  LseState st;
+  const RowSpan<E> span(x, V);
+  {
+    // scalar head and tail elements (fewer than 2*VEC per row)
+    float v[2];
+    v[0] = (tid < span.head) ? E::load(x + tid) : -INFINITY;
+    const int64_t ti = span.tail0 + tid;
+    v[1] = (ti < V) ? E::load(x + ti) : -INFINITY;
+    st.add(v);
+  }
+  const vu4* xv = reinterpret_cast<const vu4*>(x + span.head);
+  const int nvec = (int)span.nvec;
+  int i = tid;
+  for (; i + (U - 1) * NT < nvec; i += U * NT) {
+    vu4 q[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) q[u] = __builtin_nontemporal_load(xv + i + u * NT);
+    float v[U * VEC];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float w[VEC];
+      E::unpack(q[u], w);
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) v[u * VEC + k] = w[k];
+    }
+    st.add(v);
+  }
+  for (; i < nvec; i += NT) {
+    float w[VEC];
+    E::unpack(xv[i], w);
+    st.add(w);
+  }
+
+  // merge lanes: the row max and the sum re-based to it
+  float M = wave_max(st.m);
+  float s = st.s[0] + st.s[1] + st.s[2] + st.s[3];
+  const float OFF = M * kLog2e;
+  s = (st.m == -INFINITY) ? 0.f : s * fast_exp2(st.off - OFF);
+  s = wave_sum(s);
+  if constexpr (W > 1) {
+    __shared__ float sm[W], ss[W];
+    const int wv = tid / 64, lane = tid % 64;
+    if (lane == 0) {
+      sm[wv] = M;
+      ss[wv] = s;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      float Mb = sm[0];
+#pragma unroll
+      for (int k = 1; k < W; ++k) Mb = fmaxf(Mb, sm[k]);
+      const float OFFb = Mb * kLog2e;
+      float sb2 = 0.f;
+#pragma unroll
+      for (int k = 0; k < W; ++k)
+        sb2 += (sm[k] == -INFINITY) ? 0.f : ss[k] * fast_exp2(sm[k] * kLog2e - OFFb);
+      M = Mb;
+      s = sb2;
+    }
+  }
+  if (tid == 0) {
+    // s = sum 2^(x*log2e - fl(M*log2e)); undo the rounding of the offset so
+    // that logsum = log(sum exp(x - M)).
+    const float corr = fmaf(M, kLog2e, -(M * kLog2e));
+    const float logsum = logf(s) - corr * 0.6931471805599453f;
+    const float lp = (xt - M) - logsum;
+    out[row] = tmask ? 0.f : lp;
+    if (stats != nullptr) {
+      stats[2 * row] = M;
+      stats[2 * row + 1] = logsum;
+    }
+  }
+}
+
+template <class E, int W, int U>
+__global__ __launch_bounds__(64 * W) void logprob_bwd_kernel(
+    const typename E::raw* __restrict__ logits, int64_t R, int64_t Rt, int64_t V, int64_t sb,
+    int64_t sr, const int64_t* __restrict__ target, int64_t tsb, int64_t tsr, int64_t vs,
+    int64_t ve, const float* __restrict__ stats, const float* __restrict__ g, int64_t gsb,
+    int64_t gsr, typename E::raw* gin, int64_t gisb, int64_t gisr) {
+  using raw = typename E::raw;
+  constexpr int NT = 64 * W;
+  constexpr int VEC = E::kVec;
+  const int64_t row = blockIdx.x;
+  const int64_t b = row / Rt;
+  const int64_t r = row - b * Rt;
+  const int tid = threadIdx.x;
+  raw* y = gin + b * gisb + r * gisr;
+  const float gv = (r < R) ? g[b * gsb + r * gsr] : 0.f;
+  const RowSpan<E> ys(y, V);
+  vu4* yv = reinterpret_cast<vu4*>(y + ys.head);
+  const int nvec = (int)ys.nvec;
+
+  if (gv == 0.f) {
+    // (onehot - p) * 0 == 0: write the row without reading the logits.
+    const raw z = E::from_float(0.f);
+    if (tid < ys.head) y[tid] = z;
+    if (ys.tail0 + tid < V) y[ys.tail0 + tid] = z;
+    const vu4 zq = vu4{0u, 0u, 0u, 0u};
+    for (int i = tid; i < nvec; i += NT) __builtin_nontemporal_store(zq, yv + i);
+    return;
+  }
+
+  const raw* x = logits + b * sb + r * sr;
+  const int64_t srow = b * R + r;
+  const float M = stats[2 * srow];
+  const float LS = stats[2 * srow + 1];
+  const int64_t t = target[b * tsb + r * tsr];
+  // targets outside the vocabulary slice (or past this row) carry no one-hot
+  const bool tmask = (t < vs) || (t >= ve) || (t - vs >= V);
+  const int64_t tl = tmask ? -1 : (t - vs);
+
+  const RowSpan<E> xs(x, V);
+  if (xs.head != ys.head) {
+    // Input and output rows are not co-aligned: element-wise path.
+    for (int64_t j = tid; j < V; j += NT) {
+      const float p = fast_exp2(((E::load(x + j) - M) - LS) * kLog2e);
+      const float o = (j == tl) ? (1.f - p) * gv : -p * gv;
+      y[j] = E::from_float(o);
+    }
+    return;
+  }
+  auto scalar = [&](int64_t j) {
+    const float p = fast_exp2(((E::load(x + j) - M) - LS) * kLog2e);
+    y[j] = E::from_float((j == tl) ? (1.f - p) * gv : -p * gv);
+  };
+  if (tid < ys.head) scalar(tid);
+  if (ys.tail0 + tid < V) scalar(ys.tail0 + tid);
+
+  const vu4* xv = reinterpret_cast<const vu4*>(x + xs.head);
+  // vector index holding the target (or -1)
+  const int tv = (tl >= xs.head && tl < xs.tail0) ? (int)((tl - xs.head) / VEC) : -1;
+  const int tj = (tv >= 0) ? (int)((tl - xs.head) - (int64_t)tv * VEC) : 0;
+  const float ng = -gv;
+  int i = tid;
+  for (; i + (U - 1) * NT < nvec; i += U * NT) {
+    vu4 q[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) q[u] = __builtin_nontemporal_load(xv + i + u * NT);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float w[VEC];
+      E::unpack(q[u], w);
+      float o[VEC];
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) o[k] = fast_exp2(((w[k] - M) - LS) * kLog2e) * ng;
+      if (i + u * NT == tv) {
+#pragma unroll
+        for (int k = 0; k < VEC; ++k)
+          if (k == tj) o[k] = (1.f - fast_exp2(((w[k] - M) - LS) * kLog2e)) * gv;
+      }
+      __builtin_nontemporal_store(E::pack(o), yv + i + u * NT);
+    }
+  }
+  for (; i < nvec; i += NT) {
+    float w[VEC];
+    E::unpack(xv[i], w);
+    float o[VEC];
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) o[k] = fast_exp2(((w[k] - M) - LS) * kLog2e) * ng;
+    if (i == tv) {
+#pragma unroll
+      for (int k = 0; k < VEC; ++k)
+        if (k == tj) o[k] = (1.f - fast_exp2(((w[k] - M) - LS) * kLog2e)) * gv;
+    }
+    __builtin_nontemporal_store(E::pack(o), yv + i);
+  }
+}
+
+// Waves per row: enough rows in flight to fill 256 CUs, up to 16 waves (1024
+// threads) per row when there are few rows.
+int pick_waves(int64_t rows) {
+  int w = 1;
+  while (w < 16 && rows * w < 8192) w <<= 1;
+  return w;
+}
+
+template <class E, int W>
+void launch_fwd(int64_t rows, hipStream_t st, const void* logits, int64_t R, int64_t V, int64_t sb,
+                int64_t sr, const int64_t* target, int64_t tsb, int64_t tsr, int64_t vs, int64_t ve,
+                float* out, float* stats) {
+  constexpr int U = (E::kVec == 8) ? 8 : 8;
+  hipLaunchKernelGGL((logprob_fwd_kernel<E, W, U>), dim3((unsigned)rows), dim3(64 * W), 0, st,
+                     static_cast<const typename E::raw*>(logits), R, V, sb, sr, target, tsb, tsr, vs,
+                     ve, out, stats);
+}
+
+template <class E>
+void dispatch_fwd(int w, int64_t rows, hipStream_t st, const void* logits, int64_t R, int64_t V,
+                  int64_t sb, int64_t sr, const int64_t* target, int64_t tsb, int64_t tsr,
+                  int64_t vs, int64_t ve, float* out, float* stats) {
+  switch (w) {
+    case 1: launch_fwd<E, 1>(rows, st, logits, R, V, sb, sr, target, tsb, tsr, vs, ve, out, stats); break;
+    case 2: launch_fwd<E, 2>(rows, st, logits, R, V, sb, sr, target, tsb, tsr, vs, ve, out, stats); break;
+    case 4: launch_fwd<E, 4>(rows, st, logits, R, V, sb, sr, target, tsb, tsr, vs, ve, out, stats); break;
+    case 8: launch_fwd<E, 8>(rows, st, logits, R, V, sb, sr, target, tsb, tsr, vs, ve, out, stats); break;
+    default: launch_fwd<E, 16>(rows, st, logits, R, V, sb, sr, target, tsb, tsr, vs, ve, out, stats); break;
+  }
+}
+
+template <class E, int W>
+void launch_bwd(int64_t rows, hipStream_t st, const void* logits, int64_t R, int64_t Rt, int64_t V,
+                int64_t sb, int64_t sr, const int64_t* target, int64_t tsb, int64_t tsr, int64_t vs,
+                int64_t ve, const float* stats, const float* g, int64_t gsb, int64_t gsr, void* gin,
+                int64_t gisb, int64_t gisr) {
+  constexpr int U = 4;
+  hipLaunchKernelGGL((logprob_bwd_kernel<E, W, U>), dim3((unsigned)rows), dim3(64 * W), 0, st,
+                     static_cast<const typename E::raw*>(logits), R, Rt, V, sb, sr, target, tsb, tsr,
+                     vs, ve, stats, g, gsb, gsr, static_cast<typename E::raw*>(gin), gisb, gisr);
+}
+
+template <class E>
+void dispatch_bwd(int w, int64_t rows, hipStream_t st, const void* logits, int64_t R, int64_t Rt,
+                  int64_t V, int64_t sb, int64_t sr, const int64_t* target, int64_t tsb,
+                  int64_t tsr, int64_t vs, int64_t ve, const float* stats, const float* g,
+                  int64_t gsb, int64_t gsr, void* gin, int64_t gisb, int64_t gisr) {
+#define MIRL_BWD_CASE(WW)                                                                      \
+  launch_bwd<E, WW>(rows, st, logits, R, Rt, V, sb, sr, target, tsb, tsr, vs, ve, stats, g, gsb, \
+                    gsr, gin, gisb, gisr)
+  switch (w) {
+    case 1: MIRL_BWD_CASE(1); break;
+    case 2: MIRL_BWD_CASE(2); break;
+    case 4: MIRL_BWD_CASE(4); break;
+    case 8: MIRL_BWD_CASE(8); break;
+    default: MIRL_BWD_CASE(16); break;
+  }
+#undef MIRL_BWD_CASE
+}
+
+int check_dtype(int dtype) {
+  if (dtype == MIRL_DTYPE_F32 || dtype == MIRL_DTYPE_BF16 || dtype == MIRL_DTYPE_F16) return 0;
+  set_error("unsupported logits dtype code %d (expected f32, bf16 or f16)", dtype);
+  return MIRL_ERR_UNSUPPORTED;
+}
+
+}  // namespace
+}  // namespace mirl
+
+using namespace mirl;
+
+extern "C" int mirl_logprob_fwd(const void* logits, int dtype, int64_t B, int64_t R, int64_t V,
+                                int64_t stride_b, int64_t stride_r, const int64_t* target,
+                                int64_t t_stride_b, int64_t t_stride_r, int64_t vocab_start,
+                                int64_t vocab_end, float* out, float* row_stats, void* stream) {
+  clear_error();
+  if (int e = check_dtype(dtype)) return e;
+  MIRL_REQUIRE(B >= 0 && R >= 0 && V > 0, "invalid shape B=%lld R=%lld V=%lld", (long long)B,
+               (long long)R, (long long)V);
+  MIRL_REQUIRE(V < (int64_t(1) << 31), "vocabulary size %lld exceeds 2^31-1", (long long)V);
+  const int64_t rows = B * R;
+  if (rows == 0) return MIRL_OK;
+  MIRL_REQUIRE(rows < (int64_t(1) << 31), "too many rows (%lld)", (long long)rows);
+  MIRL_REQUIRE(logits && target && out, "null pointer argument");
+  const int w = pick_waves(rows);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case MIRL_DTYPE_F32:
+      dispatch_fwd<F32>(w, rows, st, logits, R, V, stride_b, stride_r, target, t_stride_b,
+                        t_stride_r, vocab_start, vocab_end, out, row_stats);
+      break;
+    case MIRL_DTYPE_BF16:
+      dispatch_fwd<BF16>(w, rows, st, logits, R, V, stride_b, stride_r, target, t_stride_b,
+                         t_stride_r, vocab_start, vocab_end, out, row_stats);
+      break;
+    default:
+      dispatch_fwd<F16>(w, rows, st, logits, R, V, stride_b, stride_r, target, t_stride_b,
+                        t_stride_r, vocab_start, vocab_end, out, row_stats);
+      break;
+  }
+  return check_launch("mirl_logprob_fwd");
+}
+
+extern "C" int mirl_logprob_bwd(const void* logits, int dtype, int64_t B, int64_t R,
+                                int64_t R_total, int64_t V, int64_t stride_b, int64_t stride_r,
+                                const int64_t* target, int64_t t_stride_b, int64_t t_stride_r,
+                                int64_t vocab_start, int64_t vocab_end, const float* row_stats,
+                                const float* grad_out, int64_t g_stride_b, int64_t g_stride_r,
+                                void* grad_in, int64_t gi_stride_b, int64_t gi_stride_r,
+                                void* stream) {
+  clear_error();
+  if (int e = check_dtype(dtype)) return e;
+  MIRL_REQUIRE(B >= 0 && R >= 0 && R_total >= R && V > 0,
+               "invalid shape B=%lld R=%lld R_total=%lld V=%lld", (long long)B, (long long)R,
+               (long long)R_total, (long long)V);
+  MIRL_REQUIRE(V < (int64_t(1) << 31), "vocabulary size %lld exceeds 2^31-1", (long long)V);
+  const int64_t rows = B * R_total;
+  if (rows == 0) return MIRL_OK;
+  MIRL_REQUIRE(rows < (int64_t(1) << 31), "too many rows (%lld)", (long long)rows);
+  MIRL_REQUIRE(grad_in != nullptr, "null grad_in");
+  MIRL_REQUIRE(R == 0 || (logits && target && row_stats && grad_out), "null pointer argument");
+  const int w = pick_waves(rows);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case MIRL_DTYPE_F32:
+      dispatch_bwd<F32>(w, rows, st, logits, R, R_total, V, stride_b, stride_r, target,
+                        t_stride_b, t_stride_r, vocab_start, vocab_end, row_stats, grad_out,
+                        g_stride_b, g_stride_r, grad_in, gi_stride_b, gi_stride_r);
+      break;
+    case MIRL_DTYPE_BF16:
+      dispatch_bwd<BF16>(w, rows, st, logits, R, R_total, V, stride_b, stride_r, target,
+                         t_stride_b, t_stride_r, vocab_start, vocab_end, row_stats, grad_out,
+                         g_stride_b, g_stride_r, grad_in, gi_stride_b, gi_stride_r);
+      break;
+    default:
+      dispatch_bwd<F16>(w, rows, st, logits, R, R_total, V, stride_b, stride_r, target,
+                        t_stride_b, t_stride_r, vocab_start, vocab_end, row_stats, grad_out,
+                        g_stride_b, g_stride_r, grad_in, gi_stride_b, gi_stride_r);
+      break;
+  }
+  return check_launch("mirl_logprob_bwd");
+}

@@ -1,0 +1,389 @@
+"""Token log-probabilities from logits: drop-in for ``nemo_rl.distributed.model_utils``.
+
+The autograd Functions and helpers keep the reference's names, call
+signatures, tensor layouts and dtypes; the arithmetic runs in the gfx950
+kernels of ``libmirl.so``:
+
+* forward: one pass over each logits row (online log-sum-exp with the target
+  gather fused in), fp32 output, no [B, S, V] temporaries;
+* backward: one read + one write per row, ``(onehot - softmax) * g`` in the
+  logits dtype; rows whose upstream gradient is zero are written without
+  being read.
+
+Scope: the vocab-parallel group must be ``None`` or of size 1 (one GPU owns
+the whole vocabulary); larger groups raise ``NotImplementedError``.  No
+collective is ever issued.  ``chunk_size`` is validated and kept in the
+signature, but it never changes results: every row is independent.
+"""
+
+from __future__ import annotations
+
+from typing import Any, Optional
+
+import torch
+
+from rl_amd import _C
+from rl_amd.algorithms.logits_sampling_utils import (
+    TrainingSamplingParams,
+    need_top_k_or_top_p_filtering,
+)
+
+__all__ = [
+    "ChunkedDistributedLogprob",
+    "DistributedLogprob",
+    "from_parallel_logits_to_logprobs",
+    "from_parallel_logits_to_logprobs_packed_sequences",
+    "get_next_token_logprobs_from_logits",
+]
+
+
+def _group_size(group: Optional[Any]) -> int:
+    if group is None:
+        return 1
+    try:
+        return torch.distributed.get_world_size(group)
+    except (RuntimeError, ValueError):
+        return 1
+
+
+def _require_single_rank(*groups: Optional[Any]) -> None:
+    for g in groups:
+        if _group_size(g) != 1:
+            raise NotImplementedError(
+                "rl_amd computes logprobs with the whole vocabulary on one GPU; "
+                f"process groups of size {_group_size(g)} are not supported"
+            )
+
+
+def _check_logits(logits: torch.Tensor) -> torch.Tensor:
+    if logits.dim() != 3:
+        raise ValueError(f"expected logits of shape [B, S, V], got {tuple(logits.shape)}")
+    if logits.stride(-1) != 1:
+        logits = logits.contiguous()
+    return logits
+
+
+def _check_chunk_size(chunk_size: Optional[int]) -> None:
+    if chunk_size is not None and int(chunk_size) <= 0:
+        raise ValueError("logprob_chunk_size must be positive")
+
+
+class _RowLogprob(torch.autograd.Function):
+    """Selected-token logprobs of rows ``0..R-1`` of ``logits`` (R = target.shape[1]).
+
+    forward:  [B, S, V] logits, [B, R] int64 targets -> [B, R] fp32.
+    backward: [B, R] fp32 -> [B, S, V] in the logits dtype (rows >= R are zero).
+    """
+
+    @staticmethod
+    def forward(  # type: ignore[override]
+        ctx: Any,
+        logits: torch.Tensor,
+        target: torch.Tensor,
+        vocab_start_index: int,
+        vocab_end_index: int,
+        inference_only: bool,
+        reuse_logits_storage: bool,
+    ) -> torch.Tensor:
+        B, R = target.shape
+        out = torch.empty((B, R), dtype=torch.float32, device=logits.device)
+        stats = None
+        if not inference_only:
+            stats = torch.empty((B, R, 2), dtype=torch.float32, device=logits.device)
+        _C.logprob_fwd(logits, target, vocab_start_index, vocab_end_index, out, stats)
+        if not inference_only:
+            ctx.save_for_backward(logits, target, stats)
+            ctx.vocab = (int(vocab_start_index), int(vocab_end_index))
+            ctx.reuse_logits_storage = bool(reuse_logits_storage)
+        return out
+
+    @staticmethod
+    def backward(ctx: Any, *grad_outputs: torch.Tensor):  # type: ignore[override]
+        (grad_output,) = grad_outputs
+        logits, target, stats = ctx.saved_tensors
+        vs, ve = ctx.vocab
+        if grad_output.dtype != torch.float32:
+            grad_output = grad_output.float()
+        reuse = ctx.reuse_logits_storage and not logits.is_leaf
+        grad_input = logits if reuse else torch.empty_like(logits)
+        _C.logprob_bwd(logits, target, vs, ve, stats, grad_output, grad_input)
+        return grad_input, None, None, None, None, None
+
+
+class DistributedLogprob(torch.autograd.Function):
+    """Drop-in for ``DistributedLogprob`` (reference model_utils.py:138-225), group size 1.
+
+    Returns [B, S] fp32 selected-token logprobs (0 where the target lies
+    outside ``[vocab_start_index, vocab_end_index)``).  Unlike the reference it
+    saves only the logits and an 8-byte per-row statistic for backward, not an
+    fp32 softmax of the whole tensor.
+    """
+
+    @staticmethod
+    def forward(  # type: ignore[override]
+        ctx: Any,
+        vocab_parallel_logits: torch.Tensor,
+        target: torch.Tensor,
+        vocab_start_index: int,
+        vocab_end_index: int,
+        group: Optional[Any],
+        inference_only: bool = False,
+    ) -> torch.Tensor:
+        _require_single_rank(group)
+        logits = _check_logits(vocab_parallel_logits)
+        out, stats = _forward_rows(logits, target, vocab_start_index, vocab_end_index, inference_only)
+        if not inference_only:
+            ctx.save_for_backward(logits, target, stats)
+            ctx.vocab = (int(vocab_start_index), int(vocab_end_index))
+            ctx.reuse_logits_storage = False
+        return out
+
+    @staticmethod
+    def backward(ctx: Any, *grad_outputs: torch.Tensor):  # type: ignore[override]
+        grad = _backward_rows(ctx, grad_outputs[0])
+        return grad, None, None, None, None, None
+
+
+class ChunkedDistributedLogprob(torch.autograd.Function):
+    """Drop-in for ``ChunkedDistributedLogprob`` (reference model_utils.py:228-349), group size 1.
+
+    ``chunk_size`` is accepted for signature compatibility; the kernels stream
+    rows independently, so the result is identical for every chunk size.
+    ``reuse_logits_storage`` writes the gradient into the logits' own storage
+    when the logits are not a leaf, as in the reference.
+    """
+
+    @staticmethod
+    def forward(  # type: ignore[override]
+        ctx: Any,
+        vocab_parallel_logits: torch.Tensor,
+        target: torch.Tensor,
+        vocab_start_index: int,
+        vocab_end_index: int,
+        chunk_size: int,
+        tp_group: Optional[Any],
+        inference_only: bool = False,
+        reuse_logits_storage: bool = False,
+    ) -> torch.Tensor:
+        _require_single_rank(tp_group)
+        _check_chunk_size(chunk_size)
+        logits = _check_logits(vocab_parallel_logits)
+        out, stats = _forward_rows(logits, target, vocab_start_index, vocab_end_index, inference_only)
+        if not inference_only:
+            ctx.save_for_backward(logits, target, stats)
+            ctx.vocab = (int(vocab_start_index), int(vocab_end_index))
+            ctx.reuse_logits_storage = bool(reuse_logits_storage)
+        return out
+
+    @staticmethod
+    def backward(ctx: Any, *grad_outputs: torch.Tensor):  # type: ignore[override]
+        grad = _backward_rows(ctx, grad_outputs[0])
+        return grad, None, None, None, None, None, None, None
+
+
+def _forward_rows(
+    logits: torch.Tensor,
+    target: torch.Tensor,
+    vocab_start_index: int,
+    vocab_end_index: int,
+    inference_only: bool,
+) -> tuple[torch.Tensor, Optional[torch.Tensor]]:
+    B, S, _ = logits.shape
+    if tuple(target.shape) != (B, S):
+        raise ValueError(
+            f"target shape {tuple(target.shape)} does not match logits rows {(B, S)}"
+        )
+    if target.dtype != torch.int64:
+        target = target.long()
+    out = torch.empty((B, S), dtype=torch.float32, device=logits.device)
+    stats = None if inference_only else torch.empty((B, S, 2), dtype=torch.float32, device=logits.device)
+    _C.logprob_fwd(logits, target, vocab_start_index, vocab_end_index, out, stats)
+    return out, stats
+
+
+def _backward_rows(ctx: Any, grad_output: torch.Tensor) -> torch.Tensor:
+    logits, target, stats = ctx.saved_tensors
+    vs, ve = ctx.vocab
+    if target.dtype != torch.int64:
+        target = target.long()
+    if grad_output.dtype != torch.float32:
+        grad_output = grad_output.float()
+    reuse = ctx.reuse_logits_storage and not logits.is_leaf
+    grad_input = logits if reuse else torch.empty_like(logits)
+    _C.logprob_bwd(logits, target, vs, ve, stats, grad_output, grad_input)
+    return grad_input
+
+
+def _next_token_targets(target: torch.Tensor, n_logit_rows: int) -> torch.Tensor:
+    """Targets of rows 0..S_t-2: ``target[:, 1:]`` (reference rolls by -1, then drops the last)."""
+    if target.dim() != 2:
+        raise ValueError(f"expected target of shape [B, S], got {tuple(target.shape)}")
+    if target.shape[1] > n_logit_rows:
+        raise ValueError(
+            f"target length {target.shape[1]} exceeds the {n_logit_rows} logits rows"
+        )
+    if target.dtype != torch.int64:
+        target = target.long()
+    return target[:, 1:]
+
+
+def from_parallel_logits_to_logprobs(
+    vocab_parallel_logits: torch.Tensor,
+    target: torch.Tensor,
+    vocab_start_index: int,
+    vocab_end_index: int,
+    tp_group: Optional[Any],
+    inference_only: bool = False,
+    cp_group: Optional[Any] = None,
+    chunk_size: Optional[int] = None,
+    sampling_params: Optional[TrainingSamplingParams] = None,
+) -> torch.Tensor:
+    """Next-token logprobs ``[B, S-1]`` (fp32) from ``[B, S, V]`` logits and ``[B, S]`` targets.
+
+    Drop-in for reference model_utils.py:967-1062 with TP = CP = 1.  Row s of
+    the result is the logprob of ``target[:, s+1]`` under ``logits[:, s]``.
+    Only the S-1 rows that survive the reference's final ``[:, :-1]`` slice
+    are computed; the backward writes zeros for the last row.
+    """
+    _require_single_rank(tp_group, cp_group)
+    _check_chunk_size(chunk_size)
+    logits = _check_logits(vocab_parallel_logits)
+    if need_top_k_or_top_p_filtering(sampling_params):
+        from rl_amd.distributed.sampling import filtered_next_token_logprobs
+
+        return filtered_next_token_logprobs(
+            logits,
+            target,
+            sampling_params.top_k,  # type: ignore[union-attr]
+            sampling_params.top_p,  # type: ignore[union-attr]
+            inference_only=inference_only,
+        )
+    tgt = _next_token_targets(target, logits.shape[1])
+    return _RowLogprob.apply(
+        logits, tgt, vocab_start_index, vocab_end_index, inference_only, False
+    )
+
+
+def from_parallel_logits_to_logprobs_packed_sequences(
+    vocab_parallel_logits: torch.Tensor,
+    target: torch.Tensor,
+    cu_seqlens_padded: Any,
+    unpacked_seqlen: int,
+    vocab_start_index: int,
+    vocab_end_index: int,
+    group: Optional[Any],
+    inference_only: bool = False,
+    cp_group: Optional[Any] = None,
+    chunk_size: Optional[int] = None,
+    sampling_params: Optional[TrainingSamplingParams] = None,
+    target_is_pre_rolled: bool = False,
+    return_packed_layout: bool = False,
+    reuse_logits_storage: bool = False,
+) -> torch.Tensor:
+    """Logprobs of packed sequences (reference model_utils.py:1065-1231), CP = TP = 1.
+
+    ``vocab_parallel_logits`` is ``[1, T, V]``; ``cu_seqlens_padded`` holds the
+    ``B + 1`` sequence boundaries.  The per-sequence target roll and the
+    unpacking to ``[B, unpacked_seqlen - 1]`` are done with index arithmetic on
+    the device instead of a host loop over sequences.
+    """
+    _require_single_rank(group, cp_group)
+    _check_chunk_size(chunk_size)
+    logits = _check_logits(vocab_parallel_logits)
+    if logits.shape[0] != 1:
+        raise ValueError(f"packed logits must have batch 1, got {tuple(logits.shape)}")
+    bounds = [int(x) for x in cu_seqlens_padded]
+    batch_size = len(bounds) - 1
+    T = logits.shape[1]
+    dev = logits.device
+    tgt = target.reshape(1, -1)
+    if tgt.dtype != torch.int64:
+        tgt = tgt.long()
+    if not target_is_pre_rolled:
+        # rolled[p] = target[p + 1] inside each sequence; the last position of
+        # a sequence wraps to its first token.
+        starts, ends = _seq_bounds(bounds, T, dev)
+        pos = torch.arange(T, device=dev)
+        nxt = pos + 1
+        seq_id = torch.bucketize(pos, ends, right=True)
+        seq_id = seq_id.clamp(max=batch_size - 1) if batch_size > 0 else seq_id
+        last = nxt == ends[seq_id]
+        nxt = torch.where(last, starts[seq_id], nxt)
+        in_seq = pos < bounds[-1]
+        src = torch.where(in_seq, nxt, pos).clamp(max=tgt.shape[1] - 1)
+        tgt = torch.where(in_seq, tgt[0, src], torch.zeros_like(pos)).unsqueeze(0)
+    if need_top_k_or_top_p_filtering(sampling_params):
+        from rl_amd.distributed.sampling import filtered_row_logprobs
+
+        probs = filtered_row_logprobs(
+            logits, tgt, sampling_params.top_k, sampling_params.top_p,  # type: ignore[union-attr]
+            inference_only=inference_only,
+        )
+    else:
+        probs = _RowLogprob.apply(
+            logits, tgt, vocab_start_index, vocab_end_index, inference_only,
+            reuse_logits_storage and chunk_size is not None,
+        )
+    probs = probs.squeeze(0)
+    if return_packed_layout:
+        return probs[:-1].unsqueeze(0)
+    out_cols = unpacked_seqlen - 1
+    starts, ends = _seq_bounds(bounds, T, dev)
+    lens = (ends - starts - 1).clamp(min=0).clamp(max=out_cols)
+    col = torch.arange(out_cols, device=dev)
+    src = starts.unsqueeze(1) + col.unsqueeze(0)
+    valid = col.unsqueeze(0) < lens.unsqueeze(1)
+    src = torch.where(valid, src, torch.zeros_like(src))
+    gathered = probs[src.reshape(-1)].reshape(batch_size, out_cols)
+    return torch.where(valid, gathered, torch.zeros_like(gathered))
+
+
+def _seq_bounds(bounds: list[int], T: int, dev: torch.device) -> tuple[torch.Tensor, torch.Tensor]:
+    b = torch.tensor(bounds, dtype=torch.int64, device=dev)
+    return b[:-1], b[1:]
+
+
+def get_next_token_logprobs_from_logits(
+    input_ids: torch.Tensor,
+    next_token_logits: torch.Tensor,
+    vocab_parallel_rank: Optional[int] = None,
+    vocab_parallel_group: Optional[Any] = None,
+    context_parallel_group: Optional[Any] = None,
+    sampling_params: Optional[TrainingSamplingParams] = None,
+    chunk_size: Optional[int] = None,
+    cp_sharder: Optional[Any] = None,
+) -> torch.Tensor:
+    """Next-token logprobs ``[B, S-1]`` (reference model_utils.py:1624-1720).
+
+    With or without a (size-1) vocab group the same kernels run; the
+    reference's fp32 upcast of the logits is implicit (the kernels read the
+    logits dtype and accumulate in fp32), and its gradient cast back to the
+    logits dtype is what the backward writes.
+    """
+    if cp_sharder is not None:
+        raise NotImplementedError("context-parallel sharders are not supported (CP = 1)")
+    if isinstance(next_token_logits, torch.distributed.tensor.DTensor):
+        raise NotImplementedError("DTensor logits are not supported (single GPU)")
+    _require_single_rank(vocab_parallel_group, context_parallel_group)
+    if vocab_parallel_group is not None:
+        assert vocab_parallel_rank is not None, (
+            "vocab_parallel_rank must be provided when vocab_parallel_group is provided"
+        )
+    use_chunking = (
+        vocab_parallel_group is not None
+        and chunk_size is not None
+        and not need_top_k_or_top_p_filtering(sampling_params)
+    )
+    V = next_token_logits.shape[-1]
+    logprobs = from_parallel_logits_to_logprobs(
+        next_token_logits,
+        input_ids,
+        vocab_start_index=0,
+        vocab_end_index=V,
+        tp_group=None,
+        inference_only=False,
+        cp_group=None,
+        sampling_params=sampling_params,
+        chunk_size=chunk_size if use_chunking else None,
+    )
+    return logprobs[:, : input_ids.shape[1] - 1]
