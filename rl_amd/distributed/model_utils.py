@@ -338,6 +338,14 @@ def from_parallel_logits_to_logprobs_packed_sequences(
     return torch.where(valid, gathered, torch.zeros_like(gathered))
 
 
+def _is_dtensor(t: torch.Tensor) -> bool:
+    try:
+        from torch.distributed.tensor import DTensor
+    except ImportError:  # torch built without distributed
+        return False
+    return isinstance(t, DTensor)
+
+
 def _seq_bounds(bounds: list[int], T: int, dev: torch.device) -> tuple[torch.Tensor, torch.Tensor]:
     b = torch.tensor(bounds, dtype=torch.int64, device=dev)
     return b[:-1], b[1:]
@@ -362,7 +370,7 @@ def get_next_token_logprobs_from_logits(
     """
     if cp_sharder is not None:
         raise NotImplementedError("context-parallel sharders are not supported (CP = 1)")
-    if isinstance(next_token_logits, torch.distributed.tensor.DTensor):
+    if _is_dtensor(next_token_logits):
         raise NotImplementedError("DTensor logits are not supported (single GPU)")
     _require_single_rank(vocab_parallel_group, context_parallel_group)
     if vocab_parallel_group is not None:
