@@ -210,6 +210,28 @@ def _stream(dev: torch.device) -> ctypes.c_void_p:
     return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
 
 
+class _OnDevice:
+    """Make `dev` current for the duration of a launch (no-op when it already is)."""
+
+    __slots__ = ("dev", "prev")
+
+    def __init__(self, dev: torch.device):
+        self.dev = dev
+        self.prev = None
+
+    def __enter__(self):
+        cur = torch.cuda.current_device()
+        if self.dev.index is not None and cur != self.dev.index:
+            self.prev = cur
+            torch.cuda.set_device(self.dev)
+        return self
+
+    def __exit__(self, *exc):
+        if self.prev is not None:
+            torch.cuda.set_device(self.prev)
+        return False
+
+
 def _dtype_code(t: torch.Tensor) -> int:
     try:
         return DTYPE_CODES[t.dtype]
@@ -242,7 +264,7 @@ def logprob_fwd(
     V = logits.shape[-1]
     assert logits.stride(-1) == 1 and out.is_contiguous()
     assert stats is None or stats.is_contiguous()
-    with torch.cuda.device(dev), _Timed("mirl_logprob_fwd", dev):
+    with _OnDevice(dev), _Timed("mirl_logprob_fwd", dev):
         st = load().mirl_logprob_fwd(
             logits.data_ptr(), _dtype_code(logits), B, R, V, logits.stride(0), logits.stride(1),
             target.data_ptr(), target.stride(0), target.stride(1), int(vocab_start),
@@ -270,7 +292,7 @@ def logprob_bwd(
     V = logits.shape[-1]
     assert grad_in.stride(-1) == 1 and logits.stride(-1) == 1
     assert grad_in.dtype == logits.dtype and grad_out.dtype == torch.float32
-    with torch.cuda.device(dev), _Timed("mirl_logprob_bwd", dev):
+    with _OnDevice(dev), _Timed("mirl_logprob_bwd", dev):
         st = load().mirl_logprob_bwd(
             logits.data_ptr(), _dtype_code(logits), B, R, Rt, V, logits.stride(0),
             logits.stride(1), target.data_ptr(), target.stride(0), target.stride(1),
@@ -314,7 +336,7 @@ def clipped_pg(
     grad_unf = torch.empty((B, L), dtype=dtype, device=dev) if unfiltered is not None else None
     lib = load()
     ws = torch.empty(int(lib.mirl_clipped_pg_workspace_elems(B)), dtype=dtype, device=dev)
-    with torch.cuda.device(dev), _Timed("mirl_clipped_pg", dev):
+    with _OnDevice(dev), _Timed("mirl_clipped_pg", dev):
         st = lib.mirl_clipped_pg(
             ctypes.byref(cfg), _dtype_code(curr), B, L, _view(curr), _view(unfiltered),
             _view(token_mask), _view(advantages), _view(prev), _view(generation),
@@ -350,7 +372,7 @@ def grpo_advantage(
     base = torch.empty_like(adv) if want_stats else None
     std = torch.empty_like(adv) if want_stats else None
     trivial = torch.empty(B, dtype=torch.bool, device=dev) if want_stats else None
-    with torch.cuda.device(dev), _Timed("mirl_grpo_advantage", dev):
+    with _OnDevice(dev), _Timed("mirl_grpo_advantage", dev):
         st = load().mirl_grpo_advantage(
             prompts.data_ptr(), B, K, prompts.stride(0), rewards.data_ptr(), _ptr(std_rewards),
             _ptr(valid_mask),

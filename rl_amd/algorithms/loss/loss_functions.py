@@ -488,12 +488,16 @@ class _ClippedPGFunction(torch.autograd.Function):
         )
         ctx.save_for_backward(grad_curr, grad_unf)
         ctx.mark_non_differentiable(metrics)
+        # no zero-filled gradient for the metrics output on the way back
+        ctx.set_materialize_grads(False)
         loss = metrics[0].clone()
         return loss, metrics
 
     @staticmethod
     def backward(ctx: Any, grad_loss: torch.Tensor, grad_metrics: torch.Tensor):  # type: ignore[override]
         grad_curr, grad_unf = ctx.saved_tensors
+        if grad_loss is None:
+            return (None,) * 13
         gc = grad_curr * grad_loss if ctx.needs_input_grad[0] else None
         gu = grad_unf * grad_loss if (grad_unf is not None and ctx.needs_input_grad[1]) else None
         return gc, gu, None, None, None, None, None, None, None, None, None, None, None
