@@ -192,21 +192,56 @@ def _require_gpu(*tensors: Optional[torch.Tensor]) -> torch.device:
     for t in tensors:
         if t is None:
             continue
-        if not t.is_cuda:
-            raise MirlError(
-                "rl_amd kernels run on a ROCm GPU; got a tensor on "
-                f"{t.device} (move inputs to a cuda device)"
-            )
+        d = t.device
         if dev is None:
-            dev = t.device
-        elif t.device != dev:
-            raise MirlError(f"tensors on different devices: {dev} and {t.device}")
+            if d.type != "cuda":
+                raise MirlError(
+                    "rl_amd kernels run on a ROCm GPU; got a tensor on "
+                    f"{d} (move inputs to a cuda device)"
+                )
+            dev = d
+        elif d != dev:
+            raise MirlError(f"tensors on different devices: {dev} and {d}")
     if dev is None:
         raise MirlError("no device tensor given")
     return dev
 
 
+def wait_and_fetch(t: torch.Tensor) -> list:
+    """Copy a small device tensor to the host and return it as a list.
+
+    The copy goes to a cached pinned buffer and completion is awaited by
+    polling an event, which returns sooner than a blocking device-to-host
+    copy once the producing kernel finishes (the caller is about to launch
+    more GPU work, so waking up late leaves the GPU idle).
+    """
+    n = t.numel()
+    key = (t.device, t.dtype, n)
+    buf = _pinned.get(key)
+    if buf is None:
+        buf = torch.empty(n, dtype=t.dtype, pin_memory=True)
+        _pinned[key] = buf
+    buf.copy_(t.reshape(-1), non_blocking=True)
+    ev = torch.cuda.Event()
+    ev.record()
+    while not ev.query():
+        pass
+    return buf.tolist()
+
+
+_pinned: dict = {}
+
+
+try:  # raw handle of the current stream without building a Stream object
+    _raw_stream = torch._C._cuda_getCurrentRawStream  # type: ignore[attr-defined]
+except AttributeError:  # pragma: no cover - older torch
+    _raw_stream = None
+
+
 def _stream(dev: torch.device) -> ctypes.c_void_p:
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    if _raw_stream is not None:
+        return ctypes.c_void_p(_raw_stream(idx))
     return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
 
 

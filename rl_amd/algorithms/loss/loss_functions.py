@@ -457,7 +457,7 @@ class ClippedPGLossFn(LossFunction):
             curr_k, unfiltered, cfg, token_mask, advantages, prev, generation, reference,
             support, sample_mask, rewards, gvs, gvt,
         )
-        values = metrics.detach().cpu().tolist()
+        values = _C.wait_and_fetch(metrics.detach())
         out = {k: float(values[_C.PG_METRIC_SLOTS[k]]) for k in self._metric_keys()}
         return loss, out
 
