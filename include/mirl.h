@@ -93,6 +93,88 @@ int mirl_logprob_bwd(const void* logits, int dtype, int64_t B, int64_t R,
                      int64_t gi_stride_b, int64_t gi_stride_r, void* stream);
 
 /* ---------------------------------------------------------------------- */
+/* top-k / top-p / temperature-filtered logprobs                            */
+/* ---------------------------------------------------------------------- */
+
+/* Kept entries saved per row by the filtered forward for the backward. */
+#define MIRL_FILTER_KEEP_CAP 256
+
+/* Per-row result of the filtered forward.  The kept set is
+ * { j : y_j > v_cut || (y_j == v_cut && j >= i_cut) }, y = the (temperature
+ * scaled) fp32 value; m is its maximum and logsum = log(sum_kept exp(y - m)). */
+typedef struct mirl_filter_row_info {
+  float m;
+  float logsum;
+  float v_cut;
+  int32_t i_cut;
+  int32_t n_kept;
+  int32_t flags;
+} mirl_filter_row_info;
+
+/*
+ * Filtered selected-token logprobs, one row per (b, r):
+ *   y = dtype(float(x) / temperature)    (skipped when temperature == 1)
+ *   top-k (top_k > 0): keep y >= k-th largest y, every tie kept;
+ *   top-p (top_p < 1): over the kept values in ascending order, ties by
+ *     vocabulary index, keep where fp32(cumsum(softmax)) > fp32(1 - top_p)
+ *     (sums accumulated in double), always keeping the maximum;
+ *   out[b,r] = (y_t - m) - logsum when target t is kept, else -inf.
+ * Writes row_info[B*R] (mirl_filter_row_info) and, for rows with at most
+ * MIRL_FILTER_KEEP_CAP kept entries, their vocabulary indices and
+ * probabilities into kept_idx / kept_p ([B*R, MIRL_FILTER_KEEP_CAP]).
+ * `out` may be NULL (then `target` may be NULL too).
+ *
+ * Replaces: apply_top_k_top_p / _apply_top_k_top_p_fn / _apply_top_k_only_fn
+ * (nemo_rl/algorithms/logits_sampling_utils.py:69-287) followed by the fp32
+ * log_softmax and gather of DistributedLogprobWithSampling.forward
+ * (nemo_rl/distributed/model_utils.py:382-432) and of the no-group path of
+ * get_next_token_logprobs_from_logits (model_utils.py:1702-1718); the optional
+ * temperature is the in-place logits.div_ of
+ * nemo_rl/models/automodel/train.py:248-262.
+ */
+int mirl_filtered_logprob_fwd(const void* logits, int dtype, int64_t B, int64_t R,
+                              int64_t V, int64_t stride_b, int64_t stride_r,
+                              const int64_t* target, int64_t t_stride_b,
+                              int64_t t_stride_r, double temperature, int top_k,
+                              double top_p, float* out, void* row_info,
+                              int32_t* kept_idx, float* kept_p, void* stream);
+
+/*
+ * Gradient of the filtered logprobs with respect to the raw logits:
+ *   g32 = (onehot(t) - p) * g on the kept set, 0 elsewhere,
+ *   grad = dtype(dtype(g32) / temperature)   (dtype(g32) when temperature == 1).
+ * Rows r >= R (up to R_total) and rows with g == 0 are written as zeros.
+ * Rows whose kept list was saved are written without reading the logits.
+ *
+ * Replaces: DistributedLogprobWithSampling.backward and
+ * ChunkedDistributedLogprobWithSampling.backward
+ * (nemo_rl/distributed/model_utils.py:434-479, :624-688) with the autograd
+ * backward of the fp32 upcast and of logits.div_(temperature).
+ */
+int mirl_filtered_logprob_bwd(const void* logits, int dtype, int64_t B, int64_t R,
+                              int64_t R_total, int64_t V, int64_t stride_b,
+                              int64_t stride_r, const int64_t* target,
+                              int64_t t_stride_b, int64_t t_stride_r,
+                              double temperature, const void* row_info,
+                              const int32_t* kept_idx, const float* kept_p,
+                              const float* grad_out, int64_t g_stride_b,
+                              int64_t g_stride_r, void* grad_in, int64_t gi_stride_b,
+                              int64_t gi_stride_r, void* stream);
+
+/*
+ * apply_top_k_top_p on N rows of V logits: filtered[i, j] = x[i, j] where kept,
+ * -inf elsewhere (in the logits dtype), keep_mask[i, j] = kept (uint8).
+ * row_info / kept_idx / kept_p are scratch of the sizes above for N rows.
+ *
+ * Replaces: apply_top_k_top_p (nemo_rl/algorithms/logits_sampling_utils.py:256-287).
+ */
+int mirl_top_k_top_p_mask(const void* logits, int dtype, int64_t N, int64_t V,
+                          int64_t row_stride, int top_k, double top_p,
+                          void* row_info, int32_t* kept_idx, float* kept_p,
+                          void* filtered, int64_t filtered_row_stride,
+                          uint8_t* keep_mask, int64_t keep_row_stride, void* stream);
+
+/* ---------------------------------------------------------------------- */
 /* ClippedPG loss epilogue                                                  */
 /* ---------------------------------------------------------------------- */
 

@@ -1,0 +1,112 @@
+"""Top-k / top-p filtering and filtered logprobs, restated on the CPU.
+
+TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).  Follows
+nemo_rl/algorithms/logits_sampling_utils.py:69-212 (the filter),
+nemo_rl/distributed/model_utils.py:352-479 (DistributedLogprobWithSampling at
+TP=1) and nemo_rl/models/automodel/train.py:248-262 (in-place temperature).
+
+One deliberate difference: the ascending sort is stable (ties ordered by
+vocabulary index), which is what the reference's GPU sort does; CPU
+torch.sort is unstable, so the CPU reference's choice among tokens tied at
+the top-p boundary is arbitrary.  The top-k set (all ties at the k-th value
+kept) does not depend on tie order.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+
+def apply_temperature(logits: torch.Tensor, temperature: float) -> torch.Tensor:
+    """logits.div_(T) in the logits dtype (reference automodel/train.py:248-262)."""
+    if temperature == 1.0:
+        return logits.clone()
+    return logits.clone().div_(temperature)
+
+
+def top_k_only(logits: torch.Tensor, top_k: int):
+    """reference logits_sampling_utils.py:69-108: keep = x >= k-th largest (ties kept)."""
+    vals, _ = torch.topk(logits, top_k, dim=-1)
+    thr = vals[..., -1:].expand_as(logits)
+    keep = logits >= thr
+    return torch.where(keep, logits, torch.tensor(-float("inf"), dtype=logits.dtype)), keep
+
+
+def top_k_top_p(logits: torch.Tensor, top_k: Optional[int], top_p: float, chunk_size: int = 256):
+    """reference logits_sampling_utils.py:111-212 with a stable ascending sort."""
+    need_k = top_k is not None and top_k > 0
+    need_p = top_p is not None and top_p != 1.0
+    if not need_p:
+        if not need_k:
+            return logits, None
+        return top_k_only(logits, top_k)
+    shape = logits.shape
+    V = shape[-1]
+    x = logits.reshape(-1, V)
+    out = torch.empty_like(x)
+    keep = torch.empty(x.shape, dtype=torch.bool)
+    for a in range(0, x.shape[0], chunk_size):
+        b = min(a + chunk_size, x.shape[0])
+        srt, idx = x[a:b].sort(dim=-1, descending=False, stable=True)
+        kmask = None
+        if need_k:
+            thr = srt.gather(-1, torch.full(srt.shape[:-1], V - top_k, dtype=torch.long).unsqueeze(-1))
+            kmask = srt >= thr
+            srt = srt.masked_fill(~kmask, -float("inf"))
+        probs = srt.softmax(dim=-1)
+        cum = torch.cumsum(probs, dim=-1)
+        pmask = cum > 1 - top_p
+        pmask[..., -1] = True
+        srt = srt.masked_fill(~pmask, -float("inf"))
+        out[a:b] = srt.scatter(-1, idx, srt)
+        m = pmask if kmask is None else (kmask & pmask)
+        keep[a:b] = m.scatter(-1, idx, m)
+    return out.view(shape), keep.view(shape)
+
+
+def filtered_logprobs(logits: torch.Tensor, target: torch.Tensor, top_k, top_p):
+    """[B, S, V] -> [B, S] fp32: DistributedLogprobWithSampling.forward at TP=1
+    (reference model_utils.py:382-432): filter, fp32 log_softmax, gather (no target
+    masking: targets outside the kept set give -inf)."""
+    filt, keep = top_k_top_p(logits, top_k, top_p)
+    lsm = torch.log_softmax(filt.to(torch.float32), dim=-1)
+    return torch.gather(lsm, -1, target.unsqueeze(-1)).squeeze(-1), keep
+
+
+def filtered_logprobs_grad(logits: torch.Tensor, target: torch.Tensor, top_k, top_p, grad_output):
+    """DistributedLogprobWithSampling.backward at TP=1 (reference model_utils.py:434-479):
+    (onehot - softmax(filtered)) * g * keep, fp32."""
+    filt, keep = top_k_top_p(logits, top_k, top_p)
+    p = torch.softmax(filt.to(torch.float32), dim=-1)
+    onehot = torch.nn.functional.one_hot(target, num_classes=logits.shape[-1]).float()
+    g = (onehot - p) * grad_output.unsqueeze(-1).float()
+    if keep is not None:
+        g = g * keep
+    return g
+
+
+def next_token_filtered(logits_raw, input_ids, top_k, top_p, temperature=1.0, grad_output=None):
+    """The full production chain for one microbatch (reference get_next_token_logprobs_from_logits,
+    model_utils.py:1660-1718, no-group path): in-place temperature in the logits dtype, fp32
+    upcast, drop the last position, filter, log_softmax, gather input_ids[:, 1:].
+
+    Returns (logprobs [B, S-1] fp32, keep [B, S-1, V] or None, grad w.r.t. the raw logits in the
+    logits dtype or None).  The gradient chain is autograd's: masked filter, fp32 -> dtype cast,
+    then the division by T in the logits dtype.
+    """
+    x = logits_raw.clone().requires_grad_(grad_output is not None)
+    # the logits-dtype division (fp32 quotient rounded to the dtype) and its
+    # backward (the gradient divided by T in the logits dtype)
+    y = x / temperature if temperature != 1.0 else x * 1
+    yf = y.to(torch.float32)[:, :-1]
+    with torch.no_grad():
+        _, keep = top_k_top_p(yf.detach(), top_k, top_p)
+    filt = yf if keep is None else torch.where(keep, yf, torch.full_like(yf, -float("inf")))
+    lsm = torch.log_softmax(filt, dim=-1)
+    lp = lsm.gather(-1, input_ids[:, 1:].unsqueeze(-1)).squeeze(-1)
+    grad = None
+    if grad_output is not None:
+        (grad,) = torch.autograd.grad(lp, [x], grad_output)
+    return lp.detach(), keep, grad

@@ -117,7 +117,24 @@ SIGNATURES = {
         _I,
         [_P, _I64, _I64, _I64, _P, _P, _P, _I, _I, _P, _P, _P, _P, _P],
     ),
+    "mirl_filtered_logprob_fwd": (
+        _I,
+        [_P, _I, _I64, _I64, _I64, _I64, _I64, _P, _I64, _I64, ctypes.c_double, _I,
+         ctypes.c_double, _P, _P, _P, _P, _P],
+    ),
+    "mirl_filtered_logprob_bwd": (
+        _I,
+        [_P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I64, _I64, ctypes.c_double, _P, _P,
+         _P, _P, _I64, _I64, _P, _I64, _I64, _P],
+    ),
+    "mirl_top_k_top_p_mask": (
+        _I,
+        [_P, _I, _I64, _I64, _I64, _I, ctypes.c_double, _P, _P, _P, _P, _I64, _P, _I64, _P],
+    ),
 }
+
+FILTER_KEEP_CAP = 256  # MIRL_FILTER_KEEP_CAP
+FILTER_ROW_INFO_BYTES = 24  # sizeof(mirl_filter_row_info)
 
 _lib: Optional[ctypes.CDLL] = None
 _lock = threading.Lock()
@@ -416,3 +433,82 @@ def grpo_advantage(
         )
     _check(st, "mirl_grpo_advantage")
     return adv, base, std, trivial
+
+
+# ---------------------------------------------------------------------------
+# top-k / top-p filtered logprobs
+# ---------------------------------------------------------------------------
+def _filter_scratch(rows: int, dev: torch.device):
+    info = torch.empty(rows * FILTER_ROW_INFO_BYTES, dtype=torch.uint8, device=dev)
+    kidx = torch.empty((rows, FILTER_KEEP_CAP), dtype=torch.int32, device=dev)
+    kp = torch.empty((rows, FILTER_KEEP_CAP), dtype=torch.float32, device=dev)
+    return info, kidx, kp
+
+
+def filtered_fwd(
+    logits: torch.Tensor,
+    target: torch.Tensor,
+    temperature: float,
+    top_k: int,
+    top_p: float,
+    out: Optional[torch.Tensor],
+):
+    """Filtered logprobs of rows 0..R-1 (R = target.shape[1]); returns (info, kept_idx, kept_p)."""
+    dev = _require_gpu(logits, target, out)
+    B, R = target.shape
+    V = logits.shape[-1]
+    assert logits.stride(-1) == 1 and (out is None or out.is_contiguous())
+    info, kidx, kp = _filter_scratch(B * R, dev)
+    with _OnDevice(dev), _Timed("mirl_filtered_logprob_fwd", dev):
+        st = load().mirl_filtered_logprob_fwd(
+            logits.data_ptr(), _dtype_code(logits), B, R, V, logits.stride(0), logits.stride(1),
+            target.data_ptr(), target.stride(0), target.stride(1), float(temperature),
+            int(top_k), float(top_p), _ptr(out), info.data_ptr(), kidx.data_ptr(),
+            kp.data_ptr(), _stream(dev),
+        )
+    _check(st, "mirl_filtered_logprob_fwd")
+    return info, kidx, kp
+
+
+def filtered_bwd(
+    logits: torch.Tensor,
+    target: torch.Tensor,
+    temperature: float,
+    info: torch.Tensor,
+    kidx: torch.Tensor,
+    kp: torch.Tensor,
+    grad_out: torch.Tensor,
+    grad_in: torch.Tensor,
+) -> None:
+    dev = _require_gpu(logits, target, grad_out, grad_in)
+    B, R = target.shape
+    Rt = grad_in.shape[1]
+    V = logits.shape[-1]
+    assert grad_in.dtype == logits.dtype and grad_out.dtype == torch.float32
+    with _OnDevice(dev), _Timed("mirl_filtered_logprob_bwd", dev):
+        st = load().mirl_filtered_logprob_bwd(
+            logits.data_ptr(), _dtype_code(logits), B, R, Rt, V, logits.stride(0),
+            logits.stride(1), target.data_ptr(), target.stride(0), target.stride(1),
+            float(temperature), info.data_ptr(), kidx.data_ptr(), kp.data_ptr(),
+            grad_out.data_ptr(), grad_out.stride(0), grad_out.stride(1), grad_in.data_ptr(),
+            grad_in.stride(0), grad_in.stride(1), _stream(dev),
+        )
+    _check(st, "mirl_filtered_logprob_bwd")
+
+
+def top_k_top_p_mask(x2d: torch.Tensor, top_k: int, top_p: float):
+    """[N, V] rows -> (filtered [N, V] in x's dtype, keep [N, V] bool)."""
+    dev = _require_gpu(x2d)
+    N, V = x2d.shape
+    assert x2d.stride(1) == 1
+    info, kidx, kp = _filter_scratch(N, dev)
+    filt = torch.empty((N, V), dtype=x2d.dtype, device=dev)
+    keep = torch.empty((N, V), dtype=torch.bool, device=dev)
+    with _OnDevice(dev), _Timed("mirl_top_k_top_p_mask", dev):
+        st = load().mirl_top_k_top_p_mask(
+            x2d.data_ptr(), _dtype_code(x2d), N, V, x2d.stride(0), int(top_k), float(top_p),
+            info.data_ptr(), kidx.data_ptr(), kp.data_ptr(), filt.data_ptr(), filt.stride(0),
+            keep.data_ptr(), keep.stride(0), _stream(dev),
+        )
+    _check(st, "mirl_top_k_top_p_mask")
+    return filt, keep

@@ -24,6 +24,7 @@ SOURCES = [
     "logprob.hip",
     "clipped_pg.hip",
     "advantage.hip",
+    "topk_filter.hip",
 ]
 
 ARCH = "gfx950"

@@ -46,6 +46,7 @@ struct F32 {
   using raw = float;
   static constexpr int kVec = 4;  // elements per 16-byte vector
   __device__ __forceinline__ static float load(const raw* p) { return *p; }
+  __device__ __forceinline__ static float load_raw(raw r) { return r; }
   __device__ __forceinline__ static void unpack(const vu4& q, float (&v)[kVec]) {
     v[0] = __uint_as_float(q.x);
     v[1] = __uint_as_float(q.y);
@@ -68,6 +69,7 @@ struct BF16 {
     return __uint_as_float(bits16 << 16);
   }
   __device__ __forceinline__ static float load(const raw* p) { return widen(*p); }
+  __device__ __forceinline__ static float load_raw(raw r) { return widen(r); }
   __device__ __forceinline__ static void unpack(const vu4& q, float (&v)[kVec]) {
     const uint32_t w[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
@@ -95,6 +97,7 @@ struct F16 {
   using raw = _Float16;
   static constexpr int kVec = 8;
   __device__ __forceinline__ static float load(const raw* p) { return (float)*p; }
+  __device__ __forceinline__ static float load_raw(raw r) { return (float)r; }
   __device__ __forceinline__ static void unpack(const vu4& q, float (&v)[kVec]) {
     typedef _Float16 h2 __attribute__((ext_vector_type(2)));
     const uint32_t w[4] = {q.x, q.y, q.z, q.w};
@@ -119,6 +122,26 @@ struct F16 {
     return vu4{w[0], w[1], w[2], w[3]};
   }
 };
+
+// Splits a row at `p` into a scalar head (up to the next 16-byte boundary), a
+// body of aligned 16-byte vectors and a scalar tail.
+template <class E>
+struct RowSpan {
+  int64_t head, nvec, tail0;
+  __device__ __forceinline__ RowSpan(const void* p, int64_t V) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    head = (int64_t)(((16u - (a & 15u)) & 15u) / sizeof(typename E::raw));
+    if (head > V) head = V;
+    nvec = (V - head) / E::kVec;
+    tail0 = head + nvec * E::kVec;
+  }
+};
+
+// fp32 value rounded to the element type and widened back.
+template <class E>
+__device__ __forceinline__ float round_trip(float f) {
+  return E::load_raw(E::from_float(f));
+}
 
 // Wave-wide reductions (64 lanes) through cross-lane shuffles.
 __device__ __forceinline__ float wave_max(float v) {

@@ -22,20 +22,6 @@
 namespace mirl {
 namespace {
 
-template <class E>
-struct RowSpan {
-  // Splits a row at `p` into a scalar head (to reach 16-byte alignment), a
-  // body of aligned 16-byte vectors and a scalar tail.
-  int64_t head, nvec, tail0;
-  __device__ __forceinline__ RowSpan(const void* p, int64_t V) {
-    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-    head = (int64_t)(((16u - (a & 15u)) & 15u) / sizeof(typename E::raw));
-    if (head > V) head = V;
-    nvec = (V - head) / E::kVec;
-    tail0 = head + nvec * E::kVec;
-  }
-};
-
 // Per-lane log-sum-exp state kept in base-2 "offset" form: the running sum is
 // sum_i 2^(x_i*log2e - off) with off = fl(m*log2e), m the running max.
 // Four partial sums break the add dependency chain.

@@ -1,0 +1,903 @@
+// Top-k / top-p / temperature-filtered token logprobs.
+//
+// Semantics (reference nemo_rl/algorithms/logits_sampling_utils.py:69-212 and
+// nemo_rl/distributed/model_utils.py:352-479, in the production chain of
+// model_utils.py:1660-1718): y = dtype(float(x) / T) — the in-place division
+// of automodel/train.py:248-262, skipped when T == 1 — read as fp32;
+//   top-k: keep y >= the k-th largest y (every tie at the k-th value kept);
+//   top-p: over the kept-k values in ascending order with ties ordered by
+//          vocabulary index (a stable sort), p = softmax, cum = cumulative sum
+//          accumulated in double and rounded to fp32, keep cum > fp32(1 - top_p),
+//          always keep the maximum;
+//   logprob(t) = (y_t - m) - log(sum_kept exp(y - m)), -inf when t is not kept.
+// The kept set is always a suffix of that ascending order, so it is described
+// by one lexicographic cut (v_cut, i_cut): j kept <=> y_j > v_cut or
+// (y_j == v_cut and j >= i_cut).
+//
+// Forward, fast path (1 <= k <= 1024): one workgroup per row streams the row
+// once, keeping per-lane maxima and per-(lane, group-of-vectors) maxima.  The
+// k-th largest lane maximum is a lower bound tau on the k-th largest value
+// (k distinct elements are >= it), so only groups whose maximum reaches tau
+// can hold a kept element; those few groups are re-read (a few KB per row,
+// mostly from cache) and their elements >= tau collected in LDS.  A radix
+// select over the candidates gives the exact top-k cut; a stable sort of the
+// candidates gives the top-p cut and the kept-set log-sum-exp.  Rows whose
+// candidates overflow LDS are flagged and redone by the general path.
+//
+// Forward, general path (top-p without top-k, k > 1024, flagged rows): exact
+// multi-pass radix selection over the row (count histograms for the top-k
+// value, probability-mass histograms for the top-p cut), re-reading the row
+// for each 8-bit digit.
+//
+// Backward: grad = (onehot(t) - p) * g on the kept set, 0 elsewhere, rounded
+// to the logits dtype, then divided by T in that dtype (the reference's
+// autograd chain through .to(float32) and div_).  When the forward saved the
+// kept list (<= kKeepCap entries) the row is written without reading the
+// logits; otherwise the row is re-read and the cut re-applied.
+
+#include "common.h"
+
+namespace mirl {
+namespace {
+
+constexpr int kCandCap = 1024;  // candidates held in LDS by the fast path
+constexpr int kKeepCap = MIRL_FILTER_KEEP_CAP;
+constexpr int kMaxGroups = 16;  // vector groups per lane in the fast path
+constexpr int kGeneralThreads = 1024;
+
+// Per-row result of the forward (layout documented as mirl_filter_row_info).
+struct RowInfo {
+  float m;        // max of the kept values
+  float logsum;   // log(sum_kept exp(y - m))
+  float v_cut;    // kept <=> y > v_cut || (y == v_cut && j >= i_cut)
+  int32_t i_cut;
+  int32_t n_kept;
+  int32_t flags;  // bit 0: row must be (re)done by the general path
+};
+static_assert(sizeof(RowInfo) == sizeof(mirl_filter_row_info), "row info layout");
+
+__device__ __forceinline__ uint32_t okey(float y) {
+  const uint32_t u = __float_as_uint(y);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float from_okey(uint32_t k) {
+  const uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+  return __uint_as_float(u);
+}
+__device__ __forceinline__ bool kept_lex(float y, int64_t j, float vc, int32_t ic) {
+  return y > vc || (y == vc && j >= (int64_t)ic);
+}
+
+struct FilterParams {
+  const void* logits;
+  int64_t R, V, sb, sr;
+  const int64_t* target;  // [B, R] view or null
+  int64_t tsb, tsr;
+  float T;
+  int has_t;
+  int top_k;  // 0: no top-k
+  int has_p;
+  float cut;  // fp32(1 - top_p)
+  float* out;  // [rows] logprobs or null
+  RowInfo* info;
+  int32_t* kept_idx;  // [rows, kKeepCap]
+  float* kept_p;      // [rows, kKeepCap]
+};
+
+// y = dtype(float(x) / T)
+template <class E>
+__device__ __forceinline__ float scaled(float xf, const FilterParams& P) {
+  return P.has_t ? round_trip<E>(__fdiv_rn(xf, P.T)) : xf;
+}
+
+// ---------------------------------------------------------------------------
+// workgroup helpers
+// ---------------------------------------------------------------------------
+template <int NT>
+__device__ float block_sum_f(float v, float* red) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x % 64, wv = threadIdx.x / 64;
+  __syncthreads();
+  if (lane == 0) red[wv] = v;
+  __syncthreads();
+  float r = 0.f;
+  for (int k = 0; k < NT / 64; ++k) r += red[k];
+  return r;
+}
+template <int NT>
+__device__ float block_max_f(float v, float* red) {
+  v = wave_max(v);
+  const int lane = threadIdx.x % 64, wv = threadIdx.x / 64;
+  __syncthreads();
+  if (lane == 0) red[wv] = v;
+  __syncthreads();
+  float r = red[0];
+  for (int k = 1; k < NT / 64; ++k) r = fmaxf(r, red[k]);
+  return r;
+}
+template <int NT>
+__device__ int block_sum_i(int v, int* red) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  const int lane = threadIdx.x % 64, wv = threadIdx.x / 64;
+  __syncthreads();
+  if (lane == 0) red[wv] = v;
+  __syncthreads();
+  int r = 0;
+  for (int k = 0; k < NT / 64; ++k) r += red[k];
+  return r;
+}
+
+// k-th largest of n keys, by one wave: the largest c with #{key >= c} >= k.
+template <class F>
+__device__ uint32_t wave_kth_largest(F key_at, int n, int k) {
+  const int lane = threadIdx.x % 64;
+  uint32_t prefix = 0;
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t cand = prefix | (1u << bit);
+    int cnt = 0;
+    for (int i = lane; i < n; i += 64) cnt += (key_at(i) >= cand) ? 1 : 0;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) cnt += __shfl_xor(cnt, off, 64);
+    if (cnt >= k) prefix = cand;
+  }
+  return prefix;
+}
+
+// Ascending bitonic sort of n 64-bit keys in LDS (N = power of two >= n, the
+// rest padded with the maximum key) by the whole workgroup.
+template <int NT>
+__device__ void block_bitonic_sort(uint64_t* keys, int n, int N) {
+  for (int i = n + (int)threadIdx.x; i < N; i += NT) keys[i] = ~0ull;
+  __syncthreads();
+  for (int k = 2; k <= N; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = threadIdx.x; i < N; i += NT) {
+        const int ixj = i ^ j;
+        if (ixj > i) {
+          const uint64_t a = keys[i], b = keys[ixj];
+          const bool asc = (i & k) == 0;
+          if ((a > b) == asc) {
+            keys[i] = b;
+            keys[ixj] = a;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// Writes the row's results.  `skeys` holds the kept-k candidates sorted
+// ascending as (okey(y) << 32 | index); `thr` is the top-k value.
+template <class E, int NT>
+__device__ void finish_row(const FilterParams& P, int64_t row, const typename E::raw* x,
+                           const uint64_t* skeys, int n_k, float thr, float* redf,
+                           int* s_first) {
+  const int tid = threadIdx.x;
+  const float m = from_okey((uint32_t)(skeys[n_k - 1] >> 32));
+  int first = 0;
+  if (P.has_p) {
+    float zpart = 0.f;
+    for (int i = tid; i < n_k; i += NT) zpart += expf(from_okey((uint32_t)(skeys[i] >> 32)) - m);
+    const float Z = block_sum_f<NT>(zpart, redf);
+    if (tid < 64) {
+      // cumulative probability in ascending order, accumulated in double
+      double run = 0.0;
+      int found = n_k - 1;  // the maximum is always kept
+      for (int base = 0; base < n_k; base += 64) {
+        const int i = base + tid;
+        double inc = (i < n_k)
+                         ? (double)(expf(from_okey((uint32_t)(skeys[i] >> 32)) - m) / Z)
+                         : 0.0;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+          const double o = __shfl_up(inc, off, 64);
+          if (tid >= off) inc += o;
+        }
+        const bool hit = (i < n_k) && ((float)(run + inc) > P.cut);
+        const uint64_t bal = __ballot(hit);
+        if (bal != 0ull) {
+          found = base + __ffsll((long long)bal) - 1;
+          break;
+        }
+        run += __shfl(inc, 63, 64);
+      }
+      if (tid == 0) *s_first = found;
+    }
+    __syncthreads();
+    first = *s_first;
+  }
+  const uint64_t ck = skeys[first];
+  const float v_cut = P.has_p ? from_okey((uint32_t)(ck >> 32)) : thr;
+  const int32_t i_cut = P.has_p ? (int32_t)(ck & 0xffffffffu) : 0;
+  const int n_kept = n_k - first;
+  float spart = 0.f;
+  for (int i = first + tid; i < n_k; i += NT) spart += expf(from_okey((uint32_t)(skeys[i] >> 32)) - m);
+  const float s = block_sum_f<NT>(spart, redf);
+  const float logsum = logf(s);
+  if (n_kept <= kKeepCap) {
+    int32_t* ki = P.kept_idx + row * kKeepCap;
+    float* kp = P.kept_p + row * kKeepCap;
+    for (int i = first + tid; i < n_k; i += NT) {
+      const float y = from_okey((uint32_t)(skeys[i] >> 32));
+      ki[i - first] = (int32_t)(skeys[i] & 0xffffffffu);
+      kp[i - first] = expf((y - m) - logsum);
+    }
+  }
+  if (tid == 0) {
+    RowInfo ri;
+    ri.m = m;
+    ri.logsum = logsum;
+    ri.v_cut = v_cut;
+    ri.i_cut = i_cut;
+    ri.n_kept = n_kept;
+    ri.flags = 0;
+    P.info[row] = ri;
+    if (P.out != nullptr) {
+      const int64_t b = row / P.R, r = row - b * P.R;
+      const int64_t t = P.target[b * P.tsb + r * P.tsr];
+      float lp = -INFINITY;
+      if (t >= 0 && t < P.V) {
+        const float yt = scaled<E>(E::load(x + t), P);
+        if (kept_lex(yt, t, v_cut, i_cut)) lp = (yt - m) - logsum;
+      }
+      P.out[row] = lp;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// fast path
+// ---------------------------------------------------------------------------
+template <class E, int W, int U>
+__global__ __launch_bounds__(64 * W) void filter_fast_kernel(FilterParams P) {
+  using raw = typename E::raw;
+  constexpr int NT = 64 * W;
+  constexpr int VEC = E::kVec;
+  __shared__ float s_gmax[kMaxGroups * NT];
+  __shared__ float s_lmax[NT];
+  __shared__ uint64_t s_cand[kCandCap];
+  __shared__ float redf[NT / 64];
+  __shared__ int s_count, s_first;
+  __shared__ float s_tau;
+  __shared__ uint32_t s_thr;
+
+  const int64_t row = blockIdx.x;
+  const int64_t b = row / P.R, r = row - b * P.R;
+  const raw* x = static_cast<const raw*>(P.logits) + b * P.sb + r * P.sr;
+  const int tid = threadIdx.x;
+  const RowSpan<E> sp(x, P.V);
+  const vu4* xv = reinterpret_cast<const vu4*>(x + sp.head);
+  const int nvec = (int)sp.nvec;
+  // vectors of lane tid: tid + j*NT, j < J; groups of GS consecutive j
+  const int Jmax = (nvec + NT - 1) / NT;
+  const int GS = U * ((Jmax + kMaxGroups * U - 1) / (kMaxGroups * U));
+  const int G = (Jmax + GS - 1) / GS;
+  if (tid == 0) s_count = 0;
+
+  // ---- pass 1: stream the row, per-group maxima of the raw values ----------
+  float lmax = -INFINITY, cur = -INFINITY;
+  int curg = 0;
+  int j = 0;
+  for (; tid + (j + U - 1) * NT < nvec; j += U) {
+    const int g = j / GS;
+    if (g != curg) {
+      s_gmax[curg * NT + tid] = cur;
+      lmax = fmaxf(lmax, cur);
+      curg = g;
+      cur = -INFINITY;
+    }
+    vu4 q[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) q[u] = __builtin_nontemporal_load(xv + tid + (j + u) * NT);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float w[VEC];
+      E::unpack(q[u], w);
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) cur = fmaxf(cur, w[k]);
+    }
+  }
+  for (; tid + j * NT < nvec; ++j) {
+    const int g = j / GS;
+    if (g != curg) {
+      s_gmax[curg * NT + tid] = cur;
+      lmax = fmaxf(lmax, cur);
+      curg = g;
+      cur = -INFINITY;
+    }
+    float w[VEC];
+    E::unpack(xv[tid + j * NT], w);
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) cur = fmaxf(cur, w[k]);
+  }
+  s_gmax[curg * NT + tid] = cur;
+  lmax = fmaxf(lmax, cur);
+  for (int g = curg + 1; g < G; ++g) s_gmax[g * NT + tid] = -INFINITY;
+  const float hv = (tid < sp.head) ? E::load(x + tid) : -INFINITY;
+  const float tv = (sp.tail0 + tid < P.V) ? E::load(x + sp.tail0 + tid) : -INFINITY;
+  lmax = fmaxf(lmax, fmaxf(hv, tv));
+  s_lmax[tid] = lmax;
+  __syncthreads();
+
+  // ---- lower bound tau: the k-th largest lane maximum ------------------------
+  if (tid < 64) {
+    const uint32_t kk = wave_kth_largest([&](int i) { return okey(s_lmax[i]); }, NT, P.top_k);
+    if (tid == 0) s_tau = scaled<E>(from_okey(kk), P);
+  }
+  __syncthreads();
+  const float tau = s_tau;
+
+  // ---- pass 2: re-read groups that can hold candidates ------------------------
+  auto push = [&](float y, int64_t idx) {
+    const int slot = atomicAdd(&s_count, 1);
+    if (slot < kCandCap) s_cand[slot] = ((uint64_t)okey(y) << 32) | (uint64_t)(uint32_t)idx;
+  };
+  for (int g = 0; g < G; ++g) {
+    if (!(scaled<E>(s_gmax[g * NT + tid], P) >= tau)) continue;
+    for (int jj = g * GS; jj < (g + 1) * GS; ++jj) {
+      const int vi = tid + jj * NT;
+      if (vi >= nvec) break;
+      float w[VEC];
+      E::unpack(xv[vi], w);
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) {
+        const float y = scaled<E>(w[k], P);
+        if (y >= tau) push(y, sp.head + (int64_t)vi * VEC + k);
+      }
+    }
+  }
+  if (tid < sp.head) {
+    const float y = scaled<E>(hv, P);
+    if (y >= tau) push(y, tid);
+  }
+  if (sp.tail0 + tid < P.V) {
+    const float y = scaled<E>(tv, P);
+    if (y >= tau) push(y, sp.tail0 + tid);
+  }
+  __syncthreads();
+  const int C = s_count;
+  if (C > kCandCap) {
+    if (tid == 0) {
+      RowInfo ri{};
+      ri.flags = 1;
+      P.info[row] = ri;
+    }
+    return;
+  }
+
+  // ---- exact top-k value among the candidates ---------------------------------
+  if (tid < 64) {
+    const uint32_t kk =
+        wave_kth_largest([&](int i) { return (uint32_t)(s_cand[i] >> 32); }, C, P.top_k);
+    if (tid == 0) s_thr = kk;
+  }
+  int N = 1;
+  while (N < C) N <<= 1;
+  block_bitonic_sort<NT>(s_cand, C, N);  // begins and ends with a barrier
+  const uint32_t thr_key = s_thr;
+  // kept-k = the sorted suffix with key >= thr_key
+  int cnt = 0;
+  for (int i = tid; i < C; i += NT) cnt += ((uint32_t)(s_cand[i] >> 32) >= thr_key) ? 1 : 0;
+  __shared__ int redi[NT / 64];
+  const int n_k = block_sum_i<NT>(cnt, redi);
+  finish_row<E, NT>(P, row, x, s_cand + (C - n_k), n_k, from_okey(thr_key), redf, &s_first);
+}
+
+// ---------------------------------------------------------------------------
+// general path: exact multi-pass radix selection over the row
+// ---------------------------------------------------------------------------
+template <class E>
+__global__ __launch_bounds__(kGeneralThreads) void filter_general_kernel(FilterParams P,
+                                                                         int all_rows) {
+  using raw = typename E::raw;
+  constexpr int NT = kGeneralThreads;
+  __shared__ int hist_i[256];
+  __shared__ double hist_d[256];
+  __shared__ float redf[NT / 64];
+  __shared__ int redi[NT / 64];
+  __shared__ uint32_t s_sel[2];
+  __shared__ double s_below;
+  __shared__ int s_cnt;
+  __shared__ uint64_t s_cand[kKeepCap];
+
+  const int64_t row = blockIdx.x;
+  if (!all_rows && (P.info[row].flags & 1) == 0) return;
+  const int64_t b = row / P.R, r = row - b * P.R;
+  const raw* x = static_cast<const raw*>(P.logits) + b * P.sb + r * P.sr;
+  const int tid = threadIdx.x;
+  const int64_t V = P.V;
+  auto yat = [&](int64_t j) { return scaled<E>(E::load(x + j), P); };
+
+  // row maximum
+  float mx = -INFINITY;
+  for (int64_t j = tid; j < V; j += NT) mx = fmaxf(mx, yat(j));
+  const float m = block_max_f<NT>(mx, redf);
+
+  // top-k value: radix select on the 32-bit order key, 8 bits per pass
+  uint32_t thr_key = 0;
+  if (P.top_k > 0) {
+    uint32_t prefix = 0, mask = 0;
+    int remaining = P.top_k;
+    for (int d = 3; d >= 0; --d) {
+      const int shift = 8 * d;
+      for (int i = tid; i < 256; i += NT) hist_i[i] = 0;
+      __syncthreads();
+      for (int64_t j = tid; j < V; j += NT) {
+        const uint32_t k = okey(yat(j));
+        if ((k & mask) == prefix) atomicAdd(&hist_i[(k >> shift) & 255u], 1);
+      }
+      __syncthreads();
+      if (tid == 0) {
+        int acc = 0, bsel = 0;
+        for (int bin = 255; bin >= 0; --bin) {
+          if (acc + hist_i[bin] >= remaining) {
+            bsel = bin;
+            break;
+          }
+          acc += hist_i[bin];
+        }
+        s_sel[0] = (uint32_t)bsel;
+        s_sel[1] = (uint32_t)(remaining - acc);
+      }
+      __syncthreads();
+      prefix |= s_sel[0] << shift;
+      mask |= 255u << shift;
+      remaining = (int)s_sel[1];
+      __syncthreads();
+    }
+    thr_key = prefix;
+  }
+
+  // top-p cut: the smallest (key, index) whose cumulative probability > cut
+  float v_cut = from_okey(thr_key);
+  int32_t i_cut = 0;
+  if (P.has_p) {
+    float zp = 0.f;
+    for (int64_t j = tid; j < V; j += NT) {
+      const float y = yat(j);
+      if (okey(y) >= thr_key) zp += expf(y - m);
+    }
+    const float Z = block_sum_f<NT>(zp, redf);
+    if (tid == 0) s_below = 0.0;
+    uint32_t prefix = 0, mask = 0;
+    bool done = false;
+    // value digits, then index digits among the elements tied at the value
+    for (int phase = 0; phase < 2 && !done; ++phase) {
+      int top_bit = 31;
+      if (phase == 1) {
+        top_bit = 0;
+        while ((int64_t(1) << (top_bit + 1)) < V) ++top_bit;
+      }
+      uint32_t iprefix = 0, imask = 0;
+      for (int hi = top_bit; hi >= 0; hi -= 8) {
+        const int lo = hi >= 7 ? hi - 7 : 0;
+        const int shift = lo;
+        const int nb = hi - lo + 1;
+        const uint32_t dmask = (nb >= 32) ? 0xffffffffu : ((1u << nb) - 1u);
+        for (int i = tid; i < 256; i += NT) hist_d[i] = 0.0;
+        __syncthreads();
+        for (int64_t j = tid; j < V; j += NT) {
+          const float y = yat(j);
+          const uint32_t k = okey(y);
+          if (k < thr_key) continue;
+          uint32_t digit;
+          if (phase == 0) {
+            if ((k & mask) != prefix) continue;
+            digit = (k >> shift) & dmask;
+          } else {
+            if (k != prefix) continue;
+            const uint32_t jj = (uint32_t)j;
+            if ((jj & imask) != iprefix) continue;
+            digit = (jj >> shift) & dmask;
+          }
+          atomicAdd(&hist_d[digit], (double)(expf(y - m) / Z));
+        }
+        __syncthreads();
+        if (tid == 0) {
+          double below = s_below;
+          int bsel = -1, last_nonempty = -1;
+          for (int bin = 0; bin <= (int)dmask; ++bin) {
+            if (hist_d[bin] == 0.0) continue;
+            last_nonempty = bin;
+            if ((float)(below + hist_d[bin]) > P.cut) {
+              bsel = bin;
+              break;
+            }
+            below += hist_d[bin];
+          }
+          if (bsel < 0) {
+            // no cumulative value exceeds the cut: only the maximum is kept
+            bsel = last_nonempty;
+            below -= hist_d[bsel];
+          }
+          s_below = below;
+          s_sel[0] = (uint32_t)bsel;
+        }
+        __syncthreads();
+        if (phase == 0) {
+          prefix |= s_sel[0] << shift;
+          mask |= dmask << shift;
+        } else {
+          iprefix |= s_sel[0] << shift;
+          imask |= dmask << shift;
+        }
+        __syncthreads();
+      }
+      if (phase == 1) i_cut = (int32_t)iprefix;
+    }
+    v_cut = from_okey(prefix);
+  }
+
+  // kept-set log-sum-exp, count and (small) kept list
+  if (tid == 0) s_cnt = 0;
+  __syncthreads();
+  float sp = 0.f;
+  int cnt = 0;
+  for (int64_t j = tid; j < V; j += NT) {
+    const float y = yat(j);
+    if (!kept_lex(y, j, v_cut, i_cut)) continue;
+    sp += expf(y - m);
+    ++cnt;
+    const int slot = atomicAdd(&s_cnt, 1);
+    if (slot < kKeepCap) s_cand[slot] = ((uint64_t)okey(y) << 32) | (uint64_t)(uint32_t)j;
+  }
+  const float s = block_sum_f<NT>(sp, redf);
+  const int n_kept = block_sum_i<NT>(cnt, redi);
+  const float logsum = logf(s);
+  if (n_kept <= kKeepCap) {
+    int32_t* ki = P.kept_idx + row * kKeepCap;
+    float* kp = P.kept_p + row * kKeepCap;
+    for (int i = tid; i < n_kept; i += NT) {
+      const float y = from_okey((uint32_t)(s_cand[i] >> 32));
+      ki[i] = (int32_t)(s_cand[i] & 0xffffffffu);
+      kp[i] = expf((y - m) - logsum);
+    }
+  }
+  if (tid == 0) {
+    RowInfo ri;
+    ri.m = m;
+    ri.logsum = logsum;
+    ri.v_cut = v_cut;
+    ri.i_cut = i_cut;
+    ri.n_kept = n_kept;
+    ri.flags = 0;
+    P.info[row] = ri;
+    if (P.out != nullptr) {
+      const int64_t t = P.target[b * P.tsb + r * P.tsr];
+      float lp = -INFINITY;
+      if (t >= 0 && t < V) {
+        const float yt = yat(t);
+        if (kept_lex(yt, t, v_cut, i_cut)) lp = (yt - m) - logsum;
+      }
+      P.out[row] = lp;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// backward
+// ---------------------------------------------------------------------------
+struct FilterBwdParams {
+  const void* logits;
+  int64_t R, Rt, V, sb, sr;
+  const int64_t* target;
+  int64_t tsb, tsr;
+  float T;
+  int has_t;
+  const RowInfo* info;
+  const int32_t* kept_idx;
+  const float* kept_p;
+  const float* g;
+  int64_t gsb, gsr;
+  void* gin;
+  int64_t gisb, gisr;
+};
+
+template <class E>
+__device__ __forceinline__ typename E::raw grad_to_dtype(float g32, const FilterBwdParams& P) {
+  if (!P.has_t) return E::from_float(g32);
+  // dtype(g) then / T in the dtype: round, divide in fp32, round again
+  return E::from_float(__fdiv_rn(round_trip<E>(g32), P.T));
+}
+
+template <class E, int W>
+__global__ __launch_bounds__(64 * W) void filter_bwd_kernel(FilterBwdParams P) {
+  using raw = typename E::raw;
+  constexpr int NT = 64 * W;
+  constexpr int VEC = E::kVec;
+  __shared__ int32_t s_idx[kKeepCap];
+  __shared__ float s_p[kKeepCap];
+  __shared__ uint32_t s_bits[2048];  // one bit per output vector (V <= 2^16 * VEC)
+
+  const int64_t row = blockIdx.x;
+  const int64_t b = row / P.Rt, r = row - b * P.Rt;
+  const int tid = threadIdx.x;
+  raw* y = static_cast<raw*>(P.gin) + b * P.gisb + r * P.gisr;
+  const float gv = (r < P.R) ? P.g[b * P.gsb + r * P.gsr] : 0.f;
+  const RowSpan<E> ys(y, P.V);
+  vu4* yv = reinterpret_cast<vu4*>(y + ys.head);
+  const int nvec = (int)ys.nvec;
+  const raw zr = E::from_float(0.f);
+  const vu4 zq = vu4{0u, 0u, 0u, 0u};
+
+  if (gv == 0.f) {
+    if (tid < ys.head) y[tid] = zr;
+    if (ys.tail0 + tid < P.V) y[ys.tail0 + tid] = zr;
+    for (int i = tid; i < nvec; i += NT) __builtin_nontemporal_store(zq, yv + i);
+    return;
+  }
+  const int64_t srow = b * P.R + r;
+  const RowInfo ri = P.info[srow];
+  const int64_t t = P.target[b * P.tsb + r * P.tsr];
+  const int nbits_words = (nvec + 31) / 32;
+
+  if (ri.n_kept <= kKeepCap && nbits_words <= 2048) {
+    // kept list -> LDS, mark output vectors that hold a kept element
+    for (int i = tid; i < ri.n_kept; i += NT) {
+      s_idx[i] = P.kept_idx[srow * kKeepCap + i];
+      s_p[i] = P.kept_p[srow * kKeepCap + i];
+    }
+    for (int i = tid; i < nbits_words; i += NT) s_bits[i] = 0u;
+    __syncthreads();
+    for (int i = tid; i < ri.n_kept; i += NT) {
+      const int64_t j = s_idx[i];
+      if (j >= ys.head && j < ys.tail0) {
+        const int v = (int)((j - ys.head) / VEC);
+        atomicOr(&s_bits[v >> 5], 1u << (v & 31));
+      }
+    }
+    __syncthreads();
+    auto value_at = [&](int64_t j) -> raw {
+      for (int i = 0; i < ri.n_kept; ++i)
+        if (s_idx[i] == j) return grad_to_dtype<E>(((j == t) ? 1.f - s_p[i] : -s_p[i]) * gv, P);
+      return zr;
+    };
+    for (int i = tid; i < nvec; i += NT)
+      if (!(s_bits[i >> 5] & (1u << (i & 31)))) __builtin_nontemporal_store(zq, yv + i);
+    if (tid < ys.head) y[tid] = value_at(tid);
+    if (ys.tail0 + tid < P.V) y[ys.tail0 + tid] = value_at(ys.tail0 + tid);
+    // vectors holding kept elements: written whole by the lane of their
+    // lowest-index kept element
+    for (int i = tid; i < ri.n_kept; i += NT) {
+      const int64_t j = s_idx[i];
+      if (j < ys.head || j >= ys.tail0) continue;
+      const int v = (int)((j - ys.head) / VEC);
+      bool owner = true;
+      for (int q = 0; q < ri.n_kept; ++q) {
+        const int64_t jq = s_idx[q];
+        if (jq < j && jq >= ys.head && jq < ys.tail0 && (int)((jq - ys.head) / VEC) == v) {
+          owner = false;
+          break;
+        }
+      }
+      if (!owner) continue;
+      raw vals[VEC];
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) vals[k] = value_at(ys.head + (int64_t)v * VEC + k);
+      vu4 out;
+      __builtin_memcpy(&out, vals, sizeof(out));
+      yv[v] = out;
+    }
+    return;
+  }
+
+  // recompute path: re-read the row and re-apply the cut
+  const raw* x = static_cast<const raw*>(P.logits) + b * P.sb + r * P.sr;
+  for (int64_t j = tid; j < P.V; j += NT) {
+    const float yy = P.has_t ? round_trip<E>(__fdiv_rn(E::load(x + j), P.T)) : E::load(x + j);
+    float g32 = 0.f;
+    if (kept_lex(yy, j, ri.v_cut, ri.i_cut)) {
+      const float p = expf((yy - ri.m) - ri.logsum);
+      g32 = ((j == t) ? 1.f - p : -p) * gv;
+    }
+    y[j] = grad_to_dtype<E>(g32, P);
+  }
+}
+
+// filtered logits (-inf outside the kept set) and the keep mask
+template <class E, int W>
+__global__ __launch_bounds__(64 * W) void filter_mask_kernel(FilterParams P, void* filtered,
+                                                             uint8_t* keep, int64_t fsr,
+                                                             int64_t ksr) {
+  using raw = typename E::raw;
+  constexpr int NT = 64 * W;
+  const int64_t row = blockIdx.x;
+  const raw* x = static_cast<const raw*>(P.logits) + row * P.sr;
+  raw* f = static_cast<raw*>(filtered) + row * fsr;
+  uint8_t* kk = keep + row * ksr;
+  const RowInfo ri = P.info[row];
+  const raw ninf = E::from_float(-INFINITY);
+  for (int64_t j = threadIdx.x; j < P.V; j += NT) {
+    const raw xr = x[j];
+    const bool k = kept_lex(E::load_raw(xr), j, ri.v_cut, ri.i_cut);
+    f[j] = k ? xr : ninf;
+    kk[j] = k ? 1 : 0;
+  }
+}
+
+int fast_waves(int top_k) {
+  int w = 4;
+  while (w < 16 && 64 * w < top_k) w <<= 1;
+  return w;
+}
+
+template <class E>
+int launch_fwd(const FilterParams& P, int64_t rows, hipStream_t st) {
+  const bool fast = P.top_k >= 1 && P.top_k <= 1024 && P.top_k <= P.V;
+  if (fast) {
+    switch (fast_waves(P.top_k)) {
+      case 4:
+        hipLaunchKernelGGL((filter_fast_kernel<E, 4, 8>), dim3((unsigned)rows), dim3(256), 0, st, P);
+        break;
+      case 8:
+        hipLaunchKernelGGL((filter_fast_kernel<E, 8, 8>), dim3((unsigned)rows), dim3(512), 0, st, P);
+        break;
+      default:
+        hipLaunchKernelGGL((filter_fast_kernel<E, 16, 4>), dim3((unsigned)rows), dim3(1024), 0, st, P);
+        break;
+    }
+    if (int e = check_launch("filter_fast_kernel")) return e;
+  }
+  hipLaunchKernelGGL((filter_general_kernel<E>), dim3((unsigned)rows), dim3(kGeneralThreads), 0, st,
+                     P, fast ? 0 : 1);
+  return check_launch("filter_general_kernel");
+}
+
+int check_filter_args(int dtype, int64_t B, int64_t R, int64_t V, int top_k, double top_p,
+                      double temperature) {
+  if (dtype != MIRL_DTYPE_F32 && dtype != MIRL_DTYPE_BF16 && dtype != MIRL_DTYPE_F16) {
+    set_error("unsupported logits dtype code %d", dtype);
+    return MIRL_ERR_UNSUPPORTED;
+  }
+  MIRL_REQUIRE(B >= 0 && R >= 0 && V > 0, "invalid shape B=%lld R=%lld V=%lld", (long long)B,
+               (long long)R, (long long)V);
+  MIRL_REQUIRE(V < (int64_t(1) << 31), "vocabulary size %lld exceeds 2^31-1", (long long)V);
+  MIRL_REQUIRE(top_k <= V, "selected index k out of range (top_k=%d, vocabulary %lld)", top_k,
+               (long long)V);
+  MIRL_REQUIRE(top_k > 0 || (top_p > 0.0 && top_p < 1.0),
+               "no filtering requested (top_k=%d, top_p=%g)", top_k, top_p);
+  MIRL_REQUIRE(top_p > 0.0 && top_p <= 1.0, "top_p must be in (0, 1], got %g", top_p);
+  MIRL_REQUIRE(temperature > 0.0, "temperature must be positive, got %g", temperature);
+  return MIRL_OK;
+}
+
+FilterParams make_params(const void* logits, int64_t R, int64_t V, int64_t sb, int64_t sr,
+                         const int64_t* target, int64_t tsb, int64_t tsr, double temperature,
+                         int top_k, double top_p, float* out, void* info, int32_t* kept_idx,
+                         float* kept_p) {
+  FilterParams P;
+  P.logits = logits;
+  P.R = R;
+  P.V = V;
+  P.sb = sb;
+  P.sr = sr;
+  P.target = target;
+  P.tsb = tsb;
+  P.tsr = tsr;
+  P.T = (float)temperature;
+  P.has_t = temperature != 1.0;
+  P.top_k = top_k > 0 ? top_k : 0;
+  P.has_p = top_p < 1.0;
+  P.cut = (float)(1.0 - top_p);
+  P.out = out;
+  P.info = static_cast<RowInfo*>(info);
+  P.kept_idx = kept_idx;
+  P.kept_p = kept_p;
+  return P;
+}
+
+}  // namespace
+}  // namespace mirl
+
+using namespace mirl;
+
+extern "C" int mirl_filtered_logprob_fwd(const void* logits, int dtype, int64_t B, int64_t R,
+                                         int64_t V, int64_t stride_b, int64_t stride_r,
+                                         const int64_t* target, int64_t t_stride_b,
+                                         int64_t t_stride_r, double temperature, int top_k,
+                                         double top_p, float* out, void* row_info,
+                                         int32_t* kept_idx, float* kept_p, void* stream) {
+  clear_error();
+  if (int e = check_filter_args(dtype, B, R, V, top_k, top_p, temperature)) return e;
+  const int64_t rows = B * R;
+  if (rows == 0) return MIRL_OK;
+  MIRL_REQUIRE(rows < (int64_t(1) << 31), "too many rows (%lld)", (long long)rows);
+  MIRL_REQUIRE(logits && row_info && kept_idx && kept_p, "null pointer argument");
+  MIRL_REQUIRE(out == nullptr || target != nullptr, "out given without target");
+  const FilterParams P = make_params(logits, R, V, stride_b, stride_r, target, t_stride_b,
+                                     t_stride_r, temperature, top_k, top_p, out, row_info,
+                                     kept_idx, kept_p);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == MIRL_DTYPE_F32) return launch_fwd<F32>(P, rows, st);
+  if (dtype == MIRL_DTYPE_BF16) return launch_fwd<BF16>(P, rows, st);
+  return launch_fwd<F16>(P, rows, st);
+}
+
+extern "C" int mirl_filtered_logprob_bwd(const void* logits, int dtype, int64_t B, int64_t R,
+                                         int64_t R_total, int64_t V, int64_t stride_b,
+                                         int64_t stride_r, const int64_t* target,
+                                         int64_t t_stride_b, int64_t t_stride_r,
+                                         double temperature, const void* row_info,
+                                         const int32_t* kept_idx, const float* kept_p,
+                                         const float* grad_out, int64_t g_stride_b,
+                                         int64_t g_stride_r, void* grad_in, int64_t gi_stride_b,
+                                         int64_t gi_stride_r, void* stream) {
+  clear_error();
+  if (dtype != MIRL_DTYPE_F32 && dtype != MIRL_DTYPE_BF16 && dtype != MIRL_DTYPE_F16) {
+    set_error("unsupported logits dtype code %d", dtype);
+    return MIRL_ERR_UNSUPPORTED;
+  }
+  MIRL_REQUIRE(B >= 0 && R >= 0 && R_total >= R && V > 0, "invalid shape");
+  MIRL_REQUIRE(temperature > 0.0, "temperature must be positive");
+  const int64_t rows = B * R_total;
+  if (rows == 0) return MIRL_OK;
+  MIRL_REQUIRE(rows < (int64_t(1) << 31), "too many rows (%lld)", (long long)rows);
+  MIRL_REQUIRE(grad_in != nullptr, "null grad_in");
+  MIRL_REQUIRE(R == 0 || (logits && target && row_info && kept_idx && kept_p && grad_out),
+               "null pointer argument");
+  FilterBwdParams P;
+  P.logits = logits;
+  P.R = R;
+  P.Rt = R_total;
+  P.V = V;
+  P.sb = stride_b;
+  P.sr = stride_r;
+  P.target = target;
+  P.tsb = t_stride_b;
+  P.tsr = t_stride_r;
+  P.T = (float)temperature;
+  P.has_t = temperature != 1.0;
+  P.info = static_cast<const RowInfo*>(row_info);
+  P.kept_idx = kept_idx;
+  P.kept_p = kept_p;
+  P.g = grad_out;
+  P.gsb = g_stride_b;
+  P.gsr = g_stride_r;
+  P.gin = grad_in;
+  P.gisb = gi_stride_b;
+  P.gisr = gi_stride_r;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == MIRL_DTYPE_F32)
+    hipLaunchKernelGGL((filter_bwd_kernel<F32, 16>), dim3((unsigned)rows), dim3(1024), 0, st, P);
+  else if (dtype == MIRL_DTYPE_BF16)
+    hipLaunchKernelGGL((filter_bwd_kernel<BF16, 16>), dim3((unsigned)rows), dim3(1024), 0, st, P);
+  else
+    hipLaunchKernelGGL((filter_bwd_kernel<F16, 16>), dim3((unsigned)rows), dim3(1024), 0, st, P);
+  return check_launch("mirl_filtered_logprob_bwd");
+}
+
+extern "C" int mirl_top_k_top_p_mask(const void* logits, int dtype, int64_t N, int64_t V,
+                                     int64_t row_stride, int top_k, double top_p,
+                                     void* row_info, int32_t* kept_idx, float* kept_p,
+                                     void* filtered, int64_t filtered_row_stride,
+                                     uint8_t* keep_mask, int64_t keep_row_stride, void* stream) {
+  clear_error();
+  if (int e = check_filter_args(dtype, N, 1, V, top_k, top_p, 1.0)) return e;
+  if (N == 0) return MIRL_OK;
+  MIRL_REQUIRE(N < (int64_t(1) << 31), "too many rows (%lld)", (long long)N);
+  MIRL_REQUIRE(logits && row_info && kept_idx && kept_p && filtered && keep_mask,
+               "null pointer argument");
+  // rows are [N, V] with row stride `row_stride`: R = 1 so that row = b
+  const FilterParams P = make_params(logits, 1, V, row_stride, 0, nullptr, 0, 0, 1.0, top_k,
+                                     top_p, nullptr, row_info, kept_idx, kept_p);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  int e;
+  if (dtype == MIRL_DTYPE_F32) e = launch_fwd<F32>(P, N, st);
+  else if (dtype == MIRL_DTYPE_BF16) e = launch_fwd<BF16>(P, N, st);
+  else e = launch_fwd<F16>(P, N, st);
+  if (e) return e;
+  FilterParams Q = P;
+  Q.sr = row_stride;  // filter_mask_kernel indexes rows by row * sr
+  if (dtype == MIRL_DTYPE_F32)
+    hipLaunchKernelGGL((filter_mask_kernel<F32, 4>), dim3((unsigned)N), dim3(256), 0, st, Q,
+                       filtered, keep_mask, filtered_row_stride, keep_row_stride);
+  else if (dtype == MIRL_DTYPE_BF16)
+    hipLaunchKernelGGL((filter_mask_kernel<BF16, 4>), dim3((unsigned)N), dim3(256), 0, st, Q,
+                       filtered, keep_mask, filtered_row_stride, keep_row_stride);
+  else
+    hipLaunchKernelGGL((filter_mask_kernel<F16, 4>), dim3((unsigned)N), dim3(256), 0, st, Q,
+                       filtered, keep_mask, filtered_row_stride, keep_row_stride);
+  return check_launch("mirl_top_k_top_p_mask");
+}

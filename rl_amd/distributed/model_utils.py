@@ -30,11 +30,22 @@ from rl_amd.algorithms.logits_sampling_utils import (
 
 __all__ = [
     "ChunkedDistributedLogprob",
+    "ChunkedDistributedLogprobWithSampling",
     "DistributedLogprob",
+    "DistributedLogprobWithSampling",
     "from_parallel_logits_to_logprobs",
     "from_parallel_logits_to_logprobs_packed_sequences",
     "get_next_token_logprobs_from_logits",
 ]
+
+
+def __getattr__(name: str):
+    # the filtered autograd Functions live with the filter kernels' bindings
+    if name in ("DistributedLogprobWithSampling", "ChunkedDistributedLogprobWithSampling"):
+        from rl_amd.distributed import sampling
+
+        return getattr(sampling, name)
+    raise AttributeError(name)
 
 
 def _group_size(group: Optional[Any]) -> int:

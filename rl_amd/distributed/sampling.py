@@ -1,0 +1,237 @@
+"""Top-k / top-p / temperature-filtered token logprobs on the gfx950 filter kernels.
+
+Autograd Functions and helpers behind the filtered branches of
+``rl_amd.distributed.model_utils`` and ``rl_amd.algorithms.logits_sampling_utils``:
+
+* forward: one streaming read of each logits row finds the exact top-k cut,
+  the stable-order top-p cut and the kept-set log-sum-exp; the kept entries
+  (indices and probabilities) of each row are saved for the backward;
+* backward: the gradient row is written without reading the logits:
+  ``(onehot - p) * g`` on the kept entries, zero elsewhere, rounded to the
+  logits dtype and, when a temperature was fused, divided by it in that dtype.
+
+``top_k`` follows the reference convention (None or <= 0 disables it) and so
+does ``top_p`` (1.0 disables it).  The temperature argument is an extension:
+the reference applies ``logits.div_(T)`` before calling these functions; passing
+``temperature=T`` here instead computes the same values and gradients without
+the extra pass over the logits.
+"""
+
+from __future__ import annotations
+
+from typing import Any, Optional
+
+import torch
+
+from rl_amd import _C
+
+
+def _k(top_k: Optional[int]) -> int:
+    return int(top_k) if top_k is not None and top_k > 0 else 0
+
+
+def _p(top_p: Optional[float]) -> float:
+    return 1.0 if top_p is None else float(top_p)
+
+
+def _enabled(top_k: Optional[int], top_p: Optional[float]) -> bool:
+    return _k(top_k) > 0 or _p(top_p) != 1.0
+
+
+class _FilteredRowLogprob(torch.autograd.Function):
+    """Filtered logprobs of rows ``0..R-1`` of ``logits`` [B, S, V] for targets [B, R]."""
+
+    @staticmethod
+    def forward(  # type: ignore[override]
+        ctx: Any,
+        logits: torch.Tensor,
+        target: torch.Tensor,
+        top_k: int,
+        top_p: float,
+        temperature: float,
+        inference_only: bool,
+    ) -> torch.Tensor:
+        B, R = target.shape
+        out = torch.empty((B, R), dtype=torch.float32, device=logits.device)
+        info, kidx, kp = _C.filtered_fwd(logits, target, temperature, top_k, top_p, out)
+        if not inference_only:
+            ctx.save_for_backward(logits, target, info, kidx, kp)
+            ctx.temperature = float(temperature)
+        return out
+
+    @staticmethod
+    def backward(ctx: Any, *grad_outputs: torch.Tensor):  # type: ignore[override]
+        (g,) = grad_outputs
+        logits, target, info, kidx, kp = ctx.saved_tensors
+        if g.dtype != torch.float32:
+            g = g.float()
+        grad = torch.empty_like(logits)
+        _C.filtered_bwd(logits, target, ctx.temperature, info, kidx, kp, g, grad)
+        return grad, None, None, None, None, None
+
+
+def _check_logits(logits: torch.Tensor) -> torch.Tensor:
+    if logits.dim() != 3:
+        raise ValueError(f"expected logits of shape [B, S, V], got {tuple(logits.shape)}")
+    return logits if logits.stride(-1) == 1 else logits.contiguous()
+
+
+def filtered_row_logprobs(
+    logits: torch.Tensor,
+    target: torch.Tensor,
+    top_k: Optional[int],
+    top_p: Optional[float],
+    inference_only: bool = False,
+    temperature: float = 1.0,
+) -> torch.Tensor:
+    """[B, S, V] logits and [B, R <= S] targets -> [B, R] fp32 filtered logprobs of rows 0..R-1.
+
+    With filtering disabled this is the plain (unfiltered) selected-token logprob.
+    """
+    logits = _check_logits(logits)
+    if target.dtype != torch.int64:
+        target = target.long()
+    if not _enabled(top_k, top_p):
+        if temperature != 1.0:
+            raise ValueError("a fused temperature needs top-k or top-p filtering")
+        from rl_amd.distributed.model_utils import _RowLogprob
+
+        return _RowLogprob.apply(logits, target, 0, logits.shape[-1], inference_only, False)
+    return _FilteredRowLogprob.apply(
+        logits, target, _k(top_k), _p(top_p), float(temperature), inference_only
+    )
+
+
+def filtered_next_token_logprobs(
+    logits: torch.Tensor,
+    input_ids: torch.Tensor,
+    top_k: Optional[int],
+    top_p: Optional[float],
+    inference_only: bool = False,
+    temperature: float = 1.0,
+) -> torch.Tensor:
+    """Next-token filtered logprobs ``[B, S-1]``: row s against ``input_ids[:, s+1]``."""
+    if input_ids.dim() != 2:
+        raise ValueError(f"expected input_ids of shape [B, S], got {tuple(input_ids.shape)}")
+    if input_ids.shape[1] > logits.shape[1]:
+        raise ValueError(
+            f"target length {input_ids.shape[1]} exceeds the {logits.shape[1]} logits rows"
+        )
+    ids = input_ids if input_ids.dtype == torch.int64 else input_ids.long()
+    return filtered_row_logprobs(logits, ids[:, 1:], top_k, top_p, inference_only, temperature)
+
+
+class _ApplyTopKTopP(torch.autograd.Function):
+    """(filtered logits, keep mask); the gradient is zero outside the kept set."""
+
+    @staticmethod
+    def forward(ctx: Any, logits: torch.Tensor, top_k: int, top_p: float):  # type: ignore[override]
+        shape = logits.shape
+        x2d = logits.reshape(-1, shape[-1])
+        if x2d.stride(-1) != 1:
+            x2d = x2d.contiguous()
+        filt, keep = _C.top_k_top_p_mask(x2d, top_k, top_p)
+        keep = keep.view(shape)
+        ctx.save_for_backward(keep)
+        ctx.mark_non_differentiable(keep)
+        return filt.view(shape), keep
+
+    @staticmethod
+    def backward(ctx: Any, grad_filtered: torch.Tensor, grad_keep: Optional[torch.Tensor]):  # type: ignore[override]
+        (keep,) = ctx.saved_tensors
+        return grad_filtered.masked_fill(~keep, 0.0), None, None
+
+
+def apply_top_k_top_p_kernel(logits: torch.Tensor, top_k: Optional[int], top_p: Optional[float]):
+    """apply_top_k_top_p on the filter kernel (filtering requested)."""
+    return _ApplyTopKTopP.apply(logits, _k(top_k), _p(top_p))
+
+
+class DistributedLogprobWithSampling(torch.autograd.Function):
+    """Drop-in for ``DistributedLogprobWithSampling`` (reference model_utils.py:352-479), group size 1.
+
+    ``[B, S, V]`` logits and already-shifted ``[B, S]`` targets give ``[B, S]``
+    fp32 filtered logprobs (``-inf`` for targets outside the kept set).
+    """
+
+    @staticmethod
+    def forward(  # type: ignore[override]
+        ctx: Any,
+        vocab_parallel_logits: torch.Tensor,
+        target: torch.Tensor,
+        tp_group: Optional[Any],
+        top_k: Optional[int],
+        top_p: float,
+        inference_only: bool = False,
+    ) -> torch.Tensor:
+        from rl_amd.distributed.model_utils import _require_single_rank
+
+        _require_single_rank(tp_group)
+        return _run_filtered(ctx, vocab_parallel_logits, target, top_k, top_p, inference_only)
+
+    @staticmethod
+    def backward(ctx: Any, *grad_outputs: torch.Tensor):  # type: ignore[override]
+        return (_backward_filtered(ctx, grad_outputs[0]),) + (None,) * 5
+
+
+class ChunkedDistributedLogprobWithSampling(torch.autograd.Function):
+    """Drop-in for ``ChunkedDistributedLogprobWithSampling`` (reference model_utils.py:482-688).
+
+    ``chunk_size`` is validated and otherwise ignored: rows are independent and
+    nothing of size [chunk, V] is ever materialised.
+    """
+
+    @staticmethod
+    def forward(  # type: ignore[override]
+        ctx: Any,
+        vocab_parallel_logits: torch.Tensor,
+        target: torch.Tensor,
+        tp_group: Optional[Any],
+        top_k: Optional[int],
+        top_p: float,
+        chunk_size: int,
+        inference_only: bool = False,
+    ) -> torch.Tensor:
+        from rl_amd.distributed.model_utils import _check_chunk_size, _require_single_rank
+
+        _require_single_rank(tp_group)
+        _check_chunk_size(chunk_size)
+        return _run_filtered(ctx, vocab_parallel_logits, target, top_k, top_p, inference_only)
+
+    @staticmethod
+    def backward(ctx: Any, *grad_outputs: torch.Tensor):  # type: ignore[override]
+        return (_backward_filtered(ctx, grad_outputs[0]),) + (None,) * 6
+
+
+def _run_filtered(ctx, logits, target, top_k, top_p, inference_only):
+    logits = _check_logits(logits)
+    B, S, _ = logits.shape
+    if tuple(target.shape) != (B, S):
+        raise ValueError(f"target shape {tuple(target.shape)} does not match logits rows {(B, S)}")
+    if target.dtype != torch.int64:
+        target = target.long()
+    ctx.filtered = _enabled(top_k, top_p)
+    out = torch.empty((B, S), dtype=torch.float32, device=logits.device)
+    if ctx.filtered:
+        info, kidx, kp = _C.filtered_fwd(logits, target, 1.0, _k(top_k), _p(top_p), out)
+        saved = (logits, target, info, kidx, kp)
+    else:
+        stats = torch.empty((B, S, 2), dtype=torch.float32, device=logits.device)
+        _C.logprob_fwd(logits, target, 0, logits.shape[-1], out, stats)
+        saved = (logits, target, stats)
+    if not inference_only:
+        ctx.save_for_backward(*saved)
+    return out
+
+
+def _backward_filtered(ctx, g):
+    if g.dtype != torch.float32:
+        g = g.float()
+    saved = ctx.saved_tensors
+    logits, target = saved[0], saved[1]
+    grad = torch.empty_like(logits)
+    if ctx.filtered:
+        _C.filtered_bwd(logits, target, 1.0, saved[2], saved[3], saved[4], g, grad)
+    else:
+        _C.logprob_bwd(logits, target, 0, logits.shape[-1], saved[2], g, grad)
+    return grad

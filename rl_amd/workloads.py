@@ -10,6 +10,10 @@ a device.  Sizes default to the full workloads; tests pass smaller sizes.
                     U{256..1536} tokens (mask 1), right padding (mask 0);
                     rewards ~ Bernoulli(0.5); prev = current logprobs + N(0, 0.05^2)
 * long_context_bf16 logits bf16 [1, 32768, 131072] ~ N(0, 1), g ~ N(0, 1)
+* topk_filter_bf16  logits bf16 [4, 4096, 151936] = N(0, 1) + a +8 boost per row
+                    at a Zipf(1.1)-ranked vocabulary id; temperature 0.7,
+                    top_k 50, top_p 0.9; 90% of targets from the row's kept set,
+                    10% outside it (those rows get a zero upstream gradient)
 """
 
 from __future__ import annotations
@@ -102,3 +106,45 @@ def long_context_bf16(B: int = 1, S: int = 32768, V: int = 131072, seed: int = 3
     ids = torch.randint(0, V, (B, S), generator=g).to(device)
     grad = torch.randn((B, S - 1), generator=g).to(device)
     return {"logits": logits, "input_ids": ids, "grad": grad}
+
+
+def topk_filter_bf16(
+    B: int = 4,
+    S: int = 4096,
+    V: int = 151936,
+    temperature: float = 0.7,
+    top_k: int = 50,
+    top_p: float = 0.9,
+    seed: int = 4,
+    device=None,
+):
+    g = _gen(seed)
+    dev = torch.device(device) if device is not None else torch.device("cpu")
+    logits = _randn_bf16((B, S, V), 1.0, g, device)
+    perm = torch.randperm(V, generator=g)
+    ranks = torch.arange(1, V + 1, dtype=torch.float64)
+    w = ranks.pow(-1.1)
+    pick = torch.multinomial(w, B * S, replacement=True, generator=g)  # rank - 1
+    boost_idx = perm[pick].view(B, S).to(dev)
+    flat = logits.view(B * S, V)
+    rows = torch.arange(B * S, device=dev)
+    flat[rows, boost_idx.view(-1)] = (flat[rows, boost_idx.view(-1)].float() + 8.0).to(torch.bfloat16)
+    # the kept set of each row (top-k, then the top-p nucleus over it), used only
+    # to choose targets: 90% inside it, 10% outside
+    y = (flat.float() / temperature).to(torch.bfloat16).float()
+    vals, idx = torch.topk(y, top_k, dim=-1)  # descending
+    p = torch.softmax(vals.double(), -1)
+    asc_cum = torch.cumsum(p.flip(-1), -1).flip(-1)  # mass of each element and everything below it
+    nucleus = (asc_cum > 1 - top_p)
+    nucleus[:, 0] = True
+    n_in = nucleus.sum(-1)
+    u = torch.rand(B * S, generator=g).to(dev)
+    choose = (u * n_in).long().clamp(max=top_k - 1)
+    inside = idx.gather(1, choose.unsqueeze(1)).squeeze(1)
+    outside = torch.randint(0, V, (B * S,), generator=g).to(dev)
+    use_inside = torch.rand(B * S, generator=g).to(dev) < 0.9
+    tgt = torch.where(use_inside, inside, outside).view(B, S)
+    ids = torch.roll(tgt, shifts=1, dims=1)  # ids[:, 1:] are the targets of rows 0..S-2
+    grad = torch.randn((B, S - 1), generator=g).to(dev) * use_inside.view(B, S)[:, :-1].float()
+    return {"logits": logits, "input_ids": ids, "grad": grad, "temperature": temperature,
+            "top_k": top_k, "top_p": top_p}

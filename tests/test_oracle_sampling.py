@@ -1,0 +1,100 @@
+"""Pinning the CPU top-k / top-p oracle (CPU only).
+
+Checks against definitions evaluated independently: brute force over every
+candidate set on tiny vocabularies (the top-k set is the k largest with ties;
+the nucleus is the shortest descending-order prefix whose mass reaches top_p,
+resolved in stable order), plus the reference tests' invariants
+(tests/unit/distributed/test_model_utils.py:1402-1490).
+"""
+
+import itertools
+import math
+
+import pytest
+import torch
+
+from oracle.sampling import filtered_logprobs, filtered_logprobs_grad, next_token_filtered, top_k_top_p
+
+
+def _definition_keep(x: list[float], k, p) -> set[int]:
+    """Keep set from the definitions, in float64, ties broken by (value, index) ascending order."""
+    order = sorted(range(len(x)), key=lambda i: (x[i], i))  # stable ascending
+    kept = list(order)
+    if k is not None and k > 0:
+        thr = sorted(x, reverse=True)[k - 1]
+        kept = [i for i in order if x[i] >= thr]
+    if p is None or p == 1.0:
+        return set(kept)
+    m = max(x[i] for i in kept)
+    e = {i: math.exp(x[i] - m) for i in kept}
+    z = sum(e.values())
+    cum = 0.0
+    out = set()
+    for pos, i in enumerate(kept):
+        cum += e[i] / z
+        if cum > 1 - p or pos == len(kept) - 1:
+            out.update(kept[pos:])
+            break
+    return out
+
+
+@pytest.mark.parametrize("k,p", [(1, 1.0), (2, 1.0), (3, 0.9), (None, 0.5), (None, 0.95), (4, 0.3), (5, 0.999)])
+def test_matches_definition_on_tiny_rows(k, p):
+    g = torch.Generator().manual_seed(0)
+    for trial in range(200):
+        V = 6
+        x = (torch.randint(-3, 4, (V,), generator=g).float() * 0.5)  # many ties
+        _, keep = top_k_top_p(x.unsqueeze(0), k, p)
+        got = set(torch.nonzero(keep[0]).flatten().tolist()) if keep is not None else set(range(V))
+        assert got == _definition_keep(x.tolist(), k, p), (x.tolist(), k, p)
+
+
+def test_reference_invariants():
+    torch.manual_seed(42)
+    logits = torch.randn(2, 4, 100)
+    for k, p in [(5, 1.0), (None, 0.9), (10, 0.8)]:
+        filt, keep = top_k_top_p(logits, k, p)
+        assert torch.equal(keep, ~torch.isinf(filt))
+        probs = torch.softmax(filt, -1)
+        assert torch.allclose(probs.sum(-1), torch.ones(2, 4), atol=1e-5)
+        if k is not None:
+            assert (keep.sum(-1) <= k).all()
+            for b, s in itertools.product(range(2), range(4)):
+                top = torch.topk(logits[b, s], k).indices
+                assert keep[b, s][torch.tensor([i for i in range(100) if i not in top.tolist()])].sum() == 0
+
+
+def test_filtered_logprob_and_grad_definitions():
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(2, 3, 40, generator=g)
+    t = torch.randint(0, 40, (2, 3), generator=g)
+    lp, keep = filtered_logprobs(x, t, 5, 0.8)
+    kept_t = keep.gather(-1, t.unsqueeze(-1)).squeeze(-1)
+    assert torch.isinf(lp[~kept_t]).all() and (lp[~kept_t] < 0).all()
+    ref = torch.log_softmax(x.double().masked_fill(~keep, -float("inf")), -1).gather(-1, t.unsqueeze(-1)).squeeze(-1)
+    torch.testing.assert_close(lp[kept_t].double(), ref[kept_t], rtol=0, atol=1e-6)
+    gout = torch.randn(2, 3, generator=g)
+    gr = filtered_logprobs_grad(x, t, 5, 0.8, gout)
+    assert (gr[~keep] == 0).all()
+    # inside the kept set the gradient is the renormalised softmax gradient
+    p = torch.softmax(x.double().masked_fill(~keep, -float("inf")), -1)
+    oh = torch.nn.functional.one_hot(t, 40).double()
+    torch.testing.assert_close(gr.double(), (oh - p) * gout.unsqueeze(-1).double() * keep, rtol=0, atol=1e-6)
+
+
+def test_temperature_chain_bf16():
+    """div_ in bf16 then the bf16 gradient chain of the reference's production path."""
+    g = torch.Generator().manual_seed(2)
+    x = (torch.randn(1, 5, 64, generator=g) * 2).to(torch.bfloat16)
+    ids = torch.randint(0, 64, (1, 5), generator=g)
+    gout = torch.randn(1, 4, generator=g)
+    lp, keep, grad = next_token_filtered(x, ids, 8, 0.9, temperature=0.7, grad_output=gout)
+    y = (x.float() / 0.7).to(torch.bfloat16).float()
+    lp2, keep2 = filtered_logprobs(y[:, :-1], ids[:, 1:], 8, 0.9)
+    assert torch.equal(keep, keep2)
+    torch.testing.assert_close(lp, lp2, rtol=0, atol=0)
+    assert grad.dtype == torch.bfloat16
+    g32 = filtered_logprobs_grad(y[:, :-1], ids[:, 1:], 8, 0.9, gout)
+    exp = (g32.to(torch.bfloat16).float() / 0.7).to(torch.bfloat16)
+    torch.testing.assert_close(grad[:, :-1].float(), exp.float(), rtol=0, atol=0)
+    assert grad[:, -1].abs().max() == 0
