@@ -60,6 +60,13 @@ def apply_top_k_top_p(
     filtering is requested.  Ties at the k-th value are all kept; top-p keeps
     the shortest suffix of the ascending (stable) order whose cumulative
     probability exceeds ``1 - top_p``, and always the maximum.
+
+    Decisions are made on the fp32 values of the logits for every input
+    dtype: the reference's production callers upcast to fp32 before
+    filtering, which is the chain reproduced here.  (A direct reference call
+    on a bf16/fp16 tensor computes the top-p probabilities in that dtype; the
+    top-k set is the same either way.)  The filtered logits keep the input
+    dtype.
     """
     if not _need_top_k_filtering(top_k) and not _need_top_p_filtering(top_p):
         return logits, None

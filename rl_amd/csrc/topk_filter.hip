@@ -56,8 +56,10 @@ struct RowInfo {
 };
 static_assert(sizeof(RowInfo) == sizeof(mirl_filter_row_info), "row info layout");
 
+// Order-preserving integer key of a float.  -0.0 maps to the key of +0.0: the
+// two compare equal, so a sort treats them as ties ordered by index.
 __device__ __forceinline__ uint32_t okey(float y) {
-  const uint32_t u = __float_as_uint(y);
+  const uint32_t u = __float_as_uint(y == 0.f ? 0.f : y);
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 __device__ __forceinline__ float from_okey(uint32_t k) {
