@@ -146,3 +146,27 @@ def unpack_logprobs(probs: torch.Tensor, cu_seqlens: list[int], unpacked_seqlen:
             if k > 0:
                 out[i, :k] = seq[:k]
     return out
+
+
+def pack_input_ids(
+    input_ids: torch.Tensor, cu_seqlens_q: list[int], cu_seqlens_q_padded: list[int], roll_shift: int = 0
+) -> torch.Tensor:
+    """[B, S, ...] -> [1, T_padded, ...] (reference loss/utils.py:355-408 at CP = 1).
+
+    Each sequence is zero-padded to its padded length, its first
+    min(actual_len, S) tokens copied, optionally rolled, and placed at its
+    padded start.
+    """
+    B = input_ids.shape[0]
+    tail = tuple(input_ids.shape[2:])
+    packed = torch.zeros((cu_seqlens_q_padded[-1], *tail), dtype=input_ids.dtype)
+    for i in range(B):
+        actual = cu_seqlens_q[i + 1] - cu_seqlens_q[i]
+        padded = cu_seqlens_q_padded[i + 1] - cu_seqlens_q_padded[i]
+        seq = torch.zeros((padded, *tail), dtype=input_ids.dtype)
+        n = min(actual, input_ids.shape[1])
+        seq[:n] = input_ids[i, :n]
+        if roll_shift != 0:
+            seq = seq.roll(shifts=roll_shift, dims=0)
+        packed[cu_seqlens_q_padded[i] : cu_seqlens_q_padded[i] + padded] = seq
+    return packed.unsqueeze(0)

@@ -11,3 +11,12 @@ from rl_amd.algorithms.loss.loss_functions import (  # noqa: F401
     ClippedPGLossDataDict,
     ClippedPGLossFn,
 )
+from rl_amd.algorithms.loss.loss_input import (  # noqa: F401
+    prepare_loss_input,
+    prepare_packed_loss_input,
+)
+from rl_amd.algorithms.loss.wrapper import (  # noqa: F401
+    SequencePackingFusionLossWrapper,
+    SequencePackingLossWrapper,
+    wrap_loss_fn_with_input_preparation,
+)

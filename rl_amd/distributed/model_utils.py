@@ -55,6 +55,10 @@ def _group_size(group: Optional[Any]) -> int:
         return torch.distributed.get_world_size(group)
     except (RuntimeError, ValueError):
         return 1
+    except (AttributeError, TypeError) as e:
+        raise TypeError(
+            f"expected a torch.distributed ProcessGroup or None, got {type(group).__name__}"
+        ) from e
 
 
 def _require_single_rank(*groups: Optional[Any]) -> None:

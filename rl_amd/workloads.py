@@ -14,6 +14,9 @@ a device.  Sizes default to the full workloads; tests pass smaller sizes.
                     at a Zipf(1.1)-ranked vocabulary id; temperature 0.7,
                     top_k 50, top_p 0.9; 90% of targets from the row's kept set,
                     10% outside it (those rows get a zero upstream gradient)
+* packed_grpo_kl_bf16 64 sequences of U{64..1024} tokens packed into logits bf16
+                    [1, ~34.8k, 256000] ~ N(0, 1.5^2); 8 prompts x 8 generations,
+                    rewards ~ Bernoulli(0.3); reference = current + N(0, 0.1^2)
 """
 
 from __future__ import annotations
@@ -148,3 +151,62 @@ def topk_filter_bf16(
     grad = torch.randn((B, S - 1), generator=g).to(dev) * use_inside.view(B, S)[:, :-1].float()
     return {"logits": logits, "input_ids": ids, "grad": grad, "temperature": temperature,
             "top_k": top_k, "top_p": top_p}
+
+
+def packed_grpo_kl_bf16(
+    n_seq: int = 64,
+    len_min: int = 64,
+    len_max: int = 1024,
+    V: int = 256000,
+    group_size: int = 8,
+    seed: int = 5,
+    device=None,
+):
+    """Packed GRPO step with a k3 KL penalty: one row [1, T, V] of n_seq sequences.
+
+    Sequence lengths ~ U{len_min..len_max}, packed back to back (cu_seqlens is
+    the cumulative sum, no padding); logits bf16 ~ N(0, 1.5^2); token ids
+    uniform; token_mask is 1 on every position but the first of a sequence;
+    n_seq / group_size prompts x group_size generations, rewards ~
+    Bernoulli(0.3).  The reference-policy noise ~ N(0, 0.1^2) is applied by
+    finish_packed_grpo_step once the current logprobs are known.
+    """
+    g = _gen(seed)
+    lens = torch.randint(len_min, len_max + 1, (n_seq,), generator=g)
+    cu = [0]
+    for n in lens.tolist():
+        cu.append(cu[-1] + n)
+    T, S = cu[-1], int(lens.max())
+    logits = _randn_bf16((1, T, V), 1.5, g, device)
+    pos = torch.arange(S).unsqueeze(0)
+    live = pos < lens.unsqueeze(1)
+    ids = torch.randint(0, V, (n_seq, S), generator=g) * live
+    token_mask = (live & (pos > 0)).float()
+    rewards = torch.bernoulli(torch.full((n_seq,), 0.3), generator=g)
+    prompt_ids = (torch.arange(n_seq) // group_size).unsqueeze(1)
+    ref_noise = torch.randn((n_seq, S), generator=g) * 0.1
+    out = {
+        "input_ids": ids,
+        "input_lengths": lens,
+        "token_mask": token_mask,
+        "sample_mask": torch.ones(n_seq),
+        "rewards": rewards,
+        "prompt_ids": prompt_ids,
+        "ref_noise": ref_noise,
+    }
+    out = {k: v.to(device) for k, v in out.items()}
+    out["logits"] = logits
+    out["cu_seqlens"] = tuple(cu)
+    return out
+
+
+def finish_packed_grpo_step(data: dict, current_logprobs: torch.Tensor) -> dict:
+    """generation = prev = current (on policy); reference = current + noise; [B, S-1] -> [B, S]."""
+    B, S = data["input_ids"].shape
+    cur = torch.zeros((B, S), dtype=torch.float32, device=current_logprobs.device)
+    cur[:, 1:] = current_logprobs.detach().float()
+    data = dict(data)
+    data["prev_logprobs"] = cur
+    data["generation_logprobs"] = cur.clone()
+    data["reference_policy_logprobs"] = cur + data["ref_noise"].to(cur.device)
+    return data

@@ -28,3 +28,17 @@ def pytest_collection_modifyitems(config, items):
     for item in items:
         if "gpu" in item.keywords:
             item.add_marker(skip)
+
+
+@pytest.fixture(scope="session")
+def single_rank_group():
+    """A real torch.distributed process group of size 1 (gloo, in-process store)."""
+    import torch.distributed as dist
+
+    created = False
+    if not dist.is_initialized():
+        dist.init_process_group("gloo", store=dist.HashStore(), rank=0, world_size=1)
+        created = True
+    yield dist.group.WORLD
+    if created:
+        dist.destroy_process_group()

@@ -75,3 +75,13 @@ def test_chunk_size_must_be_positive():
     with pytest.raises(ValueError, match="logprob_chunk_size must be positive"):
         ChunkedDistributedLogprob.apply(torch.randn(1, 2, 4), torch.zeros(1, 2, dtype=torch.long),
                                         0, 4, 0, None)
+
+
+def test_group_arguments(single_rank_group):
+    from rl_amd.distributed.model_utils import _group_size, _require_single_rank
+
+    assert _group_size(None) == 1
+    assert _group_size(single_rank_group) == 1
+    _require_single_rank(single_rank_group, None)
+    with pytest.raises(TypeError, match="ProcessGroup or None"):
+        _require_single_rank(object())

@@ -15,6 +15,7 @@ from oracle.logprob import (
     closed_form_logprobs_f64,
     next_token_logprobs,
     next_token_logprobs_grad,
+    pack_input_ids,
     pack_targets,
     selected_logprobs,
     selected_logprobs_grad,
@@ -97,3 +98,25 @@ def test_packed_roll_and_unpack_match_per_sequence_reference():
     probs = torch.arange(10, dtype=torch.float32)
     out = unpack_logprobs(probs, cu, 5)
     assert out.tolist() == [[0, 1, 0, 0], [0, 0, 0, 0], [3, 4, 5, 0], [7, 8, 0, 0]]
+
+
+def test_pack_input_ids_known_answers():
+    """Hand-computed packings: padded segments, per-segment roll, trailing dims."""
+    ids = torch.tensor([[1, 2, 3, 0], [4, 5, 0, 0]])
+    assert pack_input_ids(ids, [0, 3, 5], [0, 4, 8]).tolist() == [[1, 2, 3, 0, 4, 5, 0, 0]]
+    # roll -1: each padded segment shifts left and wraps to its own first token
+    assert pack_input_ids(ids, [0, 3, 5], [0, 4, 8], roll_shift=-1).tolist() == [[2, 3, 0, 1, 5, 0, 0, 4]]
+    # actual length beyond the row width copies only the S real tokens
+    assert pack_input_ids(ids, [0, 3, 9], [0, 4, 10]).tolist() == [[1, 2, 3, 0, 4, 5, 0, 0, 0, 0]]
+    # trailing dimensions are carried along (reference test_model_utils.py:2233-2250 layout)
+    ids3 = torch.arange(2 * 3 * 2).view(2, 3, 2)
+    got = pack_input_ids(ids3, [0, 2, 5], [0, 2, 6], roll_shift=-1)
+    assert got.tolist() == [[[2, 3], [0, 1], [8, 9], [10, 11], [0, 0], [6, 7]]]
+    # the roll of an unpadded packing is pack_targets of the plain packing
+    x = torch.randint(0, 50, (3, 6))
+    cu = [0, 6, 8, 12]
+    ids_full = torch.zeros(3, 6, dtype=torch.long)
+    for i, n in enumerate([6, 2, 4]):
+        ids_full[i, :n] = x[i, :n]
+    plain = pack_input_ids(ids_full, cu, cu)
+    assert torch.equal(pack_input_ids(ids_full, cu, cu, roll_shift=-1), pack_targets(plain, cu))
