@@ -14,6 +14,14 @@ whole step; `roofline` is the dominant kernel (the logprob backward) measured
 with HIP events around each of its launches inside the timed region;
 `cpu_baseline` times the CPU oracle (a restatement of the reference's PyTorch
 op sequence) on a bounded sample of the same workload.
+
+`--workload` selects another workload of the same path for its kernel
+roofline (the default line above is the headline measurement):
+  fwd_f32      logprob forward only, fp32 [2, 256, 32000] (8 rotating input copies)
+  long_context chunked logprob fwd+bwd, bf16 [1, 32768, 131072], chunk 4096
+  topk_filter  filtered logprob fwd+bwd, bf16 [4, 4096, 151936], T=0.7, k=50, p=0.9
+  packed_kl    packed GRPO step with k3 KL, 64 sequences in bf16 [1, ~34.8k, 256000],
+               through SequencePackingFusionLossWrapper
 """
 
 from __future__ import annotations
@@ -35,6 +43,8 @@ PEAK_HBM_GBPS = 8000.0
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--workload", default="grpo",
+                    choices=["grpo", "fwd_f32", "long_context", "topk_filter", "packed_kl"])
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-sample-rows", type=int, default=1024)
@@ -81,6 +91,9 @@ def main() -> None:
     if args.gpus != 1:
         sys.exit(f"bench.py runs on one GPU only (got --gpus {args.gpus}); this build has no "
                  "multi-GPU path: the workload shards by rows with no exchange, see DESIGN.md")
+    if args.workload != "grpo":
+        bench_workload(args)
+        return
     import torch
 
     from rl_amd import _C, workloads
@@ -223,6 +236,202 @@ def main() -> None:
             "algorithmic_bytes": bwd_bytes,
         },
         "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+def _timed(step, steps: int, warmup: int):
+    """Run `warmup` untimed steps, then `steps` timed ones; (ms per step, per-entry-point events)."""
+    import torch
+
+    from rl_amd import _C
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    timer = _C.enable_launch_timing()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    _C.disable_launch_timing()
+    ms = {k: sum(a.elapsed_time(b) for a, b in v) / max(1, len(v)) for k, v in timer.items()}
+    return (t1 - t0) * 1e3 / steps, ms
+
+
+def _roofline(kernel: str, nbytes: float, ms: float) -> dict:
+    gbps = nbytes / (ms * 1e-3) / 1e9 if ms > 0 else 0.0
+    return {"kernel": kernel, "bound": "hbm", "achieved": gbps, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+            "frac": gbps / PEAK_HBM_GBPS, "traffic": None, "algorithmic_bytes": nbytes}
+
+
+def bench_workload(args) -> None:
+    """The non-default workloads: one JSON line each, same fields as the headline line.
+
+    Algorithmic bytes per next-token row of V entries of s bytes: forward V*s
+    (read); unfiltered backward V*s read for rows with a non-zero upstream
+    gradient plus V*s written for every row; filtered backward V*s written
+    (the kept set saved by the forward replaces the re-read).
+    """
+    import torch
+
+    from rl_amd import workloads
+    from rl_amd.distributed.model_utils import from_parallel_logits_to_logprobs
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    w = args.workload
+    print(f"[bench] device {torch.cuda.get_device_name(dev)}; workload {w}", file=sys.stderr, flush=True)
+    extra: dict = {}
+    if w == "fwd_f32":
+        copies = [workloads.logprob_fwd_f32(device=dev) for _ in range(8)]  # 8 x 65.5 MB > on-die cache
+        B, S, V = copies[0]["logits"].shape
+        it = [0]
+
+        def step():
+            c = copies[it[0] % len(copies)]
+            it[0] += 1
+            return from_parallel_logits_to_logprobs(c["logits"], c["input_ids"], 0, V, None, inference_only=True)
+
+        ms_step, ms = _timed(step, args.steps, args.warmup)
+        rows = B * (S - 1)
+        esz = 4
+        roof = _roofline("mirl_logprob_fwd", rows * V * esz, ms.get("mirl_logprob_fwd", 0.0))
+        step_bytes = rows * V * esz
+        cfg = {"workload": "logprob_fwd_f32", "logits": [B, S, V], "next_token_rows": rows,
+               "rotating_copies": len(copies)}
+        dtype = "f32"
+    elif w == "long_context":
+        d = workloads.long_context_bf16(device=dev)
+        logits = d["logits"].requires_grad_(True)
+        ids, g = d["input_ids"], d["grad"]
+        B, S, V = logits.shape
+
+        def step():
+            lp = from_parallel_logits_to_logprobs(logits, ids, 0, V, None, chunk_size=4096)
+            return torch.autograd.grad(lp, [logits], g)
+
+        ms_step, ms = _timed(step, args.steps, args.warmup)
+        rows = B * (S - 1)
+        active = int((g != 0).sum().item())
+        esz = 2
+        bwd_bytes = (active + B * S) * V * esz
+        roof = _roofline("mirl_logprob_bwd", bwd_bytes, ms.get("mirl_logprob_bwd", 0.0))
+        step_bytes = rows * V * esz + bwd_bytes
+        extra["logprob_fwd_gbps"] = rows * V * esz / (ms.get("mirl_logprob_fwd", 1e9) * 1e-3) / 1e9
+        cfg = {"workload": "long_context_chunked_logprob_fwd_bwd", "logits": [B, S, V], "chunk_size": 4096,
+               "next_token_rows": rows, "active_rows": active}
+        dtype = "bf16"
+    elif w == "topk_filter":
+        from rl_amd.distributed.sampling import filtered_next_token_logprobs
+
+        d = workloads.topk_filter_bf16(device=dev)
+        logits = d["logits"].requires_grad_(True)
+        ids, g = d["input_ids"], d["grad"]
+        B, S, V = logits.shape
+        k, p, T = d["top_k"], d["top_p"], d["temperature"]
+
+        def step():
+            lp = filtered_next_token_logprobs(logits, ids, k, p, temperature=T)
+            return torch.autograd.grad(lp, [logits], g)
+
+        ms_step, ms = _timed(step, args.steps, args.warmup)
+        rows = B * (S - 1)
+        esz = 2
+        fwd_bytes, bwd_bytes = rows * V * esz, B * S * V * esz
+        fwd_ms, bwd_ms = ms.get("mirl_filtered_logprob_fwd", 0.0), ms.get("mirl_filtered_logprob_bwd", 0.0)
+        roof = _roofline("mirl_filtered_logprob_fwd", fwd_bytes, fwd_ms)
+        extra["filtered_bwd_gbps"] = bwd_bytes / (bwd_ms * 1e-3) / 1e9 if bwd_ms > 0 else None
+        step_bytes = fwd_bytes + bwd_bytes
+        cfg = {"workload": "topk_topp_temperature_filtered_logprob_fwd_bwd", "logits": [B, S, V],
+               "temperature": T, "top_k": k, "top_p": p, "next_token_rows": rows,
+               "temperature_fused": True}
+        dtype = "bf16"
+    else:  # packed_kl
+        import torch.distributed as dist
+
+        from rl_amd.algorithms.advantage_estimator import AdvEstimatorConfig, GRPOAdvantageEstimator
+        from rl_amd.algorithms.loss import (
+            ClippedPGLossConfig,
+            ClippedPGLossFn,
+            SequencePackingFusionLossWrapper,
+            prepare_packed_loss_input,
+        )
+        from rl_amd.distributed.batched_data_dict import BatchedDataDict
+
+        if not dist.is_initialized():
+            dist.init_process_group("gloo", store=dist.HashStore(), rank=0, world_size=1)
+        group = dist.group.WORLD
+        d = workloads.packed_grpo_kl_bf16(device=dev)
+        logits, cu = d["logits"], d["cu_seqlens"]
+        _, T, V = logits.shape
+        n_seq = len(cu) - 1
+        cfg_kw = dict(reference_policy_kl_penalty=0.01, reference_policy_kl_type="k3",
+                      ratio_clip_min=0.2, ratio_clip_max=0.2, token_level_loss=False)
+        loss_fn = ClippedPGLossFn(ClippedPGLossConfig(**cfg_kw))
+        with torch.no_grad():
+            cur, _ = prepare_packed_loss_input(
+                logits, BatchedDataDict({"input_ids": d["input_ids"]}), loss_fn, cu, cu,
+                vocab_parallel_rank=0, vocab_parallel_group=group)
+        d = workloads.finish_packed_grpo_step(d, cur["next_token_logprobs"])
+        est = GRPOAdvantageEstimator(AdvEstimatorConfig(use_leave_one_out_baseline=False))
+        batch = BatchedDataDict({k: d[k] for k in ("input_ids", "token_mask", "sample_mask", "prev_logprobs",
+                                                   "generation_logprobs", "reference_policy_logprobs")})
+        gvs = d["sample_mask"].sum()
+        gvt = d["token_mask"][:, 1:].sum()
+        wrapper = SequencePackingFusionLossWrapper(loss_fn, prepare_packed_loss_input, cu, cu,
+                                                   vocab_parallel_rank=0, vocab_parallel_group=group)
+        logits.requires_grad_(True)
+
+        def step():
+            batch["advantages"] = est.compute_advantage(d["prompt_ids"], d["rewards"], d["token_mask"])
+            loss, _ = wrapper(logits, batch, gvs, gvt)
+            return torch.autograd.grad(loss, [logits])
+
+        # active rows: next-token rows whose upstream gradient is non-zero
+        batch["advantages"] = est.compute_advantage(d["prompt_ids"], d["rewards"], d["token_mask"])
+        lp_leaf = cur["next_token_logprobs"].detach().requires_grad_(True)
+        l2, _ = loss_fn(next_token_logprobs=lp_leaf, data=batch, global_valid_seqs=gvs, global_valid_toks=gvt)
+        (glp,) = torch.autograd.grad(l2, [lp_leaf])
+        active = int((glp != 0).sum().item())
+        del lp_leaf, l2, glp
+        ms_step, ms = _timed(step, args.steps, args.warmup)
+        rows = T - n_seq
+        esz = 2
+        fwd_bytes = rows * V * esz
+        bwd_bytes = (active + T) * V * esz
+        roof = _roofline("mirl_logprob_bwd", bwd_bytes, ms.get("mirl_logprob_bwd", 0.0))
+        extra["logprob_fwd_gbps"] = fwd_bytes / (ms.get("mirl_logprob_fwd", 1e9) * 1e-3) / 1e9
+        step_bytes = fwd_bytes + bwd_bytes
+        cfg = {"workload": "packed_grpo_kl_fused_wrapper", "logits": [1, T, V], "sequences": n_seq,
+               "next_token_rows": rows, "active_rows": active,
+               "loss": "ClippedPG clip 0.2/0.2, k3 KL beta 0.01, sequence-level mean; GRPO adv (no LOO)"}
+        dtype = "bf16"
+
+    cfg["parallelism"] = "single-gpu"
+    step_gbps = step_bytes / (ms_step * 1e-3) / 1e9
+    out = {
+        "metric": f"{w}: next-token rows/s and HBM GB/s (% peak)",
+        "value": rows / (ms_step * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": dtype,
+        "data": "synthetic",
+        "config": cfg,
+        "hbm_gbps_step": step_gbps,
+        "hbm_frac_step": step_gbps / PEAK_HBM_GBPS,
+        "kernels_ms": {k.replace("mirl_", ""): v for k, v in ms.items()},
+        **extra,
+        "roofline": roof,
+        "cpu_baseline": None,
     }
     print(json.dumps(out), flush=True)
 
