@@ -9,6 +9,7 @@ from __future__ import annotations
 
 from collections.abc import Sequence
 
+import numpy as np
 import torch
 
 CpuIntTuple = tuple[int, ...]
@@ -45,19 +46,30 @@ def _pack_input_ids(
     tail = tuple(input_ids.shape[2:])
     if B == 0 or S == 0 or total <= 0:
         return torch.zeros((1, max(total, 0), *tail), dtype=input_ids.dtype, device=dev)
-    bounds = torch.tensor(cu_seqlens_q_padded, dtype=torch.int64, device=dev)
-    starts, ends = bounds[:-1], bounds[1:]
-    plen = ends - starts
-    qb = torch.tensor(cu_seqlens_q, dtype=torch.int64, device=dev)
-    copy_len = torch.clamp(qb[1:] - qb[:-1], max=S)  # real tokens copied per sequence
-    pos = torch.arange(total, device=dev)
-    seq = torch.bucketize(pos, ends, right=True).clamp(max=B - 1)
-    inside = (pos >= starts[seq]) & (pos < ends[seq])
-    off = pos - starts[seq]  # position inside the padded segment
+    from rl_amd.distributed.model_utils import _gather_or_zero, _host_ints_to_device
+
+    src = _pack_map(cu_seqlens_q, cu_seqlens_q_padded, S, roll_shift)
+    flat = input_ids.reshape(B * S, *tail)
+    return _gather_or_zero(flat, _host_ints_to_device(src, dev)).unsqueeze(0)
+
+
+def _pack_map(cu_q: CpuIntTuple, cu_pad: CpuIntTuple, S: int, roll_shift: int) -> np.ndarray:
+    """Row of ``input_ids.reshape(B * S)`` read by each packed position (``B * S`` reads zero)."""
+    b = np.asarray(cu_pad, dtype=np.int64)
+    q = np.asarray(cu_q, dtype=np.int64)
+    B = b.shape[0] - 1
+    total = int(b[-1])
+    starts, plen = b[:-1], b[1:] - b[:-1]
+    copy_len = np.minimum(q[1:] - q[:-1], S)
+    src = np.full(total, B * S, dtype=np.int64)
+    if B == 0 or np.any(plen < 0):
+        return src
+    # the padded segments tile [cu_pad[0], cu_pad[-1]) back to back
+    seq = np.repeat(np.arange(B), plen)
+    pos = np.arange(b[0], total, dtype=np.int64)
+    off = pos - starts[seq]
     if roll_shift != 0:
-        off = torch.remainder(off - roll_shift, plen[seq].clamp(min=1))
-    valid = inside & (off >= 0) & (off < copy_len[seq])
-    src = seq * S + off.clamp(min=0, max=S - 1)
-    packed = input_ids.reshape(B * S, *tail)[src]
-    mask = valid.view(-1, *([1] * len(tail)))
-    return torch.where(mask, packed, torch.zeros_like(packed)).unsqueeze(0)
+        off = np.mod(off - roll_shift, plen[seq])
+    ok = (off < copy_len[seq]) & (pos >= 0)
+    src[pos[ok]] = seq[ok] * S + off[ok]
+    return src

@@ -20,6 +20,7 @@ from __future__ import annotations
 
 from typing import Any, Optional
 
+import numpy as np
 import torch
 
 from rl_amd import _C
@@ -298,9 +299,11 @@ def from_parallel_logits_to_logprobs_packed_sequences(
     """Logprobs of packed sequences (reference model_utils.py:1065-1231), CP = TP = 1.
 
     ``vocab_parallel_logits`` is ``[1, T, V]``; ``cu_seqlens_padded`` holds the
-    ``B + 1`` sequence boundaries.  The per-sequence target roll and the
-    unpacking to ``[B, unpacked_seqlen - 1]`` are done with index arithmetic on
-    the device instead of a host loop over sequences.
+    ``B + 1`` sequence boundaries (host integers).  The reference's host loops
+    over sequences (target roll, unpacking to ``[B, unpacked_seqlen - 1]``)
+    become index maps built on the host from the boundaries and applied with
+    one gather each; the unpacking's backward is the inverse gather, so no
+    scatter or sort runs in the backward.
     """
     _require_single_rank(group, cp_group)
     _check_chunk_size(chunk_size)
@@ -308,25 +311,18 @@ def from_parallel_logits_to_logprobs_packed_sequences(
     if logits.shape[0] != 1:
         raise ValueError(f"packed logits must have batch 1, got {tuple(logits.shape)}")
     bounds = [int(x) for x in cu_seqlens_padded]
-    batch_size = len(bounds) - 1
     T = logits.shape[1]
     dev = logits.device
     tgt = target.reshape(1, -1)
     if tgt.dtype != torch.int64:
         tgt = tgt.long()
     if not target_is_pre_rolled:
-        # rolled[p] = target[p + 1] inside each sequence; the last position of
-        # a sequence wraps to its first token.
-        starts, ends = _seq_bounds(bounds, T, dev)
-        pos = torch.arange(T, device=dev)
-        nxt = pos + 1
-        seq_id = torch.bucketize(pos, ends, right=True)
-        seq_id = seq_id.clamp(max=batch_size - 1) if batch_size > 0 else seq_id
-        last = nxt == ends[seq_id]
-        nxt = torch.where(last, starts[seq_id], nxt)
-        in_seq = pos < bounds[-1]
-        src = torch.where(in_seq, nxt, pos).clamp(max=tgt.shape[1] - 1)
-        tgt = torch.where(in_seq, tgt[0, src], torch.zeros_like(pos)).unsqueeze(0)
+        if bounds[-1] > tgt.shape[1]:
+            raise ValueError(
+                f"cu_seqlens_padded ends at {bounds[-1]} but the packed target has {tgt.shape[1]} tokens"
+            )
+        roll = _host_ints_to_device(_roll_map(bounds, tgt.shape[1]), dev)
+        tgt = _gather_or_zero(tgt.reshape(-1), roll).unsqueeze(0)
     if need_top_k_or_top_p_filtering(sampling_params):
         from rl_amd.distributed.sampling import filtered_row_logprobs
 
@@ -342,15 +338,73 @@ def from_parallel_logits_to_logprobs_packed_sequences(
     probs = probs.squeeze(0)
     if return_packed_layout:
         return probs[:-1].unsqueeze(0)
-    out_cols = unpacked_seqlen - 1
-    starts, ends = _seq_bounds(bounds, T, dev)
-    lens = (ends - starts - 1).clamp(min=0).clamp(max=out_cols)
-    col = torch.arange(out_cols, device=dev)
-    src = starts.unsqueeze(1) + col.unsqueeze(0)
-    valid = col.unsqueeze(0) < lens.unsqueeze(1)
-    src = torch.where(valid, src, torch.zeros_like(src))
-    gathered = probs[src.reshape(-1)].reshape(batch_size, out_cols)
-    return torch.where(valid, gathered, torch.zeros_like(gathered))
+    if bounds[-1] > probs.shape[0]:
+        raise ValueError(
+            f"cu_seqlens_padded ends at {bounds[-1]} but only {probs.shape[0]} packed rows were computed"
+        )
+    out_cols = max(int(unpacked_seqlen) - 1, 0)
+    src, dst = _unpack_maps(bounds, probs.shape[0], out_cols)
+    maps = _host_ints_to_device(np.concatenate([src, dst]), dev)
+    return _UnpackRows.apply(probs, maps[: src.shape[0]], maps[src.shape[0] :], (len(bounds) - 1, out_cols))
+
+
+def _gather_or_zero(x: torch.Tensor, index: torch.Tensor) -> torch.Tensor:
+    """``x[index]`` along dim 0, where ``index == x.shape[0]`` reads a zero."""
+    pad = x.new_zeros((1, *x.shape[1:]))
+    return torch.cat([x, pad]).index_select(0, index)
+
+
+def _roll_map(bounds: list[int], n: int) -> np.ndarray:
+    """Source of each position of the per-sequence roll by -1 (reference model_utils.py:1122-1139).
+
+    Inside ``[bounds[i], bounds[i+1])`` position p reads p + 1, the segment's
+    last position its first; positions past ``bounds[-1]`` read the zero slot ``n``.
+    """
+    b = np.asarray(bounds, dtype=np.int64)
+    src = np.full(n, n, dtype=np.int64)
+    lens = b[1:] - b[:-1]
+    total = int(b[-1] - b[0])
+    if total > 0:
+        seq = np.repeat(np.arange(lens.shape[0]), lens)
+        pos = np.arange(b[0], b[-1], dtype=np.int64)
+        nxt = pos + 1
+        src[b[0] : b[-1]] = np.where(nxt == b[1:][seq], b[:-1][seq], nxt)
+    return src
+
+
+def _unpack_maps(bounds: list[int], n_rows: int, out_cols: int) -> tuple[np.ndarray, np.ndarray]:
+    """Index maps of the unpacking (reference model_utils.py:1211-1229).
+
+    ``src[i * out_cols + j]`` is the packed row copied to ``out[i, j]`` (rows
+    ``bounds[i] .. bounds[i+1] - 2``, at most ``out_cols`` of them; ``n_rows``
+    reads zero); ``dst[p]`` is the inverse (``B * out_cols`` for packed rows
+    that are not copied).
+    """
+    b = np.asarray(bounds, dtype=np.int64)
+    B = b.shape[0] - 1
+    starts = b[:-1]
+    lens = np.clip(b[1:] - starts - 1, 0, out_cols)
+    j = np.arange(out_cols, dtype=np.int64)
+    valid = j[None, :] < lens[:, None]
+    src = np.where(valid, starts[:, None] + j[None, :], n_rows).reshape(-1)
+    dst = np.full(n_rows, B * out_cols, dtype=np.int64)
+    flat_valid = valid.reshape(-1)
+    dst[src[flat_valid]] = np.nonzero(flat_valid)[0]
+    return src, dst
+
+
+class _UnpackRows(torch.autograd.Function):
+    """``[T]`` packed rows -> ``[B, C]`` via a gather map; backward is the inverse gather."""
+
+    @staticmethod
+    def forward(ctx: Any, probs: torch.Tensor, src: torch.Tensor, dst: torch.Tensor, shape: tuple) -> torch.Tensor:  # type: ignore[override]
+        ctx.save_for_backward(dst)
+        return _gather_or_zero(probs, src).view(shape)
+
+    @staticmethod
+    def backward(ctx: Any, *grad_outputs: torch.Tensor):  # type: ignore[override]
+        (dst,) = ctx.saved_tensors
+        return _gather_or_zero(grad_outputs[0].reshape(-1), dst), None, None, None
 
 
 def _is_dtensor(t: torch.Tensor) -> bool:
@@ -361,9 +415,16 @@ def _is_dtensor(t: torch.Tensor) -> bool:
     return isinstance(t, DTensor)
 
 
-def _seq_bounds(bounds: list[int], T: int, dev: torch.device) -> tuple[torch.Tensor, torch.Tensor]:
-    b = torch.tensor(bounds, dtype=torch.int64, device=dev)
-    return b[:-1], b[1:]
+def _host_ints_to_device(values: Any, dev: torch.device) -> torch.Tensor:
+    """int64 tensor of host integers on ``dev``, staged through pinned memory so
+    that the copy is queued on the stream instead of blocking the host."""
+    if isinstance(values, np.ndarray):
+        t = torch.from_numpy(np.ascontiguousarray(values, dtype=np.int64))
+    else:
+        t = torch.tensor(values, dtype=torch.int64)
+    if dev.type != "cuda":
+        return t.to(dev)
+    return t.pin_memory().to(dev, non_blocking=True)
 
 
 def get_next_token_logprobs_from_logits(
