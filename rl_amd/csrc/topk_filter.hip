@@ -18,11 +18,12 @@
 // once, keeping per-lane maxima and per-(lane, group-of-vectors) maxima.  The
 // k-th largest lane maximum is a lower bound tau on the k-th largest value
 // (k distinct elements are >= it), so only groups whose maximum reaches tau
-// can hold a kept element; those few groups are re-read (a few KB per row,
-// mostly from cache) and their elements >= tau collected in LDS.  A radix
-// select over the candidates gives the exact top-k cut; a stable sort of the
-// candidates gives the top-p cut and the kept-set log-sum-exp.  Rows whose
-// candidates overflow LDS are flagged and redone by the general path.
+// can hold a kept element; those few groups are listed in LDS and re-read by
+// the whole workgroup as independent loads (a few KB per row), and their
+// elements >= tau collected in LDS.  Sorting the candidates by (value, index)
+// gives the exact top-k value (the k-th largest), the stable-order top-p cut
+// and the kept-set log-sum-exp.  Rows whose candidates overflow LDS are
+// flagged and redone by the general path.
 //
 // Forward, general path (top-p without top-k, k > 1024, flagged rows): exact
 // multi-pass radix selection over the row (count histograms for the top-k
@@ -65,6 +66,13 @@ __device__ __forceinline__ uint32_t okey(float y) {
 __device__ __forceinline__ float from_okey(uint32_t k) {
   const uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
   return __uint_as_float(u);
+}
+// Upper 16 bits of okey(v), rounded up: from_okey(hi << 16) >= v.  Exact for
+// 16-bit inputs, whose keys have zero low halves.
+__device__ __forceinline__ uint16_t okey_hi_up(float v) {
+  const uint32_t k = okey(v);
+  const uint32_t hi = k >> 16;
+  return (uint16_t)(((k & 0xffffu) != 0u && hi < 0xffffu) ? hi + 1u : hi);
 }
 __device__ __forceinline__ bool kept_lex(float y, int64_t j, float vc, int32_t ic) {
   return y > vc || (y == vc && j >= (int64_t)ic);
@@ -130,104 +138,107 @@ __device__ int block_sum_i(int v, int* red) {
   return r;
 }
 
-// k-th largest of n keys, by one wave: the largest c with #{key >= c} >= k.
-template <class F>
-__device__ uint32_t wave_kth_largest(F key_at, int n, int k) {
+// k-th largest of the NT order keys okey(vals[i]) (vals in LDS), computed by
+// one wave: the largest c with #{key >= c} >= k, one bit per round from bit 31
+// down to LOW_BIT, counted by ballot.  Bits below LOW_BIT are left zero, so the
+// result is a lower bound when the keys have nonzero low bits (exact for values
+// of a 16-bit type with LOW_BIT = 16).  Only wave 0 may call it.
+template <int NT, int LOW_BIT>
+__device__ uint32_t wave_kth_largest(const float* vals, int k) {
+  constexpr int PER = NT / 64;
   const int lane = threadIdx.x % 64;
+  uint32_t key[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) key[i] = okey(vals[lane + 64 * i]);
   uint32_t prefix = 0;
-  for (int bit = 31; bit >= 0; --bit) {
+  for (int bit = 31; bit >= LOW_BIT; --bit) {
     const uint32_t cand = prefix | (1u << bit);
     int cnt = 0;
-    for (int i = lane; i < n; i += 64) cnt += (key_at(i) >= cand) ? 1 : 0;
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) cnt += __shfl_xor(cnt, off, 64);
+    for (int i = 0; i < PER; ++i) cnt += __popcll(__ballot(key[i] >= cand));
     if (cnt >= k) prefix = cand;
   }
   return prefix;
 }
 
-// Ascending bitonic sort of n 64-bit keys in LDS (N = power of two >= n, the
-// rest padded with the maximum key) by the whole workgroup.
+// Ascending sort of n <= kCandCap distinct 64-bit keys in LDS by the whole
+// workgroup: each key's rank is the number of smaller keys.  Must be entered
+// after a barrier that publishes the keys; ends with a barrier.
 template <int NT>
-__device__ void block_bitonic_sort(uint64_t* keys, int n, int N) {
-  for (int i = n + (int)threadIdx.x; i < N; i += NT) keys[i] = ~0ull;
-  __syncthreads();
-  for (int k = 2; k <= N; k <<= 1) {
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      for (int i = threadIdx.x; i < N; i += NT) {
-        const int ixj = i ^ j;
-        if (ixj > i) {
-          const uint64_t a = keys[i], b = keys[ixj];
-          const bool asc = (i & k) == 0;
-          if ((a > b) == asc) {
-            keys[i] = b;
-            keys[ixj] = a;
-          }
-        }
-      }
-      __syncthreads();
-    }
+__device__ void block_rank_sort(uint64_t* keys, int n) {
+  constexpr int PER = (kCandCap + NT - 1) / NT;
+  const int tid = threadIdx.x;
+  uint64_t mine[PER];
+  int rank[PER];
+#pragma unroll
+  for (int p = 0; p < PER; ++p) {
+    const int i = tid + p * NT;
+    mine[p] = i < n ? keys[i] : ~0ull;
+    rank[p] = 0;
   }
+  for (int j = 0; j < n; ++j) {
+    const uint64_t kj = keys[j];
+#pragma unroll
+    for (int p = 0; p < PER; ++p) rank[p] += (kj < mine[p]) ? 1 : 0;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int p = 0; p < PER; ++p)
+    if (tid + p * NT < n) keys[rank[p]] = mine[p];
+  __syncthreads();
 }
 
-// Writes the row's results.  `skeys` holds the kept-k candidates sorted
-// ascending as (okey(y) << 32 | index); `thr` is the top-k value.
-template <class E, int NT>
-__device__ void finish_row(const FilterParams& P, int64_t row, const typename E::raw* x,
-                           const uint64_t* skeys, int n_k, float thr, float* redf,
-                           int* s_first) {
-  const int tid = threadIdx.x;
-  const float m = from_okey((uint32_t)(skeys[n_k - 1] >> 32));
+// Writes the row's results; run by wave 0 alone (the other waves may have
+// left).  `skeys` holds the kept-k candidates sorted ascending as
+// (okey(y) << 32 | index); `thr` is the top-k value; `yt` is the target's
+// scaled logit (lane 0 only; NaN when there is no target in range).
+template <class E>
+__device__ void finish_row(const FilterParams& P, int64_t row, const uint64_t* skeys, int n_k,
+                           float thr, float yt, int64_t t) {
+  const int lane = threadIdx.x;
+  auto y_at = [&](int i) { return from_okey((uint32_t)(skeys[i] >> 32)); };
+  const float m = y_at(n_k - 1);
   int first = 0;
   if (P.has_p) {
     float zpart = 0.f;
-    for (int i = tid; i < n_k; i += NT) zpart += expf(from_okey((uint32_t)(skeys[i] >> 32)) - m);
-    const float Z = block_sum_f<NT>(zpart, redf);
-    if (tid < 64) {
-      // cumulative probability in ascending order, accumulated in double
-      double run = 0.0;
-      int found = n_k - 1;  // the maximum is always kept
-      for (int base = 0; base < n_k; base += 64) {
-        const int i = base + tid;
-        double inc = (i < n_k)
-                         ? (double)(expf(from_okey((uint32_t)(skeys[i] >> 32)) - m) / Z)
-                         : 0.0;
+    for (int i = lane; i < n_k; i += 64) zpart += expf(y_at(i) - m);
+    const float Z = wave_sum(zpart);
+    // cumulative probability in ascending order, accumulated in double
+    double run = 0.0;
+    first = n_k - 1;  // the maximum is always kept
+    for (int base = 0; base < n_k; base += 64) {
+      const int i = base + lane;
+      double inc = (i < n_k) ? (double)(expf(y_at(i) - m) / Z) : 0.0;
 #pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-          const double o = __shfl_up(inc, off, 64);
-          if (tid >= off) inc += o;
-        }
-        const bool hit = (i < n_k) && ((float)(run + inc) > P.cut);
-        const uint64_t bal = __ballot(hit);
-        if (bal != 0ull) {
-          found = base + __ffsll((long long)bal) - 1;
-          break;
-        }
-        run += __shfl(inc, 63, 64);
+      for (int off = 1; off < 64; off <<= 1) {
+        const double o = __shfl_up(inc, off, 64);
+        if (lane >= off) inc += o;
       }
-      if (tid == 0) *s_first = found;
+      const bool hit = (i < n_k) && ((float)(run + inc) > P.cut);
+      const uint64_t bal = __ballot(hit);
+      if (bal != 0ull) {
+        first = base + __ffsll((long long)bal) - 1;
+        break;
+      }
+      run += __shfl(inc, 63, 64);
     }
-    __syncthreads();
-    first = *s_first;
   }
   const uint64_t ck = skeys[first];
   const float v_cut = P.has_p ? from_okey((uint32_t)(ck >> 32)) : thr;
   const int32_t i_cut = P.has_p ? (int32_t)(ck & 0xffffffffu) : 0;
   const int n_kept = n_k - first;
   float spart = 0.f;
-  for (int i = first + tid; i < n_k; i += NT) spart += expf(from_okey((uint32_t)(skeys[i] >> 32)) - m);
-  const float s = block_sum_f<NT>(spart, redf);
-  const float logsum = logf(s);
+  for (int i = first + lane; i < n_k; i += 64) spart += expf(y_at(i) - m);
+  const float logsum = logf(wave_sum(spart));
   if (n_kept <= kKeepCap) {
     int32_t* ki = P.kept_idx + row * kKeepCap;
     float* kp = P.kept_p + row * kKeepCap;
-    for (int i = first + tid; i < n_k; i += NT) {
-      const float y = from_okey((uint32_t)(skeys[i] >> 32));
+    for (int i = first + lane; i < n_k; i += 64) {
       ki[i - first] = (int32_t)(skeys[i] & 0xffffffffu);
-      kp[i - first] = expf((y - m) - logsum);
+      kp[i - first] = expf((y_at(i) - m) - logsum);
     }
   }
-  if (tid == 0) {
+  if (lane == 0) {
     RowInfo ri;
     ri.m = m;
     ri.logsum = logsum;
@@ -237,13 +248,8 @@ __device__ void finish_row(const FilterParams& P, int64_t row, const typename E:
     ri.flags = 0;
     P.info[row] = ri;
     if (P.out != nullptr) {
-      const int64_t b = row / P.R, r = row - b * P.R;
-      const int64_t t = P.target[b * P.tsb + r * P.tsr];
       float lp = -INFINITY;
-      if (t >= 0 && t < P.V) {
-        const float yt = scaled<E>(E::load(x + t), P);
-        if (kept_lex(yt, t, v_cut, i_cut)) lp = (yt - m) - logsum;
-      }
+      if (t >= 0 && t < P.V && kept_lex(yt, t, v_cut, i_cut)) lp = (yt - m) - logsum;
       P.out[row] = lp;
     }
   }
@@ -257,13 +263,12 @@ __global__ __launch_bounds__(64 * W) void filter_fast_kernel(FilterParams P) {
   using raw = typename E::raw;
   constexpr int NT = 64 * W;
   constexpr int VEC = E::kVec;
-  __shared__ float s_gmax[kMaxGroups * NT];
+  __shared__ uint16_t s_gkey[kMaxGroups * NT];  // per-group maxima, okey_hi_up
   __shared__ float s_lmax[NT];
   __shared__ uint64_t s_cand[kCandCap];
-  __shared__ float redf[NT / 64];
-  __shared__ int s_count, s_first;
+  __shared__ uint16_t s_pairs[kCandCap];  // (lane, group) pairs to re-read
+  __shared__ int s_count, s_npairs;
   __shared__ float s_tau;
-  __shared__ uint32_t s_thr;
 
   const int64_t row = blockIdx.x;
   const int64_t b = row / P.R, r = row - b * P.R;
@@ -276,7 +281,17 @@ __global__ __launch_bounds__(64 * W) void filter_fast_kernel(FilterParams P) {
   const int Jmax = (nvec + NT - 1) / NT;
   const int GS = U * ((Jmax + kMaxGroups * U - 1) / (kMaxGroups * U));
   const int G = (Jmax + GS - 1) / GS;
-  if (tid == 0) s_count = 0;
+  if (tid == 0) {
+    s_count = 0;
+    s_npairs = 0;
+  }
+  // the target's logit, loaded now so that its latency overlaps the stream
+  int64_t t = -1;
+  float yt = NAN;
+  if (tid == 0 && P.out != nullptr) {
+    t = P.target[b * P.tsb + r * P.tsr];
+    if (t >= 0 && t < P.V) yt = scaled<E>(E::load(x + t), P);
+  }
 
   // ---- pass 1: stream the row, per-group maxima of the raw values ----------
   float lmax = -INFINITY, cur = -INFINITY;
@@ -285,7 +300,7 @@ __global__ __launch_bounds__(64 * W) void filter_fast_kernel(FilterParams P) {
   for (; tid + (j + U - 1) * NT < nvec; j += U) {
     const int g = j / GS;
     if (g != curg) {
-      s_gmax[curg * NT + tid] = cur;
+      s_gkey[curg * NT + tid] = okey_hi_up(cur);
       lmax = fmaxf(lmax, cur);
       curg = g;
       cur = -INFINITY;
@@ -304,7 +319,7 @@ __global__ __launch_bounds__(64 * W) void filter_fast_kernel(FilterParams P) {
   for (; tid + j * NT < nvec; ++j) {
     const int g = j / GS;
     if (g != curg) {
-      s_gmax[curg * NT + tid] = cur;
+      s_gkey[curg * NT + tid] = okey_hi_up(cur);
       lmax = fmaxf(lmax, cur);
       curg = g;
       cur = -INFINITY;
@@ -314,9 +329,9 @@ __global__ __launch_bounds__(64 * W) void filter_fast_kernel(FilterParams P) {
 #pragma unroll
     for (int k = 0; k < VEC; ++k) cur = fmaxf(cur, w[k]);
   }
-  s_gmax[curg * NT + tid] = cur;
+  s_gkey[curg * NT + tid] = okey_hi_up(cur);
   lmax = fmaxf(lmax, cur);
-  for (int g = curg + 1; g < G; ++g) s_gmax[g * NT + tid] = -INFINITY;
+  for (int g = curg + 1; g < G; ++g) s_gkey[g * NT + tid] = okey_hi_up(-INFINITY);
   const float hv = (tid < sp.head) ? E::load(x + tid) : -INFINITY;
   const float tv = (sp.tail0 + tid < P.V) ? E::load(x + sp.tail0 + tid) : -INFINITY;
   lmax = fmaxf(lmax, fmaxf(hv, tv));
@@ -325,7 +340,7 @@ __global__ __launch_bounds__(64 * W) void filter_fast_kernel(FilterParams P) {
 
   // ---- lower bound tau: the k-th largest lane maximum ------------------------
   if (tid < 64) {
-    const uint32_t kk = wave_kth_largest([&](int i) { return okey(s_lmax[i]); }, NT, P.top_k);
+    const uint32_t kk = wave_kth_largest<NT, sizeof(raw) == 2 ? 16 : 0>(s_lmax, P.top_k);
     if (tid == 0) s_tau = scaled<E>(from_okey(kk), P);
   }
   __syncthreads();
@@ -336,17 +351,47 @@ __global__ __launch_bounds__(64 * W) void filter_fast_kernel(FilterParams P) {
     const int slot = atomicAdd(&s_count, 1);
     if (slot < kCandCap) s_cand[slot] = ((uint64_t)okey(y) << 32) | (uint64_t)(uint32_t)idx;
   };
+  // flagged groups are listed first, then their vectors are spread over the
+  // whole workgroup so that the re-reads are independent loads
   for (int g = 0; g < G; ++g) {
-    if (!(scaled<E>(s_gmax[g * NT + tid], P) >= tau)) continue;
-    for (int jj = g * GS; jj < (g + 1) * GS; ++jj) {
-      const int vi = tid + jj * NT;
-      if (vi >= nvec) break;
-      float w[VEC];
-      E::unpack(xv[vi], w);
+    if (scaled<E>(from_okey((uint32_t)s_gkey[g * NT + tid] << 16), P) >= tau) {
+      const int slot = atomicAdd(&s_npairs, 1);
+      if (slot < kCandCap) s_pairs[slot] = (uint16_t)(tid * kMaxGroups + g);
+    }
+  }
+  __syncthreads();
+  const int npairs = s_npairs;
+  if (npairs > kCandCap) {
+    // more flagged groups than candidate slots: every flagged group holds at
+    // least one element >= tau, so the candidates overflow as well
+    if (tid == 0) s_count = kCandCap + 1;
+  } else {
+    constexpr int UR = 4;
+    const int nload = npairs * GS;
+    for (int i0 = 0; i0 < nload; i0 += NT * UR) {
+      vu4 q[UR];
+      int vi[UR];
 #pragma unroll
-      for (int k = 0; k < VEC; ++k) {
-        const float y = scaled<E>(w[k], P);
-        if (y >= tau) push(y, sp.head + (int64_t)vi * VEC + k);
+      for (int u = 0; u < UR; ++u) {
+        const int i = i0 + u * NT + tid;
+        vi[u] = -1;
+        if (i < nload) {
+          const int pr = s_pairs[i / GS];
+          const int v = pr / kMaxGroups + ((pr % kMaxGroups) * GS + i % GS) * NT;
+          if (v < nvec) vi[u] = v;
+        }
+        if (vi[u] >= 0) q[u] = xv[vi[u]];
+      }
+#pragma unroll
+      for (int u = 0; u < UR; ++u) {
+        if (vi[u] < 0) continue;
+        float w[VEC];
+        E::unpack(q[u], w);
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) {
+          const float y = scaled<E>(w[k], P);
+          if (y >= tau) push(y, sp.head + (int64_t)vi[u] * VEC + k);
+        }
       }
     }
   }
@@ -360,7 +405,7 @@ __global__ __launch_bounds__(64 * W) void filter_fast_kernel(FilterParams P) {
   }
   __syncthreads();
   const int C = s_count;
-  if (C > kCandCap) {
+  if (C > kCandCap || C < P.top_k) {
     if (tid == 0) {
       RowInfo ri{};
       ri.flags = 1;
@@ -369,22 +414,15 @@ __global__ __launch_bounds__(64 * W) void filter_fast_kernel(FilterParams P) {
     return;
   }
 
-  // ---- exact top-k value among the candidates ---------------------------------
-  if (tid < 64) {
-    const uint32_t kk =
-        wave_kth_largest([&](int i) { return (uint32_t)(s_cand[i] >> 32); }, C, P.top_k);
-    if (tid == 0) s_thr = kk;
-  }
-  int N = 1;
-  while (N < C) N <<= 1;
-  block_bitonic_sort<NT>(s_cand, C, N);  // begins and ends with a barrier
-  const uint32_t thr_key = s_thr;
+  // ---- sort the candidates; the k-th largest is the exact top-k value ----------
+  block_rank_sort<NT>(s_cand, C);
+  const uint32_t thr_key = (uint32_t)(s_cand[C - P.top_k] >> 32);
   // kept-k = the sorted suffix with key >= thr_key
   int cnt = 0;
   for (int i = tid; i < C; i += NT) cnt += ((uint32_t)(s_cand[i] >> 32) >= thr_key) ? 1 : 0;
   __shared__ int redi[NT / 64];
   const int n_k = block_sum_i<NT>(cnt, redi);
-  finish_row<E, NT>(P, row, x, s_cand + (C - n_k), n_k, from_okey(thr_key), redf, &s_first);
+  if (tid < 64) finish_row<E>(P, row, s_cand + (C - n_k), n_k, from_okey(thr_key), yt, t);
 }
 
 // ---------------------------------------------------------------------------
@@ -720,7 +758,7 @@ __global__ __launch_bounds__(64 * W) void filter_mask_kernel(FilterParams P, voi
 }
 
 int fast_waves(int top_k) {
-  int w = 4;
+  int w = 8;
   while (w < 16 && 64 * w < top_k) w <<= 1;
   return w;
 }
@@ -730,9 +768,6 @@ int launch_fwd(const FilterParams& P, int64_t rows, hipStream_t st) {
   const bool fast = P.top_k >= 1 && P.top_k <= 1024 && P.top_k <= P.V;
   if (fast) {
     switch (fast_waves(P.top_k)) {
-      case 4:
-        hipLaunchKernelGGL((filter_fast_kernel<E, 4, 8>), dim3((unsigned)rows), dim3(256), 0, st, P);
-        break;
       case 8:
         hipLaunchKernelGGL((filter_fast_kernel<E, 8, 8>), dim3((unsigned)rows), dim3(512), 0, st, P);
         break;
