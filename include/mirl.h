@@ -97,7 +97,7 @@ int mirl_logprob_bwd(const void* logits, int dtype, int64_t B, int64_t R,
 /* ---------------------------------------------------------------------- */
 
 /* Kept entries saved per row by the filtered forward for the backward. */
-#define MIRL_FILTER_KEEP_CAP 256
+#define MIRL_FILTER_KEEP_CAP 1024
 
 /* Per-row result of the filtered forward.  The kept set is
  * { j : y_j > v_cut || (y_j == v_cut && j >= i_cut) }, y = the (temperature

@@ -133,7 +133,7 @@ SIGNATURES = {
     ),
 }
 
-FILTER_KEEP_CAP = 256  # MIRL_FILTER_KEEP_CAP
+FILTER_KEEP_CAP = 1024  # MIRL_FILTER_KEEP_CAP
 FILTER_ROW_INFO_BYTES = 24  # sizeof(mirl_filter_row_info)
 
 _lib: Optional[ctypes.CDLL] = None

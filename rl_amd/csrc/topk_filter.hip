@@ -32,9 +32,10 @@
 //
 // Backward: grad = (onehot(t) - p) * g on the kept set, 0 elsewhere, rounded
 // to the logits dtype, then divided by T in that dtype (the reference's
-// autograd chain through .to(float32) and div_).  When the forward saved the
-// kept list (<= kKeepCap entries) the row is written without reading the
-// logits; otherwise the row is re-read and the cut re-applied.
+// autograd chain through .to(float32) and div_).  A write-only pass zeroes the
+// rows; a second, small pass stores the kept entries from the kept list saved
+// by the forward (<= kKeepCap entries), without reading the logits.  Rows with
+// larger kept sets are re-read and rewritten whole by the second pass.
 
 #include "common.h"
 
@@ -642,98 +643,117 @@ __device__ __forceinline__ typename E::raw grad_to_dtype(float g32, const Filter
   return E::from_float(__fdiv_rn(round_trip<E>(g32), P.T));
 }
 
+// Phase 1 over a contiguous gradient: zeros over the whole [rows, V] block,
+// one 4 KB piece per workgroup with piece boundaries on 4 KB addresses.  Many
+// short workgroups dispatched in order keep the stores inside a narrow
+// address window, which is what lets a pure write stream reach the HBM write
+// rate; row-shaped workgroups over rows that are not 4 KB multiples fall
+// short of it.
+template <class E>
+__global__ __launch_bounds__(256) void filter_bwd_zero_flat_kernel(void* gin, int64_t n, int shift) {
+  using raw = typename E::raw;
+  raw* y = static_cast<raw*>(gin);
+  const RowSpan<E> ys(y, n);
+  vu4* yv = reinterpret_cast<vu4*>(y + ys.head);
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x - shift;
+  if (i >= 0 && i < ys.nvec) __builtin_nontemporal_store(vu4{0u, 0u, 0u, 0u}, yv + i);
+  if (blockIdx.x == 0) {
+    const raw zr = E::from_float(0.f);
+    if (threadIdx.x < ys.head) y[threadIdx.x] = zr;
+    if (ys.tail0 + threadIdx.x < n) y[ys.tail0 + threadIdx.x] = zr;
+  }
+}
+
+// Phase 1 over strided rows: zeros row by row.
 template <class E, int W>
-__global__ __launch_bounds__(64 * W) void filter_bwd_kernel(FilterBwdParams P) {
+__global__ __launch_bounds__(64 * W) void filter_bwd_zero_rows_kernel(FilterBwdParams P) {
   using raw = typename E::raw;
   constexpr int NT = 64 * W;
-  constexpr int VEC = E::kVec;
-  __shared__ int32_t s_idx[kKeepCap];
-  __shared__ float s_p[kKeepCap];
-  __shared__ uint32_t s_bits[2048];  // one bit per output vector (V <= 2^16 * VEC)
-
   const int64_t row = blockIdx.x;
   const int64_t b = row / P.Rt, r = row - b * P.Rt;
-  const int tid = threadIdx.x;
   raw* y = static_cast<raw*>(P.gin) + b * P.gisb + r * P.gisr;
-  const float gv = (r < P.R) ? P.g[b * P.gsb + r * P.gsr] : 0.f;
   const RowSpan<E> ys(y, P.V);
   vu4* yv = reinterpret_cast<vu4*>(y + ys.head);
-  const int nvec = (int)ys.nvec;
+  for (int64_t i = threadIdx.x; i < ys.nvec; i += NT)
+    __builtin_nontemporal_store(vu4{0u, 0u, 0u, 0u}, yv + i);
   const raw zr = E::from_float(0.f);
-  const vu4 zq = vu4{0u, 0u, 0u, 0u};
+  if (threadIdx.x < ys.head) y[threadIdx.x] = zr;
+  if (ys.tail0 + threadIdx.x < P.V) y[ys.tail0 + threadIdx.x] = zr;
+}
 
-  if (gv == 0.f) {
-    if (tid < ys.head) y[tid] = zr;
-    if (ys.tail0 + tid < P.V) y[ys.tail0 + tid] = zr;
-    for (int i = tid; i < nvec; i += NT) __builtin_nontemporal_store(zq, yv + i);
-    return;
-  }
+// Phase 2, one wave per row with a non-zero upstream gradient: with the saved
+// kept list each kept entry is stored on its own (phase 1 zeroed the rest);
+// otherwise the row is re-read and rewritten whole.
+template <class E>
+__global__ __launch_bounds__(256) void filter_bwd_scatter_kernel(FilterBwdParams P, int64_t rows) {
+  using raw = typename E::raw;
+  constexpr int VEC = E::kVec;
+  constexpr int U = 4;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int64_t b = row / P.Rt, r = row - b * P.Rt;
+  if (r >= P.R) return;
   const int64_t srow = b * P.R + r;
+  // independent loads, issued together
+  const float gv = P.g[b * P.gsb + r * P.gsr];
   const RowInfo ri = P.info[srow];
   const int64_t t = P.target[b * P.tsb + r * P.tsr];
-  const int nbits_words = (nvec + 31) / 32;
+  const int32_t j0 = P.kept_idx[srow * kKeepCap + lane];
+  const float p0 = P.kept_p[srow * kKeepCap + lane];
+  if (gv == 0.f) return;
+  raw* y = static_cast<raw*>(P.gin) + b * P.gisb + r * P.gisr;
 
-  if (ri.n_kept <= kKeepCap && nbits_words <= 2048) {
-    // kept list -> LDS, mark output vectors that hold a kept element
-    for (int i = tid; i < ri.n_kept; i += NT) {
-      s_idx[i] = P.kept_idx[srow * kKeepCap + i];
-      s_p[i] = P.kept_p[srow * kKeepCap + i];
-    }
-    for (int i = tid; i < nbits_words; i += NT) s_bits[i] = 0u;
-    __syncthreads();
-    for (int i = tid; i < ri.n_kept; i += NT) {
-      const int64_t j = s_idx[i];
-      if (j >= ys.head && j < ys.tail0) {
-        const int v = (int)((j - ys.head) / VEC);
-        atomicOr(&s_bits[v >> 5], 1u << (v & 31));
-      }
-    }
-    __syncthreads();
-    auto value_at = [&](int64_t j) -> raw {
-      for (int i = 0; i < ri.n_kept; ++i)
-        if (s_idx[i] == j) return grad_to_dtype<E>(((j == t) ? 1.f - s_p[i] : -s_p[i]) * gv, P);
-      return zr;
-    };
-    for (int i = tid; i < nvec; i += NT)
-      if (!(s_bits[i >> 5] & (1u << (i & 31)))) __builtin_nontemporal_store(zq, yv + i);
-    if (tid < ys.head) y[tid] = value_at(tid);
-    if (ys.tail0 + tid < P.V) y[ys.tail0 + tid] = value_at(ys.tail0 + tid);
-    // vectors holding kept elements: written whole by the lane of their
-    // lowest-index kept element
-    for (int i = tid; i < ri.n_kept; i += NT) {
-      const int64_t j = s_idx[i];
-      if (j < ys.head || j >= ys.tail0) continue;
-      const int v = (int)((j - ys.head) / VEC);
-      bool owner = true;
-      for (int q = 0; q < ri.n_kept; ++q) {
-        const int64_t jq = s_idx[q];
-        if (jq < j && jq >= ys.head && jq < ys.tail0 && (int)((jq - ys.head) / VEC) == v) {
-          owner = false;
-          break;
-        }
-      }
-      if (!owner) continue;
-      raw vals[VEC];
-#pragma unroll
-      for (int k = 0; k < VEC; ++k) vals[k] = value_at(ys.head + (int64_t)v * VEC + k);
-      vu4 out;
-      __builtin_memcpy(&out, vals, sizeof(out));
-      yv[v] = out;
+  if (ri.n_kept <= kKeepCap) {
+    for (int i = lane; i < ri.n_kept; i += 64) {
+      const int64_t j = (i == lane) ? j0 : P.kept_idx[srow * kKeepCap + i];
+      const float p = (i == lane) ? p0 : P.kept_p[srow * kKeepCap + i];
+      y[j] = grad_to_dtype<E>(((j == t) ? 1.f - p : -p) * gv, P);
     }
     return;
   }
 
-  // recompute path: re-read the row and re-apply the cut
+  // whole row: re-read the logits and re-apply the cut
   const raw* x = static_cast<const raw*>(P.logits) + b * P.sb + r * P.sr;
-  for (int64_t j = tid; j < P.V; j += NT) {
-    const float yy = P.has_t ? round_trip<E>(__fdiv_rn(E::load(x + j), P.T)) : E::load(x + j);
+  auto grad_of = [&](float xf, int64_t j) -> raw {
+    const float yy = P.has_t ? round_trip<E>(__fdiv_rn(xf, P.T)) : xf;
     float g32 = 0.f;
     if (kept_lex(yy, j, ri.v_cut, ri.i_cut)) {
       const float p = expf((yy - ri.m) - ri.logsum);
       g32 = ((j == t) ? 1.f - p : -p) * gv;
     }
-    y[j] = grad_to_dtype<E>(g32, P);
+    return grad_to_dtype<E>(g32, P);
+  };
+  const RowSpan<E> xs(x, P.V);
+  const RowSpan<E> ys(y, P.V);
+  if (xs.head != ys.head) {
+    for (int64_t j = lane; j < P.V; j += 64) y[j] = grad_of(E::load(x + j), j);
+    return;
   }
+  const vu4* xv = reinterpret_cast<const vu4*>(x + xs.head);
+  vu4* yv = reinterpret_cast<vu4*>(y + ys.head);
+  const int64_t nvec = ys.nvec;
+  for (int64_t i0 = lane; i0 < nvec; i0 += 64 * U) {
+    vu4 q[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (i0 + u * 64 < nvec) q[u] = __builtin_nontemporal_load(xv + i0 + u * 64);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = i0 + u * 64;
+      if (i >= nvec) break;
+      float w[VEC];
+      E::unpack(q[u], w);
+      raw vals[VEC];
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) vals[k] = grad_of(w[k], ys.head + i * VEC + k);
+      vu4 out;
+      __builtin_memcpy(&out, vals, sizeof(out));
+      __builtin_nontemporal_store(out, yv + i);
+    }
+  }
+  if (lane < ys.head) y[lane] = grad_of(E::load(x + lane), lane);
+  for (int64_t j = ys.tail0 + lane; j < P.V; j += 64) y[j] = grad_of(E::load(x + j), j);
 }
 
 // filtered logits (-inf outside the kept set) and the keep mask
@@ -780,6 +800,31 @@ int launch_fwd(const FilterParams& P, int64_t rows, hipStream_t st) {
   hipLaunchKernelGGL((filter_general_kernel<E>), dim3((unsigned)rows), dim3(kGeneralThreads), 0, st,
                      P, fast ? 0 : 1);
   return check_launch("filter_general_kernel");
+}
+
+template <class E>
+int launch_bwd(const FilterBwdParams& P, int64_t B, int64_t rows, hipStream_t st) {
+  const bool contiguous = P.gisr == P.V && (B == 1 || P.gisb == P.Rt * P.V);
+  if (contiguous) {
+    const int64_t n = rows * P.V;
+    const uintptr_t a = reinterpret_cast<uintptr_t>(P.gin);
+    const uintptr_t a16 = (a + 15u) & ~uintptr_t(15);
+    const int to4k = (int)(((4096u - (a16 & 4095u)) & 4095u) / 16u);  // vectors before a 4 KB boundary
+    const int shift = (256 - to4k) & 255;
+    const int64_t nvec = (n * (int64_t)sizeof(typename E::raw)) / 16 + 1;
+    const int64_t grid = (nvec + shift + 255) / 256;
+    MIRL_REQUIRE(grid < (int64_t(1) << 31), "gradient too large (%lld elements)", (long long)n);
+    hipLaunchKernelGGL((filter_bwd_zero_flat_kernel<E>), dim3((unsigned)grid), dim3(256), 0, st,
+                       P.gin, n, shift);
+  } else {
+    hipLaunchKernelGGL((filter_bwd_zero_rows_kernel<E, 16>), dim3((unsigned)rows), dim3(1024), 0,
+                       st, P);
+  }
+  if (int e = check_launch("filter_bwd_zero_kernel")) return e;
+  if (P.R == 0) return MIRL_OK;
+  hipLaunchKernelGGL((filter_bwd_scatter_kernel<E>), dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
+                     st, P, rows);
+  return check_launch("filter_bwd_scatter_kernel");
 }
 
 int check_filter_args(int dtype, int64_t B, int64_t R, int64_t V, int top_k, double top_p,
@@ -896,13 +941,9 @@ extern "C" int mirl_filtered_logprob_bwd(const void* logits, int dtype, int64_t 
   P.gisb = gi_stride_b;
   P.gisr = gi_stride_r;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (dtype == MIRL_DTYPE_F32)
-    hipLaunchKernelGGL((filter_bwd_kernel<F32, 16>), dim3((unsigned)rows), dim3(1024), 0, st, P);
-  else if (dtype == MIRL_DTYPE_BF16)
-    hipLaunchKernelGGL((filter_bwd_kernel<BF16, 16>), dim3((unsigned)rows), dim3(1024), 0, st, P);
-  else
-    hipLaunchKernelGGL((filter_bwd_kernel<F16, 16>), dim3((unsigned)rows), dim3(1024), 0, st, P);
-  return check_launch("mirl_filtered_logprob_bwd");
+  if (dtype == MIRL_DTYPE_F32) return launch_bwd<F32>(P, B, rows, st);
+  if (dtype == MIRL_DTYPE_BF16) return launch_bwd<BF16>(P, B, rows, st);
+  return launch_bwd<F16>(P, B, rows, st);
 }
 
 extern "C" int mirl_top_k_top_p_mask(const void* logits, int dtype, int64_t N, int64_t V,
