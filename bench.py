@@ -362,7 +362,16 @@ def bench_workload(args) -> None:
         from rl_amd.distributed.batched_data_dict import BatchedDataDict
 
         if not dist.is_initialized():
-            dist.init_process_group("gloo", store=dist.HashStore(), rank=0, world_size=1)
+            # gloo reports its (empty) peer set on stdout; keep stdout for the JSON line
+            sys.stdout.flush()
+            saved = os.dup(1)
+            os.dup2(2, 1)
+            try:
+                dist.init_process_group("gloo", store=dist.HashStore(), rank=0, world_size=1)
+            finally:
+                sys.stdout.flush()
+                os.dup2(saved, 1)
+                os.close(saved)
         group = dist.group.WORLD
         d = workloads.packed_grpo_kl_bf16(device=dev)
         logits, cu = d["logits"], d["cu_seqlens"]

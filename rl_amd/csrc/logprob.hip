@@ -11,7 +11,9 @@
 // streams 16-byte vectors (8 bf16 / 4 fp32) at stride 64*W vectors, U vectors
 // in flight per lane, and keeps a private (offset, sum) pair; lanes and waves
 // are merged once at the end of the row.  Nothing of size V is ever written
-// in the forward.
+// in the forward.  The backward walks the gradient as one flat block of 8 KB
+// pieces when logits and gradient share a contiguous layout, and row by row
+// (zero rows first, then rows with a non-zero upstream gradient) otherwise.
 
 #include "common.h"
 
@@ -249,6 +251,77 @@ __global__ __launch_bounds__(64 * W) void logprob_bwd_kernel(
   for (; i < nvec; i += NT) __builtin_nontemporal_store(grad_vec(__builtin_nontemporal_load(xv + i), i), yv + i);
 }
 
+// Backward over a contiguous [B, Rt, V] gradient whose logits share its layout
+// (V a multiple of the vector width, both 16-byte aligned): one 8 KB block of
+// the flat gradient per workgroup (two 16-byte vectors per lane, 4 KB apart),
+// block boundaries on 4 KB addresses.  Each lane finds the rows of its two
+// vectors and loads their upstream gradient, statistics and target together;
+// vectors of rows with a zero upstream gradient are written as zeros without
+// reading the logits, the others get (onehot - p) * g.  Short workgroups
+// dispatched in order keep the traffic inside a narrow address window:
+// measured 5.95 TB/s on the GRPO rows and 5.9 on fully active rows, against
+// 5.4 for one workgroup per row.  Arithmetic is that of logprob_bwd_kernel.
+template <class E>
+__global__ __launch_bounds__(256) void logprob_bwd_flat_kernel(
+    const typename E::raw* __restrict__ logits, int64_t R, uint32_t Rt, uint32_t nvr,
+    uint32_t nvec, int shift, const int64_t* __restrict__ target, int64_t tsb, int64_t tsr,
+    int64_t vs, int64_t ve, int64_t V, const float* __restrict__ stats,
+    const float* __restrict__ g, int64_t gsb, int64_t gsr, typename E::raw* gin) {
+  constexpr int VEC = E::kVec;
+  constexpr int U = 2;
+  vu4* yv = reinterpret_cast<vu4*>(gin);
+  const vu4* xv = reinterpret_cast<const vu4*>(logits);
+  const int64_t base = (int64_t)blockIdx.x * (256 * U) + threadIdx.x - shift;
+  bool ok[U];
+  uint32_t row[U];
+  float gv[U], M[U], LS[U];
+  int64_t t[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t i = base + u * 256;
+    ok[u] = i >= 0 && i < (int64_t)nvec;
+    row[u] = (ok[u] ? (uint32_t)i : 0u) / nvr;
+    const uint32_t b = row[u] / Rt, r = row[u] - b * Rt;
+    gv[u] = 0.f;
+    M[u] = LS[u] = 0.f;
+    t[u] = -1;
+    if (ok[u] && (int64_t)r < R) {
+      const int64_t srow = (int64_t)b * R + r;
+      gv[u] = g[(int64_t)b * gsb + (int64_t)r * gsr];
+      M[u] = stats[2 * srow];
+      LS[u] = stats[2 * srow + 1];
+      t[u] = target[(int64_t)b * tsb + (int64_t)r * tsr];
+    }
+  }
+  vu4 q[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+    if (ok[u] && gv[u] != 0.f) q[u] = __builtin_nontemporal_load(xv + base + u * 256);
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    if (!ok[u]) continue;
+    const int64_t i = base + u * 256;
+    if (gv[u] == 0.f) {
+      // (onehot - p) * 0 == 0: written without reading the logits
+      __builtin_nontemporal_store(vu4{0u, 0u, 0u, 0u}, yv + i);
+      continue;
+    }
+    const bool tmask = (t[u] < vs) || (t[u] >= ve) || (t[u] - vs >= V);
+    const int64_t j0 = (int64_t)((uint32_t)i - row[u] * nvr) * VEC;  // row element of lane 0
+    const int tj = tmask ? -1 : (int)(t[u] - vs - j0);               // target lane, if here
+    float w[VEC];
+    E::unpack(q[u], w);
+    const float ng = -gv[u];
+    float o[VEC];
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) o[k] = fast_exp2(((w[k] - M[u]) - LS[u]) * kLog2e) * ng;
+#pragma unroll
+    for (int k = 0; k < VEC; ++k)
+      if (k == tj) o[k] = (1.f - fast_exp2(((w[k] - M[u]) - LS[u]) * kLog2e)) * gv[u];
+    __builtin_nontemporal_store(E::pack(o), yv + i);
+  }
+}
+
 // Waves per row for the forward: at least 4 (fewer rows in flight at a time
 // keeps the concurrently streamed address window narrower, measured +5% read
 // bandwidth over one wave per row), more when there are too few rows to give
@@ -291,6 +364,26 @@ void dispatch_bwd(int64_t rows, hipStream_t st, const void* logits, int64_t R, i
                   int64_t gsb, int64_t gsr, void* gin, int64_t gisb, int64_t gisr) {
   constexpr int W = kBwdWaves, U = 4;
   using raw = typename E::raw;
+  constexpr int VEC = E::kVec;
+  // flat path: gradient and logits share one contiguous, 16-byte aligned
+  // [B, Rt, V] layout with whole vectors per row, and the vector count fits
+  // 32-bit indexing
+  const uintptr_t ya = reinterpret_cast<uintptr_t>(gin), xa = reinterpret_cast<uintptr_t>(logits);
+  const bool contiguous = gisr == V && (rows == Rt || gisb == Rt * V);
+  const bool shared_layout = R == 0 || (sr == gisr && (rows == Rt || sb == gisb));
+  const int64_t nvr = V / VEC;
+  const int64_t nvec = rows * nvr;
+  if (V % VEC == 0 && contiguous && shared_layout && (ya & 15u) == 0 && (xa & 15u) == 0 &&
+      nvec + 512 < (int64_t(1) << 32) && rows < (int64_t(1) << 31)) {
+    const int to4k = (int)(((4096u - (ya & 4095u)) & 4095u) / 16u);  // vectors before a 4 KB boundary
+    const int shift = (256 - to4k) & 255;
+    const int64_t grid = (nvec + shift + 511) / 512;
+    hipLaunchKernelGGL((logprob_bwd_flat_kernel<E>), dim3((unsigned)grid), dim3(256), 0, st,
+                       static_cast<const raw*>(logits), R, (uint32_t)Rt, (uint32_t)nvr,
+                       (uint32_t)nvec, shift, target, tsb, tsr, vs, ve, V, stats, g, gsb, gsr,
+                       static_cast<raw*>(gin));
+    return;
+  }
   hipLaunchKernelGGL((logprob_bwd_kernel<E, W, U, kZeroRows>), dim3((unsigned)rows), dim3(64 * W),
                      0, st, static_cast<const raw*>(logits), R, Rt, V, sb, sr, target, tsb, tsr,
                      vs, ve, stats, g, gsb, gsr, static_cast<raw*>(gin), gisb, gisr);
