@@ -44,7 +44,7 @@ namespace {
 
 constexpr int kCandCap = 1024;  // candidates held in LDS by the fast path
 constexpr int kKeepCap = MIRL_FILTER_KEEP_CAP;
-constexpr int kMaxGroups = 16;  // vector groups per lane in the fast path
+constexpr int kMaxGroups = 20;  // vector groups per lane in the fast path
 constexpr int kGeneralThreads = 1024;
 
 // Per-row result of the forward (layout documented as mirl_filter_row_info).
@@ -278,9 +278,19 @@ __global__ __launch_bounds__(64 * W) void filter_fast_kernel(FilterParams P) {
   const RowSpan<E> sp(x, P.V);
   const vu4* xv = reinterpret_cast<const vu4*>(x + sp.head);
   const int nvec = (int)sp.nvec;
-  // vectors of lane tid: tid + j*NT, j < J; groups of GS consecutive j
+  // vectors of lane tid: tid + j*NT, j < Jmax, in groups of GS consecutive j
+  // (at most kMaxGroups groups).  Small groups keep the re-read short: each
+  // re-read vector costs a whole memory line.  GS is a power of two below U
+  // (whole groups inside one batch of U loads) or a multiple of U.
   const int Jmax = (nvec + NT - 1) / NT;
-  const int GS = U * ((Jmax + kMaxGroups * U - 1) / (kMaxGroups * U));
+  int GS = (Jmax + kMaxGroups - 1) / kMaxGroups;
+  if (GS < U) {
+    int p2 = 1;
+    while (p2 < GS) p2 <<= 1;
+    GS = p2;
+  } else {
+    GS = U * ((GS + U - 1) / U);
+  }
   const int G = (Jmax + GS - 1) / GS;
   if (tid == 0) {
     s_count = 0;
@@ -299,24 +309,45 @@ __global__ __launch_bounds__(64 * W) void filter_fast_kernel(FilterParams P) {
   int curg = 0;
   int j = 0;
   for (; tid + (j + U - 1) * NT < nvec; j += U) {
-    const int g = j / GS;
-    if (g != curg) {
-      s_gkey[curg * NT + tid] = okey_hi_up(cur);
-      lmax = fmaxf(lmax, cur);
-      curg = g;
-      cur = -INFINITY;
-    }
     vu4 q[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) q[u] = __builtin_nontemporal_load(xv + tid + (j + u) * NT);
+    float mm[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       float w[VEC];
       E::unpack(q[u], w);
+      mm[u] = w[0];
 #pragma unroll
-      for (int k = 0; k < VEC; ++k) cur = fmaxf(cur, w[k]);
+      for (int k = 1; k < VEC; ++k) mm[u] = fmaxf(mm[u], w[k]);
+    }
+    if (GS >= U) {
+      const int g = j / GS;
+      if (g != curg) {
+        s_gkey[curg * NT + tid] = okey_hi_up(cur);
+        lmax = fmaxf(lmax, cur);
+        curg = g;
+        cur = -INFINITY;
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) cur = fmaxf(cur, mm[u]);
+    } else {
+      // U / GS whole groups: reduce pairwise, mm[u] holds group u / GS at u % GS == 0
+#pragma unroll
+      for (int h = 1; h < U; h <<= 1)
+        if (h < GS) {
+#pragma unroll
+          for (int u = 0; u + h < U; u += 2 * h) mm[u] = fmaxf(mm[u], mm[u + h]);
+        }
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (u % GS == 0) {
+          s_gkey[((j + u) / GS) * NT + tid] = okey_hi_up(mm[u]);
+          lmax = fmaxf(lmax, mm[u]);
+        }
     }
   }
+  if (GS < U) curg = j / GS;  // every group so far is complete and stored
   for (; tid + j * NT < nvec; ++j) {
     const int g = j / GS;
     if (g != curg) {
@@ -330,8 +361,10 @@ __global__ __launch_bounds__(64 * W) void filter_fast_kernel(FilterParams P) {
 #pragma unroll
     for (int k = 0; k < VEC; ++k) cur = fmaxf(cur, w[k]);
   }
-  s_gkey[curg * NT + tid] = okey_hi_up(cur);
-  lmax = fmaxf(lmax, cur);
+  if (curg < G) {
+    s_gkey[curg * NT + tid] = okey_hi_up(cur);
+    lmax = fmaxf(lmax, cur);
+  }
   for (int g = curg + 1; g < G; ++g) s_gkey[g * NT + tid] = okey_hi_up(-INFINITY);
   const float hv = (tid < sp.head) ? E::load(x + tid) : -INFINITY;
   const float tv = (sp.tail0 + tid < P.V) ? E::load(x + sp.tail0 + tid) : -INFINITY;
