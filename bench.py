@@ -162,13 +162,7 @@ def main() -> None:
     fwd_gbps = fwd_bytes / (fwd_ms * 1e-3) / 1e9
     step_gbps = (fwd_bytes + bwd_bytes) / (ms_step * 1e-3) / 1e9
 
-    traffic = None
-    tf = ROOT / "profiles" / "traffic_logprob_bwd_grpo_bf16.json"
-    if tf.exists():
-        try:
-            traffic = json.loads(tf.read_text()).get("hbm_bytes_per_launch")
-        except Exception:
-            traffic = None
+    traffic = _traffic("grpo")
 
     if args.calibrate_copy_gib > 0:
         n = int(args.calibrate_copy_gib * (1 << 30)) // 4
@@ -261,10 +255,23 @@ def _timed(step, steps: int, warmup: int):
     return (t1 - t0) * 1e3 / steps, ms
 
 
-def _roofline(kernel: str, nbytes: float, ms: float) -> dict:
+def _traffic(workload: str):
+    """HBM bytes per call of the roofline entry point, from the committed rocprof counter runs.
+
+    profiles/traffic.json holds FETCH_SIZE + WRITE_SIZE per dispatch, scaled by
+    what the same counters read for a 1 GiB device copy; None when absent.
+    """
+    tf = ROOT / "profiles" / "traffic.json"
+    try:
+        return json.loads(tf.read_text())["workloads"][workload]["hbm_bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def _roofline(kernel: str, nbytes: float, ms: float, workload: str) -> dict:
     gbps = nbytes / (ms * 1e-3) / 1e9 if ms > 0 else 0.0
     return {"kernel": kernel, "bound": "hbm", "achieved": gbps, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-            "frac": gbps / PEAK_HBM_GBPS, "traffic": None, "algorithmic_bytes": nbytes}
+            "frac": gbps / PEAK_HBM_GBPS, "traffic": _traffic(workload), "algorithmic_bytes": nbytes}
 
 
 def bench_workload(args) -> None:
@@ -298,7 +305,7 @@ def bench_workload(args) -> None:
         ms_step, ms = _timed(step, args.steps, args.warmup)
         rows = B * (S - 1)
         esz = 4
-        roof = _roofline("mirl_logprob_fwd", rows * V * esz, ms.get("mirl_logprob_fwd", 0.0))
+        roof = _roofline("mirl_logprob_fwd", rows * V * esz, ms.get("mirl_logprob_fwd", 0.0), w)
         step_bytes = rows * V * esz
         cfg = {"workload": "logprob_fwd_f32", "logits": [B, S, V], "next_token_rows": rows,
                "rotating_copies": len(copies)}
@@ -318,7 +325,7 @@ def bench_workload(args) -> None:
         active = int((g != 0).sum().item())
         esz = 2
         bwd_bytes = (active + B * S) * V * esz
-        roof = _roofline("mirl_logprob_bwd", bwd_bytes, ms.get("mirl_logprob_bwd", 0.0))
+        roof = _roofline("mirl_logprob_bwd", bwd_bytes, ms.get("mirl_logprob_bwd", 0.0), w)
         step_bytes = rows * V * esz + bwd_bytes
         extra["logprob_fwd_gbps"] = rows * V * esz / (ms.get("mirl_logprob_fwd", 1e9) * 1e-3) / 1e9
         cfg = {"workload": "long_context_chunked_logprob_fwd_bwd", "logits": [B, S, V], "chunk_size": 4096,
@@ -342,7 +349,7 @@ def bench_workload(args) -> None:
         esz = 2
         fwd_bytes, bwd_bytes = rows * V * esz, B * S * V * esz
         fwd_ms, bwd_ms = ms.get("mirl_filtered_logprob_fwd", 0.0), ms.get("mirl_filtered_logprob_bwd", 0.0)
-        roof = _roofline("mirl_filtered_logprob_fwd", fwd_bytes, fwd_ms)
+        roof = _roofline("mirl_filtered_logprob_fwd", fwd_bytes, fwd_ms, w)
         extra["filtered_bwd_gbps"] = bwd_bytes / (bwd_ms * 1e-3) / 1e9 if bwd_ms > 0 else None
         step_bytes = fwd_bytes + bwd_bytes
         cfg = {"workload": "topk_topp_temperature_filtered_logprob_fwd_bwd", "logits": [B, S, V],
@@ -411,7 +418,7 @@ def bench_workload(args) -> None:
         esz = 2
         fwd_bytes = rows * V * esz
         bwd_bytes = (active + T) * V * esz
-        roof = _roofline("mirl_logprob_bwd", bwd_bytes, ms.get("mirl_logprob_bwd", 0.0))
+        roof = _roofline("mirl_logprob_bwd", bwd_bytes, ms.get("mirl_logprob_bwd", 0.0), w)
         extra["logprob_fwd_gbps"] = fwd_bytes / (ms.get("mirl_logprob_fwd", 1e9) * 1e-3) / 1e9
         step_bytes = fwd_bytes + bwd_bytes
         cfg = {"workload": "packed_grpo_kl_fused_wrapper", "logits": [1, T, V], "sequences": n_seq,
