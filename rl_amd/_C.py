@@ -142,12 +142,18 @@ _lock = threading.Lock()
 # Optional per-launch timing: when set, wrapped entry points record a pair of
 # events on the launch stream around each call, keyed by entry-point name.
 _timer: Optional[dict] = None
+_timer_names: Optional[frozenset] = None
 
 
-def enable_launch_timing() -> dict:
-    """Start recording (start, end) torch.cuda.Event pairs per entry point; returns the dict."""
-    global _timer
+def enable_launch_timing(names: Optional[list] = None) -> dict:
+    """Start recording (start, end) torch.cuda.Event pairs per entry point; returns the dict.
+
+    `names` restricts the recording to those entry points (each event pair
+    costs a few microseconds of GPU time between neighbouring launches).
+    """
+    global _timer, _timer_names
     _timer = {}
+    _timer_names = None if names is None else frozenset(names)
     return _timer
 
 
@@ -159,15 +165,16 @@ def disable_launch_timing() -> None:
 class _Timed:
     def __init__(self, name: str, dev: torch.device):
         self.name, self.dev = name, dev
+        self.ev = None
 
     def __enter__(self):
-        if _timer is not None:
+        if _timer is not None and (_timer_names is None or self.name in _timer_names):
             self.ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
             self.ev[0].record(torch.cuda.current_stream(self.dev))
         return self
 
     def __exit__(self, *exc):
-        if _timer is not None and exc[0] is None:
+        if self.ev is not None and _timer is not None and exc[0] is None:
             self.ev[1].record(torch.cuda.current_stream(self.dev))
             _timer.setdefault(self.name, []).append(self.ev)
         return False
