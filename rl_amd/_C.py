@@ -291,6 +291,15 @@ class _OnDevice:
         return False
 
 
+def _launch(name: str, dev: torch.device, *args):
+    """Call entry point `name` with `dev` current (and timed when launch timing is on)."""
+    fn = getattr(_lib if _lib is not None else load(), name)
+    if _timer is None and (dev.index is None or dev.index == torch.cuda.current_device()):
+        return fn(*args)
+    with _OnDevice(dev), _Timed(name, dev):
+        return fn(*args)
+
+
 def _dtype_code(t: torch.Tensor) -> int:
     try:
         return DTYPE_CODES[t.dtype]
@@ -323,12 +332,12 @@ def logprob_fwd(
     V = logits.shape[-1]
     assert logits.stride(-1) == 1 and out.is_contiguous()
     assert stats is None or stats.is_contiguous()
-    with _OnDevice(dev), _Timed("mirl_logprob_fwd", dev):
-        st = load().mirl_logprob_fwd(
-            logits.data_ptr(), _dtype_code(logits), B, R, V, logits.stride(0), logits.stride(1),
-            target.data_ptr(), target.stride(0), target.stride(1), int(vocab_start),
-            int(vocab_end), out.data_ptr(), _ptr(stats), _stream(dev),
-        )
+    st = _launch(
+        "mirl_logprob_fwd", dev,
+        logits.data_ptr(), _dtype_code(logits), B, R, V, logits.stride(0), logits.stride(1),
+        target.data_ptr(), target.stride(0), target.stride(1), int(vocab_start),
+        int(vocab_end), out.data_ptr(), _ptr(stats), _stream(dev),
+    )
     _check(st, "mirl_logprob_fwd")
 
 
@@ -351,14 +360,14 @@ def logprob_bwd(
     V = logits.shape[-1]
     assert grad_in.stride(-1) == 1 and logits.stride(-1) == 1
     assert grad_in.dtype == logits.dtype and grad_out.dtype == torch.float32
-    with _OnDevice(dev), _Timed("mirl_logprob_bwd", dev):
-        st = load().mirl_logprob_bwd(
-            logits.data_ptr(), _dtype_code(logits), B, R, Rt, V, logits.stride(0),
-            logits.stride(1), target.data_ptr(), target.stride(0), target.stride(1),
-            int(vocab_start), int(vocab_end), stats.data_ptr(), grad_out.data_ptr(),
-            grad_out.stride(0), grad_out.stride(1), grad_in.data_ptr(), grad_in.stride(0),
-            grad_in.stride(1), _stream(dev),
-        )
+    st = _launch(
+        "mirl_logprob_bwd", dev,
+        logits.data_ptr(), _dtype_code(logits), B, R, Rt, V, logits.stride(0),
+        logits.stride(1), target.data_ptr(), target.stride(0), target.stride(1),
+        int(vocab_start), int(vocab_end), stats.data_ptr(), grad_out.data_ptr(),
+        grad_out.stride(0), grad_out.stride(1), grad_in.data_ptr(), grad_in.stride(0),
+        grad_in.stride(1), _stream(dev),
+    )
     _check(st, "mirl_logprob_bwd")
 
 
@@ -395,14 +404,14 @@ def clipped_pg(
     grad_unf = torch.empty((B, L), dtype=dtype, device=dev) if unfiltered is not None else None
     lib = load()
     ws = torch.empty(int(lib.mirl_clipped_pg_workspace_elems(B)), dtype=dtype, device=dev)
-    with _OnDevice(dev), _Timed("mirl_clipped_pg", dev):
-        st = lib.mirl_clipped_pg(
-            ctypes.byref(cfg), _dtype_code(curr), B, L, _view(curr), _view(unfiltered),
-            _view(token_mask), _view(advantages), _view(prev), _view(generation),
-            _view(reference), _view(support_mask), sample_mask.data_ptr(), _ptr(rewards),
-            global_valid_seqs.data_ptr(), global_valid_toks.data_ptr(), metrics.data_ptr(),
-            grad_curr.data_ptr(), _ptr(grad_unf), ws.data_ptr(), _stream(dev),
-        )
+    st = _launch(
+        "mirl_clipped_pg", dev,
+        ctypes.byref(cfg), _dtype_code(curr), B, L, _view(curr), _view(unfiltered),
+        _view(token_mask), _view(advantages), _view(prev), _view(generation),
+        _view(reference), _view(support_mask), sample_mask.data_ptr(), _ptr(rewards),
+        global_valid_seqs.data_ptr(), global_valid_toks.data_ptr(), metrics.data_ptr(),
+        grad_curr.data_ptr(), _ptr(grad_unf), ws.data_ptr(), _stream(dev),
+    )
     _check(st, "mirl_clipped_pg")
     return metrics, grad_curr, grad_unf
 
@@ -431,13 +440,13 @@ def grpo_advantage(
     base = torch.empty_like(adv) if want_stats else None
     std = torch.empty_like(adv) if want_stats else None
     trivial = torch.empty(B, dtype=torch.bool, device=dev) if want_stats else None
-    with _OnDevice(dev), _Timed("mirl_grpo_advantage", dev):
-        st = load().mirl_grpo_advantage(
-            prompts.data_ptr(), B, K, prompts.stride(0), rewards.data_ptr(), _ptr(std_rewards),
-            _ptr(valid_mask),
-            int(bool(leave_one_out)), int(bool(normalize)), adv.data_ptr(), _ptr(base), _ptr(std),
-            _ptr(trivial), _stream(dev),
-        )
+    st = _launch(
+        "mirl_grpo_advantage", dev,
+        prompts.data_ptr(), B, K, prompts.stride(0), rewards.data_ptr(), _ptr(std_rewards),
+        _ptr(valid_mask),
+        int(bool(leave_one_out)), int(bool(normalize)), adv.data_ptr(), _ptr(base), _ptr(std),
+        _ptr(trivial), _stream(dev),
+    )
     _check(st, "mirl_grpo_advantage")
     return adv, base, std, trivial
 
@@ -466,13 +475,13 @@ def filtered_fwd(
     V = logits.shape[-1]
     assert logits.stride(-1) == 1 and (out is None or out.is_contiguous())
     info, kidx, kp = _filter_scratch(B * R, dev)
-    with _OnDevice(dev), _Timed("mirl_filtered_logprob_fwd", dev):
-        st = load().mirl_filtered_logprob_fwd(
-            logits.data_ptr(), _dtype_code(logits), B, R, V, logits.stride(0), logits.stride(1),
-            target.data_ptr(), target.stride(0), target.stride(1), float(temperature),
-            int(top_k), float(top_p), _ptr(out), info.data_ptr(), kidx.data_ptr(),
-            kp.data_ptr(), _stream(dev),
-        )
+    st = _launch(
+        "mirl_filtered_logprob_fwd", dev,
+        logits.data_ptr(), _dtype_code(logits), B, R, V, logits.stride(0), logits.stride(1),
+        target.data_ptr(), target.stride(0), target.stride(1), float(temperature),
+        int(top_k), float(top_p), _ptr(out), info.data_ptr(), kidx.data_ptr(),
+        kp.data_ptr(), _stream(dev),
+    )
     _check(st, "mirl_filtered_logprob_fwd")
     return info, kidx, kp
 
@@ -492,14 +501,14 @@ def filtered_bwd(
     Rt = grad_in.shape[1]
     V = logits.shape[-1]
     assert grad_in.dtype == logits.dtype and grad_out.dtype == torch.float32
-    with _OnDevice(dev), _Timed("mirl_filtered_logprob_bwd", dev):
-        st = load().mirl_filtered_logprob_bwd(
-            logits.data_ptr(), _dtype_code(logits), B, R, Rt, V, logits.stride(0),
-            logits.stride(1), target.data_ptr(), target.stride(0), target.stride(1),
-            float(temperature), info.data_ptr(), kidx.data_ptr(), kp.data_ptr(),
-            grad_out.data_ptr(), grad_out.stride(0), grad_out.stride(1), grad_in.data_ptr(),
-            grad_in.stride(0), grad_in.stride(1), _stream(dev),
-        )
+    st = _launch(
+        "mirl_filtered_logprob_bwd", dev,
+        logits.data_ptr(), _dtype_code(logits), B, R, Rt, V, logits.stride(0),
+        logits.stride(1), target.data_ptr(), target.stride(0), target.stride(1),
+        float(temperature), info.data_ptr(), kidx.data_ptr(), kp.data_ptr(),
+        grad_out.data_ptr(), grad_out.stride(0), grad_out.stride(1), grad_in.data_ptr(),
+        grad_in.stride(0), grad_in.stride(1), _stream(dev),
+    )
     _check(st, "mirl_filtered_logprob_bwd")
 
 
@@ -511,11 +520,11 @@ def top_k_top_p_mask(x2d: torch.Tensor, top_k: int, top_p: float):
     info, kidx, kp = _filter_scratch(N, dev)
     filt = torch.empty((N, V), dtype=x2d.dtype, device=dev)
     keep = torch.empty((N, V), dtype=torch.bool, device=dev)
-    with _OnDevice(dev), _Timed("mirl_top_k_top_p_mask", dev):
-        st = load().mirl_top_k_top_p_mask(
-            x2d.data_ptr(), _dtype_code(x2d), N, V, x2d.stride(0), int(top_k), float(top_p),
-            info.data_ptr(), kidx.data_ptr(), kp.data_ptr(), filt.data_ptr(), filt.stride(0),
-            keep.data_ptr(), keep.stride(0), _stream(dev),
-        )
+    st = _launch(
+        "mirl_top_k_top_p_mask", dev,
+        x2d.data_ptr(), _dtype_code(x2d), N, V, x2d.stride(0), int(top_k), float(top_p),
+        info.data_ptr(), kidx.data_ptr(), kp.data_ptr(), filt.data_ptr(), filt.stride(0),
+        keep.data_ptr(), keep.stride(0), _stream(dev),
+    )
     _check(st, "mirl_top_k_top_p_mask")
     return filt, keep

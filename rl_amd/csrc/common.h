@@ -45,6 +45,7 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 struct F32 {
   using raw = float;
   static constexpr int kVec = 4;  // elements per 16-byte vector
+  static constexpr uint32_t kNegInf2 = 0xFF800000u;  // one 32-bit word of -inf elements
   __device__ __forceinline__ static float load(const raw* p) { return *p; }
   __device__ __forceinline__ static float load_raw(raw r) { return r; }
   __device__ __forceinline__ static void unpack(const vu4& q, float (&v)[kVec]) {
@@ -65,6 +66,7 @@ struct F32 {
 struct BF16 {
   using raw = uint16_t;
   static constexpr int kVec = 8;
+  static constexpr uint32_t kNegInf2 = 0xFF80FF80u;
   __device__ __forceinline__ static float widen(uint32_t bits16) {
     return __uint_as_float(bits16 << 16);
   }
@@ -96,6 +98,7 @@ struct BF16 {
 struct F16 {
   using raw = _Float16;
   static constexpr int kVec = 8;
+  static constexpr uint32_t kNegInf2 = 0xFC00FC00u;
   __device__ __forceinline__ static float load(const raw* p) { return (float)*p; }
   __device__ __forceinline__ static float load_raw(raw r) { return (float)r; }
   __device__ __forceinline__ static void unpack(const vu4& q, float (&v)[kVec]) {

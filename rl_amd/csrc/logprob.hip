@@ -60,6 +60,7 @@ __global__ __launch_bounds__(64 * W) void logprob_fwd_kernel(
     float* __restrict__ out, float* __restrict__ stats) {
   constexpr int NT = 64 * W;
   constexpr int VEC = E::kVec;
+  constexpr int BATCH = U * NT;  // vectors per workgroup per batch
   const int64_t row = blockIdx.x;
   const int64_t b = row / R;
   const int64_t r = row - b * R;
@@ -70,41 +71,50 @@ __global__ __launch_bounds__(64 * W) void logprob_fwd_kernel(
   // targets outside the vocabulary slice (or past this row) carry no one-hot
   const bool tmask = (t < vs) || (t >= ve) || (t - vs >= V);
   const int64_t tl = tmask ? 0 : (t - vs);
-  float xt = 0.f;
-  if (tid == 0) xt = E::load(x + tl);
-
-  LseState st;
   const RowSpan<E> span(x, V);
-  {
-    // scalar head and tail elements (fewer than 2*VEC per row)
-    float v[2];
-    v[0] = (tid < span.head) ? E::load(x + tid) : -INFINITY;
-    const int64_t ti = span.tail0 + tid;
-    v[1] = (ti < V) ? E::load(x + ti) : -INFINITY;
-    st.add(v);
-  }
   const vu4* xv = reinterpret_cast<const vu4*>(x + span.head);
   const int nvec = (int)span.nvec;
-  int i = tid;
-  for (; i + (U - 1) * NT < nvec; i += U * NT) {
-    vu4 q[U];
+  const int nbatch = (nvec + BATCH - 1) / BATCH;
+
+  // Every batch is U loads per lane issued together; lanes past the end of the
+  // row take -inf, which leaves the running max and sum unchanged.  Masking the
+  // last batch instead of finishing it one vector at a time keeps the whole
+  // row's loads in flight when a lane has only one batch (short rows).
+  const vu4 ninf = vu4{E::kNegInf2, E::kNegInf2, E::kNegInf2, E::kNegInf2};
+  vu4 q[U];
+  auto issue = [&](int base) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) q[u] = __builtin_nontemporal_load(xv + i + u * NT);
+    for (int u = 0; u < U; ++u) {
+      const int j = base + u * NT;
+      q[u] = (j < nvec) ? __builtin_nontemporal_load(xv + j) : ninf;
+    }
+  };
+  if (nbatch > 0) issue(tid);
+  float xt = 0.f;
+  if (tid == 0) xt = E::load(x + tl);
+  // scalar head and tail elements (fewer than 2*VEC per row)
+  float ht[2];
+  ht[0] = (tid < span.head) ? E::load(x + tid) : -INFINITY;
+  const int64_t ti = span.tail0 + tid;
+  ht[1] = (ti < V) ? E::load(x + ti) : -INFINITY;
+  // keep the batch's loads ahead of the arithmetic that consumes them
+  __builtin_amdgcn_sched_barrier(0);
+
+  LseState st;
+  for (int k = 0; k < nbatch; ++k) {
     float v[U * VEC];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       float w[VEC];
       E::unpack(q[u], w);
 #pragma unroll
-      for (int k = 0; k < VEC; ++k) v[u * VEC + k] = w[k];
+      for (int e = 0; e < VEC; ++e) v[u * VEC + e] = w[e];
     }
     st.add(v);
+    if (k + 1 < nbatch) issue(tid + (k + 1) * BATCH);
+    __builtin_amdgcn_sched_barrier(0);
   }
-  for (; i < nvec; i += NT) {
-    float w[VEC];
-    E::unpack(xv[i], w);
-    st.add(w);
-  }
+  st.add(ht);
 
   // merge lanes: the row max and the sum re-based to it
   float M = wave_max(st.m);

@@ -197,6 +197,29 @@ class ChunkedDistributedLogprob(torch.autograd.Function):
         return grad, None, None, None, None, None, None, None
 
 
+def _row_logprobs(
+    logits: torch.Tensor,
+    target: torch.Tensor,
+    vocab_start_index: int,
+    vocab_end_index: int,
+    inference_only: bool,
+    reuse_logits_storage: bool,
+) -> torch.Tensor:
+    """``_RowLogprob`` when autograd will record the call, else the forward kernel alone.
+
+    With ``inference_only`` (nothing is saved for a backward, as in the
+    reference) or when no gradient can flow, the autograd Function and the
+    per-row statistics are skipped; the logprobs are the same.
+    """
+    if inference_only or not (logits.requires_grad and torch.is_grad_enabled()):
+        out = torch.empty(target.shape, dtype=torch.float32, device=logits.device)
+        _C.logprob_fwd(logits, target, vocab_start_index, vocab_end_index, out, None)
+        return out
+    return _RowLogprob.apply(
+        logits, target, vocab_start_index, vocab_end_index, False, reuse_logits_storage
+    )
+
+
 def _forward_rows(
     logits: torch.Tensor,
     target: torch.Tensor,
@@ -275,9 +298,7 @@ def from_parallel_logits_to_logprobs(
             inference_only=inference_only,
         )
     tgt = _next_token_targets(target, logits.shape[1])
-    return _RowLogprob.apply(
-        logits, tgt, vocab_start_index, vocab_end_index, inference_only, False
-    )
+    return _row_logprobs(logits, tgt, vocab_start_index, vocab_end_index, inference_only, False)
 
 
 def from_parallel_logits_to_logprobs_packed_sequences(
@@ -331,7 +352,7 @@ def from_parallel_logits_to_logprobs_packed_sequences(
             inference_only=inference_only,
         )
     else:
-        probs = _RowLogprob.apply(
+        probs = _row_logprobs(
             logits, tgt, vocab_start_index, vocab_end_index, inference_only,
             reuse_logits_storage and chunk_size is not None,
         )

@@ -94,9 +94,9 @@ def filtered_row_logprobs(
     if not _enabled(top_k, top_p):
         if temperature != 1.0:
             raise ValueError("a fused temperature needs top-k or top-p filtering")
-        from rl_amd.distributed.model_utils import _RowLogprob
+        from rl_amd.distributed.model_utils import _row_logprobs
 
-        return _RowLogprob.apply(logits, target, 0, logits.shape[-1], inference_only, False)
+        return _row_logprobs(logits, target, 0, logits.shape[-1], inference_only, False)
     return _FilteredRowLogprob.apply(
         logits, target, _k(top_k), _p(top_p), float(temperature), inference_only
     )
