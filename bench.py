@@ -22,6 +22,8 @@ roofline (the default line above is the headline measurement):
   topk_filter  filtered logprob fwd+bwd, bf16 [4, 4096, 151936], T=0.7, k=50, p=0.9
   packed_kl    packed GRPO step with k3 KL, 64 sequences in bf16 [1, ~34.8k, 256000],
                through SequencePackingFusionLossWrapper
+  linear_ce    logprobs from hidden states, fwd+bwd: bf16 hidden [2048, 8, 4096] and
+               LM-head weight [151936, 4096], chunk 256 positions (MFMA-bound: TFLOP/s)
 """
 
 from __future__ import annotations
@@ -38,13 +40,14 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "logprob+PG-loss fwd/bwd tokens/s and HBM GB/s (% peak) at V=151936 bf16"
 PEAK_HBM_GBPS = 8000.0
+PEAK_BF16_TFLOPS = 2500.0  # dense bf16 MFMA
 
 
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--workload", default="grpo",
-                    choices=["grpo", "fwd_f32", "long_context", "topk_filter", "packed_kl"])
+                    choices=["grpo", "fwd_f32", "long_context", "topk_filter", "packed_kl", "linear_ce"])
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--cpu-sample-rows", type=int, default=1024)
@@ -359,6 +362,39 @@ def bench_workload(args) -> None:
                "temperature": T, "top_k": k, "top_p": p, "next_token_rows": rows,
                "temperature_fused": True}
         dtype = "bf16"
+    elif w == "linear_ce":
+        from rl_amd.distributed.model_utils import from_parallel_hidden_states_to_logprobs
+
+        d = workloads.linear_ce_bf16(device=dev)
+        hidden = d["hidden"].requires_grad_(True)
+        weight = d["weight"].requires_grad_(True)
+        ids, g = d["input_ids"], d["grad"]
+        S, B, H = hidden.shape
+        V = weight.shape[0]
+
+        def step():
+            lp = from_parallel_hidden_states_to_logprobs(hidden, weight, False, ids, 0, V, None,
+                                                         chunk_size=256)
+            return torch.autograd.grad(lp, [hidden, weight], g)
+
+        ms_step, ms = _timed(step, args.steps, args.warmup, ["mirl_linear_ce_fwd", "mirl_linear_ce_grad"])
+        rows = B * (S - 1)
+        gemm = 2.0 * S * B * H * V  # one [S*B, H] x [H, V] product
+        fwd_ms = ms.get("mirl_linear_ce_fwd", 0.0)
+        grad_chunks = -(-S // 256)
+        grad_ms = ms.get("mirl_linear_ce_grad", 0.0) * grad_chunks
+        tflops = gemm / (fwd_ms * 1e-3) / 1e12 if fwd_ms > 0 else 0.0
+        roof = {"kernel": "mirl_linear_ce_fwd", "bound": "mfma", "achieved": tflops, "peak": PEAK_BF16_TFLOPS,
+                "unit": "TFLOP/s", "frac": tflops / PEAK_BF16_TFLOPS, "traffic": _traffic(w),
+                "algorithmic_flops": gemm}
+        extra["tflops_step"] = 4 * gemm / (ms_step * 1e-3) / 1e12
+        extra["grad_kernel_ms_per_step"] = grad_ms
+        extra["grad_kernel_tflops_nominal"] = gemm / (grad_ms * 1e-3) / 1e12 if grad_ms > 0 else None
+        step_bytes = None
+        cfg = {"workload": "hidden_state_logprobs_fwd_bwd", "hidden": [S, B, H], "weight": [V, H],
+               "chunk_size": 256, "next_token_rows": rows,
+               "flops_per_step": "4 x 2*S*B*H*V (fused fwd, fused grad recompute, dH and dW GEMMs)"}
+        dtype = "bf16"
     else:  # packed_kl
         import torch.distributed as dist
 
@@ -430,7 +466,7 @@ def bench_workload(args) -> None:
         dtype = "bf16"
 
     cfg["parallelism"] = "single-gpu"
-    step_gbps = step_bytes / (ms_step * 1e-3) / 1e9
+    step_gbps = step_bytes / (ms_step * 1e-3) / 1e9 if step_bytes is not None else None
     out = {
         "metric": f"{w}: next-token rows/s and HBM GB/s (% peak)",
         "value": rows / (ms_step * 1e-3),
@@ -446,7 +482,7 @@ def bench_workload(args) -> None:
         "data": "synthetic",
         "config": cfg,
         "hbm_gbps_step": step_gbps,
-        "hbm_frac_step": step_gbps / PEAK_HBM_GBPS,
+        "hbm_frac_step": step_gbps / PEAK_HBM_GBPS if step_gbps is not None else None,
         "kernels_ms": {k.replace("mirl_", ""): v for k, v in ms.items()},
         **extra,
         "roofline": roof,

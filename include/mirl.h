@@ -175,6 +175,57 @@ int mirl_top_k_top_p_mask(const void* logits, int dtype, int64_t N, int64_t V,
                           uint8_t* keep_mask, int64_t keep_row_stride, void* stream);
 
 /* ---------------------------------------------------------------------- */
+/* logprobs from hidden states (LM-head GEMM fused with the log-sum-exp)     */
+/* ---------------------------------------------------------------------- */
+
+/* fp32 scratch elements mirl_linear_ce_fwd needs for T rows and V columns. */
+int64_t mirl_linear_ce_workspace_elems(int64_t T, int64_t V);
+
+/*
+ * Selected-token logprobs from bf16 hidden states [T, H] (row r is sequence
+ * position s = r / B of batch row b = r % B, i.e. a [S, B, H] tensor viewed as
+ * rows) and a bf16 output weight [V, H]:
+ *   x[r, v]  = bf16(sum_k hidden[r, k] * weight[v, k])   (fp32 accumulation)
+ *   out[b,s] = (x[r, t'] - m) - log(sum_v exp(x[r, v] - m)),  t' = target[b, s] - vocab_start,
+ *   out[b,s] = 0 when target < vocab_start or >= vocab_end.
+ * The [T, V] logits are never written.  H must be a multiple of 64, row
+ * strides multiples of 8 elements, both bases 16-byte aligned.  `row_stats`
+ * (optional) receives {m, log sum} per row for mirl_linear_ce_grad;
+ * `workspace` holds mirl_linear_ce_workspace_elems(T, V) floats.
+ *
+ * Replaces: the forward of ChunkedDistributedHiddenStatesToLogprobs
+ * (nemo_rl/distributed/model_utils.py:2576-2644) as called by
+ * from_parallel_hidden_states_to_logprobs (model_utils.py:2541-2569), with a
+ * vocab group of size 1.
+ */
+int mirl_linear_ce_fwd(const void* hidden, int64_t T, int64_t H, int64_t ldh,
+                       const void* weight, int64_t V, int64_t ldw, int64_t B,
+                       const int64_t* target, int64_t t_stride_b, int64_t t_stride_s,
+                       int64_t vocab_start, int64_t vocab_end, float* out,
+                       int64_t o_stride_b, int64_t o_stride_s, float* row_stats,
+                       float* workspace, void* stream);
+
+/*
+ * Gradient of those logprobs with respect to the logits, for rows
+ * [row0, row0 + nrows), recomputing the logits tile by tile:
+ *   grad_logits[r - row0, v] = bf16((onehot(t')[v] - exp((x[r, v] - m) - logsum)) * g[b, s])
+ * (row stride ldg >= V).  Tiles whose rows all have g == 0 are written as zeros
+ * without the GEMM.  The hidden-state and weight gradients are the products
+ * grad_logits . weight and grad_logits^T . hidden.
+ *
+ * Replaces: the per-chunk logits recompute, softmax and one-hot gradient of
+ * ChunkedDistributedHiddenStatesToLogprobs.backward
+ * (nemo_rl/distributed/model_utils.py:2647-2745).
+ */
+int mirl_linear_ce_grad(const void* hidden, int64_t T, int64_t H, int64_t ldh,
+                        const void* weight, int64_t V, int64_t ldw, int64_t B,
+                        const int64_t* target, int64_t t_stride_b, int64_t t_stride_s,
+                        int64_t vocab_start, int64_t vocab_end, const float* row_stats,
+                        const float* grad_out, int64_t g_stride_b, int64_t g_stride_s,
+                        int64_t row0, int64_t nrows, void* grad_logits, int64_t ldg,
+                        void* stream);
+
+/* ---------------------------------------------------------------------- */
 /* ClippedPG loss epilogue                                                  */
 /* ---------------------------------------------------------------------- */
 

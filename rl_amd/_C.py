@@ -127,6 +127,17 @@ SIGNATURES = {
         [_P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I64, _I64, ctypes.c_double, _P, _P,
          _P, _P, _I64, _I64, _P, _I64, _I64, _P],
     ),
+    "mirl_linear_ce_workspace_elems": (_I64, [_I64, _I64]),
+    "mirl_linear_ce_fwd": (
+        _I,
+        [_P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _I64,
+         _P, _P, _P],
+    ),
+    "mirl_linear_ce_grad": (
+        _I,
+        [_P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _I64, _P, _P, _I64,
+         _I64, _I64, _I64, _P, _I64, _P],
+    ),
     "mirl_top_k_top_p_mask": (
         _I,
         [_P, _I, _I64, _I64, _I64, _I, ctypes.c_double, _P, _P, _P, _P, _I64, _P, _I64, _P],
@@ -528,3 +539,80 @@ def top_k_top_p_mask(x2d: torch.Tensor, top_k: int, top_p: float):
     )
     _check(st, "mirl_top_k_top_p_mask")
     return filt, keep
+
+
+# ---------------------------------------------------------------------------
+# logprobs from hidden states (fused LM-head GEMM + log-sum-exp)
+# ---------------------------------------------------------------------------
+def _check_linear_ce(hidden2d: torch.Tensor, weight: torch.Tensor) -> None:
+    if hidden2d.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise NotImplementedError(
+            "logprobs from hidden states run on bf16 hidden states and weight "
+            f"(got {hidden2d.dtype} and {weight.dtype})"
+        )
+    if hidden2d.stride(-1) != 1 or weight.stride(-1) != 1:
+        raise MirlError("hidden states and weight need a unit stride on the hidden dimension")
+
+
+def linear_ce_fwd(
+    hidden2d: torch.Tensor,
+    weight: torch.Tensor,
+    bsz: int,
+    target: torch.Tensor,
+    vocab_start: int,
+    vocab_end: int,
+    out: torch.Tensor,
+    stats: Optional[torch.Tensor],
+) -> None:
+    """out[b, s] = log_softmax(bf16(hidden2d[s*bsz+b] . weight^T))[target[b, s] - vocab_start].
+
+    hidden2d: [T, H] bf16 rows (row r is position (r // bsz, r % bsz)); weight:
+    [V, H] bf16; target: [B, S] int64; out: [B, S] fp32; stats: [T, 2] fp32 or None.
+    """
+    dev = _require_gpu(hidden2d, weight, target, out, stats)
+    _check_linear_ce(hidden2d, weight)
+    T, H = hidden2d.shape
+    V = weight.shape[0]
+    assert target.dtype == torch.int64 and out.dtype == torch.float32
+    assert stats is None or (stats.is_contiguous() and stats.dtype == torch.float32)
+    lib = _lib if _lib is not None else load()
+    ws = torch.empty(max(1, int(lib.mirl_linear_ce_workspace_elems(T, V))), dtype=torch.float32, device=dev)
+    st = _launch(
+        "mirl_linear_ce_fwd", dev,
+        hidden2d.data_ptr(), T, H, hidden2d.stride(0), weight.data_ptr(), V, weight.stride(0),
+        int(bsz), target.data_ptr(), target.stride(0), target.stride(1), int(vocab_start),
+        int(vocab_end), out.data_ptr(), out.stride(0), out.stride(1), _ptr(stats), ws.data_ptr(),
+        _stream(dev),
+    )
+    _check(st, "mirl_linear_ce_fwd")
+
+
+def linear_ce_grad(
+    hidden2d: torch.Tensor,
+    weight: torch.Tensor,
+    bsz: int,
+    target: torch.Tensor,
+    vocab_start: int,
+    vocab_end: int,
+    stats: torch.Tensor,
+    grad_out: torch.Tensor,
+    row0: int,
+    grad_logits: torch.Tensor,
+) -> None:
+    """grad_logits[i, :] = bf16((onehot(t) - softmax(logits)) * g) for rows row0 .. row0 + n - 1."""
+    dev = _require_gpu(hidden2d, weight, target, stats, grad_out, grad_logits)
+    _check_linear_ce(hidden2d, weight)
+    T, H = hidden2d.shape
+    V = weight.shape[0]
+    n = grad_logits.shape[0]
+    assert grad_out.dtype == torch.float32 and grad_logits.dtype == torch.bfloat16
+    assert grad_logits.stride(-1) == 1
+    st = _launch(
+        "mirl_linear_ce_grad", dev,
+        hidden2d.data_ptr(), T, H, hidden2d.stride(0), weight.data_ptr(), V, weight.stride(0),
+        int(bsz), target.data_ptr(), target.stride(0), target.stride(1), int(vocab_start),
+        int(vocab_end), stats.data_ptr(), grad_out.data_ptr(), grad_out.stride(0),
+        grad_out.stride(1), int(row0), int(n), grad_logits.data_ptr(), grad_logits.stride(0),
+        _stream(dev),
+    )
+    _check(st, "mirl_linear_ce_grad")

@@ -25,6 +25,7 @@ SOURCES = [
     "clipped_pg.hip",
     "advantage.hip",
     "topk_filter.hip",
+    "linear_ce.hip",
 ]
 
 ARCH = "gfx950"

@@ -1,0 +1,157 @@
+"""Token logprobs from hidden states and the output weight (fused LM head + log-softmax).
+
+Drop-in for ``from_parallel_hidden_states_to_logprobs`` and
+``ChunkedDistributedHiddenStatesToLogprobs`` (reference
+nemo_rl/distributed/model_utils.py:2541-2745) with a tensor-parallel group of
+size 1.  Hidden states are Megatron's sequence-first ``[S, B, H]``; the weight
+is ``[V, H]``; targets are ``[B, S]``.
+
+* forward: one gfx950 kernel forms each 256 x 256 logits tile on the MFMA units
+  (bf16 inputs, fp32 accumulation, rounded to bf16 as the reference's bf16
+  matmul output is) and reduces it to per-row partial log-sum-exps and the
+  target logit; a merge kernel finishes each row.  The ``[S*B, V]`` logits are
+  never materialised (the reference materialises an fp32 copy per chunk).
+* backward: per chunk of ``chunk_size`` sequence positions, a kernel
+  recomputes the logits tiles and writes ``G = (onehot - softmax) * g`` in
+  bf16 (tiles whose rows all have a zero upstream gradient are zero-filled
+  without the GEMM); ``dH = G . W`` and ``dW += G^T . H`` are plain library
+  GEMMs with fp32 accumulation (``dW`` accumulated in fp32 across chunks and
+  rounded once; the reference adds each chunk into a bf16 buffer).
+"""
+
+from __future__ import annotations
+
+from typing import Any, Optional
+
+import torch
+
+from rl_amd import _C
+
+__all__ = ["ChunkedDistributedHiddenStatesToLogprobs", "from_parallel_hidden_states_to_logprobs"]
+
+
+def _require_single_rank(*groups: Optional[Any]) -> None:
+    from rl_amd.distributed.model_utils import _require_single_rank as req
+
+    req(*groups)
+
+
+class ChunkedDistributedHiddenStatesToLogprobs(torch.autograd.Function):
+    """Selected-token logprobs ``[B, S]`` (fp32) of ``hidden [S, B, H] . weight[V, H]^T``.
+
+    Reference: model_utils.py:2572-2745 (forward 2576-2644, backward 2647-2745).
+    ``target`` is already aligned with the rows (the caller rolls it); targets
+    outside ``[vocab_start_index, vocab_end_index)`` give 0.
+    """
+
+    @staticmethod
+    def forward(  # type: ignore[override]
+        ctx: Any,
+        tensor_parallel_hidden_states: torch.Tensor,
+        target: torch.Tensor,
+        output_weight_layer: torch.Tensor,
+        vocab_start_index: int,
+        vocab_end_index: int,
+        chunk_size: Optional[int],
+        tp_group: Optional[Any],
+        inference_only: bool = False,
+    ) -> torch.Tensor:
+        _require_single_rank(tp_group)
+        if chunk_size is not None and int(chunk_size) <= 0:
+            raise ValueError("chunk_size must be positive")
+        hidden = tensor_parallel_hidden_states
+        if hidden.dim() != 3:
+            raise ValueError(f"expected hidden states [S, B, H], got {tuple(hidden.shape)}")
+        S, B, H = hidden.shape
+        if tuple(target.shape) != (B, S):
+            raise ValueError(f"target shape {tuple(target.shape)} does not match [B, S] = {(B, S)}")
+        weight = output_weight_layer
+        if weight.dim() != 2 or weight.shape[1] != H:
+            raise ValueError(f"weight shape {tuple(weight.shape)} does not match hidden size {H}")
+        if not hidden.is_contiguous():
+            hidden = hidden.contiguous()
+        if weight.stride(-1) != 1:
+            weight = weight.contiguous()
+        if target.dtype != torch.int64:
+            target = target.long()
+        h2 = hidden.view(S * B, H)
+        out = torch.empty((B, S), dtype=torch.float32, device=hidden.device)
+        stats = None
+        if not inference_only:
+            stats = torch.empty((S * B, 2), dtype=torch.float32, device=hidden.device)
+        _C.linear_ce_fwd(h2, weight, B, target, vocab_start_index, vocab_end_index, out, stats)
+        if not inference_only:
+            ctx.save_for_backward(hidden, target, weight, stats)
+            ctx.vocab = (int(vocab_start_index), int(vocab_end_index))
+            ctx.chunk_size = None if chunk_size is None else int(chunk_size)
+        return out
+
+    @staticmethod
+    def backward(ctx: Any, *grad_outputs: torch.Tensor):  # type: ignore[override]
+        (grad_output,) = grad_outputs
+        hidden, target, weight, stats = ctx.saved_tensors
+        vs, ve = ctx.vocab
+        S, B, H = hidden.shape
+        V = weight.shape[0]
+        T = S * B
+        if grad_output.dtype != torch.float32:
+            grad_output = grad_output.float()
+        h2 = hidden.view(T, H)
+        rows = T if ctx.chunk_size is None else min(T, ctx.chunk_size * B)
+        need_h = ctx.needs_input_grad[0]
+        need_w = ctx.needs_input_grad[2]
+        G = torch.empty((rows, V), dtype=torch.bfloat16, device=hidden.device)
+        dH = torch.empty((T, H), dtype=hidden.dtype, device=hidden.device) if need_h else None
+        dW = torch.zeros((V, H), dtype=torch.float32, device=hidden.device) if need_w else None
+        for r0 in range(0, T, rows):
+            n = min(rows, T - r0)
+            Gc = G[:n]
+            _C.linear_ce_grad(h2, weight, B, target, vs, ve, stats, grad_output, r0, Gc)
+            if need_h:
+                torch.matmul(Gc, weight, out=dH[r0 : r0 + n])
+            if need_w:
+                _accumulate_dw(dW, Gc, h2[r0 : r0 + n])
+        grad_h = dH.view(S, B, H) if need_h else None
+        grad_w = dW.to(weight.dtype) if need_w else None
+        return grad_h, None, grad_w, None, None, None, None, None
+
+
+def _accumulate_dw(dW: torch.Tensor, G: torch.Tensor, h: torch.Tensor) -> None:
+    """dW += G^T . h with bf16 inputs and fp32 accumulation and output."""
+    torch.addmm(dW, G.t(), h, out_dtype=torch.float32, out=dW)
+
+
+def from_parallel_hidden_states_to_logprobs(
+    tensor_parallel_hidden_states: torch.Tensor,
+    output_weight_layer: torch.Tensor,
+    runtime_gather_output: bool,
+    target: torch.Tensor,
+    vocab_start_index: int,
+    vocab_end_index: int,
+    tp_group: Optional[Any],
+    inference_only: bool = False,
+    cp_group: Optional[Any] = None,
+    chunk_size: Optional[int] = None,
+) -> torch.Tensor:
+    """Next-token logprobs ``[B, S-1]`` from ``[S, B, H]`` hidden states (reference model_utils.py:2541-2569).
+
+    ``target`` ``[B, S]`` is rolled by -1 along the sequence, as in the
+    reference; ``runtime_gather_output`` is accepted and unused, as there.
+    """
+    from rl_amd.distributed.model_utils import _group_size
+
+    target = target.roll(shifts=-1, dims=-1)
+    assert cp_group is None or _group_size(cp_group) == 1, (
+        "Context parallelism is not supported for linear CE fusion loss"
+    )
+    logprobs = ChunkedDistributedHiddenStatesToLogprobs.apply(
+        tensor_parallel_hidden_states,
+        target,
+        output_weight_layer,
+        vocab_start_index,
+        vocab_end_index,
+        chunk_size,
+        tp_group,
+        inference_only,
+    ).contiguous()
+    return logprobs[:, :-1]

@@ -30,10 +30,12 @@ from rl_amd.algorithms.logits_sampling_utils import (
 )
 
 __all__ = [
+    "ChunkedDistributedHiddenStatesToLogprobs",
     "ChunkedDistributedLogprob",
     "ChunkedDistributedLogprobWithSampling",
     "DistributedLogprob",
     "DistributedLogprobWithSampling",
+    "from_parallel_hidden_states_to_logprobs",
     "from_parallel_logits_to_logprobs",
     "from_parallel_logits_to_logprobs_packed_sequences",
     "get_next_token_logprobs_from_logits",
@@ -41,11 +43,16 @@ __all__ = [
 
 
 def __getattr__(name: str):
-    # the filtered autograd Functions live with the filter kernels' bindings
+    # the filtered autograd Functions live with the filter kernels' bindings,
+    # the hidden-state path with the fused LM-head kernels' bindings
     if name in ("DistributedLogprobWithSampling", "ChunkedDistributedLogprobWithSampling"):
         from rl_amd.distributed import sampling
 
         return getattr(sampling, name)
+    if name in ("ChunkedDistributedHiddenStatesToLogprobs", "from_parallel_hidden_states_to_logprobs"):
+        from rl_amd.distributed import linear_ce
+
+        return getattr(linear_ce, name)
     raise AttributeError(name)
 
 

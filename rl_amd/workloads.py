@@ -17,6 +17,11 @@ a device.  Sizes default to the full workloads; tests pass smaller sizes.
 * packed_grpo_kl_bf16 64 sequences of U{64..1024} tokens packed into logits bf16
                     [1, ~34.8k, 256000] ~ N(0, 1.5^2); 8 prompts x 8 generations,
                     rewards ~ Bernoulli(0.3); reference = current + N(0, 0.1^2)
+* linear_ce_bf16    hidden states bf16 [2048, 8, 4096] ~ N(0, 1) and an LM-head
+                    weight bf16 [151936, 4096] ~ N(0, (1.5 / 64)^2) (logits
+                    ~ N(0, 1.5^2)); uniform token ids; upstream gradient zero on
+                    the 512 prompt positions and the padding, N(0, 1) on
+                    U{256..1536} response positions
 """
 
 from __future__ import annotations
@@ -210,3 +215,26 @@ def finish_packed_grpo_step(data: dict, current_logprobs: torch.Tensor) -> dict:
     data["generation_logprobs"] = cur.clone()
     data["reference_policy_logprobs"] = cur + data["ref_noise"].to(cur.device)
     return data
+
+
+def linear_ce_bf16(
+    S: int = 2048,
+    B: int = 8,
+    H: int = 4096,
+    V: int = 151936,
+    prompt_len: int = 512,
+    resp_min: int = 256,
+    resp_max: int = 1536,
+    seed: int = 6,
+    device=None,
+):
+    """Inputs of the hidden-state logprob path (Megatron's sequence-first [S, B, H] layout)."""
+    g = _gen(seed)
+    hidden = _randn_bf16((S, B, H), 1.0, g, device)
+    weight = _randn_bf16((1, V, H), 1.5 / H**0.5, g, device)[0]
+    ids = torch.randint(0, V, (B, S), generator=g)
+    lens = torch.randint(resp_min, resp_max + 1, (B,), generator=g)
+    pos = torch.arange(S).unsqueeze(0)
+    live = (pos >= prompt_len) & (pos < prompt_len + lens.unsqueeze(1))
+    grad = torch.randn((B, S - 1), generator=g) * live[:, 1:].float()
+    return {"hidden": hidden, "weight": weight, "input_ids": ids.to(device), "grad": grad.to(device)}

@@ -1,0 +1,160 @@
+"""Logprobs from hidden states (fused LM-head GEMM + log-sum-exp) against the oracle (GPU).
+
+Tolerances.  The reference's logits are a bf16 matmul output: an fp32 sum of
+bf16 products rounded once to bf16.  The kernel forms the same sum on the MFMA
+units in another order, so a logit can round to the neighbouring bf16 value
+(one ulp, <= |x| * 2^-7).  A logprob therefore matches the oracle within
+2e-3 + |x_t| * 2^-7 (the target logit enters it directly; the log-sum-exp
+moves by far less), and most rows within 2e-3.  Gradients: the logits
+gradient G is rounded to bf16 before the two GEMMs (the reference keeps it in
+fp32), so dH and dW match the float64 oracle to 1e-2 of their largest
+magnitude; fused and unfused (materialised-logits) paths agree the same way.
+Out-of-range targets give exactly 0.
+"""
+
+import pytest
+import torch
+
+from oracle.linear_ce import (
+    hidden_state_logprob_grads,
+    hidden_state_logprobs,
+    logits_bf16,
+    next_token_hidden_state_logprobs,
+)
+from rl_amd._C import MirlError
+from rl_amd.distributed.model_utils import (
+    ChunkedDistributedHiddenStatesToLogprobs,
+    from_parallel_hidden_states_to_logprobs,
+    from_parallel_logits_to_logprobs,
+)
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda", 0)
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+
+
+def _inputs(S, B, H, V, seed, scale=1.5):
+    g = torch.Generator().manual_seed(seed)
+    hidden = torch.randn(S, B, H, generator=g).to(torch.bfloat16)
+    weight = (torch.randn(V, H, generator=g) * (scale / H**0.5)).to(torch.bfloat16)
+    target = torch.randint(0, V, (B, S), generator=g)
+    return hidden, weight, target
+
+
+def _check_logprobs(got, ref, x_t):
+    tol = 2e-3 + x_t.abs() * 2.0**-7
+    diff = (got.cpu().double() - ref.double()).abs()
+    assert torch.all(diff <= tol), f"max excess {(diff - tol).max().item():.3e}"
+    # the one-ulp flips of the target logit are rare
+    assert (diff > 2e-3).float().mean().item() < 0.1
+
+
+def _target_logits(hidden, weight, target):
+    x = logits_bf16(hidden, weight)  # [B, S, V]
+    return x.gather(-1, target.clamp(0, weight.shape[0] - 1).unsqueeze(-1)).squeeze(-1)
+
+
+@pytest.mark.parametrize("S,B,H,V", [(37, 3, 128, 1000), (16, 2, 256, 151936), (300, 1, 64, 4096),
+                                     (5, 4, 192, 257)])
+def test_forward_against_oracle(S, B, H, V):
+    say("linear-ce fwd", S, B, H, V)
+    hidden, weight, target = _inputs(S, B, H, V, seed=S + V)
+    ref = hidden_state_logprobs(hidden, target, weight, 0, V)
+    got = ChunkedDistributedHiddenStatesToLogprobs.apply(
+        hidden.to(DEV), target.to(DEV), weight.to(DEV), 0, V, 8, None, True)
+    assert got.shape == (B, S) and got.dtype == torch.float32
+    _check_logprobs(got, ref, _target_logits(hidden, weight, target))
+
+
+def test_vocab_slice_targets_are_exactly_zero():
+    say("linear-ce vocab slice")
+    S, B, H, V = 20, 3, 128, 700
+    hidden, weight, target = _inputs(S, B, H, V, seed=7)
+    target = torch.randint(0, 3 * V, (B, S), generator=torch.Generator().manual_seed(8))
+    vs, ve = V, 2 * V
+    got = ChunkedDistributedHiddenStatesToLogprobs.apply(
+        hidden.to(DEV), target.to(DEV), weight.to(DEV), vs, ve, None, None, True).cpu()
+    outside = (target < vs) | (target >= ve)
+    assert outside.any() and (~outside).any()
+    assert torch.all(got[outside] == 0)
+    ref = hidden_state_logprobs(hidden, target, weight, vs, ve)
+    _check_logprobs(got[~outside], ref[~outside], _target_logits(hidden, weight, target - vs)[~outside])
+
+
+def test_next_token_api_and_roll():
+    say("linear-ce next-token api")
+    S, B, H, V = 33, 2, 128, 3000
+    hidden, weight, target = _inputs(S, B, H, V, seed=11)
+    got = from_parallel_hidden_states_to_logprobs(
+        hidden.to(DEV), weight.to(DEV), False, target.to(DEV), 0, V, None, inference_only=True,
+        chunk_size=4)
+    assert got.shape == (B, S - 1)
+    ref = next_token_hidden_state_logprobs(hidden, weight, target, 0, V)
+    _check_logprobs(got, ref, _target_logits(hidden, weight, target.roll(-1, -1))[:, :-1])
+
+
+@pytest.mark.parametrize("chunk", [None, 1, 7])
+def test_gradients_against_oracle(chunk):
+    say("linear-ce grads chunk", chunk)
+    S, B, H, V = 24, 3, 128, 1500
+    hidden, weight, target = _inputs(S, B, H, V, seed=21)
+    g = torch.randn(B, S, generator=torch.Generator().manual_seed(22))
+    g[:, :5] = 0.0  # zero-gradient rows
+    h = hidden.to(DEV).requires_grad_(True)
+    w = weight.to(DEV).requires_grad_(True)
+    lp = ChunkedDistributedHiddenStatesToLogprobs.apply(h, target.to(DEV), w, 0, V, chunk, None, False)
+    dh, dw = torch.autograd.grad(lp, [h, w], g.to(DEV))
+    assert dh.dtype == torch.bfloat16 and dw.dtype == torch.bfloat16
+    rdh, rdw, _ = hidden_state_logprob_grads(hidden, target, weight, 0, V, g)
+    for got, ref in ((dh, rdh), (dw, rdw)):
+        err = (got.cpu().double() - ref).abs().max().item()
+        assert err <= 1e-2 * ref.abs().max().item(), (err, ref.abs().max().item())
+
+
+def test_all_zero_gradient_tiles():
+    say("linear-ce zero-gradient tiles")
+    S, B, H, V = 300, 1, 64, 600  # 300 rows: one full 256-row tile of zeros
+    hidden, weight, target = _inputs(S, B, H, V, seed=31)
+    g = torch.zeros(B, S)
+    g[:, 280:] = 1.0
+    h = hidden.to(DEV).requires_grad_(True)
+    w = weight.to(DEV).requires_grad_(True)
+    lp = ChunkedDistributedHiddenStatesToLogprobs.apply(h, target.to(DEV), w, 0, V, None, None, False)
+    dh, dw = torch.autograd.grad(lp, [h, w], g.to(DEV))
+    assert torch.all(dh[:280].cpu() == 0)
+    rdh, rdw, _ = hidden_state_logprob_grads(hidden, target, weight, 0, V, g)
+    for got, ref in ((dh, rdh), (dw, rdw)):
+        err = (got.cpu().double() - ref).abs().max().item()
+        assert err <= 1e-2 * ref.abs().max().item(), err
+
+
+def test_fused_matches_materialised_logits_path():
+    """The reference's own agreement check (linear-CE fusion vs the logits path), on one GPU."""
+    say("linear-ce fused vs unfused")
+    S, B, H, V = 64, 2, 256, 151936
+    hidden, weight, target = _inputs(S, B, H, V, seed=41)
+    hd, wd, td = hidden.to(DEV), weight.to(DEV), target.to(DEV)
+    fused = from_parallel_hidden_states_to_logprobs(hd, wd, False, td, 0, V, None, inference_only=True)
+    logits = torch.mm(hd.view(S * B, H), wd.t().contiguous()).view(S, B, V)
+    logits = logits.transpose(0, 1).contiguous()  # [B, S, V] bf16
+    unfused = from_parallel_logits_to_logprobs(logits, td, 0, V, None, inference_only=True)
+    x_t = logits.float().gather(-1, td.roll(-1, -1).unsqueeze(-1)).squeeze(-1)[:, :-1]
+    _check_logprobs(fused, unfused.cpu(), x_t.cpu())
+
+
+def test_errors():
+    say("linear-ce errors")
+    hidden, weight, target = _inputs(4, 2, 96, 50, seed=1)  # H = 96 is not a multiple of 64
+    with pytest.raises(MirlError):
+        ChunkedDistributedHiddenStatesToLogprobs.apply(
+            hidden.to(DEV), target.to(DEV), weight.to(DEV), 0, 50, None, None, True)
+    hidden, weight, target = _inputs(4, 2, 128, 50, seed=1)
+    with pytest.raises(NotImplementedError):
+        ChunkedDistributedHiddenStatesToLogprobs.apply(
+            hidden.float().to(DEV), target.to(DEV), weight.float().to(DEV), 0, 50, None, None, True)
+    with pytest.raises(ValueError):
+        ChunkedDistributedHiddenStatesToLogprobs.apply(
+            hidden.to(DEV), target.t().contiguous().to(DEV), weight.to(DEV), 0, 50, None, None, True)
