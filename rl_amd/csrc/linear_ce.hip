@@ -23,6 +23,8 @@
 // and B[k][l % 32] for k = (l / 32) * 8 + 0..7; accumulator element v of lane l
 // is C[(v / 4) * 8 + (l / 32) * 4 + v % 4][l % 32].
 
+#include <type_traits>
+
 #include "common.h"
 
 #pragma clang fp contract(off)
@@ -42,10 +44,17 @@ constexpr int kTM = kWM / 32, kTN = kWN / 32;
 constexpr int kRowBytes = kBK * 2;       // one tile row in LDS
 constexpr int kStageBytes = (kBM + kBN) * kRowBytes;
 constexpr int kLoadsPerThread = kBM * kRowBytes / 16 / kThreads;  // 16-byte chunks of A (and of B)
-constexpr int kGroupM = 8;               // row tiles sharing a sweep over the vocabulary
+constexpr int kGroupM = 4;               // row tiles sharing a sweep over the vocabulary
+constexpr int kXcds = 8;                 // accelerator dies, each with its own L2
 
 __device__ __forceinline__ int lds_off(int row, int chunk) {
   return row * kRowBytes + ((chunk ^ (row & 7)) << 4);
+}
+
+// Epilogue layout of a [256][256] bf16 tile in LDS: row-major, 16-byte chunks
+// XOR-swizzled by row % 32 (element index).
+__device__ __forceinline__ int xs_index(int row, int col) {
+  return row * kBN + ((((col >> 3) ^ (row & 31)) << 3) | (col & 7));
 }
 
 __device__ __forceinline__ float bf16_round(float f) {
@@ -82,15 +91,21 @@ void lce_tile_kernel(LceParams P) {
   __shared__ __align__(16) unsigned char lds[2 * kStageBytes];
   __shared__ int s_tcol[kBM];
   __shared__ float s_m[kBM], s_ls[kBM], s_g[kBM];
-  __shared__ float s_red[2][kBM][2];
 
-  // grouped tile order: kGroupM row tiles sweep the vocabulary together
-  const int64_t bid = blockIdx.x;
+  // Tile order.  Workgroups are dispatched to the 8 XCDs round-robin
+  // (XCD = blockIdx % 8) and each XCD has its own L2, so each XCD takes one
+  // contiguous run of a grouped order (kGroupM row tiles sweep the vocabulary
+  // together): the ~32 workgroups resident on an XCD then cover about
+  // kGroupM row tiles x 8 column tiles and share their H and W reads in L2.
+  const int64_t ntiles = P.n_mt * P.n_nt;
+  const int64_t per_xcd = (ntiles + kXcds - 1) / kXcds;
+  const int64_t gi = (int64_t)(blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
+  if (gi >= ntiles) return;
   const int64_t per_group = (int64_t)kGroupM * P.n_nt;
-  const int64_t group = bid / per_group;
+  const int64_t group = gi / per_group;
   const int64_t first_m = group * kGroupM;
   const int64_t gsize = (P.n_mt - first_m < kGroupM) ? (P.n_mt - first_m) : kGroupM;
-  const int64_t in_group = bid - group * per_group;
+  const int64_t in_group = gi - group * per_group;
   const int64_t mt = first_m + in_group % gsize;
   const int64_t nt = in_group / gsize;
   const int64_t m0 = P.row0 + mt * kBM;  // absolute first row
@@ -151,30 +166,58 @@ void lce_tile_kernel(LceParams P) {
   }
 
   // ---- main loop: acc = H[m0 : m0+256] . W[n0 : n0+256]^T ----
+  //
+  // Global -> register loads go through buffer resources covering the tile's
+  // valid rows, so rows past the end of H or W read as zero with no branch.
+  // Thread t moves the 16-byte chunk (t & 7) of rows (t >> 3) + 32 j, j < 8,
+  // of both operands; its LDS slot is fixed up to the row offset 32 j * 128.
+  //
+  // One K step (64 hidden elements) is four MFMA blocks kk = 0..3 of 16
+  // MFMAs.  While block kk runs, the operand fragments of block kk + 1 are read
+  // from LDS into the other fragment set; staged global loads are written to
+  // the other LDS stage during block 2; the step's barrier comes before block
+  // 3, whose MFMAs then cover the LDS reads of the next step's block 0.
+  // sched_barrier fences keep that order.
   const int nk = (int)(P.Hd / kBK);
+  const int64_t a_rows = (row_end - m0 < kBM) ? (row_end - m0) : kBM;
+  const int64_t b_rows = (P.V - n0 < kBN) ? (P.V - n0) : kBN;
+  const __amdgpu_buffer_rsrc_t rsrc_a = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(P.h + m0 * P.ldh), 0, (int)(a_rows * P.ldh * 2), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsrc_b = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(P.w + n0 * P.ldw), 0, (int)(b_rows * P.ldw * 2), 0x00020000);
+  const int ld_row = tid >> 3, ld_chunk = tid & 7;
+  const int voff_a = (int)((ld_row * P.ldh + ld_chunk * 8) * 2);
+  const int voff_b = (int)((ld_row * P.ldw + ld_chunk * 8) * 2);
+  const int jstride_a = (int)(32 * P.ldh * 2), jstride_b = (int)(32 * P.ldw * 2);
+  const int st_off = lds_off(ld_row, ld_chunk);  // + j * 32 rows
+
   vu4 ra[kLoadsPerThread], rb[kLoadsPerThread];
-  const vu4 zero = vu4{0u, 0u, 0u, 0u};
   auto gload = [&](int kt) {
-    const int64_t k0 = (int64_t)kt * kBK;
+    const int k_bytes = kt * kBK * 2;
 #pragma unroll
     for (int j = 0; j < kLoadsPerThread; ++j) {
-      const int q = tid + j * kThreads;
-      const int row = q >> 3, c = q & 7;
-      const int64_t ar = m0 + row;
-      ra[j] = (ar < row_end) ? *reinterpret_cast<const vu4*>(P.h + ar * P.ldh + k0 + c * 8) : zero;
-      const int64_t br = n0 + row;
-      rb[j] = (br < P.V) ? *reinterpret_cast<const vu4*>(P.w + br * P.ldw + k0 + c * 8) : zero;
+      ra[j] = __builtin_bit_cast(vu4, __builtin_amdgcn_raw_buffer_load_b128(rsrc_a, voff_a, j * jstride_a + k_bytes, 0));
+      rb[j] = __builtin_bit_cast(vu4, __builtin_amdgcn_raw_buffer_load_b128(rsrc_b, voff_b, j * jstride_b + k_bytes, 0));
     }
   };
-  auto sstore = [&](int stage) {
-    unsigned char* base = lds + stage * kStageBytes;
+  auto sstore_one = [&](unsigned char* base, int j) {
+    *reinterpret_cast<vu4*>(base + st_off + j * 32 * kRowBytes) = ra[j];
+    *reinterpret_cast<vu4*>(base + kBM * kRowBytes + st_off + j * 32 * kRowBytes) = rb[j];
+  };
+
+  // fragment read offsets: row (wm*128 | wn*128) + i*32 + (lane & 31), chunk kk*2 + (lane >> 5)
+  const int frow = lane & 31;
+  int frag_off[kBK / 16];
 #pragma unroll
-    for (int j = 0; j < kLoadsPerThread; ++j) {
-      const int q = tid + j * kThreads;
-      const int row = q >> 3, c = q & 7;
-      *reinterpret_cast<vu4*>(base + lds_off(row, c)) = ra[j];
-      *reinterpret_cast<vu4*>(base + kBM * kRowBytes + lds_off(row, c)) = rb[j];
-    }
+  for (int kk = 0; kk < kBK / 16; ++kk) frag_off[kk] = lds_off(frow, kk * 2 + (lane >> 5));
+  bf16x8 fa[2][kTM], fb[2][kTN];
+  auto fread = [&](int set, const unsigned char* stage, int kk, int idx) {
+    // idx < kTM: A fragment idx; else B fragment idx - kTM
+    if (idx < kTM)
+      fa[set][idx] = *reinterpret_cast<const bf16x8*>(stage + (wm * kWM + idx * 32) * kRowBytes + frag_off[kk]);
+    else
+      fb[set][idx - kTM] = *reinterpret_cast<const bf16x8*>(
+          stage + kBM * kRowBytes + (wn * kWN + (idx - kTM) * 32) * kRowBytes + frag_off[kk]);
   };
 
   f32x16 acc[kTM][kTN];
@@ -184,86 +227,116 @@ void lce_tile_kernel(LceParams P) {
     for (int j = 0; j < kTN; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+  auto mfma = [&](int set, int q) {
+    const int i = q / kTN, j = q % kTN;
+    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[set][i], fb[set][j], acc[i][j], 0, 0, 0);
+  };
 
+  // Prologue: step 0 into LDS stage 0, step 1's loads in flight, block 0's fragments.
   gload(0);
-  sstore(0);
+#pragma unroll
+  for (int j = 0; j < kLoadsPerThread; ++j) sstore_one(lds, j);
+  if (nk > 1) gload(1);
   __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    if (kt + 1 < nk) gload(kt + 1);
-    const unsigned char* As = lds + (kt & 1) * kStageBytes;
-    const unsigned char* Bs = As + kBM * kRowBytes;
 #pragma unroll
-    for (int kk = 0; kk < kBK / 16; ++kk) {
-      const int c = kk * 2 + (lane >> 5);
-      bf16x8 af[kTM], bfr[kTN];
-#pragma unroll
-      for (int i = 0; i < kTM; ++i)
-        af[i] = *reinterpret_cast<const bf16x8*>(As + lds_off(wm * kWM + i * 32 + (lane & 31), c));
-#pragma unroll
-      for (int j = 0; j < kTN; ++j)
-        bfr[j] = *reinterpret_cast<const bf16x8*>(Bs + lds_off(wn * kWN + j * 32 + (lane & 31), c));
-#pragma unroll
-      for (int i = 0; i < kTM; ++i)
-#pragma unroll
-        for (int j = 0; j < kTN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
-    }
-    if (kt + 1 < nk) sstore((kt + 1) & 1);
-    __syncthreads();
-  }
+  for (int idx = 0; idx < kTM + kTN; ++idx) fread(0, lds, 0, idx);
 
-  // ---- epilogue ----
+  // One K step.  NEXT: the loads of step kt + 1 (in the staging registers) are
+  // written to the other LDS stage during block 2, and the next step's block-0
+  // fragments are read during block 3.  LOAD: right after those writes the
+  // staging registers take step kt + 2's loads, a full step before they are
+  // written in turn.  Every read of the current stage happens before the
+  // step's barrier; the first write into it (step kt + 2's data) comes in the
+  // next step's block 2, after that barrier.
+  auto step = [&](int kt, auto next_c, auto load_c) {
+    constexpr bool NEXT = decltype(next_c)::value;
+    constexpr bool LOAD = decltype(load_c)::value;
+    const unsigned char* cur = lds + (kt & 1) * kStageBytes;
+    unsigned char* nxt = lds + ((kt + 1) & 1) * kStageBytes;
+#pragma unroll
+    for (int kk = 0; kk < 3; ++kk) {
+      const int set = kk & 1;
+#pragma unroll
+      for (int q = 0; q < kTM * kTN; ++q) {
+        mfma(set, q);
+        if (q < kTM + kTN) fread(set ^ 1, cur, kk + 1, q);
+        if constexpr (NEXT) {
+          if (kk == 2 && q >= 8) sstore_one(nxt, q - 8);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    if constexpr (LOAD) gload(kt + 2);
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < kTM * kTN; ++q) {
+      mfma(1, q);
+      if constexpr (NEXT) {
+        if (q < kTM + kTN) fread(0, nxt, 0, q);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  using T_ = std::integral_constant<bool, true>;
+  using F_ = std::integral_constant<bool, false>;
+  int kt = 0;
+  for (; kt + 2 < nk; ++kt) step(kt, T_{}, T_{});
+  if (kt + 1 < nk) step(kt++, T_{}, F_{});
+  step(kt, F_{}, F_{});
+
+  // ---- epilogue: the tile goes through LDS as bf16, one row per thread ----
+  //
+  // The accumulators of a row are spread over 32 lanes; instead of cross-lane
+  // reductions each wave writes its quarter to LDS (row-major [256][256] bf16,
+  // 16-byte chunks XOR-swizzled by row % 32) and thread t then walks row t
+  // (forward) or copies rows out with 16-byte stores (gradient).  The last
+  // step's barrier already ordered every read of the LDS stages before this.
+  __syncthreads();
+  uint16_t* xs = reinterpret_cast<uint16_t*>(lds);
   const int half = lane >> 5;  // which 4-row group of each 8-row band this lane holds
   const int col_lane = lane & 31;
   if (MODE == kFwd) {
 #pragma unroll
-    for (int i = 0; i < kTM; ++i) {
+    for (int i = 0; i < kTM; ++i)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int rl = wm * kWM + i * 32 + (v >> 2) * 8 + half * 4 + (v & 3);
-        float x[kTN];
-        float mx = -INFINITY;
+      for (int j = 0; j < kTN; ++j)
 #pragma unroll
-        for (int j = 0; j < kTN; ++j) {
+        for (int v = 0; v < 16; ++v) {
+          const int rl = wm * kWM + i * 32 + (v >> 2) * 8 + half * 4 + (v & 3);
           const int cl = wn * kWN + j * 32 + col_lane;
-          x[j] = (n0 + cl < P.V) ? bf16_round(acc[i][j][v]) : -INFINITY;
-          mx = fmaxf(mx, x[j]);
+          xs[xs_index(rl, cl)] = BF16::from_float(acc[i][j][v]);
         }
-#pragma unroll
-        for (int off = 1; off < 32; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-        float s = 0.f;
-        if (mx != -INFINITY) {
-#pragma unroll
-          for (int j = 0; j < kTN; ++j) s += fast_exp2((x[j] - mx) * kLog2e);
-        }
-#pragma unroll
-        for (int off = 1; off < 32; off <<= 1) s += __shfl_xor(s, off, 64);
-        const int tc = s_tcol[rl];
-        if (tc >= 0) {
-#pragma unroll
-          for (int j = 0; j < kTN; ++j)
-            if (tc == wn * kWN + j * 32 + col_lane) P.xt[m0 + rl - P.row0] = x[j];
-        }
-        if (col_lane == 0) {
-          s_red[wn][rl][0] = mx;
-          s_red[wn][rl][1] = s;
-        }
-      }
-    }
     __syncthreads();
     const int64_t r = m0 + tid;
     if (r < row_end) {
-      const float m_a = s_red[0][tid][0], s_a = s_red[0][tid][1];
-      const float m_b = s_red[1][tid][0], s_b = s_red[1][tid][1];
-      const float M = fmaxf(m_a, m_b);
-      float s = 0.f;
+      const int ncols = (P.V - n0 < kBN) ? (int)(P.V - n0) : kBN;
+      const vu4* rowp = reinterpret_cast<const vu4*>(xs + tid * kBN);
+      const int sw = tid & 31;
+      float M = -INFINITY;
+      for (int c = 0; c < kBN / 8; ++c) {
+        float w[8];
+        BF16::unpack(rowp[c ^ sw], w);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (c * 8 + e < ncols) M = fmaxf(M, w[e]);
+      }
+      float sum = 0.f;
       if (M != -INFINITY) {
-        if (m_a != -INFINITY) s += s_a * fast_exp2((m_a - M) * kLog2e);
-        if (m_b != -INFINITY) s += s_b * fast_exp2((m_b - M) * kLog2e);
+        float s4[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int c = 0; c < kBN / 8; ++c) {
+          float w[8];
+          BF16::unpack(rowp[c ^ sw], w);
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (c * 8 + e < ncols) s4[e & 3] += fast_exp2((w[e] - M) * kLog2e);
+        }
+        sum = (s4[0] + s4[1]) + (s4[2] + s4[3]);
       }
       float* dst = P.part + ((r - P.row0) * P.n_nt + nt) * 2;
       dst[0] = M;
-      dst[1] = s;
+      dst[1] = sum;
+      const int tc = s_tcol[tid];
+      if (tc >= 0) P.xt[r - P.row0] = BF16::load(xs + xs_index(tid, tc));
     }
   } else {
 #pragma unroll
@@ -271,20 +344,34 @@ void lce_tile_kernel(LceParams P) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int rl = wm * kWM + i * 32 + (v >> 2) * 8 + half * 4 + (v & 3);
-        const int64_t r = m0 + rl;
-        if (r >= row_end) continue;
         const float gv = s_g[rl], M = s_m[rl], LS = s_ls[rl];
         const int tc = s_tcol[rl];
-        uint16_t* dst = P.G + (r - P.row0) * P.ldg + n0;
 #pragma unroll
         for (int j = 0; j < kTN; ++j) {
           const int cl = wn * kWN + j * 32 + col_lane;
-          if (n0 + cl >= P.V) continue;
           const float x = bf16_round(acc[i][j][v]);
           const float p = fast_exp2(((x - M) - LS) * kLog2e);
           const float o = (cl == tc) ? (1.f - p) * gv : -p * gv;
-          dst[cl] = BF16::from_float(o);
+          xs[xs_index(rl, cl)] = BF16::from_float(o);
         }
+      }
+    }
+    __syncthreads();
+    // 32 threads per row, one 16-byte chunk each; 8 rows per pass
+    const int c = tid & 31;
+    for (int k = 0; k < kBM / 8; ++k) {
+      const int rl = (tid >> 5) + 8 * k;
+      const int64_t r = m0 + rl;
+      const int64_t col0 = n0 + c * 8;
+      if (r >= row_end || col0 >= P.V) continue;
+      const vu4 q = reinterpret_cast<const vu4*>(xs + rl * kBN)[c ^ (rl & 31)];
+      uint16_t* dst = P.G + (r - P.row0) * P.ldg + col0;
+      if (col0 + 8 <= P.V && (reinterpret_cast<uintptr_t>(dst) & 15u) == 0) {
+        *reinterpret_cast<vu4*>(dst) = q;
+      } else {
+        const uint32_t wv[4] = {q.x, q.y, q.z, q.w};
+        for (int e = 0; e < 8 && col0 + e < P.V; ++e)
+          dst[e] = (uint16_t)(wv[e >> 1] >> ((e & 1) * 16));
       }
     }
   }
@@ -387,7 +474,7 @@ extern "C" int mirl_linear_ce_fwd(const void* hidden, int64_t T, int64_t Hd, int
   P.n_nt = ceil_div(V, kBN);
   P.part = workspace;
   P.xt = workspace + T * P.n_nt * 2;
-  const int64_t grid = P.n_mt * P.n_nt;
+  const int64_t grid = ceil_div(P.n_mt * P.n_nt, kXcds) * kXcds;
   MIRL_REQUIRE(grid < (int64_t(1) << 31), "too many tiles");
   hipLaunchKernelGGL((lce_tile_kernel<kFwd>), dim3((unsigned)grid), dim3(kThreads), 0, st, P);
   hipLaunchKernelGGL(lce_merge_kernel, dim3((unsigned)ceil_div(T, 4)), dim3(256), 0, st, P.part,
@@ -435,7 +522,7 @@ extern "C" int mirl_linear_ce_grad(const void* hidden, int64_t T, int64_t Hd, in
   P.gss = g_stride_s;
   P.G = static_cast<uint16_t*>(grad_logits);
   P.ldg = ldg;
-  const int64_t grid = P.n_mt * P.n_nt;
+  const int64_t grid = ceil_div(P.n_mt * P.n_nt, kXcds) * kXcds;
   MIRL_REQUIRE(grid < (int64_t(1) << 31), "too many tiles");
   hipLaunchKernelGGL((lce_tile_kernel<kGrad>), dim3((unsigned)grid), dim3(kThreads), 0, st, P);
   return check_launch("mirl_linear_ce_grad");
