@@ -16,8 +16,8 @@
 // Tile: 256 rows x 256 columns per 256-thread workgroup, K in steps of 64,
 // two LDS stages of 64 KB.  Each wave owns a 128 x 128 quarter as 4 x 4
 // v_mfma_f32_32x32x16_bf16 tiles (256 fp32 accumulators per lane).  LDS rows are
-// 128 B with their 16-byte chunks XOR-swizzled by (row % 8), so the 32 rows
-// read by one MFMA operand load fall in distinct banks.
+// 128 B with their 16-byte chunks XOR-swizzled (see lds_off), so the rows read
+// by one MFMA operand load fall in distinct banks.
 //
 // MFMA 32x32x16 bf16 lane layout (checked on gfx950): lane l holds A[l % 32][k]
 // and B[k][l % 32] for k = (l / 32) * 8 + 0..7; accumulator element v of lane l
@@ -47,8 +47,13 @@ constexpr int kLoadsPerThread = kBM * kRowBytes / 16 / kThreads;  // 16-byte chu
 constexpr int kGroupM = 4;               // row tiles sharing a sweep over the vocabulary
 constexpr int kXcds = 8;                 // accelerator dies, each with its own L2
 
+// LDS byte offset of 16-byte chunk `chunk` of tile row `row`.  A ds_read_b128
+// serves 16 lanes per pass (16 x 16 B = the 64 four-byte banks); an MFMA
+// operand read has those lanes on 16 consecutive rows at one chunk, so the
+// chunk is XOR-ed with (row / 2) % 8: the 8 even and the 8 odd rows then each
+// hit 8 distinct chunks, i.e. 16 distinct bank groups.
 __device__ __forceinline__ int lds_off(int row, int chunk) {
-  return row * kRowBytes + ((chunk ^ (row & 7)) << 4);
+  return row * kRowBytes + ((chunk ^ ((row >> 1) & 7)) << 4);
 }
 
 // Epilogue layout of a [256][256] bf16 tile in LDS: row-major, 16-byte chunks
@@ -191,18 +196,16 @@ void lce_tile_kernel(LceParams P) {
   const int jstride_a = (int)(32 * P.ldh * 2), jstride_b = (int)(32 * P.ldw * 2);
   const int st_off = lds_off(ld_row, ld_chunk);  // + j * 32 rows
 
-  vu4 ra[kLoadsPerThread], rb[kLoadsPerThread];
-  auto gload = [&](int kt) {
+  // Two staging register sets: the data of step m lives in set m % 2.
+  vu4 ra[2][kLoadsPerThread], rb[2][kLoadsPerThread];
+  auto gload_one = [&](int set, int kt, int j) {
     const int k_bytes = kt * kBK * 2;
-#pragma unroll
-    for (int j = 0; j < kLoadsPerThread; ++j) {
-      ra[j] = __builtin_bit_cast(vu4, __builtin_amdgcn_raw_buffer_load_b128(rsrc_a, voff_a, j * jstride_a + k_bytes, 0));
-      rb[j] = __builtin_bit_cast(vu4, __builtin_amdgcn_raw_buffer_load_b128(rsrc_b, voff_b, j * jstride_b + k_bytes, 0));
-    }
+    ra[set][j] = __builtin_bit_cast(vu4, __builtin_amdgcn_raw_buffer_load_b128(rsrc_a, voff_a, j * jstride_a + k_bytes, 0));
+    rb[set][j] = __builtin_bit_cast(vu4, __builtin_amdgcn_raw_buffer_load_b128(rsrc_b, voff_b, j * jstride_b + k_bytes, 0));
   };
-  auto sstore_one = [&](unsigned char* base, int j) {
-    *reinterpret_cast<vu4*>(base + st_off + j * 32 * kRowBytes) = ra[j];
-    *reinterpret_cast<vu4*>(base + kBM * kRowBytes + st_off + j * 32 * kRowBytes) = rb[j];
+  auto sstore_one = [&](int set, unsigned char* base, int j) {
+    *reinterpret_cast<vu4*>(base + st_off + j * 32 * kRowBytes) = ra[set][j];
+    *reinterpret_cast<vu4*>(base + kBM * kRowBytes + st_off + j * 32 * kRowBytes) = rb[set][j];
   };
 
   // fragment read offsets: row (wm*128 | wn*128) + i*32 + (lane & 31), chunk kk*2 + (lane >> 5)
@@ -233,26 +236,34 @@ void lce_tile_kernel(LceParams P) {
   };
 
   // Prologue: step 0 into LDS stage 0, step 1's loads in flight, block 0's fragments.
-  gload(0);
 #pragma unroll
-  for (int j = 0; j < kLoadsPerThread; ++j) sstore_one(lds, j);
-  if (nk > 1) gload(1);
+  for (int j = 0; j < kLoadsPerThread; ++j) gload_one(0, 0, j);
+#pragma unroll
+  for (int j = 0; j < kLoadsPerThread; ++j) sstore_one(0, lds, j);
+  if (nk > 1) {
+#pragma unroll
+    for (int j = 0; j < kLoadsPerThread; ++j) gload_one(1, 1, j);
+  }
   __syncthreads();
 #pragma unroll
   for (int idx = 0; idx < kTM + kTN; ++idx) fread(0, lds, 0, idx);
 
-  // One K step.  NEXT: the loads of step kt + 1 (in the staging registers) are
-  // written to the other LDS stage during block 2, and the next step's block-0
-  // fragments are read during block 3.  LOAD: right after those writes the
-  // staging registers take step kt + 2's loads, a full step before they are
-  // written in turn.  Every read of the current stage happens before the
-  // step's barrier; the first write into it (step kt + 2's data) comes in the
-  // next step's block 2, after that barrier.
-  auto step = [&](int kt, auto next_c, auto load_c) {
+  // One K step kt (PAR = kt % 2).  Step kt + 2's loads go into staging set PAR
+  // (free since step kt's data went to LDS one step earlier), two pairs per
+  // block, a step or more before they are written; blocks 1 and 2 write step
+  // kt + 1's data (set PAR ^ 1) to the other LDS stage, one chunk pair every 4
+  // MFMAs; block 3 reads the next step's block-0 fragments after the barrier.
+  // Spreading the loads and writes keeps the address and LDS data queues from
+  // filling, which would stall the single wave of the SIMD and with it the
+  // MFMAs queued behind.  Every read of the current stage happens before the
+  // step's barrier; the next write into it (step kt + 2's data) comes in the
+  // next step's block 1.
+  auto step = [&](int kt, auto par_c, auto next_c, auto load_c) {
+    constexpr int PAR = decltype(par_c)::value;
     constexpr bool NEXT = decltype(next_c)::value;
     constexpr bool LOAD = decltype(load_c)::value;
-    const unsigned char* cur = lds + (kt & 1) * kStageBytes;
-    unsigned char* nxt = lds + ((kt + 1) & 1) * kStageBytes;
+    const unsigned char* cur = lds + PAR * kStageBytes;
+    unsigned char* nxt = lds + (PAR ^ 1) * kStageBytes;
 #pragma unroll
     for (int kk = 0; kk < 3; ++kk) {
       const int set = kk & 1;
@@ -260,13 +271,15 @@ void lce_tile_kernel(LceParams P) {
       for (int q = 0; q < kTM * kTN; ++q) {
         mfma(set, q);
         if (q < kTM + kTN) fread(set ^ 1, cur, kk + 1, q);
+        if constexpr (LOAD) {
+          if ((q & 7) == 0) gload_one(PAR, kt + 2, kk * 2 + (q >> 3));
+        }
         if constexpr (NEXT) {
-          if (kk == 2 && q >= 8) sstore_one(nxt, q - 8);
+          if (kk >= 1 && (q & 3) == 0) sstore_one(PAR ^ 1, nxt, (kk - 1) * 4 + (q >> 2));
         }
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    if constexpr (LOAD) gload(kt + 2);
     __syncthreads();
 #pragma unroll
     for (int q = 0; q < kTM * kTN; ++q) {
@@ -274,15 +287,25 @@ void lce_tile_kernel(LceParams P) {
       if constexpr (NEXT) {
         if (q < kTM + kTN) fread(0, nxt, 0, q);
       }
+      if constexpr (LOAD) {
+        if ((q & 7) == 0) gload_one(PAR, kt + 2, 6 + (q >> 3));
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
   };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
   using T_ = std::integral_constant<bool, true>;
   using F_ = std::integral_constant<bool, false>;
+  // nk is even (the hidden size is a multiple of 2 * kBK): pairs of steps,
+  // then the last pair without the loads that would run past the end.
   int kt = 0;
-  for (; kt + 2 < nk; ++kt) step(kt, T_{}, T_{});
-  if (kt + 1 < nk) step(kt++, T_{}, F_{});
-  step(kt, F_{}, F_{});
+  for (; kt + 2 < nk; kt += 2) {
+    step(kt, I0{}, T_{}, T_{});
+    step(kt + 1, I1{}, T_{}, T_{});
+  }
+  step(kt, I0{}, T_{}, F_{});
+  step(kt + 1, I1{}, F_{}, F_{});
 
   // ---- epilogue: the tile goes through LDS as bf16, one row per thread ----
   //
@@ -423,7 +446,7 @@ int check_common(const void* hidden, int64_t T, int64_t Hd, int64_t ldh, const v
                (long long)T, (long long)V, (long long)Hd, (long long)bsz);
   MIRL_REQUIRE(T % bsz == 0, "row count %lld is not a multiple of the batch size %lld",
                (long long)T, (long long)bsz);
-  MIRL_REQUIRE(Hd % kBK == 0, "hidden size %lld must be a multiple of %d", (long long)Hd, kBK);
+  MIRL_REQUIRE(Hd % (2 * kBK) == 0, "hidden size %lld must be a multiple of %d", (long long)Hd, 2 * kBK);
   MIRL_REQUIRE(ldh % 8 == 0 && ldw % 8 == 0 && ldh >= Hd && ldw >= Hd,
                "row strides (%lld, %lld) must be multiples of 8 elements and >= the hidden size",
                (long long)ldh, (long long)ldw);

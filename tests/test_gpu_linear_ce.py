@@ -57,8 +57,8 @@ def _target_logits(hidden, weight, target):
     return x.gather(-1, target.clamp(0, weight.shape[0] - 1).unsqueeze(-1)).squeeze(-1)
 
 
-@pytest.mark.parametrize("S,B,H,V", [(37, 3, 128, 1000), (16, 2, 256, 151936), (300, 1, 64, 4096),
-                                     (5, 4, 192, 257)])
+@pytest.mark.parametrize("S,B,H,V", [(37, 3, 128, 1000), (16, 2, 256, 151936), (300, 1, 128, 4096),
+                                     (5, 4, 384, 257)])
 def test_forward_against_oracle(S, B, H, V):
     say("linear-ce fwd", S, B, H, V)
     hidden, weight, target = _inputs(S, B, H, V, seed=S + V)
@@ -116,7 +116,7 @@ def test_gradients_against_oracle(chunk):
 
 def test_all_zero_gradient_tiles():
     say("linear-ce zero-gradient tiles")
-    S, B, H, V = 300, 1, 64, 600  # 300 rows: one full 256-row tile of zeros
+    S, B, H, V = 300, 1, 128, 600  # 300 rows: one full 256-row tile of zeros
     hidden, weight, target = _inputs(S, B, H, V, seed=31)
     g = torch.zeros(B, S)
     g[:, 280:] = 1.0
@@ -147,7 +147,7 @@ def test_fused_matches_materialised_logits_path():
 
 def test_errors():
     say("linear-ce errors")
-    hidden, weight, target = _inputs(4, 2, 96, 50, seed=1)  # H = 96 is not a multiple of 64
+    hidden, weight, target = _inputs(4, 2, 192, 50, seed=1)  # H = 192 is not a multiple of 128
     with pytest.raises(MirlError):
         ChunkedDistributedHiddenStatesToLogprobs.apply(
             hidden.to(DEV), target.to(DEV), weight.to(DEV), 0, 50, None, None, True)
