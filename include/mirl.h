@@ -92,6 +92,100 @@ int mirl_logprob_bwd(const void* logits, int dtype, int64_t B, int64_t R,
                      int64_t g_stride_b, int64_t g_stride_r, void* grad_in,
                      int64_t gi_stride_b, int64_t gi_stride_r, void* stream);
 
+/*
+ * Log-probabilities at K given vocabulary ids per row:
+ *   out[b,r,k] = (x[id - vocab_start] - m) - logsum   for vocab_start <= id < vocab_end,
+ *   out[b,r,k] = 0                                     otherwise,
+ * with m and logsum as in mirl_logprob_fwd (one read of the row; the K
+ * re-reads hit the row just streamed).  `indices` is an int64 [B, R, K] view;
+ * `out` is a contiguous fp32 [B, R, K] array; `row_stats` (optional) receives
+ * {m, logsum} per row for mirl_gather_logprob_bwd.
+ *
+ * Replaces: ChunkedDistributedGatherLogprob.forward
+ * (nemo_rl/distributed/model_utils.py:691-748) with a vocab group of size 1,
+ * and the single-device log_softmax + gather of
+ * get_policy_logprobs_at_sampler_topk (model_utils.py:1723-1865).
+ */
+int mirl_gather_logprob_fwd(const void* logits, int dtype, int64_t B, int64_t R,
+                            int64_t V, int64_t stride_b, int64_t stride_r,
+                            const int64_t* indices, int64_t K,
+                            int64_t i_stride_b, int64_t i_stride_r,
+                            int64_t i_stride_k, int64_t vocab_start,
+                            int64_t vocab_end, float* out, float* row_stats,
+                            void* stream);
+
+/* fp32 scratch elements mirl_gather_logprob_bwd needs (one per row). */
+int64_t mirl_gather_logprob_workspace_elems(int64_t B, int64_t R);
+
+/*
+ * Gradient of mirl_gather_logprob_fwd with respect to the logits:
+ *   grad[b,r,v] = -p[v] * sum_k g[b,r,k] + sum_{k : id_k = v, in range} g[b,r,k],
+ * p = exp((x - m) - logsum), formed in fp32 (the id terms added in k order
+ * after the dense term) and rounded once to the logits dtype.  K must be >= 1.
+ * `workspace` holds mirl_gather_logprob_workspace_elems(B, R) floats.
+ *
+ * Replaces: ChunkedDistributedGatherLogprob.backward (model_utils.py:750-805),
+ * whose fp32 gradient autograd rounds to the logits dtype.
+ */
+int mirl_gather_logprob_bwd(const void* logits, int dtype, int64_t B, int64_t R,
+                            int64_t V, int64_t stride_b, int64_t stride_r,
+                            const int64_t* indices, int64_t K,
+                            int64_t i_stride_b, int64_t i_stride_r,
+                            int64_t i_stride_k, int64_t vocab_start,
+                            int64_t vocab_end, const float* row_stats,
+                            const float* grad_out, int64_t g_stride_b,
+                            int64_t g_stride_r, int64_t g_stride_k,
+                            float* workspace, void* grad_in,
+                            int64_t gi_stride_b, int64_t gi_stride_r,
+                            void* stream);
+
+/* ---------------------------------------------------------------------- */
+/* student / teacher divergences over the full vocabulary                  */
+/* ---------------------------------------------------------------------- */
+
+/* kinds of mirl_divergence_fwd / _bwd (p = softmax(student), q = softmax(teacher)) */
+#define MIRL_DIV_ENTROPY 0       /* L = sum_v p log p (teacher unused)      */
+#define MIRL_DIV_CROSS_ENTROPY 1 /* L = -sum_v p log q                      */
+#define MIRL_DIV_REVERSE_KL 2    /* L = sum_v p (log p - log q)             */
+
+/*
+ * Per-row divergence L[b,r] (fp32) in one read of the student row (and of the
+ * teacher row for the cross entropy and reverse KL).  `row_stats` (optional)
+ * receives {m_s, logZ_s, m_t, logZ_t} per row ([B, R, 4] floats) for
+ * mirl_divergence_bwd; both tensors share the dtype.
+ *
+ * Replaces: the forwards of ChunkedDistributedEntropy,
+ * ChunkedDistributedCrossEntropyToFixedLogits and
+ * ChunkedDistributedReverseKLToFixedLogits
+ * (nemo_rl/distributed/model_utils.py:2199-2351, reduction :2377-2434) with a
+ * vocab group of size 1.
+ */
+int mirl_divergence_fwd(int kind, const void* student, const void* teacher,
+                        int dtype, int64_t B, int64_t R, int64_t V,
+                        int64_t s_stride_b, int64_t s_stride_r,
+                        int64_t t_stride_b, int64_t t_stride_r, float* out,
+                        float* row_stats, void* stream);
+
+/*
+ * Gradient of mirl_divergence_fwd with respect to the student logits:
+ *   grad[b,r,v] = (p_v * (w_v - L[b,r])) * g[b,r],
+ *   w = log p (entropy), -log q (cross entropy), log p - log q (reverse KL),
+ * in fp32, rounded once to the logits dtype.  Rows with g == 0 are written as
+ * zeros without reading the logits.
+ *
+ * Replaces: _chunked_distributed_student_teacher_backward
+ * (nemo_rl/distributed/model_utils.py:2437-2499).
+ */
+int mirl_divergence_bwd(int kind, const void* student, const void* teacher,
+                        int dtype, int64_t B, int64_t R, int64_t V,
+                        int64_t s_stride_b, int64_t s_stride_r,
+                        int64_t t_stride_b, int64_t t_stride_r,
+                        const float* out, const float* row_stats,
+                        const float* grad_out, int64_t g_stride_b,
+                        int64_t g_stride_r, void* grad_in,
+                        int64_t gi_stride_b, int64_t gi_stride_r,
+                        void* stream);
+
 /* ---------------------------------------------------------------------- */
 /* top-k / top-p / temperature-filtered logprobs                            */
 /* ---------------------------------------------------------------------- */
@@ -299,7 +393,37 @@ typedef struct mirl_view2d {
 #define MIRL_M_POSITIVE_NLL_LOSS 15
 #define MIRL_M_IS_OOB_RATIO 16
 #define MIRL_M_POLICY_SUPPORT_EXCLUDED_TOKENS 17
-#define MIRL_NUM_METRICS 18
+#define MIRL_M_SCORE_CENTERING_HEAD_MASS 18
+#define MIRL_NUM_METRICS 19
+
+/* importance-sampling modes of score centering (score_centering.py:22-129) */
+#define MIRL_SC_OFF 0
+#define MIRL_SC_IS 1
+#define MIRL_SC_TIS 2
+#define MIRL_SC_ICEPOP 3
+#define MIRL_SC_ADAPTIVE 4
+
+/*
+ * Score-centering inputs: the trainer's log-probs at the sampler's top-k ids
+ * (`plog`, [B, L, K]) and the sampler's own log-probs at those ids (`qlog`,
+ * [B, L, K]), both strided views of the loss dtype; element (b, l, k) is
+ * ptr[b*sb + l*sl + k*sk].  `lo`/`hi` are the TIS / ICEPOP bounds or
+ * adaptive-ppo-clip's lower and (offset) upper bound, `outer` its outer bound.
+ * `grad` receives a contiguous [B, L, K] array of the loss dtype: the
+ * gradient of the loss w.r.t. plog (mirl_clipped_pg) or the coefficients
+ * d term / d plog (mirl_score_centering_term).
+ */
+typedef struct mirl_score_centering_args {
+  int32_t mode;  /* MIRL_SC_* */
+  int32_t pad_;
+  int64_t K;
+  double lo, hi, outer;
+  const void* plog;
+  int64_t p_sb, p_sl, p_sk;
+  const void* qlog;
+  int64_t q_sb, q_sl, q_sk;
+  void* grad;
+} mirl_score_centering_args;
 
 /* Number of scratch elements (of the loss dtype) mirl_clipped_pg needs. */
 int64_t mirl_clipped_pg_workspace_elems(int64_t B);
@@ -314,6 +438,11 @@ int64_t mirl_clipped_pg_workspace_elems(int64_t B);
  * support_mask is uint8 (bool); sample_mask and rewards are [B] vectors;
  * global_valid_seqs / global_valid_toks are device scalars of `dtype`.
  * `workspace` holds mirl_clipped_pg_workspace_elems(B) elements of `dtype`.
+ * `score_centering` is NULL or adds the score-centering correction: the
+ * per-token term of mirl_score_centering_term at the final loss mask, times
+ * the masked advantage, reduced like the actor loss and added to it; the
+ * advantages are zeroed outside the mask; metrics[MIRL_M_SCORE_CENTERING_HEAD_MASS]
+ * is the masked mean head mass; score_centering->grad receives dloss/dplog.
  *
  * Replaces: ClippedPGLossFn.__call__ (loss_functions.py:698-1183) with
  * clipped_pg_actor_objective / clipped_pg_diagnostic_metrics
@@ -329,8 +458,31 @@ int mirl_clipped_pg(const mirl_pg_config* cfg, int dtype, int64_t B, int64_t L,
                     const void* sample_mask, const void* rewards,
                     const void* global_valid_seqs,
                     const void* global_valid_toks, void* metrics,
-                    void* grad_curr, void* grad_unfiltered, void* workspace,
-                    void* stream);
+                    void* grad_curr, void* grad_unfiltered,
+                    const mirl_score_centering_args* score_centering,
+                    void* workspace, void* stream);
+
+/*
+ * Per-token score-centering term over [B, L] tokens:
+ *   p = exp(plog), q = exp(qlog), head = sum_k q, rho = max(1 - head, 0) / max(1 - sum_k p, 1e-6)
+ *   mode off: mass = q, alpha = rho;  is: mass = p, alpha = 1
+ *   tis: mass = min(max(p, lo q), hi q), alpha = min(max(1, lo rho), hi rho)
+ *   icepop: mass = p where lo <= p/q <= hi else 0, alpha = [lo <= 1/rho <= hi]
+ *   adaptive-ppo-clip: as icepop with the advantage-signed bounds and `outer`
+ *   coef = mass - alpha p,   term = sum_k coef_k plog_k,   head_mass = head,
+ * all 0 where token_mask is 0.  Writes term[B, L], head_mass[B, L]
+ * (contiguous, the loss dtype) and coef into args->grad.  `advantages` (a
+ * [B, L] view, read by adaptive-ppo-clip only) may have a NULL pointer
+ * otherwise.
+ *
+ * Replaces: compute_score_centering_term
+ * (nemo_rl/algorithms/loss/score_centering.py:22-129); its autograd backward
+ * is coef * d(term).
+ */
+int mirl_score_centering_term(int dtype, int64_t B, int64_t L,
+                              const mirl_score_centering_args* args,
+                              mirl_view2d token_mask, mirl_view2d advantages,
+                              void* term, void* head_mass, void* stream);
 
 /* ---------------------------------------------------------------------- */
 /* GRPO group-normalised advantages                                         */

@@ -38,6 +38,7 @@ DEFAULTS: dict[str, Any] = dict(
     use_cispo=False,
     positive_example_nll_weight=0.0,
     metrics_level="full",
+    score_centering=False,
 )
 
 
@@ -110,6 +111,7 @@ def clipped_pg_loss(
     global_valid_seqs: torch.Tensor,
     global_valid_toks: torch.Tensor,
     policy_support_mask: Optional[torch.Tensor] = None,
+    policy_logprobs_at_sampler_topk: Optional[torch.Tensor] = None,
     **cfg: Any,
 ) -> tuple[torch.Tensor, dict[str, float]]:
     """Loss and metric dict of ClippedPGLossFn.__call__ (reference loss_functions.py:698-1183)."""
@@ -149,6 +151,8 @@ def clipped_pg_loss(
     curr = torch.where(mask.bool(), curr, 0.0)
     prev = torch.where(mask.bool(), prev, 0.0)
     gen = torch.where(mask.bool(), gen, 0.0)
+    if c["score_centering"]:
+        adv = torch.where(mask.bool(), adv.detach(), 0.0)
 
     if beta != 0:
         if c["use_on_policy_kl_approximation"]:
@@ -205,6 +209,35 @@ def clipped_pg_loss(
     use_iw = iw if c["use_importance_sampling_correction"] else None
     actor, ratios, ratios_c = _actor_objective(curr, prev, adv, token_mask, mask, sample_mask,
                                                use_iw, gvt, gvs, c)
+    sc_metrics: dict = {}
+    if c["score_centering"]:
+        # reference loss_functions.py:1070-1097 with _get_score_centering_is_bounds (:659-671)
+        from oracle.score_centering import score_centering_term
+
+        mode = (tis_type or "is") if c["use_importance_sampling_correction"] else "off"
+        if mode in ("tis", "icepop"):
+            bounds = (tis_min or 0.0, tis_ratio)
+        elif mode == "adaptive-ppo-clip":
+            bounds = (tis_min, tis_ratio + c["adaptive_ppo_clip_k"])
+        else:
+            bounds = None
+        centering, head_mass = score_centering_term(
+            policy_logprobs_at_sampler_topk,
+            sampler_topk_logprobs=data["sampler_topk_logprobs"][:, 1:],
+            importance_sampling_mode=mode,
+            is_bounds=bounds,
+            token_mask=mask,
+            adaptive_ppo_clip_advantages=adv,
+            adaptive_ppo_clip_outer_bound=c["truncated_importance_sampling_adaptive_outer_bound"],
+        )
+        correction = adv * centering
+        if c["token_level_loss"]:
+            actor = actor + masked_mean(correction, mask, global_normalization_factor=gvt)
+        else:
+            actor = actor + masked_mean(masked_mean(correction, token_mask, dim=-1), sample_mask,
+                                        global_normalization_factor=gvs)
+        sc_metrics["score_centering_head_mass"] = masked_mean(head_mass, mask,
+                                                              global_normalization_factor=gvt)
     if need_iw:
         if c["sequence_level_importance_ratios"]:
             sir = masked_mean(iw.squeeze(-1), sample_mask, global_normalization_factor=gvs)
@@ -250,6 +283,7 @@ def clipped_pg_loss(
         m["num_valid_samples"] = sample_mask.sum()
         m["positive_nll_loss"] = nll
         m.update(filt)
+        m.update({k: v.detach() for k, v in sc_metrics.items()})
         m["policy_support_excluded_tokens"] = (kl_mask - mask).sum()
     vals = torch.stack([v.detach().to(loss.dtype).reshape(()) for v in m.values()]).tolist()
     return loss, dict(zip(m, vals))

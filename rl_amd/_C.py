@@ -48,8 +48,15 @@ PG_METRIC_SLOTS = {
     "positive_nll_loss": 15,
     "is_oob_ratio": 16,
     "policy_support_excluded_tokens": 17,
+    "score_centering_head_mass": 18,
 }
-PG_NUM_METRICS = 18
+PG_NUM_METRICS = 19
+
+# score-centering importance-sampling modes (MIRL_SC_* in include/mirl.h)
+SC_MODES = {"off": 0, "is": 1, "tis": 2, "icepop": 3, "adaptive-ppo-clip": 4}
+
+# divergence kinds (MIRL_DIV_* in include/mirl.h)
+DIV_KINDS = {"entropy": 0, "cross_entropy": 1, "reverse_kl": 2}
 
 
 class MirlError(RuntimeError):
@@ -92,6 +99,28 @@ class View2D(ctypes.Structure):
     _fields_ = [("ptr", ctypes.c_void_p), ("sb", ctypes.c_int64), ("sl", ctypes.c_int64)]
 
 
+class ScArgs(ctypes.Structure):
+    """mirl_score_centering_args."""
+
+    _fields_ = [
+        ("mode", ctypes.c_int32),
+        ("pad_", ctypes.c_int32),
+        ("K", ctypes.c_int64),
+        ("lo", ctypes.c_double),
+        ("hi", ctypes.c_double),
+        ("outer", ctypes.c_double),
+        ("plog", ctypes.c_void_p),
+        ("p_sb", ctypes.c_int64),
+        ("p_sl", ctypes.c_int64),
+        ("p_sk", ctypes.c_int64),
+        ("qlog", ctypes.c_void_p),
+        ("q_sb", ctypes.c_int64),
+        ("q_sl", ctypes.c_int64),
+        ("q_sk", ctypes.c_int64),
+        ("grad", ctypes.c_void_p),
+    ]
+
+
 # exported symbol -> (restype, argtypes)
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -111,7 +140,32 @@ SIGNATURES = {
     "mirl_clipped_pg_workspace_elems": (_I64, [_I64]),
     "mirl_clipped_pg": (
         _I,
-        [ctypes.POINTER(PgConfig), _I, _I64, _I64] + [View2D] * 8 + [_P] * 9,
+        [ctypes.POINTER(PgConfig), _I, _I64, _I64] + [View2D] * 8 + [_P] * 7
+        + [ctypes.POINTER(ScArgs), _P, _P],
+    ),
+    "mirl_score_centering_term": (
+        _I,
+        [_I, _I64, _I64, ctypes.POINTER(ScArgs), View2D, View2D, _P, _P, _P],
+    ),
+    "mirl_gather_logprob_fwd": (
+        _I,
+        [_P, _I, _I64, _I64, _I64, _I64, _I64, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P,
+         _P],
+    ),
+    "mirl_gather_logprob_workspace_elems": (_I64, [_I64, _I64]),
+    "mirl_gather_logprob_bwd": (
+        _I,
+        [_P, _I, _I64, _I64, _I64, _I64, _I64, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P,
+         _I64, _I64, _I64, _P, _P, _I64, _I64, _P],
+    ),
+    "mirl_divergence_fwd": (
+        _I,
+        [_I, _P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _P],
+    ),
+    "mirl_divergence_bwd": (
+        _I,
+        [_I, _P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _I64, _I64, _P,
+         _I64, _I64, _P],
     ),
     "mirl_grpo_advantage": (
         _I,
@@ -405,8 +459,14 @@ def clipped_pg(
     rewards: Optional[torch.Tensor],
     global_valid_seqs: torch.Tensor,
     global_valid_toks: torch.Tensor,
+    score_centering: Optional[ScArgs] = None,
 ) -> tuple[torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
-    """Run the fused ClippedPG kernel; returns (metrics[18], grad_curr, grad_unfiltered)."""
+    """Run the fused ClippedPG kernel; returns (metrics[19], grad_curr, grad_unfiltered).
+
+    With ``score_centering`` (a filled ScArgs whose ``grad`` points at a
+    [B, L, K] buffer of the loss dtype) the correction is added to the loss and
+    dloss/dplog is written into that buffer.
+    """
     dev = _require_gpu(curr, token_mask, advantages, generation, sample_mask)
     B, L = curr.shape
     dtype = curr.dtype
@@ -421,10 +481,166 @@ def clipped_pg(
         _view(token_mask), _view(advantages), _view(prev), _view(generation),
         _view(reference), _view(support_mask), sample_mask.data_ptr(), _ptr(rewards),
         global_valid_seqs.data_ptr(), global_valid_toks.data_ptr(), metrics.data_ptr(),
-        grad_curr.data_ptr(), _ptr(grad_unf), ws.data_ptr(), _stream(dev),
+        grad_curr.data_ptr(), _ptr(grad_unf),
+        None if score_centering is None else ctypes.byref(score_centering), ws.data_ptr(),
+        _stream(dev),
     )
     _check(st, "mirl_clipped_pg")
     return metrics, grad_curr, grad_unf
+
+
+def score_centering_args(
+    mode: str,
+    bounds: Optional[tuple],
+    outer: Optional[float],
+    plog: torch.Tensor,
+    qlog: torch.Tensor,
+    grad: torch.Tensor,
+) -> ScArgs:
+    """Fill mirl_score_centering_args for [B, L, K] views plog / qlog and a contiguous grad buffer."""
+    try:
+        code = SC_MODES[mode]
+    except KeyError:
+        raise ValueError(f"Unsupported score-centering IS mode {mode!r}") from None
+    assert plog.dim() == 3 and qlog.shape == plog.shape and grad.shape == plog.shape
+    assert plog.dtype == qlog.dtype == grad.dtype and grad.is_contiguous()
+    lo, hi = bounds if bounds is not None else (0.0, 0.0)
+    return ScArgs(
+        code, 0, plog.shape[2], float(lo), float(hi), float(outer if outer is not None else 0.0),
+        plog.data_ptr(), plog.stride(0), plog.stride(1), plog.stride(2),
+        qlog.data_ptr(), qlog.stride(0), qlog.stride(1), qlog.stride(2),
+        grad.data_ptr(),
+    )
+
+
+def score_centering_term(
+    args: ScArgs,
+    dtype: torch.dtype,
+    token_mask: torch.Tensor,
+    advantages: Optional[torch.Tensor],
+    term: torch.Tensor,
+    head_mass: torch.Tensor,
+) -> None:
+    """term / head_mass [B, L] (contiguous) and coef (into args.grad) of compute_score_centering_term."""
+    dev = _require_gpu(token_mask, advantages, term, head_mass)
+    B, L = token_mask.shape
+    assert term.is_contiguous() and head_mass.is_contiguous()
+    st = _launch(
+        "mirl_score_centering_term", dev,
+        DTYPE_CODES[dtype], B, L, ctypes.byref(args), _view(token_mask), _view(advantages),
+        term.data_ptr(), head_mass.data_ptr(), _stream(dev),
+    )
+    _check(st, "mirl_score_centering_term")
+
+
+# ---------------------------------------------------------------------------
+# logprobs at K ids per row
+# ---------------------------------------------------------------------------
+def gather_logprob_fwd(
+    logits: torch.Tensor,
+    indices: torch.Tensor,
+    vocab_start: int,
+    vocab_end: int,
+    out: torch.Tensor,
+    stats: Optional[torch.Tensor],
+) -> None:
+    """out[b, r, k] = log_softmax(logits[b, r])[indices[b, r, k] - vocab_start] (0 out of range).
+
+    logits: [B, R, V] (unit stride on V); indices: [B, R, K] int64; out: [B, R, K]
+    fp32 contiguous; stats: [B, R, 2] fp32 contiguous or None.
+    """
+    dev = _require_gpu(logits, indices, out, stats)
+    B, R, K = indices.shape
+    V = logits.shape[-1]
+    assert logits.stride(-1) == 1 and out.is_contiguous() and indices.dtype == torch.int64
+    assert stats is None or stats.is_contiguous()
+    st = _launch(
+        "mirl_gather_logprob_fwd", dev,
+        logits.data_ptr(), _dtype_code(logits), B, R, V, logits.stride(0), logits.stride(1),
+        indices.data_ptr(), K, indices.stride(0), indices.stride(1), indices.stride(2),
+        int(vocab_start), int(vocab_end), out.data_ptr(), _ptr(stats), _stream(dev),
+    )
+    _check(st, "mirl_gather_logprob_fwd")
+
+
+def gather_logprob_bwd(
+    logits: torch.Tensor,
+    indices: torch.Tensor,
+    vocab_start: int,
+    vocab_end: int,
+    stats: torch.Tensor,
+    grad_out: torch.Tensor,
+    grad_in: torch.Tensor,
+) -> None:
+    """grad_in = -softmax * sum_k g_k + scatter of g_k at the in-range ids (rounded once)."""
+    dev = _require_gpu(logits, indices, stats, grad_out, grad_in)
+    B, R, K = indices.shape
+    V = logits.shape[-1]
+    assert grad_in.stride(-1) == 1 and logits.stride(-1) == 1
+    assert grad_in.dtype == logits.dtype and grad_out.dtype == torch.float32
+    lib = load()
+    ws = torch.empty(int(lib.mirl_gather_logprob_workspace_elems(B, R)), dtype=torch.float32,
+                     device=dev)
+    st = _launch(
+        "mirl_gather_logprob_bwd", dev,
+        logits.data_ptr(), _dtype_code(logits), B, R, V, logits.stride(0), logits.stride(1),
+        indices.data_ptr(), K, indices.stride(0), indices.stride(1), indices.stride(2),
+        int(vocab_start), int(vocab_end), stats.data_ptr(), grad_out.data_ptr(),
+        grad_out.stride(0), grad_out.stride(1), grad_out.stride(2), ws.data_ptr(),
+        grad_in.data_ptr(), grad_in.stride(0), grad_in.stride(1), _stream(dev),
+    )
+    _check(st, "mirl_gather_logprob_bwd")
+
+
+# ---------------------------------------------------------------------------
+# student / teacher divergences
+# ---------------------------------------------------------------------------
+def divergence_fwd(
+    kind: str,
+    student: torch.Tensor,
+    teacher: Optional[torch.Tensor],
+    out: torch.Tensor,
+    stats: Optional[torch.Tensor],
+) -> None:
+    """out[b, r] = entropy / cross entropy / reverse KL of the row; stats [B, R, 4] or None."""
+    dev = _require_gpu(student, teacher, out, stats)
+    B, R, V = student.shape
+    assert student.stride(-1) == 1 and out.is_contiguous()
+    assert teacher is None or (teacher.stride(-1) == 1 and teacher.dtype == student.dtype)
+    assert stats is None or stats.is_contiguous()
+    t = teacher if teacher is not None else student
+    st = _launch(
+        "mirl_divergence_fwd", dev,
+        DIV_KINDS[kind], student.data_ptr(), _ptr(teacher), _dtype_code(student), B, R, V,
+        student.stride(0), student.stride(1), t.stride(0), t.stride(1), out.data_ptr(),
+        _ptr(stats), _stream(dev),
+    )
+    _check(st, "mirl_divergence_fwd")
+
+
+def divergence_bwd(
+    kind: str,
+    student: torch.Tensor,
+    teacher: Optional[torch.Tensor],
+    out: torch.Tensor,
+    stats: torch.Tensor,
+    grad_out: torch.Tensor,
+    grad_in: torch.Tensor,
+) -> None:
+    """grad_in[b, r, v] = (p_v (w_v - out[b, r])) * grad_out[b, r] in the logits dtype."""
+    dev = _require_gpu(student, teacher, out, stats, grad_out, grad_in)
+    B, R, V = student.shape
+    assert grad_in.stride(-1) == 1 and grad_in.dtype == student.dtype
+    assert grad_out.dtype == torch.float32
+    t = teacher if teacher is not None else student
+    st = _launch(
+        "mirl_divergence_bwd", dev,
+        DIV_KINDS[kind], student.data_ptr(), _ptr(teacher), _dtype_code(student), B, R, V,
+        student.stride(0), student.stride(1), t.stride(0), t.stride(1), out.data_ptr(),
+        stats.data_ptr(), grad_out.data_ptr(), grad_out.stride(0), grad_out.stride(1),
+        grad_in.data_ptr(), grad_in.stride(0), grad_in.stride(1), _stream(dev),
+    )
+    _check(st, "mirl_divergence_bwd")
 
 
 # ---------------------------------------------------------------------------

@@ -8,8 +8,12 @@ and the closed-form gradient with respect to ``next_token_logprobs`` (and
 back to the host in one device-to-host copy, as the reference's
 ``materialize_scalar_metrics`` does.
 
-Unsupported options raise ``NotImplementedError``: ``opd_full``,
-``score_centering``, ``seq_logprob_error_in_loss`` and fused linear logprobs.
+With ``score_centering`` the same kernels add the score-centering correction
+(reference score_centering.py:22-129, loss_functions.py:1070-1097) and its
+gradient with respect to ``policy_logprobs_at_sampler_topk``.
+
+Unsupported options raise ``NotImplementedError``: ``opd_full`` and
+``seq_logprob_error_in_loss``.
 """
 
 from __future__ import annotations
@@ -227,6 +231,22 @@ class ClippedPGLossFn(LossFunction):
                 )
         self.cur_adaptive_ppo_clip_k: float | None = 0.0 if self.has_adaptive_loss_state() else None
         self.score_centering = cfg.score_centering
+        if self.score_centering:
+            assert self.opd_full is None and not use_fused_linear_logprobs, (
+                "score_centering needs the policy-gradient loss on full logits"
+            )
+            assert not self.sequence_level_importance_ratios and (
+                not self.use_importance_sampling_correction
+                or self.truncated_importance_sampling_type in (None, "tis", "icepop", "adaptive-ppo-clip")
+            ), (
+                "score_centering composes only with importance sampling off or "
+                "token-level untruncated IS, 'tis', 'icepop', or 'adaptive-ppo-clip'"
+            )
+        self._score_centering_is_mode = (
+            (self.truncated_importance_sampling_type or "is")
+            if self.use_importance_sampling_correction
+            else "off"
+        )
         if self.reference_policy_kl_type not in _C.KL_TYPES and self.reference_policy_kl_penalty != 0:
             # the reference raises at call time (calculate_kl); keep that timing
             pass
@@ -319,6 +339,18 @@ class ClippedPGLossFn(LossFunction):
             cur_k += self.truncated_importance_sampling_adaptive_k_step
         self.set_adaptive_ppo_clip_k(cur_k)
 
+    def _get_score_centering_is_bounds(self) -> tuple[float, float] | None:
+        """Bounds that set the score-centering head and tail masses this step (reference :659-671)."""
+        if self._score_centering_is_mode in ("tis", "icepop"):
+            assert self.truncated_importance_sampling_ratio is not None
+            return (
+                self.truncated_importance_sampling_ratio_min or 0.0,
+                self.truncated_importance_sampling_ratio,
+            )
+        elif self._score_centering_is_mode == "adaptive-ppo-clip":
+            return self._get_adaptive_ppo_clip_bounds()
+        return None
+
     @property
     def requires_survivor_normalization(self) -> bool:
         return self.seq_logprob_error_in_loss
@@ -387,6 +419,8 @@ class ClippedPGLossFn(LossFunction):
         keys += ["kl_penalty", "num_valid_samples", "positive_nll_loss"]
         if self.truncated_importance_sampling_ratio is not None:
             keys.append("is_oob_ratio")
+        if self.score_centering:
+            keys.append("score_centering_head_mass")
         keys.append("policy_support_excluded_tokens")
         return keys
 
@@ -409,8 +443,6 @@ class ClippedPGLossFn(LossFunction):
         assert global_valid_toks is not None, "ClippedPGLossFn requires global_valid_toks"
         if self.opd_full is not None:
             raise NotImplementedError("opd_full is not supported by the rl_amd loss")
-        if self.score_centering:
-            raise NotImplementedError("score_centering is not supported by the rl_amd loss")
         if self.seq_logprob_error_in_loss:
             raise NotImplementedError("seq_logprob_error_in_loss is not supported by the rl_amd loss")
         assert next_token_logprobs is not None, "ClippedPGLossFn requires next_token_logprobs"
@@ -452,10 +484,34 @@ class ClippedPGLossFn(LossFunction):
         gvt = prep(global_valid_toks).reshape(())
         curr_k = curr if curr.dtype == dtype else curr.to(dtype)
         cfg = self._kernel_config(rewards is not None, support is not None, unfiltered is not None)
+        plog = None
+        sc = None
+        if self.score_centering:
+            assert policy_logprobs_at_sampler_topk is not None, (
+                "score_centering requires policy_logprobs_at_sampler_topk from prepare_loss_input"
+            )
+            plog = policy_logprobs_at_sampler_topk
+            if plog.dtype != dtype:
+                plog = plog.to(dtype)
+            qlog = data["sampler_topk_logprobs"][:, 1:]
+            qlog = torch.as_tensor(qlog).to(device=dev, dtype=dtype).detach()
+            if plog.dim() != 3 or tuple(plog.shape[:2]) != tuple(curr.shape):
+                raise ValueError(
+                    f"policy_logprobs_at_sampler_topk shape {tuple(plog.shape)} does not match "
+                    f"next_token_logprobs {tuple(curr.shape)} + [k]"
+                )
+            if tuple(qlog.shape) != tuple(plog.shape):
+                raise ValueError(
+                    f"sampler_topk_logprobs[:, 1:] shape {tuple(qlog.shape)} does not match "
+                    f"policy_logprobs_at_sampler_topk {tuple(plog.shape)}"
+                )
+            bounds = self._get_score_centering_is_bounds()
+            sc = (self._score_centering_is_mode, bounds,
+                  self.truncated_importance_sampling_adaptive_outer_bound, qlog)
 
         loss, metrics = _ClippedPGFunction.apply(
             curr_k, unfiltered, cfg, token_mask, advantages, prev, generation, reference,
-            support, sample_mask, rewards, gvs, gvt,
+            support, sample_mask, rewards, gvs, gvt, plog, sc,
         )
         values = _C.wait_and_fetch(metrics.detach())
         out = {k: float(values[_C.PG_METRIC_SLOTS[k]]) for k in self._metric_keys()}
@@ -481,12 +537,20 @@ class _ClippedPGFunction(torch.autograd.Function):
         rewards: Optional[torch.Tensor],
         gvs: torch.Tensor,
         gvt: torch.Tensor,
+        plog: Optional[torch.Tensor],
+        sc: Optional[tuple],
     ):
+        sc_args = None
+        grad_plog = None
+        if plog is not None:
+            mode, bounds, outer, qlog = sc
+            grad_plog = torch.empty(plog.shape, dtype=plog.dtype, device=plog.device)
+            sc_args = _C.score_centering_args(mode, bounds, outer, plog, qlog, grad_plog)
         metrics, grad_curr, grad_unf = _C.clipped_pg(
             cfg, curr, unfiltered, token_mask, advantages, prev, generation, reference, support,
-            sample_mask, rewards, gvs, gvt,
+            sample_mask, rewards, gvs, gvt, sc_args,
         )
-        ctx.save_for_backward(grad_curr, grad_unf)
+        ctx.save_for_backward(grad_curr, grad_unf, grad_plog)
         ctx.mark_non_differentiable(metrics)
         # no zero-filled gradient for the metrics output on the way back
         ctx.set_materialize_grads(False)
@@ -495,9 +559,10 @@ class _ClippedPGFunction(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx: Any, grad_loss: torch.Tensor, grad_metrics: torch.Tensor):  # type: ignore[override]
-        grad_curr, grad_unf = ctx.saved_tensors
+        grad_curr, grad_unf, grad_plog = ctx.saved_tensors
         if grad_loss is None:
-            return (None,) * 13
+            return (None,) * 15
         gc = grad_curr * grad_loss if ctx.needs_input_grad[0] else None
         gu = grad_unf * grad_loss if (grad_unf is not None and ctx.needs_input_grad[1]) else None
-        return gc, gu, None, None, None, None, None, None, None, None, None, None, None
+        gp = grad_plog * grad_loss if (grad_plog is not None and ctx.needs_input_grad[13]) else None
+        return (gc, gu) + (None,) * 11 + (gp, None)

@@ -31,10 +31,24 @@ from rl_amd.distributed.model_utils import (
     from_parallel_logits_to_logprobs_packed_sequences,
     get_next_token_logprobs_from_logits,
 )
+from rl_amd.distributed.vocab_reductions import get_policy_logprobs_at_sampler_topk
 
 
 def _unsupported(what: str) -> NotImplementedError:
     return NotImplementedError(f"{what} is not supported by the rl_amd logprob path")
+
+
+def _validate_score_centering_data(data: Any) -> None:
+    """Reject missing sampler inputs before computing trainer logprobs (reference loss_input.py:53-66)."""
+    missing = [
+        key for key in ("sampler_topk_token_ids", "sampler_topk_logprobs") if key not in data
+    ]
+    if missing:
+        raise ValueError(
+            f"Score centering requires {', '.join(missing)}: use SingleController "
+            "with NeMo Gym + vLLM, token_capture.enabled=true and "
+            "policy.generation.top_logprobs > 0."
+        )
 
 
 def prepare_loss_input(
@@ -53,11 +67,12 @@ def prepare_loss_input(
     """``(loss_input, data)`` for ``loss_fn`` (reference loss_input.py:215-322).
 
     LOGIT passes the logits through; LOGPROB computes next-token logprobs
-    (filtered when ``sampling_params`` asks for it).  The other input types
-    (OPD, distillation, draft) are outside this path and raise.
+    (filtered when ``sampling_params`` asks for it) and, for a loss with
+    ``score_centering``, the log-probs at the sampler's top-k ids.  The other
+    input types (OPD, distillation, draft) are outside this path and raise.
     """
     if getattr(loss_fn, "score_centering", False):
-        raise _unsupported("score centering")
+        _validate_score_centering_data(data)
     if loss_fn.input_type == LossInputType.LOGIT:
         return {"logits": logits}, data
     if loss_fn.input_type != LossInputType.LOGPROB:
@@ -96,6 +111,16 @@ def prepare_loss_input(
     loss_input: dict[str, Any] = {"next_token_logprobs": logprobs}
     if filtering:
         loss_input["policy_support_mask"] = ~torch.isneginf(logprobs)
+    if getattr(loss_fn, "score_centering", False):
+        loss_input["policy_logprobs_at_sampler_topk"] = get_policy_logprobs_at_sampler_topk(
+            sampler_topk_token_ids=data["sampler_topk_token_ids"],
+            next_token_logits=logits,
+            vocab_parallel_rank=vocab_parallel_rank,
+            vocab_parallel_group=vocab_parallel_group,
+            context_parallel_group=context_parallel_group,
+            chunk_size=chunk_size,
+            cp_sharder=cp_sharder,
+        )
     return loss_input, data
 
 
@@ -132,7 +157,7 @@ def prepare_packed_loss_input(
         "vocab_parallel_rank must be provided with vocab_parallel_group."
     )
     if getattr(loss_fn, "score_centering", False):
-        raise _unsupported("score centering")
+        _validate_score_centering_data(data)
     cp_size = _group_size(context_parallel_group)
     if cp_size != 1:
         raise _unsupported("context parallelism")
@@ -176,4 +201,21 @@ def prepare_packed_loss_input(
     loss_input: dict[str, Any] = {"next_token_logprobs": logprobs}
     if filtering:
         loss_input["policy_support_mask"] = ~torch.isneginf(logprobs)
+    if getattr(loss_fn, "score_centering", False):
+        sampler_ids = data["sampler_topk_token_ids"]
+        packed_sampler_ids = _pack_input_ids(
+            sampler_ids.to(logits.device), cu_seqlens_q, cu_seqlens_q_padded, cp_rank=0,
+            cp_size=1, roll_shift=-1,
+        )
+        loss_input["policy_logprobs_at_sampler_topk"] = get_policy_logprobs_at_sampler_topk(
+            sampler_topk_token_ids=sampler_ids,
+            next_token_logits=logits,
+            vocab_parallel_rank=vocab_parallel_rank,
+            vocab_parallel_group=vocab_parallel_group,
+            context_parallel_group=context_parallel_group,
+            chunk_size=chunk_size,
+            cu_seqlens_q=cu_seqlens_q,
+            cu_seqlens_q_padded=cu_seqlens_q_padded,
+            packed_sampler_topk_token_ids=packed_sampler_ids,
+        )
     return loss_input, data

@@ -26,6 +26,7 @@ SOURCES = [
     "advantage.hip",
     "topk_filter.hip",
     "linear_ce.hip",
+    "divergence.hip",
 ]
 
 ARCH = "gfx950"

@@ -47,6 +47,8 @@ enum Slot {
   P_NLL,
   P_OOB,
   P_EXCL,
+  P_SC,  // score-centering correction
+  P_HM,  // score-centering head mass
   NUM_SLOTS
 };
 
@@ -192,6 +194,81 @@ __device__ __forceinline__ T truncate_is(const mirl_pg_config& cfg, T w, T A, T 
   return w;
 }
 
+// torch.maximum / torch.minimum: NaN in either operand propagates.
+template <class T>
+__device__ __forceinline__ T tmaximum(T a, T b) {
+  return (isnan(a) || isnan(b)) ? a + b : (a > b ? a : b);
+}
+template <class T>
+__device__ __forceinline__ T tminimum(T a, T b) {
+  return (isnan(a) || isnan(b)) ? a + b : (a < b ? a : b);
+}
+
+// adaptive_ppo_clip_kept_mask (clipped_pg.py:38-50)
+template <class T>
+__device__ __forceinline__ bool adaptive_kept(T w, T A, T lo, T hi, T outer) {
+  return (w <= outer) && ((A >= T(0)) || (w >= lo)) && ((A <= T(0)) || (w <= hi));
+}
+
+// Score centering of one active token (score_centering.py:76-129): returns
+// term = sum_k coef_k plog_k and the head mass sum_k q_k, and writes
+// coef_k * scale to out[k] (contiguous).  A is the token's advantage (read by
+// adaptive-ppo-clip only).
+template <class T>
+__device__ void score_centering_token(const mirl_score_centering_args& sc, int64_t b, int64_t l,
+                                      T A, T scale, T* __restrict__ out, T* term_out,
+                                      T* head_out) {
+  const T* pl = static_cast<const T*>(sc.plog) + b * sc.p_sb + l * sc.p_sl;
+  const T* ql = static_cast<const T*>(sc.qlog) + b * sc.q_sb + l * sc.q_sl;
+  const int64_t K = sc.K;
+  T head = T(0), psum = T(0);
+  for (int64_t k = 0; k < K; ++k) {
+    head += dexp(ql[k * sc.q_sk]);
+    psum += dexp(pl[k * sc.p_sk]);
+  }
+  // rho = clamp(1 - head, min=0) / clamp(1 - sum p, min=1e-6)
+  T num = T(1) - head;
+  num = isnan(num) ? num : (num < T(0) ? T(0) : num);
+  T den = T(1) - psum;
+  den = isnan(den) ? den : (den < T(1e-6) ? T(1e-6) : den);
+  const T rho = num / den;
+  const T lo = T(sc.lo), hi = T(sc.hi), outer = T(sc.outer);
+  T alpha;
+  switch (sc.mode) {
+    case MIRL_SC_OFF: alpha = rho; break;
+    case MIRL_SC_IS: alpha = T(1); break;
+    case MIRL_SC_TIS: alpha = tminimum(tmaximum(T(1), lo * rho), hi * rho); break;
+    case MIRL_SC_ICEPOP: {
+      const T tr = T(1) / rho;
+      alpha = (tr >= lo && tr <= hi) ? T(1) : T(0);
+      break;
+    }
+    default: alpha = adaptive_kept(T(1) / rho, A, lo, hi, outer) ? T(1) : T(0); break;
+  }
+  T term = T(0);
+  for (int64_t k = 0; k < K; ++k) {
+    const T plk = pl[k * sc.p_sk], qlk = ql[k * sc.q_sk];
+    const T p = dexp(plk), q = dexp(qlk);
+    T mass;
+    switch (sc.mode) {
+      case MIRL_SC_OFF: mass = q; break;
+      case MIRL_SC_IS: mass = p; break;
+      case MIRL_SC_TIS: mass = tminimum(tmaximum(p, lo * q), hi * q); break;
+      case MIRL_SC_ICEPOP: {
+        const T r = dexp(plk - qlk);
+        mass = (r >= lo && r <= hi) ? p : T(0);
+        break;
+      }
+      default: mass = adaptive_kept(dexp(plk - qlk), A, lo, hi, outer) ? p : T(0); break;
+    }
+    const T coef = mass - alpha * p;
+    term += coef * plk;
+    out[k] = coef * scale;
+  }
+  *term_out = term;
+  *head_out = head;
+}
+
 template <class T>
 struct Inputs {
   View<T> curr, unf, tm, adv, prev, gen, ref;
@@ -206,7 +283,9 @@ template <class T>
 __global__ __launch_bounds__(kRowThreads) void pg_rows_kernel(mirl_pg_config cfg, int64_t L,
                                                               Inputs<T> in, T* __restrict__ gcurr,
                                                               T* __restrict__ gunf,
-                                                              T* __restrict__ part) {
+                                                              T* __restrict__ part,
+                                                              mirl_score_centering_args sc,
+                                                              int has_sc) {
   __shared__ T scratch[kRowThreads / 64];
   const int64_t b = blockIdx.x;
   const int tid = threadIdx.x;
@@ -299,7 +378,9 @@ __global__ __launch_bounds__(kRowThreads) void pg_rows_kernel(mirl_pg_config cfg
     const T c = on ? craw : T(0);
     const T pv = on ? prev_of(l) : T(0);
     const T gv = on ? in.gen(b, l) : T(0);
-    const T A = in.adv(b, l);
+    // score centering zeroes the advantages outside the final mask
+    // (loss_functions.py:841-842)
+    const T A = (has_sc && !on) ? T(0) : in.adv(b, l);
     T gc = T(0);  // dloss/dcurr (this token)
     T gu = T(0);  // dloss/dunfiltered
 
@@ -410,6 +491,18 @@ __global__ __launch_bounds__(kRowThreads) void pg_rows_kernel(mirl_pg_config cfg
       alpha = sm2 * tm2 / (actor_row_norm * gvs);
       acc[P_ACTOR] += v * tm2;  // scaled per row below
     }
+    if (has_sc) {
+      // correction A * term, normalised like the actor loss (loss_functions.py:1070-1097)
+      T* go = static_cast<T*>(sc.grad) + (b * L + l) * sc.K;
+      if (on) {
+        T term, head;
+        score_centering_token<T>(sc, b, l, A, alpha * A, go, &term, &head);
+        acc[P_SC] += (A * term) * (cfg.token_level_loss ? mask2 : tm2);
+        acc[P_HM] += head * mask2;
+      } else {
+        for (int64_t k = 0; k < sc.K; ++k) go[k] = T(0);
+      }
+    }
     if (cfg.use_cispo) {
       gc += on ? alpha * wv * dcl_dc_direct : T(0);
     } else if (seq_ratio) {
@@ -469,7 +562,7 @@ __global__ __launch_bounds__(kRowThreads) void pg_rows_kernel(mirl_pg_config cfg
     else if (k == P_RATIO_MAX || k == P_RATIO_C_MAX) v = block_max<T, kRowThreads>(acc[k], scratch);
     else v = block_sum<T, kRowThreads>(acc[k], scratch);
     if (tid == 0) {
-      if (k == P_ACTOR && !cfg.token_level_loss) v = sm2 * (v / actor_row_norm);
+      if ((k == P_ACTOR || k == P_SC) && !cfg.token_level_loss) v = sm2 * (v / actor_row_norm);
       if (k == P_KL && !cfg.token_level_loss) v = sm * (v / kl_row_norm);
       if (k == P_SIR && cfg.sequence_level_is) {
         bool oob = false;
@@ -487,7 +580,8 @@ __global__ __launch_bounds__(kFinalThreads) void pg_final_kernel(mirl_pg_config 
                                                                  int64_t L, Inputs<T> in,
                                                                  const T* __restrict__ part,
                                                                  T* __restrict__ metrics,
-                                                                 T* __restrict__ gcurr) {
+                                                                 T* __restrict__ gcurr,
+                                                                 int has_sc) {
   __shared__ T tot[NUM_SLOTS];
   const int tid = threadIdx.x;
   if (tid < NUM_SLOTS) {
@@ -518,7 +612,8 @@ __global__ __launch_bounds__(kFinalThreads) void pg_final_kernel(mirl_pg_config 
   const T cvt = tot[P_CVT];
   const bool nll_on = cfg.has_rewards && cfg.nll_weight > 0.0;
   if (tid == 0) {
-    const T actor = tot[P_ACTOR] / (cfg.token_level_loss ? gvt : gvs);
+    T actor = tot[P_ACTOR] / (cfg.token_level_loss ? gvt : gvs);
+    if (has_sc) actor = actor + tot[P_SC] / (cfg.token_level_loss ? gvt : gvs);
     const T kl = cfg.kl_penalty != 0.0 ? tot[P_KL] / (cfg.token_level_loss ? gvt : gvs) : T(0);
     const T nll = (nll_on && cvt > T(0)) ? tot[P_NLL] / (cvt + eps) : T(0);
     const T loss = (actor + kl) + T(cfg.nll_weight) * nll;
@@ -541,6 +636,7 @@ __global__ __launch_bounds__(kFinalThreads) void pg_final_kernel(mirl_pg_config 
     m[MIRL_M_POSITIVE_NLL_LOSS] = nll;
     m[MIRL_M_IS_OOB_RATIO] = tot[P_OOB] / (cfg.tis_type == MIRL_TIS_SEQ_MASK ? gvs : gvt);
     m[MIRL_M_POLICY_SUPPORT_EXCLUDED_TOKENS] = tot[P_EXCL];
+    m[MIRL_M_SCORE_CENTERING_HEAD_MASS] = has_sc ? tot[P_HM] / gvt : T(0);
   }
   if (nll_on && cvt > T(0)) {
     // d(mu * nll)/dcurr = -mu * correct_mask / (cvt + 1e-8)
@@ -566,7 +662,8 @@ __global__ __launch_bounds__(kFinalThreads) void pg_final_kernel(mirl_pg_config 
 template <class T>
 int run(const mirl_pg_config* cfg, int64_t B, int64_t L, const mirl_view2d* v,
         const void* sample_mask, const void* rewards, const void* gvs, const void* gvt,
-        void* metrics, void* gcurr, void* gunf, void* ws, hipStream_t st) {
+        void* metrics, void* gcurr, void* gunf, const mirl_score_centering_args* sc, void* ws,
+        hipStream_t st) {
   Inputs<T> in;
   auto mk = [](const mirl_view2d& x) { return View<T>{static_cast<const T*>(x.ptr), x.sb, x.sl}; };
   in.curr = mk(v[0]);
@@ -582,12 +679,51 @@ int run(const mirl_pg_config* cfg, int64_t B, int64_t L, const mirl_view2d* v,
   in.gvs = static_cast<const T*>(gvs);
   in.gvt = static_cast<const T*>(gvt);
   T* part = static_cast<T*>(ws);
+  mirl_score_centering_args scv{};
+  if (sc != nullptr) scv = *sc;
+  const int has_sc = sc != nullptr ? 1 : 0;
   hipLaunchKernelGGL((pg_rows_kernel<T>), dim3((unsigned)B), dim3(kRowThreads), 0, st, *cfg, L, in,
-                     static_cast<T*>(gcurr), static_cast<T*>(gunf), part);
+                     static_cast<T*>(gcurr), static_cast<T*>(gunf), part, scv, has_sc);
   if (int e = check_launch("mirl_clipped_pg(rows)")) return e;
   hipLaunchKernelGGL((pg_final_kernel<T>), dim3(1), dim3(kFinalThreads), 0, st, *cfg, B, L, in,
-                     static_cast<const T*>(part), static_cast<T*>(metrics), static_cast<T*>(gcurr));
+                     static_cast<const T*>(part), static_cast<T*>(metrics), static_cast<T*>(gcurr),
+                     has_sc);
   return check_launch("mirl_clipped_pg(final)");
+}
+
+// compute_score_centering_term over [B, L] tokens, one thread per token.
+template <class T>
+__global__ __launch_bounds__(256) void sc_term_kernel(mirl_score_centering_args sc, int64_t B,
+                                                      int64_t L, View<T> tm, View<T> adv,
+                                                      int has_adv, T* __restrict__ term,
+                                                      T* __restrict__ head) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= B * L) return;
+  const int64_t b = i / L, l = i - b * L;
+  T* coef = static_cast<T*>(sc.grad) + i * sc.K;
+  if (tm(b, l) == T(0)) {
+    term[i] = T(0);
+    head[i] = T(0);
+    for (int64_t k = 0; k < sc.K; ++k) coef[k] = T(0);
+    return;
+  }
+  const T A = has_adv ? adv(b, l) : T(0);
+  T t, h;
+  score_centering_token<T>(sc, b, l, A, T(1), coef, &t, &h);
+  term[i] = t;
+  head[i] = h;
+}
+
+template <class T>
+int run_sc_term(int64_t B, int64_t L, const mirl_score_centering_args* sc, mirl_view2d tm,
+                mirl_view2d adv, void* term, void* head, hipStream_t st) {
+  const int64_t n = B * L;
+  View<T> tmv{static_cast<const T*>(tm.ptr), tm.sb, tm.sl};
+  View<T> av{static_cast<const T*>(adv.ptr), adv.sb, adv.sl};
+  hipLaunchKernelGGL((sc_term_kernel<T>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, *sc,
+                     B, L, tmv, av, adv.ptr != nullptr ? 1 : 0, static_cast<T*>(term),
+                     static_cast<T*>(head));
+  return check_launch("mirl_score_centering_term");
 }
 
 }  // namespace
@@ -604,7 +740,8 @@ extern "C" int mirl_clipped_pg(const mirl_pg_config* cfg, int dtype, int64_t B, 
                                const void* sample_mask, const void* rewards,
                                const void* global_valid_seqs, const void* global_valid_toks,
                                void* metrics, void* grad_curr, void* grad_unfiltered,
-                               void* workspace, void* stream) {
+                               const mirl_score_centering_args* score_centering, void* workspace,
+                               void* stream) {
   clear_error();
   MIRL_REQUIRE(cfg != nullptr, "null config");
   MIRL_REQUIRE(B > 0 && L >= 0, "invalid shape B=%lld L=%lld", (long long)B, (long long)L);
@@ -622,15 +759,49 @@ extern "C" int mirl_clipped_pg(const mirl_pg_config* cfg, int dtype, int64_t B, 
                cfg->kl_type);
   MIRL_REQUIRE(cfg->tis_type >= MIRL_TIS_NONE && cfg->tis_type <= MIRL_TIS_SEQ_MASK,
                "invalid truncated IS type %d", cfg->tis_type);
+  if (score_centering != nullptr) {
+    const mirl_score_centering_args& sc = *score_centering;
+    MIRL_REQUIRE(sc.mode >= MIRL_SC_OFF && sc.mode <= MIRL_SC_ADAPTIVE,
+                 "invalid score-centering mode %d", sc.mode);
+    MIRL_REQUIRE(sc.K >= 0, "invalid score-centering K=%lld", (long long)sc.K);
+    MIRL_REQUIRE(sc.K == 0 || (sc.plog && sc.qlog && sc.grad),
+                 "score centering needs plog, qlog and a gradient buffer");
+  }
   const mirl_view2d views[8] = {curr, unfiltered, token_mask, advantages,
                                 prev, generation, reference, support_mask};
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == MIRL_DTYPE_F32)
     return run<float>(cfg, B, L, views, sample_mask, rewards, global_valid_seqs, global_valid_toks,
-                      metrics, grad_curr, grad_unfiltered, workspace, st);
+                      metrics, grad_curr, grad_unfiltered, score_centering, workspace, st);
   if (dtype == MIRL_DTYPE_F64)
     return run<double>(cfg, B, L, views, sample_mask, rewards, global_valid_seqs,
-                       global_valid_toks, metrics, grad_curr, grad_unfiltered, workspace, st);
+                       global_valid_toks, metrics, grad_curr, grad_unfiltered, score_centering,
+                       workspace, st);
   set_error("mirl_clipped_pg: dtype must be f32 or f64 (got %d)", dtype);
+  return MIRL_ERR_UNSUPPORTED;
+}
+
+extern "C" int mirl_score_centering_term(int dtype, int64_t B, int64_t L,
+                                         const mirl_score_centering_args* args,
+                                         mirl_view2d token_mask, mirl_view2d advantages,
+                                         void* term, void* head_mass, void* stream) {
+  clear_error();
+  MIRL_REQUIRE(args != nullptr, "null score-centering arguments");
+  MIRL_REQUIRE(B >= 0 && L >= 0 && args->K >= 0, "invalid shape B=%lld L=%lld K=%lld",
+               (long long)B, (long long)L, (long long)args->K);
+  MIRL_REQUIRE(args->mode >= MIRL_SC_OFF && args->mode <= MIRL_SC_ADAPTIVE,
+               "invalid score-centering mode %d", args->mode);
+  MIRL_REQUIRE(args->mode != MIRL_SC_ADAPTIVE || advantages.ptr != nullptr,
+               "adaptive-ppo-clip score centering needs the advantages");
+  if (B * L == 0) return MIRL_OK;
+  MIRL_REQUIRE(B * L < (int64_t(1) << 40), "too many tokens");
+  MIRL_REQUIRE(token_mask.ptr && term && head_mass && (args->K == 0 || (args->plog && args->qlog && args->grad)),
+               "null pointer argument");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == MIRL_DTYPE_F32)
+    return run_sc_term<float>(B, L, args, token_mask, advantages, term, head_mass, st);
+  if (dtype == MIRL_DTYPE_F64)
+    return run_sc_term<double>(B, L, args, token_mask, advantages, term, head_mass, st);
+  set_error("mirl_score_centering_term: dtype must be f32 or f64 (got %d)", dtype);
   return MIRL_ERR_UNSUPPORTED;
 }

@@ -46,6 +46,8 @@ struct F32 {
   using raw = float;
   static constexpr int kVec = 4;  // elements per 16-byte vector
   static constexpr uint32_t kNegInf2 = 0xFF800000u;  // one 32-bit word of -inf elements
+  // one word of -2^100 elements: very low, finite, and x*log2e is exact in fp32
+  static constexpr uint32_t kLowPad2 = 0xF1800000u;
   __device__ __forceinline__ static float load(const raw* p) { return *p; }
   __device__ __forceinline__ static float load_raw(raw r) { return r; }
   __device__ __forceinline__ static void unpack(const vu4& q, float (&v)[kVec]) {
@@ -67,6 +69,7 @@ struct BF16 {
   using raw = uint16_t;
   static constexpr int kVec = 8;
   static constexpr uint32_t kNegInf2 = 0xFF80FF80u;
+  static constexpr uint32_t kLowPad2 = 0xF180F180u;  // -2^100 (see F32)
   __device__ __forceinline__ static float widen(uint32_t bits16) {
     return __uint_as_float(bits16 << 16);
   }
@@ -99,6 +102,7 @@ struct F16 {
   using raw = _Float16;
   static constexpr int kVec = 8;
   static constexpr uint32_t kNegInf2 = 0xFC00FC00u;
+  static constexpr uint32_t kLowPad2 = 0xF800F800u;  // -2^15 (see F32)
   __device__ __forceinline__ static float load(const raw* p) { return (float)*p; }
   __device__ __forceinline__ static float load_raw(raw r) { return (float)r; }
   __device__ __forceinline__ static void unpack(const vu4& q, float (&v)[kVec]) {

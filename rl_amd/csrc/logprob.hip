@@ -53,24 +53,17 @@ struct LseState {
   }
 };
 
-template <class E, int W, int U>
-__global__ __launch_bounds__(64 * W) void logprob_fwd_kernel(
-    const typename E::raw* __restrict__ logits, int64_t R, int64_t V, int64_t sb, int64_t sr,
-    const int64_t* __restrict__ target, int64_t tsb, int64_t tsr, int64_t vs, int64_t ve,
-    float* __restrict__ out, float* __restrict__ stats) {
+// Streams one row of V logits through per-lane online log-sum-exp states and
+// merges lanes and waves.  On thread 0 it returns the row max M and
+// logsum = log(sum exp(x - M)); other threads' outputs are unspecified.
+// `between` runs once, after the first batch of loads is issued, so that the
+// caller's own scalar loads overlap the row's first vector loads.
+template <class E, int W, int U, class F>
+__device__ __forceinline__ void row_lse(const typename E::raw* x, int64_t V, int tid, F&& between,
+                                        float& M_out, float& logsum_out) {
   constexpr int NT = 64 * W;
   constexpr int VEC = E::kVec;
   constexpr int BATCH = U * NT;  // vectors per workgroup per batch
-  const int64_t row = blockIdx.x;
-  const int64_t b = row / R;
-  const int64_t r = row - b * R;
-  const typename E::raw* x = logits + b * sb + r * sr;
-  const int tid = threadIdx.x;
-
-  const int64_t t = target[b * tsb + r * tsr];
-  // targets outside the vocabulary slice (or past this row) carry no one-hot
-  const bool tmask = (t < vs) || (t >= ve) || (t - vs >= V);
-  const int64_t tl = tmask ? 0 : (t - vs);
   const RowSpan<E> span(x, V);
   const vu4* xv = reinterpret_cast<const vu4*>(x + span.head);
   const int nvec = (int)span.nvec;
@@ -90,8 +83,7 @@ __global__ __launch_bounds__(64 * W) void logprob_fwd_kernel(
     }
   };
   if (nbatch > 0) issue(tid);
-  float xt = 0.f;
-  if (tid == 0) xt = E::load(x + tl);
+  between();
   // scalar head and tail elements (fewer than 2*VEC per row)
   float ht[2];
   ht[0] = (tid < span.head) ? E::load(x + tid) : -INFINITY;
@@ -143,17 +135,73 @@ __global__ __launch_bounds__(64 * W) void logprob_fwd_kernel(
       s = sb2;
     }
   }
+  // s = sum 2^(x*log2e - fl(M*log2e)); undo the rounding of the offset so
+  // that logsum = log(sum exp(x - M)).
+  const float corr = fmaf(M, kLog2e, -(M * kLog2e));
+  M_out = M;
+  logsum_out = logf(s) - corr * 0.6931471805599453f;
+}
+
+template <class E, int W, int U>
+__global__ __launch_bounds__(64 * W) void logprob_fwd_kernel(
+    const typename E::raw* __restrict__ logits, int64_t R, int64_t V, int64_t sb, int64_t sr,
+    const int64_t* __restrict__ target, int64_t tsb, int64_t tsr, int64_t vs, int64_t ve,
+    float* __restrict__ out, float* __restrict__ stats) {
+  const int64_t row = blockIdx.x;
+  const int64_t b = row / R;
+  const int64_t r = row - b * R;
+  const typename E::raw* x = logits + b * sb + r * sr;
+  const int tid = threadIdx.x;
+
+  const int64_t t = target[b * tsb + r * tsr];
+  // targets outside the vocabulary slice (or past this row) carry no one-hot
+  const bool tmask = (t < vs) || (t >= ve) || (t - vs >= V);
+  const int64_t tl = tmask ? 0 : (t - vs);
+  float xt = 0.f, M, logsum;
+  row_lse<E, W, U>(x, V, tid, [&] { if (tid == 0) xt = E::load(x + tl); }, M, logsum);
   if (tid == 0) {
-    // s = sum 2^(x*log2e - fl(M*log2e)); undo the rounding of the offset so
-    // that logsum = log(sum exp(x - M)).
-    const float corr = fmaf(M, kLog2e, -(M * kLog2e));
-    const float logsum = logf(s) - corr * 0.6931471805599453f;
     const float lp = (xt - M) - logsum;
     out[row] = tmask ? 0.f : lp;
     if (stats != nullptr) {
       stats[2 * row] = M;
       stats[2 * row + 1] = logsum;
     }
+  }
+}
+
+// Logprobs at K given vocabulary ids per row (ChunkedDistributedGatherLogprob,
+// reference model_utils.py:691-748): the row's log-sum-exp as in
+// logprob_fwd_kernel, then out[row, k] = (x[id_k] - M) - logsum for ids in
+// [vs, ve) and 0 for the others.  The K re-reads hit the row just streamed.
+template <class E, int W, int U>
+__global__ __launch_bounds__(64 * W) void gather_logprob_fwd_kernel(
+    const typename E::raw* __restrict__ logits, int64_t R, int64_t V, int64_t sb, int64_t sr,
+    const int64_t* __restrict__ idx, int64_t K, int64_t isb, int64_t isr, int64_t isk,
+    int64_t vs, int64_t ve, float* __restrict__ out, float* __restrict__ stats) {
+  const int64_t row = blockIdx.x;
+  const int64_t b = row / R;
+  const int64_t r = row - b * R;
+  const typename E::raw* x = logits + b * sb + r * sr;
+  const int tid = threadIdx.x;
+  float M, logsum;
+  row_lse<E, W, U>(x, V, tid, [] {}, M, logsum);
+  __shared__ float sh[2];
+  if (tid == 0) {
+    sh[0] = M;
+    sh[1] = logsum;
+    if (stats != nullptr) {
+      stats[2 * row] = M;
+      stats[2 * row + 1] = logsum;
+    }
+  }
+  __syncthreads();
+  M = sh[0];
+  logsum = sh[1];
+  const int64_t* ir = idx + b * isb + r * isr;
+  for (int64_t k = tid; k < K; k += 64 * W) {
+    const int64_t t = ir[k * isk];
+    const bool in_range = (t >= vs) && (t < ve) && (t - vs < V);
+    out[row * K + k] = in_range ? (E::load(x + (t - vs)) - M) - logsum : 0.f;
   }
 }
 
@@ -335,6 +383,55 @@ __global__ __launch_bounds__(256) void logprob_bwd_flat_kernel(
   }
 }
 
+// Backward of the K-id gather (reference model_utils.py:750-805):
+//   grad = -p * sum_k g_k, plus g_k added at each in-range id_k, in fp32,
+// rounded once to the logits dtype.  Three launches: gather_gsum_kernel forms
+// sum_k g_k per row, the logprob backward writes the dense -p * gsum part (no
+// target), and gather_fixup_kernel rewrites the <= K entries at the ids.
+__global__ __launch_bounds__(256) void gather_gsum_kernel(const float* __restrict__ g, int64_t R,
+                                                         int64_t gsb, int64_t gsr, int64_t gsk,
+                                                         int64_t K, int64_t rows,
+                                                         float* __restrict__ gsum) {
+  const int64_t row = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (row >= rows) return;
+  const int64_t b = row / R, r = row - b * R;
+  const float* gr = g + b * gsb + r * gsr;
+  float s = 0.f;
+  for (int64_t k = 0; k < K; ++k) s += gr[k * gsk];
+  gsum[row] = s;
+}
+
+// One thread per (row, k).  The first occurrence of each in-range id in a row
+// recomputes the dense value -p * gsum exactly as the dense pass formed it,
+// adds the upstream gradient of every k' with the same id in k' order (the
+// order of scatter_add), and stores the sum rounded to the dtype; repeated
+// and out-of-range ids write nothing.
+template <class E>
+__global__ __launch_bounds__(256) void gather_fixup_kernel(
+    const typename E::raw* __restrict__ logits, int64_t R, int64_t V, int64_t sb, int64_t sr,
+    const int64_t* __restrict__ idx, int64_t K, int64_t isb, int64_t isr, int64_t isk,
+    int64_t vs, int64_t ve, const float* __restrict__ stats, const float* __restrict__ g,
+    int64_t gsb, int64_t gsr, int64_t gsk, const float* __restrict__ gsum,
+    typename E::raw* gin, int64_t gisb, int64_t gisr, int64_t total) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= total) return;
+  const int64_t row = i / K, k = i - row * K;
+  const int64_t b = row / R, r = row - b * R;
+  const int64_t* ir = idx + b * isb + r * isr;
+  const int64_t t = ir[k * isk];
+  if (t < vs || t >= ve || t - vs >= V) return;
+  for (int64_t j = 0; j < k; ++j)
+    if (ir[j * isk] == t) return;
+  const int64_t tl = t - vs;
+  const float M = stats[2 * row], LS = stats[2 * row + 1];
+  const float xv = E::load(logits + b * sb + r * sr + tl);
+  float o = fast_exp2(((xv - M) - LS) * kLog2e) * (-gsum[row]);
+  const float* gr = g + b * gsb + r * gsr;
+  for (int64_t j = k; j < K; ++j)
+    if (ir[j * isk] == t) o += gr[j * gsk];
+  gin[b * gisb + r * gisr + tl] = E::from_float(o);
+}
+
 // Waves per row for the forward: at least 4 (fewer rows in flight at a time
 // keeps the concurrently streamed address window narrower, measured +5% read
 // bandwidth over one wave per row), more when there are too few rows to give
@@ -367,6 +464,29 @@ void dispatch_fwd(int w, int64_t rows, hipStream_t st, const void* logits, int64
     case 4: launch_fwd<E, 4>(rows, st, logits, R, V, sb, sr, target, tsb, tsr, vs, ve, out, stats); break;
     case 8: launch_fwd<E, 8>(rows, st, logits, R, V, sb, sr, target, tsb, tsr, vs, ve, out, stats); break;
     default: launch_fwd<E, 16>(rows, st, logits, R, V, sb, sr, target, tsb, tsr, vs, ve, out, stats); break;
+  }
+}
+
+template <class E, int W>
+void launch_gather_fwd(int64_t rows, hipStream_t st, const void* logits, int64_t R, int64_t V,
+                       int64_t sb, int64_t sr, const int64_t* idx, int64_t K, int64_t isb,
+                       int64_t isr, int64_t isk, int64_t vs, int64_t ve, float* out,
+                       float* stats) {
+  constexpr int U = 8;
+  hipLaunchKernelGGL((gather_logprob_fwd_kernel<E, W, U>), dim3((unsigned)rows), dim3(64 * W), 0,
+                     st, static_cast<const typename E::raw*>(logits), R, V, sb, sr, idx, K, isb,
+                     isr, isk, vs, ve, out, stats);
+}
+
+template <class E>
+void dispatch_gather_fwd(int w, int64_t rows, hipStream_t st, const void* logits, int64_t R,
+                         int64_t V, int64_t sb, int64_t sr, const int64_t* idx, int64_t K,
+                         int64_t isb, int64_t isr, int64_t isk, int64_t vs, int64_t ve,
+                         float* out, float* stats) {
+  switch (w) {
+    case 4: launch_gather_fwd<E, 4>(rows, st, logits, R, V, sb, sr, idx, K, isb, isr, isk, vs, ve, out, stats); break;
+    case 8: launch_gather_fwd<E, 8>(rows, st, logits, R, V, sb, sr, idx, K, isb, isr, isk, vs, ve, out, stats); break;
+    default: launch_gather_fwd<E, 16>(rows, st, logits, R, V, sb, sr, idx, K, isb, isr, isk, vs, ve, out, stats); break;
   }
 }
 
@@ -405,6 +525,25 @@ void dispatch_bwd(int64_t rows, hipStream_t st, const void* logits, int64_t R, i
                      dim3(64 * W), 0, st, static_cast<const raw*>(logits), R, Rt, V, sb, sr,
                      target, tsb, tsr, vs, ve, stats, g, gsb, gsr, static_cast<raw*>(gin), gisb,
                      gisr);
+}
+
+template <class E>
+void gather_bwd(int64_t rows, hipStream_t st, const void* logits, int64_t R, int64_t V,
+                int64_t sb, int64_t sr, const int64_t* idx, int64_t K, int64_t isb, int64_t isr,
+                int64_t isk, int64_t vs, int64_t ve, const float* stats, const float* g,
+                int64_t gsb, int64_t gsr, int64_t gsk, float* gsum, void* gin, int64_t gisb,
+                int64_t gisr) {
+  hipLaunchKernelGGL(gather_gsum_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, st,
+                     g, R, gsb, gsr, gsk, K, rows, gsum);
+  // dense part: no target (an empty vocabulary slice masks every id), upstream gsum
+  dispatch_bwd<E>(rows, st, logits, R, R, V, sb, sr, idx, isb, isr, 0, 0, stats, gsum, R, 1,
+                  gin, gisb, gisr);
+  const int64_t total = rows * K;
+  if (total == 0) return;
+  hipLaunchKernelGGL((gather_fixup_kernel<E>), dim3((unsigned)((total + 255) / 256)), dim3(256),
+                     0, st, static_cast<const typename E::raw*>(logits), R, V, sb, sr, idx, K, isb,
+                     isr, isk, vs, ve, stats, g, gsb, gsr, gsk, gsum,
+                     static_cast<typename E::raw*>(gin), gisb, gisr, total);
 }
 
 int check_dtype(int dtype) {
@@ -487,4 +626,88 @@ extern "C" int mirl_logprob_bwd(const void* logits, int dtype, int64_t B, int64_
       break;
   }
   return check_launch("mirl_logprob_bwd");
+}
+
+extern "C" int mirl_gather_logprob_fwd(const void* logits, int dtype, int64_t B, int64_t R,
+                                       int64_t V, int64_t stride_b, int64_t stride_r,
+                                       const int64_t* indices, int64_t K, int64_t i_stride_b,
+                                       int64_t i_stride_r, int64_t i_stride_k,
+                                       int64_t vocab_start, int64_t vocab_end, float* out,
+                                       float* row_stats, void* stream) {
+  clear_error();
+  if (int e = check_dtype(dtype)) return e;
+  MIRL_REQUIRE(B >= 0 && R >= 0 && V > 0 && K >= 0, "invalid shape B=%lld R=%lld V=%lld K=%lld",
+               (long long)B, (long long)R, (long long)V, (long long)K);
+  MIRL_REQUIRE(V < (int64_t(1) << 31), "vocabulary size %lld exceeds 2^31-1", (long long)V);
+  const int64_t rows = B * R;
+  if (rows == 0) return MIRL_OK;
+  MIRL_REQUIRE(rows < (int64_t(1) << 31), "too many rows (%lld)", (long long)rows);
+  MIRL_REQUIRE(logits && (K == 0 || indices) && (K == 0 || out), "null pointer argument");
+  const int w = pick_waves(rows);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case MIRL_DTYPE_F32:
+      dispatch_gather_fwd<F32>(w, rows, st, logits, R, V, stride_b, stride_r, indices, K,
+                               i_stride_b, i_stride_r, i_stride_k, vocab_start, vocab_end, out,
+                               row_stats);
+      break;
+    case MIRL_DTYPE_BF16:
+      dispatch_gather_fwd<BF16>(w, rows, st, logits, R, V, stride_b, stride_r, indices, K,
+                                i_stride_b, i_stride_r, i_stride_k, vocab_start, vocab_end, out,
+                                row_stats);
+      break;
+    default:
+      dispatch_gather_fwd<F16>(w, rows, st, logits, R, V, stride_b, stride_r, indices, K,
+                               i_stride_b, i_stride_r, i_stride_k, vocab_start, vocab_end, out,
+                               row_stats);
+      break;
+  }
+  return check_launch("mirl_gather_logprob_fwd");
+}
+
+extern "C" int64_t mirl_gather_logprob_workspace_elems(int64_t B, int64_t R) { return B * R; }
+
+extern "C" int mirl_gather_logprob_bwd(const void* logits, int dtype, int64_t B, int64_t R,
+                                       int64_t V, int64_t stride_b, int64_t stride_r,
+                                       const int64_t* indices, int64_t K, int64_t i_stride_b,
+                                       int64_t i_stride_r, int64_t i_stride_k,
+                                       int64_t vocab_start, int64_t vocab_end,
+                                       const float* row_stats, const float* grad_out,
+                                       int64_t g_stride_b, int64_t g_stride_r,
+                                       int64_t g_stride_k, float* workspace, void* grad_in,
+                                       int64_t gi_stride_b, int64_t gi_stride_r, void* stream) {
+  clear_error();
+  if (int e = check_dtype(dtype)) return e;
+  MIRL_REQUIRE(B >= 0 && R >= 0 && V > 0 && K >= 0, "invalid shape B=%lld R=%lld V=%lld K=%lld",
+               (long long)B, (long long)R, (long long)V, (long long)K);
+  MIRL_REQUIRE(V < (int64_t(1) << 31), "vocabulary size %lld exceeds 2^31-1", (long long)V);
+  const int64_t rows = B * R;
+  if (rows == 0) return MIRL_OK;
+  MIRL_REQUIRE(rows < (int64_t(1) << 31) && rows * K < (int64_t(1) << 40), "too many rows (%lld)",
+               (long long)rows);
+  MIRL_REQUIRE(K > 0, "at least one id per row is required (K=%lld)", (long long)K);
+  MIRL_REQUIRE(logits && indices && row_stats && grad_in && workspace && grad_out,
+               "null pointer argument");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case MIRL_DTYPE_F32:
+      gather_bwd<F32>(rows, st, logits, R, V, stride_b, stride_r, indices, K, i_stride_b,
+                      i_stride_r, i_stride_k, vocab_start, vocab_end, row_stats, grad_out,
+                      g_stride_b, g_stride_r, g_stride_k, workspace, grad_in, gi_stride_b,
+                      gi_stride_r);
+      break;
+    case MIRL_DTYPE_BF16:
+      gather_bwd<BF16>(rows, st, logits, R, V, stride_b, stride_r, indices, K, i_stride_b,
+                       i_stride_r, i_stride_k, vocab_start, vocab_end, row_stats, grad_out,
+                       g_stride_b, g_stride_r, g_stride_k, workspace, grad_in, gi_stride_b,
+                       gi_stride_r);
+      break;
+    default:
+      gather_bwd<F16>(rows, st, logits, R, V, stride_b, stride_r, indices, K, i_stride_b,
+                      i_stride_r, i_stride_k, vocab_start, vocab_end, row_stats, grad_out,
+                      g_stride_b, g_stride_r, g_stride_k, workspace, grad_in, gi_stride_b,
+                      gi_stride_r);
+      break;
+  }
+  return check_launch("mirl_gather_logprob_bwd");
 }

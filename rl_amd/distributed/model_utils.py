@@ -30,21 +30,35 @@ from rl_amd.algorithms.logits_sampling_utils import (
 )
 
 __all__ = [
+    "ChunkedDistributedCrossEntropyToFixedLogits",
+    "ChunkedDistributedEntropy",
+    "ChunkedDistributedGatherLogprob",
     "ChunkedDistributedHiddenStatesToLogprobs",
     "ChunkedDistributedLogprob",
     "ChunkedDistributedLogprobWithSampling",
+    "ChunkedDistributedReverseKLToFixedLogits",
     "DistributedLogprob",
     "DistributedLogprobWithSampling",
     "from_parallel_hidden_states_to_logprobs",
     "from_parallel_logits_to_logprobs",
     "from_parallel_logits_to_logprobs_packed_sequences",
     "get_next_token_logprobs_from_logits",
+    "get_policy_logprobs_at_sampler_topk",
 ]
+
+_VOCAB_REDUCTIONS = (
+    "ChunkedDistributedGatherLogprob",
+    "get_policy_logprobs_at_sampler_topk",
+    "ChunkedDistributedEntropy",
+    "ChunkedDistributedCrossEntropyToFixedLogits",
+    "ChunkedDistributedReverseKLToFixedLogits",
+)
 
 
 def __getattr__(name: str):
     # the filtered autograd Functions live with the filter kernels' bindings,
-    # the hidden-state path with the fused LM-head kernels' bindings
+    # the hidden-state path with the fused LM-head kernels' bindings, the
+    # K-id gather and the divergences in vocab_reductions
     if name in ("DistributedLogprobWithSampling", "ChunkedDistributedLogprobWithSampling"):
         from rl_amd.distributed import sampling
 
@@ -53,6 +67,10 @@ def __getattr__(name: str):
         from rl_amd.distributed import linear_ce
 
         return getattr(linear_ce, name)
+    if name in _VOCAB_REDUCTIONS:
+        from rl_amd.distributed import vocab_reductions
+
+        return getattr(vocab_reductions, name)
     raise AttributeError(name)
 
 

@@ -85,3 +85,48 @@ def test_group_arguments(single_rank_group):
     _require_single_rank(single_rank_group, None)
     with pytest.raises(TypeError, match="ProcessGroup or None"):
         _require_single_rank(object())
+
+
+@pytest.mark.parametrize("missing", ["sampler_topk_token_ids", "sampler_topk_logprobs"])
+def test_score_centering_rejects_missing_sampler_data(missing):
+    """Reference test_score_centering.py:54-87: the check runs before any logprob work."""
+    from types import SimpleNamespace
+
+    from rl_amd.algorithms.loss import LossInputType, prepare_loss_input
+
+    data = {
+        "input_ids": torch.zeros(1, 4, dtype=torch.long),
+        "sampler_topk_token_ids": torch.zeros(1, 4, 2, dtype=torch.int32),
+        "sampler_topk_logprobs": torch.zeros(1, 4, 2),
+    }
+    del data[missing]
+    loss_fn = SimpleNamespace(input_type=LossInputType.LOGPROB, score_centering=True)
+    with pytest.raises(ValueError, match=f"{missing}.*SingleController.*policy.generation.top_logprobs"):
+        prepare_loss_input(torch.randn(1, 4, 7), data, loss_fn)
+
+
+def test_score_centering_config_validation():
+    with pytest.raises(AssertionError, match="score_centering composes only"):
+        ClippedPGLossFn(ClippedPGLossConfig(
+            score_centering=True, token_level_loss=False, sequence_level_importance_ratios=True))
+    fn = ClippedPGLossFn(ClippedPGLossConfig(score_centering=True))
+    assert fn._score_centering_is_mode == "off"
+    assert fn.metric_normalizations["score_centering_head_mass"] == MetricNormalizer.TOKENS
+    fn = ClippedPGLossFn(ClippedPGLossConfig(
+        score_centering=True, use_importance_sampling_correction=True,
+        truncated_importance_sampling_type="icepop", truncated_importance_sampling_ratio=2.0,
+        truncated_importance_sampling_ratio_min=0.5))
+    assert fn._score_centering_is_mode == "icepop"
+    assert fn._get_score_centering_is_bounds() == (0.5, 2.0)
+
+
+@pytest.mark.parametrize(("student_shape", "teacher_shape", "match"),
+                         [((2, 5, 9), (2, 5, 8), r"same \[B, S, V_local\] shape"),
+                          ((5, 9), (5, 9), "must be rank 3")])
+def test_student_teacher_shapes_are_validated_first(student_shape, teacher_shape, match):
+    """Reference test_model_utils.py:2016-2023: rejected before any kernel work."""
+    from rl_amd.distributed.model_utils import ChunkedDistributedReverseKLToFixedLogits
+
+    with pytest.raises(ValueError, match=match):
+        ChunkedDistributedReverseKLToFixedLogits.apply(
+            torch.randn(*student_shape), torch.randn(*teacher_shape), 2, None, True)
