@@ -47,7 +47,8 @@ def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--workload", default="grpo",
-                    choices=["grpo", "fwd_f32", "long_context", "topk_filter", "packed_kl", "linear_ce"])
+                    choices=["grpo", "fwd_f32", "long_context", "topk_filter", "packed_kl", "linear_ce",
+                             "distill_rkl", "score_centering"])
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--cpu-sample-rows", type=int, default=1024)
@@ -394,6 +395,99 @@ def bench_workload(args) -> None:
         cfg = {"workload": "hidden_state_logprobs_fwd_bwd", "hidden": [S, B, H], "weight": [V, H],
                "chunk_size": 256, "next_token_rows": rows,
                "flops_per_step": "4 x 2*S*B*H*V (fused fwd, fused grad recompute, dH and dW GEMMs)"}
+        dtype = "bf16"
+    elif w == "distill_rkl":
+        from rl_amd.distributed.model_utils import ChunkedDistributedReverseKLToFixedLogits
+
+        d = workloads.distill_rkl_bf16(device=dev)
+        student = d["student"].requires_grad_(True)
+        teacher = d["teacher"]
+        B, S, V = student.shape
+        m = d["token_mask"][:, 1:]
+        n_tok = m.sum()
+
+        def step():
+            rkl = ChunkedDistributedReverseKLToFixedLogits.apply(student, teacher, 4096, None, False)
+            loss = (rkl[:, :-1] * m).sum() / n_tok
+            return torch.autograd.grad(loss, [student])
+
+        ms_step, ms = _timed(step, args.steps, args.warmup, ["mirl_divergence_fwd", "mirl_divergence_bwd"])
+        rows = B * (S - 1)
+        active = int((m != 0).sum().item())
+        esz = 2
+        fwd_bytes = 2 * B * S * V * esz
+        bwd_bytes = (2 * active + B * S) * V * esz
+        fwd_ms, bwd_ms = ms.get("mirl_divergence_fwd", 0.0), ms.get("mirl_divergence_bwd", 0.0)
+        roof = _roofline("mirl_divergence_bwd", bwd_bytes, bwd_ms, w)
+        extra["divergence_fwd_gbps"] = fwd_bytes / (fwd_ms * 1e-3) / 1e9 if fwd_ms > 0 else None
+        step_bytes = fwd_bytes + bwd_bytes
+        cfg = {"workload": "reverse_kl_to_fixed_teacher_fwd_bwd", "student": [B, S, V], "teacher": [B, S, V],
+               "next_token_rows": rows, "active_rows": active,
+               "loss": "masked mean of per-token reverse KL over response tokens"}
+        dtype = "bf16"
+    elif w == "score_centering":
+        from types import SimpleNamespace
+
+        from rl_amd.algorithms.advantage_estimator import AdvEstimatorConfig, GRPOAdvantageEstimator
+        from rl_amd.algorithms.loss import (
+            ClippedPGLossConfig,
+            ClippedPGLossFn,
+            LossInputType,
+            prepare_loss_input,
+        )
+
+        d = workloads.score_centering_bf16(device=dev)
+        logits = d["logits"].requires_grad_(True)
+        B, S, V = logits.shape
+        K = d["sampler_topk_token_ids"].shape[-1]
+        probe = SimpleNamespace(input_type=LossInputType.LOGPROB, score_centering=True)
+        with torch.no_grad():
+            cur, _ = prepare_loss_input(logits, {"input_ids": d["input_ids"],
+                                                 "sampler_topk_token_ids": d["sampler_topk_token_ids"],
+                                                 "sampler_topk_logprobs": d["sampler_noise"]}, probe)
+        d = workloads.finish_score_centering_step(d, cur["next_token_logprobs"],
+                                                  cur["policy_logprobs_at_sampler_topk"])
+        loss_cfg = ClippedPGLossConfig(reference_policy_kl_penalty=0.0, score_centering=True)
+        loss_fn = ClippedPGLossFn(loss_cfg)
+        est = GRPOAdvantageEstimator(AdvEstimatorConfig(use_leave_one_out_baseline=False), loss_cfg)
+        gvs = d["sample_mask"].sum()
+        gvt = (d["token_mask"][:, 1:] * d["sample_mask"][:, None]).sum()
+        batch = {k: d[k] for k in ("input_ids", "token_mask", "sample_mask", "prev_logprobs",
+                                   "generation_logprobs", "reference_policy_logprobs",
+                                   "sampler_topk_token_ids", "sampler_topk_logprobs")}
+
+        def step():
+            batch["advantages"] = est.compute_advantage(d["prompt_ids"], d["rewards"], d["token_mask"])
+            li, _ = prepare_loss_input(logits, batch, loss_fn)
+            loss, _ = loss_fn(data=batch, global_valid_seqs=gvs, global_valid_toks=gvt, **li)
+            return torch.autograd.grad(loss, [logits])
+
+        # rows whose upstream gradient is non-zero, for each of the two logprob outputs
+        batch["advantages"] = est.compute_advantage(d["prompt_ids"], d["rewards"], d["token_mask"])
+        lp_leaf = cur["next_token_logprobs"].detach().requires_grad_(True)
+        pk_leaf = cur["policy_logprobs_at_sampler_topk"].detach().requires_grad_(True)
+        l2, _ = loss_fn(next_token_logprobs=lp_leaf, policy_logprobs_at_sampler_topk=pk_leaf, data=batch,
+                        global_valid_seqs=gvs, global_valid_toks=gvt)
+        g_lp, g_pk = torch.autograd.grad(l2, [lp_leaf, pk_leaf])
+        # the one K+1-id backward reads a row when g_target + sum_k g_k != 0
+        active = int(((g_lp + g_pk.sum(-1)) != 0).sum().item())
+        del lp_leaf, pk_leaf, l2, g_lp, g_pk
+
+        ms_step, ms = _timed(step, args.steps, args.warmup,
+                             ["mirl_gather_logprob_fwd", "mirl_gather_logprob_bwd"])
+        rows = B * (S - 1)
+        esz = 2
+        # next-token and top-k logprobs share one K+1-id pass over all B*S rows;
+        # one backward reads the active rows and writes every row
+        fwd_bytes = B * S * V * esz
+        bwd_bytes = (active + B * S) * V * esz
+        gfwd_ms, gbwd_ms = ms.get("mirl_gather_logprob_fwd", 0.0), ms.get("mirl_gather_logprob_bwd", 0.0)
+        roof = _roofline("mirl_gather_logprob_bwd", bwd_bytes, gbwd_ms, w)
+        extra["gather_fwd_gbps"] = fwd_bytes / (gfwd_ms * 1e-3) / 1e9 if gfwd_ms > 0 else None
+        step_bytes = fwd_bytes + bwd_bytes
+        cfg = {"workload": "grpo_score_centering_fwd_bwd", "logits": [B, S, V], "sampler_topk": K,
+               "next_token_rows": rows, "active_rows": active, "ids_per_row": K + 1,
+               "loss": "ClippedPG clip 0.2/0.2 token-level + score centering (IS off); GRPO adv"}
         dtype = "bf16"
     else:  # packed_kl
         import torch.distributed as dist

@@ -31,7 +31,11 @@ from rl_amd.distributed.model_utils import (
     from_parallel_logits_to_logprobs_packed_sequences,
     get_next_token_logprobs_from_logits,
 )
-from rl_amd.distributed.vocab_reductions import get_policy_logprobs_at_sampler_topk
+from rl_amd.distributed.model_utils import _is_dtensor
+from rl_amd.distributed.vocab_reductions import (
+    get_policy_logprobs_at_sampler_topk,
+    next_token_and_sampler_topk_logprobs,
+)
 
 
 def _unsupported(what: str) -> NotImplementedError:
@@ -80,7 +84,21 @@ def prepare_loss_input(
             raise _unsupported(f"loss input type {loss_fn.input_type}")
         raise ValueError(f"Unknown loss function input type: {loss_fn.input_type}")
 
-    if getattr(loss_fn, "use_fused_linear_logprobs", False):
+    score_centering = getattr(loss_fn, "score_centering", False)
+    fused_linear = getattr(loss_fn, "use_fused_linear_logprobs", False)
+    both = None
+    if (score_centering and not fused_linear and cp_sharder is None
+            and not need_top_k_or_top_p_filtering(sampling_params)
+            and not _is_dtensor(logits) and _group_size(context_parallel_group) == 1):
+        # next-token and sampler top-k logprobs from one pass over the logits
+        both = next_token_and_sampler_topk_logprobs(
+            data["input_ids"], data["sampler_topk_token_ids"], logits,
+            vocab_parallel_rank=vocab_parallel_rank, vocab_parallel_group=vocab_parallel_group,
+            chunk_size=chunk_size,
+        )
+    if both is not None:
+        logprobs = both[0]
+    elif fused_linear:
         # the logits argument already holds next-token logprobs [B, >= S-1]
         logprobs = logits.to(torch.float32)[:, : data["input_ids"].shape[1] - 1]
     else:
@@ -111,7 +129,9 @@ def prepare_loss_input(
     loss_input: dict[str, Any] = {"next_token_logprobs": logprobs}
     if filtering:
         loss_input["policy_support_mask"] = ~torch.isneginf(logprobs)
-    if getattr(loss_fn, "score_centering", False):
+    if both is not None:
+        loss_input["policy_logprobs_at_sampler_topk"] = both[1]
+    elif score_centering:
         loss_input["policy_logprobs_at_sampler_topk"] = get_policy_logprobs_at_sampler_topk(
             sampler_topk_token_ids=data["sampler_topk_token_ids"],
             next_token_logits=logits,

@@ -172,19 +172,26 @@ __global__ __launch_bounds__(64 * W) void logprob_fwd_kernel(
 // Logprobs at K given vocabulary ids per row (ChunkedDistributedGatherLogprob,
 // reference model_utils.py:691-748): the row's log-sum-exp as in
 // logprob_fwd_kernel, then out[row, k] = (x[id_k] - M) - logsum for ids in
-// [vs, ve) and 0 for the others.  The K re-reads hit the row just streamed.
+// [vs, ve) and 0 for the others.  Thread k < 64*W loads x[id_k] while the
+// row's first loads are in flight (as the single-target kernel does with its
+// target); ids beyond the first 64*W are read after the row.
 template <class E, int W, int U>
 __global__ __launch_bounds__(64 * W) void gather_logprob_fwd_kernel(
     const typename E::raw* __restrict__ logits, int64_t R, int64_t V, int64_t sb, int64_t sr,
     const int64_t* __restrict__ idx, int64_t K, int64_t isb, int64_t isr, int64_t isk,
     int64_t vs, int64_t ve, float* __restrict__ out, float* __restrict__ stats) {
+  constexpr int NT = 64 * W;
   const int64_t row = blockIdx.x;
   const int64_t b = row / R;
   const int64_t r = row - b * R;
   const typename E::raw* x = logits + b * sb + r * sr;
   const int tid = threadIdx.x;
-  float M, logsum;
-  row_lse<E, W, U>(x, V, tid, [] {}, M, logsum);
+  const int64_t* ir = idx + b * isb + r * isr;
+  const bool mine = tid < K;
+  const int64_t t = mine ? ir[tid * isk] : 0;
+  const bool in_range = mine && (t >= vs) && (t < ve) && (t - vs < V);
+  float xk = 0.f, M, logsum;
+  row_lse<E, W, U>(x, V, tid, [&] { if (in_range) xk = E::load(x + (t - vs)); }, M, logsum);
   __shared__ float sh[2];
   if (tid == 0) {
     sh[0] = M;
@@ -197,11 +204,11 @@ __global__ __launch_bounds__(64 * W) void gather_logprob_fwd_kernel(
   __syncthreads();
   M = sh[0];
   logsum = sh[1];
-  const int64_t* ir = idx + b * isb + r * isr;
-  for (int64_t k = tid; k < K; k += 64 * W) {
-    const int64_t t = ir[k * isk];
-    const bool in_range = (t >= vs) && (t < ve) && (t - vs < V);
-    out[row * K + k] = in_range ? (E::load(x + (t - vs)) - M) - logsum : 0.f;
+  if (mine) out[row * K + tid] = in_range ? (xk - M) - logsum : 0.f;
+  for (int64_t k = NT + tid; k < K; k += NT) {
+    const int64_t tk = ir[k * isk];
+    const bool ok = (tk >= vs) && (tk < ve) && (tk - vs < V);
+    out[row * K + k] = ok ? (E::load(x + (tk - vs)) - M) - logsum : 0.f;
   }
 }
 

@@ -29,6 +29,7 @@ __all__ = [
     "ChunkedDistributedGatherLogprob",
     "ChunkedDistributedReverseKLToFixedLogits",
     "get_policy_logprobs_at_sampler_topk",
+    "next_token_and_sampler_topk_logprobs",
 ]
 
 
@@ -169,6 +170,48 @@ def get_policy_logprobs_at_sampler_topk(
         row = row[:, :w]
         rows.append(torch.cat([row, row.new_zeros(1, S_ids - 1 - w, k)], dim=1))
     return torch.cat(rows, dim=0)
+
+
+def next_token_and_sampler_topk_logprobs(
+    input_ids: torch.Tensor,
+    sampler_topk_token_ids: torch.Tensor,
+    next_token_logits: torch.Tensor,
+    vocab_parallel_rank: Optional[int] = None,
+    vocab_parallel_group: Optional[Any] = None,
+    chunk_size: Optional[int] = None,
+) -> Optional[tuple[torch.Tensor, torch.Tensor]]:
+    """``(next_token_logprobs [B, S-1], policy_logprobs_at_sampler_topk [B, S-1, k])`` in one pass.
+
+    The next-token target is one more id per row, so both inputs of a
+    score-centering loss come from a single K+1-id gather over the logits
+    (one read of each row) and a single backward that writes the summed
+    gradient (one read + one write), instead of two forward passes, two
+    backward passes and autograd's sum of the two logits gradients.  Values
+    equal those of get_next_token_logprobs_from_logits and
+    get_policy_logprobs_at_sampler_topk; the gradient is their sum rounded once
+    to the logits dtype (the reference rounds each and then adds).  Returns
+    None when the shapes call for the separate paths (ids shorter than the
+    logits).
+    """
+    from rl_amd.distributed.model_utils import _check_chunk_size, _check_logits
+
+    _single_rank(vocab_parallel_group)
+    _check_chunk_size(chunk_size)
+    logits = _check_logits(next_token_logits)
+    B, S, V = logits.shape
+    if (input_ids.dim() != 2 or tuple(input_ids.shape) != (B, S) or sampler_topk_token_ids.dim() != 3
+            or tuple(sampler_topk_token_ids.shape[:2]) != (B, S)):
+        return None
+    dev = logits.device
+    ids = torch.cat([input_ids.to(device=dev, dtype=torch.long).unsqueeze(-1),
+                     sampler_topk_token_ids.to(device=dev, dtype=torch.long)], dim=-1)
+    ids = ids.roll(-1, dims=1)  # row s holds the ids of position s + 1
+    rank = 0 if vocab_parallel_rank is None else int(vocab_parallel_rank)
+    out = ChunkedDistributedGatherLogprob.apply(
+        logits, ids, rank * V, (rank + 1) * V, chunk_size if chunk_size is not None else S,
+        vocab_parallel_group, False,
+    )
+    return out[:, : S - 1, 0], out[:, : S - 1, 1:]
 
 
 def _validate_student_teacher_logits(

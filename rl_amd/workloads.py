@@ -17,6 +17,13 @@ a device.  Sizes default to the full workloads; tests pass smaller sizes.
 * packed_grpo_kl_bf16 64 sequences of U{64..1024} tokens packed into logits bf16
                     [1, ~34.8k, 256000] ~ N(0, 1.5^2); 8 prompts x 8 generations,
                     rewards ~ Bernoulli(0.3); reference = current + N(0, 0.1^2)
+* distill_rkl_bf16  student and teacher logits bf16 [8, 2048, 151936], both
+                    ~ N(0, 1.5^2); the GRPO batch's response mask (512-token
+                    prompt, U{256..1536} response tokens, padding)
+* score_centering_bf16 the GRPO step plus 20 sampler top-k ids per position
+                    (the sampled token first, then uniform ids); the sampler's
+                    log-probs are the current ones + N(0, 0.05^2) (see
+                    finish_score_centering_step)
 * linear_ce_bf16    hidden states bf16 [2048, 8, 4096] ~ N(0, 1) and an LM-head
                     weight bf16 [151936, 4096] ~ N(0, (1.5 / 64)^2) (logits
                     ~ N(0, 1.5^2)); uniform token ids; upstream gradient zero on
@@ -238,3 +245,51 @@ def linear_ce_bf16(
     live = (pos >= prompt_len) & (pos < prompt_len + lens.unsqueeze(1))
     grad = torch.randn((B, S - 1), generator=g) * live[:, 1:].float()
     return {"hidden": hidden, "weight": weight, "input_ids": ids.to(device), "grad": grad.to(device)}
+
+
+def _response_mask(B, S, prompt_len, resp_min, resp_max, g):
+    lens = torch.randint(resp_min, resp_max + 1, (B,), generator=g)
+    pos = torch.arange(S).unsqueeze(0)
+    return ((pos >= prompt_len) & (pos < prompt_len + lens.unsqueeze(1))).float()
+
+
+def distill_rkl_bf16(
+    B: int = 8,
+    S: int = 2048,
+    V: int = 151936,
+    prompt_len: int = 512,
+    resp_min: int = 256,
+    resp_max: int = 1536,
+    seed: int = 7,
+    device=None,
+):
+    """Student/teacher logits of a full-vocabulary reverse-KL distillation step."""
+    g = _gen(seed)
+    student = _randn_bf16((B, S, V), 1.5, g, device)
+    teacher = _randn_bf16((B, S, V), 1.5, g, device)
+    token_mask = _response_mask(B, S, prompt_len, resp_min, resp_max, g)
+    return {"student": student, "teacher": teacher, "token_mask": token_mask.to(device)}
+
+
+def score_centering_bf16(K: int = 20, seed: int = 8, device=None, **grpo_kw):
+    """The GRPO step's inputs plus sampler top-k ids [B, S, K] (id 0 = the sampled token)."""
+    data = grpo_step_bf16(device=device, **grpo_kw)
+    g = _gen(seed)
+    B, S = data["input_ids"].shape
+    V = data["logits"].shape[-1]
+    ids = torch.randint(0, V, (B, S, K), generator=g).to(data["input_ids"].device)
+    ids[..., 0] = data["input_ids"]
+    data["sampler_topk_token_ids"] = ids
+    data["sampler_noise"] = (torch.randn((B, S, K), generator=g) * 0.05).to(ids.device)
+    return data
+
+
+def finish_score_centering_step(data: dict, current_logprobs: torch.Tensor,
+                                current_topk_logprobs: torch.Tensor) -> dict:
+    """finish_grpo_step plus sampler log-probs = current top-k log-probs + noise, [B, S, K]."""
+    data = finish_grpo_step(data, current_logprobs)
+    B, S, K = data["sampler_topk_token_ids"].shape
+    q = torch.zeros((B, S, K), dtype=torch.float32, device=current_topk_logprobs.device)
+    q[:, 1:] = current_topk_logprobs.detach().float() + data["sampler_noise"][:, 1:]
+    data["sampler_topk_logprobs"] = q
+    return data

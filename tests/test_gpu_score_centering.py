@@ -197,3 +197,59 @@ def test_prepare_loss_input_values_and_gradients():
     got = torch.autograd.grad(prepared["policy_logprobs_at_sampler_topk"].sum(), ld)[0]
     exp = torch.autograd.grad(reference.sum(), lr)[0]
     torch.testing.assert_close(got.cpu(), exp, rtol=1e-5, atol=1e-6)
+
+
+def test_one_pass_inputs_match_the_separate_paths():
+    """prepare_loss_input's one K+1-id pass against get_next_token_logprobs_from_logits +
+    get_policy_logprobs_at_sampler_topk: values bit-identical; the gradient is the fp32 sum of
+    the two rounded once, checked against the oracle (within 1e-3 or one bf16 ulp).  The
+    separate paths round each gradient and then their sum, so they may sit up to two bf16
+    ulps from it (where the sampled token is also a top-k id, both add a one-hot term)."""
+    say("one-pass score-centering inputs")
+    from types import SimpleNamespace
+
+    from rl_amd.distributed.model_utils import (
+        get_next_token_logprobs_from_logits,
+        get_policy_logprobs_at_sampler_topk,
+    )
+    from tests.helpers import assert_close_or_ulp_bf16
+
+    g = torch.Generator().manual_seed(21)
+    B, S, V, K = 2, 64, 151936, 20
+    logits = (torch.randn(B, S, V, generator=g) * 1.5).bfloat16().to(DEV)
+    ids = torch.randint(0, V, (B, S), generator=g).to(DEV)
+    sids = torch.randint(0, V, (B, S, K), generator=g).to(DEV)
+    sids[..., 0] = ids
+    sids[1, 5, 3] = sids[1, 5, 4]  # a repeated id
+    w1 = torch.randn(B, S - 1, generator=g).to(DEV)
+    w2 = torch.randn(B, S - 1, K, generator=g).to(DEV)
+    loss_fn = SimpleNamespace(input_type=LossInputType.LOGPROB, score_centering=True)
+
+    l1 = logits.clone().requires_grad_(True)
+    li, _ = prepare_loss_input(l1, {"input_ids": ids, "sampler_topk_token_ids": sids,
+                                    "sampler_topk_logprobs": torch.zeros(B, S, K, device=DEV)}, loss_fn)
+    ((li["next_token_logprobs"] * w1).sum() + (li["policy_logprobs_at_sampler_topk"] * w2).sum()).backward()
+
+    l2 = logits.clone().requires_grad_(True)
+    a = get_next_token_logprobs_from_logits(ids, l2)
+    b = get_policy_logprobs_at_sampler_topk(sids, l2)
+    (g1,) = torch.autograd.grad((a * w1).sum(), l2, retain_graph=True)
+    (g2,) = torch.autograd.grad((b * w2).sum(), l2)
+
+    assert torch.equal(li["next_token_logprobs"], a)
+    assert torch.equal(li["policy_logprobs_at_sampler_topk"], b)
+    from oracle.vocab_reduce import gather_logprobs_grad
+
+    idx = torch.cat([ids.unsqueeze(-1), sids], -1).roll(-1, dims=1).cpu()
+    go = torch.zeros(B, S, K + 1)
+    go[:, : S - 1, 0] = w1.cpu()
+    go[:, : S - 1, 1:] = w2.cpu()
+    assert_close_or_ulp_bf16(l1.grad, gather_logprobs_grad(logits.cpu(), idx, 0, V, go), 1e-3)
+    # the separate paths: each gradient rounded to bf16, then their sum rounded again.
+    # They differ from the single rounding by at most those three roundings
+    # (2^-8 relative each, bf16 keeps 8 significant bits).
+    ga = l1.grad.cpu().float()
+    g1, g2 = g1.cpu().float(), g2.cpu().float()
+    sep = (g1 + g2).bfloat16().float()
+    bound = (g1.abs() + g2.abs() + sep.abs() + ga.abs()) * 2.0 ** -8 + 1e-30
+    assert torch.all((ga - sep).abs() <= bound)
