@@ -156,15 +156,7 @@ def main() -> None:
 
     traffic = _traffic("grpo")
 
-    if args.calibrate_copy_gib > 0:
-        n = int(args.calibrate_copy_gib * (1 << 30)) // 4
-        a = torch.empty(n, dtype=torch.float32, device=dev).fill_(1.0)
-        b = torch.empty_like(a)
-        torch.cuda.synchronize()
-        for _ in range(3):
-            b.copy_(a)
-        torch.cuda.synchronize()
-        del a, b
+    _calibration_copy(args, dev)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -224,6 +216,23 @@ def main() -> None:
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
+
+
+def _calibration_copy(args, dev) -> None:
+    """A plain device copy of --calibrate-copy-gib GiB (three times), whose HBM
+    counter readings scale FETCH_SIZE / WRITE_SIZE to bytes."""
+    if args.calibrate_copy_gib <= 0:
+        return
+    import torch
+
+    n = int(args.calibrate_copy_gib * (1 << 30)) // 4
+    a = torch.empty(n, dtype=torch.float32, device=dev).fill_(1.0)
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    del a, b
 
 
 def _timed(step, steps: int, warmup: int, main_kernels: list):
@@ -559,6 +568,7 @@ def bench_workload(args) -> None:
                "loss": "ClippedPG clip 0.2/0.2, k3 KL beta 0.01, sequence-level mean; GRPO adv (no LOO)"}
         dtype = "bf16"
 
+    _calibration_copy(args, dev)
     cfg["parallelism"] = "single-gpu"
     step_gbps = step_bytes / (ms_step * 1e-3) / 1e9 if step_bytes is not None else None
     out = {

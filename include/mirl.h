@@ -425,8 +425,9 @@ typedef struct mirl_score_centering_args {
   void* grad;
 } mirl_score_centering_args;
 
-/* Number of scratch elements (of the loss dtype) mirl_clipped_pg needs. */
-int64_t mirl_clipped_pg_workspace_elems(int64_t B);
+/* Number of scratch elements (of the loss dtype) mirl_clipped_pg needs for
+ * [B, L] tokens, with or without score centering. */
+int64_t mirl_clipped_pg_workspace_elems(int64_t B, int64_t L, int score_centering);
 
 /*
  * Fused ClippedPG loss forward + closed-form backward over [B, L] tokens
@@ -437,7 +438,8 @@ int64_t mirl_clipped_pg_workspace_elems(int64_t B);
  * `dtype` is MIRL_DTYPE_F32 or MIRL_DTYPE_F64 for every float tensor;
  * support_mask is uint8 (bool); sample_mask and rewards are [B] vectors;
  * global_valid_seqs / global_valid_toks are device scalars of `dtype`.
- * `workspace` holds mirl_clipped_pg_workspace_elems(B) elements of `dtype`.
+ * `workspace` holds mirl_clipped_pg_workspace_elems(B, L, score_centering != NULL)
+ * elements of `dtype`.
  * `score_centering` is NULL or adds the score-centering correction: the
  * per-token term of mirl_score_centering_term at the final loss mask, times
  * the masked advantage, reduced like the actor loss and added to it; the

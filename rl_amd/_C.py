@@ -137,7 +137,7 @@ SIGNATURES = {
         [_P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I64, _I64, _I64, _I64, _P, _P, _I64,
          _I64, _P, _I64, _I64, _P],
     ),
-    "mirl_clipped_pg_workspace_elems": (_I64, [_I64]),
+    "mirl_clipped_pg_workspace_elems": (_I64, [_I64, _I64, _I]),
     "mirl_clipped_pg": (
         _I,
         [ctypes.POINTER(PgConfig), _I, _I64, _I64] + [View2D] * 8 + [_P] * 7
@@ -474,7 +474,8 @@ def clipped_pg(
     grad_curr = torch.empty((B, L), dtype=dtype, device=dev)
     grad_unf = torch.empty((B, L), dtype=dtype, device=dev) if unfiltered is not None else None
     lib = load()
-    ws = torch.empty(int(lib.mirl_clipped_pg_workspace_elems(B)), dtype=dtype, device=dev)
+    ws = torch.empty(int(lib.mirl_clipped_pg_workspace_elems(B, L, int(score_centering is not None))),
+                     dtype=dtype, device=dev)
     st = _launch(
         "mirl_clipped_pg", dev,
         ctypes.byref(cfg), _dtype_code(curr), B, L, _view(curr), _view(unfiltered),

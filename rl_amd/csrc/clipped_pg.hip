@@ -269,6 +269,16 @@ __device__ void score_centering_token(const mirl_score_centering_args& sc, int64
   *head_out = head;
 }
 
+// Score-centering scratch: per-token term and head mass (written by
+// sc_term_kernel) and the gradient scale alpha * A (written by pg_rows_kernel,
+// read by sc_scale_kernel); each [B, L].
+template <class T>
+struct ScWork {
+  T* term;
+  T* head;
+  T* scale;
+};
+
 template <class T>
 struct Inputs {
   View<T> curr, unf, tm, adv, prev, gen, ref;
@@ -284,8 +294,7 @@ __global__ __launch_bounds__(kRowThreads) void pg_rows_kernel(mirl_pg_config cfg
                                                               Inputs<T> in, T* __restrict__ gcurr,
                                                               T* __restrict__ gunf,
                                                               T* __restrict__ part,
-                                                              mirl_score_centering_args sc,
-                                                              int has_sc) {
+                                                              ScWork<T> sc_ws, int has_sc) {
   __shared__ T scratch[kRowThreads / 64];
   const int64_t b = blockIdx.x;
   const int tid = threadIdx.x;
@@ -492,16 +501,14 @@ __global__ __launch_bounds__(kRowThreads) void pg_rows_kernel(mirl_pg_config cfg
       acc[P_ACTOR] += v * tm2;  // scaled per row below
     }
     if (has_sc) {
-      // correction A * term, normalised like the actor loss (loss_functions.py:1070-1097)
-      T* go = static_cast<T*>(sc.grad) + (b * L + l) * sc.K;
+      // correction A * term, normalised like the actor loss (loss_functions.py:1070-1097);
+      // term / head come from sc_term_kernel, the gradient scale goes to sc_scale_kernel
+      const int64_t i = b * L + l;
       if (on) {
-        T term, head;
-        score_centering_token<T>(sc, b, l, A, alpha * A, go, &term, &head);
-        acc[P_SC] += (A * term) * (cfg.token_level_loss ? mask2 : tm2);
-        acc[P_HM] += head * mask2;
-      } else {
-        for (int64_t k = 0; k < sc.K; ++k) go[k] = T(0);
+        acc[P_SC] += (A * sc_ws.term[i]) * (cfg.token_level_loss ? mask2 : tm2);
+        acc[P_HM] += sc_ws.head[i] * mask2;
       }
+      sc_ws.scale[i] = on ? alpha * A : T(0);
     }
     if (cfg.use_cispo) {
       gc += on ? alpha * wv * dcl_dc_direct : T(0);
@@ -659,6 +666,45 @@ __global__ __launch_bounds__(kFinalThreads) void pg_final_kernel(mirl_pg_config 
   }
 }
 
+// compute_score_centering_term over [B, L] tokens, one thread per token.
+// Tokens with token_mask == 0 (or, when `sample_mask` is given, in a sample
+// whose mask is 0) get zero term, head mass and coefficients.
+template <class T>
+__global__ __launch_bounds__(256) void sc_term_kernel(mirl_score_centering_args sc, int64_t B,
+                                                      int64_t L, View<T> tm,
+                                                      const T* __restrict__ sample_mask,
+                                                      View<T> adv, int has_adv,
+                                                      T* __restrict__ term,
+                                                      T* __restrict__ head) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= B * L) return;
+  const int64_t b = i / L, l = i - b * L;
+  T* coef = static_cast<T*>(sc.grad) + i * sc.K;
+  if (tm(b, l) == T(0) || (sample_mask != nullptr && sample_mask[b] == T(0))) {
+    term[i] = T(0);
+    head[i] = T(0);
+    for (int64_t k = 0; k < sc.K; ++k) coef[k] = T(0);
+    return;
+  }
+  const T A = has_adv ? adv(b, l) : T(0);
+  T t, h;
+  score_centering_token<T>(sc, b, l, A, T(1), coef, &t, &h);
+  term[i] = t;
+  head[i] = h;
+}
+
+// dloss/dplog[b, l, k] = coef[b, l, k] * scale[b, l]; exactly 0 where the
+// scale is 0 (tokens outside the final loss mask).  One thread per element.
+template <class T>
+__global__ __launch_bounds__(256) void sc_scale_kernel(T* __restrict__ grad,
+                                                       const T* __restrict__ scale, int64_t K,
+                                                       int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const T sc = scale[i / K];
+  grad[i] = (sc == T(0)) ? T(0) : grad[i] * sc;
+}
+
 template <class T>
 int run(const mirl_pg_config* cfg, int64_t B, int64_t L, const mirl_view2d* v,
         const void* sample_mask, const void* rewards, const void* gvs, const void* gvt,
@@ -679,39 +725,30 @@ int run(const mirl_pg_config* cfg, int64_t B, int64_t L, const mirl_view2d* v,
   in.gvs = static_cast<const T*>(gvs);
   in.gvt = static_cast<const T*>(gvt);
   T* part = static_cast<T*>(ws);
-  mirl_score_centering_args scv{};
-  if (sc != nullptr) scv = *sc;
   const int has_sc = sc != nullptr ? 1 : 0;
+  ScWork<T> scw{nullptr, nullptr, nullptr};
+  const int64_t n = B * L;
+  if (has_sc) {
+    // workspace layout: row partials, then term, head mass and scale ([B, L] each)
+    scw.term = part + B * NUM_SLOTS;
+    scw.head = scw.term + n;
+    scw.scale = scw.head + n;
+    if (n > 0)
+      hipLaunchKernelGGL((sc_term_kernel<T>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                         *sc, B, L, in.tm, in.sample_mask, in.adv, 1, scw.term, scw.head);
+  }
   hipLaunchKernelGGL((pg_rows_kernel<T>), dim3((unsigned)B), dim3(kRowThreads), 0, st, *cfg, L, in,
-                     static_cast<T*>(gcurr), static_cast<T*>(gunf), part, scv, has_sc);
+                     static_cast<T*>(gcurr), static_cast<T*>(gunf), part, scw, has_sc);
   if (int e = check_launch("mirl_clipped_pg(rows)")) return e;
   hipLaunchKernelGGL((pg_final_kernel<T>), dim3(1), dim3(kFinalThreads), 0, st, *cfg, B, L, in,
                      static_cast<const T*>(part), static_cast<T*>(metrics), static_cast<T*>(gcurr),
                      has_sc);
-  return check_launch("mirl_clipped_pg(final)");
-}
-
-// compute_score_centering_term over [B, L] tokens, one thread per token.
-template <class T>
-__global__ __launch_bounds__(256) void sc_term_kernel(mirl_score_centering_args sc, int64_t B,
-                                                      int64_t L, View<T> tm, View<T> adv,
-                                                      int has_adv, T* __restrict__ term,
-                                                      T* __restrict__ head) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= B * L) return;
-  const int64_t b = i / L, l = i - b * L;
-  T* coef = static_cast<T*>(sc.grad) + i * sc.K;
-  if (tm(b, l) == T(0)) {
-    term[i] = T(0);
-    head[i] = T(0);
-    for (int64_t k = 0; k < sc.K; ++k) coef[k] = T(0);
-    return;
+  if (has_sc && n * sc->K > 0) {
+    const int64_t ne = n * sc->K;
+    hipLaunchKernelGGL((sc_scale_kernel<T>), dim3((unsigned)((ne + 255) / 256)), dim3(256), 0, st,
+                       static_cast<T*>(sc->grad), static_cast<const T*>(scw.scale), sc->K, ne);
   }
-  const T A = has_adv ? adv(b, l) : T(0);
-  T t, h;
-  score_centering_token<T>(sc, b, l, A, T(1), coef, &t, &h);
-  term[i] = t;
-  head[i] = h;
+  return check_launch("mirl_clipped_pg(final)");
 }
 
 template <class T>
@@ -721,8 +758,8 @@ int run_sc_term(int64_t B, int64_t L, const mirl_score_centering_args* sc, mirl_
   View<T> tmv{static_cast<const T*>(tm.ptr), tm.sb, tm.sl};
   View<T> av{static_cast<const T*>(adv.ptr), adv.sb, adv.sl};
   hipLaunchKernelGGL((sc_term_kernel<T>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, *sc,
-                     B, L, tmv, av, adv.ptr != nullptr ? 1 : 0, static_cast<T*>(term),
-                     static_cast<T*>(head));
+                     B, L, tmv, static_cast<const T*>(nullptr), av, adv.ptr != nullptr ? 1 : 0,
+                     static_cast<T*>(term), static_cast<T*>(head));
   return check_launch("mirl_score_centering_term");
 }
 
@@ -731,7 +768,9 @@ int run_sc_term(int64_t B, int64_t L, const mirl_score_centering_args* sc, mirl_
 
 using namespace mirl;
 
-extern "C" int64_t mirl_clipped_pg_workspace_elems(int64_t B) { return B * NUM_SLOTS; }
+extern "C" int64_t mirl_clipped_pg_workspace_elems(int64_t B, int64_t L, int score_centering) {
+  return B * NUM_SLOTS + (score_centering ? 3 * B * L : 0);
+}
 
 extern "C" int mirl_clipped_pg(const mirl_pg_config* cfg, int dtype, int64_t B, int64_t L,
                                mirl_view2d curr, mirl_view2d unfiltered, mirl_view2d token_mask,

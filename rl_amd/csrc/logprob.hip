@@ -394,7 +394,10 @@ __global__ __launch_bounds__(256) void logprob_bwd_flat_kernel(
 //   grad = -p * sum_k g_k, plus g_k added at each in-range id_k, in fp32,
 // rounded once to the logits dtype.  Three launches: gather_gsum_kernel forms
 // sum_k g_k per row, the logprob backward writes the dense -p * gsum part (no
-// target), and gather_fixup_kernel rewrites the <= K entries at the ids.
+// target), and gather_fixup_kernel rewrites the <= K entries at the ids.  (A
+// single launch that stages each 8 KB piece's ids in LDS measured slower on
+// the [8, 2048, 151936] bf16 rows with 21 ids, 1.47 vs 1.30 ms: the staging
+// round in front of every piece's logits load cuts the bytes in flight.)
 __global__ __launch_bounds__(256) void gather_gsum_kernel(const float* __restrict__ g, int64_t R,
                                                          int64_t gsb, int64_t gsr, int64_t gsk,
                                                          int64_t K, int64_t rows,

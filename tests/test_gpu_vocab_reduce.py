@@ -55,7 +55,7 @@ def _check_grad(got, ref, dtype):
 @pytest.mark.parametrize("dtype,V", [(torch.float32, 997), (torch.bfloat16, 1000),
                                      (torch.bfloat16, 1003), (torch.float16, 512),
                                      (torch.bfloat16, 151936)])
-@pytest.mark.parametrize("K", [1, 5, 20])
+@pytest.mark.parametrize("K", [1, 5, 20, 70])
 def test_gather_fwd_bwd_parity(dtype, V, K):
     say("gather", dtype, "V", V, "K", K)
     g = torch.Generator().manual_seed(V + K)

@@ -57,4 +57,5 @@ def test_invalid_arguments_return_status_not_abort():
     st = lib.mirl_logprob_fwd(None, 0, 1, 1, 0, 0, 0, None, 1, 1, 0, 10, None, None, None)
     assert st != 0
     assert "shape" in lib.mirl_last_error().decode()
-    assert lib.mirl_clipped_pg_workspace_elems(8) > 0
+    assert lib.mirl_clipped_pg_workspace_elems(8, 100, 0) > 0
+    assert lib.mirl_clipped_pg_workspace_elems(8, 100, 1) == lib.mirl_clipped_pg_workspace_elems(8, 100, 0) + 2400
