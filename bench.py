@@ -48,7 +48,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--workload", default="grpo",
                     choices=["grpo", "fwd_f32", "long_context", "topk_filter", "packed_kl", "linear_ce",
-                             "distill_rkl", "score_centering"])
+                             "distill_rkl", "score_centering", "topk_export"])
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--cpu-sample-rows", type=int, default=1024)
@@ -497,6 +497,27 @@ def bench_workload(args) -> None:
         cfg = {"workload": "grpo_score_centering_fwd_bwd", "logits": [B, S, V], "sampler_topk": K,
                "next_token_rows": rows, "active_rows": active, "ids_per_row": K + 1,
                "loss": "ClippedPG clip 0.2/0.2 token-level + score centering (IS off); GRPO adv"}
+        dtype = "bf16"
+    elif w == "topk_export":
+        from rl_amd.distributed.model_utils import distributed_vocab_topk
+
+        d = workloads.distill_rkl_bf16(device=dev)
+        teacher = d["teacher"]
+        del d
+        B, S, V = teacher.shape
+        k = 64
+
+        def step():
+            return distributed_vocab_topk(teacher, k, None, vocab_start_index=0, vocab_end_index=V)
+
+        ms_step, ms = _timed(step, args.steps, args.warmup, ["mirl_vocab_topk"])
+        rows = B * S
+        esz = 2
+        fwd_bytes = rows * V * esz + rows * k * 12
+        roof = _roofline("mirl_vocab_topk", fwd_bytes, ms.get("mirl_vocab_topk", 0.0), w)
+        step_bytes = fwd_bytes
+        cfg = {"workload": "teacher_topk_export", "logits": [B, S, V], "k": k, "rows": rows,
+               "outputs": "fp32 values + int64 ids [B, S, k]"}
         dtype = "bf16"
     else:  # packed_kl
         import torch.distributed as dist

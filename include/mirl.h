@@ -139,6 +139,26 @@ int mirl_gather_logprob_bwd(const void* logits, int dtype, int64_t B, int64_t R,
                             int64_t gi_stride_b, int64_t gi_stride_r,
                             void* stream);
 
+/* Bytes of scratch mirl_vocab_topk needs for `rows` rows. */
+int64_t mirl_vocab_topk_workspace_bytes(int64_t rows);
+
+/*
+ * The k largest logits of each row and their global ids (1 <= k <= min(1024, V)):
+ *   values[b,r,i]  = the (i+1)-th largest x[b,r,:] (as fp32, exact),
+ *   indices[b,r,i] = vocab_start + its position; equal values are ordered by
+ *                    ascending position (the lower id first);
+ * both contiguous [B, R, k].  NaN sorts above every number, -0.0 ties +0.0.
+ * One streaming pass per row; rows with more than 1024 candidates at or above
+ * the k-th largest lane maximum (many equal values) are redone by an exact
+ * radix selection.  `workspace` holds mirl_vocab_topk_workspace_bytes(B*R).
+ *
+ * Replaces: distributed_vocab_topk (nemo_rl/distributed/model_utils.py:1867-1935)
+ * with a vocab group of size 1 (torch.topk of the fp32 logits + the vocab offset).
+ */
+int mirl_vocab_topk(const void* logits, int dtype, int64_t B, int64_t R, int64_t V,
+                    int64_t stride_b, int64_t stride_r, int k, int64_t vocab_start,
+                    float* values, int64_t* indices, void* workspace, void* stream);
+
 /* ---------------------------------------------------------------------- */
 /* student / teacher divergences over the full vocabulary                  */
 /* ---------------------------------------------------------------------- */

@@ -134,3 +134,13 @@ def divergence_f64(kind: str, student: torch.Tensor, teacher: Optional[torch.Ten
     if kind == "cross_entropy":
         return -(p * lt).sum(-1)
     return (p * (ls - lt)).sum(-1)
+
+
+def vocab_topk(logits: torch.Tensor, k: int, vocab_start: int = 0):
+    """(values fp32, global ids) of the k largest logits per row, descending, equal values
+    by ascending position (distributed_vocab_topk at TP=1, reference model_utils.py:1867-1935,
+    is torch.topk of the fp32 logits plus the vocabulary offset; the tie order is this build's
+    choice, a stable descending sort)."""
+    x = logits.float()
+    vals, idx = torch.sort(x, dim=-1, descending=True, stable=True)
+    return vals[..., :k].contiguous(), idx[..., :k] + vocab_start

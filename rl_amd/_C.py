@@ -158,6 +158,11 @@ SIGNATURES = {
         [_P, _I, _I64, _I64, _I64, _I64, _I64, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P,
          _I64, _I64, _I64, _P, _P, _I64, _I64, _P],
     ),
+    "mirl_vocab_topk_workspace_bytes": (_I64, [_I64]),
+    "mirl_vocab_topk": (
+        _I,
+        [_P, _I, _I64, _I64, _I64, _I64, _I64, _I, _I64, _P, _P, _P, _P],
+    ),
     "mirl_divergence_fwd": (
         _I,
         [_I, _P, _P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _P],
@@ -591,6 +596,25 @@ def gather_logprob_bwd(
         grad_in.data_ptr(), grad_in.stride(0), grad_in.stride(1), _stream(dev),
     )
     _check(st, "mirl_gather_logprob_bwd")
+
+
+def vocab_topk(logits: torch.Tensor, k: int, vocab_start: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """(values fp32 [B, R, k], global ids int64 [B, R, k]) of the k largest logits per row."""
+    dev = _require_gpu(logits)
+    B, R, V = logits.shape
+    assert logits.stride(-1) == 1
+    vals = torch.empty((B, R, k), dtype=torch.float32, device=dev)
+    idx = torch.empty((B, R, k), dtype=torch.int64, device=dev)
+    lib = load()
+    ws = torch.empty(max(1, int(lib.mirl_vocab_topk_workspace_bytes(B * R))), dtype=torch.uint8,
+                     device=dev)
+    st = _launch(
+        "mirl_vocab_topk", dev,
+        logits.data_ptr(), _dtype_code(logits), B, R, V, logits.stride(0), logits.stride(1),
+        int(k), int(vocab_start), vals.data_ptr(), idx.data_ptr(), ws.data_ptr(), _stream(dev),
+    )
+    _check(st, "mirl_vocab_topk")
+    return vals, idx
 
 
 # ---------------------------------------------------------------------------

@@ -93,6 +93,10 @@ struct FilterParams {
   RowInfo* info;
   int32_t* kept_idx;  // [rows, kKeepCap]
   float* kept_p;      // [rows, kKeepCap]
+  // top-k export (vocab_topk): [rows, top_k] values and global ids, or null
+  float* tk_vals;
+  int64_t* tk_idx;
+  int64_t tk_base;
 };
 
 // y = dtype(float(x) / T)
@@ -256,10 +260,145 @@ __device__ void finish_row(const FilterParams& P, int64_t row, const uint64_t* s
   }
 }
 
+// Top-k export epilogue: `top` holds the k largest (okey(y) << 32 | ~index)
+// keys in ascending order; entry i of the output is the (i+1)-th largest, its
+// value re-read from the logits (exact, including the sign of zero).
+template <class E>
+__device__ void export_topk(const FilterParams& P, int64_t row, const typename E::raw* x,
+                            const uint64_t* top) {
+  const int k = P.top_k;
+  for (int i = threadIdx.x; i < k; i += blockDim.x) {
+    const int64_t j = (int64_t)(~(uint32_t)(top[k - 1 - i] & 0xffffffffu));
+    P.tk_vals[row * k + i] = E::load(x + j);
+    P.tk_idx[row * k + i] = P.tk_base + j;
+  }
+  if (threadIdx.x == 0) P.info[row].flags = 0;
+}
+
+// Order key of the export: every NaN (either sign) above +inf, as torch.topk ranks it.
+__device__ __forceinline__ uint32_t okey_export(float y) {
+  return (y != y) ? 0xffffffffu : okey(y);
+}
+
+// k-th largest order key of the row by radix selection (8 bits per pass), and
+// how many elements equal to it belong to the top k ("remaining").
+template <int NT, class Y>
+__device__ uint32_t radix_kth_key(Y&& yat, int64_t V, int k, int* hist_i, uint32_t* s_sel,
+                                  int* remaining_out, bool nan_high) {
+  const int tid = threadIdx.x;
+  uint32_t prefix = 0, mask = 0;
+  int remaining = k;
+  for (int d = 3; d >= 0; --d) {
+    const int shift = 8 * d;
+    for (int i = tid; i < 256; i += NT) hist_i[i] = 0;
+    __syncthreads();
+    for (int64_t j = tid; j < V; j += NT) {
+      const float y = yat(j);
+      const uint32_t kk = nan_high ? okey_export(y) : okey(y);
+      if ((kk & mask) == prefix) atomicAdd(&hist_i[(kk >> shift) & 255u], 1);
+    }
+    __syncthreads();
+    if (tid == 0) {
+      int acc = 0, bsel = 0;
+      for (int bin = 255; bin >= 0; --bin) {
+        if (acc + hist_i[bin] >= remaining) {
+          bsel = bin;
+          break;
+        }
+        acc += hist_i[bin];
+      }
+      s_sel[0] = (uint32_t)bsel;
+      s_sel[1] = (uint32_t)(remaining - acc);
+    }
+    __syncthreads();
+    prefix |= s_sel[0] << shift;
+    mask |= 255u << shift;
+    remaining = (int)s_sel[1];
+    __syncthreads();
+  }
+  *remaining_out = remaining;
+  return prefix;
+}
+
+// General top-k export for the rows the fast path flagged (candidate
+// overflow, i.e. many equal values): the k-th largest value by radix
+// selection, then among the elements equal to it the `remaining` lowest
+// indices (radix selection on the index bits), then exactly k entries
+// collected and rank-sorted.
+template <class E>
+__global__ __launch_bounds__(kGeneralThreads) void topk_export_general_kernel(FilterParams P) {
+  using raw = typename E::raw;
+  constexpr int NT = kGeneralThreads;
+  __shared__ int hist_i[256];
+  __shared__ uint32_t s_sel[2];
+  __shared__ int s_cnt;
+  __shared__ uint64_t s_cand[kCandCap];
+  const int64_t row = blockIdx.x;
+  if ((P.info[row].flags & 1) == 0) return;
+  const int64_t b = row / P.R, r = row - b * P.R;
+  const raw* x = static_cast<const raw*>(P.logits) + b * P.sb + r * P.sr;
+  const int tid = threadIdx.x;
+  const int64_t V = P.V;
+  auto yat = [&](int64_t j) { return E::load(x + j); };
+  int remaining = 0;
+  const uint32_t thr = radix_kth_key<NT>(yat, V, P.top_k, hist_i, s_sel, &remaining, true);
+
+  // the remaining-th smallest index among the elements whose key equals thr
+  int top_bit = 0;
+  while ((int64_t(1) << (top_bit + 1)) < V) ++top_bit;
+  uint32_t iprefix = 0, imask = 0;
+  int need = remaining;
+  for (int hi = top_bit; hi >= 0; hi -= 8) {
+    const int lo = hi >= 7 ? hi - 7 : 0;
+    const int nb = hi - lo + 1;
+    const uint32_t dmask = (1u << nb) - 1u;
+    for (int i = tid; i < 256; i += NT) hist_i[i] = 0;
+    __syncthreads();
+    for (int64_t j = tid; j < V; j += NT) {
+      if (okey_export(yat(j)) != thr) continue;
+      const uint32_t jj = (uint32_t)j;
+      if ((jj & imask) != iprefix) continue;
+      atomicAdd(&hist_i[(jj >> lo) & dmask], 1);
+    }
+    __syncthreads();
+    if (tid == 0) {
+      int acc = 0, bsel = 0;
+      for (int bin = 0; bin <= (int)dmask; ++bin) {
+        if (acc + hist_i[bin] >= need) {
+          bsel = bin;
+          break;
+        }
+        acc += hist_i[bin];
+      }
+      s_sel[0] = (uint32_t)bsel;
+      s_sel[1] = (uint32_t)(need - acc);
+    }
+    __syncthreads();
+    iprefix |= s_sel[0] << lo;
+    imask |= dmask << lo;
+    need = (int)s_sel[1];
+    __syncthreads();
+  }
+  const uint32_t i_last = iprefix;
+
+  if (tid == 0) s_cnt = 0;
+  __syncthreads();
+  for (int64_t j = tid; j < V; j += NT) {
+    const uint32_t kk = okey_export(yat(j));
+    if (kk > thr || (kk == thr && (uint32_t)j <= i_last)) {
+      const int slot = atomicAdd(&s_cnt, 1);
+      if (slot < kCandCap) s_cand[slot] = ((uint64_t)kk << 32) | (uint64_t)(~(uint32_t)j);
+    }
+  }
+  __syncthreads();
+  block_rank_sort<NT>(s_cand, P.top_k);
+  export_topk<E>(P, row, x, s_cand);
+}
+
 // ---------------------------------------------------------------------------
 // fast path
 // ---------------------------------------------------------------------------
-template <class E, int W, int U>
+template <class E, int W, int U, bool EXPORT = false>
 __global__ __launch_bounds__(64 * W) void filter_fast_kernel(FilterParams P) {
   using raw = typename E::raw;
   constexpr int NT = 64 * W;
@@ -306,6 +445,7 @@ __global__ __launch_bounds__(64 * W) void filter_fast_kernel(FilterParams P) {
 
   // ---- pass 1: stream the row, per-group maxima of the raw values ----------
   float lmax = -INFINITY, cur = -INFINITY;
+  bool saw_nan = false;  // the export ranks NaN above every number; fmaxf drops it
   int curg = 0;
   int j = 0;
   for (; tid + (j + U - 1) * NT < nvec; j += U) {
@@ -320,6 +460,10 @@ __global__ __launch_bounds__(64 * W) void filter_fast_kernel(FilterParams P) {
       mm[u] = w[0];
 #pragma unroll
       for (int k = 1; k < VEC; ++k) mm[u] = fmaxf(mm[u], w[k]);
+      if constexpr (EXPORT) {
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) saw_nan |= (w[k] != w[k]);
+      }
     }
     if (GS >= U) {
       const int g = j / GS;
@@ -360,6 +504,10 @@ __global__ __launch_bounds__(64 * W) void filter_fast_kernel(FilterParams P) {
     E::unpack(xv[tid + j * NT], w);
 #pragma unroll
     for (int k = 0; k < VEC; ++k) cur = fmaxf(cur, w[k]);
+    if constexpr (EXPORT) {
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) saw_nan |= (w[k] != w[k]);
+    }
   }
   if (curg < G) {
     s_gkey[curg * NT + tid] = okey_hi_up(cur);
@@ -370,6 +518,14 @@ __global__ __launch_bounds__(64 * W) void filter_fast_kernel(FilterParams P) {
   const float tv = (sp.tail0 + tid < P.V) ? E::load(x + sp.tail0 + tid) : -INFINITY;
   lmax = fmaxf(lmax, fmaxf(hv, tv));
   s_lmax[tid] = lmax;
+  if constexpr (EXPORT) {
+    saw_nan |= (hv != hv) || (tv != tv);
+    if (__syncthreads_or(saw_nan)) {
+      // a NaN is the largest element: the exact general path handles the row
+      if (tid == 0) P.info[row].flags = 1;
+      return;
+    }
+  }
   __syncthreads();
 
   // ---- lower bound tau: the k-th largest lane maximum ------------------------
@@ -381,9 +537,12 @@ __global__ __launch_bounds__(64 * W) void filter_fast_kernel(FilterParams P) {
   const float tau = s_tau;
 
   // ---- pass 2: re-read groups that can hold candidates ------------------------
+  // (value key, index) for the filter; (value key, ~index) for the export, so
+  // that among equal values the lower index sorts higher
   auto push = [&](float y, int64_t idx) {
     const int slot = atomicAdd(&s_count, 1);
-    if (slot < kCandCap) s_cand[slot] = ((uint64_t)okey(y) << 32) | (uint64_t)(uint32_t)idx;
+    const uint32_t lo = EXPORT ? ~(uint32_t)idx : (uint32_t)idx;
+    if (slot < kCandCap) s_cand[slot] = ((uint64_t)okey(y) << 32) | (uint64_t)lo;
   };
   // flagged groups are listed first, then their vectors are spread over the
   // whole workgroup so that the re-reads are independent loads
@@ -450,6 +609,10 @@ __global__ __launch_bounds__(64 * W) void filter_fast_kernel(FilterParams P) {
 
   // ---- sort the candidates; the k-th largest is the exact top-k value ----------
   block_rank_sort<NT>(s_cand, C);
+  if constexpr (EXPORT) {
+    export_topk<E>(P, row, x, s_cand + (C - P.top_k));
+    return;
+  }
   const uint32_t thr_key = (uint32_t)(s_cand[C - P.top_k] >> 32);
   // kept-k = the sorted suffix with key >= thr_key
   int cnt = 0;
@@ -492,36 +655,8 @@ __global__ __launch_bounds__(kGeneralThreads) void filter_general_kernel(FilterP
   // top-k value: radix select on the 32-bit order key, 8 bits per pass
   uint32_t thr_key = 0;
   if (P.top_k > 0) {
-    uint32_t prefix = 0, mask = 0;
-    int remaining = P.top_k;
-    for (int d = 3; d >= 0; --d) {
-      const int shift = 8 * d;
-      for (int i = tid; i < 256; i += NT) hist_i[i] = 0;
-      __syncthreads();
-      for (int64_t j = tid; j < V; j += NT) {
-        const uint32_t k = okey(yat(j));
-        if ((k & mask) == prefix) atomicAdd(&hist_i[(k >> shift) & 255u], 1);
-      }
-      __syncthreads();
-      if (tid == 0) {
-        int acc = 0, bsel = 0;
-        for (int bin = 255; bin >= 0; --bin) {
-          if (acc + hist_i[bin] >= remaining) {
-            bsel = bin;
-            break;
-          }
-          acc += hist_i[bin];
-        }
-        s_sel[0] = (uint32_t)bsel;
-        s_sel[1] = (uint32_t)(remaining - acc);
-      }
-      __syncthreads();
-      prefix |= s_sel[0] << shift;
-      mask |= 255u << shift;
-      remaining = (int)s_sel[1];
-      __syncthreads();
-    }
-    thr_key = prefix;
+    int remaining = 0;
+    thr_key = radix_kth_key<NT>(yat, V, P.top_k, hist_i, s_sel, &remaining, false);
   }
 
   // top-p cut: the smallest (key, index) whose cumulative probability > cut
@@ -836,6 +971,23 @@ int launch_fwd(const FilterParams& P, int64_t rows, hipStream_t st) {
 }
 
 template <class E>
+int launch_topk_export(const FilterParams& P, int64_t rows, hipStream_t st) {
+  switch (fast_waves(P.top_k)) {
+    case 8:
+      hipLaunchKernelGGL((filter_fast_kernel<E, 8, 8, true>), dim3((unsigned)rows), dim3(512), 0, st, P);
+      break;
+    default:
+      hipLaunchKernelGGL((filter_fast_kernel<E, 16, 4, true>), dim3((unsigned)rows), dim3(1024), 0,
+                         st, P);
+      break;
+  }
+  if (int e = check_launch("filter_fast_kernel(export)")) return e;
+  hipLaunchKernelGGL((topk_export_general_kernel<E>), dim3((unsigned)rows), dim3(kGeneralThreads), 0,
+                     st, P);
+  return check_launch("topk_export_general_kernel");
+}
+
+template <class E>
 int launch_bwd(const FilterBwdParams& P, int64_t B, int64_t rows, hipStream_t st) {
   const bool contiguous = P.gisr == P.V && (B == 1 || P.gisb == P.Rt * P.V);
   if (contiguous) {
@@ -900,6 +1052,9 @@ FilterParams make_params(const void* logits, int64_t R, int64_t V, int64_t sb, i
   P.info = static_cast<RowInfo*>(info);
   P.kept_idx = kept_idx;
   P.kept_p = kept_p;
+  P.tk_vals = nullptr;
+  P.tk_idx = nullptr;
+  P.tk_base = 0;
   return P;
 }
 
@@ -1011,4 +1166,36 @@ extern "C" int mirl_top_k_top_p_mask(const void* logits, int dtype, int64_t N, i
     hipLaunchKernelGGL((filter_mask_kernel<F16, 4>), dim3((unsigned)N), dim3(256), 0, st, Q,
                        filtered, keep_mask, filtered_row_stride, keep_row_stride);
   return check_launch("mirl_top_k_top_p_mask");
+}
+
+extern "C" int64_t mirl_vocab_topk_workspace_bytes(int64_t rows) {
+  return rows * (int64_t)sizeof(RowInfo);
+}
+
+extern "C" int mirl_vocab_topk(const void* logits, int dtype, int64_t B, int64_t R, int64_t V,
+                               int64_t stride_b, int64_t stride_r, int k, int64_t vocab_start,
+                               float* values, int64_t* indices, void* workspace, void* stream) {
+  clear_error();
+  if (dtype != MIRL_DTYPE_F32 && dtype != MIRL_DTYPE_BF16 && dtype != MIRL_DTYPE_F16) {
+    set_error("unsupported logits dtype code %d", dtype);
+    return MIRL_ERR_UNSUPPORTED;
+  }
+  MIRL_REQUIRE(B >= 0 && R >= 0 && V > 0, "invalid shape B=%lld R=%lld V=%lld", (long long)B,
+               (long long)R, (long long)V);
+  MIRL_REQUIRE(V < (int64_t(1) << 31), "vocabulary size %lld exceeds 2^31-1", (long long)V);
+  MIRL_REQUIRE(k >= 1 && k <= kCandCap && k <= V, "k=%d must be in [1, min(%d, V=%lld)]", k,
+               kCandCap, (long long)V);
+  const int64_t rows = B * R;
+  if (rows == 0) return MIRL_OK;
+  MIRL_REQUIRE(rows < (int64_t(1) << 31), "too many rows (%lld)", (long long)rows);
+  MIRL_REQUIRE(logits && values && indices && workspace, "null pointer argument");
+  FilterParams P = make_params(logits, R, V, stride_b, stride_r, nullptr, 0, 0, 1.0, k, 1.0,
+                               nullptr, workspace, nullptr, nullptr);
+  P.tk_vals = values;
+  P.tk_idx = indices;
+  P.tk_base = vocab_start;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == MIRL_DTYPE_F32) return launch_topk_export<F32>(P, rows, st);
+  if (dtype == MIRL_DTYPE_BF16) return launch_topk_export<BF16>(P, rows, st);
+  return launch_topk_export<F16>(P, rows, st);
 }

@@ -38,6 +38,7 @@ __all__ = [
     "ChunkedDistributedLogprobWithSampling",
     "ChunkedDistributedReverseKLToFixedLogits",
     "DistributedLogprob",
+    "distributed_vocab_topk",
     "DistributedLogprobWithSampling",
     "from_parallel_hidden_states_to_logprobs",
     "from_parallel_logits_to_logprobs",
@@ -52,6 +53,7 @@ _VOCAB_REDUCTIONS = (
     "ChunkedDistributedEntropy",
     "ChunkedDistributedCrossEntropyToFixedLogits",
     "ChunkedDistributedReverseKLToFixedLogits",
+    "distributed_vocab_topk",
 )
 
 

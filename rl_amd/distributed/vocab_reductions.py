@@ -1,5 +1,5 @@
-"""Other reductions over the vocabulary: logprobs at K ids per row, and the
-student/teacher entropy, cross entropy and reverse KL.
+"""Other reductions over the vocabulary: logprobs at K ids per row, the
+student/teacher entropy, cross entropy and reverse KL, and the top-k export.
 
 Drop-ins, with a vocab group of size 1, for these names of
 ``nemo_rl.distributed.model_utils``:
@@ -7,7 +7,8 @@ Drop-ins, with a vocab group of size 1, for these names of
 * ``ChunkedDistributedGatherLogprob`` and ``get_policy_logprobs_at_sampler_topk``
   (reference model_utils.py:691-805, 1723-1865), the score-centering inputs;
 * ``ChunkedDistributedEntropy``, ``ChunkedDistributedCrossEntropyToFixedLogits``
-  and ``ChunkedDistributedReverseKLToFixedLogits`` (model_utils.py:2199-2538).
+  and ``ChunkedDistributedReverseKLToFixedLogits`` (model_utils.py:2199-2538);
+* ``distributed_vocab_topk`` (model_utils.py:1867-1935), the teacher top-k export.
 
 Each forward is one streaming pass over the logits row (both rows for the
 teacher divergences) in a gfx950 kernel; each backward is one read and one write
@@ -28,6 +29,7 @@ __all__ = [
     "ChunkedDistributedEntropy",
     "ChunkedDistributedGatherLogprob",
     "ChunkedDistributedReverseKLToFixedLogits",
+    "distributed_vocab_topk",
     "get_policy_logprobs_at_sampler_topk",
     "next_token_and_sampler_topk_logprobs",
 ]
@@ -212,6 +214,36 @@ def next_token_and_sampler_topk_logprobs(
         vocab_parallel_group, False,
     )
     return out[:, : S - 1, 0], out[:, : S - 1, 1:]
+
+
+@torch.no_grad()
+def distributed_vocab_topk(
+    vocab_parallel_logits: torch.Tensor,
+    k: int,
+    tp_group: Optional[Any],
+    *,
+    vocab_start_index: int,
+    vocab_end_index: int,
+    chunk_size: Optional[int] = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Top-k values ``[B, S, k]`` (fp32) and global token ids ``[B, S, k]`` (reference model_utils.py:1867-1935).
+
+    One streaming kernel pass per row (group of size 1: no candidate exchange).
+    Values are the exact logits, descending; equal values are ordered by
+    ascending id.  ``k`` is clamped to the vocabulary size as in the reference;
+    values of ``k`` above 1024 raise ``NotImplementedError``.
+    """
+    assert vocab_end_index > vocab_start_index
+    _single_rank(tp_group)
+    _chunk(chunk_size)
+    logits = _unit_stride(vocab_parallel_logits)
+    if logits.dim() != 3:
+        raise ValueError(f"expected logits of shape [B, S, V_local], got {tuple(logits.shape)}")
+    V = logits.shape[-1]
+    k_eff = int(min(k, max(1, V)))
+    if k_eff > 1024:
+        raise NotImplementedError(f"top-k export supports k <= 1024, got {k_eff}")
+    return _C.vocab_topk(logits, k_eff, int(vocab_start_index))
 
 
 def _validate_student_teacher_logits(

@@ -1,0 +1,80 @@
+"""gfx950 teacher top-k export (distributed_vocab_topk with a group of size 1) against the
+CPU oracle (GPU).
+
+Top-k values and id sets are exact: values are the logits themselves (fp32), descending;
+equal values are ordered by ascending id (the oracle's stable descending sort).  The
+reference test's own checks (tests/unit/distributed/test_model_utils.py:1701-1730) run too:
+values equal torch.topk's fp32 values and regathering at the ids returns them.
+"""
+
+import pytest
+import torch
+
+from oracle.vocab_reduce import vocab_topk
+from rl_amd.distributed.model_utils import distributed_vocab_topk
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda", 0)
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+
+
+def _run(x, k, vs=0, chunk=None):
+    return distributed_vocab_topk(x.to(DEV), k, None, vocab_start_index=vs,
+                                  vocab_end_index=vs + x.shape[-1], chunk_size=chunk)
+
+
+def test_reference_case():
+    say("reference case [2,16,256] k=5")
+    torch.manual_seed(1337)
+    full = torch.randn(2, 16, 256, dtype=torch.bfloat16)
+    vals, idx = _run(full, 5, chunk=4)
+    exp_vals, _ = torch.topk(full.float(), 5, dim=-1)
+    assert torch.equal(vals.cpu(), exp_vals)
+    assert torch.equal(torch.gather(full.float(), -1, idx.cpu()), vals.cpu())
+
+
+@pytest.mark.parametrize("dtype,V,k", [(torch.bfloat16, 151936, 64), (torch.bfloat16, 151936, 1),
+                                       (torch.float32, 32000, 20), (torch.float16, 50000, 100),
+                                       (torch.bfloat16, 1000, 600), (torch.bfloat16, 4096, 1024),
+                                       (torch.bfloat16, 37, 37)])
+def test_random_rows_exact(dtype, V, k):
+    say("random", dtype, V, k)
+    g = torch.Generator().manual_seed(V + k)
+    x = (torch.randn(2, 5, V, generator=g) * 2).to(dtype)
+    vals, idx = _run(x, k, vs=7 * V)
+    ev, ei = vocab_topk(x, k, vocab_start=7 * V)
+    assert torch.equal(vals.cpu(), ev)
+    assert torch.equal(idx.cpu(), ei)
+
+
+def test_tie_heavy_rows_take_the_general_path():
+    """Rows with thousands of equal values overflow the fast path's candidate store."""
+    say("ties")
+    g = torch.Generator().manual_seed(5)
+    V = 151936
+    x = (torch.randn(3, 4, V, generator=g)).bfloat16()
+    x[0, 0] = 0.0                                          # every value equal
+    x[0, 1] = torch.randint(0, 3, (V,), generator=g).bfloat16()  # three distinct values
+    x[1, 2, ::7] = 5.0                                     # 21706 elements tied at the top
+    x[2, 3, 100] = float("nan")                            # NaN sorts first
+    x[2, 3, 5] = -0.0
+    for k in (1, 64, 1000):
+        vals, idx = _run(x, k)
+        ev, ei = vocab_topk(x, k)
+        assert torch.equal(idx.cpu(), ei), k
+        torch.testing.assert_close(vals.cpu(), ev, rtol=0, atol=0, equal_nan=True)
+
+
+def test_strided_logits_and_k_clamped_to_vocab():
+    say("strided / clamp")
+    g = torch.Generator().manual_seed(9)
+    base = torch.randn(2, 6, 3, 500, generator=g).bfloat16()
+    x = base[:, :, 1, :300]  # row stride 1500, 300 ids
+    vals, idx = _run(x, 40, vs=300)
+    ev, ei = vocab_topk(x, 40, vocab_start=300)
+    assert torch.equal(vals.cpu(), ev) and torch.equal(idx.cpu(), ei)
+    vals, idx = _run(x[:, :, :10].contiguous(), 50)  # k > V: the reference clamps to V
+    assert vals.shape[-1] == 10

@@ -128,3 +128,40 @@ def test_divergence_grad_dtype_is_the_logits_dtype():
     t = torch.randn(1, 2, 16, generator=g).bfloat16()
     out = divergence_grad("reverse_kl", s, t, torch.ones(1, 2))
     assert out.dtype == torch.bfloat16
+
+
+def test_vocab_topk_values_are_torch_topk_and_ids_point_at_them():
+    """The reference test's checks (test_model_utils.py:1701-1730): values equal the fp32
+    torch.topk values exactly and regathering at the ids returns them."""
+    from oracle.vocab_reduce import vocab_topk
+
+    torch.manual_seed(1337)
+    x = torch.randn(2, 16, 256, dtype=torch.bfloat16)
+    vals, idx = vocab_topk(x, 5)
+    exp_vals, _ = torch.topk(x.float(), 5, dim=-1)
+    assert torch.equal(vals, exp_vals)
+    assert torch.equal(torch.gather(x.float(), -1, idx), vals)
+
+
+def test_vocab_topk_brute_force_with_ties_nan_and_signed_zero():
+    """Rank of element j = #{i : x_i > x_j or (x_i == x_j and i < j)}; the top k are ranks < k."""
+    from oracle.vocab_reduce import vocab_topk
+
+    x = torch.tensor([[[1.0, 3.0, 3.0, -0.0, 0.0, 2.0, 3.0, float("nan"), -1.0]]])
+    vals, idx = vocab_topk(x, 6, vocab_start=100)
+    xs = x[0, 0].tolist()
+    import math
+
+    def gt(a, b):  # a sorts above b
+        if math.isnan(a):
+            return not math.isnan(b)
+        return (not math.isnan(b)) and a > b
+
+    ranks = []
+    for j, xj in enumerate(xs):
+        r = sum(1 for i, xi in enumerate(xs) if gt(xi, xj) or (not gt(xj, xi) and not gt(xi, xj) and i < j))
+        ranks.append(r)
+    order = sorted(range(len(xs)), key=lambda j: ranks[j])[:6]
+    assert idx[0, 0].tolist() == [100 + j for j in order]
+    got = vals[0, 0].tolist()
+    assert math.isnan(got[0]) and got[1:] == [xs[j] for j in order[1:]]
