@@ -93,6 +93,28 @@ int mirl_logprob_bwd(const void* logits, int dtype, int64_t B, int64_t R,
                      int64_t gi_stride_b, int64_t gi_stride_r, void* stream);
 
 /*
+ * Early-backward check for mirl_logprob_bwd.  A caller that launched
+ * mirl_logprob_bwd for an upstream gradient `grad_used` (contiguous fp32
+ * [B, R]) before the real upstream gradient `grad_out` was known passes both
+ * here: one kernel compares them bit for bit and writes *flag (device int,
+ * 1 = they differ); a second recomputes grad_in from grad_out when *flag is 1
+ * and returns at once otherwise.  Arguments as for mirl_logprob_bwd.
+ *
+ * Replaces: nothing in the reference (an ordering device: it lets the
+ * backward start before the host has synchronised on the loss's metrics).
+ */
+int mirl_logprob_bwd_recheck(const void* logits, int dtype, int64_t B, int64_t R,
+                             int64_t R_total, int64_t V, int64_t stride_b,
+                             int64_t stride_r, const int64_t* target,
+                             int64_t t_stride_b, int64_t t_stride_r,
+                             int64_t vocab_start, int64_t vocab_end,
+                             const float* row_stats, const float* grad_out,
+                             int64_t g_stride_b, int64_t g_stride_r,
+                             const float* grad_used, void* grad_in,
+                             int64_t gi_stride_b, int64_t gi_stride_r, int* flag,
+                             void* stream);
+
+/*
  * Log-probabilities at K given vocabulary ids per row:
  *   out[b,r,k] = (x[id - vocab_start] - m) - logsum   for vocab_start <= id < vocab_end,
  *   out[b,r,k] = 0                                     otherwise,

@@ -137,6 +137,11 @@ SIGNATURES = {
         [_P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I64, _I64, _I64, _I64, _P, _P, _I64,
          _I64, _P, _I64, _I64, _P],
     ),
+    "mirl_logprob_bwd_recheck": (
+        _I,
+        [_P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I64, _I64, _I64, _I64, _P, _P, _I64,
+         _I64, _P, _P, _I64, _I64, _P, _P],
+    ),
     "mirl_clipped_pg_workspace_elems": (_I64, [_I64, _I64, _I]),
     "mirl_clipped_pg": (
         _I,
@@ -301,14 +306,10 @@ def _require_gpu(*tensors: Optional[torch.Tensor]) -> torch.device:
     return dev
 
 
-def wait_and_fetch(t: torch.Tensor) -> list:
-    """Copy a small device tensor to the host and return it as a list.
-
-    The copy goes to a cached pinned buffer and completion is awaited by
-    polling an event, which returns sooner than a blocking device-to-host
-    copy once the producing kernel finishes (the caller is about to launch
-    more GPU work, so waking up late leaves the GPU idle).
-    """
+def start_fetch(t: torch.Tensor):
+    """Enqueue a copy of a small device tensor into a cached pinned buffer and
+    record an event after it; finish_fetch waits for that event.  Work the caller
+    enqueues in between runs after the copy, so the wait does not include it."""
     n = t.numel()
     key = (t.device, t.dtype, n)
     buf = _pinned.get(key)
@@ -318,9 +319,21 @@ def wait_and_fetch(t: torch.Tensor) -> list:
     buf.copy_(t.reshape(-1), non_blocking=True)
     ev = torch.cuda.Event()
     ev.record()
+    return buf, ev
+
+
+def finish_fetch(handle) -> list:
+    """Wait for start_fetch's copy by polling its event (wakes up sooner than a
+    blocking device-to-host copy) and return the values as a list."""
+    buf, ev = handle
     while not ev.query():
         pass
     return buf.tolist()
+
+
+def wait_and_fetch(t: torch.Tensor) -> list:
+    """Copy a small device tensor to the host and return it as a list."""
+    return finish_fetch(start_fetch(t))
 
 
 _pinned: dict = {}
@@ -439,6 +452,35 @@ def logprob_bwd(
         grad_in.stride(1), _stream(dev),
     )
     _check(st, "mirl_logprob_bwd")
+
+
+def logprob_bwd_recheck(
+    logits: torch.Tensor,
+    target: torch.Tensor,
+    vocab_start: int,
+    vocab_end: int,
+    stats: torch.Tensor,
+    grad_out: torch.Tensor,
+    grad_used: torch.Tensor,
+    grad_in: torch.Tensor,
+) -> None:
+    """grad_in was written by logprob_bwd for grad_used; make it right for grad_out (device-side check)."""
+    dev = _require_gpu(logits, target, stats, grad_out, grad_used, grad_in)
+    B, R = target.shape
+    Rt = grad_in.shape[1]
+    V = logits.shape[-1]
+    assert grad_used.is_contiguous() and tuple(grad_used.shape) == (B, R)
+    assert grad_out.dtype == torch.float32 and grad_used.dtype == torch.float32
+    flag = torch.empty(1, dtype=torch.int32, device=dev)
+    st = _launch(
+        "mirl_logprob_bwd_recheck", dev,
+        logits.data_ptr(), _dtype_code(logits), B, R, Rt, V, logits.stride(0), logits.stride(1),
+        target.data_ptr(), target.stride(0), target.stride(1), int(vocab_start), int(vocab_end),
+        stats.data_ptr(), grad_out.data_ptr(), grad_out.stride(0), grad_out.stride(1),
+        grad_used.data_ptr(), grad_in.data_ptr(), grad_in.stride(0), grad_in.stride(1),
+        flag.data_ptr(), _stream(dev),
+    )
+    _check(st, "mirl_logprob_bwd_recheck")
 
 
 # ---------------------------------------------------------------------------

@@ -513,7 +513,14 @@ class ClippedPGLossFn(LossFunction):
             curr_k, unfiltered, cfg, token_mask, advantages, prev, generation, reference,
             support, sample_mask, rewards, gvs, gvt, plog, sc,
         )
-        values = _C.wait_and_fetch(metrics.detach())
+        fetch = _C.start_fetch(metrics.detach())
+        if curr_k is curr and loss.grad_fn is not None and curr.requires_grad:
+            # d(loss)/d(curr) is known now (grad_loss = 1): start the logits
+            # backward behind the metrics copy, before the host waits for it
+            from rl_amd.distributed.model_utils import launch_early_backward
+
+            launch_early_backward(curr, loss.grad_fn.grad_curr)
+        values = _C.finish_fetch(fetch)
         out = {k: float(values[_C.PG_METRIC_SLOTS[k]]) for k in self._metric_keys()}
         return loss, out
 
@@ -551,6 +558,7 @@ class _ClippedPGFunction(torch.autograd.Function):
             sample_mask, rewards, gvs, gvt, sc_args,
         )
         ctx.save_for_backward(grad_curr, grad_unf, grad_plog)
+        ctx.grad_curr = grad_curr  # d(loss)/d(curr) at grad_loss = 1, for launch_early_backward
         ctx.mark_non_differentiable(metrics)
         # no zero-filled gradient for the metrics output on the way back
         ctx.set_materialize_grads(False)

@@ -442,6 +442,66 @@ __global__ __launch_bounds__(256) void gather_fixup_kernel(
   gin[b * gisb + r * gisr + tl] = E::from_float(o);
 }
 
+// Early-backward check.  A caller that knows the upstream gradient in closed
+// form launches the logprob backward for it (`g_used`) before autograd asks
+// for it; when autograd does, bwd_check_kernel compares the real upstream
+// gradient with g_used bit for bit (one workgroup, no atomics: it writes the
+// flag outright), and bwd_redo_kernel recomputes the whole gradient from the
+// real one only when they differ (a scaled loss, a second consumer of the
+// logprobs).  Otherwise both launches are a few microseconds of GPU time.
+__global__ __launch_bounds__(1024) void bwd_check_kernel(const float* __restrict__ g, int64_t gsb,
+                                                         int64_t gsr, const float* __restrict__ g_used,
+                                                         int64_t B, int64_t R, int* __restrict__ flag) {
+  __shared__ int s_any[16];
+  int any = 0;
+  const int64_t n = B * R;
+  for (int64_t i = threadIdx.x; i < n; i += 1024) {
+    const int64_t b = i / R, r = i - b * R;
+    any |= (__float_as_uint(g[b * gsb + r * gsr]) != __float_as_uint(g_used[i])) ? 1 : 0;
+  }
+  const int wv = threadIdx.x / 64, lane = threadIdx.x % 64;
+  const bool w = __ballot(any != 0) != 0ull;
+  if (lane == 0) s_any[wv] = w ? 1 : 0;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int a = 0;
+    for (int k = 0; k < 16; ++k) a |= s_any[k];
+    *flag = a;
+  }
+}
+
+// Grid-stride recomputation of (onehot - p) * g over rows [0, B * Rt), run only
+// when the check flagged a difference (every workgroup returns at once
+// otherwise).  Same arithmetic as the other backward kernels.
+template <class E>
+__global__ __launch_bounds__(256) void bwd_redo_kernel(
+    const typename E::raw* __restrict__ logits, int64_t R, int64_t Rt, int64_t V, int64_t sb,
+    int64_t sr, const int64_t* __restrict__ target, int64_t tsb, int64_t tsr, int64_t vs,
+    int64_t ve, const float* __restrict__ stats, const float* __restrict__ g, int64_t gsb,
+    int64_t gsr, typename E::raw* gin, int64_t gisb, int64_t gisr, int64_t rows,
+    const int* __restrict__ flag) {
+  if (*flag == 0) return;
+  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+    const int64_t b = row / Rt, r = row - b * Rt;
+    typename E::raw* y = gin + b * gisb + r * gisr;
+    const float gv = (r < R) ? g[b * gsb + r * gsr] : 0.f;
+    if (gv == 0.f) {
+      for (int64_t j = threadIdx.x; j < V; j += 256) y[j] = E::from_float(0.f);
+      continue;
+    }
+    const typename E::raw* x = logits + b * sb + r * sr;
+    const int64_t srow = b * R + r;
+    const float M = stats[2 * srow], LS = stats[2 * srow + 1];
+    const int64_t t = target[b * tsb + r * tsr];
+    const bool tmask = (t < vs) || (t >= ve) || (t - vs >= V);
+    const int64_t tl = tmask ? -1 : (t - vs);
+    for (int64_t j = threadIdx.x; j < V; j += 256) {
+      const float p = fast_exp2(((E::load(x + j) - M) - LS) * kLog2e);
+      y[j] = E::from_float((j == tl) ? (1.f - p) * gv : -p * gv);
+    }
+  }
+}
+
 // Waves per row for the forward: at least 4 (fewer rows in flight at a time
 // keeps the concurrently streamed address window narrower, measured +5% read
 // bandwidth over one wave per row), more when there are too few rows to give
@@ -720,4 +780,54 @@ extern "C" int mirl_gather_logprob_bwd(const void* logits, int dtype, int64_t B,
       break;
   }
   return check_launch("mirl_gather_logprob_bwd");
+}
+
+extern "C" int mirl_logprob_bwd_recheck(const void* logits, int dtype, int64_t B, int64_t R,
+                                        int64_t R_total, int64_t V, int64_t stride_b,
+                                        int64_t stride_r, const int64_t* target,
+                                        int64_t t_stride_b, int64_t t_stride_r,
+                                        int64_t vocab_start, int64_t vocab_end,
+                                        const float* row_stats, const float* grad_out,
+                                        int64_t g_stride_b, int64_t g_stride_r,
+                                        const float* grad_used, void* grad_in,
+                                        int64_t gi_stride_b, int64_t gi_stride_r, int* flag,
+                                        void* stream) {
+  clear_error();
+  if (int e = check_dtype(dtype)) return e;
+  MIRL_REQUIRE(B >= 0 && R >= 0 && R_total >= R && V > 0,
+               "invalid shape B=%lld R=%lld R_total=%lld V=%lld", (long long)B, (long long)R,
+               (long long)R_total, (long long)V);
+  const int64_t rows = B * R_total;
+  if (rows == 0 || R == 0) return MIRL_OK;
+  MIRL_REQUIRE(rows < (int64_t(1) << 31), "too many rows (%lld)", (long long)rows);
+  MIRL_REQUIRE(logits && target && row_stats && grad_out && grad_used && grad_in && flag,
+               "null pointer argument");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(bwd_check_kernel, dim3(1), dim3(1024), 0, st, grad_out, g_stride_b,
+                     g_stride_r, grad_used, B, R, flag);
+  const unsigned grid = (unsigned)(rows < 4096 ? rows : 4096);
+  switch (dtype) {
+    case MIRL_DTYPE_F32:
+      hipLaunchKernelGGL((bwd_redo_kernel<F32>), dim3(grid), dim3(256), 0, st,
+                         static_cast<const float*>(logits), R, R_total, V, stride_b, stride_r,
+                         target, t_stride_b, t_stride_r, vocab_start, vocab_end, row_stats,
+                         grad_out, g_stride_b, g_stride_r, static_cast<float*>(grad_in),
+                         gi_stride_b, gi_stride_r, rows, flag);
+      break;
+    case MIRL_DTYPE_BF16:
+      hipLaunchKernelGGL((bwd_redo_kernel<BF16>), dim3(grid), dim3(256), 0, st,
+                         static_cast<const uint16_t*>(logits), R, R_total, V, stride_b, stride_r,
+                         target, t_stride_b, t_stride_r, vocab_start, vocab_end, row_stats,
+                         grad_out, g_stride_b, g_stride_r, static_cast<uint16_t*>(grad_in),
+                         gi_stride_b, gi_stride_r, rows, flag);
+      break;
+    default:
+      hipLaunchKernelGGL((bwd_redo_kernel<F16>), dim3(grid), dim3(256), 0, st,
+                         static_cast<const _Float16*>(logits), R, R_total, V, stride_b, stride_r,
+                         target, t_stride_b, t_stride_r, vocab_start, vocab_end, row_stats,
+                         grad_out, g_stride_b, g_stride_r, static_cast<_Float16*>(grad_in),
+                         gi_stride_b, gi_stride_r, rows, flag);
+      break;
+  }
+  return check_launch("mirl_logprob_bwd_recheck");
 }

@@ -147,10 +147,46 @@ class _RowLogprob(torch.autograd.Function):
         vs, ve = ctx.vocab
         if grad_output.dtype != torch.float32:
             grad_output = grad_output.float()
+        early = getattr(ctx, "early", None)
+        if early is not None:
+            # launched by launch_early_backward: check it against the real gradient
+            ctx.early = None
+            grad_input, grad_used = early
+            _C.logprob_bwd_recheck(logits, target, vs, ve, stats, grad_output, grad_used, grad_input)
+            return grad_input, None, None, None, None, None
         reuse = ctx.reuse_logits_storage and not logits.is_leaf
         grad_input = logits if reuse else torch.empty_like(logits)
         _C.logprob_bwd(logits, target, vs, ve, stats, grad_output, grad_input)
         return grad_input, None, None, None, None, None
+
+
+def launch_early_backward(logprobs: torch.Tensor, grad: torch.Tensor) -> bool:
+    """Start the logits backward of ``logprobs`` for the upstream gradient ``grad`` now.
+
+    For a consumer (the ClippedPG loss) that knows d(loss)/d(logprobs) in closed
+    form before autograd runs: the backward kernel is enqueued right away, ahead
+    of the host-side synchronisation on the loss's metrics and of autograd's own
+    bookkeeping, so the GPU does not wait for them.  When autograd later calls
+    the backward, a device-side check compares its real upstream gradient with
+    ``grad`` bit for bit and recomputes only if they differ (a scaled loss, a
+    second consumer of the logprobs), so results never depend on the guess.
+    Applies only to logprobs produced directly by this module's row kernel;
+    returns whether the backward was started.
+    """
+    fn = logprobs.grad_fn
+    if not isinstance(fn, _RowLogprob._backward_cls):
+        return False
+    if getattr(fn, "early", None) is not None or getattr(fn, "reuse_logits_storage", True):
+        return False
+    if grad.dtype != torch.float32 or tuple(grad.shape) != tuple(logprobs.shape):
+        return False
+    logits, target, stats = fn.saved_tensors
+    grad = grad.contiguous()
+    grad_input = torch.empty_like(logits)
+    vs, ve = fn.vocab
+    _C.logprob_bwd(logits, target, vs, ve, stats, grad, grad_input)
+    fn.early = (grad_input, grad)
+    return True
 
 
 class DistributedLogprob(torch.autograd.Function):
@@ -518,4 +554,6 @@ def get_next_token_logprobs_from_logits(
         sampling_params=sampling_params,
         chunk_size=chunk_size if use_chunking else None,
     )
+    if logprobs.shape[1] == input_ids.shape[1] - 1:
+        return logprobs  # the slice below would be the whole tensor
     return logprobs[:, : input_ids.shape[1] - 1]
