@@ -96,13 +96,15 @@ int mirl_logprob_bwd(const void* logits, int dtype, int64_t B, int64_t R,
  * Early-backward check for mirl_logprob_bwd.  A caller that launched
  * mirl_logprob_bwd for an upstream gradient `grad_used` (contiguous fp32
  * [B, R]) before the real upstream gradient `grad_out` was known passes both
- * here: one kernel compares them bit for bit and writes *flag (device int,
- * 1 = they differ); a second recomputes grad_in from grad_out when *flag is 1
- * and returns at once otherwise.  Arguments as for mirl_logprob_bwd.
+ * here: one kernel compares them bit for bit and writes `flag` (device ints,
+ * one per checking workgroup, at most MIRL_RECHECK_FLAGS; nonzero = they
+ * differ); a second recomputes grad_in from grad_out when any flag is set and
+ * returns at once otherwise.  Arguments as for mirl_logprob_bwd.
  *
  * Replaces: nothing in the reference (an ordering device: it lets the
  * backward start before the host has synchronised on the loss's metrics).
  */
+#define MIRL_RECHECK_FLAGS 64
 int mirl_logprob_bwd_recheck(const void* logits, int dtype, int64_t B, int64_t R,
                              int64_t R_total, int64_t V, int64_t stride_b,
                              int64_t stride_r, const int64_t* target,

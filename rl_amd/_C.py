@@ -471,7 +471,7 @@ def logprob_bwd_recheck(
     V = logits.shape[-1]
     assert grad_used.is_contiguous() and tuple(grad_used.shape) == (B, R)
     assert grad_out.dtype == torch.float32 and grad_used.dtype == torch.float32
-    flag = torch.empty(1, dtype=torch.int32, device=dev)
+    flag = torch.empty(64, dtype=torch.int32, device=dev)  # MIRL_RECHECK_FLAGS
     st = _launch(
         "mirl_logprob_bwd_recheck", dev,
         logits.data_ptr(), _dtype_code(logits), B, R, Rt, V, logits.stride(0), logits.stride(1),

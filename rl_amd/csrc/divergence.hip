@@ -291,26 +291,30 @@ __device__ __forceinline__ float div_grad(float xs, float xt, float M, float log
 }
 
 // Flat backward over contiguous [rows, V] student / teacher / gradient arrays
-// with whole 16-byte vectors per row: one 8 KB piece of the gradient per
-// workgroup (two vectors per lane, 4 KB apart), piece boundaries on 4 KB
-// gradient addresses.
+// with whole 16-byte vectors per row: one 4 KB piece of the gradient per
+// 128-thread workgroup (two vectors per lane, 2 KB apart), piece boundaries on
+// 4 KB gradient addresses, nontemporal loads and stores (reverse KL on bf16
+// [8, 2048, 151936]: 1.59 ms, against 1.67 ms for 8 KB pieces of 256 threads
+// with plain loads).
+constexpr int kDivFlatThreads = 128;
+
 template <class E, int KIND>
-__global__ __launch_bounds__(256) void divergence_bwd_flat_kernel(
+__global__ __launch_bounds__(kDivFlatThreads) void divergence_bwd_flat_kernel(
     const typename E::raw* __restrict__ xs, const typename E::raw* __restrict__ xt, uint32_t nvr,
     uint32_t nvec, int shift, const float* __restrict__ Lrow, const float* __restrict__ stats,
     const float* __restrict__ g, int64_t R, int64_t gsb, int64_t gsr, typename E::raw* gin) {
   constexpr bool kTeacher = DivTraits<KIND>::kTeacher;
   constexpr int VEC = E::kVec;
-  constexpr int U = 2;
+  constexpr int NT = kDivFlatThreads, U = 2;
   vu4* yv = reinterpret_cast<vu4*>(gin);
   const vu4* xv = reinterpret_cast<const vu4*>(xs);
   const vu4* tv = reinterpret_cast<const vu4*>(xt);
-  const int64_t base = (int64_t)blockIdx.x * (256 * U) + threadIdx.x - shift;
+  const int64_t base = (int64_t)blockIdx.x * (NT * U) + threadIdx.x - shift;
   bool ok[U];
   float gv[U], M[U], LZ[U], Mt[U], LZt[U], L[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    const int64_t i = base + u * 256;
+    const int64_t i = base + u * NT;
     ok[u] = i >= 0 && i < (int64_t)nvec;
     const uint32_t row = (ok[u] ? (uint32_t)i : 0u) / nvr;
     gv[u] = M[u] = LZ[u] = Mt[u] = LZt[u] = L[u] = 0.f;
@@ -329,14 +333,14 @@ __global__ __launch_bounds__(256) void divergence_bwd_flat_kernel(
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     if (ok[u] && gv[u] != 0.f) {
-      q[u] = xv[base + u * 256];
-      if constexpr (kTeacher) qt[u] = tv[base + u * 256];
+      q[u] = __builtin_nontemporal_load(xv + base + u * NT);
+      if constexpr (kTeacher) qt[u] = __builtin_nontemporal_load(tv + base + u * NT);
     }
   }
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     if (!ok[u]) continue;
-    const int64_t i = base + u * 256;
+    const int64_t i = base + u * NT;
     if (gv[u] == 0.f) {
       __builtin_nontemporal_store(vu4{0u, 0u, 0u, 0u}, yv + i);
       continue;
@@ -457,12 +461,13 @@ void dispatch_bwd(int64_t rows, hipStream_t st, const void* xs, const void* xt, 
   if (V % VEC == 0 && contig && (ya & 15u) == 0 && (xa & 15u) == 0 &&
       (!kTeacher || (ta & 15u) == 0) && nvec + 512 < (int64_t(1) << 32)) {
     const int to4k = (int)(((4096u - (ya & 4095u)) & 4095u) / 16u);
-    const int shift = (256 - to4k) & 255;
-    const int64_t grid = (nvec + shift + 511) / 512;
-    hipLaunchKernelGGL((divergence_bwd_flat_kernel<E, KIND>), dim3((unsigned)grid), dim3(256), 0,
-                       st, static_cast<const raw*>(xs), static_cast<const raw*>(xt),
-                       (uint32_t)nvr, (uint32_t)nvec, shift, L, stats, g, R, gsb, gsr,
-                       static_cast<raw*>(gin));
+    constexpr int P = kDivFlatThreads * 2;  // vectors per 4 KB piece
+    const int shift = (P - to4k) & (P - 1);
+    const int64_t grid = (nvec + shift + P - 1) / P;
+    hipLaunchKernelGGL((divergence_bwd_flat_kernel<E, KIND>), dim3((unsigned)grid),
+                       dim3(kDivFlatThreads), 0, st, static_cast<const raw*>(xs),
+                       static_cast<const raw*>(xt), (uint32_t)nvr, (uint32_t)nvec, shift, L, stats,
+                       g, R, gsb, gsr, static_cast<raw*>(gin));
     return;
   }
   hipLaunchKernelGGL((divergence_bwd_row_kernel<E, KIND>), dim3((unsigned)rows), dim3(256), 0, st,

@@ -317,33 +317,39 @@ __global__ __launch_bounds__(64 * W) void logprob_bwd_kernel(
 }
 
 // Backward over a contiguous [B, Rt, V] gradient whose logits share its layout
-// (V a multiple of the vector width, both 16-byte aligned): one 8 KB block of
-// the flat gradient per workgroup (two 16-byte vectors per lane, 4 KB apart),
-// block boundaries on 4 KB addresses.  Each lane finds the rows of its two
-// vectors and loads their upstream gradient, statistics and target together;
-// vectors of rows with a zero upstream gradient are written as zeros without
-// reading the logits, the others get (onehot - p) * g.  Short workgroups
-// dispatched in order keep the traffic inside a narrow address window:
-// measured 6.27 TB/s on the GRPO rows, against 5.4 for one workgroup per row.
-// Arithmetic is that of logprob_bwd_kernel.
+// (V a multiple of the vector width, both 16-byte aligned): one 4 KB piece of
+// the flat gradient per 128-thread workgroup (two 16-byte vectors per lane,
+// 2 KB apart), piece boundaries on 4 KB addresses.  Each lane finds the rows
+// of its two vectors and loads their upstream gradient, statistics and target
+// together; vectors of rows with a zero upstream gradient are written as zeros
+// without reading the logits, the others get (onehot - p) * g.  Short
+// workgroups dispatched in order keep the traffic inside a narrow address
+// window.  Measured on MI355X (backward of the [8, 2048, 151936] GRPO rows /
+// of the [1, 32768, 131072] rows): 128 x 2 vectors with nontemporal loads
+// 1.198 / 2.722 ms; 256 x 2 with plain loads 1.231 / 2.849 ms; one vector per
+// lane (the per-vector row lookups dominate) 1.34-1.45 / 3.07-3.19 ms; 256 x 4
+// and 512 x 2 1.30-1.34 / 2.92 ms.  Arithmetic is that of logprob_bwd_kernel.
+constexpr int kFlatThreads = 128;
+constexpr int kFlatVecs = 2;
+
 template <class E>
-__global__ __launch_bounds__(256) void logprob_bwd_flat_kernel(
+__global__ __launch_bounds__(kFlatThreads) void logprob_bwd_flat_kernel(
     const typename E::raw* __restrict__ logits, int64_t R, uint32_t Rt, uint32_t nvr,
     uint32_t nvec, int shift, const int64_t* __restrict__ target, int64_t tsb, int64_t tsr,
     int64_t vs, int64_t ve, int64_t V, const float* __restrict__ stats,
     const float* __restrict__ g, int64_t gsb, int64_t gsr, typename E::raw* gin) {
   constexpr int VEC = E::kVec;
-  constexpr int U = 2;
+  constexpr int NT = kFlatThreads, U = kFlatVecs;
   vu4* yv = reinterpret_cast<vu4*>(gin);
   const vu4* xv = reinterpret_cast<const vu4*>(logits);
-  const int64_t base = (int64_t)blockIdx.x * (256 * U) + threadIdx.x - shift;
+  const int64_t base = (int64_t)blockIdx.x * (NT * U) + threadIdx.x - shift;
   bool ok[U];
   uint32_t row[U];
   float gv[U], M[U], LS[U];
   int64_t t[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    const int64_t i = base + u * 256;
+    const int64_t i = base + u * NT;
     ok[u] = i >= 0 && i < (int64_t)nvec;
     row[u] = (ok[u] ? (uint32_t)i : 0u) / nvr;
     const uint32_t b = row[u] / Rt, r = row[u] - b * Rt;
@@ -358,17 +364,17 @@ __global__ __launch_bounds__(256) void logprob_bwd_flat_kernel(
       t[u] = target[(int64_t)b * tsb + (int64_t)r * tsr];
     }
   }
-  // Plain loads here, nontemporal stores below: on the GRPO rows a nontemporal
-  // load costs 3% (1.25 vs 1.22 ms) and changes nothing for the next forward,
-  // while plain stores slow both this kernel and the next forward by ~15%.
+  // Nontemporal loads and stores: with 4 KB pieces the streaming loads measured
+  // 2-4% faster than plain ones, and plain stores slow both this kernel and the
+  // next forward by ~15% (they leave the memory-side cache full of dirty lines).
   vu4 q[U];
 #pragma unroll
   for (int u = 0; u < U; ++u)
-    if (ok[u] && gv[u] != 0.f) q[u] = xv[base + u * 256];
+    if (ok[u] && gv[u] != 0.f) q[u] = __builtin_nontemporal_load(xv + base + u * NT);
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     if (!ok[u]) continue;
-    const int64_t i = base + u * 256;
+    const int64_t i = base + u * NT;
     if (gv[u] == 0.f) {
       // (onehot - p) * 0 == 0: written without reading the logits
       __builtin_nontemporal_store(vu4{0u, 0u, 0u, 0u}, yv + i);
@@ -445,17 +451,24 @@ __global__ __launch_bounds__(256) void gather_fixup_kernel(
 // Early-backward check.  A caller that knows the upstream gradient in closed
 // form launches the logprob backward for it (`g_used`) before autograd asks
 // for it; when autograd does, bwd_check_kernel compares the real upstream
-// gradient with g_used bit for bit (one workgroup, no atomics: it writes the
-// flag outright), and bwd_redo_kernel recomputes the whole gradient from the
-// real one only when they differ (a scaled loss, a second consumer of the
+// gradient with g_used bit for bit (up to kCheckBlocks workgroups, each writing
+// its own flag), and bwd_redo_kernel recomputes the whole gradient from the
+// real one only when some flag is set (a scaled loss, a second consumer of the
 // logprobs).  Otherwise both launches are a few microseconds of GPU time.
-__global__ __launch_bounds__(1024) void bwd_check_kernel(const float* __restrict__ g, int64_t gsb,
-                                                         int64_t gsr, const float* __restrict__ g_used,
-                                                         int64_t B, int64_t R, int* __restrict__ flag) {
-  __shared__ int s_any[16];
+// Each workgroup compares a contiguous share of the [B, R] gradients and
+// writes its own flag slot outright (no atomics, nothing to clear first).
+constexpr int kCheckBlocks = 64;
+
+__global__ __launch_bounds__(256) void bwd_check_kernel(const float* __restrict__ g, int64_t gsb,
+                                                        int64_t gsr, const float* __restrict__ g_used,
+                                                        int64_t B, int64_t R, int* __restrict__ flags) {
+  __shared__ int s_any[4];
   int any = 0;
   const int64_t n = B * R;
-  for (int64_t i = threadIdx.x; i < n; i += 1024) {
+  const int64_t per = (n + gridDim.x - 1) / gridDim.x;
+  const int64_t i0 = (int64_t)blockIdx.x * per;
+  const int64_t i1 = (i0 + per < n) ? i0 + per : n;
+  for (int64_t i = i0 + threadIdx.x; i < i1; i += 256) {
     const int64_t b = i / R, r = i - b * R;
     any |= (__float_as_uint(g[b * gsb + r * gsr]) != __float_as_uint(g_used[i])) ? 1 : 0;
   }
@@ -463,11 +476,7 @@ __global__ __launch_bounds__(1024) void bwd_check_kernel(const float* __restrict
   const bool w = __ballot(any != 0) != 0ull;
   if (lane == 0) s_any[wv] = w ? 1 : 0;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    int a = 0;
-    for (int k = 0; k < 16; ++k) a |= s_any[k];
-    *flag = a;
-  }
+  if (threadIdx.x == 0) flags[blockIdx.x] = s_any[0] | s_any[1] | s_any[2] | s_any[3];
 }
 
 // Grid-stride recomputation of (onehot - p) * g over rows [0, B * Rt), run only
@@ -479,8 +488,10 @@ __global__ __launch_bounds__(256) void bwd_redo_kernel(
     int64_t sr, const int64_t* __restrict__ target, int64_t tsb, int64_t tsr, int64_t vs,
     int64_t ve, const float* __restrict__ stats, const float* __restrict__ g, int64_t gsb,
     int64_t gsr, typename E::raw* gin, int64_t gisb, int64_t gisr, int64_t rows,
-    const int* __restrict__ flag) {
-  if (*flag == 0) return;
+    const int* __restrict__ flags, int nflags) {
+  int any = 0;
+  for (int k = 0; k < nflags; ++k) any |= flags[k];
+  if (any == 0) return;
   for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
     const int64_t b = row / Rt, r = row - b * Rt;
     typename E::raw* y = gin + b * gisb + r * gisr;
@@ -578,10 +589,11 @@ void dispatch_bwd(int64_t rows, hipStream_t st, const void* logits, int64_t R, i
   const int64_t nvec = rows * nvr;
   if (V % VEC == 0 && contiguous && shared_layout && (ya & 15u) == 0 && (xa & 15u) == 0 &&
       nvec + 512 < (int64_t(1) << 32) && rows < (int64_t(1) << 31)) {
+    constexpr int P = kFlatThreads * kFlatVecs;  // vectors per 4 KB piece
     const int to4k = (int)(((4096u - (ya & 4095u)) & 4095u) / 16u);  // vectors before a 4 KB boundary
-    const int shift = (256 - to4k) & 255;
-    const int64_t grid = (nvec + shift + 511) / 512;
-    hipLaunchKernelGGL((logprob_bwd_flat_kernel<E>), dim3((unsigned)grid), dim3(256), 0, st,
+    const int shift = (P - to4k) & (P - 1);
+    const int64_t grid = (nvec + shift + P - 1) / P;
+    hipLaunchKernelGGL((logprob_bwd_flat_kernel<E>), dim3((unsigned)grid), dim3(kFlatThreads), 0, st,
                        static_cast<const raw*>(logits), R, (uint32_t)Rt, (uint32_t)nvr,
                        (uint32_t)nvec, shift, target, tsb, tsr, vs, ve, V, stats, g, gsb, gsr,
                        static_cast<raw*>(gin));
@@ -803,30 +815,32 @@ extern "C" int mirl_logprob_bwd_recheck(const void* logits, int dtype, int64_t B
   MIRL_REQUIRE(logits && target && row_stats && grad_out && grad_used && grad_in && flag,
                "null pointer argument");
   hipStream_t st = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(bwd_check_kernel, dim3(1), dim3(1024), 0, st, grad_out, g_stride_b,
-                     g_stride_r, grad_used, B, R, flag);
-  const unsigned grid = (unsigned)(rows < 4096 ? rows : 4096);
+  const int64_t n = B * R;
+  const int nflags = (int)(n < kCheckBlocks ? n : kCheckBlocks);
+  hipLaunchKernelGGL(bwd_check_kernel, dim3((unsigned)nflags), dim3(256), 0, st, grad_out,
+                     g_stride_b, g_stride_r, grad_used, B, R, flag);
+  const unsigned grid = (unsigned)(rows < 1024 ? rows : 1024);
   switch (dtype) {
     case MIRL_DTYPE_F32:
       hipLaunchKernelGGL((bwd_redo_kernel<F32>), dim3(grid), dim3(256), 0, st,
                          static_cast<const float*>(logits), R, R_total, V, stride_b, stride_r,
                          target, t_stride_b, t_stride_r, vocab_start, vocab_end, row_stats,
                          grad_out, g_stride_b, g_stride_r, static_cast<float*>(grad_in),
-                         gi_stride_b, gi_stride_r, rows, flag);
+                         gi_stride_b, gi_stride_r, rows, flag, nflags);
       break;
     case MIRL_DTYPE_BF16:
       hipLaunchKernelGGL((bwd_redo_kernel<BF16>), dim3(grid), dim3(256), 0, st,
                          static_cast<const uint16_t*>(logits), R, R_total, V, stride_b, stride_r,
                          target, t_stride_b, t_stride_r, vocab_start, vocab_end, row_stats,
                          grad_out, g_stride_b, g_stride_r, static_cast<uint16_t*>(grad_in),
-                         gi_stride_b, gi_stride_r, rows, flag);
+                         gi_stride_b, gi_stride_r, rows, flag, nflags);
       break;
     default:
       hipLaunchKernelGGL((bwd_redo_kernel<F16>), dim3(grid), dim3(256), 0, st,
                          static_cast<const _Float16*>(logits), R, R_total, V, stride_b, stride_r,
                          target, t_stride_b, t_stride_r, vocab_start, vocab_end, row_stats,
                          grad_out, g_stride_b, g_stride_r, static_cast<_Float16*>(grad_in),
-                         gi_stride_b, gi_stride_r, rows, flag);
+                         gi_stride_b, gi_stride_r, rows, flag, nflags);
       break;
   }
   return check_launch("mirl_logprob_bwd_recheck");
