@@ -13,11 +13,16 @@
 // tiles of a row.  The gradient kernel recomputes a logits tile and writes the
 // bf16 G tile (the two GEMMs that consume G are plain library GEMMs).
 //
-// Tile: 256 rows x 256 columns per 256-thread workgroup, K in steps of 64,
-// two LDS stages of 64 KB.  Each wave owns a 128 x 128 quarter as 4 x 4
-// v_mfma_f32_32x32x16_bf16 tiles (256 fp32 accumulators per lane).  LDS rows are
-// 128 B with their 16-byte chunks XOR-swizzled (see lds_off), so the rows read
-// by one MFMA operand load fall in distinct banks.
+// Tile: 256 rows x 256 columns per 256-thread workgroup.  Each wave owns a
+// 128 x 128 quarter as 4 x 4 v_mfma_f32_32x32x16_bf16 tiles (256 fp32
+// accumulators per lane).  The hidden dimension streams through two LDS stages
+// of 64 elements (64 KB each: 256 rows of H and 256 rows of W, 128 B per row),
+// filled by direct global->LDS loads (buffer_load_dwordx4 ... lds) one stage
+// ahead of the MFMAs: no staging registers and no LDS store instructions sit
+// between the loads and the MFMAs, and the only waits are one vmcnt + barrier
+// per stage.  Each row of a stage is one 128-byte line of H or W.  A row's
+// eight 16-byte chunks are XOR-swizzled by (row / 2) % 8 (see lds_off), so the
+// 16 rows read by one pass of an MFMA operand load fall in distinct banks.
 //
 // MFMA 32x32x16 bf16 lane layout (checked on gfx950): lane l holds A[l % 32][k]
 // and B[k][l % 32] for k = (l / 32) * 8 + 0..7; accumulator element v of lane l
@@ -34,32 +39,52 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 constexpr int kBM = 256;                 // rows per tile
 constexpr int kBN = 256;                 // vocabulary columns per tile
-constexpr int kBK = 64;                  // hidden elements per K step
+constexpr int kSK = 64;                  // hidden elements per LDS stage
+constexpr int kStages = 2;
 constexpr int kThreads = 256;            // 4 waves in a 2 x 2 arrangement
+constexpr int kWaves = kThreads / kWave;
 constexpr int kWM = 128, kWN = 128;      // per-wave quarter
 constexpr int kTM = kWM / 32, kTN = kWN / 32;
-constexpr int kRowBytes = kBK * 2;       // one tile row in LDS
-constexpr int kStageBytes = (kBM + kBN) * kRowBytes;
-constexpr int kLoadsPerThread = kBM * kRowBytes / 16 / kThreads;  // 16-byte chunks of A (and of B)
-constexpr int kGroupM = 4;               // row tiles sharing a sweep over the vocabulary
+constexpr int kRowBytes = kSK * 2;       // 128 B: one tile row of a stage
+constexpr int kHalfBytes = kBM * kRowBytes;    // 32 KB: the H (or W) rows of a stage
+constexpr int kStageBytes = 2 * kHalfBytes;    // 64 KB
+constexpr int kDmaBytes = kWave * 16;          // one direct load: 64 lanes x 16 B = 8 rows
+constexpr int kDmaRows = kDmaBytes / kRowBytes;
+constexpr int kDmaPerWave = kHalfBytes / kDmaBytes / kWaves;  // loads of H (and of W) per wave and stage
+constexpr int kEpiRows = kStageBytes / (kBN * 2);  // epilogue tile rows held by one stage array
+constexpr int kGroupM = 8;               // row tiles sharing a sweep over the vocabulary
 constexpr int kXcds = 8;                 // accelerator dies, each with its own L2
+static_assert(kBM == kBN, "H and W halves of a stage have the same size");
+static_assert(kEpiRows * kStages == kBM, "the epilogue tile fills the stage arrays");
+static_assert(kEpiRows == kWM, "a wave's epilogue rows live in one stage array");
 
-// LDS byte offset of 16-byte chunk `chunk` of tile row `row`.  A ds_read_b128
-// serves 16 lanes per pass (16 x 16 B = the 64 four-byte banks); an MFMA
-// operand read has those lanes on 16 consecutive rows at one chunk, so the
-// chunk is XOR-ed with (row / 2) % 8: the 8 even and the 8 odd rows then each
-// hit 8 distinct chunks, i.e. 16 distinct bank groups.
+// LDS byte offset (within a stage half) of 16-byte chunk `chunk` of tile row
+// `row`.  A ds_read_b128 serves 16 lanes per pass (16 x 16 B = the 64
+// four-byte banks); an MFMA operand read has those lanes on 16 consecutive rows
+// at one chunk.  Two 128-byte rows span the 64 banks, so the chunk is XOR-ed
+// with (row / 2) % 8: the 8 even and the 8 odd rows then each hit 8 distinct
+// chunks, i.e. 16 distinct bank groups.
 __device__ __forceinline__ int lds_off(int row, int chunk) {
   return row * kRowBytes + ((chunk ^ ((row >> 1) & 7)) << 4);
 }
 
-// Epilogue layout of a [256][256] bf16 tile in LDS: row-major, 16-byte chunks
-// XOR-swizzled by row % 32 (element index).
+// Epilogue layout of the [256][256] bf16 tile: row r lives in stage array
+// r / 128 at local row r % 128, row-major, 16-byte chunks XOR-swizzled by
+// r % 32 (element index within the array).
 __device__ __forceinline__ int xs_index(int row, int col) {
-  return row * kBN + ((((col >> 3) ^ (row & 31)) << 3) | (col & 7));
+  return (row & (kEpiRows - 1)) * kBN + ((((col >> 3) ^ (row & 31)) << 3) | (col & 7));
+}
+
+// s_waitcnt vmcnt(N) lgkmcnt(0), then s_barrier.  The memory clobber keeps the
+// compiler from moving LDS accesses across the barrier.
+template <int N>
+__device__ __forceinline__ void wait_vm_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
 __device__ __forceinline__ float bf16_round(float f) {
@@ -93,15 +118,19 @@ struct LceParams {
 template <int MODE>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void lce_tile_kernel(LceParams P) {
-  __shared__ __align__(16) unsigned char lds[2 * kStageBytes];
+  // Two arrays rather than one, so that the compiler tracks the direct loads
+  // into each stage on their own and an LDS read waits only for its stage.
+  __shared__ __align__(1024) unsigned char st0[kStageBytes];
+  __shared__ __align__(1024) unsigned char st1[kStageBytes];
   __shared__ int s_tcol[kBM];
   __shared__ float s_m[kBM], s_ls[kBM], s_g[kBM];
+  auto stage_ptr = [&](int s) -> unsigned char* { return s == 0 ? st0 : st1; };
 
   // Tile order.  Workgroups are dispatched to the 8 XCDs round-robin
   // (XCD = blockIdx % 8) and each XCD has its own L2, so each XCD takes one
   // contiguous run of a grouped order (kGroupM row tiles sweep the vocabulary
   // together): the ~32 workgroups resident on an XCD then cover about
-  // kGroupM row tiles x 8 column tiles and share their H and W reads in L2.
+  // kGroupM row tiles x 4 column tiles and share their H and W reads in L2.
   const int64_t ntiles = P.n_mt * P.n_nt;
   const int64_t per_xcd = (ntiles + kXcds - 1) / kXcds;
   const int64_t gi = (int64_t)(blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
@@ -172,47 +201,51 @@ void lce_tile_kernel(LceParams P) {
 
   // ---- main loop: acc = H[m0 : m0+256] . W[n0 : n0+256]^T ----
   //
-  // Global -> register loads go through buffer resources covering the tile's
-  // valid rows, so rows past the end of H or W read as zero with no branch.
-  // Thread t moves the 16-byte chunk (t & 7) of rows (t >> 3) + 32 j, j < 8,
-  // of both operands; its LDS slot is fixed up to the row offset 32 j * 128.
+  // Direct loads go through buffer resources covering the tile's valid rows.
+  // The row offset is in the VGPR offset, which the range check covers, so rows
+  // past the end of H or W read as zero with no branch; the SGPR offset carries
+  // only the stage's hidden offset, which stays inside a valid row.
   //
-  // One K step (64 hidden elements) is four MFMA blocks kk = 0..3 of 16
-  // MFMAs.  While block kk runs, the operand fragments of block kk + 1 are read
-  // from LDS into the other fragment set; staged global loads are written to
-  // the other LDS stage during block 2; the step's barrier comes before block
-  // 3, whose MFMAs then cover the LDS reads of the next step's block 0.
-  // sched_barrier fences keep that order.
-  const int nk = (int)(P.Hd / kBK);
+  // One direct load moves 8 rows x 128 B: lane l writes LDS bytes
+  // [16 l, 16 l + 16) of the load's 1 KB block, i.e. row l / 8, slot l % 8, so
+  // it fetches global chunk (l % 8) ^ ((row / 2) % 8) of that row (the inverse
+  // of the lds_off swizzle).  Each wave issues kDmaPerWave loads of H and of W
+  // per stage.
+  const int nst = (int)(P.Hd / kSK);  // a multiple of kStages
   const int64_t a_rows = (row_end - m0 < kBM) ? (row_end - m0) : kBM;
   const int64_t b_rows = (P.V - n0 < kBN) ? (P.V - n0) : kBN;
   const __amdgpu_buffer_rsrc_t rsrc_a = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(P.h + m0 * P.ldh), 0, (int)(a_rows * P.ldh * 2), 0x00020000);
   const __amdgpu_buffer_rsrc_t rsrc_b = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(P.w + n0 * P.ldw), 0, (int)(b_rows * P.ldw * 2), 0x00020000);
-  const int ld_row = tid >> 3, ld_chunk = tid & 7;
-  const int voff_a = (int)((ld_row * P.ldh + ld_chunk * 8) * 2);
-  const int voff_b = (int)((ld_row * P.ldw + ld_chunk * 8) * 2);
-  const int jstride_a = (int)(32 * P.ldh * 2), jstride_b = (int)(32 * P.ldw * 2);
-  const int st_off = lds_off(ld_row, ld_chunk);  // + j * 32 rows
-
-  // Two staging register sets: the data of step m lives in set m % 2.
-  vu4 ra[2][kLoadsPerThread], rb[2][kLoadsPerThread];
-  auto gload_one = [&](int set, int kt, int j) {
-    const int k_bytes = kt * kBK * 2;
-    ra[set][j] = __builtin_bit_cast(vu4, __builtin_amdgcn_raw_buffer_load_b128(rsrc_a, voff_a, j * jstride_a + k_bytes, 0));
-    rb[set][j] = __builtin_bit_cast(vu4, __builtin_amdgcn_raw_buffer_load_b128(rsrc_b, voff_b, j * jstride_b + k_bytes, 0));
-  };
-  auto sstore_one = [&](int set, unsigned char* base, int j) {
-    *reinterpret_cast<vu4*>(base + st_off + j * 32 * kRowBytes) = ra[set][j];
-    *reinterpret_cast<vu4*>(base + kBM * kRowBytes + st_off + j * 32 * kRowBytes) = rb[set][j];
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  int voff_a[kDmaPerWave], voff_b[kDmaPerWave];
+#pragma unroll
+  for (int i = 0; i < kDmaPerWave; ++i) {
+    const int row = (wave * kDmaPerWave + i) * kDmaRows + (lane >> 3);
+    const int chunk = (lane & 7) ^ ((row >> 1) & 7);
+    voff_a[i] = (int)(row * P.ldh * 2) + chunk * 16;
+    voff_b[i] = (int)(row * P.ldw * 2) + chunk * 16;
+  }
+  // load q of stage data t: q < kDmaPerWave is an H block, else a W block
+  auto dma = [&](unsigned char* stage, int t, int q) {
+    const int soff = t * kRowBytes;
+    if (q < kDmaPerWave) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rsrc_a, (lds_ptr_t)(stage + (wave_u * kDmaPerWave + q) * kDmaBytes), 16, voff_a[q], soff, 0, 0);
+    } else {
+      const int qb = q - kDmaPerWave;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rsrc_b, (lds_ptr_t)(stage + kHalfBytes + (wave_u * kDmaPerWave + qb) * kDmaBytes), 16,
+          voff_b[qb], soff, 0, 0);
+    }
   };
 
   // fragment read offsets: row (wm*128 | wn*128) + i*32 + (lane & 31), chunk kk*2 + (lane >> 5)
   const int frow = lane & 31;
-  int frag_off[kBK / 16];
+  int frag_off[kSK / 16];
 #pragma unroll
-  for (int kk = 0; kk < kBK / 16; ++kk) frag_off[kk] = lds_off(frow, kk * 2 + (lane >> 5));
+  for (int kk = 0; kk < kSK / 16; ++kk) frag_off[kk] = lds_off(frow, kk * 2 + (lane >> 5));
   bf16x8 fa[2][kTM], fb[2][kTN];
   auto fread = [&](int set, const unsigned char* stage, int kk, int idx) {
     // idx < kTM: A fragment idx; else B fragment idx - kTM
@@ -220,7 +253,7 @@ void lce_tile_kernel(LceParams P) {
       fa[set][idx] = *reinterpret_cast<const bf16x8*>(stage + (wm * kWM + idx * 32) * kRowBytes + frag_off[kk]);
     else
       fb[set][idx - kTM] = *reinterpret_cast<const bf16x8*>(
-          stage + kBM * kRowBytes + (wn * kWN + (idx - kTM) * 32) * kRowBytes + frag_off[kk]);
+          stage + kHalfBytes + (wn * kWN + (idx - kTM) * 32) * kRowBytes + frag_off[kk]);
   };
 
   f32x16 acc[kTM][kTN];
@@ -235,92 +268,82 @@ void lce_tile_kernel(LceParams P) {
     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[set][i], fb[set][j], acc[i][j], 0, 0, 0);
   };
 
-  // Prologue: step 0 into LDS stage 0, step 1's loads in flight, block 0's fragments.
+  constexpr int kL = 2 * kDmaPerWave;  // direct loads per wave and stage
+  // Prologue: stage data 0 and 1 in flight; wait for 0 and read its block-0 fragments.
 #pragma unroll
-  for (int j = 0; j < kLoadsPerThread; ++j) gload_one(0, 0, j);
+  for (int q = 0; q < kL; ++q) dma(st0, 0, q);
 #pragma unroll
-  for (int j = 0; j < kLoadsPerThread; ++j) sstore_one(0, lds, j);
-  if (nk > 1) {
+  for (int q = 0; q < kL; ++q) dma(st1, 1, q);
+  wait_vm_barrier<kL>();
 #pragma unroll
-    for (int j = 0; j < kLoadsPerThread; ++j) gload_one(1, 1, j);
-  }
-  __syncthreads();
-#pragma unroll
-  for (int idx = 0; idx < kTM + kTN; ++idx) fread(0, lds, 0, idx);
+  for (int idx = 0; idx < kTM + kTN; ++idx) fread(0, st0, 0, idx);
 
-  // One K step kt (PAR = kt % 2).  Step kt + 2's loads go into staging set PAR
-  // (free since step kt's data went to LDS one step earlier), two pairs per
-  // block, a step or more before they are written; blocks 1 and 2 write step
-  // kt + 1's data (set PAR ^ 1) to the other LDS stage, one chunk pair every 4
-  // MFMAs; block 3 reads the next step's block-0 fragments after the barrier.
-  // Spreading the loads and writes keeps the address and LDS data queues from
-  // filling, which would stall the single wave of the SIMD and with it the
-  // MFMAs queued behind.  Every read of the current stage happens before the
-  // step's barrier; the next write into it (step kt + 2's data) comes in the
-  // next step's block 1.
-  auto step = [&](int kt, auto par_c, auto next_c, auto load_c) {
-    constexpr int PAR = decltype(par_c)::value;
+  // One stage t (S = t % 2): four MFMA blocks kk = 0..3 of 16 MFMAs (16 hidden
+  // elements each).  While block kk runs on fragment set kk % 2, block kk + 1's
+  // fragments are read into the other set.  Before block 3 this wave waits for
+  // its loads of stage data t + 1 (the only ones in flight) and the workgroup
+  // barrier makes every wave's loads visible and ends every read of stage S
+  // (block 3's fragments were read during block 2).  Block 3 then reads the
+  // next stage's block-0 fragments and issues the direct loads of stage data
+  // t + 2 into stage S: a full stage ahead of their use.
+  auto step = [&](int t, auto s_c, auto next_c, auto load_c) {
+    constexpr int S = decltype(s_c)::value;
     constexpr bool NEXT = decltype(next_c)::value;
     constexpr bool LOAD = decltype(load_c)::value;
-    const unsigned char* cur = lds + PAR * kStageBytes;
-    unsigned char* nxt = lds + (PAR ^ 1) * kStageBytes;
+    unsigned char* cur = stage_ptr(S);
+    const unsigned char* nxt = stage_ptr(S ^ 1);
 #pragma unroll
     for (int kk = 0; kk < 3; ++kk) {
-      const int set = kk & 1;
 #pragma unroll
       for (int q = 0; q < kTM * kTN; ++q) {
-        mfma(set, q);
-        if (q < kTM + kTN) fread(set ^ 1, cur, kk + 1, q);
-        if constexpr (LOAD) {
-          if ((q & 7) == 0) gload_one(PAR, kt + 2, kk * 2 + (q >> 3));
-        }
-        if constexpr (NEXT) {
-          if (kk >= 1 && (q & 3) == 0) sstore_one(PAR ^ 1, nxt, (kk - 1) * 4 + (q >> 2));
-        }
+        mfma(kk & 1, q);
+        if (q < kTM + kTN) fread((kk + 1) & 1, cur, kk + 1, q);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    __syncthreads();
+    if constexpr (NEXT) wait_vm_barrier<0>();
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int q = 0; q < kTM * kTN; ++q) {
       mfma(1, q);
       if constexpr (NEXT) {
         if (q < kTM + kTN) fread(0, nxt, 0, q);
       }
-      if constexpr (LOAD) {
-        if ((q & 7) == 0) gload_one(PAR, kt + 2, 6 + (q >> 3));
-      }
+      if constexpr (LOAD) dma(cur, t + 2, q);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
-  using I0 = std::integral_constant<int, 0>;
-  using I1 = std::integral_constant<int, 1>;
+  static_assert(kL == kTM * kTN, "one direct load per MFMA of block 3");
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
   using T_ = std::integral_constant<bool, true>;
   using F_ = std::integral_constant<bool, false>;
-  // nk is even (the hidden size is a multiple of 2 * kBK): pairs of steps,
-  // then the last pair without the loads that would run past the end.
-  int kt = 0;
-  for (; kt + 2 < nk; kt += 2) {
-    step(kt, I0{}, T_{}, T_{});
-    step(kt + 1, I1{}, T_{}, T_{});
+  int t = 0;
+  for (; t < nst - kStages; t += kStages) {
+    step(t, S0{}, T_{}, T_{});
+    step(t + 1, S1{}, T_{}, T_{});
   }
-  step(kt, I0{}, T_{}, F_{});
-  step(kt + 1, I1{}, F_{}, F_{});
+  step(t, S0{}, T_{}, F_{});
+  step(t + 1, S1{}, F_{}, F_{});
 
   // ---- epilogue: the tile goes through LDS as bf16, one row per thread ----
   //
   // The accumulators of a row are spread over 32 lanes; instead of cross-lane
-  // reductions each wave writes its quarter to LDS (row-major [256][256] bf16,
-  // 16-byte chunks XOR-swizzled by row % 32) and thread t then walks row t
-  // (forward) or copies rows out with 16-byte stores (gradient).  The last
-  // step's barrier already ordered every read of the LDS stages before this.
-  __syncthreads();
-  uint16_t* xs = reinterpret_cast<uint16_t*>(lds);
+  // reductions each wave writes its quarter to LDS (row-major [256][256] bf16
+  // over the two stage arrays, 16-byte chunks XOR-swizzled by row % 32) and
+  // thread t then walks row t (forward) or copies rows out with 16-byte stores
+  // (gradient).  Every direct load has landed (the last wait was vmcnt(0)); the
+  // barrier orders every wave's last fragment reads before the stores.
+  wait_vm_barrier<0>();
   const int half = lane >> 5;  // which 4-row group of each 8-row band this lane holds
   const int col_lane = lane & 31;
+  const int wm_u = wave_u >> 1;
+  // the epilogue rows of this wave's quarter live in stage array wm
+  auto xq = [&](int) { return reinterpret_cast<uint16_t*>(stage_ptr(wm_u)); };
   if (MODE == kFwd) {
 #pragma unroll
-    for (int i = 0; i < kTM; ++i)
+    for (int i = 0; i < kTM; ++i) {
+      uint16_t* xs = xq(i);
 #pragma unroll
       for (int j = 0; j < kTN; ++j)
 #pragma unroll
@@ -329,32 +352,43 @@ void lce_tile_kernel(LceParams P) {
           const int cl = wn * kWN + j * 32 + col_lane;
           xs[xs_index(rl, cl)] = BF16::from_float(acc[i][j][v]);
         }
+    }
     __syncthreads();
     const int64_t r = m0 + tid;
     if (r < row_end) {
+      // row tid is local row tid % 128 of stage array tid / 128
+      const uint16_t* xs = reinterpret_cast<const uint16_t*>(stage_ptr(wm_u));
       const int ncols = (P.V - n0 < kBN) ? (int)(P.V - n0) : kBN;
-      const vu4* rowp = reinterpret_cast<const vu4*>(xs + tid * kBN);
+      const vu4* rowp = reinterpret_cast<const vu4*>(xs + (tid & (kEpiRows - 1)) * kBN);
       const int sw = tid & 31;
-      float M = -INFINITY;
-      for (int c = 0; c < kBN / 8; ++c) {
-        float w[8];
-        BF16::unpack(rowp[c ^ sw], w);
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          if (c * 8 + e < ncols) M = fmaxf(M, w[e]);
-      }
-      float sum = 0.f;
-      if (M != -INFINITY) {
-        float s4[4] = {0.f, 0.f, 0.f, 0.f};
+      float M = -INFINITY, sum = 0.f;
+      // two passes (max, then sum of exp); the column bound is only checked in
+      // the last, partial column tile
+      auto walk = [&](auto full_c) {
+        constexpr bool FULL = decltype(full_c)::value;
         for (int c = 0; c < kBN / 8; ++c) {
           float w[8];
           BF16::unpack(rowp[c ^ sw], w);
 #pragma unroll
           for (int e = 0; e < 8; ++e)
-            if (c * 8 + e < ncols) s4[e & 3] += fast_exp2((w[e] - M) * kLog2e);
+            if (FULL || c * 8 + e < ncols) M = fmaxf(M, w[e]);
         }
-        sum = (s4[0] + s4[1]) + (s4[2] + s4[3]);
-      }
+        if (M != -INFINITY) {
+          float s4[4] = {0.f, 0.f, 0.f, 0.f};
+          for (int c = 0; c < kBN / 8; ++c) {
+            float w[8];
+            BF16::unpack(rowp[c ^ sw], w);
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+              if (FULL || c * 8 + e < ncols) s4[e & 3] += fast_exp2((w[e] - M) * kLog2e);
+          }
+          sum = (s4[0] + s4[1]) + (s4[2] + s4[3]);
+        }
+      };
+      if (ncols == kBN)
+        walk(std::true_type{});
+      else
+        walk(std::false_type{});
       float* dst = P.part + ((r - P.row0) * P.n_nt + nt) * 2;
       dst[0] = M;
       dst[1] = sum;
@@ -364,6 +398,7 @@ void lce_tile_kernel(LceParams P) {
   } else {
 #pragma unroll
     for (int i = 0; i < kTM; ++i) {
+      uint16_t* xs = xq(i);
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int rl = wm * kWM + i * 32 + (v >> 2) * 8 + half * 4 + (v & 3);
@@ -382,12 +417,14 @@ void lce_tile_kernel(LceParams P) {
     __syncthreads();
     // 32 threads per row, one 16-byte chunk each; 8 rows per pass
     const int c = tid & 31;
+#pragma unroll 4
     for (int k = 0; k < kBM / 8; ++k) {
       const int rl = (tid >> 5) + 8 * k;
       const int64_t r = m0 + rl;
       const int64_t col0 = n0 + c * 8;
       if (r >= row_end || col0 >= P.V) continue;
-      const vu4 q = reinterpret_cast<const vu4*>(xs + rl * kBN)[c ^ (rl & 31)];
+      const uint16_t* xs = reinterpret_cast<const uint16_t*>(stage_ptr(rl / kEpiRows));
+      const vu4 q = reinterpret_cast<const vu4*>(xs + (rl & (kEpiRows - 1)) * kBN)[c ^ (rl & 31)];
       uint16_t* dst = P.G + (r - P.row0) * P.ldg + col0;
       if (col0 + 8 <= P.V && (reinterpret_cast<uintptr_t>(dst) & 15u) == 0) {
         *reinterpret_cast<vu4*>(dst) = q;
@@ -446,7 +483,10 @@ int check_common(const void* hidden, int64_t T, int64_t Hd, int64_t ldh, const v
                (long long)T, (long long)V, (long long)Hd, (long long)bsz);
   MIRL_REQUIRE(T % bsz == 0, "row count %lld is not a multiple of the batch size %lld",
                (long long)T, (long long)bsz);
-  MIRL_REQUIRE(Hd % (2 * kBK) == 0, "hidden size %lld must be a multiple of %d", (long long)Hd, 2 * kBK);
+  MIRL_REQUIRE(Hd % (kStages * kSK) == 0, "hidden size %lld must be a multiple of %d", (long long)Hd,
+               kStages * kSK);
+  MIRL_REQUIRE(ldh < (int64_t(1) << 22) && ldw < (int64_t(1) << 22),
+               "row strides (%lld, %lld) must be below 2^22 elements", (long long)ldh, (long long)ldw);
   MIRL_REQUIRE(ldh % 8 == 0 && ldw % 8 == 0 && ldh >= Hd && ldw >= Hd,
                "row strides (%lld, %lld) must be multiples of 8 elements and >= the hidden size",
                (long long)ldh, (long long)ldw);
