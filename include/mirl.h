@@ -562,6 +562,55 @@ int mirl_grpo_advantage(const int64_t* prompts, int64_t B, int64_t K,
                         int normalize, float* adv, float* baseline, float* std,
                         uint8_t* trivial, void* stream);
 
+/* ---------------------------------------------------------------------- */
+/* Packed-sequence glue                                                    */
+/* ---------------------------------------------------------------------- */
+/* Sequence boundaries are int64 DEVICE arrays of n_seq + 1 nondecreasing
+ * entries (cu_seqlens / cu_seqlens_padded uploaded by the caller).  Each
+ * thread finds its sequence by a binary search of them; reads are guarded, so
+ * boundaries that break the ordering give zeros, never an access outside the
+ * buffers.
+ *
+ * mirl_pack_sequences: out[p, e] (p < total = cu_seqlens_padded[B],
+ * e < row_elems, elements of elem_bytes = 1, 2, 4 or 8 bytes) =
+ *   x[seq * S + off, e]  for p in [cu_pad[seq], cu_pad[seq + 1]),
+ *                        off = (p - cu_pad[seq] - roll_shift) mod the
+ *                        segment length (no roll when roll_shift == 0),
+ *                        when off < min(cu_seqlens[seq+1] - cu_seqlens[seq], S);
+ *   0                    otherwise (and for p < cu_pad[0]).
+ * x is [B, S, row_elems] contiguous; out [total, row_elems] contiguous.
+ * Replaces: _pack_input_ids (nemo_rl/algorithms/loss/utils.py:355-408), CP = 1.
+ */
+int mirl_pack_sequences(const void* x, int64_t B, int64_t S, int64_t row_elems,
+                        int32_t elem_bytes, const int64_t* cu_seqlens,
+                        const int64_t* cu_seqlens_padded, int64_t roll_shift,
+                        void* out, int64_t total, void* stream);
+
+/* mirl_packed_roll_targets: out[p] = target[p + 1] inside a segment
+ * [b[i], b[i+1]), target[b[i]] at the segment's last position, 0 for p
+ * outside [b[0], b[n_seq]).  target and out are [n] int64.
+ * Replaces: the per-sequence target roll of
+ * from_parallel_logits_to_logprobs_packed_sequences
+ * (nemo_rl/distributed/model_utils.py:1116-1139).
+ */
+int mirl_packed_roll_targets(const int64_t* target, int64_t n, const int64_t* bounds,
+                             int64_t n_seq, int64_t* out, void* stream);
+
+/* mirl_unpack_rows_fwd: out[i, j] = packed[b[i] + j] for
+ * j < clip(b[i+1] - b[i] - 1, 0, cols), else 0; out is [n_seq, cols] fp32,
+ * packed [n_rows] fp32.
+ * mirl_unpack_rows_bwd: its backward, grad_packed[p] = grad_out[i, p - b[i]]
+ * for the packed rows the forward copied, 0 elsewhere ([n_rows] fp32;
+ * grad_out [n_seq, cols] contiguous).
+ * Replaces: the unpacking loop of from_parallel_logits_to_logprobs_packed_sequences
+ * (nemo_rl/distributed/model_utils.py:1211-1229) and its autograd backward.
+ */
+int mirl_unpack_rows_fwd(const float* packed, int64_t n_rows, const int64_t* bounds,
+                         int64_t n_seq, int64_t cols, float* out, void* stream);
+int mirl_unpack_rows_bwd(const float* grad_out, int64_t n_seq, int64_t cols,
+                         const int64_t* bounds, int64_t n_rows, float* grad_packed,
+                         void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -206,6 +206,13 @@ SIGNATURES = {
         _I,
         [_P, _I, _I64, _I64, _I64, _I, ctypes.c_double, _P, _P, _P, _P, _I64, _P, _I64, _P],
     ),
+    "mirl_pack_sequences": (
+        _I,
+        [_P, _I64, _I64, _I64, ctypes.c_int32, _P, _P, _I64, _P, _I64, _P],
+    ),
+    "mirl_packed_roll_targets": (_I, [_P, _I64, _P, _I64, _P, _P]),
+    "mirl_unpack_rows_fwd": (_I, [_P, _I64, _P, _I64, _I64, _P, _P]),
+    "mirl_unpack_rows_bwd": (_I, [_P, _I64, _I64, _P, _I64, _P, _P]),
 }
 
 FILTER_KEEP_CAP = 1024  # MIRL_FILTER_KEEP_CAP
@@ -743,6 +750,77 @@ def grpo_advantage(
     )
     _check(st, "mirl_grpo_advantage")
     return adv, base, std, trivial
+
+
+# ---------------------------------------------------------------------------
+# packed-sequence glue
+# ---------------------------------------------------------------------------
+def pack_sequences(
+    x: torch.Tensor, cu_seqlens: torch.Tensor, cu_seqlens_padded: torch.Tensor, roll_shift: int,
+    total: int,
+) -> torch.Tensor:
+    """``[B, S, ...]`` rows packed to ``[total, ...]`` along the padded boundaries (device int64)."""
+    dev = _require_gpu(x, cu_seqlens, cu_seqlens_padded)
+    assert x.is_contiguous() and x.dim() >= 2
+    assert cu_seqlens.dtype == torch.int64 and cu_seqlens_padded.dtype == torch.int64
+    B, S = x.shape[0], x.shape[1]
+    tail = tuple(x.shape[2:])
+    row = 1
+    for d in tail:
+        row *= d
+    out = torch.empty((total, *tail), dtype=x.dtype, device=dev)
+    if total == 0 or row == 0:
+        return out.zero_()
+    st = _launch(
+        "mirl_pack_sequences", dev,
+        x.data_ptr(), B, S, row, x.element_size(), cu_seqlens.data_ptr(),
+        cu_seqlens_padded.data_ptr(), int(roll_shift), out.data_ptr(), total, _stream(dev),
+    )
+    _check(st, "mirl_pack_sequences")
+    return out
+
+
+def packed_roll_targets(target: torch.Tensor, bounds: torch.Tensor) -> torch.Tensor:
+    """Per-segment roll by -1 of packed int64 targets ``[n]`` (0 outside the segments)."""
+    dev = _require_gpu(target, bounds)
+    assert target.dtype == torch.int64 and target.is_contiguous() and bounds.dtype == torch.int64
+    out = torch.empty_like(target)
+    st = _launch(
+        "mirl_packed_roll_targets", dev,
+        target.data_ptr(), target.numel(), bounds.data_ptr(), bounds.numel() - 1, out.data_ptr(),
+        _stream(dev),
+    )
+    _check(st, "mirl_packed_roll_targets")
+    return out
+
+
+def unpack_rows_fwd(packed: torch.Tensor, bounds: torch.Tensor, cols: int) -> torch.Tensor:
+    """Packed fp32 rows ``[n_rows]`` -> ``[n_seq, cols]`` (zeros after each sequence)."""
+    dev = _require_gpu(packed, bounds)
+    assert packed.dtype == torch.float32 and packed.is_contiguous() and bounds.dtype == torch.int64
+    n_seq = bounds.numel() - 1
+    out = torch.empty((n_seq, cols), dtype=torch.float32, device=dev)
+    st = _launch(
+        "mirl_unpack_rows_fwd", dev,
+        packed.data_ptr(), packed.numel(), bounds.data_ptr(), n_seq, cols, out.data_ptr(),
+        _stream(dev),
+    )
+    _check(st, "mirl_unpack_rows_fwd")
+    return out
+
+
+def unpack_rows_bwd(grad_out: torch.Tensor, bounds: torch.Tensor, n_rows: int) -> torch.Tensor:
+    """Backward of unpack_rows_fwd: ``[n_seq, cols]`` -> ``[n_rows]`` (zeros for rows not copied)."""
+    dev = _require_gpu(grad_out, bounds)
+    g = grad_out.float().contiguous()
+    n_seq, cols = g.shape
+    out = torch.empty(n_rows, dtype=torch.float32, device=dev)
+    st = _launch(
+        "mirl_unpack_rows_bwd", dev,
+        g.data_ptr(), n_seq, cols, bounds.data_ptr(), n_rows, out.data_ptr(), _stream(dev),
+    )
+    _check(st, "mirl_unpack_rows_bwd")
+    return out
 
 
 # ---------------------------------------------------------------------------

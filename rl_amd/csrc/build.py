@@ -27,6 +27,7 @@ SOURCES = [
     "topk_filter.hip",
     "linear_ce.hip",
     "divergence.hip",
+    "packing.hip",
 ]
 
 ARCH = "gfx950"

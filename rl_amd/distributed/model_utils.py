@@ -385,9 +385,9 @@ def from_parallel_logits_to_logprobs_packed_sequences(
     ``vocab_parallel_logits`` is ``[1, T, V]``; ``cu_seqlens_padded`` holds the
     ``B + 1`` sequence boundaries (host integers).  The reference's host loops
     over sequences (target roll, unpacking to ``[B, unpacked_seqlen - 1]``)
-    become index maps built on the host from the boundaries and applied with
-    one gather each; the unpacking's backward is the inverse gather, so no
-    scatter or sort runs in the backward.
+    become one gfx950 kernel each over the uploaded boundaries
+    (``mirl_packed_roll_targets``, ``mirl_unpack_rows_fwd``); the unpacking's
+    backward is the inverse kernel (``mirl_unpack_rows_bwd``).
     """
     _require_single_rank(group, cp_group)
     _check_chunk_size(chunk_size)
@@ -395,8 +395,10 @@ def from_parallel_logits_to_logprobs_packed_sequences(
     if logits.shape[0] != 1:
         raise ValueError(f"packed logits must have batch 1, got {tuple(logits.shape)}")
     bounds = [int(x) for x in cu_seqlens_padded]
-    T = logits.shape[1]
+    if len(bounds) < 1 or any(b1 < b0 for b0, b1 in zip(bounds, bounds[1:])) or bounds[0] < 0:
+        raise ValueError(f"cu_seqlens_padded must be nondecreasing and nonnegative, got {bounds}")
     dev = logits.device
+    bdev = _host_ints_to_device(bounds, dev)
     tgt = target.reshape(1, -1)
     if tgt.dtype != torch.int64:
         tgt = tgt.long()
@@ -405,8 +407,7 @@ def from_parallel_logits_to_logprobs_packed_sequences(
             raise ValueError(
                 f"cu_seqlens_padded ends at {bounds[-1]} but the packed target has {tgt.shape[1]} tokens"
             )
-        roll = _host_ints_to_device(_roll_map(bounds, tgt.shape[1]), dev)
-        tgt = _gather_or_zero(tgt.reshape(-1), roll).unsqueeze(0)
+        tgt = _C.packed_roll_targets(tgt.reshape(-1).contiguous(), bdev).unsqueeze(0)
     if need_top_k_or_top_p_filtering(sampling_params):
         from rl_amd.distributed.sampling import filtered_row_logprobs
 
@@ -427,9 +428,7 @@ def from_parallel_logits_to_logprobs_packed_sequences(
             f"cu_seqlens_padded ends at {bounds[-1]} but only {probs.shape[0]} packed rows were computed"
         )
     out_cols = max(int(unpacked_seqlen) - 1, 0)
-    src, dst = _unpack_maps(bounds, probs.shape[0], out_cols)
-    maps = _host_ints_to_device(np.concatenate([src, dst]), dev)
-    return _UnpackRows.apply(probs, maps[: src.shape[0]], maps[src.shape[0] :], (len(bounds) - 1, out_cols))
+    return _UnpackRows.apply(probs, bdev, out_cols)
 
 
 def _gather_or_zero(x: torch.Tensor, index: torch.Tensor) -> torch.Tensor:
@@ -438,57 +437,19 @@ def _gather_or_zero(x: torch.Tensor, index: torch.Tensor) -> torch.Tensor:
     return torch.cat([x, pad]).index_select(0, index)
 
 
-def _roll_map(bounds: list[int], n: int) -> np.ndarray:
-    """Source of each position of the per-sequence roll by -1 (reference model_utils.py:1122-1139).
-
-    Inside ``[bounds[i], bounds[i+1])`` position p reads p + 1, the segment's
-    last position its first; positions past ``bounds[-1]`` read the zero slot ``n``.
-    """
-    b = np.asarray(bounds, dtype=np.int64)
-    src = np.full(n, n, dtype=np.int64)
-    lens = b[1:] - b[:-1]
-    total = int(b[-1] - b[0])
-    if total > 0:
-        seq = np.repeat(np.arange(lens.shape[0]), lens)
-        pos = np.arange(b[0], b[-1], dtype=np.int64)
-        nxt = pos + 1
-        src[b[0] : b[-1]] = np.where(nxt == b[1:][seq], b[:-1][seq], nxt)
-    return src
-
-
-def _unpack_maps(bounds: list[int], n_rows: int, out_cols: int) -> tuple[np.ndarray, np.ndarray]:
-    """Index maps of the unpacking (reference model_utils.py:1211-1229).
-
-    ``src[i * out_cols + j]`` is the packed row copied to ``out[i, j]`` (rows
-    ``bounds[i] .. bounds[i+1] - 2``, at most ``out_cols`` of them; ``n_rows``
-    reads zero); ``dst[p]`` is the inverse (``B * out_cols`` for packed rows
-    that are not copied).
-    """
-    b = np.asarray(bounds, dtype=np.int64)
-    B = b.shape[0] - 1
-    starts = b[:-1]
-    lens = np.clip(b[1:] - starts - 1, 0, out_cols)
-    j = np.arange(out_cols, dtype=np.int64)
-    valid = j[None, :] < lens[:, None]
-    src = np.where(valid, starts[:, None] + j[None, :], n_rows).reshape(-1)
-    dst = np.full(n_rows, B * out_cols, dtype=np.int64)
-    flat_valid = valid.reshape(-1)
-    dst[src[flat_valid]] = np.nonzero(flat_valid)[0]
-    return src, dst
-
-
 class _UnpackRows(torch.autograd.Function):
-    """``[T]`` packed rows -> ``[B, C]`` via a gather map; backward is the inverse gather."""
+    """``[T]`` packed fp32 rows -> ``[B, C]`` by the sequence boundaries; backward is the inverse."""
 
     @staticmethod
-    def forward(ctx: Any, probs: torch.Tensor, src: torch.Tensor, dst: torch.Tensor, shape: tuple) -> torch.Tensor:  # type: ignore[override]
-        ctx.save_for_backward(dst)
-        return _gather_or_zero(probs, src).view(shape)
+    def forward(ctx: Any, probs: torch.Tensor, bounds: torch.Tensor, cols: int) -> torch.Tensor:  # type: ignore[override]
+        ctx.save_for_backward(bounds)
+        ctx.n_rows = probs.shape[0]
+        return _C.unpack_rows_fwd(probs.contiguous(), bounds, cols)
 
     @staticmethod
     def backward(ctx: Any, *grad_outputs: torch.Tensor):  # type: ignore[override]
-        (dst,) = ctx.saved_tensors
-        return _gather_or_zero(grad_outputs[0].reshape(-1), dst), None, None, None
+        (bounds,) = ctx.saved_tensors
+        return _C.unpack_rows_bwd(grad_outputs[0], bounds, ctx.n_rows), None, None
 
 
 def _is_dtensor(t: torch.Tensor) -> bool:

@@ -1,12 +1,12 @@
 """Host logic of the packed-sequence path (CPU only): target packing, loss-input
 preparation plumbing and the sequence-packing wrappers' metric reduction.
 
-``_pack_input_ids`` and the packed-logprob roll/unpack are host-built index
-maps applied with one gather (no HIP kernel), so they run here against the
-oracle's loop restatements (reference loss/utils.py:355-408,
-model_utils.py:1122-1139 and :1211-1229).  The
-kernels themselves are replaced by stand-ins where the reference's own tests
-do the same (test_sequence_packing_fusion.py:44-111).
+``_pack_input_ids`` on host tensors builds its position map with numpy and
+applies it as one gather (device tensors go through the gfx950 packing kernel,
+tested in test_gpu_packing_kernels.py), so it runs here against the oracle's
+loop restatement (reference loss/utils.py:355-408).  The logprob kernels are
+replaced by stand-ins where the reference's own tests do the same
+(test_sequence_packing_fusion.py:44-111).
 """
 
 import math
@@ -225,32 +225,3 @@ def test_wrap_loss_fn_with_input_preparation_passes_through():
     data = {"input_ids": torch.zeros(1, 4, dtype=torch.long), "token_mask": torch.ones(1, 4)}
     loss, m = wrap_loss_fn_with_input_preparation(x, data, torch.tensor(1.0), torch.tensor(3.0), fake, _fake_prepare)
     assert float(loss) == 0 + 2 + 4
-
-
-def test_roll_and_unpack_maps_match_oracle():
-    """Host index maps of the packed logprob path against the oracle's per-sequence loops;
-    the inverse (backward) map against autograd of the forward gather."""
-    import numpy as np
-
-    from oracle.logprob import pack_targets, unpack_logprobs
-    from rl_amd.distributed.model_utils import _roll_map, _unpack_maps
-
-    for seed in range(30):
-        rng = np.random.default_rng(seed)
-        lens = rng.integers(0, 9, size=int(rng.integers(1, 6)))
-        b = [0] + [int(x) for x in np.cumsum(lens)]
-        T = b[-1] + int(rng.integers(0, 3))
-        ids = torch.arange(T) + 100
-        m = torch.from_numpy(_roll_map(b, T))
-        got = torch.cat([ids, torch.zeros(1, dtype=ids.dtype)])[m]
-        exp = torch.cat([pack_targets(ids[: b[-1]].unsqueeze(0), b)[0], torch.zeros(T - b[-1], dtype=ids.dtype)])
-        assert torch.equal(got, exp), (seed, b)
-        S = int(rng.integers(1, 10))
-        probs = torch.randn(T, dtype=torch.float64)
-        src, dst = _unpack_maps(b, T, S - 1)
-        pr = probs.clone().requires_grad_(True)
-        out = torch.cat([pr, pr.new_zeros(1)])[torch.from_numpy(src)].view(len(b) - 1, S - 1)
-        assert torch.equal(out.detach(), unpack_logprobs(probs[: b[-1]], b, S)), seed
-        g = torch.randn(len(b) - 1, S - 1, dtype=torch.float64)
-        (ga,) = torch.autograd.grad(out, [pr], g)
-        assert torch.equal(torch.cat([g.reshape(-1), g.new_zeros(1)])[torch.from_numpy(dst)], ga), seed
