@@ -438,6 +438,38 @@ class ClippedPGLossFn(LossFunction):
         policy_logprobs_at_sampler_topk: Optional[torch.Tensor] = None,
     ) -> tuple[torch.Tensor, dict]:
         """Scalar loss (differentiable w.r.t. ``next_token_logprobs``) and its metric dict."""
+        loss, metrics, early = self._loss_on_device(
+            next_token_logprobs, data, global_valid_seqs, global_valid_toks, opd_full_divergence,
+            opd_full_entropy, opd_full_cross_entropy, policy_support_mask,
+            policy_logprobs_at_sampler_topk,
+        )
+        fetch = _C.start_fetch(metrics)
+        if early is not None:
+            # d(loss)/d(curr) is known now (grad_loss = 1): start the logits
+            # backward behind the metrics copy, before the host waits for it
+            from rl_amd.distributed.model_utils import launch_early_backward
+
+            launch_early_backward(*early)
+        return loss, self.metrics_from_values(_C.finish_fetch(fetch))
+
+    def metrics_from_values(self, values: list) -> dict:
+        """The metric dict from the kernel's metric slots (a host list)."""
+        return {k: float(values[_C.PG_METRIC_SLOTS[k]]) for k in self._metric_keys()}
+
+    def _loss_on_device(
+        self,
+        next_token_logprobs: Optional[torch.Tensor],
+        data: Optional[Mapping[str, Any]],
+        global_valid_seqs: Optional[torch.Tensor],
+        global_valid_toks: Optional[torch.Tensor],
+        opd_full_divergence: Optional[torch.Tensor] = None,
+        opd_full_entropy: Optional[torch.Tensor] = None,
+        opd_full_cross_entropy: Optional[torch.Tensor] = None,
+        policy_support_mask: Optional[torch.Tensor] = None,
+        policy_logprobs_at_sampler_topk: Optional[torch.Tensor] = None,
+    ) -> tuple[torch.Tensor, torch.Tensor, Optional[tuple]]:
+        """The loss, the device metric slots ``[MIRL_NUM_METRICS]`` and, when the early
+        logits backward applies, its ``(logprobs, gradient)`` pair; nothing is synchronised."""
         assert data is not None, "ClippedPGLossFn requires data"
         assert global_valid_seqs is not None, "ClippedPGLossFn requires global_valid_seqs"
         assert global_valid_toks is not None, "ClippedPGLossFn requires global_valid_toks"
@@ -513,16 +545,10 @@ class ClippedPGLossFn(LossFunction):
             curr_k, unfiltered, cfg, token_mask, advantages, prev, generation, reference,
             support, sample_mask, rewards, gvs, gvt, plog, sc,
         )
-        fetch = _C.start_fetch(metrics.detach())
+        early = None
         if curr_k is curr and loss.grad_fn is not None and curr.requires_grad:
-            # d(loss)/d(curr) is known now (grad_loss = 1): start the logits
-            # backward behind the metrics copy, before the host waits for it
-            from rl_amd.distributed.model_utils import launch_early_backward
-
-            launch_early_backward(curr, loss.grad_fn.grad_curr)
-        values = _C.finish_fetch(fetch)
-        out = {k: float(values[_C.PG_METRIC_SLOTS[k]]) for k in self._metric_keys()}
-        return loss, out
+            early = (curr, loss.grad_fn.grad_curr)
+        return loss, metrics.detach(), early
 
 
 class _ClippedPGFunction(torch.autograd.Function):

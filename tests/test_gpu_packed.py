@@ -175,6 +175,50 @@ def test_fusion_wrapper_matches_per_sequence_wrapper(dtype, chunk_size, reuse, s
     assert l1.item() == pytest.approx(lo.item(), rel=1e-4, abs=1e-6)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=str)
+@pytest.mark.parametrize("sampling", [False, True], ids=["plain", "topk-topp"])
+def test_per_sequence_wrapper_one_pass_equals_per_sequence_calls(dtype, sampling, single_rank_group):
+    """The per-sequence wrapper takes every sequence's logprobs from one pass over the packed
+    row and fetches all sequences' ClippedPG metrics with one copy; its loss, metrics and
+    gradient equal a loop of the public per-sequence calls on narrowed logits (the
+    reference's wrapper.py:95-182 loop, each call with its own metrics synchronisation).
+    The logprob kernel may split rows differently for the two row counts, so values agree
+    to fp32 rounding (loss and metrics 1e-6 relative) and gradients to one bf16 ulp or 1e-6."""
+    print("[case] per-sequence wrapper one pass", dtype, sampling, flush=True)
+    from rl_amd.algorithms.loss.wrapper import _combine_metric
+
+    tc = _case(dtype)
+    data = BatchedDataDict({k: v.to(DEV) for k, v in tc["data"].items()})
+    loss_fn = ClippedPGLossFn(ClippedPGLossConfig(reference_policy_kl_penalty=0.01))
+    sp = TrainingSamplingParams(top_k=8, top_p=0.9, temperature=1.0) if sampling else None
+    seq, _ = _wrappers(tc, loss_fn, single_rank_group, sampling_params=sp)
+    assert seq._packed_prepare_kwargs(tc["make"]()[1], data, [b - a for a, b in zip(tc["cu"][:-1], tc["cu"][1:])]) is not None
+    l0, m0, g0, _ = _run(seq, tc, BatchedDataDict(dict(data)))
+
+    local, packed = tc["make"]()
+    cu, cu_pad = tc["cu"], tc["cu_pad"]
+    loss_acc, m_acc = 0, {}
+    for i, (a, b) in enumerate(zip(cu_pad[:-1], cu_pad[1:])):
+        L = cu[i + 1] - cu[i]
+        sd = {k: (v[:, :L] if v.ndim > 1 and v.shape[1] > 1 else v) for k, v in data.slice(i, i + 1).items()}
+        li, sd = prepare_loss_input(packed.narrow(1, a, b - a), sd, loss_fn, 0, single_rank_group,
+                                    sampling_params=sp)
+        loss, m = loss_fn(data=sd, global_valid_seqs=tc["gvs"], global_valid_toks=tc["gvt"], **li)
+        loss_acc = loss_acc + loss
+        for k, v in m.items():
+            _combine_metric(m_acc, k, v)
+    loss_acc.backward()
+    assert l0.item() == pytest.approx(loss_acc.item(), rel=1e-6, abs=1e-9)
+    assert set(m0) == set(m_acc)
+    for k in m0:
+        assert m0[k] == pytest.approx(m_acc[k], rel=1e-6, abs=1e-9), k
+    assert g0.abs().sum() > 0
+    if dtype == torch.bfloat16:
+        assert_close_or_ulp_bf16(g0, local.grad.cpu(), 1e-6)
+    else:
+        torch.testing.assert_close(g0, local.grad, rtol=1e-5, atol=1e-6)
+
+
 def test_fusion_wrapper_with_sampling_params(single_rank_group):
     print("[case] fusion vs baseline with sampling", flush=True)
     tc = _case(torch.float32)
