@@ -163,6 +163,30 @@ int mirl_gather_logprob_bwd(const void* logits, int dtype, int64_t B, int64_t R,
                             int64_t gi_stride_b, int64_t gi_stride_r,
                             void* stream);
 
+/*
+ * mirl_gather_logprob_bwd for a gradient launched early: `grad_used` is the
+ * contiguous [B, R, K] upstream gradient an earlier mirl_gather_logprob_bwd
+ * already wrote `grad_in` for.  This compares `grad_out` with it bit for bit
+ * (`flags`: MIRL_RECHECK_FLAGS ints of scratch, written before they are read)
+ * and recomputes grad_in from grad_out only if they differ, without a host
+ * synchronisation.  Same arguments otherwise.
+ * Replaces: nothing in the reference (it is the device side of an early start
+ * of ChunkedDistributedGatherLogprob.backward, model_utils.py:750-805, for a
+ * loss that knows its gradient in closed form).
+ */
+int mirl_gather_logprob_bwd_recheck(const void* logits, int dtype, int64_t B, int64_t R,
+                                    int64_t V, int64_t stride_b, int64_t stride_r,
+                                    const int64_t* indices, int64_t K,
+                                    int64_t i_stride_b, int64_t i_stride_r,
+                                    int64_t i_stride_k, int64_t vocab_start,
+                                    int64_t vocab_end, const float* row_stats,
+                                    const float* grad_out, int64_t g_stride_b,
+                                    int64_t g_stride_r, int64_t g_stride_k,
+                                    const float* grad_used, int* flags,
+                                    float* workspace, void* grad_in,
+                                    int64_t gi_stride_b, int64_t gi_stride_r,
+                                    void* stream);
+
 /* Bytes of scratch mirl_vocab_topk needs for `rows` rows. */
 int64_t mirl_vocab_topk_workspace_bytes(int64_t rows);
 

@@ -163,6 +163,11 @@ SIGNATURES = {
         [_P, _I, _I64, _I64, _I64, _I64, _I64, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P,
          _I64, _I64, _I64, _P, _P, _I64, _I64, _P],
     ),
+    "mirl_gather_logprob_bwd_recheck": (
+        _I,
+        [_P, _I, _I64, _I64, _I64, _I64, _I64, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P,
+         _I64, _I64, _I64, _P, _P, _P, _P, _I64, _I64, _P],
+    ),
     "mirl_vocab_topk_workspace_bytes": (_I64, [_I64]),
     "mirl_vocab_topk": (
         _I,
@@ -645,6 +650,39 @@ def gather_logprob_bwd(
         grad_in.data_ptr(), grad_in.stride(0), grad_in.stride(1), _stream(dev),
     )
     _check(st, "mirl_gather_logprob_bwd")
+
+
+def gather_logprob_bwd_recheck(
+    logits: torch.Tensor,
+    indices: torch.Tensor,
+    vocab_start: int,
+    vocab_end: int,
+    stats: torch.Tensor,
+    grad_out: torch.Tensor,
+    grad_used: torch.Tensor,
+    grad_in: torch.Tensor,
+) -> None:
+    """Recompute grad_in from grad_out on the device only if it differs from grad_used."""
+    dev = _require_gpu(logits, indices, stats, grad_out, grad_used, grad_in)
+    B, R, K = indices.shape
+    V = logits.shape[-1]
+    assert grad_in.stride(-1) == 1 and logits.stride(-1) == 1
+    assert grad_out.dtype == torch.float32 and grad_used.dtype == torch.float32
+    assert grad_used.is_contiguous() and tuple(grad_used.shape) == (B, R, K)
+    lib = load()
+    ws = torch.empty(int(lib.mirl_gather_logprob_workspace_elems(B, R)), dtype=torch.float32,
+                     device=dev)
+    flags = torch.empty(64, dtype=torch.int32, device=dev)  # MIRL_RECHECK_FLAGS
+    st = _launch(
+        "mirl_gather_logprob_bwd_recheck", dev,
+        logits.data_ptr(), _dtype_code(logits), B, R, V, logits.stride(0), logits.stride(1),
+        indices.data_ptr(), K, indices.stride(0), indices.stride(1), indices.stride(2),
+        int(vocab_start), int(vocab_end), stats.data_ptr(), grad_out.data_ptr(),
+        grad_out.stride(0), grad_out.stride(1), grad_out.stride(2), grad_used.data_ptr(),
+        flags.data_ptr(), ws.data_ptr(), grad_in.data_ptr(), grad_in.stride(0), grad_in.stride(1),
+        _stream(dev),
+    )
+    _check(st, "mirl_gather_logprob_bwd_recheck")
 
 
 def vocab_topk(logits: torch.Tensor, k: int, vocab_start: int) -> tuple[torch.Tensor, torch.Tensor]:

@@ -447,9 +447,9 @@ class ClippedPGLossFn(LossFunction):
         if early is not None:
             # d(loss)/d(curr) is known now (grad_loss = 1): start the logits
             # backward behind the metrics copy, before the host waits for it
-            from rl_amd.distributed.model_utils import launch_early_backward
+            from rl_amd.distributed.model_utils import launch_early_backward, launch_early_backward_pair
 
-            launch_early_backward(*early)
+            (launch_early_backward if len(early) == 2 else launch_early_backward_pair)(*early)
         return loss, self.metrics_from_values(_C.finish_fetch(fetch))
 
     def metrics_from_values(self, values: list) -> dict:
@@ -548,6 +548,10 @@ class ClippedPGLossFn(LossFunction):
         early = None
         if curr_k is curr and loss.grad_fn is not None and curr.requires_grad:
             early = (curr, loss.grad_fn.grad_curr)
+            if plog is not None:
+                # score centering: the gradient of the sampler-id logprobs too
+                early = (curr, loss.grad_fn.grad_curr, plog, loss.grad_fn.grad_plog) if (
+                    plog is policy_logprobs_at_sampler_topk and plog.requires_grad) else None
         return loss, metrics.detach(), early
 
 
@@ -585,6 +589,7 @@ class _ClippedPGFunction(torch.autograd.Function):
         )
         ctx.save_for_backward(grad_curr, grad_unf, grad_plog)
         ctx.grad_curr = grad_curr  # d(loss)/d(curr) at grad_loss = 1, for launch_early_backward
+        ctx.grad_plog = grad_plog
         ctx.mark_non_differentiable(metrics)
         # no zero-filled gradient for the metrics output on the way back
         ctx.set_materialize_grads(False)

@@ -154,7 +154,8 @@ class SequencePackingLossWrapper:
             # each sequence's loss enters the sum with weight 1: its logits
             # backward can start behind the copy (checked again in the backward)
             for e in early:
-                launch_early_backward(*e)
+                if len(e) == 2:
+                    launch_early_backward(*e)
             values = _C.finish_fetch(fetch)
             m = seq_metrics[0].numel()
             for i in range(len(seq_metrics)):

@@ -404,12 +404,23 @@ __global__ __launch_bounds__(kFlatThreads) void logprob_bwd_flat_kernel(
 // single launch that stages each 8 KB piece's ids in LDS measured slower on
 // the [8, 2048, 151936] bf16 rows with 21 ids, 1.47 vs 1.30 ms: the staging
 // round in front of every piece's logits load cuts the bytes in flight.)
+//
+// `flags` (nflags ints, or null) makes a launch conditional: it does nothing
+// unless some flag is set (the early-backward recheck's redo).
+__device__ __forceinline__ bool any_flag(const int* __restrict__ flags, int nflags) {
+  if (flags == nullptr) return true;
+  int any = 0;
+  for (int k = 0; k < nflags; ++k) any |= flags[k];
+  return any != 0;
+}
+
 __global__ __launch_bounds__(256) void gather_gsum_kernel(const float* __restrict__ g, int64_t R,
                                                          int64_t gsb, int64_t gsr, int64_t gsk,
                                                          int64_t K, int64_t rows,
-                                                         float* __restrict__ gsum) {
+                                                         float* __restrict__ gsum,
+                                                         const int* __restrict__ flags, int nflags) {
   const int64_t row = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (row >= rows) return;
+  if (row >= rows || !any_flag(flags, nflags)) return;
   const int64_t b = row / R, r = row - b * R;
   const float* gr = g + b * gsb + r * gsr;
   float s = 0.f;
@@ -428,9 +439,10 @@ __global__ __launch_bounds__(256) void gather_fixup_kernel(
     const int64_t* __restrict__ idx, int64_t K, int64_t isb, int64_t isr, int64_t isk,
     int64_t vs, int64_t ve, const float* __restrict__ stats, const float* __restrict__ g,
     int64_t gsb, int64_t gsr, int64_t gsk, const float* __restrict__ gsum,
-    typename E::raw* gin, int64_t gisb, int64_t gisr, int64_t total) {
+    typename E::raw* gin, int64_t gisb, int64_t gisr, int64_t total,
+    const int* __restrict__ flags, int nflags) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= total) return;
+  if (i >= total || !any_flag(flags, nflags)) return;
   const int64_t row = i / K, k = i - row * K;
   const int64_t b = row / R, r = row - b * R;
   const int64_t* ir = idx + b * isb + r * isr;
@@ -616,7 +628,7 @@ void gather_bwd(int64_t rows, hipStream_t st, const void* logits, int64_t R, int
                 int64_t gsb, int64_t gsr, int64_t gsk, float* gsum, void* gin, int64_t gisb,
                 int64_t gisr) {
   hipLaunchKernelGGL(gather_gsum_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, st,
-                     g, R, gsb, gsr, gsk, K, rows, gsum);
+                     g, R, gsb, gsr, gsk, K, rows, gsum, nullptr, 0);
   // dense part: no target (an empty vocabulary slice masks every id), upstream gsum
   dispatch_bwd<E>(rows, st, logits, R, R, V, sb, sr, idx, isb, isr, 0, 0, stats, gsum, R, 1,
                   gin, gisb, gisr);
@@ -625,7 +637,56 @@ void gather_bwd(int64_t rows, hipStream_t st, const void* logits, int64_t R, int
   hipLaunchKernelGGL((gather_fixup_kernel<E>), dim3((unsigned)((total + 255) / 256)), dim3(256),
                      0, st, static_cast<const typename E::raw*>(logits), R, V, sb, sr, idx, K, isb,
                      isr, isk, vs, ve, stats, g, gsb, gsr, gsk, gsum,
-                     static_cast<typename E::raw*>(gin), gisb, gisr, total);
+                     static_cast<typename E::raw*>(gin), gisb, gisr, total, nullptr, 0);
+}
+
+// The K-id gather's early-backward recheck: gather_check_kernel compares the
+// real [B, R, K] upstream gradient with the one the early launch used (flags as
+// in bwd_check_kernel), then the three backward parts run again, each launch
+// returning at once unless a flag is set.  The dense part's redo is
+// bwd_redo_kernel with no target, whose arithmetic equals the flat kernel's.
+__global__ __launch_bounds__(256) void gather_check_kernel(
+    const float* __restrict__ g, int64_t R, int64_t K, int64_t gsb, int64_t gsr, int64_t gsk,
+    const float* __restrict__ g_used, int64_t n, int* __restrict__ flags) {
+  __shared__ int s_any[4];
+  int any = 0;
+  const int64_t per = (n + gridDim.x - 1) / gridDim.x;
+  const int64_t i0 = (int64_t)blockIdx.x * per;
+  const int64_t i1 = (i0 + per < n) ? i0 + per : n;
+  for (int64_t i = i0 + threadIdx.x; i < i1; i += 256) {
+    const int64_t row = i / K, k = i - row * K;
+    const int64_t b = row / R, r = row - b * R;
+    any |= (__float_as_uint(g[b * gsb + r * gsr + k * gsk]) != __float_as_uint(g_used[i])) ? 1 : 0;
+  }
+  const int wv = threadIdx.x / 64, lane = threadIdx.x % 64;
+  const bool w = __ballot(any != 0) != 0ull;
+  if (lane == 0) s_any[wv] = w ? 1 : 0;
+  __syncthreads();
+  if (threadIdx.x == 0) flags[blockIdx.x] = s_any[0] | s_any[1] | s_any[2] | s_any[3];
+}
+
+template <class E>
+void gather_bwd_recheck(int64_t rows, hipStream_t st, const void* logits, int64_t R, int64_t V,
+                        int64_t sb, int64_t sr, const int64_t* idx, int64_t K, int64_t isb,
+                        int64_t isr, int64_t isk, int64_t vs, int64_t ve, const float* stats,
+                        const float* g, int64_t gsb, int64_t gsr, int64_t gsk, const float* g_used,
+                        int* flags, float* gsum, void* gin, int64_t gisb, int64_t gisr) {
+  using raw = typename E::raw;
+  const int64_t total = rows * K;
+  const int nflags = (int)(total < kCheckBlocks ? total : kCheckBlocks);
+  hipLaunchKernelGGL(gather_check_kernel, dim3((unsigned)nflags), dim3(256), 0, st, g, R, K, gsb,
+                     gsr, gsk, g_used, total, flags);
+  hipLaunchKernelGGL(gather_gsum_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, st,
+                     g, R, gsb, gsr, gsk, K, rows, gsum, flags, nflags);
+  const unsigned grid = (unsigned)(rows < 1024 ? rows : 1024);
+  hipLaunchKernelGGL((bwd_redo_kernel<E>), dim3(grid), dim3(256), 0, st,
+                     static_cast<const raw*>(logits), R, R, V, sb, sr, idx, isb, isr, (int64_t)0,
+                     (int64_t)0, stats, gsum, R, (int64_t)1, static_cast<raw*>(gin), gisb, gisr,
+                     rows, flags, nflags);
+  hipLaunchKernelGGL((gather_fixup_kernel<E>), dim3((unsigned)((total + 255) / 256)), dim3(256),
+                     0, st, static_cast<const raw*>(logits), R, V, sb, sr, idx, K, isb, isr, isk,
+                     vs, ve, stats, g, gsb, gsr, gsk, gsum, static_cast<raw*>(gin), gisb, gisr,
+                     total, flags, nflags);
 }
 
 int check_dtype(int dtype) {
@@ -792,6 +853,41 @@ extern "C" int mirl_gather_logprob_bwd(const void* logits, int dtype, int64_t B,
       break;
   }
   return check_launch("mirl_gather_logprob_bwd");
+}
+
+extern "C" int mirl_gather_logprob_bwd_recheck(
+    const void* logits, int dtype, int64_t B, int64_t R, int64_t V, int64_t stride_b,
+    int64_t stride_r, const int64_t* indices, int64_t K, int64_t i_stride_b, int64_t i_stride_r,
+    int64_t i_stride_k, int64_t vocab_start, int64_t vocab_end, const float* row_stats,
+    const float* grad_out, int64_t g_stride_b, int64_t g_stride_r, int64_t g_stride_k,
+    const float* grad_used, int* flags, float* workspace, void* grad_in, int64_t gi_stride_b,
+    int64_t gi_stride_r, void* stream) {
+  clear_error();
+  if (int e = check_dtype(dtype)) return e;
+  MIRL_REQUIRE(B >= 0 && R >= 0 && V > 0 && K >= 0, "invalid shape B=%lld R=%lld V=%lld K=%lld",
+               (long long)B, (long long)R, (long long)V, (long long)K);
+  MIRL_REQUIRE(V < (int64_t(1) << 31), "vocabulary size %lld exceeds 2^31-1", (long long)V);
+  const int64_t rows = B * R;
+  if (rows == 0) return MIRL_OK;
+  MIRL_REQUIRE(rows < (int64_t(1) << 31) && rows * K < (int64_t(1) << 40), "too many rows (%lld)",
+               (long long)rows);
+  MIRL_REQUIRE(K > 0, "at least one id per row is required (K=%lld)", (long long)K);
+  MIRL_REQUIRE(logits && indices && row_stats && grad_in && workspace && grad_out && grad_used &&
+                   flags,
+               "null pointer argument");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+#define MIRL_GATHER_RECHECK(E)                                                                   \
+  gather_bwd_recheck<E>(rows, st, logits, R, V, stride_b, stride_r, indices, K, i_stride_b,      \
+                        i_stride_r, i_stride_k, vocab_start, vocab_end, row_stats, grad_out,     \
+                        g_stride_b, g_stride_r, g_stride_k, grad_used, flags, workspace,         \
+                        grad_in, gi_stride_b, gi_stride_r)
+  switch (dtype) {
+    case MIRL_DTYPE_F32: MIRL_GATHER_RECHECK(F32); break;
+    case MIRL_DTYPE_BF16: MIRL_GATHER_RECHECK(BF16); break;
+    default: MIRL_GATHER_RECHECK(F16); break;
+  }
+#undef MIRL_GATHER_RECHECK
+  return check_launch("mirl_gather_logprob_bwd_recheck");
 }
 
 extern "C" int mirl_logprob_bwd_recheck(const void* logits, int dtype, int64_t B, int64_t R,

@@ -160,6 +160,38 @@ class _RowLogprob(torch.autograd.Function):
         return grad_input, None, None, None, None, None
 
 
+def launch_early_backward_pair(
+    curr: torch.Tensor, grad_curr: torch.Tensor, plog: torch.Tensor, grad_plog: torch.Tensor
+) -> bool:
+    """launch_early_backward for the next-token and sampler top-k logprobs of one K+1-id
+    gather (``next_token_and_sampler_topk_logprobs``): the gather's upstream gradient is
+    assembled the way autograd assembles it from the two views (each view's gradient
+    scattered into zeros, the two added), its backward is launched, and the gather's
+    backward later checks it against the real one on the device."""
+    node = getattr(curr, "_mirl_gather_node", None)
+    if node is None or getattr(plog, "_mirl_gather_node", None) is not node:
+        return False
+    if getattr(node, "early", None) is not None:
+        return False
+    if grad_curr.dtype != torch.float32 or grad_plog.dtype != torch.float32:
+        return False
+    logits, idx, stats = node.saved_tensors
+    B, S, K1 = idx.shape
+    if (tuple(curr.shape) != (B, S - 1) or tuple(plog.shape) != (B, S - 1, K1 - 1)
+            or tuple(grad_curr.shape) != tuple(curr.shape) or tuple(grad_plog.shape) != tuple(plog.shape)):
+        return False
+    g_a = torch.zeros((B, S, K1), dtype=torch.float32, device=logits.device)
+    g_a[:, : S - 1, 0] = grad_curr
+    g_b = torch.zeros_like(g_a)
+    g_b[:, : S - 1, 1:] = grad_plog
+    g = g_a + g_b
+    grad_input = torch.empty_like(logits)
+    vs, ve = node.vocab
+    _C.gather_logprob_bwd(logits, idx, vs, ve, stats, g, grad_input)
+    node.early = (grad_input, g)
+    return True
+
+
 def launch_early_backward(logprobs: torch.Tensor, grad: torch.Tensor) -> bool:
     """Start the logits backward of ``logprobs`` for the upstream gradient ``grad`` now.
 
@@ -170,17 +202,33 @@ def launch_early_backward(logprobs: torch.Tensor, grad: torch.Tensor) -> bool:
     the backward, a device-side check compares its real upstream gradient with
     ``grad`` bit for bit and recomputes only if they differ (a scaled loss, a
     second consumer of the logprobs), so results never depend on the guess.
-    Applies only to logprobs produced directly by this module's row kernel;
-    returns whether the backward was started.
+    Applies to logprobs produced directly by this module's row kernel and to
+    their unpacking from packed sequences; returns whether the backward was
+    started.
     """
     fn = logprobs.grad_fn
+    if grad.dtype != torch.float32 or tuple(grad.shape) != tuple(logprobs.shape):
+        return False
+    if isinstance(fn, _UnpackRows._backward_cls):
+        # packed sequences: the row kernel's upstream gradient is the unpacking's
+        # backward of `grad` (the same kernel autograd will run on the real one)
+        src = getattr(fn, "src", None)
+        if src is None:
+            return False
+        (bounds,) = fn.saved_tensors
+        return _launch_early_on_node(src, _C.unpack_rows_bwd(grad, bounds, fn.n_rows).view(1, -1))
+    return _launch_early_on_node(fn, grad)
+
+
+def _launch_early_on_node(fn: Any, grad: torch.Tensor) -> bool:
+    """launch_early_backward for the autograd node of a row-kernel output."""
     if not isinstance(fn, _RowLogprob._backward_cls):
         return False
     if getattr(fn, "early", None) is not None or getattr(fn, "reuse_logits_storage", True):
         return False
-    if grad.dtype != torch.float32 or tuple(grad.shape) != tuple(logprobs.shape):
-        return False
     logits, target, stats = fn.saved_tensors
+    if tuple(grad.shape) != tuple(target.shape):
+        return False
     grad = grad.contiguous()
     grad_input = torch.empty_like(logits)
     vs, ve = fn.vocab
@@ -420,6 +468,7 @@ def from_parallel_logits_to_logprobs_packed_sequences(
             logits, tgt, vocab_start_index, vocab_end_index, inference_only,
             reuse_logits_storage and chunk_size is not None,
         )
+    rows = probs
     probs = probs.squeeze(0)
     if return_packed_layout:
         return probs[:-1].unsqueeze(0)
@@ -428,7 +477,10 @@ def from_parallel_logits_to_logprobs_packed_sequences(
             f"cu_seqlens_padded ends at {bounds[-1]} but only {probs.shape[0]} packed rows were computed"
         )
     out_cols = max(int(unpacked_seqlen) - 1, 0)
-    return _UnpackRows.apply(probs, bdev, out_cols)
+    out = _UnpackRows.apply(probs, bdev, out_cols)
+    if out.grad_fn is not None:
+        out.grad_fn.src = rows.grad_fn  # for launch_early_backward
+    return out
 
 
 def _gather_or_zero(x: torch.Tensor, index: torch.Tensor) -> torch.Tensor:

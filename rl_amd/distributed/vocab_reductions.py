@@ -101,6 +101,13 @@ class ChunkedDistributedGatherLogprob(torch.autograd.Function):
             return torch.zeros_like(logits), None, None, None, None, None, None
         if grad_output.dtype != torch.float32:
             grad_output = grad_output.float()
+        early = getattr(ctx, "early", None)
+        if early is not None:
+            # launched by launch_early_backward: check it against the real gradient
+            ctx.early = None
+            grad_input, grad_used = early
+            _C.gather_logprob_bwd_recheck(logits, idx, vs, ve, stats, grad_output, grad_used, grad_input)
+            return grad_input, None, None, None, None, None, None
         grad_input = torch.empty_like(logits)
         _C.gather_logprob_bwd(logits, idx, vs, ve, stats, grad_output, grad_input)
         return grad_input, None, None, None, None, None, None
@@ -213,7 +220,12 @@ def next_token_and_sampler_topk_logprobs(
         logits, ids, rank * V, (rank + 1) * V, chunk_size if chunk_size is not None else S,
         vocab_parallel_group, False,
     )
-    return out[:, : S - 1, 0], out[:, : S - 1, 1:]
+    curr, plog = out[:, : S - 1, 0], out[:, : S - 1, 1:]
+    if out.grad_fn is not None:
+        # both views come from one gather node: launch_early_backward can start
+        # its backward once the loss knows the gradients of both
+        curr._mirl_gather_node = plog._mirl_gather_node = out.grad_fn
+    return curr, plog
 
 
 @torch.no_grad()

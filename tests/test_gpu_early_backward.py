@@ -94,3 +94,116 @@ def test_no_backward_releases_memory():
     del loss, lp, logits
     torch.cuda.synchronize()
     assert torch.cuda.memory_allocated(DEV) == base
+
+
+def _packed_setup(seed):
+    """A small packed batch: 4 sequences in one padded row, bf16 logits."""
+    from rl_amd.algorithms.loss.utils import _pack_input_ids
+
+    g = torch.Generator().manual_seed(seed)
+    lens, S, V = [37, 80, 5, 64], 96, 2048
+    B = len(lens)
+    cu, cu_pad = [0], [0]
+    for n in lens:
+        cu.append(cu[-1] + n)
+        cu_pad.append(cu_pad[-1] + -(-n // 8) * 8)
+    ids = torch.randint(0, V, (B, S), generator=g)
+    mask = (torch.arange(S)[None, :] < torch.tensor(lens)[:, None]).float()
+    d = {
+        "input_ids": ids.to(DEV),
+        "token_mask": mask.to(DEV),
+        "sample_mask": torch.ones(B, device=DEV),
+        "advantages": torch.randn(B, S, generator=g).to(DEV),
+        "prev_logprobs": (-3.0 + 0.1 * torch.randn(B, S, generator=g)).to(DEV),
+        "generation_logprobs": (-3.0 + 0.1 * torch.randn(B, S, generator=g)).to(DEV),
+        "logits": (1.5 * torch.randn(1, cu_pad[-1], V, generator=g)).to(torch.bfloat16).to(DEV),
+    }
+    d["packed_ids"] = _pack_input_ids(d["input_ids"], tuple(cu), tuple(cu_pad))
+    gvs = d["sample_mask"].sum()
+    gvt = (d["token_mask"][:, 1:]).sum()
+    return d, tuple(cu_pad), S, gvs, gvt
+
+
+def _packed_grad(d, cu_pad, S, gvs, gvt, early: bool, scale=1.0):
+    from rl_amd.distributed.model_utils import from_parallel_logits_to_logprobs_packed_sequences
+
+    logits = d["logits"].detach().clone().requires_grad_(True)
+    V = logits.shape[-1]
+    lp = from_parallel_logits_to_logprobs_packed_sequences(logits, d["packed_ids"], cu_pad, S, 0, V, None)
+    feed = lp if early else lp.clone()
+    fn = ClippedPGLossFn(ClippedPGLossConfig(reference_policy_kl_penalty=0.0))
+    loss, _ = fn(feed, d, gvs, gvt)
+    started = getattr(lp.grad_fn.src, "early", None) is not None
+    (g,) = torch.autograd.grad(loss * scale, [logits])
+    return g, started
+
+
+@pytest.mark.parametrize("scale", [1.0, 3.0])
+def test_packed_sequences_early_backward(scale):
+    """Packed logprobs: the early launch goes through the unpacking's backward; exact either way."""
+    say("early backward: packed", scale)
+    d, cu_pad, S, gvs, gvt = _packed_setup(7)
+    g1, started = _packed_grad(d, cu_pad, S, gvs, gvt, early=True, scale=scale)
+    g0, started0 = _packed_grad(d, cu_pad, S, gvs, gvt, early=False, scale=scale)
+    assert started and not started0
+    assert g0.abs().sum() > 0
+    assert torch.equal(g1, g0)
+
+
+def _sc_setup(seed):
+    """Score-centering inputs: next-token and 5 sampler-id logprobs from one K+1-id gather."""
+    from types import SimpleNamespace
+
+    from rl_amd.algorithms.loss import LossInputType, prepare_loss_input
+
+    d = workloads.score_centering_bf16(K=5, seed=seed, device=DEV, B=4, S=256, V=4096,
+                                       prompt_len=64, resp_min=64, resp_max=150)
+    probe = SimpleNamespace(input_type=LossInputType.LOGPROB, score_centering=True)
+    with torch.no_grad():
+        cur, _ = prepare_loss_input(d["logits"], {"input_ids": d["input_ids"],
+                                                  "sampler_topk_token_ids": d["sampler_topk_token_ids"],
+                                                  "sampler_topk_logprobs": d["sampler_noise"]}, probe)
+    d = workloads.finish_score_centering_step(d, cur["next_token_logprobs"], cur["policy_logprobs_at_sampler_topk"])
+    d["advantages"] = torch.randn(d["token_mask"].shape, device=DEV)
+    gvs = d["sample_mask"].sum()
+    gvt = (d["token_mask"][:, 1:] * d["sample_mask"][:, None]).sum()
+    return d, gvs, gvt
+
+
+def _sc_grad(d, gvs, gvt, early: bool, scale=1.0, extra=None):
+    from rl_amd.algorithms.loss import prepare_loss_input
+
+    logits = d["logits"].detach().clone().requires_grad_(True)
+    fn = ClippedPGLossFn(ClippedPGLossConfig(reference_policy_kl_penalty=0.0, score_centering=True))
+    batch = {k: d[k] for k in ("input_ids", "token_mask", "sample_mask", "prev_logprobs", "advantages",
+                               "generation_logprobs", "sampler_topk_token_ids", "sampler_topk_logprobs")}
+    li, _ = prepare_loss_input(logits, batch, fn)
+    node = li["next_token_logprobs"]._mirl_gather_node
+    if not early:
+        li = {k: v.clone() for k, v in li.items()}  # the clones are not the gather's views
+    loss, _ = fn(data=batch, global_valid_seqs=gvs, global_valid_toks=gvt, **li)
+    started = getattr(node, "early", None) is not None
+    total = loss * scale
+    if extra is not None:
+        total = total + (li["policy_logprobs_at_sampler_topk"] * extra).sum()
+    (g,) = torch.autograd.grad(total, [logits])
+    return g, started
+
+
+@pytest.mark.parametrize("case", ["plain", "scaled", "second-consumer"])
+def test_score_centering_gather_early_backward(case):
+    """The K+1-id gather's backward starts early from both gradients of the loss; the
+    gather's own backward checks it on the device and recomputes when the guess is wrong."""
+    say("early backward: score-centering gather", case)
+    d, gvs, gvt = _sc_setup(9)
+    kw = {}
+    if case == "scaled":
+        kw["scale"] = 0.25
+    elif case == "second-consumer":
+        B, S = d["input_ids"].shape
+        kw["extra"] = torch.randn(B, S - 1, 5, device=DEV) * 1e-3
+    g1, started = _sc_grad(d, gvs, gvt, early=True, **kw)
+    g0, started0 = _sc_grad(d, gvs, gvt, early=False, **kw)
+    assert started and not started0
+    assert g0.abs().sum() > 0
+    assert torch.equal(g1, g0)
