@@ -390,20 +390,23 @@ def bench_workload(args) -> None:
         ms_step, ms = _timed(step, args.steps, args.warmup, ["mirl_linear_ce_fwd", "mirl_linear_ce_grad"])
         rows = B * (S - 1)
         gemm = 2.0 * S * B * H * V  # one [S*B, H] x [H, V] product
+        # the backward runs the rows with a non-zero upstream gradient, chunk_size * B at a time
+        active = int((g != 0).sum().item())
         fwd_ms = ms.get("mirl_linear_ce_fwd", 0.0)
-        grad_chunks = -(-S // 256)
+        grad_chunks = -(-active // (256 * B))
         grad_ms = ms.get("mirl_linear_ce_grad", 0.0) * grad_chunks
+        gemm_act = 2.0 * active * H * V
         tflops = gemm / (fwd_ms * 1e-3) / 1e12 if fwd_ms > 0 else 0.0
         roof = {"kernel": "mirl_linear_ce_fwd", "bound": "mfma", "achieved": tflops, "peak": PEAK_BF16_TFLOPS,
                 "unit": "TFLOP/s", "frac": tflops / PEAK_BF16_TFLOPS, "traffic": _traffic(w),
                 "algorithmic_flops": gemm}
-        extra["tflops_step"] = 4 * gemm / (ms_step * 1e-3) / 1e12
+        extra["tflops_step"] = (gemm + 3 * gemm_act) / (ms_step * 1e-3) / 1e12
         extra["grad_kernel_ms_per_step"] = grad_ms
-        extra["grad_kernel_tflops_nominal"] = gemm / (grad_ms * 1e-3) / 1e12 if grad_ms > 0 else None
+        extra["grad_kernel_tflops"] = gemm_act / (grad_ms * 1e-3) / 1e12 if grad_ms > 0 else None
         step_bytes = None
         cfg = {"workload": "hidden_state_logprobs_fwd_bwd", "hidden": [S, B, H], "weight": [V, H],
-               "chunk_size": 256, "next_token_rows": rows,
-               "flops_per_step": "4 x 2*S*B*H*V (fused fwd, fused grad recompute, dH and dW GEMMs)"}
+               "chunk_size": 256, "next_token_rows": rows, "active_rows": active,
+               "flops_per_step": "2*S*B*H*V (fused fwd) + 3 x 2*active*H*V (fused grad recompute, dH, dW)"}
         dtype = "bf16"
     elif w == "distill_rkl":
         from rl_amd.distributed.model_utils import ChunkedDistributedReverseKLToFixedLogits

@@ -11,12 +11,13 @@ is ``[V, H]``; targets are ``[B, S]``.
   matmul output is) and reduces it to per-row partial log-sum-exps and the
   target logit; a merge kernel finishes each row.  The ``[S*B, V]`` logits are
   never materialised (the reference materialises an fp32 copy per chunk).
-* backward: per chunk of ``chunk_size`` sequence positions, a kernel
-  recomputes the logits tiles and writes ``G = (onehot - softmax) * g`` in
-  bf16 (tiles whose rows all have a zero upstream gradient are zero-filled
-  without the GEMM); ``dH = G . W`` and ``dW += G^T . H`` are plain library
-  GEMMs with fp32 accumulation (``dW`` accumulated in fp32 across chunks and
-  rounded once; the reference adds each chunk into a bf16 buffer).
+* backward: the rows with a non-zero upstream gradient are gathered (the
+  others have a zero logits gradient: zero dH rows, nothing added to dW);
+  per chunk of ``chunk_size * B`` of those rows a kernel recomputes the logits
+  tiles and writes ``G = (onehot - softmax) * g`` in bf16, and ``dH = G . W``
+  and ``dW += G^T . H`` are plain library GEMMs with fp32 accumulation (``dW``
+  accumulated in fp32 across chunks and rounded once; the reference adds each
+  chunk into a bf16 buffer).
 """
 
 from __future__ import annotations
@@ -97,20 +98,41 @@ class ChunkedDistributedHiddenStatesToLogprobs(torch.autograd.Function):
         if grad_output.dtype != torch.float32:
             grad_output = grad_output.float()
         h2 = hidden.view(T, H)
-        rows = T if ctx.chunk_size is None else min(T, ctx.chunk_size * B)
         need_h = ctx.needs_input_grad[0]
         need_w = ctx.needs_input_grad[2]
-        G = torch.empty((rows, V), dtype=torch.bfloat16, device=hidden.device)
-        dH = torch.empty((T, H), dtype=hidden.dtype, device=hidden.device) if need_h else None
-        dW = torch.zeros((V, H), dtype=torch.float32, device=hidden.device) if need_w else None
-        for r0 in range(0, T, rows):
-            n = min(rows, T - r0)
-            Gc = G[:n]
-            _C.linear_ce_grad(h2, weight, B, target, vs, ve, stats, grad_output, r0, Gc)
-            if need_h:
-                torch.matmul(Gc, weight, out=dH[r0 : r0 + n])
-            if need_w:
-                _accumulate_dw(dW, Gc, h2[r0 : r0 + n])
+        dev = hidden.device
+        # Rows whose upstream gradient is exactly zero (prompt, padding) have a
+        # zero logits gradient, so they add nothing to dW and their dH rows are
+        # zero: only the active rows are gathered and run through the gradient
+        # kernel and both GEMMs (one host synchronisation for their count).
+        g_rows = grad_output.t().reshape(T)  # row r = (s, b) is position s of sample b
+        active = torch.nonzero(g_rows != 0).squeeze(1)
+        n_act = active.numel()
+        dH = torch.zeros((T, H), dtype=hidden.dtype, device=dev) if need_h else None
+        dW = torch.zeros((V, H), dtype=torch.float32, device=dev) if need_w else None
+        if n_act > 0:
+            if n_act == T:
+                h_a, bsz, tgt_a, st_a, g_a = h2, B, target, stats, grad_output
+            else:
+                h_a = h2.index_select(0, active)
+                bsz = 1
+                tgt_a = target.t().reshape(T).index_select(0, active).view(1, n_act)
+                st_a = stats.index_select(0, active)
+                g_a = g_rows.index_select(0, active).view(1, n_act)
+            rows = n_act if ctx.chunk_size is None else min(n_act, ctx.chunk_size * B)
+            G = torch.empty((rows, V), dtype=torch.bfloat16, device=dev)
+            dH_a = dH if (need_h and n_act == T) else (
+                torch.empty((n_act, H), dtype=hidden.dtype, device=dev) if need_h else None)
+            for r0 in range(0, n_act, rows):
+                n = min(rows, n_act - r0)
+                Gc = G[:n]
+                _C.linear_ce_grad(h_a, weight, bsz, tgt_a, vs, ve, st_a, g_a, r0, Gc)
+                if need_h:
+                    torch.matmul(Gc, weight, out=dH_a[r0 : r0 + n])
+                if need_w:
+                    _accumulate_dw(dW, Gc, h_a[r0 : r0 + n])
+            if need_h and n_act < T:
+                dH.index_copy_(0, active, dH_a)
         grad_h = dH.view(S, B, H) if need_h else None
         grad_w = dW.to(weight.dtype) if need_w else None
         return grad_h, None, grad_w, None, None, None, None, None

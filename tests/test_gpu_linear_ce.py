@@ -158,3 +158,31 @@ def test_errors():
     with pytest.raises(ValueError):
         ChunkedDistributedHiddenStatesToLogprobs.apply(
             hidden.to(DEV), target.t().contiguous().to(DEV), weight.to(DEV), 0, 50, None, None, True)
+
+
+@pytest.mark.parametrize("pattern", ["none", "all", "scattered"])
+def test_gradient_row_compaction(pattern):
+    """The backward runs only rows with a non-zero upstream gradient: no such row (zero
+    gradients), every row (the uncompacted path) and scattered rows across chunks."""
+    say("linear-ce grad rows", pattern)
+    S, B, H, V = 40, 3, 128, 2000
+    hidden, weight, target = _inputs(S, B, H, V, seed=51)
+    gen = torch.Generator().manual_seed(52)
+    g = torch.randn(B, S, generator=gen)
+    if pattern == "none":
+        g.zero_()
+    elif pattern == "scattered":
+        g *= (torch.rand(B, S, generator=gen) < 0.3).float()
+    h = hidden.to(DEV).requires_grad_(True)
+    w = weight.to(DEV).requires_grad_(True)
+    lp = ChunkedDistributedHiddenStatesToLogprobs.apply(h, target.to(DEV), w, 0, V, 7, None, False)
+    dh, dw = torch.autograd.grad(lp, [h, w], g.to(DEV))
+    if pattern == "none":
+        assert not dh.any() and not dw.any()
+        return
+    rdh, rdw, _ = hidden_state_logprob_grads(hidden, target, weight, 0, V, g)
+    for got, ref in ((dh, rdh), (dw, rdw)):
+        err = (got.cpu().double() - ref).abs().max().item()
+        assert err <= 1e-2 * ref.abs().max().item(), (pattern, err)
+    zero_rows = (g == 0).t()  # [S, B], the layout of dh
+    assert not dh.cpu()[zero_rows].any()
