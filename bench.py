@@ -390,10 +390,13 @@ def bench_workload(args) -> None:
         ms_step, ms = _timed(step, args.steps, args.warmup, ["mirl_linear_ce_fwd", "mirl_linear_ce_grad"])
         rows = B * (S - 1)
         gemm = 2.0 * S * B * H * V  # one [S*B, H] x [H, V] product
-        # the backward runs the rows with a non-zero upstream gradient, chunk_size * B at a time
+        # the backward runs the rows with a non-zero upstream gradient, in blocks of
+        # _BLOCK_CHUNKS * chunk_size * B rows
+        from rl_amd.distributed.linear_ce import _BLOCK_CHUNKS
+
         active = int((g != 0).sum().item())
         fwd_ms = ms.get("mirl_linear_ce_fwd", 0.0)
-        grad_chunks = -(-active // (256 * B))
+        grad_chunks = -(-active // (_BLOCK_CHUNKS * 256 * B))
         grad_ms = ms.get("mirl_linear_ce_grad", 0.0) * grad_chunks
         gemm_act = 2.0 * active * H * V
         tflops = gemm / (fwd_ms * 1e-3) / 1e12 if fwd_ms > 0 else 0.0

@@ -13,11 +13,11 @@ is ``[V, H]``; targets are ``[B, S]``.
   never materialised (the reference materialises an fp32 copy per chunk).
 * backward: the rows with a non-zero upstream gradient are gathered (the
   others have a zero logits gradient: zero dH rows, nothing added to dW);
-  per chunk of ``chunk_size * B`` of those rows a kernel recomputes the logits
+  per block of up to ``4 * chunk_size * B`` of those rows a kernel recomputes the logits
   tiles and writes ``G = (onehot - softmax) * g`` in bf16, and ``dH = G . W``
   and ``dW += G^T . H`` are plain library GEMMs with fp32 accumulation (``dW``
-  accumulated in fp32 across chunks and rounded once; the reference adds each
-  chunk into a bf16 buffer).
+  accumulated in fp32 across blocks and rounded once, by the GEMM itself when
+  there is one block; the reference adds each chunk into a bf16 buffer).
 """
 
 from __future__ import annotations
@@ -109,7 +109,7 @@ class ChunkedDistributedHiddenStatesToLogprobs(torch.autograd.Function):
         active = torch.nonzero(g_rows != 0).squeeze(1)
         n_act = active.numel()
         dH = torch.zeros((T, H), dtype=hidden.dtype, device=dev) if need_h else None
-        dW = torch.zeros((V, H), dtype=torch.float32, device=dev) if need_w else None
+        dW = None
         if n_act > 0:
             if n_act == T:
                 h_a, bsz, tgt_a, st_a, g_a = h2, B, target, stats, grad_output
@@ -119,23 +119,45 @@ class ChunkedDistributedHiddenStatesToLogprobs(torch.autograd.Function):
                 tgt_a = target.t().reshape(T).index_select(0, active).view(1, n_act)
                 st_a = stats.index_select(0, active)
                 g_a = g_rows.index_select(0, active).view(1, n_act)
-            rows = n_act if ctx.chunk_size is None else min(n_act, ctx.chunk_size * B)
+            # Blocks of up to 4 chunks of rows: the bf16 G buffer (4 * chunk_size * B
+            # rows) stays below one reference chunk's fp32 logits, softmax and
+            # one-hot temporaries, and fewer, larger blocks cut dW's fp32
+            # read-modify-write passes and give the GEMMs larger shapes.
+            rows = n_act if ctx.chunk_size is None else min(n_act, _BLOCK_CHUNKS * ctx.chunk_size * B)
             G = torch.empty((rows, V), dtype=torch.bfloat16, device=dev)
             dH_a = dH if (need_h and n_act == T) else (
                 torch.empty((n_act, H), dtype=hidden.dtype, device=dev) if need_h else None)
+            # dH in sub-blocks of one chunk of rows: the library picks a markedly
+            # slower kernel for some large, uneven row counts (measured 0.76 vs
+            # 1.5 PFLOP/s at 5871 vs 2048 rows of [*, 151936] x [151936, 4096])
+            sub = rows if ctx.chunk_size is None else ctx.chunk_size * B
             for r0 in range(0, n_act, rows):
                 n = min(rows, n_act - r0)
                 Gc = G[:n]
                 _C.linear_ce_grad(h_a, weight, bsz, tgt_a, vs, ve, st_a, g_a, r0, Gc)
                 if need_h:
-                    torch.matmul(Gc, weight, out=dH_a[r0 : r0 + n])
+                    for q0 in range(0, n, sub):
+                        q1 = min(n, q0 + sub)
+                        torch.matmul(Gc[q0:q1], weight, out=dH_a[r0 + q0 : r0 + q1])
                 if need_w:
-                    _accumulate_dw(dW, Gc, h_a[r0 : r0 + n])
+                    if rows >= n_act:
+                        # one block: the GEMM accumulates in fp32 and rounds once to the
+                        # weight dtype itself
+                        dW = torch.mm(Gc.t(), h_a[r0 : r0 + n])
+                    elif dW is None:
+                        dW = torch.mm(Gc.t(), h_a[r0 : r0 + n], out_dtype=torch.float32)
+                    else:
+                        _accumulate_dw(dW, Gc, h_a[r0 : r0 + n])
             if need_h and n_act < T:
                 dH.index_copy_(0, active, dH_a)
+        if need_w and dW is None:
+            dW = torch.zeros((V, H), dtype=weight.dtype, device=dev)
         grad_h = dH.view(S, B, H) if need_h else None
-        grad_w = dW.to(weight.dtype) if need_w else None
+        grad_w = (dW if dW.dtype == weight.dtype else dW.to(weight.dtype)) if need_w else None
         return grad_h, None, grad_w, None, None, None, None, None
+
+
+_BLOCK_CHUNKS = 4  # chunks of active rows per backward block
 
 
 def _accumulate_dw(dW: torch.Tensor, G: torch.Tensor, h: torch.Tensor) -> None:
