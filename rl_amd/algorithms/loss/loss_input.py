@@ -176,6 +176,30 @@ def prepare_packed_loss_input(
     assert vocab_parallel_rank is not None, (
         "vocab_parallel_rank must be provided with vocab_parallel_group."
     )
+    return _prepare_packed(
+        logits, data, loss_fn, cu_seqlens_q, cu_seqlens_q_padded, vocab_parallel_rank,
+        vocab_parallel_group, context_parallel_group, sampling_params, chunk_size,
+        reuse_logits_storage,
+    )
+
+
+def _prepare_packed(
+    logits: torch.Tensor,
+    data: Any,
+    loss_fn: LossFunction,
+    cu_seqlens_q: CpuIntTuple,
+    cu_seqlens_q_padded: CpuIntTuple,
+    vocab_parallel_rank: Optional[int],
+    vocab_parallel_group: Optional[Any],
+    context_parallel_group: Optional[Any],
+    sampling_params: Optional[TrainingSamplingParams],
+    chunk_size: Optional[int],
+    reuse_logits_storage: bool,
+) -> tuple[dict[str, Any], Any]:
+    """prepare_packed_loss_input without its Megatron-only argument checks (a missing
+    vocab group is the single-device case: rank 0, the whole vocabulary)."""
+    if vocab_parallel_rank is None:
+        vocab_parallel_rank = 0
     if getattr(loss_fn, "score_centering", False):
         _validate_score_centering_data(data)
     cp_size = _group_size(context_parallel_group)

@@ -177,7 +177,8 @@ def test_fusion_wrapper_matches_per_sequence_wrapper(dtype, chunk_size, reuse, s
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=str)
 @pytest.mark.parametrize("sampling", [False, True], ids=["plain", "topk-topp"])
-def test_per_sequence_wrapper_one_pass_equals_per_sequence_calls(dtype, sampling, single_rank_group):
+@pytest.mark.parametrize("with_group", [True, False], ids=["group", "nogroup"])
+def test_per_sequence_wrapper_one_pass_equals_per_sequence_calls(dtype, sampling, with_group, single_rank_group):
     """The per-sequence wrapper takes every sequence's logprobs from one pass over the packed
     row and fetches all sequences' ClippedPG metrics with one copy; its loss, metrics and
     gradient equal a loop of the public per-sequence calls on narrowed logits (the
@@ -191,7 +192,10 @@ def test_per_sequence_wrapper_one_pass_equals_per_sequence_calls(dtype, sampling
     data = BatchedDataDict({k: v.to(DEV) for k, v in tc["data"].items()})
     loss_fn = ClippedPGLossFn(ClippedPGLossConfig(reference_policy_kl_penalty=0.01))
     sp = TrainingSamplingParams(top_k=8, top_p=0.9, temperature=1.0) if sampling else None
-    seq, _ = _wrappers(tc, loss_fn, single_rank_group, sampling_params=sp)
+    group = single_rank_group if with_group else None
+    seq, _ = _wrappers(tc, loss_fn, group, sampling_params=sp)
+    if not with_group:
+        seq.vocab_parallel_rank = None
     assert seq._packed_prepare_kwargs(tc["make"]()[1], data, [b - a for a, b in zip(tc["cu"][:-1], tc["cu"][1:])]) is not None
     l0, m0, g0, _ = _run(seq, tc, BatchedDataDict(dict(data)))
 
@@ -201,8 +205,8 @@ def test_per_sequence_wrapper_one_pass_equals_per_sequence_calls(dtype, sampling
     for i, (a, b) in enumerate(zip(cu_pad[:-1], cu_pad[1:])):
         L = cu[i + 1] - cu[i]
         sd = {k: (v[:, :L] if v.ndim > 1 and v.shape[1] > 1 else v) for k, v in data.slice(i, i + 1).items()}
-        li, sd = prepare_loss_input(packed.narrow(1, a, b - a), sd, loss_fn, 0, single_rank_group,
-                                    sampling_params=sp)
+        li, sd = prepare_loss_input(packed.narrow(1, a, b - a), sd, loss_fn, 0 if with_group else None,
+                                    group, sampling_params=sp)
         loss, m = loss_fn(data=sd, global_valid_seqs=tc["gvs"], global_valid_toks=tc["gvt"], **li)
         loss_acc = loss_acc + loss
         for k, v in m.items():
