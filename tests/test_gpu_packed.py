@@ -223,6 +223,43 @@ def test_per_sequence_wrapper_one_pass_equals_per_sequence_calls(dtype, sampling
         torch.testing.assert_close(g0, local.grad, rtol=1e-5, atol=1e-6)
 
 
+def test_per_sequence_wrapper_loop_path_single_fetch(single_rank_group):
+    """A preparation function other than prepare_loss_input keeps the per-sequence loop; the
+    ClippedPG losses' metrics still come back with one copy, and loss, metrics and gradient
+    equal the loop of public per-sequence calls bit for bit (same calls, same order)."""
+    print("[case] per-sequence wrapper loop path", flush=True)
+    from rl_amd.algorithms.loss.wrapper import _combine_metric
+
+    tc = _case(torch.bfloat16)
+    data = BatchedDataDict({k: v.to(DEV) for k, v in tc["data"].items()})
+    loss_fn = ClippedPGLossFn(ClippedPGLossConfig(reference_policy_kl_penalty=0.01))
+
+    def prep(**kw):  # not prepare_loss_input itself: the wrapper keeps its loop
+        return prepare_loss_input(**kw)
+
+    seq = SequencePackingLossWrapper(loss_fn=loss_fn, prepare_fn=prep, cu_seqlens_q=tc["cu"],
+                                     cu_seqlens_q_padded=tc["cu_pad"], vocab_parallel_rank=0,
+                                     vocab_parallel_group=single_rank_group)
+    assert seq._packed_prepare_kwargs(tc["make"]()[1], data, list(tc["lens"])) is None
+    l0, m0, g0, _ = _run(seq, tc, BatchedDataDict(dict(data)))
+    local, packed = tc["make"]()
+    cu, cu_pad = tc["cu"], tc["cu_pad"]
+    loss_acc, m_acc = 0, {}
+    for i, (a, b) in enumerate(zip(cu_pad[:-1], cu_pad[1:])):
+        L = cu[i + 1] - cu[i]
+        sd = {k: (v[:, :L] if v.ndim > 1 and v.shape[1] > 1 else v) for k, v in data.slice(i, i + 1).items()}
+        li, sd = prepare_loss_input(logits=packed.narrow(1, a, b - a), data=sd, loss_fn=loss_fn,
+                                    vocab_parallel_rank=0, vocab_parallel_group=single_rank_group)
+        loss, m = loss_fn(data=sd, global_valid_seqs=tc["gvs"], global_valid_toks=tc["gvt"], **li)
+        loss_acc = loss_acc + loss
+        for k, v in m.items():
+            _combine_metric(m_acc, k, v)
+    loss_acc.backward()
+    assert torch.equal(l0, loss_acc.detach())
+    assert m0 == m_acc
+    assert torch.equal(g0, local.grad)
+
+
 def test_fusion_wrapper_with_sampling_params(single_rank_group):
     print("[case] fusion vs baseline with sampling", flush=True)
     tc = _case(torch.float32)
