@@ -129,45 +129,62 @@ __device__ T block_sum(T v, T* scratch) {
   return r;
 }
 
+// Reductions of N values at once.  Value k is reduced with kind(k): a sum, or a
+// min / max that propagates NaN (torch's amin / amax).  Each value takes the
+// same xor butterfly inside a wave and the same wave order as a separate
+// block_sum would (the N shuffle chains interleave instead of running one after
+// the other behind two barriers each), so the results are bitwise the same.
+enum RedKind { R_SUM = 0, R_MIN = 1, R_MAX = 2 };
+
 template <class T>
-__device__ __forceinline__ T wave_min_t(T v) {
+__device__ __forceinline__ T red_combine(int kind, T a, T b) {
+  if (kind == R_MIN) return (b < a || isnan(b)) ? b : a;
+  if (kind == R_MAX) return (b > a || isnan(b)) ? b : a;
+  return a + b;
+}
+
+// Leaves wave w's result for value k in scratch[k * (NT / 64) + w]; scratch
+// holds N * (NT / 64) values.
+template <class T, int NT, int N, class Kind>
+__device__ __forceinline__ void block_exchange_n(T (&v)[N], Kind kind, T* scratch) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {
-    const T o = __shfl_xor(v, off, 64);
-    v = (o < v || isnan(o)) ? o : v;
-  }
-  return v;
-}
-template <class T>
-__device__ __forceinline__ T wave_max_t(T v) {
+    T o[N];
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    const T o = __shfl_xor(v, off, 64);
-    v = (o > v || isnan(o)) ? o : v;
+    for (int k = 0; k < N; ++k) o[k] = __shfl_xor(v[k], off, 64);
+#pragma unroll
+    for (int k = 0; k < N; ++k) v[k] = red_combine(kind(k), v[k], o[k]);
   }
-  return v;
-}
-template <class T, int NT>
-__device__ T block_min(T v, T* scratch) {
-  v = wave_min_t(v);
   const int lane = threadIdx.x % 64, wv = threadIdx.x / 64;
+  __syncthreads();  // an earlier reduction's readers are done with scratch
+  if (lane == 0) {
+#pragma unroll
+    for (int k = 0; k < N; ++k) scratch[k * (NT / 64) + wv] = v[k];
+  }
   __syncthreads();
-  if (lane == 0) scratch[wv] = v;
-  __syncthreads();
-  T r = scratch[0];
-  for (int k = 1; k < NT / 64; ++k) r = (scratch[k] < r || isnan(scratch[k])) ? scratch[k] : r;
+}
+
+// Workgroup total of value k over the wave partials left by block_exchange_n.
+template <class T, int NT>
+__device__ __forceinline__ T block_total(int kind, int k, const T* scratch) {
+  const T* p = scratch + k * (NT / 64);
+  T r = (kind == R_SUM) ? T(0) : p[0];
+  for (int w = (kind == R_SUM) ? 0 : 1; w < NT / 64; ++w) r = red_combine(kind, r, p[w]);
   return r;
 }
-template <class T, int NT>
-__device__ T block_max(T v, T* scratch) {
-  v = wave_max_t(v);
-  const int lane = threadIdx.x % 64, wv = threadIdx.x / 64;
-  __syncthreads();
-  if (lane == 0) scratch[wv] = v;
-  __syncthreads();
-  T r = scratch[0];
-  for (int k = 1; k < NT / 64; ++k) r = (scratch[k] > r || isnan(scratch[k])) ? scratch[k] : r;
-  return r;
+
+// N sums at once, every thread receiving every total.
+template <class T, int NT, int N>
+__device__ __forceinline__ void block_sum_n(T (&v)[N], T* scratch) {
+  block_exchange_n<T, NT, N>(v, [](int) { return int(R_SUM); }, scratch);
+#pragma unroll
+  for (int k = 0; k < N; ++k) v[k] = block_total<T, NT>(R_SUM, k, scratch);
+}
+
+__device__ __forceinline__ int slot_kind(int k) {
+  if (k == P_RATIO_MIN || k == P_RATIO_C_MIN) return R_MIN;
+  if (k == P_RATIO_MAX || k == P_RATIO_C_MAX) return R_MAX;
+  return R_SUM;
 }
 
 // Truncated importance sampling applied to one weight (loss_functions.py:921-1013).
@@ -299,7 +316,7 @@ __global__ __launch_bounds__(NT) void pg_rows_kernel(mirl_pg_config cfg, int64_t
                                                               T* __restrict__ gunf,
                                                               T* __restrict__ part,
                                                               ScWork<T> sc_ws, int has_sc) {
-  __shared__ T scratch[NT / 64];
+  __shared__ T scratch[NUM_SLOTS * (NT / 64)];
   const int64_t b = blockIdx.x;
   const int tid = threadIdx.x;
   const T eps = T(1e-8);
@@ -324,10 +341,14 @@ __global__ __launch_bounds__(NT) void pg_rows_kernel(mirl_pg_config cfg, int64_t
     sum_tm += tmv;
     sum_tm2 += tm2;
   }
-  any_tm = block_sum<T, NT>(any_tm, scratch);
-  any_tm2 = block_sum<T, NT>(any_tm2, scratch);
-  sum_tm = block_sum<T, NT>(sum_tm, scratch);
-  sum_tm2 = block_sum<T, NT>(sum_tm2, scratch);
+  {
+    T r[4] = {any_tm, any_tm2, sum_tm, sum_tm2};
+    block_sum_n<T, NT>(r, scratch);
+    any_tm = r[0];
+    any_tm2 = r[1];
+    sum_tm = r[2];
+    sum_tm2 = r[3];
+  }
   const T sm = in.sample_mask[b] * (any_tm > T(0) ? T(1) : T(0));
   const T sm2 = cfg.has_support_mask ? sm * (any_tm2 > T(0) ? T(1) : T(0)) : sm;
   // tokens of this row after the support adjustment (token_mask in the objective)
@@ -352,9 +373,11 @@ __global__ __launch_bounds__(NT) void pg_rows_kernel(mirl_pg_config cfg, int64_t
       seq_is += (pv - gv) * mask2;
       seq_lir += nan_to_zero_all(pv - gv) * tm2;
     }
-    seq_lr = block_sum<T, NT>(seq_lr, scratch);
-    seq_is = block_sum<T, NT>(seq_is, scratch);
-    seq_lir = block_sum<T, NT>(seq_lir, scratch);
+    T r[3] = {seq_lr, seq_is, seq_lir};
+    block_sum_n<T, NT>(r, scratch);
+    seq_lr = r[0];
+    seq_is = r[1];
+    seq_lir = r[2];
   }
   // clamp bounds are formed in double, as Python does, then rounded once
   const T lo = T(1.0 - cfg.ratio_clip_min);
@@ -566,23 +589,19 @@ __global__ __launch_bounds__(NT) void pg_rows_kernel(mirl_pg_config cfg, int64_t
 
   // ---- row partials ------------------------------------------------------
   T* out = part + b * NUM_SLOTS;
-#pragma unroll
-  for (int k = 0; k < NUM_SLOTS; ++k) {
-    T v;
-    if (k == P_RATIO_MIN || k == P_RATIO_C_MIN) v = block_min<T, NT>(acc[k], scratch);
-    else if (k == P_RATIO_MAX || k == P_RATIO_C_MAX) v = block_max<T, NT>(acc[k], scratch);
-    else v = block_sum<T, NT>(acc[k], scratch);
-    if (tid == 0) {
-      if ((k == P_ACTOR || k == P_SC) && !cfg.token_level_loss) v = sm2 * (v / actor_row_norm);
-      if (k == P_KL && !cfg.token_level_loss) v = sm * (v / kl_row_norm);
-      if (k == P_SIR && cfg.sequence_level_is) {
-        bool oob = false;
-        v = truncate_is(cfg, w_seq, T(0), seq_kept, &oob) * sm2;
-      }
-      if (k == P_NVS) v = sm2;
-      if (k == P_OOB && cfg.tis_type == MIRL_TIS_SEQ_MASK) v = (T(1) - seq_kept) * sm2;
-      out[k] = v;
+  block_exchange_n<T, NT, NUM_SLOTS>(acc, [](int k) { return slot_kind(k); }, scratch);
+  if (tid < NUM_SLOTS) {
+    const int k = tid;  // thread k finishes slot k
+    T v = block_total<T, NT>(slot_kind(k), k, scratch);
+    if ((k == P_ACTOR || k == P_SC) && !cfg.token_level_loss) v = sm2 * (v / actor_row_norm);
+    if (k == P_KL && !cfg.token_level_loss) v = sm * (v / kl_row_norm);
+    if (k == P_SIR && cfg.sequence_level_is) {
+      bool oob = false;
+      v = truncate_is(cfg, w_seq, T(0), seq_kept, &oob) * sm2;
     }
+    if (k == P_NVS) v = sm2;
+    if (k == P_OOB && cfg.tis_type == MIRL_TIS_SEQ_MASK) v = (T(1) - seq_kept) * sm2;
+    out[k] = v;
   }
 }
 

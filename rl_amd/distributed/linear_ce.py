@@ -80,7 +80,8 @@ class ChunkedDistributedHiddenStatesToLogprobs(torch.autograd.Function):
         stats = None
         if not inference_only:
             stats = torch.empty((S * B, 2), dtype=torch.float32, device=hidden.device)
-        _C.linear_ce_fwd(h2, weight, B, target, vocab_start_index, vocab_end_index, out, stats)
+        _C.linear_ce_fwd(_kernel_operand(h2), _kernel_operand(weight), B, target, vocab_start_index,
+                         vocab_end_index, out, stats)
         if not inference_only:
             ctx.save_for_backward(hidden, target, weight, stats)
             ctx.vocab = (int(vocab_start_index), int(vocab_end_index))
@@ -140,10 +141,11 @@ class ChunkedDistributedHiddenStatesToLogprobs(torch.autograd.Function):
             # A shorter last piece is moved back to end at the block's end and
             # overlaps the previous one (its rows are recomputed, not added).
             sub = rows if ctx.chunk_size is None else ctx.chunk_size * B
+            hk_a, wk = _kernel_operand(h_a), _kernel_operand(weight)
             for r0 in range(0, n_act, rows):
                 n = min(rows, n_act - r0)
                 Gc = G[:n]
-                _C.linear_ce_grad(h_a, weight, bsz, tgt_a, vs, ve, st_a, g_a, r0, Gc)
+                _C.linear_ce_grad(hk_a, wk, bsz, tgt_a, vs, ve, st_a, g_a, r0, Gc)
                 if need_h:
                     for q0 in range(0, n, sub):
                         q0 = max(0, min(q0, n - sub))
@@ -174,6 +176,25 @@ class ChunkedDistributedHiddenStatesToLogprobs(torch.autograd.Function):
 
 _BLOCK_CHUNKS = 4  # chunks of active rows per backward block
 _K_ALIGN = 128  # dW's reduction length is padded with zero rows to a multiple of this
+_H_ALIGN = 128  # the fused kernels step through the hidden dimension 128 elements at a time
+
+
+def _kernel_operand(x: torch.Tensor) -> torch.Tensor:
+    """``x [N, H]`` (bf16) as the fused kernels read it: ``H`` a multiple of 128, a row
+    stride that is a multiple of 8 elements (16 bytes) and a 16-byte-aligned start.
+
+    Other operands (small models' hidden sizes such as 64, sliced weights) are
+    copied into a zero-padded ``[N, round_up(H, 128)]`` buffer: the padding adds
+    exact zeros to every dot product, so the logits are the same sums.  The
+    library GEMMs of the backward take the unpadded tensors.
+    """
+    N, H = x.shape
+    if (H % _H_ALIGN == 0 and x.stride(-1) == 1 and x.stride(0) % 8 == 0 and x.stride(0) >= H
+            and x.data_ptr() % 16 == 0):
+        return x
+    out = torch.zeros((N, _round_up(H, _H_ALIGN)), dtype=x.dtype, device=x.device)
+    out[:, :H].copy_(x)
+    return out
 
 
 def _round_up(n: int, m: int) -> int:

@@ -21,7 +21,6 @@ from oracle.linear_ce import (
     logits_bf16,
     next_token_hidden_state_logprobs,
 )
-from rl_amd._C import MirlError
 from rl_amd.distributed.model_utils import (
     ChunkedDistributedHiddenStatesToLogprobs,
     from_parallel_hidden_states_to_logprobs,
@@ -58,7 +57,7 @@ def _target_logits(hidden, weight, target):
 
 
 @pytest.mark.parametrize("S,B,H,V", [(37, 3, 128, 1000), (16, 2, 256, 151936), (300, 1, 128, 4096),
-                                     (5, 4, 384, 257)])
+                                     (5, 4, 384, 257), (29, 2, 64, 1000), (9, 3, 192, 3001)])
 def test_forward_against_oracle(S, B, H, V):
     say("linear-ce fwd", S, B, H, V)
     hidden, weight, target = _inputs(S, B, H, V, seed=S + V)
@@ -145,12 +144,36 @@ def test_fused_matches_materialised_logits_path():
     _check_logprobs(fused, unfused.cpu(), x_t.cpu())
 
 
+@pytest.mark.parametrize("H", [64, 200])
+def test_unaligned_hidden_sizes_and_sliced_weight(H):
+    """Hidden sizes that are not a multiple of 128 (small models' 64) and a weight that is
+    a column slice of a wider matrix (row stride not a multiple of 8, unaligned start) run
+    through zero-padded copies; logprobs and both gradients match the oracle."""
+    say("linear-ce unaligned H", H)
+    S, B, V = 19, 3, 1234
+    hidden, weight, target = _inputs(S, B, H, V, seed=61 + H)
+    wide = torch.zeros(V, H + 3, dtype=torch.bfloat16)
+    wide[:, 1 : H + 1] = weight
+    g = torch.randn(B, S, generator=torch.Generator().manual_seed(62))
+    g[:, :4] = 0.0
+    h = hidden.to(DEV).requires_grad_(True)
+    wd = wide.to(DEV).requires_grad_(True)
+    w = wd[:, 1 : H + 1]
+    assert w.stride(0) % 8 != 0 and w.data_ptr() % 16 != 0
+    lp = ChunkedDistributedHiddenStatesToLogprobs.apply(h, target.to(DEV), w, 0, V, 5, None, False)
+    _check_logprobs(lp.detach(), hidden_state_logprobs(hidden, target, weight, 0, V),
+                    _target_logits(hidden, weight, target))
+    dh, dwide = torch.autograd.grad(lp, [h, wd], g.to(DEV))
+    dw = dwide[:, 1 : H + 1]
+    assert not dwide[:, 0].any() and not dwide[:, H + 1 :].any()
+    rdh, rdw, _ = hidden_state_logprob_grads(hidden, target, weight, 0, V, g)
+    for got, ref in ((dh, rdh), (dw, rdw)):
+        err = (got.cpu().double() - ref).abs().max().item()
+        assert err <= 1e-2 * ref.abs().max().item(), (err, ref.abs().max().item())
+
+
 def test_errors():
     say("linear-ce errors")
-    hidden, weight, target = _inputs(4, 2, 192, 50, seed=1)  # H = 192 is not a multiple of 128
-    with pytest.raises(MirlError):
-        ChunkedDistributedHiddenStatesToLogprobs.apply(
-            hidden.to(DEV), target.to(DEV), weight.to(DEV), 0, 50, None, None, True)
     hidden, weight, target = _inputs(4, 2, 128, 50, seed=1)
     with pytest.raises(NotImplementedError):
         ChunkedDistributedHiddenStatesToLogprobs.apply(
