@@ -242,10 +242,26 @@ __device__ void score_centering_token(const mirl_score_centering_args& sc, int64
   const T* pl = static_cast<const T*>(sc.plog) + b * sc.p_sb + l * sc.p_sl;
   const T* ql = static_cast<const T*>(sc.qlog) + b * sc.q_sb + l * sc.q_sl;
   const int64_t K = sc.K;
+  // The ids are read kChunk at a time, all loads of a chunk issued before any
+  // is used (one dependent load per id measured 15 us for 16 K tokens x 20 ids);
+  // sums still run in k order.
+  constexpr int kChunk = 8;
   T head = T(0), psum = T(0);
-  for (int64_t k = 0; k < K; ++k) {
-    head += dexp(ql[k * sc.q_sk]);
-    psum += dexp(pl[k * sc.p_sk]);
+  for (int64_t k0 = 0; k0 < K; k0 += kChunk) {
+    T qv[kChunk], pv[kChunk];
+#pragma unroll
+    for (int u = 0; u < kChunk; ++u) {
+      const int64_t k = k0 + u < K ? k0 + u : K - 1;
+      qv[u] = ql[k * sc.q_sk];
+      pv[u] = pl[k * sc.p_sk];
+    }
+#pragma unroll
+    for (int u = 0; u < kChunk; ++u) {
+      if (k0 + u < K) {
+        head += dexp(qv[u]);
+        psum += dexp(pv[u]);
+      }
+    }
   }
   // rho = clamp(1 - head, min=0) / clamp(1 - sum p, min=1e-6)
   T num = T(1) - head;
@@ -267,24 +283,36 @@ __device__ void score_centering_token(const mirl_score_centering_args& sc, int64
     default: alpha = adaptive_kept(T(1) / rho, A, lo, hi, outer) ? T(1) : T(0); break;
   }
   T term = T(0);
-  for (int64_t k = 0; k < K; ++k) {
-    const T plk = pl[k * sc.p_sk], qlk = ql[k * sc.q_sk];
-    const T p = dexp(plk), q = dexp(qlk);
-    T mass;
-    switch (sc.mode) {
-      case MIRL_SC_OFF: mass = q; break;
-      case MIRL_SC_IS: mass = p; break;
-      case MIRL_SC_TIS: mass = tminimum(tmaximum(p, lo * q), hi * q); break;
-      case MIRL_SC_ICEPOP: {
-        const T r = dexp(plk - qlk);
-        mass = (r >= lo && r <= hi) ? p : T(0);
-        break;
-      }
-      default: mass = adaptive_kept(dexp(plk - qlk), A, lo, hi, outer) ? p : T(0); break;
+  for (int64_t k0 = 0; k0 < K; k0 += kChunk) {
+    T pv[kChunk], qv[kChunk];
+#pragma unroll
+    for (int u = 0; u < kChunk; ++u) {
+      const int64_t k = k0 + u < K ? k0 + u : K - 1;
+      pv[u] = pl[k * sc.p_sk];
+      qv[u] = ql[k * sc.q_sk];
     }
-    const T coef = mass - alpha * p;
-    term += coef * plk;
-    out[k] = coef * scale;
+#pragma unroll
+    for (int u = 0; u < kChunk; ++u) {
+      const int64_t k = k0 + u;
+      if (k >= K) break;
+      const T plk = pv[u], qlk = qv[u];
+      const T p = dexp(plk), q = dexp(qlk);
+      T mass;
+      switch (sc.mode) {
+        case MIRL_SC_OFF: mass = q; break;
+        case MIRL_SC_IS: mass = p; break;
+        case MIRL_SC_TIS: mass = tminimum(tmaximum(p, lo * q), hi * q); break;
+        case MIRL_SC_ICEPOP: {
+          const T r = dexp(plk - qlk);
+          mass = (r >= lo && r <= hi) ? p : T(0);
+          break;
+        }
+        default: mass = adaptive_kept(dexp(plk - qlk), A, lo, hi, outer) ? p : T(0); break;
+      }
+      const T coef = mass - alpha * p;
+      term += coef * plk;
+      out[k] = coef * scale;
+    }
   }
   *term_out = term;
   *head_out = head;
@@ -692,14 +720,18 @@ __global__ __launch_bounds__(kFinalThreads) void pg_final_kernel(mirl_pg_config 
 // compute_score_centering_term over [B, L] tokens, one thread per token.
 // Tokens with token_mask == 0 (or, when `sample_mask` is given, in a sample
 // whose mask is 0) get zero term, head mass and coefficients.
+// 64 threads per workgroup: one token per thread, spread over as many CUs as
+// there are 64-token groups.
+constexpr int kScTermThreads = 64;
+
 template <class T>
-__global__ __launch_bounds__(256) void sc_term_kernel(mirl_score_centering_args sc, int64_t B,
+__global__ __launch_bounds__(kScTermThreads) void sc_term_kernel(mirl_score_centering_args sc, int64_t B,
                                                       int64_t L, View<T> tm,
                                                       const T* __restrict__ sample_mask,
                                                       View<T> adv, int has_adv,
                                                       T* __restrict__ term,
                                                       T* __restrict__ head) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t i = (int64_t)blockIdx.x * kScTermThreads + threadIdx.x;
   if (i >= B * L) return;
   const int64_t b = i / L, l = i - b * L;
   T* coef = static_cast<T*>(sc.grad) + i * sc.K;
@@ -757,7 +789,8 @@ int run(const mirl_pg_config* cfg, int64_t B, int64_t L, const mirl_view2d* v,
     scw.head = scw.term + n;
     scw.scale = scw.head + n;
     if (n > 0)
-      hipLaunchKernelGGL((sc_term_kernel<T>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+      hipLaunchKernelGGL((sc_term_kernel<T>), dim3((unsigned)((n + kScTermThreads - 1) / kScTermThreads)),
+                         dim3(kScTermThreads), 0, st,
                          *sc, B, L, in.tm, in.sample_mask, in.adv, 1, scw.term, scw.head);
   }
   hipLaunchKernelGGL((pg_rows_kernel<T, row_threads<T>()>), dim3((unsigned)B), dim3(row_threads<T>()), 0, st, *cfg, L, in,
@@ -780,7 +813,8 @@ int run_sc_term(int64_t B, int64_t L, const mirl_score_centering_args* sc, mirl_
   const int64_t n = B * L;
   View<T> tmv{static_cast<const T*>(tm.ptr), tm.sb, tm.sl};
   View<T> av{static_cast<const T*>(adv.ptr), adv.sb, adv.sl};
-  hipLaunchKernelGGL((sc_term_kernel<T>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, *sc,
+  hipLaunchKernelGGL((sc_term_kernel<T>), dim3((unsigned)((n + kScTermThreads - 1) / kScTermThreads)),
+                         dim3(kScTermThreads), 0, st, *sc,
                      B, L, tmv, static_cast<const T*>(nullptr), av, adv.ptr != nullptr ? 1 : 0,
                      static_cast<T*>(term), static_cast<T*>(head));
   return check_launch("mirl_score_centering_term");

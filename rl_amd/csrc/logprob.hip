@@ -406,12 +406,15 @@ __global__ __launch_bounds__(kFlatThreads) void logprob_bwd_flat_kernel(
 // round in front of every piece's logits load cuts the bytes in flight.)
 //
 // `flags` (nflags ints, or null) makes a launch conditional: it does nothing
-// unless some flag is set (the early-backward recheck's redo).
+// unless some flag is set (the early-backward recheck's redo).  Each thread
+// loads at most a few flags and the workgroup ORs them in one barrier (a
+// serial loop over 64 flags per thread measured 13 us for a launch that then
+// did nothing); every thread of the workgroup must call it.
 __device__ __forceinline__ bool any_flag(const int* __restrict__ flags, int nflags) {
   if (flags == nullptr) return true;
-  int any = 0;
-  for (int k = 0; k < nflags; ++k) any |= flags[k];
-  return any != 0;
+  int v = 0;
+  for (int k = threadIdx.x; k < nflags; k += blockDim.x) v |= flags[k];
+  return __syncthreads_or(v) != 0;
 }
 
 __global__ __launch_bounds__(256) void gather_gsum_kernel(const float* __restrict__ g, int64_t R,
@@ -420,7 +423,7 @@ __global__ __launch_bounds__(256) void gather_gsum_kernel(const float* __restric
                                                          float* __restrict__ gsum,
                                                          const int* __restrict__ flags, int nflags) {
   const int64_t row = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (row >= rows || !any_flag(flags, nflags)) return;
+  if (!any_flag(flags, nflags) || row >= rows) return;
   const int64_t b = row / R, r = row - b * R;
   const float* gr = g + b * gsb + r * gsr;
   float s = 0.f;
@@ -442,7 +445,7 @@ __global__ __launch_bounds__(256) void gather_fixup_kernel(
     typename E::raw* gin, int64_t gisb, int64_t gisr, int64_t total,
     const int* __restrict__ flags, int nflags) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= total || !any_flag(flags, nflags)) return;
+  if (!any_flag(flags, nflags) || i >= total) return;
   const int64_t row = i / K, k = i - row * K;
   const int64_t b = row / R, r = row - b * R;
   const int64_t* ir = idx + b * isb + r * isr;
@@ -458,6 +461,71 @@ __global__ __launch_bounds__(256) void gather_fixup_kernel(
   for (int64_t j = k; j < K; ++j)
     if (ir[j * isk] == t) o += gr[j * gsk];
   gin[b * gisb + r * gisr + tl] = E::from_float(o);
+}
+
+// The same fix-up with one wave per row, for K <= 64: lane k holds id_k and
+// g_k, and the duplicate test and the in-order sum over equal ids read the
+// other lanes' values through cross-lane shuffles instead of up to K dependent
+// loads per thread (the per-(row, k) kernel above measured 25 us on the
+// [8, 2048] rows with 21 ids).  Same arithmetic in the same order.
+constexpr int kFixupRowsPerBlock = 4;
+
+template <class E>
+__global__ __launch_bounds__(64 * kFixupRowsPerBlock) void gather_fixup_wave_kernel(
+    const typename E::raw* __restrict__ logits, int64_t R, int64_t V, int64_t sb, int64_t sr,
+    const int64_t* __restrict__ idx, int64_t K, int64_t isb, int64_t isr, int64_t isk,
+    int64_t vs, int64_t ve, const float* __restrict__ stats, const float* __restrict__ g,
+    int64_t gsb, int64_t gsr, int64_t gsk, const float* __restrict__ gsum,
+    typename E::raw* gin, int64_t gisb, int64_t gisr, int64_t rows,
+    const int* __restrict__ flags, int nflags) {
+  const int64_t row = (int64_t)blockIdx.x * kFixupRowsPerBlock + threadIdx.x / 64;
+  const int lane = threadIdx.x % 64;
+  // both conditions are uniform over the wave, so every shuffle below sees all 64 lanes
+  if (!any_flag(flags, nflags) || row >= rows) return;
+  const int64_t b = row / R, r = row - b * R;
+  const int64_t* ir = idx + b * isb + r * isr;
+  const float* gr = g + b * gsb + r * gsr;
+  const bool has = lane < K;
+  const int64_t t = has ? ir[lane * isk] : int64_t(-1);
+  const float gk = has ? gr[lane * gsk] : 0.f;
+  const bool in_range = has && !(t < vs || t >= ve || t - vs >= V);
+  float o = 0.f;
+  if (in_range) {
+    const float M = stats[2 * row], LS = stats[2 * row + 1];
+    const float xv = E::load(logits + b * sb + r * sr + (t - vs));
+    o = fast_exp2(((xv - M) - LS) * kLog2e) * (-gsum[row]);
+  }
+  bool first = in_range;
+  const int tlo = (int)(uint32_t)(uint64_t)t, thi = (int)(uint32_t)((uint64_t)t >> 32);
+  for (int j = 0; j < (int)K; ++j) {
+    const int jlo = __shfl(tlo, j, 64), jhi = __shfl(thi, j, 64);
+    const float gj = __shfl(gk, j, 64);
+    const bool same = (jlo == tlo) && (jhi == thi);
+    if (same && j < lane) first = false;  // an earlier k holds the same id
+    if (same && j >= lane) o += gj;       // scatter_add order: k, then later equal ids
+  }
+  if (first) gin[b * gisb + r * gisr + (t - vs)] = E::from_float(o);
+}
+
+template <class E>
+void launch_gather_fixup(int64_t rows, hipStream_t st, const typename E::raw* logits, int64_t R,
+                         int64_t V, int64_t sb, int64_t sr, const int64_t* idx, int64_t K,
+                         int64_t isb, int64_t isr, int64_t isk, int64_t vs, int64_t ve,
+                         const float* stats, const float* g, int64_t gsb, int64_t gsr,
+                         int64_t gsk, const float* gsum, typename E::raw* gin, int64_t gisb,
+                         int64_t gisr, const int* flags, int nflags) {
+  if (K <= 64) {
+    const int64_t grid = (rows + kFixupRowsPerBlock - 1) / kFixupRowsPerBlock;
+    hipLaunchKernelGGL((gather_fixup_wave_kernel<E>), dim3((unsigned)grid),
+                       dim3(64 * kFixupRowsPerBlock), 0, st, logits, R, V, sb, sr, idx, K, isb,
+                       isr, isk, vs, ve, stats, g, gsb, gsr, gsk, gsum, gin, gisb, gisr, rows,
+                       flags, nflags);
+    return;
+  }
+  const int64_t total = rows * K;
+  hipLaunchKernelGGL((gather_fixup_kernel<E>), dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                     st, logits, R, V, sb, sr, idx, K, isb, isr, isk, vs, ve, stats, g, gsb, gsr,
+                     gsk, gsum, gin, gisb, gisr, total, flags, nflags);
 }
 
 // Early-backward check.  A caller that knows the upstream gradient in closed
@@ -501,9 +569,7 @@ __global__ __launch_bounds__(256) void bwd_redo_kernel(
     int64_t ve, const float* __restrict__ stats, const float* __restrict__ g, int64_t gsb,
     int64_t gsr, typename E::raw* gin, int64_t gisb, int64_t gisr, int64_t rows,
     const int* __restrict__ flags, int nflags) {
-  int any = 0;
-  for (int k = 0; k < nflags; ++k) any |= flags[k];
-  if (any == 0) return;
+  if (!any_flag(flags, nflags)) return;
   for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
     const int64_t b = row / Rt, r = row - b * Rt;
     typename E::raw* y = gin + b * gisb + r * gisr;
@@ -634,10 +700,9 @@ void gather_bwd(int64_t rows, hipStream_t st, const void* logits, int64_t R, int
                   gin, gisb, gisr);
   const int64_t total = rows * K;
   if (total == 0) return;
-  hipLaunchKernelGGL((gather_fixup_kernel<E>), dim3((unsigned)((total + 255) / 256)), dim3(256),
-                     0, st, static_cast<const typename E::raw*>(logits), R, V, sb, sr, idx, K, isb,
-                     isr, isk, vs, ve, stats, g, gsb, gsr, gsk, gsum,
-                     static_cast<typename E::raw*>(gin), gisb, gisr, total, nullptr, 0);
+  launch_gather_fixup<E>(rows, st, static_cast<const typename E::raw*>(logits), R, V, sb, sr, idx,
+                         K, isb, isr, isk, vs, ve, stats, g, gsb, gsr, gsk, gsum,
+                         static_cast<typename E::raw*>(gin), gisb, gisr, nullptr, 0);
 }
 
 // The K-id gather's early-backward recheck: gather_check_kernel compares the
@@ -645,24 +710,39 @@ void gather_bwd(int64_t rows, hipStream_t st, const void* logits, int64_t R, int
 // in bwd_check_kernel), then the three backward parts run again, each launch
 // returning at once unless a flag is set.  The dense part's redo is
 // bwd_redo_kernel with no target, whose arithmetic equals the flat kernel's.
-__global__ __launch_bounds__(256) void gather_check_kernel(
+constexpr int kGatherCheckThreads = 1024;
+
+__global__ __launch_bounds__(kGatherCheckThreads) void gather_check_kernel(
     const float* __restrict__ g, int64_t R, int64_t K, int64_t gsb, int64_t gsr, int64_t gsk,
     const float* __restrict__ g_used, int64_t n, int* __restrict__ flags) {
-  __shared__ int s_any[4];
+  constexpr int NT = kGatherCheckThreads, U = 4;  // U loads in flight per thread
   int any = 0;
   const int64_t per = (n + gridDim.x - 1) / gridDim.x;
   const int64_t i0 = (int64_t)blockIdx.x * per;
   const int64_t i1 = (i0 + per < n) ? i0 + per : n;
-  for (int64_t i = i0 + threadIdx.x; i < i1; i += 256) {
-    const int64_t row = i / K, k = i - row * K;
-    const int64_t b = row / R, r = row - b * R;
-    any |= (__float_as_uint(g[b * gsb + r * gsr + k * gsk]) != __float_as_uint(g_used[i])) ? 1 : 0;
+  const bool flat = gsk == 1 && gsr == K && gsb == R * K;  // g laid out like g_used
+  for (int64_t i = i0 + threadIdx.x; i < i1; i += U * NT) {
+    float a[U], c[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t j = i + u * NT;
+      a[u] = c[u] = 0.f;
+      if (j < i1) {
+        int64_t off = j;
+        if (!flat) {
+          const int64_t row = j / K, k = j - row * K;
+          const int64_t b = row / R, r = row - b * R;
+          off = b * gsb + r * gsr + k * gsk;
+        }
+        a[u] = g[off];
+        c[u] = g_used[j];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) any |= (__float_as_uint(a[u]) != __float_as_uint(c[u])) ? 1 : 0;
   }
-  const int wv = threadIdx.x / 64, lane = threadIdx.x % 64;
-  const bool w = __ballot(any != 0) != 0ull;
-  if (lane == 0) s_any[wv] = w ? 1 : 0;
-  __syncthreads();
-  if (threadIdx.x == 0) flags[blockIdx.x] = s_any[0] | s_any[1] | s_any[2] | s_any[3];
+  any = __syncthreads_or(any);
+  if (threadIdx.x == 0) flags[blockIdx.x] = any != 0 ? 1 : 0;
 }
 
 template <class E>
@@ -674,8 +754,8 @@ void gather_bwd_recheck(int64_t rows, hipStream_t st, const void* logits, int64_
   using raw = typename E::raw;
   const int64_t total = rows * K;
   const int nflags = (int)(total < kCheckBlocks ? total : kCheckBlocks);
-  hipLaunchKernelGGL(gather_check_kernel, dim3((unsigned)nflags), dim3(256), 0, st, g, R, K, gsb,
-                     gsr, gsk, g_used, total, flags);
+  hipLaunchKernelGGL(gather_check_kernel, dim3((unsigned)nflags), dim3(kGatherCheckThreads), 0, st,
+                     g, R, K, gsb, gsr, gsk, g_used, total, flags);
   hipLaunchKernelGGL(gather_gsum_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, st,
                      g, R, gsb, gsr, gsk, K, rows, gsum, flags, nflags);
   const unsigned grid = (unsigned)(rows < 1024 ? rows : 1024);
@@ -683,10 +763,9 @@ void gather_bwd_recheck(int64_t rows, hipStream_t st, const void* logits, int64_
                      static_cast<const raw*>(logits), R, R, V, sb, sr, idx, isb, isr, (int64_t)0,
                      (int64_t)0, stats, gsum, R, (int64_t)1, static_cast<raw*>(gin), gisb, gisr,
                      rows, flags, nflags);
-  hipLaunchKernelGGL((gather_fixup_kernel<E>), dim3((unsigned)((total + 255) / 256)), dim3(256),
-                     0, st, static_cast<const raw*>(logits), R, V, sb, sr, idx, K, isb, isr, isk,
-                     vs, ve, stats, g, gsb, gsr, gsk, gsum, static_cast<raw*>(gin), gisb, gisr,
-                     total, flags, nflags);
+  launch_gather_fixup<E>(rows, st, static_cast<const raw*>(logits), R, V, sb, sr, idx, K, isb, isr,
+                         isk, vs, ve, stats, g, gsb, gsr, gsk, gsum, static_cast<raw*>(gin), gisb,
+                         gisr, flags, nflags);
 }
 
 int check_dtype(int dtype) {

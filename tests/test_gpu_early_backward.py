@@ -72,10 +72,17 @@ def test_scaled_loss_recomputes(scale):
     assert torch.equal(g1, g0)
 
 
-def test_second_consumer_recomputes():
-    say("early backward: second consumer")
+@pytest.mark.parametrize("where", ["all", "first", "last"])
+def test_second_consumer_recomputes(where):
+    """A second consumer of every logprob, or of only the first or the last one (a
+    difference that only one checking workgroup sees)."""
+    say("early backward: second consumer", where)
     d, gvs, gvt = _setup(5)
     w = torch.randn(d["input_ids"].shape[0], d["input_ids"].shape[1] - 1, device=DEV) * 1e-3
+    if where != "all":
+        keep = torch.zeros_like(w)
+        keep.view(-1)[0 if where == "first" else -1] = 1.0
+        w = w * keep
     g1, started = _grad(d, gvs, gvt, early=True, extra=w)
     g0, _ = _grad(d, gvs, gvt, early=False, extra=w)
     assert started
@@ -190,7 +197,7 @@ def _sc_grad(d, gvs, gvt, early: bool, scale=1.0, extra=None):
     return g, started
 
 
-@pytest.mark.parametrize("case", ["plain", "scaled", "second-consumer"])
+@pytest.mark.parametrize("case", ["plain", "scaled", "second-consumer", "one-id"])
 def test_score_centering_gather_early_backward(case):
     """The K+1-id gather's backward starts early from both gradients of the loss; the
     gather's own backward checks it on the device and recomputes when the guess is wrong."""
@@ -202,6 +209,12 @@ def test_score_centering_gather_early_backward(case):
     elif case == "second-consumer":
         B, S = d["input_ids"].shape
         kw["extra"] = torch.randn(B, S - 1, 5, device=DEV) * 1e-3
+    elif case == "one-id":
+        # one sampler id of the last token: only the last checking workgroup sees it
+        B, S = d["input_ids"].shape
+        extra = torch.zeros(B, S - 1, 5, device=DEV)
+        extra[-1, -1, -1] = 1e-3
+        kw["extra"] = extra
     g1, started = _sc_grad(d, gvs, gvt, early=True, **kw)
     g0, started0 = _sc_grad(d, gvs, gvt, early=False, **kw)
     assert started and not started0

@@ -55,7 +55,7 @@ def _check_grad(got, ref, dtype):
 @pytest.mark.parametrize("dtype,V", [(torch.float32, 997), (torch.bfloat16, 1000),
                                      (torch.bfloat16, 1003), (torch.float16, 512),
                                      (torch.bfloat16, 151936)])
-@pytest.mark.parametrize("K", [1, 5, 20, 70])
+@pytest.mark.parametrize("K", [1, 5, 20, 64, 70])
 def test_gather_fwd_bwd_parity(dtype, V, K):
     say("gather", dtype, "V", V, "K", K)
     g = torch.Generator().manual_seed(V + K)
@@ -64,6 +64,7 @@ def test_gather_fwd_bwd_parity(dtype, V, K):
     idx = torch.randint(0, V, (B, S, K), generator=g)
     if K >= 5:
         idx[0, 0, :3] = idx[0, 0, 0]          # repeated ids accumulate
+        idx[0, 1, K - 1] = idx[0, 1, 0]       # ... also from the first to the last k
         idx[1, 3, 1] = V + 7                  # out of range: 0 out, no scatter term
         idx[1, 4, 0] = -3
     go = torch.randn(B, S, K, generator=g)
