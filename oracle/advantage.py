@@ -11,8 +11,13 @@ from __future__ import annotations
 import torch
 
 
-def baseline_and_std_per_prompt(prompts, rewards, valid_mask, leave_one_out_baseline=True):
-    """Returns (baseline, std, is_trivial) per sample, fp32 matmul formulation of the reference."""
+def baseline_and_std_per_prompt(prompts, rewards, valid_mask, leave_one_out_baseline=True, std_rewards=None):
+    """Returns (baseline, std, is_trivial) per sample, fp32 matmul formulation of the reference.
+
+    ``std_rewards`` (reference utils.py:161-162, 190-203) replaces the rewards in the
+    spread (std) and in the trivial-group test; the baseline stays on ``rewards``.
+    """
+    q_all = rewards if std_rewards is None else std_rewards
     baseline = torch.zeros_like(rewards)
     std = torch.zeros_like(rewards)
     trivial = torch.ones_like(rewards, dtype=torch.bool)
@@ -26,14 +31,16 @@ def baseline_and_std_per_prompt(prompts, rewards, valid_mask, leave_one_out_base
             continue
         nv = v.float().sum() - int(leave_one_out_baseline)
         b = torch.matmul(M, rewards[idx] * v) / nv
-        sq = torch.matmul(M, torch.pow(rewards[idx], 2) * v) / nv
+        q = q_all[idx]
+        bq = b if std_rewards is None else torch.matmul(M, q * v) / nv
+        sq = torch.matmul(M, torch.pow(q, 2) * v) / nv
         comp = M.bool() & v.bool().unsqueeze(0)
-        rr = rewards[idx].unsqueeze(0).expand(n, -1)
+        rr = q.unsqueeze(0).expand(n, -1)
         cmin = rr.masked_fill(~comp, torch.inf).amin(dim=1)
         cmax = rr.masked_fill(~comp, -torch.inf).amax(dim=1)
         baseline[idx] = b
         trivial[idx] = cmin == cmax
-        std[idx] = ((sq - b.square()) * (nv / (nv - 1))).sqrt().nan_to_num(0)
+        std[idx] = ((sq - bq.square()) * (nv / (nv - 1))).sqrt().nan_to_num(0)
     return baseline, std, trivial
 
 

@@ -62,3 +62,57 @@ def assert_close_or_ulp_bf16(actual: torch.Tensor, expected: torch.Tensor, atol:
         ulps = (ai - ei).abs()
         assert int(ulps.max()) <= 1, f"{int(bad.sum())} elements off by more than 1 bf16 ulp"
     return int(bad.sum())
+
+
+# Known answers of calculate_baseline_and_std_per_prompt from the reference's own tests
+# (tests/unit/algorithms/test_utils.py): prompts, rewards, valid mask, leave-one-out flag,
+# std_rewards, then the expected baseline, std and trivial flags (None = not pinned there).
+_P23 = [[1, 2, 3], [4, 5, 6]]
+ADVANTAGE_KNOWN_ANSWERS = [
+    ("basic:830", [_P23[0]] * 3 + [_P23[1]] * 3, [1.0, 2, 3, 4, 5, 6], [1.0] * 6, True, None,
+     [2.5, 2.0, 1.5, 5.5, 5.0, 4.5], [0.707107, 1.414214, 0.707107] * 2, None),
+    ("single_generation:859", _P23, [2.5, 4.0], [1.0, 1.0], True, None, [2.5, 4.0], [0.0, 0.0], None),
+    ("identical_rewards:883", [_P23[0]] * 3 + [_P23[1]] * 3, [3.0, 3, 3, 7, 7, 7], [1.0] * 6, True, None,
+     [3.0, 3, 3, 7, 7, 7], [0.0] * 6, [True] * 6),
+    ("trivial_leave_one_out:911", [[0]] * 8, [0.0] + [0.95] * 7, [1.0] * 8, True, None,
+     None, None, [True] + [False] * 7),
+    ("trivial_full_group_without_loo:974", [[0]] * 8, [0.0] + [0.95] * 7, [1.0] * 8, False, None,
+     None, None, [False] * 8),
+    ("trivial_from_std_rewards:954", [[0]] * 3 + [[1]] * 3, [0.0, -0.2, -1.0, 1.0, 0.0, 1.0], [1.0] * 6, False,
+     [0.0, 0.0, 0.0, 1.0, 0.0, 1.0], None, [0.0, 0.0, 0.0, None, None, None], [True] * 3 + [False] * 3),
+    ("mixed_prompt_sizes:991", [_P23[0]] * 2 + [_P23[1]] * 3, [1.0, 2, 4, 5, 6], [1.0] * 5, True, None,
+     [2.0, 1.0, 5.5, 5.0, 4.5], [0.0, 0.0, 0.707107, 1.414214, 0.707107], None),
+    ("masked_sample:1034", [_P23[0]] * 3 + [_P23[1]] * 3, [1.0, 999, 3, 4, 5, 6], [1.0, 0, 1, 1, 1, 1], True,
+     None, [3.0, 4.0, 1.0, 5.5, 5.0, 4.5], [0.0, 0.0, 0.0, 0.707107, 1.414214, 0.707107], None),
+    ("two_per_prompt:1063", [_P23[0]] * 2 + [_P23[1]] * 2, [1.0, 2, 3, 4], [1.0] * 4, True, None,
+     [2.0, 1.0, 4.0, 3.0], [0.0] * 4, None),
+    ("numerical_precision:1095", [_P23[0]] * 3 + [_P23[1]] * 3, [1e-8, 2e-8, 3e-8, 1e8, 2e8, 3e8], [1.0] * 6,
+     True, None, [2.5e-8, 2e-8, 1.5e-8, 2.5e8, 2e8, 1.5e8], None, None),
+]
+
+
+def check_advantage_known_answer(case, baseline, std, trivial) -> None:
+    """Compares one result of calculate_baseline_and_std_per_prompt with a known answer
+    (rtol 1e-5, as the reference's tests; std must be finite everywhere)."""
+    name, _, _, _, _, _, eb, es, et = case
+    baseline, std, trivial = baseline.cpu().double(), std.cpu().double(), trivial.cpu()
+    assert torch.isfinite(std).all(), name
+    if eb is not None:
+        assert torch.allclose(baseline, torch.tensor(eb, dtype=torch.float64), rtol=1e-5), (name, baseline)
+    if es is not None:
+        for i, e in enumerate(es):
+            if e is None:
+                assert std[i] > 0, (name, i, std)
+            else:
+                assert abs(std[i].item() - e) <= 1e-5 * abs(e) + 1e-8, (name, i, std)
+    if et is not None:
+        assert trivial.tolist() == et, (name, trivial)
+
+
+def advantage_case_inputs(case, device="cpu"):
+    _, prompts, rewards, valid, loo, std_rewards, _, _, _ = case
+    p = torch.tensor(prompts, dtype=torch.long, device=device)
+    r = torch.tensor(rewards, dtype=torch.float32, device=device)
+    v = torch.tensor(valid, dtype=torch.float32, device=device)
+    q = None if std_rewards is None else torch.tensor(std_rewards, dtype=torch.float32, device=device)
+    return p, r, v, loo, q

@@ -6,6 +6,7 @@ import torch
 from oracle.advantage import baseline_and_std_per_prompt, grpo_advantages
 from rl_amd.algorithms.advantage_estimator import AdvEstimatorConfig, GRPOAdvantageEstimator
 from rl_amd.algorithms.utils import calculate_baseline_and_std_per_prompt
+from tests.helpers import ADVANTAGE_KNOWN_ANSWERS, advantage_case_inputs, check_advantage_known_answer
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda", 0)
@@ -23,6 +24,20 @@ def test_known_answers():
     assert b.device.type == "cpu"  # CPU inputs come back on the CPU
     assert torch.allclose(b, torch.tensor([3.0, 4.0, 1.0, 5.5, 5.0, 4.5]), rtol=1e-5)
     assert torch.allclose(s, torch.tensor([0.0, 0.0, 0.0, 0.707107, 1.414214, 0.707107]), rtol=1e-5)
+
+
+@pytest.mark.parametrize("case", ADVANTAGE_KNOWN_ANSWERS, ids=[c[0] for c in ADVANTAGE_KNOWN_ANSWERS])
+def test_reference_known_answers(case):
+    """Every known answer of reference tests/unit/algorithms/test_utils.py:830-1120, on the
+    device, and the oracle on the same inputs (trivial flags equal, values to fp32 rounding)."""
+    p, r, v, loo, q = advantage_case_inputs(case, DEV)
+    b, s, t = calculate_baseline_and_std_per_prompt(p, r, v, loo, q)
+    assert b.device.type == "cuda"
+    check_advantage_known_answer(case, b, s, t)
+    ob, os_, ot = baseline_and_std_per_prompt(p.cpu(), r.cpu(), v.cpu(), loo, std_rewards=None if q is None else q.cpu())
+    assert torch.equal(t.cpu(), ot)
+    torch.testing.assert_close(b.cpu(), ob, rtol=1e-6, atol=0)
+    torch.testing.assert_close(s.cpu(), os_, rtol=1e-5, atol=1e-6)
 
 
 def test_trivial_flags_and_std_rewards():

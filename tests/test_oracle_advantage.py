@@ -4,6 +4,7 @@ import pytest
 import torch
 
 from oracle.advantage import baseline_and_std_per_prompt, grpo_advantages
+from tests.helpers import ADVANTAGE_KNOWN_ANSWERS, advantage_case_inputs, check_advantage_known_answer
 
 P6 = torch.tensor([[1, 2, 3]] * 3 + [[4, 5, 6]] * 3)
 
@@ -53,3 +54,20 @@ def test_brute_force_random_groups():
         if len(grp) > 1:
             assert b[i].item() == pytest.approx(grp.mean().item(), abs=1e-6)
             assert s[i].item() == pytest.approx(grp.std(unbiased=True).item(), abs=1e-5)
+
+
+@pytest.mark.parametrize("case", ADVANTAGE_KNOWN_ANSWERS, ids=[c[0] for c in ADVANTAGE_KNOWN_ANSWERS])
+def test_reference_known_answers(case):
+    """Every known answer of reference tests/unit/algorithms/test_utils.py:830-1120 (the
+    id names the test and its first line)."""
+    p, r, v, loo, q = advantage_case_inputs(case)
+    check_advantage_known_answer(case, *baseline_and_std_per_prompt(p, r, v, loo, std_rewards=q))
+
+
+def test_known_answer_checker_catches_a_dropped_leave_one_out():
+    """A plausible oracle mistake (the leave-one-out count not subtracted) fails the table."""
+    case = ADVANTAGE_KNOWN_ANSWERS[0]
+    p, r, v, _, _ = advantage_case_inputs(case)
+    b, s, t = baseline_and_std_per_prompt(p, r, v, False)  # full-group mean instead of leave-one-out
+    with pytest.raises(AssertionError):
+        check_advantage_known_answer(case, b, s, t)
