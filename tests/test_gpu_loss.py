@@ -174,3 +174,32 @@ def test_grpo_workload_shape_loss():
     torch.testing.assert_close(g.cpu(), g_o, rtol=1e-4, atol=1e-9)
     for k, v in m_o.items():
         assert m[k] == pytest.approx(v, rel=1e-4, abs=1e-7), k
+
+
+@pytest.mark.parametrize("clamped", [False, True])
+@pytest.mark.parametrize("kl_type", ["k1", "k2", "k3"])
+def test_fused_kl_known_answers(kl_type, clamped):
+    """The kernel's KL term on the reference's calculate_kl known answers
+    (tests/unit/algorithms/test_loss_functions.py:1000-1039): logprobs -1 against reference
+    logprobs (0, -15, -30), no actor term (zero advantages, ratio 1); the kl_penalty metric
+    is the token mean of the per-token values."""
+    print("[case] fused kl", kl_type, clamped, flush=True)
+    vals = {"k1": ([-1.0, 14.0, 29.0], [-1.0, 10.0, 10.0]), "k2": ([0.5, 98.0, 420.5], [0.5, 10.0, 10.0]),
+            "k3": ([0.7182818, 13.0, 28.0], [0.7182818, 10.0, 10.0])}[kl_type][int(clamped)]
+    curr = torch.full((1, 3), -1.0, device=DEV, requires_grad=True)
+    pad = torch.zeros(1, 1, device=DEV)
+    data = {
+        "token_mask": torch.ones(1, 4, device=DEV),
+        "sample_mask": torch.ones(1, device=DEV),
+        "advantages": torch.zeros(1, 4, device=DEV),
+        "prev_logprobs": torch.cat([pad, curr.detach()], 1),
+        "generation_logprobs": torch.cat([pad, curr.detach()], 1),
+        "reference_policy_logprobs": torch.tensor([[0.0, -0.0, -15.0, -30.0]], device=DEV),
+    }
+    clamps = {} if clamped else {"kl_input_clamp_value": None, "kl_output_clamp_value": None}
+    fn = ClippedPGLossFn(ClippedPGLossConfig(reference_policy_kl_penalty=0.5, reference_policy_kl_type=kl_type,
+                                             **clamps))
+    loss, m = fn(curr, data, torch.tensor(1.0, device=DEV), torch.tensor(3.0, device=DEV))
+    mean = sum(vals) / 3
+    assert m["kl_penalty"] == pytest.approx(mean, rel=1e-3)
+    assert loss.item() == pytest.approx(0.5 * mean, rel=1e-3)

@@ -76,3 +76,66 @@ def test_oracle_known_answer_ppo_clipping():
                                   torch.tensor(1.0, dtype=torch.float64),
                                   reference_policy_kl_penalty=0.0)
         assert loss.item() == pytest.approx(expected / (1 + 1e-8), rel=1e-12)
+
+
+# reference tests/unit/algorithms/test_loss_functions.py:1000-1039: logprobs -1, reference
+# logprobs (0, -15, -30); un-clamped and clamped (input 20, output 10) KL values (rtol 1e-3)
+KL_KNOWN = {
+    "k1": ([-1.0, 14.0, 29.0], [-1.0, 10.0, 10.0]),
+    "k2": ([0.5, 98.0, 420.5], [0.5, 10.0, 10.0]),
+    "k3": ([0.7183, 13.0, 28.0], [0.7183, 10.0, 10.0]),
+}
+
+
+def _kl_impls():
+    from oracle.loss import calculate_kl as oracle_kl
+    from rl_amd.algorithms.utils import calculate_kl as api_kl
+
+    return [oracle_kl, api_kl]
+
+
+@pytest.mark.parametrize("impl", [0, 1], ids=["oracle", "api"])
+@pytest.mark.parametrize("kl_type", list(KL_KNOWN))
+def test_calculate_kl_known_answers(kl_type, impl):
+    kl_fn = _kl_impls()[impl]
+    lp = torch.tensor([[-1.0, -1.0, -1.0]])
+    ref = torch.tensor([[-0.0, -15.0, -30.0]])
+    raw, clamped = KL_KNOWN[kl_type]
+    kl = kl_fn(lp, ref, kl_type, input_clamp_value=None, output_clamp_value=None)
+    assert torch.allclose(kl, torch.tensor([raw]), rtol=1e-3)
+    kl = kl_fn(lp, ref, kl_type, input_clamp_value=20.0, output_clamp_value=10.0)
+    assert torch.allclose(kl, torch.tensor([clamped]), rtol=1e-3)
+
+
+@pytest.mark.parametrize("impl", [0, 1], ids=["oracle", "api"])
+def test_calculate_kl_importance_weight_rules(impl):
+    """reference test_loss_functions.py:1042-1097: an input-clamped term detaches its IS
+    weight (gradient 0 there, -1 elsewhere); the output clamp applies after the IS weight."""
+    kl_fn = _kl_impls()[impl]
+    lp = torch.tensor([[-3.0, -1.0]], requires_grad=True)
+    kl = kl_fn(lp, torch.zeros_like(lp), "k3", input_clamp_value=2.0, output_clamp_value=None,
+               importance_sampling_weights=torch.exp(lp - lp.detach()))
+    torch.testing.assert_close(kl.detach(), torch.tensor([[4.389056, 0.7182818]]))
+    kl.sum().backward()
+    torch.testing.assert_close(lp.grad, torch.tensor([[0.0, -1.0]]), atol=1e-6, rtol=1e-6)
+    lp = torch.tensor([[-1.0]], requires_grad=True)
+    kl = kl_fn(lp, torch.zeros_like(lp), "k3", input_clamp_value=None, output_clamp_value=1.0,
+               importance_sampling_weights=100.0 * torch.exp(lp - lp.detach()))
+    torch.testing.assert_close(kl.detach(), torch.tensor([[1.0]]))
+    kl.sum().backward()
+    torch.testing.assert_close(lp.grad, torch.zeros_like(lp), atol=1e-6, rtol=1e-6)
+
+
+def test_masked_mean_all_zeros():
+    """reference test_loss_functions.py:1839-1858 (the +1e-8 keeps an empty mask at 0)."""
+    from oracle.loss import masked_mean as oracle_mm
+    from rl_amd.algorithms.utils import masked_mean as api_mm
+
+    for mm in (oracle_mm, api_mm):
+        values = torch.tensor([1.0, 2.0, 3.0, 4.0])
+        mask = torch.zeros_like(values)
+        assert mm(values, mask).item() == 0.0
+        mask[0] = 1
+        assert mm(values, mask).item() == pytest.approx(1.0)
+        v2 = torch.tensor([[1.0, 2.0], [3.0, 4.0]])
+        assert torch.equal(mm(v2, torch.zeros_like(v2), dim=1), torch.zeros(2))
