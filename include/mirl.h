@@ -351,7 +351,8 @@ int64_t mirl_linear_ce_workspace_elems(int64_t T, int64_t V);
  *   out[b,s] = (x[r, t'] - m) - log(sum_v exp(x[r, v] - m)),  t' = target[b, s] - vocab_start,
  *   out[b,s] = 0 when target < vocab_start or >= vocab_end.
  * The [T, V] logits are never written.  H must be a multiple of 128, row
- * strides multiples of 8 elements, both bases 16-byte aligned.  `row_stats`
+ * strides multiples of 8 elements, both bases 16-byte aligned (the Python
+ * layer copies other operands into zero-padded buffers first).  `row_stats`
  * (optional) receives {m, log sum} per row for mirl_linear_ce_grad;
  * `workspace` holds mirl_linear_ce_workspace_elems(T, V) floats.
  *
