@@ -101,8 +101,9 @@ def cpu_baseline(x, tgt, d: dict, chunk: int, min_seconds: float = 10.0, max_pas
 def main() -> None:
     args = parse()
     if args.gpus != 1:
-        sys.exit(f"bench.py runs on one GPU only (got --gpus {args.gpus}); this build has no "
-                 "multi-GPU path: the workload shards by rows with no exchange, see DESIGN.md")
+        sys.exit(f"bench.py runs on one GPU only (got --gpus {args.gpus}): there is no multi-GPU "
+                 "path; the rows of the workload are independent, so it would shard by rows "
+                 "with no exchange of logits")
     if args.workload != "grpo":
         bench_workload(args)
         return
