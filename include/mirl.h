@@ -501,7 +501,9 @@ int64_t mirl_clipped_pg_workspace_elems(int64_t B, int64_t L, int score_centerin
 /*
  * Fused ClippedPG loss forward + closed-form backward over [B, L] tokens
  * (L = S - 1; the caller passes the [:, 1:] views of the [B, S] data).
- * Writes: metrics[MIRL_NUM_METRICS] (metrics[MIRL_M_LOSS] is the loss),
+ * Writes: metrics[MIRL_NUM_METRICS] (metrics[MIRL_M_LOSS] is the loss), the
+ * loss again into `loss` (one element; optional, NULL skips it: a caller that
+ * needs the loss apart from the metrics saves a copy kernel),
  * grad_curr[B, L] = dloss/dnext_token_logprobs, and, when
  * cfg->has_unfiltered, grad_unfiltered[B, L] = dloss/dcurr_logprobs_unfiltered.
  * `dtype` is MIRL_DTYPE_F32 or MIRL_DTYPE_F64 for every float tensor;
@@ -528,7 +530,7 @@ int mirl_clipped_pg(const mirl_pg_config* cfg, int dtype, int64_t B, int64_t L,
                     mirl_view2d reference, mirl_view2d support_mask,
                     const void* sample_mask, const void* rewards,
                     const void* global_valid_seqs,
-                    const void* global_valid_toks, void* metrics,
+                    const void* global_valid_toks, void* metrics, void* loss,
                     void* grad_curr, void* grad_unfiltered,
                     const mirl_score_centering_args* score_centering,
                     void* workspace, void* stream);

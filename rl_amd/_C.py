@@ -145,7 +145,7 @@ SIGNATURES = {
     "mirl_clipped_pg_workspace_elems": (_I64, [_I64, _I64, _I]),
     "mirl_clipped_pg": (
         _I,
-        [ctypes.POINTER(PgConfig), _I, _I64, _I64] + [View2D] * 8 + [_P] * 7
+        [ctypes.POINTER(PgConfig), _I, _I64, _I64] + [View2D] * 8 + [_P] * 8
         + [ctypes.POINTER(ScArgs), _P, _P],
     ),
     "mirl_score_centering_term": (
@@ -320,17 +320,30 @@ def _require_gpu(*tensors: Optional[torch.Tensor]) -> torch.device:
 
 def start_fetch(t: torch.Tensor):
     """Enqueue a copy of a small device tensor into a cached pinned buffer and
-    record an event after it; finish_fetch waits for that event.  Work the caller
-    enqueues in between runs after the copy, so the wait does not include it."""
+    record an event after it; finish_fetch waits for that event.
+
+    The copy runs on a side stream (default priority) behind everything already
+    enqueued on the current stream, so work the caller enqueues next on the
+    current stream (the early logits backward) starts without waiting for the
+    copy, and the wait does not include that work either."""
     n = t.numel()
-    key = (t.device, t.dtype, n)
+    dev = t.device
+    key = (dev, t.dtype, n)
     buf = _pinned.get(key)
     if buf is None:
         buf = torch.empty(n, dtype=t.dtype, pin_memory=True)
         _pinned[key] = buf
-    buf.copy_(t.reshape(-1), non_blocking=True)
-    ev = torch.cuda.Event()
-    ev.record()
+    side = _fetch_streams.get(dev)
+    if side is None:
+        side = torch.cuda.Stream(dev)
+        _fetch_streams[dev] = side
+    side.wait_stream(torch.cuda.current_stream(dev))
+    src = t.reshape(-1)
+    with torch.cuda.stream(side):
+        buf.copy_(src, non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record(side)
+    src.record_stream(side)  # the allocator keeps src until the side stream has read it
     return buf, ev
 
 
@@ -349,6 +362,7 @@ def wait_and_fetch(t: torch.Tensor) -> list:
 
 
 _pinned: dict = {}
+_fetch_streams: dict = {}
 
 
 try:  # raw handle of the current stream without building a Stream object
@@ -519,13 +533,19 @@ def clipped_pg(
     global_valid_seqs: torch.Tensor,
     global_valid_toks: torch.Tensor,
     score_centering: Optional[ScArgs] = None,
+    loss_out: Optional[torch.Tensor] = None,
 ) -> tuple[torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
     """Run the fused ClippedPG kernel; returns (metrics[19], grad_curr, grad_unfiltered).
+
+    ``loss_out`` (optional, one element of the loss dtype) receives the loss as
+    well, written by the kernel itself (no copy out of the metrics).
 
     With ``score_centering`` (a filled ScArgs whose ``grad`` points at a
     [B, L, K] buffer of the loss dtype) the correction is added to the loss and
     dloss/dplog is written into that buffer.
     """
+    if loss_out is not None:
+        assert loss_out.numel() == 1 and loss_out.dtype == curr.dtype and loss_out.is_contiguous()
     dev = _require_gpu(curr, token_mask, advantages, generation, sample_mask)
     B, L = curr.shape
     dtype = curr.dtype
@@ -541,7 +561,7 @@ def clipped_pg(
         _view(token_mask), _view(advantages), _view(prev), _view(generation),
         _view(reference), _view(support_mask), sample_mask.data_ptr(), _ptr(rewards),
         global_valid_seqs.data_ptr(), global_valid_toks.data_ptr(), metrics.data_ptr(),
-        grad_curr.data_ptr(), _ptr(grad_unf),
+        _ptr(loss_out), grad_curr.data_ptr(), _ptr(grad_unf),
         None if score_centering is None else ctypes.byref(score_centering), ws.data_ptr(),
         _stream(dev),
     )

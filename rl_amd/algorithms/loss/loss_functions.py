@@ -583,9 +583,12 @@ class _ClippedPGFunction(torch.autograd.Function):
             mode, bounds, outer, qlog = sc
             grad_plog = torch.empty(plog.shape, dtype=plog.dtype, device=plog.device)
             sc_args = _C.score_centering_args(mode, bounds, outer, plog, qlog, grad_plog)
+        # the kernel writes the loss into its own 0-d tensor too: a copy out of
+        # the metrics would sit on the stream between the loss and the early backward
+        loss = torch.empty((), dtype=curr.dtype, device=curr.device)
         metrics, grad_curr, grad_unf = _C.clipped_pg(
             cfg, curr, unfiltered, token_mask, advantages, prev, generation, reference, support,
-            sample_mask, rewards, gvs, gvt, sc_args,
+            sample_mask, rewards, gvs, gvt, sc_args, loss_out=loss,
         )
         ctx.save_for_backward(grad_curr, grad_unf, grad_plog)
         ctx.grad_curr = grad_curr  # d(loss)/d(curr) at grad_loss = 1, for launch_early_backward
@@ -593,7 +596,6 @@ class _ClippedPGFunction(torch.autograd.Function):
         ctx.mark_non_differentiable(metrics)
         # no zero-filled gradient for the metrics output on the way back
         ctx.set_materialize_grads(False)
-        loss = metrics[0].clone()
         return loss, metrics
 
     @staticmethod

@@ -638,6 +638,7 @@ __global__ __launch_bounds__(kFinalThreads) void pg_final_kernel(mirl_pg_config 
                                                                  int64_t L, Inputs<T> in,
                                                                  const T* __restrict__ part,
                                                                  T* __restrict__ metrics,
+                                                                 T* __restrict__ loss_out,
                                                                  T* __restrict__ gcurr,
                                                                  int has_sc) {
   __shared__ T tot[NUM_SLOTS];
@@ -677,6 +678,7 @@ __global__ __launch_bounds__(kFinalThreads) void pg_final_kernel(mirl_pg_config 
     const T loss = (actor + kl) + T(cfg.nll_weight) * nll;
     T* m = metrics;
     m[MIRL_M_LOSS] = loss;
+    if (loss_out != nullptr) *loss_out = loss;  // the loss on its own, for callers that want it apart
     m[MIRL_M_TOKEN_MULT_PROB_ERROR] = tot[P_TMPE] / gvt;
     m[MIRL_M_PROBS_RATIO] = tot[P_RATIO] / gvt;
     m[MIRL_M_PROBS_RATIO_CLAMPED] = tot[P_RATIO_C] / gvt;
@@ -763,8 +765,8 @@ __global__ __launch_bounds__(256) void sc_scale_kernel(T* __restrict__ grad,
 template <class T>
 int run(const mirl_pg_config* cfg, int64_t B, int64_t L, const mirl_view2d* v,
         const void* sample_mask, const void* rewards, const void* gvs, const void* gvt,
-        void* metrics, void* gcurr, void* gunf, const mirl_score_centering_args* sc, void* ws,
-        hipStream_t st) {
+        void* metrics, void* loss_out, void* gcurr, void* gunf,
+        const mirl_score_centering_args* sc, void* ws, hipStream_t st) {
   Inputs<T> in;
   auto mk = [](const mirl_view2d& x) { return View<T>{static_cast<const T*>(x.ptr), x.sb, x.sl}; };
   in.curr = mk(v[0]);
@@ -797,8 +799,8 @@ int run(const mirl_pg_config* cfg, int64_t B, int64_t L, const mirl_view2d* v,
                      static_cast<T*>(gcurr), static_cast<T*>(gunf), part, scw, has_sc);
   if (int e = check_launch("mirl_clipped_pg(rows)")) return e;
   hipLaunchKernelGGL((pg_final_kernel<T>), dim3(1), dim3(kFinalThreads), 0, st, *cfg, B, L, in,
-                     static_cast<const T*>(part), static_cast<T*>(metrics), static_cast<T*>(gcurr),
-                     has_sc);
+                     static_cast<const T*>(part), static_cast<T*>(metrics),
+                     static_cast<T*>(loss_out), static_cast<T*>(gcurr), has_sc);
   if (has_sc && n * sc->K > 0) {
     const int64_t ne = n * sc->K;
     hipLaunchKernelGGL((sc_scale_kernel<T>), dim3((unsigned)((ne + 255) / 256)), dim3(256), 0, st,
@@ -835,7 +837,7 @@ extern "C" int mirl_clipped_pg(const mirl_pg_config* cfg, int dtype, int64_t B, 
                                mirl_view2d reference, mirl_view2d support_mask,
                                const void* sample_mask, const void* rewards,
                                const void* global_valid_seqs, const void* global_valid_toks,
-                               void* metrics, void* grad_curr, void* grad_unfiltered,
+                               void* metrics, void* loss, void* grad_curr, void* grad_unfiltered,
                                const mirl_score_centering_args* score_centering, void* workspace,
                                void* stream) {
   clear_error();
@@ -868,10 +870,10 @@ extern "C" int mirl_clipped_pg(const mirl_pg_config* cfg, int dtype, int64_t B, 
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == MIRL_DTYPE_F32)
     return run<float>(cfg, B, L, views, sample_mask, rewards, global_valid_seqs, global_valid_toks,
-                      metrics, grad_curr, grad_unfiltered, score_centering, workspace, st);
+                      metrics, loss, grad_curr, grad_unfiltered, score_centering, workspace, st);
   if (dtype == MIRL_DTYPE_F64)
     return run<double>(cfg, B, L, views, sample_mask, rewards, global_valid_seqs,
-                       global_valid_toks, metrics, grad_curr, grad_unfiltered, score_centering,
+                       global_valid_toks, metrics, loss, grad_curr, grad_unfiltered, score_centering,
                        workspace, st);
   set_error("mirl_clipped_pg: dtype must be f32 or f64 (got %d)", dtype);
   return MIRL_ERR_UNSUPPORTED;
