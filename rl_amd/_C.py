@@ -298,6 +298,13 @@ def _check(status: int, what: str) -> None:
         raise MirlError(f"{what} failed (status {status}): {msg}")
 
 
+def _require(cond: bool, what: str) -> None:
+    """Argument check that survives ``python -O``: a wrong layout or dtype would
+    otherwise reach the kernels as raw pointers."""
+    if not cond:
+        raise MirlError(f"invalid argument: {what}")
+
+
 def _require_gpu(*tensors: Optional[torch.Tensor]) -> torch.device:
     dev = None
     for t in tensors:
@@ -439,8 +446,8 @@ def logprob_fwd(
     dev = _require_gpu(logits, target, out, stats)
     B, R = target.shape
     V = logits.shape[-1]
-    assert logits.stride(-1) == 1 and out.is_contiguous()
-    assert stats is None or stats.is_contiguous()
+    _require(logits.stride(-1) == 1 and out.is_contiguous(), "logits.stride(-1) == 1 and out.is_contiguous()")
+    _require(stats is None or stats.is_contiguous(), "stats is None or stats.is_contiguous()")
     st = _launch(
         "mirl_logprob_fwd", dev,
         logits.data_ptr(), _dtype_code(logits), B, R, V, logits.stride(0), logits.stride(1),
@@ -467,8 +474,8 @@ def logprob_bwd(
     B, R = target.shape
     Rt = grad_in.shape[1]
     V = logits.shape[-1]
-    assert grad_in.stride(-1) == 1 and logits.stride(-1) == 1
-    assert grad_in.dtype == logits.dtype and grad_out.dtype == torch.float32
+    _require(grad_in.stride(-1) == 1 and logits.stride(-1) == 1, "grad_in.stride(-1) == 1 and logits.stride(-1) == 1")
+    _require(grad_in.dtype == logits.dtype and grad_out.dtype == torch.float32, "grad_in.dtype == logits.dtype and grad_out.dtype == torch.float32")
     st = _launch(
         "mirl_logprob_bwd", dev,
         logits.data_ptr(), _dtype_code(logits), B, R, Rt, V, logits.stride(0),
@@ -495,8 +502,8 @@ def logprob_bwd_recheck(
     B, R = target.shape
     Rt = grad_in.shape[1]
     V = logits.shape[-1]
-    assert grad_used.is_contiguous() and tuple(grad_used.shape) == (B, R)
-    assert grad_out.dtype == torch.float32 and grad_used.dtype == torch.float32
+    _require(grad_used.is_contiguous() and tuple(grad_used.shape) == (B, R), "grad_used.is_contiguous() and tuple(grad_used.shape) == (B, R)")
+    _require(grad_out.dtype == torch.float32 and grad_used.dtype == torch.float32, "grad_out.dtype == torch.float32 and grad_used.dtype == torch.float32")
     flag = torch.empty(64, dtype=torch.int32, device=dev)  # MIRL_RECHECK_FLAGS
     st = _launch(
         "mirl_logprob_bwd_recheck", dev,
@@ -544,11 +551,17 @@ def clipped_pg(
     [B, L, K] buffer of the loss dtype) the correction is added to the loss and
     dloss/dplog is written into that buffer.
     """
-    if loss_out is not None:
-        assert loss_out.numel() == 1 and loss_out.dtype == curr.dtype and loss_out.is_contiguous()
     dev = _require_gpu(curr, token_mask, advantages, generation, sample_mask)
     B, L = curr.shape
     dtype = curr.dtype
+    if loss_out is not None and (
+        loss_out.numel() != 1 or loss_out.dtype != dtype or not loss_out.is_contiguous()
+        or loss_out.device != dev
+    ):
+        raise MirlError(
+            f"loss_out must be one contiguous {dtype} element on {dev}; got "
+            f"{tuple(loss_out.shape)} {loss_out.dtype} on {loss_out.device}"
+        )
     metrics = torch.empty(PG_NUM_METRICS, dtype=dtype, device=dev)
     grad_curr = torch.empty((B, L), dtype=dtype, device=dev)
     grad_unf = torch.empty((B, L), dtype=dtype, device=dev) if unfiltered is not None else None
@@ -582,8 +595,8 @@ def score_centering_args(
         code = SC_MODES[mode]
     except KeyError:
         raise ValueError(f"Unsupported score-centering IS mode {mode!r}") from None
-    assert plog.dim() == 3 and qlog.shape == plog.shape and grad.shape == plog.shape
-    assert plog.dtype == qlog.dtype == grad.dtype and grad.is_contiguous()
+    _require(plog.dim() == 3 and qlog.shape == plog.shape and grad.shape == plog.shape, "plog.dim() == 3 and qlog.shape == plog.shape and grad.shape == plog.shape")
+    _require(plog.dtype == qlog.dtype == grad.dtype and grad.is_contiguous(), "plog.dtype == qlog.dtype == grad.dtype and grad.is_contiguous()")
     lo, hi = bounds if bounds is not None else (0.0, 0.0)
     return ScArgs(
         code, 0, plog.shape[2], float(lo), float(hi), float(outer if outer is not None else 0.0),
@@ -604,7 +617,7 @@ def score_centering_term(
     """term / head_mass [B, L] (contiguous) and coef (into args.grad) of compute_score_centering_term."""
     dev = _require_gpu(token_mask, advantages, term, head_mass)
     B, L = token_mask.shape
-    assert term.is_contiguous() and head_mass.is_contiguous()
+    _require(term.is_contiguous() and head_mass.is_contiguous(), "term.is_contiguous() and head_mass.is_contiguous()")
     st = _launch(
         "mirl_score_centering_term", dev,
         DTYPE_CODES[dtype], B, L, ctypes.byref(args), _view(token_mask), _view(advantages),
@@ -632,8 +645,8 @@ def gather_logprob_fwd(
     dev = _require_gpu(logits, indices, out, stats)
     B, R, K = indices.shape
     V = logits.shape[-1]
-    assert logits.stride(-1) == 1 and out.is_contiguous() and indices.dtype == torch.int64
-    assert stats is None or stats.is_contiguous()
+    _require(logits.stride(-1) == 1 and out.is_contiguous() and indices.dtype == torch.int64, "logits.stride(-1) == 1 and out.is_contiguous() and indices.dtype == torch.int64")
+    _require(stats is None or stats.is_contiguous(), "stats is None or stats.is_contiguous()")
     st = _launch(
         "mirl_gather_logprob_fwd", dev,
         logits.data_ptr(), _dtype_code(logits), B, R, V, logits.stride(0), logits.stride(1),
@@ -656,8 +669,8 @@ def gather_logprob_bwd(
     dev = _require_gpu(logits, indices, stats, grad_out, grad_in)
     B, R, K = indices.shape
     V = logits.shape[-1]
-    assert grad_in.stride(-1) == 1 and logits.stride(-1) == 1
-    assert grad_in.dtype == logits.dtype and grad_out.dtype == torch.float32
+    _require(grad_in.stride(-1) == 1 and logits.stride(-1) == 1, "grad_in.stride(-1) == 1 and logits.stride(-1) == 1")
+    _require(grad_in.dtype == logits.dtype and grad_out.dtype == torch.float32, "grad_in.dtype == logits.dtype and grad_out.dtype == torch.float32")
     lib = load()
     ws = torch.empty(int(lib.mirl_gather_logprob_workspace_elems(B, R)), dtype=torch.float32,
                      device=dev)
@@ -686,9 +699,9 @@ def gather_logprob_bwd_recheck(
     dev = _require_gpu(logits, indices, stats, grad_out, grad_used, grad_in)
     B, R, K = indices.shape
     V = logits.shape[-1]
-    assert grad_in.stride(-1) == 1 and logits.stride(-1) == 1
-    assert grad_out.dtype == torch.float32 and grad_used.dtype == torch.float32
-    assert grad_used.is_contiguous() and tuple(grad_used.shape) == (B, R, K)
+    _require(grad_in.stride(-1) == 1 and logits.stride(-1) == 1, "grad_in.stride(-1) == 1 and logits.stride(-1) == 1")
+    _require(grad_out.dtype == torch.float32 and grad_used.dtype == torch.float32, "grad_out.dtype == torch.float32 and grad_used.dtype == torch.float32")
+    _require(grad_used.is_contiguous() and tuple(grad_used.shape) == (B, R, K), "grad_used.is_contiguous() and tuple(grad_used.shape) == (B, R, K)")
     lib = load()
     ws = torch.empty(int(lib.mirl_gather_logprob_workspace_elems(B, R)), dtype=torch.float32,
                      device=dev)
@@ -709,7 +722,7 @@ def vocab_topk(logits: torch.Tensor, k: int, vocab_start: int) -> tuple[torch.Te
     """(values fp32 [B, R, k], global ids int64 [B, R, k]) of the k largest logits per row."""
     dev = _require_gpu(logits)
     B, R, V = logits.shape
-    assert logits.stride(-1) == 1
+    _require(logits.stride(-1) == 1, "logits.stride(-1) == 1")
     vals = torch.empty((B, R, k), dtype=torch.float32, device=dev)
     idx = torch.empty((B, R, k), dtype=torch.int64, device=dev)
     lib = load()
@@ -737,9 +750,9 @@ def divergence_fwd(
     """out[b, r] = entropy / cross entropy / reverse KL of the row; stats [B, R, 4] or None."""
     dev = _require_gpu(student, teacher, out, stats)
     B, R, V = student.shape
-    assert student.stride(-1) == 1 and out.is_contiguous()
-    assert teacher is None or (teacher.stride(-1) == 1 and teacher.dtype == student.dtype)
-    assert stats is None or stats.is_contiguous()
+    _require(student.stride(-1) == 1 and out.is_contiguous(), "student.stride(-1) == 1 and out.is_contiguous()")
+    _require(teacher is None or (teacher.stride(-1) == 1 and teacher.dtype == student.dtype), "teacher is None or (teacher.stride(-1) == 1 and teacher.dtype == student.dtype)")
+    _require(stats is None or stats.is_contiguous(), "stats is None or stats.is_contiguous()")
     t = teacher if teacher is not None else student
     st = _launch(
         "mirl_divergence_fwd", dev,
@@ -762,8 +775,8 @@ def divergence_bwd(
     """grad_in[b, r, v] = (p_v (w_v - out[b, r])) * grad_out[b, r] in the logits dtype."""
     dev = _require_gpu(student, teacher, out, stats, grad_out, grad_in)
     B, R, V = student.shape
-    assert grad_in.stride(-1) == 1 and grad_in.dtype == student.dtype
-    assert grad_out.dtype == torch.float32
+    _require(grad_in.stride(-1) == 1 and grad_in.dtype == student.dtype, "grad_in.stride(-1) == 1 and grad_in.dtype == student.dtype")
+    _require(grad_out.dtype == torch.float32, "grad_out.dtype == torch.float32")
     t = teacher if teacher is not None else student
     st = _launch(
         "mirl_divergence_bwd", dev,
@@ -793,8 +806,8 @@ def grpo_advantage(
     dev = _require_gpu(prompts, rewards, valid_mask)
     B = rewards.shape[0]
     K = prompts.shape[1]
-    assert prompts.dtype == torch.int64 and prompts.stride(1) == 1
-    assert rewards.dtype == torch.float32 and rewards.is_contiguous()
+    _require(prompts.dtype == torch.int64 and prompts.stride(1) == 1, "prompts.dtype == torch.int64 and prompts.stride(1) == 1")
+    _require(rewards.dtype == torch.float32 and rewards.is_contiguous(), "rewards.dtype == torch.float32 and rewards.is_contiguous()")
     adv = torch.empty(B, dtype=torch.float32, device=dev)
     base = torch.empty_like(adv) if want_stats else None
     std = torch.empty_like(adv) if want_stats else None
@@ -819,8 +832,8 @@ def pack_sequences(
 ) -> torch.Tensor:
     """``[B, S, ...]`` rows packed to ``[total, ...]`` along the padded boundaries (device int64)."""
     dev = _require_gpu(x, cu_seqlens, cu_seqlens_padded)
-    assert x.is_contiguous() and x.dim() >= 2
-    assert cu_seqlens.dtype == torch.int64 and cu_seqlens_padded.dtype == torch.int64
+    _require(x.is_contiguous() and x.dim() >= 2, "x.is_contiguous() and x.dim() >= 2")
+    _require(cu_seqlens.dtype == torch.int64 and cu_seqlens_padded.dtype == torch.int64, "cu_seqlens.dtype == torch.int64 and cu_seqlens_padded.dtype == torch.int64")
     B, S = x.shape[0], x.shape[1]
     tail = tuple(x.shape[2:])
     row = 1
@@ -841,7 +854,7 @@ def pack_sequences(
 def packed_roll_targets(target: torch.Tensor, bounds: torch.Tensor) -> torch.Tensor:
     """Per-segment roll by -1 of packed int64 targets ``[n]`` (0 outside the segments)."""
     dev = _require_gpu(target, bounds)
-    assert target.dtype == torch.int64 and target.is_contiguous() and bounds.dtype == torch.int64
+    _require(target.dtype == torch.int64 and target.is_contiguous() and bounds.dtype == torch.int64, "target.dtype == torch.int64 and target.is_contiguous() and bounds.dtype == torch.int64")
     out = torch.empty_like(target)
     st = _launch(
         "mirl_packed_roll_targets", dev,
@@ -855,7 +868,7 @@ def packed_roll_targets(target: torch.Tensor, bounds: torch.Tensor) -> torch.Ten
 def unpack_rows_fwd(packed: torch.Tensor, bounds: torch.Tensor, cols: int) -> torch.Tensor:
     """Packed fp32 rows ``[n_rows]`` -> ``[n_seq, cols]`` (zeros after each sequence)."""
     dev = _require_gpu(packed, bounds)
-    assert packed.dtype == torch.float32 and packed.is_contiguous() and bounds.dtype == torch.int64
+    _require(packed.dtype == torch.float32 and packed.is_contiguous() and bounds.dtype == torch.int64, "packed.dtype == torch.float32 and packed.is_contiguous() and bounds.dtype == torch.int64")
     n_seq = bounds.numel() - 1
     out = torch.empty((n_seq, cols), dtype=torch.float32, device=dev)
     st = _launch(
@@ -903,7 +916,7 @@ def filtered_fwd(
     dev = _require_gpu(logits, target, out)
     B, R = target.shape
     V = logits.shape[-1]
-    assert logits.stride(-1) == 1 and (out is None or out.is_contiguous())
+    _require(logits.stride(-1) == 1 and (out is None or out.is_contiguous()), "logits.stride(-1) == 1 and (out is None or out.is_contiguous())")
     info, kidx, kp = _filter_scratch(B * R, dev)
     st = _launch(
         "mirl_filtered_logprob_fwd", dev,
@@ -930,7 +943,7 @@ def filtered_bwd(
     B, R = target.shape
     Rt = grad_in.shape[1]
     V = logits.shape[-1]
-    assert grad_in.dtype == logits.dtype and grad_out.dtype == torch.float32
+    _require(grad_in.dtype == logits.dtype and grad_out.dtype == torch.float32, "grad_in.dtype == logits.dtype and grad_out.dtype == torch.float32")
     st = _launch(
         "mirl_filtered_logprob_bwd", dev,
         logits.data_ptr(), _dtype_code(logits), B, R, Rt, V, logits.stride(0),
@@ -946,7 +959,7 @@ def top_k_top_p_mask(x2d: torch.Tensor, top_k: int, top_p: float):
     """[N, V] rows -> (filtered [N, V] in x's dtype, keep [N, V] bool)."""
     dev = _require_gpu(x2d)
     N, V = x2d.shape
-    assert x2d.stride(1) == 1
+    _require(x2d.stride(1) == 1, "x2d.stride(1) == 1")
     info, kidx, kp = _filter_scratch(N, dev)
     filt = torch.empty((N, V), dtype=x2d.dtype, device=dev)
     keep = torch.empty((N, V), dtype=torch.bool, device=dev)
@@ -992,8 +1005,8 @@ def linear_ce_fwd(
     _check_linear_ce(hidden2d, weight)
     T, H = hidden2d.shape
     V = weight.shape[0]
-    assert target.dtype == torch.int64 and out.dtype == torch.float32
-    assert stats is None or (stats.is_contiguous() and stats.dtype == torch.float32)
+    _require(target.dtype == torch.int64 and out.dtype == torch.float32, "target.dtype == torch.int64 and out.dtype == torch.float32")
+    _require(stats is None or (stats.is_contiguous() and stats.dtype == torch.float32), "stats is None or (stats.is_contiguous() and stats.dtype == torch.float32)")
     lib = _lib if _lib is not None else load()
     ws = torch.empty(max(1, int(lib.mirl_linear_ce_workspace_elems(T, V))), dtype=torch.float32, device=dev)
     st = _launch(
@@ -1024,8 +1037,8 @@ def linear_ce_grad(
     T, H = hidden2d.shape
     V = weight.shape[0]
     n = grad_logits.shape[0]
-    assert grad_out.dtype == torch.float32 and grad_logits.dtype == torch.bfloat16
-    assert grad_logits.stride(-1) == 1
+    _require(grad_out.dtype == torch.float32 and grad_logits.dtype == torch.bfloat16, "grad_out.dtype == torch.float32 and grad_logits.dtype == torch.bfloat16")
+    _require(grad_logits.stride(-1) == 1, "grad_logits.stride(-1) == 1")
     st = _launch(
         "mirl_linear_ce_grad", dev,
         hidden2d.data_ptr(), T, H, hidden2d.stride(0), weight.data_ptr(), V, weight.stride(0),
