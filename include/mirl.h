@@ -535,6 +535,36 @@ int mirl_clipped_pg(const mirl_pg_config* cfg, int dtype, int64_t B, int64_t L,
                     const mirl_score_centering_args* score_centering,
                     void* workspace, void* stream);
 
+/* Bytes of scratch held by mirl_clipped_pg_noalloc on each GPU (4 MiB). */
+int64_t mirl_clipped_pg_noalloc_max_scratch_bytes(void);
+
+/*
+ * mirl_clipped_pg without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.
+ * Arguments and results are those of mirl_clipped_pg; the scratch is a fixed
+ * array of mirl_clipped_pg_noalloc_max_scratch_bytes() bytes in the
+ * library's device data, one copy per GPU, held until the process ends.
+ * Inputs whose workspace (mirl_clipped_pg_workspace_elems(B, L, sc) elements
+ * of `dtype`) exceeds it are rejected with MIRL_ERR_INVALID_ARGUMENT.  The
+ * call allocates nothing: no hipMalloc / hipFree or allocating library call.
+ * The first call on a device looks up that device's scratch address; later
+ * calls reuse it.  Every call on one GPU shares that GPU's scratch, so calls
+ * that overlap on one GPU (two streams, two threads) race and must be
+ * serialised by the caller.
+ */
+int mirl_clipped_pg_noalloc(const mirl_pg_config* cfg, int dtype, int64_t B, int64_t L,
+                            mirl_view2d curr, mirl_view2d unfiltered,
+                            mirl_view2d token_mask, mirl_view2d advantages,
+                            mirl_view2d prev, mirl_view2d generation,
+                            mirl_view2d reference, mirl_view2d support_mask,
+                            const void* sample_mask, const void* rewards,
+                            const void* global_valid_seqs,
+                            const void* global_valid_toks, void* metrics, void* loss,
+                            void* grad_curr, void* grad_unfiltered,
+                            const mirl_score_centering_args* score_centering,
+                            void* stream);
+
 /*
  * Per-token score-centering term over [B, L] tokens:
  *   p = exp(plog), q = exp(qlog), head = sum_k q, rho = max(1 - head, 0) / max(1 - sum_k p, 1e-6)

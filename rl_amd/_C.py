@@ -148,6 +148,12 @@ SIGNATURES = {
         [ctypes.POINTER(PgConfig), _I, _I64, _I64] + [View2D] * 8 + [_P] * 8
         + [ctypes.POINTER(ScArgs), _P, _P],
     ),
+    "mirl_clipped_pg_noalloc_max_scratch_bytes": (_I64, []),
+    "mirl_clipped_pg_noalloc": (
+        _I,
+        [ctypes.POINTER(PgConfig), _I, _I64, _I64] + [View2D] * 8 + [_P] * 8
+        + [ctypes.POINTER(ScArgs), _P],
+    ),
     "mirl_score_centering_term": (
         _I,
         [_I, _I64, _I64, ctypes.POINTER(ScArgs), View2D, View2D, _P, _P, _P],
@@ -541,11 +547,16 @@ def clipped_pg(
     global_valid_toks: torch.Tensor,
     score_centering: Optional[ScArgs] = None,
     loss_out: Optional[torch.Tensor] = None,
+    noalloc: bool = False,
 ) -> tuple[torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
     """Run the fused ClippedPG kernel; returns (metrics[19], grad_curr, grad_unfiltered).
 
     ``loss_out`` (optional, one element of the loss dtype) receives the loss as
     well, written by the kernel itself (no copy out of the metrics).
+
+    ``noalloc=True`` calls ``mirl_clipped_pg_noalloc``, whose scratch is the
+    library's fixed per-GPU array instead of a workspace tensor (the outputs
+    are still allocated here).
 
     With ``score_centering`` (a filled ScArgs whose ``grad`` points at a
     [B, L, K] buffer of the loss dtype) the correction is added to the loss and
@@ -566,19 +577,25 @@ def clipped_pg(
     grad_curr = torch.empty((B, L), dtype=dtype, device=dev)
     grad_unf = torch.empty((B, L), dtype=dtype, device=dev) if unfiltered is not None else None
     lib = load()
-    ws = torch.empty(int(lib.mirl_clipped_pg_workspace_elems(B, L, int(score_centering is not None))),
-                     dtype=dtype, device=dev)
-    st = _launch(
-        "mirl_clipped_pg", dev,
+    args = [
         ctypes.byref(cfg), _dtype_code(curr), B, L, _view(curr), _view(unfiltered),
         _view(token_mask), _view(advantages), _view(prev), _view(generation),
         _view(reference), _view(support_mask), sample_mask.data_ptr(), _ptr(rewards),
         global_valid_seqs.data_ptr(), global_valid_toks.data_ptr(), metrics.data_ptr(),
         _ptr(loss_out), grad_curr.data_ptr(), _ptr(grad_unf),
-        None if score_centering is None else ctypes.byref(score_centering), ws.data_ptr(),
-        _stream(dev),
-    )
-    _check(st, "mirl_clipped_pg")
+        None if score_centering is None else ctypes.byref(score_centering),
+    ]
+    if noalloc:
+        name = "mirl_clipped_pg_noalloc"
+        st = _launch(name, dev, *args, _stream(dev))
+    else:
+        name = "mirl_clipped_pg"
+        ws = torch.empty(
+            int(lib.mirl_clipped_pg_workspace_elems(B, L, int(score_centering is not None))),
+            dtype=dtype, device=dev,
+        )
+        st = _launch(name, dev, *args, ws.data_ptr(), _stream(dev))
+    _check(st, name)
     return metrics, grad_curr, grad_unf
 
 

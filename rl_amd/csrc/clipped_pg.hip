@@ -18,6 +18,8 @@
 // the closed interval, where() passes it to the selected branch, nan_to_num
 // passes it where the input was finite.
 
+#include <mutex>
+
 #include "common.h"
 
 namespace mirl {
@@ -829,6 +831,90 @@ using namespace mirl;
 
 extern "C" int64_t mirl_clipped_pg_workspace_elems(int64_t B, int64_t L, int score_centering) {
   return B * NUM_SLOTS + (score_centering ? 3 * B * L : 0);
+}
+
+// ---------------------------------------------------------------------------
+// Scratch of mirl_clipped_pg_noalloc: a fixed array in the library's own
+// device data, one copy on every GPU the library runs on, held until the
+// process ends.  Host code never passes the array's name to a kernel (on the
+// host it is only a stand-in for the device symbol): the device address of
+// each GPU's copy is looked up once per device with hipGetSymbolAddress and
+// that address is what the kernels receive.
+// ---------------------------------------------------------------------------
+namespace mirl {
+namespace {
+
+constexpr int64_t kNoAllocScratchBytes = int64_t(4) << 20;
+constexpr int kMaxDevices = 64;
+
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of the current device's scratch copy (looked up on the first
+// call per device, then cached).
+int scratch_address(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_error("hipGetDevice failed: %s", hipGetErrorString(e));
+    return MIRL_ERR_HIP;
+  }
+  MIRL_REQUIRE(dev >= 0 && dev < kMaxDevices, "device index %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      set_error("hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                hipGetErrorString(e));
+      return MIRL_ERR_HIP;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return MIRL_OK;
+}
+
+}  // namespace
+}  // namespace mirl
+
+extern "C" int64_t mirl_clipped_pg_noalloc_max_scratch_bytes(void) { return kNoAllocScratchBytes; }
+
+extern "C" int mirl_clipped_pg_noalloc(const mirl_pg_config* cfg, int dtype, int64_t B, int64_t L,
+                                       mirl_view2d curr, mirl_view2d unfiltered,
+                                       mirl_view2d token_mask, mirl_view2d advantages,
+                                       mirl_view2d prev, mirl_view2d generation,
+                                       mirl_view2d reference, mirl_view2d support_mask,
+                                       const void* sample_mask, const void* rewards,
+                                       const void* global_valid_seqs,
+                                       const void* global_valid_toks, void* metrics, void* loss,
+                                       void* grad_curr, void* grad_unfiltered,
+                                       const mirl_score_centering_args* score_centering,
+                                       void* stream) {
+  clear_error();
+  MIRL_REQUIRE(dtype == MIRL_DTYPE_F32 || dtype == MIRL_DTYPE_F64,
+               "mirl_clipped_pg_noalloc: dtype must be f32 or f64 (got %d)", dtype);
+  MIRL_REQUIRE(B > 0 && L >= 0 && B < (int64_t(1) << 31) && L < (int64_t(1) << 40),
+               "invalid shape B=%lld L=%lld", (long long)B, (long long)L);
+  const int64_t elem = dtype == MIRL_DTYPE_F64 ? 8 : 4;
+  const int64_t need =
+      mirl_clipped_pg_workspace_elems(B, L, score_centering != nullptr ? 1 : 0) * elem;
+  MIRL_REQUIRE(need <= kNoAllocScratchBytes,
+               "mirl_clipped_pg_noalloc: B=%lld L=%lld needs %lld bytes of scratch; the "
+               "no-allocation entry point holds at most %lld bytes (use mirl_clipped_pg with a "
+               "caller workspace)",
+               (long long)B, (long long)L, (long long)need, (long long)kNoAllocScratchBytes);
+  void* ws = nullptr;
+  if (int e = scratch_address(&ws)) return e;
+  // Every scratch element the kernels read is written earlier in the same
+  // call (row partials by pg_rows_kernel, score-centering terms by
+  // sc_term_kernel), so nothing needs clearing between calls.
+  return mirl_clipped_pg(cfg, dtype, B, L, curr, unfiltered, token_mask, advantages, prev,
+                         generation, reference, support_mask, sample_mask, rewards,
+                         global_valid_seqs, global_valid_toks, metrics, loss, grad_curr,
+                         grad_unfiltered, score_centering, ws, stream);
 }
 
 extern "C" int mirl_clipped_pg(const mirl_pg_config* cfg, int dtype, int64_t B, int64_t L,
