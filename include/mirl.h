@@ -278,8 +278,15 @@ typedef struct mirl_filter_row_info {
  *   y = dtype(float(x) / temperature)    (skipped when temperature == 1)
  *   top-k (top_k > 0): keep y >= k-th largest y, every tie kept;
  *   top-p (top_p < 1): over the kept values in ascending order, ties by
- *     vocabulary index, keep where fp32(cumsum(softmax)) > fp32(1 - top_p)
- *     (sums accumulated in double), always keeping the maximum;
+ *     vocabulary index, p = softmax, keep where cumsum(p) > 1 - top_p,
+ *     always keeping the maximum.  p_dtype selects the arithmetic:
+ *     MIRL_DTYPE_F32: p in fp32 (exp(y - m) * (1 / Z)), the cumulative sum
+ *       accumulated in double and rounded to fp32, compared with
+ *       fp32(1 - top_p) -- the reference on an fp32 (upcast) tensor;
+ *     the logits dtype (BF16/F16): p = dtype(exp(y - m) / Z), the cumulative
+ *       sum accumulated one element at a time in fp32 with each partial sum
+ *       rounded to the dtype, compared with dtype(fp32(1 - top_p)) -- the
+ *       reference on the 16-bit tensor itself;
  *   out[b,r] = (y_t - m) - logsum when target t is kept, else -inf.
  * Writes row_info[B*R] (mirl_filter_row_info) and, for rows with at most
  * MIRL_FILTER_KEEP_CAP kept entries, their vocabulary indices and
@@ -292,13 +299,14 @@ typedef struct mirl_filter_row_info {
  * (nemo_rl/distributed/model_utils.py:382-432) and of the no-group path of
  * get_next_token_logprobs_from_logits (model_utils.py:1702-1718); the optional
  * temperature is the in-place logits.div_ of
- * nemo_rl/models/automodel/train.py:248-262.
+ * nemo_rl/models/automodel/train.py:248-262.  The 16-bit p_dtype is limited
+ * to vocabularies below 589824 when top_p < 1.
  */
 int mirl_filtered_logprob_fwd(const void* logits, int dtype, int64_t B, int64_t R,
                               int64_t V, int64_t stride_b, int64_t stride_r,
                               const int64_t* target, int64_t t_stride_b,
                               int64_t t_stride_r, double temperature, int top_k,
-                              double top_p, float* out, void* row_info,
+                              double top_p, int p_dtype, float* out, void* row_info,
                               int32_t* kept_idx, float* kept_p, void* stream);
 
 /*
@@ -326,12 +334,13 @@ int mirl_filtered_logprob_bwd(const void* logits, int dtype, int64_t B, int64_t 
 /*
  * apply_top_k_top_p on N rows of V logits: filtered[i, j] = x[i, j] where kept,
  * -inf elsewhere (in the logits dtype), keep_mask[i, j] = kept (uint8).
- * row_info / kept_idx / kept_p are scratch of the sizes above for N rows.
+ * row_info / kept_idx / kept_p are scratch of the sizes above for N rows;
+ * p_dtype as for mirl_filtered_logprob_fwd.
  *
  * Replaces: apply_top_k_top_p (nemo_rl/algorithms/logits_sampling_utils.py:256-287).
  */
 int mirl_top_k_top_p_mask(const void* logits, int dtype, int64_t N, int64_t V,
-                          int64_t row_stride, int top_k, double top_p,
+                          int64_t row_stride, int top_k, double top_p, int p_dtype,
                           void* row_info, int32_t* kept_idx, float* kept_p,
                           void* filtered, int64_t filtered_row_stride,
                           uint8_t* keep_mask, int64_t keep_row_stride, void* stream);

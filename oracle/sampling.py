@@ -34,8 +34,26 @@ def top_k_only(logits: torch.Tensor, top_k: int):
     return torch.where(keep, logits, torch.tensor(-float("inf"), dtype=logits.dtype)), keep
 
 
-def top_k_top_p(logits: torch.Tensor, top_k: Optional[int], top_p: float, chunk_size: int = 256):
-    """reference logits_sampling_utils.py:111-212 with a stable ascending sort."""
+def _softmax_exact_normaliser(srt: torch.Tensor) -> torch.Tensor:
+    """softmax of sorted rows with the normaliser summed in float64 and rounded
+    once to fp32 (CPU torch sums it in fp32, in vector-lane order); the
+    probabilities are fp32 exp * (1 / Z) for fp32 rows and exp / Z rounded to
+    the dtype for 16-bit rows."""
+    x = srt.float()
+    e = torch.exp(x - x.amax(-1, keepdim=True))
+    z = e.double().sum(-1, keepdim=True).float()
+    if srt.dtype == torch.float32:
+        return e * (1.0 / z)
+    return (e / z).to(srt.dtype)
+
+
+def top_k_top_p(logits: torch.Tensor, top_k: Optional[int], top_p: float, chunk_size: int = 256,
+                exact_normaliser: bool = False):
+    """reference logits_sampling_utils.py:111-212 with a stable ascending sort.
+
+    ``exact_normaliser`` replaces the softmax's fp32 normaliser by the exactly
+    rounded one (see _softmax_exact_normaliser); it isolates CPU torch's
+    summation rounding from the filter's rule."""
     need_k = top_k is not None and top_k > 0
     need_p = top_p is not None and top_p != 1.0
     if not need_p:
@@ -55,7 +73,7 @@ def top_k_top_p(logits: torch.Tensor, top_k: Optional[int], top_p: float, chunk_
             thr = srt.gather(-1, torch.full(srt.shape[:-1], V - top_k, dtype=torch.long).unsqueeze(-1))
             kmask = srt >= thr
             srt = srt.masked_fill(~kmask, -float("inf"))
-        probs = srt.softmax(dim=-1)
+        probs = _softmax_exact_normaliser(srt) if exact_normaliser else srt.softmax(dim=-1)
         cum = torch.cumsum(probs, dim=-1)
         pmask = cum > 1 - top_p
         pmask[..., -1] = True

@@ -195,7 +195,7 @@ SIGNATURES = {
     "mirl_filtered_logprob_fwd": (
         _I,
         [_P, _I, _I64, _I64, _I64, _I64, _I64, _P, _I64, _I64, ctypes.c_double, _I,
-         ctypes.c_double, _P, _P, _P, _P, _P],
+         ctypes.c_double, _I, _P, _P, _P, _P, _P],
     ),
     "mirl_filtered_logprob_bwd": (
         _I,
@@ -215,7 +215,7 @@ SIGNATURES = {
     ),
     "mirl_top_k_top_p_mask": (
         _I,
-        [_P, _I, _I64, _I64, _I64, _I, ctypes.c_double, _P, _P, _P, _P, _I64, _P, _I64, _P],
+        [_P, _I, _I64, _I64, _I64, _I, ctypes.c_double, _I, _P, _P, _P, _P, _I64, _P, _I64, _P],
     ),
     "mirl_pack_sequences": (
         _I,
@@ -921,6 +921,14 @@ def _filter_scratch(rows: int, dev: torch.device):
     return info, kidx, kp
 
 
+def _decision_code(logits: torch.Tensor, decision_dtype: Optional[torch.dtype]) -> int:
+    """MIRL dtype code of the top-p decision: the logits dtype (None) or fp32."""
+    d = logits.dtype if decision_dtype is None else decision_dtype
+    if d not in (torch.float32, logits.dtype):
+        raise MirlError(f"top-p decision dtype must be float32 or the logits dtype {logits.dtype}, got {d}")
+    return DTYPE_CODES[d]
+
+
 def filtered_fwd(
     logits: torch.Tensor,
     target: torch.Tensor,
@@ -928,8 +936,13 @@ def filtered_fwd(
     top_k: int,
     top_p: float,
     out: Optional[torch.Tensor],
+    decision_dtype: Optional[torch.dtype] = None,
 ):
-    """Filtered logprobs of rows 0..R-1 (R = target.shape[1]); returns (info, kept_idx, kept_p)."""
+    """Filtered logprobs of rows 0..R-1 (R = target.shape[1]); returns (info, kept_idx, kept_p).
+
+    ``decision_dtype`` is the dtype the top-p probabilities and their cumulative
+    sum are formed in: None = the logits dtype (the reference on that tensor),
+    torch.float32 = after an fp32 upcast."""
     dev = _require_gpu(logits, target, out)
     B, R = target.shape
     V = logits.shape[-1]
@@ -939,8 +952,8 @@ def filtered_fwd(
         "mirl_filtered_logprob_fwd", dev,
         logits.data_ptr(), _dtype_code(logits), B, R, V, logits.stride(0), logits.stride(1),
         target.data_ptr(), target.stride(0), target.stride(1), float(temperature),
-        int(top_k), float(top_p), _ptr(out), info.data_ptr(), kidx.data_ptr(),
-        kp.data_ptr(), _stream(dev),
+        int(top_k), float(top_p), _decision_code(logits, decision_dtype), _ptr(out),
+        info.data_ptr(), kidx.data_ptr(), kp.data_ptr(), _stream(dev),
     )
     _check(st, "mirl_filtered_logprob_fwd")
     return info, kidx, kp
@@ -972,8 +985,10 @@ def filtered_bwd(
     _check(st, "mirl_filtered_logprob_bwd")
 
 
-def top_k_top_p_mask(x2d: torch.Tensor, top_k: int, top_p: float):
-    """[N, V] rows -> (filtered [N, V] in x's dtype, keep [N, V] bool)."""
+def top_k_top_p_mask(x2d: torch.Tensor, top_k: int, top_p: float,
+                     decision_dtype: Optional[torch.dtype] = None):
+    """[N, V] rows -> (filtered [N, V] in x's dtype, keep [N, V] bool); ``decision_dtype``
+    as for filtered_fwd."""
     dev = _require_gpu(x2d)
     N, V = x2d.shape
     _require(x2d.stride(1) == 1, "x2d.stride(1) == 1")
@@ -983,7 +998,7 @@ def top_k_top_p_mask(x2d: torch.Tensor, top_k: int, top_p: float):
     st = _launch(
         "mirl_top_k_top_p_mask", dev,
         x2d.data_ptr(), _dtype_code(x2d), N, V, x2d.stride(0), int(top_k), float(top_p),
-        info.data_ptr(), kidx.data_ptr(), kp.data_ptr(), filt.data_ptr(), filt.stride(0),
+        _decision_code(x2d, decision_dtype), info.data_ptr(), kidx.data_ptr(), kp.data_ptr(), filt.data_ptr(), filt.stride(0),
         keep.data_ptr(), keep.stride(0), _stream(dev),
     )
     _check(st, "mirl_top_k_top_p_mask")

@@ -25,6 +25,7 @@ SOURCES = [
     "clipped_pg.hip",
     "advantage.hip",
     "topk_filter.hip",
+    "topk_hist.hip",
     "linear_ce.hip",
     "divergence.hip",
     "packing.hip",

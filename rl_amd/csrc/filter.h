@@ -1,0 +1,123 @@
+// Shared definitions of the top-k / top-p filter kernels (topk_filter.hip,
+// topk_hist.hip): the per-row result record, the launch parameters, order
+// keys of floating-point values and workgroup reductions.
+#pragma once
+
+#include <type_traits>
+
+#include "common.h"
+
+namespace mirl {
+
+template <class E>
+constexpr int dtype_code() {
+  return std::is_same<E, F32>::value ? MIRL_DTYPE_F32
+         : std::is_same<E, BF16>::value ? MIRL_DTYPE_BF16 : MIRL_DTYPE_F16;
+}
+
+constexpr int kKeepCap = MIRL_FILTER_KEEP_CAP;
+
+// Per-row result of the forward (layout documented as mirl_filter_row_info).
+struct RowInfo {
+  float m;        // max of the kept values
+  float logsum;   // log(sum_kept exp(y - m))
+  float v_cut;    // kept <=> y > v_cut || (y == v_cut && j >= i_cut)
+  int32_t i_cut;
+  int32_t n_kept;
+  int32_t flags;  // bit 0: row must be (re)done by a general path
+};
+static_assert(sizeof(RowInfo) == sizeof(mirl_filter_row_info), "row info layout");
+
+struct FilterParams {
+  const void* logits;
+  int64_t R, V, sb, sr;
+  const int64_t* target;  // [B, R] view or null
+  int64_t tsb, tsr;
+  float T;
+  int has_t;
+  int top_k;  // 0: no top-k
+  int has_p;
+  float cut;  // fp32(1 - top_p)
+  // top-p decided in the 16-bit logits dtype: probabilities rounded to the
+  // dtype, their cumulative sum accumulated one element at a time in fp32 and
+  // each partial sum rounded to the dtype, compared with thr16 =
+  // dtype(fp32(1 - top_p)).  0: decided in fp32 (cumulative sum in double,
+  // rounded to fp32, compared with `cut`).
+  int dec16;
+  float thr16;
+  float* out;  // [rows] logprobs or null
+  RowInfo* info;
+  int32_t* kept_idx;  // [rows, kKeepCap]
+  float* kept_p;      // [rows, kKeepCap]
+  // top-k export (vocab_topk): [rows, top_k] values and global ids, or null
+  float* tk_vals;
+  int64_t* tk_idx;
+  int64_t tk_base;
+};
+
+// Order-preserving integer key of a float.  -0.0 maps to the key of +0.0: the
+// two compare equal, so a sort treats them as ties ordered by index.
+__device__ __forceinline__ uint32_t okey(float y) {
+  const uint32_t u = __float_as_uint(y == 0.f ? 0.f : y);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float from_okey(uint32_t k) {
+  const uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+  return __uint_as_float(u);
+}
+__device__ __forceinline__ bool kept_lex(float y, int64_t j, float vc, int32_t ic) {
+  return y > vc || (y == vc && j >= (int64_t)ic);
+}
+
+// y = dtype(float(x) / T)
+template <class E>
+__device__ __forceinline__ float scaled(float xf, const FilterParams& P) {
+  return P.has_t ? round_trip<E>(__fdiv_rn(xf, P.T)) : xf;
+}
+
+// Workgroup reductions over NT threads; `red` holds NT / 64 values.
+template <int NT>
+__device__ float block_sum_f(float v, float* red) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x % 64, wv = threadIdx.x / 64;
+  __syncthreads();
+  if (lane == 0) red[wv] = v;
+  __syncthreads();
+  float r = 0.f;
+  for (int k = 0; k < NT / 64; ++k) r += red[k];
+  return r;
+}
+template <int NT>
+__device__ float block_max_f(float v, float* red) {
+  v = wave_max(v);
+  const int lane = threadIdx.x % 64, wv = threadIdx.x / 64;
+  __syncthreads();
+  if (lane == 0) red[wv] = v;
+  __syncthreads();
+  float r = red[0];
+  for (int k = 1; k < NT / 64; ++k) r = fmaxf(r, red[k]);
+  return r;
+}
+template <int NT>
+__device__ int block_sum_i(int v, int* red) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  const int lane = threadIdx.x % 64, wv = threadIdx.x / 64;
+  __syncthreads();
+  if (lane == 0) red[wv] = v;
+  __syncthreads();
+  int r = 0;
+  for (int k = 0; k < NT / 64; ++k) r += red[k];
+  return r;
+}
+
+// Forward over 16-bit logits by the histogram kernel (topk_hist.hip): every
+// row when all_rows != 0, else only the rows whose info.flags bit 0 is set.
+int launch_hist_rows(const FilterParams& P, int dtype, int64_t rows, int all_rows,
+                     hipStream_t st);
+
+// Largest vocabulary the histogram kernel accepts (its exact-count table
+// covers at most 8 values repeated 65536 times or more).
+constexpr int64_t kHistMaxV = 9 * 65536 - 1;
+
+}  // namespace mirl

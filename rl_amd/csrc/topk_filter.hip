@@ -37,37 +37,15 @@
 // by the forward (<= kKeepCap entries), without reading the logits.  Rows with
 // larger kept sets are re-read and rewritten whole by the second pass.
 
-#include "common.h"
+#include "filter.h"
 
 namespace mirl {
 namespace {
 
 constexpr int kCandCap = 1024;  // candidates held in LDS by the fast path
-constexpr int kKeepCap = MIRL_FILTER_KEEP_CAP;
 constexpr int kMaxGroups = 20;  // vector groups per lane in the fast path
 constexpr int kGeneralThreads = 1024;
 
-// Per-row result of the forward (layout documented as mirl_filter_row_info).
-struct RowInfo {
-  float m;        // max of the kept values
-  float logsum;   // log(sum_kept exp(y - m))
-  float v_cut;    // kept <=> y > v_cut || (y == v_cut && j >= i_cut)
-  int32_t i_cut;
-  int32_t n_kept;
-  int32_t flags;  // bit 0: row must be (re)done by the general path
-};
-static_assert(sizeof(RowInfo) == sizeof(mirl_filter_row_info), "row info layout");
-
-// Order-preserving integer key of a float.  -0.0 maps to the key of +0.0: the
-// two compare equal, so a sort treats them as ties ordered by index.
-__device__ __forceinline__ uint32_t okey(float y) {
-  const uint32_t u = __float_as_uint(y == 0.f ? 0.f : y);
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-__device__ __forceinline__ float from_okey(uint32_t k) {
-  const uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
-  return __uint_as_float(u);
-}
 // Upper 16 bits of okey(v), rounded up: from_okey(hi << 16) >= v.  Exact for
 // 16-bit inputs, whose keys have zero low halves.
 __device__ __forceinline__ uint16_t okey_hi_up(float v) {
@@ -75,74 +53,6 @@ __device__ __forceinline__ uint16_t okey_hi_up(float v) {
   const uint32_t hi = k >> 16;
   return (uint16_t)(((k & 0xffffu) != 0u && hi < 0xffffu) ? hi + 1u : hi);
 }
-__device__ __forceinline__ bool kept_lex(float y, int64_t j, float vc, int32_t ic) {
-  return y > vc || (y == vc && j >= (int64_t)ic);
-}
-
-struct FilterParams {
-  const void* logits;
-  int64_t R, V, sb, sr;
-  const int64_t* target;  // [B, R] view or null
-  int64_t tsb, tsr;
-  float T;
-  int has_t;
-  int top_k;  // 0: no top-k
-  int has_p;
-  float cut;  // fp32(1 - top_p)
-  float* out;  // [rows] logprobs or null
-  RowInfo* info;
-  int32_t* kept_idx;  // [rows, kKeepCap]
-  float* kept_p;      // [rows, kKeepCap]
-  // top-k export (vocab_topk): [rows, top_k] values and global ids, or null
-  float* tk_vals;
-  int64_t* tk_idx;
-  int64_t tk_base;
-};
-
-// y = dtype(float(x) / T)
-template <class E>
-__device__ __forceinline__ float scaled(float xf, const FilterParams& P) {
-  return P.has_t ? round_trip<E>(__fdiv_rn(xf, P.T)) : xf;
-}
-
-// ---------------------------------------------------------------------------
-// workgroup helpers
-// ---------------------------------------------------------------------------
-template <int NT>
-__device__ float block_sum_f(float v, float* red) {
-  v = wave_sum(v);
-  const int lane = threadIdx.x % 64, wv = threadIdx.x / 64;
-  __syncthreads();
-  if (lane == 0) red[wv] = v;
-  __syncthreads();
-  float r = 0.f;
-  for (int k = 0; k < NT / 64; ++k) r += red[k];
-  return r;
-}
-template <int NT>
-__device__ float block_max_f(float v, float* red) {
-  v = wave_max(v);
-  const int lane = threadIdx.x % 64, wv = threadIdx.x / 64;
-  __syncthreads();
-  if (lane == 0) red[wv] = v;
-  __syncthreads();
-  float r = red[0];
-  for (int k = 1; k < NT / 64; ++k) r = fmaxf(r, red[k]);
-  return r;
-}
-template <int NT>
-__device__ int block_sum_i(int v, int* red) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  const int lane = threadIdx.x % 64, wv = threadIdx.x / 64;
-  __syncthreads();
-  if (lane == 0) red[wv] = v;
-  __syncthreads();
-  int r = 0;
-  for (int k = 0; k < NT / 64; ++k) r += red[k];
-  return r;
-}
-
 // k-th largest of the NT order keys okey(vals[i]) (vals in LDS), computed by
 // one wave: the largest c with #{key >= c} >= k, one bit per round from bit 31
 // down to LOW_BIT, counted by ballot.  Bits below LOW_BIT are left zero, so the
@@ -205,27 +115,52 @@ __device__ void finish_row(const FilterParams& P, int64_t row, const uint64_t* s
   const float m = y_at(n_k - 1);
   int first = 0;
   if (P.has_p) {
-    float zpart = 0.f;
-    for (int i = lane; i < n_k; i += 64) zpart += expf(y_at(i) - m);
-    const float Z = wave_sum(zpart);
-    // cumulative probability in ascending order, accumulated in double
-    double run = 0.0;
+    // the softmax normaliser, summed in double and rounded once to fp32
+    double zpart = 0.0;
+    for (int i = lane; i < n_k; i += 64) zpart += (double)expf(y_at(i) - m);
+    const float Z = (float)wave_sum(zpart);
     first = n_k - 1;  // the maximum is always kept
-    for (int base = 0; base < n_k; base += 64) {
-      const int i = base + lane;
-      double inc = (i < n_k) ? (double)(expf(y_at(i) - m) / Z) : 0.0;
+    if (P.dec16) {
+      // probabilities rounded to the logits dtype; the cumulative sum is
+      // accumulated one element at a time in fp32, in ascending order (every
+      // lane holds the same running sum and adds each element read from its
+      // lane), and each partial sum is rounded to the dtype before the compare
+      float S = 0.f;
+      for (int base = 0; base < n_k; base += 64) {
+        const int i = base + lane;
+        const float p = (i < n_k) ? round_trip<E>(expf(y_at(i) - m) / Z) : 0.f;
+        float mine = 0.f;
 #pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const double o = __shfl_up(inc, off, 64);
-        if (lane >= off) inc += o;
+        for (int l = 0; l < 64; ++l) {
+          S += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), l));
+          mine = (lane == l) ? S : mine;
+        }
+        const uint64_t bal = __ballot((i < n_k) && (round_trip<E>(mine) > P.thr16));
+        if (bal != 0ull) {
+          first = base + __ffsll((long long)bal) - 1;
+          break;
+        }
       }
-      const bool hit = (i < n_k) && ((float)(run + inc) > P.cut);
-      const uint64_t bal = __ballot(hit);
-      if (bal != 0ull) {
-        first = base + __ffsll((long long)bal) - 1;
-        break;
+    } else {
+      // cumulative probability in ascending order, accumulated in double
+      const float inv = 1.0f / Z;
+      double run = 0.0;
+      for (int base = 0; base < n_k; base += 64) {
+        const int i = base + lane;
+        double inc = (i < n_k) ? (double)(expf(y_at(i) - m) * inv) : 0.0;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+          const double o = __shfl_up(inc, off, 64);
+          if (lane >= off) inc += o;
+        }
+        const bool hit = (i < n_k) && ((float)(run + inc) > P.cut);
+        const uint64_t bal = __ballot(hit);
+        if (bal != 0ull) {
+          first = base + __ffsll((long long)bal) - 1;
+          break;
+        }
+        run += __shfl(inc, 63, 64);
       }
-      run += __shfl(inc, 63, 64);
     }
   }
   const uint64_t ck = skeys[first];
@@ -971,6 +906,9 @@ int launch_fwd(const FilterParams& P, int64_t rows, hipStream_t st) {
     }
     if (int e = check_launch("filter_fast_kernel")) return e;
   }
+  // the rows left to a general path: all of them, or those the fast kernel flagged
+  if (sizeof(typename E::raw) == 2 && P.V <= kHistMaxV)
+    return launch_hist_rows(P, dtype_code<E>(), rows, fast ? 0 : 1, st);
   hipLaunchKernelGGL((filter_general_kernel<E>), dim3((unsigned)rows), dim3(kGeneralThreads), 0, st,
                      P, fast ? 0 : 1);
   return check_launch("filter_general_kernel");
@@ -1019,9 +957,17 @@ int launch_bwd(const FilterBwdParams& P, int64_t B, int64_t rows, hipStream_t st
 }
 
 int check_filter_args(int dtype, int64_t B, int64_t R, int64_t V, int top_k, double top_p,
-                      double temperature) {
+                      double temperature, int p_dtype) {
   if (dtype != MIRL_DTYPE_F32 && dtype != MIRL_DTYPE_BF16 && dtype != MIRL_DTYPE_F16) {
     set_error("unsupported logits dtype code %d", dtype);
+    return MIRL_ERR_UNSUPPORTED;
+  }
+  MIRL_REQUIRE(p_dtype == MIRL_DTYPE_F32 || p_dtype == dtype,
+               "top-p decision dtype %d must be fp32 (%d) or the logits dtype (%d)", p_dtype,
+               MIRL_DTYPE_F32, dtype);
+  if (p_dtype != MIRL_DTYPE_F32 && top_p < 1.0 && V > kHistMaxV) {
+    set_error("top-p decided in a 16-bit dtype supports vocabularies up to %lld (got %lld)",
+              (long long)kHistMaxV, (long long)V);
     return MIRL_ERR_UNSUPPORTED;
   }
   MIRL_REQUIRE(B >= 0 && R >= 0 && V > 0, "invalid shape B=%lld R=%lld V=%lld", (long long)B,
@@ -1036,10 +982,20 @@ int check_filter_args(int dtype, int64_t B, int64_t R, int64_t V, int top_k, dou
   return MIRL_OK;
 }
 
+// fp32 -> bf16 -> fp32, round to nearest even (finite inputs)
+float round_bf16_host(float f) {
+  uint32_t u;
+  __builtin_memcpy(&u, &f, 4);
+  u = (u + 0x7fffu + ((u >> 16) & 1u)) & 0xffff0000u;
+  float r;
+  __builtin_memcpy(&r, &u, 4);
+  return r;
+}
+
 FilterParams make_params(const void* logits, int64_t R, int64_t V, int64_t sb, int64_t sr,
                          const int64_t* target, int64_t tsb, int64_t tsr, double temperature,
-                         int top_k, double top_p, float* out, void* info, int32_t* kept_idx,
-                         float* kept_p) {
+                         int top_k, double top_p, int p_dtype, float* out, void* info,
+                         int32_t* kept_idx, float* kept_p) {
   FilterParams P;
   P.logits = logits;
   P.R = R;
@@ -1054,6 +1010,11 @@ FilterParams make_params(const void* logits, int64_t R, int64_t V, int64_t sb, i
   P.top_k = top_k > 0 ? top_k : 0;
   P.has_p = top_p < 1.0;
   P.cut = (float)(1.0 - top_p);
+  P.dec16 = p_dtype != MIRL_DTYPE_F32 && P.has_p;
+  // the Python float 1 - top_p meets a 16-bit tensor as that dtype: double ->
+  // float -> dtype, each rounding to nearest even
+  P.thr16 = p_dtype == MIRL_DTYPE_BF16 ? round_bf16_host(P.cut)
+            : p_dtype == MIRL_DTYPE_F16 ? (float)(_Float16)P.cut : P.cut;
   P.out = out;
   P.info = static_cast<RowInfo*>(info);
   P.kept_idx = kept_idx;
@@ -1073,18 +1034,18 @@ extern "C" int mirl_filtered_logprob_fwd(const void* logits, int dtype, int64_t 
                                          int64_t V, int64_t stride_b, int64_t stride_r,
                                          const int64_t* target, int64_t t_stride_b,
                                          int64_t t_stride_r, double temperature, int top_k,
-                                         double top_p, float* out, void* row_info,
+                                         double top_p, int p_dtype, float* out, void* row_info,
                                          int32_t* kept_idx, float* kept_p, void* stream) {
   clear_error();
-  if (int e = check_filter_args(dtype, B, R, V, top_k, top_p, temperature)) return e;
+  if (int e = check_filter_args(dtype, B, R, V, top_k, top_p, temperature, p_dtype)) return e;
   const int64_t rows = B * R;
   if (rows == 0) return MIRL_OK;
   MIRL_REQUIRE(rows < (int64_t(1) << 31), "too many rows (%lld)", (long long)rows);
   MIRL_REQUIRE(logits && row_info && kept_idx && kept_p, "null pointer argument");
   MIRL_REQUIRE(out == nullptr || target != nullptr, "out given without target");
   const FilterParams P = make_params(logits, R, V, stride_b, stride_r, target, t_stride_b,
-                                     t_stride_r, temperature, top_k, top_p, out, row_info,
-                                     kept_idx, kept_p);
+                                     t_stride_r, temperature, top_k, top_p, p_dtype, out,
+                                     row_info, kept_idx, kept_p);
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == MIRL_DTYPE_F32) return launch_fwd<F32>(P, rows, st);
   if (dtype == MIRL_DTYPE_BF16) return launch_fwd<BF16>(P, rows, st);
@@ -1141,19 +1102,19 @@ extern "C" int mirl_filtered_logprob_bwd(const void* logits, int dtype, int64_t 
 }
 
 extern "C" int mirl_top_k_top_p_mask(const void* logits, int dtype, int64_t N, int64_t V,
-                                     int64_t row_stride, int top_k, double top_p,
+                                     int64_t row_stride, int top_k, double top_p, int p_dtype,
                                      void* row_info, int32_t* kept_idx, float* kept_p,
                                      void* filtered, int64_t filtered_row_stride,
                                      uint8_t* keep_mask, int64_t keep_row_stride, void* stream) {
   clear_error();
-  if (int e = check_filter_args(dtype, N, 1, V, top_k, top_p, 1.0)) return e;
+  if (int e = check_filter_args(dtype, N, 1, V, top_k, top_p, 1.0, p_dtype)) return e;
   if (N == 0) return MIRL_OK;
   MIRL_REQUIRE(N < (int64_t(1) << 31), "too many rows (%lld)", (long long)N);
   MIRL_REQUIRE(logits && row_info && kept_idx && kept_p && filtered && keep_mask,
                "null pointer argument");
   // rows are [N, V] with row stride `row_stride`: R = 1 so that row = b
   const FilterParams P = make_params(logits, 1, V, row_stride, 0, nullptr, 0, 0, 1.0, top_k,
-                                     top_p, nullptr, row_info, kept_idx, kept_p);
+                                     top_p, p_dtype, nullptr, row_info, kept_idx, kept_p);
   hipStream_t st = static_cast<hipStream_t>(stream);
   int e;
   if (dtype == MIRL_DTYPE_F32) e = launch_fwd<F32>(P, N, st);
@@ -1196,7 +1157,7 @@ extern "C" int mirl_vocab_topk(const void* logits, int dtype, int64_t B, int64_t
   MIRL_REQUIRE(rows < (int64_t(1) << 31), "too many rows (%lld)", (long long)rows);
   MIRL_REQUIRE(logits && values && indices && workspace, "null pointer argument");
   FilterParams P = make_params(logits, R, V, stride_b, stride_r, nullptr, 0, 0, 1.0, k, 1.0,
-                               nullptr, workspace, nullptr, nullptr);
+                               MIRL_DTYPE_F32, nullptr, workspace, nullptr, nullptr);
   P.tk_vals = values;
   P.tk_idx = indices;
   P.tk_base = vocab_start;

@@ -1,0 +1,810 @@
+// Filtered-logprob forward for 16-bit logits (bf16 / fp16) from an exact
+// count table of the row's values: the general path of the filter for top-p
+// without top-k, k > 1024, and rows the fast path flagged.
+//
+// Semantics: those of topk_filter.hip (reference
+// nemo_rl/algorithms/logits_sampling_utils.py:111-212 and
+// nemo_rl/distributed/model_utils.py:382-432).  The kept set is a suffix of the
+// ascending (value, index) order, described by the cut (v_cut, i_cut).
+//
+// One 1024-thread workgroup per row reads the row once with 16-byte
+// nontemporal loads and keeps it in registers when it fits (kRegVec vectors
+// per lane, 163840 elements).  Every raw value is counted into a table of
+// 65536 16-bit counts in LDS (128 KB), indexed by an order-preserving key of
+// the raw bits; the values that occur are the table's non-empty entries, and
+// the value y = dtype(x / T) of an entry is computed from its key.  So the
+// top-k value, the normaliser, the cumulative probability in ascending order
+// and the kept set's log-sum-exp all follow from the table, each thread
+// owning 64 consecutive keys:
+//   top-k:  suffix counts over the keys give the k-th largest value;
+//   Z:      sum over kept-k keys of count * exp(y - m);
+//   top-p:  masses count * p(y) summed in key order give the cumulative
+//           probability at the end of every entry; the cut is the first
+//           element at which it passes the threshold.  With fp32 decisions the
+//           sum is exact in double and rounded to fp32, as the reference's
+//           double-accumulated cumsum is.  With 16-bit decisions the
+//           reference accumulates the dtype-rounded probabilities one at a
+//           time in fp32: the exact sum plus a rigorous bound on that
+//           sequence's rounding (zero inside a binade when the addend is a
+//           multiple of the accumulator's ulp, half an ulp per binade crossing
+//           or per addition otherwise) decides the cut for almost every row;
+//           a row where the bound leaves the cut undecided is walked exactly
+//           by one wave (additions of equal values inside one binade are
+//           applied in closed form).
+// A second sweep over the registers finds the index cut inside the tied
+// values (the r-th smallest index among them); a third, for rows with at most
+// MIRL_FILTER_KEEP_CAP kept entries, writes the kept list for the backward.
+// Counts of 65536 or more wrap the 16-bit entries; the total then differs from
+// V, and two more sweeps count the affected 256-key blocks exactly.
+
+#include "filter.h"
+
+namespace mirl {
+namespace {
+
+constexpr int kHT = 1024;          // threads per row
+constexpr int kHW = kHT / 64;      // waves per row
+constexpr int kHistWords = 32768;  // 65536 16-bit counts
+constexpr int kOvfSlots = 8;       // 256-key blocks with exact 32-bit counts
+constexpr int kRegVec = 0;         // 16-byte vectors per lane held in registers (0: sweeps re-read the row)
+
+struct HistShared {
+  uint32_t hist[kHistWords];
+  uint32_t ovf_cnt[kOvfSlots * 256];
+  uint32_t coarse[256];
+  uint32_t tcnt[kHT];  // elements per thread's key range
+  double red_d[kHW * 4];
+  uint32_t red_u[kHW * 4];
+  uint32_t ovf_block[kOvfSlots];
+  int novf;
+  int first_lo, first_hi;
+  uint32_t key_lo, pos_lo, key_hi, pos_hi;
+  uint32_t kth_key;
+  int walk_hit;
+  int32_t elem_index;
+  int nk;
+};
+
+template <class E>
+__device__ __forceinline__ uint32_t bits16(typename E::raw v) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, v);
+}
+template <class E>
+__device__ __forceinline__ float value16(uint32_t r) {
+  if constexpr (std::is_same<E, BF16>::value)
+    return __uint_as_float(r << 16);
+  else
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)r);
+}
+template <class E>
+__device__ __forceinline__ uint32_t raw_of_value16(float f) {
+  return bits16<E>(E::from_float(f));
+}
+// Order-preserving key of raw 16-bit float bits; -0 is counted as +0.
+__device__ __forceinline__ uint32_t okey16(uint32_t r) {
+  r &= 0xffffu;
+  if (r == 0x8000u) r = 0u;
+  return (r & 0x8000u) ? (~r & 0xffffu) : (r | 0x8000u);
+}
+__device__ __forceinline__ uint32_t raw_of_okey16(uint32_t k) {
+  return (k & 0x8000u) ? (k & 0x7fffu) : (~k & 0xffffu);
+}
+
+template <class T>
+__device__ __forceinline__ T wave_incl_scan(T v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const T o = __shfl_up(v, off, 64);
+    if (lane >= off) v += o;
+  }
+  return v;
+}
+
+// Exclusive prefix over the workgroup in thread order; *total = the sum.
+template <class T>
+__device__ T block_excl_scan(T v, T* red, T* total) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const T inc = wave_incl_scan(v);
+  T ex = __shfl_up(inc, 1, 64);
+  if (lane == 0) ex = T(0);
+  __syncthreads();
+  if (lane == 63) red[wv] = inc;
+  __syncthreads();
+  T base = T(0), tot = T(0);
+  for (int w = 0; w < kHW; ++w) {
+    const T s = red[w];
+    if (w < wv) base += s;
+    tot += s;
+  }
+  *total = tot;
+  return base + ex;
+}
+
+template <class T, int N>
+__device__ void block_sum_n(T (&v)[N], T* red) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+#pragma unroll
+  for (int i = 0; i < N; ++i)
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v[i] += __shfl_xor(v[i], off, 64);
+  __syncthreads();
+  if (lane == 0)
+#pragma unroll
+    for (int i = 0; i < N; ++i) red[i * kHW + wv] = v[i];
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    T s = T(0);
+    for (int w = 0; w < kHW; ++w) s += red[i * kHW + w];
+    v[i] = s;
+  }
+}
+
+__device__ uint32_t block_max_u(uint32_t v, uint32_t* red) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, off, 64));
+  __syncthreads();
+  if (lane == 0) red[wv] = v;
+  __syncthreads();
+  uint32_t r = red[0];
+  for (int w = 1; w < kHW; ++w) r = max(r, red[w]);
+  return r;
+}
+
+// Bound on the rounding of n fp32 additions S <- fl(S + p) that take an exact
+// running sum from X0 to X1 (> 0), given that S stays within a factor 2 of
+// the exact sum (true for fewer than 2^22 additions).  S then stays below
+// 2^(e1 + 1), e1 = ilogb(X1) + 1, where the ulp is u.  An addend that is a
+// multiple of u adds exactly inside each binade and can round only where S
+// enters a new binade (at most e1 - ilogb(X0) + 2 times, half an ulp each);
+// any other addend may round on every addition.
+__device__ double run_error_bound(uint32_t n, double p, double X0, double X1) {
+  if (p == 0.0 || n == 0u) return 0.0;
+  const int e1 = ilogb(X1) + 1;
+  const int eu = (e1 < -126 ? -126 : e1) - 23;
+  const double u = ldexp(1.0, eu);
+  const double q = ldexp(p, -eu);
+  if (q == floor(q)) {
+    const int e0 = X0 > 0.0 ? ilogb(X0) : ilogb(p);
+    return (double)(e1 - e0 + 2) * 0.5 * u;
+  }
+  return (double)n * 0.5 * u;
+}
+
+// n additions S <- fl32(S + p) of one value p >= 0.  Returns true when a
+// partial sum reaches B (S >= B); *at is then the 1-based addition that did.
+// Inside the binade [2^e, 2^(e+1)) of S every addition adds p rounded to the
+// binade's ulp u (to nearest, a tie going to the even multiple of u), so runs
+// of additions that stay inside the binade are applied at once.
+__device__ bool seq_add_run(float& S, float p, uint32_t n, float B, uint32_t* at) {
+  uint32_t done = 0;
+  while (done < n) {
+    if (S == 0.f || n - done <= 2u) {
+      S = S + p;
+      ++done;
+      if (S >= B) {
+        *at = done;
+        return true;
+      }
+      continue;
+    }
+    int eS = ilogbf(S);
+    if (eS < -126) eS = -126;
+    const int eu = eS - 23;
+    const double Su = ldexp((double)S, -eu);  // integer < 2^24
+    const double Tu = 16777216.0;             // 2^(eS + 1) in units of u
+    const double q = ldexp((double)p, -eu);
+    const double fq = floor(q);
+    double d;
+    if (q == fq) {
+      d = q;
+    } else if (q - fq != 0.5) {
+      d = (q - fq < 0.5) ? fq : fq + 1.0;
+    } else if (fmod(Su, 2.0) == 0.0) {
+      // a tie from an even multiple: rounding to even keeps S even
+      d = (fmod(fq, 2.0) == 0.0) ? fq : fq + 1.0;
+    } else {
+      S = S + p;  // a tie from an odd multiple rounds up to an even one
+      ++done;
+      if (S >= B) {
+        *at = done;
+        return true;
+      }
+      continue;
+    }
+    if (d == 0.0) return false;  // the remaining additions leave S unchanged
+    const double smax = floor((Tu - 1.0 - Su) / d);  // additions that stay in the binade
+    const double rem = (double)(n - done);
+    const double s = smax < rem ? smax : rem;
+    const double Bu = ldexp((double)B, -eu);  // B > S >= 2^eS: an integer in units of u
+    if (s > 0.0 && Su + s * d >= Bu) {
+      const double need = ceil((Bu - Su) / d);
+      S = (float)ldexp(Su + need * d, eu);
+      done += (uint32_t)need;
+      *at = done;
+      return true;
+    }
+    S = (float)ldexp(Su + s * d, eu);
+    done += (uint32_t)s;
+    if (done < n && s == smax) {  // the next addition leaves the binade
+      S = S + p;
+      ++done;
+      if (S >= B) {
+        *at = done;
+        return true;
+      }
+    }
+  }
+  return false;
+}
+
+// WALK = false: rows whose 16-bit cut the bound leaves undecided are flagged
+// (info.flags bit 0) and left to the WALK = true launch, which decides them by
+// the exact sequence.
+template <class E, int NV, bool WALK>
+__global__ __launch_bounds__(kHT) void filter_hist_kernel(FilterParams P, int all_rows) {
+  using raw = typename E::raw;
+  __shared__ HistShared sh;
+  const int64_t row = blockIdx.x;
+  if (!all_rows && (P.info[row].flags & 1) == 0) return;
+  const int64_t b = row / P.R, r = row - b * P.R;
+  const raw* x = static_cast<const raw*>(P.logits) + b * P.sb + r * P.sr;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int64_t V = P.V;
+  const RowSpan<E> sp(x, V);
+  const vu4* xv = reinterpret_cast<const vu4*>(x + sp.head);
+  const int64_t nvec = sp.nvec;
+
+  // ---- pass 1: the row into registers, then every value into the table ----
+  vu4 q[NV > 0 ? NV : 1];
+  if constexpr (NV > 0) {
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int64_t v = tid + (int64_t)j * kHT;
+      if (v < nvec) q[j] = __builtin_nontemporal_load(xv + v);
+    }
+  }
+  const bool has_h = tid < sp.head;
+  const bool has_tl = sp.tail0 + tid < V;
+  const uint32_t hraw = has_h ? bits16<E>(x[tid]) : 0u;
+  const uint32_t traw = has_tl ? bits16<E>(x[sp.tail0 + tid]) : 0u;
+  {
+    vu4* h4 = reinterpret_cast<vu4*>(sh.hist);
+    for (int i = tid; i < kHistWords / 4; i += kHT) h4[i] = vu4{0u, 0u, 0u, 0u};
+  }
+  if (tid == 0) {
+    sh.novf = 0;
+    sh.first_lo = kHT;
+    sh.first_hi = kHT;
+    sh.nk = 0;
+    sh.walk_hit = 0;
+    sh.elem_index = 0;
+    sh.kth_key = 0;
+    sh.key_lo = sh.pos_lo = sh.key_hi = sh.pos_hi = 0;
+  }
+  __syncthreads();
+
+  // calls f(index, raw bits) for every element of this thread, in index order
+  // within each of its segments: head element, register/vector slots, tail
+  auto sweep = [&](auto&& f) {
+    if (has_h) f((int64_t)tid, hraw);
+    if constexpr (NV > 0) {
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        const int64_t v = tid + (int64_t)j * kHT;
+        if (v < nvec) {
+          const uint32_t w[4] = {q[j].x, q[j].y, q[j].z, q[j].w};
+          const int64_t base = sp.head + v * 8;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            f(base + 2 * e, w[e] & 0xffffu);
+            f(base + 2 * e + 1, w[e] >> 16);
+          }
+        }
+      }
+    } else {
+      for (int64_t v = tid; v < nvec; v += kHT) {
+        const vu4 t = __builtin_nontemporal_load(xv + v);
+        const uint32_t w[4] = {t.x, t.y, t.z, t.w};
+        const int64_t base = sp.head + v * 8;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          f(base + 2 * e, w[e] & 0xffffu);
+          f(base + 2 * e + 1, w[e] >> 16);
+        }
+      }
+    }
+    if (has_tl) f(sp.tail0 + tid, traw);
+  };
+
+  uint32_t kmax = 0;
+  sweep([&](int64_t, uint32_t rw) {
+    const uint32_t k = okey16(rw);
+    atomicAdd(&sh.hist[k >> 1], (k & 1u) ? 0x10000u : 1u);
+    kmax = max(kmax, k);
+  });
+  const uint32_t kmx = block_max_u(kmax, sh.red_u);  // its barriers complete the table
+
+  // ---- the table: counts, repaired where 16-bit entries wrapped ----------
+  const uint32_t k0 = (uint32_t)tid * 64u;
+  uint32_t ct = 0;
+#pragma unroll 4
+  for (int w = 0; w < 32; ++w) {
+    const uint32_t word = sh.hist[tid * 32 + w];
+    ct += (word & 0xffffu) + (word >> 16);
+  }
+  {
+    uint32_t tot[1] = {ct};
+    block_sum_n<uint32_t, 1>(tot, sh.red_u);
+    if (tot[0] != (uint32_t)V) {
+      // some value occurs 65536 times or more: find its 256-key blocks by exact
+      // block counts, then count those blocks exactly
+      for (int i = tid; i < 256; i += kHT) sh.coarse[i] = 0u;
+      __syncthreads();
+      sweep([&](int64_t, uint32_t rw) { atomicAdd(&sh.coarse[okey16(rw) >> 8], 1u); });
+      __syncthreads();
+      if (tid < 256) {
+        uint32_t fine = 0;
+        for (int i = 0; i < 128; ++i) {
+          const uint32_t word = sh.hist[tid * 128 + i];
+          fine += (word & 0xffffu) + (word >> 16);
+        }
+        if (fine != sh.coarse[tid]) {
+          const int s = atomicAdd(&sh.novf, 1);
+          if (s < kOvfSlots) sh.ovf_block[s] = (uint32_t)tid;
+        }
+      }
+      __syncthreads();
+      const int nb = sh.novf;
+      if (nb > kOvfSlots) {  // not reachable for V <= kHistMaxV
+        if (tid == 0) {
+          RowInfo ri{};
+          ri.flags = 2;
+          P.info[row] = ri;
+        }
+        return;
+      }
+      for (int i = tid; i < nb * 256; i += kHT) sh.ovf_cnt[i] = 0u;
+      __syncthreads();
+      sweep([&](int64_t, uint32_t rw) {
+        const uint32_t k = okey16(rw);
+        for (int s = 0; s < nb; ++s)
+          if (sh.ovf_block[s] == (k >> 8)) atomicAdd(&sh.ovf_cnt[s * 256 + (k & 255u)], 1u);
+      });
+      __syncthreads();
+    }
+  }
+  const int novf = sh.novf;
+  auto kcount = [&](uint32_t k) -> uint32_t {
+    if (novf > 0) {
+      for (int s = 0; s < novf; ++s)
+        if (sh.ovf_block[s] == (k >> 8)) return sh.ovf_cnt[s * 256 + (k & 255u)];
+    }
+    return (sh.hist[k >> 1] >> ((k & 1u) << 4)) & 0xffffu;
+  };
+  // f(key, count) over this thread's 64 keys with a non-zero count, ascending
+  auto for_range = [&](auto&& f) {
+#pragma unroll 1
+    for (int w = 0; w < 32; ++w) {
+      const uint32_t word = sh.hist[tid * 32 + w];
+      if (word == 0u && novf == 0) continue;
+      const uint32_t ka = k0 + 2u * (uint32_t)w;
+      const uint32_t na = novf ? kcount(ka) : (word & 0xffffu);
+      const uint32_t nb = novf ? kcount(ka + 1u) : (word >> 16);
+      if (na) f(ka, na);
+      if (nb) f(ka + 1u, nb);
+    }
+  };
+  if (novf > 0) {
+    ct = 0;
+    for_range([&](uint32_t, uint32_t n) { ct += n; });
+  }
+  sh.tcnt[tid] = ct;
+
+  auto yk = [&](uint32_t k) { return scaled<E>(value16<E>(raw_of_okey16(k)), P); };
+  // smallest key in [lo, hi] whose value is >= y (hi + 1 if none)
+  auto lowest_ge = [&](uint32_t lo, uint32_t hi, float y) {
+    uint32_t a = lo, c = hi + 1u;
+    while (a < c) {
+      const uint32_t mid = (a + c) >> 1;
+      if (yk(mid) >= y) c = mid; else a = mid + 1u;
+    }
+    return a;
+  };
+  // largest key in [lo, hi] whose value is <= y (lo - 1 if none)
+  auto highest_le = [&](uint32_t lo, uint32_t hi, float y) {
+    uint32_t a = lo, c = hi + 1u;
+    while (a < c) {
+      const uint32_t mid = (a + c) >> 1;
+      if (yk(mid) <= y) a = mid + 1u; else c = mid;
+    }
+    return a - 1u;
+  };
+  const float m = yk(kmx);
+
+  // ---- top-k: the k-th largest value from suffix counts ---------------------
+  uint32_t thr_key = 0;
+  float y_thr = -INFINITY;
+  if (P.top_k > 0) {
+    __syncthreads();
+    const int rr = kHT - 1 - tid;  // thread tid scans key range rr (descending order)
+    const uint32_t crev = sh.tcnt[rr];
+    uint32_t tot;
+    const uint32_t above = block_excl_scan<uint32_t>(crev, sh.red_u, &tot);
+    const uint32_t kk = (uint32_t)P.top_k;
+    if (above < kk && kk <= above + crev) {
+      uint32_t acc = above;
+#pragma unroll 1
+      for (int i = 63; i >= 0; --i) {
+        const uint32_t key = (uint32_t)rr * 64u + (uint32_t)i;
+        acc += kcount(key);
+        if (acc >= kk) {
+          sh.kth_key = key;
+          break;
+        }
+      }
+    }
+    __syncthreads();
+    y_thr = yk(sh.kth_key);
+    thr_key = lowest_ge(0u, sh.kth_key, y_thr);
+  }
+
+  // ---- normaliser over the kept-k values ------------------------------------
+  double zsum[1] = {0.0};
+  for_range([&](uint32_t key, uint32_t n) {
+    if (key >= thr_key) zsum[0] += (double)n * (double)expf(yk(key) - m);
+  });
+  block_sum_n<double, 1>(zsum, sh.red_d);
+  const float Z = (float)zsum[0];
+
+  // ---- top-p cut -----------------------------------------------------------
+  // (cut_key, cut_pos): the cut is the cut_pos-th element (1-based) of key
+  // cut_key in the ascending order; no cut keeps the maximum only
+  bool have_cut = false;
+  uint32_t cut_key = 0, cut_pos = 0;
+  if (P.has_p) {
+    const float inv = 1.0f / Z;
+    auto pmass = [&](uint32_t key) -> double {
+      const float e = expf(yk(key) - m);
+      return P.dec16 ? (double)round_trip<E>(e / Z) : (double)(e * inv);
+    };
+    double mt = 0.0;
+    for_range([&](uint32_t key, uint32_t n) {
+      if (key >= thr_key) mt += (double)n * pmass(key);
+    });
+    double mtot;
+    const double X0 = block_excl_scan<double>(mt, sh.red_d, &mtot);
+    // first addition t in [1, n] of a run X + t p for which hit() holds (hit(X + n p) is true)
+    auto first_in_run = [&](double X, double p, uint32_t n, auto&& hit) {
+      uint32_t a = 1u, c = n;
+      while (a < c) {
+        const uint32_t mid = a + ((c - a) >> 1);
+        if (hit(X + (double)mid * p)) c = mid; else a = mid + 1u;
+      }
+      return a;
+    };
+    if (!P.dec16) {
+      const float cut = P.cut;
+      auto hit = [&](double X) { return (float)X > cut; };
+      double X = X0;
+      bool found = false;
+      uint32_t fk = 0, fp = 0;
+      for_range([&](uint32_t key, uint32_t n) {
+        if (found || key < thr_key) return;
+        const double p = pmass(key);
+        if (hit(X + (double)n * p)) {
+          found = true;
+          fk = key;
+          fp = hit(X) ? 1u : first_in_run(X, p, n, hit);
+        }
+        X += (double)n * p;
+      });
+      if (found) atomicMin(&sh.first_lo, tid);
+      __syncthreads();
+      if (sh.first_lo == tid) {
+        sh.key_lo = fk;
+        sh.pos_lo = fp;
+      }
+      __syncthreads();
+      have_cut = sh.first_lo < kHT;
+      cut_key = sh.key_lo;
+      cut_pos = sh.pos_lo;
+    } else {
+      // smallest fp32 S whose rounding to the dtype exceeds thr16
+      const float thr = P.thr16;
+      const float nxt = value16<E>(raw_of_value16<E>(thr) + 1u);
+      const float mid = 0.5f * (thr + nxt);
+      const float Bthr = round_trip<E>(mid) > thr ? mid : nextafterf(mid, INFINITY);
+      const double Bd = (double)Bthr;
+      // rounding bounds of the sequential sum, then the cut for S = X - D and X + D
+      double bt = 0.0;
+      {
+        double X = X0;
+        for_range([&](uint32_t key, uint32_t n) {
+          if (key < thr_key) return;
+          const double p = pmass(key);
+          const double X1 = X + (double)n * p;
+          bt += run_error_bound(n, p, X, X1);
+          X = X1;
+        });
+      }
+      double btot;
+      const double D0 = block_excl_scan<double>(bt, sh.red_d, &btot);
+      {
+        double X = X0, D = D0;
+        bool flo = false, fhi = false;
+        uint32_t klo = 0, plo = 0, khi = 0, phi = 0;
+        for_range([&](uint32_t key, uint32_t n) {
+          if ((flo && fhi) || key < thr_key) return;
+          const double p = pmass(key);
+          const double X1 = X + (double)n * p;
+          const double Db = D + run_error_bound(n, p, X, X1);
+          auto hlo = [&](double v) { return v + Db >= Bd; };
+          auto hhi = [&](double v) { return v - Db >= Bd; };
+          if (!flo && hlo(X1)) {
+            flo = true;
+            klo = key;
+            plo = hlo(X) ? 1u : first_in_run(X, p, n, hlo);
+          }
+          if (!fhi && hhi(X1)) {
+            fhi = true;
+            khi = key;
+            phi = hhi(X) ? 1u : first_in_run(X, p, n, hhi);
+          }
+          X = X1;
+          D = Db;
+        });
+        if (flo) atomicMin(&sh.first_lo, tid);
+        if (fhi) atomicMin(&sh.first_hi, tid);
+        __syncthreads();
+        if (sh.first_lo == tid) {
+          sh.key_lo = klo;
+          sh.pos_lo = plo;
+        }
+        if (sh.first_hi == tid) {
+          sh.key_hi = khi;
+          sh.pos_hi = phi;
+        }
+        __syncthreads();
+      }
+      const bool none_lo = sh.first_lo >= kHT, none_hi = sh.first_hi >= kHT;
+      const bool certain = (none_lo && none_hi) ||
+                           (!none_lo && !none_hi && sh.key_lo == sh.key_hi &&
+                            sh.pos_lo == sh.pos_hi);
+      if (certain) {
+        have_cut = !none_hi;
+        cut_key = sh.key_hi;
+        cut_pos = sh.pos_hi;
+      } else if constexpr (!WALK) {
+        if (tid == 0) {
+          RowInfo ri{};
+          ri.flags = 1;
+          P.info[row] = ri;
+        }
+        return;
+      } else {
+        // the exact sequence, one wave: ranges whose additions are all exact
+        // and stay inside S's binade below the threshold are added at once
+        __syncthreads();
+        if (tid < 64) {
+          float S = 0.f;
+          bool hit = false;
+          uint32_t hk = 0, hp = 0;
+          for (int t = 0; t < kHT && !hit; ++t) {
+            if (sh.tcnt[t] == 0u) continue;
+            const uint32_t key = (uint32_t)t * 64u + (uint32_t)lane;
+            const uint32_t n = key >= thr_key ? kcount(key) : 0u;
+            const float p = n ? (float)pmass(key) : 0.f;
+            bool batched = false;
+            if (S > 0.f) {
+              int eS = ilogbf(S);
+              if (eS < -126) eS = -126;
+              const double qp = ldexp((double)p, 23 - eS);
+              const bool exact = n == 0u || qp == floor(qp);
+              double sum = (double)n * (double)p;
+#pragma unroll
+              for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+              const double top = ldexp(1.0, eS + 1);
+              if (__ballot(!exact) == 0ull && (double)S + sum < top && (double)S + sum < Bd) {
+                S = (float)((double)S + sum);
+                batched = true;
+              }
+            }
+            if (!batched) {
+              uint64_t nz = __ballot(n > 0u);
+              while (nz != 0ull) {
+                const int l = __ffsll((long long)nz) - 1;
+                nz &= nz - 1ull;
+                const uint32_t nl = (uint32_t)__builtin_amdgcn_readlane((int)n, l);
+                const float pl = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), l));
+                uint32_t at = 0;
+                if (seq_add_run(S, pl, nl, Bthr, &at)) {
+                  hit = true;
+                  hk = (uint32_t)t * 64u + (uint32_t)l;
+                  hp = at;
+                  break;
+                }
+              }
+            }
+          }
+          if (lane == 0) {
+            sh.walk_hit = hit ? 1 : 0;
+            sh.key_lo = hk;
+            sh.pos_lo = hp;
+          }
+        }
+        __syncthreads();
+        have_cut = sh.walk_hit != 0;
+        cut_key = sh.key_lo;
+        cut_pos = sh.pos_lo;
+      }
+    }
+  }
+
+  // ---- the cut's value group, kept count and log-sum-exp --------------------
+  uint32_t g_lo, g_hi;
+  float v_cut;
+  if (!P.has_p) {
+    v_cut = y_thr;
+    g_lo = thr_key;
+    g_hi = highest_le(thr_key, 65535u, y_thr);
+  } else {
+    const uint32_t ck = have_cut ? cut_key : kmx;
+    v_cut = yk(ck);
+    g_lo = lowest_ge(thr_key, ck, v_cut);
+    g_hi = highest_le(ck, 65535u, v_cut);
+  }
+  double sums[2] = {0.0, 0.0};      // kept mass above the group, group size (as exact doubles)
+  uint32_t cnts[2] = {0u, 0u};      // elements above the group, group elements before the cut
+  for_range([&](uint32_t key, uint32_t n) {
+    if (key > g_hi) {
+      cnts[0] += n;
+      sums[0] += (double)n * (double)expf(yk(key) - m);
+    } else if (key >= g_lo) {
+      sums[1] += (double)n;
+      if (have_cut && key < cut_key) cnts[1] += n;
+    }
+  });
+  block_sum_n<double, 2>(sums, sh.red_d);
+  block_sum_n<uint32_t, 2>(cnts, sh.red_u);
+  const uint32_t n_group = (uint32_t)sums[1];
+  uint32_t rcut = 0;  // group elements (in index order) before the cut
+  if (P.has_p) rcut = have_cut ? cnts[1] + cut_pos - 1u : n_group - 1u;
+  const uint32_t n_kept = cnts[0] + (n_group - rcut);
+  const double ksum = sums[0] + (double)(n_group - rcut) * (double)expf(v_cut - m);
+  const float logsum = logf((float)ksum);
+
+  // ---- index cut inside the group: its rcut-th smallest index ---------------
+  int32_t i_cut = 0;
+  if (rcut > 0u) {
+    auto member = [&](uint32_t rw) {
+      const uint32_t k = okey16(rw);
+      return k >= g_lo && k <= g_hi;
+    };
+    uint32_t run = 0;
+    bool done = false;
+    // one segment of consecutive indices per thread: base index and a bit
+    // mask of its members (bit e = element base + e)
+    auto segment = [&](int64_t base, uint32_t mask) {
+      const uint32_t c = (uint32_t)__popc(mask);
+      uint32_t tot;
+      const uint32_t ex = block_excl_scan<uint32_t>(c, sh.red_u, &tot);
+      if (run + tot > rcut) {
+        const uint32_t want = rcut - run;
+        if (ex <= want && want < ex + c) {
+          uint32_t mm = mask;
+          for (uint32_t i = 0; i < want - ex; ++i) mm &= mm - 1u;
+          sh.elem_index = (int32_t)(base + (__ffs(mm) - 1));
+        }
+        done = true;
+      }
+      run += tot;
+    };
+    segment((int64_t)tid, (has_h && member(hraw)) ? 1u : 0u);
+    if constexpr (NV > 0) {
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        if (done) break;
+        const int64_t v = tid + (int64_t)j * kHT;
+        if ((int64_t)j * kHT >= nvec) break;
+        uint32_t mask = 0;
+        if (v < nvec) {
+          const uint32_t w[4] = {q[j].x, q[j].y, q[j].z, q[j].w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            mask |= member(w[e] & 0xffffu) ? (1u << (2 * e)) : 0u;
+            mask |= member(w[e] >> 16) ? (2u << (2 * e)) : 0u;
+          }
+        }
+        segment(sp.head + v * 8, mask);
+      }
+    } else {
+      for (int64_t v0 = 0; v0 < nvec && !done; v0 += kHT) {
+        const int64_t v = v0 + tid;
+        uint32_t mask = 0;
+        if (v < nvec) {
+          const vu4 t = xv[v];
+          const uint32_t w[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            mask |= member(w[e] & 0xffffu) ? (1u << (2 * e)) : 0u;
+            mask |= member(w[e] >> 16) ? (2u << (2 * e)) : 0u;
+          }
+        }
+        segment(sp.head + v * 8, mask);
+      }
+    }
+    if (!done) segment(sp.tail0 + tid, (has_tl && member(traw)) ? 1u : 0u);
+    __syncthreads();
+    i_cut = sh.elem_index;
+  }
+
+  // ---- kept list for the backward -------------------------------------------
+  if (n_kept <= (uint32_t)kKeepCap) {
+    int32_t* ki = P.kept_idx + row * kKeepCap;
+    float* kp = P.kept_p + row * kKeepCap;
+    sweep([&](int64_t j, uint32_t rw) {
+      const uint32_t k = okey16(rw);
+      if (k > g_hi || (k >= g_lo && j >= (int64_t)i_cut)) {
+        const int s = atomicAdd(&sh.nk, 1);
+        if (s < kKeepCap) {
+          ki[s] = (int32_t)j;
+          kp[s] = expf((yk(k) - m) - logsum);
+        }
+      }
+    });
+  }
+
+  if (tid == 0) {
+    RowInfo ri;
+    ri.m = m;
+    ri.logsum = logsum;
+    ri.v_cut = v_cut;
+    ri.i_cut = i_cut;
+    ri.n_kept = (int32_t)n_kept;
+    ri.flags = 0;
+    P.info[row] = ri;
+    if (P.out != nullptr) {
+      const int64_t t = P.target[b * P.tsb + r * P.tsr];
+      float lp = -INFINITY;
+      if (t >= 0 && t < V) {
+        const float yt = scaled<E>(E::load(x + t), P);
+        if (kept_lex(yt, t, v_cut, i_cut)) lp = (yt - m) - logsum;
+      }
+      P.out[row] = lp;
+    }
+  }
+}
+
+template <class E>
+int launch_hist(const FilterParams& P, int64_t rows, int all_rows, hipStream_t st) {
+  // rows whose vectors fit kRegVec per lane stay in registers between sweeps
+  const int64_t nvec_max = (P.V + 7) / 8;
+  if (nvec_max <= (int64_t)kRegVec * kHT)
+    hipLaunchKernelGGL((filter_hist_kernel<E, kRegVec, false>), dim3((unsigned)rows), dim3(kHT), 0,
+                       st, P, all_rows);
+  else
+    hipLaunchKernelGGL((filter_hist_kernel<E, 0, false>), dim3((unsigned)rows), dim3(kHT), 0, st,
+                       P, all_rows);
+  if (int e = check_launch("filter_hist_kernel")) return e;
+  if (!P.dec16) return MIRL_OK;
+  // rows the rounding bound left undecided
+  hipLaunchKernelGGL((filter_hist_kernel<E, 0, true>), dim3((unsigned)rows), dim3(kHT), 0, st, P,
+                     0);
+  return check_launch("filter_hist_kernel(walk)");
+}
+
+}  // namespace
+
+int launch_hist_rows(const FilterParams& P, int dtype, int64_t rows, int all_rows,
+                     hipStream_t st) {
+  MIRL_REQUIRE(P.V <= kHistMaxV, "vocabulary %lld exceeds the histogram path's %lld",
+               (long long)P.V, (long long)kHistMaxV);
+  if (dtype == MIRL_DTYPE_BF16) return launch_hist<BF16>(P, rows, all_rows, st);
+  MIRL_REQUIRE(dtype == MIRL_DTYPE_F16, "histogram path: 16-bit logits only (dtype %d)", dtype);
+  return launch_hist<F16>(P, rows, all_rows, st);
+}
+
+}  // namespace mirl

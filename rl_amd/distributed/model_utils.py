@@ -393,11 +393,20 @@ def from_parallel_logits_to_logprobs(
     Drop-in for reference model_utils.py:967-1062 with TP = CP = 1.  Row s of
     the result is the logprob of ``target[:, s+1]`` under ``logits[:, s]``.
     Only the S-1 rows that survive the reference's final ``[:, :-1]`` slice
-    are computed; the backward writes zeros for the last row.
+    are computed; the backward writes zeros for the last row.  With
+    ``sampling_params`` the filter decides top-p in the logits' own dtype, as
+    the reference's DistributedLogprobWithSampling does on this tensor.
     """
+    return _next_token_logprobs(vocab_parallel_logits, target, vocab_start_index,
+                                vocab_end_index, tp_group, inference_only, cp_group, chunk_size,
+                                sampling_params, None)
+
+
+def _next_token_logprobs(logits, target, vocab_start_index, vocab_end_index, tp_group,
+                         inference_only, cp_group, chunk_size, sampling_params, decision_dtype):
     _require_single_rank(tp_group, cp_group)
     _check_chunk_size(chunk_size)
-    logits = _check_logits(vocab_parallel_logits)
+    logits = _check_logits(logits)
     if need_top_k_or_top_p_filtering(sampling_params):
         from rl_amd.distributed.sampling import filtered_next_token_logprobs
 
@@ -407,6 +416,7 @@ def from_parallel_logits_to_logprobs(
             sampling_params.top_k,  # type: ignore[union-attr]
             sampling_params.top_p,  # type: ignore[union-attr]
             inference_only=inference_only,
+            decision_dtype=decision_dtype,
         )
     tgt = _next_token_targets(target, logits.shape[1])
     return _row_logprobs(logits, tgt, vocab_start_index, vocab_end_index, inference_only, False)
@@ -435,8 +445,21 @@ def from_parallel_logits_to_logprobs_packed_sequences(
     over sequences (target roll, unpacking to ``[B, unpacked_seqlen - 1]``)
     become one gfx950 kernel each over the uploaded boundaries
     (``mirl_packed_roll_targets``, ``mirl_unpack_rows_fwd``); the unpacking's
-    backward is the inverse kernel (``mirl_unpack_rows_bwd``).
+    backward is the inverse kernel (``mirl_unpack_rows_bwd``).  With
+    ``sampling_params`` the filter decides top-p in the logits' own dtype, as
+    the reference's DistributedLogprobWithSampling does on this tensor.
     """
+    return _packed_sequence_logprobs(
+        vocab_parallel_logits, target, cu_seqlens_padded, unpacked_seqlen, vocab_start_index,
+        vocab_end_index, group, inference_only, cp_group, chunk_size, sampling_params,
+        target_is_pre_rolled, return_packed_layout, reuse_logits_storage, None,
+    )
+
+
+def _packed_sequence_logprobs(vocab_parallel_logits, target, cu_seqlens_padded, unpacked_seqlen,
+                              vocab_start_index, vocab_end_index, group, inference_only, cp_group,
+                              chunk_size, sampling_params, target_is_pre_rolled,
+                              return_packed_layout, reuse_logits_storage, decision_dtype):
     _require_single_rank(group, cp_group)
     _check_chunk_size(chunk_size)
     logits = _check_logits(vocab_parallel_logits)
@@ -461,7 +484,7 @@ def from_parallel_logits_to_logprobs_packed_sequences(
 
         probs = filtered_row_logprobs(
             logits, tgt, sampling_params.top_k, sampling_params.top_p,  # type: ignore[union-attr]
-            inference_only=inference_only,
+            inference_only=inference_only, decision_dtype=decision_dtype,
         )
     else:
         probs = _row_logprobs(
@@ -556,16 +579,11 @@ def get_next_token_logprobs_from_logits(
         and not need_top_k_or_top_p_filtering(sampling_params)
     )
     V = next_token_logits.shape[-1]
-    logprobs = from_parallel_logits_to_logprobs(
-        next_token_logits,
-        input_ids,
-        vocab_start_index=0,
-        vocab_end_index=V,
-        tp_group=None,
-        inference_only=False,
-        cp_group=None,
-        sampling_params=sampling_params,
-        chunk_size=chunk_size if use_chunking else None,
+    # the reference upcasts to fp32 here (model_utils.py:1660-1666), so the
+    # filter decides top-p in fp32; the kernels read the logits dtype directly
+    logprobs = _next_token_logprobs(
+        next_token_logits, input_ids, 0, V, None, False, None,
+        chunk_size if use_chunking else None, sampling_params, torch.float32,
     )
     if logprobs.shape[1] == input_ids.shape[1] - 1:
         return logprobs  # the slice below would be the whole tensor

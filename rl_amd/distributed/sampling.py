@@ -15,6 +15,14 @@ does ``top_p`` (1.0 disables it).  The temperature argument is an extension:
 the reference applies ``logits.div_(T)`` before calling these functions; passing
 ``temperature=T`` here instead computes the same values and gradients without
 the extra pass over the logits.
+
+Top-p is decided in the dtype the reference decides it in: a direct call on a
+bf16/fp16 tensor (``apply_top_k_top_p``, ``DistributedLogprobWithSampling``,
+``from_parallel_logits_to_logprobs``) forms the softmax and its cumulative sum
+in that dtype (reference logits_sampling_utils.py:189-191 on the un-upcast
+tensor, model_utils.py:409); ``get_next_token_logprobs_from_logits`` upcasts
+first (model_utils.py:1660-1666) and decides in fp32.  ``decision_dtype``
+selects between the two (None = the logits dtype).
 """
 
 from __future__ import annotations
@@ -50,10 +58,12 @@ class _FilteredRowLogprob(torch.autograd.Function):
         top_p: float,
         temperature: float,
         inference_only: bool,
+        decision_dtype: Optional[torch.dtype],
     ) -> torch.Tensor:
         B, R = target.shape
         out = torch.empty((B, R), dtype=torch.float32, device=logits.device)
-        info, kidx, kp = _C.filtered_fwd(logits, target, temperature, top_k, top_p, out)
+        info, kidx, kp = _C.filtered_fwd(logits, target, temperature, top_k, top_p, out,
+                                         decision_dtype)
         if not inference_only:
             ctx.save_for_backward(logits, target, info, kidx, kp)
             ctx.temperature = float(temperature)
@@ -67,7 +77,7 @@ class _FilteredRowLogprob(torch.autograd.Function):
             g = g.float()
         grad = torch.empty_like(logits)
         _C.filtered_bwd(logits, target, ctx.temperature, info, kidx, kp, g, grad)
-        return grad, None, None, None, None, None
+        return grad, None, None, None, None, None, None
 
 
 def _check_logits(logits: torch.Tensor) -> torch.Tensor:
@@ -83,10 +93,12 @@ def filtered_row_logprobs(
     top_p: Optional[float],
     inference_only: bool = False,
     temperature: float = 1.0,
+    decision_dtype: Optional[torch.dtype] = None,
 ) -> torch.Tensor:
     """[B, S, V] logits and [B, R <= S] targets -> [B, R] fp32 filtered logprobs of rows 0..R-1.
 
     With filtering disabled this is the plain (unfiltered) selected-token logprob.
+    ``decision_dtype``: None decides top-p in the logits dtype, torch.float32 in fp32.
     """
     logits = _check_logits(logits)
     if target.dtype != torch.int64:
@@ -98,7 +110,7 @@ def filtered_row_logprobs(
 
         return _row_logprobs(logits, target, 0, logits.shape[-1], inference_only, False)
     return _FilteredRowLogprob.apply(
-        logits, target, _k(top_k), _p(top_p), float(temperature), inference_only
+        logits, target, _k(top_k), _p(top_p), float(temperature), inference_only, decision_dtype
     )
 
 
@@ -109,6 +121,7 @@ def filtered_next_token_logprobs(
     top_p: Optional[float],
     inference_only: bool = False,
     temperature: float = 1.0,
+    decision_dtype: Optional[torch.dtype] = None,
 ) -> torch.Tensor:
     """Next-token filtered logprobs ``[B, S-1]``: row s against ``input_ids[:, s+1]``."""
     if input_ids.dim() != 2:
@@ -118,7 +131,8 @@ def filtered_next_token_logprobs(
             f"target length {input_ids.shape[1]} exceeds the {logits.shape[1]} logits rows"
         )
     ids = input_ids if input_ids.dtype == torch.int64 else input_ids.long()
-    return filtered_row_logprobs(logits, ids[:, 1:], top_k, top_p, inference_only, temperature)
+    return filtered_row_logprobs(logits, ids[:, 1:], top_k, top_p, inference_only, temperature,
+                                 decision_dtype)
 
 
 class _ApplyTopKTopP(torch.autograd.Function):
@@ -130,7 +144,7 @@ class _ApplyTopKTopP(torch.autograd.Function):
         x2d = logits.reshape(-1, shape[-1])
         if x2d.stride(-1) != 1:
             x2d = x2d.contiguous()
-        filt, keep = _C.top_k_top_p_mask(x2d, top_k, top_p)
+        filt, keep = _C.top_k_top_p_mask(x2d, top_k, top_p)  # decided in the logits dtype
         keep = keep.view(shape)
         ctx.save_for_backward(keep)
         ctx.mark_non_differentiable(keep)
@@ -213,6 +227,7 @@ def _run_filtered(ctx, logits, target, top_k, top_p, inference_only):
     ctx.filtered = _enabled(top_k, top_p)
     out = torch.empty((B, S), dtype=torch.float32, device=logits.device)
     if ctx.filtered:
+        # the reference filters these logits in their own dtype (model_utils.py:409)
         info, kidx, kp = _C.filtered_fwd(logits, target, 1.0, _k(top_k), _p(top_p), out)
         saved = (logits, target, info, kidx, kp)
     else:

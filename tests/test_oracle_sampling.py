@@ -5,11 +5,22 @@ candidate set on tiny vocabularies (the top-k set is the k largest with ties;
 the nucleus is the shortest descending-order prefix whose mass reaches top_p,
 resolved in stable order), plus the reference tests' invariants
 (tests/unit/distributed/test_model_utils.py:1402-1490).
+
+For 16-bit tensors the reference's own op sequence decides top-p in the
+tensor's dtype (logits_sampling_utils.py:189-191 on an un-upcast tensor): the
+softmax output is rounded to the dtype, torch's CPU cumsum accumulates it in
+fp32 and rounds every partial sum to the dtype, and the Python float 1 - top_p
+is compared in the dtype.  That rule is written out below with numpy scalars
+(fp32 exponentials and sums, explicit round-to-nearest-even to bf16/fp16) and
+checked against the oracle on tiny rows, where the CPU softmax sums its few
+terms one by one; two hand-derived rows pin the cases where the 16-bit rule and
+the fp32 rule keep different sets.
 """
 
 import itertools
 import math
 
+import numpy as np
 import pytest
 import torch
 
@@ -98,3 +109,73 @@ def test_temperature_chain_bf16():
     exp = (g32.to(torch.bfloat16).float() / 0.7).to(torch.bfloat16)
     torch.testing.assert_close(grad[:, :-1].float(), exp.float(), rtol=0, atol=0)
     assert grad[:, -1].abs().max() == 0
+
+
+def _round16(v: float, dtype) -> float:
+    """fp32 value rounded to bf16 / fp16 (nearest even), as a Python float."""
+    f = np.float32(v)
+    if dtype is torch.float16:
+        return float(np.float16(f))
+    u = int(np.array([f], dtype=np.float32).view(np.uint32)[0])
+    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    return float(np.array([u], dtype=np.uint32).view(np.float32)[0])
+
+
+def _definition_keep16(x: list[float], k, p, dtype) -> set[int]:
+    """16-bit keep set: exp and their sum in fp32 (one term at a time), probabilities
+    rounded to the dtype, cumulative sum in fp32 rounded to the dtype at every step,
+    compared with dtype(fp32(1 - top_p)); ties in stable ascending order."""
+    order = sorted(range(len(x)), key=lambda i: (x[i], i))
+    kept = list(order)
+    if k is not None and k > 0:
+        thr = sorted(x, reverse=True)[k - 1]
+        kept = [i for i in order if x[i] >= thr]
+    if p is None or p == 1.0:
+        return set(kept)
+    m = max(x[i] for i in kept)
+    e = [np.float32(math.exp(x[i] - m)) for i in kept]
+    z = np.float32(0.0)
+    for v in e:
+        z = np.float32(z + v)
+    probs = [_round16(float(np.float32(v / z)), dtype) for v in e]
+    thr16 = _round16(float(np.float32(1.0 - p)), dtype)
+    cum = np.float32(0.0)
+    for pos, i in enumerate(kept):
+        cum = np.float32(cum + np.float32(probs[pos]))
+        if _round16(float(cum), dtype) > thr16 or pos == len(kept) - 1:
+            return set(kept[pos:])
+    return set()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("k,p", [(2, 1.0), (3, 0.9), (None, 0.5), (None, 0.95), (4, 0.3), (5, 0.999)])
+def test_16bit_rule_matches_definition_on_tiny_rows(k, p, dtype):
+    g = torch.Generator().manual_seed(3)
+    for trial in range(200):
+        V = 6
+        x = (torch.randint(-3, 4, (V,), generator=g).float() * 0.5).to(dtype)
+        _, keep = top_k_top_p(x.unsqueeze(0), k, p)
+        got = set(torch.nonzero(keep[0]).flatten().tolist())
+        assert got == _definition_keep16(x.float().tolist(), k, p, dtype), (x.tolist(), k, p)
+
+
+@pytest.mark.parametrize(
+    "dtype,row",
+    [
+        # bf16: p0 = p1 = 0.050107 (fp32) round to 0.050048828125; their bf16 cumsum
+        # is 0.10009765625 = bf16(1 - 0.9), not above it, while the fp32 cumsum
+        # 0.100214 exceeds fp32(1 - 0.9) = 0.099999994
+        (torch.bfloat16, [-0.013, -0.013, 2.875]),
+        # fp16: p0 = p1 = 0.0500014 round to 0.04998779296875; the fp16 cumsum is
+        # 0.0999755859375 = fp16(1 - 0.9), not above it; the fp32 cumsum 0.1000029 is
+        (torch.float16, [0.000285, 0.000285, 2.890625]),
+    ],
+)
+def test_16bit_rule_known_answers(dtype, row):
+    x = torch.tensor([row], dtype=dtype)
+    _, keep16 = top_k_top_p(x, None, 0.9)
+    _, keep32 = top_k_top_p(x.float(), None, 0.9)
+    assert keep16.tolist() == [[False, False, True]]
+    assert keep32.tolist() == [[False, True, True]]
+    assert _definition_keep16(x.float()[0].tolist(), None, 0.9, dtype) == {2}
+    assert _definition_keep(x.float()[0].tolist(), None, 0.9) == {1, 2}
