@@ -312,7 +312,10 @@ int mirl_filtered_logprob_fwd(const void* logits, int dtype, int64_t B, int64_t 
 /*
  * Gradient of the filtered logprobs with respect to the raw logits:
  *   g32 = (onehot(t) - p) * g on the kept set, 0 elsewhere,
- *   grad = dtype(dtype(g32) / temperature)   (dtype(g32) when temperature == 1).
+ *   grad = dtype(dtype(g32) / temperature)   (dtype(g32) when temperature == 1),
+ *   then, when grad_temperature != 1, grad = dtype(grad / grad_temperature): the
+ *   backward of an in-place division of the logits by grad_temperature made
+ *   before the forward (mirl_temperature_scale), folded into this write.
  * Rows r >= R (up to R_total) and rows with g == 0 are written as zeros.
  * Rows whose kept list was saved are written without reading the logits.
  *
@@ -325,11 +328,11 @@ int mirl_filtered_logprob_bwd(const void* logits, int dtype, int64_t B, int64_t 
                               int64_t R_total, int64_t V, int64_t stride_b,
                               int64_t stride_r, const int64_t* target,
                               int64_t t_stride_b, int64_t t_stride_r,
-                              double temperature, const void* row_info,
-                              const int32_t* kept_idx, const float* kept_p,
-                              const float* grad_out, int64_t g_stride_b,
-                              int64_t g_stride_r, void* grad_in, int64_t gi_stride_b,
-                              int64_t gi_stride_r, void* stream);
+                              double temperature, double grad_temperature,
+                              const void* row_info, const int32_t* kept_idx,
+                              const float* kept_p, const float* grad_out,
+                              int64_t g_stride_b, int64_t g_stride_r, void* grad_in,
+                              int64_t gi_stride_b, int64_t gi_stride_r, void* stream);
 
 /*
  * apply_top_k_top_p on N rows of V logits: filtered[i, j] = x[i, j] where kept,
@@ -344,6 +347,33 @@ int mirl_top_k_top_p_mask(const void* logits, int dtype, int64_t N, int64_t V,
                           void* row_info, int32_t* kept_idx, float* kept_p,
                           void* filtered, int64_t filtered_row_stride,
                           uint8_t* keep_mask, int64_t keep_row_stride, void* stream);
+
+/*
+ * In-place temperature scaling of [B, R, V] logits (unit stride on V):
+ *   x = dtype(float(x) / float(temperature)), rounded to nearest even.
+ *
+ * Replaces: apply_temperature_scaling's logits.div_(temperature)
+ * (nemo_rl/models/automodel/train.py:248-262,
+ * nemo_rl/models/megatron/train.py:280-294).
+ */
+int mirl_temperature_scale(void* logits, int dtype, int64_t B, int64_t R, int64_t V,
+                           int64_t stride_b, int64_t stride_r, double temperature,
+                           void* stream);
+
+/*
+ * Backward of mirl_temperature_scale: out = dtype(float(g) / float(T)); with
+ * `grad2` non-NULL, out = dtype(float(dtype(float(g) + float(grad2))) / float(T))
+ * (two consumers' gradients accumulated in the dtype first).  All three are
+ * [B, R, V] views with unit stride on V; `out` may alias `grad`.
+ *
+ * Replaces: the autograd backward of logits.div_(temperature) (DivBackward)
+ * and the accumulation of two gradients into it.
+ */
+int mirl_temperature_scale_grad(const void* grad, int dtype, int64_t B, int64_t R,
+                                int64_t V, int64_t g_stride_b, int64_t g_stride_r,
+                                const void* grad2, int64_t g2_stride_b,
+                                int64_t g2_stride_r, double temperature, void* out,
+                                int64_t o_stride_b, int64_t o_stride_r, void* stream);
 
 /* ---------------------------------------------------------------------- */
 /* logprobs from hidden states (LM-head GEMM fused with the log-sum-exp)     */

@@ -199,8 +199,14 @@ SIGNATURES = {
     ),
     "mirl_filtered_logprob_bwd": (
         _I,
-        [_P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I64, _I64, ctypes.c_double, _P, _P,
-         _P, _P, _I64, _I64, _P, _I64, _I64, _P],
+        [_P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I64, _I64, ctypes.c_double,
+         ctypes.c_double, _P, _P, _P, _P, _I64, _I64, _P, _I64, _I64, _P],
+    ),
+    "mirl_temperature_scale": (_I, [_P, _I, _I64, _I64, _I64, _I64, _I64, ctypes.c_double, _P]),
+    "mirl_temperature_scale_grad": (
+        _I,
+        [_P, _I, _I64, _I64, _I64, _I64, _I64, _P, _I64, _I64, ctypes.c_double, _P, _I64, _I64,
+         _P],
     ),
     "mirl_linear_ce_workspace_elems": (_I64, [_I64, _I64]),
     "mirl_linear_ce_fwd": (
@@ -562,17 +568,17 @@ def clipped_pg(
     [B, L, K] buffer of the loss dtype) the correction is added to the loss and
     dloss/dplog is written into that buffer.
     """
-    dev = _require_gpu(curr, token_mask, advantages, generation, sample_mask)
     B, L = curr.shape
     dtype = curr.dtype
     if loss_out is not None and (
         loss_out.numel() != 1 or loss_out.dtype != dtype or not loss_out.is_contiguous()
-        or loss_out.device != dev
+        or loss_out.device != curr.device
     ):
         raise MirlError(
-            f"loss_out must be one contiguous {dtype} element on {dev}; got "
+            f"loss_out must be one contiguous {dtype} element on {curr.device}; got "
             f"{tuple(loss_out.shape)} {loss_out.dtype} on {loss_out.device}"
         )
+    dev = _require_gpu(curr, token_mask, advantages, generation, sample_mask)
     metrics = torch.empty(PG_NUM_METRICS, dtype=dtype, device=dev)
     grad_curr = torch.empty((B, L), dtype=dtype, device=dev)
     grad_unf = torch.empty((B, L), dtype=dtype, device=dev) if unfiltered is not None else None
@@ -968,7 +974,11 @@ def filtered_bwd(
     kp: torch.Tensor,
     grad_out: torch.Tensor,
     grad_in: torch.Tensor,
+    grad_temperature: float = 1.0,
 ) -> None:
+    """``grad_temperature`` != 1 divides the written gradient by it last (in the
+    dtype): the backward of an in-place division of the logits made before the
+    forward, folded into this write."""
     dev = _require_gpu(logits, target, grad_out, grad_in)
     B, R = target.shape
     Rt = grad_in.shape[1]
@@ -978,11 +988,66 @@ def filtered_bwd(
         "mirl_filtered_logprob_bwd", dev,
         logits.data_ptr(), _dtype_code(logits), B, R, Rt, V, logits.stride(0),
         logits.stride(1), target.data_ptr(), target.stride(0), target.stride(1),
-        float(temperature), info.data_ptr(), kidx.data_ptr(), kp.data_ptr(),
+        float(temperature), float(grad_temperature), info.data_ptr(), kidx.data_ptr(), kp.data_ptr(),
         grad_out.data_ptr(), grad_out.stride(0), grad_out.stride(1), grad_in.data_ptr(),
         grad_in.stride(0), grad_in.stride(1), _stream(dev),
     )
     _check(st, "mirl_filtered_logprob_bwd")
+
+
+def _rows3(t: torch.Tensor):
+    """(B, R, V, stride_b, stride_r) of a tensor viewed as [B, R, V] rows of its last dim."""
+    _require(t.dim() >= 1 and (t.dim() == 1 or t.stride(-1) == 1 or t.shape[-1] == 1),
+             "the last dimension must have unit stride")
+    if t.dim() == 1:
+        return 1, 1, t.shape[0], t.shape[0], t.shape[0]
+    if t.dim() == 2:
+        return 1, t.shape[0], t.shape[1], t.shape[0] * t.stride(0), t.stride(0)
+    lead = t.shape[:-2]
+    B = 1
+    for d in lead:
+        B *= d
+    # leading dims must collapse to one stride
+    sb = t.stride(-3) if t.dim() >= 3 else t.shape[-2] * t.stride(-2)
+    expect = sb
+    for i in range(t.dim() - 3, -1, -1):
+        _require(t.shape[i] == 1 or t.stride(i) == expect, "leading dimensions do not collapse")
+        expect *= t.shape[i]
+    return B, t.shape[-2], t.shape[-1], sb, t.stride(-2)
+
+
+def temperature_scale_(logits: torch.Tensor, temperature: float) -> torch.Tensor:
+    """In place: logits = dtype(float(logits) / T) (mirl_temperature_scale)."""
+    dev = _require_gpu(logits)
+    B, R, V, sb, sr = _rows3(logits)
+    st = _launch("mirl_temperature_scale", dev, logits.data_ptr(), _dtype_code(logits), B, R, V,
+                 sb, sr, float(temperature), _stream(dev))
+    _check(st, "mirl_temperature_scale")
+    return logits
+
+
+def temperature_scale_grad(grad: torch.Tensor, grad2: Optional[torch.Tensor],
+                           temperature: float) -> torch.Tensor:
+    """dtype(float(grad [+ grad2, accumulated in the dtype]) / T) as a new tensor."""
+    dev = _require_gpu(grad, grad2)
+    if grad2 is not None:
+        _require(grad2.shape == grad.shape and grad2.dtype == grad.dtype, "grad2 matches grad")
+    out = torch.empty(grad.shape, dtype=grad.dtype, device=dev)
+    if grad.stride(-1) != 1:
+        grad = grad.contiguous()
+    if grad2 is not None and grad2.stride(-1) != 1:
+        grad2 = grad2.contiguous()
+    B, R, V, sb, sr = _rows3(grad)
+    if grad2 is not None:
+        _, _, _, sb2, sr2 = _rows3(grad2)
+    else:
+        sb2 = sr2 = 0
+    _, _, _, osb, osr = _rows3(out)
+    st = _launch("mirl_temperature_scale_grad", dev, grad.data_ptr(), _dtype_code(grad), B, R, V,
+                 sb, sr, _ptr(grad2), sb2, sr2, float(temperature), out.data_ptr(), osb, osr,
+                 _stream(dev))
+    _check(st, "mirl_temperature_scale_grad")
+    return out
 
 
 def top_k_top_p_mask(x2d: torch.Tensor, top_k: int, top_p: float,

@@ -23,7 +23,7 @@ class TrainingSamplingParams:
     """Sampling parameters mirrored from generation (reference :29-44).
 
     top_k: None or <= 0 disables top-k; top_p: 1.0 disables top-p;
-    temperature is applied by the caller (see ``apply_temperature_scaling``).
+    temperature is applied by the caller (``apply_temperature_scaling``).
     """
 
     top_k: int | None = None
@@ -75,13 +75,29 @@ def apply_top_k_top_p(
     return apply_top_k_top_p_kernel(logits, top_k, top_p)
 
 
-def apply_temperature_scaling(logits: torch.Tensor, temperature: float) -> torch.Tensor:
-    """In-place ``logits.div_(temperature)`` in the logits dtype (reference automodel/train.py:248-262).
+def need_temperature_scaling(sampling_params: Optional[TrainingSamplingParams]) -> bool:
+    """Whether apply_temperature_scaling will mutate the logits in place
+    (reference nemo_rl/models/automodel/train.py:241-245)."""
+    return sampling_params is not None and sampling_params.temperature != 1.0
 
-    Kept as the reference's plain tensor op: a single elementwise pass whose
-    rounding (fp32 quotient rounded to the logits dtype) the filtered kernels
-    reproduce when they fuse the temperature instead.
+
+def apply_temperature_scaling(
+    logits: torch.Tensor, sampling_params: Optional[TrainingSamplingParams]
+) -> torch.Tensor:
+    """``logits.div_(sampling_params.temperature)`` in place, in the logits dtype
+    (reference nemo_rl/models/automodel/train.py:248-262,
+    nemo_rl/models/megatron/train.py:280-294); a no-op for None or T == 1.
+
+    The division runs on the gfx950 temperature kernel (fp32 quotient rounded
+    to the logits dtype, as ``div_`` rounds it) and is recorded for autograd;
+    its backward is the same division of the gradient.  When the filtered
+    logprobs of this package are the only consumer of the scaled logits, that
+    division is folded into their backward's write.  A gradient requested for
+    the scaled tensor itself (``autograd.grad`` with it as an input, or
+    ``retain_grad``) then sees no contribution from those logprobs.
     """
-    if temperature != 1.0:
-        logits.div_(temperature)
+    if need_temperature_scaling(sampling_params):
+        from rl_amd.distributed.sampling import temperature_scale_
+
+        return temperature_scale_(logits, sampling_params.temperature)  # type: ignore[union-attr]
     return logits

@@ -29,6 +29,7 @@ SOURCES = [
     "linear_ce.hip",
     "divergence.hip",
     "packing.hip",
+    "temperature.hip",
 ]
 
 ARCH = "gfx950"

@@ -1,0 +1,198 @@
+// In-place temperature scaling of logits and its backward.
+//
+// Semantics (reference nemo_rl/models/automodel/train.py:248-262 and
+// nemo_rl/models/megatron/train.py:280-294): logits.div_(T) in the logits
+// dtype, i.e. y = dtype(float(x) / float(T)) rounded to nearest even, and the
+// autograd backward of that division, grad_x = dtype(float(g) / float(T)).
+// When a second gradient is given, the two are first added in the dtype (the
+// autograd engine's accumulation of two consumers' gradients):
+// grad_x = dtype(float(dtype(float(g) + float(g2))) / float(T)).
+//
+// Contiguous tensors are walked as one flat array of 16-byte vectors (a scalar
+// head up to the first 16-byte boundary and a scalar tail), with nontemporal
+// loads and stores; other layouts element by element over [B, R, V].
+
+#include "common.h"
+
+namespace mirl {
+namespace {
+
+// x[i] <- dtype(float(x[i]) / T) over n contiguous elements.
+template <class E>
+__global__ __launch_bounds__(256) void scale_flat_kernel(void* x, int64_t n, float T) {
+  using raw = typename E::raw;
+  raw* p = static_cast<raw*>(x);
+  const RowSpan<E> sp(p, n);
+  vu4* pv = reinterpret_cast<vu4*>(p + sp.head);
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < sp.nvec; i += stride) {
+    const vu4 q = __builtin_nontemporal_load(pv + i);
+    float w[E::kVec];
+    E::unpack(q, w);
+#pragma unroll
+    for (int k = 0; k < E::kVec; ++k) w[k] = __fdiv_rn(w[k], T);
+    __builtin_nontemporal_store(E::pack(w), pv + i);
+  }
+  if (blockIdx.x == 0) {
+    if (threadIdx.x < sp.head) p[threadIdx.x] = E::from_float(__fdiv_rn(E::load(p + threadIdx.x), T));
+    if (sp.tail0 + threadIdx.x < n)
+      p[sp.tail0 + threadIdx.x] = E::from_float(__fdiv_rn(E::load(p + sp.tail0 + threadIdx.x), T));
+  }
+}
+
+// out[i] = dtype(float(dtype(float(g[i]) (+ float(g2[i])))) / T) over n
+// contiguous elements; g, g2 and out share their offset from a 16-byte boundary.
+template <class E>
+__global__ __launch_bounds__(256) void scale_grad_flat_kernel(const void* g, const void* g2,
+                                                              void* out, int64_t n, float T) {
+  using raw = typename E::raw;
+  const raw* a = static_cast<const raw*>(g);
+  const raw* b = static_cast<const raw*>(g2);
+  raw* o = static_cast<raw*>(out);
+  const RowSpan<E> sp(a, n);
+  const vu4* av = reinterpret_cast<const vu4*>(a + sp.head);
+  const vu4* bv = reinterpret_cast<const vu4*>(b + sp.head);
+  vu4* ov = reinterpret_cast<vu4*>(o + sp.head);
+  auto one = [&](float x, float y, bool two) {
+    const float s = two ? round_trip<E>(x + y) : x;
+    return __fdiv_rn(s, T);
+  };
+  const bool two = b != nullptr;
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < sp.nvec; i += stride) {
+    float w[E::kVec], w2[E::kVec];
+    E::unpack(__builtin_nontemporal_load(av + i), w);
+    if (two) E::unpack(__builtin_nontemporal_load(bv + i), w2);
+#pragma unroll
+    for (int k = 0; k < E::kVec; ++k) w[k] = one(w[k], two ? w2[k] : 0.f, two);
+    __builtin_nontemporal_store(E::pack(w), ov + i);
+  }
+  if (blockIdx.x == 0) {
+    auto at = [&](int64_t j) {
+      o[j] = E::from_float(one(E::load(a + j), two ? E::load(b + j) : 0.f, two));
+    };
+    if (threadIdx.x < sp.head) at(threadIdx.x);
+    if (sp.tail0 + threadIdx.x < n) at(sp.tail0 + threadIdx.x);
+  }
+}
+
+struct Strided3 {
+  void* p;
+  int64_t sb, sr;
+};
+
+// Element-wise over [B, R, V] with row strides (unit stride on V).
+template <class E>
+__global__ __launch_bounds__(256) void scale_rows_kernel(Strided3 x, const void* g2, int64_t g2_sb,
+                                                         int64_t g2_sr, Strided3 out, int64_t R,
+                                                         int64_t V, int64_t total, float T,
+                                                         int grad) {
+  using raw = typename E::raw;
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += stride) {
+    const int64_t row = i / V, v = i - row * V;
+    const int64_t b = row / R, r = row - b * R;
+    const raw* src = static_cast<const raw*>(x.p) + b * x.sb + r * x.sr + v;
+    float s = E::load(src);
+    if (grad && g2 != nullptr)
+      s = round_trip<E>(s + E::load(static_cast<const raw*>(g2) + b * g2_sb + r * g2_sr + v));
+    static_cast<raw*>(out.p)[b * out.sb + r * out.sr + v] = E::from_float(__fdiv_rn(s, T));
+  }
+}
+
+int grid_for(int64_t work) {
+  const int64_t blocks = (work + 255) / 256;
+  return (int)(blocks < 8192 ? (blocks > 0 ? blocks : 1) : 8192);
+}
+
+bool contiguous(int64_t B, int64_t R, int64_t V, int64_t sb, int64_t sr) {
+  return sr == V && (B == 1 || sb == R * V);
+}
+
+template <class E>
+int run_scale(void* x, int64_t B, int64_t R, int64_t V, int64_t sb, int64_t sr, float T,
+              hipStream_t st) {
+  const int64_t n = B * R * V;
+  if (contiguous(B, R, V, sb, sr)) {
+    hipLaunchKernelGGL((scale_flat_kernel<E>), dim3(grid_for(n / E::kVec)), dim3(256), 0, st, x, n,
+                       T);
+  } else {
+    const Strided3 s{x, sb, sr};
+    hipLaunchKernelGGL((scale_rows_kernel<E>), dim3(grid_for(n)), dim3(256), 0, st, s, nullptr,
+                       int64_t(0), int64_t(0), s, R, V, n, T, 0);
+  }
+  return check_launch("mirl_temperature_scale");
+}
+
+template <class E>
+int run_grad(const void* g, int64_t g_sb, int64_t g_sr, const void* g2, int64_t g2_sb,
+             int64_t g2_sr, void* out, int64_t o_sb, int64_t o_sr, int64_t B, int64_t R, int64_t V,
+             float T, hipStream_t st) {
+  const int64_t n = B * R * V;
+  const uintptr_t mis = (reinterpret_cast<uintptr_t>(g) & 15u);
+  const bool flat = contiguous(B, R, V, g_sb, g_sr) && contiguous(B, R, V, o_sb, o_sr) &&
+                    (reinterpret_cast<uintptr_t>(out) & 15u) == mis &&
+                    (g2 == nullptr ||
+                     (contiguous(B, R, V, g2_sb, g2_sr) && (reinterpret_cast<uintptr_t>(g2) & 15u) == mis));
+  if (flat) {
+    hipLaunchKernelGGL((scale_grad_flat_kernel<E>), dim3(grid_for(n / E::kVec)), dim3(256), 0, st, g,
+                       g2, out, n, T);
+  } else {
+    const Strided3 a{const_cast<void*>(g), g_sb, g_sr};
+    const Strided3 o{out, o_sb, o_sr};
+    hipLaunchKernelGGL((scale_rows_kernel<E>), dim3(grid_for(n)), dim3(256), 0, st, a, g2, g2_sb,
+                       g2_sr, o, R, V, n, T, 1);
+  }
+  return check_launch("mirl_temperature_scale_grad");
+}
+
+int check_args(int dtype, int64_t B, int64_t R, int64_t V, double temperature) {
+  if (dtype != MIRL_DTYPE_F32 && dtype != MIRL_DTYPE_BF16 && dtype != MIRL_DTYPE_F16) {
+    set_error("unsupported logits dtype code %d", dtype);
+    return MIRL_ERR_UNSUPPORTED;
+  }
+  MIRL_REQUIRE(B >= 0 && R >= 0 && V >= 0, "invalid shape B=%lld R=%lld V=%lld", (long long)B,
+               (long long)R, (long long)V);
+  MIRL_REQUIRE(temperature > 0.0, "temperature must be positive, got %g", temperature);
+  return MIRL_OK;
+}
+
+}  // namespace
+}  // namespace mirl
+
+using namespace mirl;
+
+extern "C" int mirl_temperature_scale(void* logits, int dtype, int64_t B, int64_t R, int64_t V,
+                                      int64_t stride_b, int64_t stride_r, double temperature,
+                                      void* stream) {
+  clear_error();
+  if (int e = check_args(dtype, B, R, V, temperature)) return e;
+  if (B * R * V == 0) return MIRL_OK;
+  MIRL_REQUIRE(logits != nullptr, "null pointer argument");
+  const float T = (float)temperature;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == MIRL_DTYPE_F32) return run_scale<F32>(logits, B, R, V, stride_b, stride_r, T, st);
+  if (dtype == MIRL_DTYPE_BF16) return run_scale<BF16>(logits, B, R, V, stride_b, stride_r, T, st);
+  return run_scale<F16>(logits, B, R, V, stride_b, stride_r, T, st);
+}
+
+extern "C" int mirl_temperature_scale_grad(const void* grad, int dtype, int64_t B, int64_t R,
+                                           int64_t V, int64_t g_stride_b, int64_t g_stride_r,
+                                           const void* grad2, int64_t g2_stride_b,
+                                           int64_t g2_stride_r, double temperature, void* out,
+                                           int64_t o_stride_b, int64_t o_stride_r, void* stream) {
+  clear_error();
+  if (int e = check_args(dtype, B, R, V, temperature)) return e;
+  if (B * R * V == 0) return MIRL_OK;
+  MIRL_REQUIRE(grad != nullptr && out != nullptr, "null pointer argument");
+  const float T = (float)temperature;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == MIRL_DTYPE_F32)
+    return run_grad<F32>(grad, g_stride_b, g_stride_r, grad2, g2_stride_b, g2_stride_r, out,
+                         o_stride_b, o_stride_r, B, R, V, T, st);
+  if (dtype == MIRL_DTYPE_BF16)
+    return run_grad<BF16>(grad, g_stride_b, g_stride_r, grad2, g2_stride_b, g2_stride_r, out,
+                          o_stride_b, o_stride_r, B, R, V, T, st);
+  return run_grad<F16>(grad, g_stride_b, g_stride_r, grad2, g2_stride_b, g2_stride_r, out,
+                       o_stride_b, o_stride_r, B, R, V, T, st);
+}

@@ -730,6 +730,8 @@ struct FilterBwdParams {
   int64_t tsb, tsr;
   float T;
   int has_t;
+  float GT;   // the gradient is divided by GT in the dtype last (an earlier in-place division)
+  int has_gt;
   const RowInfo* info;
   const int32_t* kept_idx;
   const float* kept_p;
@@ -741,9 +743,14 @@ struct FilterBwdParams {
 
 template <class E>
 __device__ __forceinline__ typename E::raw grad_to_dtype(float g32, const FilterBwdParams& P) {
-  if (!P.has_t) return E::from_float(g32);
-  // dtype(g) then / T in the dtype: round, divide in fp32, round again
-  return E::from_float(__fdiv_rn(round_trip<E>(g32), P.T));
+  if (!P.has_t && !P.has_gt) return E::from_float(g32);
+  // dtype(g) then / T in the dtype (round, divide in fp32, round again), then
+  // / GT in the dtype: the backward of the fused temperature and of an
+  // in-place division applied to the logits before this call
+  float r = round_trip<E>(g32);
+  if (P.has_t) r = round_trip<E>(__fdiv_rn(r, P.T));
+  if (P.has_gt) r = round_trip<E>(__fdiv_rn(r, P.GT));
+  return E::from_float(r);
 }
 
 // Phase 1 over a contiguous gradient: zeros over the whole [rows, V] block,
@@ -1056,18 +1063,18 @@ extern "C" int mirl_filtered_logprob_bwd(const void* logits, int dtype, int64_t 
                                          int64_t R_total, int64_t V, int64_t stride_b,
                                          int64_t stride_r, const int64_t* target,
                                          int64_t t_stride_b, int64_t t_stride_r,
-                                         double temperature, const void* row_info,
-                                         const int32_t* kept_idx, const float* kept_p,
-                                         const float* grad_out, int64_t g_stride_b,
-                                         int64_t g_stride_r, void* grad_in, int64_t gi_stride_b,
-                                         int64_t gi_stride_r, void* stream) {
+                                         double temperature, double grad_temperature,
+                                         const void* row_info, const int32_t* kept_idx,
+                                         const float* kept_p, const float* grad_out,
+                                         int64_t g_stride_b, int64_t g_stride_r, void* grad_in,
+                                         int64_t gi_stride_b, int64_t gi_stride_r, void* stream) {
   clear_error();
   if (dtype != MIRL_DTYPE_F32 && dtype != MIRL_DTYPE_BF16 && dtype != MIRL_DTYPE_F16) {
     set_error("unsupported logits dtype code %d", dtype);
     return MIRL_ERR_UNSUPPORTED;
   }
   MIRL_REQUIRE(B >= 0 && R >= 0 && R_total >= R && V > 0, "invalid shape");
-  MIRL_REQUIRE(temperature > 0.0, "temperature must be positive");
+  MIRL_REQUIRE(temperature > 0.0 && grad_temperature > 0.0, "temperature must be positive");
   const int64_t rows = B * R_total;
   if (rows == 0) return MIRL_OK;
   MIRL_REQUIRE(rows < (int64_t(1) << 31), "too many rows (%lld)", (long long)rows);
@@ -1086,6 +1093,8 @@ extern "C" int mirl_filtered_logprob_bwd(const void* logits, int dtype, int64_t 
   P.tsr = t_stride_r;
   P.T = (float)temperature;
   P.has_t = temperature != 1.0;
+  P.GT = (float)grad_temperature;
+  P.has_gt = grad_temperature != 1.0;
   P.info = static_cast<const RowInfo*>(row_info);
   P.kept_idx = kept_idx;
   P.kept_p = kept_p;

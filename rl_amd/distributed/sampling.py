@@ -34,6 +34,75 @@ import torch
 from rl_amd import _C
 
 
+class _TemperatureScale(torch.autograd.Function):
+    """``logits.div_(T)`` in place on the temperature kernel; backward ``dtype(g / T)``.
+
+    A filtered-logprob op that reads these logits folds the division into its
+    own backward (the write of the raw-logits gradient) and hands that gradient
+    over through ``prediv`` instead of returning it; with no other consumer this
+    node returns it unchanged.  If other consumers contributed a gradient as
+    well, the filtered gradient is recomputed undivided and accumulated with
+    theirs in the dtype before the division, as autograd accumulates two
+    consumers' gradients into the reference's division backward.
+    """
+
+    @staticmethod
+    def forward(ctx: Any, logits: torch.Tensor, temperature: float) -> torch.Tensor:  # type: ignore[override]
+        _C.temperature_scale_(logits, temperature)
+        ctx.mark_dirty(logits)
+        ctx.temperature = float(temperature)
+        ctx.prediv = None  # (raw-logits gradient, recompute of the undivided one)
+        ctx.set_materialize_grads(False)
+        return logits
+
+    @staticmethod
+    def backward(ctx: Any, grad: Optional[torch.Tensor]):  # type: ignore[override]
+        pre, ctx.prediv = ctx.prediv, None
+        if pre is None:
+            return (None if grad is None else _C.temperature_scale_grad(grad, None, ctx.temperature)), None
+        prediv, undivided = pre
+        if grad is None:
+            return prediv, None
+        return _C.temperature_scale_grad(grad, undivided(), ctx.temperature), None
+
+
+def temperature_scale_(logits: torch.Tensor, temperature: float) -> torch.Tensor:
+    """In-place ``dtype(float(logits) / T)``, recorded for autograd when the logits need it."""
+    if torch.is_grad_enabled() and logits.requires_grad:
+        return _TemperatureScale.apply(logits, temperature)
+    return _C.temperature_scale_(logits, temperature)
+
+
+def _temperature_node(logits: torch.Tensor):
+    """The _TemperatureScale node that produced ``logits``, if that is its history."""
+    fn = logits.grad_fn
+    if fn is not None and type(fn).__name__ == "_TemperatureScaleBackward":
+        return fn
+    return None
+
+
+def _filtered_grad(ctx: Any, logits, target, temperature, info, kidx, kp, g):
+    """The logits gradient of a filtered op: folded into the in-place temperature
+    node ahead of it when that node has no gradient from another filtered op yet
+    (then None is returned for autograd), else returned as usual."""
+    node = getattr(ctx, "temperature_node", None)
+    if node is not None and node.prediv is None:
+        grad = torch.empty_like(logits)
+        _C.filtered_bwd(logits, target, temperature, info, kidx, kp, g, grad,
+                        grad_temperature=node.temperature)
+
+        def undivided() -> torch.Tensor:
+            raw = torch.empty_like(logits)
+            _C.filtered_bwd(logits, target, temperature, info, kidx, kp, g, raw)
+            return raw
+
+        node.prediv = (grad, undivided)
+        return None
+    grad = torch.empty_like(logits)
+    _C.filtered_bwd(logits, target, temperature, info, kidx, kp, g, grad)
+    return grad
+
+
 def _k(top_k: Optional[int]) -> int:
     return int(top_k) if top_k is not None and top_k > 0 else 0
 
@@ -67,6 +136,7 @@ class _FilteredRowLogprob(torch.autograd.Function):
         if not inference_only:
             ctx.save_for_backward(logits, target, info, kidx, kp)
             ctx.temperature = float(temperature)
+            ctx.temperature_node = _temperature_node(logits)
         return out
 
     @staticmethod
@@ -75,8 +145,7 @@ class _FilteredRowLogprob(torch.autograd.Function):
         logits, target, info, kidx, kp = ctx.saved_tensors
         if g.dtype != torch.float32:
             g = g.float()
-        grad = torch.empty_like(logits)
-        _C.filtered_bwd(logits, target, ctx.temperature, info, kidx, kp, g, grad)
+        grad = _filtered_grad(ctx, logits, target, ctx.temperature, info, kidx, kp, g)
         return grad, None, None, None, None, None, None
 
 
@@ -230,6 +299,7 @@ def _run_filtered(ctx, logits, target, top_k, top_p, inference_only):
         # the reference filters these logits in their own dtype (model_utils.py:409)
         info, kidx, kp = _C.filtered_fwd(logits, target, 1.0, _k(top_k), _p(top_p), out)
         saved = (logits, target, info, kidx, kp)
+        ctx.temperature_node = _temperature_node(logits) if not inference_only else None
     else:
         stats = torch.empty((B, S, 2), dtype=torch.float32, device=logits.device)
         _C.logprob_fwd(logits, target, 0, logits.shape[-1], out, stats)
@@ -244,9 +314,8 @@ def _backward_filtered(ctx, g):
         g = g.float()
     saved = ctx.saved_tensors
     logits, target = saved[0], saved[1]
-    grad = torch.empty_like(logits)
     if ctx.filtered:
-        _C.filtered_bwd(logits, target, 1.0, saved[2], saved[3], saved[4], g, grad)
-    else:
-        _C.logprob_bwd(logits, target, 0, logits.shape[-1], saved[2], g, grad)
+        return _filtered_grad(ctx, logits, target, 1.0, saved[2], saved[3], saved[4], g)
+    grad = torch.empty_like(logits)
+    _C.logprob_bwd(logits, target, 0, logits.shape[-1], saved[2], g, grad)
     return grad

@@ -130,3 +130,42 @@ def test_student_teacher_shapes_are_validated_first(student_shape, teacher_shape
     with pytest.raises(ValueError, match=match):
         ChunkedDistributedReverseKLToFixedLogits.apply(
             torch.randn(*student_shape), torch.randn(*teacher_shape), 2, None, True)
+
+
+def test_temperature_scaling_signatures_and_no_ops():
+    """apply_temperature_scaling / need_temperature_scaling keep the reference's signatures
+    (nemo_rl/models/automodel/train.py:241-262): (logits, sampling_params) and (sampling_params);
+    None or T == 1 leave the logits untouched; any other T mutates in place on the GPU kernel,
+    so a CPU tensor is refused rather than divided by a CPU fallback."""
+    import inspect
+
+    from rl_amd.algorithms.logits_sampling_utils import (
+        apply_temperature_scaling,
+        need_temperature_scaling,
+    )
+
+    assert list(inspect.signature(apply_temperature_scaling).parameters) == ["logits", "sampling_params"]
+    assert list(inspect.signature(need_temperature_scaling).parameters) == ["sampling_params"]
+    assert not need_temperature_scaling(None)
+    assert not need_temperature_scaling(TrainingSamplingParams())
+    assert need_temperature_scaling(TrainingSamplingParams(temperature=0.7))
+    x = torch.randn(2, 3, 5)
+    before = x.clone()
+    assert apply_temperature_scaling(x, None) is x
+    assert apply_temperature_scaling(x, TrainingSamplingParams(top_k=3)) is x
+    assert torch.equal(x, before)
+    with pytest.raises(_C.MirlError):
+        apply_temperature_scaling(x, TrainingSamplingParams(temperature=0.7))
+    assert torch.equal(x, before)
+
+
+def test_loss_out_is_checked_before_any_launch():
+    """A wrong-dtype loss_out is refused by the binding (no assert that python -O strips)."""
+    cfg = ClippedPGLossFn(ClippedPGLossConfig())._kernel_config(False, False, False)
+    t = torch.zeros(2, 3)
+    with pytest.raises(_C.MirlError, match="loss_out must be one contiguous"):
+        _C.clipped_pg(cfg, t, None, t, t, t, t, t, None, torch.ones(2), None, torch.tensor(2.0),
+                      torch.tensor(6.0), loss_out=torch.zeros((), dtype=torch.float64))
+    with pytest.raises(_C.MirlError, match="loss_out must be one contiguous"):
+        _C.clipped_pg(cfg, t, None, t, t, t, t, t, None, torch.ones(2), None, torch.tensor(2.0),
+                      torch.tensor(6.0), loss_out=torch.zeros(2))
