@@ -19,11 +19,25 @@ op sequence) on a bounded sample of the same workload.
 roofline (the default line above is the headline measurement):
   fwd_f32      logprob forward only, fp32 [2, 256, 32000] (8 rotating input copies)
   long_context chunked logprob fwd+bwd, bf16 [1, 32768, 131072], chunk 4096
-  topk_filter  filtered logprob fwd+bwd, bf16 [4, 4096, 151936], T=0.7, k=50, p=0.9
+  topk_filter  filtered logprob fwd+bwd, bf16 [4, 4096, 151936], T=0.7, k=50, p=0.9,
+               through the reference's call shape: the model's logits divided in place
+               (apply_temperature_scaling), get_next_token_logprobs_from_logits with the
+               sampling params, backward to the raw logits
+  topk_filter_fused  the same rows with the temperature fused into the filter
+               (filtered_next_token_logprobs(..., temperature=T))
+  topp_only    as topk_filter with top-p 0.9 alone (no top-k): the histogram path
+  topk2000     as topk_filter with k = 2000, p = 0.9: the histogram path
+  filtered16_fwd  forward-only filtered logprobs decided in bf16 (the Megatron logprob
+               post-processor's call on the scaled bf16 logits), T=0.7, p=0.9
   packed_kl    packed GRPO step with k3 KL, 64 sequences in bf16 [1, ~34.8k, 256000],
                through SequencePackingFusionLossWrapper
   linear_ce    logprobs from hidden states, fwd+bwd: bf16 hidden [2048, 8, 4096] and
                LM-head weight [151936, 4096], chunk 256 positions (MFMA-bound: TFLOP/s)
+  distill_rkl, score_centering, topk_export: the other rows of the path (see below)
+
+Every line carries a `cpu_baseline`: the oracle timed on this host's cores on a
+bounded sample of the same workload (stated in `sample`), with the CPU model
+and torch version.
 """
 
 from __future__ import annotations
@@ -47,8 +61,14 @@ def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--workload", default="grpo",
-                    choices=["grpo", "fwd_f32", "long_context", "topk_filter", "packed_kl", "linear_ce",
+                    choices=["grpo", "fwd_f32", "long_context", "topk_filter", "topk_filter_fused",
+                             "topp_only", "topk2000", "filtered16_fwd", "packed_kl", "linear_ce",
                              "distill_rkl", "score_centering", "topk_export"])
+    ap.add_argument("--loss-scale", type=float, default=1.0,
+                    help="grpo: multiply the loss by this before the backward (as callers that "
+                         "scale the loss by the data-parallel size or microbatch count do)")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="minimum CPU time of the cpu_baseline sample")
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--cpu-chunk", type=int, default=128,
@@ -57,6 +77,51 @@ def parse():
     ap.add_argument("--calibrate-copy-gib", type=float, default=0.0,
                     help="also run a plain device copy of this many GiB (HBM counter calibration)")
     return ap.parse_args()
+
+
+def _cpu_threads() -> int:
+    import torch
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or len(os.sched_getaffinity(0))
+    threads = min(threads, len(os.sched_getaffinity(0)))
+    torch.set_num_threads(threads)
+    return threads
+
+
+def _cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or "unknown"
+
+
+def _cpu_fields(value: float, unit: str, threads: int, sample: str) -> dict:
+    import torch
+
+    return {"value": value, "unit": unit, "cores": threads, "kind": "port", "sample": sample,
+            "cpu_model": _cpu_model(), "torch": torch.__version__,
+            "cpu_capability": torch.backends.cpu.get_cpu_capability()}
+
+
+def _cpu_timed(run_pass, rows_per_pass: int, sample: str, min_seconds: float,
+               max_passes: int = 200, unit: str = "tokens/s") -> dict:
+    """Repeat the oracle pass `run_pass` until `min_seconds` have run; rows per second."""
+    threads = _cpu_threads()
+    passes = 0
+    t0 = time.perf_counter()
+    while True:
+        run_pass()
+        passes += 1
+        dt = time.perf_counter() - t0
+        if dt >= min_seconds or passes >= max_passes:
+            break
+    return _cpu_fields(passes * rows_per_pass / dt, unit, threads,
+                       f"{sample}; {passes} pass(es) in {dt:.1f} s")
 
 
 def cpu_baseline(x, tgt, d: dict, chunk: int, min_seconds: float = 10.0, max_passes: int = 3) -> dict:
@@ -71,9 +136,7 @@ def cpu_baseline(x, tgt, d: dict, chunk: int, min_seconds: float = 10.0, max_pas
     from oracle.logprob import selected_logprobs, selected_logprobs_grad
     from oracle.loss import clipped_pg_loss
 
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or len(os.sched_getaffinity(0))
-    threads = min(threads, len(os.sched_getaffinity(0)))
-    torch.set_num_threads(threads)
+    threads = _cpu_threads()
     B, R, V = x.shape
     passes = 0
     t0 = time.perf_counter()
@@ -88,14 +151,9 @@ def cpu_baseline(x, tgt, d: dict, chunk: int, min_seconds: float = 10.0, max_pas
         dt = time.perf_counter() - t0
         if dt >= min_seconds or passes >= max_passes:
             break
-    return {
-        "value": passes * B * R / dt,
-        "unit": "tokens/s",
-        "cores": threads,
-        "kind": "port",
-        "sample": f"the whole step's {B}x{R} next-token rows (V={V}, bf16) x {passes} pass(es): "
-                  f"fwd in chunks of {chunk} positions + ClippedPG loss + bwd, {dt:.1f} s",
-    }
+    return _cpu_fields(passes * B * R / dt, "tokens/s", threads,
+                       f"the whole step's {B}x{R} next-token rows (V={V}, bf16) x {passes} pass(es): "
+                       f"fwd in chunks of {chunk} positions + ClippedPG loss + bwd, {dt:.1f} s")
 
 
 def main() -> None:
@@ -137,6 +195,8 @@ def main() -> None:
         batch["advantages"] = adv
         lp = from_parallel_logits_to_logprobs(logits, ids, 0, V, None)
         loss, metrics = loss_fn(lp, batch, gvs, gvt)
+        if args.loss_scale != 1.0:
+            loss = loss * args.loss_scale
         (grad,) = torch.autograd.grad(loss, [logits])
         return grad, lp, metrics
 
@@ -148,7 +208,8 @@ def main() -> None:
     active_rows = int((glp != 0).sum().item())
     del grad, lp, lp2, l2, glp
 
-    ms_step, ms = _timed(step, args.steps, args.warmup, ["mirl_logprob_fwd", "mirl_logprob_bwd"])
+    main_kernels = ["mirl_logprob_fwd", "mirl_logprob_bwd", "mirl_logprob_bwd_recheck"]
+    ms_step, ms = _timed(step, args.steps, args.warmup, main_kernels)
 
     def avg_ms(name):
         return ms.get(name, 0.0)
@@ -158,6 +219,9 @@ def main() -> None:
     fwd_bytes = rows * V * esz
     bwd_bytes = active_rows * V * esz + B * S * V * esz
     fwd_ms, bwd_ms = avg_ms("mirl_logprob_fwd"), avg_ms("mirl_logprob_bwd")
+    # with a scaled loss the early backward (launched for the unit loss gradient)
+    # is checked and redone by the recheck launch; both are the step's backward
+    recheck_ms = avg_ms("mirl_logprob_bwd_recheck")
     loss_ms, adv_ms = avg_ms("mirl_clipped_pg"), avg_ms("mirl_grpo_advantage")
     bwd_gbps = bwd_bytes / (bwd_ms * 1e-3) / 1e9
     fwd_gbps = fwd_bytes / (fwd_ms * 1e-3) / 1e9
@@ -182,7 +246,7 @@ def main() -> None:
         }
         print(f"[bench] timing the CPU oracle on the step's {x_rows.shape[0] * x_rows.shape[1]} rows",
               file=sys.stderr, flush=True)
-        cpu = cpu_baseline(x_rows, tgt_rows, d, chunk=args.cpu_chunk)
+        cpu = cpu_baseline(x_rows, tgt_rows, d, chunk=args.cpu_chunk, min_seconds=args.cpu_seconds)
         del x_rows
 
     out = {
@@ -204,12 +268,13 @@ def main() -> None:
             "next_token_rows": rows,
             "active_rows": active_rows,
             "loss": "ClippedPG clip 0.2/0.2 token-level, no KL; GRPO adv (no LOO)",
+            "loss_scale": args.loss_scale,
             "parallelism": "single-gpu",
         },
         "hbm_gbps_step": step_gbps,
         "hbm_frac_step": step_gbps / PEAK_HBM_GBPS,
         "kernels_ms": {"logprob_fwd": fwd_ms, "logprob_bwd": bwd_ms, "clipped_pg": loss_ms,
-                       "grpo_advantage": adv_ms},
+                       "grpo_advantage": adv_ms, "logprob_bwd_recheck": recheck_ms},
         "logprob_fwd_gbps": fwd_gbps,
         "roofline": {
             "kernel": "mirl_logprob_bwd",
@@ -297,13 +362,78 @@ def _roofline(kernel: str, nbytes: float, ms: float, workload: str) -> dict:
             "frac": gbps / PEAK_HBM_GBPS, "traffic": _traffic(workload), "algorithmic_bytes": nbytes}
 
 
+def _timed_split(prepare, path, steps: int, warmup: int, main_kernels: list):
+    """Like _timed, for steps whose inputs must be rebuilt first (in-place work):
+    `prepare()` runs outside the timed window of each step; the step time is
+    the mean of HIP-event intervals around `path(prepare())` on the current stream."""
+    import torch
+
+    from rl_amd import _C
+
+    for _ in range(warmup):
+        path(prepare())
+    torch.cuda.synchronize()
+    timer = _C.enable_launch_timing(main_kernels)
+    evs = []
+    for _ in range(steps):
+        x = prepare()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        path(x)
+        e1.record()
+        evs.append((e0, e1))
+    torch.cuda.synchronize()
+    _C.disable_launch_timing()
+    ms = {k: sum(a.elapsed_time(b) for a, b in v) / max(1, len(v)) for k, v in timer.items()}
+    step_ms = sum(a.elapsed_time(b) for a, b in evs) / max(1, len(evs))
+    rest = _C.enable_launch_timing()
+    for _ in range(min(steps, 5)):
+        path(prepare())
+    torch.cuda.synchronize()
+    _C.disable_launch_timing()
+    for k, v in rest.items():
+        if k not in ms:
+            ms[k] = sum(a.elapsed_time(b) for a, b in v) / max(1, len(v))
+    return step_ms, ms
+
+
+def _dominant(candidates: list, ms: dict, workload: str) -> dict:
+    """Roofline of the entry point with the largest average time among
+    (name, algorithmic bytes) candidates."""
+    name, nbytes = max(candidates, key=lambda c: ms.get(c[0], 0.0))
+    return _roofline(name, nbytes, ms.get(name, 0.0), workload)
+
+
+def _filtered_cpu(x, ids, g, k, p, T, rows: int, min_seconds: float, forward_only: bool = False,
+                  decide_16bit: bool = False):
+    """The oracle's filtered chain on the first `rows` next-token rows of sequence 0."""
+    from oracle.sampling import apply_temperature, filtered_logprobs, next_token_filtered
+
+    xs = x[0:1, : rows + 1].detach().cpu()
+    ids_s = ids[0:1, : rows + 1].cpu()
+    gs = None if g is None else g[0:1, :rows].cpu()
+    if decide_16bit:
+        def run():
+            y = apply_temperature(xs, T)
+            filtered_logprobs(y[:, :-1], ids_s[:, 1:], k, p)
+        what = "T-division in bf16, top-p decided in bf16, forward"
+    else:
+        def run():
+            next_token_filtered(xs, ids_s, k, p, temperature=T, grad_output=None if forward_only else gs)
+        what = "T-division in bf16, fp32 upcast, filter, log_softmax, gather" + (
+            "" if forward_only else ", backward to the raw logits")
+    return lambda: _cpu_timed(run, rows, f"{rows} next-token rows of [1, {rows + 1}, {x.shape[-1]}] bf16 "
+                              f"(k={k}, p={p}, T={T}): {what}", min_seconds)
+
+
 def bench_workload(args) -> None:
     """The non-default workloads: one JSON line each, same fields as the headline line.
 
     Algorithmic bytes per next-token row of V entries of s bytes: forward V*s
     (read); unfiltered backward V*s read for rows with a non-zero upstream
     gradient plus V*s written for every row; filtered backward V*s written
-    (the kept set saved by the forward replaces the re-read).
+    (the kept set saved by the forward replaces the re-read); the in-place
+    temperature division V*s read + V*s written for every row.
     """
     import torch
 
@@ -315,6 +445,8 @@ def bench_workload(args) -> None:
     w = args.workload
     print(f"[bench] device {torch.cuda.get_device_name(dev)}; workload {w}", file=sys.stderr, flush=True)
     extra: dict = {}
+    cpu_fn = None
+    secs = args.cpu_seconds
     if w == "fwd_f32":
         copies = [workloads.logprob_fwd_f32(device=dev) for _ in range(8)]  # 8 x 65.5 MB > on-die cache
         B, S, V = copies[0]["logits"].shape
@@ -333,6 +465,13 @@ def bench_workload(args) -> None:
         cfg = {"workload": "logprob_fwd_f32", "logits": [B, S, V], "next_token_rows": rows,
                "rotating_copies": len(copies)}
         dtype = "f32"
+        xc, tc = copies[0]["logits"].cpu(), copies[0]["input_ids"].cpu()
+
+        def cpu_fn():
+            from oracle.logprob import selected_logprobs
+
+            return _cpu_timed(lambda: selected_logprobs(xc[:, :-1], tc[:, 1:], 0, V), rows,
+                              f"the whole fp32 [{B}, {S}, {V}] batch ({rows} next-token rows), forward", secs)
     elif w == "long_context":
         d = workloads.long_context_bf16(device=dev)
         logits = d["logits"].requires_grad_(True)
@@ -354,7 +493,104 @@ def bench_workload(args) -> None:
         cfg = {"workload": "long_context_chunked_logprob_fwd_bwd", "logits": [B, S, V], "chunk_size": 4096,
                "next_token_rows": rows, "active_rows": active}
         dtype = "bf16"
-    elif w == "topk_filter":
+        n_s = 2048
+        xs, ts, gs = logits.detach()[:, :n_s].cpu(), ids[:, 1 : n_s + 1].cpu(), g[:, :n_s].cpu()
+
+        def cpu_fn():
+            from oracle.logprob import selected_logprobs, selected_logprobs_grad
+
+            def run():
+                selected_logprobs(xs, ts, 0, V, chunk_size=4096)
+                selected_logprobs_grad(xs, ts, 0, V, gs, chunk_size=4096, out_dtype=torch.bfloat16)
+
+            return _cpu_timed(run, n_s, f"the first {n_s} of the {rows} next-token rows (V={V}, bf16, "
+                              "chunk 4096): forward + backward", secs)
+    elif w in ("topk_filter", "topp_only", "topk2000", "filtered16_fwd"):
+        from rl_amd.algorithms.logits_sampling_utils import TrainingSamplingParams, apply_temperature_scaling
+        from rl_amd.distributed.model_utils import get_next_token_logprobs_from_logits
+
+        if w == "topk_filter":
+            d = workloads.topk_filter_bf16(device=dev)
+        elif w == "topk2000":
+            d = workloads.general_filter_bf16(top_k=2000, top_p=0.9, device=dev)
+        else:
+            d = workloads.general_filter_bf16(top_k=None, top_p=0.9, device=dev)
+        raw = d["logits"]
+        ids, g = d["input_ids"], d["grad"]
+        B, S, V = raw.shape
+        k, p, T = d["top_k"], d["top_p"], d["temperature"]
+        sp = TrainingSamplingParams(top_k=k, top_p=p, temperature=T)
+        rows = B * (S - 1)
+        esz = 2
+        scale_bytes = 2 * B * S * V * esz
+        fwd_bytes, bwd_bytes = rows * V * esz, B * S * V * esz
+        if w == "filtered16_fwd":
+            work = torch.empty_like(raw)
+
+            def prepare():
+                work.copy_(raw)  # the model's output of this step, outside the timed window
+                return work
+
+            def path(logits):
+                apply_temperature_scaling(logits, sp)
+                return from_parallel_logits_to_logprobs(logits, ids, 0, V, None, inference_only=True,
+                                                        sampling_params=sp)
+
+            ms_step, ms = _timed_split(prepare, path, args.steps, args.warmup,
+                                       ["mirl_temperature_scale", "mirl_filtered_logprob_fwd"])
+            roof = _dominant([("mirl_temperature_scale", scale_bytes),
+                              ("mirl_filtered_logprob_fwd", fwd_bytes)], ms, w)
+            step_bytes = scale_bytes + fwd_bytes
+            cfg = {"workload": "bf16_decided_filtered_logprob_fwd", "logits": [B, S, V], "temperature": T,
+                   "top_k": k, "top_p": p, "next_token_rows": rows,
+                   "call": "apply_temperature_scaling in place, then from_parallel_logits_to_logprobs("
+                           "sampling_params, inference_only=True): top-p decided in bf16"}
+            cpu_fn = _filtered_cpu(raw, ids, None, k, p, T, 1024, secs, forward_only=True, decide_16bit=True)
+        else:
+            raw.requires_grad_(True)
+
+            class _ModelOutput(torch.autograd.Function):
+                """Stands in for the LM head: a fresh logits tensor each step (copied from
+                the resident logits outside the timed window); its backward hands the
+                raw-logits gradient on unchanged."""
+
+                @staticmethod
+                def forward(ctx, x):  # type: ignore[override]
+                    return x.detach().clone()
+
+                @staticmethod
+                def backward(ctx, grad):  # type: ignore[override]
+                    return grad
+
+            def prepare():
+                return _ModelOutput.apply(raw)
+
+            def path(logits):
+                logits = apply_temperature_scaling(logits, sp)
+                lp = get_next_token_logprobs_from_logits(ids, logits, sampling_params=sp)
+                return torch.autograd.grad(lp, [raw], g)
+
+            kern = ["mirl_temperature_scale", "mirl_filtered_logprob_fwd", "mirl_filtered_logprob_bwd"]
+            ms_step, ms = _timed_split(prepare, path, args.steps, args.warmup, kern)
+            roof = _dominant([("mirl_temperature_scale", scale_bytes), ("mirl_filtered_logprob_fwd", fwd_bytes),
+                              ("mirl_filtered_logprob_bwd", bwd_bytes)], ms, w)
+            step_bytes = scale_bytes + fwd_bytes + bwd_bytes
+            cfg = {"workload": {"topk_filter": "topk_topp_temperature_filtered_logprob_fwd_bwd",
+                                "topp_only": "topp_temperature_filtered_logprob_fwd_bwd",
+                                "topk2000": "topk2000_topp_temperature_filtered_logprob_fwd_bwd"}[w],
+                   "logits": [B, S, V], "temperature": T, "top_k": k, "top_p": p, "next_token_rows": rows,
+                   "call": "apply_temperature_scaling in place, get_next_token_logprobs_from_logits("
+                           "sampling_params), backward to the raw logits (the division's backward "
+                           "folded into the filtered backward)"}
+            cpu_fn = _filtered_cpu(raw, ids, g, k, p, T, 1024, secs)
+        fwd_ms = ms.get("mirl_filtered_logprob_fwd", 0.0)
+        bwd_ms = ms.get("mirl_filtered_logprob_bwd", 0.0)
+        sc_ms = ms.get("mirl_temperature_scale", 0.0)
+        extra["filtered_fwd_gbps"] = fwd_bytes / (fwd_ms * 1e-3) / 1e9 if fwd_ms > 0 else None
+        extra["filtered_bwd_gbps"] = bwd_bytes / (bwd_ms * 1e-3) / 1e9 if bwd_ms > 0 else None
+        extra["temperature_scale_gbps"] = scale_bytes / (sc_ms * 1e-3) / 1e9 if sc_ms > 0 else None
+        dtype = "bf16"
+    elif w == "topk_filter_fused":
         from rl_amd.distributed.sampling import filtered_next_token_logprobs
 
         d = workloads.topk_filter_bf16(device=dev)
@@ -364,7 +600,7 @@ def bench_workload(args) -> None:
         k, p, T = d["top_k"], d["top_p"], d["temperature"]
 
         def step():
-            lp = filtered_next_token_logprobs(logits, ids, k, p, temperature=T)
+            lp = filtered_next_token_logprobs(logits, ids, k, p, temperature=T, decision_dtype=torch.float32)
             return torch.autograd.grad(lp, [logits], g)
 
         ms_step, ms = _timed(step, args.steps, args.warmup,
@@ -376,10 +612,12 @@ def bench_workload(args) -> None:
         roof = _roofline("mirl_filtered_logprob_fwd", fwd_bytes, fwd_ms, w)
         extra["filtered_bwd_gbps"] = bwd_bytes / (bwd_ms * 1e-3) / 1e9 if bwd_ms > 0 else None
         step_bytes = fwd_bytes + bwd_bytes
-        cfg = {"workload": "topk_topp_temperature_filtered_logprob_fwd_bwd", "logits": [B, S, V],
+        cfg = {"workload": "topk_topp_temperature_filtered_logprob_fwd_bwd_fused", "logits": [B, S, V],
                "temperature": T, "top_k": k, "top_p": p, "next_token_rows": rows,
-               "temperature_fused": True}
+               "call": "filtered_next_token_logprobs(..., temperature=T, decision_dtype=float32): the "
+                       "division fused into the filter (an extension of the reference's API)"}
         dtype = "bf16"
+        cpu_fn = _filtered_cpu(logits, ids, g, k, p, T, 1024, secs)
     elif w == "linear_ce":
         from rl_amd.distributed.model_utils import from_parallel_hidden_states_to_logprobs
 
@@ -419,6 +657,15 @@ def bench_workload(args) -> None:
                "chunk_size": 256, "next_token_rows": rows, "active_rows": active,
                "flops_per_step": "2*S*B*H*V (fused fwd) + 3 x 2*active*H*V (fused grad recompute, dH, dW)"}
         dtype = "bf16"
+        n_pos = 32
+        hs, ws_, ts = hidden.detach()[:n_pos].cpu(), weight.detach().cpu(), torch.roll(ids, -1, 1)[:, :n_pos].cpu()
+
+        def cpu_fn():
+            from oracle.linear_ce import hidden_state_logprobs
+
+            return _cpu_timed(lambda: hidden_state_logprobs(hs, ts, ws_, 0, V), n_pos * B,
+                              f"{n_pos * B} rows ({n_pos} positions x {B}) of the hidden states against "
+                              f"the whole [{V}, {H}] weight: forward (logits, log-sum-exp, gather)", secs)
     elif w == "distill_rkl":
         from rl_amd.distributed.model_utils import ChunkedDistributedReverseKLToFixedLogits
 
@@ -448,6 +695,19 @@ def bench_workload(args) -> None:
                "next_token_rows": rows, "active_rows": active,
                "loss": "masked mean of per-token reverse KL over response tokens"}
         dtype = "bf16"
+        n_s = 1024
+        ss, tt = student.detach()[0:1, :n_s].cpu(), teacher[0:1, :n_s].cpu()
+        gg = torch.ones(1, n_s)
+
+        def cpu_fn():
+            from oracle.vocab_reduce import divergence, divergence_grad
+
+            def run():
+                divergence("reverse_kl", ss, tt, chunk_size=4096)
+                divergence_grad("reverse_kl", ss, tt, gg, chunk_size=4096)
+
+            return _cpu_timed(run, n_s, f"{n_s} rows of the student/teacher [1, {n_s}, {V}] bf16 pair: "
+                              "reverse KL forward + backward", secs)
     elif w == "score_centering":
         from types import SimpleNamespace
 
@@ -512,6 +772,21 @@ def bench_workload(args) -> None:
                "next_token_rows": rows, "active_rows": active, "ids_per_row": K + 1,
                "loss": "ClippedPG clip 0.2/0.2 token-level + score centering (IS off); GRPO adv"}
         dtype = "bf16"
+        n_s = 1024
+        xs = logits.detach()[0:1, :n_s].cpu()
+        idx = torch.cat([d["input_ids"][0:1, 1 : n_s + 1].unsqueeze(-1),
+                         d["sampler_topk_token_ids"][0:1, :n_s]], -1).cpu()
+        gg = torch.randn(idx.shape, generator=torch.Generator().manual_seed(0))
+
+        def cpu_fn():
+            from oracle.vocab_reduce import gather_logprobs, gather_logprobs_grad
+
+            def run():
+                gather_logprobs(xs, idx, 0, V)
+                gather_logprobs_grad(xs, idx, 0, V, gg)
+
+            return _cpu_timed(run, n_s, f"{n_s} rows of [1, {n_s}, {V}] bf16 at {K + 1} ids per row: "
+                              "log-softmax gather forward + backward (the loss kernels excluded)", secs)
     elif w == "topk_export":
         from rl_amd.distributed.model_utils import distributed_vocab_topk
 
@@ -533,6 +808,15 @@ def bench_workload(args) -> None:
         cfg = {"workload": "teacher_topk_export", "logits": [B, S, V], "k": k, "rows": rows,
                "outputs": "fp32 values + int64 ids [B, S, k]"}
         dtype = "bf16"
+        n_s = 1024
+        xs = teacher[0:1, :n_s].cpu()
+
+        def cpu_fn():
+            from oracle.vocab_reduce import vocab_topk
+
+            return _cpu_timed(lambda: vocab_topk(xs, k), n_s,
+                              f"{n_s} rows of [1, {n_s}, {V}] bf16: top-{k} values and ids", secs,
+                              unit="rows/s")
     else:  # packed_kl
         import torch.distributed as dist
 
@@ -602,10 +886,29 @@ def bench_workload(args) -> None:
                "next_token_rows": rows, "active_rows": active,
                "loss": "ClippedPG clip 0.2/0.2, k3 KL beta 0.01, sequence-level mean; GRPO adv (no LOO)"}
         dtype = "bf16"
+        n_s = 2048
+        xs = logits.detach()[:, :n_s].cpu()
+        ts = _packed_targets(d["input_ids"], cu)[:, :n_s].cpu()
+        gg = torch.randn(1, n_s, generator=torch.Generator().manual_seed(0))
+
+        def cpu_fn():
+            from oracle.logprob import selected_logprobs, selected_logprobs_grad
+
+            def run():
+                selected_logprobs(xs, ts, 0, V, chunk_size=1024)
+                selected_logprobs_grad(xs, ts, 0, V, gg, chunk_size=1024, out_dtype=torch.bfloat16)
+
+            return _cpu_timed(run, n_s, f"the first {n_s} of the {T} packed rows (V={V}, bf16): logprob "
+                              "forward + backward in chunks of 1024 rows (the loss, ~0.3% of the "
+                              "step, excluded)", secs)
 
     _calibration_copy(args, dev)
     cfg["parallelism"] = "single-gpu"
     step_gbps = step_bytes / (ms_step * 1e-3) / 1e9 if step_bytes is not None else None
+    cpu = None
+    if not args.no_cpu_baseline and cpu_fn is not None:
+        print("[bench] timing the CPU oracle", file=sys.stderr, flush=True)
+        cpu = cpu_fn()
     out = {
         "metric": f"{w}: next-token rows/s and HBM GB/s (% peak)",
         "value": rows / (ms_step * 1e-3),
@@ -625,9 +928,17 @@ def bench_workload(args) -> None:
         "kernels_ms": {k.replace("mirl_", ""): v for k, v in ms.items()},
         **extra,
         "roofline": roof,
-        "cpu_baseline": None,
+        "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
+
+
+def _packed_targets(input_ids, cu):
+    """Packed next-token targets [1, T] of the [n, S] ids (the oracle's packing with the
+    per-sequence roll), for the CPU baseline's sample."""
+    from oracle.logprob import pack_input_ids
+
+    return pack_input_ids(input_ids.cpu(), list(cu), list(cu), roll_shift=-1)
 
 
 if __name__ == "__main__":

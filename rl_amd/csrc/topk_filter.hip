@@ -107,7 +107,7 @@ __device__ void block_rank_sort(uint64_t* keys, int n) {
 // left).  `skeys` holds the kept-k candidates sorted ascending as
 // (okey(y) << 32 | index); `thr` is the top-k value; `yt` is the target's
 // scaled logit (lane 0 only; NaN when there is no target in range).
-template <class E>
+template <class E, bool DEC16>
 __device__ void finish_row(const FilterParams& P, int64_t row, const uint64_t* skeys, int n_k,
                            float thr, float yt, int64_t t) {
   const int lane = threadIdx.x;
@@ -120,7 +120,7 @@ __device__ void finish_row(const FilterParams& P, int64_t row, const uint64_t* s
     for (int i = lane; i < n_k; i += 64) zpart += (double)expf(y_at(i) - m);
     const float Z = (float)wave_sum(zpart);
     first = n_k - 1;  // the maximum is always kept
-    if (P.dec16) {
+    if constexpr (DEC16) {
       // probabilities rounded to the logits dtype; the cumulative sum is
       // accumulated one element at a time in fp32, in ascending order (every
       // lane holds the same running sum and adds each element read from its
@@ -130,8 +130,8 @@ __device__ void finish_row(const FilterParams& P, int64_t row, const uint64_t* s
         const int i = base + lane;
         const float p = (i < n_k) ? round_trip<E>(expf(y_at(i) - m) / Z) : 0.f;
         float mine = 0.f;
-#pragma unroll
-        for (int l = 0; l < 64; ++l) {
+        const int n_here = n_k - base < 64 ? n_k - base : 64;
+        for (int l = 0; l < n_here; ++l) {
           S += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), l));
           mine = (lane == l) ? S : mine;
         }
@@ -333,7 +333,7 @@ __global__ __launch_bounds__(kGeneralThreads) void topk_export_general_kernel(Fi
 // ---------------------------------------------------------------------------
 // fast path
 // ---------------------------------------------------------------------------
-template <class E, int W, int U, bool EXPORT = false>
+template <class E, int W, int U, bool EXPORT = false, bool DEC16 = false>
 __global__ __launch_bounds__(64 * W) void filter_fast_kernel(FilterParams P) {
   using raw = typename E::raw;
   constexpr int NT = 64 * W;
@@ -554,7 +554,7 @@ __global__ __launch_bounds__(64 * W) void filter_fast_kernel(FilterParams P) {
   for (int i = tid; i < C; i += NT) cnt += ((uint32_t)(s_cand[i] >> 32) >= thr_key) ? 1 : 0;
   __shared__ int redi[NT / 64];
   const int n_k = block_sum_i<NT>(cnt, redi);
-  if (tid < 64) finish_row<E>(P, row, s_cand + (C - n_k), n_k, from_okey(thr_key), yt, t);
+  if (tid < 64) finish_row<E, DEC16>(P, row, s_cand + (C - n_k), n_k, from_okey(thr_key), yt, t);
 }
 
 // ---------------------------------------------------------------------------
@@ -905,10 +905,19 @@ int launch_fwd(const FilterParams& P, int64_t rows, hipStream_t st) {
   if (fast) {
     switch (fast_waves(P.top_k)) {
       case 8:
-        hipLaunchKernelGGL((filter_fast_kernel<E, 8, 4>), dim3((unsigned)rows), dim3(512), 0, st, P);
+        if (P.dec16)
+          hipLaunchKernelGGL((filter_fast_kernel<E, 8, 4, false, true>), dim3((unsigned)rows), dim3(512),
+                             0, st, P);
+        else
+          hipLaunchKernelGGL((filter_fast_kernel<E, 8, 4>), dim3((unsigned)rows), dim3(512), 0, st, P);
         break;
       default:
-        hipLaunchKernelGGL((filter_fast_kernel<E, 16, 4>), dim3((unsigned)rows), dim3(1024), 0, st, P);
+        if (P.dec16)
+          hipLaunchKernelGGL((filter_fast_kernel<E, 16, 4, false, true>), dim3((unsigned)rows),
+                             dim3(1024), 0, st, P);
+        else
+          hipLaunchKernelGGL((filter_fast_kernel<E, 16, 4>), dim3((unsigned)rows), dim3(1024), 0, st,
+                             P);
         break;
     }
     if (int e = check_launch("filter_fast_kernel")) return e;

@@ -90,6 +90,15 @@ __device__ __forceinline__ uint32_t raw_of_okey16(uint32_t k) {
   return (k & 0x8000u) ? (k & 0x7fffu) : (~k & 0xffffu);
 }
 
+// Physical table word of logical word L (= key >> 1).  Thread t owns logical
+// words 32t .. 32t + 31 (keys 64t .. 64t + 63); their order inside the block is
+// rotated by t / 2 so that the 64 lanes of a wave reading their own word w hit
+// 64 different banks.
+__device__ __forceinline__ uint32_t hword(uint32_t L) {
+  const uint32_t t = L >> 5;
+  return (t << 5) | (((L & 31u) + (t >> 1)) & 31u);
+}
+
 template <class T>
 __device__ __forceinline__ T wave_incl_scan(T v) {
   const int lane = threadIdx.x & 63;
@@ -153,22 +162,31 @@ __device__ uint32_t block_max_u(uint32_t v, uint32_t* red) {
   return r;
 }
 
-// Bound on the rounding of n fp32 additions S <- fl(S + p) that take an exact
-// running sum from X0 to X1 (> 0), given that S stays within a factor 2 of
-// the exact sum (true for fewer than 2^22 additions).  S then stays below
-// 2^(e1 + 1), e1 = ilogb(X1) + 1, where the ulp is u.  An addend that is a
+// Relative distance within which the fp32 running sum S is kept from the
+// exact sum X: the bound below assumes |S - X| <= kSlack * X, which the
+// certification checks as it goes.
+constexpr double kSlack = 1.0 / 4096.0;
+
+// Bound on the rounding of n fp32 additions S <- fl(S + p) that take the
+// exact running sum from X0 to X1 (> 0), with S within kSlack * X of X.  S
+// stays in [X0 (1 - kSlack), X1 (1 + kSlack)], below 2^(e + 1) for
+// e = ilogb(X1 (1 + kSlack)), where the ulp is u.  An addend that is a
 // multiple of u adds exactly inside each binade and can round only where S
-// enters a new binade (at most e1 - ilogb(X0) + 2 times, half an ulp each);
-// any other addend may round on every addition.
+// enters a new binade: once per power of two in that interval, by at most
+// half that binade's ulp (<= u / 2).  Any other addend may round on every
+// addition, by at most u / 2.
 __device__ double run_error_bound(uint32_t n, double p, double X0, double X1) {
   if (p == 0.0 || n == 0u) return 0.0;
-  const int e1 = ilogb(X1) + 1;
-  const int eu = (e1 < -126 ? -126 : e1) - 23;
+  const double hi = X1 * (1.0 + kSlack);
+  const int e = ilogb(hi);
+  const int eu = (e < -126 ? -126 : e) - 23;
   const double u = ldexp(1.0, eu);
   const double q = ldexp(p, -eu);
   if (q == floor(q)) {
-    const int e0 = X0 > 0.0 ? ilogb(X0) : ilogb(p);
-    return (double)(e1 - e0 + 2) * 0.5 * u;
+    // the first addition to an empty sum is exact (S = p); binades are entered above it
+    const double lo = X0 > 0.0 ? X0 * (1.0 - kSlack) : p;
+    const int crossings = e - ilogb(lo);
+    return (double)crossings * 0.5 * u;
   }
   return (double)n * 0.5 * u;
 }
@@ -305,14 +323,26 @@ __global__ __launch_bounds__(kHT) void filter_hist_kernel(FilterParams P, int al
         }
       }
     } else {
-      for (int64_t v = tid; v < nvec; v += kHT) {
-        const vu4 t = __builtin_nontemporal_load(xv + v);
-        const uint32_t w[4] = {t.x, t.y, t.z, t.w};
-        const int64_t base = sp.head + v * 8;
+      // batches of 8 independent loads per lane
+      constexpr int UB = 8;
+      for (int64_t v0 = tid; v0 < nvec; v0 += (int64_t)UB * kHT) {
+        vu4 t[UB];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          f(base + 2 * e, w[e] & 0xffffu);
-          f(base + 2 * e + 1, w[e] >> 16);
+        for (int u = 0; u < UB; ++u) {
+          const int64_t v = v0 + (int64_t)u * kHT;
+          if (v < nvec) t[u] = __builtin_nontemporal_load(xv + v);
+        }
+#pragma unroll
+        for (int u = 0; u < UB; ++u) {
+          const int64_t v = v0 + (int64_t)u * kHT;
+          if (v >= nvec) break;
+          const uint32_t w[4] = {t[u].x, t[u].y, t[u].z, t[u].w};
+          const int64_t base = sp.head + v * 8;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            f(base + 2 * e, w[e] & 0xffffu);
+            f(base + 2 * e + 1, w[e] >> 16);
+          }
         }
       }
     }
@@ -322,7 +352,7 @@ __global__ __launch_bounds__(kHT) void filter_hist_kernel(FilterParams P, int al
   uint32_t kmax = 0;
   sweep([&](int64_t, uint32_t rw) {
     const uint32_t k = okey16(rw);
-    atomicAdd(&sh.hist[k >> 1], (k & 1u) ? 0x10000u : 1u);
+    atomicAdd(&sh.hist[hword(k >> 1)], (k & 1u) ? 0x10000u : 1u);
     kmax = max(kmax, k);
   });
   const uint32_t kmx = block_max_u(kmax, sh.red_u);  // its barriers complete the table
@@ -332,7 +362,7 @@ __global__ __launch_bounds__(kHT) void filter_hist_kernel(FilterParams P, int al
   uint32_t ct = 0;
 #pragma unroll 4
   for (int w = 0; w < 32; ++w) {
-    const uint32_t word = sh.hist[tid * 32 + w];
+    const uint32_t word = sh.hist[hword(tid * 32 + w)];
     ct += (word & 0xffffu) + (word >> 16);
   }
   {
@@ -348,7 +378,7 @@ __global__ __launch_bounds__(kHT) void filter_hist_kernel(FilterParams P, int al
       if (tid < 256) {
         uint32_t fine = 0;
         for (int i = 0; i < 128; ++i) {
-          const uint32_t word = sh.hist[tid * 128 + i];
+          const uint32_t word = sh.hist[hword(tid * 128 + i)];
           fine += (word & 0xffffu) + (word >> 16);
         }
         if (fine != sh.coarse[tid]) {
@@ -382,13 +412,13 @@ __global__ __launch_bounds__(kHT) void filter_hist_kernel(FilterParams P, int al
       for (int s = 0; s < novf; ++s)
         if (sh.ovf_block[s] == (k >> 8)) return sh.ovf_cnt[s * 256 + (k & 255u)];
     }
-    return (sh.hist[k >> 1] >> ((k & 1u) << 4)) & 0xffffu;
+    return (sh.hist[hword(k >> 1)] >> ((k & 1u) << 4)) & 0xffffu;
   };
   // f(key, count) over this thread's 64 keys with a non-zero count, ascending
   auto for_range = [&](auto&& f) {
 #pragma unroll 1
     for (int w = 0; w < 32; ++w) {
-      const uint32_t word = sh.hist[tid * 32 + w];
+      const uint32_t word = sh.hist[hword(tid * 32 + w)];
       if (word == 0u && novf == 0) continue;
       const uint32_t ka = k0 + 2u * (uint32_t)w;
       const uint32_t na = novf ? kcount(ka) : (word & 0xffffu);
@@ -534,13 +564,14 @@ __global__ __launch_bounds__(kHT) void filter_hist_kernel(FilterParams P, int al
       const double D0 = block_excl_scan<double>(bt, sh.red_d, &btot);
       {
         double X = X0, D = D0;
-        bool flo = false, fhi = false;
+        bool flo = false, fhi = false, slack_ok = true;
         uint32_t klo = 0, plo = 0, khi = 0, phi = 0;
         for_range([&](uint32_t key, uint32_t n) {
           if ((flo && fhi) || key < thr_key) return;
           const double p = pmass(key);
           const double X1 = X + (double)n * p;
           const double Db = D + run_error_bound(n, p, X, X1);
+          if (Db > 0.5 * kSlack * X1) slack_ok = false;  // the bound's premise fails: walk the row
           auto hlo = [&](double v) { return v + Db >= Bd; };
           auto hhi = [&](double v) { return v - Db >= Bd; };
           if (!flo && hlo(X1)) {
@@ -558,6 +589,7 @@ __global__ __launch_bounds__(kHT) void filter_hist_kernel(FilterParams P, int al
         });
         if (flo) atomicMin(&sh.first_lo, tid);
         if (fhi) atomicMin(&sh.first_hi, tid);
+        if (!slack_ok) sh.walk_hit = -1;
         __syncthreads();
         if (sh.first_lo == tid) {
           sh.key_lo = klo;
@@ -570,9 +602,10 @@ __global__ __launch_bounds__(kHT) void filter_hist_kernel(FilterParams P, int al
         __syncthreads();
       }
       const bool none_lo = sh.first_lo >= kHT, none_hi = sh.first_hi >= kHT;
-      const bool certain = (none_lo && none_hi) ||
-                           (!none_lo && !none_hi && sh.key_lo == sh.key_hi &&
-                            sh.pos_lo == sh.pos_hi);
+      const bool certain = sh.walk_hit == 0 &&
+                           ((none_lo && none_hi) ||
+                            (!none_lo && !none_hi && sh.key_lo == sh.key_hi &&
+                             sh.pos_lo == sh.pos_hi));
       if (certain) {
         have_cut = !none_hi;
         cut_key = sh.key_hi;

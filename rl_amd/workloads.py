@@ -165,6 +165,54 @@ def topk_filter_bf16(
             "top_k": top_k, "top_p": top_p}
 
 
+def general_filter_bf16(
+    B: int = 4,
+    S: int = 4096,
+    V: int = 151936,
+    temperature: float = 0.7,
+    top_k: Optional[int] = None,
+    top_p: float = 0.9,
+    seed: int = 9,
+    device=None,
+):
+    """Logits shaped like the filtered workload (N(0, 1) plus one Zipf-ranked +8
+    boost per row) for filters that keep large sets (top-p alone, k = 2000);
+    targets 90% uniform over each row's kept set (found with a descending sort
+    in chunks of 512 rows), 10% uniform over the vocabulary."""
+    g = _gen(seed)
+    dev = torch.device(device) if device is not None else torch.device("cpu")
+    logits = _randn_bf16((B, S, V), 1.0, g, device)
+    perm = torch.randperm(V, generator=g)
+    ranks = torch.arange(1, V + 1, dtype=torch.float64)
+    pick = torch.multinomial(ranks.pow(-1.1), B * S, replacement=True, generator=g)
+    boost_idx = perm[pick].view(B, S).to(dev)
+    flat = logits.view(B * S, V)
+    rows = torch.arange(B * S, device=dev)
+    flat[rows, boost_idx.view(-1)] = (flat[rows, boost_idx.view(-1)].float() + 8.0).to(torch.bfloat16)
+    u = torch.rand(B * S, generator=g).to(dev)
+    outside = torch.randint(0, V, (B * S,), generator=g).to(dev)
+    use_inside = torch.rand(B * S, generator=g).to(dev) < 0.9
+    inside = torch.empty(B * S, dtype=torch.long, device=dev)
+    for a in range(0, B * S, 512):
+        y = (flat[a : a + 512].float() / temperature).to(torch.bfloat16).float()
+        vals, idx = torch.sort(y, dim=-1, descending=True)
+        n_in = torch.full((vals.shape[0],), V, device=dev)
+        if top_k is not None and top_k > 0:
+            n_in = torch.clamp(n_in, max=top_k)
+            vals = torch.where(torch.arange(V, device=dev) < top_k, vals, torch.full_like(vals, -float("inf")))
+        p = torch.softmax(vals.double(), -1)
+        below = 1.0 - torch.cumsum(p, -1) + p  # mass of each element and everything after it
+        n_in = torch.minimum(n_in, (below > 1 - top_p).sum(-1).clamp(min=1))
+        choose = (u[a : a + 512] * n_in).long().clamp(max=V - 1)
+        inside[a : a + 512] = idx.gather(1, choose.unsqueeze(1)).squeeze(1)
+        del y, vals, idx, p, below
+    tgt = torch.where(use_inside, inside, outside).view(B, S)
+    ids = torch.roll(tgt, shifts=1, dims=1)
+    grad = torch.randn((B, S - 1), generator=g).to(dev) * use_inside.view(B, S)[:, :-1].float()
+    return {"logits": logits, "input_ids": ids, "grad": grad, "temperature": temperature,
+            "top_k": top_k, "top_p": top_p}
+
+
 def packed_grpo_kl_bf16(
     n_seq: int = 64,
     len_min: int = 64,
