@@ -210,6 +210,15 @@ def main() -> None:
 
     main_kernels = ["mirl_logprob_fwd", "mirl_logprob_bwd", "mirl_logprob_bwd_recheck"]
     ms_step, ms = _timed(step, args.steps, args.warmup, main_kernels)
+    always = None
+    if args.loss_scale != 1.0:
+        # the default (adaptive) policy stops speculating after the first checked
+        # miss; time the redo itself with speculation forced on every step
+        from rl_amd.distributed.model_utils import set_early_backward
+
+        set_early_backward("always")
+        always = _timed(step, args.steps, args.warmup, main_kernels)
+        set_early_backward("adaptive")
 
     def avg_ms(name):
         return ms.get(name, 0.0)
@@ -222,6 +231,8 @@ def main() -> None:
     # with a scaled loss the early backward (launched for the unit loss gradient)
     # is checked and redone by the recheck launch; both are the step's backward
     recheck_ms = avg_ms("mirl_logprob_bwd_recheck")
+    if always is not None:
+        recheck_ms = always[1].get("mirl_logprob_bwd_recheck", 0.0)
     loss_ms, adv_ms = avg_ms("mirl_clipped_pg"), avg_ms("mirl_grpo_advantage")
     bwd_gbps = bwd_bytes / (bwd_ms * 1e-3) / 1e9
     fwd_gbps = fwd_bytes / (fwd_ms * 1e-3) / 1e9
@@ -276,6 +287,10 @@ def main() -> None:
         "kernels_ms": {"logprob_fwd": fwd_ms, "logprob_bwd": bwd_ms, "clipped_pg": loss_ms,
                        "grpo_advantage": adv_ms, "logprob_bwd_recheck": recheck_ms},
         "logprob_fwd_gbps": fwd_gbps,
+        # loss_scale != 1 only: the step with the early backward forced on every
+        # step (wasted early backward + check + redo), and the redo's rate
+        "always_speculate_ms_per_step": None if always is None else always[0],
+        "logprob_bwd_recheck_gbps": (bwd_bytes / (recheck_ms * 1e-3) / 1e9) if always is not None and recheck_ms > 0 else None,
         "roofline": {
             "kernel": "mirl_logprob_bwd",
             "bound": "hbm",

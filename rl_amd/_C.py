@@ -338,20 +338,22 @@ def _require_gpu(*tensors: Optional[torch.Tensor]) -> torch.device:
 
 
 def start_fetch(t: torch.Tensor):
-    """Enqueue a copy of a small device tensor into a cached pinned buffer and
-    record an event after it; finish_fetch waits for that event.
+    """Enqueue a copy of a small device tensor into a pinned host buffer and
+    record an event after it; finish_fetch waits for that event, poll_fetch
+    only tests it.
 
     The copy runs on a side stream (default priority) behind everything already
     enqueued on the current stream, so work the caller enqueues next on the
     current stream (the early logits backward) starts without waiting for the
-    copy, and the wait does not include that work either."""
+    copy, and the wait does not include that work either.  Pinned buffers come
+    from a pool keyed on (device, dtype, power-of-two size class) and go back to
+    it when the values have been read, so overlapping fetches never share a
+    buffer and varying sizes reuse a few buffers."""
     n = t.numel()
     dev = t.device
-    key = (dev, t.dtype, n)
-    buf = _pinned.get(key)
-    if buf is None:
-        buf = torch.empty(n, dtype=t.dtype, pin_memory=True)
-        _pinned[key] = buf
+    key = (dev, t.dtype, max(16, 1 << max(n - 1, 0).bit_length()))
+    pool = _pinned.setdefault(key, [])
+    buf = pool.pop() if pool else torch.empty(key[2], dtype=t.dtype, pin_memory=True)
     side = _fetch_streams.get(dev)
     if side is None:
         side = torch.cuda.Stream(dev)
@@ -359,20 +361,37 @@ def start_fetch(t: torch.Tensor):
     side.wait_stream(torch.cuda.current_stream(dev))
     src = t.reshape(-1)
     with torch.cuda.stream(side):
-        buf.copy_(src, non_blocking=True)
+        buf[:n].copy_(src, non_blocking=True)
         ev = torch.cuda.Event()
         ev.record(side)
     src.record_stream(side)  # the allocator keeps src until the side stream has read it
-    return buf, ev
+    return [buf, ev, n, key]
+
+
+def _read_fetch(handle) -> list:
+    buf, _, n, key = handle
+    values = buf[:n].tolist()
+    handle[0] = None
+    _pinned[key].append(buf)  # reusable: the copy into it has completed
+    return values
 
 
 def finish_fetch(handle) -> list:
     """Wait for start_fetch's copy by polling its event (wakes up sooner than a
     blocking device-to-host copy) and return the values as a list."""
-    buf, ev = handle
+    _require(handle[0] is not None, "this fetch was already read")
+    ev = handle[1]
     while not ev.query():
         pass
-    return buf.tolist()
+    return _read_fetch(handle)
+
+
+def poll_fetch(handle) -> Optional[list]:
+    """start_fetch's values if its copy has completed, else None (never waits)."""
+    _require(handle[0] is not None, "this fetch was already read")
+    if not handle[1].query():
+        return None
+    return _read_fetch(handle)
 
 
 def wait_and_fetch(t: torch.Tensor) -> list:
@@ -508,8 +527,11 @@ def logprob_bwd_recheck(
     grad_out: torch.Tensor,
     grad_used: torch.Tensor,
     grad_in: torch.Tensor,
-) -> None:
-    """grad_in was written by logprob_bwd for grad_used; make it right for grad_out (device-side check)."""
+) -> torch.Tensor:
+    """grad_in was written by logprob_bwd for grad_used; make it right for grad_out (device-side check).
+
+    Returns the check's flags ([64] int32 on the device, all zero when grad_out
+    equals grad_used bit for bit): one flag per check workgroup."""
     dev = _require_gpu(logits, target, stats, grad_out, grad_used, grad_in)
     B, R = target.shape
     Rt = grad_in.shape[1]
@@ -526,6 +548,7 @@ def logprob_bwd_recheck(
         flag.data_ptr(), _stream(dev),
     )
     _check(st, "mirl_logprob_bwd_recheck")
+    return flag[: min(B * R, 64)]  # one flag per check workgroup
 
 
 # ---------------------------------------------------------------------------
@@ -717,8 +740,10 @@ def gather_logprob_bwd_recheck(
     grad_out: torch.Tensor,
     grad_used: torch.Tensor,
     grad_in: torch.Tensor,
-) -> None:
-    """Recompute grad_in from grad_out on the device only if it differs from grad_used."""
+) -> torch.Tensor:
+    """Recompute grad_in from grad_out on the device only if it differs from grad_used.
+
+    Returns the check's flags (int32 on the device, all zero when nothing differed)."""
     dev = _require_gpu(logits, indices, stats, grad_out, grad_used, grad_in)
     B, R, K = indices.shape
     V = logits.shape[-1]
@@ -739,6 +764,7 @@ def gather_logprob_bwd_recheck(
         _stream(dev),
     )
     _check(st, "mirl_gather_logprob_bwd_recheck")
+    return flags[: min(B * R * K, 64)]  # one flag per check workgroup
 
 
 def vocab_topk(logits: torch.Tensor, k: int, vocab_start: int) -> tuple[torch.Tensor, torch.Tensor]:

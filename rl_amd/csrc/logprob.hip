@@ -316,6 +316,18 @@ __global__ __launch_bounds__(64 * W) void logprob_bwd_kernel(
   for (; i < nvec; i += NT) __builtin_nontemporal_store(grad_vec(__builtin_nontemporal_load(xv + i), i), yv + i);
 }
 
+// `flags` (nflags ints, or null) makes a launch conditional: it does nothing
+// unless some flag is set (the early-backward recheck's redo).  Each thread
+// loads at most a few flags and the workgroup ORs them in one barrier (a
+// serial loop over 64 flags per thread measured 13 us for a launch that then
+// did nothing); every thread of the workgroup must call it.
+__device__ __forceinline__ bool any_flag(const int* __restrict__ flags, int nflags) {
+  if (flags == nullptr) return true;
+  int v = 0;
+  for (int k = threadIdx.x; k < nflags; k += blockDim.x) v |= flags[k];
+  return __syncthreads_or(v) != 0;
+}
+
 // Backward over a contiguous [B, Rt, V] gradient whose logits share its layout
 // (V a multiple of the vector width, both 16-byte aligned): one 4 KB piece of
 // the flat gradient per 128-thread workgroup (two 16-byte vectors per lane,
@@ -332,17 +344,34 @@ __global__ __launch_bounds__(64 * W) void logprob_bwd_kernel(
 constexpr int kFlatThreads = 128;
 constexpr int kFlatVecs = 2;
 
-template <class E>
-__global__ __launch_bounds__(kFlatThreads) void logprob_bwd_flat_kernel(
-    const typename E::raw* __restrict__ logits, int64_t R, uint32_t Rt, uint32_t nvr,
-    uint32_t nvec, int shift, const int64_t* __restrict__ target, int64_t tsb, int64_t tsr,
-    int64_t vs, int64_t ve, int64_t V, const float* __restrict__ stats,
-    const float* __restrict__ g, int64_t gsb, int64_t gsr, typename E::raw* gin) {
+struct FlatBwd {
+  const void* logits;
+  int64_t R;
+  uint32_t Rt, nvr, nvec;
+  int shift;
+  const int64_t* target;
+  int64_t tsb, tsr, vs, ve, V;
+  const float* stats;
+  const float* g;
+  int64_t gsb, gsr;
+  void* gin;
+};
+
+// One 4 KB piece (256 16-byte vectors) by a workgroup of NT threads, U vectors
+// per lane NT vectors apart.
+template <class E, int NT, int U>
+__device__ __forceinline__ void bwd_flat_piece(const FlatBwd& A, int64_t piece) {
+  static_assert(NT * U == kFlatThreads * kFlatVecs, "a piece is 256 vectors");
   constexpr int VEC = E::kVec;
-  constexpr int NT = kFlatThreads, U = kFlatVecs;
-  vu4* yv = reinterpret_cast<vu4*>(gin);
-  const vu4* xv = reinterpret_cast<const vu4*>(logits);
-  const int64_t base = (int64_t)blockIdx.x * (NT * U) + threadIdx.x - shift;
+  const int64_t R = A.R, vs = A.vs, ve = A.ve, V = A.V;
+  const uint32_t Rt = A.Rt, nvr = A.nvr, nvec = A.nvec;
+  const float* __restrict__ stats = A.stats;
+  const float* __restrict__ g = A.g;
+  const int64_t* __restrict__ target = A.target;
+  const int64_t gsb = A.gsb, gsr = A.gsr, tsb = A.tsb, tsr = A.tsr;
+  vu4* yv = static_cast<vu4*>(A.gin);
+  const vu4* xv = static_cast<const vu4*>(A.logits);
+  const int64_t base = piece * (NT * U) + threadIdx.x - A.shift;
   bool ok[U];
   uint32_t row[U];
   float gv[U], M[U], LS[U];
@@ -396,6 +425,32 @@ __global__ __launch_bounds__(kFlatThreads) void logprob_bwd_flat_kernel(
   }
 }
 
+template <class E>
+__global__ __launch_bounds__(kFlatThreads) void logprob_bwd_flat_kernel(FlatBwd A) {
+  bwd_flat_piece<E, kFlatThreads, kFlatVecs>(A, blockIdx.x);
+}
+
+// The early-backward recheck's redo on the flat schedule.  Launches with no
+// flag set are the common case, and their cost is the number of (empty)
+// workgroups dispatched; the redo itself is fastest with one workgroup per
+// piece.  Compromise: single-wave workgroups (four vectors per lane) in a
+// grid-stride loop over the pieces, kRedoGrid of them (two per wave slot, so
+// the later ones fill slots that free up early).  Measured on the backward of the
+// [8, 2048, 151936] bf16 GRPO rows: redo 1.50 ms and 15 us with no flag set;
+// one two-wave workgroup per piece 1.26 ms but 0.28 ms with no flag set; two-wave
+// workgroups over all 8192 wave slots 1.62 ms.  The flags are tested per wave
+// (one load per lane and a ballot, no barrier).  Same pieces and arithmetic as
+// logprob_bwd_flat_kernel.
+template <class E>
+__global__ __launch_bounds__(64) void logprob_bwd_flat_redo_kernel(
+    FlatBwd A, int64_t npieces, const int* __restrict__ flags, int nflags) {
+  const int lane = threadIdx.x & 63;
+  const int f = lane < nflags ? flags[lane] : 0;
+  if (__ballot(f != 0) == 0ull) return;
+  for (int64_t piece = blockIdx.x; piece < npieces; piece += gridDim.x)
+    bwd_flat_piece<E, 64, 4>(A, piece);
+}
+
 // Backward of the K-id gather (reference model_utils.py:750-805):
 //   grad = -p * sum_k g_k, plus g_k added at each in-range id_k, in fp32,
 // rounded once to the logits dtype.  Three launches: gather_gsum_kernel forms
@@ -405,17 +460,8 @@ __global__ __launch_bounds__(kFlatThreads) void logprob_bwd_flat_kernel(
 // the [8, 2048, 151936] bf16 rows with 21 ids, 1.47 vs 1.30 ms: the staging
 // round in front of every piece's logits load cuts the bytes in flight.)
 //
-// `flags` (nflags ints, or null) makes a launch conditional: it does nothing
-// unless some flag is set (the early-backward recheck's redo).  Each thread
-// loads at most a few flags and the workgroup ORs them in one barrier (a
-// serial loop over 64 flags per thread measured 13 us for a launch that then
-// did nothing); every thread of the workgroup must call it.
-__device__ __forceinline__ bool any_flag(const int* __restrict__ flags, int nflags) {
-  if (flags == nullptr) return true;
-  int v = 0;
-  for (int k = threadIdx.x; k < nflags; k += blockDim.x) v |= flags[k];
-  return __syncthreads_or(v) != 0;
-}
+// `flags` (nflags ints, or null) makes a launch conditional (the early-backward
+// recheck's redo); any_flag above tests them.
 
 __global__ __launch_bounds__(256) void gather_gsum_kernel(const float* __restrict__ g, int64_t R,
                                                          int64_t gsb, int64_t gsr, int64_t gsk,
@@ -649,6 +695,63 @@ void dispatch_gather_fwd(int w, int64_t rows, hipStream_t st, const void* logits
   }
 }
 
+// The flat backward applies when gradient and logits share one contiguous,
+// 16-byte aligned [B, Rt, V] layout with whole vectors per row and the vector
+// count fits 32-bit indexing; fills the launch arguments and the piece count.
+template <class E>
+bool flat_bwd_layout(int64_t rows, const void* logits, int64_t R, int64_t Rt, int64_t V,
+                     int64_t sb, int64_t sr, const int64_t* target, int64_t tsb, int64_t tsr,
+                     int64_t vs, int64_t ve, const float* stats, const float* g, int64_t gsb,
+                     int64_t gsr, void* gin, int64_t gisb, int64_t gisr, FlatBwd* A,
+                     int64_t* npieces) {
+  constexpr int VEC = E::kVec;
+  const uintptr_t ya = reinterpret_cast<uintptr_t>(gin), xa = reinterpret_cast<uintptr_t>(logits);
+  const bool contiguous = gisr == V && (rows == Rt || gisb == Rt * V);
+  const bool shared_layout = R == 0 || (sr == gisr && (rows == Rt || sb == gisb));
+  const int64_t nvr = V / VEC;
+  const int64_t nvec = rows * nvr;
+  if (!(V % VEC == 0 && contiguous && shared_layout && (ya & 15u) == 0 && (xa & 15u) == 0 &&
+        nvec + 512 < (int64_t(1) << 32) && rows < (int64_t(1) << 31)))
+    return false;
+  constexpr int P = kFlatThreads * kFlatVecs;  // vectors per 4 KB piece
+  const int to4k = (int)(((4096u - (ya & 4095u)) & 4095u) / 16u);  // vectors before a 4 KB boundary
+  const int shift = (P - to4k) & (P - 1);
+  *npieces = (nvec + shift + P - 1) / P;
+  *A = FlatBwd{logits, R, (uint32_t)Rt, (uint32_t)nvr, (uint32_t)nvec, shift, target, tsb, tsr,
+               vs, ve, V, stats, g, gsb, gsr, gin};
+  return true;
+}
+
+// Single-wave workgroups of the flat redo's grid-stride launch: two per wave
+// slot of the 256 CUs (32 slots each).
+constexpr int64_t kRedoGrid = 256 * 32 * 2;
+static_assert(kCheckBlocks <= 64, "the flat redo tests at most 64 flags, one per lane");
+
+// Redo of the backward after a failed early-backward check (every launch
+// returns at once when no flag is set): the flat schedule when the layout
+// allows it, row by row otherwise.
+template <class E>
+void dispatch_bwd_redo(int64_t rows, hipStream_t st, const void* logits, int64_t R, int64_t Rt,
+                       int64_t V, int64_t sb, int64_t sr, const int64_t* target, int64_t tsb,
+                       int64_t tsr, int64_t vs, int64_t ve, const float* stats, const float* g,
+                       int64_t gsb, int64_t gsr, void* gin, int64_t gisb, int64_t gisr,
+                       const int* flags, int nflags) {
+  using raw = typename E::raw;
+  FlatBwd A;
+  int64_t npieces = 0;
+  if (flat_bwd_layout<E>(rows, logits, R, Rt, V, sb, sr, target, tsb, tsr, vs, ve, stats, g, gsb,
+                         gsr, gin, gisb, gisr, &A, &npieces)) {
+    const int64_t grid = npieces < kRedoGrid ? npieces : kRedoGrid;
+    hipLaunchKernelGGL((logprob_bwd_flat_redo_kernel<E>), dim3((unsigned)grid), dim3(64), 0, st, A,
+                       npieces, flags, nflags);
+    return;
+  }
+  const unsigned grid = (unsigned)(rows < 1024 ? rows : 1024);
+  hipLaunchKernelGGL((bwd_redo_kernel<E>), dim3(grid), dim3(256), 0, st,
+                     static_cast<const raw*>(logits), R, Rt, V, sb, sr, target, tsb, tsr, vs, ve,
+                     stats, g, gsb, gsr, static_cast<raw*>(gin), gisb, gisr, rows, flags, nflags);
+}
+
 template <class E>
 void dispatch_bwd(int64_t rows, hipStream_t st, const void* logits, int64_t R, int64_t Rt,
                   int64_t V, int64_t sb, int64_t sr, const int64_t* target, int64_t tsb,
@@ -656,25 +759,12 @@ void dispatch_bwd(int64_t rows, hipStream_t st, const void* logits, int64_t R, i
                   int64_t gsb, int64_t gsr, void* gin, int64_t gisb, int64_t gisr) {
   constexpr int W = kBwdWaves, U = 4;
   using raw = typename E::raw;
-  constexpr int VEC = E::kVec;
-  // flat path: gradient and logits share one contiguous, 16-byte aligned
-  // [B, Rt, V] layout with whole vectors per row, and the vector count fits
-  // 32-bit indexing
-  const uintptr_t ya = reinterpret_cast<uintptr_t>(gin), xa = reinterpret_cast<uintptr_t>(logits);
-  const bool contiguous = gisr == V && (rows == Rt || gisb == Rt * V);
-  const bool shared_layout = R == 0 || (sr == gisr && (rows == Rt || sb == gisb));
-  const int64_t nvr = V / VEC;
-  const int64_t nvec = rows * nvr;
-  if (V % VEC == 0 && contiguous && shared_layout && (ya & 15u) == 0 && (xa & 15u) == 0 &&
-      nvec + 512 < (int64_t(1) << 32) && rows < (int64_t(1) << 31)) {
-    constexpr int P = kFlatThreads * kFlatVecs;  // vectors per 4 KB piece
-    const int to4k = (int)(((4096u - (ya & 4095u)) & 4095u) / 16u);  // vectors before a 4 KB boundary
-    const int shift = (P - to4k) & (P - 1);
-    const int64_t grid = (nvec + shift + P - 1) / P;
-    hipLaunchKernelGGL((logprob_bwd_flat_kernel<E>), dim3((unsigned)grid), dim3(kFlatThreads), 0, st,
-                       static_cast<const raw*>(logits), R, (uint32_t)Rt, (uint32_t)nvr,
-                       (uint32_t)nvec, shift, target, tsb, tsr, vs, ve, V, stats, g, gsb, gsr,
-                       static_cast<raw*>(gin));
+  FlatBwd A;
+  int64_t npieces = 0;
+  if (flat_bwd_layout<E>(rows, logits, R, Rt, V, sb, sr, target, tsb, tsr, vs, ve, stats, g, gsb,
+                         gsr, gin, gisb, gisr, &A, &npieces)) {
+    hipLaunchKernelGGL((logprob_bwd_flat_kernel<E>), dim3((unsigned)npieces), dim3(kFlatThreads), 0,
+                       st, A);
     return;
   }
   hipLaunchKernelGGL((logprob_bwd_kernel<E, W, U, kZeroRows>), dim3((unsigned)rows), dim3(64 * W),
@@ -758,11 +848,8 @@ void gather_bwd_recheck(int64_t rows, hipStream_t st, const void* logits, int64_
                      g, R, K, gsb, gsr, gsk, g_used, total, flags);
   hipLaunchKernelGGL(gather_gsum_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, st,
                      g, R, gsb, gsr, gsk, K, rows, gsum, flags, nflags);
-  const unsigned grid = (unsigned)(rows < 1024 ? rows : 1024);
-  hipLaunchKernelGGL((bwd_redo_kernel<E>), dim3(grid), dim3(256), 0, st,
-                     static_cast<const raw*>(logits), R, R, V, sb, sr, idx, isb, isr, (int64_t)0,
-                     (int64_t)0, stats, gsum, R, (int64_t)1, static_cast<raw*>(gin), gisb, gisr,
-                     rows, flags, nflags);
+  dispatch_bwd_redo<E>(rows, st, logits, R, R, V, sb, sr, idx, isb, isr, 0, 0, stats, gsum, R, 1,
+                       gin, gisb, gisr, flags, nflags);
   launch_gather_fixup<E>(rows, st, static_cast<const raw*>(logits), R, V, sb, sr, idx, K, isb, isr,
                          isk, vs, ve, stats, g, gsb, gsr, gsk, gsum, static_cast<raw*>(gin), gisb,
                          gisr, flags, nflags);
@@ -994,29 +1081,15 @@ extern "C" int mirl_logprob_bwd_recheck(const void* logits, int dtype, int64_t B
   const int nflags = (int)(n < kCheckBlocks ? n : kCheckBlocks);
   hipLaunchKernelGGL(bwd_check_kernel, dim3((unsigned)nflags), dim3(256), 0, st, grad_out,
                      g_stride_b, g_stride_r, grad_used, B, R, flag);
-  const unsigned grid = (unsigned)(rows < 1024 ? rows : 1024);
+#define MIRL_REDO(E)                                                                          \
+  dispatch_bwd_redo<E>(rows, st, logits, R, R_total, V, stride_b, stride_r, target, t_stride_b, \
+                       t_stride_r, vocab_start, vocab_end, row_stats, grad_out, g_stride_b,     \
+                       g_stride_r, grad_in, gi_stride_b, gi_stride_r, flag, nflags)
   switch (dtype) {
-    case MIRL_DTYPE_F32:
-      hipLaunchKernelGGL((bwd_redo_kernel<F32>), dim3(grid), dim3(256), 0, st,
-                         static_cast<const float*>(logits), R, R_total, V, stride_b, stride_r,
-                         target, t_stride_b, t_stride_r, vocab_start, vocab_end, row_stats,
-                         grad_out, g_stride_b, g_stride_r, static_cast<float*>(grad_in),
-                         gi_stride_b, gi_stride_r, rows, flag, nflags);
-      break;
-    case MIRL_DTYPE_BF16:
-      hipLaunchKernelGGL((bwd_redo_kernel<BF16>), dim3(grid), dim3(256), 0, st,
-                         static_cast<const uint16_t*>(logits), R, R_total, V, stride_b, stride_r,
-                         target, t_stride_b, t_stride_r, vocab_start, vocab_end, row_stats,
-                         grad_out, g_stride_b, g_stride_r, static_cast<uint16_t*>(grad_in),
-                         gi_stride_b, gi_stride_r, rows, flag, nflags);
-      break;
-    default:
-      hipLaunchKernelGGL((bwd_redo_kernel<F16>), dim3(grid), dim3(256), 0, st,
-                         static_cast<const _Float16*>(logits), R, R_total, V, stride_b, stride_r,
-                         target, t_stride_b, t_stride_r, vocab_start, vocab_end, row_stats,
-                         grad_out, g_stride_b, g_stride_r, static_cast<_Float16*>(grad_in),
-                         gi_stride_b, gi_stride_r, rows, flag, nflags);
-      break;
+    case MIRL_DTYPE_F32: MIRL_REDO(F32); break;
+    case MIRL_DTYPE_BF16: MIRL_REDO(BF16); break;
+    default: MIRL_REDO(F16); break;
   }
+#undef MIRL_REDO
   return check_launch("mirl_logprob_bwd_recheck");
 }

@@ -24,6 +24,7 @@ import numpy as np
 import torch
 
 from rl_amd import _C
+from rl_amd.distributed.early_backward import POLICY, set_early_backward
 from rl_amd.algorithms.logits_sampling_utils import (
     TrainingSamplingParams,
     need_top_k_or_top_p_filtering,
@@ -45,6 +46,7 @@ __all__ = [
     "from_parallel_logits_to_logprobs_packed_sequences",
     "get_next_token_logprobs_from_logits",
     "get_policy_logprobs_at_sampler_topk",
+    "set_early_backward",
 ]
 
 _VOCAB_REDUCTIONS = (
@@ -152,7 +154,8 @@ class _RowLogprob(torch.autograd.Function):
             # launched by launch_early_backward: check it against the real gradient
             ctx.early = None
             grad_input, grad_used = early
-            _C.logprob_bwd_recheck(logits, target, vs, ve, stats, grad_output, grad_used, grad_input)
+            POLICY.checked(
+                _C.logprob_bwd_recheck(logits, target, vs, ve, stats, grad_output, grad_used, grad_input))
             return grad_input, None, None, None, None, None
         reuse = ctx.reuse_logits_storage and not logits.is_leaf
         grad_input = logits if reuse else torch.empty_like(logits)
@@ -172,6 +175,8 @@ def launch_early_backward_pair(
     if node is None or getattr(plog, "_mirl_gather_node", None) is not node:
         return False
     if getattr(node, "early", None) is not None:
+        return False
+    if not POLICY.should_launch():
         return False
     if grad_curr.dtype != torch.float32 or grad_plog.dtype != torch.float32:
         return False
@@ -204,7 +209,8 @@ def launch_early_backward(logprobs: torch.Tensor, grad: torch.Tensor) -> bool:
     second consumer of the logprobs), so results never depend on the guess.
     Applies to logprobs produced directly by this module's row kernel and to
     their unpacking from packed sequences; returns whether the backward was
-    started.
+    started.  set_early_backward chooses when it is (by default it is not
+    started again for a while after a check found a different gradient).
     """
     fn = logprobs.grad_fn
     if grad.dtype != torch.float32 or tuple(grad.shape) != tuple(logprobs.shape):
@@ -225,6 +231,8 @@ def _launch_early_on_node(fn: Any, grad: torch.Tensor) -> bool:
     if not isinstance(fn, _RowLogprob._backward_cls):
         return False
     if getattr(fn, "early", None) is not None or getattr(fn, "reuse_logits_storage", True):
+        return False
+    if not POLICY.should_launch():
         return False
     logits, target, stats = fn.saved_tensors
     if tuple(grad.shape) != tuple(target.shape):

@@ -23,6 +23,7 @@ from typing import Any, Optional
 import torch
 
 from rl_amd import _C
+from rl_amd.distributed.early_backward import POLICY
 
 __all__ = [
     "ChunkedDistributedCrossEntropyToFixedLogits",
@@ -106,7 +107,8 @@ class ChunkedDistributedGatherLogprob(torch.autograd.Function):
             # launched by launch_early_backward: check it against the real gradient
             ctx.early = None
             grad_input, grad_used = early
-            _C.gather_logprob_bwd_recheck(logits, idx, vs, ve, stats, grad_output, grad_used, grad_input)
+            POLICY.checked(
+                _C.gather_logprob_bwd_recheck(logits, idx, vs, ve, stats, grad_output, grad_used, grad_input))
             return grad_input, None, None, None, None, None, None
         grad_input = torch.empty_like(logits)
         _C.gather_logprob_bwd(logits, idx, vs, ve, stats, grad_output, grad_input)

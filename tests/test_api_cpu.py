@@ -169,3 +169,39 @@ def test_loss_out_is_checked_before_any_launch():
     with pytest.raises(_C.MirlError, match="loss_out must be one contiguous"):
         _C.clipped_pg(cfg, t, None, t, t, t, t, t, None, torch.ones(2), None, torch.tensor(2.0),
                       torch.tensor(6.0), loss_out=torch.zeros(2))
+
+
+def test_early_backward_policy_logic(monkeypatch):
+    """The adaptive early-backward policy on the host: a read miss skips retry_after
+    opportunities; an unread check (copy in flight) does not block speculation."""
+    from rl_amd.distributed import early_backward as eb
+
+    results = {}
+
+    def fake_start(flags):
+        return ["h", flags]
+
+    def fake_poll(handle):
+        return results.get("ready")
+
+    monkeypatch.setattr(eb._C, "start_fetch", fake_start)
+    monkeypatch.setattr(eb._C, "poll_fetch", fake_poll)
+    pol = eb.EarlyBackwardPolicy("adaptive", retry_after=3)
+    assert pol.should_launch()
+    pol.checked([1])
+    results["ready"] = None  # copy still in flight: keep speculating
+    assert pol.should_launch() and pol.pending is not None
+    results["ready"] = [0, 1]
+    assert [pol.should_launch() for _ in range(5)] == [False, False, False, True, True]
+    assert pol.misses == 1 and pol.skipped == 3
+    pol.checked([0])
+    results["ready"] = [0, 0]
+    assert pol.should_launch() and pol.misses == 1
+    pol.configure("always")
+    assert pol.should_launch()
+    pol.configure("never")
+    assert not pol.should_launch()
+    with pytest.raises(ValueError):
+        pol.configure("sometimes")
+    with pytest.raises(ValueError):
+        pol.configure("adaptive", retry_after=-1)

@@ -14,10 +14,19 @@ import torch
 
 from rl_amd import workloads
 from rl_amd.algorithms.loss import ClippedPGLossConfig, ClippedPGLossFn
+from rl_amd.distributed.early_backward import POLICY, set_early_backward
 from rl_amd.distributed.model_utils import from_parallel_logits_to_logprobs
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda", 0)
+
+
+@pytest.fixture(autouse=True)
+def _speculate_always():
+    """These cases test the device-side check, so every eligible call speculates."""
+    set_early_backward("always")
+    yield
+    set_early_backward("adaptive")
 
 
 def say(*a):
@@ -220,3 +229,39 @@ def test_score_centering_gather_early_backward(case):
     assert started and not started0
     assert g0.abs().sum() > 0
     assert torch.equal(g1, g0)
+
+
+def test_adaptive_policy_skips_after_miss():
+    """Adaptive mode: a scaled loss makes the check miss; once the flags have reached the host
+    the next retry_after eligible calls run the plain backward, then speculation resumes.
+    Gradients are exact throughout."""
+    say("early backward: adaptive policy")
+    set_early_backward("adaptive", retry_after=2)
+    d, gvs, gvt = _setup(8)
+    g_ref, _ = _grad(d, gvs, gvt, early=False, scale=0.5)
+    seen = []
+    for _ in range(4):
+        g, started = _grad(d, gvs, gvt, early=True, scale=0.5)
+        torch.cuda.synchronize()  # the check's flags reach the host before the next decision
+        seen.append(started)
+        assert torch.equal(g, g_ref)
+    assert seen == [True, False, False, True]
+    POLICY._drain()  # read the last check too
+    assert POLICY.misses == 2 and POLICY.skipped == 2
+    # an unscaled loss: every check agrees, every call speculates
+    set_early_backward("adaptive", retry_after=2)
+    g_ref, _ = _grad(d, gvs, gvt, early=False)
+    for _ in range(3):
+        g, started = _grad(d, gvs, gvt, early=True)
+        torch.cuda.synchronize()
+        assert started and torch.equal(g, g_ref)
+    assert POLICY.misses == 0
+
+
+def test_never_mode_runs_plain_backward():
+    say("early backward: never")
+    set_early_backward("never")
+    d, gvs, gvt = _setup(8)
+    g_ref, _ = _grad(d, gvs, gvt, early=False)
+    g, started = _grad(d, gvs, gvt, early=True)
+    assert not started and torch.equal(g, g_ref)
