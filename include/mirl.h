@@ -191,14 +191,17 @@ int mirl_gather_logprob_bwd_recheck(const void* logits, int dtype, int64_t B, in
 int64_t mirl_vocab_topk_workspace_bytes(int64_t rows);
 
 /*
- * The k largest logits of each row and their global ids (1 <= k <= min(1024, V)):
+ * The k largest logits of each row and their global ids (1 <= k <= V):
  *   values[b,r,i]  = the (i+1)-th largest x[b,r,:] (as fp32, exact),
  *   indices[b,r,i] = vocab_start + its position; equal values are ordered by
  *                    ascending position (the lower id first);
  * both contiguous [B, R, k].  NaN sorts above every number, -0.0 ties +0.0.
- * One streaming pass per row; rows with more than 1024 candidates at or above
- * the k-th largest lane maximum (many equal values) are redone by an exact
- * radix selection.  `workspace` holds mirl_vocab_topk_workspace_bytes(B*R).
+ * For k <= 1024 one streaming pass per row; rows with more than 1024
+ * candidates at or above the k-th largest lane maximum (many equal values) are
+ * redone by an exact radix selection.  Larger k take the exact radix selection
+ * of the cut, then a sort of the k entries inside the kernel (in LDS up to
+ * 16384 entries, else in the `indices` row itself).  `workspace` holds
+ * mirl_vocab_topk_workspace_bytes(B*R).
  *
  * Replaces: distributed_vocab_topk (nemo_rl/distributed/model_utils.py:1867-1935)
  * with a vocab group of size 1 (torch.topk of the fp32 logits + the vocab offset).
@@ -706,6 +709,38 @@ int mirl_unpack_rows_fwd(const float* packed, int64_t n_rows, const int64_t* bou
 int mirl_unpack_rows_bwd(const float* grad_out, int64_t n_seq, int64_t cols,
                          const int64_t* bounds, int64_t n_rows, float* grad_packed,
                          void* stream);
+
+/* ---------------------------------------------------------------------- */
+/* token-level post-processing of logprobs                                  */
+/* ---------------------------------------------------------------------- */
+
+/*
+ * out[b, s] = mask[b, s] != 0 ? logprobs[b, s] : 0 over [B, S] fp32 views with
+ * element strides (a stride of 0 broadcasts); out may alias logprobs.
+ *
+ * Replaces: mask_filtered_logprobs_outside_tokens
+ * (nemo_rl/algorithms/utils.py:309-326), applied after the filtered logprobs
+ * by the Megatron logprob post-processor (nemo_rl/models/megatron/train.py:960-964).
+ */
+int mirl_mask_outside_tokens(const float* logprobs, int64_t B, int64_t S, int64_t lp_sb,
+                             int64_t lp_ss, const float* mask, int64_t m_sb, int64_t m_ss,
+                             float* out, int64_t o_sb, int64_t o_ss, void* stream);
+
+/*
+ * Per sequence b of [B, S] fp32 views (element strides), w_s = token_mask[b, s]
+ * * sample_mask[b]:
+ *   errors[b] = sum_s exp(e_s * w_s) * w_s / max(sum_s w_s, 1),
+ *   e_s = w_s != 0 ? |generation[b, s] - policy[b, s]| : 0,
+ *   valid[b]  = sum_s w_s > 0 (uint8).
+ * A non-finite logprob on a valid token makes errors[b] non-finite.
+ *
+ * Replaces: compute_seq_logprob_errors (nemo_rl/algorithms/utils.py:273-291).
+ */
+int mirl_seq_logprob_errors(const float* policy, int64_t p_sb, int64_t p_ss,
+                            const float* generation, int64_t g_sb, int64_t g_ss,
+                            const float* token_mask, int64_t t_sb, int64_t t_ss,
+                            const float* sample_mask, int64_t s_sb, int64_t B, int64_t S,
+                            float* errors, uint8_t* valid, void* stream);
 
 #ifdef __cplusplus
 }

@@ -228,6 +228,10 @@ SIGNATURES = {
         [_P, _I64, _I64, _I64, ctypes.c_int32, _P, _P, _I64, _P, _I64, _P],
     ),
     "mirl_packed_roll_targets": (_I, [_P, _I64, _P, _I64, _P, _P]),
+    "mirl_mask_outside_tokens": (_I, [_P, _I64, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P]),
+    "mirl_seq_logprob_errors": (
+        _I, [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _I64, _P, _P, _P]
+    ),
     "mirl_unpack_rows_fwd": (_I, [_P, _I64, _P, _I64, _I64, _P, _P]),
     "mirl_unpack_rows_bwd": (_I, [_P, _I64, _I64, _P, _I64, _P, _P]),
 }
@@ -1171,3 +1175,55 @@ def linear_ce_grad(
         _stream(dev),
     )
     _check(st, "mirl_linear_ce_grad")
+
+
+# ---------------------------------------------------------------------------
+# token-level post-processing of logprobs
+# ---------------------------------------------------------------------------
+def _as_f32(t: torch.Tensor) -> torch.Tensor:
+    return t if t.dtype == torch.float32 else t.to(torch.float32)
+
+
+def mask_outside_tokens(logprobs: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
+    """where(mask != 0, logprobs, 0) for [B, S] (or [S]) fp32 logprobs and a mask that
+    broadcasts to them; returns a new fp32 tensor."""
+    dev = _require_gpu(logprobs, mask)
+    _require(logprobs.dtype == torch.float32, "logprobs.dtype == torch.float32")
+    _require(logprobs.dim() in (1, 2), "logprobs of shape [B, S] or [S]")
+    lp = logprobs if logprobs.dim() == 2 else logprobs.unsqueeze(0)
+    m = _as_f32(mask)
+    m = m if m.dim() == 2 else m.reshape((1,) * (2 - m.dim()) + tuple(m.shape))
+    m = m.expand(lp.shape)
+    out = torch.empty(lp.shape, dtype=torch.float32, device=dev)
+    B, S = lp.shape
+    st = _launch(
+        "mirl_mask_outside_tokens", dev, lp.data_ptr(), B, S, lp.stride(0), lp.stride(1),
+        m.data_ptr(), m.stride(0), m.stride(1), out.data_ptr(), out.stride(0), out.stride(1),
+        _stream(dev),
+    )
+    _check(st, "mirl_mask_outside_tokens")
+    return out if logprobs.dim() == 2 else out[0]
+
+
+def seq_logprob_errors(policy: torch.Tensor, generation: torch.Tensor, token_mask: torch.Tensor,
+                       sample_mask: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """(errors fp32 [B], valid bool [B]) of the mean multiplicative logprob error per sequence."""
+    dev = _require_gpu(policy, generation, token_mask, sample_mask)
+    _require(policy.dim() == 2 and tuple(generation.shape) == tuple(policy.shape),
+             "policy and generation logprobs of one [B, S] shape")
+    B, S = policy.shape
+    _require(policy.dtype == torch.float32 and generation.dtype == torch.float32,
+             "policy.dtype == generation.dtype == torch.float32")
+    tm = _as_f32(token_mask).expand(B, S)
+    sm = _as_f32(sample_mask)
+    _require(sm.dim() == 1 and sm.shape[0] == B, "sample_mask of shape [B]")
+    errors = torch.empty(B, dtype=torch.float32, device=dev)
+    valid = torch.empty(B, dtype=torch.bool, device=dev)
+    st = _launch(
+        "mirl_seq_logprob_errors", dev, policy.data_ptr(), policy.stride(0), policy.stride(1),
+        generation.data_ptr(), generation.stride(0), generation.stride(1), tm.data_ptr(),
+        tm.stride(0), tm.stride(1), sm.data_ptr(), sm.stride(0), B, S, errors.data_ptr(),
+        valid.data_ptr(), _stream(dev),
+    )
+    _check(st, "mirl_seq_logprob_errors")
+    return errors, valid

@@ -4,7 +4,8 @@
 formulas (reference utils.py:56-115, :294-306), kept as plain tensor code for
 callers that use them directly; ``ClippedPGLossFn`` does not call them — its
 kernel fuses the same arithmetic.  ``calculate_baseline_and_std_per_prompt``
-runs the GRPO group-statistics kernel.
+runs the GRPO group-statistics kernel.  ``mask_filtered_logprobs_outside_tokens``
+and ``compute_seq_logprob_errors`` run token-level kernels (seq_errors.hip).
 """
 
 from __future__ import annotations
@@ -61,6 +62,37 @@ def masked_mean(
         torch.sum(mask, dim=dim) if global_normalization_factor is None else global_normalization_factor
     )
     return torch.sum(values * mask, dim=dim) / (normalization_factor + 1e-8)
+
+
+def mask_filtered_logprobs_outside_tokens(logprobs: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
+    """Zero filtered logprobs outside ``mask`` (reference utils.py:309-326).
+
+    ``where(mask.bool(), logprobs, 0.0)``: tokens outside the valid-token mask
+    (prompt, padding) get 0 instead of the -inf the filter may have given them;
+    valid tokens keep -inf.  Returns a new tensor of ``logprobs``' dtype (16-bit
+    logprobs are widened to fp32 for the kernel and narrowed back, exactly).
+    """
+    out = _C.mask_outside_tokens(logprobs.to(torch.float32), mask)
+    return out if logprobs.dtype == torch.float32 else out.to(logprobs.dtype)
+
+
+@torch.no_grad()
+def compute_seq_logprob_errors(
+    *,
+    policy_logprobs: torch.Tensor,
+    generation_logprobs: torch.Tensor,
+    token_mask: torch.Tensor,
+    sample_mask: torch.Tensor,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Mean multiplicative absolute logprob error and validity per sequence (reference utils.py:273-291).
+
+    Inputs are aligned to predicted tokens; with ``w = token_mask * sample_mask[:, None]``,
+    ``errors = sum(exp(|gen - pol| * w) * w) / max(sum(w), 1)`` over masked-in tokens and
+    ``valid = sum(w) > 0``.  A non-finite logprob on a valid token makes its sequence's error
+    non-finite.  Logprobs are computed on in fp32 (others are widened first).
+    """
+    return _C.seq_logprob_errors(policy_logprobs.to(torch.float32), generation_logprobs.to(torch.float32),
+                                 token_mask, sample_mask)
 
 
 def _to_device_inputs(prompts, rewards, valid_mask):

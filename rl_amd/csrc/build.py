@@ -30,6 +30,7 @@ SOURCES = [
     "divergence.hip",
     "packing.hip",
     "temperature.hip",
+    "seq_errors.hip",
 ]
 
 ARCH = "gfx950"

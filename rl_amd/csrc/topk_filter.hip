@@ -255,28 +255,17 @@ __device__ uint32_t radix_kth_key(Y&& yat, int64_t V, int k, int* hist_i, uint32
   return prefix;
 }
 
-// General top-k export for the rows the fast path flagged (candidate
-// overflow, i.e. many equal values): the k-th largest value by radix
-// selection, then among the elements equal to it the `remaining` lowest
-// indices (radix selection on the index bits), then exactly k entries
-// collected and rank-sorted.
-template <class E>
-__global__ __launch_bounds__(kGeneralThreads) void topk_export_general_kernel(FilterParams P) {
-  using raw = typename E::raw;
-  constexpr int NT = kGeneralThreads;
-  __shared__ int hist_i[256];
-  __shared__ uint32_t s_sel[2];
-  __shared__ int s_cnt;
-  __shared__ uint64_t s_cand[kCandCap];
-  const int64_t row = blockIdx.x;
-  if ((P.info[row].flags & 1) == 0) return;
-  const int64_t b = row / P.R, r = row - b * P.R;
-  const raw* x = static_cast<const raw*>(P.logits) + b * P.sb + r * P.sr;
+// The export's exact cut for k: the k-th largest order key thr (radix
+// selection over the value bits) and i_last, the index of the last element
+// equal to thr that belongs to the top k (the `remaining`-th smallest index
+// among them, by radix selection over the index bits).  The top k are then the
+// elements with key > thr, or key == thr and index <= i_last.
+template <int NT, class Y>
+__device__ void export_cut(Y&& yat, int64_t V, int k, int* hist_i, uint32_t* s_sel, uint32_t* thr_out,
+                           uint32_t* i_last_out) {
   const int tid = threadIdx.x;
-  const int64_t V = P.V;
-  auto yat = [&](int64_t j) { return E::load(x + j); };
   int remaining = 0;
-  const uint32_t thr = radix_kth_key<NT>(yat, V, P.top_k, hist_i, s_sel, &remaining, true);
+  const uint32_t thr = radix_kth_key<NT>(yat, V, k, hist_i, s_sel, &remaining, true);
 
   // the remaining-th smallest index among the elements whose key equals thr
   int top_bit = 0;
@@ -314,7 +303,30 @@ __global__ __launch_bounds__(kGeneralThreads) void topk_export_general_kernel(Fi
     need = (int)s_sel[1];
     __syncthreads();
   }
-  const uint32_t i_last = iprefix;
+  *thr_out = thr;
+  *i_last_out = iprefix;
+}
+
+// General top-k export for the rows the fast path flagged (candidate
+// overflow, i.e. many equal values): the exact cut, then exactly k entries
+// collected and rank-sorted.
+template <class E>
+__global__ __launch_bounds__(kGeneralThreads) void topk_export_general_kernel(FilterParams P) {
+  using raw = typename E::raw;
+  constexpr int NT = kGeneralThreads;
+  __shared__ int hist_i[256];
+  __shared__ uint32_t s_sel[2];
+  __shared__ int s_cnt;
+  __shared__ uint64_t s_cand[kCandCap];
+  const int64_t row = blockIdx.x;
+  if ((P.info[row].flags & 1) == 0) return;
+  const int64_t b = row / P.R, r = row - b * P.R;
+  const raw* x = static_cast<const raw*>(P.logits) + b * P.sb + r * P.sr;
+  const int tid = threadIdx.x;
+  const int64_t V = P.V;
+  auto yat = [&](int64_t j) { return E::load(x + j); };
+  uint32_t thr, i_last;
+  export_cut<NT>(yat, V, P.top_k, hist_i, s_sel, &thr, &i_last);
 
   if (tid == 0) s_cnt = 0;
   __syncthreads();
@@ -328,6 +340,97 @@ __global__ __launch_bounds__(kGeneralThreads) void topk_export_general_kernel(Fi
   __syncthreads();
   block_rank_sort<NT>(s_cand, P.top_k);
   export_topk<E>(P, row, x, s_cand);
+}
+
+// Descending sort of n 64-bit keys at `a` (LDS or global memory) by the whole
+// workgroup: a bitonic network in which every merge compares in the same
+// direction (the first step of each merge pairs i with its mirror in the
+// block), so positions >= n act as keys below every real one and are never
+// touched, for any n.  Every thread must enter it.
+template <int NT>
+__device__ void bitonic_sort_desc(uint64_t* a, int64_t n) {
+  int64_t N = 1;
+  while (N < n) N <<= 1;
+  for (int64_t blk = 2; blk <= N; blk <<= 1) {
+    // mirror step: i in the lower half of its block against blk - 1 - (i mod blk)
+    for (int64_t t = threadIdx.x; t < N / 2; t += NT) {
+      const int64_t base = (t / (blk / 2)) * blk, off = t % (blk / 2);
+      const int64_t i = base + off, l = base + blk - 1 - off;
+      if (l < n) {
+        const uint64_t u = a[i], v = a[l];
+        if (u < v) {
+          a[i] = v;
+          a[l] = u;
+        }
+      }
+    }
+    __syncthreads();
+    for (int64_t j = blk / 4; j >= 1; j >>= 1) {
+      for (int64_t t = threadIdx.x; t < N / 2; t += NT) {
+        const int64_t i = (t / j) * 2 * j + (t % j), l = i + j;
+        if (l < n) {
+          const uint64_t u = a[i], v = a[l];
+          if (u < v) {
+            a[i] = v;
+            a[l] = u;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// Rows held in LDS by the large-k export's sort (16384 keys, 128 KB); larger
+// k sort in place in the row's own index output.
+constexpr int kExportLdsKeys = 16384;
+
+// Top-k export for k > kCandCap: the exact cut, the k entries collected as
+// sort keys (order key << 32 | ~index: larger = higher value, then lower id)
+// and sorted descending, then written out with their values re-read.
+template <class E>
+__global__ __launch_bounds__(kGeneralThreads) void topk_export_large_kernel(FilterParams P) {
+  using raw = typename E::raw;
+  constexpr int NT = kGeneralThreads;
+  __shared__ int hist_i[256];
+  __shared__ uint32_t s_sel[2];
+  __shared__ int s_cnt;
+  __shared__ uint64_t s_keys[kExportLdsKeys];
+  const int64_t row = blockIdx.x;
+  const int64_t b = row / P.R, r = row - b * P.R;
+  const raw* x = static_cast<const raw*>(P.logits) + b * P.sb + r * P.sr;
+  const int tid = threadIdx.x;
+  const int64_t V = P.V;
+  const int k = P.top_k;
+  auto yat = [&](int64_t j) { return E::load(x + j); };
+  uint32_t thr, i_last;
+  export_cut<NT>(yat, V, k, hist_i, s_sel, &thr, &i_last);
+  uint64_t* keys = k <= kExportLdsKeys ? s_keys
+                                       : reinterpret_cast<uint64_t*>(P.tk_idx + row * (int64_t)k);
+  if (tid == 0) s_cnt = 0;
+  __syncthreads();
+  for (int64_t j = tid; j < V; j += NT) {
+    const uint32_t kk = okey_export(yat(j));
+    if (kk > thr || (kk == thr && (uint32_t)j <= i_last)) {
+      const int slot = atomicAdd(&s_cnt, 1);
+      if (slot < k) keys[slot] = ((uint64_t)kk << 32) | (uint64_t)(~(uint32_t)j);
+    }
+  }
+  __syncthreads();
+  bitonic_sort_desc<NT>(keys, k);
+  // each thread reads its keys before any output is written over them
+  for (int64_t i0 = 0; i0 < k; i0 += NT) {
+    const int64_t i = i0 + tid;
+    uint64_t key = 0;
+    if (i < k) key = keys[i];
+    __syncthreads();
+    if (i < k) {
+      const int64_t j = (int64_t)(~(uint32_t)(key & 0xffffffffu));
+      P.tk_vals[row * k + i] = E::load(x + j);
+      P.tk_idx[row * k + i] = P.tk_base + j;
+    }
+    __syncthreads();
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -932,6 +1035,11 @@ int launch_fwd(const FilterParams& P, int64_t rows, hipStream_t st) {
 
 template <class E>
 int launch_topk_export(const FilterParams& P, int64_t rows, hipStream_t st) {
+  if (P.top_k > kCandCap) {
+    hipLaunchKernelGGL((topk_export_large_kernel<E>), dim3((unsigned)rows), dim3(kGeneralThreads), 0,
+                       st, P);
+    return check_launch("topk_export_large_kernel");
+  }
   switch (fast_waves(P.top_k)) {
     case 8:
       hipLaunchKernelGGL((filter_fast_kernel<E, 8, 4, true>), dim3((unsigned)rows), dim3(512), 0, st, P);
@@ -1168,8 +1276,7 @@ extern "C" int mirl_vocab_topk(const void* logits, int dtype, int64_t B, int64_t
   MIRL_REQUIRE(B >= 0 && R >= 0 && V > 0, "invalid shape B=%lld R=%lld V=%lld", (long long)B,
                (long long)R, (long long)V);
   MIRL_REQUIRE(V < (int64_t(1) << 31), "vocabulary size %lld exceeds 2^31-1", (long long)V);
-  MIRL_REQUIRE(k >= 1 && k <= kCandCap && k <= V, "k=%d must be in [1, min(%d, V=%lld)]", k,
-               kCandCap, (long long)V);
+  MIRL_REQUIRE(k >= 1 && k <= V, "k=%d must be in [1, V=%lld]", k, (long long)V);
   const int64_t rows = B * R;
   if (rows == 0) return MIRL_OK;
   MIRL_REQUIRE(rows < (int64_t(1) << 31), "too many rows (%lld)", (long long)rows);

@@ -242,10 +242,11 @@ def distributed_vocab_topk(
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """Top-k values ``[B, S, k]`` (fp32) and global token ids ``[B, S, k]`` (reference model_utils.py:1867-1935).
 
-    One streaming kernel pass per row (group of size 1: no candidate exchange).
-    Values are the exact logits, descending; equal values are ordered by
-    ascending id.  ``k`` is clamped to the vocabulary size as in the reference;
-    values of ``k`` above 1024 raise ``NotImplementedError``.
+    One streaming kernel pass per row for k <= 1024 (group of size 1: no
+    candidate exchange); larger k select the exact cut by radix selection and
+    sort the k entries in the kernel.  Values are the exact logits, descending;
+    equal values are ordered by ascending id.  ``k`` is clamped to the
+    vocabulary size as in the reference.
     """
     assert vocab_end_index > vocab_start_index
     _single_rank(tp_group)
@@ -255,8 +256,6 @@ def distributed_vocab_topk(
         raise ValueError(f"expected logits of shape [B, S, V_local], got {tuple(logits.shape)}")
     V = logits.shape[-1]
     k_eff = int(min(k, max(1, V)))
-    if k_eff > 1024:
-        raise NotImplementedError(f"top-k export supports k <= 1024, got {k_eff}")
     return _C.vocab_topk(logits, k_eff, int(vocab_start_index))
 
 

@@ -1,0 +1,94 @@
+"""mask_filtered_logprobs_outside_tokens and compute_seq_logprob_errors on the device
+against the CPU oracle (GPU).
+
+Masking is exact (a select); sequence errors agree to 2e-6 relative (fp32 sums in
+different orders), validity and non-finite patterns exactly.
+"""
+
+import pytest
+import torch
+
+from oracle.token_metrics import mask_outside_tokens, seq_logprob_errors
+from rl_amd.algorithms.utils import compute_seq_logprob_errors, mask_filtered_logprobs_outside_tokens
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda", 0)
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+
+
+@pytest.mark.parametrize("B,S", [(8, 2047), (1, 1), (3, 300), (0, 5)])
+@pytest.mark.parametrize("mask_kind", ["float", "bool", "row"])
+def test_mask_outside_tokens(B, S, mask_kind):
+    say("mask outside", B, S, mask_kind)
+    g = torch.Generator().manual_seed(B * 7 + S)
+    lp = -torch.rand(B, S, generator=g) * 5
+    lp[torch.rand(B, S, generator=g) < 0.2] = -float("inf")
+    if mask_kind == "row":
+        mask = (torch.rand(S, generator=g) < 0.6).float()
+    else:
+        mask = (torch.rand(B, S, generator=g) < 0.6).float()
+        if mask_kind == "bool":
+            mask = mask.bool()
+    want = mask_outside_tokens(lp, mask)
+    got = mask_filtered_logprobs_outside_tokens(lp.to(DEV), mask.to(DEV))
+    assert got.dtype == torch.float32 and got.shape == want.shape
+    assert torch.equal(got.cpu(), want)
+
+
+def test_mask_outside_tokens_strided_and_16bit():
+    say("mask outside strided / bf16")
+    g = torch.Generator().manual_seed(3)
+    base = -torch.rand(4, 2, 100, generator=g)
+    lp = base[:, 1, :]  # row stride 200
+    mask = torch.rand(4, 100, generator=g) < 0.5
+    got = mask_filtered_logprobs_outside_tokens(lp.to(DEV), mask.to(DEV))
+    assert torch.equal(got.cpu(), torch.where(mask, lp, 0.0))
+    lp16 = lp.bfloat16()
+    got16 = mask_filtered_logprobs_outside_tokens(lp16.to(DEV), mask.to(DEV))
+    assert got16.dtype == torch.bfloat16 and torch.equal(got16.cpu(), torch.where(mask, lp16, 0.0))
+
+
+@pytest.mark.parametrize("B,S", [(64, 2047), (5, 1), (3, 4097), (0, 3)])
+def test_seq_logprob_errors(B, S):
+    say("seq errors", B, S)
+    g = torch.Generator().manual_seed(B + S)
+    pol = -torch.rand(B, S, generator=g) * 4
+    gen = pol + 0.05 * torch.randn(B, S, generator=g)
+    tm = (torch.rand(B, S, generator=g) < 0.7).float()
+    sm = (torch.rand(B, generator=g) < 0.8).float()
+    if B > 2:
+        tm[1] = 0.0          # a sequence with no valid token
+        pol[2, 0] = float("nan")
+        tm[2, 0] = 0.0       # NaN on a masked token: ignored
+    if B > 4:
+        gen[4, S // 2] = -float("inf")
+        tm[4, S // 2] = 1.0
+        sm[4] = 1.0          # -inf on a valid token: the error is inf
+    want_e, want_v = seq_logprob_errors(pol, gen, tm, sm)
+    got_e, got_v = compute_seq_logprob_errors(policy_logprobs=pol.to(DEV), generation_logprobs=gen.to(DEV),
+                                              token_mask=tm.to(DEV), sample_mask=sm.to(DEV))
+    assert got_v.dtype == torch.bool and torch.equal(got_v.cpu(), want_v)
+    torch.testing.assert_close(got_e.cpu(), want_e, rtol=2e-6, atol=0, equal_nan=True)
+    # the reference's own expression on the device agrees too
+    mask = tm * sm.unsqueeze(-1)
+    counts = mask.sum(-1)
+    err = torch.where(mask.bool(), (gen - pol).abs(), 0.0)
+    ref = (torch.exp(err * mask) * mask).sum(-1) / counts.clamp(min=1)
+    torch.testing.assert_close(got_e.cpu(), ref, rtol=2e-6, atol=0, equal_nan=True)
+
+
+def test_seq_logprob_errors_bool_masks_and_strides():
+    say("seq errors bool masks")
+    g = torch.Generator().manual_seed(11)
+    pol = -torch.rand(6, 2, 50, generator=g)[:, 0]
+    gen = -torch.rand(6, 50, generator=g)
+    tm = torch.rand(6, 50, generator=g) < 0.5
+    sm = torch.tensor([True, False, True, True, False, True])
+    want_e, want_v = seq_logprob_errors(pol, gen, tm, sm)
+    got_e, got_v = compute_seq_logprob_errors(policy_logprobs=pol.to(DEV), generation_logprobs=gen.to(DEV),
+                                              token_mask=tm.to(DEV), sample_mask=sm.to(DEV))
+    assert torch.equal(got_v.cpu(), want_v)
+    torch.testing.assert_close(got_e.cpu(), want_e, rtol=2e-6, atol=0)

@@ -78,3 +78,36 @@ def test_strided_logits_and_k_clamped_to_vocab():
     assert torch.equal(vals.cpu(), ev) and torch.equal(idx.cpu(), ei)
     vals, idx = _run(x[:, :, :10].contiguous(), 50)  # k > V: the reference clamps to V
     assert vals.shape[-1] == 10
+
+
+@pytest.mark.parametrize("dtype,V,k,R", [(torch.bfloat16, 151936, 2000, 3), (torch.float32, 32000, 1025, 4),
+                                         (torch.float16, 50000, 16384, 2), (torch.bfloat16, 40000, 20000, 2),
+                                         (torch.bfloat16, 3001, 3001, 3), (torch.float32, 70000, 16385, 1)])
+def test_large_k_exact(dtype, V, k, R):
+    """k > 1024: the exact cut by radix selection and an in-kernel sort (LDS up to 16384
+    entries, the row's index output beyond), against the oracle's stable sort."""
+    say("large k", dtype, V, k)
+    g = torch.Generator().manual_seed(V + k + 1)
+    x = (torch.randn(2, R, V, generator=g) * 2).to(dtype)
+    x[0, 0, ::3] = 1.0  # many ties inside the top k
+    vals, idx = _run(x, k, vs=11)
+    ev, ei = vocab_topk(x, k, vocab_start=11)
+    assert torch.equal(idx.cpu(), ei)
+    assert torch.equal(vals.cpu(), ev)
+
+
+def test_large_k_ties_and_nan():
+    say("large k ties / nan")
+    g = torch.Generator().manual_seed(21)
+    V = 20000
+    x = torch.randn(2, 2, V, generator=g).bfloat16()
+    x[0, 0] = 0.0
+    x[0, 1] = torch.randint(0, 3, (V,), generator=g).bfloat16()
+    x[1, 0, 7] = float("nan")
+    x[1, 0, 9] = -0.0
+    x[1, 1, ::5] = 4.0
+    for k in (1500, 5000, 17000):
+        vals, idx = _run(x, k)
+        ev, ei = vocab_topk(x, k)
+        assert torch.equal(idx.cpu(), ei), k
+        torch.testing.assert_close(vals.cpu(), ev, rtol=0, atol=0, equal_nan=True)
