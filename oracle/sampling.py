@@ -128,3 +128,43 @@ def next_token_filtered(logits_raw, input_ids, top_k, top_p, temperature=1.0, gr
     if grad_output is not None:
         (grad,) = torch.autograd.grad(lp, [x], grad_output)
     return lp.detach(), keep, grad
+
+
+def top_k_top_p_candidates(logits: torch.Tensor, top_k: int, top_p: float, z_ulps: int = 0):
+    """Keep masks of ``top_k_top_p(logits, top_k, top_p, exact_normaliser=True)`` for fp32
+    rows, evaluated on the top-k candidates only, plus per-row statistics of the cut.
+
+    After the top-k mask every other entry of the sorted row is -inf: it adds an exact zero
+    to the normaliser and to the ascending cumulative sum, so the row reduces to its
+    candidates (every value >= the k-th largest, ties included) in (value, index) order.
+    ``z_ulps`` moves the normaliser by that many fp32 ulps (the sensitivity of the cut to
+    the normaliser's rounding).  Returns (keep [R, V] bool, stats dict of [R] tensors:
+    n_kept, group (elements equal to the smallest kept value), kept_in_group)."""
+    x = logits.reshape(-1, logits.shape[-1]).float()
+    R, V = x.shape
+    kth = torch.topk(x, top_k, dim=-1).values[:, -1:]
+    cand = x >= kth
+    L = int(cand.sum(-1).max())
+    vals, idx = torch.topk(x, L, dim=-1)
+    # (value, index) ascending: sort by index, then stably by value
+    o = idx.argsort(dim=-1)
+    vals, idx = vals.gather(-1, o), idx.gather(-1, o)
+    o = vals.argsort(dim=-1, stable=True)
+    vals, idx = vals.gather(-1, o), idx.gather(-1, o)
+    real = vals >= kth
+    v = vals.masked_fill(~real, -float("inf"))
+    e = torch.exp(v - v.amax(-1, keepdim=True))
+    z = e.double().sum(-1, keepdim=True).float()
+    for _ in range(abs(z_ulps)):
+        z = torch.nextafter(z, torch.full_like(z, float("inf") if z_ulps > 0 else 0.0))
+    p = e * (1.0 / z)
+    cum = torch.cumsum(p, dim=-1)
+    pm = cum > 1 - top_p
+    pm[:, -1] = True
+    pm &= real
+    keep = torch.zeros((R, V), dtype=torch.bool)
+    keep.scatter_(-1, idx, pm)
+    vmin = torch.where(pm, vals, torch.full_like(vals, float("inf"))).amin(-1, keepdim=True)
+    group = (real & (vals == vmin)).sum(-1)
+    kept_in_group = (pm & (vals == vmin)).sum(-1)
+    return keep.view(logits.shape), {"n_kept": pm.sum(-1), "group": group, "kept_in_group": kept_in_group}

@@ -61,11 +61,12 @@ def apply_top_k_top_p(
     the shortest suffix of the ascending (stable) order whose cumulative
     probability exceeds ``1 - top_p``, and always the maximum.
 
-    Decisions are made on the fp32 values of the logits for every input
-    dtype: the reference's production callers upcast to fp32 before
-    filtering, which is the chain reproduced here.  (A direct reference call
-    on a bf16/fp16 tensor computes the top-p probabilities in that dtype; the
-    top-k set is the same either way.)  The filtered logits keep the input
+    Top-p is decided in the tensor's own dtype, as the reference's op
+    sequence does on an un-upcast tensor (logits_sampling_utils.py:189-191):
+    for bf16/fp16 the probabilities are rounded to the dtype and their
+    cumulative sum is rounded to it at every step; fp32 tensors (what the
+    production callers pass after their upcast) decide in fp32.  The top-k
+    set does not depend on the dtype.  The filtered logits keep the input
     dtype.
     """
     if not _need_top_k_filtering(top_k) and not _need_top_p_filtering(top_p):

@@ -1,0 +1,230 @@
+"""Every row of the full-size workloads against the CPU oracle (GPU).
+
+The kernel's outputs are copied back chunk by chunk and compared row by row with
+the oracle at the tolerances of the contract: logprobs within 2e-3 (bf16 logits),
+bf16 logits gradients within 1e-3 or one bf16 ulp, keep sets bit-exact.
+
+  [8, 2048, 151936] bf16 GRPO step: logprobs, loss (fp64 oracle loss on the
+      kernel's logprobs) and the logits gradient of the loss, every row;
+  [1, 32768, 131072] bf16, chunk 4096: logprobs and logits gradient, every row;
+  [4, 4096, 151936] bf16, T = 0.7, top-k 50, top-p 0.9 (fp32 decisions, the
+      get_next_token path after the in-place temperature): keep set, logprob and
+      gradient of every row; the rows whose keep set moves when the normaliser
+      moves by one fp32 ulp, and the rows with ties at the cut, are counted and
+      printed;
+  64 packed sequences, V = 256000: logprobs and the logits gradient of the
+      GRPO + KL loss, every row.
+"""
+
+import pytest
+import torch
+
+from oracle.logprob import next_token_logprobs, next_token_logprobs_grad, selected_logprobs, selected_logprobs_grad
+from oracle.loss import clipped_pg_loss
+from oracle.sampling import top_k_top_p, top_k_top_p_candidates
+from rl_amd import workloads
+from rl_amd.algorithms.loss import ClippedPGLossConfig, ClippedPGLossFn
+from rl_amd.distributed.model_utils import from_parallel_logits_to_logprobs
+from rl_amd.algorithms.logits_sampling_utils import apply_top_k_top_p
+from rl_amd.distributed.sampling import filtered_next_token_logprobs
+from tests.helpers import assert_close_or_ulp_bf16
+
+pytestmark = [pytest.mark.gpu, pytest.mark.timeout(900)]
+DEV = torch.device("cuda", 0)
+CH = 128  # rows per oracle chunk
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+
+
+def _check_rows(x, ids_next, lp, gr, glp, chunk=CH):
+    """Every row r = (b, s) of x [B, S, V] with target ids_next[b, s]: logprob and gradient."""
+    B, S, V = x.shape
+    n_bad = 0
+    for b in range(B):
+        for s0 in range(0, S, chunk):
+            s1 = min(S, s0 + chunk)
+            xc = x[b : b + 1, s0:s1].cpu()
+            tc = ids_next[b : b + 1, s0:s1].cpu()
+            ref = selected_logprobs(xc, tc, 0, V)
+            torch.testing.assert_close(lp[b : b + 1, s0:s1].cpu(), ref, rtol=0, atol=2e-3)
+            refg = selected_logprobs_grad(xc, tc, 0, V, glp[b : b + 1, s0:s1].cpu())
+            n_bad += assert_close_or_ulp_bf16(gr[b : b + 1, s0:s1], refg, 1e-3)
+    return n_bad
+
+
+def test_grpo_step_every_row():
+    say("every row: GRPO [8, 2048, 151936] bf16")
+    data = workloads.grpo_step_bf16(device=DEV)
+    logits = data["logits"]
+    ids = data["input_ids"]
+    B, S, V = logits.shape
+    with torch.no_grad():
+        cur = from_parallel_logits_to_logprobs(logits, ids, 0, V, None, inference_only=True)
+    data = workloads.finish_grpo_step(data, cur)
+    cfg = dict(reference_policy_kl_penalty=0.0)
+    fn = ClippedPGLossFn(ClippedPGLossConfig(**cfg))
+    from rl_amd.algorithms.advantage_estimator import AdvEstimatorConfig, GRPOAdvantageEstimator
+
+    est = GRPOAdvantageEstimator(AdvEstimatorConfig(use_leave_one_out_baseline=False), ClippedPGLossConfig(**cfg))
+    data["advantages"] = est.compute_advantage(data["prompt_ids"], data["rewards"], data["token_mask"])
+    gvs = data["sample_mask"].sum()
+    gvt = (data["token_mask"][:, 1:] * data["sample_mask"][:, None]).sum()
+    batch = {k: data[k] for k in ("token_mask", "sample_mask", "prev_logprobs", "advantages",
+                                   "generation_logprobs", "reference_policy_logprobs")}
+    x = logits.detach().requires_grad_(True)
+    lp = from_parallel_logits_to_logprobs(x, ids, 0, V, None)
+    loss, _ = fn(lp, batch, gvs, gvt)
+    (gr,) = torch.autograd.grad(loss, [x])
+    # the loss and its gradient w.r.t. the logprobs from the fp64 oracle
+    cpu = {k: v.double().cpu() for k, v in batch.items()}
+    lpo = lp.detach().double().cpu().requires_grad_(True)
+    lo, _ = clipped_pg_loss(lpo, cpu, gvs.cpu().double(), gvt.cpu().double(), **cfg)
+    (glp,) = torch.autograd.grad(lo, [lpo])
+    assert loss.item() == pytest.approx(lo.item(), rel=1e-4, abs=1e-7)
+    ids_next = torch.roll(ids, -1, dims=1)
+    glp_full = torch.zeros(B, S, dtype=torch.float32)
+    glp_full[:, : S - 1] = glp.float()
+    lp_full = torch.zeros(B, S, dtype=torch.float32, device=DEV)
+    lp_full[:, : S - 1] = lp.detach()
+    # the last column (no next token) is compared as a row with zero upstream gradient;
+    # its logprob is not an output, so give the oracle's own value there
+    ref_last = selected_logprobs(logits[:, -1:].cpu(), ids_next[:, -1:].cpu(), 0, V)
+    lp_full[:, -1] = ref_last[:, 0].to(DEV)
+    n = _check_rows(logits.detach(), ids_next, lp_full, gr, glp_full)
+    say("rows", B * (S - 1), "gradient elements off by one bf16 ulp beyond 1e-3:", n)
+    del x, gr
+
+
+def test_long_context_chunked_every_row():
+    say("every row: [1, 32768, 131072] bf16, chunk 4096")
+    d = workloads.long_context_bf16(device=DEV)
+    x, ids, gout = d["logits"], d["input_ids"], d["grad"]
+    B, S, V = x.shape
+    xl = x.requires_grad_(True)
+    lp = from_parallel_logits_to_logprobs(xl, ids, 0, V, None, chunk_size=4096)
+    (gr,) = torch.autograd.grad(lp, [xl], gout)
+    ids_next = torch.roll(ids, -1, dims=1)
+    glp_full = torch.zeros(B, S)
+    glp_full[:, : S - 1] = gout.cpu()
+    lp_full = torch.zeros(B, S, device=DEV)
+    lp_full[:, : S - 1] = lp.detach()
+    lp_full[:, -1] = selected_logprobs(x.detach()[:, -1:].cpu(), ids_next[:, -1:].cpu(), 0, V)[:, 0].to(DEV)
+    n = _check_rows(x.detach(), ids_next, lp_full, gr, glp_full, chunk=256)
+    say("rows", B * (S - 1), "gradient elements off by one bf16 ulp beyond 1e-3:", n)
+    del xl, gr
+
+
+def test_filtered_every_row_keep_sets_exact():
+    say("every row: filtered [4, 4096, 151936] bf16, T=0.7, k=50, p=0.9")
+    d = workloads.topk_filter_bf16(device=DEV)
+    x, ids, gout = d["logits"], d["input_ids"], d["grad"]
+    B, S, V = x.shape
+    T, k, p = 0.7, 50, 0.9
+    xl = x.requires_grad_(True)
+    lp = filtered_next_token_logprobs(xl, ids, k, p, temperature=T, decision_dtype=torch.float32)
+    (gr,) = torch.autograd.grad(lp, [xl], gout)
+    lp = lp.detach()
+    stats = {"rows": 0, "keep_mismatch": 0, "flip_one_ulp": 0, "group_gt1": 0, "tie_split": 0,
+             "cpu_torch_mismatch": 0, "cpu_torch_rows": 0}
+    n_bad = 0
+    for b in range(B):
+        for s0 in range(0, S - 1, 512):
+            s1 = min(S - 1, s0 + 512)
+            y = (x.detach()[b, s0:s1].float() / T).to(torch.bfloat16).float()  # the in-place division
+            yc = y.cpu()
+            keep, st = top_k_top_p_candidates(yc, k, p)
+            _, keep_gpu = apply_top_k_top_p(y, k, p)
+            stats["rows"] += s1 - s0
+            stats["keep_mismatch"] += int((keep_gpu.cpu() != keep).any(-1).sum())
+            kp, _ = top_k_top_p_candidates(yc, k, p, z_ulps=1)
+            km, _ = top_k_top_p_candidates(yc, k, p, z_ulps=-1)
+            stats["flip_one_ulp"] += int(((kp != keep).any(-1) | (km != keep).any(-1)).sum())
+            stats["group_gt1"] += int((st["group"] > 1).sum())
+            stats["tie_split"] += int((st["kept_in_group"] < st["group"]).sum())
+            if s0 == 0:
+                # CPU torch's own softmax (fp32 normaliser in vector-lane order) on a sample
+                _, keep_t = top_k_top_p(yc[:64], k, p)
+                stats["cpu_torch_rows"] += 64
+                stats["cpu_torch_mismatch"] += int((keep_t != keep[:64]).any(-1).sum())
+            # logprobs: log_softmax over the kept set, at the target
+            t = ids[b, s0 + 1 : s1 + 1].cpu()
+            filt = torch.where(keep, yc, torch.full_like(yc, -float("inf")))
+            lsm = torch.log_softmax(filt, -1)
+            ref = lsm.gather(-1, t[:, None])[:, 0]
+            got = lp[b, s0:s1].cpu()
+            assert torch.equal(torch.isinf(got), torch.isinf(ref))
+            fin = torch.isfinite(ref)
+            torch.testing.assert_close(got[fin], ref[fin], rtol=0, atol=2e-3)
+            # gradient: (onehot - p) * g on the kept set, rounded to bf16, then / T in bf16
+            g = gout[b, s0:s1].cpu()
+            pk = lsm.exp()
+            oh = torch.zeros_like(pk)
+            oh[torch.arange(s1 - s0), t] = 1.0
+            g32 = torch.where(keep, (oh - pk) * g[:, None], torch.zeros_like(pk))
+            refg = (g32.to(torch.bfloat16).float() / T).to(torch.bfloat16)
+            grc = gr[b, s0:s1]
+            assert int(((grc != 0).cpu() & ~keep).sum()) == 0  # zero outside the kept set
+            n_bad += assert_close_or_ulp_bf16(grc, refg, 1e-3)
+    say("filter statistics over every row:", stats, "gradient elements off by one ulp:", n_bad)
+    assert stats["keep_mismatch"] == 0
+    assert gr[:, -1].abs().max().item() == 0
+    del xl, gr
+
+
+def test_packed_grpo_kl_every_row(single_rank_group):
+    say("every row: 64 packed sequences, V = 256000")
+    from rl_amd.algorithms.advantage_estimator import AdvEstimatorConfig, GRPOAdvantageEstimator
+    from rl_amd.algorithms.loss import SequencePackingFusionLossWrapper, prepare_packed_loss_input
+    from rl_amd.distributed.batched_data_dict import BatchedDataDict
+
+    d = workloads.packed_grpo_kl_bf16(device=DEV)
+    logits, cu = d["logits"], d["cu_seqlens"]
+    ids = d["input_ids"]
+    B, S = ids.shape
+    V = logits.shape[-1]
+    with torch.no_grad():
+        cur, _ = prepare_packed_loss_input(
+            logits, BatchedDataDict({"input_ids": ids}),
+            ClippedPGLossFn(ClippedPGLossConfig(reference_policy_kl_penalty=0)), cu, cu,
+            vocab_parallel_rank=0, vocab_parallel_group=single_rank_group)
+    data = workloads.finish_packed_grpo_step(d, cur["next_token_logprobs"])
+    est = GRPOAdvantageEstimator(AdvEstimatorConfig(normalize_rewards=True, use_leave_one_out_baseline=False))
+    data["advantages"] = est.compute_advantage(data["prompt_ids"], data["rewards"], data["token_mask"])
+    batch = BatchedDataDict({k: data[k] for k in (
+        "input_ids", "token_mask", "sample_mask", "advantages", "prev_logprobs",
+        "generation_logprobs", "reference_policy_logprobs")})
+    cfg = dict(reference_policy_kl_penalty=0.01, reference_policy_kl_type="k3",
+               ratio_clip_min=0.2, ratio_clip_max=0.2, token_level_loss=False)
+    loss_fn = ClippedPGLossFn(ClippedPGLossConfig(**cfg))
+    wrapper = SequencePackingFusionLossWrapper(
+        loss_fn, prepare_packed_loss_input, cu, cu, vocab_parallel_rank=0,
+        vocab_parallel_group=single_rank_group)
+    gvs = torch.tensor(float(B), device=DEV)
+    gvt = batch["token_mask"][:, 1:].sum()
+    x = logits.detach().requires_grad_(True)
+    loss, _ = wrapper(x, batch, gvs, gvt)
+    (gr,) = torch.autograd.grad(loss, [x])
+    lp = cur["next_token_logprobs"]
+    # upstream gradient of the logprobs from the fp64 oracle loss
+    cpu = {k: v.double().cpu() for k, v in batch.items() if k != "input_ids"}
+    lpo = lp.double().cpu().requires_grad_(True)
+    lo, _ = clipped_pg_loss(lpo, cpu, gvs.cpu().double(), gvt.cpu().double(), **cfg)
+    (glp,) = torch.autograd.grad(lo, [lpo])
+    assert loss.item() == pytest.approx(lo.item(), rel=1e-4, abs=1e-7)
+    n_bad = 0
+    for i in range(B):
+        a, b = cu[i], cu[i + 1]
+        L = b - a
+        xs = logits.detach()[:, a:b].cpu()
+        sid = ids[i : i + 1, :L].cpu()
+        exp = next_token_logprobs(xs, sid, chunk_size=128)
+        torch.testing.assert_close(lp[i, : L - 1].cpu(), exp[0], rtol=0, atol=2e-3)
+        gexp = next_token_logprobs_grad(xs, sid, glp[i : i + 1, : L - 1].float(), chunk_size=128,
+                                        out_dtype=torch.bfloat16)
+        n_bad += assert_close_or_ulp_bf16(gr[:, a:b], gexp, 1e-3)
+    # rows past the last sequence carry no gradient
+    assert gr[:, cu[-1]:].abs().max().item() == 0 if gr.shape[1] > cu[-1] else True
+    say("sequences", B, "rows", cu[-1], "gradient elements off by one bf16 ulp beyond 1e-3:", n_bad)
+    del x, gr

@@ -179,3 +179,25 @@ def test_16bit_rule_known_answers(dtype, row):
     assert keep32.tolist() == [[False, True, True]]
     assert _definition_keep16(x.float()[0].tolist(), None, 0.9, dtype) == {2}
     assert _definition_keep(x.float()[0].tolist(), None, 0.9) == {1, 2}
+
+
+@pytest.mark.parametrize("k,p", [(50, 0.9), (5, 0.5), (20, 0.99), (3, 0.2)])
+def test_candidate_restriction_matches_full_sort(k, p):
+    """The top-k-candidate evaluation equals the full-row oracle (exact normaliser) on
+    random rows, tie-heavy rows and rows with a peaked head."""
+    from oracle.sampling import top_k_top_p_candidates
+
+    g = torch.Generator().manual_seed(k)
+    V = 3000
+    x = torch.randn(24, V, generator=g) * 2
+    x[0] = (torch.randint(-4, 4, (V,), generator=g).float()) * 0.5   # heavy ties everywhere
+    x[1, ::3] = 5.0                                                   # ties at the top
+    x[2, 17] = 30.0                                                   # one-hot row
+    x[3] = (torch.randn(V, generator=g) * 2).bfloat16().float()       # bf16 values
+    x[4, :100] = 7.0                                                  # a tied block above the rest
+    _, want = top_k_top_p(x, k, p, exact_normaliser=True)
+    got, st = top_k_top_p_candidates(x, k, p)
+    assert torch.equal(got, want)
+    assert torch.equal(st["n_kept"], want.sum(-1))
+    # every kept value is >= the smallest kept one, and the group counts are consistent
+    assert (st["kept_in_group"] >= 1).all() and (st["kept_in_group"] <= st["group"]).all()
