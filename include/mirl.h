@@ -321,6 +321,10 @@ int mirl_filtered_logprob_fwd(const void* logits, int dtype, int64_t B, int64_t 
  *   before the forward (mirl_temperature_scale), folded into this write.
  * Rows r >= R (up to R_total) and rows with g == 0 are written as zeros.
  * Rows whose kept list was saved are written without reading the logits.
+ * top_k is the forward's: it selects the schedule only (with 1 <= top_k <=
+ * 1024 the rows carry kept lists, so the gradient is zeroed in one flat pass
+ * and the kept entries stored; otherwise the rows are rewritten whole, each
+ * row written once); any value gives the same gradient.
  *
  * Replaces: DistributedLogprobWithSampling.backward and
  * ChunkedDistributedLogprobWithSampling.backward
@@ -331,7 +335,7 @@ int mirl_filtered_logprob_bwd(const void* logits, int dtype, int64_t B, int64_t 
                               int64_t R_total, int64_t V, int64_t stride_b,
                               int64_t stride_r, const int64_t* target,
                               int64_t t_stride_b, int64_t t_stride_r,
-                              double temperature, double grad_temperature,
+                              double temperature, double grad_temperature, int top_k,
                               const void* row_info, const int32_t* kept_idx,
                               const float* kept_p, const float* grad_out,
                               int64_t g_stride_b, int64_t g_stride_r, void* grad_in,

@@ -200,7 +200,7 @@ SIGNATURES = {
     "mirl_filtered_logprob_bwd": (
         _I,
         [_P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I64, _I64, ctypes.c_double,
-         ctypes.c_double, _P, _P, _P, _P, _I64, _I64, _P, _I64, _I64, _P],
+         ctypes.c_double, _I, _P, _P, _P, _P, _I64, _I64, _P, _I64, _I64, _P],
     ),
     "mirl_temperature_scale": (_I, [_P, _I, _I64, _I64, _I64, _I64, _I64, ctypes.c_double, _P]),
     "mirl_temperature_scale_grad": (
@@ -1005,10 +1005,12 @@ def filtered_bwd(
     grad_out: torch.Tensor,
     grad_in: torch.Tensor,
     grad_temperature: float = 1.0,
+    top_k: int = 0,
 ) -> None:
     """``grad_temperature`` != 1 divides the written gradient by it last (in the
     dtype): the backward of an in-place division of the logits made before the
-    forward, folded into this write."""
+    forward, folded into this write.  ``top_k`` is the forward's; it picks the
+    kernel schedule only (rows with kept lists for 1 <= top_k <= 1024)."""
     dev = _require_gpu(logits, target, grad_out, grad_in)
     B, R = target.shape
     Rt = grad_in.shape[1]
@@ -1018,7 +1020,8 @@ def filtered_bwd(
         "mirl_filtered_logprob_bwd", dev,
         logits.data_ptr(), _dtype_code(logits), B, R, Rt, V, logits.stride(0),
         logits.stride(1), target.data_ptr(), target.stride(0), target.stride(1),
-        float(temperature), float(grad_temperature), info.data_ptr(), kidx.data_ptr(), kp.data_ptr(),
+        float(temperature), float(grad_temperature), int(top_k), info.data_ptr(), kidx.data_ptr(),
+        kp.data_ptr(),
         grad_out.data_ptr(), grad_out.stride(0), grad_out.stride(1), grad_in.data_ptr(),
         grad_in.stride(0), grad_in.stride(1), _stream(dev),
     )

@@ -22,10 +22,12 @@ struct RowInfo {
   float m;        // max of the kept values
   float logsum;   // log(sum_kept exp(y - m))
   float v_cut;    // kept <=> y > v_cut || (y == v_cut && j >= i_cut)
-  int32_t i_cut;
+  int32_t i_cut;  // < 0: rank form, kept among y == v_cut <=> rank in index order >= -1 - i_cut
   int32_t n_kept;
-  int32_t flags;  // bit 0: row must be (re)done by a general path
+  int32_t flags;  // bit 0: row must be (re)done by a general path; bit 2: no kept list
 };
+constexpr int kFlagRedo = 1;
+constexpr int kFlagNoKeptList = 4;
 static_assert(sizeof(RowInfo) == sizeof(mirl_filter_row_info), "row info layout");
 
 struct FilterParams {
@@ -115,6 +117,10 @@ __device__ int block_sum_i(int v, int* red) {
 // row when all_rows != 0, else only the rows whose info.flags bit 0 is set.
 int launch_hist_rows(const FilterParams& P, int dtype, int64_t rows, int all_rows,
                      hipStream_t st);
+
+// Rewrites every row whose index cut is in rank form (RowInfo.i_cut < 0) into
+// index form (16-bit logits; fp32 rows are always in index form).
+int launch_resolve_rows(const FilterParams& P, int dtype, int64_t rows, hipStream_t st);
 
 // Largest vocabulary the histogram kernel accepts (its exact-count table
 // covers at most 8 values repeated 65536 times or more).

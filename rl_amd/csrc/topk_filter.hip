@@ -835,6 +835,7 @@ struct FilterBwdParams {
   int has_t;
   float GT;   // the gradient is divided by GT in the dtype last (an earlier in-place division)
   int has_gt;
+  int zero_rows;  // phase 2 zeroes the rows it does not rewrite (no phase 1)
   const RowInfo* info;
   const int32_t* kept_idx;
   const float* kept_p;
@@ -906,7 +907,20 @@ __global__ __launch_bounds__(256) void filter_bwd_scatter_kernel(FilterBwdParams
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
   const int64_t b = row / P.Rt, r = row - b * P.Rt;
-  if (r >= P.R) return;
+  raw* y = static_cast<raw*>(P.gin) + b * P.gisb + r * P.gisr;
+  // zeros over the row (zero_rows mode: rows not rewritten below)
+  auto zero_row = [&]() {
+    const RowSpan<E> zs(y, P.V);
+    vu4* zv = reinterpret_cast<vu4*>(y + zs.head);
+    for (int64_t i = lane; i < zs.nvec; i += 64) __builtin_nontemporal_store(vu4{0u, 0u, 0u, 0u}, zv + i);
+    const raw zr = E::from_float(0.f);
+    if (lane < zs.head) y[lane] = zr;
+    if (zs.tail0 + lane < P.V) y[zs.tail0 + lane] = zr;
+  };
+  if (r >= P.R) {
+    if (P.zero_rows) zero_row();
+    return;
+  }
   const int64_t srow = b * P.R + r;
   // independent loads, issued together
   const float gv = P.g[b * P.gsb + r * P.gsr];
@@ -914,10 +928,12 @@ __global__ __launch_bounds__(256) void filter_bwd_scatter_kernel(FilterBwdParams
   const int64_t t = P.target[b * P.tsb + r * P.tsr];
   const int32_t j0 = P.kept_idx[srow * kKeepCap + lane];
   const float p0 = P.kept_p[srow * kKeepCap + lane];
-  if (gv == 0.f) return;
-  raw* y = static_cast<raw*>(P.gin) + b * P.gisb + r * P.gisr;
+  if (gv == 0.f) {
+    if (P.zero_rows) zero_row();
+    return;
+  }
 
-  if (ri.n_kept <= kKeepCap) {
+  if (!P.zero_rows && ri.n_kept <= kKeepCap && (ri.flags & kFlagNoKeptList) == 0) {
     for (int i = lane; i < ri.n_kept; i += 64) {
       const int64_t j = (i == lane) ? j0 : P.kept_idx[srow * kKeepCap + i];
       const float p = (i == lane) ? p0 : P.kept_p[srow * kKeepCap + i];
@@ -926,47 +942,101 @@ __global__ __launch_bounds__(256) void filter_bwd_scatter_kernel(FilterBwdParams
     return;
   }
 
-  // whole row: re-read the logits and re-apply the cut
+  // Whole row: re-read the logits and re-apply the cut, in index order (the
+  // head, the vectors, the tail), counting the elements equal to v_cut as they
+  // come so that a cut in rank form is applied too.  Elements outside the kept
+  // set are written as zeros without the exponential.
   const raw* x = static_cast<const raw*>(P.logits) + b * P.sb + r * P.sr;
-  auto grad_of = [&](float xf, int64_t j) -> raw {
-    const float yy = P.has_t ? round_trip<E>(__fdiv_rn(xf, P.T)) : xf;
+  const float vc = ri.v_cut;
+  const bool rank_form = ri.i_cut < 0;
+  const uint32_t rcut = rank_form ? (uint32_t)(-1 - ri.i_cut) : 0u;
+  const int64_t icut = ri.i_cut;
+  const uint64_t below = (1ull << lane) - 1ull;
+  uint32_t seen = 0;  // elements equal to v_cut met so far (the same in every lane)
+  auto yval = [&](float xf) { return P.has_t ? round_trip<E>(__fdiv_rn(xf, P.T)) : xf; };
+  auto grad_at = [&](float yy, int64_t j, bool kept) -> raw {
     float g32 = 0.f;
-    if (kept_lex(yy, j, ri.v_cut, ri.i_cut)) {
-      const float p = expf((yy - ri.m) - ri.logsum);
+    if (kept) {
+      const float p = fast_exp2(((yy - ri.m) - ri.logsum) * kLog2e);
       g32 = ((j == t) ? 1.f - p : -p) * gv;
     }
     return grad_to_dtype<E>(g32, P);
   };
+  auto tied_kept = [&](uint32_t rank, int64_t j) { return rank_form ? rank >= rcut : j >= icut; };
+  // one element per lane, consecutive indices across the lanes; every lane calls it
+  auto lane_step = [&](int64_t j, bool valid) {
+    const float yy = valid ? yval(E::load(x + j)) : 0.f;
+    const bool tie = valid && yy == vc;
+    const uint64_t bal = __ballot(tie);
+    bool kept = valid && yy > vc;
+    if (tie) kept = tied_kept(seen + (uint32_t)__popcll(bal & below), j);
+    seen += (uint32_t)__popcll(bal);
+    if (valid) y[j] = grad_at(yy, j, kept);
+  };
   const RowSpan<E> xs(x, P.V);
   const RowSpan<E> ys(y, P.V);
   if (xs.head != ys.head) {
-    for (int64_t j = lane; j < P.V; j += 64) y[j] = grad_of(E::load(x + j), j);
+    for (int64_t j0r = 0; j0r < P.V; j0r += 64) lane_step(j0r + lane, j0r + lane < P.V);
     return;
   }
+  lane_step(lane, lane < ys.head);
   const vu4* xv = reinterpret_cast<const vu4*>(x + xs.head);
   vu4* yv = reinterpret_cast<vu4*>(y + ys.head);
   const int64_t nvec = ys.nvec;
-  for (int64_t i0 = lane; i0 < nvec; i0 += 64 * U) {
+  for (int64_t base = 0; base < nvec; base += 64 * U) {
     vu4 q[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u)
-      if (i0 + u * 64 < nvec) q[u] = __builtin_nontemporal_load(xv + i0 + u * 64);
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = base + u * 64 + lane;
+      if (i < nvec) q[u] = __builtin_nontemporal_load(xv + i);
+    }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int64_t i = i0 + u * 64;
-      if (i >= nvec) break;
+      const int64_t i = base + u * 64 + lane;
+      const bool valid = i < nvec;
+      const int64_t jb = ys.head + i * VEC;
       float w[VEC];
-      E::unpack(q[u], w);
-      raw vals[VEC];
+      if (valid) {
+        E::unpack(q[u], w);
 #pragma unroll
-      for (int k = 0; k < VEC; ++k) vals[k] = grad_of(w[k], ys.head + i * VEC + k);
-      vu4 out;
-      __builtin_memcpy(&out, vals, sizeof(out));
-      __builtin_nontemporal_store(out, yv + i);
+        for (int k = 0; k < VEC; ++k) w[k] = yval(w[k]);
+      }
+      uint32_t tie8 = 0, keep8 = 0;
+      if (valid) {
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) {
+          tie8 |= (w[k] == vc ? 1u : 0u) << k;
+          keep8 |= (w[k] > vc ? 1u : 0u) << k;
+        }
+      }
+      const uint32_t c = (uint32_t)__popc(tie8);
+      if (__ballot(c != 0u) != 0ull) {
+        // ranks of the tied elements: the wave's exclusive prefix of the counts
+        uint32_t inc = c;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+          const uint32_t o = (uint32_t)__shfl_up((int)inc, off, 64);
+          if (lane >= off) inc += o;
+        }
+        const uint32_t ex = inc - c;
+        const uint32_t total = (uint32_t)__shfl((int)inc, 63, 64);
+        for (uint32_t m = tie8; m != 0u; m &= m - 1u) {
+          const int k = __ffs(m) - 1;
+          if (tied_kept(seen + ex + (uint32_t)__popc(tie8 & ((1u << k) - 1u)), jb + k)) keep8 |= 1u << k;
+        }
+        seen += total;
+      }
+      if (valid) {
+        raw vals[VEC];
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) vals[k] = grad_at(w[k], jb + k, (keep8 >> k) & 1u);
+        vu4 out;
+        __builtin_memcpy(&out, vals, sizeof(out));
+        __builtin_nontemporal_store(out, yv + i);
+      }
     }
   }
-  if (lane < ys.head) y[lane] = grad_of(E::load(x + lane), lane);
-  for (int64_t j = ys.tail0 + lane; j < P.V; j += 64) y[j] = grad_of(E::load(x + j), j);
+  lane_step(ys.tail0 + lane, ys.tail0 + lane < P.V);
 }
 
 // filtered logits (-inf outside the kept set) and the keep mask
@@ -1057,6 +1127,13 @@ int launch_topk_export(const FilterParams& P, int64_t rows, hipStream_t st) {
 
 template <class E>
 int launch_bwd(const FilterBwdParams& P, int64_t B, int64_t rows, hipStream_t st) {
+  if (P.zero_rows) {
+    // rows without kept lists: each row written once by phase 2
+    if (rows == 0) return MIRL_OK;
+    hipLaunchKernelGGL((filter_bwd_scatter_kernel<E>), dim3((unsigned)((rows + 3) / 4)), dim3(256),
+                       0, st, P, rows);
+    return check_launch("filter_bwd_scatter_kernel");
+  }
   const bool contiguous = P.gisr == P.V && (B == 1 || P.gisb == P.Rt * P.V);
   if (contiguous) {
     const int64_t n = rows * P.V;
@@ -1180,7 +1257,7 @@ extern "C" int mirl_filtered_logprob_bwd(const void* logits, int dtype, int64_t 
                                          int64_t R_total, int64_t V, int64_t stride_b,
                                          int64_t stride_r, const int64_t* target,
                                          int64_t t_stride_b, int64_t t_stride_r,
-                                         double temperature, double grad_temperature,
+                                         double temperature, double grad_temperature, int top_k,
                                          const void* row_info, const int32_t* kept_idx,
                                          const float* kept_p, const float* grad_out,
                                          int64_t g_stride_b, int64_t g_stride_r, void* grad_in,
@@ -1221,6 +1298,10 @@ extern "C" int mirl_filtered_logprob_bwd(const void* logits, int dtype, int64_t 
   P.gin = grad_in;
   P.gisb = gi_stride_b;
   P.gisr = gi_stride_r;
+  // the forward keeps kept lists for the rows of 1 <= top_k <= 1024 (fast path):
+  // zero the gradient in one flat pass, then scatter; otherwise rows are
+  // rewritten whole and each row is written once
+  P.zero_rows = !(top_k >= 1 && top_k <= kCandCap);
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == MIRL_DTYPE_F32) return launch_bwd<F32>(P, B, rows, st);
   if (dtype == MIRL_DTYPE_BF16) return launch_bwd<BF16>(P, B, rows, st);
@@ -1247,6 +1328,7 @@ extern "C" int mirl_top_k_top_p_mask(const void* logits, int dtype, int64_t N, i
   else if (dtype == MIRL_DTYPE_BF16) e = launch_fwd<BF16>(P, N, st);
   else e = launch_fwd<F16>(P, N, st);
   if (e) return e;
+  if (int e2 = launch_resolve_rows(P, dtype, N, st)) return e2;  // index form for the mask kernel
   FilterParams Q = P;
   Q.sr = row_stride;  // filter_mask_kernel indexes rows by row * sr
   if (dtype == MIRL_DTYPE_F32)

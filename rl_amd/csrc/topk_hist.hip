@@ -7,15 +7,13 @@
 // nemo_rl/distributed/model_utils.py:382-432).  The kept set is a suffix of the
 // ascending (value, index) order, described by the cut (v_cut, i_cut).
 //
-// One 1024-thread workgroup per row reads the row once with 16-byte
-// nontemporal loads and keeps it in registers when it fits (kRegVec vectors
-// per lane, 163840 elements).  Every raw value is counted into a table of
-// 65536 16-bit counts in LDS (128 KB), indexed by an order-preserving key of
-// the raw bits; the values that occur are the table's non-empty entries, and
-// the value y = dtype(x / T) of an entry is computed from its key.  So the
-// top-k value, the normaliser, the cumulative probability in ascending order
-// and the kept set's log-sum-exp all follow from the table, each thread
-// owning 64 consecutive keys:
+// One 1024-thread workgroup per row reads the row with 16-byte nontemporal
+// loads.  Every raw value is counted into a table of 65536 16-bit counts in
+// LDS (128 KB), indexed by an order-preserving key of the raw bits; the values
+// that occur are the table's non-empty entries, and the value y = dtype(x / T)
+// of an entry is computed from its key.  So the top-k value, the normaliser,
+// the cumulative probability in ascending order and the kept set's
+// log-sum-exp all follow from the table:
 //   top-k:  suffix counts over the keys give the k-th largest value;
 //   Z:      sum over kept-k keys of count * exp(y - m);
 //   top-p:  masses count * p(y) summed in key order give the cumulative
@@ -31,11 +29,17 @@
 //           a row where the bound leaves the cut undecided is walked exactly
 //           by one wave (additions of equal values inside one binade are
 //           applied in closed form).
-// A second sweep over the registers finds the index cut inside the tied
-// values (the r-th smallest index among them); a third, for rows with at most
-// MIRL_FILTER_KEEP_CAP kept entries, writes the kept list for the backward.
-// Counts of 65536 or more wrap the 16-bit entries; the total then differs from
-// V, and two more sweeps count the affected 256-key blocks exactly.
+//
+// filter_compact_kernel (first) lists the occupied keys once, with their y and
+// exp(y - m), and works over contiguous shares of that list; it leaves the
+// index cut inside the tied values in rank form and writes no kept list.
+// filter_hist_kernel (for the rows the compact kernel flags) works over the
+// table itself, each thread owning 64 consecutive keys; a second sweep over
+// the row finds the index cut (the r-th smallest index among the tied
+// values), a third writes the kept list of rows with at most
+// MIRL_FILTER_KEEP_CAP kept entries, and counts of 65536 or more (which wrap
+// the 16-bit entries, so the total differs from V) are repaired by two more
+// sweeps that count the affected 256-key blocks exactly.
 
 #include "filter.h"
 
@@ -46,7 +50,6 @@ constexpr int kHT = 1024;          // threads per row
 constexpr int kHW = kHT / 64;      // waves per row
 constexpr int kHistWords = 32768;  // 65536 16-bit counts
 constexpr int kOvfSlots = 8;       // 256-key blocks with exact 32-bit counts
-constexpr int kRegVec = 0;         // 16-byte vectors per lane held in registers (0: sweeps re-read the row)
 
 struct HistShared {
   uint32_t hist[kHistWords];
@@ -811,16 +814,491 @@ __global__ __launch_bounds__(kHT) void filter_hist_kernel(FilterParams P, int al
   }
 }
 
+// ---------------------------------------------------------------------------
+// Compact form: the occupied keys as an entry list
+// ---------------------------------------------------------------------------
+// The table phases above evaluate y = dtype(x / T) and exp(y - m) per occupied
+// key, several times, and a thread owns 64 consecutive keys, so the occupied
+// keys (a few thousand of the 65536) crowd into a few waves.  This kernel
+// counts the row the same way, then lists the occupied keys in ascending
+// order as entries {key | count << 16, y, exp(y - m)} over the table's
+// memory, each computed once and spread over all lanes; top-k, the normaliser,
+// the cut and the value group then run over contiguous shares of the list.
+// The index cut inside the value group is left in rank form (the group's
+// rcut-th element in index order, RowInfo.i_cut = -1 - rcut) for the
+// consumers that walk the row in index order, so the row is read once; the
+// target's rank is counted only when its value is the cut value.  No kept
+// list is written (flags bit 2): the backward rewrites such rows whole.
+// Rows it cannot finish (a count of 65536 or more, more than kEntCap occupied
+// keys, a 16-bit cut the rounding bound leaves undecided) are flagged
+// (flags bit 0) for filter_hist_kernel.
+constexpr int kPadWords = kHistWords + kHistWords / 32;  // one pad word per 32
+constexpr int kEntCap = kPadWords / 3;                     // 12-byte entries over the same bytes
+
+struct CompactShared {
+  union {
+    uint32_t hist[kPadWords];  // logical word L at L + L / 32
+    struct {
+      uint32_t kc[kEntCap];
+      float y[kEntCap];
+      float e[kEntCap];
+    } ent;
+  } u;
+  double red_d[kHW * 4];
+  uint32_t red_u[kHW * 4];
+  uint32_t sel[4];
+  int first_lo, first_hi;
+  uint32_t ent_lo, pos_lo, ent_hi, pos_hi;
+  int fail;
+};
+
+__device__ __forceinline__ uint32_t padded(uint32_t L) { return L + (L >> 5); }
+
+// Order keys of the two 16-bit values of a word, in the word's halves: a
+// negative value's bits inverted, a positive value's sign bit set.
+__device__ __forceinline__ uint32_t okey16x2(uint32_t w) {
+  const uint32_t neg = (w >> 15) & 0x00010001u;
+  return w ^ ((neg * 0xffffu) | 0x80008000u);
+}
+
+template <class E>
+__global__ __launch_bounds__(kHT) void filter_compact_kernel(FilterParams P, int all_rows) {
+  using raw = typename E::raw;
+  __shared__ CompactShared sh;
+  const int64_t row = blockIdx.x;
+  if (!all_rows && (P.info[row].flags & 1) == 0) return;
+  const int64_t b = row / P.R, r = row - b * P.R;
+  const raw* x = static_cast<const raw*>(P.logits) + b * P.sb + r * P.sr;
+  const int tid = threadIdx.x;
+  const int64_t V = P.V;
+  const RowSpan<E> sp(x, V);
+  const vu4* xv = reinterpret_cast<const vu4*>(x + sp.head);
+  const int64_t nvec = sp.nvec;
+
+  {
+    vu4* h4 = reinterpret_cast<vu4*>(sh.u.hist);
+    for (int i = tid; i < kPadWords / 4; i += kHT) h4[i] = vu4{0u, 0u, 0u, 0u};
+  }
+  if (tid == 0) {
+    sh.first_lo = kHT;
+    sh.first_hi = kHT;
+    sh.fail = 0;
+    sh.sel[0] = sh.sel[1] = sh.sel[2] = sh.sel[3] = 0u;
+    sh.ent_lo = sh.pos_lo = sh.ent_hi = sh.pos_hi = 0u;
+  }
+  __syncthreads();
+
+  // ---- one pass over the row: every value counted under its order key ----
+  auto count_key = [&](uint32_t k) {
+    const uint32_t L = k >> 1;
+    atomicAdd(&sh.u.hist[padded(L)], 1u + (k & 1u) * 0xffffu);
+  };
+  auto count_word = [&](uint32_t w) {
+    const uint32_t k2 = okey16x2(w);
+    count_key(k2 & 0xffffu);
+    count_key(k2 >> 16);
+  };
+  if (tid < sp.head) count_key(okey16x2(bits16<E>(x[tid])) & 0xffffu);
+  if (sp.tail0 + tid < V) count_key(okey16x2(bits16<E>(x[sp.tail0 + tid])) & 0xffffu);
+  {
+    constexpr int UB = 8;
+    for (int64_t v0 = tid; v0 < nvec; v0 += (int64_t)UB * kHT) {
+      vu4 t[UB];
+#pragma unroll
+      for (int u = 0; u < UB; ++u) {
+        const int64_t v = v0 + (int64_t)u * kHT;
+        if (v < nvec) t[u] = __builtin_nontemporal_load(xv + v);
+      }
+#pragma unroll
+      for (int u = 0; u < UB; ++u) {
+        const int64_t v = v0 + (int64_t)u * kHT;
+        if (v >= nvec) break;
+        count_word(t[u].x);
+        count_word(t[u].y);
+        count_word(t[u].z);
+        count_word(t[u].w);
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- the occupied keys: counted, checked, listed in ascending order ------
+  // thread t owns logical words 32t .. 32t + 31 (keys 64t .. 64t + 63), which
+  // sit at physical words 33t .. 33t + 31
+  uint32_t ct = 0, nz = 0, klast = 0;
+#pragma unroll 8
+  for (int w = 0; w < 32; ++w) {
+    const uint32_t word = sh.u.hist[33 * tid + w];
+    const uint32_t lo = word & 0xffffu, hi = word >> 16;
+    ct += lo + hi;
+    nz += (lo != 0u ? 1u : 0u) + (hi != 0u ? 1u : 0u);
+    if (lo != 0u) klast = (uint32_t)tid * 64u + 2u * (uint32_t)w;
+    if (hi != 0u) klast = (uint32_t)tid * 64u + 2u * (uint32_t)w + 1u;
+  }
+  uint32_t tot[1] = {ct};
+  block_sum_n<uint32_t, 1>(tot, sh.red_u);
+  uint32_t N;
+  const uint32_t off = block_excl_scan<uint32_t>(nz, sh.red_u, &N);
+  const uint32_t kmx = block_max_u(ct > 0u ? klast : 0u, sh.red_u);
+  // a 16-bit count that wrapped loses a multiple of 65536 from the total
+  if (tot[0] != (uint32_t)V || N > (uint32_t)kEntCap) {
+    if (tid == 0) {
+      RowInfo ri{};
+      ri.flags = 1;
+      P.info[row] = ri;
+    }
+    return;
+  }
+  uint32_t wd[32];
+#pragma unroll
+  for (int w = 0; w < 32; ++w) wd[w] = sh.u.hist[33 * tid + w];
+  __syncthreads();  // every table word is in registers: the entries overwrite the table
+  {
+    uint32_t j = off;
+#pragma unroll
+    for (int w = 0; w < 32; ++w) {
+      const uint32_t lo = wd[w] & 0xffffu, hi = wd[w] >> 16;
+      const uint32_t k0 = (uint32_t)tid * 64u + 2u * (uint32_t)w;
+      if (lo != 0u) sh.u.ent.kc[j++] = k0 | (lo << 16);
+      if (hi != 0u) sh.u.ent.kc[j++] = (k0 + 1u) | (hi << 16);
+    }
+  }
+  __syncthreads();
+  auto yk = [&](uint32_t k) { return scaled<E>(value16<E>(raw_of_okey16(k)), P); };
+  const float m = yk(kmx);
+  for (uint32_t j = tid; j < N; j += kHT) {
+    const float y = yk(sh.u.ent.kc[j] & 0xffffu);
+    sh.u.ent.y[j] = y;
+    sh.u.ent.e[j] = expf(y - m);
+  }
+  __syncthreads();
+  const uint32_t* kc = sh.u.ent.kc;
+  const float* ey = sh.u.ent.y;
+  const float* ee = sh.u.ent.e;
+  auto cnt = [&](uint32_t j) { return kc[j] >> 16; };
+  // this thread's share of the list
+  const uint32_t C = (N + kHT - 1) / kHT;
+  const uint32_t j0 = min(N, (uint32_t)tid * C), j1 = min(N, j0 + C);
+  // first entry in [lo, hi] whose y >= v (hi + 1 if none); last entry whose y <= v (lo - 1 if none)
+  auto first_ge = [&](uint32_t lo, uint32_t hi, float v) {
+    uint32_t a = lo, c = hi + 1u;
+    while (a < c) {
+      const uint32_t mid = (a + c) >> 1;
+      if (ey[mid] >= v) c = mid; else a = mid + 1u;
+    }
+    return a;
+  };
+  auto last_le = [&](uint32_t lo, uint32_t hi, float v) {
+    uint32_t a = lo, c = hi + 1u;
+    while (a < c) {
+      const uint32_t mid = (a + c) >> 1;
+      if (ey[mid] <= v) a = mid + 1u; else c = mid;
+    }
+    return a - 1u;
+  };
+
+  // ---- top-k: the k-th largest value by suffix counts over the list --------
+  uint32_t thr = 0;  // first entry of the kept-k values
+  float y_thr = -INFINITY;
+  if (P.top_k > 0) {
+    const int rr = kHT - 1 - tid;  // shares in descending order
+    const uint32_t a0 = min(N, (uint32_t)rr * C), a1 = min(N, a0 + C);
+    uint32_t cr = 0;
+    for (uint32_t j = a0; j < a1; ++j) cr += cnt(j);
+    uint32_t tk;
+    const uint32_t above = block_excl_scan<uint32_t>(cr, sh.red_u, &tk);
+    const uint32_t kk = (uint32_t)P.top_k;
+    if (above < kk && kk <= above + cr) {
+      uint32_t acc = above;
+      for (uint32_t j = a1; j > a0; --j) {
+        acc += cnt(j - 1u);
+        if (acc >= kk) {
+          sh.sel[0] = j - 1u;
+          break;
+        }
+      }
+    }
+    __syncthreads();
+    const uint32_t jk = sh.sel[0];
+    y_thr = ey[jk];
+    thr = first_ge(0u, jk, y_thr);
+  }
+
+  // ---- normaliser over the kept-k values ------------------------------------
+  double zs[1] = {0.0};
+  for (uint32_t j = max(j0, thr); j < j1; ++j) zs[0] += (double)cnt(j) * (double)ee[j];
+  block_sum_n<double, 1>(zs, sh.red_d);
+  const float Z = (float)zs[0];
+
+  // ---- top-p cut: (entry, 1-based position inside it) -----------------------
+  bool have_cut = false;
+  uint32_t cut_ent = 0, cut_pos = 0;
+  if (P.has_p) {
+    const float inv = 1.0f / Z;
+    auto pmass = [&](uint32_t j) -> double {
+      return P.dec16 ? (double)round_trip<E>(ee[j] / Z) : (double)(ee[j] * inv);
+    };
+    double mt = 0.0;
+    for (uint32_t j = max(j0, thr); j < j1; ++j) mt += (double)cnt(j) * pmass(j);
+    double mtot;
+    const double X0 = block_excl_scan<double>(mt, sh.red_d, &mtot);
+    auto first_in_run = [&](double X, double p, uint32_t n, auto&& hit) {
+      uint32_t a = 1u, c = n;
+      while (a < c) {
+        const uint32_t mid = a + ((c - a) >> 1);
+        if (hit(X + (double)mid * p)) c = mid; else a = mid + 1u;
+      }
+      return a;
+    };
+    if (!P.dec16) {
+      const float cut = P.cut;
+      auto hit = [&](double X) { return (float)X > cut; };
+      double X = X0;
+      bool found = false;
+      uint32_t fk = 0, fp = 0;
+      for (uint32_t j = max(j0, thr); j < j1 && !found; ++j) {
+        const double p = pmass(j);
+        const uint32_t n = cnt(j);
+        if (hit(X + (double)n * p)) {
+          found = true;
+          fk = j;
+          fp = hit(X) ? 1u : first_in_run(X, p, n, hit);
+        }
+        X += (double)n * p;
+      }
+      if (found) atomicMin(&sh.first_lo, tid);
+      __syncthreads();
+      if (sh.first_lo == tid) {
+        sh.ent_lo = fk;
+        sh.pos_lo = fp;
+      }
+      __syncthreads();
+      have_cut = sh.first_lo < kHT;
+      cut_ent = sh.ent_lo;
+      cut_pos = sh.pos_lo;
+    } else {
+      // smallest fp32 S whose rounding to the dtype exceeds thr16
+      const float t16 = P.thr16;
+      const float nxt = value16<E>(raw_of_value16<E>(t16) + 1u);
+      const float mid = 0.5f * (t16 + nxt);
+      const float Bthr = round_trip<E>(mid) > t16 ? mid : nextafterf(mid, INFINITY);
+      const double Bd = (double)Bthr;
+      double bt = 0.0;
+      {
+        double X = X0;
+        for (uint32_t j = max(j0, thr); j < j1; ++j) {
+          const double p = pmass(j);
+          const uint32_t n = cnt(j);
+          const double X1 = X + (double)n * p;
+          bt += run_error_bound(n, p, X, X1);
+          X = X1;
+        }
+      }
+      double btot;
+      const double D0 = block_excl_scan<double>(bt, sh.red_d, &btot);
+      bool flo = false, fhi = false, slack_ok = true;
+      uint32_t klo = 0, plo = 0, khi = 0, phi = 0;
+      {
+        double X = X0, D = D0;
+        for (uint32_t j = max(j0, thr); j < j1 && !(flo && fhi); ++j) {
+          const double p = pmass(j);
+          const uint32_t n = cnt(j);
+          const double X1 = X + (double)n * p;
+          const double Db = D + run_error_bound(n, p, X, X1);
+          if (Db > 0.5 * kSlack * X1) slack_ok = false;
+          auto hlo = [&](double v) { return v + Db >= Bd; };
+          auto hhi = [&](double v) { return v - Db >= Bd; };
+          if (!flo && hlo(X1)) {
+            flo = true;
+            klo = j;
+            plo = hlo(X) ? 1u : first_in_run(X, p, n, hlo);
+          }
+          if (!fhi && hhi(X1)) {
+            fhi = true;
+            khi = j;
+            phi = hhi(X) ? 1u : first_in_run(X, p, n, hhi);
+          }
+          X = X1;
+          D = Db;
+        }
+      }
+      if (flo) atomicMin(&sh.first_lo, tid);
+      if (fhi) atomicMin(&sh.first_hi, tid);
+      if (!slack_ok) sh.fail = 1;
+      __syncthreads();
+      if (sh.first_lo == tid) {
+        sh.ent_lo = klo;
+        sh.pos_lo = plo;
+      }
+      if (sh.first_hi == tid) {
+        sh.ent_hi = khi;
+        sh.pos_hi = phi;
+      }
+      __syncthreads();
+      const bool none_lo = sh.first_lo >= kHT, none_hi = sh.first_hi >= kHT;
+      const bool certain = sh.fail == 0 &&
+                           ((none_lo && none_hi) ||
+                            (!none_lo && !none_hi && sh.ent_lo == sh.ent_hi && sh.pos_lo == sh.pos_hi));
+      if (!certain) {
+        // the exact sequence is walked by filter_hist_kernel
+        if (tid == 0) {
+          RowInfo ri{};
+          ri.flags = 1;
+          P.info[row] = ri;
+        }
+        return;
+      }
+      have_cut = !none_hi;
+      cut_ent = sh.ent_hi;
+      cut_pos = sh.pos_hi;
+    }
+  }
+
+  // ---- the cut's value group, kept count and log-sum-exp --------------------
+  uint32_t g_lo, g_hi;
+  float v_cut;
+  if (!P.has_p) {
+    v_cut = y_thr;
+    g_lo = thr;
+    g_hi = last_le(thr, N - 1u, y_thr);
+  } else {
+    const uint32_t ck = have_cut ? cut_ent : N - 1u;
+    v_cut = ey[ck];
+    g_lo = first_ge(thr, ck, v_cut);
+    g_hi = last_le(ck, N - 1u, v_cut);
+  }
+  double sums[1] = {0.0};   // kept mass above the group
+  uint32_t cnts[3] = {0u, 0u, 0u};  // elements above the group, in it, in it before the cut entry
+  for (uint32_t j = j0; j < j1; ++j) {
+    const uint32_t n = cnt(j);
+    if (j > g_hi) {
+      cnts[0] += n;
+      sums[0] += (double)n * (double)ee[j];
+    } else if (j >= g_lo) {
+      cnts[1] += n;
+      if (have_cut && j < cut_ent) cnts[2] += n;
+    }
+  }
+  block_sum_n<double, 1>(sums, sh.red_d);
+  block_sum_n<uint32_t, 3>(cnts, sh.red_u);
+  const uint32_t n_group = cnts[1];
+  uint32_t rcut = 0;  // group elements (in index order) before the cut
+  if (P.has_p) rcut = have_cut ? cnts[2] + cut_pos - 1u : n_group - 1u;
+  const uint32_t n_kept = cnts[0] + (n_group - rcut);
+  const double ksum = sums[0] + (double)(n_group - rcut) * (double)ee[g_lo];
+  const float logsum = logf((float)ksum);
+  const uint32_t gk_lo = kc[g_lo] & 0xffffu, gk_hi = kc[g_hi] & 0xffffu;
+
+  // ---- the target --------------------------------------------------------
+  float lp = -INFINITY;
+  int64_t t = -1;
+  if (P.out != nullptr) t = P.target[b * P.tsb + r * P.tsr];
+  if (t >= 0 && t < V) {
+    const uint32_t kt = okey16x2(bits16<E>(x[t])) & 0xffffu;
+    const float yt = yk(kt);
+    bool kept = yt > v_cut;
+    if (yt == v_cut) {
+      kept = true;
+      if (rcut > 0u) {
+        // the target's rank among the group's elements in index order
+        uint32_t before = 0;
+        for (int64_t j = tid; j < t; j += kHT) {
+          const uint32_t kj = okey16x2(bits16<E>(x[j])) & 0xffffu;
+          before += (kj >= gk_lo && kj <= gk_hi) ? 1u : 0u;
+        }
+        uint32_t bs[1] = {before};
+        block_sum_n<uint32_t, 1>(bs, sh.red_u);
+        kept = bs[0] >= rcut;
+      }
+    }
+    if (kept) lp = (yt - m) - logsum;
+  }
+
+  if (tid == 0) {
+    RowInfo ri;
+    ri.m = m;
+    ri.logsum = logsum;
+    ri.v_cut = v_cut;
+    ri.i_cut = rcut > 0u ? -1 - (int32_t)rcut : 0;
+    ri.n_kept = (int32_t)n_kept;
+    ri.flags = 4;
+    P.info[row] = ri;
+    if (P.out != nullptr) P.out[row] = lp;
+  }
+}
+
+// The index cut of a row left in rank form (i_cut = -1 - rcut): the index of
+// the group's element of rank rcut in index order, the group being the
+// elements whose scaled value equals v_cut.  One workgroup per row; rows in
+// index form return at once.  Each thread counts the group's elements in its
+// own contiguous share of the row, a workgroup scan places the shares, and
+// the thread holding rank rcut reads its share again.
+template <class E>
+__global__ __launch_bounds__(kHT) void filter_resolve_kernel(FilterParams P) {
+  using raw = typename E::raw;
+  __shared__ uint32_t red[kHW * 4];
+  __shared__ int32_t s_idx;
+  const int64_t row = blockIdx.x;
+  const RowInfo ri = P.info[row];
+  if (ri.i_cut >= 0) return;
+  const uint32_t rcut = (uint32_t)(-1 - ri.i_cut);
+  const int64_t b = row / P.R, r = row - b * P.R;
+  const raw* x = static_cast<const raw*>(P.logits) + b * P.sb + r * P.sr;
+  const int tid = threadIdx.x;
+  const int64_t V = P.V;
+  auto yk = [&](uint32_t k) { return scaled<E>(value16<E>(raw_of_okey16(k)), P); };
+  // the group's key range, searched between the keys of -inf and +inf (NaN keys lie outside)
+  const uint32_t klo = okey16x2(raw_of_value16<E>(-INFINITY)) & 0xffffu;
+  const uint32_t khi = okey16x2(raw_of_value16<E>(INFINITY)) & 0xffffu;
+  const float v = ri.v_cut;
+  uint32_t a = klo, c = khi + 1u;
+  while (a < c) {
+    const uint32_t mid = (a + c) >> 1;
+    if (yk(mid) >= v) c = mid; else a = mid + 1u;
+  }
+  const uint32_t g_lo = a;
+  a = klo;
+  c = khi + 1u;
+  while (a < c) {
+    const uint32_t mid = (a + c) >> 1;
+    if (yk(mid) <= v) a = mid + 1u; else c = mid;
+  }
+  const uint32_t g_hi = a - 1u;
+  auto member = [&](int64_t j) {
+    const uint32_t k = okey16x2(bits16<E>(x[j])) & 0xffffu;
+    return k >= g_lo && k <= g_hi;
+  };
+  const int64_t C = (V + kHT - 1) / kHT;
+  const int64_t j0 = min(V, (int64_t)tid * C), j1 = min(V, j0 + C);
+  uint32_t n = 0;
+  for (int64_t j = j0; j < j1; ++j) n += member(j) ? 1u : 0u;
+  uint32_t tot;
+  const uint32_t before = block_excl_scan<uint32_t>(n, red, &tot);
+  if (tid == 0) s_idx = 0;
+  __syncthreads();
+  if (before <= rcut && rcut < before + n) {
+    uint32_t seen = before;
+    for (int64_t j = j0; j < j1; ++j) {
+      if (!member(j)) continue;
+      if (seen == rcut) {
+        s_idx = (int32_t)j;
+        break;
+      }
+      ++seen;
+    }
+  }
+  __syncthreads();
+  if (tid == 0) P.info[row].i_cut = s_idx;
+}
+
 template <class E>
 int launch_hist(const FilterParams& P, int64_t rows, int all_rows, hipStream_t st) {
-  // rows whose vectors fit kRegVec per lane stay in registers between sweeps
-  const int64_t nvec_max = (P.V + 7) / 8;
-  if (nvec_max <= (int64_t)kRegVec * kHT)
-    hipLaunchKernelGGL((filter_hist_kernel<E, kRegVec, false>), dim3((unsigned)rows), dim3(kHT), 0,
-                       st, P, all_rows);
-  else
-    hipLaunchKernelGGL((filter_hist_kernel<E, 0, false>), dim3((unsigned)rows), dim3(kHT), 0, st,
-                       P, all_rows);
+  // the compact kernel first; the rows it flags go to filter_hist_kernel
+  hipLaunchKernelGGL((filter_compact_kernel<E>), dim3((unsigned)rows), dim3(kHT), 0, st, P,
+                     all_rows);
+  if (int e = check_launch("filter_compact_kernel")) return e;
+  hipLaunchKernelGGL((filter_hist_kernel<E, 0, false>), dim3((unsigned)rows), dim3(kHT), 0, st, P,
+                     0);
   if (int e = check_launch("filter_hist_kernel")) return e;
   if (!P.dec16) return MIRL_OK;
   // rows the rounding bound left undecided
@@ -830,6 +1308,16 @@ int launch_hist(const FilterParams& P, int64_t rows, int all_rows, hipStream_t s
 }
 
 }  // namespace
+
+int launch_resolve_rows(const FilterParams& P, int dtype, int64_t rows, hipStream_t st) {
+  if (dtype == MIRL_DTYPE_BF16)
+    hipLaunchKernelGGL((filter_resolve_kernel<BF16>), dim3((unsigned)rows), dim3(kHT), 0, st, P);
+  else if (dtype == MIRL_DTYPE_F16)
+    hipLaunchKernelGGL((filter_resolve_kernel<F16>), dim3((unsigned)rows), dim3(kHT), 0, st, P);
+  else
+    return MIRL_OK;  // fp32 rows never leave the cut in rank form
+  return check_launch("filter_resolve_kernel");
+}
 
 int launch_hist_rows(const FilterParams& P, int dtype, int64_t rows, int all_rows,
                      hipStream_t st) {

@@ -82,6 +82,7 @@ def _temperature_node(logits: torch.Tensor):
 
 
 def _filtered_grad(ctx: Any, logits, target, temperature, info, kidx, kp, g):
+    top_k = getattr(ctx, "top_k", 0)
     """The logits gradient of a filtered op: folded into the in-place temperature
     node ahead of it when that node has no gradient from another filtered op yet
     (then None is returned for autograd), else returned as usual."""
@@ -89,17 +90,17 @@ def _filtered_grad(ctx: Any, logits, target, temperature, info, kidx, kp, g):
     if node is not None and node.prediv is None:
         grad = torch.empty_like(logits)
         _C.filtered_bwd(logits, target, temperature, info, kidx, kp, g, grad,
-                        grad_temperature=node.temperature)
+                        grad_temperature=node.temperature, top_k=top_k)
 
         def undivided() -> torch.Tensor:
             raw = torch.empty_like(logits)
-            _C.filtered_bwd(logits, target, temperature, info, kidx, kp, g, raw)
+            _C.filtered_bwd(logits, target, temperature, info, kidx, kp, g, raw, top_k=top_k)
             return raw
 
         node.prediv = (grad, undivided)
         return None
     grad = torch.empty_like(logits)
-    _C.filtered_bwd(logits, target, temperature, info, kidx, kp, g, grad)
+    _C.filtered_bwd(logits, target, temperature, info, kidx, kp, g, grad, top_k=top_k)
     return grad
 
 
@@ -136,6 +137,7 @@ class _FilteredRowLogprob(torch.autograd.Function):
         if not inference_only:
             ctx.save_for_backward(logits, target, info, kidx, kp)
             ctx.temperature = float(temperature)
+            ctx.top_k = int(top_k)
             ctx.temperature_node = _temperature_node(logits)
         return out
 
@@ -299,6 +301,7 @@ def _run_filtered(ctx, logits, target, top_k, top_p, inference_only):
         # the reference filters these logits in their own dtype (model_utils.py:409)
         info, kidx, kp = _C.filtered_fwd(logits, target, 1.0, _k(top_k), _p(top_p), out)
         saved = (logits, target, info, kidx, kp)
+        ctx.top_k = _k(top_k)
         ctx.temperature_node = _temperature_node(logits) if not inference_only else None
     else:
         stats = torch.empty((B, S, 2), dtype=torch.float32, device=logits.device)
