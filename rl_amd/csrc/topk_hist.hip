@@ -194,6 +194,12 @@ __device__ double run_error_bound(uint32_t n, double p, double X0, double X1) {
   return (double)n * 0.5 * u;
 }
 
+// Whether the non-negative integer-valued double v is even (every double of
+// 2^53 or more is).
+__device__ __forceinline__ bool even_int(double v) {
+  return v >= 9007199254740992.0 || (((uint64_t)v) & 1u) == 0u;
+}
+
 // n additions S <- fl32(S + p) of one value p >= 0.  Returns true when a
 // partial sum reaches B (S >= B); *at is then the 1-based addition that did.
 // Inside the binade [2^e, 2^(e+1)) of S every addition adds p rounded to the
@@ -223,9 +229,9 @@ __device__ bool seq_add_run(float& S, float p, uint32_t n, float B, uint32_t* at
       d = q;
     } else if (q - fq != 0.5) {
       d = (q - fq < 0.5) ? fq : fq + 1.0;
-    } else if (fmod(Su, 2.0) == 0.0) {
+    } else if (even_int(Su)) {
       // a tie from an even multiple: rounding to even keeps S even
-      d = (fmod(fq, 2.0) == 0.0) ? fq : fq + 1.0;
+      d = even_int(fq) ? fq : fq + 1.0;
     } else {
       S = S + p;  // a tie from an odd multiple rounds up to an even one
       ++done;
@@ -829,9 +835,9 @@ __global__ __launch_bounds__(kHT) void filter_hist_kernel(FilterParams P, int al
 // consumers that walk the row in index order, so the row is read once; the
 // target's rank is counted only when its value is the cut value.  No kept
 // list is written (flags bit 2): the backward rewrites such rows whole.
-// Rows it cannot finish (a count of 65536 or more, more than kEntCap occupied
-// keys, a 16-bit cut the rounding bound leaves undecided) are flagged
-// (flags bit 0) for filter_hist_kernel.
+// A 16-bit cut that the rounding bound leaves undecided is walked exactly over
+// the list by one wave.  Rows it cannot finish (a count of 65536 or more, more
+// than kEntCap occupied keys) are flagged (flags bit 0) for filter_hist_kernel.
 constexpr int kPadWords = kHistWords + kHistWords / 32;  // one pad word per 32
 constexpr int kEntCap = kPadWords / 3;                     // 12-byte entries over the same bytes
 
@@ -850,6 +856,8 @@ struct CompactShared {
   int first_lo, first_hi;
   uint32_t ent_lo, pos_lo, ent_hi, pos_hi;
   int fail;
+  int walk_hit;
+  uint32_t walk_ent, walk_pos;
 };
 
 __device__ __forceinline__ uint32_t padded(uint32_t L) { return L + (L >> 5); }
@@ -1139,18 +1147,82 @@ __global__ __launch_bounds__(kHT) void filter_compact_kernel(FilterParams P, int
       const bool certain = sh.fail == 0 &&
                            ((none_lo && none_hi) ||
                             (!none_lo && !none_hi && sh.ent_lo == sh.ent_hi && sh.pos_lo == sh.pos_hi));
-      if (!certain) {
-        // the exact sequence is walked by filter_hist_kernel
-        if (tid == 0) {
-          RowInfo ri{};
-          ri.flags = 1;
-          P.info[row] = ri;
+      if (certain) {
+        have_cut = !none_hi;
+        cut_ent = sh.ent_hi;
+        cut_pos = sh.pos_hi;
+      } else {
+        // the exact sequence, one wave, 64 entries at a time: a group whose
+        // additions are all exact and stay inside S's binade below the
+        // threshold is added at once, the others entry by entry (a run of one
+        // value in closed form)
+        __syncthreads();  // every thread has read the certification's results
+        if (tid < 64) {
+          const int lane = tid;
+          float S = 0.f;
+          bool hit = false;
+          uint32_t hk = 0, hp = 0;
+          for (uint32_t g0 = thr; g0 < N && !hit; g0 += 64u) {
+            const uint32_t j = g0 + (uint32_t)lane;
+            const uint32_t n = j < N ? cnt(j) : 0u;
+            const float p = n ? (float)pmass(j) : 0.f;
+            int l0 = 0;  // first lane of the group not added yet
+            while (l0 < 64 && !hit) {
+              if (S > 0.f) {
+                // inside S's binade (ulp u) every addition adds p rounded to
+                // a multiple of u, the same for every S there unless p / u
+                // ends in exactly one half (then the rounding depends on S's
+                // parity): lanes l0.. up to the first such tie, the first
+                // that would leave the binade or reach the threshold, are
+                // added at once
+                int eS = ilogbf(S);
+                if (eS < -126) eS = -126;
+                const int eu = eS - 23;
+                const double q = ldexp((double)p, -eu);
+                const double fq = floor(q);
+                const bool mine = lane >= l0;
+                const bool tie = mine && n != 0u && q - fq == 0.5;
+                const double units = mine ? (double)n * ((q - fq) < 0.5 ? fq : fq + 1.0) : 0.0;
+                double incl = units;
+#pragma unroll
+                for (int o = 1; o < 64; o <<= 1) {
+                  const double v = __shfl_up(incl, o, 64);
+                  if (lane >= o) incl += v;
+                }
+                const double Su = ldexp((double)S, -eu) + incl;  // in units of u
+                const bool bad = mine && (tie || Su >= 16777216.0 || ldexp(Su, eu) >= Bd);
+                const uint64_t badm = __ballot(bad);
+                const int lb = badm ? __ffsll((long long)badm) - 1 : 64;
+                if (lb > l0) {
+                  const double s_at = __shfl(Su, lb - 1, 64);
+                  S = (float)ldexp(s_at, eu);
+                  l0 = lb;
+                  continue;
+                }
+              }
+              // lane l0 alone: a tie, a binade crossing, the threshold, or S == 0
+              const uint32_t nl = (uint32_t)__builtin_amdgcn_readlane((int)n, l0);
+              const float pl = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), l0));
+              uint32_t at = 0;
+              if (nl != 0u && seq_add_run(S, pl, nl, Bthr, &at)) {
+                hit = true;
+                hk = g0 + (uint32_t)l0;
+                hp = at;
+              }
+              ++l0;
+            }
+          }
+          if (lane == 0) {
+            sh.walk_hit = hit ? 1 : 0;
+            sh.walk_ent = hk;
+            sh.walk_pos = hp;
+          }
         }
-        return;
+        __syncthreads();
+        have_cut = sh.walk_hit != 0;
+        cut_ent = sh.walk_ent;
+        cut_pos = sh.walk_pos;
       }
-      have_cut = !none_hi;
-      cut_ent = sh.ent_hi;
-      cut_pos = sh.pos_hi;
     }
   }
 
