@@ -5,11 +5,11 @@ ChunkedDistributedHiddenStatesToLogprobs at TP=1 (reference
 nemo_rl/distributed/model_utils.py:2576-2745) and
 from_parallel_hidden_states_to_logprobs (model_utils.py:2541-2569).
 
-The reference's logits are the bf16 output of a bf16 matmul: an fp32 sum of
-products, rounded once to bf16.  Here the sum is taken exactly (float64) and
-rounded once to bf16 (``logits_bf16``); a GPU's fp32 sum of the same products
-can land on the other side of a bf16 rounding boundary, so individual logits
-may differ by one bf16 ulp.  The backward follows the reference in float64
+The reference's logits are the output of a matmul in the inputs' dtype: an
+fp32 sum of products, rounded once to that dtype.  Here the sum is taken
+exactly (float64) and rounded once to the dtype (``logits_bf16``); a GPU's fp32
+sum of the same products can land on the other side of a rounding boundary, so
+individual logits may differ by one ulp of the dtype.  The backward follows the reference in float64
 from those logits: ``grad_input = (onehot - softmax) * g`` (model_utils.py:2682-2700),
 ``dH = grad_input . W`` (2701-2703), ``dW = sum over chunks of H^T . grad_input``
 (2704-2716).
@@ -25,9 +25,10 @@ from oracle.logprob import _masks
 
 
 def logits_bf16(hidden: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
-    """[S, B, H] x [V, H] -> [B, S, V] float32 holding bf16-rounded exact products."""
+    """[S, B, H] x [V, H] -> [B, S, V] float32 holding the exact products rounded once to
+    the inputs' dtype (the reference's matmul output dtype: bf16, fp16 or fp32)."""
     x = torch.matmul(hidden.double(), weight.double().t())  # [S, B, V]
-    return x.to(torch.bfloat16).float().transpose(0, 1).contiguous()
+    return x.to(hidden.dtype).float().transpose(0, 1).contiguous()
 
 
 def hidden_state_logprobs(

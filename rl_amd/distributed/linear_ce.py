@@ -18,6 +18,12 @@ is ``[V, H]``; targets are ``[B, S]``.
   and ``dW += G^T . H`` are plain library GEMMs with fp32 accumulation (``dW``
   accumulated in fp32 across blocks and rounded once, by the GEMM itself when
   there is one block; the reference adds each chunk into a bf16 buffer).
+* fp16 and fp32 hidden states and weights take the reference's chunked shape
+  instead: per chunk of sequence positions the logits are one library GEMM in
+  the input dtype (the reference's ``torch.matmul`` output), and the row
+  kernels of the logits path (``mirl_logprob_fwd`` / ``mirl_logprob_bwd``)
+  form the logprobs and, in place, the logits gradient; ``dH`` and ``dW`` are
+  library GEMMs over it, ``dW`` accumulated in fp32 across chunks.
 """
 
 from __future__ import annotations
@@ -75,6 +81,10 @@ class ChunkedDistributedHiddenStatesToLogprobs(torch.autograd.Function):
             weight = weight.contiguous()
         if target.dtype != torch.int64:
             target = target.long()
+        if hidden.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+            return _chunked_forward(ctx, hidden, target, weight, vocab_start_index, vocab_end_index,
+                                    chunk_size, inference_only)
+        ctx.chunked = False
         h2 = hidden.view(S * B, H)
         out = torch.empty((B, S), dtype=torch.float32, device=hidden.device)
         stats = None
@@ -91,6 +101,8 @@ class ChunkedDistributedHiddenStatesToLogprobs(torch.autograd.Function):
     @staticmethod
     def backward(ctx: Any, *grad_outputs: torch.Tensor):  # type: ignore[override]
         (grad_output,) = grad_outputs
+        if ctx.chunked:
+            return _chunked_backward(ctx, grad_output)
         hidden, target, weight, stats = ctx.saved_tensors
         vs, ve = ctx.vocab
         S, B, H = hidden.shape
@@ -172,6 +184,71 @@ class ChunkedDistributedHiddenStatesToLogprobs(torch.autograd.Function):
         grad_h = dH.view(S, B, H) if need_h else None
         grad_w = (dW if dW.dtype == weight.dtype else dW.to(weight.dtype)) if need_w else None
         return grad_h, None, grad_w, None, None, None, None, None
+
+
+def _chunks(S: int, chunk_size: Optional[int]) -> list[tuple[int, int]]:
+    cs = S if chunk_size is None else chunk_size
+    return [(c0, min(S, c0 + cs)) for c0 in range(0, S, cs)] if S > 0 else []
+
+
+def _chunked_forward(ctx, hidden, target, weight, vs, ve, chunk_size, inference_only):
+    """fp16 / fp32: per chunk of positions, logits = hidden[c] . weight^T in the input
+    dtype (one library GEMM, [c, B, V]), then the logprob row kernel over them viewed
+    as [B, c, V] (reference model_utils.py:2608-2630)."""
+    S, B, H = hidden.shape
+    dev = hidden.device
+    out = torch.empty((B, S), dtype=torch.float32, device=dev)
+    # the saved row statistics: chunk [c0, c1) is the contiguous [B, c1 - c0, 2]
+    # block at offset 2 * B * c0
+    stats = None if inference_only else torch.empty(2 * B * S, dtype=torch.float32, device=dev)
+    for c0, c1 in _chunks(S, chunk_size):
+        logits = torch.matmul(hidden[c0:c1], weight.t())  # [c, B, V]
+        out_c = torch.empty((B, c1 - c0), dtype=torch.float32, device=dev)
+        st_c = None if stats is None else stats[2 * B * c0 : 2 * B * c1].view(B, c1 - c0, 2)
+        _C.logprob_fwd(logits.permute(1, 0, 2), target[:, c0:c1], vs, ve, out_c, st_c)
+        out[:, c0:c1] = out_c
+        del logits
+    ctx.chunked = True
+    if not inference_only:
+        ctx.save_for_backward(hidden, target, weight, stats)
+        ctx.vocab = (int(vs), int(ve))
+        ctx.chunk_size = None if chunk_size is None else int(chunk_size)
+    return out
+
+
+def _chunked_backward(ctx, grad_output):
+    """fp16 / fp32 backward (reference model_utils.py:2647-2745): per chunk the logits
+    are recomputed by the library GEMM and the logprob backward kernel overwrites them
+    with (onehot - softmax) * g in the input dtype; dH = G . W per chunk and
+    dW = sum over chunks of G^T . H, accumulated in fp32."""
+    hidden, target, weight, stats = ctx.saved_tensors
+    vs, ve = ctx.vocab
+    S, B, H = hidden.shape
+    V = weight.shape[0]
+    dev = hidden.device
+    if grad_output.dtype != torch.float32:
+        grad_output = grad_output.float()
+    need_h, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[2]
+    dH = torch.empty_like(hidden) if need_h else None
+    dW = torch.zeros((V, H), dtype=torch.float32, device=dev) if need_w else None
+    for c0, c1 in _chunks(S, ctx.chunk_size):
+        logits = torch.matmul(hidden[c0:c1], weight.t())  # [c, B, V]
+        lv = logits.permute(1, 0, 2)
+        st_c = stats[2 * B * c0 : 2 * B * c1].view(B, c1 - c0, 2)
+        _C.logprob_bwd(lv, target[:, c0:c1], vs, ve, st_c, grad_output[:, c0:c1],
+                       lv)  # the gradient overwrites the logits
+        if need_h:
+            torch.matmul(logits, weight, out=dH[c0:c1])
+        if need_w:
+            g2 = logits.reshape(-1, V)
+            h2 = hidden[c0:c1].reshape(-1, H)
+            if weight.dtype == torch.float32:
+                torch.addmm(dW, g2.t(), h2, out=dW)
+            else:
+                torch.addmm(dW, g2.t(), h2, out_dtype=torch.float32, out=dW)
+        del logits
+    grad_w = (dW if dW.dtype == weight.dtype else dW.to(weight.dtype)) if need_w else None
+    return dH, None, grad_w, None, None, None, None, None
 
 
 _BLOCK_CHUNKS = 4  # chunks of active rows per backward block

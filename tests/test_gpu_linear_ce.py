@@ -175,9 +175,9 @@ def test_unaligned_hidden_sizes_and_sliced_weight(H):
 def test_errors():
     say("linear-ce errors")
     hidden, weight, target = _inputs(4, 2, 128, 50, seed=1)
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(RuntimeError):  # mixed dtypes: torch.matmul's own error, as in the reference
         ChunkedDistributedHiddenStatesToLogprobs.apply(
-            hidden.float().to(DEV), target.to(DEV), weight.float().to(DEV), 0, 50, None, None, True)
+            hidden.float().to(DEV), target.to(DEV), weight.to(DEV), 0, 50, None, None, True)
     with pytest.raises(ValueError):
         ChunkedDistributedHiddenStatesToLogprobs.apply(
             hidden.to(DEV), target.t().contiguous().to(DEV), weight.to(DEV), 0, 50, None, None, True)
@@ -209,3 +209,39 @@ def test_gradient_row_compaction(pattern):
         assert err <= 1e-2 * ref.abs().max().item(), (pattern, err)
     zero_rows = (g == 0).t()  # [S, B], the layout of dh
     assert not dh.cpu()[zero_rows].any()
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("S,B,H,V,chunk", [(37, 3, 128, 1000, 8), (16, 2, 64, 151936, None), (9, 3, 200, 3001, 4)])
+def test_fp16_fp32_forward_and_gradients(dtype, S, B, H, V, chunk):
+    """fp16 / fp32 inputs: per chunk a library GEMM in the input dtype, then the logprob row
+    kernels (the reference's chunked shape).  The oracle rounds the exact products to the
+    dtype; logprobs within 2e-3 (fp16) / 1e-5 (fp32) plus the target logit's last-ulp
+    rounding, dH and dW against the float64 oracle to 1e-2 (fp16, G rounded to fp16) /
+    1e-4 (fp32) of their largest magnitude."""
+    say("linear-ce", dtype, S, B, H, V, chunk)
+    g0 = torch.Generator().manual_seed(S * V + H)
+    hidden = torch.randn(S, B, H, generator=g0).to(dtype)
+    weight = (torch.randn(V, H, generator=g0) * (1.5 / H**0.5)).to(dtype)
+    target = torch.randint(0, V + 50, (B, S), generator=g0)  # some targets outside the slice
+    g = torch.randn(B, S, generator=g0)
+    g[:, :2] = 0.0
+    ref = hidden_state_logprobs(hidden, target, weight, 0, V)
+    h = hidden.to(DEV).requires_grad_(True)
+    w = weight.to(DEV).requires_grad_(True)
+    lp = ChunkedDistributedHiddenStatesToLogprobs.apply(h, target.to(DEV), w, 0, V, chunk, None, False)
+    assert lp.dtype == torch.float32 and lp.shape == (B, S)
+    outside = target >= V
+    assert torch.all(lp.detach().cpu()[outside] == 0)
+    eps = 2.0**-10 if dtype == torch.float16 else 2.0**-22
+    base = 2e-3 if dtype == torch.float16 else 1e-5
+    x_t = _target_logits(hidden, weight, target.clamp(max=V - 1))
+    diff = (lp.detach().cpu().double() - ref.double()).abs()
+    assert torch.all(diff[~outside] <= base + x_t[~outside].abs() * eps), diff.max().item()
+    dh, dw = torch.autograd.grad(lp, [h, w], g.to(DEV))
+    assert dh.dtype == dtype and dw.dtype == dtype
+    rdh, rdw, _ = hidden_state_logprob_grads(hidden, target, weight, 0, V, g)
+    rel = 1e-2 if dtype == torch.float16 else 1e-4
+    for got, want in ((dh, rdh), (dw, rdw)):
+        err = (got.cpu().double() - want).abs().max().item()
+        assert err <= rel * want.abs().max().item(), (err, want.abs().max().item())
