@@ -648,7 +648,9 @@ def bench_workload(args) -> None:
                                                          chunk_size=256)
             return torch.autograd.grad(lp, [hidden, weight], g)
 
-        ms_step, ms = _timed(step, args.steps, args.warmup, ["mirl_linear_ce_fwd", "mirl_linear_ce_grad"])
+        ms_step, ms = _timed(step, args.steps, args.warmup,
+                             ["mirl_linear_ce_fwd", "mirl_linear_ce_grad", "mirl_gemm_bf16_abt",
+                              "mirl_transpose_bf16", "mirl_sum_splits_bf16"])
         rows = B * (S - 1)
         gemm = 2.0 * S * B * H * V  # one [S*B, H] x [H, V] product
         # the backward runs the rows with a non-zero upstream gradient, in blocks of
@@ -667,6 +669,11 @@ def bench_workload(args) -> None:
         extra["tflops_step"] = (gemm + 3 * gemm_act) / (ms_step * 1e-3) / 1e12
         extra["grad_kernel_ms_per_step"] = grad_ms
         extra["grad_kernel_tflops"] = gemm_act / (grad_ms * 1e-3) / 1e12 if grad_ms > 0 else None
+        # dH and dW: two products of 2 * active * H * V each on mirl_gemm_bf16_abt
+        # (average launch x launches per step: one dH and one dW per block)
+        gemm_ms = ms.get("mirl_gemm_bf16_abt", 0.0) * 2 * grad_chunks
+        extra["dh_dw_gemm_ms_per_step"] = gemm_ms
+        extra["dh_dw_gemm_tflops"] = 2 * gemm_act / (gemm_ms * 1e-3) / 1e12 if gemm_ms > 0 else None
         step_bytes = None
         cfg = {"workload": "hidden_state_logprobs_fwd_bwd", "hidden": [S, B, H], "weight": [V, H],
                "chunk_size": 256, "next_token_rows": rows, "active_rows": active,

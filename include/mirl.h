@@ -420,7 +420,10 @@ int mirl_linear_ce_fwd(const void* hidden, int64_t T, int64_t H, int64_t ldh,
  *   grad_logits[r - row0, v] = bf16((onehot(t')[v] - exp((x[r, v] - m) - logsum)) * g[b, s])
  * (row stride ldg >= V).  Tiles whose rows all have g == 0 are written as zeros
  * without the GEMM.  The hidden-state and weight gradients are the products
- * grad_logits . weight and grad_logits^T . hidden.
+ * grad_logits . weight and grad_logits^T . hidden.  When grad_logits_t is not
+ * NULL it also receives the transpose, grad_logits_t[v, r - row0], for the
+ * 256-row tiles covering the range (rows past row0 + nrows as zeros; row
+ * stride ldgt >= nrows rounded up to 256, a multiple of 8, 16-byte aligned).
  *
  * Replaces: the per-chunk logits recompute, softmax and one-hot gradient of
  * ChunkedDistributedHiddenStatesToLogprobs.backward
@@ -432,7 +435,38 @@ int mirl_linear_ce_grad(const void* hidden, int64_t T, int64_t H, int64_t ldh,
                         int64_t vocab_start, int64_t vocab_end, const float* row_stats,
                         const float* grad_out, int64_t g_stride_b, int64_t g_stride_s,
                         int64_t row0, int64_t nrows, void* grad_logits, int64_t ldg,
-                        void* stream);
+                        void* grad_logits_t, int64_t ldgt, void* stream);
+
+/*
+ * C = A . B^T for bf16 A [M, K] and B [N, K] (row strides lda, ldb, multiples
+ * of 8 elements; K a multiple of 128; 16-byte aligned), with fp32
+ * accumulation on the MFMA units (the tile loop of mirl_linear_ce_fwd):
+ *   Cb != NULL: Cb[m, n] = bf16(C[m, n])          (row stride ldcb);
+ *   else:       C[s, m, n] = the product over the s-th of k_splits ranges of
+ *               K ([k_splits][M][ldc] fp32), or C[m, n] += C when accumulate
+ *               (k_splits = 1).
+ * The backward of the hidden-state logprobs forms dH = G . W and
+ * dW = G^T . H with it, from G, its transpose and transposed copies of W and H.
+ *
+ * Replaces: the dH and dW matmuls of ChunkedDistributedHiddenStatesToLogprobs.backward
+ * (nemo_rl/distributed/model_utils.py:2701-2716).
+ */
+int mirl_gemm_bf16_abt(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M,
+                       int64_t N, int64_t K, int64_t k_splits, float* C, int64_t ldc,
+                       int accumulate, void* Cb, int64_t ldcb, void* stream);
+
+/* out[m, n] = bf16(sum_s part[s, m, n]) summed in s order (part [k_splits][M][ld] fp32,
+ * out row stride ldo): the splits of mirl_gemm_bf16_abt.
+ * Replaces: part of the dH matmul above (model_utils.py:2701-2703). */
+int mirl_sum_splits_bf16(const float* part, int64_t k_splits, int64_t M, int64_t N,
+                         int64_t ld, void* out, int64_t ldo, void* stream);
+
+/* dst[c, r] = src[r, c] (bf16) for r < R, c < C, and 0 for R <= r < R_pad
+ * (src row stride lds, dst row stride ldd >= R_pad): the transposed operands of
+ * the hidden-state backward.
+ * Replaces: the transposes inside the dH / dW matmuls (model_utils.py:2701-2716). */
+int mirl_transpose_bf16(const void* src, int64_t R, int64_t C, int64_t lds, void* dst,
+                        int64_t ldd, int64_t R_pad, void* stream);
 
 /* ---------------------------------------------------------------------- */
 /* ClippedPG loss epilogue                                                  */

@@ -217,8 +217,13 @@ SIGNATURES = {
     "mirl_linear_ce_grad": (
         _I,
         [_P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _I64, _P, _P, _I64,
-         _I64, _I64, _I64, _P, _I64, _P],
+         _I64, _I64, _I64, _P, _I64, _P, _I64, _P],
     ),
+    "mirl_gemm_bf16_abt": (
+        _I, [_P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _I, _P, _I64, _P]
+    ),
+    "mirl_sum_splits_bf16": (_I, [_P, _I64, _I64, _I64, _I64, _P, _I64, _P]),
+    "mirl_transpose_bf16": (_I, [_P, _I64, _I64, _I64, _P, _I64, _I64, _P]),
     "mirl_top_k_top_p_mask": (
         _I,
         [_P, _I, _I64, _I64, _I64, _I, ctypes.c_double, _I, _P, _P, _P, _P, _I64, _P, _I64, _P],
@@ -1160,8 +1165,10 @@ def linear_ce_grad(
     grad_out: torch.Tensor,
     row0: int,
     grad_logits: torch.Tensor,
+    grad_logits_t: Optional[torch.Tensor] = None,
 ) -> None:
-    """grad_logits[i, :] = bf16((onehot(t) - softmax(logits)) * g) for rows row0 .. row0 + n - 1."""
+    """grad_logits[i, :] = bf16((onehot(t) - softmax(logits)) * g) for rows row0 .. row0 + n - 1;
+    grad_logits_t (or None) receives the transpose [V, >= round_up(n, 256)]."""
     dev = _require_gpu(hidden2d, weight, target, stats, grad_out, grad_logits)
     _check_linear_ce(hidden2d, weight)
     T, H = hidden2d.shape
@@ -1175,9 +1182,55 @@ def linear_ce_grad(
         int(bsz), target.data_ptr(), target.stride(0), target.stride(1), int(vocab_start),
         int(vocab_end), stats.data_ptr(), grad_out.data_ptr(), grad_out.stride(0),
         grad_out.stride(1), int(row0), int(n), grad_logits.data_ptr(), grad_logits.stride(0),
-        _stream(dev),
+        _ptr(grad_logits_t), 0 if grad_logits_t is None else grad_logits_t.stride(0), _stream(dev),
     )
     _check(st, "mirl_linear_ce_grad")
+
+
+def gemm_bf16_abt(a: torch.Tensor, b: torch.Tensor, k: int, out: torch.Tensor, k_splits: int = 1,
+                  accumulate: bool = False) -> None:
+    """out = a[:, :k] . b[:, :k]^T with fp32 accumulation on the MFMA units.
+
+    a [M, >=k], b [N, >=k] bf16 (unit stride, rows multiples of 8 elements, k a
+    multiple of 128); out bf16 [M, N] (k_splits 1, no accumulation), fp32 [M, N]
+    (out = or +=), or fp32 [k_splits, M, N] (one partial product per k range)."""
+    dev = _require_gpu(a, b, out)
+    _require(a.dtype == torch.bfloat16 and b.dtype == torch.bfloat16, "bf16 operands")
+    _require(a.stride(-1) == 1 and b.stride(-1) == 1 and out.stride(-1) == 1, "unit stride on the last dim")
+    M, N = a.shape[0], b.shape[0]
+    if out.dtype == torch.bfloat16:
+        cb, ldcb, c, ldc = out.data_ptr(), out.stride(0), None, 0
+    else:
+        _require(out.dtype == torch.float32, "out is bf16 or fp32")
+        cb, ldcb, c, ldc = None, 0, out.data_ptr(), out.stride(-2)
+    st = _launch(
+        "mirl_gemm_bf16_abt", dev, a.data_ptr(), a.stride(0), b.data_ptr(), b.stride(0), M, N,
+        int(k), int(k_splits), c, ldc, int(bool(accumulate)), cb, ldcb, _stream(dev),
+    )
+    _check(st, "mirl_gemm_bf16_abt")
+
+
+def sum_splits_bf16(part: torch.Tensor, out: torch.Tensor) -> None:
+    """out [M, N] bf16 = sum over dim 0 of part [S, M, N] fp32, in order."""
+    dev = _require_gpu(part, out)
+    S, M, N = part.shape
+    _require(part.is_contiguous() and out.dtype == torch.bfloat16 and out.stride(-1) == 1,
+             "contiguous fp32 partials and a bf16 output")
+    st = _launch("mirl_sum_splits_bf16", dev, part.data_ptr(), S, M, N, N, out.data_ptr(),
+                 out.stride(0), _stream(dev))
+    _check(st, "mirl_sum_splits_bf16")
+
+
+def transpose_bf16(src: torch.Tensor, rows: int, dst: torch.Tensor) -> None:
+    """dst[c, r] = src[r, c] for r < rows, zero for rows <= r < dst.shape[1]."""
+    dev = _require_gpu(src, dst)
+    _require(src.dtype == torch.bfloat16 and dst.dtype == torch.bfloat16, "bf16 tensors")
+    _require(src.stride(-1) == 1 and dst.stride(-1) == 1, "unit stride on the last dim")
+    C = src.shape[1]
+    _require(dst.shape[0] >= C, "dst has a row per source column")
+    st = _launch("mirl_transpose_bf16", dev, src.data_ptr(), int(rows), C, src.stride(0),
+                 dst.data_ptr(), dst.stride(0), dst.shape[1], _stream(dev))
+    _check(st, "mirl_transpose_bf16")
 
 
 # ---------------------------------------------------------------------------

@@ -91,7 +91,7 @@ __device__ __forceinline__ float bf16_round(float f) {
   return __uint_as_float((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f) << 16);
 }
 
-enum LceMode { kFwd = 0, kGrad = 1 };
+enum LceMode { kFwd = 0, kGrad = 1, kGemm = 2 };
 
 struct LceParams {
   const uint16_t* h;  // [T, Hd] bf16, row stride ldh
@@ -113,6 +113,16 @@ struct LceParams {
   int64_t gsb, gss;
   uint16_t* G;          // [nrows, V] bf16, row stride ldg
   int64_t ldg;
+  uint16_t* Gt;         // or null: G transposed, [V, ldgt] bf16 (column r - row0 of row v)
+  int64_t ldgt;
+  // plain GEMM (kGemm): C = A . B^T with A = h [nrows, Hd], B = w [V, Hd]; the
+  // hidden dimension is split into n_ks ranges of kb_len (C holds n_ks
+  // partial products [n_ks][nrows][ldc]), or Cb receives bf16(C) (n_ks = 1)
+  int64_t n_ks, kb_len;
+  float* C;
+  uint16_t* Cb;
+  int64_t ldc;
+  int accumulate;       // C += A . B^T instead of C = A . B^T (n_ks = 1)
 };
 
 template <int MODE>
@@ -131,10 +141,14 @@ void lce_tile_kernel(LceParams P) {
   // contiguous run of a grouped order (kGroupM row tiles sweep the vocabulary
   // together): the ~32 workgroups resident on an XCD then cover about
   // kGroupM row tiles x 4 column tiles and share their H and W reads in L2.
-  const int64_t ntiles = P.n_mt * P.n_nt;
+  // (A plain GEMM's hidden-dimension splits are the outermost index.)
+  const int64_t tiles2 = P.n_mt * P.n_nt;
+  const int64_t ntiles = tiles2 * (MODE == kGemm ? P.n_ks : 1);
   const int64_t per_xcd = (ntiles + kXcds - 1) / kXcds;
-  const int64_t gi = (int64_t)(blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
-  if (gi >= ntiles) return;
+  const int64_t gi0 = (int64_t)(blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
+  if (gi0 >= ntiles) return;
+  const int64_t ks = gi0 / tiles2;
+  const int64_t gi = gi0 - ks * tiles2;
   const int64_t per_group = (int64_t)kGroupM * P.n_nt;
   const int64_t group = gi / per_group;
   const int64_t first_m = group * kGroupM;
@@ -153,7 +167,7 @@ void lce_tile_kernel(LceParams P) {
 
   // per-row metadata of the tile (kThreads == kBM: one row per thread)
   float my_g = 0.f;
-  {
+  if constexpr (MODE != kGemm) {
     const int64_t r = m0 + tid;
     int tc = -1;
     float lm = 0.f, ll = 0.f;
@@ -195,6 +209,10 @@ void lce_tile_kernel(LceParams P) {
           for (int e = 0; e < 8 && c + e < P.V; ++e) dst[e] = 0;
         }
       }
+      if (P.Gt != nullptr && n0 + tid < P.V) {
+        uint16_t* dt = P.Gt + (n0 + tid) * P.ldgt + (m0 - P.row0);
+        for (int r8 = 0; r8 < kBM / 8; ++r8) *reinterpret_cast<vu4*>(dt + r8 * 8) = vu4{0u, 0u, 0u, 0u};
+      }
       return;
     }
   }
@@ -211,13 +229,18 @@ void lce_tile_kernel(LceParams P) {
   // it fetches global chunk (l % 8) ^ ((row / 2) % 8) of that row (the inverse
   // of the lds_off swizzle).  Each wave issues kDmaPerWave loads of H and of W
   // per stage.
-  const int nst = (int)(P.Hd / kSK);  // a multiple of kStages
+  // this tile's range of the hidden dimension (the whole of it but for split GEMMs)
+  const int64_t kbase = (MODE == kGemm) ? ks * P.kb_len : 0;
+  const int64_t klen = (MODE == kGemm) ? ((P.Hd - kbase < P.kb_len) ? P.Hd - kbase : P.kb_len) : P.Hd;
+  const int nst = (int)(klen / kSK);  // a multiple of kStages
   const int64_t a_rows = (row_end - m0 < kBM) ? (row_end - m0) : kBM;
   const int64_t b_rows = (P.V - n0 < kBN) ? (P.V - n0) : kBN;
   const __amdgpu_buffer_rsrc_t rsrc_a = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(P.h + m0 * P.ldh), 0, (int)(a_rows * P.ldh * 2), 0x00020000);
+      const_cast<uint16_t*>(P.h + m0 * P.ldh + kbase), 0, (int)((a_rows * P.ldh - kbase) * 2),
+      0x00020000);
   const __amdgpu_buffer_rsrc_t rsrc_b = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(P.w + n0 * P.ldw), 0, (int)(b_rows * P.ldw * 2), 0x00020000);
+      const_cast<uint16_t*>(P.w + n0 * P.ldw + kbase), 0, (int)((b_rows * P.ldw - kbase) * 2),
+      0x00020000);
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   int voff_a[kDmaPerWave], voff_b[kDmaPerWave];
 #pragma unroll
@@ -325,6 +348,30 @@ void lce_tile_kernel(LceParams P) {
   }
   step(t, S0{}, T_{}, F_{});
   step(t + 1, S1{}, F_{}, F_{});
+
+  if constexpr (MODE == kGemm) {
+    // ---- plain GEMM: the accumulators go straight to C ----
+    // accumulator v of lane l in MFMA tile (i, j) is C[(v / 4) * 8 + (l / 32) * 4 + v % 4][l % 32];
+    // lanes 0-31 (32-63) store 32 consecutive columns of one row
+    const int half_g = lane >> 5, col_g = lane & 31;
+#pragma unroll
+    for (int i = 0; i < kTM; ++i)
+#pragma unroll
+      for (int j = 0; j < kTN; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int64_t row = m0 + wm * kWM + i * 32 + (v >> 2) * 8 + half_g * 4 + (v & 3);
+          const int64_t col = n0 + wn * kWN + j * 32 + col_g;
+          if (row >= row_end || col >= P.V) continue;
+          if (P.Cb != nullptr) {
+            P.Cb[row * P.ldc + col] = BF16::from_float(acc[i][j][v]);
+          } else {
+            float* c = P.C + (ks * P.nrows + row) * P.ldc + col;
+            *c = P.accumulate ? *c + acc[i][j][v] : acc[i][j][v];
+          }
+        }
+    return;
+  }
 
   // ---- epilogue: the tile goes through LDS as bf16, one row per thread ----
   //
@@ -434,7 +481,67 @@ void lce_tile_kernel(LceParams P) {
           dst[e] = (uint16_t)(wv[e >> 1] >> ((e & 1) * 16));
       }
     }
+    if (P.Gt != nullptr) {
+      // the transposed tile: thread t writes column t of the tile as 256
+      // consecutive elements of G^T row n0 + t (rows of G past its end are
+      // zeros, which the caller's padded reduction length relies on)
+      const int64_t col = n0 + tid;
+      if (col < P.V) {
+        uint16_t* dst = P.Gt + col * P.ldgt + (m0 - P.row0);
+        const uint16_t* x0 = reinterpret_cast<const uint16_t*>(stage_ptr(0));
+        const uint16_t* x1 = reinterpret_cast<const uint16_t*>(stage_ptr(1));
+#pragma unroll 4
+        for (int r8 = 0; r8 < kBM / 8; ++r8) {
+          uint32_t wv[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int ra = r8 * 8 + 2 * e, rb = ra + 1;
+            const uint32_t lo = (ra < kEpiRows ? x0 : x1)[xs_index(ra, tid)];
+            const uint32_t hi = (rb < kEpiRows ? x0 : x1)[xs_index(rb, tid)];
+            wv[e] = lo | (hi << 16);
+          }
+          *reinterpret_cast<vu4*>(dst + r8 * 8) = vu4{wv[0], wv[1], wv[2], wv[3]};
+        }
+      }
+    }
   }
+}
+
+// dst[c][r] = src[r][c] for r < R, c < C, and dst[c][r] = 0 for R <= r < Rp
+// (bf16; dst rows of stride ldd >= Rp).  64 x 64 tiles through LDS.
+__global__ __launch_bounds__(256) void transpose_bf16_kernel(const uint16_t* __restrict__ src,
+                                                             int64_t R, int64_t C, int64_t lds,
+                                                             uint16_t* __restrict__ dst,
+                                                             int64_t ldd, int64_t Rp,
+                                                             int64_t n_ct) {
+  __shared__ uint16_t tile[64][66];
+  const int64_t tr = blockIdx.x / n_ct, tc = blockIdx.x - tr * n_ct;
+  const int64_t r0 = tr * 64, c0 = tc * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+#pragma unroll 4
+  for (int k = 0; k < 16; ++k) {
+    const int64_t r = r0 + ty + 4 * k, c = c0 + tx;
+    tile[ty + 4 * k][tx] = (r < R && c < C) ? src[r * lds + c] : (uint16_t)0;
+  }
+  __syncthreads();
+#pragma unroll 4
+  for (int k = 0; k < 16; ++k) {
+    const int64_t c = c0 + ty + 4 * k, r = r0 + tx;
+    if (c < C && r < Rp) dst[c * ldd + r] = tile[tx][ty + 4 * k];
+  }
+}
+
+// out[m][n] = bf16(sum over s of part[s][m][n]), summed in split order.
+__global__ __launch_bounds__(256) void sum_splits_kernel(const float* __restrict__ part,
+                                                         int64_t n_ks, int64_t M, int64_t N,
+                                                         int64_t ld, uint16_t* __restrict__ out,
+                                                         int64_t ldo) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= M * N) return;
+  const int64_t m = i / N, n = i - m * N;
+  float acc = 0.f;
+  for (int64_t s = 0; s < n_ks; ++s) acc += part[(s * M + m) * ld + n];
+  out[m * ldo + n] = BF16::from_float(acc);
 }
 
 // Per row: combine the column-tile partials into the row's max and log-sum-exp,
@@ -552,7 +659,8 @@ extern "C" int mirl_linear_ce_grad(const void* hidden, int64_t T, int64_t Hd, in
                                    int64_t t_stride_s, int64_t vocab_start, int64_t vocab_end,
                                    const float* row_stats, const float* grad_out,
                                    int64_t g_stride_b, int64_t g_stride_s, int64_t row0,
-                                   int64_t nrows, void* grad_logits, int64_t ldg, void* stream) {
+                                   int64_t nrows, void* grad_logits, int64_t ldg,
+                                   void* grad_logits_t, int64_t ldgt, void* stream) {
   clear_error();
   if (int e = check_common(hidden, T, Hd, ldh, weight, V, ldw, target, bsz)) return e;
   MIRL_REQUIRE(row0 >= 0 && nrows >= 0 && row0 + nrows <= T, "row range [%lld, %lld) outside [0, %lld)",
@@ -561,6 +669,13 @@ extern "C" int mirl_linear_ce_grad(const void* hidden, int64_t T, int64_t Hd, in
   MIRL_REQUIRE(row_stats && grad_out && grad_logits, "null pointer argument");
   MIRL_REQUIRE(ldg >= V, "gradient row stride %lld is smaller than V=%lld", (long long)ldg,
                (long long)V);
+  // the transposed tiles cover whole 256-row tiles, written as 16-byte vectors
+  MIRL_REQUIRE(grad_logits_t == nullptr ||
+                   (ldgt >= ceil_div(nrows, kBM) * kBM && ldgt % 8 == 0 &&
+                    (reinterpret_cast<uintptr_t>(grad_logits_t) & 15u) == 0),
+               "transposed gradient: row stride %lld must cover %lld rows in whole 256-row tiles, "
+               "be a multiple of 8 elements and start 16-byte aligned",
+               (long long)ldgt, (long long)nrows);
   hipStream_t st = static_cast<hipStream_t>(stream);
   LceParams P{};
   P.h = static_cast<const uint16_t*>(hidden);
@@ -585,8 +700,93 @@ extern "C" int mirl_linear_ce_grad(const void* hidden, int64_t T, int64_t Hd, in
   P.gss = g_stride_s;
   P.G = static_cast<uint16_t*>(grad_logits);
   P.ldg = ldg;
+  P.Gt = static_cast<uint16_t*>(grad_logits_t);
+  P.ldgt = ldgt;
   const int64_t grid = ceil_div(P.n_mt * P.n_nt, kXcds) * kXcds;
   MIRL_REQUIRE(grid < (int64_t(1) << 31), "too many tiles");
   hipLaunchKernelGGL((lce_tile_kernel<kGrad>), dim3((unsigned)grid), dim3(kThreads), 0, st, P);
   return check_launch("mirl_linear_ce_grad");
+}
+
+extern "C" int mirl_gemm_bf16_abt(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M,
+                                  int64_t N, int64_t K, int64_t k_splits, float* C, int64_t ldc,
+                                  int accumulate, void* Cb, int64_t ldcb, void* stream) {
+  clear_error();
+  MIRL_REQUIRE(M >= 0 && N >= 0 && K > 0 && k_splits >= 1, "invalid shape M=%lld N=%lld K=%lld splits=%lld",
+               (long long)M, (long long)N, (long long)K, (long long)k_splits);
+  if (M == 0 || N == 0) return MIRL_OK;
+  MIRL_REQUIRE(A && B && (C || Cb), "null pointer argument");
+  const int64_t kstep = (int64_t)kStages * kSK;
+  MIRL_REQUIRE(K % kstep == 0, "reduction length %lld must be a multiple of %lld", (long long)K,
+               (long long)kstep);
+  const int64_t kb = ceil_div(ceil_div(K, k_splits), kstep) * kstep;
+  const int64_t n_ks = ceil_div(K, kb);
+  MIRL_REQUIRE(n_ks == k_splits,
+               "%lld splits of K=%lld in ranges of %lld leave %lld non-empty (choose a split count "
+               "that divides into whole 128-element ranges)",
+               (long long)k_splits, (long long)K, (long long)kb, (long long)n_ks);
+  MIRL_REQUIRE(Cb == nullptr || (n_ks == 1 && !accumulate),
+               "a bf16 output takes one split and no accumulation");
+  MIRL_REQUIRE(!accumulate || n_ks == 1, "accumulation takes one split");
+  MIRL_REQUIRE(lda % 8 == 0 && ldb % 8 == 0 && lda >= K && ldb >= K,
+               "row strides (%lld, %lld) must be multiples of 8 elements and >= K", (long long)lda,
+               (long long)ldb);
+  MIRL_REQUIRE((reinterpret_cast<uintptr_t>(A) & 15u) == 0 && (reinterpret_cast<uintptr_t>(B) & 15u) == 0,
+               "operands must be 16-byte aligned");
+  // buffer ranges of one 256-row tile are 32-bit byte counts
+  MIRL_REQUIRE(kBM * lda * 2 < (int64_t(1) << 31) && kBN * ldb * 2 < (int64_t(1) << 31),
+               "row strides (%lld, %lld) too large", (long long)lda, (long long)ldb);
+  MIRL_REQUIRE(M < (int64_t(1) << 31) && N < (int64_t(1) << 31), "sizes exceed 2^31-1");
+  MIRL_REQUIRE(ldc >= N || Cb != nullptr, "output row stride %lld is smaller than N=%lld",
+               (long long)ldc, (long long)N);
+  MIRL_REQUIRE(Cb == nullptr || ldcb >= N, "output row stride %lld is smaller than N=%lld",
+               (long long)ldcb, (long long)N);
+  LceParams P{};
+  P.h = static_cast<const uint16_t*>(A);
+  P.w = static_cast<const uint16_t*>(B);
+  P.ldh = lda;
+  P.ldw = ldb;
+  P.V = N;
+  P.Hd = K;
+  P.row0 = 0;
+  P.nrows = M;
+  P.n_mt = ceil_div(M, kBM);
+  P.n_nt = ceil_div(N, kBN);
+  P.n_ks = n_ks;
+  P.kb_len = kb;
+  P.C = C;
+  P.Cb = static_cast<uint16_t*>(Cb);
+  P.ldc = Cb != nullptr ? ldcb : ldc;
+  P.accumulate = accumulate;
+  const int64_t grid = ceil_div(P.n_mt * P.n_nt * n_ks, kXcds) * kXcds;
+  MIRL_REQUIRE(grid < (int64_t(1) << 31), "too many tiles");
+  hipLaunchKernelGGL((lce_tile_kernel<kGemm>), dim3((unsigned)grid), dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), P);
+  return check_launch("mirl_gemm_bf16_abt");
+}
+
+extern "C" int mirl_sum_splits_bf16(const float* part, int64_t k_splits, int64_t M, int64_t N,
+                                    int64_t ld, void* out, int64_t ldo, void* stream) {
+  clear_error();
+  MIRL_REQUIRE(M >= 0 && N >= 0 && k_splits >= 1 && ld >= N && ldo >= N, "invalid shape");
+  if (M == 0 || N == 0) return MIRL_OK;
+  MIRL_REQUIRE(part && out, "null pointer argument");
+  hipLaunchKernelGGL(sum_splits_kernel, dim3((unsigned)ceil_div(M * N, 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), part, k_splits, M, N, ld,
+                     static_cast<uint16_t*>(out), ldo);
+  return check_launch("mirl_sum_splits_bf16");
+}
+
+extern "C" int mirl_transpose_bf16(const void* src, int64_t R, int64_t C, int64_t lds, void* dst,
+                                   int64_t ldd, int64_t R_pad, void* stream) {
+  clear_error();
+  MIRL_REQUIRE(R >= 0 && C >= 0 && R_pad >= R && lds >= C && ldd >= R_pad, "invalid shape");
+  if (C == 0 || R_pad == 0) return MIRL_OK;
+  MIRL_REQUIRE(src && dst, "null pointer argument");
+  const int64_t n_rt = ceil_div(R_pad, 64), n_ct = ceil_div(C, 64);
+  MIRL_REQUIRE(n_rt * n_ct < (int64_t(1) << 31), "too many tiles");
+  hipLaunchKernelGGL(transpose_bf16_kernel, dim3((unsigned)(n_rt * n_ct)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(src), R, C,
+                     lds, static_cast<uint16_t*>(dst), ldd, R_pad, n_ct);
+  return check_launch("mirl_transpose_bf16");
 }

@@ -14,10 +14,12 @@ is ``[V, H]``; targets are ``[B, S]``.
 * backward: the rows with a non-zero upstream gradient are gathered (the
   others have a zero logits gradient: zero dH rows, nothing added to dW);
   per block of up to ``4 * chunk_size * B`` of those rows a kernel recomputes the logits
-  tiles and writes ``G = (onehot - softmax) * g`` in bf16, and ``dH = G . W``
-  and ``dW += G^T . H`` are plain library GEMMs with fp32 accumulation (``dW``
-  accumulated in fp32 across blocks and rounded once, by the GEMM itself when
-  there is one block; the reference adds each chunk into a bf16 buffer).
+  tiles and writes ``G = (onehot - softmax) * g`` in bf16 and its transpose, and
+  ``dH = G . W`` and ``dW += G^T . H`` run on the same MFMA tile loop
+  (``mirl_gemm_bf16_abt``) against transposed copies of W (kept while the weight
+  is unchanged) and of the active hidden rows, with fp32 accumulation (``dW``
+  accumulated in fp32 across blocks and rounded once, by the kernel itself
+  when there is one block; the reference adds each chunk into a bf16 buffer).
 * fp16 and fp32 hidden states and weights take the reference's chunked shape
   instead: per chunk of sequence positions the logits are one library GEMM in
   the input dtype (the reference's ``torch.matmul`` output), and the row
@@ -117,7 +119,7 @@ class ChunkedDistributedHiddenStatesToLogprobs(torch.autograd.Function):
         # Rows whose upstream gradient is exactly zero (prompt, padding) have a
         # zero logits gradient, so they add nothing to dW and their dH rows are
         # zero: only the active rows are gathered and run through the gradient
-        # kernel and both GEMMs (one host synchronisation for their count).
+        # kernel and both products (one host synchronisation for their count).
         g_rows = grad_output.t().reshape(T)  # row r = (s, b) is position s of sample b
         active = torch.nonzero(g_rows != 0).squeeze(1)
         n_act = active.numel()
@@ -128,55 +130,59 @@ class ChunkedDistributedHiddenStatesToLogprobs(torch.autograd.Function):
             if not compact:
                 h_a, bsz, tgt_a, st_a, g_a = h2, B, target, stats, grad_output
             else:
-                # + _K_ALIGN zero rows: dW's reduction length is rounded up to a
-                # multiple of _K_ALIGN over zero G rows (the library's kernels for
-                # such lengths measured 5% faster: 6.31 vs 6.63 ms at 5888 vs 5871)
-                h_a = torch.empty((n_act + _K_ALIGN, H), dtype=hidden.dtype, device=dev)
-                h_a[n_act:].zero_()
-                torch.index_select(h2, 0, active, out=h_a[:n_act])
+                h_a = torch.index_select(h2, 0, active)
                 bsz = 1
                 tgt_a = target.t().reshape(T).index_select(0, active).view(1, n_act)
                 st_a = stats.index_select(0, active)
                 g_a = g_rows.index_select(0, active).view(1, n_act)
-            # Blocks of up to 4 chunks of rows: the bf16 G buffer (4 * chunk_size * B
-            # rows) stays below one reference chunk's fp32 logits, softmax and
-            # one-hot temporaries, and fewer, larger blocks cut dW's fp32
-            # read-modify-write passes and give the GEMMs larger shapes.
-            rows = n_act if ctx.chunk_size is None else min(n_act, _BLOCK_CHUNKS * ctx.chunk_size * B)
-            G = torch.empty((_round_up(rows, _K_ALIGN) if compact else rows, V), dtype=torch.bfloat16,
-                            device=dev)
+            # Blocks of up to 4 chunks of rows (whole 256-row tiles): the bf16 G
+            # buffer stays below one reference chunk's fp32 logits, softmax and
+            # one-hot temporaries.
+            rows = n_act if ctx.chunk_size is None else min(
+                n_act, _round_up(_BLOCK_CHUNKS * ctx.chunk_size * B, 256))
+            Vp = _round_up(V, _K_ALIGN)
+            # G [rows, Vp] (columns past V zero: dH's padded reduction length)
+            G = torch.empty((rows, Vp), dtype=torch.bfloat16, device=dev)
+            if Vp > V:
+                G[:, V:].zero_()
+            # G^T [V, rows rounded to 256] and H^T of the active rows [H, n_act
+            # rounded to 256] for dW = (G^T) . (H^T)^T, zero past the rows
+            Gt = torch.empty((V, _round_up(rows, 256)), dtype=torch.bfloat16, device=dev) if need_w else None
+            hT = None
+            if need_w:
+                hT = torch.empty((H, _round_up(n_act, 256)), dtype=torch.bfloat16, device=dev)
+                _C.transpose_bf16(h_a, n_act, hT)
+            wT = _weight_transposed(weight, Vp) if need_h else None
             dH_a = dH if (need_h and n_act == T) else (
                 torch.empty((n_act, H), dtype=hidden.dtype, device=dev) if need_h else None)
-            # dH in pieces of one chunk of rows: the library picks a markedly
-            # slower kernel for some large, uneven row counts (measured 0.76 vs
-            # 1.33 PFLOP/s at 5871 vs 2048 rows of [*, 151936] x [151936, 4096]).
-            # A shorter last piece is moved back to end at the block's end and
-            # overlaps the previous one (its rows are recomputed, not added).
-            sub = rows if ctx.chunk_size is None else ctx.chunk_size * B
             hk_a, wk = _kernel_operand(h_a), _kernel_operand(weight)
+            one_block = rows >= n_act
+            dW32 = None
             for r0 in range(0, n_act, rows):
                 n = min(rows, n_act - r0)
                 Gc = G[:n]
-                _C.linear_ce_grad(hk_a, wk, bsz, tgt_a, vs, ve, st_a, g_a, r0, Gc)
+                _C.linear_ce_grad(hk_a, wk, bsz, tgt_a, vs, ve, st_a, g_a, r0, Gc, Gt)
                 if need_h:
-                    for q0 in range(0, n, sub):
-                        q0 = max(0, min(q0, n - sub))
-                        q1 = min(n, q0 + sub)
-                        torch.matmul(Gc[q0:q1], weight, out=dH_a[r0 + q0 : r0 + q1])
+                    # dH = G . W = G . (W^T)^T on the MFMA units, the reduction over
+                    # the vocabulary split so that the tiles fill the CUs
+                    splits = _dh_splits(n, H, Vp)
+                    part = torch.empty((splits, n, H), dtype=torch.float32, device=dev)
+                    _C.gemm_bf16_abt(Gc, wT, Vp, part, k_splits=splits)
+                    _C.sum_splits_bf16(part, dH_a[r0 : r0 + n])
+                    del part
                 if need_w:
-                    nk = n
-                    if compact:
-                        nk = _round_up(n, _K_ALIGN)
-                        G[n:nk].zero_()
-                    Gk, hk = G[:nk], h_a[r0 : r0 + nk]
-                    if rows >= n_act:
-                        # one block: the GEMM accumulates in fp32 and rounds once to the
-                        # weight dtype itself
-                        dW = torch.mm(Gk.t(), hk)
-                    elif dW is None:
-                        dW = torch.mm(Gk.t(), hk, out_dtype=torch.float32)
+                    nk = _round_up(n, _K_ALIGN)
+                    hb = hT[:, r0 : r0 + nk]
+                    if one_block:
+                        # one block: fp32 accumulation, rounded once to bf16 by the kernel
+                        dW = torch.empty((V, H), dtype=torch.bfloat16, device=dev)
+                        _C.gemm_bf16_abt(Gt, hb, nk, dW)
                     else:
-                        _accumulate_dw(dW, Gk, hk)
+                        if dW32 is None:
+                            dW32 = torch.empty((V, H), dtype=torch.float32, device=dev)
+                        _C.gemm_bf16_abt(Gt, hb, nk, dW32, accumulate=r0 > 0)
+            if dW32 is not None:
+                dW = dW32
             if need_h and n_act < T:
                 dH.index_copy_(0, active, dH_a)
         if need_w and dW is None:
@@ -278,9 +284,43 @@ def _round_up(n: int, m: int) -> int:
     return (n + m - 1) // m * m
 
 
-def _accumulate_dw(dW: torch.Tensor, G: torch.Tensor, h: torch.Tensor) -> None:
-    """dW += G^T . h with bf16 inputs and fp32 accumulation and output."""
-    torch.addmm(dW, G.t(), h, out_dtype=torch.float32, out=dW)
+def _dh_splits(n: int, H: int, K: int) -> int:
+    """Splits of dH's reduction length (each adds an fp32 partial product to read
+    back).  dH has few 256 x 256 tiles over a long reduction, so the count that
+    fills the last round of tiles over the 256 CUs best wins, the smaller on a
+    tie (measured on [5871, 151936] x [151936, 4096]: 1 split 7.62 ms, 2 6.09,
+    3 6.81, 4 6.23).  The kernel cuts K into ranges of round_up(ceil(K / s), 128);
+    only counts for which that gives exactly s ranges, each of at least 1024, qualify."""
+    tiles = ((n + 255) // 256) * ((H + 255) // 256)
+    best, best_eff = 1, tiles / (256 * -(-tiles // 256))
+    for s in range(2, 9):
+        kb = _round_up(-(-K // s), 128)
+        if kb < 1024 or -(-K // kb) != s:
+            continue
+        t = tiles * s
+        eff = t / (256 * -(-t // 256))
+        if eff > best_eff + 1e-9:
+            best, best_eff = s, eff
+    return best
+
+
+_WT_CACHE: dict = {}
+
+
+def _weight_transposed(weight: torch.Tensor, Vp: int) -> torch.Tensor:
+    """W^T [H, Vp] bf16 (columns past V zero).  The last one is kept and reused while
+    the weight's storage, shape and version are unchanged (the backward of every
+    microbatch between two optimizer steps)."""
+    V, H = weight.shape
+    key = (weight.device, weight.data_ptr(), weight._version, V, H, weight.stride(0), Vp)
+    hit = _WT_CACHE.get("w")
+    if hit is not None and hit[0] == key:
+        return hit[1]
+    _WT_CACHE.clear()
+    wT = torch.empty((H, Vp), dtype=torch.bfloat16, device=weight.device)
+    _C.transpose_bf16(weight, V, wT)
+    _WT_CACHE["w"] = (key, wT)
+    return wT
 
 
 def from_parallel_hidden_states_to_logprobs(
