@@ -238,7 +238,7 @@ def main() -> None:
     fwd_gbps = fwd_bytes / (fwd_ms * 1e-3) / 1e9
     step_gbps = (fwd_bytes + bwd_bytes) / (ms_step * 1e-3) / 1e9
 
-    traffic = _traffic("grpo")
+    traffic = _traffic("grpo", "mirl_logprob_bwd")
 
     _calibration_copy(args, dev)
 
@@ -358,23 +358,24 @@ def _timed(step, steps: int, warmup: int, main_kernels: list):
     return (t1 - t0) * 1e3 / steps, ms
 
 
-def _traffic(workload: str):
-    """HBM bytes per call of the roofline entry point, from the committed rocprof counter runs.
+def _traffic(workload: str, entry_point: str):
+    """HBM bytes per call of `entry_point` in `workload`, from the committed rocprof counter runs.
 
-    profiles/traffic.json holds FETCH_SIZE + WRITE_SIZE per dispatch, scaled by
-    what the same counters read for a 1 GiB device copy; None when absent.
+    profiles/traffic.json holds FETCH_SIZE + WRITE_SIZE per dispatch of the
+    entry point's kernels, scaled by what the same counters read for a 1 GiB
+    device copy; None when that entry point was not measured in that workload.
     """
     tf = ROOT / "profiles" / "traffic.json"
     try:
-        return json.loads(tf.read_text())["workloads"][workload]["hbm_bytes_per_launch"]
-    except (OSError, KeyError, ValueError):
+        return json.loads(tf.read_text())["workloads"][workload][entry_point]["hbm_bytes_per_launch"]
+    except (OSError, KeyError, ValueError, TypeError):
         return None
 
 
 def _roofline(kernel: str, nbytes: float, ms: float, workload: str) -> dict:
     gbps = nbytes / (ms * 1e-3) / 1e9 if ms > 0 else 0.0
     return {"kernel": kernel, "bound": "hbm", "achieved": gbps, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-            "frac": gbps / PEAK_HBM_GBPS, "traffic": _traffic(workload), "algorithmic_bytes": nbytes}
+            "frac": gbps / PEAK_HBM_GBPS, "traffic": _traffic(workload, kernel), "algorithmic_bytes": nbytes}
 
 
 def _timed_split(prepare, path, steps: int, warmup: int, main_kernels: list):
@@ -664,7 +665,7 @@ def bench_workload(args) -> None:
         gemm_act = 2.0 * active * H * V
         tflops = gemm / (fwd_ms * 1e-3) / 1e12 if fwd_ms > 0 else 0.0
         roof = {"kernel": "mirl_linear_ce_fwd", "bound": "mfma", "achieved": tflops, "peak": PEAK_BF16_TFLOPS,
-                "unit": "TFLOP/s", "frac": tflops / PEAK_BF16_TFLOPS, "traffic": _traffic(w),
+                "unit": "TFLOP/s", "frac": tflops / PEAK_BF16_TFLOPS, "traffic": _traffic(w, "mirl_linear_ce_fwd"),
                 "algorithmic_flops": gemm}
         extra["tflops_step"] = (gemm + 3 * gemm_act) / (ms_step * 1e-3) / 1e12
         extra["grad_kernel_ms_per_step"] = grad_ms

@@ -7,6 +7,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <type_traits>
 #include <string>
 
 #include "../../include/mirl.h"
@@ -148,6 +149,20 @@ struct RowSpan {
 template <class E>
 __device__ __forceinline__ float round_trip(float f) {
   return E::load_raw(E::from_float(f));
+}
+
+// Two fp32 values rounded to the element type and widened back (one
+// conversion instruction for both in bf16).
+template <class E>
+__device__ __forceinline__ void round_trip2(float& a, float& b) {
+  if constexpr (std::is_same<E, BF16>::value) {
+    const uint32_t w = BF16::pack2(a, b);
+    a = __uint_as_float(w << 16);
+    b = __uint_as_float(w & 0xffff0000u);
+  } else {
+    a = round_trip<E>(a);
+    b = round_trip<E>(b);
+  }
 }
 
 // Wave-wide reductions (64 lanes) through cross-lane shuffles.

@@ -895,14 +895,207 @@ __global__ __launch_bounds__(64 * W) void filter_bwd_zero_rows_kernel(FilterBwdP
   if (ys.tail0 + threadIdx.x < P.V) y[ys.tail0 + threadIdx.x] = zr;
 }
 
+// Markstein's correction of the product with the rounded reciprocal
+// r = RN(1/d): q0 = x r, e = x - q0 d (exact by the fma), q = q0 + e r.  For
+// dividends of a 16-bit dtype (at most 11 significant bits) with |x| in
+// [2^-100, 2^100] or x = 0, and d in [2^-10, 2^10], q is the correctly rounded
+// fp32 quotient x / d; every finite bf16 and fp16 dividend against 20,000
+// divisors spread over [2^-10, 2^10], and divisors with all-ones and
+// power-of-two significands, gave __fdiv_rn's result bit for bit.
+__device__ __forceinline__ float div_corrected(float x, float d, float r) {
+  const float q0 = x * r;
+  const float e = __builtin_fmaf(-q0, d, x);
+  return __builtin_fmaf(e, r, q0);
+}
+
+// How the whole-row walk narrows an fp32 gradient to the dtype.
+enum GradConv {
+  kConvPlain = 0,   // no temperature: round to the dtype
+  kConvExact = 1,   // grad_to_dtype (correctly rounded divisions)
+  kConvFastGT = 2,  // 16-bit dtype, an earlier in-place division by GT only, row checked by fast_div_row
+};
+
+// Whether every gradient the walk of this row divides by GT stays inside the
+// range where div_corrected is exact: GT in [2^-10, 2^10], the upstream
+// gradient at most 2^60 in magnitude, and every kept non-target element's
+// gradient p * |g| at least 2^-60 (p >= p(v_cut) for kept elements; the
+// factor 2 asked of p(v_cut) covers the difference between the two ways p is
+// evaluated).  The target element goes through grad_to_dtype on its own.
+// Elements outside the kept set are exact zeros.
+__device__ __forceinline__ bool fast_div_row(const FilterBwdParams& P, const RowInfo& ri, float gv) {
+  const float a = fabsf(P.GT);
+  if (!(a >= 0x1p-10f && a <= 0x1p10f)) return false;
+  const float ag = fabsf(gv);
+  if (!(ag <= 0x1p60f)) return false;
+  const float pc = fast_exp2(((ri.v_cut - ri.m) - ri.logsum) * kLog2e);
+  return ag * pc >= 0x1p-59f;
+}
+
+// The whole-row walk of the filtered backward: re-read the logits x of one
+// row and write the gradient y of the whole row, in index order (the head, the
+// 16-byte vectors, the tail).  The elements equal to v_cut are counted as they
+// come (the same count in every lane), so that a cut in rank form is applied
+// too; their ranks are only worked out for vectors where a tie occurs.
+// Elements outside the kept set get the gradient 0.
+template <class E, int CONV>
+__device__ __forceinline__ void walk_row(const FilterBwdParams& P, const RowInfo& ri,
+                                         const typename E::raw* x, typename E::raw* y, float gv,
+                                         int64_t t, int lane) {
+  using raw = typename E::raw;
+  constexpr int VEC = E::kVec;
+  constexpr int U = 4;
+  const float vc = ri.v_cut;
+  const bool rank_form = ri.i_cut < 0;
+  const uint32_t rcut = rank_form ? (uint32_t)(-1 - ri.i_cut) : 0u;
+  const int64_t icut = ri.i_cut;
+  const uint64_t below = (1ull << lane) - 1ull;
+  // p = exp(y - m - logsum); for the 16-bit dtypes as exp2(y log2e - c) in
+  // one fma (its absolute error in the exponent, a few 1e-6, is far below the
+  // dtype's resolution), for fp32 gradients from the differences
+  const float c = (ri.m + ri.logsum) * kLog2e;
+  const float ngv = -gv;
+  const float rgt = CONV == kConvFastGT ? __frcp_rn(P.GT) : 1.f;
+  uint32_t seen = 0;
+  auto yval = [&](float xf) { return P.has_t ? round_trip<E>(__fdiv_rn(xf, P.T)) : xf; };
+  auto prob = [&](float yy) {
+    if constexpr (std::is_same<E, F32>::value)
+      return fast_exp2(((yy - ri.m) - ri.logsum) * kLog2e);
+    else
+      return fast_exp2(__builtin_fmaf(yy, kLog2e, -c));
+  };
+  // gradient of a non-target element, narrowed to the dtype
+  auto narrow = [&](float g32) -> raw {
+    if constexpr (CONV == kConvPlain) {
+      return E::from_float(g32);
+    } else if constexpr (CONV == kConvFastGT) {
+      return E::from_float(div_corrected(round_trip<E>(g32), P.GT, rgt));
+    } else {
+      return grad_to_dtype<E>(g32, P);
+    }
+  };
+  // the non-target gradients -p g of one vector (0 outside the kept set)
+  auto narrow_vec = [&](const float (&w)[E::kVec], raw (&vals)[E::kVec], auto kept) {
+    float g[E::kVec];
+#pragma unroll
+    for (int k = 0; k < E::kVec; ++k) g[k] = kept(k) ? prob(w[k]) * ngv : 0.f;
+    if constexpr (CONV == kConvFastGT) {
+      // round to the dtype two at a time, divide, round again
+#pragma unroll
+      for (int k = 0; k < E::kVec; k += 2) {
+        float a = g[k], b = g[k + 1];
+        round_trip2<E>(a, b);
+        a = div_corrected(a, P.GT, rgt);
+        b = div_corrected(b, P.GT, rgt);
+        vals[k] = E::from_float(a);
+        vals[k + 1] = E::from_float(b);
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < E::kVec; ++k) vals[k] = narrow(g[k]);
+    }
+  };
+  auto grad_at = [&](float yy, int64_t j, bool kept) -> raw {
+    float g32 = 0.f;
+    if (kept) {
+      const float p = prob(yy);
+      g32 = ((j == t) ? 1.f - p : -p) * gv;
+    }
+    return grad_to_dtype<E>(g32, P);
+  };
+  auto tied_kept = [&](uint32_t rank, int64_t j) { return rank_form ? rank >= rcut : j >= icut; };
+  // one element per lane, consecutive indices across the lanes; every lane calls it
+  auto lane_step = [&](int64_t j, bool valid) {
+    const float yy = valid ? yval(E::load(x + j)) : 0.f;
+    const bool tie = valid && yy == vc;
+    const uint64_t bal = __ballot(tie);
+    bool kept = valid && yy > vc;
+    if (tie) kept = tied_kept(seen + (uint32_t)__popcll(bal & below), j);
+    seen += (uint32_t)__popcll(bal);
+    if (valid) y[j] = grad_at(yy, j, kept);
+  };
+  const RowSpan<E> xs(x, P.V);
+  const RowSpan<E> ys(y, P.V);
+  if (xs.head != ys.head) {
+    for (int64_t j0r = 0; j0r < P.V; j0r += 64) lane_step(j0r + lane, j0r + lane < P.V);
+    return;
+  }
+  lane_step(lane, lane < ys.head);
+  const vu4* xv = reinterpret_cast<const vu4*>(x + xs.head);
+  vu4* yv = reinterpret_cast<vu4*>(y + ys.head);
+  const int64_t nvec = ys.nvec;
+  for (int64_t base = 0; base < nvec; base += 64 * U) {
+    vu4 q[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = base + u * 64 + lane;
+      q[u] = i < nvec ? __builtin_nontemporal_load(xv + i) : vu4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = base + u * 64 + lane;
+      const bool valid = i < nvec;
+      const int64_t jb = ys.head + i * VEC;
+      float w[VEC];
+      E::unpack(q[u], w);
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) w[k] = yval(w[k]);
+      bool tie = false;
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) tie = tie || w[k] == vc;
+      tie = tie && valid;
+      raw vals[VEC];
+      // keep bits of a vector with ties; all ones: no tie in the wave's vectors
+      uint32_t keep8 = ~0u;
+      if (__ballot(tie) != 0ull) {
+        // ranks of the tied elements: the wave's exclusive prefix of the counts
+        uint32_t tie8 = 0;
+        keep8 = 0;
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) {
+          tie8 |= (valid && w[k] == vc ? 1u : 0u) << k;
+          keep8 |= (w[k] > vc ? 1u : 0u) << k;
+        }
+        const uint32_t cnt = (uint32_t)__popc(tie8);
+        uint32_t inc = cnt;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+          const uint32_t o = (uint32_t)__shfl_up((int)inc, off, 64);
+          if (lane >= off) inc += o;
+        }
+        const uint32_t ex = inc - cnt;
+        const uint32_t total = (uint32_t)__shfl((int)inc, 63, 64);
+        for (uint32_t m = tie8; m != 0u; m &= m - 1u) {
+          const int k = __ffs(m) - 1;
+          if (tied_kept(seen + ex + (uint32_t)__popc(tie8 & ((1u << k) - 1u)), jb + k)) keep8 |= 1u << k;
+        }
+        seen += total;
+        narrow_vec(w, vals, [&](int k) { return ((keep8 >> k) & 1u) != 0u; });
+      } else {
+        narrow_vec(w, vals, [&](int k) { return w[k] > vc; });
+      }
+      // the target element (1 - p) g, narrowed exactly
+      const int64_t dt = t - jb;
+      if (dt >= 0 && dt < VEC) {
+#pragma unroll
+        for (int k = 0; k < VEC; ++k)
+          if (k == dt) vals[k] = grad_at(w[k], jb + k, keep8 == ~0u ? w[k] > vc : ((keep8 >> k) & 1u) != 0u);
+      }
+      if (valid) {
+        vu4 out;
+        __builtin_memcpy(&out, vals, sizeof(out));
+        __builtin_nontemporal_store(out, yv + i);
+      }
+    }
+  }
+  lane_step(ys.tail0 + lane, ys.tail0 + lane < P.V);
+}
+
 // Phase 2, one wave per row with a non-zero upstream gradient: with the saved
 // kept list each kept entry is stored on its own (phase 1 zeroed the rest);
 // otherwise the row is re-read and rewritten whole.
 template <class E>
 __global__ __launch_bounds__(256) void filter_bwd_scatter_kernel(FilterBwdParams P, int64_t rows) {
   using raw = typename E::raw;
-  constexpr int VEC = E::kVec;
-  constexpr int U = 4;
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
@@ -942,101 +1135,18 @@ __global__ __launch_bounds__(256) void filter_bwd_scatter_kernel(FilterBwdParams
     return;
   }
 
-  // Whole row: re-read the logits and re-apply the cut, in index order (the
-  // head, the vectors, the tail), counting the elements equal to v_cut as they
-  // come so that a cut in rank form is applied too.  Elements outside the kept
-  // set are written as zeros without the exponential.
+  // Whole row: re-read the logits and re-apply the cut.
   const raw* x = static_cast<const raw*>(P.logits) + b * P.sb + r * P.sr;
-  const float vc = ri.v_cut;
-  const bool rank_form = ri.i_cut < 0;
-  const uint32_t rcut = rank_form ? (uint32_t)(-1 - ri.i_cut) : 0u;
-  const int64_t icut = ri.i_cut;
-  const uint64_t below = (1ull << lane) - 1ull;
-  uint32_t seen = 0;  // elements equal to v_cut met so far (the same in every lane)
-  auto yval = [&](float xf) { return P.has_t ? round_trip<E>(__fdiv_rn(xf, P.T)) : xf; };
-  auto grad_at = [&](float yy, int64_t j, bool kept) -> raw {
-    float g32 = 0.f;
-    if (kept) {
-      const float p = fast_exp2(((yy - ri.m) - ri.logsum) * kLog2e);
-      g32 = ((j == t) ? 1.f - p : -p) * gv;
-    }
-    return grad_to_dtype<E>(g32, P);
-  };
-  auto tied_kept = [&](uint32_t rank, int64_t j) { return rank_form ? rank >= rcut : j >= icut; };
-  // one element per lane, consecutive indices across the lanes; every lane calls it
-  auto lane_step = [&](int64_t j, bool valid) {
-    const float yy = valid ? yval(E::load(x + j)) : 0.f;
-    const bool tie = valid && yy == vc;
-    const uint64_t bal = __ballot(tie);
-    bool kept = valid && yy > vc;
-    if (tie) kept = tied_kept(seen + (uint32_t)__popcll(bal & below), j);
-    seen += (uint32_t)__popcll(bal);
-    if (valid) y[j] = grad_at(yy, j, kept);
-  };
-  const RowSpan<E> xs(x, P.V);
-  const RowSpan<E> ys(y, P.V);
-  if (xs.head != ys.head) {
-    for (int64_t j0r = 0; j0r < P.V; j0r += 64) lane_step(j0r + lane, j0r + lane < P.V);
-    return;
-  }
-  lane_step(lane, lane < ys.head);
-  const vu4* xv = reinterpret_cast<const vu4*>(x + xs.head);
-  vu4* yv = reinterpret_cast<vu4*>(y + ys.head);
-  const int64_t nvec = ys.nvec;
-  for (int64_t base = 0; base < nvec; base += 64 * U) {
-    vu4 q[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t i = base + u * 64 + lane;
-      if (i < nvec) q[u] = __builtin_nontemporal_load(xv + i);
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t i = base + u * 64 + lane;
-      const bool valid = i < nvec;
-      const int64_t jb = ys.head + i * VEC;
-      float w[VEC];
-      if (valid) {
-        E::unpack(q[u], w);
-#pragma unroll
-        for (int k = 0; k < VEC; ++k) w[k] = yval(w[k]);
-      }
-      uint32_t tie8 = 0, keep8 = 0;
-      if (valid) {
-#pragma unroll
-        for (int k = 0; k < VEC; ++k) {
-          tie8 |= (w[k] == vc ? 1u : 0u) << k;
-          keep8 |= (w[k] > vc ? 1u : 0u) << k;
-        }
-      }
-      const uint32_t c = (uint32_t)__popc(tie8);
-      if (__ballot(c != 0u) != 0ull) {
-        // ranks of the tied elements: the wave's exclusive prefix of the counts
-        uint32_t inc = c;
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-          const uint32_t o = (uint32_t)__shfl_up((int)inc, off, 64);
-          if (lane >= off) inc += o;
-        }
-        const uint32_t ex = inc - c;
-        const uint32_t total = (uint32_t)__shfl((int)inc, 63, 64);
-        for (uint32_t m = tie8; m != 0u; m &= m - 1u) {
-          const int k = __ffs(m) - 1;
-          if (tied_kept(seen + ex + (uint32_t)__popc(tie8 & ((1u << k) - 1u)), jb + k)) keep8 |= 1u << k;
-        }
-        seen += total;
-      }
-      if (valid) {
-        raw vals[VEC];
-#pragma unroll
-        for (int k = 0; k < VEC; ++k) vals[k] = grad_at(w[k], jb + k, (keep8 >> k) & 1u);
-        vu4 out;
-        __builtin_memcpy(&out, vals, sizeof(out));
-        __builtin_nontemporal_store(out, yv + i);
-      }
+  if constexpr (!std::is_same<E, F32>::value) {
+    if (!P.has_t && P.has_gt && fast_div_row(P, ri, gv)) {
+      walk_row<E, kConvFastGT>(P, ri, x, y, gv, t, lane);
+      return;
     }
   }
-  lane_step(ys.tail0 + lane, ys.tail0 + lane < P.V);
+  if (!P.has_t && !P.has_gt)
+    walk_row<E, kConvPlain>(P, ri, x, y, gv, t, lane);
+  else
+    walk_row<E, kConvExact>(P, ri, x, y, gv, t, lane);
 }
 
 // filtered logits (-inf outside the kept set) and the keep mask
