@@ -113,8 +113,8 @@ __device__ __forceinline__ T wave_incl_scan(T v) {
   return v;
 }
 
-// Exclusive prefix over the workgroup in thread order; *total = the sum.
-template <class T>
+// Exclusive prefix over the workgroup (NW waves) in thread order; *total = the sum.
+template <class T, int NW = kHW>
 __device__ T block_excl_scan(T v, T* red, T* total) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const T inc = wave_incl_scan(v);
@@ -124,7 +124,7 @@ __device__ T block_excl_scan(T v, T* red, T* total) {
   if (lane == 63) red[wv] = inc;
   __syncthreads();
   T base = T(0), tot = T(0);
-  for (int w = 0; w < kHW; ++w) {
+  for (int w = 0; w < NW; ++w) {
     const T s = red[w];
     if (w < wv) base += s;
     tot += s;
@@ -133,7 +133,7 @@ __device__ T block_excl_scan(T v, T* red, T* total) {
   return base + ex;
 }
 
-template <class T, int N>
+template <class T, int N, int NW = kHW>
 __device__ void block_sum_n(T (&v)[N], T* red) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
 #pragma unroll
@@ -143,16 +143,17 @@ __device__ void block_sum_n(T (&v)[N], T* red) {
   __syncthreads();
   if (lane == 0)
 #pragma unroll
-    for (int i = 0; i < N; ++i) red[i * kHW + wv] = v[i];
+    for (int i = 0; i < N; ++i) red[i * NW + wv] = v[i];
   __syncthreads();
 #pragma unroll
   for (int i = 0; i < N; ++i) {
     T s = T(0);
-    for (int w = 0; w < kHW; ++w) s += red[i * kHW + w];
+    for (int w = 0; w < NW; ++w) s += red[i * NW + w];
     v[i] = s;
   }
 }
 
+template <int NW = kHW>
 __device__ uint32_t block_max_u(uint32_t v, uint32_t* red) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
 #pragma unroll
@@ -161,8 +162,90 @@ __device__ uint32_t block_max_u(uint32_t v, uint32_t* red) {
   if (lane == 0) red[wv] = v;
   __syncthreads();
   uint32_t r = red[0];
-  for (int w = 1; w < kHW; ++w) r = max(r, red[w]);
+  for (int w = 1; w < NW; ++w) r = max(r, red[w]);
   return r;
+}
+
+// Cross-lane moves by DPP (no LDS traffic): row_shr:n shifts within rows of 16
+// lanes, row_bcast:15 / row_bcast:31 pass a row's last lane on to the next
+// row(s).  Lanes with no source, and rows outside ROWMASK, read 0, the
+// identity of the sums and unsigned maxima below.
+template <int CTRL, int ROWMASK = 0xf>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROWMASK, 0xf, false);
+}
+template <int CTRL, int ROWMASK = 0xf>
+__device__ __forceinline__ double dpp_f64(double v) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const uint64_t lo = dpp_u32<CTRL, ROWMASK>((uint32_t)u);
+  const uint64_t hi = dpp_u32<CTRL, ROWMASK>((uint32_t)(u >> 32));
+  return __builtin_bit_cast(double, (hi << 32) | lo);
+}
+template <int CTRL, int ROWMASK = 0xf, class T>
+__device__ __forceinline__ T dpp_move(T v) {
+  if constexpr (std::is_same<T, double>::value)
+    return dpp_f64<CTRL, ROWMASK>(v);
+  else
+    return (T)dpp_u32<CTRL, ROWMASK>((uint32_t)v);
+}
+
+// Inclusive scan over the 64 lanes of a wave with op(a, b) (sum, or unsigned
+// max): four in-row steps, then the two row broadcasts.
+struct OpAdd {
+  template <class T>
+  __device__ __forceinline__ T operator()(T a, T b) const { return a + b; }
+};
+struct OpMaxU {
+  __device__ __forceinline__ uint32_t operator()(uint32_t a, uint32_t b) const { return max(a, b); }
+};
+template <class T, class Op = OpAdd>
+__device__ __forceinline__ T wave_scan_dpp(T v, Op op = Op()) {
+  v = op(v, dpp_move<0x111>(v));
+  v = op(v, dpp_move<0x112>(v));
+  v = op(v, dpp_move<0x114>(v));
+  v = op(v, dpp_move<0x118>(v));
+  v = op(v, dpp_move<0x142, 0xa>(v));
+  v = op(v, dpp_move<0x143, 0xc>(v));
+  return v;
+}
+
+// Workgroup-wide exclusive scan (thread order) and total with one barrier.
+// `red` (NW entries) must be used by no other reduction of the same kernel
+// invocation, so no barrier is needed before it is written.
+template <class T, int NW>
+__device__ __forceinline__ T block_excl_scan1(T v, T* red, T* total) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const T inc = wave_scan_dpp(v);
+  if (lane == 63) red[wv] = inc;
+  __syncthreads();
+  T base = T(0), tot = T(0);
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    const T s = red[w];
+    base += (w < wv) ? s : T(0);
+    tot += s;
+  }
+  *total = tot;
+  return base + inc - v;
+}
+// Workgroup-wide sums of N values with one barrier (`red`: N * NW entries,
+// used by no other reduction of the same kernel invocation).
+template <class T, int N, int NW>
+__device__ __forceinline__ void block_sum1(T (&v)[N], T* red) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const T inc = wave_scan_dpp(v[i]);
+    if (lane == 63) red[i * NW + wv] = inc;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    T s = T(0);
+#pragma unroll
+    for (int w = 0; w < NW; ++w) s += red[i * NW + w];
+    v[i] = s;
+  }
 }
 
 // Relative distance within which the fp32 running sum S is kept from the
@@ -838,20 +921,51 @@ __global__ __launch_bounds__(kHT) void filter_hist_kernel(FilterParams P, int al
 // A 16-bit cut that the rounding bound leaves undecided is walked exactly over
 // the list by one wave.  Rows it cannot finish (a count of 65536 or more, more
 // than kEntCap occupied keys) are flagged (flags bit 0) for filter_hist_kernel.
-constexpr int kPadWords = kHistWords + kHistWords / 32;  // one pad word per 32
-constexpr int kEntCap = kPadWords / 3;                     // 12-byte entries over the same bytes
+//
+// Two table geometries:
+//  - CompactFull: 1024 threads, every one of the 65536 keys (fp16 logits, and
+//    bf16 rows outside the window below);
+//  - CompactWindow: 512 threads, the bf16 values of |x| < 512: word m (the
+//    magnitude bits, m < 0x4400) counts +x in its low half and -x in its high
+//    half (70 KB of counts), so two rows share a CU and one row's list phases
+//    run while the other row is being counted.  Per value: an and and a clamp
+//    (two values at a time), an address and an increment.  A value outside
+//    the window (|x| >= 512, +-inf, NaN) lands in word 0x4400 and flags the
+//    row for filter_hist_kernel.
+struct CompactFull {
+  static constexpr int NT = 1024;
+  static constexpr uint32_t kBase = 0;      // first key of the table
+  static constexpr int kWords = 32768;      // logical words (2 keys each)
+  static constexpr bool kWindow = false;
+  static constexpr bool kPad = true;        // one pad word per 32 (strided reads of 32 words)
+};
+struct CompactWindow {
+  static constexpr int NT = 512;
+  static constexpr uint32_t kBase = 0u;     // (unused: words are indexed by magnitude)
+  static constexpr int kWords = 0x4400;     // magnitudes below bf16 512.0
+  static constexpr bool kWindow = true;
+  static constexpr bool kPad = false;       // strided reads of 34 words: 2-way bank conflicts
+};
 
+template <class G>
 struct CompactShared {
+  static constexpr int kWPT = G::kWords / G::NT;          // logical words per thread
+  // the table's physical words, then one word counting the values outside it
+  static constexpr int kPadWords = G::kWords + (G::kPad ? G::kWords / 32 : 0) + 1;
+  static constexpr int kEntCap = kPadWords / 3;          // 12-byte entries over the same bytes
+  static constexpr int NW = G::NT / 64;
+  static_assert(kWPT * G::NT == G::kWords, "table words split evenly over the threads");
   union {
-    uint32_t hist[kPadWords];  // logical word L at L + L / 32
+    uint32_t hist[kPadWords];  // logical word L at L (+ L / 32 with padding)
     struct {
       uint32_t kc[kEntCap];
       float y[kEntCap];
       float e[kEntCap];
     } ent;
   } u;
-  double red_d[kHW * 4];
-  uint32_t red_u[kHW * 4];
+  // one slot of NW entries per reduction of a row (each written once)
+  double red_d[NW * 4];
+  uint32_t red_u[NW * 9];
   uint32_t sel[4];
   int first_lo, first_hi;
   uint32_t ent_lo, pos_lo, ent_hi, pos_hi;
@@ -869,27 +983,37 @@ __device__ __forceinline__ uint32_t okey16x2(uint32_t w) {
   return w ^ ((neg * 0xffffu) | 0x80008000u);
 }
 
-template <class E>
-__global__ __launch_bounds__(kHT) void filter_compact_kernel(FilterParams P, int all_rows) {
+template <class E, class G, bool DEC16>
+__global__ __launch_bounds__(G::NT, 2048 / G::NT) void filter_compact_kernel(FilterParams P, int all_rows) {
   using raw = typename E::raw;
-  __shared__ CompactShared sh;
+  using SH = CompactShared<G>;
+  constexpr int NT = G::NT, NW = SH::NW, kWPT = SH::kWPT, kEntCap = SH::kEntCap;
+  __shared__ SH sh;
   const int64_t row = blockIdx.x;
   if (!all_rows && (P.info[row].flags & 1) == 0) return;
   const int64_t b = row / P.R, r = row - b * P.R;
   const raw* x = static_cast<const raw*>(P.logits) + b * P.sb + r * P.sr;
   const int tid = threadIdx.x;
   const int64_t V = P.V;
+  // the target and its value, loaded while the row is counted
+  int64_t t = -1;
+  uint32_t xt_bits = 0u;
+  if (P.out != nullptr) {
+    t = P.target[b * P.tsb + r * P.tsr];
+    if (t >= 0 && t < V) xt_bits = bits16<E>(x[t]);
+  }
   const RowSpan<E> sp(x, V);
   const vu4* xv = reinterpret_cast<const vu4*>(x + sp.head);
   const int64_t nvec = sp.nvec;
 
   {
     vu4* h4 = reinterpret_cast<vu4*>(sh.u.hist);
-    for (int i = tid; i < kPadWords / 4; i += kHT) h4[i] = vu4{0u, 0u, 0u, 0u};
+    for (int i = tid; i < SH::kPadWords / 4; i += NT) h4[i] = vu4{0u, 0u, 0u, 0u};
+    for (int i = (SH::kPadWords / 4) * 4 + tid; i < SH::kPadWords; i += NT) sh.u.hist[i] = 0u;
   }
   if (tid == 0) {
-    sh.first_lo = kHT;
-    sh.first_hi = kHT;
+    sh.first_lo = NT;
+    sh.first_hi = NT;
     sh.fail = 0;
     sh.sel[0] = sh.sel[1] = sh.sel[2] = sh.sel[3] = 0u;
     sh.ent_lo = sh.pos_lo = sh.ent_hi = sh.pos_hi = 0u;
@@ -897,59 +1021,170 @@ __global__ __launch_bounds__(kHT) void filter_compact_kernel(FilterParams P, int
   __syncthreads();
 
   // ---- one pass over the row: every value counted under its order key ----
+  // A key outside the table (window geometry) is clamped to kLimit, whose
+  // logical word kWords is the word after the table: it counts those values
+  // (kLimit is even, so in its low half).  Branch-free per element.
+  constexpr uint32_t kLimit = 2u * (uint32_t)G::kWords;
+  auto phys = [](uint32_t L) { return G::kPad ? padded(L) : L; };
   auto count_key = [&](uint32_t k) {
-    const uint32_t L = k >> 1;
-    atomicAdd(&sh.u.hist[padded(L)], 1u + (k & 1u) * 0xffffu);
+    const uint32_t rel = min(k - G::kBase, kLimit);
+    atomicAdd(&sh.u.hist[phys(rel >> 1)], 1u + (rel & 1u) * 0xffffu);
   };
+  // two values per 32-bit word; the window layout clamps both magnitudes in
+  // one packed 16-bit operation and takes byte addresses straight from them
+  typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
   auto count_word = [&](uint32_t w) {
-    const uint32_t k2 = okey16x2(w);
-    count_key(k2 & 0xffffu);
-    count_key(k2 >> 16);
+    if constexpr (G::kPad) {
+      const uint32_t k2 = okey16x2(w);
+      count_key(k2 & 0xffffu);
+      count_key(k2 >> 16);
+    } else {
+      // word min(|x| bits, kWords), the sign choosing the half
+      const u16x2 mag = __builtin_bit_cast(u16x2, w & 0x7fff7fffu);
+      const uint32_t c =
+          __builtin_bit_cast(uint32_t, __builtin_elementwise_min(mag, (u16x2)(uint16_t)G::kWords));
+      char* base = reinterpret_cast<char*>(sh.u.hist);
+      atomicAdd(reinterpret_cast<uint32_t*>(base + ((c & 0xffffu) << 2)),
+                1u + ((w >> 15) & 1u) * 0xffffu);
+      atomicAdd(reinterpret_cast<uint32_t*>(base + ((c >> 16) << 2)), 1u + (w >> 31) * 0xffffu);
+    }
   };
-  if (tid < sp.head) count_key(okey16x2(bits16<E>(x[tid])) & 0xffffu);
-  if (sp.tail0 + tid < V) count_key(okey16x2(bits16<E>(x[sp.tail0 + tid])) & 0xffffu);
+  // one value (a row's unaligned head and tail), in the table's layout
+  auto count_one = [&](uint32_t r) {
+    if constexpr (G::kWindow) {
+      const uint32_t c = min(r & 0x7fffu, (uint32_t)G::kWords);
+      atomicAdd(&sh.u.hist[c], 1u + ((r >> 15) & 1u) * 0xffffu);
+    } else {
+      count_key(okey16x2(r) & 0xffffu);
+    }
+  };
+  if (tid < sp.head) count_one(bits16<E>(x[tid]));
+  if (sp.tail0 + tid < V) count_one(bits16<E>(x[sp.tail0 + tid]));
   {
+    // Full batches (UB vectors per lane, every lane in bounds) are addressed
+    // from a uniform batch base plus per-lane offsets that do not change, and
+    // two are in flight: the next one is issued before the current one is
+    // counted.  A prefetch past the last full batch reads that batch again
+    // (from cache, not counted), so that every issue is unconditional and the
+    // waits exact.  The remaining vectors follow as one guarded batch.
     constexpr int UB = 8;
-    for (int64_t v0 = tid; v0 < nvec; v0 += (int64_t)UB * kHT) {
-      vu4 t[UB];
+    constexpr int kStep = UB * NT;
+    const int nv = (int)nvec;  // < 2^28: V < 2^31
+    const int nfull = nv / kStep;
+    const char* xb = reinterpret_cast<const char*>(xv);
+    vu4 qa[UB], qb[UB];
+    auto issue = [&](vu4(&q)[UB], int bi) {
+      const char* bp = xb + (size_t)bi * (size_t)kStep * 16u;
+#pragma unroll
+      for (int u = 0; u < UB; ++u)
+        q[u] = __builtin_nontemporal_load(
+            reinterpret_cast<const vu4*>(bp + (uint32_t)(tid + u * NT) * 16u));
+      __builtin_amdgcn_sched_barrier(0);  // every load issued before the counting that follows
+    };
+    auto count_vec = [&](const vu4& q) {
+      count_word(q.x);
+      count_word(q.y);
+      count_word(q.z);
+      count_word(q.w);
+    };
+    // one vector at a time: the scheduler is kept from hoisting the key
+    // arithmetic of later vectors (registers for two workgroups per CU)
+    auto count_batch = [&](const vu4(&q)[UB]) {
 #pragma unroll
       for (int u = 0; u < UB; ++u) {
-        const int64_t v = v0 + (int64_t)u * kHT;
-        if (v < nvec) t[u] = __builtin_nontemporal_load(xv + v);
+        count_vec(q[u]);
+        __builtin_amdgcn_sched_barrier(0);
       }
+    };
+    // pairs of batches with unconditional uses (so that no load is moved
+    // past the counting it should overlap); an odd last batch is in qa
+    if (nfull > 0) issue(qa, 0);
+    const int npairs = nfull / 2;
+    for (int pi = 0; pi < npairs; ++pi) {
+      issue(qb, 2 * pi + 1);
+      count_batch(qa);
+      issue(qa, min(2 * pi + 2, nfull - 1));
+      count_batch(qb);
+    }
+    if (nfull & 1) count_batch(qa);
 #pragma unroll
-      for (int u = 0; u < UB; ++u) {
-        const int64_t v = v0 + (int64_t)u * kHT;
-        if (v >= nvec) break;
-        count_word(t[u].x);
-        count_word(t[u].y);
-        count_word(t[u].z);
-        count_word(t[u].w);
-      }
+    for (int u = 0; u < UB; ++u) {
+      const int v = nfull * kStep + tid + u * NT;
+      if (v < nv) count_vec(__builtin_nontemporal_load(xv + v));
     }
   }
   __syncthreads();
 
   // ---- the occupied keys: counted, checked, listed in ascending order ------
-  // thread t owns logical words 32t .. 32t + 31 (keys 64t .. 64t + 63), which
-  // sit at physical words 33t .. 33t + 31
-  uint32_t ct = 0, nz = 0, klast = 0;
+  // Thread t owns logical words kWPT*t .. kWPT*t + kWPT - 1.  Key layout: word
+  // L holds keys kBase + 2L (low half) and kBase + 2L + 1.  Window layout: word
+  // m holds +m (low half, key 0x8000 | m) and -m (high half, key 0x7fff - m),
+  // so the list is the negative entries by descending m (threads in reverse
+  // order), then the positive ones by ascending m.
+  const uint32_t L0 = (uint32_t)tid * (uint32_t)kWPT;
+  const uint32_t key0 = G::kBase + 2u * L0;
+  uint32_t ct = 0, nzp = 0, nzn = 0, kloc = 0;
+  {
+    uint32_t kpos = 0, kneg = 0;
+    bool seen_neg = false;
 #pragma unroll 8
-  for (int w = 0; w < 32; ++w) {
-    const uint32_t word = sh.u.hist[33 * tid + w];
-    const uint32_t lo = word & 0xffffu, hi = word >> 16;
-    ct += lo + hi;
-    nz += (lo != 0u ? 1u : 0u) + (hi != 0u ? 1u : 0u);
-    if (lo != 0u) klast = (uint32_t)tid * 64u + 2u * (uint32_t)w;
-    if (hi != 0u) klast = (uint32_t)tid * 64u + 2u * (uint32_t)w + 1u;
+    for (int w = 0; w < kWPT; ++w) {
+      const uint32_t word = sh.u.hist[phys(L0 + (uint32_t)w)];
+      const uint32_t lo = word & 0xffffu, hi = word >> 16;
+      ct += lo + hi;
+      if constexpr (G::kWindow) {
+        nzp += lo != 0u ? 1u : 0u;
+        nzn += hi != 0u ? 1u : 0u;
+        if (lo != 0u) kpos = 0x8000u | (L0 + (uint32_t)w);
+        if (hi != 0u && !seen_neg) {
+          kneg = 0x7fffu - (L0 + (uint32_t)w);
+          seen_neg = true;
+        }
+      } else {
+        nzp += (lo != 0u ? 1u : 0u) + (hi != 0u ? 1u : 0u);
+        if (lo != 0u) kpos = key0 + 2u * (uint32_t)w;
+        if (hi != 0u) kpos = key0 + 2u * (uint32_t)w + 1u;
+      }
+    }
+    kloc = kpos != 0u ? kpos : kneg;  // key 0 (the largest NaN) orders below every other
   }
-  uint32_t tot[1] = {ct};
-  block_sum_n<uint32_t, 1>(tot, sh.red_u);
-  uint32_t N;
-  const uint32_t off = block_excl_scan<uint32_t>(nz, sh.red_u, &N);
-  const uint32_t kmx = block_max_u(ct > 0u ? klast : 0u, sh.red_u);
+  // one barrier for the entry offsets, the numbers of entries, the total
+  // count and the largest occupied key
+  uint32_t N, Nn, tot, kmx;
+  uint32_t off_p, off_n;
+  {
+    const int lane = tid & 63, wv = tid >> 6;
+    const uint32_t ip = wave_scan_dpp(nzp);
+    const uint32_t in_ = wave_scan_dpp(nzn);
+    const uint32_t ict = wave_scan_dpp(ct);
+    const uint32_t ikm = wave_scan_dpp(kloc, OpMaxU());
+    if (lane == 63) {
+      sh.red_u[wv] = ip;
+      sh.red_u[NW + wv] = in_;
+      sh.red_u[2 * NW + wv] = ict;
+      sh.red_u[3 * NW + wv] = ikm;
+    }
+    __syncthreads();
+    uint32_t bp = 0u, bn = 0u, Np = 0u;
+    Nn = 0u;
+    tot = 0u;
+    kmx = 0u;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const uint32_t a = sh.red_u[w], an = sh.red_u[NW + w];
+      bp += (w < wv) ? a : 0u;
+      bn += (w < wv) ? an : 0u;
+      Np += a;
+      Nn += an;
+      tot += sh.red_u[2 * NW + w];
+      kmx = max(kmx, sh.red_u[3 * NW + w]);
+    }
+    N = Np + Nn;
+    off_p = Nn + bp + ip - nzp;  // the positive (or key-layout) entries, ascending
+    off_n = Nn - (bn + in_);     // the negative entries of later threads come first
+  }
   // a 16-bit count that wrapped loses a multiple of 65536 from the total
-  if (tot[0] != (uint32_t)V || N > (uint32_t)kEntCap) {
+  if (tot != (uint32_t)V || sh.u.hist[phys((uint32_t)G::kWords)] != 0u || N > (uint32_t)kEntCap) {
     if (tid == 0) {
       RowInfo ri{};
       ri.flags = 1;
@@ -957,16 +1192,29 @@ __global__ __launch_bounds__(kHT) void filter_compact_kernel(FilterParams P, int
     }
     return;
   }
-  uint32_t wd[32];
+  uint32_t wd[kWPT];
 #pragma unroll
-  for (int w = 0; w < 32; ++w) wd[w] = sh.u.hist[33 * tid + w];
+  for (int w = 0; w < kWPT; ++w) wd[w] = sh.u.hist[phys(L0 + (uint32_t)w)];
   __syncthreads();  // every table word is in registers: the entries overwrite the table
-  {
-    uint32_t j = off;
+  if constexpr (G::kWindow) {
+    uint32_t j = off_n;
 #pragma unroll
-    for (int w = 0; w < 32; ++w) {
+    for (int w = kWPT - 1; w >= 0; --w) {
+      const uint32_t hi = wd[w] >> 16;
+      if (hi != 0u) sh.u.ent.kc[j++] = (0x7fffu - (L0 + (uint32_t)w)) | (hi << 16);
+    }
+    j = off_p;
+#pragma unroll
+    for (int w = 0; w < kWPT; ++w) {
+      const uint32_t lo = wd[w] & 0xffffu;
+      if (lo != 0u) sh.u.ent.kc[j++] = (0x8000u | (L0 + (uint32_t)w)) | (lo << 16);
+    }
+  } else {
+    uint32_t j = off_p;
+#pragma unroll
+    for (int w = 0; w < kWPT; ++w) {
       const uint32_t lo = wd[w] & 0xffffu, hi = wd[w] >> 16;
-      const uint32_t k0 = (uint32_t)tid * 64u + 2u * (uint32_t)w;
+      const uint32_t k0 = key0 + 2u * (uint32_t)w;
       if (lo != 0u) sh.u.ent.kc[j++] = k0 | (lo << 16);
       if (hi != 0u) sh.u.ent.kc[j++] = (k0 + 1u) | (hi << 16);
     }
@@ -974,19 +1222,34 @@ __global__ __launch_bounds__(kHT) void filter_compact_kernel(FilterParams P, int
   __syncthreads();
   auto yk = [&](uint32_t k) { return scaled<E>(value16<E>(raw_of_okey16(k)), P); };
   const float m = yk(kmx);
-  for (uint32_t j = tid; j < N; j += kHT) {
-    const float y = yk(sh.u.ent.kc[j] & 0xffffu);
-    sh.u.ent.y[j] = y;
-    sh.u.ent.e[j] = expf(y - m);
+  // Each thread's share of the list (entries j0 .. j1 - 1, at most CMAX) is
+  // evaluated once and kept in registers for the phases below; y and
+  // exp(y - m) also go to LDS for the searches and the exact walk.
+  constexpr int CMAX = (kEntCap + NT - 1) / NT;
+  const uint32_t C = (N + NT - 1) / NT;  // the same for every thread
+  const uint32_t j0 = min(N, (uint32_t)tid * C), j1 = min(N, j0 + C);
+  uint32_t rn[CMAX];  // counts, 0 past the share
+  float re[CMAX];     // exp(y - m)
+#pragma unroll
+  for (int i = 0; i < CMAX; ++i) {
+    rn[i] = 0u;
+    re[i] = 0.f;
+    if ((uint32_t)i < C && j0 + (uint32_t)i < j1) {
+      const uint32_t j = j0 + (uint32_t)i;
+      const uint32_t kcj = sh.u.ent.kc[j];
+      const float y = yk(kcj & 0xffffu);
+      const float e = expf(y - m);
+      sh.u.ent.y[j] = y;
+      sh.u.ent.e[j] = e;
+      rn[i] = kcj >> 16;
+      re[i] = e;
+    }
   }
   __syncthreads();
   const uint32_t* kc = sh.u.ent.kc;
   const float* ey = sh.u.ent.y;
   const float* ee = sh.u.ent.e;
   auto cnt = [&](uint32_t j) { return kc[j] >> 16; };
-  // this thread's share of the list
-  const uint32_t C = (N + kHT - 1) / kHT;
-  const uint32_t j0 = min(N, (uint32_t)tid * C), j1 = min(N, j0 + C);
   // first entry in [lo, hi] whose y >= v (hi + 1 if none); last entry whose y <= v (lo - 1 if none)
   auto first_ge = [&](uint32_t lo, uint32_t hi, float v) {
     uint32_t a = lo, c = hi + 1u;
@@ -1009,20 +1272,22 @@ __global__ __launch_bounds__(kHT) void filter_compact_kernel(FilterParams P, int
   uint32_t thr = 0;  // first entry of the kept-k values
   float y_thr = -INFINITY;
   if (P.top_k > 0) {
-    const int rr = kHT - 1 - tid;  // shares in descending order
-    const uint32_t a0 = min(N, (uint32_t)rr * C), a1 = min(N, a0 + C);
     uint32_t cr = 0;
-    for (uint32_t j = a0; j < a1; ++j) cr += cnt(j);
+#pragma unroll
+    for (int i = 0; i < CMAX; ++i) cr += rn[i];
     uint32_t tk;
-    const uint32_t above = block_excl_scan<uint32_t>(cr, sh.red_u, &tk);
+    const uint32_t below = block_excl_scan1<uint32_t, NW>(cr, sh.red_u + 4 * NW, &tk);
+    const uint32_t above = tk - below - cr;  // elements of the later (larger) entries
     const uint32_t kk = (uint32_t)P.top_k;
     if (above < kk && kk <= above + cr) {
       uint32_t acc = above;
-      for (uint32_t j = a1; j > a0; --j) {
-        acc += cnt(j - 1u);
-        if (acc >= kk) {
-          sh.sel[0] = j - 1u;
-          break;
+      bool done = false;
+#pragma unroll
+      for (int i = CMAX - 1; i >= 0; --i) {
+        acc += rn[i];
+        if (!done && rn[i] != 0u && acc >= kk) {
+          sh.sel[0] = j0 + (uint32_t)i;
+          done = true;
         }
       }
     }
@@ -1031,11 +1296,15 @@ __global__ __launch_bounds__(kHT) void filter_compact_kernel(FilterParams P, int
     y_thr = ey[jk];
     thr = first_ge(0u, jk, y_thr);
   }
+  // entry i of the share is inside the kept-k values
+  auto in_k = [&](int i) { return rn[i] != 0u && j0 + (uint32_t)i >= thr; };
 
   // ---- normaliser over the kept-k values ------------------------------------
   double zs[1] = {0.0};
-  for (uint32_t j = max(j0, thr); j < j1; ++j) zs[0] += (double)cnt(j) * (double)ee[j];
-  block_sum_n<double, 1>(zs, sh.red_d);
+#pragma unroll
+  for (int i = 0; i < CMAX; ++i)
+    if (in_k(i)) zs[0] += (double)rn[i] * (double)re[i];
+  block_sum1<double, 1, NW>(zs, sh.red_d);
   const float Z = (float)zs[0];
 
   // ---- top-p cut: (entry, 1-based position inside it) -----------------------
@@ -1044,12 +1313,19 @@ __global__ __launch_bounds__(kHT) void filter_compact_kernel(FilterParams P, int
   if (P.has_p) {
     const float inv = 1.0f / Z;
     auto pmass = [&](uint32_t j) -> double {
-      return P.dec16 ? (double)round_trip<E>(ee[j] / Z) : (double)(ee[j] * inv);
+      return DEC16 ? (double)round_trip<E>(ee[j] / Z) : (double)(ee[j] * inv);
     };
+    // the share's probabilities (in place of the exponentials, which the
+    // group phase reads from LDS)
+    float* rp = re;
+#pragma unroll
+    for (int i = 0; i < CMAX; ++i) rp[i] = DEC16 ? round_trip<E>(re[i] / Z) : re[i] * inv;
     double mt = 0.0;
-    for (uint32_t j = max(j0, thr); j < j1; ++j) mt += (double)cnt(j) * pmass(j);
+#pragma unroll
+    for (int i = 0; i < CMAX; ++i)
+      if (in_k(i)) mt += (double)rn[i] * (double)rp[i];
     double mtot;
-    const double X0 = block_excl_scan<double>(mt, sh.red_d, &mtot);
+    const double X0 = block_excl_scan1<double, NW>(mt, sh.red_d + NW, &mtot);
     auto first_in_run = [&](double X, double p, uint32_t n, auto&& hit) {
       uint32_t a = 1u, c = n;
       while (a < c) {
@@ -1058,21 +1334,24 @@ __global__ __launch_bounds__(kHT) void filter_compact_kernel(FilterParams P, int
       }
       return a;
     };
-    if (!P.dec16) {
+    if constexpr (!DEC16) {
       const float cut = P.cut;
       auto hit = [&](double X) { return (float)X > cut; };
       double X = X0;
       bool found = false;
       uint32_t fk = 0, fp = 0;
-      for (uint32_t j = max(j0, thr); j < j1 && !found; ++j) {
-        const double p = pmass(j);
-        const uint32_t n = cnt(j);
-        if (hit(X + (double)n * p)) {
-          found = true;
-          fk = j;
-          fp = hit(X) ? 1u : first_in_run(X, p, n, hit);
+#pragma unroll
+      for (int i = 0; i < CMAX; ++i) {
+        if (!found && in_k(i)) {
+          const double p = (double)rp[i];
+          const uint32_t n = rn[i];
+          if (hit(X + (double)n * p)) {
+            found = true;
+            fk = j0 + (uint32_t)i;
+            fp = hit(X) ? 1u : first_in_run(X, p, n, hit);
+          }
+          X += (double)n * p;
         }
-        X += (double)n * p;
       }
       if (found) atomicMin(&sh.first_lo, tid);
       __syncthreads();
@@ -1081,7 +1360,7 @@ __global__ __launch_bounds__(kHT) void filter_compact_kernel(FilterParams P, int
         sh.pos_lo = fp;
       }
       __syncthreads();
-      have_cut = sh.first_lo < kHT;
+      have_cut = sh.first_lo < NT;
       cut_ent = sh.ent_lo;
       cut_pos = sh.pos_lo;
     } else {
@@ -1094,40 +1373,47 @@ __global__ __launch_bounds__(kHT) void filter_compact_kernel(FilterParams P, int
       double bt = 0.0;
       {
         double X = X0;
-        for (uint32_t j = max(j0, thr); j < j1; ++j) {
-          const double p = pmass(j);
-          const uint32_t n = cnt(j);
-          const double X1 = X + (double)n * p;
-          bt += run_error_bound(n, p, X, X1);
-          X = X1;
+#pragma unroll
+        for (int i = 0; i < CMAX; ++i) {
+          if (in_k(i)) {
+            const double p = (double)rp[i];
+            const uint32_t n = rn[i];
+            const double X1 = X + (double)n * p;
+            bt += run_error_bound(n, p, X, X1);
+            X = X1;
+          }
         }
       }
       double btot;
-      const double D0 = block_excl_scan<double>(bt, sh.red_d, &btot);
+      const double D0 = block_excl_scan1<double, NW>(bt, sh.red_d + 2 * NW, &btot);
       bool flo = false, fhi = false, slack_ok = true;
       uint32_t klo = 0, plo = 0, khi = 0, phi = 0;
       {
         double X = X0, D = D0;
-        for (uint32_t j = max(j0, thr); j < j1 && !(flo && fhi); ++j) {
-          const double p = pmass(j);
-          const uint32_t n = cnt(j);
-          const double X1 = X + (double)n * p;
-          const double Db = D + run_error_bound(n, p, X, X1);
-          if (Db > 0.5 * kSlack * X1) slack_ok = false;
-          auto hlo = [&](double v) { return v + Db >= Bd; };
-          auto hhi = [&](double v) { return v - Db >= Bd; };
-          if (!flo && hlo(X1)) {
-            flo = true;
-            klo = j;
-            plo = hlo(X) ? 1u : first_in_run(X, p, n, hlo);
+#pragma unroll
+        for (int i = 0; i < CMAX; ++i) {
+          if (!(flo && fhi) && in_k(i)) {
+            const double p = (double)rp[i];
+            const uint32_t n = rn[i];
+            const uint32_t j = j0 + (uint32_t)i;
+            const double X1 = X + (double)n * p;
+            const double Db = D + run_error_bound(n, p, X, X1);
+            if (Db > 0.5 * kSlack * X1) slack_ok = false;
+            auto hlo = [&](double v) { return v + Db >= Bd; };
+            auto hhi = [&](double v) { return v - Db >= Bd; };
+            if (!flo && hlo(X1)) {
+              flo = true;
+              klo = j;
+              plo = hlo(X) ? 1u : first_in_run(X, p, n, hlo);
+            }
+            if (!fhi && hhi(X1)) {
+              fhi = true;
+              khi = j;
+              phi = hhi(X) ? 1u : first_in_run(X, p, n, hhi);
+            }
+            X = X1;
+            D = Db;
           }
-          if (!fhi && hhi(X1)) {
-            fhi = true;
-            khi = j;
-            phi = hhi(X) ? 1u : first_in_run(X, p, n, hhi);
-          }
-          X = X1;
-          D = Db;
         }
       }
       if (flo) atomicMin(&sh.first_lo, tid);
@@ -1143,7 +1429,7 @@ __global__ __launch_bounds__(kHT) void filter_compact_kernel(FilterParams P, int
         sh.pos_hi = phi;
       }
       __syncthreads();
-      const bool none_lo = sh.first_lo >= kHT, none_hi = sh.first_hi >= kHT;
+      const bool none_lo = sh.first_lo >= NT, none_hi = sh.first_hi >= NT;
       const bool certain = sh.fail == 0 &&
                            ((none_lo && none_hi) ||
                             (!none_lo && !none_hi && sh.ent_lo == sh.ent_hi && sh.pos_lo == sh.pos_hi));
@@ -1239,20 +1525,45 @@ __global__ __launch_bounds__(kHT) void filter_compact_kernel(FilterParams P, int
     g_lo = first_ge(thr, ck, v_cut);
     g_hi = last_le(ck, N - 1u, v_cut);
   }
-  double sums[1] = {0.0};   // kept mass above the group
+  double ksum_above = 0.0;  // kept mass above the group
   uint32_t cnts[3] = {0u, 0u, 0u};  // elements above the group, in it, in it before the cut entry
-  for (uint32_t j = j0; j < j1; ++j) {
-    const uint32_t n = cnt(j);
+#pragma unroll
+  for (int i = 0; i < CMAX; ++i) {
+    const uint32_t j = j0 + (uint32_t)i;
+    const uint32_t n = rn[i];
+    if (n == 0u) continue;
     if (j > g_hi) {
       cnts[0] += n;
-      sums[0] += (double)n * (double)ee[j];
+      ksum_above += (double)n * (double)ee[j];
     } else if (j >= g_lo) {
       cnts[1] += n;
       if (have_cut && j < cut_ent) cnts[2] += n;
     }
   }
-  block_sum_n<double, 1>(sums, sh.red_d);
-  block_sum_n<uint32_t, 3>(cnts, sh.red_u);
+  {  // the four sums with one barrier
+    const int lane = tid & 63, wv = tid >> 6;
+    const double isum = wave_scan_dpp(ksum_above);
+    uint32_t ic[3];
+#pragma unroll
+    for (int q = 0; q < 3; ++q) ic[q] = wave_scan_dpp(cnts[q]);
+    if (lane == 63) {
+      sh.red_d[3 * NW + wv] = isum;
+#pragma unroll
+      for (int q = 0; q < 3; ++q) sh.red_u[(5 + q) * NW + wv] = ic[q];
+    }
+    __syncthreads();
+    ksum_above = 0.0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) ksum_above += sh.red_d[3 * NW + w];
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+      uint32_t sq = 0u;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) sq += sh.red_u[(5 + q) * NW + w];
+      cnts[q] = sq;
+    }
+  }
+  double sums[1] = {ksum_above};
   const uint32_t n_group = cnts[1];
   uint32_t rcut = 0;  // group elements (in index order) before the cut
   if (P.has_p) rcut = have_cut ? cnts[2] + cut_pos - 1u : n_group - 1u;
@@ -1263,10 +1574,8 @@ __global__ __launch_bounds__(kHT) void filter_compact_kernel(FilterParams P, int
 
   // ---- the target --------------------------------------------------------
   float lp = -INFINITY;
-  int64_t t = -1;
-  if (P.out != nullptr) t = P.target[b * P.tsb + r * P.tsr];
   if (t >= 0 && t < V) {
-    const uint32_t kt = okey16x2(bits16<E>(x[t])) & 0xffffu;
+    const uint32_t kt = okey16x2(xt_bits) & 0xffffu;
     const float yt = yk(kt);
     bool kept = yt > v_cut;
     if (yt == v_cut) {
@@ -1274,12 +1583,12 @@ __global__ __launch_bounds__(kHT) void filter_compact_kernel(FilterParams P, int
       if (rcut > 0u) {
         // the target's rank among the group's elements in index order
         uint32_t before = 0;
-        for (int64_t j = tid; j < t; j += kHT) {
+        for (int64_t j = tid; j < t; j += NT) {
           const uint32_t kj = okey16x2(bits16<E>(x[j])) & 0xffffu;
           before += (kj >= gk_lo && kj <= gk_hi) ? 1u : 0u;
         }
         uint32_t bs[1] = {before};
-        block_sum_n<uint32_t, 1>(bs, sh.red_u);
+        block_sum1<uint32_t, 1, NW>(bs, sh.red_u + 8 * NW);
         kept = bs[0] >= rcut;
       }
     }
@@ -1366,8 +1675,14 @@ __global__ __launch_bounds__(kHT) void filter_resolve_kernel(FilterParams P) {
 template <class E>
 int launch_hist(const FilterParams& P, int64_t rows, int all_rows, hipStream_t st) {
   // the compact kernel first; the rows it flags go to filter_hist_kernel
-  hipLaunchKernelGGL((filter_compact_kernel<E>), dim3((unsigned)rows), dim3(kHT), 0, st, P,
-                     all_rows);
+  using G = typename std::conditional<std::is_same<E, BF16>::value, CompactWindow,
+                                      CompactFull>::type;
+  if (P.dec16)
+    hipLaunchKernelGGL((filter_compact_kernel<E, G, true>), dim3((unsigned)rows), dim3(G::NT), 0, st,
+                       P, all_rows);
+  else
+    hipLaunchKernelGGL((filter_compact_kernel<E, G, false>), dim3((unsigned)rows), dim3(G::NT), 0,
+                       st, P, all_rows);
   if (int e = check_launch("filter_compact_kernel")) return e;
   hipLaunchKernelGGL((filter_hist_kernel<E, 0, false>), dim3((unsigned)rows), dim3(kHT), 0, st, P,
                      0);
