@@ -57,10 +57,14 @@ struct LseState {
 // merges lanes and waves.  On thread 0 it returns the row max M and
 // logsum = log(sum exp(x - M)); other threads' outputs are unspecified.
 // `between` runs once, after the first batch of loads is issued, so that the
-// caller's own scalar loads overlap the row's first vector loads.
+// caller's own scalar loads overlap the row's first vector loads.  With
+// 0 <= pick < V, *picked (thread 0) is x[pick], taken from the streamed
+// values by the lane that holds it (no load of its own that would have to wait
+// for the target index), and 0 otherwise.
 template <class E, int W, int U, class F>
 __device__ __forceinline__ void row_lse(const typename E::raw* x, int64_t V, int tid, F&& between,
-                                        float& M_out, float& logsum_out) {
+                                        float& M_out, float& logsum_out, int64_t pick = -1,
+                                        float* picked = nullptr) {
   constexpr int NT = 64 * W;
   constexpr int VEC = E::kVec;
   constexpr int BATCH = U * NT;  // vectors per workgroup per batch
@@ -70,16 +74,21 @@ __device__ __forceinline__ void row_lse(const typename E::raw* x, int64_t V, int
   const int nbatch = (nvec + BATCH - 1) / BATCH;
 
   // Every batch is U loads per lane issued together; lanes past the end of the
-  // row take -inf, which leaves the running max and sum unchanged.  Masking the
-  // last batch instead of finishing it one vector at a time keeps the whole
-  // row's loads in flight when a lane has only one batch (short rows).
-  const vu4 ninf = vu4{E::kNegInf2, E::kNegInf2, E::kNegInf2, E::kNegInf2};
+  // row read the row's last vector again and take -inf in its place, which
+  // leaves the running max and sum unchanged.  Masking the last batch instead of
+  // finishing it one vector at a time keeps the whole row's loads in flight when
+  // a lane has only one batch (short rows); issuing every load unconditionally
+  // (the mask applied where the values are used) lets the scalar loads that
+  // follow go out while the batch is still in flight.
   vu4 q[U];
+  uint32_t live = 0;  // bit u: vector u of the batch is inside the row
   auto issue = [&](int base) {
+    live = 0;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int j = base + u * NT;
-      q[u] = (j < nvec) ? __builtin_nontemporal_load(xv + j) : ninf;
+      q[u] = __builtin_nontemporal_load(xv + min(j, nvec - 1));
+      live |= (j < nvec ? 1u : 0u) << u;
     }
   };
   if (nbatch > 0) issue(tid);
@@ -92,21 +101,44 @@ __device__ __forceinline__ void row_lse(const typename E::raw* x, int64_t V, int
   // keep the batch's loads ahead of the arithmetic that consumes them
   __builtin_amdgcn_sched_barrier(0);
 
+  // the picked element's vector and position in it (pvec = -1: in the head or
+  // tail, or no pick)
+  const bool want = picked != nullptr && pick >= 0 && pick < V;
+  const int64_t pb = want ? pick - span.head : -1;
+  const int pvec = (pb >= 0 && pb < (int64_t)nvec * VEC) ? (int)(pb / VEC) : -1;
+  const int pel = pvec >= 0 ? (int)(pb - (int64_t)pvec * VEC) : 0;
+  float pv = 0.f;
   LseState st;
+  constexpr int UC = U < 8 ? U : 8;  // vectors per add (bounds the unpacked registers)
   for (int k = 0; k < nbatch; ++k) {
-    float v[U * VEC];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      float w[VEC];
-      E::unpack(q[u], w);
+    for (int u0 = 0; u0 < U; u0 += UC) {
+      float v[UC * VEC];
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) v[u * VEC + e] = w[e];
+      for (int uu = 0; uu < UC; ++uu) {
+        const int u = u0 + uu;
+        float w[VEC];
+        E::unpack(q[u], w);
+        const bool in_row = ((live >> u) & 1u) != 0u;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) v[uu * VEC + e] = in_row ? w[e] : -INFINITY;
+        if (tid + k * BATCH + u * NT == pvec) {
+#pragma unroll
+          for (int e = 0; e < VEC; ++e)
+            if (e == pel) pv = w[e];
+        }
+      }
+      st.add(v);
+      __builtin_amdgcn_sched_barrier(0);  // one chunk's registers at a time
     }
-    st.add(v);
     if (k + 1 < nbatch) issue(tid + (k + 1) * BATCH);
     __builtin_amdgcn_sched_barrier(0);
   }
   st.add(ht);
+  if (want && pvec < 0) {
+    if (tid == pick) pv = ht[0];
+    if (ti == pick) pv = ht[1];
+  }
 
   // merge lanes: the row max and the sum re-based to it
   float M = wave_max(st.m);
@@ -114,12 +146,15 @@ __device__ __forceinline__ void row_lse(const typename E::raw* x, int64_t V, int
   const float OFF = M * kLog2e;
   s = (st.m == -INFINITY) ? 0.f : s * fast_exp2(st.off - OFF);
   s = wave_sum(s);
+  // one lane holds the picked value, every other lane 0: the sums are exact
+  if (want) pv = wave_sum(pv);
   if constexpr (W > 1) {
-    __shared__ float sm[W], ss[W];
+    __shared__ float sm[W], ss[W], sp[W];
     const int wv = tid / 64, lane = tid % 64;
     if (lane == 0) {
       sm[wv] = M;
       ss[wv] = s;
+      sp[wv] = pv;
     }
     __syncthreads();
     if (tid == 0) {
@@ -133,8 +168,15 @@ __device__ __forceinline__ void row_lse(const typename E::raw* x, int64_t V, int
         sb2 += (sm[k] == -INFINITY) ? 0.f : ss[k] * fast_exp2(sm[k] * kLog2e - OFFb);
       M = Mb;
       s = sb2;
+      if (want) {
+        float pt = 0.f;
+#pragma unroll
+        for (int k = 0; k < W; ++k) pt += sp[k];
+        pv = pt;
+      }
     }
   }
+  if (picked != nullptr) *picked = pv;
   // s = sum 2^(x*log2e - fl(M*log2e)); undo the rounding of the offset so
   // that logsum = log(sum exp(x - M)).
   const float corr = fmaf(M, kLog2e, -(M * kLog2e));
@@ -143,7 +185,7 @@ __device__ __forceinline__ void row_lse(const typename E::raw* x, int64_t V, int
 }
 
 template <class E, int W, int U>
-__global__ __launch_bounds__(64 * W) void logprob_fwd_kernel(
+__global__ __launch_bounds__(64 * W, U > 8 ? 4 : 1) void logprob_fwd_kernel(
     const typename E::raw* __restrict__ logits, int64_t R, int64_t V, int64_t sb, int64_t sr,
     const int64_t* __restrict__ target, int64_t tsb, int64_t tsr, int64_t vs, int64_t ve,
     float* __restrict__ out, float* __restrict__ stats) {
@@ -156,9 +198,9 @@ __global__ __launch_bounds__(64 * W) void logprob_fwd_kernel(
   const int64_t t = target[b * tsb + r * tsr];
   // targets outside the vocabulary slice (or past this row) carry no one-hot
   const bool tmask = (t < vs) || (t >= ve) || (t - vs >= V);
-  const int64_t tl = tmask ? 0 : (t - vs);
+  const int64_t tl = tmask ? -1 : (t - vs);
   float xt = 0.f, M, logsum;
-  row_lse<E, W, U>(x, V, tid, [&] { if (tid == 0) xt = E::load(x + tl); }, M, logsum);
+  row_lse<E, W, U>(x, V, tid, [] {}, M, logsum, tl, &xt);
   if (tid == 0) {
     const float lp = (xt - M) - logsum;
     out[row] = tmask ? 0.f : lp;
@@ -357,11 +399,12 @@ struct FlatBwd {
   void* gin;
 };
 
-// One 4 KB piece (256 16-byte vectors) by a workgroup of NT threads, U vectors
-// per lane NT vectors apart.
+// One span of NT * U 16-byte vectors (piece `piece` of that size; 256 vectors
+// is a 4 KB piece) by a workgroup of NT threads, U vectors per lane NT
+// vectors apart.
 template <class E, int NT, int U>
 __device__ __forceinline__ void bwd_flat_piece(const FlatBwd& A, int64_t piece) {
-  static_assert(NT * U == kFlatThreads * kFlatVecs, "a piece is 256 vectors");
+  static_assert((NT * U) % (kFlatThreads * kFlatVecs) == 0, "whole 4 KB pieces");
   constexpr int VEC = E::kVec;
   const int64_t R = A.R, vs = A.vs, ve = A.ve, V = A.V;
   const uint32_t Rt = A.Rt, nvr = A.nvr, nvec = A.nvec;
@@ -433,22 +476,24 @@ __global__ __launch_bounds__(kFlatThreads) void logprob_bwd_flat_kernel(FlatBwd 
 // The early-backward recheck's redo on the flat schedule.  Launches with no
 // flag set are the common case, and their cost is the number of (empty)
 // workgroups dispatched; the redo itself is fastest with one workgroup per
-// piece.  Compromise: single-wave workgroups (four vectors per lane) in a
-// grid-stride loop over the pieces, kRedoGrid of them (two per wave slot, so
-// the later ones fill slots that free up early).  Measured on the backward of the
-// [8, 2048, 151936] bf16 GRPO rows: redo 1.50 ms and 15 us with no flag set;
-// one two-wave workgroup per piece 1.26 ms but 0.28 ms with no flag set; two-wave
-// workgroups over all 8192 wave slots 1.62 ms.  The flags are tested per wave
-// (one load per lane and a ballot, no barrier).  Same pieces and arithmetic as
-// logprob_bwd_flat_kernel.
+// piece.  Compromise: single-wave workgroups in a grid-stride loop, kRedoGrid
+// of them (two per wave slot, so the later ones fill slots that free up
+// early), one 4 KB piece (four vectors per lane) per step.  Measured on the
+// backward of the [8, 2048, 151936] bf16 GRPO rows: 1.50 ms and 15 us with no
+// flag set; two pieces per step 1.54 ms; one two-wave workgroup per piece
+// 1.26 ms but 0.28 ms with no flag set; two-wave workgroups over all 8192
+// wave slots 1.62 ms.  The flags are tested per wave (one load per lane and a
+// ballot, no barrier).  Same pieces and arithmetic as logprob_bwd_flat_kernel.
+constexpr int kRedoPieces = 1;  // 4 KB pieces per grid-stride step
 template <class E>
 __global__ __launch_bounds__(64) void logprob_bwd_flat_redo_kernel(
     FlatBwd A, int64_t npieces, const int* __restrict__ flags, int nflags) {
   const int lane = threadIdx.x & 63;
   const int f = lane < nflags ? flags[lane] : 0;
   if (__ballot(f != 0) == 0ull) return;
-  for (int64_t piece = blockIdx.x; piece < npieces; piece += gridDim.x)
-    bwd_flat_piece<E, 64, 4>(A, piece);
+  const int64_t nsteps = (npieces + kRedoPieces - 1) / kRedoPieces;
+  for (int64_t step = blockIdx.x; step < nsteps; step += gridDim.x)
+    bwd_flat_piece<E, 64, 4 * kRedoPieces>(A, step);
 }
 
 // Backward of the K-id gather (reference model_utils.py:750-805):
@@ -637,25 +682,22 @@ __global__ __launch_bounds__(256) void bwd_redo_kernel(
   }
 }
 
-// Waves per row for the forward: at least 4 (fewer rows in flight at a time
-// keeps the concurrently streamed address window narrower, measured +5% read
-// bandwidth over one wave per row), more when there are too few rows to give
-// every CU work.
-int pick_waves(int64_t rows) {
-  int w = 4;
-  while (w < 16 && rows * w < 8192) w <<= 1;
-  return w;
-}
+// Waves per row for the forward: 4 (fewer rows in flight at a time keeps the
+// concurrently streamed address window narrower, measured +5% read bandwidth
+// over one wave per row), 8 when there are too few rows to give every CU work.
+// Not 16: two 512-thread rows fit a CU at these register counts, one
+// 1024-thread row does, so 510 rows of 1024 threads ran in two rounds (fp32
+// [2, 255, 32000]: 15.6 us at 16 waves, 13.9 us at 8).
+int pick_waves(int64_t rows) { return rows * 4 < 8192 ? 8 : 4; }
 
 // The backward always uses 16-wave (1024-thread) rows: measured best for
 // both phases on the GRPO workload.
 constexpr int kBwdWaves = 16;
 
-template <class E, int W>
+template <class E, int W, int U = 8>
 void launch_fwd(int64_t rows, hipStream_t st, const void* logits, int64_t R, int64_t V, int64_t sb,
                 int64_t sr, const int64_t* target, int64_t tsb, int64_t tsr, int64_t vs, int64_t ve,
                 float* out, float* stats) {
-  constexpr int U = 8;
   hipLaunchKernelGGL((logprob_fwd_kernel<E, W, U>), dim3((unsigned)rows), dim3(64 * W), 0, st,
                      static_cast<const typename E::raw*>(logits), R, V, sb, sr, target, tsb, tsr, vs,
                      ve, out, stats);
@@ -667,8 +709,7 @@ void dispatch_fwd(int w, int64_t rows, hipStream_t st, const void* logits, int64
                   int64_t vs, int64_t ve, float* out, float* stats) {
   switch (w) {
     case 4: launch_fwd<E, 4>(rows, st, logits, R, V, sb, sr, target, tsb, tsr, vs, ve, out, stats); break;
-    case 8: launch_fwd<E, 8>(rows, st, logits, R, V, sb, sr, target, tsb, tsr, vs, ve, out, stats); break;
-    default: launch_fwd<E, 16>(rows, st, logits, R, V, sb, sr, target, tsb, tsr, vs, ve, out, stats); break;
+    default: launch_fwd<E, 8>(rows, st, logits, R, V, sb, sr, target, tsb, tsr, vs, ve, out, stats); break;
   }
 }
 

@@ -995,13 +995,6 @@ __global__ __launch_bounds__(G::NT, 2048 / G::NT) void filter_compact_kernel(Fil
   const raw* x = static_cast<const raw*>(P.logits) + b * P.sb + r * P.sr;
   const int tid = threadIdx.x;
   const int64_t V = P.V;
-  // the target and its value, loaded while the row is counted
-  int64_t t = -1;
-  uint32_t xt_bits = 0u;
-  if (P.out != nullptr) {
-    t = P.target[b * P.tsb + r * P.tsr];
-    if (t >= 0 && t < V) xt_bits = bits16<E>(x[t]);
-  }
   const RowSpan<E> sp(x, V);
   const vu4* xv = reinterpret_cast<const vu4*>(x + sp.head);
   const int64_t nvec = sp.nvec;
@@ -1019,6 +1012,13 @@ __global__ __launch_bounds__(G::NT, 2048 / G::NT) void filter_compact_kernel(Fil
     sh.ent_lo = sh.pos_lo = sh.ent_hi = sh.pos_hi = 0u;
   }
   __syncthreads();
+  // the target and its value, loaded while the row is counted
+  int64_t t = -1;
+  uint32_t xt_bits = 0u;
+  if (P.out != nullptr) {
+    t = P.target[b * P.tsb + r * P.tsr];
+    if (t >= 0 && t < V) xt_bits = bits16<E>(x[t]);
+  }
 
   // ---- one pass over the row: every value counted under its order key ----
   // A key outside the table (window geometry) is clamped to kLimit, whose
