@@ -540,6 +540,13 @@ def bench_workload(args) -> None:
         esz = 2
         scale_bytes = 2 * B * S * V * esz
         fwd_bytes, bwd_bytes = rows * V * esz, B * S * V * esz
+        kept_list = k is not None and 1 <= k <= 1024
+        if not kept_list:
+            # No kept list is saved for these rows (top-p alone keeps most of the
+            # vocabulary: a list of kept ids and probabilities would outweigh the
+            # row), so the backward re-reads the logits of every row with a
+            # non-zero upstream gradient: those bytes are compulsory here.
+            bwd_bytes += int((g[:, : S - 1] != 0).sum().item()) * V * esz
         if w == "filtered16_fwd":
             work = torch.empty_like(raw)
 
