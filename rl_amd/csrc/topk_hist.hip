@@ -1064,9 +1064,10 @@ __global__ __launch_bounds__(G::NT, 2048 / G::NT) void filter_compact_kernel(Fil
     // Full batches (UB vectors per lane, every lane in bounds) are addressed
     // from a uniform batch base plus per-lane offsets that do not change, and
     // two are in flight: the next one is issued before the current one is
-    // counted.  A prefetch past the last full batch reads that batch again
-    // (from cache, not counted), so that every issue is unconditional and the
-    // waits exact.  The remaining vectors follow as one guarded batch.
+    // counted.  A prefetch past the last full batch reads the row's first
+    // vector in every lane (one line, not counted), so that every issue is
+    // unconditional and the waits exact.  The remaining vectors follow as one
+    // guarded batch.
     constexpr int UB = 8;
     constexpr int kStep = UB * NT;
     const int nv = (int)nvec;  // < 2^28: V < 2^31
@@ -1074,11 +1075,14 @@ __global__ __launch_bounds__(G::NT, 2048 / G::NT) void filter_compact_kernel(Fil
     const char* xb = reinterpret_cast<const char*>(xv);
     vu4 qa[UB], qb[UB];
     auto issue = [&](vu4(&q)[UB], int bi) {
-      const char* bp = xb + (size_t)bi * (size_t)kStep * 16u;
+      // all ones for a batch of the row, zero past the last one (masks, not
+      // selects: the compiler keeps masks branch-free)
+      const uint32_t real = 0u - (uint32_t)(bi < nfull);
+      const char* bp = xb + (size_t)((uint32_t)bi & real) * (size_t)kStep * 16u;
 #pragma unroll
       for (int u = 0; u < UB; ++u)
         q[u] = __builtin_nontemporal_load(
-            reinterpret_cast<const vu4*>(bp + (uint32_t)(tid + u * NT) * 16u));
+            reinterpret_cast<const vu4*>(bp + (((uint32_t)(tid + u * NT) * 16u) & real)));
       __builtin_amdgcn_sched_barrier(0);  // every load issued before the counting that follows
     };
     auto count_vec = [&](const vu4& q) {
@@ -1103,7 +1107,7 @@ __global__ __launch_bounds__(G::NT, 2048 / G::NT) void filter_compact_kernel(Fil
     for (int pi = 0; pi < npairs; ++pi) {
       issue(qb, 2 * pi + 1);
       count_batch(qa);
-      issue(qa, min(2 * pi + 2, nfull - 1));
+      issue(qa, 2 * pi + 2);
       count_batch(qb);
     }
     if (nfull & 1) count_batch(qa);
