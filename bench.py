@@ -448,12 +448,14 @@ def bench_workload(args) -> None:
     Algorithmic bytes per next-token row of V entries of s bytes: forward V*s
     (read); unfiltered backward V*s read for rows with a non-zero upstream
     gradient plus V*s written for every row; filtered backward V*s written
-    (the kept set saved by the forward replaces the re-read); the in-place
-    temperature division V*s read + V*s written for every row.
+    (the kept set saved by the forward replaces the re-read) plus, for rows
+    without a kept list (top-p alone, k > 1024), V*s read for rows with a
+    non-zero upstream gradient; the in-place temperature division V*s read +
+    V*s written for every row.
     """
     import torch
 
-    from rl_amd import workloads
+    from rl_amd import _C, workloads
     from rl_amd.distributed.model_utils import from_parallel_logits_to_logprobs
 
     dev = torch.device("cuda", 0)
@@ -476,6 +478,26 @@ def bench_workload(args) -> None:
         ms_step, ms = _timed(step, args.steps, args.warmup, ["mirl_logprob_fwd"])
         rows = B * (S - 1)
         esz = 4
+        # An event pair around one 14-us launch measures the pair's own cost as
+        # well; the kernel's launch duration comes from one pair of events
+        # around a burst of back-to-back launches of the entry point (the same
+        # inputs and outputs, the rotating copies in turn).
+        outs = [torch.empty((B, S - 1), dtype=torch.float32, device=dev) for _ in copies]
+        tgts = [c["input_ids"][:, 1:] for c in copies]
+        burst = 200
+        for k in range(len(copies)):
+            _C.logprob_fwd(copies[k]["logits"], tgts[k], 0, V, outs[k], None)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for k in range(burst):
+            j = k % len(copies)
+            _C.logprob_fwd(copies[j]["logits"], tgts[j], 0, V, outs[j], None)
+        e1.record()
+        torch.cuda.synchronize()
+        extra["logprob_fwd_event_pair_ms"] = ms.get("mirl_logprob_fwd", 0.0)
+        ms["mirl_logprob_fwd"] = e0.elapsed_time(e1) / burst
+        extra["launch_duration_from"] = f"events around {burst} back-to-back launches"
         roof = _roofline("mirl_logprob_fwd", rows * V * esz, ms.get("mirl_logprob_fwd", 0.0), w)
         step_bytes = rows * V * esz
         cfg = {"workload": "logprob_fwd_f32", "logits": [B, S, V], "next_token_rows": rows,
@@ -487,7 +509,8 @@ def bench_workload(args) -> None:
             from oracle.logprob import selected_logprobs
 
             return _cpu_timed(lambda: selected_logprobs(xc[:, :-1], tc[:, 1:], 0, V), rows,
-                              f"the whole fp32 [{B}, {S}, {V}] batch ({rows} next-token rows), forward", secs)
+                              f"the whole fp32 [{B}, {S}, {V}] batch ({rows} next-token rows), forward", secs,
+                              max_passes=100000)
     elif w == "long_context":
         d = workloads.long_context_bf16(device=dev)
         logits = d["logits"].requires_grad_(True)
