@@ -304,3 +304,37 @@ def test_full_size_workload_sampled_rows():
         assert torch.equal(keep1.cpu(), keep_o1)
     assert gr[:, -1].abs().max().item() == 0
     del x, gr
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("k,p", [(None, 0.9), (None, 0.5), (3000, 0.9)])
+def test_values_outside_the_bf16_count_window(dtype, k, p):
+    """Rows holding values of magnitude 512 and beyond (and -inf, +-0) next to ordinary ones.
+
+    The bf16 histogram kernel counts |x| < 512 in its window table and hands rows
+    with any other value to the full-table kernel; both must give the oracle's
+    keep sets and logprobs.  Rows: plain N(0, 1); one huge logit (+600); -inf
+    entries and -1000; a mix of +-0 and large negatives; odd V so that rows are
+    not 16-byte aligned (unaligned heads and tails)."""
+    print("[case] window outliers", dtype, k, p, flush=True)
+    V = 6001
+    g = torch.Generator().manual_seed(31)
+    x = torch.randn(2, 5, V, generator=g)
+    x[0, 1, 17] = 600.0
+    x[0, 2, :50] = -float("inf")
+    x[0, 2, 60] = -1000.0
+    x[1, 0, ::7] = 0.0
+    x[1, 0, 1::11] = -0.0
+    x[1, 0, 5] = -700.0
+    x[1, 3, 100:] = (x[1, 3, 100:] * 300.0)
+    x = x.to(dtype)
+    ids = torch.randint(0, V, (2, 5), generator=g)
+    ids[0, 1] = 17
+    lp_o, keep_o = filtered_logprobs(x, ids, k, p)
+    lp = DistributedLogprobWithSampling.apply(x.to(DEV), ids.to(DEV), None, k, p, True)
+    lp_c = lp.cpu()
+    assert torch.equal(torch.isinf(lp_c), torch.isinf(lp_o))
+    fin = torch.isfinite(lp_o)
+    torch.testing.assert_close(lp_c[fin], lp_o[fin], rtol=0, atol=2e-3)
+    _, keep = apply_top_k_top_p(x.to(DEV), k, p)
+    assert torch.equal(keep.cpu(), keep_o)
