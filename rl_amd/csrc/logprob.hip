@@ -109,28 +109,22 @@ __device__ __forceinline__ void row_lse(const typename E::raw* x, int64_t V, int
   const int pel = pvec >= 0 ? (int)(pb - (int64_t)pvec * VEC) : 0;
   float pv = 0.f;
   LseState st;
-  constexpr int UC = U < 8 ? U : 8;  // vectors per add (bounds the unpacked registers)
   for (int k = 0; k < nbatch; ++k) {
+    float v[U * VEC];
 #pragma unroll
-    for (int u0 = 0; u0 < U; u0 += UC) {
-      float v[UC * VEC];
+    for (int u = 0; u < U; ++u) {
+      float w[VEC];
+      E::unpack(q[u], w);
+      const bool in_row = ((live >> u) & 1u) != 0u;
 #pragma unroll
-      for (int uu = 0; uu < UC; ++uu) {
-        const int u = u0 + uu;
-        float w[VEC];
-        E::unpack(q[u], w);
-        const bool in_row = ((live >> u) & 1u) != 0u;
+      for (int e = 0; e < VEC; ++e) v[u * VEC + e] = in_row ? w[e] : -INFINITY;
+      if (tid + k * BATCH + u * NT == pvec) {
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) v[uu * VEC + e] = in_row ? w[e] : -INFINITY;
-        if (tid + k * BATCH + u * NT == pvec) {
-#pragma unroll
-          for (int e = 0; e < VEC; ++e)
-            if (e == pel) pv = w[e];
-        }
+        for (int e = 0; e < VEC; ++e)
+          if (e == pel) pv = w[e];
       }
-      st.add(v);
-      __builtin_amdgcn_sched_barrier(0);  // one chunk's registers at a time
     }
+    st.add(v);
     if (k + 1 < nbatch) issue(tid + (k + 1) * BATCH);
     __builtin_amdgcn_sched_barrier(0);
   }
@@ -185,7 +179,7 @@ __device__ __forceinline__ void row_lse(const typename E::raw* x, int64_t V, int
 }
 
 template <class E, int W, int U>
-__global__ __launch_bounds__(64 * W, U > 8 ? 4 : 1) void logprob_fwd_kernel(
+__global__ __launch_bounds__(64 * W) void logprob_fwd_kernel(
     const typename E::raw* __restrict__ logits, int64_t R, int64_t V, int64_t sb, int64_t sr,
     const int64_t* __restrict__ target, int64_t tsb, int64_t tsr, int64_t vs, int64_t ve,
     float* __restrict__ out, float* __restrict__ stats) {

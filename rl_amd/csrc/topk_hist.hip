@@ -983,6 +983,9 @@ __device__ __forceinline__ uint32_t okey16x2(uint32_t w) {
   return w ^ ((neg * 0xffffu) | 0x80008000u);
 }
 
+// The second launch bound is the minimum number of waves per SIMD: four 128-register
+// waves (two 512-thread rows per CU for the window table; one 1024-thread row for
+// the full one).
 template <class E, class G, bool DEC16>
 __global__ __launch_bounds__(G::NT, 2048 / G::NT) void filter_compact_kernel(FilterParams P, int all_rows) {
   using raw = typename E::raw;
