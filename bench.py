@@ -227,6 +227,7 @@ def main() -> None:
     esz = logits.element_size()
     fwd_bytes = rows * V * esz
     bwd_bytes = active_rows * V * esz + B * S * V * esz
+    redo_bytes = 2 * active_rows * V * esz
     fwd_ms, bwd_ms = avg_ms("mirl_logprob_fwd"), avg_ms("mirl_logprob_bwd")
     # with a scaled loss the early backward (launched for the unit loss gradient)
     # is checked and redone by the recheck launch; both are the step's backward
@@ -290,7 +291,9 @@ def main() -> None:
         # loss_scale != 1 only: the step with the early backward forced on every
         # step (wasted early backward + check + redo), and the redo's rate
         "always_speculate_ms_per_step": None if always is None else always[0],
-        "logprob_bwd_recheck_gbps": (bwd_bytes / (recheck_ms * 1e-3) / 1e9) if always is not None and recheck_ms > 0 else None,
+        # the redo reads and rewrites the rows whose upstream gradient the scale
+        # changed (the active rows) and leaves the zero-gradient rows as they are
+        "logprob_bwd_recheck_gbps": (redo_bytes / (recheck_ms * 1e-3) / 1e9) if always is not None and recheck_ms > 0 else None,
         "roofline": {
             "kernel": "mirl_logprob_bwd",
             "bound": "hbm",

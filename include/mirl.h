@@ -99,7 +99,10 @@ int mirl_logprob_bwd(const void* logits, int dtype, int64_t B, int64_t R,
  * here: one kernel compares them bit for bit and writes `flag` (device ints,
  * one per checking workgroup, at most MIRL_RECHECK_FLAGS; nonzero = they
  * differ); a second recomputes grad_in from grad_out when any flag is set and
- * returns at once otherwise.  Arguments as for mirl_logprob_bwd.
+ * returns at once otherwise.  The recomputation leaves the rows whose
+ * grad_out equals grad_used (and the rows past R) as the earlier call wrote
+ * them, so grad_in must still hold that call's output there.  Arguments as
+ * for mirl_logprob_bwd.
  *
  * Replaces: nothing in the reference (an ordering device: it lets the
  * backward start before the host has synchronised on the loss's metrics).

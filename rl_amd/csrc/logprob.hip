@@ -391,12 +391,16 @@ struct FlatBwd {
   const float* g;
   int64_t gsb, gsr;
   void* gin;
+  const float* gu;  // redo only: the [B, R] upstream gradient the gradient was formed with
 };
 
 // One span of NT * U 16-byte vectors (piece `piece` of that size; 256 vectors
 // is a 4 KB piece) by a workgroup of NT threads, U vectors per lane NT
-// vectors apart.
-template <class E, int NT, int U>
+// vectors apart.  SKIP (the redo): vectors of rows whose upstream gradient
+// equals A.gu's bit for bit already hold what this would write (same
+// arithmetic from the same inputs) and are neither read nor written; rows past
+// R hold zeros either way.
+template <class E, int NT, int U, bool SKIP = false>
 __device__ __forceinline__ void bwd_flat_piece(const FlatBwd& A, int64_t piece) {
   static_assert((NT * U) % (kFlatThreads * kFlatVecs) == 0, "whole 4 KB pieces");
   constexpr int VEC = E::kVec;
@@ -422,9 +426,11 @@ __device__ __forceinline__ void bwd_flat_piece(const FlatBwd& A, int64_t piece) 
     gv[u] = 0.f;
     M[u] = LS[u] = 0.f;
     t[u] = -1;
+    if (SKIP && (int64_t)r >= R) ok[u] = false;
     if (ok[u] && (int64_t)r < R) {
       const int64_t srow = (int64_t)b * R + r;
       gv[u] = g[(int64_t)b * gsb + (int64_t)r * gsr];
+      if (SKIP && __float_as_uint(gv[u]) == __float_as_uint(A.gu[srow])) ok[u] = false;
       M[u] = stats[2 * srow];
       LS[u] = stats[2 * srow + 1];
       t[u] = target[(int64_t)b * tsb + (int64_t)r * tsr];
@@ -478,8 +484,10 @@ __global__ __launch_bounds__(kFlatThreads) void logprob_bwd_flat_kernel(FlatBwd 
 // 1.26 ms but 0.28 ms with no flag set; two-wave workgroups over all 8192
 // wave slots 1.62 ms.  The flags are tested per wave (one load per lane and a
 // ballot, no barrier).  Same pieces and arithmetic as logprob_bwd_flat_kernel.
+// SKIP: rows whose upstream gradient matched (the zero-gradient rows of a
+// scaled loss) are left as the early backward wrote them.
 constexpr int kRedoPieces = 1;  // 4 KB pieces per grid-stride step
-template <class E>
+template <class E, bool SKIP>
 __global__ __launch_bounds__(64) void logprob_bwd_flat_redo_kernel(
     FlatBwd A, int64_t npieces, const int* __restrict__ flags, int nflags) {
   const int lane = threadIdx.x & 63;
@@ -487,7 +495,7 @@ __global__ __launch_bounds__(64) void logprob_bwd_flat_redo_kernel(
   if (__ballot(f != 0) == 0ull) return;
   const int64_t nsteps = (npieces + kRedoPieces - 1) / kRedoPieces;
   for (int64_t step = blockIdx.x; step < nsteps; step += gridDim.x)
-    bwd_flat_piece<E, 64, 4 * kRedoPieces>(A, step);
+    bwd_flat_piece<E, 64, 4 * kRedoPieces, SKIP>(A, step);
 }
 
 // Backward of the K-id gather (reference model_utils.py:750-805):
@@ -753,7 +761,7 @@ bool flat_bwd_layout(int64_t rows, const void* logits, int64_t R, int64_t Rt, in
   const int shift = (P - to4k) & (P - 1);
   *npieces = (nvec + shift + P - 1) / P;
   *A = FlatBwd{logits, R, (uint32_t)Rt, (uint32_t)nvr, (uint32_t)nvec, shift, target, tsb, tsr,
-               vs, ve, V, stats, g, gsb, gsr, gin};
+               vs, ve, V, stats, g, gsb, gsr, gin, nullptr};
   return true;
 }
 
@@ -764,21 +772,28 @@ static_assert(kCheckBlocks <= 64, "the flat redo tests at most 64 flags, one per
 
 // Redo of the backward after a failed early-backward check (every launch
 // returns at once when no flag is set): the flat schedule when the layout
-// allows it, row by row otherwise.
+// allows it, row by row otherwise.  g_used (contiguous [B, R], or null): the
+// upstream gradient the early backward used; the flat redo leaves the rows
+// where it equals g alone.
 template <class E>
 void dispatch_bwd_redo(int64_t rows, hipStream_t st, const void* logits, int64_t R, int64_t Rt,
                        int64_t V, int64_t sb, int64_t sr, const int64_t* target, int64_t tsb,
                        int64_t tsr, int64_t vs, int64_t ve, const float* stats, const float* g,
                        int64_t gsb, int64_t gsr, void* gin, int64_t gisb, int64_t gisr,
-                       const int* flags, int nflags) {
+                       const int* flags, int nflags, const float* g_used) {
   using raw = typename E::raw;
   FlatBwd A;
   int64_t npieces = 0;
   if (flat_bwd_layout<E>(rows, logits, R, Rt, V, sb, sr, target, tsb, tsr, vs, ve, stats, g, gsb,
                          gsr, gin, gisb, gisr, &A, &npieces)) {
     const int64_t grid = npieces < kRedoGrid ? npieces : kRedoGrid;
-    hipLaunchKernelGGL((logprob_bwd_flat_redo_kernel<E>), dim3((unsigned)grid), dim3(64), 0, st, A,
-                       npieces, flags, nflags);
+    A.gu = g_used;
+    if (g_used)
+      hipLaunchKernelGGL((logprob_bwd_flat_redo_kernel<E, true>), dim3((unsigned)grid), dim3(64), 0,
+                         st, A, npieces, flags, nflags);
+    else
+      hipLaunchKernelGGL((logprob_bwd_flat_redo_kernel<E, false>), dim3((unsigned)grid), dim3(64),
+                         0, st, A, npieces, flags, nflags);
     return;
   }
   const unsigned grid = (unsigned)(rows < 1024 ? rows : 1024);
@@ -884,7 +899,7 @@ void gather_bwd_recheck(int64_t rows, hipStream_t st, const void* logits, int64_
   hipLaunchKernelGGL(gather_gsum_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, st,
                      g, R, gsb, gsr, gsk, K, rows, gsum, flags, nflags);
   dispatch_bwd_redo<E>(rows, st, logits, R, R, V, sb, sr, idx, isb, isr, 0, 0, stats, gsum, R, 1,
-                       gin, gisb, gisr, flags, nflags);
+                       gin, gisb, gisr, flags, nflags, nullptr);
   launch_gather_fixup<E>(rows, st, static_cast<const raw*>(logits), R, V, sb, sr, idx, K, isb, isr,
                          isk, vs, ve, stats, g, gsb, gsr, gsk, gsum, static_cast<raw*>(gin), gisb,
                          gisr, flags, nflags);
@@ -1119,7 +1134,7 @@ extern "C" int mirl_logprob_bwd_recheck(const void* logits, int dtype, int64_t B
 #define MIRL_REDO(E)                                                                          \
   dispatch_bwd_redo<E>(rows, st, logits, R, R_total, V, stride_b, stride_r, target, t_stride_b, \
                        t_stride_r, vocab_start, vocab_end, row_stats, grad_out, g_stride_b,     \
-                       g_stride_r, grad_in, gi_stride_b, gi_stride_r, flag, nflags)
+                       g_stride_r, grad_in, gi_stride_b, gi_stride_r, flag, nflags, grad_used)
   switch (dtype) {
     case MIRL_DTYPE_F32: MIRL_REDO(F32); break;
     case MIRL_DTYPE_BF16: MIRL_REDO(BF16); break;

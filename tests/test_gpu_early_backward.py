@@ -71,8 +71,11 @@ def test_plain_loss_bit_identical():
     assert torch.equal(g1, g0)
 
 
-@pytest.mark.parametrize("scale", [2.0, 0.5])
+@pytest.mark.parametrize("scale", [2.0, 0.5, 0.0])
 def test_scaled_loss_recomputes(scale):
+    """The redo rewrites the rows whose upstream gradient changed (all active rows; at
+    scale 0 they become zeros) and leaves the zero-gradient rows as the early launch
+    wrote them."""
     say("early backward: scaled", scale)
     d, gvs, gvt = _setup(4)
     g1, started = _grad(d, gvs, gvt, early=True, scale=scale)
