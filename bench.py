@@ -687,14 +687,17 @@ def bench_workload(args) -> None:
                               "mirl_transpose_bf16", "mirl_sum_splits_bf16"])
         rows = B * (S - 1)
         gemm = 2.0 * S * B * H * V  # one [S*B, H] x [H, V] product
-        # the backward runs the rows with a non-zero upstream gradient, in blocks of
-        # _BLOCK_CHUNKS * chunk_size * B rows
+        # the backward moves the rows with a non-zero upstream gradient to the front
+        # and runs all rows in blocks of _BLOCK_CHUNKS * chunk_size * B rows (counted
+        # on the device; launches of blocks past the active rows return at once):
+        # per-step kernel times are the average launch times the launches per step
         from rl_amd.distributed.linear_ce import _BLOCK_CHUNKS
 
         active = int((g != 0).sum().item())
         fwd_ms = ms.get("mirl_linear_ce_fwd", 0.0)
-        grad_chunks = -(-active // (_BLOCK_CHUNKS * 256 * B))
-        grad_ms = ms.get("mirl_linear_ce_grad", 0.0) * grad_chunks
+        T = S * B
+        n_blocks = -(-T // min(T, -(-(_BLOCK_CHUNKS * 256 * B) // 256) * 256))
+        grad_ms = ms.get("mirl_linear_ce_grad", 0.0) * n_blocks
         gemm_act = 2.0 * active * H * V
         tflops = gemm / (fwd_ms * 1e-3) / 1e12 if fwd_ms > 0 else 0.0
         roof = {"kernel": "mirl_linear_ce_fwd", "bound": "mfma", "achieved": tflops, "peak": PEAK_BF16_TFLOPS,
@@ -705,7 +708,7 @@ def bench_workload(args) -> None:
         extra["grad_kernel_tflops"] = gemm_act / (grad_ms * 1e-3) / 1e12 if grad_ms > 0 else None
         # dH and dW: two products of 2 * active * H * V each on mirl_gemm_bf16_abt
         # (average launch x launches per step: one dH and one dW per block)
-        gemm_ms = ms.get("mirl_gemm_bf16_abt", 0.0) * 2 * grad_chunks
+        gemm_ms = ms.get("mirl_gemm_bf16_abt", 0.0) * 2 * n_blocks
         extra["dh_dw_gemm_ms_per_step"] = gemm_ms
         extra["dh_dw_gemm_tflops"] = 2 * gemm_act / (gemm_ms * 1e-3) / 1e12 if gemm_ms > 0 else None
         step_bytes = None

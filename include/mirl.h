@@ -427,6 +427,11 @@ int mirl_linear_ce_fwd(const void* hidden, int64_t T, int64_t H, int64_t ldh,
  * NULL it also receives the transpose, grad_logits_t[v, r - row0], for the
  * 256-row tiles covering the range (rows past row0 + nrows as zeros; row
  * stride ldgt >= nrows rounded up to 256, a multiple of 8, 16-byte aligned).
+ * `row_count` (a device int64, or NULL): rows r >= *row_count are absent, as
+ * if nrows ended there; nothing is written for them in grad_logits, and
+ * grad_logits_t holds zeros for them only inside the 256-row tile that holds
+ * row *row_count - 1 (the caller's compacted active rows, counted on the
+ * device so that the host need not wait for the count).
  *
  * Replaces: the per-chunk logits recompute, softmax and one-hot gradient of
  * ChunkedDistributedHiddenStatesToLogprobs.backward
@@ -438,7 +443,8 @@ int mirl_linear_ce_grad(const void* hidden, int64_t T, int64_t H, int64_t ldh,
                         int64_t vocab_start, int64_t vocab_end, const float* row_stats,
                         const float* grad_out, int64_t g_stride_b, int64_t g_stride_s,
                         int64_t row0, int64_t nrows, void* grad_logits, int64_t ldg,
-                        void* grad_logits_t, int64_t ldgt, void* stream);
+                        void* grad_logits_t, int64_t ldgt, const int64_t* row_count,
+                        void* stream);
 
 /*
  * C = A . B^T for bf16 A [M, K] and B [N, K] (row strides lda, ldb, multiples
@@ -448,28 +454,48 @@ int mirl_linear_ce_grad(const void* hidden, int64_t T, int64_t H, int64_t ldh,
  *   else:       C[s, m, n] = the product over the s-th of k_splits ranges of
  *               K ([k_splits][M][ldc] fp32), or C[m, n] += C when accumulate
  *               (k_splits = 1).
+ * `count` (a device int64, or NULL) with c = *count - count_off:
+ *   count_axis MIRL_COUNT_ROWS: rows m >= c of A are absent (not read; their
+ *               output rows are not written);
+ *   count_axis MIRL_COUNT_K: the reduction stops at round_up(c, 128) (columns
+ *               of A and B past c up to there must hold finite values, zeros
+ *               for an exact product); with accumulate set and c <= 0 nothing
+ *               is written.  With both C and Cb given (k_splits = 1): the
+ *               output goes to Cb = bf16(A . B^T (+ C when accumulate)) when
+ *               *count <= final_at, to C otherwise: blocks of reduction rows
+ *               accumulate in fp32 and the last non-empty one rounds once.
  * The backward of the hidden-state logprobs forms dH = G . W and
  * dW = G^T . H with it, from G, its transpose and transposed copies of W and H.
  *
  * Replaces: the dH and dW matmuls of ChunkedDistributedHiddenStatesToLogprobs.backward
  * (nemo_rl/distributed/model_utils.py:2701-2716).
  */
+#define MIRL_COUNT_ROWS 0
+#define MIRL_COUNT_K 1
 int mirl_gemm_bf16_abt(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M,
                        int64_t N, int64_t K, int64_t k_splits, float* C, int64_t ldc,
-                       int accumulate, void* Cb, int64_t ldcb, void* stream);
+                       int accumulate, void* Cb, int64_t ldcb, const int64_t* count,
+                       int64_t count_off, int count_axis, int64_t final_at, void* stream);
 
-/* out[m, n] = bf16(sum_s part[s, m, n]) summed in s order (part [k_splits][M][ld] fp32,
- * out row stride ldo): the splits of mirl_gemm_bf16_abt.
- * Replaces: part of the dH matmul above (model_utils.py:2701-2703). */
+/* out[r(m), n] = bf16(sum_s part[s, m, n]) summed in s order (part [k_splits][M][ld]
+ * fp32, out row stride ldo): the splits of mirl_gemm_bf16_abt.  r(m) = out_rows[m]
+ * (a device int64 row map; rows mapped outside [0, out_nrows) are skipped) or m
+ * when out_rows is NULL.  With `count` (a device int64, or NULL), rows
+ * m >= *count - count_off are written as zeros without reading part.
+ * Replaces: part of the dH matmul above (model_utils.py:2701-2703) and the
+ * scatter of the active rows' dH back to their positions. */
 int mirl_sum_splits_bf16(const float* part, int64_t k_splits, int64_t M, int64_t N,
-                         int64_t ld, void* out, int64_t ldo, void* stream);
+                         int64_t ld, void* out, int64_t ldo, const int64_t* out_rows,
+                         int64_t out_nrows, const int64_t* count, int64_t count_off,
+                         void* stream);
 
 /* dst[c, r] = src[r, c] (bf16) for r < R, c < C, and 0 for R <= r < R_pad
- * (src row stride lds, dst row stride ldd >= R_pad): the transposed operands of
- * the hidden-state backward.
+ * (src row stride lds, dst row stride ldd >= R_pad), R = min(R, *count) when
+ * `count` (a device int64) is given: the transposed operands of the
+ * hidden-state backward.
  * Replaces: the transposes inside the dH / dW matmuls (model_utils.py:2701-2716). */
 int mirl_transpose_bf16(const void* src, int64_t R, int64_t C, int64_t lds, void* dst,
-                        int64_t ldd, int64_t R_pad, void* stream);
+                        int64_t ldd, int64_t R_pad, const int64_t* count, void* stream);
 
 /* ---------------------------------------------------------------------- */
 /* ClippedPG loss epilogue                                                  */

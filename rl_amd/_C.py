@@ -217,13 +217,14 @@ SIGNATURES = {
     "mirl_linear_ce_grad": (
         _I,
         [_P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _I64, _P, _P, _I64,
-         _I64, _I64, _I64, _P, _I64, _P, _I64, _P],
+         _I64, _I64, _I64, _P, _I64, _P, _I64, _P, _P],
     ),
     "mirl_gemm_bf16_abt": (
-        _I, [_P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _I, _P, _I64, _P]
+        _I, [_P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _I, _P, _I64, _P, _I64, _I,
+             _I64, _P]
     ),
-    "mirl_sum_splits_bf16": (_I, [_P, _I64, _I64, _I64, _I64, _P, _I64, _P]),
-    "mirl_transpose_bf16": (_I, [_P, _I64, _I64, _I64, _P, _I64, _I64, _P]),
+    "mirl_sum_splits_bf16": (_I, [_P, _I64, _I64, _I64, _I64, _P, _I64, _P, _I64, _P, _I64, _P]),
+    "mirl_transpose_bf16": (_I, [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _P]),
     "mirl_top_k_top_p_mask": (
         _I,
         [_P, _I, _I64, _I64, _I64, _I, ctypes.c_double, _I, _P, _P, _P, _P, _I64, _P, _I64, _P],
@@ -1166,10 +1167,13 @@ def linear_ce_grad(
     row0: int,
     grad_logits: torch.Tensor,
     grad_logits_t: Optional[torch.Tensor] = None,
+    count: Optional[torch.Tensor] = None,
 ) -> None:
     """grad_logits[i, :] = bf16((onehot(t) - softmax(logits)) * g) for rows row0 .. row0 + n - 1;
-    grad_logits_t (or None) receives the transpose [V, >= round_up(n, 256)]."""
+    grad_logits_t (or None) receives the transpose [V, >= round_up(n, 256)].  `count` (a
+    device int64 tensor of one element, or None): rows at or past it are absent."""
     dev = _require_gpu(hidden2d, weight, target, stats, grad_out, grad_logits)
+    _check_count(count, dev)
     _check_linear_ce(hidden2d, weight)
     T, H = hidden2d.shape
     V = weight.shape[0]
@@ -1182,54 +1186,99 @@ def linear_ce_grad(
         int(bsz), target.data_ptr(), target.stride(0), target.stride(1), int(vocab_start),
         int(vocab_end), stats.data_ptr(), grad_out.data_ptr(), grad_out.stride(0),
         grad_out.stride(1), int(row0), int(n), grad_logits.data_ptr(), grad_logits.stride(0),
-        _ptr(grad_logits_t), 0 if grad_logits_t is None else grad_logits_t.stride(0), _stream(dev),
+        _ptr(grad_logits_t), 0 if grad_logits_t is None else grad_logits_t.stride(0), _ptr(count),
+        _stream(dev),
     )
     _check(st, "mirl_linear_ce_grad")
 
 
+COUNT_ROWS = 0  # MIRL_COUNT_ROWS
+COUNT_K = 1  # MIRL_COUNT_K
+
+
+def _check_count(count: Optional[torch.Tensor], dev: torch.device) -> None:
+    if count is None:
+        return
+    _require(count.dtype == torch.int64 and count.numel() == 1 and count.device == dev,
+             "count is a one-element int64 tensor on the operands' device")
+
+
 def gemm_bf16_abt(a: torch.Tensor, b: torch.Tensor, k: int, out: torch.Tensor, k_splits: int = 1,
-                  accumulate: bool = False) -> None:
+                  accumulate: bool = False, count: Optional[torch.Tensor] = None,
+                  count_off: int = 0, count_axis: int = COUNT_ROWS,
+                  out_bf16: Optional[torch.Tensor] = None, final_at: int = 0) -> None:
     """out = a[:, :k] . b[:, :k]^T with fp32 accumulation on the MFMA units.
 
     a [M, >=k], b [N, >=k] bf16 (unit stride, rows multiples of 8 elements, k a
     multiple of 128); out bf16 [M, N] (k_splits 1, no accumulation), fp32 [M, N]
-    (out = or +=), or fp32 [k_splits, M, N] (one partial product per k range)."""
+    (out = or +=), or fp32 [k_splits, M, N] (one partial product per k range).
+    `count` (device int64, one element) with c = count - count_off: COUNT_ROWS
+    leaves rows of a at or past c absent; COUNT_K stops the reduction at
+    round_up(c, 128), and with `out_bf16` (out fp32 [M, N]) the result goes to
+    out_bf16 = bf16(product (+ out when accumulate)) when count <= final_at, to
+    out otherwise."""
     dev = _require_gpu(a, b, out)
+    _check_count(count, dev)
     _require(a.dtype == torch.bfloat16 and b.dtype == torch.bfloat16, "bf16 operands")
     _require(a.stride(-1) == 1 and b.stride(-1) == 1 and out.stride(-1) == 1, "unit stride on the last dim")
     M, N = a.shape[0], b.shape[0]
     if out.dtype == torch.bfloat16:
+        _require(out_bf16 is None, "out_bf16 goes with an fp32 out")
         cb, ldcb, c, ldc = out.data_ptr(), out.stride(0), None, 0
     else:
         _require(out.dtype == torch.float32, "out is bf16 or fp32")
         cb, ldcb, c, ldc = None, 0, out.data_ptr(), out.stride(-2)
+        if out_bf16 is not None:
+            _require(out_bf16.dtype == torch.bfloat16 and out_bf16.device == dev
+                     and out_bf16.stride(-1) == 1 and tuple(out_bf16.shape) == (M, N),
+                     "out_bf16 is a bf16 [M, N] tensor with unit stride on the last dim")
+            _require(out.dim() == 2 and tuple(out.shape) == (M, N), "out is fp32 [M, N]")
+            cb, ldcb = out_bf16.data_ptr(), out_bf16.stride(0)
     st = _launch(
         "mirl_gemm_bf16_abt", dev, a.data_ptr(), a.stride(0), b.data_ptr(), b.stride(0), M, N,
-        int(k), int(k_splits), c, ldc, int(bool(accumulate)), cb, ldcb, _stream(dev),
+        int(k), int(k_splits), c, ldc, int(bool(accumulate)), cb, ldcb, _ptr(count),
+        int(count_off), int(count_axis), int(final_at), _stream(dev),
     )
     _check(st, "mirl_gemm_bf16_abt")
 
 
-def sum_splits_bf16(part: torch.Tensor, out: torch.Tensor) -> None:
-    """out [M, N] bf16 = sum over dim 0 of part [S, M, N] fp32, in order."""
+def sum_splits_bf16(part: torch.Tensor, out: torch.Tensor, count: Optional[torch.Tensor] = None,
+                    count_off: int = 0, out_rows: Optional[torch.Tensor] = None) -> None:
+    """out [M, N] bf16 = sum over dim 0 of part [S, M, N] fp32, in order; with `count`,
+    rows at or past count - count_off are zeros (part not read there).  With `out_rows`
+    (int64 [M] on the device) row m goes to out[out_rows[m]] instead (out [R, N], rows
+    mapped outside [0, R) skipped)."""
     dev = _require_gpu(part, out)
+    _check_count(count, dev)
     S, M, N = part.shape
-    _require(part.is_contiguous() and out.dtype == torch.bfloat16 and out.stride(-1) == 1,
-             "contiguous fp32 partials and a bf16 output")
+    _require(part.is_contiguous() and part.dtype == torch.float32 and out.dtype == torch.bfloat16
+             and out.stride(-1) == 1 and out.dim() == 2 and out.shape[1] == N,
+             "contiguous fp32 partials and a bf16 [R, N] output")
+    if out_rows is None:
+        _require(out.shape[0] == M, "out has the partials' rows")
+    else:
+        _require(out_rows.dtype == torch.int64 and out_rows.device == dev and out_rows.dim() == 1
+                 and out_rows.shape[0] == M and out_rows.is_contiguous(),
+                 "out_rows is a contiguous int64 [M] tensor on the device")
     st = _launch("mirl_sum_splits_bf16", dev, part.data_ptr(), S, M, N, N, out.data_ptr(),
-                 out.stride(0), _stream(dev))
+                 out.stride(0), _ptr(out_rows), out.shape[0], _ptr(count), int(count_off),
+                 _stream(dev))
     _check(st, "mirl_sum_splits_bf16")
 
 
-def transpose_bf16(src: torch.Tensor, rows: int, dst: torch.Tensor) -> None:
-    """dst[c, r] = src[r, c] for r < rows, zero for rows <= r < dst.shape[1]."""
+def transpose_bf16(src: torch.Tensor, rows: int, dst: torch.Tensor,
+                   count: Optional[torch.Tensor] = None) -> None:
+    """dst[c, r] = src[r, c] for r < rows, zero for rows <= r < dst.shape[1]; rows is
+    lowered to `count` (device int64, one element) when that is given."""
     dev = _require_gpu(src, dst)
+    _check_count(count, dev)
     _require(src.dtype == torch.bfloat16 and dst.dtype == torch.bfloat16, "bf16 tensors")
     _require(src.stride(-1) == 1 and dst.stride(-1) == 1, "unit stride on the last dim")
     C = src.shape[1]
     _require(dst.shape[0] >= C, "dst has a row per source column")
+    _require(src.shape[0] >= rows, "src has the rows to transpose")
     st = _launch("mirl_transpose_bf16", dev, src.data_ptr(), int(rows), C, src.stride(0),
-                 dst.data_ptr(), dst.stride(0), dst.shape[1], _stream(dev))
+                 dst.data_ptr(), dst.stride(0), dst.shape[1], _ptr(count), _stream(dev))
     _check(st, "mirl_transpose_bf16")
 
 

@@ -11,7 +11,10 @@
 // The forward kernel writes, per row and per 256-column tile, the tile's
 // (max, sum exp(x - max)) and the target logit; a merge kernel combines the
 // tiles of a row.  The gradient kernel recomputes a logits tile and writes the
-// bf16 G tile (the two GEMMs that consume G are plain library GEMMs).
+// bf16 G tile and its transpose; the two products that consume G run on the
+// same tile loop as a plain GEMM.  Row counts may live on the device (the
+// backward's active rows): the kernels read them and skip what lies past them,
+// so the host never waits for them.
 //
 // Tile: 256 rows x 256 columns per 256-thread workgroup.  Each wave owns a
 // 128 x 128 quarter as 4 x 4 v_mfma_f32_32x32x16_bf16 tiles (256 fp32
@@ -121,8 +124,17 @@ struct LceParams {
   int64_t n_ks, kb_len;
   float* C;
   uint16_t* Cb;
-  int64_t ldc;
+  int64_t ldc, ldcb;
   int accumulate;       // C += A . B^T instead of C = A . B^T (n_ks = 1)
+  // device count (or null): c = *count - count_off.  kFwd/kGrad and count_axis
+  // 0: rows r >= c are absent (not read, not written); count_axis 1 (kGemm):
+  // the reduction stops at round_up(c, 128).  With both C and Cb, the output
+  // is Cb = bf16(A . B^T (+ C when accumulate)) if *count <= final_at and C
+  // otherwise; an empty reduction with accumulate set writes nothing.
+  const int64_t* count;
+  int64_t count_off;
+  int count_axis;
+  int64_t final_at;
 };
 
 template <int MODE>
@@ -142,9 +154,31 @@ void lce_tile_kernel(LceParams P) {
   // together): the ~32 workgroups resident on an XCD then cover about
   // kGroupM row tiles x 4 column tiles and share their H and W reads in L2.
   // (A plain GEMM's hidden-dimension splits are the outermost index.)
-  const int64_t tiles2 = P.n_mt * P.n_nt;
+  // A device count of rows shortens the row range; the tile order then covers
+  // only the row tiles that hold rows (so every XCD keeps its share of the
+  // work) and the workgroups past them return at once.
+  int64_t row_end = P.row0 + P.nrows;
+  int64_t k_end = P.Hd;
+  bool to_bf16 = P.Cb != nullptr;
+  if (P.count != nullptr) {
+    const int64_t c = *P.count - P.count_off;
+    if (MODE != kGemm || P.count_axis == 0) {
+      if (c < row_end) row_end = c;
+    } else {
+      constexpr int64_t kstep = kStages * kSK;
+      const int64_t ke = c <= 0 ? 0 : (c + kstep - 1) / kstep * kstep;
+      if (ke < k_end) k_end = ke;
+      if (ke == 0 && P.accumulate) return;
+      if (P.C != nullptr && P.Cb != nullptr) to_bf16 = *P.count <= P.final_at;
+    }
+  }
+  if (row_end <= P.row0) return;
+  const int64_t n_mt = (row_end - P.row0 + kBM - 1) / kBM;  // <= P.n_mt
+  const int64_t tiles2 = n_mt * P.n_nt;
   const int64_t ntiles = tiles2 * (MODE == kGemm ? P.n_ks : 1);
   const int64_t per_xcd = (ntiles + kXcds - 1) / kXcds;
+  // (the grid holds per_xcd workgroups per XCD only without a count)
+  if ((int64_t)(blockIdx.x / kXcds) >= per_xcd) return;
   const int64_t gi0 = (int64_t)(blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
   if (gi0 >= ntiles) return;
   const int64_t ks = gi0 / tiles2;
@@ -152,13 +186,12 @@ void lce_tile_kernel(LceParams P) {
   const int64_t per_group = (int64_t)kGroupM * P.n_nt;
   const int64_t group = gi / per_group;
   const int64_t first_m = group * kGroupM;
-  const int64_t gsize = (P.n_mt - first_m < kGroupM) ? (P.n_mt - first_m) : kGroupM;
+  const int64_t gsize = (n_mt - first_m < kGroupM) ? (n_mt - first_m) : kGroupM;
   const int64_t in_group = gi - group * per_group;
   const int64_t mt = first_m + in_group % gsize;
   const int64_t nt = in_group / gsize;
   const int64_t m0 = P.row0 + mt * kBM;  // absolute first row
   const int64_t n0 = nt * kBN;
-  const int64_t row_end = P.row0 + P.nrows;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -231,8 +264,24 @@ void lce_tile_kernel(LceParams P) {
   // per stage.
   // this tile's range of the hidden dimension (the whole of it but for split GEMMs)
   const int64_t kbase = (MODE == kGemm) ? ks * P.kb_len : 0;
-  const int64_t klen = (MODE == kGemm) ? ((P.Hd - kbase < P.kb_len) ? P.Hd - kbase : P.kb_len) : P.Hd;
-  const int nst = (int)(klen / kSK);  // a multiple of kStages
+  const int64_t krest = k_end - kbase < 0 ? 0 : k_end - kbase;
+  const int64_t klen = (MODE == kGemm) ? (krest < P.kb_len ? krest : P.kb_len) : P.Hd;
+  const int nst = (int)(klen / kSK);  // a multiple of kStages (0: an empty reduction)
+  if (MODE == kGemm && nst == 0) {
+    // an empty reduction range (a reduction-length count, or a split past it):
+    // the product is zero; handled here, before the accumulators exist
+    for (int q = threadIdx.x; q < kBM * kBN; q += kThreads) {
+      const int64_t row = m0 + q / kBN, col = n0 + q % kBN;
+      if (row >= row_end || col >= P.V) continue;
+      if (to_bf16) {
+        const float o = (P.accumulate && P.C != nullptr) ? P.C[row * P.ldc + col] : 0.f;
+        P.Cb[row * P.ldcb + col] = BF16::from_float(o);
+      } else if (!P.accumulate) {
+        P.C[(ks * P.nrows + row) * P.ldc + col] = 0.f;
+      }
+    }
+    return;
+  }
   const int64_t a_rows = (row_end - m0 < kBM) ? (row_end - m0) : kBM;
   const int64_t b_rows = (P.V - n0 < kBN) ? (P.V - n0) : kBN;
   const __amdgpu_buffer_rsrc_t rsrc_a = __builtin_amdgcn_make_buffer_rsrc(
@@ -292,6 +341,7 @@ void lce_tile_kernel(LceParams P) {
   };
 
   constexpr int kL = 2 * kDmaPerWave;  // direct loads per wave and stage
+  static_assert(kL == kTM * kTN, "one direct load per MFMA of block 3");
   // Prologue: stage data 0 and 1 in flight; wait for 0 and read its block-0 fragments.
 #pragma unroll
   for (int q = 0; q < kL; ++q) dma(st0, 0, q);
@@ -336,7 +386,6 @@ void lce_tile_kernel(LceParams P) {
       __builtin_amdgcn_sched_barrier(0);
     }
   };
-  static_assert(kL == kTM * kTN, "one direct load per MFMA of block 3");
   using S0 = std::integral_constant<int, 0>;
   using S1 = std::integral_constant<int, 1>;
   using T_ = std::integral_constant<bool, true>;
@@ -354,6 +403,9 @@ void lce_tile_kernel(LceParams P) {
     // accumulator v of lane l in MFMA tile (i, j) is C[(v / 4) * 8 + (l / 32) * 4 + v % 4][l % 32];
     // lanes 0-31 (32-63) store 32 consecutive columns of one row
     const int half_g = lane >> 5, col_g = lane & 31;
+    // a bf16 output over an fp32 running sum: the sum is completed in C first,
+    // then each thread rounds the elements it wrote
+    const bool via_c = to_bf16 && P.accumulate && P.C != nullptr;
 #pragma unroll
     for (int i = 0; i < kTM; ++i)
 #pragma unroll
@@ -363,13 +415,25 @@ void lce_tile_kernel(LceParams P) {
           const int64_t row = m0 + wm * kWM + i * 32 + (v >> 2) * 8 + half_g * 4 + (v & 3);
           const int64_t col = n0 + wn * kWN + j * 32 + col_g;
           if (row >= row_end || col >= P.V) continue;
-          if (P.Cb != nullptr) {
-            P.Cb[row * P.ldc + col] = BF16::from_float(acc[i][j][v]);
+          if (to_bf16 && !via_c) {
+            P.Cb[row * P.ldcb + col] = BF16::from_float(acc[i][j][v]);
           } else {
             float* c = P.C + (ks * P.nrows + row) * P.ldc + col;
             *c = P.accumulate ? *c + acc[i][j][v] : acc[i][j][v];
           }
         }
+    if (via_c) {
+#pragma unroll
+      for (int i = 0; i < kTM; ++i)
+#pragma unroll
+        for (int j = 0; j < kTN; ++j)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int64_t row = m0 + wm * kWM + i * 32 + (v >> 2) * 8 + half_g * 4 + (v & 3);
+            const int64_t col = n0 + wn * kWN + j * 32 + col_g;
+            if (row < row_end && col < P.V) P.Cb[row * P.ldcb + col] = BF16::from_float(P.C[row * P.ldc + col]);
+          }
+    }
     return;
   }
 
@@ -508,13 +572,16 @@ void lce_tile_kernel(LceParams P) {
 }
 
 // dst[c][r] = src[r][c] for r < R, c < C, and dst[c][r] = 0 for R <= r < Rp
-// (bf16; dst rows of stride ldd >= Rp).  64 x 64 tiles through LDS.
+// (bf16; dst rows of stride ldd >= Rp), R = min(R, *count) when count is
+// given.  64 x 64 tiles through LDS.
 __global__ __launch_bounds__(256) void transpose_bf16_kernel(const uint16_t* __restrict__ src,
                                                              int64_t R, int64_t C, int64_t lds,
                                                              uint16_t* __restrict__ dst,
                                                              int64_t ldd, int64_t Rp,
-                                                             int64_t n_ct) {
+                                                             int64_t n_ct,
+                                                             const int64_t* __restrict__ count) {
   __shared__ uint16_t tile[64][66];
+  if (count != nullptr && *count < R) R = *count;
   const int64_t tr = blockIdx.x / n_ct, tc = blockIdx.x - tr * n_ct;
   const int64_t r0 = tr * 64, c0 = tc * 64;
   const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
@@ -531,17 +598,55 @@ __global__ __launch_bounds__(256) void transpose_bf16_kernel(const uint16_t* __r
   }
 }
 
-// out[m][n] = bf16(sum over s of part[s][m][n]), summed in split order.
+// out[r(m)][n] = bf16(sum over s of part[s][m][n]), summed in split order,
+// with r(m) = out_rows[m] when a row map is given (rows mapped outside
+// [0, out_nrows) are skipped) and m otherwise; with a count, rows
+// m >= *count - count_off are written as zeros without reading.  VEC
+// consecutive elements per thread (N and ld multiples of VEC).
+template <int VEC>
 __global__ __launch_bounds__(256) void sum_splits_kernel(const float* __restrict__ part,
                                                          int64_t n_ks, int64_t M, int64_t N,
                                                          int64_t ld, uint16_t* __restrict__ out,
-                                                         int64_t ldo) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+                                                         int64_t ldo,
+                                                         const int64_t* __restrict__ out_rows,
+                                                         int64_t out_nrows,
+                                                         const int64_t* __restrict__ count,
+                                                         int64_t count_off) {
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * VEC;
   if (i >= M * N) return;
   const int64_t m = i / N, n = i - m * N;
-  float acc = 0.f;
-  for (int64_t s = 0; s < n_ks; ++s) acc += part[(s * M + m) * ld + n];
-  out[m * ldo + n] = BF16::from_float(acc);
+  int64_t r = m;
+  if (out_rows != nullptr) {
+    r = out_rows[m];
+    if (r < 0 || r >= out_nrows) return;
+  }
+  float acc[VEC];
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
+  if (count == nullptr || m < *count - count_off) {
+    for (int64_t s = 0; s < n_ks; ++s) {
+      const float* src = part + (s * M + m) * ld + n;
+      if constexpr (VEC == 4) {
+        const float4 q = *reinterpret_cast<const float4*>(src);
+        acc[0] += q.x;
+        acc[1] += q.y;
+        acc[2] += q.z;
+        acc[3] += q.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) acc[e] += src[e];
+      }
+    }
+  }
+  uint16_t* dst = out + r * ldo + n;
+  if constexpr (VEC == 4) {
+    const uint32_t lo = (uint32_t)BF16::from_float(acc[0]) | ((uint32_t)BF16::from_float(acc[1]) << 16);
+    const uint32_t hi = (uint32_t)BF16::from_float(acc[2]) | ((uint32_t)BF16::from_float(acc[3]) << 16);
+    *reinterpret_cast<uint2*>(dst) = uint2{lo, hi};
+  } else {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) dst[e] = BF16::from_float(acc[e]);
+  }
 }
 
 // Per row: combine the column-tile partials into the row's max and log-sum-exp,
@@ -660,7 +765,8 @@ extern "C" int mirl_linear_ce_grad(const void* hidden, int64_t T, int64_t Hd, in
                                    const float* row_stats, const float* grad_out,
                                    int64_t g_stride_b, int64_t g_stride_s, int64_t row0,
                                    int64_t nrows, void* grad_logits, int64_t ldg,
-                                   void* grad_logits_t, int64_t ldgt, void* stream) {
+                                   void* grad_logits_t, int64_t ldgt, const int64_t* row_count,
+                                   void* stream) {
   clear_error();
   if (int e = check_common(hidden, T, Hd, ldh, weight, V, ldw, target, bsz)) return e;
   MIRL_REQUIRE(row0 >= 0 && nrows >= 0 && row0 + nrows <= T, "row range [%lld, %lld) outside [0, %lld)",
@@ -702,6 +808,7 @@ extern "C" int mirl_linear_ce_grad(const void* hidden, int64_t T, int64_t Hd, in
   P.ldg = ldg;
   P.Gt = static_cast<uint16_t*>(grad_logits_t);
   P.ldgt = ldgt;
+  P.count = row_count;
   const int64_t grid = ceil_div(P.n_mt * P.n_nt, kXcds) * kXcds;
   MIRL_REQUIRE(grid < (int64_t(1) << 31), "too many tiles");
   hipLaunchKernelGGL((lce_tile_kernel<kGrad>), dim3((unsigned)grid), dim3(kThreads), 0, st, P);
@@ -710,7 +817,9 @@ extern "C" int mirl_linear_ce_grad(const void* hidden, int64_t T, int64_t Hd, in
 
 extern "C" int mirl_gemm_bf16_abt(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M,
                                   int64_t N, int64_t K, int64_t k_splits, float* C, int64_t ldc,
-                                  int accumulate, void* Cb, int64_t ldcb, void* stream) {
+                                  int accumulate, void* Cb, int64_t ldcb, const int64_t* count,
+                                  int64_t count_off, int count_axis, int64_t final_at,
+                                  void* stream) {
   clear_error();
   MIRL_REQUIRE(M >= 0 && N >= 0 && K > 0 && k_splits >= 1, "invalid shape M=%lld N=%lld K=%lld splits=%lld",
                (long long)M, (long long)N, (long long)K, (long long)k_splits);
@@ -725,8 +834,13 @@ extern "C" int mirl_gemm_bf16_abt(const void* A, int64_t lda, const void* B, int
                "%lld splits of K=%lld in ranges of %lld leave %lld non-empty (choose a split count "
                "that divides into whole 128-element ranges)",
                (long long)k_splits, (long long)K, (long long)kb, (long long)n_ks);
-  MIRL_REQUIRE(Cb == nullptr || (n_ks == 1 && !accumulate),
-               "a bf16 output takes one split and no accumulation");
+  MIRL_REQUIRE(count_axis == MIRL_COUNT_ROWS || count_axis == MIRL_COUNT_K, "invalid count axis %d",
+               count_axis);
+  const bool both = C != nullptr && Cb != nullptr;
+  MIRL_REQUIRE(!both || (count != nullptr && count_axis == MIRL_COUNT_K && n_ks == 1),
+               "an fp32 and a bf16 output together take a reduction-length count and one split");
+  MIRL_REQUIRE(Cb == nullptr || (n_ks == 1 && (!accumulate || both)),
+               "a bf16 output takes one split and accumulates only over the fp32 output");
   MIRL_REQUIRE(!accumulate || n_ks == 1, "accumulation takes one split");
   MIRL_REQUIRE(lda % 8 == 0 && ldb % 8 == 0 && lda >= K && ldb >= K,
                "row strides (%lld, %lld) must be multiples of 8 elements and >= K", (long long)lda,
@@ -737,7 +851,7 @@ extern "C" int mirl_gemm_bf16_abt(const void* A, int64_t lda, const void* B, int
   MIRL_REQUIRE(kBM * lda * 2 < (int64_t(1) << 31) && kBN * ldb * 2 < (int64_t(1) << 31),
                "row strides (%lld, %lld) too large", (long long)lda, (long long)ldb);
   MIRL_REQUIRE(M < (int64_t(1) << 31) && N < (int64_t(1) << 31), "sizes exceed 2^31-1");
-  MIRL_REQUIRE(ldc >= N || Cb != nullptr, "output row stride %lld is smaller than N=%lld",
+  MIRL_REQUIRE(C == nullptr || ldc >= N, "output row stride %lld is smaller than N=%lld",
                (long long)ldc, (long long)N);
   MIRL_REQUIRE(Cb == nullptr || ldcb >= N, "output row stride %lld is smaller than N=%lld",
                (long long)ldcb, (long long)N);
@@ -756,8 +870,13 @@ extern "C" int mirl_gemm_bf16_abt(const void* A, int64_t lda, const void* B, int
   P.kb_len = kb;
   P.C = C;
   P.Cb = static_cast<uint16_t*>(Cb);
-  P.ldc = Cb != nullptr ? ldcb : ldc;
+  P.ldc = ldc;
+  P.ldcb = ldcb;
   P.accumulate = accumulate;
+  P.count = count;
+  P.count_off = count_off;
+  P.count_axis = count_axis;
+  P.final_at = final_at;
   const int64_t grid = ceil_div(P.n_mt * P.n_nt * n_ks, kXcds) * kXcds;
   MIRL_REQUIRE(grid < (int64_t(1) << 31), "too many tiles");
   hipLaunchKernelGGL((lce_tile_kernel<kGemm>), dim3((unsigned)grid), dim3(kThreads), 0,
@@ -766,19 +885,32 @@ extern "C" int mirl_gemm_bf16_abt(const void* A, int64_t lda, const void* B, int
 }
 
 extern "C" int mirl_sum_splits_bf16(const float* part, int64_t k_splits, int64_t M, int64_t N,
-                                    int64_t ld, void* out, int64_t ldo, void* stream) {
+                                    int64_t ld, void* out, int64_t ldo, const int64_t* out_rows,
+                                    int64_t out_nrows, const int64_t* count, int64_t count_off,
+                                    void* stream) {
   clear_error();
   MIRL_REQUIRE(M >= 0 && N >= 0 && k_splits >= 1 && ld >= N && ldo >= N, "invalid shape");
   if (M == 0 || N == 0) return MIRL_OK;
   MIRL_REQUIRE(part && out, "null pointer argument");
-  hipLaunchKernelGGL(sum_splits_kernel, dim3((unsigned)ceil_div(M * N, 256)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), part, k_splits, M, N, ld,
-                     static_cast<uint16_t*>(out), ldo);
+  MIRL_REQUIRE(out_rows == nullptr || out_nrows >= 0, "invalid output row count");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool vec4 = N % 4 == 0 && ld % 4 == 0 && ldo % 4 == 0 &&
+                    (reinterpret_cast<uintptr_t>(part) & 15u) == 0 &&
+                    (reinterpret_cast<uintptr_t>(out) & 7u) == 0;
+  if (vec4)
+    hipLaunchKernelGGL((sum_splits_kernel<4>), dim3((unsigned)ceil_div(M * N / 4, 256)), dim3(256), 0,
+                       st, part, k_splits, M, N, ld, static_cast<uint16_t*>(out), ldo, out_rows,
+                       out_nrows, count, count_off);
+  else
+    hipLaunchKernelGGL((sum_splits_kernel<1>), dim3((unsigned)ceil_div(M * N, 256)), dim3(256), 0,
+                       st, part, k_splits, M, N, ld, static_cast<uint16_t*>(out), ldo, out_rows,
+                       out_nrows, count, count_off);
   return check_launch("mirl_sum_splits_bf16");
 }
 
 extern "C" int mirl_transpose_bf16(const void* src, int64_t R, int64_t C, int64_t lds, void* dst,
-                                   int64_t ldd, int64_t R_pad, void* stream) {
+                                   int64_t ldd, int64_t R_pad, const int64_t* count,
+                                   void* stream) {
   clear_error();
   MIRL_REQUIRE(R >= 0 && C >= 0 && R_pad >= R && lds >= C && ldd >= R_pad, "invalid shape");
   if (C == 0 || R_pad == 0) return MIRL_OK;
@@ -787,6 +919,6 @@ extern "C" int mirl_transpose_bf16(const void* src, int64_t R, int64_t C, int64_
   MIRL_REQUIRE(n_rt * n_ct < (int64_t(1) << 31), "too many tiles");
   hipLaunchKernelGGL(transpose_bf16_kernel, dim3((unsigned)(n_rt * n_ct)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(src), R, C,
-                     lds, static_cast<uint16_t*>(dst), ldd, R_pad, n_ct);
+                     lds, static_cast<uint16_t*>(dst), ldd, R_pad, n_ct, count);
   return check_launch("mirl_transpose_bf16");
 }

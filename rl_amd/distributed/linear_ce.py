@@ -11,9 +11,10 @@ is ``[V, H]``; targets are ``[B, S]``.
   matmul output is) and reduces it to per-row partial log-sum-exps and the
   target logit; a merge kernel finishes each row.  The ``[S*B, V]`` logits are
   never materialised (the reference materialises an fp32 copy per chunk).
-* backward: the rows with a non-zero upstream gradient are gathered (the
-  others have a zero logits gradient: zero dH rows, nothing added to dW);
-  per block of up to ``4 * chunk_size * B`` of those rows a kernel recomputes the logits
+* backward: the rows with a non-zero upstream gradient are moved to the front
+  (the others have a zero logits gradient: zero dH rows, nothing added to dW)
+  and counted on the device, where the kernels read the count (no host
+  synchronisation); per block of up to ``4 * chunk_size * B`` rows a kernel recomputes the logits
   tiles and writes ``G = (onehot - softmax) * g`` in bf16 and its transpose, and
   ``dH = G . W`` and ``dW += G^T . H`` run on the same MFMA tile loop
   (``mirl_gemm_bf16_abt``) against transposed copies of W (kept while the weight
@@ -118,75 +119,68 @@ class ChunkedDistributedHiddenStatesToLogprobs(torch.autograd.Function):
         dev = hidden.device
         # Rows whose upstream gradient is exactly zero (prompt, padding) have a
         # zero logits gradient, so they add nothing to dW and their dH rows are
-        # zero: only the active rows are gathered and run through the gradient
-        # kernel and both products (one host synchronisation for their count).
+        # zero.  The rows are permuted so that the active ones come first (in row
+        # order) and their count stays on the device: every kernel below reads it
+        # and skips what lies past it, so the host never waits for the count.
         g_rows = grad_output.t().reshape(T)  # row r = (s, b) is position s of sample b
-        active = torch.nonzero(g_rows != 0).squeeze(1)
-        n_act = active.numel()
-        dH = torch.zeros((T, H), dtype=hidden.dtype, device=dev) if need_h else None
-        dW = None
-        if n_act > 0:
-            compact = n_act < T
-            if not compact:
-                h_a, bsz, tgt_a, st_a, g_a = h2, B, target, stats, grad_output
-            else:
-                h_a = torch.index_select(h2, 0, active)
-                bsz = 1
-                tgt_a = target.t().reshape(T).index_select(0, active).view(1, n_act)
-                st_a = stats.index_select(0, active)
-                g_a = g_rows.index_select(0, active).view(1, n_act)
-            # Blocks of up to 4 chunks of rows (whole 256-row tiles): the bf16 G
-            # buffer stays below one reference chunk's fp32 logits, softmax and
-            # one-hot temporaries.
-            rows = n_act if ctx.chunk_size is None else min(
-                n_act, _round_up(_BLOCK_CHUNKS * ctx.chunk_size * B, 256))
-            Vp = _round_up(V, _K_ALIGN)
-            # G [rows, Vp] (columns past V zero: dH's padded reduction length)
-            G = torch.empty((rows, Vp), dtype=torch.bfloat16, device=dev)
-            if Vp > V:
-                G[:, V:].zero_()
-            # G^T [V, rows rounded to 256] and H^T of the active rows [H, n_act
-            # rounded to 256] for dW = (G^T) . (H^T)^T, zero past the rows
-            Gt = torch.empty((V, _round_up(rows, 256)), dtype=torch.bfloat16, device=dev) if need_w else None
-            hT = None
+        nz = g_rows != 0
+        perm = torch.argsort(torch.logical_not(nz).to(torch.uint8), stable=True)
+        count = nz.sum(dtype=torch.int64).view(1)
+        h_a = torch.index_select(h2, 0, perm)
+        tgt_a = target.t().reshape(T).index_select(0, perm).view(1, T)
+        st_a = stats.index_select(0, perm)
+        g_a = g_rows.index_select(0, perm).view(1, T)
+        # Blocks of up to 4 chunks of rows (whole 256-row tiles): the bf16 G
+        # buffer stays below one reference chunk's fp32 logits, softmax and
+        # one-hot temporaries.  Blocks past the count return at once.
+        rows = T if ctx.chunk_size is None else min(T, _round_up(_BLOCK_CHUNKS * ctx.chunk_size * B, 256))
+        n_blocks = -(-T // rows)
+        Vp = _round_up(V, _K_ALIGN)
+        # G [rows, Vp] (columns past V zero: dH's padded reduction length)
+        G = torch.empty((rows, Vp), dtype=torch.bfloat16, device=dev)
+        if Vp > V:
+            G[:, V:].zero_()
+        # G^T [V, rows rounded to 256] and H^T of the permuted rows [H, T rounded
+        # to 256] for dW = (G^T) . (H^T)^T; H^T is zero past the count and G^T in
+        # the tile that holds the last active row, which covers dW's reduction
+        # (stopped at the count rounded up to 128)
+        Gt = torch.empty((V, _padded_width(rows)), dtype=torch.bfloat16, device=dev) if need_w else None
+        hT = None
+        if need_w:
+            hT = torch.empty((H, _padded_width(T)), dtype=torch.bfloat16, device=dev)
+            _C.transpose_bf16(h_a, T, hT, count=count)
+        wT = _weight_transposed(weight, Vp) if need_h else None
+        # dH is written row by row at each permuted row's own position
+        dH = torch.empty((T, H), dtype=hidden.dtype, device=dev) if need_h else None
+        hk_a, wk = _kernel_operand(h_a), _kernel_operand(weight)
+        if need_w:
+            dW = torch.empty((V, H), dtype=torch.bfloat16, device=dev)
+            # fp32 across blocks, rounded once by the last block with active rows
+            # (allocated, never touched, when that is the first)
+            dW32 = torch.empty((V, H), dtype=torch.float32, device=dev) if n_blocks > 1 else None
+        for r0 in range(0, T, rows):
+            n = min(rows, T - r0)
+            Gc = G[:n]
+            _C.linear_ce_grad(hk_a, wk, 1, tgt_a, vs, ve, st_a, g_a, r0, Gc, Gt, count=count)
+            if need_h:
+                # dH = G . W = G . (W^T)^T on the MFMA units, the reduction over
+                # the vocabulary split so that the tiles fill the CUs; rows past
+                # the count are written as zeros
+                splits = _dh_splits(n, H, Vp, count_known=False)
+                part = torch.empty((splits, n, H), dtype=torch.float32, device=dev)
+                _C.gemm_bf16_abt(Gc, wT, Vp, part, k_splits=splits, count=count, count_off=r0,
+                                 count_axis=_C.COUNT_ROWS)
+                _C.sum_splits_bf16(part, dH, count=count, count_off=r0, out_rows=perm[r0 : r0 + n])
+                del part
             if need_w:
-                hT = torch.empty((H, _round_up(n_act, 256)), dtype=torch.bfloat16, device=dev)
-                _C.transpose_bf16(h_a, n_act, hT)
-            wT = _weight_transposed(weight, Vp) if need_h else None
-            dH_a = dH if (need_h and n_act == T) else (
-                torch.empty((n_act, H), dtype=hidden.dtype, device=dev) if need_h else None)
-            hk_a, wk = _kernel_operand(h_a), _kernel_operand(weight)
-            one_block = rows >= n_act
-            dW32 = None
-            for r0 in range(0, n_act, rows):
-                n = min(rows, n_act - r0)
-                Gc = G[:n]
-                _C.linear_ce_grad(hk_a, wk, bsz, tgt_a, vs, ve, st_a, g_a, r0, Gc, Gt)
-                if need_h:
-                    # dH = G . W = G . (W^T)^T on the MFMA units, the reduction over
-                    # the vocabulary split so that the tiles fill the CUs
-                    splits = _dh_splits(n, H, Vp)
-                    part = torch.empty((splits, n, H), dtype=torch.float32, device=dev)
-                    _C.gemm_bf16_abt(Gc, wT, Vp, part, k_splits=splits)
-                    _C.sum_splits_bf16(part, dH_a[r0 : r0 + n])
-                    del part
-                if need_w:
-                    nk = _round_up(n, _K_ALIGN)
-                    hb = hT[:, r0 : r0 + nk]
-                    if one_block:
-                        # one block: fp32 accumulation, rounded once to bf16 by the kernel
-                        dW = torch.empty((V, H), dtype=torch.bfloat16, device=dev)
-                        _C.gemm_bf16_abt(Gt, hb, nk, dW)
-                    else:
-                        if dW32 is None:
-                            dW32 = torch.empty((V, H), dtype=torch.float32, device=dev)
-                        _C.gemm_bf16_abt(Gt, hb, nk, dW32, accumulate=r0 > 0)
-            if dW32 is not None:
-                dW = dW32
-            if need_h and n_act < T:
-                dH.index_copy_(0, active, dH_a)
-        if need_w and dW is None:
-            dW = torch.zeros((V, H), dtype=weight.dtype, device=dev)
+                nk = _round_up(n, _K_ALIGN)
+                hb = hT[:, r0 : r0 + nk]
+                if dW32 is None:
+                    # one block: fp32 accumulation, rounded once to bf16 by the kernel
+                    _C.gemm_bf16_abt(Gt, hb, nk, dW, count=count, count_off=r0, count_axis=_C.COUNT_K)
+                else:
+                    _C.gemm_bf16_abt(Gt, hb, nk, dW32, accumulate=r0 > 0, count=count, count_off=r0,
+                                     count_axis=_C.COUNT_K, out_bf16=dW, final_at=r0 + n)
         grad_h = dH.view(S, B, H) if need_h else None
         grad_w = (dW if dW.dtype == weight.dtype else dW.to(weight.dtype)) if need_w else None
         return grad_h, None, grad_w, None, None, None, None, None
@@ -284,23 +278,38 @@ def _round_up(n: int, m: int) -> int:
     return (n + m - 1) // m * m
 
 
-def _dh_splits(n: int, H: int, K: int) -> int:
+def _padded_width(rows: int) -> int:
+    """Row length of the transposed operands of dW: whole 256-row tiles plus one
+    128-byte line, so that the rows a tile reads together do not all start at the
+    same offset of a power-of-two stride."""
+    return _round_up(rows, 256) + 64
+
+
+def _dh_splits(n: int, H: int, K: int, count_known: bool = True) -> int:
     """Splits of dH's reduction length (each adds an fp32 partial product to read
     back).  dH has few 256 x 256 tiles over a long reduction, so the count that
     fills the last round of tiles over the 256 CUs best wins, the smaller on a
     tie (measured on [5871, 151936] x [151936, 4096]: 1 split 7.62 ms, 2 6.09,
     3 6.81, 4 6.23).  The kernel cuts K into ranges of round_up(ceil(K / s), 128);
-    only counts for which that gives exactly s ranges, each of at least 1024, qualify."""
+    only counts for which that gives exactly s ranges, each of at least 1024, qualify.
+    With count_known False, n is an upper bound (the active rows are counted on the
+    device) and at least two splits are taken where they qualify: fewer active rows
+    leave the single-split tiles short of the CUs, and a second split costs one more
+    fp32 partial of n x H."""
     tiles = ((n + 255) // 256) * ((H + 255) // 256)
     best, best_eff = 1, tiles / (256 * -(-tiles // 256))
+    qualifying = []
     for s in range(2, 9):
         kb = _round_up(-(-K // s), 128)
         if kb < 1024 or -(-K // kb) != s:
             continue
+        qualifying.append(s)
         t = tiles * s
         eff = t / (256 * -(-t // 256))
         if eff > best_eff + 1e-9:
             best, best_eff = s, eff
+    if not count_known and best == 1 and qualifying:
+        best = qualifying[0]
     return best
 
 

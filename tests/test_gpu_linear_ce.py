@@ -245,3 +245,85 @@ def test_fp16_fp32_forward_and_gradients(dtype, S, B, H, V, chunk):
     for got, want in ((dh, rdh), (dw, rdw)):
         err = (got.cpu().double() - want).abs().max().item()
         assert err <= rel * want.abs().max().item(), (err, want.abs().max().item())
+
+
+@pytest.mark.parametrize("active", [0.0, 0.2, 0.6, 1.0])
+def test_gradient_blocks_with_device_count(active):
+    """Several backward blocks (600 rows, 256 per block at chunk 7): the active-row count
+    lives on the device, so the blocks past it return at once and dW is rounded by the
+    last block holding active rows (none, the first, the second, the third)."""
+    say("linear-ce grad blocks active", active)
+    S, B, H, V = 200, 3, 128, 2000
+    hidden, weight, target = _inputs(S, B, H, V, seed=61)
+    gen = torch.Generator().manual_seed(62)
+    g = torch.randn(B, S, generator=gen) * (torch.rand(B, S, generator=gen) < active).float()
+    h = hidden.to(DEV).requires_grad_(True)
+    w = weight.to(DEV).requires_grad_(True)
+    lp = ChunkedDistributedHiddenStatesToLogprobs.apply(h, target.to(DEV), w, 0, V, 7, None, False)
+    dh, dw = torch.autograd.grad(lp, [h, w], g.to(DEV))
+    if active == 0.0:
+        assert not dh.any() and not dw.any()
+        return
+    rdh, rdw, _ = hidden_state_logprob_grads(hidden, target, weight, 0, V, g)
+    for got, ref in ((dh, rdh), (dw, rdw)):
+        err = (got.cpu().double() - ref).abs().max().item()
+        assert err <= 1e-2 * ref.abs().max().item(), (active, err)
+    assert not dh.cpu()[(g == 0).t()].any()
+
+
+def test_gemm_primitives_with_device_counts():
+    """The GEMM, split sum and transpose with a device count equal the same calls on the
+    host-trimmed operands, bit for bit."""
+    from rl_amd import _C
+
+    say("linear-ce primitives with device counts")
+    gen = torch.Generator().manual_seed(71)
+    M, N, K = 600, 300, 512
+    a = torch.randn(M, K, generator=gen).to(torch.bfloat16).to(DEV)
+    b = torch.randn(N, K, generator=gen).to(torch.bfloat16).to(DEV)
+    for c in (0, 1, 255, 257, 600):
+        cnt = torch.tensor([c + 100], dtype=torch.int64, device=DEV)  # count_off 100
+        # rows: absent rows of a leave their output rows untouched
+        part = torch.full((2, M, N), 7.0, device=DEV)
+        _C.gemm_bf16_abt(a, b, K, part, k_splits=2, count=cnt, count_off=100, count_axis=_C.COUNT_ROWS)
+        if c > 0:
+            ref = torch.empty((2, c, N), device=DEV)
+            _C.gemm_bf16_abt(a[:c], b, K, ref, k_splits=2)
+            assert torch.equal(part[:, :c], ref)
+        assert torch.all(part[:, c:] == 7.0)
+        out = torch.full((M, N), 3.0, dtype=torch.bfloat16, device=DEV)
+        _C.sum_splits_bf16(part, out, count=cnt, count_off=100)
+        ref_out = torch.empty((M, N), dtype=torch.bfloat16, device=DEV)
+        _C.sum_splits_bf16(part, ref_out)
+        assert torch.equal(out[:c], ref_out[:c]) and not out[c:].any()
+        # a row map writes each row at its own position (here a permutation)
+        rmap = torch.randperm(M, generator=gen).to(DEV)
+        mapped = torch.full((M, N), 3.0, dtype=torch.bfloat16, device=DEV)
+        _C.sum_splits_bf16(part, mapped, count=cnt, count_off=100, out_rows=rmap)
+        assert torch.equal(mapped[rmap], out)
+        # transpose with the count: zeros past it
+        t = torch.full((K, 640), 5.0, dtype=torch.bfloat16, device=DEV)
+        _C.transpose_bf16(a, M, t, count=torch.tensor([c], dtype=torch.int64, device=DEV))
+        t_ref = torch.empty((K, 640), dtype=torch.bfloat16, device=DEV)
+        _C.transpose_bf16(a, c, t_ref)
+        assert torch.equal(t, t_ref)
+    # reduction length: c rows of the reduction, blocks of 256 accumulated in fp32 and
+    # rounded once by the last block holding rows
+    at = torch.zeros((N, 768), dtype=torch.bfloat16, device=DEV)
+    bt = torch.zeros((K, 768), dtype=torch.bfloat16, device=DEV)
+    for c in (0, 100, 256, 300, 700):
+        at.zero_()
+        bt.zero_()
+        at[:, :c] = torch.randn(N, c, generator=gen).to(torch.bfloat16).to(DEV)
+        bt[:, :c] = torch.randn(K, c, generator=gen).to(torch.bfloat16).to(DEV)
+        cnt = torch.tensor([c], dtype=torch.int64, device=DEV)
+        ref32 = torch.zeros((N, K), device=DEV)
+        for r0 in range(0, 768, 256):
+            _C.gemm_bf16_abt(at[:, r0:r0 + 256], bt[:, r0:r0 + 256], 256, ref32, accumulate=r0 > 0)
+        out16 = torch.full((N, K), 9.0, dtype=torch.bfloat16, device=DEV)
+        acc32 = torch.empty((N, K), device=DEV)
+        for r0 in range(0, 768, 256):
+            _C.gemm_bf16_abt(at[:, r0:r0 + 256], bt[:, r0:r0 + 256], 256, acc32, accumulate=r0 > 0,
+                             count=cnt, count_off=r0, count_axis=_C.COUNT_K, out_bf16=out16,
+                             final_at=r0 + 256)
+        assert torch.equal(out16, ref32.to(torch.bfloat16)), c
