@@ -931,40 +931,41 @@ __device__ __forceinline__ bool fast_div_row(const FilterBwdParams& P, const Row
   return ag * pc >= 0x1p-59f;
 }
 
-// The whole-row walk of the filtered backward: re-read the logits x of one
-// row and write the gradient y of the whole row, in index order (the head, the
-// 16-byte vectors, the tail).  The elements equal to v_cut are counted as they
-// come (the same count in every lane), so that a cut in rank form is applied
-// too; their ranks are only worked out for vectors where a tie occurs.
-// Elements outside the kept set get the gradient 0.
+// Per-row arithmetic of the whole-row walks below: the kept test of elements
+// equal to v_cut, the probability of a kept element and the gradient narrowed
+// to the dtype.
 template <class E, int CONV>
-__device__ __forceinline__ void walk_row(const FilterBwdParams& P, const RowInfo& ri,
-                                         const typename E::raw* x, typename E::raw* y, float gv,
-                                         int64_t t, int lane) {
+struct WalkMath {
   using raw = typename E::raw;
-  constexpr int VEC = E::kVec;
-  constexpr int U = 4;
-  const float vc = ri.v_cut;
-  const bool rank_form = ri.i_cut < 0;
-  const uint32_t rcut = rank_form ? (uint32_t)(-1 - ri.i_cut) : 0u;
-  const int64_t icut = ri.i_cut;
-  const uint64_t below = (1ull << lane) - 1ull;
-  // p = exp(y - m - logsum); for the 16-bit dtypes as exp2(y log2e - c) in
-  // one fma (its absolute error in the exponent, a few 1e-6, is far below the
-  // dtype's resolution), for fp32 gradients from the differences
-  const float c = (ri.m + ri.logsum) * kLog2e;
-  const float ngv = -gv;
-  const float rgt = CONV == kConvFastGT ? __frcp_rn(P.GT) : 1.f;
-  uint32_t seen = 0;
-  auto yval = [&](float xf) { return P.has_t ? round_trip<E>(__fdiv_rn(xf, P.T)) : xf; };
-  auto prob = [&](float yy) {
+  const FilterBwdParams& P;
+  const RowInfo& ri;
+  float gv, ngv, c, rgt, vc;
+  int64_t t;
+  bool rank_form;
+  uint32_t rcut;
+  int64_t icut;
+  __device__ WalkMath(const FilterBwdParams& P_, const RowInfo& ri_, float gv_, int64_t t_)
+      : P(P_), ri(ri_), gv(gv_), t(t_) {
+    vc = ri.v_cut;
+    rank_form = ri.i_cut < 0;
+    rcut = rank_form ? (uint32_t)(-1 - ri.i_cut) : 0u;
+    icut = ri.i_cut;
+    // p = exp(y - m - logsum); for the 16-bit dtypes as exp2(y log2e - c) in
+    // one fma (its absolute error in the exponent, a few 1e-6, is far below the
+    // dtype's resolution), for fp32 gradients from the differences
+    c = (ri.m + ri.logsum) * kLog2e;
+    ngv = -gv;
+    rgt = CONV == kConvFastGT ? __frcp_rn(P.GT) : 1.f;
+  }
+  __device__ float yval(float xf) const { return P.has_t ? round_trip<E>(__fdiv_rn(xf, P.T)) : xf; }
+  __device__ float prob(float yy) const {
     if constexpr (std::is_same<E, F32>::value)
       return fast_exp2(((yy - ri.m) - ri.logsum) * kLog2e);
     else
       return fast_exp2(__builtin_fmaf(yy, kLog2e, -c));
-  };
+  }
   // gradient of a non-target element, narrowed to the dtype
-  auto narrow = [&](float g32) -> raw {
+  __device__ raw narrow(float g32) const {
     if constexpr (CONV == kConvPlain) {
       return E::from_float(g32);
     } else if constexpr (CONV == kConvFastGT) {
@@ -972,9 +973,10 @@ __device__ __forceinline__ void walk_row(const FilterBwdParams& P, const RowInfo
     } else {
       return grad_to_dtype<E>(g32, P);
     }
-  };
+  }
   // the non-target gradients -p g of one vector (0 outside the kept set)
-  auto narrow_vec = [&](const float (&w)[E::kVec], raw (&vals)[E::kVec], auto kept) {
+  template <class Kept>
+  __device__ void narrow_vec(const float (&w)[E::kVec], raw (&vals)[E::kVec], Kept kept) const {
     float g[E::kVec];
 #pragma unroll
     for (int k = 0; k < E::kVec; ++k) g[k] = kept(k) ? prob(w[k]) * ngv : 0.f;
@@ -993,25 +995,44 @@ __device__ __forceinline__ void walk_row(const FilterBwdParams& P, const RowInfo
 #pragma unroll
       for (int k = 0; k < E::kVec; ++k) vals[k] = narrow(g[k]);
     }
-  };
-  auto grad_at = [&](float yy, int64_t j, bool kept) -> raw {
+  }
+  __device__ raw grad_at(float yy, int64_t j, bool kept) const {
     float g32 = 0.f;
     if (kept) {
       const float p = prob(yy);
       g32 = ((j == t) ? 1.f - p : -p) * gv;
     }
     return grad_to_dtype<E>(g32, P);
-  };
-  auto tied_kept = [&](uint32_t rank, int64_t j) { return rank_form ? rank >= rcut : j >= icut; };
+  }
+  __device__ bool tied_kept(uint32_t rank, int64_t j) const { return rank_form ? rank >= rcut : j >= icut; }
+};
+
+// The whole-row walk of the filtered backward: re-read the logits x of one
+// row and write the gradient y of the whole row, in index order (the head, the
+// 16-byte vectors, the tail).  The elements equal to v_cut are counted as they
+// come (the same count in every lane), so that a cut in rank form is applied
+// too; their ranks are only worked out for vectors where a tie occurs.
+// Elements outside the kept set get the gradient 0.  One wave per row.
+template <class E, int CONV>
+__device__ __forceinline__ void walk_row(const FilterBwdParams& P, const RowInfo& ri,
+                                         const typename E::raw* x, typename E::raw* y, float gv,
+                                         int64_t t, int lane) {
+  using raw = typename E::raw;
+  constexpr int VEC = E::kVec;
+  constexpr int U = 4;
+  const WalkMath<E, CONV> W(P, ri, gv, t);
+  const float vc = W.vc;
+  const uint64_t below = (1ull << lane) - 1ull;
+  uint32_t seen = 0;
   // one element per lane, consecutive indices across the lanes; every lane calls it
   auto lane_step = [&](int64_t j, bool valid) {
-    const float yy = valid ? yval(E::load(x + j)) : 0.f;
+    const float yy = valid ? W.yval(E::load(x + j)) : 0.f;
     const bool tie = valid && yy == vc;
     const uint64_t bal = __ballot(tie);
     bool kept = valid && yy > vc;
-    if (tie) kept = tied_kept(seen + (uint32_t)__popcll(bal & below), j);
+    if (tie) kept = W.tied_kept(seen + (uint32_t)__popcll(bal & below), j);
     seen += (uint32_t)__popcll(bal);
-    if (valid) y[j] = grad_at(yy, j, kept);
+    if (valid) y[j] = W.grad_at(yy, j, kept);
   };
   const RowSpan<E> xs(x, P.V);
   const RowSpan<E> ys(y, P.V);
@@ -1038,7 +1059,7 @@ __device__ __forceinline__ void walk_row(const FilterBwdParams& P, const RowInfo
       float w[VEC];
       E::unpack(q[u], w);
 #pragma unroll
-      for (int k = 0; k < VEC; ++k) w[k] = yval(w[k]);
+      for (int k = 0; k < VEC; ++k) w[k] = W.yval(w[k]);
       bool tie = false;
 #pragma unroll
       for (int k = 0; k < VEC; ++k) tie = tie || w[k] == vc;
@@ -1066,19 +1087,19 @@ __device__ __forceinline__ void walk_row(const FilterBwdParams& P, const RowInfo
         const uint32_t total = (uint32_t)__shfl((int)inc, 63, 64);
         for (uint32_t m = tie8; m != 0u; m &= m - 1u) {
           const int k = __ffs(m) - 1;
-          if (tied_kept(seen + ex + (uint32_t)__popc(tie8 & ((1u << k) - 1u)), jb + k)) keep8 |= 1u << k;
+          if (W.tied_kept(seen + ex + (uint32_t)__popc(tie8 & ((1u << k) - 1u)), jb + k)) keep8 |= 1u << k;
         }
         seen += total;
-        narrow_vec(w, vals, [&](int k) { return ((keep8 >> k) & 1u) != 0u; });
+        W.narrow_vec(w, vals, [&](int k) { return ((keep8 >> k) & 1u) != 0u; });
       } else {
-        narrow_vec(w, vals, [&](int k) { return w[k] > vc; });
+        W.narrow_vec(w, vals, [&](int k) { return w[k] > vc; });
       }
       // the target element (1 - p) g, narrowed exactly
       const int64_t dt = t - jb;
       if (dt >= 0 && dt < VEC) {
 #pragma unroll
         for (int k = 0; k < VEC; ++k)
-          if (k == dt) vals[k] = grad_at(w[k], jb + k, keep8 == ~0u ? w[k] > vc : ((keep8 >> k) & 1u) != 0u);
+          if (k == dt) vals[k] = W.grad_at(w[k], jb + k, keep8 == ~0u ? w[k] > vc : ((keep8 >> k) & 1u) != 0u);
       }
       if (valid) {
         vu4 out;
@@ -1088,6 +1109,261 @@ __device__ __forceinline__ void walk_row(const FilterBwdParams& P, const RowInfo
     }
   }
   lane_step(ys.tail0 + lane, ys.tail0 + lane < P.V);
+}
+
+// The whole-row walk by a workgroup of kRowWaves waves per row: each round
+// covers kRowThreads * kRowVecs consecutive 16-byte vectors (vector
+// base + u * kRowThreads + thread), so far fewer rows are streamed at once
+// than with one wave per row and the traffic stays in a narrower address
+// window.  A cut in rank form needs each tied element's rank among the row's
+// ties in index order: every wave counts its ties per u, the counts meet in
+// LDS (one barrier per round, the count array alternating between two halves
+// so that a round's writes never meet the previous round's reads), and each
+// wave takes the exclusive prefix over the (u, wave) order.  The head and the
+// tail are counted by every wave alike (the same running count everywhere)
+// and written by wave 0.
+constexpr int kRowWaves = 16;
+constexpr int kRowThreads = 64 * kRowWaves;
+constexpr int kRowVecs = 2;
+
+template <class E, int CONV>
+__device__ __forceinline__ void walk_row_block(const FilterBwdParams& P, const RowInfo& ri,
+                                               const typename E::raw* x, typename E::raw* y,
+                                               float gv, int64_t t, uint32_t* s_cnt) {
+  using raw = typename E::raw;
+  constexpr int VEC = E::kVec;
+  constexpr int U = kRowVecs;
+  constexpr int NT = kRowThreads;
+  constexpr int NC = U * kRowWaves;  // counts per round
+  static_assert(NC <= 64, "one count per lane");
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const WalkMath<E, CONV> W(P, ri, gv, t);
+  const float vc = W.vc;
+  const uint64_t below = (1ull << lane) - 1ull;
+  uint32_t seen = 0;  // ties before the current position, the same in every wave
+  auto lane_step = [&](int64_t j, bool valid, bool write) {
+    const float yy = valid ? W.yval(E::load(x + j)) : 0.f;
+    const bool tie = valid && yy == vc;
+    const uint64_t bal = __ballot(tie);
+    bool kept = valid && yy > vc;
+    if (tie) kept = W.tied_kept(seen + (uint32_t)__popcll(bal & below), j);
+    seen += (uint32_t)__popcll(bal);
+    if (valid && write) y[j] = W.grad_at(yy, j, kept);
+  };
+  auto incl_scan = [&](uint32_t v) {
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const uint32_t o = (uint32_t)__shfl_up((int)v, off, 64);
+      if (lane >= off) v += o;
+    }
+    return v;
+  };
+  const RowSpan<E> xs(x, P.V);
+  const RowSpan<E> ys(y, P.V);
+  if (xs.head != ys.head) {
+    // logits and gradient not co-aligned: one wave walks the row element by element
+    if (wave == 0)
+      for (int64_t j0r = 0; j0r < P.V; j0r += 64) lane_step(j0r + lane, j0r + lane < P.V, true);
+    return;
+  }
+  lane_step(lane, lane < ys.head, wave == 0);
+  const vu4* xv = reinterpret_cast<const vu4*>(x + xs.head);
+  vu4* yv = reinterpret_cast<vu4*>(y + ys.head);
+  const int64_t nvec = ys.nvec;
+  int par = 0;
+  float t_y = 0.f;
+  bool t_kept = false, t_mine = false;
+  // the next round's loads are issued before this round is worked on (two
+  // rounds in flight); indices past the row are clamped to its last vector
+  // (loaded, never used), so that no load is conditional
+  const int64_t last = nvec > 0 ? nvec - 1 : 0;
+  vu4 q[U], qn[U];
+  if (nvec > 0) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = u * NT + tid;
+      q[u] = __builtin_nontemporal_load(xv + (i < last ? i : last));
+    }
+  }
+  for (int64_t base = 0; base < nvec; base += NT * U) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = base + NT * U + u * NT + tid;
+      qn[u] = __builtin_nontemporal_load(xv + (i < last ? i : last));
+    }
+    // Ties (elements equal to v_cut) are rare and a row's kept ties are the
+    // tail of its ties in index order (rank >= rcut, or index >= i_cut).  So
+    // each (wave, u) span of the round is one of: all its ties dropped, all
+    // kept, or the one span of the row holding the cut, where each tie's rank
+    // (or index) is worked out.  Ranks need the wave counts of the round's
+    // earlier spans: they meet in LDS, one barrier per round, and only while
+    // the running count has not yet reached rcut (the mode is the same for
+    // the whole workgroup).
+    float w[U][VEC];
+    bool anytie[U];
+    uint32_t wcnt[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const bool valid = base + u * NT + tid < nvec;
+      E::unpack(q[u], w[u]);
+      bool tie = false;
+      uint32_t c = 0u;
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) {
+        w[u][k] = W.yval(w[u][k]);
+        const bool e = valid && w[u][k] == vc;
+        tie = tie || e;
+        c += (uint32_t)__popcll(__ballot(e));
+      }
+      anytie[u] = tie;
+      wcnt[u] = c;
+    }
+    auto tie_bits = [&](int u) {
+      uint32_t m = 0u;
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) m |= (w[u][k] == vc ? 1u : 0u) << k;
+      return anytie[u] ? m : 0u;
+    };
+    // per span: 0 = drop its ties, 1 = keep them, 2 = exact (keepT bits)
+    int mode[U];
+    uint32_t keepT[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      mode[u] = 0;
+      keepT[u] = 0u;
+    }
+    if (W.rank_form) {
+      if (seen >= W.rcut) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) mode[u] = 1;
+      } else {
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+          if (lane == 0) s_cnt[par * NC + u * kRowWaves + wave] = wcnt[u];
+        __syncthreads();
+        const uint32_t c = lane < NC ? s_cnt[par * NC + lane] : 0u;
+        const uint32_t inc = incl_scan(c);
+        const uint32_t total = (uint32_t)__shfl((int)inc, NC - 1, 64);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const uint32_t start = seen + (uint32_t)__shfl((int)(inc - c), u * kRowWaves + wave, 64);
+          if (start >= W.rcut) {
+            mode[u] = 1;
+          } else if (start + wcnt[u] > W.rcut) {
+            // the span holding the cut: this lane's ties ranked after the
+            // ties of the wave's earlier lanes
+            mode[u] = 2;
+            const uint32_t tb = tie_bits(u);
+            const uint32_t cnt = (uint32_t)__popc(tb);
+            const uint32_t r0 = start + incl_scan(cnt) - cnt;
+            for (uint32_t m = tb; m != 0u; m &= m - 1u) {
+              const int k = __ffs(m) - 1;
+              if (r0 + (uint32_t)__popc(tb & ((1u << k) - 1u)) >= W.rcut) keepT[u] |= 1u << k;
+            }
+          }
+        }
+        seen += total;
+        par ^= 1;
+      }
+    } else {
+      // index form: a tie is kept from index i_cut on
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t span0 = ys.head + (base + u * NT + wave * 64) * VEC;
+        if (span0 >= W.icut) {
+          mode[u] = 1;
+        } else if (span0 + 64 * VEC > W.icut) {
+          mode[u] = 2;
+          const int64_t jb = ys.head + (base + u * NT + tid) * VEC;
+          for (uint32_t m = tie_bits(u); m != 0u; m &= m - 1u) {
+            const int k = __ffs(m) - 1;
+            if (jb + k >= W.icut) keepT[u] |= 1u << k;
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = base + u * NT + tid;
+      const int64_t jb = ys.head + i * VEC;
+      raw vals[VEC];
+      const uint32_t kt = keepT[u];
+      const bool all = mode[u] == 1;
+      if (mode[u] == 2)
+        W.narrow_vec(w[u], vals, [&](int k) { return w[u][k] > vc || ((kt >> k) & 1u) != 0u; });
+      else if (all)
+        W.narrow_vec(w[u], vals, [&](int k) { return w[u][k] >= vc; });
+      else
+        W.narrow_vec(w[u], vals, [&](int k) { return w[u][k] > vc; });
+      // the target element: its value and kept test are kept for the store
+      // of (1 - p) g after the walk, by this thread
+      const int64_t dt = t - jb;
+      if (dt >= 0 && dt < VEC && i < nvec) {
+#pragma unroll
+        for (int k = 0; k < VEC; ++k)
+          if (k == dt) {
+            const bool tk = mode[u] == 2 ? ((kt >> k) & 1u) != 0u : all;
+            t_y = w[u][k];
+            t_kept = w[u][k] > vc || (w[u][k] == vc && tk);
+            t_mine = true;
+          }
+      }
+      if (i < nvec) {
+        vu4 out;
+        __builtin_memcpy(&out, vals, sizeof(out));
+        __builtin_nontemporal_store(out, yv + i);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) q[u] = qn[u];
+  }
+  // the target's (1 - p) g, narrowed exactly, over the -p g stored above (a
+  // later store of the same thread)
+  if (t_mine) y[t] = W.grad_at(t_y, t, t_kept);
+  lane_step(ys.tail0 + lane, ys.tail0 + lane < P.V, wave == 0);
+}
+
+// The backward when no row has a kept list (top-p without top-k, k above the
+// kept-list cap): one kRowThreads workgroup per row writes the whole row, as
+// zeros (rows past R and rows with a zero upstream gradient) or by the walk.
+// (at most 64 VGPRs: two workgroups per CU, i.e. 8 waves per SIMD)
+template <class E>
+__global__ __launch_bounds__(kRowThreads, 8) void filter_bwd_row_kernel(FilterBwdParams P) {
+  using raw = typename E::raw;
+  __shared__ uint32_t s_cnt[2 * kRowVecs * kRowWaves];
+  const int tid = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  const int64_t b = row / P.Rt, r = row - b * P.Rt;
+  raw* y = static_cast<raw*>(P.gin) + b * P.gisb + r * P.gisr;
+  float gv = 0.f;
+  int64_t srow = 0;
+  if (r < P.R) {
+    srow = b * P.R + r;
+    gv = P.g[b * P.gsb + r * P.gsr];
+  }
+  if (gv == 0.f) {
+    const RowSpan<E> zs(y, P.V);
+    vu4* zv = reinterpret_cast<vu4*>(y + zs.head);
+    for (int64_t i = tid; i < zs.nvec; i += kRowThreads) __builtin_nontemporal_store(vu4{0u, 0u, 0u, 0u}, zv + i);
+    const raw zr = E::from_float(0.f);
+    if (tid < zs.head) y[tid] = zr;
+    if (zs.tail0 + tid < P.V) y[zs.tail0 + tid] = zr;
+    return;
+  }
+  const RowInfo ri = P.info[srow];
+  const int64_t t = P.target[b * P.tsb + r * P.tsr];
+  const raw* x = static_cast<const raw*>(P.logits) + b * P.sb + r * P.sr;
+  if constexpr (!std::is_same<E, F32>::value) {
+    if (!P.has_t && P.has_gt && fast_div_row(P, ri, gv)) {
+      walk_row_block<E, kConvFastGT>(P, ri, x, y, gv, t, s_cnt);
+      return;
+    }
+  }
+  if (!P.has_t && !P.has_gt)
+    walk_row_block<E, kConvPlain>(P, ri, x, y, gv, t, s_cnt);
+  else
+    walk_row_block<E, kConvExact>(P, ri, x, y, gv, t, s_cnt);
 }
 
 // Phase 2, one wave per row with a non-zero upstream gradient: with the saved
@@ -1238,11 +1514,10 @@ int launch_topk_export(const FilterParams& P, int64_t rows, hipStream_t st) {
 template <class E>
 int launch_bwd(const FilterBwdParams& P, int64_t B, int64_t rows, hipStream_t st) {
   if (P.zero_rows) {
-    // rows without kept lists: each row written once by phase 2
+    // rows without kept lists: each row written once, by a workgroup of its own
     if (rows == 0) return MIRL_OK;
-    hipLaunchKernelGGL((filter_bwd_scatter_kernel<E>), dim3((unsigned)((rows + 3) / 4)), dim3(256),
-                       0, st, P, rows);
-    return check_launch("filter_bwd_scatter_kernel");
+    hipLaunchKernelGGL((filter_bwd_row_kernel<E>), dim3((unsigned)rows), dim3(kRowThreads), 0, st, P);
+    return check_launch("filter_bwd_row_kernel");
   }
   const bool contiguous = P.gisr == P.V && (B == 1 || P.gisb == P.Rt * P.V);
   if (contiguous) {
