@@ -943,7 +943,7 @@ struct WalkMath {
   int64_t t;
   bool rank_form;
   uint32_t rcut;
-  int64_t icut;
+  int32_t icut;
   __device__ WalkMath(const FilterBwdParams& P_, const RowInfo& ri_, float gv_, int64_t t_)
       : P(P_), ri(ri_), gv(gv_), t(t_) {
     vc = ri.v_cut;
@@ -1121,8 +1121,15 @@ __device__ __forceinline__ void walk_row(const FilterBwdParams& P, const RowInfo
 // so that a round's writes never meet the previous round's reads), and each
 // wave takes the exclusive prefix over the (u, wave) order.  The head and the
 // tail are counted by every wave alike (the same running count everywhere)
-// and written by wave 0.
-constexpr int kRowWaves = 16;
+// and written by wave 0.  Measured on the top-p-alone backward of bf16
+// [4, 4096, 151936] rows (9.48 GB): one wave per row 1.99 ms; 16-wave rows,
+// two per CU, 1.87 ms; 12-wave rows, two per CU (6 waves per SIMD, so more
+// scalar registers per wave), 1.84 ms.  The walk is issue-bound rather than
+// HBM-bound: about 25 VALU instructions per element (the probability, its
+// rounding, the division of an earlier in-place temperature, the kept test),
+// 93% of the VALU issue slots over the kernel (SQ_INSTS_VALU against
+// GRBM_GUI_ACTIVE).
+constexpr int kRowWaves = 12;
 constexpr int kRowThreads = 64 * kRowWaves;
 constexpr int kRowVecs = 2;
 
@@ -1170,26 +1177,29 @@ __device__ __forceinline__ void walk_row_block(const FilterBwdParams& P, const R
   lane_step(lane, lane < ys.head, wave == 0);
   const vu4* xv = reinterpret_cast<const vu4*>(x + xs.head);
   vu4* yv = reinterpret_cast<vu4*>(y + ys.head);
-  const int64_t nvec = ys.nvec;
+  // 32-bit indices in the vector loop (rows hold fewer than 2^31 elements)
+  const int nvec = (int)ys.nvec;
+  const int head = (int)ys.head;
+  const int tt = (t >= 0 && t < P.V) ? (int)t : -1;
   int par = 0;
   float t_y = 0.f;
   bool t_kept = false, t_mine = false;
   // the next round's loads are issued before this round is worked on (two
   // rounds in flight); indices past the row are clamped to its last vector
   // (loaded, never used), so that no load is conditional
-  const int64_t last = nvec > 0 ? nvec - 1 : 0;
+  const int last = nvec > 0 ? nvec - 1 : 0;
   vu4 q[U], qn[U];
   if (nvec > 0) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int64_t i = u * NT + tid;
+      const int i = u * NT + tid;
       q[u] = __builtin_nontemporal_load(xv + (i < last ? i : last));
     }
   }
-  for (int64_t base = 0; base < nvec; base += NT * U) {
+  for (int base = 0; base < nvec; base += NT * U) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int64_t i = base + NT * U + u * NT + tid;
+      const int i = base + NT * U + u * NT + tid;
       qn[u] = __builtin_nontemporal_load(xv + (i < last ? i : last));
     }
     // Ties (elements equal to v_cut) are rare and a row's kept ties are the
@@ -1218,6 +1228,7 @@ __device__ __forceinline__ void walk_row_block(const FilterBwdParams& P, const R
       }
       anytie[u] = tie;
       wcnt[u] = c;
+      __builtin_amdgcn_sched_barrier(0);
     }
     auto tie_bits = [&](int u) {
       uint32_t m = 0u;
@@ -1270,12 +1281,12 @@ __device__ __forceinline__ void walk_row_block(const FilterBwdParams& P, const R
       // index form: a tie is kept from index i_cut on
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const int64_t span0 = ys.head + (base + u * NT + wave * 64) * VEC;
+        const int span0 = head + (base + u * NT + wave * 64) * VEC;
         if (span0 >= W.icut) {
           mode[u] = 1;
         } else if (span0 + 64 * VEC > W.icut) {
           mode[u] = 2;
-          const int64_t jb = ys.head + (base + u * NT + tid) * VEC;
+          const int jb = head + (base + u * NT + tid) * VEC;
           for (uint32_t m = tie_bits(u); m != 0u; m &= m - 1u) {
             const int k = __ffs(m) - 1;
             if (jb + k >= W.icut) keepT[u] |= 1u << k;
@@ -1285,8 +1296,8 @@ __device__ __forceinline__ void walk_row_block(const FilterBwdParams& P, const R
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int64_t i = base + u * NT + tid;
-      const int64_t jb = ys.head + i * VEC;
+      const int i = base + u * NT + tid;
+      const int jb = head + i * VEC;
       raw vals[VEC];
       const uint32_t kt = keepT[u];
       const bool all = mode[u] == 1;
@@ -1298,7 +1309,7 @@ __device__ __forceinline__ void walk_row_block(const FilterBwdParams& P, const R
         W.narrow_vec(w[u], vals, [&](int k) { return w[u][k] > vc; });
       // the target element: its value and kept test are kept for the store
       // of (1 - p) g after the walk, by this thread
-      const int64_t dt = t - jb;
+      const int dt = tt - jb;
       if (dt >= 0 && dt < VEC && i < nvec) {
 #pragma unroll
         for (int k = 0; k < VEC; ++k)
@@ -1314,6 +1325,7 @@ __device__ __forceinline__ void walk_row_block(const FilterBwdParams& P, const R
         __builtin_memcpy(&out, vals, sizeof(out));
         __builtin_nontemporal_store(out, yv + i);
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) q[u] = qn[u];
@@ -1327,9 +1339,13 @@ __device__ __forceinline__ void walk_row_block(const FilterBwdParams& P, const R
 // The backward when no row has a kept list (top-p without top-k, k above the
 // kept-list cap): one kRowThreads workgroup per row writes the whole row, as
 // zeros (rows past R and rows with a zero upstream gradient) or by the walk.
-// (at most 64 VGPRs: two workgroups per CU, i.e. 8 waves per SIMD)
-template <class E>
-__global__ __launch_bounds__(kRowThreads, 8) void filter_bwd_row_kernel(FilterBwdParams P) {
+// (two workgroups per CU: 6 waves per SIMD).  KIND
+// picks the conversions the launch needs (kRowPlain: none; kRowGT: an earlier
+// in-place division only; kRowExact: the rest), so that each kernel holds the
+// walks it uses and no more.
+enum RowKind { kRowPlain = 0, kRowGT = 1, kRowExact = 2 };
+template <class E, int KIND>
+__global__ __launch_bounds__(kRowThreads, 6) void filter_bwd_row_kernel(FilterBwdParams P) {
   using raw = typename E::raw;
   __shared__ uint32_t s_cnt[2 * kRowVecs * kRowWaves];
   const int tid = threadIdx.x;
@@ -1354,16 +1370,17 @@ __global__ __launch_bounds__(kRowThreads, 8) void filter_bwd_row_kernel(FilterBw
   const RowInfo ri = P.info[srow];
   const int64_t t = P.target[b * P.tsb + r * P.tsr];
   const raw* x = static_cast<const raw*>(P.logits) + b * P.sb + r * P.sr;
-  if constexpr (!std::is_same<E, F32>::value) {
-    if (!P.has_t && P.has_gt && fast_div_row(P, ri, gv)) {
-      walk_row_block<E, kConvFastGT>(P, ri, x, y, gv, t, s_cnt);
-      return;
-    }
-  }
-  if (!P.has_t && !P.has_gt)
+  if constexpr (KIND == kRowPlain) {
     walk_row_block<E, kConvPlain>(P, ri, x, y, gv, t, s_cnt);
-  else
+  } else {
+    if constexpr (KIND == kRowGT && !std::is_same<E, F32>::value) {
+      if (fast_div_row(P, ri, gv)) {
+        walk_row_block<E, kConvFastGT>(P, ri, x, y, gv, t, s_cnt);
+        return;
+      }
+    }
     walk_row_block<E, kConvExact>(P, ri, x, y, gv, t, s_cnt);
+  }
 }
 
 // Phase 2, one wave per row with a non-zero upstream gradient: with the saved
@@ -1516,7 +1533,15 @@ int launch_bwd(const FilterBwdParams& P, int64_t B, int64_t rows, hipStream_t st
   if (P.zero_rows) {
     // rows without kept lists: each row written once, by a workgroup of its own
     if (rows == 0) return MIRL_OK;
-    hipLaunchKernelGGL((filter_bwd_row_kernel<E>), dim3((unsigned)rows), dim3(kRowThreads), 0, st, P);
+    if (!P.has_t && !P.has_gt)
+      hipLaunchKernelGGL((filter_bwd_row_kernel<E, kRowPlain>), dim3((unsigned)rows), dim3(kRowThreads),
+                         0, st, P);
+    else if (!P.has_t)
+      hipLaunchKernelGGL((filter_bwd_row_kernel<E, kRowGT>), dim3((unsigned)rows), dim3(kRowThreads), 0,
+                         st, P);
+    else
+      hipLaunchKernelGGL((filter_bwd_row_kernel<E, kRowExact>), dim3((unsigned)rows), dim3(kRowThreads),
+                         0, st, P);
     return check_launch("filter_bwd_row_kernel");
   }
   const bool contiguous = P.gisr == P.V && (B == 1 || P.gisb == P.Rt * P.V);
