@@ -59,3 +59,49 @@ def test_invalid_arguments_return_status_not_abort():
     assert "shape" in lib.mirl_last_error().decode()
     assert lib.mirl_clipped_pg_workspace_elems(8, 100, 0) > 0
     assert lib.mirl_clipped_pg_workspace_elems(8, 100, 1) == lib.mirl_clipped_pg_workspace_elems(8, 100, 0) + 2400
+
+
+def _prototypes() -> dict:
+    """name -> (return type, [parameter types]) for every prototype in the header."""
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    text = re.sub(r"^\s*#.*$", "", text, flags=re.M)
+    out = {}
+    for ret, name, params in re.findall(r"([A-Za-z_][\w\s\*]*?)\s*\b(mirl_\w+)\s*\(([^)]*)\)\s*;", text):
+        ps = [p.strip() for p in params.split(",") if p.strip() and p.strip() != "void"]
+        # drop the parameter name: what remains is the type
+        types = [re.sub(r"\s*\b\w+$", "", p).replace(" *", "*").strip() for p in ps]
+        out[name] = (ret.split()[-1] if ret.strip() else ret, types)
+    return out
+
+
+def _ctype_matches(ctype_name: str, ct) -> bool:
+    import ctypes
+
+    if ctype_name.endswith("*"):
+        return ct in (ctypes.c_void_p, ctypes.c_char_p) or (
+            isinstance(ct, type) and issubclass(ct, ctypes._Pointer))
+    scalar = {"int64_t": ctypes.c_int64, "int": ctypes.c_int, "double": ctypes.c_double,
+              "float": ctypes.c_float, "uint32_t": ctypes.c_uint32, "int32_t": ctypes.c_int32}
+    if ctype_name in scalar:
+        return ct is scalar[ctype_name]
+    # a struct passed by value
+    return isinstance(ct, type) and issubclass(ct, ctypes.Structure) and ct.__name__ != ""
+
+
+def test_binding_argument_types_follow_the_header():
+    """Every entry point's ctypes argument list has the header's arity and, position by
+    position, the same kind of type (a changed C signature must change the binding too)."""
+    from rl_amd import _C
+
+    protos = _prototypes()
+    assert set(protos) == set(_C.SIGNATURES)
+    bad = []
+    for name, (_, ptypes) in protos.items():
+        _, argtypes = _C.SIGNATURES[name]
+        if len(argtypes) != len(ptypes):
+            bad.append((name, "arity", len(ptypes), len(argtypes)))
+            continue
+        for k, (pt, ct) in enumerate(zip(ptypes, argtypes)):
+            if not _ctype_matches(pt, ct):
+                bad.append((name, k, pt, ct))
+    assert not bad, bad
