@@ -48,6 +48,7 @@ import os
 import sys
 import time
 from pathlib import Path
+from typing import Optional
 
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
@@ -326,13 +327,15 @@ def _calibration_copy(args, dev) -> None:
     del a, b
 
 
-def _timed(step, steps: int, warmup: int, main_kernels: list):
+def _timed(step, steps: int, warmup: int, main_kernels: list, region_events: Optional[dict] = None):
     """Run `warmup` untimed steps, then `steps` timed ones; (ms per step, ms per entry point).
 
     Inside the timed region HIP events bracket only the `main_kernels` entry
     points (each event pair adds a few microseconds of GPU time between
     neighbouring launches); the other entry points are timed afterwards over a
-    few more steps.
+    few more steps.  With `region_events` (a dict), one event pair on the
+    current stream also brackets the whole timed region and its GPU time per
+    step is stored under "gpu_ms_per_step".
     """
     import torch
 
@@ -341,14 +344,24 @@ def _timed(step, steps: int, warmup: int, main_kernels: list):
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
-    timer = _C.enable_launch_timing(main_kernels)
+    timer = _C.enable_launch_timing(main_kernels) if main_kernels else None
     torch.cuda.synchronize()
+    if region_events is not None:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
+    if region_events is not None:
+        e0.record()
     for _ in range(steps):
         step()
+    if region_events is not None:
+        e1.record()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
+    if region_events is not None:
+        region_events["gpu_ms_per_step"] = e0.elapsed_time(e1) / steps
     _C.disable_launch_timing()
+    if timer is None:
+        timer = {}
     ms = {k: sum(a.elapsed_time(b) for a, b in v) / max(1, len(v)) for k, v in timer.items()}
     rest = _C.enable_launch_timing()
     for _ in range(min(steps, 5)):
@@ -478,13 +491,16 @@ def bench_workload(args) -> None:
             it[0] += 1
             return from_parallel_logits_to_logprobs(c["logits"], c["input_ids"], 0, V, None, inference_only=True)
 
-        ms_step, ms = _timed(step, args.steps, args.warmup, ["mirl_logprob_fwd"])
+        # No events inside the timed steps: an event pair around a 13-us launch
+        # costs host and GPU time of its own (with them the step read 23 us
+        # against 10 us of host work per call and a 13-us kernel).
+        region = {}
+        ms_step, ms = _timed(step, args.steps, args.warmup, [], region)
         rows = B * (S - 1)
         esz = 4
-        # An event pair around one 14-us launch measures the pair's own cost as
-        # well; the kernel's launch duration comes from one pair of events
-        # around a burst of back-to-back launches of the entry point (the same
-        # inputs and outputs, the rotating copies in turn).
+        # The kernel's launch duration comes from one pair of events around a
+        # burst of back-to-back launches of the entry point (the same inputs and
+        # outputs, the rotating copies in turn).
         outs = [torch.empty((B, S - 1), dtype=torch.float32, device=dev) for _ in copies]
         tgts = [c["input_ids"][:, 1:] for c in copies]
         burst = 200
@@ -499,8 +515,12 @@ def bench_workload(args) -> None:
         e1.record()
         torch.cuda.synchronize()
         extra["logprob_fwd_event_pair_ms"] = ms.get("mirl_logprob_fwd", 0.0)
-        ms["mirl_logprob_fwd"] = e0.elapsed_time(e1) / burst
-        extra["launch_duration_from"] = f"events around {burst} back-to-back launches"
+        extra["logprob_fwd_burst_ms"] = e0.elapsed_time(e1) / burst
+        # the launch duration: GPU time of the timed region (one event pair on
+        # the launch stream around all timed steps, one launch per step) per step
+        ms["mirl_logprob_fwd"] = region["gpu_ms_per_step"]
+        extra["launch_duration_from"] = ("one event pair around the timed steps (one launch per step); "
+                                         f"burst of {burst} back-to-back launches alongside")
         roof = _roofline("mirl_logprob_fwd", rows * V * esz, ms.get("mirl_logprob_fwd", 0.0), w)
         step_bytes = rows * V * esz
         cfg = {"workload": "logprob_fwd_f32", "logits": [B, S, V], "next_token_rows": rows,
