@@ -21,9 +21,12 @@
 #include <mutex>
 
 #include "common.h"
+#include "pg_token.h"
 
 namespace mirl {
 namespace {
+
+using namespace pg;
 
 // Threads per sequence row: 1024 for fp32 rows (measured 25 vs 29 us at 256 on
 // 8 rows of 2047 tokens, where one workgroup per row leaves most CUs idle),
@@ -57,65 +60,6 @@ enum Slot {
   P_HM,  // score-centering head mass
   NUM_SLOTS
 };
-
-template <class T>
-struct View {
-  const T* p;
-  int64_t sb, sl;
-  __device__ __forceinline__ T operator()(int64_t b, int64_t l) const { return p[b * sb + l * sl]; }
-};
-
-struct MaskView {
-  const uint8_t* p;
-  int64_t sb, sl;
-  __device__ __forceinline__ bool operator()(int64_t b, int64_t l) const {
-    return p[b * sb + l * sl] != 0;
-  }
-};
-
-template <class T>
-__device__ __forceinline__ T dexp(T x) {
-  if constexpr (sizeof(T) == 8) return exp(x); else return expf(x);
-}
-template <class T>
-__device__ __forceinline__ T dlog(T x) {
-  if constexpr (sizeof(T) == 8) return log(x); else return logf(x);
-}
-template <class T>
-__device__ __forceinline__ T dabs(T x) {
-  if constexpr (sizeof(T) == 8) return fabs(x); else return fabsf(x);
-}
-template <class T>
-__device__ __forceinline__ T nan_to_zero_all(T x) {
-  // nan_to_num(x, nan=0, posinf=0, neginf=0)
-  return isfinite(x) ? x : T(0);
-}
-template <class T>
-__device__ __forceinline__ T dclamp(T x, T lo, T hi) {
-  // torch.clamp: min then max, NaN propagates
-  if (isnan(x)) return x;
-  return x < lo ? lo : (x > hi ? hi : x);
-}
-
-// maximum(a, b) gradient share of a (PyTorch: ties split evenly)
-template <class T>
-__device__ __forceinline__ T max_share_a(T a, T b) {
-  return a > b ? T(1) : (a < b ? T(0) : T(0.5));
-}
-
-// Per-token KL estimate k(logr) and its derivative dk/dlogr.
-template <class T>
-__device__ __forceinline__ T kl_value(int type, T lr) {
-  if (type == MIRL_KL_K1) return -lr;
-  if (type == MIRL_KL_K2) return (lr * lr) / T(2);
-  return (dexp(lr) - T(1)) - lr;
-}
-template <class T>
-__device__ __forceinline__ T kl_deriv(int type, T lr) {
-  if (type == MIRL_KL_K1) return T(-1);
-  if (type == MIRL_KL_K2) return lr;
-  return dexp(lr) - T(1);
-}
 
 // Block-wide reductions over row_threads<T>() / kFinalThreads threads.
 template <class T, int NT>
@@ -187,34 +131,6 @@ __device__ __forceinline__ int slot_kind(int k) {
   if (k == P_RATIO_MIN || k == P_RATIO_C_MIN) return R_MIN;
   if (k == P_RATIO_MAX || k == P_RATIO_C_MAX) return R_MAX;
   return R_SUM;
-}
-
-// Truncated importance sampling applied to one weight (loss_functions.py:921-1013).
-// `oob` reports whether the weight fell outside the truncation bounds.
-template <class T>
-__device__ __forceinline__ T truncate_is(const mirl_pg_config& cfg, T w, T A, T seq_kept, bool* oob) {
-  if (cfg.tis_type == MIRL_TIS_TIS) {
-    const T tmin = T(cfg.tis_ratio_min), tmax = T(cfg.tis_ratio);
-    *oob = (w > tmax) || (w < tmin);
-    return dclamp(w, tmin, tmax);
-  }
-  if (cfg.tis_type == MIRL_TIS_ICEPOP) {
-    const bool kept = (w >= T(cfg.tis_ratio_min)) && (w <= T(cfg.tis_ratio));
-    *oob = !kept;
-    return kept ? w : T(0);
-  }
-  if (cfg.tis_type == MIRL_TIS_ADAPTIVE) {
-    const bool kept = (w <= T(cfg.adaptive_outer)) && ((A >= T(0)) || (w >= T(cfg.tis_ratio_min))) &&
-                      ((A <= T(0)) || (w <= T(cfg.adaptive_hi)));
-    *oob = !kept;
-    return kept ? w : T(0);
-  }
-  if (cfg.tis_type == MIRL_TIS_SEQ_MASK) {
-    *oob = false;
-    return w * seq_kept;
-  }
-  *oob = false;
-  return w;
 }
 
 // torch.maximum / torch.minimum: NaN in either operand propagates.
@@ -353,7 +269,6 @@ __global__ __launch_bounds__(NT) void pg_rows_kernel(mirl_pg_config cfg, int64_t
   const T gvt = *in.gvt + eps;
   const T gvs = *in.gvs + eps;
   const bool has_kl = cfg.kl_penalty != 0.0;
-  const T beta = T(cfg.kl_penalty);
 
   // ---- pass A: row masks --------------------------------------------------
   // support'(l) = psm & ~isneginf(prev) & ~isneginf(gen)
@@ -409,9 +324,6 @@ __global__ __launch_bounds__(NT) void pg_rows_kernel(mirl_pg_config cfg, int64_t
     seq_is = r[1];
     seq_lir = r[2];
   }
-  // clamp bounds are formed in double, as Python does, then rounded once
-  const T lo = T(1.0 - cfg.ratio_clip_min);
-  const T hi = T(1.0 + cfg.ratio_clip_max);
   const bool seq_ratio = cfg.sequence_level_is && !cfg.disable_ppo_ratio && !cfg.force_on_policy;
   const T r_seq = seq_ratio ? dexp(seq_lr / (sum_tm2 + eps)) : T(0);
   const T w_seq = nan_to_zero_all(dexp(seq_is));
@@ -447,116 +359,37 @@ __global__ __launch_bounds__(NT) void pg_rows_kernel(mirl_pg_config cfg, int64_t
     // score centering zeroes the advantages outside the final mask
     // (loss_functions.py:841-842)
     const T A = (has_sc && !on) ? T(0) : in.adv(b, l);
-    T gc = T(0);  // dloss/dcurr (this token)
-    T gu = T(0);  // dloss/dunfiltered
-
-    // KL term ------------------------------------------------------------
-    if (has_kl) {
-      const bool kon = kl_mask != T(0);
-      const T cu = kon ? (cfg.has_unfiltered ? in.unf(b, l) : craw) : T(0);
-      const T rf = kon ? in.ref(b, l) : T(0);
-      const T kgen = kon ? in.gen(b, l) : T(0);
-      // importance weight exp(cu - X), X detached
-      const T e = cfg.use_on_policy_kl ? dexp(cu - kgen) : dexp(cu - cu);
-      const T w = nan_to_zero_all(e);
-      const T dw = isfinite(e) ? e : T(0);
-      T lr = rf - cu;
-      T dlr_pass = T(1);  // d(clamped logr)/d(logr)
-      bool w_grad = true;
-      if (cfg.has_kl_input_clamp) {
-        const T ic = T(cfg.kl_input_clamp);
-        const T lc = dclamp(lr, -ic, ic);
-        w_grad = (lr == lc);
-        dlr_pass = (lr >= -ic && lr <= ic) ? T(1) : T(0);
-        lr = lc;
-      }
-      const T k = kl_value<T>(cfg.kl_type, lr);
-      T kw = w * k;
-      T out_pass = T(1);
-      if (cfg.has_kl_output_clamp) {
-        const T oc = T(cfg.kl_output_clamp);
-        out_pass = (kw >= -oc && kw <= oc) ? T(1) : T(0);
-        kw = dclamp(kw, -oc, oc);
-      }
-      const T klt = beta * kw;
-      T kappa;
-      if (cfg.token_level_loss) {
-        kappa = kl_mask / gvt;
-        acc[P_KL] += klt * kl_mask;
-      } else {
-        kappa = sm * tmv / (kl_row_norm * gvs);
-        acc[P_KL] += klt * tmv;  // scaled per row below
-      }
-      // d kl_t / d cu
-      const T dk = kl_deriv<T>(cfg.kl_type, lr) * dlr_pass * T(-1);
-      const T dkl = beta * out_pass * ((w_grad ? dw : T(0)) * k + w * dk);
-      const T g = kon ? kappa * dkl : T(0);
-      if (cfg.has_unfiltered) gu = g; else gc += g;
-    }
-
-    // importance weights -------------------------------------------------
-    T w = T(1);
-    bool has_w = false;
-    if (cfg.need_is) {
-      has_w = true;
-      w = cfg.sequence_level_is ? w_seq : nan_to_zero_all(dexp(pv - gv));
-      bool oob = false;
-      w = truncate_is(cfg, w, A, seq_kept, &oob);
-      acc[P_OOB] += (oob ? T(1) : T(0)) * mask2;
-    }
-    const bool use_w = cfg.use_is_correction != 0;
-
-    // actor objective ------------------------------------------------------
-    T r, rc, dr_dc, drc_dr;
-    if (cfg.force_on_policy) {
-      r = dexp(c - c);
-      rc = r;
-      dr_dc = r;
-      drc_dr = T(1);
-    } else if (!cfg.disable_ppo_ratio) {
-      if (cfg.sequence_level_is) {
-        r = r_seq;
-        dr_dc = T(0);  // handled through gspo_sum
-      } else {
-        r = dexp(c - pv);
-        dr_dc = r;
-      }
-      rc = dclamp(r, lo, hi);
-      drc_dr = (r >= lo && r <= hi) ? T(1) : T(0);
-    } else {
-      r = c;
-      rc = c;
-      dr_dc = T(1);
-      drc_dr = T(1);
-    }
-    const T na = -A;
-    T cl, dcl_dr = T(0), dcl_dc_direct = T(0);
-    if (cfg.use_cispo) {
-      cl = (na * rc) * c;
-      dcl_dc_direct = na * rc;
-    } else {
-      const T a1 = na * r, a2 = na * rc;
-      cl = a1 > a2 ? a1 : (a1 < a2 ? a2 : a1);
-      if (isnan(a1) || isnan(a2)) cl = a1 + a2;
-      const T sa = max_share_a(a1, a2);
-      dcl_dr = sa * na + (T(1) - sa) * na * drc_dr;
-      if (cfg.ratio_clip_c > 0.0 && A < T(0)) {
-        const T z = na * T(cfg.ratio_clip_c);
-        const T s = cl < z ? T(1) : (cl > z ? T(0) : T(0.5));
-        cl = cl < z ? cl : z;
-        dcl_dr *= s;
-      }
-    }
-    const T wv = (has_w && use_w) ? w : T(1);
-    const T v = wv * cl;
-    T alpha;
-    if (cfg.token_level_loss) {
-      alpha = mask2 / gvt;
-      acc[P_ACTOR] += v * mask2;
-    } else {
-      alpha = sm2 * tm2 / (actor_row_norm * gvs);
-      acc[P_ACTOR] += v * tm2;  // scaled per row below
-    }
+    TokenIn<T> ti;
+    ti.tmv = tmv;
+    ti.tm2 = tm2;
+    ti.sm = sm;
+    ti.sm2 = sm2;
+    ti.craw = craw;
+    ti.c = c;
+    ti.pv = pv;
+    ti.gv = gv;
+    ti.A = A;
+    const bool kon = kl_mask != T(0);
+    ti.cu = (has_kl && kon) ? (cfg.has_unfiltered ? in.unf(b, l) : craw) : T(0);
+    ti.rf = (has_kl && kon) ? in.ref(b, l) : T(0);
+    ti.kgen = (has_kl && kon) ? in.gen(b, l) : T(0);
+    ti.gvt = gvt;
+    ti.gvs = gvs;
+    ti.actor_row_norm = actor_row_norm;
+    ti.kl_row_norm = kl_row_norm;
+    ti.r_seq = r_seq;
+    ti.w_seq = w_seq;
+    ti.seq_kept = seq_kept;
+    ti.seq_ratio = seq_ratio;
+    const TokenOut<T> to = token_terms<T>(cfg, ti);
+    T gc = to.gc;  // dloss/dcurr (this token)
+    const T gu = to.gu;  // dloss/dunfiltered
+    if (has_kl) acc[P_KL] += to.klt * (cfg.token_level_loss ? kl_mask : tmv);
+    const T w = to.w;
+    if (cfg.need_is) acc[P_OOB] += (to.oob ? T(1) : T(0)) * mask2;
+    const T r = to.r, rc = to.rc;
+    const T alpha = to.alpha;
+    acc[P_ACTOR] += to.v * (cfg.token_level_loss ? mask2 : tm2);
     if (has_sc) {
       // correction A * term, normalised like the actor loss (loss_functions.py:1070-1097);
       // term / head come from sc_term_kernel, the gradient scale goes to sc_scale_kernel
@@ -567,13 +400,7 @@ __global__ __launch_bounds__(NT) void pg_rows_kernel(mirl_pg_config cfg, int64_t
       }
       sc_ws.scale[i] = on ? alpha * A : T(0);
     }
-    if (cfg.use_cispo) {
-      gc += on ? alpha * wv * dcl_dc_direct : T(0);
-    } else if (seq_ratio) {
-      gspo_sum += alpha * wv * dcl_dr;
-    } else {
-      gc += on ? alpha * wv * dcl_dr * dr_dc : T(0);
-    }
+    if (seq_ratio) gspo_sum += to.gspo;
 
     // NLL bookkeeping (gradient added by the final kernel)
     if (correct) {
