@@ -2,13 +2,11 @@
 //
 // One thread per sample.  A sample's group is every row whose prompt key
 // equals its own (exact row equality, as torch.unique(prompts, dim=0) groups
-// them), found by a scan over the other samples in ascending order.  A pair of
-// rows is told apart by its first elements in almost every case; rows that
-// agree there are compared with independent loads, so a long key (prompt token
-// rows) costs O(B^2 + B n K) for groups of n, not a chain of dependent loads.
-// Measured on MI355X: B = 8200 rows of 16 (512) tokens in 512 groups, 2.8
-// (57) ms; a variant that hashed every key once in one workgroup and compared
-// hashes took 27.5 (981) ms, since one workgroup cannot match the scan's 32.
+// them), found by a scan over the other samples in ascending order: one thread
+// per sample for single-element keys (group ids), one wave per sample for
+// longer keys (prompt token rows), where a pair is told apart by its first
+// elements in almost every case and rows that agree there are compared 64
+// elements at a time with coalesced loads, O(B^2 + B n K) for groups of n.
 // Group sums are accumulated in double and rounded once to fp32, where the
 // reference uses an fp32 matrix-vector product; the two agree to the last
 // fp32 ulp of the sum.
@@ -105,6 +103,27 @@ __global__ __launch_bounds__(256) void grpo_advantage_kernel(AdvArgs A) {
   sample_advantage(A, i, [&](int64_t j) { return same_key(A, i, j); });
 }
 
+// Keys of more than one element: one wave per sample.  The wave walks the
+// other samples together (every lane runs the same accumulation in the same
+// order, so every lane holds the thread kernel's bits); a row that agrees on
+// its first element is compared 64 elements at a time with coalesced loads and
+// a ballot.
+__global__ __launch_bounds__(256) void grpo_advantage_wave_kernel(AdvArgs A) {
+  const int64_t i = (int64_t)blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+  if (i >= A.B) return;  // whole waves leave together
+  const int lane = threadIdx.x % kWave;
+  const int64_t* pi = A.prompts + i * A.ps;
+  const int64_t p0 = pi[0];
+  sample_advantage(A, i, [&](int64_t j) {
+    if (j == i) return true;
+    const int64_t* pj = A.prompts + j * A.ps;
+    if (pj[0] != p0) return false;
+    uint64_t diff = 0;
+    for (int64_t k = 1 + lane; k < A.K; k += kWave) diff |= (uint64_t)(pi[k] ^ pj[k]);
+    return __ballot(diff != 0) == 0ull;
+  });
+}
+
 }  // namespace
 }  // namespace mirl
 
@@ -123,7 +142,12 @@ extern "C" int mirl_grpo_advantage(const int64_t* prompts, int64_t B, int64_t K,
   AdvArgs a{prompts, B, K, prompt_stride, rewards, std_rewards, valid_mask, leave_one_out, normalize,
             adv, baseline, std, trivial};
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const unsigned blocks = (unsigned)((B + 255) / 256);
-  hipLaunchKernelGGL(grpo_advantage_kernel, dim3(blocks), dim3(256), 0, st, a);
+  if (K > 1) {
+    const unsigned blocks = (unsigned)((B + 3) / 4);  // four samples (waves) per workgroup
+    hipLaunchKernelGGL(grpo_advantage_wave_kernel, dim3(blocks), dim3(256), 0, st, a);
+  } else {
+    const unsigned blocks = (unsigned)((B + 255) / 256);
+    hipLaunchKernelGGL(grpo_advantage_kernel, dim3(blocks), dim3(256), 0, st, a);
+  }
   return check_launch("mirl_grpo_advantage");
 }
