@@ -281,7 +281,8 @@ typedef struct mirl_filter_row_info {
 
 /*
  * Filtered selected-token logprobs, one row per (b, r):
- *   y = dtype(float(x) / temperature)    (skipped when temperature == 1)
+ *   y = dtype(fl32(float(x) * r)), r = fl32(1.0 / temperature) formed in
+ *     double (skipped when temperature == 1): torch's GPU x.div_(temperature)
  *   top-k (top_k > 0): keep y >= k-th largest y, every tie kept;
  *   top-p (top_p < 1): over the kept values in ascending order, ties by
  *     vocabulary index, p = softmax, keep where cumsum(p) > 1 - top_p,
@@ -318,10 +319,11 @@ int mirl_filtered_logprob_fwd(const void* logits, int dtype, int64_t B, int64_t 
 /*
  * Gradient of the filtered logprobs with respect to the raw logits:
  *   g32 = (onehot(t) - p) * g on the kept set, 0 elsewhere,
- *   grad = dtype(dtype(g32) / temperature)   (dtype(g32) when temperature == 1),
- *   then, when grad_temperature != 1, grad = dtype(grad / grad_temperature): the
- *   backward of an in-place division of the logits by grad_temperature made
- *   before the forward (mirl_temperature_scale), folded into this write.
+ *   grad = dtype(fl32(dtype(g32) * fl32(1.0 / temperature)))   (dtype(g32) when
+ *   temperature == 1), then, when grad_temperature != 1,
+ *   grad = dtype(fl32(grad * fl32(1.0 / grad_temperature))): the backward of an
+ *   in-place division of the logits by grad_temperature made before the forward
+ *   (mirl_temperature_scale), folded into this write.
  * Rows r >= R (up to R_total) and rows with g == 0 are written as zeros.
  * Rows whose kept list was saved are written without reading the logits.
  * top_k is the forward's: it selects the schedule only (with 1 <= top_k <=
@@ -360,7 +362,9 @@ int mirl_top_k_top_p_mask(const void* logits, int dtype, int64_t N, int64_t V,
 
 /*
  * In-place temperature scaling of [B, R, V] logits (unit stride on V):
- *   x = dtype(float(x) / float(temperature)), rounded to nearest even.
+ *   x = dtype(fl32(float(x) * fl32(1.0 / temperature))), each rounding to
+ *   nearest even, the reciprocal formed in double: torch's GPU division of a
+ *   tensor by a Python scalar, which is where the reference runs it.
  *
  * Replaces: apply_temperature_scaling's logits.div_(temperature)
  * (nemo_rl/models/automodel/train.py:248-262,
@@ -371,8 +375,9 @@ int mirl_temperature_scale(void* logits, int dtype, int64_t B, int64_t R, int64_
                            void* stream);
 
 /*
- * Backward of mirl_temperature_scale: out = dtype(float(g) / float(T)); with
- * `grad2` non-NULL, out = dtype(float(dtype(float(g) + float(grad2))) / float(T))
+ * Backward of mirl_temperature_scale: out = dtype(fl32(float(g) * r)), r =
+ * fl32(1.0 / T); with `grad2` non-NULL,
+ * out = dtype(fl32(float(dtype(float(g) + float(grad2))) * r))
  * (two consumers' gradients accumulated in the dtype first).  All three are
  * [B, R, V] views with unit stride on V; `out` may alias `grad`.
  *
@@ -393,10 +398,11 @@ int mirl_temperature_scale_grad(const void* grad, int dtype, int64_t B, int64_t 
 int64_t mirl_linear_ce_workspace_elems(int64_t T, int64_t V);
 
 /*
- * Selected-token logprobs from bf16 hidden states [T, H] (row r is sequence
+ * Selected-token logprobs from hidden states [T, H] (row r is sequence
  * position s = r / B of batch row b = r % B, i.e. a [S, B, H] tensor viewed as
- * rows) and a bf16 output weight [V, H]:
- *   x[r, v]  = bf16(sum_k hidden[r, k] * weight[v, k])   (fp32 accumulation)
+ * rows) and an output weight [V, H], both of `dtype` (MIRL_DTYPE_BF16 or
+ * MIRL_DTYPE_F16):
+ *   x[r, v]  = dtype(sum_k hidden[r, k] * weight[v, k])   (fp32 accumulation)
  *   out[b,s] = (x[r, t'] - m) - log(sum_v exp(x[r, v] - m)),  t' = target[b, s] - vocab_start,
  *   out[b,s] = 0 when target < vocab_start or >= vocab_end.
  * The [T, V] logits are never written.  H must be a multiple of 128, row
@@ -410,7 +416,7 @@ int64_t mirl_linear_ce_workspace_elems(int64_t T, int64_t V);
  * from_parallel_hidden_states_to_logprobs (model_utils.py:2541-2569), with a
  * vocab group of size 1.
  */
-int mirl_linear_ce_fwd(const void* hidden, int64_t T, int64_t H, int64_t ldh,
+int mirl_linear_ce_fwd(const void* hidden, int dtype, int64_t T, int64_t H, int64_t ldh,
                        const void* weight, int64_t V, int64_t ldw, int64_t B,
                        const int64_t* target, int64_t t_stride_b, int64_t t_stride_s,
                        int64_t vocab_start, int64_t vocab_end, float* out,
@@ -419,7 +425,9 @@ int mirl_linear_ce_fwd(const void* hidden, int64_t T, int64_t H, int64_t ldh,
 
 /*
  * Gradient of those logprobs with respect to the logits, for rows
- * [row0, row0 + nrows), recomputing the logits tile by tile:
+ * [row0, row0 + nrows), recomputing the logits tile by tile (x in `dtype` as
+ * above; the gradient is bf16 for either dtype, whose exponent range keeps the
+ * small softmax terms that fp16 would flush):
  *   grad_logits[r - row0, v] = bf16((onehot(t')[v] - exp((x[r, v] - m) - logsum)) * g[b, s])
  * (row stride ldg >= V).  Tiles whose rows all have g == 0 are written as zeros
  * without the GEMM.  The hidden-state and weight gradients are the products
@@ -437,7 +445,7 @@ int mirl_linear_ce_fwd(const void* hidden, int64_t T, int64_t H, int64_t ldh,
  * ChunkedDistributedHiddenStatesToLogprobs.backward
  * (nemo_rl/distributed/model_utils.py:2647-2745).
  */
-int mirl_linear_ce_grad(const void* hidden, int64_t T, int64_t H, int64_t ldh,
+int mirl_linear_ce_grad(const void* hidden, int dtype, int64_t T, int64_t H, int64_t ldh,
                         const void* weight, int64_t V, int64_t ldw, int64_t B,
                         const int64_t* target, int64_t t_stride_b, int64_t t_stride_s,
                         int64_t vocab_start, int64_t vocab_end, const float* row_stats,
@@ -450,7 +458,8 @@ int mirl_linear_ce_grad(const void* hidden, int64_t T, int64_t H, int64_t ldh,
  * C = A . B^T for bf16 A [M, K] and B [N, K] (row strides lda, ldb, multiples
  * of 8 elements; K a multiple of 128; 16-byte aligned), with fp32
  * accumulation on the MFMA units (the tile loop of mirl_linear_ce_fwd):
- *   Cb != NULL: Cb[m, n] = bf16(C[m, n])          (row stride ldcb);
+ *   Cb != NULL: Cb[m, n] = cb_dtype(C[m, n])      (row stride ldcb; cb_dtype
+ *               MIRL_DTYPE_BF16 or MIRL_DTYPE_F16);
  *   else:       C[s, m, n] = the product over the s-th of k_splits ranges of
  *               K ([k_splits][M][ldc] fp32), or C[m, n] += C when accumulate
  *               (k_splits = 1).
@@ -474,28 +483,32 @@ int mirl_linear_ce_grad(const void* hidden, int64_t T, int64_t H, int64_t ldh,
 #define MIRL_COUNT_K 1
 int mirl_gemm_bf16_abt(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M,
                        int64_t N, int64_t K, int64_t k_splits, float* C, int64_t ldc,
-                       int accumulate, void* Cb, int64_t ldcb, const int64_t* count,
-                       int64_t count_off, int count_axis, int64_t final_at, void* stream);
+                       int accumulate, void* Cb, int64_t ldcb, int cb_dtype,
+                       const int64_t* count, int64_t count_off, int count_axis,
+                       int64_t final_at, void* stream);
 
-/* out[r(m), n] = bf16(sum_s part[s, m, n]) summed in s order (part [k_splits][M][ld]
- * fp32, out row stride ldo): the splits of mirl_gemm_bf16_abt.  r(m) = out_rows[m]
+/* out[r(m), n] = out_dtype(sum_s part[s, m, n]) summed in s order (part [k_splits][M][ld]
+ * fp32, out row stride ldo, out_dtype MIRL_DTYPE_BF16 or MIRL_DTYPE_F16): the
+ * splits of mirl_gemm_bf16_abt.  r(m) = out_rows[m]
  * (a device int64 row map; rows mapped outside [0, out_nrows) are skipped) or m
  * when out_rows is NULL.  With `count` (a device int64, or NULL), rows
  * m >= *count - count_off are written as zeros without reading part.
  * Replaces: part of the dH matmul above (model_utils.py:2701-2703) and the
  * scatter of the active rows' dH back to their positions. */
 int mirl_sum_splits_bf16(const float* part, int64_t k_splits, int64_t M, int64_t N,
-                         int64_t ld, void* out, int64_t ldo, const int64_t* out_rows,
-                         int64_t out_nrows, const int64_t* count, int64_t count_off,
-                         void* stream);
+                         int64_t ld, void* out, int64_t ldo, int out_dtype,
+                         const int64_t* out_rows, int64_t out_nrows, const int64_t* count,
+                         int64_t count_off, void* stream);
 
-/* dst[c, r] = src[r, c] (bf16) for r < R, c < C, and 0 for R <= r < R_pad
+/* dst[c, r] = bf16(src[r, c]) (src of src_dtype, MIRL_DTYPE_BF16 or
+ * MIRL_DTYPE_F16; dst bf16) for r < R, c < C, and 0 for R <= r < R_pad
  * (src row stride lds, dst row stride ldd >= R_pad), R = min(R, *count) when
  * `count` (a device int64) is given: the transposed operands of the
  * hidden-state backward.
  * Replaces: the transposes inside the dH / dW matmuls (model_utils.py:2701-2716). */
-int mirl_transpose_bf16(const void* src, int64_t R, int64_t C, int64_t lds, void* dst,
-                        int64_t ldd, int64_t R_pad, const int64_t* count, void* stream);
+int mirl_transpose_bf16(const void* src, int src_dtype, int64_t R, int64_t C, int64_t lds,
+                        void* dst, int64_t ldd, int64_t R_pad, const int64_t* count,
+                        void* stream);
 
 /* ---------------------------------------------------------------------- */
 /* ClippedPG loss epilogue                                                  */
@@ -782,16 +795,19 @@ int mirl_unpack_rows_bwd(const float* grad_out, int64_t n_seq, int64_t cols,
 /* ---------------------------------------------------------------------- */
 
 /*
- * out[b, s] = mask[b, s] != 0 ? logprobs[b, s] : 0 over [B, S] fp32 views with
- * element strides (a stride of 0 broadcasts); out may alias logprobs.
+ * out[b, s] = mask[b, s] != 0 ? logprobs[b, s] : 0 over [B, S] views with
+ * element strides (a stride of 0 broadcasts); logprobs and out are of `dtype`
+ * (F32, BF16, F16 or F64; the selected values are copied bit for bit), the mask
+ * is fp32; out may alias logprobs.  The same call with the upstream gradient in
+ * place of the logprobs is the selection's backward.
  *
  * Replaces: mask_filtered_logprobs_outside_tokens
  * (nemo_rl/algorithms/utils.py:309-326), applied after the filtered logprobs
  * by the Megatron logprob post-processor (nemo_rl/models/megatron/train.py:960-964).
  */
-int mirl_mask_outside_tokens(const float* logprobs, int64_t B, int64_t S, int64_t lp_sb,
-                             int64_t lp_ss, const float* mask, int64_t m_sb, int64_t m_ss,
-                             float* out, int64_t o_sb, int64_t o_ss, void* stream);
+int mirl_mask_outside_tokens(const void* logprobs, int dtype, int64_t B, int64_t S,
+                             int64_t lp_sb, int64_t lp_ss, const float* mask, int64_t m_sb,
+                             int64_t m_ss, void* out, int64_t o_sb, int64_t o_ss, void* stream);
 
 /*
  * Per sequence b of [B, S] fp32 views (element strides), w_s = token_mask[b, s]

@@ -5,11 +5,15 @@ nemo_rl/algorithms/logits_sampling_utils.py:69-212 (the filter),
 nemo_rl/distributed/model_utils.py:352-479 (DistributedLogprobWithSampling at
 TP=1) and nemo_rl/models/automodel/train.py:248-262 (in-place temperature).
 
-One deliberate difference: the ascending sort is stable (ties ordered by
-vocabulary index), which is what the reference's GPU sort does; CPU
-torch.sort is unstable, so the CPU reference's choice among tokens tied at
-the top-p boundary is arbitrary.  The top-k set (all ties at the k-th value
-kept) does not depend on tie order.
+Two points follow the reference as it runs on the GPU rather than CPU torch:
+- the ascending sort is stable (ties ordered by vocabulary index), which is
+  what the reference's GPU sort does; CPU torch.sort is unstable, so the CPU
+  reference's choice among tokens tied at the top-p boundary is arbitrary.
+  The top-k set (all ties at the k-th value kept) does not depend on tie order;
+- the in-place temperature ``logits.div_(T)`` is the product with
+  ``fl32(1.0 / T)`` that torch's GPU division by a Python scalar computes
+  (forward and autograd backward), not CPU torch's exact quotient
+  (``temperature_recip``).
 """
 
 from __future__ import annotations
@@ -19,11 +23,22 @@ from typing import Optional
 import torch
 
 
+def temperature_recip(temperature: float) -> torch.Tensor:
+    """fl32(1.0 / T) as a 0-d fp32 tensor (the quotient formed in double, rounded once).
+
+    The reference divides its logits by a Python float on the GPU, where torch
+    evaluates ``x.div_(T)`` as ``x * fl32(1.0 / T)`` in fp32 and its autograd
+    backward as ``g * fl32(1.0 / T)``; CPU torch divides exactly instead, so the
+    oracle writes the product out."""
+    return torch.tensor(1.0 / temperature, dtype=torch.float32)
+
+
 def apply_temperature(logits: torch.Tensor, temperature: float) -> torch.Tensor:
-    """logits.div_(T) in the logits dtype (reference automodel/train.py:248-262)."""
+    """logits.div_(T) in the logits dtype as the reference runs it on the GPU
+    (automodel/train.py:248-262): dtype(fl32(float(x) * fl32(1.0 / T)))."""
     if temperature == 1.0:
         return logits.clone()
-    return logits.clone().div_(temperature)
+    return (logits.float() * temperature_recip(temperature)).to(logits.dtype)
 
 
 def top_k_only(logits: torch.Tensor, top_k: int):
@@ -107,7 +122,8 @@ def filtered_logprobs_grad(logits: torch.Tensor, target: torch.Tensor, top_k, to
 
 def next_token_filtered(logits_raw, input_ids, top_k, top_p, temperature=1.0, grad_output=None):
     """The full production chain for one microbatch (reference get_next_token_logprobs_from_logits,
-    model_utils.py:1660-1718, no-group path): in-place temperature in the logits dtype, fp32
+    model_utils.py:1660-1718, no-group path): in-place temperature in the logits dtype (as
+    torch runs it on the GPU, see temperature_recip), fp32
     upcast, drop the last position, filter, log_softmax, gather input_ids[:, 1:].
 
     Returns (logprobs [B, S-1] fp32, keep [B, S-1, V] or None, grad w.r.t. the raw logits in the
@@ -115,9 +131,12 @@ def next_token_filtered(logits_raw, input_ids, top_k, top_p, temperature=1.0, gr
     then the division by T in the logits dtype.
     """
     x = logits_raw.clone().requires_grad_(grad_output is not None)
-    # the logits-dtype division (fp32 quotient rounded to the dtype) and its
-    # backward (the gradient divided by T in the logits dtype)
-    y = x / temperature if temperature != 1.0 else x * 1
+    # the logits-dtype division as a product with fl32(1.0 / T), rounded to the
+    # dtype, and through autograd its backward, dtype(fl32(float(g) * fl32(1.0 / T)))
+    if temperature != 1.0:
+        y = (x.float() * temperature_recip(temperature)).to(x.dtype)
+    else:
+        y = x * 1
     yf = y.to(torch.float32)[:, :-1]
     with torch.no_grad():
         _, keep = top_k_top_p(yf.detach(), top_k, top_p)

@@ -211,20 +211,21 @@ SIGNATURES = {
     "mirl_linear_ce_workspace_elems": (_I64, [_I64, _I64]),
     "mirl_linear_ce_fwd": (
         _I,
-        [_P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _I64,
-         _P, _P, _P],
+        [_P, _I, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64,
+         _I64, _P, _P, _P],
     ),
     "mirl_linear_ce_grad": (
         _I,
-        [_P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _I64, _P, _P, _I64,
-         _I64, _I64, _I64, _P, _I64, _P, _I64, _P, _P],
+        [_P, _I, _I64, _I64, _I64, _P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _I64, _P, _P,
+         _I64, _I64, _I64, _I64, _P, _I64, _P, _I64, _P, _P],
     ),
     "mirl_gemm_bf16_abt": (
-        _I, [_P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _I, _P, _I64, _P, _I64, _I,
+        _I, [_P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _I, _P, _I64, _I, _P, _I64, _I,
              _I64, _P]
     ),
-    "mirl_sum_splits_bf16": (_I, [_P, _I64, _I64, _I64, _I64, _P, _I64, _P, _I64, _P, _I64, _P]),
-    "mirl_transpose_bf16": (_I, [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _P]),
+    "mirl_sum_splits_bf16": (_I, [_P, _I64, _I64, _I64, _I64, _P, _I64, _I, _P, _I64, _P, _I64,
+                                  _P]),
+    "mirl_transpose_bf16": (_I, [_P, _I, _I64, _I64, _I64, _P, _I64, _I64, _P, _P]),
     "mirl_top_k_top_p_mask": (
         _I,
         [_P, _I, _I64, _I64, _I64, _I, ctypes.c_double, _I, _P, _P, _P, _P, _I64, _P, _I64, _P],
@@ -234,7 +235,7 @@ SIGNATURES = {
         [_P, _I64, _I64, _I64, ctypes.c_int32, _P, _P, _I64, _P, _I64, _P],
     ),
     "mirl_packed_roll_targets": (_I, [_P, _I64, _P, _I64, _P, _P]),
-    "mirl_mask_outside_tokens": (_I, [_P, _I64, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P]),
+    "mirl_mask_outside_tokens": (_I, [_P, _I, _I64, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P]),
     "mirl_seq_logprob_errors": (
         _I, [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _I64, _P, _P, _P]
     ),
@@ -1013,9 +1014,9 @@ def filtered_bwd(
     grad_temperature: float = 1.0,
     top_k: int = 0,
 ) -> None:
-    """``grad_temperature`` != 1 divides the written gradient by it last (in the
-    dtype): the backward of an in-place division of the logits made before the
-    forward, folded into this write.  ``top_k`` is the forward's; it picks the
+    """``grad_temperature`` != 1 applies the backward of an in-place division of the
+    logits by it, made before the forward, to the written gradient last (the product
+    with ``fl32(1.0 / grad_temperature)`` in the dtype), folded into this write.  ``top_k`` is the forward's; it picks the
     kernel schedule only (rows with kept lists for 1 <= top_k <= 1024)."""
     dev = _require_gpu(logits, target, grad_out, grad_in)
     B, R = target.shape
@@ -1056,7 +1057,8 @@ def _rows3(t: torch.Tensor):
 
 
 def temperature_scale_(logits: torch.Tensor, temperature: float) -> torch.Tensor:
-    """In place: logits = dtype(float(logits) / T) (mirl_temperature_scale)."""
+    """In place: logits = dtype(fl32(float(logits) * fl32(1.0 / T))), torch's GPU
+    ``div_`` by a Python scalar (mirl_temperature_scale)."""
     dev = _require_gpu(logits)
     B, R, V, sb, sr = _rows3(logits)
     st = _launch("mirl_temperature_scale", dev, logits.data_ptr(), _dtype_code(logits), B, R, V,
@@ -1067,7 +1069,8 @@ def temperature_scale_(logits: torch.Tensor, temperature: float) -> torch.Tensor
 
 def temperature_scale_grad(grad: torch.Tensor, grad2: Optional[torch.Tensor],
                            temperature: float) -> torch.Tensor:
-    """dtype(float(grad [+ grad2, accumulated in the dtype]) / T) as a new tensor."""
+    """dtype(fl32(float(grad [+ grad2, accumulated in the dtype]) * fl32(1.0 / T))) as a new
+    tensor: the autograd backward of the in-place division."""
     dev = _require_gpu(grad, grad2)
     if grad2 is not None:
         _require(grad2.shape == grad.shape and grad2.dtype == grad.dtype, "grad2 matches grad")
@@ -1112,11 +1115,14 @@ def top_k_top_p_mask(x2d: torch.Tensor, top_k: int, top_p: float,
 # ---------------------------------------------------------------------------
 # logprobs from hidden states (fused LM-head GEMM + log-sum-exp)
 # ---------------------------------------------------------------------------
+_LCE_DTYPES = (torch.bfloat16, torch.float16)
+
+
 def _check_linear_ce(hidden2d: torch.Tensor, weight: torch.Tensor) -> None:
-    if hidden2d.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+    if hidden2d.dtype not in _LCE_DTYPES or weight.dtype != hidden2d.dtype:
         raise NotImplementedError(
-            "logprobs from hidden states run on bf16 hidden states and weight "
-            f"(got {hidden2d.dtype} and {weight.dtype})"
+            "the fused hidden-state kernels take bf16 or fp16 hidden states and weight of one "
+            f"dtype (got {hidden2d.dtype} and {weight.dtype})"
         )
     if hidden2d.stride(-1) != 1 or weight.stride(-1) != 1:
         raise MirlError("hidden states and weight need a unit stride on the hidden dimension")
@@ -1132,10 +1138,11 @@ def linear_ce_fwd(
     out: torch.Tensor,
     stats: Optional[torch.Tensor],
 ) -> None:
-    """out[b, s] = log_softmax(bf16(hidden2d[s*bsz+b] . weight^T))[target[b, s] - vocab_start].
+    """out[b, s] = log_softmax(dtype(hidden2d[s*bsz+b] . weight^T))[target[b, s] - vocab_start].
 
-    hidden2d: [T, H] bf16 rows (row r is position (r // bsz, r % bsz)); weight:
-    [V, H] bf16; target: [B, S] int64; out: [B, S] fp32; stats: [T, 2] fp32 or None.
+    hidden2d: [T, H] bf16 or fp16 rows (row r is position (r // bsz, r % bsz)); weight:
+    [V, H] of the same dtype; target: [B, S] int64; out: [B, S] fp32; stats: [T, 2] fp32
+    or None.
     """
     dev = _require_gpu(hidden2d, weight, target, out, stats)
     _check_linear_ce(hidden2d, weight)
@@ -1147,7 +1154,7 @@ def linear_ce_fwd(
     ws = torch.empty(max(1, int(lib.mirl_linear_ce_workspace_elems(T, V))), dtype=torch.float32, device=dev)
     st = _launch(
         "mirl_linear_ce_fwd", dev,
-        hidden2d.data_ptr(), T, H, hidden2d.stride(0), weight.data_ptr(), V, weight.stride(0),
+        hidden2d.data_ptr(), _dtype_code(hidden2d), T, H, hidden2d.stride(0), weight.data_ptr(), V, weight.stride(0),
         int(bsz), target.data_ptr(), target.stride(0), target.stride(1), int(vocab_start),
         int(vocab_end), out.data_ptr(), out.stride(0), out.stride(1), _ptr(stats), ws.data_ptr(),
         _stream(dev),
@@ -1169,7 +1176,8 @@ def linear_ce_grad(
     grad_logits_t: Optional[torch.Tensor] = None,
     count: Optional[torch.Tensor] = None,
 ) -> None:
-    """grad_logits[i, :] = bf16((onehot(t) - softmax(logits)) * g) for rows row0 .. row0 + n - 1;
+    """grad_logits[i, :] = bf16((onehot(t) - softmax(logits)) * g) for rows row0 .. row0 + n - 1
+    (bf16 for either operand dtype);
     grad_logits_t (or None) receives the transpose [V, >= round_up(n, 256)].  `count` (a
     device int64 tensor of one element, or None): rows at or past it are absent."""
     dev = _require_gpu(hidden2d, weight, target, stats, grad_out, grad_logits)
@@ -1182,7 +1190,7 @@ def linear_ce_grad(
     _require(grad_logits.stride(-1) == 1, "grad_logits.stride(-1) == 1")
     st = _launch(
         "mirl_linear_ce_grad", dev,
-        hidden2d.data_ptr(), T, H, hidden2d.stride(0), weight.data_ptr(), V, weight.stride(0),
+        hidden2d.data_ptr(), _dtype_code(hidden2d), T, H, hidden2d.stride(0), weight.data_ptr(), V, weight.stride(0),
         int(bsz), target.data_ptr(), target.stride(0), target.stride(1), int(vocab_start),
         int(vocab_end), stats.data_ptr(), grad_out.data_ptr(), grad_out.stride(0),
         grad_out.stride(1), int(row0), int(n), grad_logits.data_ptr(), grad_logits.stride(0),
@@ -1210,33 +1218,36 @@ def gemm_bf16_abt(a: torch.Tensor, b: torch.Tensor, k: int, out: torch.Tensor, k
     """out = a[:, :k] . b[:, :k]^T with fp32 accumulation on the MFMA units.
 
     a [M, >=k], b [N, >=k] bf16 (unit stride, rows multiples of 8 elements, k a
-    multiple of 128); out bf16 [M, N] (k_splits 1, no accumulation), fp32 [M, N]
+    multiple of 128); out bf16 or fp16 [M, N] (k_splits 1, no accumulation), fp32 [M, N]
     (out = or +=), or fp32 [k_splits, M, N] (one partial product per k range).
     `count` (device int64, one element) with c = count - count_off: COUNT_ROWS
     leaves rows of a at or past c absent; COUNT_K stops the reduction at
-    round_up(c, 128), and with `out_bf16` (out fp32 [M, N]) the result goes to
-    out_bf16 = bf16(product (+ out when accumulate)) when count <= final_at, to
-    out otherwise."""
+    round_up(c, 128), and with `out_bf16` (a bf16 or fp16 [M, N] tensor, out fp32 [M, N])
+    the result goes to out_bf16 = its dtype(product (+ out when accumulate)) when
+    count <= final_at, to out otherwise."""
     dev = _require_gpu(a, b, out)
     _check_count(count, dev)
     _require(a.dtype == torch.bfloat16 and b.dtype == torch.bfloat16, "bf16 operands")
     _require(a.stride(-1) == 1 and b.stride(-1) == 1 and out.stride(-1) == 1, "unit stride on the last dim")
     M, N = a.shape[0], b.shape[0]
-    if out.dtype == torch.bfloat16:
+    cb_dtype = 1
+    if out.dtype in _LCE_DTYPES:
         _require(out_bf16 is None, "out_bf16 goes with an fp32 out")
         cb, ldcb, c, ldc = out.data_ptr(), out.stride(0), None, 0
+        cb_dtype = _dtype_code(out)
     else:
-        _require(out.dtype == torch.float32, "out is bf16 or fp32")
+        _require(out.dtype == torch.float32, "out is bf16, fp16 or fp32")
         cb, ldcb, c, ldc = None, 0, out.data_ptr(), out.stride(-2)
         if out_bf16 is not None:
-            _require(out_bf16.dtype == torch.bfloat16 and out_bf16.device == dev
+            _require(out_bf16.dtype in _LCE_DTYPES and out_bf16.device == dev
                      and out_bf16.stride(-1) == 1 and tuple(out_bf16.shape) == (M, N),
                      "out_bf16 is a bf16 [M, N] tensor with unit stride on the last dim")
             _require(out.dim() == 2 and tuple(out.shape) == (M, N), "out is fp32 [M, N]")
             cb, ldcb = out_bf16.data_ptr(), out_bf16.stride(0)
+            cb_dtype = _dtype_code(out_bf16)
     st = _launch(
         "mirl_gemm_bf16_abt", dev, a.data_ptr(), a.stride(0), b.data_ptr(), b.stride(0), M, N,
-        int(k), int(k_splits), c, ldc, int(bool(accumulate)), cb, ldcb, _ptr(count),
+        int(k), int(k_splits), c, ldc, int(bool(accumulate)), cb, ldcb, cb_dtype, _ptr(count),
         int(count_off), int(count_axis), int(final_at), _stream(dev),
     )
     _check(st, "mirl_gemm_bf16_abt")
@@ -1244,16 +1255,16 @@ def gemm_bf16_abt(a: torch.Tensor, b: torch.Tensor, k: int, out: torch.Tensor, k
 
 def sum_splits_bf16(part: torch.Tensor, out: torch.Tensor, count: Optional[torch.Tensor] = None,
                     count_off: int = 0, out_rows: Optional[torch.Tensor] = None) -> None:
-    """out [M, N] bf16 = sum over dim 0 of part [S, M, N] fp32, in order; with `count`,
+    """out [M, N] bf16 or fp16 = sum over dim 0 of part [S, M, N] fp32, in order; with `count`,
     rows at or past count - count_off are zeros (part not read there).  With `out_rows`
     (int64 [M] on the device) row m goes to out[out_rows[m]] instead (out [R, N], rows
     mapped outside [0, R) skipped)."""
     dev = _require_gpu(part, out)
     _check_count(count, dev)
     S, M, N = part.shape
-    _require(part.is_contiguous() and part.dtype == torch.float32 and out.dtype == torch.bfloat16
+    _require(part.is_contiguous() and part.dtype == torch.float32 and out.dtype in _LCE_DTYPES
              and out.stride(-1) == 1 and out.dim() == 2 and out.shape[1] == N,
-             "contiguous fp32 partials and a bf16 [R, N] output")
+             "contiguous fp32 partials and a bf16 or fp16 [R, N] output")
     if out_rows is None:
         _require(out.shape[0] == M, "out has the partials' rows")
     else:
@@ -1261,23 +1272,24 @@ def sum_splits_bf16(part: torch.Tensor, out: torch.Tensor, count: Optional[torch
                  and out_rows.shape[0] == M and out_rows.is_contiguous(),
                  "out_rows is a contiguous int64 [M] tensor on the device")
     st = _launch("mirl_sum_splits_bf16", dev, part.data_ptr(), S, M, N, N, out.data_ptr(),
-                 out.stride(0), _ptr(out_rows), out.shape[0], _ptr(count), int(count_off),
+                 out.stride(0), _dtype_code(out), _ptr(out_rows), out.shape[0], _ptr(count), int(count_off),
                  _stream(dev))
     _check(st, "mirl_sum_splits_bf16")
 
 
 def transpose_bf16(src: torch.Tensor, rows: int, dst: torch.Tensor,
                    count: Optional[torch.Tensor] = None) -> None:
-    """dst[c, r] = src[r, c] for r < rows, zero for rows <= r < dst.shape[1]; rows is
-    lowered to `count` (device int64, one element) when that is given."""
+    """dst[c, r] = bf16(src[r, c]) for r < rows, zero for rows <= r < dst.shape[1] (src
+    bf16 or fp16, dst bf16); rows is lowered to `count` (device int64, one element) when
+    that is given."""
     dev = _require_gpu(src, dst)
     _check_count(count, dev)
-    _require(src.dtype == torch.bfloat16 and dst.dtype == torch.bfloat16, "bf16 tensors")
+    _require(src.dtype in _LCE_DTYPES and dst.dtype == torch.bfloat16, "bf16 or fp16 source, bf16 destination")
     _require(src.stride(-1) == 1 and dst.stride(-1) == 1, "unit stride on the last dim")
     C = src.shape[1]
     _require(dst.shape[0] >= C, "dst has a row per source column")
     _require(src.shape[0] >= rows, "src has the rows to transpose")
-    st = _launch("mirl_transpose_bf16", dev, src.data_ptr(), int(rows), C, src.stride(0),
+    st = _launch("mirl_transpose_bf16", dev, src.data_ptr(), _dtype_code(src), int(rows), C, src.stride(0),
                  dst.data_ptr(), dst.stride(0), dst.shape[1], _ptr(count), _stream(dev))
     _check(st, "mirl_transpose_bf16")
 
@@ -1290,21 +1302,20 @@ def _as_f32(t: torch.Tensor) -> torch.Tensor:
 
 
 def mask_outside_tokens(logprobs: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
-    """where(mask != 0, logprobs, 0) for [B, S] (or [S]) fp32 logprobs and a mask that
-    broadcasts to them; returns a new fp32 tensor."""
+    """where(mask != 0, logprobs, 0) for [B, S] (or [S]) logprobs of any float dtype and a
+    mask that broadcasts to them; returns a new tensor of the logprobs' dtype."""
     dev = _require_gpu(logprobs, mask)
-    _require(logprobs.dtype == torch.float32, "logprobs.dtype == torch.float32")
     _require(logprobs.dim() in (1, 2), "logprobs of shape [B, S] or [S]")
     lp = logprobs if logprobs.dim() == 2 else logprobs.unsqueeze(0)
     m = _as_f32(mask)
     m = m if m.dim() == 2 else m.reshape((1,) * (2 - m.dim()) + tuple(m.shape))
     m = m.expand(lp.shape)
-    out = torch.empty(lp.shape, dtype=torch.float32, device=dev)
+    out = torch.empty(lp.shape, dtype=lp.dtype, device=dev)
     B, S = lp.shape
     st = _launch(
-        "mirl_mask_outside_tokens", dev, lp.data_ptr(), B, S, lp.stride(0), lp.stride(1),
-        m.data_ptr(), m.stride(0), m.stride(1), out.data_ptr(), out.stride(0), out.stride(1),
-        _stream(dev),
+        "mirl_mask_outside_tokens", dev, lp.data_ptr(), _dtype_code(lp), B, S, lp.stride(0),
+        lp.stride(1), m.data_ptr(), m.stride(0), m.stride(1), out.data_ptr(), out.stride(0),
+        out.stride(1), _stream(dev),
     )
     _check(st, "mirl_mask_outside_tokens")
     return out if logprobs.dim() == 2 else out[0]

@@ -89,13 +89,15 @@ def apply_temperature_scaling(
     (reference nemo_rl/models/automodel/train.py:248-262,
     nemo_rl/models/megatron/train.py:280-294); a no-op for None or T == 1.
 
-    The division runs on the gfx950 temperature kernel (fp32 quotient rounded
-    to the logits dtype, as ``div_`` rounds it) and is recorded for autograd;
-    its backward is the same division of the gradient.  When the filtered
-    logprobs of this package are the only consumer of the scaled logits, that
-    division is folded into their backward's write.  A gradient requested for
-    the scaled tensor itself (``autograd.grad`` with it as an input, or
-    ``retain_grad``) then sees no contribution from those logprobs.
+    The division runs on the gfx950 temperature kernel with the arithmetic of
+    torch's GPU ``div_`` by a Python scalar (the product with ``fl32(1.0 / T)``,
+    rounded to the logits dtype) and is recorded for autograd; its backward is
+    the same product applied to the gradient.  When the filtered logprobs of
+    this package are the only consumer of the scaled logits, that backward is
+    folded into their own gradient write, unless the scaled tensor retains its
+    gradient (``retain_grad``).  A caller that asks ``autograd.grad`` for the
+    scaled tensor itself turns the fold off first
+    (``rl_amd.distributed.sampling.set_temperature_fold(False)``).
     """
     if need_temperature_scaling(sampling_params):
         from rl_amd.distributed.sampling import temperature_scale_

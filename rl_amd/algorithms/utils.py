@@ -10,7 +10,7 @@ and ``compute_seq_logprob_errors`` run token-level kernels (seq_errors.hip).
 
 from __future__ import annotations
 
-from typing import Optional
+from typing import Any, Optional
 
 import torch
 
@@ -64,16 +64,32 @@ def masked_mean(
     return torch.sum(values * mask, dim=dim) / (normalization_factor + 1e-8)
 
 
+class _MaskOutsideTokens(torch.autograd.Function):
+    """where(mask, logprobs, 0) on the select kernel; backward where(mask, g, 0) on the same."""
+
+    @staticmethod
+    def forward(ctx: Any, logprobs: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:  # type: ignore[override]
+        ctx.save_for_backward(mask)
+        return _C.mask_outside_tokens(logprobs, mask)
+
+    @staticmethod
+    def backward(ctx: Any, grad: torch.Tensor):  # type: ignore[override]
+        (mask,) = ctx.saved_tensors
+        return _C.mask_outside_tokens(grad, mask), None
+
+
 def mask_filtered_logprobs_outside_tokens(logprobs: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
     """Zero filtered logprobs outside ``mask`` (reference utils.py:309-326).
 
     ``where(mask.bool(), logprobs, 0.0)``: tokens outside the valid-token mask
     (prompt, padding) get 0 instead of the -inf the filter may have given them;
-    valid tokens keep -inf.  Returns a new tensor of ``logprobs``' dtype (16-bit
-    logprobs are widened to fp32 for the kernel and narrowed back, exactly).
+    valid tokens keep -inf.  Returns a new tensor of ``logprobs``' dtype (the
+    kernel copies the selected values bit for bit, so fp64 stays exact) and keeps
+    autograd: the gradient is ``where(mask, g, 0)``, as for the reference's ``where``.
     """
-    out = _C.mask_outside_tokens(logprobs.to(torch.float32), mask)
-    return out if logprobs.dtype == torch.float32 else out.to(logprobs.dtype)
+    if torch.is_grad_enabled() and logprobs.requires_grad:
+        return _MaskOutsideTokens.apply(logprobs, mask)
+    return _C.mask_outside_tokens(logprobs, mask)
 
 
 @torch.no_grad()

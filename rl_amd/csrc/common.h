@@ -42,6 +42,26 @@ constexpr int kWave = 64;
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// The reference's in-place temperature, logits.div_(T), runs on the GPU, where
+// torch divides a tensor by a Python scalar as a product with the reciprocal
+// formed in double and rounded once to fp32: y = dtype(fl32(float(x) * r)),
+// r = fl32(1.0 / T); autograd's backward of that division does the same to the
+// gradient.  The host forms r with temperature_recip.
+inline float temperature_recip(double T) { return (float)(1.0 / T); }
+
+// fl32(x * r) as a product rounded on its own: contraction is off in this
+// scope, so the multiply is never fused with an add that consumes it, and the
+// empty asm makes the fp32 product opaque, so that a narrowing to fp16 that
+// follows rounds that product (two roundings, as torch's vectorised kernel
+// does) instead of being folded with the multiply into one mixed-precision
+// instruction that rounds the exact product once.
+__device__ __forceinline__ float mul_rn(float x, float r) {
+#pragma clang fp contract(off)
+  float p = x * r;
+  asm("" : "+v"(p));
+  return p;
+}
+
 // Element loaders: raw storage type -> fp32.
 struct F32 {
   using raw = float;

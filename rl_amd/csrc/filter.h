@@ -35,7 +35,7 @@ struct FilterParams {
   int64_t R, V, sb, sr;
   const int64_t* target;  // [B, R] view or null
   int64_t tsb, tsr;
-  float T;
+  float rT;   // temperature_recip(T): y = dtype(fl32(float(x) * rT))
   int has_t;
   int top_k;  // 0: no top-k
   int has_p;
@@ -71,10 +71,10 @@ __device__ __forceinline__ bool kept_lex(float y, int64_t j, float vc, int32_t i
   return y > vc || (y == vc && j >= (int64_t)ic);
 }
 
-// y = dtype(float(x) / T)
+// y = dtype(fl32(float(x) * rT)), the logits after the in-place temperature
 template <class E>
 __device__ __forceinline__ float scaled(float xf, const FilterParams& P) {
-  return P.has_t ? round_trip<E>(__fdiv_rn(xf, P.T)) : xf;
+  return P.has_t ? round_trip<E>(mul_rn(xf, P.rT)) : xf;
 }
 
 // Workgroup reductions over NT threads; `red` holds NT / 64 values.

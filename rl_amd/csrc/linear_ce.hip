@@ -40,8 +40,36 @@
 namespace mirl {
 namespace {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// Operand dtype of the logits GEMM (bf16 or fp16): the 32x32x16 MFMA and its
+// 8-element fragment.  The two instructions share one lane layout.
+template <class E>
+struct Mma;
+template <>
+struct Mma<BF16> {
+  typedef __bf16 frag __attribute__((ext_vector_type(8)));
+  __device__ __forceinline__ static f32x16 run(frag a, frag b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct Mma<F16> {
+  typedef _Float16 frag __attribute__((ext_vector_type(8)));
+  __device__ __forceinline__ static f32x16 run(frag a, frag b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+// 16-bit element bits <-> fp32 for a dtype E (round to nearest even).
+template <class E>
+__device__ __forceinline__ uint16_t bits_of(float f) {
+  return __builtin_bit_cast(uint16_t, E::from_float(f));
+}
+template <class E>
+__device__ __forceinline__ float value_of(uint16_t b) {
+  return E::load_raw(__builtin_bit_cast(typename E::raw, b));
+}
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 constexpr int kBM = 256;                 // rows per tile
@@ -90,15 +118,11 @@ __device__ __forceinline__ void wait_vm_barrier() {
   asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
-__device__ __forceinline__ float bf16_round(float f) {
-  return __uint_as_float((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f) << 16);
-}
-
 enum LceMode { kFwd = 0, kGrad = 1, kGemm = 2 };
 
 struct LceParams {
-  const uint16_t* h;  // [T, Hd] bf16, row stride ldh
-  const uint16_t* w;  // [V, Hd] bf16, row stride ldw
+  const uint16_t* h;  // [T, Hd] bf16 or fp16 (the kernel's E), row stride ldh
+  const uint16_t* w;  // [V, Hd] of the same dtype, row stride ldw
   int64_t ldh, ldw;
   int64_t V, Hd;
   int64_t row0, nrows;  // rows handled: [row0, row0 + nrows)
@@ -123,7 +147,8 @@ struct LceParams {
   // partial products [n_ks][nrows][ldc]), or Cb receives bf16(C) (n_ks = 1)
   int64_t n_ks, kb_len;
   float* C;
-  uint16_t* Cb;
+  uint16_t* Cb;        // bf16 output, fp16 with cb_f16
+  int cb_f16;
   int64_t ldc, ldcb;
   int accumulate;       // C += A . B^T instead of C = A . B^T (n_ks = 1)
   // device count (or null): c = *count - count_off.  kFwd/kGrad and count_axis
@@ -137,9 +162,10 @@ struct LceParams {
   int64_t final_at;
 };
 
-template <int MODE>
+template <int MODE, class E>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void lce_tile_kernel(LceParams P) {
+  using frag = typename Mma<E>::frag;
   // Two arrays rather than one, so that the compiler tracks the direct loads
   // into each stage on their own and an LDS read waits only for its stage.
   __shared__ __align__(1024) unsigned char st0[kStageBytes];
@@ -275,7 +301,7 @@ void lce_tile_kernel(LceParams P) {
       if (row >= row_end || col >= P.V) continue;
       if (to_bf16) {
         const float o = (P.accumulate && P.C != nullptr) ? P.C[row * P.ldc + col] : 0.f;
-        P.Cb[row * P.ldcb + col] = BF16::from_float(o);
+        P.Cb[row * P.ldcb + col] = P.cb_f16 ? bits_of<F16>(o) : bits_of<BF16>(o);
       } else if (!P.accumulate) {
         P.C[(ks * P.nrows + row) * P.ldc + col] = 0.f;
       }
@@ -318,13 +344,13 @@ void lce_tile_kernel(LceParams P) {
   int frag_off[kSK / 16];
 #pragma unroll
   for (int kk = 0; kk < kSK / 16; ++kk) frag_off[kk] = lds_off(frow, kk * 2 + (lane >> 5));
-  bf16x8 fa[2][kTM], fb[2][kTN];
+  frag fa[2][kTM], fb[2][kTN];
   auto fread = [&](int set, const unsigned char* stage, int kk, int idx) {
     // idx < kTM: A fragment idx; else B fragment idx - kTM
     if (idx < kTM)
-      fa[set][idx] = *reinterpret_cast<const bf16x8*>(stage + (wm * kWM + idx * 32) * kRowBytes + frag_off[kk]);
+      fa[set][idx] = *reinterpret_cast<const frag*>(stage + (wm * kWM + idx * 32) * kRowBytes + frag_off[kk]);
     else
-      fb[set][idx - kTM] = *reinterpret_cast<const bf16x8*>(
+      fb[set][idx - kTM] = *reinterpret_cast<const frag*>(
           stage + kHalfBytes + (wn * kWN + (idx - kTM) * 32) * kRowBytes + frag_off[kk]);
   };
 
@@ -337,7 +363,7 @@ void lce_tile_kernel(LceParams P) {
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
   auto mfma = [&](int set, int q) {
     const int i = q / kTN, j = q % kTN;
-    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[set][i], fb[set][j], acc[i][j], 0, 0, 0);
+    acc[i][j] = Mma<E>::run(fa[set][i], fb[set][j], acc[i][j]);
   };
 
   constexpr int kL = 2 * kDmaPerWave;  // direct loads per wave and stage
@@ -416,7 +442,8 @@ void lce_tile_kernel(LceParams P) {
           const int64_t col = n0 + wn * kWN + j * 32 + col_g;
           if (row >= row_end || col >= P.V) continue;
           if (to_bf16 && !via_c) {
-            P.Cb[row * P.ldcb + col] = BF16::from_float(acc[i][j][v]);
+            const float o = acc[i][j][v];
+            P.Cb[row * P.ldcb + col] = P.cb_f16 ? bits_of<F16>(o) : bits_of<BF16>(o);
           } else {
             float* c = P.C + (ks * P.nrows + row) * P.ldc + col;
             *c = P.accumulate ? *c + acc[i][j][v] : acc[i][j][v];
@@ -431,7 +458,10 @@ void lce_tile_kernel(LceParams P) {
           for (int v = 0; v < 16; ++v) {
             const int64_t row = m0 + wm * kWM + i * 32 + (v >> 2) * 8 + half_g * 4 + (v & 3);
             const int64_t col = n0 + wn * kWN + j * 32 + col_g;
-            if (row < row_end && col < P.V) P.Cb[row * P.ldcb + col] = BF16::from_float(P.C[row * P.ldc + col]);
+            if (row < row_end && col < P.V) {
+              const float o = P.C[row * P.ldc + col];
+              P.Cb[row * P.ldcb + col] = P.cb_f16 ? bits_of<F16>(o) : bits_of<BF16>(o);
+            }
           }
     }
     return;
@@ -461,7 +491,7 @@ void lce_tile_kernel(LceParams P) {
         for (int v = 0; v < 16; ++v) {
           const int rl = wm * kWM + i * 32 + (v >> 2) * 8 + half * 4 + (v & 3);
           const int cl = wn * kWN + j * 32 + col_lane;
-          xs[xs_index(rl, cl)] = BF16::from_float(acc[i][j][v]);
+          xs[xs_index(rl, cl)] = bits_of<E>(acc[i][j][v]);
         }
     }
     __syncthreads();
@@ -479,7 +509,7 @@ void lce_tile_kernel(LceParams P) {
         constexpr bool FULL = decltype(full_c)::value;
         for (int c = 0; c < kBN / 8; ++c) {
           float w[8];
-          BF16::unpack(rowp[c ^ sw], w);
+          E::unpack(rowp[c ^ sw], w);
 #pragma unroll
           for (int e = 0; e < 8; ++e)
             if (FULL || c * 8 + e < ncols) M = fmaxf(M, w[e]);
@@ -488,7 +518,7 @@ void lce_tile_kernel(LceParams P) {
           float s4[4] = {0.f, 0.f, 0.f, 0.f};
           for (int c = 0; c < kBN / 8; ++c) {
             float w[8];
-            BF16::unpack(rowp[c ^ sw], w);
+            E::unpack(rowp[c ^ sw], w);
 #pragma unroll
             for (int e = 0; e < 8; ++e)
               if (FULL || c * 8 + e < ncols) s4[e & 3] += fast_exp2((w[e] - M) * kLog2e);
@@ -504,7 +534,7 @@ void lce_tile_kernel(LceParams P) {
       dst[0] = M;
       dst[1] = sum;
       const int tc = s_tcol[tid];
-      if (tc >= 0) P.xt[r - P.row0] = BF16::load(xs + xs_index(tid, tc));
+      if (tc >= 0) P.xt[r - P.row0] = value_of<E>(xs[xs_index(tid, tc)]);
     }
   } else {
 #pragma unroll
@@ -518,10 +548,10 @@ void lce_tile_kernel(LceParams P) {
 #pragma unroll
         for (int j = 0; j < kTN; ++j) {
           const int cl = wn * kWN + j * 32 + col_lane;
-          const float x = bf16_round(acc[i][j][v]);
+          const float x = round_trip<E>(acc[i][j][v]);  // the logit in the operand dtype
           const float p = fast_exp2(((x - M) - LS) * kLog2e);
           const float o = (cl == tc) ? (1.f - p) * gv : -p * gv;
-          xs[xs_index(rl, cl)] = BF16::from_float(o);
+          xs[xs_index(rl, cl)] = bits_of<BF16>(o);  // G is bf16 for either operand dtype
         }
       }
     }
@@ -571,9 +601,10 @@ void lce_tile_kernel(LceParams P) {
   }
 }
 
-// dst[c][r] = src[r][c] for r < R, c < C, and dst[c][r] = 0 for R <= r < Rp
-// (bf16; dst rows of stride ldd >= Rp), R = min(R, *count) when count is
-// given.  64 x 64 tiles through LDS.
+// dst[c][r] = bf16(src[r][c]) for r < R, c < C, and dst[c][r] = 0 for
+// R <= r < Rp (src of dtype ES, bf16 or fp16; dst rows of stride ldd >= Rp),
+// R = min(R, *count) when count is given.  64 x 64 tiles through LDS.
+template <class ES>
 __global__ __launch_bounds__(256) void transpose_bf16_kernel(const uint16_t* __restrict__ src,
                                                              int64_t R, int64_t C, int64_t lds,
                                                              uint16_t* __restrict__ dst,
@@ -588,7 +619,9 @@ __global__ __launch_bounds__(256) void transpose_bf16_kernel(const uint16_t* __r
 #pragma unroll 4
   for (int k = 0; k < 16; ++k) {
     const int64_t r = r0 + ty + 4 * k, c = c0 + tx;
-    tile[ty + 4 * k][tx] = (r < R && c < C) ? src[r * lds + c] : (uint16_t)0;
+    uint16_t v = (r < R && c < C) ? src[r * lds + c] : (uint16_t)0;
+    if constexpr (std::is_same<ES, F16>::value) v = bits_of<BF16>(value_of<F16>(v));
+    tile[ty + 4 * k][tx] = v;
   }
   __syncthreads();
 #pragma unroll 4
@@ -598,12 +631,12 @@ __global__ __launch_bounds__(256) void transpose_bf16_kernel(const uint16_t* __r
   }
 }
 
-// out[r(m)][n] = bf16(sum over s of part[s][m][n]), summed in split order,
+// out[r(m)][n] = EO(sum over s of part[s][m][n]) (EO bf16 or fp16), summed in split order,
 // with r(m) = out_rows[m] when a row map is given (rows mapped outside
 // [0, out_nrows) are skipped) and m otherwise; with a count, rows
 // m >= *count - count_off are written as zeros without reading.  VEC
 // consecutive elements per thread (N and ld multiples of VEC).
-template <int VEC>
+template <int VEC, class EO>
 __global__ __launch_bounds__(256) void sum_splits_kernel(const float* __restrict__ part,
                                                          int64_t n_ks, int64_t M, int64_t N,
                                                          int64_t ld, uint16_t* __restrict__ out,
@@ -640,12 +673,12 @@ __global__ __launch_bounds__(256) void sum_splits_kernel(const float* __restrict
   }
   uint16_t* dst = out + r * ldo + n;
   if constexpr (VEC == 4) {
-    const uint32_t lo = (uint32_t)BF16::from_float(acc[0]) | ((uint32_t)BF16::from_float(acc[1]) << 16);
-    const uint32_t hi = (uint32_t)BF16::from_float(acc[2]) | ((uint32_t)BF16::from_float(acc[3]) << 16);
+    const uint32_t lo = (uint32_t)bits_of<EO>(acc[0]) | ((uint32_t)bits_of<EO>(acc[1]) << 16);
+    const uint32_t hi = (uint32_t)bits_of<EO>(acc[2]) | ((uint32_t)bits_of<EO>(acc[3]) << 16);
     *reinterpret_cast<uint2*>(dst) = uint2{lo, hi};
   } else {
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) dst[e] = BF16::from_float(acc[e]);
+    for (int e = 0; e < VEC; ++e) dst[e] = bits_of<EO>(acc[e]);
   }
 }
 
@@ -719,13 +752,17 @@ extern "C" int64_t mirl_linear_ce_workspace_elems(int64_t T, int64_t V) {
   return T * ceil_div(V, kBN) * 2 + T;
 }
 
-extern "C" int mirl_linear_ce_fwd(const void* hidden, int64_t T, int64_t Hd, int64_t ldh,
+static bool lce_dtype_ok(int dtype) { return dtype == MIRL_DTYPE_BF16 || dtype == MIRL_DTYPE_F16; }
+
+extern "C" int mirl_linear_ce_fwd(const void* hidden, int dtype, int64_t T, int64_t Hd, int64_t ldh,
                                   const void* weight, int64_t V, int64_t ldw, int64_t bsz,
                                   const int64_t* target, int64_t t_stride_b, int64_t t_stride_s,
                                   int64_t vocab_start, int64_t vocab_end, float* out,
                                   int64_t o_stride_b, int64_t o_stride_s, float* row_stats,
                                   float* workspace, void* stream) {
   clear_error();
+  MIRL_REQUIRE(lce_dtype_ok(dtype), "hidden states and weight must be bf16 or fp16 (dtype code %d)",
+               dtype);
   if (int e = check_common(hidden, T, Hd, ldh, weight, V, ldw, target, bsz)) return e;
   if (T == 0) return MIRL_OK;
   MIRL_REQUIRE(out && workspace, "null pointer argument");
@@ -751,14 +788,17 @@ extern "C" int mirl_linear_ce_fwd(const void* hidden, int64_t T, int64_t Hd, int
   P.xt = workspace + T * P.n_nt * 2;
   const int64_t grid = ceil_div(P.n_mt * P.n_nt, kXcds) * kXcds;
   MIRL_REQUIRE(grid < (int64_t(1) << 31), "too many tiles");
-  hipLaunchKernelGGL((lce_tile_kernel<kFwd>), dim3((unsigned)grid), dim3(kThreads), 0, st, P);
+  if (dtype == MIRL_DTYPE_BF16)
+    hipLaunchKernelGGL((lce_tile_kernel<kFwd, BF16>), dim3((unsigned)grid), dim3(kThreads), 0, st, P);
+  else
+    hipLaunchKernelGGL((lce_tile_kernel<kFwd, F16>), dim3((unsigned)grid), dim3(kThreads), 0, st, P);
   hipLaunchKernelGGL(lce_merge_kernel, dim3((unsigned)ceil_div(T, 4)), dim3(256), 0, st, P.part,
                      P.xt, (int64_t)0, T, P.n_nt, bsz, target, t_stride_b, t_stride_s,
                      vocab_start, vocab_end, V, out, o_stride_b, o_stride_s, row_stats);
   return check_launch("mirl_linear_ce_fwd");
 }
 
-extern "C" int mirl_linear_ce_grad(const void* hidden, int64_t T, int64_t Hd, int64_t ldh,
+extern "C" int mirl_linear_ce_grad(const void* hidden, int dtype, int64_t T, int64_t Hd, int64_t ldh,
                                    const void* weight, int64_t V, int64_t ldw, int64_t bsz,
                                    const int64_t* target, int64_t t_stride_b,
                                    int64_t t_stride_s, int64_t vocab_start, int64_t vocab_end,
@@ -768,6 +808,8 @@ extern "C" int mirl_linear_ce_grad(const void* hidden, int64_t T, int64_t Hd, in
                                    void* grad_logits_t, int64_t ldgt, const int64_t* row_count,
                                    void* stream) {
   clear_error();
+  MIRL_REQUIRE(lce_dtype_ok(dtype), "hidden states and weight must be bf16 or fp16 (dtype code %d)",
+               dtype);
   if (int e = check_common(hidden, T, Hd, ldh, weight, V, ldw, target, bsz)) return e;
   MIRL_REQUIRE(row0 >= 0 && nrows >= 0 && row0 + nrows <= T, "row range [%lld, %lld) outside [0, %lld)",
                (long long)row0, (long long)(row0 + nrows), (long long)T);
@@ -811,16 +853,21 @@ extern "C" int mirl_linear_ce_grad(const void* hidden, int64_t T, int64_t Hd, in
   P.count = row_count;
   const int64_t grid = ceil_div(P.n_mt * P.n_nt, kXcds) * kXcds;
   MIRL_REQUIRE(grid < (int64_t(1) << 31), "too many tiles");
-  hipLaunchKernelGGL((lce_tile_kernel<kGrad>), dim3((unsigned)grid), dim3(kThreads), 0, st, P);
+  if (dtype == MIRL_DTYPE_BF16)
+    hipLaunchKernelGGL((lce_tile_kernel<kGrad, BF16>), dim3((unsigned)grid), dim3(kThreads), 0, st, P);
+  else
+    hipLaunchKernelGGL((lce_tile_kernel<kGrad, F16>), dim3((unsigned)grid), dim3(kThreads), 0, st, P);
   return check_launch("mirl_linear_ce_grad");
 }
 
 extern "C" int mirl_gemm_bf16_abt(const void* A, int64_t lda, const void* B, int64_t ldb, int64_t M,
                                   int64_t N, int64_t K, int64_t k_splits, float* C, int64_t ldc,
-                                  int accumulate, void* Cb, int64_t ldcb, const int64_t* count,
-                                  int64_t count_off, int count_axis, int64_t final_at,
-                                  void* stream) {
+                                  int accumulate, void* Cb, int64_t ldcb, int cb_dtype,
+                                  const int64_t* count, int64_t count_off, int count_axis,
+                                  int64_t final_at, void* stream) {
   clear_error();
+  MIRL_REQUIRE(Cb == nullptr || lce_dtype_ok(cb_dtype), "the 16-bit output must be bf16 or fp16 (dtype code %d)",
+               cb_dtype);
   MIRL_REQUIRE(M >= 0 && N >= 0 && K > 0 && k_splits >= 1, "invalid shape M=%lld N=%lld K=%lld splits=%lld",
                (long long)M, (long long)N, (long long)K, (long long)k_splits);
   if (M == 0 || N == 0) return MIRL_OK;
@@ -870,6 +917,7 @@ extern "C" int mirl_gemm_bf16_abt(const void* A, int64_t lda, const void* B, int
   P.kb_len = kb;
   P.C = C;
   P.Cb = static_cast<uint16_t*>(Cb);
+  P.cb_f16 = cb_dtype == MIRL_DTYPE_F16;
   P.ldc = ldc;
   P.ldcb = ldcb;
   P.accumulate = accumulate;
@@ -879,16 +927,17 @@ extern "C" int mirl_gemm_bf16_abt(const void* A, int64_t lda, const void* B, int
   P.final_at = final_at;
   const int64_t grid = ceil_div(P.n_mt * P.n_nt * n_ks, kXcds) * kXcds;
   MIRL_REQUIRE(grid < (int64_t(1) << 31), "too many tiles");
-  hipLaunchKernelGGL((lce_tile_kernel<kGemm>), dim3((unsigned)grid), dim3(kThreads), 0,
+  hipLaunchKernelGGL((lce_tile_kernel<kGemm, BF16>), dim3((unsigned)grid), dim3(kThreads), 0,
                      static_cast<hipStream_t>(stream), P);
   return check_launch("mirl_gemm_bf16_abt");
 }
 
 extern "C" int mirl_sum_splits_bf16(const float* part, int64_t k_splits, int64_t M, int64_t N,
-                                    int64_t ld, void* out, int64_t ldo, const int64_t* out_rows,
-                                    int64_t out_nrows, const int64_t* count, int64_t count_off,
-                                    void* stream) {
+                                    int64_t ld, void* out, int64_t ldo, int out_dtype,
+                                    const int64_t* out_rows, int64_t out_nrows,
+                                    const int64_t* count, int64_t count_off, void* stream) {
   clear_error();
+  MIRL_REQUIRE(lce_dtype_ok(out_dtype), "the output must be bf16 or fp16 (dtype code %d)", out_dtype);
   MIRL_REQUIRE(M >= 0 && N >= 0 && k_splits >= 1 && ld >= N && ldo >= N, "invalid shape");
   if (M == 0 || N == 0) return MIRL_OK;
   MIRL_REQUIRE(part && out, "null pointer argument");
@@ -897,28 +946,39 @@ extern "C" int mirl_sum_splits_bf16(const float* part, int64_t k_splits, int64_t
   const bool vec4 = N % 4 == 0 && ld % 4 == 0 && ldo % 4 == 0 &&
                     (reinterpret_cast<uintptr_t>(part) & 15u) == 0 &&
                     (reinterpret_cast<uintptr_t>(out) & 7u) == 0;
-  if (vec4)
-    hipLaunchKernelGGL((sum_splits_kernel<4>), dim3((unsigned)ceil_div(M * N / 4, 256)), dim3(256), 0,
-                       st, part, k_splits, M, N, ld, static_cast<uint16_t*>(out), ldo, out_rows,
-                       out_nrows, count, count_off);
-  else
-    hipLaunchKernelGGL((sum_splits_kernel<1>), dim3((unsigned)ceil_div(M * N, 256)), dim3(256), 0,
-                       st, part, k_splits, M, N, ld, static_cast<uint16_t*>(out), ldo, out_rows,
-                       out_nrows, count, count_off);
+  auto launch = [&](auto vec_c, auto eo) {
+    constexpr int VEC = decltype(vec_c)::value;
+    using EO = decltype(eo);
+    hipLaunchKernelGGL((sum_splits_kernel<VEC, EO>), dim3((unsigned)ceil_div(M * N / VEC, 256)),
+                       dim3(256), 0, st, part, k_splits, M, N, ld, static_cast<uint16_t*>(out), ldo,
+                       out_rows, out_nrows, count, count_off);
+  };
+  using V4 = std::integral_constant<int, 4>;
+  using V1 = std::integral_constant<int, 1>;
+  if (out_dtype == MIRL_DTYPE_BF16) {
+    if (vec4) launch(V4{}, BF16{}); else launch(V1{}, BF16{});
+  } else {
+    if (vec4) launch(V4{}, F16{}); else launch(V1{}, F16{});
+  }
   return check_launch("mirl_sum_splits_bf16");
 }
 
-extern "C" int mirl_transpose_bf16(const void* src, int64_t R, int64_t C, int64_t lds, void* dst,
-                                   int64_t ldd, int64_t R_pad, const int64_t* count,
-                                   void* stream) {
+extern "C" int mirl_transpose_bf16(const void* src, int src_dtype, int64_t R, int64_t C,
+                                   int64_t lds, void* dst, int64_t ldd, int64_t R_pad,
+                                   const int64_t* count, void* stream) {
   clear_error();
+  MIRL_REQUIRE(lce_dtype_ok(src_dtype), "the source must be bf16 or fp16 (dtype code %d)", src_dtype);
   MIRL_REQUIRE(R >= 0 && C >= 0 && R_pad >= R && lds >= C && ldd >= R_pad, "invalid shape");
   if (C == 0 || R_pad == 0) return MIRL_OK;
   MIRL_REQUIRE(src && dst, "null pointer argument");
   const int64_t n_rt = ceil_div(R_pad, 64), n_ct = ceil_div(C, 64);
   MIRL_REQUIRE(n_rt * n_ct < (int64_t(1) << 31), "too many tiles");
-  hipLaunchKernelGGL(transpose_bf16_kernel, dim3((unsigned)(n_rt * n_ct)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(src), R, C,
-                     lds, static_cast<uint16_t*>(dst), ldd, R_pad, n_ct, count);
+  auto launch = [&](auto es) {
+    using ES = decltype(es);
+    hipLaunchKernelGGL((transpose_bf16_kernel<ES>), dim3((unsigned)(n_rt * n_ct)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(src), R, C,
+                       lds, static_cast<uint16_t*>(dst), ldd, R_pad, n_ct, count);
+  };
+  if (src_dtype == MIRL_DTYPE_BF16) launch(BF16{}); else launch(F16{});
   return check_launch("mirl_transpose_bf16");
 }

@@ -25,13 +25,17 @@ struct Strided2 {
   __device__ float at(int64_t b, int64_t s) const { return p[b * sb + s * ss]; }
 };
 
-__global__ __launch_bounds__(256) void mask_outside_kernel(Strided2 lp, Strided2 mask, float* out,
-                                                           int64_t osb, int64_t oss, int64_t S,
-                                                           int64_t n) {
+// out = mask != 0 ? logprobs : 0, element by element, for an element of W bytes
+// (the select copies the value's bits, so any float dtype of that width is exact;
+// all-zero bits are +0.0 in every float format).
+template <class W>
+__global__ __launch_bounds__(256) void mask_outside_kernel(const W* lp, int64_t lsb, int64_t lss,
+                                                           Strided2 mask, W* out, int64_t osb,
+                                                           int64_t oss, int64_t S, int64_t n) {
   const int64_t stride = (int64_t)gridDim.x * 256;
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) {
     const int64_t b = i / S, s = i - b * S;
-    out[b * osb + s * oss] = mask.at(b, s) != 0.f ? lp.at(b, s) : 0.f;
+    out[b * osb + s * oss] = mask.at(b, s) != 0.f ? lp[b * lsb + s * lss] : W(0);
   }
 }
 
@@ -69,18 +73,32 @@ int grid_for(int64_t n) {
 
 using namespace mirl;
 
-extern "C" int mirl_mask_outside_tokens(const float* logprobs, int64_t B, int64_t S, int64_t lp_sb,
-                                        int64_t lp_ss, const float* mask, int64_t m_sb,
-                                        int64_t m_ss, float* out, int64_t o_sb, int64_t o_ss,
-                                        void* stream) {
+extern "C" int mirl_mask_outside_tokens(const void* logprobs, int dtype, int64_t B, int64_t S,
+                                        int64_t lp_sb, int64_t lp_ss, const float* mask,
+                                        int64_t m_sb, int64_t m_ss, void* out, int64_t o_sb,
+                                        int64_t o_ss, void* stream) {
   clear_error();
   MIRL_REQUIRE(B >= 0 && S >= 0, "invalid shape B=%lld S=%lld", (long long)B, (long long)S);
+  MIRL_REQUIRE(dtype == MIRL_DTYPE_F32 || dtype == MIRL_DTYPE_BF16 || dtype == MIRL_DTYPE_F16 ||
+                   dtype == MIRL_DTYPE_F64,
+               "unsupported logprobs dtype code %d", dtype);
   const int64_t n = B * S;
   if (n == 0) return MIRL_OK;
   MIRL_REQUIRE(logprobs && mask && out, "null pointer argument");
-  hipLaunchKernelGGL(mask_outside_kernel, dim3(grid_for(n)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), Strided2{logprobs, lp_sb, lp_ss},
-                     Strided2{mask, m_sb, m_ss}, out, o_sb, o_ss, S, n);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const Strided2 m{mask, m_sb, m_ss};
+  if (dtype == MIRL_DTYPE_F32)
+    hipLaunchKernelGGL(mask_outside_kernel<uint32_t>, dim3(grid_for(n)), dim3(256), 0, st,
+                       static_cast<const uint32_t*>(logprobs), lp_sb, lp_ss, m,
+                       static_cast<uint32_t*>(out), o_sb, o_ss, S, n);
+  else if (dtype == MIRL_DTYPE_F64)
+    hipLaunchKernelGGL(mask_outside_kernel<uint64_t>, dim3(grid_for(n)), dim3(256), 0, st,
+                       static_cast<const uint64_t*>(logprobs), lp_sb, lp_ss, m,
+                       static_cast<uint64_t*>(out), o_sb, o_ss, S, n);
+  else
+    hipLaunchKernelGGL(mask_outside_kernel<uint16_t>, dim3(grid_for(n)), dim3(256), 0, st,
+                       static_cast<const uint16_t*>(logprobs), lp_sb, lp_ss, m,
+                       static_cast<uint16_t*>(out), o_sb, o_ss, S, n);
   return check_launch("mirl_mask_outside_tokens");
 }
 

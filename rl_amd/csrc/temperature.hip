@@ -2,11 +2,12 @@
 //
 // Semantics (reference nemo_rl/models/automodel/train.py:248-262 and
 // nemo_rl/models/megatron/train.py:280-294): logits.div_(T) in the logits
-// dtype, i.e. y = dtype(float(x) / float(T)) rounded to nearest even, and the
-// autograd backward of that division, grad_x = dtype(float(g) / float(T)).
-// When a second gradient is given, the two are first added in the dtype (the
-// autograd engine's accumulation of two consumers' gradients):
-// grad_x = dtype(float(dtype(float(g) + float(g2))) / float(T)).
+// dtype as torch runs it on the GPU, a product with the reciprocal formed in
+// double and rounded once, y = dtype(fl32(float(x) * r)) with r = fl32(1.0 / T)
+// (each rounding to nearest even), and the autograd backward of that division,
+// grad_x = dtype(fl32(float(g) * r)).  When a second gradient is given, the two
+// are first added in the dtype (the autograd engine's accumulation of two
+// consumers' gradients): grad_x = dtype(fl32(float(dtype(float(g) + float(g2))) * r)).
 //
 // Contiguous tensors are walked as one flat array of 16-byte vectors (a scalar
 // head up to the first 16-byte boundary and a scalar tail), with nontemporal
@@ -45,9 +46,9 @@ Pieces pieces_of(const void* base, int64_t n) {
   return Pieces{(nvec + shift + kPieceVecs - 1) / kPieceVecs, shift};
 }
 
-// x[i] <- dtype(float(x[i]) / T) over n contiguous elements.
+// x[i] <- dtype(fl32(float(x[i]) * r)) over n contiguous elements.
 template <class E>
-__global__ __launch_bounds__(kPieceThreads) void scale_flat_kernel(void* x, int64_t n, float T,
+__global__ __launch_bounds__(kPieceThreads) void scale_flat_kernel(void* x, int64_t n, float r,
                                                                    int shift) {
   using raw = typename E::raw;
   raw* p = static_cast<raw*>(x);
@@ -67,21 +68,21 @@ __global__ __launch_bounds__(kPieceThreads) void scale_flat_kernel(void* x, int6
     float w[E::kVec];
     E::unpack(q[u], w);
 #pragma unroll
-    for (int k = 0; k < E::kVec; ++k) w[k] = __fdiv_rn(w[k], T);
+    for (int k = 0; k < E::kVec; ++k) w[k] = mul_rn(w[k], r);
     __builtin_nontemporal_store(E::pack(w), pv + i);
   }
   if (blockIdx.x == 0) {
-    if (threadIdx.x < sp.head) p[threadIdx.x] = E::from_float(__fdiv_rn(E::load(p + threadIdx.x), T));
+    if (threadIdx.x < sp.head) p[threadIdx.x] = E::from_float(mul_rn(E::load(p + threadIdx.x), r));
     if (sp.tail0 + threadIdx.x < n)
-      p[sp.tail0 + threadIdx.x] = E::from_float(__fdiv_rn(E::load(p + sp.tail0 + threadIdx.x), T));
+      p[sp.tail0 + threadIdx.x] = E::from_float(mul_rn(E::load(p + sp.tail0 + threadIdx.x), r));
   }
 }
 
-// out[i] = dtype(float(dtype(float(g[i]) (+ float(g2[i])))) / T) over n
+// out[i] = dtype(fl32(float(dtype(float(g[i]) (+ float(g2[i])))) * r)) over n
 // contiguous elements; g, g2 and out share their offset from a 16-byte boundary.
 template <class E>
 __global__ __launch_bounds__(kPieceThreads) void scale_grad_flat_kernel(const void* g, const void* g2,
-                                                                        void* out, int64_t n, float T,
+                                                                        void* out, int64_t n, float r,
                                                                         int shift) {
   using raw = typename E::raw;
   const raw* a = static_cast<const raw*>(g);
@@ -93,7 +94,7 @@ __global__ __launch_bounds__(kPieceThreads) void scale_grad_flat_kernel(const vo
   vu4* ov = reinterpret_cast<vu4*>(o + sp.head);
   auto one = [&](float x, float y, bool two) {
     const float s = two ? round_trip<E>(x + y) : x;
-    return __fdiv_rn(s, T);
+    return mul_rn(s, r);
   };
   const bool two = b != nullptr;
   const int64_t base = (int64_t)blockIdx.x * kPieceVecs + threadIdx.x - shift;
@@ -135,7 +136,7 @@ struct Strided3 {
 template <class E>
 __global__ __launch_bounds__(256) void scale_rows_kernel(Strided3 x, const void* g2, int64_t g2_sb,
                                                          int64_t g2_sr, Strided3 out, int64_t R,
-                                                         int64_t V, int64_t total, float T,
+                                                         int64_t V, int64_t total, float rr,
                                                          int grad) {
   using raw = typename E::raw;
   const int64_t stride = (int64_t)gridDim.x * 256;
@@ -146,7 +147,7 @@ __global__ __launch_bounds__(256) void scale_rows_kernel(Strided3 x, const void*
     float s = E::load(src);
     if (grad && g2 != nullptr)
       s = round_trip<E>(s + E::load(static_cast<const raw*>(g2) + b * g2_sb + r * g2_sr + v));
-    static_cast<raw*>(out.p)[b * out.sb + r * out.sr + v] = E::from_float(__fdiv_rn(s, T));
+    static_cast<raw*>(out.p)[b * out.sb + r * out.sr + v] = E::from_float(mul_rn(s, rr));
   }
 }
 
@@ -160,17 +161,17 @@ bool contiguous(int64_t B, int64_t R, int64_t V, int64_t sb, int64_t sr) {
 }
 
 template <class E>
-int run_scale(void* x, int64_t B, int64_t R, int64_t V, int64_t sb, int64_t sr, float T,
+int run_scale(void* x, int64_t B, int64_t R, int64_t V, int64_t sb, int64_t sr, float r,
               hipStream_t st) {
   const int64_t n = B * R * V;
   if (contiguous(B, R, V, sb, sr)) {
     const Pieces pc = pieces_of<E>(x, n);
     hipLaunchKernelGGL((scale_flat_kernel<E>), dim3((unsigned)(pc.grid > 0 ? pc.grid : 1)),
-                       dim3(kPieceThreads), 0, st, x, n, T, pc.shift);
+                       dim3(kPieceThreads), 0, st, x, n, r, pc.shift);
   } else {
     const Strided3 s{x, sb, sr};
     hipLaunchKernelGGL((scale_rows_kernel<E>), dim3(grid_for(n)), dim3(256), 0, st, s, nullptr,
-                       int64_t(0), int64_t(0), s, R, V, n, T, 0);
+                       int64_t(0), int64_t(0), s, R, V, n, r, 0);
   }
   return check_launch("mirl_temperature_scale");
 }
@@ -178,7 +179,7 @@ int run_scale(void* x, int64_t B, int64_t R, int64_t V, int64_t sb, int64_t sr, 
 template <class E>
 int run_grad(const void* g, int64_t g_sb, int64_t g_sr, const void* g2, int64_t g2_sb,
              int64_t g2_sr, void* out, int64_t o_sb, int64_t o_sr, int64_t B, int64_t R, int64_t V,
-             float T, hipStream_t st) {
+             float r, hipStream_t st) {
   const int64_t n = B * R * V;
   const uintptr_t mis = (reinterpret_cast<uintptr_t>(g) & 15u);
   const bool flat = contiguous(B, R, V, g_sb, g_sr) && contiguous(B, R, V, o_sb, o_sr) &&
@@ -188,12 +189,12 @@ int run_grad(const void* g, int64_t g_sb, int64_t g_sr, const void* g2, int64_t 
   if (flat) {
     const Pieces pc = pieces_of<E>(g, n);
     hipLaunchKernelGGL((scale_grad_flat_kernel<E>), dim3((unsigned)(pc.grid > 0 ? pc.grid : 1)),
-                       dim3(kPieceThreads), 0, st, g, g2, out, n, T, pc.shift);
+                       dim3(kPieceThreads), 0, st, g, g2, out, n, r, pc.shift);
   } else {
     const Strided3 a{const_cast<void*>(g), g_sb, g_sr};
     const Strided3 o{out, o_sb, o_sr};
     hipLaunchKernelGGL((scale_rows_kernel<E>), dim3(grid_for(n)), dim3(256), 0, st, a, g2, g2_sb,
-                       g2_sr, o, R, V, n, T, 1);
+                       g2_sr, o, R, V, n, r, 1);
   }
   return check_launch("mirl_temperature_scale_grad");
 }
@@ -221,11 +222,11 @@ extern "C" int mirl_temperature_scale(void* logits, int dtype, int64_t B, int64_
   if (int e = check_args(dtype, B, R, V, temperature)) return e;
   if (B * R * V == 0) return MIRL_OK;
   MIRL_REQUIRE(logits != nullptr, "null pointer argument");
-  const float T = (float)temperature;
+  const float r = temperature_recip(temperature);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (dtype == MIRL_DTYPE_F32) return run_scale<F32>(logits, B, R, V, stride_b, stride_r, T, st);
-  if (dtype == MIRL_DTYPE_BF16) return run_scale<BF16>(logits, B, R, V, stride_b, stride_r, T, st);
-  return run_scale<F16>(logits, B, R, V, stride_b, stride_r, T, st);
+  if (dtype == MIRL_DTYPE_F32) return run_scale<F32>(logits, B, R, V, stride_b, stride_r, r, st);
+  if (dtype == MIRL_DTYPE_BF16) return run_scale<BF16>(logits, B, R, V, stride_b, stride_r, r, st);
+  return run_scale<F16>(logits, B, R, V, stride_b, stride_r, r, st);
 }
 
 extern "C" int mirl_temperature_scale_grad(const void* grad, int dtype, int64_t B, int64_t R,
@@ -237,14 +238,14 @@ extern "C" int mirl_temperature_scale_grad(const void* grad, int dtype, int64_t 
   if (int e = check_args(dtype, B, R, V, temperature)) return e;
   if (B * R * V == 0) return MIRL_OK;
   MIRL_REQUIRE(grad != nullptr && out != nullptr, "null pointer argument");
-  const float T = (float)temperature;
+  const float r = temperature_recip(temperature);
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == MIRL_DTYPE_F32)
     return run_grad<F32>(grad, g_stride_b, g_stride_r, grad2, g2_stride_b, g2_stride_r, out,
-                         o_stride_b, o_stride_r, B, R, V, T, st);
+                         o_stride_b, o_stride_r, B, R, V, r, st);
   if (dtype == MIRL_DTYPE_BF16)
     return run_grad<BF16>(grad, g_stride_b, g_stride_r, grad2, g2_stride_b, g2_stride_r, out,
-                          o_stride_b, o_stride_r, B, R, V, T, st);
+                          o_stride_b, o_stride_r, B, R, V, r, st);
   return run_grad<F16>(grad, g_stride_b, g_stride_r, grad2, g2_stride_b, g2_stride_r, out,
-                       o_stride_b, o_stride_r, B, R, V, T, st);
+                       o_stride_b, o_stride_r, B, R, V, r, st);
 }

@@ -2,8 +2,9 @@
 //
 // Semantics (reference nemo_rl/algorithms/logits_sampling_utils.py:69-212 and
 // nemo_rl/distributed/model_utils.py:352-479, in the production chain of
-// model_utils.py:1660-1718): y = dtype(float(x) / T) — the in-place division
-// of automodel/train.py:248-262, skipped when T == 1 — read as fp32;
+// model_utils.py:1660-1718): y = dtype(fl32(float(x) * fl32(1.0 / T))) — the
+// in-place division of automodel/train.py:248-262 as torch runs it on the GPU
+// (a product with the rounded reciprocal), skipped when T == 1 — read as fp32;
 //   top-k: keep y >= the k-th largest y (every tie at the k-th value kept);
 //   top-p: over the kept-k values in ascending order with ties ordered by
 //          vocabulary index (a stable sort), p = softmax, cum = cumulative sum
@@ -31,8 +32,9 @@
 // for each 8-bit digit.
 //
 // Backward: grad = (onehot(t) - p) * g on the kept set, 0 elsewhere, rounded
-// to the logits dtype, then divided by T in that dtype (the reference's
-// autograd chain through .to(float32) and div_).  A write-only pass zeroes the
+// to the logits dtype, then multiplied by fl32(1.0 / T) and rounded to that
+// dtype again (the reference's autograd chain through .to(float32) and div_,
+// as torch runs it on the GPU).  A write-only pass zeroes the
 // rows; a second, small pass stores the kept entries from the kept list saved
 // by the forward (<= kKeepCap entries), without reading the logits.  Rows with
 // larger kept sets are re-read and rewritten whole by the second pass.
@@ -831,9 +833,9 @@ struct FilterBwdParams {
   int64_t R, Rt, V, sb, sr;
   const int64_t* target;
   int64_t tsb, tsr;
-  float T;
+  float rT;   // temperature_recip of the fused temperature
   int has_t;
-  float GT;   // the gradient is divided by GT in the dtype last (an earlier in-place division)
+  float rGT;  // temperature_recip of an earlier in-place division, applied to the gradient last
   int has_gt;
   int zero_rows;  // phase 2 zeroes the rows it does not rewrite (no phase 1)
   const RowInfo* info;
@@ -848,12 +850,13 @@ struct FilterBwdParams {
 template <class E>
 __device__ __forceinline__ typename E::raw grad_to_dtype(float g32, const FilterBwdParams& P) {
   if (!P.has_t && !P.has_gt) return E::from_float(g32);
-  // dtype(g) then / T in the dtype (round, divide in fp32, round again), then
-  // / GT in the dtype: the backward of the fused temperature and of an
-  // in-place division applied to the logits before this call
+  // dtype(g), then the backward of the fused temperature (fl32 product with
+  // rT, rounded to the dtype), then that of an in-place division applied to
+  // the logits before this call (the same with rGT): autograd's chain of the
+  // fp32 upcast and the two divisions as torch runs them on the GPU
   float r = round_trip<E>(g32);
-  if (P.has_t) r = round_trip<E>(__fdiv_rn(r, P.T));
-  if (P.has_gt) r = round_trip<E>(__fdiv_rn(r, P.GT));
+  if (P.has_t) r = round_trip<E>(mul_rn(r, P.rT));
+  if (P.has_gt) r = round_trip<E>(mul_rn(r, P.rGT));
   return E::from_float(r);
 }
 
@@ -895,41 +898,12 @@ __global__ __launch_bounds__(64 * W) void filter_bwd_zero_rows_kernel(FilterBwdP
   if (ys.tail0 + threadIdx.x < P.V) y[ys.tail0 + threadIdx.x] = zr;
 }
 
-// Markstein's correction of the product with the rounded reciprocal
-// r = RN(1/d): q0 = x r, e = x - q0 d (exact by the fma), q = q0 + e r.  For
-// dividends of a 16-bit dtype (at most 11 significant bits) with |x| in
-// [2^-100, 2^100] or x = 0, and d in [2^-10, 2^10], q is the correctly rounded
-// fp32 quotient x / d; every finite bf16 and fp16 dividend against 20,000
-// divisors spread over [2^-10, 2^10], and divisors with all-ones and
-// power-of-two significands, gave __fdiv_rn's result bit for bit.
-__device__ __forceinline__ float div_corrected(float x, float d, float r) {
-  const float q0 = x * r;
-  const float e = __builtin_fmaf(-q0, d, x);
-  return __builtin_fmaf(e, r, q0);
-}
-
 // How the whole-row walk narrows an fp32 gradient to the dtype.
 enum GradConv {
-  kConvPlain = 0,   // no temperature: round to the dtype
-  kConvExact = 1,   // grad_to_dtype (correctly rounded divisions)
-  kConvFastGT = 2,  // 16-bit dtype, an earlier in-place division by GT only, row checked by fast_div_row
+  kConvPlain = 0,  // no temperature: round to the dtype
+  kConvOne = 1,    // one temperature (fused or earlier in place): round, product, round
+  kConvTwo = 2,    // both: grad_to_dtype
 };
-
-// Whether every gradient the walk of this row divides by GT stays inside the
-// range where div_corrected is exact: GT in [2^-10, 2^10], the upstream
-// gradient at most 2^60 in magnitude, and every kept non-target element's
-// gradient p * |g| at least 2^-60 (p >= p(v_cut) for kept elements; the
-// factor 2 asked of p(v_cut) covers the difference between the two ways p is
-// evaluated).  The target element goes through grad_to_dtype on its own.
-// Elements outside the kept set are exact zeros.
-__device__ __forceinline__ bool fast_div_row(const FilterBwdParams& P, const RowInfo& ri, float gv) {
-  const float a = fabsf(P.GT);
-  if (!(a >= 0x1p-10f && a <= 0x1p10f)) return false;
-  const float ag = fabsf(gv);
-  if (!(ag <= 0x1p60f)) return false;
-  const float pc = fast_exp2(((ri.v_cut - ri.m) - ri.logsum) * kLog2e);
-  return ag * pc >= 0x1p-59f;
-}
 
 // Per-row arithmetic of the whole-row walks below: the kept test of elements
 // equal to v_cut, the probability of a kept element and the gradient narrowed
@@ -939,7 +913,7 @@ struct WalkMath {
   using raw = typename E::raw;
   const FilterBwdParams& P;
   const RowInfo& ri;
-  float gv, ngv, c, rgt, vc;
+  float gv, ngv, c, rone, vc;
   int64_t t;
   bool rank_form;
   uint32_t rcut;
@@ -955,9 +929,9 @@ struct WalkMath {
     // dtype's resolution), for fp32 gradients from the differences
     c = (ri.m + ri.logsum) * kLog2e;
     ngv = -gv;
-    rgt = CONV == kConvFastGT ? __frcp_rn(P.GT) : 1.f;
+    rone = P.has_t ? P.rT : P.rGT;
   }
-  __device__ float yval(float xf) const { return P.has_t ? round_trip<E>(__fdiv_rn(xf, P.T)) : xf; }
+  __device__ float yval(float xf) const { return P.has_t ? round_trip<E>(mul_rn(xf, P.rT)) : xf; }
   __device__ float prob(float yy) const {
     if constexpr (std::is_same<E, F32>::value)
       return fast_exp2(((yy - ri.m) - ri.logsum) * kLog2e);
@@ -968,8 +942,8 @@ struct WalkMath {
   __device__ raw narrow(float g32) const {
     if constexpr (CONV == kConvPlain) {
       return E::from_float(g32);
-    } else if constexpr (CONV == kConvFastGT) {
-      return E::from_float(div_corrected(round_trip<E>(g32), P.GT, rgt));
+    } else if constexpr (CONV == kConvOne) {
+      return E::from_float(mul_rn(round_trip<E>(g32), rone));
     } else {
       return grad_to_dtype<E>(g32, P);
     }
@@ -980,14 +954,14 @@ struct WalkMath {
     float g[E::kVec];
 #pragma unroll
     for (int k = 0; k < E::kVec; ++k) g[k] = kept(k) ? prob(w[k]) * ngv : 0.f;
-    if constexpr (CONV == kConvFastGT) {
-      // round to the dtype two at a time, divide, round again
+    if constexpr (CONV == kConvOne) {
+      // round to the dtype two at a time, multiply, round again
 #pragma unroll
       for (int k = 0; k < E::kVec; k += 2) {
         float a = g[k], b = g[k + 1];
         round_trip2<E>(a, b);
-        a = div_corrected(a, P.GT, rgt);
-        b = div_corrected(b, P.GT, rgt);
+        a = mul_rn(a, rone);
+        b = mul_rn(b, rone);
         vals[k] = E::from_float(a);
         vals[k + 1] = E::from_float(b);
       }
@@ -1340,10 +1314,8 @@ __device__ __forceinline__ void walk_row_block(const FilterBwdParams& P, const R
 // kept-list cap): one kRowThreads workgroup per row writes the whole row, as
 // zeros (rows past R and rows with a zero upstream gradient) or by the walk.
 // (two workgroups per CU: 6 waves per SIMD).  KIND
-// picks the conversions the launch needs (kRowPlain: none; kRowGT: an earlier
-// in-place division only; kRowExact: the rest), so that each kernel holds the
-// walks it uses and no more.
-enum RowKind { kRowPlain = 0, kRowGT = 1, kRowExact = 2 };
+// is the GradConv of the launch (the temperatures it applies to the gradient),
+// so that each kernel holds the walk it uses and no more.
 template <class E, int KIND>
 __global__ __launch_bounds__(kRowThreads, 6) void filter_bwd_row_kernel(FilterBwdParams P) {
   using raw = typename E::raw;
@@ -1370,17 +1342,7 @@ __global__ __launch_bounds__(kRowThreads, 6) void filter_bwd_row_kernel(FilterBw
   const RowInfo ri = P.info[srow];
   const int64_t t = P.target[b * P.tsb + r * P.tsr];
   const raw* x = static_cast<const raw*>(P.logits) + b * P.sb + r * P.sr;
-  if constexpr (KIND == kRowPlain) {
-    walk_row_block<E, kConvPlain>(P, ri, x, y, gv, t, s_cnt);
-  } else {
-    if constexpr (KIND == kRowGT && !std::is_same<E, F32>::value) {
-      if (fast_div_row(P, ri, gv)) {
-        walk_row_block<E, kConvFastGT>(P, ri, x, y, gv, t, s_cnt);
-        return;
-      }
-    }
-    walk_row_block<E, kConvExact>(P, ri, x, y, gv, t, s_cnt);
-  }
+  walk_row_block<E, KIND>(P, ri, x, y, gv, t, s_cnt);
 }
 
 // Phase 2, one wave per row with a non-zero upstream gradient: with the saved
@@ -1430,16 +1392,12 @@ __global__ __launch_bounds__(256) void filter_bwd_scatter_kernel(FilterBwdParams
 
   // Whole row: re-read the logits and re-apply the cut.
   const raw* x = static_cast<const raw*>(P.logits) + b * P.sb + r * P.sr;
-  if constexpr (!std::is_same<E, F32>::value) {
-    if (!P.has_t && P.has_gt && fast_div_row(P, ri, gv)) {
-      walk_row<E, kConvFastGT>(P, ri, x, y, gv, t, lane);
-      return;
-    }
-  }
   if (!P.has_t && !P.has_gt)
     walk_row<E, kConvPlain>(P, ri, x, y, gv, t, lane);
+  else if (!P.has_t || !P.has_gt)
+    walk_row<E, kConvOne>(P, ri, x, y, gv, t, lane);
   else
-    walk_row<E, kConvExact>(P, ri, x, y, gv, t, lane);
+    walk_row<E, kConvTwo>(P, ri, x, y, gv, t, lane);
 }
 
 // filtered logits (-inf outside the kept set) and the keep mask
@@ -1534,13 +1492,13 @@ int launch_bwd(const FilterBwdParams& P, int64_t B, int64_t rows, hipStream_t st
     // rows without kept lists: each row written once, by a workgroup of its own
     if (rows == 0) return MIRL_OK;
     if (!P.has_t && !P.has_gt)
-      hipLaunchKernelGGL((filter_bwd_row_kernel<E, kRowPlain>), dim3((unsigned)rows), dim3(kRowThreads),
+      hipLaunchKernelGGL((filter_bwd_row_kernel<E, kConvPlain>), dim3((unsigned)rows), dim3(kRowThreads),
                          0, st, P);
-    else if (!P.has_t)
-      hipLaunchKernelGGL((filter_bwd_row_kernel<E, kRowGT>), dim3((unsigned)rows), dim3(kRowThreads), 0,
+    else if (!P.has_t || !P.has_gt)
+      hipLaunchKernelGGL((filter_bwd_row_kernel<E, kConvOne>), dim3((unsigned)rows), dim3(kRowThreads), 0,
                          st, P);
     else
-      hipLaunchKernelGGL((filter_bwd_row_kernel<E, kRowExact>), dim3((unsigned)rows), dim3(kRowThreads),
+      hipLaunchKernelGGL((filter_bwd_row_kernel<E, kConvTwo>), dim3((unsigned)rows), dim3(kRowThreads),
                          0, st, P);
     return check_launch("filter_bwd_row_kernel");
   }
@@ -1616,7 +1574,7 @@ FilterParams make_params(const void* logits, int64_t R, int64_t V, int64_t sb, i
   P.target = target;
   P.tsb = tsb;
   P.tsr = tsr;
-  P.T = (float)temperature;
+  P.rT = temperature_recip(temperature);
   P.has_t = temperature != 1.0;
   P.top_k = top_k > 0 ? top_k : 0;
   P.has_p = top_p < 1.0;
@@ -1695,9 +1653,9 @@ extern "C" int mirl_filtered_logprob_bwd(const void* logits, int dtype, int64_t 
   P.target = target;
   P.tsb = t_stride_b;
   P.tsr = t_stride_r;
-  P.T = (float)temperature;
+  P.rT = temperature_recip(temperature);
   P.has_t = temperature != 1.0;
-  P.GT = (float)grad_temperature;
+  P.rGT = temperature_recip(grad_temperature);
   P.has_gt = grad_temperature != 1.0;
   P.info = static_cast<const RowInfo*>(row_info);
   P.kept_idx = kept_idx;

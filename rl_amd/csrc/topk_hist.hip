@@ -10,7 +10,7 @@
 // One 1024-thread workgroup per row reads the row with 16-byte nontemporal
 // loads.  Every raw value is counted into a table of 65536 16-bit counts in
 // LDS (128 KB), indexed by an order-preserving key of the raw bits; the values
-// that occur are the table's non-empty entries, and the value y = dtype(x / T)
+// that occur are the table's non-empty entries, and the value y = dtype(x * rT)
 // of an entry is computed from its key.  So the top-k value, the normaliser,
 // the cumulative probability in ascending order and the kept set's
 // log-sum-exp all follow from the table:
@@ -906,7 +906,7 @@ __global__ __launch_bounds__(kHT) void filter_hist_kernel(FilterParams P, int al
 // ---------------------------------------------------------------------------
 // Compact form: the occupied keys as an entry list
 // ---------------------------------------------------------------------------
-// The table phases above evaluate y = dtype(x / T) and exp(y - m) per occupied
+// The table phases above evaluate y = dtype(x * rT) and exp(y - m) per occupied
 // key, several times, and a thread owns 64 consecutive keys, so the occupied
 // keys (a few thousand of the 65536) crowd into a few waves.  This kernel
 // counts the row the same way, then lists the occupied keys in ascending

@@ -7,9 +7,9 @@ size 1.  Hidden states are Megatron's sequence-first ``[S, B, H]``; the weight
 is ``[V, H]``; targets are ``[B, S]``.
 
 * forward: one gfx950 kernel forms each 256 x 256 logits tile on the MFMA units
-  (bf16 inputs, fp32 accumulation, rounded to bf16 as the reference's bf16
-  matmul output is) and reduces it to per-row partial log-sum-exps and the
-  target logit; a merge kernel finishes each row.  The ``[S*B, V]`` logits are
+  (bf16 or fp16 inputs, fp32 accumulation, rounded to the input dtype as the
+  reference's matmul output is) and reduces it to per-row partial log-sum-exps
+  and the target logit; a merge kernel finishes each row.  The ``[S*B, V]`` logits are
   never materialised (the reference materialises an fp32 copy per chunk).
 * backward: the rows with a non-zero upstream gradient are moved to the front
   (the others have a zero logits gradient: zero dH rows, nothing added to dW)
@@ -17,16 +17,23 @@ is ``[V, H]``; targets are ``[B, S]``.
   synchronisation); per block of up to ``4 * chunk_size * B`` rows a kernel recomputes the logits
   tiles and writes ``G = (onehot - softmax) * g`` in bf16 and its transpose, and
   ``dH = G . W`` and ``dW += G^T . H`` run on the same MFMA tile loop
-  (``mirl_gemm_bf16_abt``) against transposed copies of W (kept while the weight
-  is unchanged) and of the active hidden rows, with fp32 accumulation (``dW``
-  accumulated in fp32 across blocks and rounded once, by the kernel itself
-  when there is one block; the reference adds each chunk into a bf16 buffer).
-* fp16 and fp32 hidden states and weights take the reference's chunked shape
-  instead: per chunk of sequence positions the logits are one library GEMM in
-  the input dtype (the reference's ``torch.matmul`` output), and the row
-  kernels of the logits path (``mirl_logprob_fwd`` / ``mirl_logprob_bwd``)
-  form the logprobs and, in place, the logits gradient; ``dH`` and ``dW`` are
-  library GEMMs over it, ``dW`` accumulated in fp32 across chunks.
+  (``mirl_gemm_bf16_abt``) against bf16 transposed copies of W (formed in every
+  backward) and of the active hidden rows, with fp32 accumulation (``dW``
+  accumulated in fp32 across blocks and rounded once to the weight's dtype, by
+  the kernel itself when there is one block; the reference adds each chunk into
+  a buffer of the weight's dtype).  G is bf16 for fp16 inputs too: fp16's
+  exponent range would flush the small ``-p * g`` terms of the vocabulary's
+  tail, which together make up most of ``dH``; the transposes round fp16 W and
+  H to bf16 for those two products.
+* fp32 hidden states and weights take the reference's chunked shape instead:
+  per chunk of sequence positions the logits are one library GEMM in fp32 (the
+  reference's ``torch.matmul`` output), and the row kernels of the logits path
+  (``mirl_logprob_fwd`` / ``mirl_logprob_bwd``) form the logprobs and, in
+  place, the logits gradient; ``dH`` and ``dW`` are library GEMMs over it,
+  ``dW`` accumulated in fp32 across chunks.  An fp32 GEMM here is bound by the
+  fp32 MFMA rate (1/16 of bf16's) at over a thousand flops per byte of logits,
+  so the per-chunk logits write and read that fusion would save cost under 1%
+  of the step.
 """
 
 from __future__ import annotations
@@ -84,7 +91,7 @@ class ChunkedDistributedHiddenStatesToLogprobs(torch.autograd.Function):
             weight = weight.contiguous()
         if target.dtype != torch.int64:
             target = target.long()
-        if hidden.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        if hidden.dtype not in _FUSED_DTYPES or weight.dtype != hidden.dtype:
             return _chunked_forward(ctx, hidden, target, weight, vocab_start_index, vocab_end_index,
                                     chunk_size, inference_only)
         ctx.chunked = False
@@ -154,7 +161,7 @@ class ChunkedDistributedHiddenStatesToLogprobs(torch.autograd.Function):
         dH = torch.empty((T, H), dtype=hidden.dtype, device=dev) if need_h else None
         hk_a, wk = _kernel_operand(h_a), _kernel_operand(weight)
         if need_w:
-            dW = torch.empty((V, H), dtype=torch.bfloat16, device=dev)
+            dW = torch.empty((V, H), dtype=weight.dtype, device=dev)
             # fp32 across blocks, rounded once by the last block with active rows
             # (allocated, never touched, when that is the first)
             dW32 = torch.empty((V, H), dtype=torch.float32, device=dev) if n_blocks > 1 else None
@@ -192,7 +199,7 @@ def _chunks(S: int, chunk_size: Optional[int]) -> list[tuple[int, int]]:
 
 
 def _chunked_forward(ctx, hidden, target, weight, vs, ve, chunk_size, inference_only):
-    """fp16 / fp32: per chunk of positions, logits = hidden[c] . weight^T in the input
+    """fp32 (or mixed dtypes): per chunk of positions, logits = hidden[c] . weight^T in the input
     dtype (one library GEMM, [c, B, V]), then the logprob row kernel over them viewed
     as [B, c, V] (reference model_utils.py:2608-2630)."""
     S, B, H = hidden.shape
@@ -217,7 +224,7 @@ def _chunked_forward(ctx, hidden, target, weight, vs, ve, chunk_size, inference_
 
 
 def _chunked_backward(ctx, grad_output):
-    """fp16 / fp32 backward (reference model_utils.py:2647-2745): per chunk the logits
+    """fp32 backward (reference model_utils.py:2647-2745): per chunk the logits
     are recomputed by the library GEMM and the logprob backward kernel overwrites them
     with (onehot - softmax) * g in the input dtype; dH = G . W per chunk and
     dW = sum over chunks of G^T . H, accumulated in fp32."""
@@ -251,13 +258,14 @@ def _chunked_backward(ctx, grad_output):
     return dH, None, grad_w, None, None, None, None, None
 
 
+_FUSED_DTYPES = (torch.bfloat16, torch.float16)  # operand dtypes of the fused kernels
 _BLOCK_CHUNKS = 4  # chunks of active rows per backward block
 _K_ALIGN = 128  # dW's reduction length is padded with zero rows to a multiple of this
 _H_ALIGN = 128  # the fused kernels step through the hidden dimension 128 elements at a time
 
 
 def _kernel_operand(x: torch.Tensor) -> torch.Tensor:
-    """``x [N, H]`` (bf16) as the fused kernels read it: ``H`` a multiple of 128, a row
+    """``x [N, H]`` (bf16 or fp16) as the fused kernels read it: ``H`` a multiple of 128, a row
     stride that is a multiple of 8 elements (16 bytes) and a 16-byte-aligned start.
 
     Other operands (small models' hidden sizes such as 64, sliced weights) are
@@ -313,22 +321,16 @@ def _dh_splits(n: int, H: int, K: int, count_known: bool = True) -> int:
     return best
 
 
-_WT_CACHE: dict = {}
-
-
 def _weight_transposed(weight: torch.Tensor, Vp: int) -> torch.Tensor:
-    """W^T [H, Vp] bf16 (columns past V zero).  The last one is kept and reused while
-    the weight's storage, shape and version are unchanged (the backward of every
-    microbatch between two optimizer steps)."""
+    """W^T [H, Vp] bf16 (columns past V zero; an fp16 weight rounded), formed from the weight's current contents
+    in every backward (one read and one write of W, about 0.5 ms at [151936, 4096]).
+
+    Nothing is kept across calls: a weight can change without its version counter
+    moving (``p.data.copy_``, collectives writing into parameter storage), so a copy
+    reused by key could silently give dH from an old weight."""
     V, H = weight.shape
-    key = (weight.device, weight.data_ptr(), weight._version, V, H, weight.stride(0), Vp)
-    hit = _WT_CACHE.get("w")
-    if hit is not None and hit[0] == key:
-        return hit[1]
-    _WT_CACHE.clear()
     wT = torch.empty((H, Vp), dtype=torch.bfloat16, device=weight.device)
     _C.transpose_bf16(weight, V, wT)
-    _WT_CACHE["w"] = (key, wT)
     return wT
 
 

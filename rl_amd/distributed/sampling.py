@@ -8,7 +8,9 @@ Autograd Functions and helpers behind the filtered branches of
   (indices and probabilities) of each row are saved for the backward;
 * backward: the gradient row is written without reading the logits:
   ``(onehot - p) * g`` on the kept entries, zero elsewhere, rounded to the
-  logits dtype and, when a temperature was fused, divided by it in that dtype.
+  logits dtype and, when a temperature was fused, put through the backward of
+  that division in that dtype (a product with ``fl32(1.0 / T)``, as torch's GPU
+  ``div_`` and its autograd backward compute it).
 
 ``top_k`` follows the reference convention (None or <= 0 disables it) and so
 does ``top_p`` (1.0 disables it).  The temperature argument is an extension:
@@ -27,6 +29,7 @@ selects between the two (None = the logits dtype).
 
 from __future__ import annotations
 
+import weakref
 from typing import Any, Optional
 
 import torch
@@ -35,12 +38,15 @@ from rl_amd import _C
 
 
 class _TemperatureScale(torch.autograd.Function):
-    """``logits.div_(T)`` in place on the temperature kernel; backward ``dtype(g / T)``.
+    """``logits.div_(T)`` in place on the temperature kernel, as torch computes it on
+    the GPU: ``dtype(fl32(x * fl32(1.0 / T)))``; backward ``dtype(fl32(g * fl32(1.0 / T)))``.
 
     A filtered-logprob op that reads these logits folds the division into its
     own backward (the write of the raw-logits gradient) and hands that gradient
     over through ``prediv`` instead of returning it; with no other consumer this
-    node returns it unchanged.  If other consumers contributed a gradient as
+    node returns it unchanged.  The fold is skipped when the scaled logits retain
+    their gradient (``retain_grad``) or folding is switched off
+    (``set_temperature_fold``).  If other consumers contributed a gradient as
     well, the filtered gradient is recomputed undivided and accumulated with
     theirs in the dtype before the division, as autograd accumulates two
     consumers' gradients into the reference's division backward.
@@ -67,14 +73,33 @@ class _TemperatureScale(torch.autograd.Function):
 
 
 def temperature_scale_(logits: torch.Tensor, temperature: float) -> torch.Tensor:
-    """In-place ``dtype(float(logits) / T)``, recorded for autograd when the logits need it."""
+    """In-place ``logits.div_(T)`` (the product with ``fl32(1.0 / T)``), recorded for autograd
+    when the logits need it."""
     if torch.is_grad_enabled() and logits.requires_grad:
         return _TemperatureScale.apply(logits, temperature)
     return _C.temperature_scale_(logits, temperature)
 
 
+_FOLD = {"enabled": True}
+
+
+def set_temperature_fold(enabled: bool) -> None:
+    """Whether a filtered logprob op may fold the backward of an in-place temperature
+    ahead of it into its own gradient write (default on).
+
+    Folding saves one read and one write of the logits gradient, but the gradient
+    of the scaled logits themselves then never holds the filtered op's part: a
+    caller that takes ``autograd.grad`` with the scaled tensor as an input turns
+    folding off (``retain_grad`` on the scaled tensor is detected and needs nothing).
+    """
+    _FOLD["enabled"] = bool(enabled)
+
+
 def _temperature_node(logits: torch.Tensor):
-    """The _TemperatureScale node that produced ``logits``, if that is its history."""
+    """The _TemperatureScale node that produced ``logits``, if that is its history and
+    folding is on."""
+    if not _FOLD["enabled"]:
+        return None
     fn = logits.grad_fn
     if fn is not None and type(fn).__name__ == "_TemperatureScaleBackward":
         return fn
@@ -87,6 +112,10 @@ def _filtered_grad(ctx: Any, logits, target, temperature, info, kidx, kp, g):
     node ahead of it when that node has no gradient from another filtered op yet
     (then None is returned for autograd), else returned as usual."""
     node = getattr(ctx, "temperature_node", None)
+    ref = getattr(ctx, "logits_ref", None)
+    scaled = ref() if ref is not None else None
+    if scaled is not None and scaled.retains_grad:
+        node = None  # the scaled logits' own gradient must hold this op's part
     if node is not None and node.prediv is None:
         grad = torch.empty_like(logits)
         _C.filtered_bwd(logits, target, temperature, info, kidx, kp, g, grad,
@@ -139,6 +168,7 @@ class _FilteredRowLogprob(torch.autograd.Function):
             ctx.temperature = float(temperature)
             ctx.top_k = int(top_k)
             ctx.temperature_node = _temperature_node(logits)
+            ctx.logits_ref = weakref.ref(logits)
         return out
 
     @staticmethod
@@ -303,6 +333,7 @@ def _run_filtered(ctx, logits, target, top_k, top_p, inference_only):
         saved = (logits, target, info, kidx, kp)
         ctx.top_k = _k(top_k)
         ctx.temperature_node = _temperature_node(logits) if not inference_only else None
+        ctx.logits_ref = weakref.ref(logits)
     else:
         stats = torch.empty((B, S, 2), dtype=torch.float32, device=logits.device)
         _C.logprob_fwd(logits, target, 0, logits.shape[-1], out, stats)

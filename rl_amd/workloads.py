@@ -123,6 +123,11 @@ def long_context_bf16(B: int = 1, S: int = 32768, V: int = 131072, seed: int = 3
     return {"logits": logits, "input_ids": ids, "grad": grad}
 
 
+def _recip(temperature: float, dev) -> torch.Tensor:
+    """fl32(1.0 / T): the in-place temperature on the GPU multiplies by it."""
+    return torch.tensor(1.0 / temperature, dtype=torch.float32, device=dev)
+
+
 def topk_filter_bf16(
     B: int = 4,
     S: int = 4096,
@@ -146,7 +151,7 @@ def topk_filter_bf16(
     flat[rows, boost_idx.view(-1)] = (flat[rows, boost_idx.view(-1)].float() + 8.0).to(torch.bfloat16)
     # the kept set of each row (top-k, then the top-p nucleus over it), used only
     # to choose targets: 90% inside it, 10% outside
-    y = (flat.float() / temperature).to(torch.bfloat16).float()
+    y = (flat.float() * _recip(temperature, dev)).to(torch.bfloat16).float()
     vals, idx = torch.topk(y, top_k, dim=-1)  # descending
     p = torch.softmax(vals.double(), -1)
     asc_cum = torch.cumsum(p.flip(-1), -1).flip(-1)  # mass of each element and everything below it
@@ -194,7 +199,7 @@ def general_filter_bf16(
     use_inside = torch.rand(B * S, generator=g).to(dev) < 0.9
     inside = torch.empty(B * S, dtype=torch.long, device=dev)
     for a in range(0, B * S, 512):
-        y = (flat[a : a + 512].float() / temperature).to(torch.bfloat16).float()
+        y = (flat[a : a + 512].float() * _recip(temperature, dev)).to(torch.bfloat16).float()
         vals, idx = torch.sort(y, dim=-1, descending=True)
         n_in = torch.full((vals.shape[0],), V, device=dev)
         if top_k is not None and top_k > 0:

@@ -116,3 +116,47 @@ def advantage_case_inputs(case, device="cpu"):
     v = torch.tensor(valid, dtype=torch.float32, device=device)
     q = None if std_rewards is None else torch.tensor(std_rewards, dtype=torch.float32, device=device)
     return p, r, v, loo, q
+
+
+def keep_from_row_info(y: torch.Tensor, info: torch.Tensor) -> torch.Tensor:
+    """Keep sets [N, V] of the rows a filtered forward recorded, decoded from its row
+    records (``mirl_filter_row_info``: m, logsum, v_cut, i_cut, n_kept, flags).
+
+    ``y`` [N, V] holds the values the kernel filtered (after the temperature) as fp32
+    on the CPU; ``info`` is the forward's raw record buffer for those N rows.  Kept:
+    y > v_cut, or y == v_cut and, with i_cut >= 0, index >= i_cut; with i_cut < 0 (rank
+    form), rank among the row's values equal to v_cut in index order >= -1 - i_cut.
+    The decoded set's size is checked against n_kept."""
+    rec = info.cpu().view(torch.int32).view(-1, 6)
+    n = y.shape[0]
+    assert rec.shape[0] == n
+    v_cut = rec[:, 2].clone().view(torch.float32)
+    i_cut = rec[:, 3].long()
+    n_kept = rec[:, 4].long()
+    V = y.shape[1]
+    j = torch.arange(V)
+    gt = y > v_cut[:, None]
+    tie = y == v_cut[:, None]
+    by_index = gt | (tie & (j[None, :] >= i_cut[:, None]))
+    rank = tie.long().cumsum(-1) - 1
+    by_rank = gt | (tie & (rank >= (-1 - i_cut)[:, None]))
+    keep = torch.where((i_cut >= 0)[:, None], by_index, by_rank)
+    assert torch.equal(keep.sum(-1), n_kept), "decoded keep set size differs from n_kept"
+    return keep
+
+
+def kept_lists_match(keep: torch.Tensor, info: torch.Tensor, kidx: torch.Tensor) -> int:
+    """Rows whose saved kept list (ids of kept entries, for rows with at most 1024 kept
+    and flags bit 2 clear) differs from the keep set; returns the number of rows checked."""
+    rec = info.cpu().view(torch.int32).view(-1, 6)
+    kidx = kidx.cpu()
+    checked = 0
+    for r in range(keep.shape[0]):
+        nk, flags = int(rec[r, 4]), int(rec[r, 5])
+        if nk > kidx.shape[1] or (flags & 4):
+            continue
+        got = torch.sort(kidx[r, :nk].long()).values
+        exp = torch.nonzero(keep[r]).view(-1)
+        assert torch.equal(got, exp), f"row {r}: kept list differs from the keep set"
+        checked += 1
+    return checked

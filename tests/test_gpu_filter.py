@@ -16,7 +16,15 @@ one bf16 ulp.  The oracle resolves ties at the top-p boundary in stable
 import pytest
 import torch
 
-from oracle.sampling import filtered_logprobs, filtered_logprobs_grad, next_token_filtered, top_k_top_p
+from oracle.sampling import (
+    apply_temperature,
+    filtered_logprobs,
+    filtered_logprobs_grad,
+    next_token_filtered,
+    top_k_top_p,
+    top_k_top_p_candidates,
+)
+from rl_amd import _C
 from rl_amd.algorithms.logits_sampling_utils import apply_top_k_top_p
 from rl_amd.distributed.model_utils import (
     ChunkedDistributedLogprobWithSampling,
@@ -25,7 +33,7 @@ from rl_amd.distributed.model_utils import (
 )
 from rl_amd.distributed.sampling import filtered_next_token_logprobs
 from rl_amd.algorithms.logits_sampling_utils import TrainingSamplingParams
-from tests.helpers import assert_close_or_ulp_bf16
+from tests.helpers import assert_close_or_ulp_bf16, keep_from_row_info, kept_lists_match
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda", 0)
@@ -124,6 +132,22 @@ def test_next_token_fwd_bwd_against_oracle(k, p, dtype, T):
         assert_close_or_ulp_bf16(gr, grad_o, 1e-3)
     else:
         torch.testing.assert_close(gr.float().cpu(), grad_o.float(), rtol=0, atol=1e-3)
+    # keep sets of the kernel that ran (temperature fused, fp32 decisions), decoded from
+    # its row records, and its kept lists
+    info, kidx, _ = _C.filtered_fwd(xd.detach(), ids.to(DEV)[:, 1:], T, k or 0, p, None, torch.float32)
+    y = apply_temperature(x, T).float()[:, :-1].reshape(-1, V)
+    _, keep_exp = top_k_top_p(y, k, p, exact_normaliser=True)  # the fp32 rule
+    keep_rec = keep_from_row_info(y, info)
+    assert torch.equal(keep_rec, keep_exp)
+    kept_lists_match(keep_rec, info, kidx)
+    # the drop-in shape: the logits scaled in place in their dtype, then filtered with
+    # fp32 decisions (the get_next_token upcast)
+    y_dev = xd.detach()[:, :-1].clone()
+    if T != 1.0:
+        y_dev.div_(T)  # torch's own GPU division
+    assert torch.equal(y_dev.float().cpu().reshape(-1, V), y)
+    _, keep_d = _C.top_k_top_p_mask(y_dev.reshape(-1, V), k or 0, p, decision_dtype=torch.float32)
+    assert torch.equal(keep_d.cpu(), keep_exp)
 
 
 @pytest.mark.parametrize("k,p", CASES)
@@ -297,10 +321,11 @@ def test_full_size_workload_sampled_rows():
         else:
             assert abs(got - lp_o.item()) <= 2e-3
         assert_close_or_ulp_bf16(gr[b : b + 1, s : s + 1], grad_o[:, :1], 1e-3)
-        # keep set of this row, bit-exact
-        y = (xr[:, :1].float() / 0.7).to(torch.bfloat16).float()
-        _, keep_o1 = top_k_top_p(y, 50, 0.9)
-        _, keep1 = apply_top_k_top_p(y.to(DEV), 50, 0.9)
+        # keep set of this row, bit-exact, from the drop-in shape's kernel: the bf16 row
+        # scaled in place on the GPU, filtered with fp32 decisions
+        y_dev = x.detach()[b, s : s + 1].clone().div_(0.7)
+        keep_o1, _ = top_k_top_p_candidates(y_dev.float().cpu(), 50, 0.9)
+        _, keep1 = _C.top_k_top_p_mask(y_dev, 50, 0.9, decision_dtype=torch.float32)
         assert torch.equal(keep1.cpu(), keep_o1)
     assert gr[:, -1].abs().max().item() == 0
     del x, gr

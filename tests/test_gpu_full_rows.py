@@ -2,14 +2,17 @@
 
 The kernel's outputs are copied back chunk by chunk and compared row by row with
 the oracle at the tolerances of the contract: logprobs within 2e-3 (bf16 logits),
-bf16 logits gradients within 1e-3 or one bf16 ulp, keep sets bit-exact.
+bf16 logits gradients within 1e-3 (the one-bf16-ulp allowance of the smaller tests is
+asserted unused here), keep sets bit-exact.
 
   [8, 2048, 151936] bf16 GRPO step: logprobs, loss (fp64 oracle loss on the
       kernel's logprobs) and the logits gradient of the loss, every row;
   [1, 32768, 131072] bf16, chunk 4096: logprobs and logits gradient, every row;
   [4, 4096, 151936] bf16, T = 0.7, top-k 50, top-p 0.9 (fp32 decisions, the
-      get_next_token path after the in-place temperature): keep set, logprob and
-      gradient of every row; the rows whose keep set moves when the normaliser
+      get_next_token path after the in-place temperature): keep set (from the
+      fused-temperature kernel's row records and kept lists, and from the drop-in
+      shape's filter of the scaled bf16 tensor), logprob and gradient of every row;
+      the rows whose keep set moves when the normaliser
       moves by one fp32 ulp, and the rows with ties at the cut, are counted and
       printed;
   64 packed sequences, V = 256000: logprobs and the logits gradient of the
@@ -21,13 +24,12 @@ import torch
 
 from oracle.logprob import next_token_logprobs, next_token_logprobs_grad, selected_logprobs, selected_logprobs_grad
 from oracle.loss import clipped_pg_loss
-from oracle.sampling import top_k_top_p, top_k_top_p_candidates
-from rl_amd import workloads
+from oracle.sampling import temperature_recip, top_k_top_p, top_k_top_p_candidates
+from rl_amd import _C, workloads
 from rl_amd.algorithms.loss import ClippedPGLossConfig, ClippedPGLossFn
 from rl_amd.distributed.model_utils import from_parallel_logits_to_logprobs
-from rl_amd.algorithms.logits_sampling_utils import apply_top_k_top_p
 from rl_amd.distributed.sampling import filtered_next_token_logprobs
-from tests.helpers import assert_close_or_ulp_bf16
+from tests.helpers import assert_close_or_ulp_bf16, keep_from_row_info, kept_lists_match
 
 pytestmark = [pytest.mark.gpu, pytest.mark.timeout(900)]
 DEV = torch.device("cuda", 0)
@@ -94,6 +96,7 @@ def test_grpo_step_every_row():
     lp_full[:, -1] = ref_last[:, 0].to(DEV)
     n = _check_rows(logits.detach(), ids_next, lp_full, gr, glp_full)
     say("rows", B * (S - 1), "gradient elements off by one bf16 ulp beyond 1e-3:", n)
+    assert n == 0
     del x, gr
 
 
@@ -113,10 +116,14 @@ def test_long_context_chunked_every_row():
     lp_full[:, -1] = selected_logprobs(x.detach()[:, -1:].cpu(), ids_next[:, -1:].cpu(), 0, V)[:, 0].to(DEV)
     n = _check_rows(x.detach(), ids_next, lp_full, gr, glp_full, chunk=256)
     say("rows", B * (S - 1), "gradient elements off by one bf16 ulp beyond 1e-3:", n)
+    assert n == 0
     del xl, gr
 
 
 def test_filtered_every_row_keep_sets_exact():
+    """Keep sets of every row, bit-exact, from the two kernels the workload runs: the
+    fused-temperature filter (its row records, decoded, and its kept lists) and the
+    drop-in shape's filter of the bf16 tensor scaled in place (its keep mask)."""
     say("every row: filtered [4, 4096, 151936] bf16, T=0.7, k=50, p=0.9")
     d = workloads.topk_filter_bf16(device=DEV)
     x, ids, gout = d["logits"], d["input_ids"], d["grad"]
@@ -126,18 +133,31 @@ def test_filtered_every_row_keep_sets_exact():
     lp = filtered_next_token_logprobs(xl, ids, k, p, temperature=T, decision_dtype=torch.float32)
     (gr,) = torch.autograd.grad(lp, [xl], gout)
     lp = lp.detach()
-    stats = {"rows": 0, "keep_mismatch": 0, "flip_one_ulp": 0, "group_gt1": 0, "tie_split": 0,
-             "cpu_torch_mismatch": 0, "cpu_torch_rows": 0}
+    # the row records and kept lists of that forward (the same launch, run again)
+    info_f, kidx_f, _ = _C.filtered_fwd(x.detach(), ids[:, 1:], T, k, p, None, torch.float32)
+    info_f = info_f.view(B, S - 1, -1)
+    kidx_f = kidx_f.view(B, S - 1, -1)
+    stats = {"rows": 0, "keep_mismatch_fused": 0, "keep_mismatch_dropin": 0, "kept_lists_checked": 0,
+             "flip_one_ulp": 0, "group_gt1": 0, "tie_split": 0, "cpu_torch_mismatch": 0,
+             "cpu_torch_rows": 0}
     n_bad = 0
+    r = temperature_recip(T)
     for b in range(B):
         for s0 in range(0, S - 1, 512):
             s1 = min(S - 1, s0 + 512)
-            y = (x.detach()[b, s0:s1].float() / T).to(torch.bfloat16).float()  # the in-place division
-            yc = y.cpu()
+            # the in-place division as the reference runs it: torch on the GPU
+            y_dev = x.detach()[b, s0:s1].clone().div_(T)
+            yc = y_dev.float().cpu()
+            assert torch.equal(yc, (x.detach()[b, s0:s1].cpu().float() * r).to(torch.bfloat16).float())
             keep, st = top_k_top_p_candidates(yc, k, p)
-            _, keep_gpu = apply_top_k_top_p(y, k, p)
             stats["rows"] += s1 - s0
-            stats["keep_mismatch"] += int((keep_gpu.cpu() != keep).any(-1).sum())
+            # the fused-temperature kernel: its row records decoded, and its kept lists
+            keep_f = keep_from_row_info(yc, info_f[b, s0:s1])
+            stats["keep_mismatch_fused"] += int((keep_f != keep).any(-1).sum())
+            stats["kept_lists_checked"] += kept_lists_match(keep_f, info_f[b, s0:s1], kidx_f[b, s0:s1])
+            # the drop-in shape: the bf16 scaled tensor, decided in fp32 (the get_next_token upcast)
+            _, keep_d = _C.top_k_top_p_mask(y_dev, k, p, decision_dtype=torch.float32)
+            stats["keep_mismatch_dropin"] += int((keep_d.cpu() != keep).any(-1).sum())
             kp, _ = top_k_top_p_candidates(yc, k, p, z_ulps=1)
             km, _ = top_k_top_p_candidates(yc, k, p, z_ulps=-1)
             stats["flip_one_ulp"] += int(((kp != keep).any(-1) | (km != keep).any(-1)).sum())
@@ -157,18 +177,22 @@ def test_filtered_every_row_keep_sets_exact():
             assert torch.equal(torch.isinf(got), torch.isinf(ref))
             fin = torch.isfinite(ref)
             torch.testing.assert_close(got[fin], ref[fin], rtol=0, atol=2e-3)
-            # gradient: (onehot - p) * g on the kept set, rounded to bf16, then / T in bf16
+            # gradient: (onehot - p) * g on the kept set, rounded to bf16, then the division's
+            # backward in bf16 (the product with fl32(1 / T))
             g = gout[b, s0:s1].cpu()
             pk = lsm.exp()
             oh = torch.zeros_like(pk)
             oh[torch.arange(s1 - s0), t] = 1.0
             g32 = torch.where(keep, (oh - pk) * g[:, None], torch.zeros_like(pk))
-            refg = (g32.to(torch.bfloat16).float() / T).to(torch.bfloat16)
+            refg = (g32.to(torch.bfloat16).float() * r).to(torch.bfloat16)
             grc = gr[b, s0:s1]
             assert int(((grc != 0).cpu() & ~keep).sum()) == 0  # zero outside the kept set
             n_bad += assert_close_or_ulp_bf16(grc, refg, 1e-3)
     say("filter statistics over every row:", stats, "gradient elements off by one ulp:", n_bad)
-    assert stats["keep_mismatch"] == 0
+    assert stats["keep_mismatch_fused"] == 0
+    assert stats["keep_mismatch_dropin"] == 0
+    assert stats["kept_lists_checked"] > 0
+    assert n_bad == 0
     assert gr[:, -1].abs().max().item() == 0
     del xl, gr
 
@@ -227,4 +251,5 @@ def test_packed_grpo_kl_every_row(single_rank_group):
     # rows past the last sequence carry no gradient
     assert gr[:, cu[-1]:].abs().max().item() == 0 if gr.shape[1] > cu[-1] else True
     say("sequences", B, "rows", cu[-1], "gradient elements off by one bf16 ulp beyond 1e-3:", n_bad)
+    assert n_bad == 0
     del x, gr

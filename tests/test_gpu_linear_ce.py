@@ -214,11 +214,12 @@ def test_gradient_row_compaction(pattern):
 @pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
 @pytest.mark.parametrize("S,B,H,V,chunk", [(37, 3, 128, 1000, 8), (16, 2, 64, 151936, None), (9, 3, 200, 3001, 4)])
 def test_fp16_fp32_forward_and_gradients(dtype, S, B, H, V, chunk):
-    """fp16 / fp32 inputs: per chunk a library GEMM in the input dtype, then the logprob row
-    kernels (the reference's chunked shape).  The oracle rounds the exact products to the
-    dtype; logprobs within 2e-3 (fp16) / 1e-5 (fp32) plus the target logit's last-ulp
-    rounding, dH and dW against the float64 oracle to 1e-2 (fp16, G rounded to fp16) /
-    1e-4 (fp32) of their largest magnitude."""
+    """fp16 inputs run the fused kernels (logits tiles on the fp16 MFMA, rounded to fp16;
+    G in bf16 and W, H rounded to bf16 for dH and dW); fp32 inputs take per chunk a library
+    GEMM in fp32, then the logprob row kernels (the reference's chunked shape).  The oracle
+    rounds the exact products to the dtype; logprobs within 2e-3 (fp16) / 1e-5 (fp32) plus
+    the target logit's last-ulp rounding, dH and dW against the float64 oracle to 1e-2
+    (fp16, bf16 operands of the two products) / 1e-4 (fp32) of their largest magnitude."""
     say("linear-ce", dtype, S, B, H, V, chunk)
     g0 = torch.Generator().manual_seed(S * V + H)
     hidden = torch.randn(S, B, H, generator=g0).to(dtype)
@@ -327,3 +328,30 @@ def test_gemm_primitives_with_device_counts():
                              count=cnt, count_off=r0, count_axis=_C.COUNT_K, out_bf16=out16,
                              final_at=r0 + 256)
         assert torch.equal(out16, ref32.to(torch.bfloat16)), c
+
+
+def test_weight_written_in_place_between_backwards():
+    """A weight changed without its version counter moving (``p.data.copy_``, as Megatron
+    and collectives write parameters) gives the next backward the new weight: dH and dW
+    equal, bit for bit, those of a fresh weight tensor holding the same values."""
+    say("linear-ce weight written in place")
+    S, B, H, V = 40, 2, 256, 3001
+    hidden, weight, target = _inputs(S, B, H, V, seed=51)
+    _, weight2, _ = _inputs(S, B, H, V, seed=52)
+    g = torch.randn(B, S, generator=torch.Generator().manual_seed(53))
+    h = hidden.to(DEV).requires_grad_(True)
+    w = weight.to(DEV).requires_grad_(True)
+
+    def grads(wt):
+        lp = ChunkedDistributedHiddenStatesToLogprobs.apply(h, target.to(DEV), wt, 0, V, 8, None, False)
+        return torch.autograd.grad(lp, [h, wt], g.to(DEV))
+
+    dh1, dw1 = grads(w)
+    version = w._version
+    w.data.copy_(weight2.to(DEV))
+    assert w._version == version  # the write is invisible to the version counter
+    dh2, dw2 = grads(w)
+    fresh = weight2.to(DEV).requires_grad_(True)
+    dh_f, dw_f = grads(fresh)
+    assert torch.equal(dh2, dh_f) and torch.equal(dw2, dw_f)
+    assert not torch.equal(dh2, dh1)

@@ -6,6 +6,8 @@ checked against the float64 goldens at 1e-5 relative, inside the 1e-4
 relative loss tolerance of the contract.
 """
 
+import zlib
+
 import pytest
 import torch
 
@@ -116,7 +118,9 @@ def _random_batch(B, S, seed, support=False, unfiltered=False):
 def test_random_batches_against_oracle(name, support, unfiltered):
     print("[case]", name, "support", support, "unfiltered", unfiltered, flush=True)
     cfg = RANDOM_CONFIGS[name]
-    curr, data, psm = _random_batch(6, 97, seed=hash(name) % 1000, support=support, unfiltered=unfiltered)
+    # a fixed seed per case (Python's str hash is salted per process)
+    curr, data, psm = _random_batch(6, 97, seed=zlib.crc32(name.encode()) % 1000, support=support,
+                                    unfiltered=unfiltered)
     gvs = data["sample_mask"].sum()
     gvt = (data["token_mask"][:, 1:] * data["sample_mask"][:, None]).sum()
     # oracle

@@ -10,6 +10,8 @@ are run through the GPU path as well.
 
 import itertools
 
+import zlib
+
 import pytest
 import torch
 
@@ -90,7 +92,8 @@ def _run_oracle(cfg, ntl, plog, data, gvs, gvt):
 def test_clipped_pg_with_score_centering_matches_oracle(mode, token_level, dtype):
     say("score centering loss", mode, "token_level", token_level, dtype)
     cfg = dict(MODES[mode], token_level_loss=token_level, reference_policy_kl_penalty=0.05)
-    ins = _inputs(hash((mode, token_level)) % 1000, dtype=dtype)
+    # a fixed seed per case (Python's str hash is salted per process)
+    ins = _inputs(zlib.crc32(f"{mode}/{token_level}".encode()) % 1000, dtype=dtype)
     gl, gm, gn, gp = _run_gpu(cfg, *ins)
     ol, om, on, op = _run_oracle(cfg, *ins)
     assert list(gm) == list(om)

@@ -49,6 +49,31 @@ def test_mask_outside_tokens_strided_and_16bit():
     lp16 = lp.bfloat16()
     got16 = mask_filtered_logprobs_outside_tokens(lp16.to(DEV), mask.to(DEV))
     assert got16.dtype == torch.bfloat16 and torch.equal(got16.cpu(), torch.where(mask, lp16, 0.0))
+    lp64 = lp.double() - 1e-12  # bits below fp32's resolution survive the select
+    got64 = mask_filtered_logprobs_outside_tokens(lp64.to(DEV), mask.to(DEV))
+    assert got64.dtype == torch.float64 and torch.equal(got64.cpu(), torch.where(mask, lp64, 0.0))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.bfloat16])
+def test_mask_outside_tokens_keeps_autograd(dtype):
+    """Logprobs that require grad: the result keeps a grad_fn, and the gradient is the
+    reference's where(mask, g, 0), including a non-finite upstream gradient at a masked
+    position (the where drops it)."""
+    say("mask outside autograd", dtype)
+    g = torch.Generator().manual_seed(4)
+    lp = (-torch.rand(3, 50, generator=g) * 3).to(dtype)
+    mask = (torch.rand(3, 50, generator=g) < 0.5).float()
+    up = torch.randn(3, 50, generator=g).to(dtype)
+    up[mask == 0] = float("nan")
+    ref_in = lp.clone().requires_grad_(True)
+    ref_out = torch.where(mask.bool(), ref_in, 0.0)
+    (ref_g,) = torch.autograd.grad(ref_out, [ref_in], up)
+    x = lp.to(DEV).requires_grad_(True)
+    out = mask_filtered_logprobs_outside_tokens(x, mask.to(DEV))
+    assert out.requires_grad and out.grad_fn is not None and out.dtype == dtype
+    assert torch.equal(out.detach().cpu(), ref_out.detach())
+    (gx,) = torch.autograd.grad(out, [x], up.to(DEV))
+    assert torch.equal(gx.cpu(), ref_g)
 
 
 @pytest.mark.parametrize("B,S", [(64, 2047), (5, 1), (3, 4097), (0, 3)])

@@ -24,7 +24,14 @@ import numpy as np
 import pytest
 import torch
 
-from oracle.sampling import filtered_logprobs, filtered_logprobs_grad, next_token_filtered, top_k_top_p
+from oracle.sampling import (
+    apply_temperature,
+    filtered_logprobs,
+    filtered_logprobs_grad,
+    next_token_filtered,
+    temperature_recip,
+    top_k_top_p,
+)
 
 
 def _definition_keep(x: list[float], k, p) -> set[int]:
@@ -93,21 +100,44 @@ def test_filtered_logprob_and_grad_definitions():
     torch.testing.assert_close(gr.double(), (oh - p) * gout.unsqueeze(-1).double() * keep, rtol=0, atol=1e-6)
 
 
+def _times_recip16(values, T: float, dtype) -> torch.Tensor:
+    """dtype(fl32(v * fl32(1.0 / T))) element by element with numpy scalars."""
+    r = np.float32(1.0 / T)
+    out = [_round16(float(np.float32(np.float32(v) * r)), dtype) for v in values.reshape(-1).tolist()]
+    return torch.tensor(out, dtype=torch.float32).view(values.shape)
+
+
+def test_temperature_reciprocal_known_answers():
+    """The in-place temperature's reciprocal is 1.0 / T formed in double and rounded once.
+
+    At T = 1.1 that is 0x3F68BA2F, where the reciprocal of the fp32 temperature,
+    1.0f / fl32(1.1), is one ulp lower: a reciprocal formed in fp32 fails here.  At
+    T = 0.7 the product and the exact quotient round differently for x = 5 in fp32."""
+    assert int(temperature_recip(1.1).view(torch.int32)) == 0x3F68BA2F
+    wrong = torch.tensor(1.0, dtype=torch.float32) / torch.tensor(1.1, dtype=torch.float32)
+    assert int(wrong.view(torch.int32)) == 0x3F68BA2E
+    x = torch.tensor([5.0], dtype=torch.float32)
+    prod = apply_temperature(x, 0.7)
+    assert prod.item() == float(np.float32(np.float32(5.0) * np.float32(1.0 / 0.7)))
+    assert prod.item() != (x / 0.7).item()  # CPU torch's exact quotient differs by one ulp
+
+
 def test_temperature_chain_bf16():
-    """div_ in bf16 then the bf16 gradient chain of the reference's production path."""
+    """div_ in bf16 then the bf16 gradient chain of the reference's production path,
+    against the same chain written out with numpy scalars."""
     g = torch.Generator().manual_seed(2)
     x = (torch.randn(1, 5, 64, generator=g) * 2).to(torch.bfloat16)
     ids = torch.randint(0, 64, (1, 5), generator=g)
     gout = torch.randn(1, 4, generator=g)
     lp, keep, grad = next_token_filtered(x, ids, 8, 0.9, temperature=0.7, grad_output=gout)
-    y = (x.float() / 0.7).to(torch.bfloat16).float()
+    y = _times_recip16(x.float(), 0.7, torch.bfloat16)
     lp2, keep2 = filtered_logprobs(y[:, :-1], ids[:, 1:], 8, 0.9)
     assert torch.equal(keep, keep2)
     torch.testing.assert_close(lp, lp2, rtol=0, atol=0)
     assert grad.dtype == torch.bfloat16
     g32 = filtered_logprobs_grad(y[:, :-1], ids[:, 1:], 8, 0.9, gout)
-    exp = (g32.to(torch.bfloat16).float() / 0.7).to(torch.bfloat16)
-    torch.testing.assert_close(grad[:, :-1].float(), exp.float(), rtol=0, atol=0)
+    exp = _times_recip16(g32.to(torch.bfloat16).float(), 0.7, torch.bfloat16)
+    torch.testing.assert_close(grad[:, :-1].float(), exp, rtol=0, atol=0)
     assert grad[:, -1].abs().max() == 0
 
 
