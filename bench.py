@@ -55,7 +55,8 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "logprob+PG-loss fwd/bwd tokens/s and HBM GB/s (% peak) at V=151936 bf16"
 PEAK_HBM_GBPS = 8000.0
-PEAK_BF16_TFLOPS = 2500.0  # dense bf16 MFMA
+PEAK_BF16_TFLOPS = 2500.0  # dense bf16 MFMA (fp16 the same)
+PEAK_FP32_TFLOPS = 157.3  # dense fp32 MFMA
 
 
 def parse():
@@ -65,6 +66,8 @@ def parse():
                     choices=["grpo", "fwd_f32", "long_context", "topk_filter", "topk_filter_fused",
                              "topp_only", "topk2000", "filtered16_fwd", "packed_kl", "linear_ce",
                              "distill_rkl", "score_centering", "topk_export"])
+    ap.add_argument("--dtype", default="bf16", choices=["bf16", "fp16", "fp32"],
+                    help="linear_ce: dtype of the hidden states and weight")
     ap.add_argument("--loss-scale", type=float, default=1.0,
                     help="grpo: multiply the loss by this before the backward (as callers that "
                          "scale the loss by the data-parallel size or microbatch count do)")
@@ -691,8 +694,10 @@ def bench_workload(args) -> None:
         from rl_amd.distributed.model_utils import from_parallel_hidden_states_to_logprobs
 
         d = workloads.linear_ce_bf16(device=dev)
-        hidden = d["hidden"].requires_grad_(True)
-        weight = d["weight"].requires_grad_(True)
+        tdt = {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32}[args.dtype]
+        hidden = d["hidden"].to(tdt).requires_grad_(True)
+        weight = d["weight"].to(tdt).requires_grad_(True)
+        del d["hidden"], d["weight"]
         ids, g = d["input_ids"], d["grad"]
         S, B, H = hidden.shape
         V = weight.shape[0]
@@ -702,9 +707,11 @@ def bench_workload(args) -> None:
                                                          chunk_size=256)
             return torch.autograd.grad(lp, [hidden, weight], g)
 
-        ms_step, ms = _timed(step, args.steps, args.warmup,
-                             ["mirl_linear_ce_fwd", "mirl_linear_ce_grad", "mirl_gemm_bf16_abt",
-                              "mirl_transpose_bf16", "mirl_sum_splits_bf16"])
+        lce_kernels = (["mirl_linear_ce_fwd", "mirl_linear_ce_grad", "mirl_gemm_bf16_abt",
+                        "mirl_transpose_bf16", "mirl_sum_splits_bf16"] if args.dtype != "fp32" else
+                       ["mirl_logprob_fwd", "mirl_logprob_bwd"])
+        region = {}
+        ms_step, ms = _timed(step, args.steps, args.warmup, lce_kernels, region_events=region)
         rows = B * (S - 1)
         gemm = 2.0 * S * B * H * V  # one [S*B, H] x [H, V] product
         # the backward moves the rows with a non-zero upstream gradient to the front
@@ -720,9 +727,20 @@ def bench_workload(args) -> None:
         grad_ms = ms.get("mirl_linear_ce_grad", 0.0) * n_blocks
         gemm_act = 2.0 * active * H * V
         tflops = gemm / (fwd_ms * 1e-3) / 1e12 if fwd_ms > 0 else 0.0
-        roof = {"kernel": "mirl_linear_ce_fwd", "bound": "mfma", "achieved": tflops, "peak": PEAK_BF16_TFLOPS,
-                "unit": "TFLOP/s", "frac": tflops / PEAK_BF16_TFLOPS, "traffic": _traffic(w, "mirl_linear_ce_fwd"),
-                "algorithmic_flops": gemm}
+        peak = PEAK_FP32_TFLOPS if args.dtype == "fp32" else PEAK_BF16_TFLOPS
+        if args.dtype == "fp32":
+            # library GEMMs per chunk plus the logprob row kernels: the whole step's
+            # algorithmic flops over its GPU time (one event pair around the timed steps)
+            gpu_ms = region.get("gpu_ms_per_step", ms_step)
+            tflops = (gemm + 3 * gemm_act) / (gpu_ms * 1e-3) / 1e12
+            roof = {"kernel": "step (library fp32 GEMMs + mirl_logprob_fwd/bwd)", "bound": "mfma",
+                    "achieved": tflops, "peak": peak, "unit": "TFLOP/s", "frac": tflops / peak,
+                    "traffic": None, "algorithmic_flops": gemm + 3 * gemm_act}
+        else:
+            roof = {"kernel": "mirl_linear_ce_fwd", "bound": "mfma", "achieved": tflops, "peak": peak,
+                    "unit": "TFLOP/s", "frac": tflops / peak,
+                    "traffic": _traffic(w if args.dtype == "bf16" else f"{w}_{args.dtype}", "mirl_linear_ce_fwd"),
+                    "algorithmic_flops": gemm}
         extra["tflops_step"] = (gemm + 3 * gemm_act) / (ms_step * 1e-3) / 1e12
         extra["grad_kernel_ms_per_step"] = grad_ms
         extra["grad_kernel_tflops"] = gemm_act / (grad_ms * 1e-3) / 1e12 if grad_ms > 0 else None
@@ -735,7 +753,7 @@ def bench_workload(args) -> None:
         cfg = {"workload": "hidden_state_logprobs_fwd_bwd", "hidden": [S, B, H], "weight": [V, H],
                "chunk_size": 256, "next_token_rows": rows, "active_rows": active,
                "flops_per_step": "2*S*B*H*V (fused fwd) + 3 x 2*active*H*V (fused grad recompute, dH, dW)"}
-        dtype = "bf16"
+        dtype = args.dtype
         n_pos = 32
         hs, ws_, ts = hidden.detach()[:n_pos].cpu(), weight.detach().cpu(), torch.roll(ids, -1, 1)[:, :n_pos].cpu()
 
