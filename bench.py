@@ -71,6 +71,9 @@ def parse():
     ap.add_argument("--loss-scale", type=float, default=1.0,
                     help="grpo: multiply the loss by this before the backward (as callers that "
                          "scale the loss by the data-parallel size or microbatch count do)")
+    ap.add_argument("--hint-loss-scale", action="store_true",
+                    help="grpo: state --loss-scale to the early backward "
+                         "(set_early_backward(loss_scale=...)), as a data-parallel caller would")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="minimum CPU time of the cpu_baseline sample")
     ap.add_argument("--steps", type=int, default=50)
@@ -179,6 +182,10 @@ def main() -> None:
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     print(f"[bench] device {torch.cuda.get_device_name(dev)}; building inputs", file=sys.stderr, flush=True)
+    if args.hint_loss_scale:
+        from rl_amd.distributed.model_utils import set_early_backward
+
+        set_early_backward("adaptive", loss_scale=args.loss_scale)
     data = workloads.grpo_step_bf16(device=dev)
     logits = data["logits"].requires_grad_(True)
     ids = data["input_ids"]
@@ -215,7 +222,7 @@ def main() -> None:
     main_kernels = ["mirl_logprob_fwd", "mirl_logprob_bwd", "mirl_logprob_bwd_recheck"]
     ms_step, ms = _timed(step, args.steps, args.warmup, main_kernels)
     always = None
-    if args.loss_scale != 1.0:
+    if args.loss_scale != 1.0 and not args.hint_loss_scale:
         # the default (adaptive) policy stops speculating after the first checked
         # miss; time the redo itself with speculation forced on every step
         from rl_amd.distributed.model_utils import set_early_backward
@@ -285,6 +292,7 @@ def main() -> None:
             "active_rows": active_rows,
             "loss": "ClippedPG clip 0.2/0.2 token-level, no KL; GRPO adv (no LOO)",
             "loss_scale": args.loss_scale,
+            "loss_scale_hinted": bool(args.hint_loss_scale),
             "parallelism": "single-gpu",
         },
         "hbm_gbps_step": step_gbps,
@@ -310,6 +318,11 @@ def main() -> None:
         },
         "cpu_baseline": cpu,
     }
+    from rl_amd.distributed.early_backward import POLICY
+
+    POLICY._drain()
+    out["early_backward"] = {"mode": POLICY.mode, "loss_scale_hint": POLICY.loss_scale,
+                             "checks_missed": POLICY.misses, "opportunities_skipped": POLICY.skipped}
     print(json.dumps(out), flush=True)
 
 

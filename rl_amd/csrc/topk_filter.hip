@@ -901,9 +901,22 @@ __global__ __launch_bounds__(64 * W) void filter_bwd_zero_rows_kernel(FilterBwdP
 // How the whole-row walk narrows an fp32 gradient to the dtype.
 enum GradConv {
   kConvPlain = 0,  // no temperature: round to the dtype
-  kConvOne = 1,    // one temperature (fused or earlier in place): round, product, round
-  kConvTwo = 2,    // both: grad_to_dtype
+  kConvGT = 1,     // an earlier in-place temperature only: round, product with rGT, round
+  kConvT = 2,      // the fused temperature only: values scaled; round, product with rT, round
+  kConvTwo = 3,    // both: values scaled; grad_to_dtype
 };
+template <int CONV>
+constexpr bool conv_scales_values() {
+  return CONV == kConvT || CONV == kConvTwo;
+}
+template <int CONV>
+constexpr bool conv_one_product() {
+  return CONV == kConvGT || CONV == kConvT;
+}
+// The GradConv for a launch's temperatures.
+__host__ __device__ inline int grad_conv(bool has_t, bool has_gt) {
+  return has_t ? (has_gt ? kConvTwo : kConvT) : (has_gt ? kConvGT : kConvPlain);
+}
 
 // Per-row arithmetic of the whole-row walks below: the kept test of elements
 // equal to v_cut, the probability of a kept element and the gradient narrowed
@@ -929,9 +942,14 @@ struct WalkMath {
     // dtype's resolution), for fp32 gradients from the differences
     c = (ri.m + ri.logsum) * kLog2e;
     ngv = -gv;
-    rone = P.has_t ? P.rT : P.rGT;
+    rone = CONV == kConvT ? P.rT : P.rGT;
   }
-  __device__ float yval(float xf) const { return P.has_t ? round_trip<E>(mul_rn(xf, P.rT)) : xf; }
+  __device__ float yval(float xf) const {
+    if constexpr (conv_scales_values<CONV>())
+      return round_trip<E>(mul_rn(xf, P.rT));
+    else
+      return xf;
+  }
   __device__ float prob(float yy) const {
     if constexpr (std::is_same<E, F32>::value)
       return fast_exp2(((yy - ri.m) - ri.logsum) * kLog2e);
@@ -942,7 +960,7 @@ struct WalkMath {
   __device__ raw narrow(float g32) const {
     if constexpr (CONV == kConvPlain) {
       return E::from_float(g32);
-    } else if constexpr (CONV == kConvOne) {
+    } else if constexpr (conv_one_product<CONV>()) {
       return E::from_float(mul_rn(round_trip<E>(g32), rone));
     } else {
       return grad_to_dtype<E>(g32, P);
@@ -954,7 +972,7 @@ struct WalkMath {
     float g[E::kVec];
 #pragma unroll
     for (int k = 0; k < E::kVec; ++k) g[k] = kept(k) ? prob(w[k]) * ngv : 0.f;
-    if constexpr (CONV == kConvOne) {
+    if constexpr (conv_one_product<CONV>()) {
       // round to the dtype two at a time, multiply, round again
 #pragma unroll
       for (int k = 0; k < E::kVec; k += 2) {
@@ -1103,6 +1121,13 @@ __device__ __forceinline__ void walk_row(const FilterBwdParams& P, const RowInfo
 // rounding, the division of an earlier in-place temperature, the kept test),
 // 93% of the VALU issue slots over the kernel (SQ_INSTS_VALU against
 // GRBM_GUI_ACTIVE).
+// Sum of a 32-bit count over the 64 lanes of a wave (every lane gets the sum).
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += (uint32_t)__shfl_xor((int)v, off, 64);
+  return v;
+}
+
 constexpr int kRowWaves = 12;
 constexpr int kRowThreads = 64 * kRowWaves;
 constexpr int kRowVecs = 2;
@@ -1184,33 +1209,24 @@ __device__ __forceinline__ void walk_row_block(const FilterBwdParams& P, const R
     // earlier spans: they meet in LDS, one barrier per round, and only while
     // the running count has not yet reached rcut (the mode is the same for
     // the whole workgroup).
+    // the round's values (after the fused temperature, when there is one)
     float w[U][VEC];
-    bool anytie[U];
-    uint32_t wcnt[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const bool valid = base + u * NT + tid < nvec;
       E::unpack(q[u], w[u]);
-      bool tie = false;
-      uint32_t c = 0u;
 #pragma unroll
-      for (int k = 0; k < VEC; ++k) {
-        w[u][k] = W.yval(w[u][k]);
-        const bool e = valid && w[u][k] == vc;
-        tie = tie || e;
-        c += (uint32_t)__popcll(__ballot(e));
-      }
-      anytie[u] = tie;
-      wcnt[u] = c;
-      __builtin_amdgcn_sched_barrier(0);
+      for (int k = 0; k < VEC; ++k) w[u][k] = W.yval(w[u][k]);
     }
+    // this lane's ties (elements equal to v_cut) in span u, one bit per element
     auto tie_bits = [&](int u) {
       uint32_t m = 0u;
+      if (base + u * NT + tid < nvec) {
 #pragma unroll
-      for (int k = 0; k < VEC; ++k) m |= (w[u][k] == vc ? 1u : 0u) << k;
-      return anytie[u] ? m : 0u;
+        for (int k = 0; k < VEC; ++k) m |= (w[u][k] == vc ? 1u : 0u) << k;
+      }
+      return m;
     };
-    // per span: 0 = drop its ties, 1 = keep them, 2 = exact (keepT bits)
+    // per span (wave-uniform): 0 = drop its ties, 1 = keep them, 2 = exact (keepT bits)
     int mode[U];
     uint32_t keepT[U];
 #pragma unroll
@@ -1223,6 +1239,18 @@ __device__ __forceinline__ void walk_row_block(const FilterBwdParams& P, const R
 #pragma unroll
         for (int u = 0; u < U; ++u) mode[u] = 1;
       } else {
+        // the tie counts of the round's (wave, u) spans: a count per lane, summed
+        // over the wave (two instructions per element, only while the cut lies ahead)
+        uint32_t wcnt[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          uint32_t cl = 0u;
+          if (base + u * NT + tid < nvec) {
+#pragma unroll
+            for (int k = 0; k < VEC; ++k) cl += (w[u][k] == vc) ? 1u : 0u;
+          }
+          wcnt[u] = wave_sum_u32(cl);
+        }
 #pragma unroll
         for (int u = 0; u < U; ++u)
           if (lane == 0) s_cnt[par * NC + u * kRowWaves + wave] = wcnt[u];
@@ -1274,10 +1302,11 @@ __device__ __forceinline__ void walk_row_block(const FilterBwdParams& P, const R
       const int jb = head + i * VEC;
       raw vals[VEC];
       const uint32_t kt = keepT[u];
-      const bool all = mode[u] == 1;
-      if (mode[u] == 2)
+      // the mode is the same in every lane of the wave: a scalar branch
+      const int md = __builtin_amdgcn_readfirstlane(mode[u]);
+      if (md == 2)
         W.narrow_vec(w[u], vals, [&](int k) { return w[u][k] > vc || ((kt >> k) & 1u) != 0u; });
-      else if (all)
+      else if (md == 1)
         W.narrow_vec(w[u], vals, [&](int k) { return w[u][k] >= vc; });
       else
         W.narrow_vec(w[u], vals, [&](int k) { return w[u][k] > vc; });
@@ -1288,7 +1317,7 @@ __device__ __forceinline__ void walk_row_block(const FilterBwdParams& P, const R
 #pragma unroll
         for (int k = 0; k < VEC; ++k)
           if (k == dt) {
-            const bool tk = mode[u] == 2 ? ((kt >> k) & 1u) != 0u : all;
+            const bool tk = md == 2 ? ((kt >> k) & 1u) != 0u : md == 1;
             t_y = w[u][k];
             t_kept = w[u][k] > vc || (w[u][k] == vc && tk);
             t_mine = true;
@@ -1392,12 +1421,12 @@ __global__ __launch_bounds__(256) void filter_bwd_scatter_kernel(FilterBwdParams
 
   // Whole row: re-read the logits and re-apply the cut.
   const raw* x = static_cast<const raw*>(P.logits) + b * P.sb + r * P.sr;
-  if (!P.has_t && !P.has_gt)
-    walk_row<E, kConvPlain>(P, ri, x, y, gv, t, lane);
-  else if (!P.has_t || !P.has_gt)
-    walk_row<E, kConvOne>(P, ri, x, y, gv, t, lane);
-  else
-    walk_row<E, kConvTwo>(P, ri, x, y, gv, t, lane);
+  switch (grad_conv(P.has_t, P.has_gt)) {
+    case kConvPlain: walk_row<E, kConvPlain>(P, ri, x, y, gv, t, lane); break;
+    case kConvGT: walk_row<E, kConvGT>(P, ri, x, y, gv, t, lane); break;
+    case kConvT: walk_row<E, kConvT>(P, ri, x, y, gv, t, lane); break;
+    default: walk_row<E, kConvTwo>(P, ri, x, y, gv, t, lane); break;
+  }
 }
 
 // filtered logits (-inf outside the kept set) and the keep mask
@@ -1491,15 +1520,17 @@ int launch_bwd(const FilterBwdParams& P, int64_t B, int64_t rows, hipStream_t st
   if (P.zero_rows) {
     // rows without kept lists: each row written once, by a workgroup of its own
     if (rows == 0) return MIRL_OK;
-    if (!P.has_t && !P.has_gt)
-      hipLaunchKernelGGL((filter_bwd_row_kernel<E, kConvPlain>), dim3((unsigned)rows), dim3(kRowThreads),
-                         0, st, P);
-    else if (!P.has_t || !P.has_gt)
-      hipLaunchKernelGGL((filter_bwd_row_kernel<E, kConvOne>), dim3((unsigned)rows), dim3(kRowThreads), 0,
+    auto launch = [&](auto conv) {
+      constexpr int CONV = decltype(conv)::value;
+      hipLaunchKernelGGL((filter_bwd_row_kernel<E, CONV>), dim3((unsigned)rows), dim3(kRowThreads), 0,
                          st, P);
-    else
-      hipLaunchKernelGGL((filter_bwd_row_kernel<E, kConvTwo>), dim3((unsigned)rows), dim3(kRowThreads),
-                         0, st, P);
+    };
+    switch (grad_conv(P.has_t, P.has_gt)) {
+      case kConvPlain: launch(std::integral_constant<int, kConvPlain>{}); break;
+      case kConvGT: launch(std::integral_constant<int, kConvGT>{}); break;
+      case kConvT: launch(std::integral_constant<int, kConvT>{}); break;
+      default: launch(std::integral_constant<int, kConvTwo>{}); break;
+    }
     return check_launch("filter_bwd_row_kernel");
   }
   const bool contiguous = P.gisr == P.V && (B == 1 || P.gisb == P.Rt * P.V);

@@ -8,6 +8,14 @@ loss, a second consumer of the logprobs).  The guess costs nothing when it is
 right and a wasted backward plus the redo when it is wrong, so the policy
 follows the outcome of the last check:
 
+Callers that scale the loss before its backward (Automodel multiplies it by
+``dp_size * cp_size / cp_gradient_fanout``, nemo_rl/models/automodel/train.py:587-593)
+can state the scale with ``loss_scale``: the early backward then uses
+``fl32(d(loss)/d(logprobs) * fl32(loss_scale))``, the gradient autograd hands
+the logprob backward when the loss's upstream gradient is ``fl32(loss_scale)``,
+so the check finds no difference.  A wrong hint costs what a miss costs (the
+check recomputes), never a wrong gradient.
+
 ``"adaptive"`` (the default) starts the backward early unless the last check
 whose result has reached the host found a different gradient; after such a
 miss the next ``retry_after`` opportunities run the plain backward instead (no
@@ -31,16 +39,21 @@ MODES = ("adaptive", "always", "never")
 
 
 class EarlyBackwardPolicy:
-    def __init__(self, mode: str = "adaptive", retry_after: int = 16) -> None:
-        self.configure(mode, retry_after)
+    def __init__(self, mode: str = "adaptive", retry_after: int = 16, loss_scale: float = 1.0) -> None:
+        self.configure(mode, retry_after, loss_scale)
 
-    def configure(self, mode: str, retry_after: int = 16) -> None:
+    def configure(self, mode: str, retry_after: int = 16, loss_scale: float = 1.0) -> None:
         if mode not in MODES:
             raise ValueError(f"early-backward mode must be one of {MODES}, got {mode!r}")
         if int(retry_after) < 0:
             raise ValueError(f"retry_after must be >= 0, got {retry_after}")
+        loss_scale = float(loss_scale)
+        if not (loss_scale == loss_scale and abs(loss_scale) != float("inf")):
+            raise ValueError(f"loss_scale must be finite, got {loss_scale}")
         self.mode = mode
         self.retry_after = int(retry_after)
+        self.loss_scale = loss_scale
+        self._scale_tensors: dict = {}  # device -> fp32 0-d tensor holding fl32(loss_scale)
         self.pending: Optional[list] = None  # start_fetch handle of the last check's flags
         self.skip = 0
         self.misses = 0  # checks that found a different gradient (read on the host)
@@ -70,6 +83,17 @@ class EarlyBackwardPolicy:
             return False
         return True
 
+    def hinted(self, grad: torch.Tensor) -> torch.Tensor:
+        """``grad`` (d(loss)/d(x) at a unit loss gradient) times the stated loss scale, as
+        the loss's autograd backward forms it (an fp32 product with a 0-d fp32 tensor)."""
+        if self.loss_scale == 1.0:
+            return grad
+        t = self._scale_tensors.get(grad.device)
+        if t is None:
+            t = torch.tensor(self.loss_scale, dtype=torch.float32, device=grad.device)
+            self._scale_tensors[grad.device] = t
+        return grad * t
+
     def checked(self, flags: torch.Tensor) -> None:
         """Record a device-side check (its flags tensor); read later without waiting."""
         if self.mode != "adaptive":
@@ -82,9 +106,10 @@ class EarlyBackwardPolicy:
 POLICY = EarlyBackwardPolicy()
 
 
-def set_early_backward(mode: str = "adaptive", retry_after: int = 16) -> None:
-    """Choose when launch_early_backward starts the logits backward (see the module doc)."""
-    POLICY.configure(mode, retry_after)
+def set_early_backward(mode: str = "adaptive", retry_after: int = 16, loss_scale: float = 1.0) -> None:
+    """Choose when launch_early_backward starts the logits backward, and the scale the
+    caller applies to the loss before its backward (see the module doc)."""
+    POLICY.configure(mode, retry_after, loss_scale)
 
 
 def early_backward_mode() -> str:

@@ -186,9 +186,9 @@ def launch_early_backward_pair(
             or tuple(grad_curr.shape) != tuple(curr.shape) or tuple(grad_plog.shape) != tuple(plog.shape)):
         return False
     g_a = torch.zeros((B, S, K1), dtype=torch.float32, device=logits.device)
-    g_a[:, : S - 1, 0] = grad_curr
+    g_a[:, : S - 1, 0] = POLICY.hinted(grad_curr)
     g_b = torch.zeros_like(g_a)
-    g_b[:, : S - 1, 1:] = grad_plog
+    g_b[:, : S - 1, 1:] = POLICY.hinted(grad_plog)
     g = g_a + g_b
     grad_input = torch.empty_like(logits)
     vs, ve = node.vocab
@@ -210,7 +210,8 @@ def launch_early_backward(logprobs: torch.Tensor, grad: torch.Tensor) -> bool:
     Applies to logprobs produced directly by this module's row kernel and to
     their unpacking from packed sequences; returns whether the backward was
     started.  set_early_backward chooses when it is (by default it is not
-    started again for a while after a check found a different gradient).
+    started again for a while after a check found a different gradient) and the
+    loss scale the caller applies, which ``grad`` is multiplied by first.
     """
     fn = logprobs.grad_fn
     if grad.dtype != torch.float32 or tuple(grad.shape) != tuple(logprobs.shape):
@@ -222,22 +223,25 @@ def launch_early_backward(logprobs: torch.Tensor, grad: torch.Tensor) -> bool:
         if src is None:
             return False
         (bounds,) = fn.saved_tensors
-        return _launch_early_on_node(src, _C.unpack_rows_bwd(grad, bounds, fn.n_rows).view(1, -1))
-    return _launch_early_on_node(fn, grad)
+        return _launch_early_on_node(
+            src, (1, fn.n_rows),
+            lambda: _C.unpack_rows_bwd(POLICY.hinted(grad), bounds, fn.n_rows).view(1, -1))
+    return _launch_early_on_node(fn, tuple(grad.shape), lambda: POLICY.hinted(grad))
 
 
-def _launch_early_on_node(fn: Any, grad: torch.Tensor) -> bool:
-    """launch_early_backward for the autograd node of a row-kernel output."""
+def _launch_early_on_node(fn: Any, grad_shape: tuple, make_grad) -> bool:
+    """launch_early_backward for the autograd node of a row-kernel output; ``make_grad()``
+    forms the node's upstream gradient (shape ``grad_shape``), only once the launch is on."""
     if not isinstance(fn, _RowLogprob._backward_cls):
         return False
     if getattr(fn, "early", None) is not None or getattr(fn, "reuse_logits_storage", True):
         return False
+    logits, target, stats = fn.saved_tensors
+    if tuple(grad_shape) != tuple(target.shape):
+        return False
     if not POLICY.should_launch():
         return False
-    logits, target, stats = fn.saved_tensors
-    if tuple(grad.shape) != tuple(target.shape):
-        return False
-    grad = grad.contiguous()
+    grad = make_grad().contiguous()
     grad_input = torch.empty_like(logits)
     vs, ve = fn.vocab
     _C.logprob_bwd(logits, target, vs, ve, stats, grad, grad_input)

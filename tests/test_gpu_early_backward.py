@@ -268,3 +268,45 @@ def test_never_mode_runs_plain_backward():
     g_ref, _ = _grad(d, gvs, gvt, early=False)
     g, started = _grad(d, gvs, gvt, early=True)
     assert not started and torch.equal(g, g_ref)
+
+
+def _misses_after(run, n=3):
+    """Run `run()` n times in adaptive mode, each check's flags reaching the host before the
+    next decision; the number of checks that found a different gradient."""
+    for _ in range(n):
+        run()
+        torch.cuda.synchronize()
+    POLICY._drain()
+    return POLICY.misses
+
+
+@pytest.mark.parametrize("path", ["rows", "packed", "score-centering"])
+@pytest.mark.parametrize("scale,hint", [(8.0, 8.0), (8.0, 4.0), (0.5, 0.5), (1.0, 2.0)])
+def test_loss_scale_hint(path, scale, hint):
+    """A stated loss scale (set_early_backward(loss_scale=...)): with the scale the caller
+    really applies, the early backward uses the scaled gradient and no check misses; with a
+    wrong one every check recomputes.  The gradients are bit-identical to the plain
+    backward's either way."""
+    say("early backward: loss-scale hint", path, scale, hint)
+    if path == "rows":
+        d, gvs, gvt = _setup(10)
+        run = lambda early: _grad(d, gvs, gvt, early=early, scale=scale)  # noqa: E731
+    elif path == "packed":
+        d, cu_pad, S, gvs, gvt = _packed_setup(11)
+        run = lambda early: _packed_grad(d, cu_pad, S, gvs, gvt, early=early, scale=scale)  # noqa: E731
+    else:
+        d, gvs, gvt = _sc_setup(12)
+        run = lambda early: _sc_grad(d, gvs, gvt, early=early, scale=scale)  # noqa: E731
+    g_ref, _ = run(False)
+    set_early_backward("adaptive", retry_after=0, loss_scale=hint)
+    got = []
+
+    def one():
+        g, started = run(True)
+        assert started
+        got.append(g)
+
+    misses = _misses_after(one)
+    for g in got:
+        assert torch.equal(g, g_ref)
+    assert misses == (0 if hint == scale else len(got))
