@@ -27,6 +27,7 @@ roofline (the default line above is the headline measurement):
                (filtered_next_token_logprobs(..., temperature=T))
   topp_only    as topk_filter with top-p 0.9 alone (no top-k): the histogram path
   topk2000     as topk_filter with k = 2000, p = 0.9: the histogram path
+  topp_only_f32 as topp_only with fp32 logits: the fp32 two-pass path
   filtered16_fwd  forward-only filtered logprobs decided in bf16 (the Megatron logprob
                post-processor's call on the scaled bf16 logits), T=0.7, p=0.9
   packed_kl    packed GRPO step with k3 KL, 64 sequences in bf16 [1, ~34.8k, 256000],
@@ -64,7 +65,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--workload", default="grpo",
                     choices=["grpo", "fwd_f32", "long_context", "topk_filter", "topk_filter_fused",
-                             "topp_only", "topk2000", "filtered16_fwd", "packed_kl", "linear_ce",
+                             "topp_only", "topk2000", "topp_only_f32", "filtered16_fwd", "packed_kl",
+                             "linear_ce",
                              "distill_rkl", "score_centering", "topk_export"])
     ap.add_argument("--dtype", default="bf16", choices=["bf16", "fp16", "fp32"],
                     help="linear_ce: dtype of the hidden states and weight")
@@ -455,11 +457,14 @@ def _dominant(candidates: list, ms: dict, workload: str) -> dict:
 def _filtered_cpu(x, ids, g, k, p, T, rows: int, min_seconds: float, forward_only: bool = False,
                   decide_16bit: bool = False):
     """The oracle's filtered chain on the first `rows` next-token rows of sequence 0."""
+    import torch
+
     from oracle.sampling import apply_temperature, filtered_logprobs, next_token_filtered
 
     xs = x[0:1, : rows + 1].detach().cpu()
     ids_s = ids[0:1, : rows + 1].cpu()
     gs = None if g is None else g[0:1, :rows].cpu()
+    dt = {torch.bfloat16: "bf16", torch.float16: "fp16", torch.float32: "fp32"}[x.dtype]
     if decide_16bit:
         def run():
             y = apply_temperature(xs, T)
@@ -468,9 +473,9 @@ def _filtered_cpu(x, ids, g, k, p, T, rows: int, min_seconds: float, forward_onl
     else:
         def run():
             next_token_filtered(xs, ids_s, k, p, temperature=T, grad_output=None if forward_only else gs)
-        what = "T-division in bf16, fp32 upcast, filter, log_softmax, gather" + (
+        what = f"T-division in {dt}, fp32 upcast, filter, log_softmax, gather" + (
             "" if forward_only else ", backward to the raw logits")
-    return lambda: _cpu_timed(run, rows, f"{rows} next-token rows of [1, {rows + 1}, {x.shape[-1]}] bf16 "
+    return lambda: _cpu_timed(run, rows, f"{rows} next-token rows of [1, {rows + 1}, {x.shape[-1]}] {dt} "
                               f"(k={k}, p={p}, T={T}): {what}", min_seconds)
 
 
@@ -583,7 +588,7 @@ def bench_workload(args) -> None:
 
             return _cpu_timed(run, n_s, f"the first {n_s} of the {rows} next-token rows (V={V}, bf16, "
                               "chunk 4096): forward + backward", secs)
-    elif w in ("topk_filter", "topp_only", "topk2000", "filtered16_fwd"):
+    elif w in ("topk_filter", "topp_only", "topk2000", "topp_only_f32", "filtered16_fwd"):
         from rl_amd.algorithms.logits_sampling_utils import TrainingSamplingParams, apply_temperature_scaling
         from rl_amd.distributed.model_utils import get_next_token_logprobs_from_logits
 
@@ -591,6 +596,8 @@ def bench_workload(args) -> None:
             d = workloads.topk_filter_bf16(device=dev)
         elif w == "topk2000":
             d = workloads.general_filter_bf16(top_k=2000, top_p=0.9, device=dev)
+        elif w == "topp_only_f32":
+            d = workloads.general_filter_bf16(top_k=None, top_p=0.9, device=dev, dtype=torch.float32)
         else:
             d = workloads.general_filter_bf16(top_k=None, top_p=0.9, device=dev)
         raw = d["logits"]
@@ -599,7 +606,7 @@ def bench_workload(args) -> None:
         k, p, T = d["top_k"], d["top_p"], d["temperature"]
         sp = TrainingSamplingParams(top_k=k, top_p=p, temperature=T)
         rows = B * (S - 1)
-        esz = 2
+        esz = raw.element_size()
         scale_bytes = 2 * B * S * V * esz
         fwd_bytes, bwd_bytes = rows * V * esz, B * S * V * esz
         kept_list = k is not None and 1 <= k <= 1024
@@ -662,7 +669,8 @@ def bench_workload(args) -> None:
             step_bytes = scale_bytes + fwd_bytes + bwd_bytes
             cfg = {"workload": {"topk_filter": "topk_topp_temperature_filtered_logprob_fwd_bwd",
                                 "topp_only": "topp_temperature_filtered_logprob_fwd_bwd",
-                                "topk2000": "topk2000_topp_temperature_filtered_logprob_fwd_bwd"}[w],
+                                "topk2000": "topk2000_topp_temperature_filtered_logprob_fwd_bwd",
+                                "topp_only_f32": "fp32_topp_temperature_filtered_logprob_fwd_bwd"}[w],
                    "logits": [B, S, V], "temperature": T, "top_k": k, "top_p": p, "next_token_rows": rows,
                    "call": "apply_temperature_scaling in place, get_next_token_logprobs_from_logits("
                            "sampling_params), backward to the raw logits (the division's backward "
@@ -674,7 +682,7 @@ def bench_workload(args) -> None:
         extra["filtered_fwd_gbps"] = fwd_bytes / (fwd_ms * 1e-3) / 1e9 if fwd_ms > 0 else None
         extra["filtered_bwd_gbps"] = bwd_bytes / (bwd_ms * 1e-3) / 1e9 if bwd_ms > 0 else None
         extra["temperature_scale_gbps"] = scale_bytes / (sc_ms * 1e-3) / 1e9 if sc_ms > 0 else None
-        dtype = "bf16"
+        dtype = "fp32" if esz == 4 else "bf16"
     elif w == "topk_filter_fused":
         from rl_amd.distributed.sampling import filtered_next_token_logprobs
 

@@ -42,14 +42,16 @@ def _gen(seed: int) -> torch.Generator:
     return torch.Generator().manual_seed(seed)
 
 
-def _randn_bf16(shape, std: float, g: torch.Generator, device: Optional[torch.device]) -> torch.Tensor:
-    """N(0, std^2) rounded to bf16, generated in row blocks to bound memory.
+def _randn_bf16(shape, std: float, g: torch.Generator, device: Optional[torch.device],
+                dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """N(0, std^2) rounded to `dtype` (bf16 by default), generated in row blocks to
+    bound memory.
 
     On a GPU device the values come from a device generator seeded from `g`
     (fast); checkers copy the rows they need back to the host.
     """
     B, S, V = shape
-    out = torch.empty(shape, dtype=torch.bfloat16, device=device)
+    out = torch.empty(shape, dtype=dtype, device=device)
     step = max(1, (1 << 26) // V)  # ~64M elements per block
     dev = torch.device(device) if device is not None else torch.device("cpu")
     if dev.type == "cuda":
@@ -60,7 +62,7 @@ def _randn_bf16(shape, std: float, g: torch.Generator, device: Optional[torch.de
         for s0 in range(0, S, step):
             s1 = min(S, s0 + step)
             blk = torch.randn((s1 - s0, V), generator=gd, device=dev) * std
-            out[b, s0:s1].copy_(blk.to(torch.bfloat16))
+            out[b, s0:s1].copy_(blk.to(dtype))
     return out
 
 
@@ -179,27 +181,29 @@ def general_filter_bf16(
     top_p: float = 0.9,
     seed: int = 9,
     device=None,
+    dtype: torch.dtype = torch.bfloat16,
 ):
     """Logits shaped like the filtered workload (N(0, 1) plus one Zipf-ranked +8
     boost per row) for filters that keep large sets (top-p alone, k = 2000);
     targets 90% uniform over each row's kept set (found with a descending sort
-    in chunks of 512 rows), 10% uniform over the vocabulary."""
+    in chunks of 512 rows), 10% uniform over the vocabulary.  `dtype` is the
+    logits dtype (bf16 or fp32)."""
     g = _gen(seed)
     dev = torch.device(device) if device is not None else torch.device("cpu")
-    logits = _randn_bf16((B, S, V), 1.0, g, device)
+    logits = _randn_bf16((B, S, V), 1.0, g, device, dtype)
     perm = torch.randperm(V, generator=g)
     ranks = torch.arange(1, V + 1, dtype=torch.float64)
     pick = torch.multinomial(ranks.pow(-1.1), B * S, replacement=True, generator=g)
     boost_idx = perm[pick].view(B, S).to(dev)
     flat = logits.view(B * S, V)
     rows = torch.arange(B * S, device=dev)
-    flat[rows, boost_idx.view(-1)] = (flat[rows, boost_idx.view(-1)].float() + 8.0).to(torch.bfloat16)
+    flat[rows, boost_idx.view(-1)] = (flat[rows, boost_idx.view(-1)].float() + 8.0).to(dtype)
     u = torch.rand(B * S, generator=g).to(dev)
     outside = torch.randint(0, V, (B * S,), generator=g).to(dev)
     use_inside = torch.rand(B * S, generator=g).to(dev) < 0.9
     inside = torch.empty(B * S, dtype=torch.long, device=dev)
     for a in range(0, B * S, 512):
-        y = (flat[a : a + 512].float() * _recip(temperature, dev)).to(torch.bfloat16).float()
+        y = (flat[a : a + 512].float() * _recip(temperature, dev)).to(dtype).float()
         vals, idx = torch.sort(y, dim=-1, descending=True)
         n_in = torch.full((vals.shape[0],), V, device=dev)
         if top_k is not None and top_k > 0:
