@@ -26,6 +26,7 @@ SOURCES = [
     "advantage.hip",
     "topk_filter.hip",
     "topk_hist.hip",
+    "topk_f32.hip",
     "linear_ce.hip",
     "divergence.hip",
     "packing.hip",

@@ -55,6 +55,10 @@ struct FilterParams {
   float* tk_vals;
   int64_t* tk_idx;
   int64_t tk_base;
+  // fp32 two-pass kernel: sum the mass below the cut's bracket exactly in a
+  // third pass on every row instead of bounding it (environment variable
+  // MIRL_F32_FILTER_EXACT_BELOW=1; tests use it to cover that pass)
+  int f32_exact_below;
 };
 
 // Order-preserving integer key of a float.  -0.0 maps to the key of +0.0: the
@@ -89,8 +93,21 @@ __device__ float block_sum_f(float v, float* red) {
   for (int k = 0; k < NT / 64; ++k) r += red[k];
   return r;
 }
+// Sum over NT threads in double; `red` holds NT / 64 doubles.
 template <int NT>
-__device__ float block_max_f(float v, float* red) {
+__device__ double block_sum_d(double v, double* red) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x % 64, wv = threadIdx.x / 64;
+  __syncthreads();
+  if (lane == 0) red[wv] = v;
+  __syncthreads();
+  double r = 0.0;
+  for (int k = 0; k < NT / 64; ++k) r += red[k];
+  __syncthreads();
+  return r;
+}
+template <int NT>
+__device__ __forceinline__ float block_max_f(float v, float* red) {
   v = wave_max(v);
   const int lane = threadIdx.x % 64, wv = threadIdx.x / 64;
   __syncthreads();
@@ -113,6 +130,51 @@ __device__ int block_sum_i(int v, int* red) {
   return r;
 }
 
+// Cross-lane moves by DPP (no LDS traffic): row_shr:n shifts within rows of 16
+// lanes, row_bcast:15 / row_bcast:31 pass a row's last lane on to the next
+// row(s).  Lanes with no source, and rows outside ROWMASK, read 0, the
+// identity of the sums and unsigned maxima below.
+template <int CTRL, int ROWMASK = 0xf>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROWMASK, 0xf, false);
+}
+template <int CTRL, int ROWMASK = 0xf>
+__device__ __forceinline__ double dpp_f64(double v) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const uint64_t lo = dpp_u32<CTRL, ROWMASK>((uint32_t)u);
+  const uint64_t hi = dpp_u32<CTRL, ROWMASK>((uint32_t)(u >> 32));
+  return __builtin_bit_cast(double, (hi << 32) | lo);
+}
+template <int CTRL, int ROWMASK = 0xf, class T>
+__device__ __forceinline__ T dpp_move(T v) {
+  if constexpr (std::is_same<T, double>::value)
+    return dpp_f64<CTRL, ROWMASK>(v);
+  else if constexpr (std::is_same<T, float>::value)
+    return __uint_as_float(dpp_u32<CTRL, ROWMASK>(__float_as_uint(v)));
+  else
+    return (T)dpp_u32<CTRL, ROWMASK>((uint32_t)v);
+}
+
+// Inclusive scan over the 64 lanes of a wave with op(a, b) (sum, or unsigned
+// max): four in-row steps, then the two row broadcasts.
+struct OpAdd {
+  template <class T>
+  __device__ __forceinline__ T operator()(T a, T b) const { return a + b; }
+};
+struct OpMaxU {
+  __device__ __forceinline__ uint32_t operator()(uint32_t a, uint32_t b) const { return max(a, b); }
+};
+template <class T, class Op = OpAdd>
+__device__ __forceinline__ T wave_scan_dpp(T v, Op op = Op()) {
+  v = op(v, dpp_move<0x111>(v));
+  v = op(v, dpp_move<0x112>(v));
+  v = op(v, dpp_move<0x114>(v));
+  v = op(v, dpp_move<0x118>(v));
+  v = op(v, dpp_move<0x142, 0xa>(v));
+  v = op(v, dpp_move<0x143, 0xc>(v));
+  return v;
+}
+
 // Forward over 16-bit logits by the histogram kernel (topk_hist.hip): every
 // row when all_rows != 0, else only the rows whose info.flags bit 0 is set.
 int launch_hist_rows(const FilterParams& P, int dtype, int64_t rows, int all_rows,
@@ -121,6 +183,10 @@ int launch_hist_rows(const FilterParams& P, int dtype, int64_t rows, int all_row
 // Rewrites every row whose index cut is in rank form (RowInfo.i_cut < 0) into
 // index form (16-bit logits; fp32 rows are always in index form).
 int launch_resolve_rows(const FilterParams& P, int dtype, int64_t rows, hipStream_t st);
+
+// Forward over fp32 logits in two passes (topk_f32.hip), every row; rows it
+// cannot finish are flagged (info.flags bit 0) for filter_general_kernel.
+int launch_f32_rows(const FilterParams& P, int64_t rows, hipStream_t st);
 
 // Largest vocabulary the histogram kernel accepts (its exact-count table
 // covers at most 8 values repeated 65536 times or more).

@@ -26,10 +26,12 @@
 // and the kept-set log-sum-exp.  Rows whose candidates overflow LDS are
 // flagged and redone by the general path.
 //
-// Forward, general path (top-p without top-k, k > 1024, flagged rows): exact
-// multi-pass radix selection over the row (count histograms for the top-k
-// value, probability-mass histograms for the top-p cut), re-reading the row
-// for each 8-bit digit.
+// Forward, general path (top-p without top-k, k > 1024, flagged rows): 16-bit
+// rows go to the histogram kernels (topk_hist.hip), fp32 rows to the two-pass
+// kernel (topk_f32.hip); what those cannot finish (values outside their
+// tables, candidate overflow) to an exact multi-pass radix selection over the
+// row (count histograms for the top-k value, probability-mass histograms for
+// the top-p cut), re-reading the row for each 8-bit digit.
 //
 // Backward: grad = (onehot(t) - p) * g on the kept set, 0 elsewhere, rounded
 // to the logits dtype, then multiplied by fl32(1.0 / T) and rounded to that
@@ -38,6 +40,8 @@
 // rows; a second, small pass stores the kept entries from the kept list saved
 // by the forward (<= kKeepCap entries), without reading the logits.  Rows with
 // larger kept sets are re-read and rewritten whole by the second pass.
+
+#include <cstdlib>
 
 #include "filter.h"
 
@@ -677,6 +681,7 @@ __global__ __launch_bounds__(kGeneralThreads) void filter_general_kernel(FilterP
   __shared__ uint32_t s_sel[2];
   __shared__ double s_below;
   __shared__ int s_cnt;
+  __shared__ int s_grp;  // elements under the last selected digit
   __shared__ uint64_t s_cand[kKeepCap];
 
   const int64_t row = blockIdx.x;
@@ -703,12 +708,14 @@ __global__ __launch_bounds__(kGeneralThreads) void filter_general_kernel(FilterP
   float v_cut = from_okey(thr_key);
   int32_t i_cut = 0;
   if (P.has_p) {
-    float zp = 0.f;
+    // the normaliser summed in double and rounded once; p = fl32(e * fl32(1 / Z))
+    double zp = 0.0;
     for (int64_t j = tid; j < V; j += NT) {
       const float y = yat(j);
-      if (okey(y) >= thr_key) zp += expf(y - m);
+      if (okey(y) >= thr_key) zp += (double)expf(y - m);
     }
-    const float Z = block_sum_f<NT>(zp, redf);
+    const float Z = (float)block_sum_d<NT>(zp, hist_d);
+    const float inv = 1.0f / Z;
     if (tid == 0) s_below = 0.0;
     uint32_t prefix = 0, mask = 0;
     bool done = false;
@@ -725,7 +732,10 @@ __global__ __launch_bounds__(kGeneralThreads) void filter_general_kernel(FilterP
         const int shift = lo;
         const int nb = hi - lo + 1;
         const uint32_t dmask = (nb >= 32) ? 0xffffffffu : ((1u << nb) - 1u);
-        for (int i = tid; i < 256; i += NT) hist_d[i] = 0.0;
+        for (int i = tid; i < 256; i += NT) {
+          hist_d[i] = 0.0;
+          hist_i[i] = 0;
+        }
         __syncthreads();
         for (int64_t j = tid; j < V; j += NT) {
           const float y = yat(j);
@@ -741,7 +751,8 @@ __global__ __launch_bounds__(kGeneralThreads) void filter_general_kernel(FilterP
             if ((jj & imask) != iprefix) continue;
             digit = (jj >> shift) & dmask;
           }
-          atomicAdd(&hist_d[digit], (double)(expf(y - m) / Z));
+          atomicAdd(&hist_d[digit], (double)(expf(y - m) * inv));
+          atomicAdd(&hist_i[digit], 1);
         }
         __syncthreads();
         if (tid == 0) {
@@ -763,6 +774,7 @@ __global__ __launch_bounds__(kGeneralThreads) void filter_general_kernel(FilterP
           }
           s_below = below;
           s_sel[0] = (uint32_t)bsel;
+          s_grp = hist_i[bsel];
         }
         __syncthreads();
         if (phase == 0) {
@@ -775,6 +787,8 @@ __global__ __launch_bounds__(kGeneralThreads) void filter_general_kernel(FilterP
         __syncthreads();
       }
       if (phase == 1) i_cut = (int32_t)iprefix;
+      // a value held by one element needs no index digits (i_cut 0 keeps it)
+      if (phase == 0 && s_grp == 1) done = true;
     }
     v_cut = from_okey(prefix);
   }
@@ -1488,8 +1502,14 @@ int launch_fwd(const FilterParams& P, int64_t rows, hipStream_t st) {
   // the rows left to a general path: all of them, or those the fast kernel flagged
   if (sizeof(typename E::raw) == 2 && P.V <= kHistMaxV)
     return launch_hist_rows(P, dtype_code<E>(), rows, fast ? 0 : 1, st);
+  bool all = !fast;
+  if (std::is_same<E, F32>::value && !fast) {
+    // fp32 rows in two passes; the rows it flags go to the radix kernel
+    if (int e = launch_f32_rows(P, rows, st)) return e;
+    all = false;
+  }
   hipLaunchKernelGGL((filter_general_kernel<E>), dim3((unsigned)rows), dim3(kGeneralThreads), 0, st,
-                     P, fast ? 0 : 1);
+                     P, all ? 1 : 0);
   return check_launch("filter_general_kernel");
 }
 
@@ -1622,6 +1642,8 @@ FilterParams make_params(const void* logits, int64_t R, int64_t V, int64_t sb, i
   P.tk_vals = nullptr;
   P.tk_idx = nullptr;
   P.tk_base = 0;
+  const char* ex = std::getenv("MIRL_F32_FILTER_EXACT_BELOW");
+  P.f32_exact_below = (ex != nullptr && ex[0] == '1') ? 1 : 0;
   return P;
 }
 

@@ -166,49 +166,6 @@ __device__ uint32_t block_max_u(uint32_t v, uint32_t* red) {
   return r;
 }
 
-// Cross-lane moves by DPP (no LDS traffic): row_shr:n shifts within rows of 16
-// lanes, row_bcast:15 / row_bcast:31 pass a row's last lane on to the next
-// row(s).  Lanes with no source, and rows outside ROWMASK, read 0, the
-// identity of the sums and unsigned maxima below.
-template <int CTRL, int ROWMASK = 0xf>
-__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
-  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROWMASK, 0xf, false);
-}
-template <int CTRL, int ROWMASK = 0xf>
-__device__ __forceinline__ double dpp_f64(double v) {
-  const uint64_t u = __builtin_bit_cast(uint64_t, v);
-  const uint64_t lo = dpp_u32<CTRL, ROWMASK>((uint32_t)u);
-  const uint64_t hi = dpp_u32<CTRL, ROWMASK>((uint32_t)(u >> 32));
-  return __builtin_bit_cast(double, (hi << 32) | lo);
-}
-template <int CTRL, int ROWMASK = 0xf, class T>
-__device__ __forceinline__ T dpp_move(T v) {
-  if constexpr (std::is_same<T, double>::value)
-    return dpp_f64<CTRL, ROWMASK>(v);
-  else
-    return (T)dpp_u32<CTRL, ROWMASK>((uint32_t)v);
-}
-
-// Inclusive scan over the 64 lanes of a wave with op(a, b) (sum, or unsigned
-// max): four in-row steps, then the two row broadcasts.
-struct OpAdd {
-  template <class T>
-  __device__ __forceinline__ T operator()(T a, T b) const { return a + b; }
-};
-struct OpMaxU {
-  __device__ __forceinline__ uint32_t operator()(uint32_t a, uint32_t b) const { return max(a, b); }
-};
-template <class T, class Op = OpAdd>
-__device__ __forceinline__ T wave_scan_dpp(T v, Op op = Op()) {
-  v = op(v, dpp_move<0x111>(v));
-  v = op(v, dpp_move<0x112>(v));
-  v = op(v, dpp_move<0x114>(v));
-  v = op(v, dpp_move<0x118>(v));
-  v = op(v, dpp_move<0x142, 0xa>(v));
-  v = op(v, dpp_move<0x143, 0xc>(v));
-  return v;
-}
-
 // Workgroup-wide exclusive scan (thread order) and total with one barrier.
 // `red` (NW entries) must be used by no other reduction of the same kernel
 // invocation, so no barrier is needed before it is written.
