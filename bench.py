@@ -730,7 +730,8 @@ def bench_workload(args) -> None:
 
         lce_kernels = (["mirl_linear_ce_fwd", "mirl_linear_ce_grad", "mirl_gemm_bf16_abt",
                         "mirl_transpose_bf16", "mirl_sum_splits_bf16"] if args.dtype != "fp32" else
-                       ["mirl_logprob_fwd", "mirl_logprob_bwd"])
+                       ["mirl_gemm_f32_abt", "mirl_logprob_fwd", "mirl_logprob_bwd", "mirl_transpose_f32",
+                        "mirl_sum_splits_bf16"])
         region = {}
         ms_step, ms = _timed(step, args.steps, args.warmup, lce_kernels, region_events=region)
         rows = B * (S - 1)
@@ -750,11 +751,13 @@ def bench_workload(args) -> None:
         tflops = gemm / (fwd_ms * 1e-3) / 1e12 if fwd_ms > 0 else 0.0
         peak = PEAK_FP32_TFLOPS if args.dtype == "fp32" else PEAK_BF16_TFLOPS
         if args.dtype == "fp32":
-            # library GEMMs per chunk plus the logprob row kernels: the whole step's
-            # algorithmic flops over its GPU time (one event pair around the timed steps)
+            # the fp32 tile loop per chunk (forward logits; per backward block the active
+            # rows' logits, dH and dW) plus the logprob row kernels and the transposes: the
+            # whole step's algorithmic flops over its GPU time (one event pair around the
+            # timed steps)
             gpu_ms = region.get("gpu_ms_per_step", ms_step)
             tflops = (gemm + 3 * gemm_act) / (gpu_ms * 1e-3) / 1e12
-            roof = {"kernel": "step (library fp32 GEMMs + mirl_logprob_fwd/bwd)", "bound": "mfma",
+            roof = {"kernel": "step (mirl_gemm_f32_abt + mirl_logprob_fwd/bwd)", "bound": "mfma",
                     "achieved": tflops, "peak": peak, "unit": "TFLOP/s", "frac": tflops / peak,
                     "traffic": None, "algorithmic_flops": gemm + 3 * gemm_act}
         else:

@@ -487,9 +487,26 @@ int mirl_gemm_bf16_abt(const void* A, int64_t lda, const void* B, int64_t ldb, i
                        const int64_t* count, int64_t count_off, int count_axis,
                        int64_t final_at, void* stream);
 
+/* C = A[:, :K] . B[:, :K]^T in fp32 (A [M, >=K], B [N, >=K] fp32, row strides lda,
+ * ldb multiples of 4 elements, 16-byte aligned; K a multiple of 64) on the same
+ * MFMA tile loop, each 16-byte operand fragment feeding four
+ * v_mfma_f32_32x32x2_f32.  C: fp32 [M, ldc] (C = or, with accumulate, C +=),
+ * or [k_splits][M][ldc] partial products over k_splits ranges of K (ranges of
+ * round_up(ceil(K / k_splits), 64), each non-empty).  `count` as for
+ * mirl_gemm_bf16_abt (MIRL_COUNT_ROWS: rows of A at or past *count - count_off
+ * are neither read nor written; MIRL_COUNT_K: the reduction stops at
+ * round_up(*count - count_off, 64), and with accumulate set an empty reduction
+ * writes nothing).
+ * Replaces: the fp32 matmuls of ChunkedDistributedHiddenStatesToLogprobs
+ * (nemo_rl/distributed/model_utils.py:2611-2616 logits, 2701-2716 dH and dW). */
+int mirl_gemm_f32_abt(const float* A, int64_t lda, const float* B, int64_t ldb, int64_t M,
+                      int64_t N, int64_t K, int64_t k_splits, float* C, int64_t ldc,
+                      int accumulate, const int64_t* count, int64_t count_off, int count_axis,
+                      void* stream);
+
 /* out[r(m), n] = out_dtype(sum_s part[s, m, n]) summed in s order (part [k_splits][M][ld]
- * fp32, out row stride ldo, out_dtype MIRL_DTYPE_BF16 or MIRL_DTYPE_F16): the
- * splits of mirl_gemm_bf16_abt.  r(m) = out_rows[m]
+ * fp32, out row stride ldo, out_dtype MIRL_DTYPE_BF16, MIRL_DTYPE_F16 or
+ * MIRL_DTYPE_F32): the splits of mirl_gemm_bf16_abt / mirl_gemm_f32_abt.  r(m) = out_rows[m]
  * (a device int64 row map; rows mapped outside [0, out_nrows) are skipped) or m
  * when out_rows is NULL.  With `count` (a device int64, or NULL), rows
  * m >= *count - count_off are written as zeros without reading part.
@@ -509,6 +526,15 @@ int mirl_sum_splits_bf16(const float* part, int64_t k_splits, int64_t M, int64_t
 int mirl_transpose_bf16(const void* src, int src_dtype, int64_t R, int64_t C, int64_t lds,
                         void* dst, int64_t ldd, int64_t R_pad, const int64_t* count,
                         void* stream);
+
+/* dst[c, r] = src[r, c] in fp32 for r < R, c < C, and 0 for R <= r < R_pad (src row
+ * stride lds, dst row stride ldd >= R_pad), R = min(R, *count - count_off) when
+ * `count` (a device int64) is given: the transposed operands of the fp32
+ * hidden-state backward (W, the active hidden rows, the logits gradient).
+ * Replaces: the transposes inside the fp32 dH / dW matmuls (model_utils.py:2701-2716). */
+int mirl_transpose_f32(const float* src, int64_t R, int64_t C, int64_t lds, float* dst,
+                       int64_t ldd, int64_t R_pad, const int64_t* count, int64_t count_off,
+                       void* stream);
 
 /* ---------------------------------------------------------------------- */
 /* ClippedPG loss epilogue                                                  */

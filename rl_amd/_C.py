@@ -226,6 +226,10 @@ SIGNATURES = {
     "mirl_sum_splits_bf16": (_I, [_P, _I64, _I64, _I64, _I64, _P, _I64, _I, _P, _I64, _P, _I64,
                                   _P]),
     "mirl_transpose_bf16": (_I, [_P, _I, _I64, _I64, _I64, _P, _I64, _I64, _P, _P]),
+    "mirl_gemm_f32_abt": (
+        _I, [_P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _I, _P, _I64, _I, _P]
+    ),
+    "mirl_transpose_f32": (_I, [_P, _I64, _I64, _I64, _P, _I64, _I64, _P, _I64, _P]),
     "mirl_top_k_top_p_mask": (
         _I,
         [_P, _I, _I64, _I64, _I64, _I, ctypes.c_double, _I, _P, _P, _P, _P, _I64, _P, _I64, _P],
@@ -1253,18 +1257,59 @@ def gemm_bf16_abt(a: torch.Tensor, b: torch.Tensor, k: int, out: torch.Tensor, k
     _check(st, "mirl_gemm_bf16_abt")
 
 
+def gemm_f32_abt(a: torch.Tensor, b: torch.Tensor, k: int, out: torch.Tensor, k_splits: int = 1,
+                 accumulate: bool = False, count: Optional[torch.Tensor] = None,
+                 count_off: int = 0, count_axis: int = COUNT_ROWS) -> None:
+    """out = a[:, :k] . b[:, :k]^T in fp32 on the MFMA units (fp32 MFMA).
+
+    a [M, >=k], b [N, >=k] fp32 (unit stride, row strides multiples of 4 elements,
+    16-byte aligned, k a multiple of 64); out fp32 [M, N] (out = or +=), or
+    [k_splits, M, N] (one partial product per k range).  `count` (device int64, one
+    element) with c = count - count_off: COUNT_ROWS leaves rows of a at or past c
+    absent (not read, not written); COUNT_K stops the reduction at round_up(c, 64)."""
+    dev = _require_gpu(a, b, out)
+    _check_count(count, dev)
+    _require(a.dtype == torch.float32 and b.dtype == torch.float32 and out.dtype == torch.float32,
+             "fp32 operands and output")
+    _require(a.stride(-1) == 1 and b.stride(-1) == 1 and out.stride(-1) == 1, "unit stride on the last dim")
+    M, N = a.shape[0], b.shape[0]
+    st = _launch(
+        "mirl_gemm_f32_abt", dev, a.data_ptr(), a.stride(0), b.data_ptr(), b.stride(0), M, N, int(k),
+        int(k_splits), out.data_ptr(), out.stride(-2), int(bool(accumulate)), _ptr(count), int(count_off),
+        int(count_axis), _stream(dev),
+    )
+    _check(st, "mirl_gemm_f32_abt")
+
+
+def transpose_f32(src: torch.Tensor, rows: int, dst: torch.Tensor, count: Optional[torch.Tensor] = None,
+                  count_off: int = 0) -> None:
+    """dst[c, r] = src[r, c] (fp32) for r < rows, zero for rows <= r < dst.shape[1]; rows is
+    lowered to count - count_off (`count` a device int64, one element) when that is given."""
+    dev = _require_gpu(src, dst)
+    _check_count(count, dev)
+    _require(src.dtype == torch.float32 and dst.dtype == torch.float32, "fp32 source and destination")
+    _require(src.stride(-1) == 1 and dst.stride(-1) == 1, "unit stride on the last dim")
+    C = src.shape[1]
+    _require(dst.shape[0] >= C, "dst has a row per source column")
+    _require(src.shape[0] >= rows, "src has the rows to transpose")
+    st = _launch("mirl_transpose_f32", dev, src.data_ptr(), int(rows), C, src.stride(0), dst.data_ptr(),
+                 dst.stride(0), dst.shape[1], _ptr(count), int(count_off), _stream(dev))
+    _check(st, "mirl_transpose_f32")
+
+
 def sum_splits_bf16(part: torch.Tensor, out: torch.Tensor, count: Optional[torch.Tensor] = None,
                     count_off: int = 0, out_rows: Optional[torch.Tensor] = None) -> None:
-    """out [M, N] bf16 or fp16 = sum over dim 0 of part [S, M, N] fp32, in order; with `count`,
+    """out [M, N] bf16, fp16 or fp32 = sum over dim 0 of part [S, M, N] fp32, in order; with `count`,
     rows at or past count - count_off are zeros (part not read there).  With `out_rows`
     (int64 [M] on the device) row m goes to out[out_rows[m]] instead (out [R, N], rows
     mapped outside [0, R) skipped)."""
     dev = _require_gpu(part, out)
     _check_count(count, dev)
     S, M, N = part.shape
-    _require(part.is_contiguous() and part.dtype == torch.float32 and out.dtype in _LCE_DTYPES
+    _require(part.is_contiguous() and part.dtype == torch.float32
+             and (out.dtype in _LCE_DTYPES or out.dtype == torch.float32)
              and out.stride(-1) == 1 and out.dim() == 2 and out.shape[1] == N,
-             "contiguous fp32 partials and a bf16 or fp16 [R, N] output")
+             "contiguous fp32 partials and a bf16, fp16 or fp32 [R, N] output")
     if out_rows is None:
         _require(out.shape[0] == M, "out has the partials' rows")
     else:

@@ -60,6 +60,24 @@ struct Mma<F16> {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
   }
 };
+// fp32 operands (plain GEMM only): a 16-byte fragment holds four hidden
+// elements of a row, k = (l / 32) * 4 + 0..3, and feeds four
+// v_mfma_f32_32x32x2_f32, element e of both fragments to the e-th one.  That
+// instruction takes A[l % 32][l / 32] and B[l / 32][l % 32] from lane l, so the
+// four together sum the products over the fragment's eight hidden elements
+// (element e of the lanes below 32 is k = e, of the others k = 4 + e), in the
+// same accumulator layout as the 16-bit instructions.
+template <>
+struct Mma<F32> {
+  typedef float frag __attribute__((ext_vector_type(4)));
+  __device__ __forceinline__ static f32x16 run(frag a, frag b, f32x16 c) {
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(a[0], b[0], c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(a[1], b[1], c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(a[2], b[2], c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(a[3], b[3], c, 0, 0, 0);
+    return c;
+  }
+};
 
 // 16-bit element bits <-> fp32 for a dtype E (round to nearest even).
 template <class E>
@@ -74,13 +92,14 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 constexpr int kBM = 256;                 // rows per tile
 constexpr int kBN = 256;                 // vocabulary columns per tile
-constexpr int kSK = 64;                  // hidden elements per LDS stage
+constexpr int kSK = 64;                  // 16-bit hidden elements per LDS stage (128 bytes)
 constexpr int kStages = 2;
 constexpr int kThreads = 256;            // 4 waves in a 2 x 2 arrangement
 constexpr int kWaves = kThreads / kWave;
 constexpr int kWM = 128, kWN = 128;      // per-wave quarter
 constexpr int kTM = kWM / 32, kTN = kWN / 32;
 constexpr int kRowBytes = kSK * 2;       // 128 B: one tile row of a stage
+constexpr int kKK = kRowBytes / 32;      // fragment steps per stage (two 16-byte chunks each)
 constexpr int kHalfBytes = kBM * kRowBytes;    // 32 KB: the H (or W) rows of a stage
 constexpr int kStageBytes = 2 * kHalfBytes;    // 64 KB
 constexpr int kDmaBytes = kWave * 16;          // one direct load: 64 lanes x 16 B = 8 rows
@@ -121,8 +140,8 @@ __device__ __forceinline__ void wait_vm_barrier() {
 enum LceMode { kFwd = 0, kGrad = 1, kGemm = 2 };
 
 struct LceParams {
-  const uint16_t* h;  // [T, Hd] bf16 or fp16 (the kernel's E), row stride ldh
-  const uint16_t* w;  // [V, Hd] of the same dtype, row stride ldw
+  const void* h;  // [T, Hd] of the kernel's E (bf16, fp16; fp32 for the plain GEMM), row stride ldh
+  const void* w;  // [V, Hd] of the same dtype, row stride ldw
   int64_t ldh, ldw;
   int64_t V, Hd;
   int64_t row0, nrows;  // rows handled: [row0, row0 + nrows)
@@ -166,6 +185,9 @@ template <int MODE, class E>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void lce_tile_kernel(LceParams P) {
   using frag = typename Mma<E>::frag;
+  static_assert(MODE == kGemm || sizeof(typename E::raw) == 2, "fp32 operands: plain GEMM only");
+  constexpr int kES = (int)sizeof(typename E::raw);  // bytes per element
+  constexpr int kSKE = kRowBytes / kES;              // hidden elements per stage
   // Two arrays rather than one, so that the compiler tracks the direct loads
   // into each stage on their own and an LDS read waits only for its stage.
   __shared__ __align__(1024) unsigned char st0[kStageBytes];
@@ -191,7 +213,7 @@ void lce_tile_kernel(LceParams P) {
     if (MODE != kGemm || P.count_axis == 0) {
       if (c < row_end) row_end = c;
     } else {
-      constexpr int64_t kstep = kStages * kSK;
+      constexpr int64_t kstep = kStages * kSKE;
       const int64_t ke = c <= 0 ? 0 : (c + kstep - 1) / kstep * kstep;
       if (ke < k_end) k_end = ke;
       if (ke == 0 && P.accumulate) return;
@@ -292,7 +314,7 @@ void lce_tile_kernel(LceParams P) {
   const int64_t kbase = (MODE == kGemm) ? ks * P.kb_len : 0;
   const int64_t krest = k_end - kbase < 0 ? 0 : k_end - kbase;
   const int64_t klen = (MODE == kGemm) ? (krest < P.kb_len ? krest : P.kb_len) : P.Hd;
-  const int nst = (int)(klen / kSK);  // a multiple of kStages (0: an empty reduction)
+  const int nst = (int)(klen / kSKE);  // a multiple of kStages (0: an empty reduction)
   if (MODE == kGemm && nst == 0) {
     // an empty reduction range (a reduction-length count, or a split past it):
     // the product is zero; handled here, before the accumulators exist
@@ -311,19 +333,19 @@ void lce_tile_kernel(LceParams P) {
   const int64_t a_rows = (row_end - m0 < kBM) ? (row_end - m0) : kBM;
   const int64_t b_rows = (P.V - n0 < kBN) ? (P.V - n0) : kBN;
   const __amdgpu_buffer_rsrc_t rsrc_a = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(P.h + m0 * P.ldh + kbase), 0, (int)((a_rows * P.ldh - kbase) * 2),
-      0x00020000);
+      const_cast<char*>(static_cast<const char*>(P.h) + (m0 * P.ldh + kbase) * kES), 0,
+      (int)((a_rows * P.ldh - kbase) * kES), 0x00020000);
   const __amdgpu_buffer_rsrc_t rsrc_b = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint16_t*>(P.w + n0 * P.ldw + kbase), 0, (int)((b_rows * P.ldw - kbase) * 2),
-      0x00020000);
+      const_cast<char*>(static_cast<const char*>(P.w) + (n0 * P.ldw + kbase) * kES), 0,
+      (int)((b_rows * P.ldw - kbase) * kES), 0x00020000);
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   int voff_a[kDmaPerWave], voff_b[kDmaPerWave];
 #pragma unroll
   for (int i = 0; i < kDmaPerWave; ++i) {
     const int row = (wave * kDmaPerWave + i) * kDmaRows + (lane >> 3);
     const int chunk = (lane & 7) ^ ((row >> 1) & 7);
-    voff_a[i] = (int)(row * P.ldh * 2) + chunk * 16;
-    voff_b[i] = (int)(row * P.ldw * 2) + chunk * 16;
+    voff_a[i] = (int)(row * P.ldh * kES) + chunk * 16;
+    voff_b[i] = (int)(row * P.ldw * kES) + chunk * 16;
   }
   // load q of stage data t: q < kDmaPerWave is an H block, else a W block
   auto dma = [&](unsigned char* stage, int t, int q) {
@@ -341,9 +363,9 @@ void lce_tile_kernel(LceParams P) {
 
   // fragment read offsets: row (wm*128 | wn*128) + i*32 + (lane & 31), chunk kk*2 + (lane >> 5)
   const int frow = lane & 31;
-  int frag_off[kSK / 16];
+  int frag_off[kKK];
 #pragma unroll
-  for (int kk = 0; kk < kSK / 16; ++kk) frag_off[kk] = lds_off(frow, kk * 2 + (lane >> 5));
+  for (int kk = 0; kk < kKK; ++kk) frag_off[kk] = lds_off(frow, kk * 2 + (lane >> 5));
   frag fa[2][kTM], fb[2][kTN];
   auto fread = [&](int set, const unsigned char* stage, int kk, int idx) {
     // idx < kTM: A fragment idx; else B fragment idx - kTM
@@ -378,7 +400,7 @@ void lce_tile_kernel(LceParams P) {
   for (int idx = 0; idx < kTM + kTN; ++idx) fread(0, st0, 0, idx);
 
   // One stage t (S = t % 2): four MFMA blocks kk = 0..3 of 16 MFMAs (16 hidden
-  // elements each).  While block kk runs on fragment set kk % 2, block kk + 1's
+  // elements each for 16-bit operands; for fp32, 8 elements in four instructions).  While block kk runs on fragment set kk % 2, block kk + 1's
   // fragments are read into the other set.  Before block 3 this wave waits for
   // its loads of stage data t + 1 (the only ones in flight) and the workgroup
   // barrier makes every wave's loads visible and ends every read of stage S
@@ -464,9 +486,7 @@ void lce_tile_kernel(LceParams P) {
             }
           }
     }
-    return;
-  }
-
+  } else {
   // ---- epilogue: the tile goes through LDS as bf16, one row per thread ----
   //
   // The accumulators of a row are spread over 32 lanes; instead of cross-lane
@@ -599,6 +619,7 @@ void lce_tile_kernel(LceParams P) {
       }
     }
   }
+  }  // the fused epilogues
 }
 
 // dst[c][r] = bf16(src[r][c]) for r < R, c < C, and dst[c][r] = 0 for
@@ -631,7 +652,37 @@ __global__ __launch_bounds__(256) void transpose_bf16_kernel(const uint16_t* __r
   }
 }
 
-// out[r(m)][n] = EO(sum over s of part[s][m][n]) (EO bf16 or fp16), summed in split order,
+// dst[c][r] = src[r][c] for r < R, c < C, and dst[c][r] = 0 for R <= r < Rp
+// (fp32; dst rows of stride ldd >= Rp), R = min(R, *count - count_off) when
+// count is given.  64 x 64 tiles through LDS.
+__global__ __launch_bounds__(256) void transpose_f32_kernel(const float* __restrict__ src, int64_t R,
+                                                            int64_t C, int64_t lds,
+                                                            float* __restrict__ dst, int64_t ldd,
+                                                            int64_t Rp, int64_t n_ct,
+                                                            const int64_t* __restrict__ count,
+                                                            int64_t count_off) {
+  __shared__ float tile[64][65];
+  if (count != nullptr) {
+    const int64_t c = *count - count_off;
+    if (c < R) R = c < 0 ? 0 : c;
+  }
+  const int64_t tr = blockIdx.x / n_ct, tc = blockIdx.x - tr * n_ct;
+  const int64_t r0 = tr * 64, c0 = tc * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+#pragma unroll 4
+  for (int k = 0; k < 16; ++k) {
+    const int64_t r = r0 + ty + 4 * k, c = c0 + tx;
+    tile[ty + 4 * k][tx] = (r < R && c < C) ? src[r * lds + c] : 0.f;
+  }
+  __syncthreads();
+#pragma unroll 4
+  for (int k = 0; k < 16; ++k) {
+    const int64_t c = c0 + ty + 4 * k, r = r0 + tx;
+    if (c < C && r < Rp) dst[c * ldd + r] = tile[tx][ty + 4 * k];
+  }
+}
+
+// out[r(m)][n] = EO(sum over s of part[s][m][n]) (EO bf16, fp16 or fp32), summed in split order,
 // with r(m) = out_rows[m] when a row map is given (rows mapped outside
 // [0, out_nrows) are skipped) and m otherwise; with a count, rows
 // m >= *count - count_off are written as zeros without reading.  VEC
@@ -639,7 +690,7 @@ __global__ __launch_bounds__(256) void transpose_bf16_kernel(const uint16_t* __r
 template <int VEC, class EO>
 __global__ __launch_bounds__(256) void sum_splits_kernel(const float* __restrict__ part,
                                                          int64_t n_ks, int64_t M, int64_t N,
-                                                         int64_t ld, uint16_t* __restrict__ out,
+                                                         int64_t ld, void* __restrict__ out,
                                                          int64_t ldo,
                                                          const int64_t* __restrict__ out_rows,
                                                          int64_t out_nrows,
@@ -671,14 +722,24 @@ __global__ __launch_bounds__(256) void sum_splits_kernel(const float* __restrict
       }
     }
   }
-  uint16_t* dst = out + r * ldo + n;
-  if constexpr (VEC == 4) {
-    const uint32_t lo = (uint32_t)bits_of<EO>(acc[0]) | ((uint32_t)bits_of<EO>(acc[1]) << 16);
-    const uint32_t hi = (uint32_t)bits_of<EO>(acc[2]) | ((uint32_t)bits_of<EO>(acc[3]) << 16);
-    *reinterpret_cast<uint2*>(dst) = uint2{lo, hi};
-  } else {
+  if constexpr (std::is_same<EO, F32>::value) {
+    float* dst = static_cast<float*>(out) + r * ldo + n;
+    if constexpr (VEC == 4) {
+      *reinterpret_cast<float4*>(dst) = float4{acc[0], acc[1], acc[2], acc[3]};
+    } else {
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) dst[e] = bits_of<EO>(acc[e]);
+      for (int e = 0; e < VEC; ++e) dst[e] = acc[e];
+    }
+  } else {
+    uint16_t* dst = static_cast<uint16_t*>(out) + r * ldo + n;
+    if constexpr (VEC == 4) {
+      const uint32_t lo = (uint32_t)bits_of<EO>(acc[0]) | ((uint32_t)bits_of<EO>(acc[1]) << 16);
+      const uint32_t hi = (uint32_t)bits_of<EO>(acc[2]) | ((uint32_t)bits_of<EO>(acc[3]) << 16);
+      *reinterpret_cast<uint2*>(dst) = uint2{lo, hi};
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) dst[e] = bits_of<EO>(acc[e]);
+    }
   }
 }
 
@@ -937,28 +998,32 @@ extern "C" int mirl_sum_splits_bf16(const float* part, int64_t k_splits, int64_t
                                     const int64_t* out_rows, int64_t out_nrows,
                                     const int64_t* count, int64_t count_off, void* stream) {
   clear_error();
-  MIRL_REQUIRE(lce_dtype_ok(out_dtype), "the output must be bf16 or fp16 (dtype code %d)", out_dtype);
+  MIRL_REQUIRE(lce_dtype_ok(out_dtype) || out_dtype == MIRL_DTYPE_F32,
+               "the output must be bf16, fp16 or fp32 (dtype code %d)", out_dtype);
   MIRL_REQUIRE(M >= 0 && N >= 0 && k_splits >= 1 && ld >= N && ldo >= N, "invalid shape");
   if (M == 0 || N == 0) return MIRL_OK;
   MIRL_REQUIRE(part && out, "null pointer argument");
   MIRL_REQUIRE(out_rows == nullptr || out_nrows >= 0, "invalid output row count");
   hipStream_t st = static_cast<hipStream_t>(stream);
+  const uintptr_t out_align = out_dtype == MIRL_DTYPE_F32 ? 15u : 7u;  // 4 elements
   const bool vec4 = N % 4 == 0 && ld % 4 == 0 && ldo % 4 == 0 &&
                     (reinterpret_cast<uintptr_t>(part) & 15u) == 0 &&
-                    (reinterpret_cast<uintptr_t>(out) & 7u) == 0;
+                    (reinterpret_cast<uintptr_t>(out) & out_align) == 0;
   auto launch = [&](auto vec_c, auto eo) {
     constexpr int VEC = decltype(vec_c)::value;
     using EO = decltype(eo);
     hipLaunchKernelGGL((sum_splits_kernel<VEC, EO>), dim3((unsigned)ceil_div(M * N / VEC, 256)),
-                       dim3(256), 0, st, part, k_splits, M, N, ld, static_cast<uint16_t*>(out), ldo,
-                       out_rows, out_nrows, count, count_off);
+                       dim3(256), 0, st, part, k_splits, M, N, ld, out, ldo, out_rows, out_nrows,
+                       count, count_off);
   };
   using V4 = std::integral_constant<int, 4>;
   using V1 = std::integral_constant<int, 1>;
   if (out_dtype == MIRL_DTYPE_BF16) {
     if (vec4) launch(V4{}, BF16{}); else launch(V1{}, BF16{});
-  } else {
+  } else if (out_dtype == MIRL_DTYPE_F16) {
     if (vec4) launch(V4{}, F16{}); else launch(V1{}, F16{});
+  } else {
+    if (vec4) launch(V4{}, F32{}); else launch(V1{}, F32{});
   }
   return check_launch("mirl_sum_splits_bf16");
 }
@@ -981,4 +1046,78 @@ extern "C" int mirl_transpose_bf16(const void* src, int src_dtype, int64_t R, in
   };
   if (src_dtype == MIRL_DTYPE_BF16) launch(BF16{}); else launch(F16{});
   return check_launch("mirl_transpose_bf16");
+}
+
+extern "C" int mirl_gemm_f32_abt(const float* A, int64_t lda, const float* B, int64_t ldb, int64_t M,
+                                 int64_t N, int64_t K, int64_t k_splits, float* C, int64_t ldc,
+                                 int accumulate, const int64_t* count, int64_t count_off,
+                                 int count_axis, void* stream) {
+  clear_error();
+  MIRL_REQUIRE(M >= 0 && N >= 0 && K > 0 && k_splits >= 1, "invalid shape M=%lld N=%lld K=%lld splits=%lld",
+               (long long)M, (long long)N, (long long)K, (long long)k_splits);
+  if (M == 0 || N == 0) return MIRL_OK;
+  MIRL_REQUIRE(A && B && C, "null pointer argument");
+  const int64_t kstep = (int64_t)kStages * (kRowBytes / 4);
+  MIRL_REQUIRE(K % kstep == 0, "reduction length %lld must be a multiple of %lld", (long long)K,
+               (long long)kstep);
+  const int64_t kb = ceil_div(ceil_div(K, k_splits), kstep) * kstep;
+  const int64_t n_ks = ceil_div(K, kb);
+  MIRL_REQUIRE(n_ks == k_splits,
+               "%lld splits of K=%lld in ranges of %lld leave %lld non-empty (choose a split count "
+               "that divides into whole 64-element ranges)",
+               (long long)k_splits, (long long)K, (long long)kb, (long long)n_ks);
+  MIRL_REQUIRE(count_axis == MIRL_COUNT_ROWS || count_axis == MIRL_COUNT_K, "invalid count axis %d",
+               count_axis);
+  MIRL_REQUIRE(!accumulate || n_ks == 1, "accumulation takes one split");
+  MIRL_REQUIRE(lda % 4 == 0 && ldb % 4 == 0 && lda >= K && ldb >= K,
+               "row strides (%lld, %lld) must be multiples of 4 elements and >= K", (long long)lda,
+               (long long)ldb);
+  MIRL_REQUIRE((reinterpret_cast<uintptr_t>(A) & 15u) == 0 && (reinterpret_cast<uintptr_t>(B) & 15u) == 0,
+               "operands must be 16-byte aligned");
+  // buffer ranges of one 256-row tile are 32-bit byte counts
+  MIRL_REQUIRE(kBM * lda * 4 < (int64_t(1) << 31) && kBN * ldb * 4 < (int64_t(1) << 31),
+               "row strides (%lld, %lld) too large", (long long)lda, (long long)ldb);
+  MIRL_REQUIRE(M < (int64_t(1) << 31) && N < (int64_t(1) << 31), "sizes exceed 2^31-1");
+  MIRL_REQUIRE(ldc >= N, "output row stride %lld is smaller than N=%lld", (long long)ldc, (long long)N);
+  LceParams P{};
+  P.h = A;
+  P.w = B;
+  P.ldh = lda;
+  P.ldw = ldb;
+  P.V = N;
+  P.Hd = K;
+  P.row0 = 0;
+  P.nrows = M;
+  P.n_mt = ceil_div(M, kBM);
+  P.n_nt = ceil_div(N, kBN);
+  P.n_ks = n_ks;
+  P.kb_len = kb;
+  P.C = C;
+  P.Cb = nullptr;
+  P.ldc = ldc;
+  P.accumulate = accumulate;
+  P.count = count;
+  P.count_off = count_off;
+  P.count_axis = count_axis;
+  P.final_at = 0;
+  const int64_t grid = ceil_div(P.n_mt * P.n_nt * n_ks, kXcds) * kXcds;
+  MIRL_REQUIRE(grid < (int64_t(1) << 31), "too many tiles");
+  hipLaunchKernelGGL((lce_tile_kernel<kGemm, F32>), dim3((unsigned)grid), dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), P);
+  return check_launch("mirl_gemm_f32_abt");
+}
+
+extern "C" int mirl_transpose_f32(const float* src, int64_t R, int64_t C, int64_t lds, float* dst,
+                                  int64_t ldd, int64_t R_pad, const int64_t* count, int64_t count_off,
+                                  void* stream) {
+  clear_error();
+  MIRL_REQUIRE(R >= 0 && C >= 0 && R_pad >= R && lds >= C && ldd >= R_pad, "invalid shape");
+  if (C == 0 || R_pad == 0) return MIRL_OK;
+  MIRL_REQUIRE(src && dst, "null pointer argument");
+  const int64_t n_rt = ceil_div(R_pad, 64), n_ct = ceil_div(C, 64);
+  MIRL_REQUIRE(n_rt * n_ct < (int64_t(1) << 31), "too many tiles");
+  hipLaunchKernelGGL(transpose_f32_kernel, dim3((unsigned)(n_rt * n_ct)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), src, R, C, lds, dst, ldd, R_pad, n_ct, count,
+                     count_off);
+  return check_launch("mirl_transpose_f32");
 }

@@ -25,15 +25,23 @@ is ``[V, H]``; targets are ``[B, S]``.
   exponent range would flush the small ``-p * g`` terms of the vocabulary's
   tail, which together make up most of ``dH``; the transposes round fp16 W and
   H to bf16 for those two products.
-* fp32 hidden states and weights take the reference's chunked shape instead:
-  per chunk of sequence positions the logits are one library GEMM in fp32 (the
-  reference's ``torch.matmul`` output), and the row kernels of the logits path
+* fp32 hidden states and weights keep the reference's chunked shape on this
+  library's kernels: per chunk of sequence positions the fp32 logits are one
+  product on the same MFMA tile loop with fp32 operands (``mirl_gemm_f32_abt``,
+  four ``v_mfma_f32_32x32x2_f32`` per 16-byte fragment pair; the reference's
+  ``torch.matmul`` output), and the row kernels of the logits path
   (``mirl_logprob_fwd`` / ``mirl_logprob_bwd``) form the logprobs and, in
-  place, the logits gradient; ``dH`` and ``dW`` are library GEMMs over it,
-  ``dW`` accumulated in fp32 across chunks.  An fp32 GEMM here is bound by the
-  fp32 MFMA rate (1/16 of bf16's) at over a thousand flops per byte of logits,
-  so the per-chunk logits write and read that fusion would save cost under 1%
-  of the step.
+  place, the logits gradient.  The backward moves the rows with a non-zero
+  upstream gradient to the front and counts them on the device, as above; per
+  block of one chunk of rows it recomputes their logits, forms G in place,
+  and runs ``dH = G . W`` and ``dW += G^T . H`` in fp32 on the same tile loop
+  (fp32 transposed copies of W, of the active hidden rows and of G).  An fp32
+  GEMM here is bound by the fp32 MFMA rate (1/16 of bf16's) at over a
+  thousand flops per byte of logits, so the per-chunk logits write and read
+  that a fused epilogue would save cost under 1% of the step; skipping the
+  rows with a zero upstream gradient saves most of the backward's products.
+* other dtypes (fp64, or hidden states and weight of different dtypes) take
+  the reference's chunked shape with the library's ``torch.matmul``.
 """
 
 from __future__ import annotations
@@ -91,10 +99,14 @@ class ChunkedDistributedHiddenStatesToLogprobs(torch.autograd.Function):
             weight = weight.contiguous()
         if target.dtype != torch.int64:
             target = target.long()
+        if hidden.dtype == torch.float32 and weight.dtype == torch.float32:
+            return _f32_forward(ctx, hidden, target, weight, vocab_start_index, vocab_end_index,
+                                chunk_size, inference_only)
         if hidden.dtype not in _FUSED_DTYPES or weight.dtype != hidden.dtype:
             return _chunked_forward(ctx, hidden, target, weight, vocab_start_index, vocab_end_index,
                                     chunk_size, inference_only)
         ctx.chunked = False
+        ctx.f32 = False
         h2 = hidden.view(S * B, H)
         out = torch.empty((B, S), dtype=torch.float32, device=hidden.device)
         stats = None
@@ -111,6 +123,8 @@ class ChunkedDistributedHiddenStatesToLogprobs(torch.autograd.Function):
     @staticmethod
     def backward(ctx: Any, *grad_outputs: torch.Tensor):  # type: ignore[override]
         (grad_output,) = grad_outputs
+        if ctx.f32:
+            return _f32_backward(ctx, grad_output)
         if ctx.chunked:
             return _chunked_backward(ctx, grad_output)
         hidden, target, weight, stats = ctx.saved_tensors
@@ -216,6 +230,7 @@ def _chunked_forward(ctx, hidden, target, weight, vs, ve, chunk_size, inference_
         out[:, c0:c1] = out_c
         del logits
     ctx.chunked = True
+    ctx.f32 = False
     if not inference_only:
         ctx.save_for_backward(hidden, target, weight, stats)
         ctx.vocab = (int(vs), int(ve))
@@ -258,7 +273,122 @@ def _chunked_backward(ctx, grad_output):
     return dH, None, grad_w, None, None, None, None, None
 
 
+def _f32_operand(x: torch.Tensor) -> torch.Tensor:
+    """``x [N, H]`` fp32 as the fp32 tile loop reads it: ``H`` a multiple of 64, a row stride
+    that is a multiple of 4 elements (16 bytes) and a 16-byte-aligned start; otherwise a
+    zero-padded ``[N, round_up(H, 64)]`` copy (the padding adds exact zeros to every dot
+    product)."""
+    N, H = x.shape
+    if (H % _F32_K_ALIGN == 0 and x.stride(-1) == 1 and x.stride(0) % 4 == 0 and x.stride(0) >= H
+            and x.data_ptr() % 16 == 0):
+        return x
+    out = torch.zeros((N, _round_up(H, _F32_K_ALIGN)), dtype=x.dtype, device=x.device)
+    out[:, :H].copy_(x)
+    return out
+
+
+def _f32_forward(ctx, hidden, target, weight, vs, ve, chunk_size, inference_only):
+    """fp32: per chunk of positions, logits = hidden[c] . weight^T (fp32 tile loop, rows in
+    (position, sample) order), then the logprob row kernel over them (reference
+    model_utils.py:2608-2630).  The row statistics are saved per row r = s * B + b."""
+    S, B, H = hidden.shape
+    V = weight.shape[0]
+    T = S * B
+    dev = hidden.device
+    h2 = _f32_operand(hidden.view(T, H))
+    w2 = _f32_operand(weight)
+    K = h2.shape[1]
+    tgt_rows = target.t().reshape(1, T)  # row r = (s, b): position s of sample b
+    out_rows = torch.empty((1, T), dtype=torch.float32, device=dev)
+    stats = None if inference_only else torch.empty((T, 2), dtype=torch.float32, device=dev)
+    chunks = _chunks(S, chunk_size)
+    logits = torch.empty((max((c1 - c0) * B for c0, c1 in chunks), V), dtype=torch.float32, device=dev) \
+        if chunks else None
+    for c0, c1 in chunks:
+        r0, r1 = c0 * B, c1 * B
+        lc = logits[: r1 - r0]
+        _C.gemm_f32_abt(h2[r0:r1], w2, K, lc)
+        st_c = None if stats is None else stats[r0:r1].view(1, r1 - r0, 2)
+        _C.logprob_fwd(lc.view(1, r1 - r0, V), tgt_rows[:, r0:r1], vs, ve, out_rows[:, r0:r1], st_c)
+    del logits
+    ctx.chunked = False
+    ctx.f32 = True
+    if not inference_only:
+        ctx.save_for_backward(hidden, target, weight, stats)
+        ctx.vocab = (int(vs), int(ve))
+        ctx.chunk_size = None if chunk_size is None else int(chunk_size)
+    return out_rows.view(S, B).t().contiguous()
+
+
+def _f32_backward(ctx, grad_output):
+    """fp32 backward (reference model_utils.py:2647-2745) over the rows with a non-zero
+    upstream gradient, moved to the front and counted on the device (the others have a zero
+    logits gradient: zero dH rows, nothing added to dW).  Per block of one chunk of rows:
+    the logits recomputed on the fp32 tile loop, G = (onehot - softmax) * g written over them
+    by the logprob backward kernel, dH = G . W against W^T, and dW += G^T . H, fp32
+    throughout."""
+    hidden, target, weight, stats = ctx.saved_tensors
+    vs, ve = ctx.vocab
+    S, B, H = hidden.shape
+    V = weight.shape[0]
+    T = S * B
+    dev = hidden.device
+    if grad_output.dtype != torch.float32:
+        grad_output = grad_output.float()
+    need_h, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[2]
+    h2 = hidden.view(T, H)
+    g_rows = grad_output.t().reshape(T)
+    nz = g_rows != 0
+    perm = torch.argsort(torch.logical_not(nz).to(torch.uint8), stable=True)
+    count = nz.sum(dtype=torch.int64).view(1)
+    h_a = torch.index_select(h2, 0, perm)
+    tgt_a = target.t().reshape(T).index_select(0, perm).view(1, T)
+    st_a = stats.index_select(0, perm)
+    g_a = g_rows.index_select(0, perm).view(1, T)
+    hk_a, wk = _f32_operand(h_a), _f32_operand(weight)
+    K = hk_a.shape[1]
+    rows = T if ctx.chunk_size is None else min(T, _round_up(ctx.chunk_size * B, 256))
+    Vp = _round_up(V, _F32_K_ALIGN)
+    L = torch.empty((rows, Vp), dtype=torch.float32, device=dev)  # logits, then G
+    if Vp > V:
+        L[:, V:].zero_()  # dH's padded reduction length
+    dH = torch.empty((T, H), dtype=torch.float32, device=dev) if need_h else None
+    if need_h:
+        wT = torch.empty((H, Vp), dtype=torch.float32, device=dev)
+        _C.transpose_f32(weight, V, wT)
+    if need_w:
+        dW = torch.empty((V, H), dtype=torch.float32, device=dev)
+        hT = torch.empty((H, _padded_width(T)), dtype=torch.float32, device=dev)
+        _C.transpose_f32(h_a, T, hT, count=count)
+        Gt = torch.empty((V, _padded_width(rows)), dtype=torch.float32, device=dev)
+    for r0 in range(0, T, rows):
+        n = min(rows, T - r0)
+        Lc = L[:n]
+        # the block's active rows (rows past the count are not computed)
+        _C.gemm_f32_abt(hk_a[r0 : r0 + n], wk, K, Lc, count=count, count_off=r0,
+                        count_axis=_C.COUNT_ROWS)
+        lv = Lc[:, :V].view(1, n, V)
+        _C.logprob_bwd(lv, tgt_a[:, r0 : r0 + n], vs, ve, st_a[r0 : r0 + n].view(1, n, 2),
+                       g_a[:, r0 : r0 + n], lv)  # G over the logits; zeros past the count
+        if need_h:
+            splits = _dh_splits(n, H, Vp, count_known=False)
+            part = torch.empty((splits, n, H), dtype=torch.float32, device=dev)
+            _C.gemm_f32_abt(Lc, wT, Vp, part, k_splits=splits, count=count, count_off=r0,
+                            count_axis=_C.COUNT_ROWS)
+            _C.sum_splits_bf16(part, dH, count=count, count_off=r0, out_rows=perm[r0 : r0 + n])
+            del part
+        if need_w:
+            nk = _round_up(n, _K_ALIGN)
+            _C.transpose_f32(Lc[:, :V], n, Gt, count=count, count_off=r0)
+            _C.gemm_f32_abt(Gt, hT[:, r0 : r0 + nk], nk, dW, accumulate=r0 > 0, count=count,
+                            count_off=r0, count_axis=_C.COUNT_K)
+    grad_h = dH.view(S, B, H) if need_h else None
+    grad_w = dW if need_w else None
+    return grad_h, None, grad_w, None, None, None, None, None
+
+
 _FUSED_DTYPES = (torch.bfloat16, torch.float16)  # operand dtypes of the fused kernels
+_F32_K_ALIGN = 64  # the fp32 tile loop steps through the reduction 64 elements at a time
 _BLOCK_CHUNKS = 4  # chunks of active rows per backward block
 _K_ALIGN = 128  # dW's reduction length is padded with zero rows to a multiple of this
 _H_ALIGN = 128  # the fused kernels step through the hidden dimension 128 elements at a time

@@ -215,8 +215,9 @@ def test_gradient_row_compaction(pattern):
 @pytest.mark.parametrize("S,B,H,V,chunk", [(37, 3, 128, 1000, 8), (16, 2, 64, 151936, None), (9, 3, 200, 3001, 4)])
 def test_fp16_fp32_forward_and_gradients(dtype, S, B, H, V, chunk):
     """fp16 inputs run the fused kernels (logits tiles on the fp16 MFMA, rounded to fp16;
-    G in bf16 and W, H rounded to bf16 for dH and dW); fp32 inputs take per chunk a library
-    GEMM in fp32, then the logprob row kernels (the reference's chunked shape).  The oracle
+    G in bf16 and W, H rounded to bf16 for dH and dW); fp32 inputs take per chunk the fp32
+    tile loop (fp32 MFMA), then the logprob row kernels (the reference's chunked shape), and
+    the backward's three products on the fp32 tile loop over the active rows.  The oracle
     rounds the exact products to the dtype; logprobs within 2e-3 (fp16) / 1e-5 (fp32) plus
     the target logit's last-ulp rounding, dH and dW against the float64 oracle to 1e-2
     (fp16, bf16 operands of the two products) / 1e-4 (fp32) of their largest magnitude."""
@@ -328,6 +329,100 @@ def test_gemm_primitives_with_device_counts():
                              count=cnt, count_off=r0, count_axis=_C.COUNT_K, out_bf16=out16,
                              final_at=r0 + 256)
         assert torch.equal(out16, ref32.to(torch.bfloat16)), c
+
+
+def test_gemm_f32_primitives():
+    """The fp32 tile loop (four v_mfma_f32_32x32x2_f32 per fragment pair): C = A . B^T
+    against float64 within fp32 summation error; k splits sum to the same product; with a
+    device row count absent rows are untouched and the others equal the uncounted call bit
+    for bit; a reduction-length count over blocks accumulated in fp32 equals the
+    host-trimmed reduction; the fp32 transpose and split sum with counts and a row map."""
+    from rl_amd import _C
+
+    say("linear-ce fp32 primitives")
+    gen = torch.Generator().manual_seed(81)
+    M, N, K = 600, 300, 512
+    a = torch.randn(M, K, generator=gen).to(DEV)
+    b = torch.randn(N, K, generator=gen).to(DEV)
+    ref = (a.double() @ b.double().t()).cpu()
+    out = torch.empty((M, N), device=DEV)
+    _C.gemm_f32_abt(a, b, K, out)
+    bound = K * 2.0**-23 * (a.abs().double() @ b.abs().double().t()).cpu()  # fp32 summation error
+    assert torch.all((out.cpu().double() - ref).abs() <= bound)
+    part = torch.empty((2, M, N), device=DEV)
+    _C.gemm_f32_abt(a, b, K, part, k_splits=2)
+    assert torch.all((part.sum(0).cpu().double() - ref).abs() <= bound)
+    # a strided B (rows of a wider buffer) and accumulation
+    wide = torch.zeros((N, K + 64), device=DEV)
+    wide[:, :K] = b
+    acc = out.clone()
+    _C.gemm_f32_abt(a, wide, K, acc, accumulate=True)
+    assert torch.all((acc.cpu().double() - 2 * ref).abs() <= 2 * bound + 1e-6)
+    for c in (0, 1, 255, 257, 600):
+        cnt = torch.tensor([c + 100], dtype=torch.int64, device=DEV)  # count_off 100
+        pc = torch.full((2, M, N), 7.0, device=DEV)
+        _C.gemm_f32_abt(a, b, K, pc, k_splits=2, count=cnt, count_off=100, count_axis=_C.COUNT_ROWS)
+        assert torch.equal(pc[:, :c], part[:, :c]) and torch.all(pc[:, c:] == 7.0)
+        # split sum into fp32 rows, through a row map
+        rmap = torch.randperm(M, generator=gen).to(DEV)
+        o32 = torch.full((M, N), 3.0, device=DEV)
+        _C.sum_splits_bf16(pc, o32, count=cnt, count_off=100, out_rows=rmap)
+        direct = torch.empty((M, N), device=DEV)
+        _C.sum_splits_bf16(part, direct)
+        assert torch.equal(o32[rmap][:c], direct[:c]) and not o32[rmap][c:].any()
+        assert torch.equal(direct, part[0] + part[1])
+        # fp32 transpose with the count and an offset: zeros past it
+        t = torch.full((K, 640), 5.0, device=DEV)
+        _C.transpose_f32(a, M, t, count=torch.tensor([c + 30], dtype=torch.int64, device=DEV), count_off=30)
+        t_ref = torch.zeros((K, 640), device=DEV)
+        t_ref[:, :c] = a[:c].t()
+        assert torch.equal(t, t_ref)
+    # reduction length: c rows of the reduction over blocks of 256, accumulated in fp32
+    at = torch.zeros((N, 768), device=DEV)
+    bt = torch.zeros((K, 768), device=DEV)
+    for c in (0, 100, 256, 300, 700):
+        at.zero_()
+        bt.zero_()
+        at[:, :c] = torch.randn(N, c, generator=gen).to(DEV)
+        bt[:, :c] = torch.randn(K, c, generator=gen).to(DEV)
+        cnt = torch.tensor([c], dtype=torch.int64, device=DEV)
+        ref32 = torch.zeros((N, K), device=DEV)
+        for r0 in range(0, 768, 256):
+            _C.gemm_f32_abt(at[:, r0:r0 + 256], bt[:, r0:r0 + 256], 256, ref32, accumulate=r0 > 0)
+        acc32 = torch.full((N, K), 9.0, device=DEV)
+        for r0 in range(0, 768, 256):
+            _C.gemm_f32_abt(at[:, r0:r0 + 256], bt[:, r0:r0 + 256], 256, acc32, accumulate=r0 > 0,
+                            count=cnt, count_off=r0, count_axis=_C.COUNT_K)
+        assert torch.equal(acc32, ref32), c
+
+
+def test_f32_path_runs_no_library_gemm(monkeypatch):
+    """fp32 hidden states and weight: forward and backward run on this library's kernels;
+    torch's GEMM entry points are made to fail during the call."""
+    say("linear-ce fp32 without library GEMMs")
+    S, B, H, V = 24, 2, 128, 3000
+    g0 = torch.Generator().manual_seed(91)
+    hidden = torch.randn(S, B, H, generator=g0)
+    weight = torch.randn(V, H, generator=g0) * (1.5 / H**0.5)
+    target = torch.randint(0, V, (B, S), generator=g0)
+    g = torch.randn(B, S, generator=g0)
+    h = hidden.to(DEV).requires_grad_(True)
+    w = weight.to(DEV).requires_grad_(True)
+
+    def refuse(*a, **k):
+        raise AssertionError("a library GEMM ran on the fp32 hidden-state path")
+
+    for name in ("matmul", "mm", "addmm", "bmm", "baddbmm", "einsum"):
+        monkeypatch.setattr(torch, name, refuse)
+    monkeypatch.setattr(torch.Tensor, "__matmul__", refuse)
+    lp = ChunkedDistributedHiddenStatesToLogprobs.apply(h, target.to(DEV), w, 0, V, 5, None, False)
+    dh, dw = torch.autograd.grad(lp, [h, w], g.to(DEV))
+    monkeypatch.undo()
+    ref = hidden_state_logprobs(hidden, target, weight, 0, V)
+    assert (lp.detach().cpu().double() - ref.double()).abs().max().item() < 1e-4
+    rdh, rdw, _ = hidden_state_logprob_grads(hidden, target, weight, 0, V, g)
+    for got, want in ((dh, rdh), (dw, rdw)):
+        assert (got.cpu().double() - want).abs().max().item() <= 1e-4 * want.abs().max().item()
 
 
 def test_weight_written_in_place_between_backwards():
