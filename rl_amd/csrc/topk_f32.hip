@@ -142,15 +142,21 @@ __device__ __forceinline__ void bin_bounds(uint32_t k16, float M, double& elo, d
   ehi = (double)(fminf(__builtin_amdgcn_exp2f((vhi - M) * kLog2e), 1.0f) * (1.0f + kSlack));
 }
 
-// Streams the row's fp32 values through f(y, index): an unaligned head and
-// tail element by element, the body as 16-byte vectors in batches of UB per
-// lane with the next batch in flight while the current one is visited.
+// Streams the row's fp32 values through f(y, index, valid): an unaligned head
+// and tail element by element (visited by every lane of wave 0, valid only
+// where an element is, so that a wave's ballots and the counts kept from them
+// stay the same in all its lanes), the body as 16-byte vectors in batches of
+// UB per lane with the next batch in flight while the current one is visited.
 template <int UB, bool HAS_T, class F>
 __device__ __forceinline__ void stream_row(const float* x, int64_t V, float rT, F&& f) {
   const int tid = threadIdx.x;
   const RowSpan<F32> sp(x, V);
-  if (tid < sp.head) f(y_of<HAS_T>(x[tid], rT), (uint32_t)tid);
-  if (sp.tail0 + tid < V) f(y_of<HAS_T>(x[sp.tail0 + tid], rT), (uint32_t)(sp.tail0 + tid));
+  if (tid < kWave) {  // the whole of wave 0
+    const bool hv = tid < sp.head;
+    f(hv ? y_of<HAS_T>(x[tid], rT) : 0.f, (uint32_t)tid, hv);
+    const bool tv = sp.tail0 + tid < V;
+    f(tv ? y_of<HAS_T>(x[sp.tail0 + tid], rT) : 0.f, (uint32_t)(sp.tail0 + tid), tv);
+  }
   const vu4* xv = reinterpret_cast<const vu4*>(x + sp.head);
   const int nv = (int)sp.nvec;  // < 2^29: V < 2^31
   constexpr int kStep = UB * kFT;
@@ -165,10 +171,10 @@ __device__ __forceinline__ void stream_row(const float* x, int64_t V, float rT, 
 #pragma unroll
     for (int u = 0; u < UB; ++u) {
       const uint32_t j0 = head + 4u * (uint32_t)(bi * kStep + tid + u * kFT);
-      f(y_of<HAS_T>(__uint_as_float(q[u].x), rT), j0);
-      f(y_of<HAS_T>(__uint_as_float(q[u].y), rT), j0 + 1u);
-      f(y_of<HAS_T>(__uint_as_float(q[u].z), rT), j0 + 2u);
-      f(y_of<HAS_T>(__uint_as_float(q[u].w), rT), j0 + 3u);
+      f(y_of<HAS_T>(__uint_as_float(q[u].x), rT), j0, true);
+      f(y_of<HAS_T>(__uint_as_float(q[u].y), rT), j0 + 1u, true);
+      f(y_of<HAS_T>(__uint_as_float(q[u].z), rT), j0 + 2u, true);
+      f(y_of<HAS_T>(__uint_as_float(q[u].w), rT), j0 + 3u, true);
       __builtin_amdgcn_sched_barrier(0);  // one vector at a time (register budget)
     }
   };
@@ -184,14 +190,14 @@ __device__ __forceinline__ void stream_row(const float* x, int64_t V, float rT, 
 #pragma unroll
   for (int u = 0; u < UB; ++u) {
     const int v = nfull * kStep + tid + u * kFT;
-    if (v < nv) {
-      const vu4 q = __builtin_nontemporal_load(xv + v);
-      const uint32_t j0 = head + 4u * (uint32_t)v;
-      f(y_of<HAS_T>(__uint_as_float(q.x), rT), j0);
-      f(y_of<HAS_T>(__uint_as_float(q.y), rT), j0 + 1u);
-      f(y_of<HAS_T>(__uint_as_float(q.z), rT), j0 + 2u);
-      f(y_of<HAS_T>(__uint_as_float(q.w), rT), j0 + 3u);
-    }
+    // the remaining vectors: every lane of a wave visits them, valid where one is
+    const bool vv = v < nv;
+    const vu4 q = vv ? __builtin_nontemporal_load(xv + v) : vu4{0u, 0u, 0u, 0u};
+    const uint32_t j0 = head + 4u * (uint32_t)v;
+    f(y_of<HAS_T>(__uint_as_float(q.x), rT), j0, vv);
+    f(y_of<HAS_T>(__uint_as_float(q.y), rT), j0 + 1u, vv);
+    f(y_of<HAS_T>(__uint_as_float(q.z), rT), j0 + 2u, vv);
+    f(y_of<HAS_T>(__uint_as_float(q.w), rT), j0 + 3u, vv);
   }
 }
 
@@ -421,15 +427,15 @@ __device__ __forceinline__ void pass2(const float* x, int64_t V, const FilterPar
   // each wave appends to its own segment at a wave-uniform count: no atomics
   uint64_t* seg = sh.u.cand + (threadIdx.x >> 6) * kWaveCap;
   uint32_t wc = 0u;
-  stream_row<kUB, HAS_T>(x, V, P.rT, [&](float y, uint32_t j) {
-    const double de = (double)exp_le0(y - M);
+  stream_row<kUB, HAS_T>(x, V, P.rT, [&](float y, uint32_t j, bool valid) {
+    const double de = valid ? (double)exp_le0(y - M) : 0.0;
     const bool below = y < vb1;
-    bool coll = !below && y < vb2e;
+    bool coll = valid && !below && y < vb2e;
     if constexpr (TOPK) {
       const bool incl = y >= vinc;
       zall += incl ? de : 0.0;
       db += (incl && below) ? de : 0.0;
-      coll = coll || (y >= vlo && y < vloe);
+      coll = coll || (valid && y >= vlo && y < vloe);
     } else {
       zall += de;
       db += below ? de : 0.0;
@@ -479,7 +485,8 @@ __global__ __launch_bounds__(kFT, 4) void filter_f32_kernel(FilterParams P) {
   {
     char* hb = reinterpret_cast<char*>(sh.u.hist);
     with_t(P.has_t, [&](auto ht) {
-      stream_row<kUB, decltype(ht)::value>(x, V, P.rT, [&](float y, uint32_t) {
+      stream_row<kUB, decltype(ht)::value>(x, V, P.rT, [&](float y, uint32_t, bool valid) {
+        if (!valid) return;
         y = canon(y);  // -0.0 counted with +0.0, as the order key has it
         mloc = fmaxf(mloc, y);
         const uint32_t u = __float_as_uint(y);
@@ -759,8 +766,8 @@ __global__ __launch_bounds__(kFT, 4) void filter_f32_kernel(FilterParams P) {
       double dx = 0.0;
       __builtin_amdgcn_s_setprio(0);
       with_t(P.has_t, [&](auto ht) {
-        stream_row<kUB, decltype(ht)::value>(x, V, P.rT, [&](float y, uint32_t) {
-          const bool below_b1 = y >= vinc && y < vb1;
+        stream_row<kUB, decltype(ht)::value>(x, V, P.rT, [&](float y, uint32_t, bool valid) {
+          const bool below_b1 = valid && y >= vinc && y < vb1;
           dx += below_b1 ? (double)(exp_le0(y - M) * inv) : 0.0;
         });
       });
