@@ -266,6 +266,8 @@ int mirl_divergence_bwd(int kind, const void* student, const void* teacher,
 
 /* Kept entries saved per row by the filtered forward for the backward. */
 #define MIRL_FILTER_KEEP_CAP 1024
+/* Ties listed per 8 KB piece of a row by the filtered backward (its workspace). */
+#define MIRL_FILTER_PIECE_TIE_CAP 14
 
 /* Per-row result of the filtered forward.  The kept set is
  * { j : y_j > v_cut || (y_j == v_cut && j >= i_cut) }, y = the (temperature
@@ -330,6 +332,13 @@ int mirl_filtered_logprob_fwd(const void* logits, int dtype, int64_t B, int64_t 
  * 1024 the rows carry kept lists, so the gradient is zeroed in one flat pass
  * and the kept entries stored; otherwise the rows are rewritten whole, each
  * row written once); any value gives the same gradient.
+ * workspace (or NULL): mirl_filtered_logprob_bwd_workspace_bytes(dtype, B, R, V)
+ * bytes.  With it, rows without kept lists whose logits and gradient rows all
+ * start at the same offset from a 16-byte boundary are written in 8 KB pieces
+ * in address order; the ties of a cut in rank form are counted and listed
+ * there per piece and settled by a per-row pass.  Without it (or for other
+ * layouts) a workgroup walks each row.  Either way the gradient is the same.
+ * Calls that share a workspace must not overlap.
  *
  * Replaces: DistributedLogprobWithSampling.backward and
  * ChunkedDistributedLogprobWithSampling.backward
@@ -344,7 +353,12 @@ int mirl_filtered_logprob_bwd(const void* logits, int dtype, int64_t B, int64_t 
                               const void* row_info, const int32_t* kept_idx,
                               const float* kept_p, const float* grad_out,
                               int64_t g_stride_b, int64_t g_stride_r, void* grad_in,
-                              int64_t gi_stride_b, int64_t gi_stride_r, void* stream);
+                              int64_t gi_stride_b, int64_t gi_stride_r, void* workspace,
+                              void* stream);
+
+/* Bytes of mirl_filtered_logprob_bwd's workspace for B x R rows of V elements
+ * (32 per 8 KB piece of a row), or -1 with the error set. */
+int64_t mirl_filtered_logprob_bwd_workspace_bytes(int dtype, int64_t B, int64_t R, int64_t V);
 
 /*
  * apply_top_k_top_p on N rows of V logits: filtered[i, j] = x[i, j] where kept,

@@ -200,8 +200,9 @@ SIGNATURES = {
     "mirl_filtered_logprob_bwd": (
         _I,
         [_P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I64, _I64, ctypes.c_double,
-         ctypes.c_double, _I, _P, _P, _P, _P, _I64, _I64, _P, _I64, _I64, _P],
+         ctypes.c_double, _I, _P, _P, _P, _P, _I64, _I64, _P, _I64, _I64, _P, _P],
     ),
+    "mirl_filtered_logprob_bwd_workspace_bytes": (_I64, [_I, _I64, _I64, _I64]),
     "mirl_temperature_scale": (_I, [_P, _I, _I64, _I64, _I64, _I64, _I64, ctypes.c_double, _P]),
     "mirl_temperature_scale_grad": (
         _I,
@@ -1017,16 +1018,25 @@ def filtered_bwd(
     grad_in: torch.Tensor,
     grad_temperature: float = 1.0,
     top_k: int = 0,
+    pieces: bool = True,
 ) -> None:
     """``grad_temperature`` != 1 applies the backward of an in-place division of the
     logits by it, made before the forward, to the written gradient last (the product
     with ``fl32(1.0 / grad_temperature)`` in the dtype), folded into this write.  ``top_k`` is the forward's; it picks the
-    kernel schedule only (rows with kept lists for 1 <= top_k <= 1024)."""
+    kernel schedule only (rows with kept lists for 1 <= top_k <= 1024).  Rows without
+    kept lists are written in 4 KB pieces with a workspace allocated here (``pieces``;
+    False walks each row with a workgroup of its own: the same gradient)."""
     dev = _require_gpu(logits, target, grad_out, grad_in)
     B, R = target.shape
     Rt = grad_in.shape[1]
     V = logits.shape[-1]
     _require(grad_in.dtype == logits.dtype and grad_out.dtype == torch.float32, "grad_in.dtype == logits.dtype and grad_out.dtype == torch.float32")
+    ws = None
+    if pieces and not (1 <= top_k <= FILTER_KEEP_CAP) and B * R > 0:
+        lib = _lib if _lib is not None else load()
+        nbytes = int(lib.mirl_filtered_logprob_bwd_workspace_bytes(_dtype_code(logits), B, R, V))
+        _require(nbytes >= 0, "workspace size")
+        ws = torch.empty(max(1, (nbytes + 3) // 4), dtype=torch.int32, device=dev)
     st = _launch(
         "mirl_filtered_logprob_bwd", dev,
         logits.data_ptr(), _dtype_code(logits), B, R, Rt, V, logits.stride(0),
@@ -1034,7 +1044,7 @@ def filtered_bwd(
         float(temperature), float(grad_temperature), int(top_k), info.data_ptr(), kidx.data_ptr(),
         kp.data_ptr(),
         grad_out.data_ptr(), grad_out.stride(0), grad_out.stride(1), grad_in.data_ptr(),
-        grad_in.stride(0), grad_in.stride(1), _stream(dev),
+        grad_in.stride(0), grad_in.stride(1), _ptr(ws), _stream(dev),
     )
     _check(st, "mirl_filtered_logprob_bwd")
 

@@ -136,15 +136,25 @@ struct F16 {
       v[2 * k + 1] = (float)h.y;
     }
   }
-  __device__ __forceinline__ static raw from_float(float f) { return (_Float16)f; }
+  // The value is narrowed as an fp32 register holds it: the empty asm keeps
+  // the compiler from folding a product that feeds the narrowing into one
+  // mixed-precision fma (v_fma_mix), which rounds the exact product to fp16
+  // once and so differs from fl16(fl32(a * b)) where fl32(a * b) falls
+  // exactly between two fp16 values.
+  __device__ __forceinline__ static raw from_float(float f) {
+    asm("" : "+v"(f));
+    return (_Float16)f;
+  }
   __device__ __forceinline__ static vu4 pack(const float (&v)[kVec]) {
     typedef _Float16 h2 __attribute__((ext_vector_type(2)));
     uint32_t w[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
+      float a = v[2 * k], b = v[2 * k + 1];
+      asm("" : "+v"(a), "+v"(b));
       h2 h;
-      h.x = (_Float16)v[2 * k];
-      h.y = (_Float16)v[2 * k + 1];
+      h.x = (_Float16)a;
+      h.y = (_Float16)b;
       w[k] = __builtin_bit_cast(uint32_t, h);
     }
     return vu4{w[0], w[1], w[2], w[3]};

@@ -935,6 +935,15 @@ __host__ __device__ inline int grad_conv(bool has_t, bool has_gt) {
 // Per-row arithmetic of the whole-row walks below: the kept test of elements
 // equal to v_cut, the probability of a kept element and the gradient narrowed
 // to the dtype.
+// The least float above v (for non-NaN y: y > v <=> y >= next_float_up(v)):
+// -0.0 taken as +0.0, NaN above +inf and NaN (nothing compares >= it).
+__device__ __forceinline__ float next_float_up(float v) {
+  v = v + 0.0f;
+  const uint32_t u = __float_as_uint(v);
+  if (v != v || u == 0x7f800000u) return __uint_as_float(0x7fc00000u);
+  return __uint_as_float((int32_t)u >= 0 ? u + 1u : u - 1u);
+}
+
 template <class E, int CONV>
 struct WalkMath {
   using raw = typename E::raw;
@@ -1000,6 +1009,27 @@ struct WalkMath {
     } else {
 #pragma unroll
       for (int k = 0; k < E::kVec; ++k) vals[k] = narrow(g[k]);
+    }
+  }
+  // a vector of fp32 gradients narrowed to the dtype as narrow() does, packed
+  __device__ vu4 pack_vec(float (&g)[E::kVec]) const {
+    if constexpr (CONV == kConvPlain) {
+      return E::pack(g);
+    } else if constexpr (conv_one_product<CONV>()) {
+#pragma unroll
+      for (int k = 0; k < E::kVec; k += 2) {
+        round_trip2<E>(g[k], g[k + 1]);
+        g[k] = mul_rn(g[k], rone);
+        g[k + 1] = mul_rn(g[k + 1], rone);
+      }
+      return E::pack(g);
+    } else {
+      raw vals[E::kVec];
+#pragma unroll
+      for (int k = 0; k < E::kVec; ++k) vals[k] = grad_to_dtype<E>(g[k], P);
+      vu4 out;
+      __builtin_memcpy(&out, vals, sizeof(out));
+      return out;
     }
   }
   __device__ raw grad_at(float yy, int64_t j, bool kept) const {
@@ -1388,6 +1418,296 @@ __global__ __launch_bounds__(kRowThreads, 6) void filter_bwd_row_kernel(FilterBw
   walk_row_block<E, KIND>(P, ri, x, y, gv, t, s_cnt);
 }
 
+// The backward of rows without kept lists on 8 KB pieces: a workgroup of 256
+// threads writes one piece of one row, two 16-byte vectors per thread (the
+// first piece of a row also the elements before the row's first 16-byte
+// boundary, the last one those after its last), pieces numbered in address
+// order within the row and rows one after another.  Consecutive workgroups
+// then cover consecutive addresses, so the chip's reads and writes stay in a
+// narrow address window: a plain copy of [16380, 151936] bf16 rows moves at
+// 6.4 TB/s on such pieces and at 5.2 TB/s with a workgroup streaming each
+// row (the DRAM pages of hundreds of rows open at once).  The row's upstream
+// gradient, cut and target are the workgroup's (scalar loads, issued
+// together).  Measured on the top-k 2000 backward of bf16 [4, 4096, 151936]
+// rows (9.48 GB): 1.49 ms on 8 KB pieces, 1.83 ms on 4 KB pieces (a piece's
+// dependent loads amortized over half the bytes), 1.65 ms on 16 KB pieces;
+// 2.10 ms for the row walk.
+//
+// A cut in index form (j kept among the elements equal to v_cut from i_cut
+// on) is applied per element.  In rank form (kept among those ties from rank
+// rcut on, in index order) a piece cannot know its ties' ranks: it writes
+// every tie as kept, stores its tie count, and lists its ties' offsets in
+// index order (up to kPieceTieCap; a workgroup scan ranks them); a per-row
+// fix-up then ranks the pieces by their counts and writes zeros over the ties
+// of rank < rcut, reading a piece again only where its list overflowed.
+constexpr int kPcThreads = 256;
+constexpr int kPcVecs = 2;                          // 16-byte vectors per thread
+constexpr int kPcVectors = kPcThreads * kPcVecs;    // per piece
+constexpr int kPieceTieCap = MIRL_FILTER_PIECE_TIE_CAP;
+static_assert(kPieceTieCap % 2 == 0, "a piece's list is read as 32-bit words");
+
+struct PieceGeom {
+  int ppr;            // pieces per row
+  int nvec;           // 16-byte vectors per row (the same in every row)
+  int head;           // elements before the first vector
+  uint32_t* tie_cnt;  // [B * R * ppr]: the piece's tie count (rank-form rows with rcut > 0)
+  uint16_t* tie_pos;  // [B * R * ppr][kPieceTieCap]: tie offsets from the piece's first element
+};
+
+// first element of piece pc (piece 0 starts at the row's element 0)
+__device__ __forceinline__ int piece_j0(const PieceGeom& Gm, int pc, int vec) {
+  return pc == 0 ? 0 : Gm.head + pc * kPcVectors * vec;
+}
+
+template <class E, int CONV>
+__global__ __launch_bounds__(kPcThreads) void filter_bwd_piece_kernel(FilterBwdParams P, PieceGeom Gm) {
+  using raw = typename E::raw;
+  constexpr int VEC = E::kVec, NT = kPcThreads, U = kPcVecs, NW = NT / 64;
+  __shared__ uint32_t s_cnt[U * NW + 2];  // body ties per (u, wave), then the head's and the tail's
+  // 32-bit index arithmetic: rows < 2^31, V < 2^31
+  const uint32_t blk = blockIdx.x;
+  const uint32_t row = blk / (uint32_t)Gm.ppr;
+  const int pc = (int)(blk - row * (uint32_t)Gm.ppr);
+  const uint32_t b = row / (uint32_t)P.Rt, r = row - b * (uint32_t)P.Rt;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // the row's upstream gradient, cut and target, loaded together
+  const bool live = r < (uint32_t)P.R;
+  const uint32_t srow = b * (uint32_t)P.R + r;
+  float gv = 0.f;
+  RowInfo ri{};
+  int64_t t = -1;
+  if (live) {
+    gv = P.g[(int64_t)b * P.gsb + (int64_t)r * P.gsr];
+    ri = P.info[srow];
+    t = P.target[(int64_t)b * P.tsb + (int64_t)r * P.tsr];
+  }
+  raw* y = static_cast<raw*>(P.gin) + (int64_t)b * P.gisb + (int64_t)r * P.gisr;
+  vu4* yv = reinterpret_cast<vu4*>(y + Gm.head);
+  const int i0 = pc * kPcVectors + tid;  // this thread's first vector
+  const int tail0 = Gm.head + Gm.nvec * VEC;
+  const bool hv = pc == 0 && tid < Gm.head;                         // a head element
+  const bool tv = pc == Gm.ppr - 1 && tail0 + tid < (int)P.V;       // a tail element
+  const raw zr = E::from_float(0.f);
+  if (gv == 0.f) {
+    // rows past R and rows with a zero upstream gradient: zeros, the logits unread
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (i0 + u * NT < Gm.nvec) __builtin_nontemporal_store(vu4{0u, 0u, 0u, 0u}, yv + i0 + u * NT);
+    if (hv) y[tid] = zr;
+    if (tv) y[tail0 + tid] = zr;
+    return;
+  }
+  const raw* x = static_cast<const raw*>(P.logits) + (int64_t)b * P.sb + (int64_t)r * P.sr;
+  const vu4* xv = reinterpret_cast<const vu4*>(x + Gm.head);
+  vu4 q[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+    q[u] = i0 + u * NT < Gm.nvec ? __builtin_nontemporal_load(xv + i0 + u * NT) : vu4{0u, 0u, 0u, 0u};
+  const float xh = hv ? E::load(x + tid) : 0.f;
+  const float xt = tv ? E::load(x + tail0 + tid) : 0.f;
+  const WalkMath<E, CONV> W(P, ri, gv, t);
+  const float vc = W.vc;
+  const float yh = W.yval(xh), ytl = W.yval(xt);
+  float w[U][VEC];
+  bool anyt[U];  // the vector holds an element equal to v_cut
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    E::unpack(q[u], w[u]);
+    bool a = false;
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) {
+      w[u][k] = W.yval(w[u][k]);
+      a = a || w[u][k] == vc;
+    }
+    anyt[u] = a && i0 + u * NT < Gm.nvec;
+  }
+  auto tie_bits = [&](int u) {
+    uint32_t m = 0u;
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) m |= (w[u][k] == vc ? 1u : 0u) << k;
+    return anyt[u] ? m : 0u;
+  };
+  const bool th = hv && yh == vc, tt = tv && ytl == vc;
+  // per vector: kept <=> y >= thr (v_cut: its ties kept; the next float up:
+  // dropped), then the ties in `drop` zeroed, which only the vector holding an
+  // index-form cut has.  Rank form: every tie kept here (settled by the
+  // fix-up where rcut > 0).
+  const float vnext = next_float_up(vc);
+  float thr[U];
+  uint32_t drop[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    thr[u] = vc;
+    drop[u] = 0u;
+  }
+  bool keepH = th, keepTl = tt;
+  if (!W.rank_form) {
+    const int icut = W.icut;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int jb = Gm.head + (i0 + u * NT) * VEC;
+      if (jb + VEC <= icut) thr[u] = vnext;
+      const bool cutvec = jb < icut && jb + VEC > icut && anyt[u];
+      if (__ballot(cutvec) != 0ull && cutvec) drop[u] = tie_bits(u) & ((1u << (icut - jb)) - 1u);
+    }
+    keepH = th && tid >= icut;
+    keepTl = tt && tail0 + tid >= icut;
+  } else if (W.rcut > 0u) {
+    // the piece's ties in index order: the head's, the body's by (u, thread), the tail's
+    uint32_t tb[U], cnt[U], inc[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      tb[u] = 0u;
+      inc[u] = 0u;
+      if (__ballot(anyt[u]) != 0ull) {
+        tb[u] = tie_bits(u);
+        inc[u] = wave_scan_dpp((uint32_t)__popc(tb[u]));
+      }
+      cnt[u] = (uint32_t)__popc(tb[u]);
+      if (lane == 63) s_cnt[u * NW + wave] = inc[u];
+    }
+    const uint64_t bh = __ballot(th), bt = __ballot(tt);
+    if (tid == 0) {
+      s_cnt[U * NW] = (uint32_t)__popcll(bh);
+      s_cnt[U * NW + 1] = (uint32_t)__popcll(bt);
+    }
+    __syncthreads();
+    const uint32_t nh = s_cnt[U * NW];
+    uint32_t before[U];  // ties of the piece before this thread's span u
+    uint32_t base = nh;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      uint32_t span = 0u;
+      before[u] = base;
+#pragma unroll
+      for (int v = 0; v < NW; ++v) {
+        before[u] += v < wave ? s_cnt[u * NW + v] : 0u;
+        span += s_cnt[u * NW + v];
+      }
+      before[u] += inc[u] - cnt[u];
+      base += span;
+    }
+    // the count and the list (offsets in index order, up to kPieceTieCap)
+    const uint64_t below = (1ull << lane) - 1ull;
+    const int j0 = piece_j0(Gm, pc, VEC);
+    const int64_t slot = (int64_t)srow * Gm.ppr + pc;
+    uint16_t* lst = Gm.tie_pos + slot * kPieceTieCap;
+    if (th) {
+      const uint32_t a = (uint32_t)__popcll(bh & below);
+      if (a < (uint32_t)kPieceTieCap) lst[a] = (uint16_t)(tid - j0);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int jb = Gm.head + (i0 + u * NT) * VEC;
+      uint32_t a = before[u];
+      for (uint32_t m = tb[u]; m != 0u; m &= m - 1u, ++a) {
+        const int k = __ffs(m) - 1;
+        if (a < (uint32_t)kPieceTieCap) lst[a] = (uint16_t)(jb + k - j0);
+      }
+    }
+    if (tt) {
+      const uint32_t at = base + (uint32_t)__popcll(bt & below);
+      if (at < (uint32_t)kPieceTieCap) lst[at] = (uint16_t)(tail0 + tid - j0);
+    }
+    if (tid == 0) Gm.tie_cnt[slot] = base + s_cnt[U * NW + 1];
+  }
+  const float ngv = -gv;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int i = i0 + u * NT;
+    const int jb = Gm.head + i * VEC;
+    float o[VEC];
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) o[k] = w[u][k] >= thr[u] ? W.prob(w[u][k]) * ngv : 0.f;
+    if (__ballot(drop[u] != 0u) != 0ull) {
+#pragma unroll
+      for (int k = 0; k < VEC; ++k)
+        if ((drop[u] >> k) & 1u) o[k] = 0.f;
+    }
+    // the target element: (1 - p) g where kept
+    const int64_t dt = t - jb;
+    if (dt >= 0 && dt < VEC) {
+#pragma unroll
+      for (int k = 0; k < VEC; ++k)
+        if (k == dt) {
+          const bool kept = w[u][k] >= thr[u] && ((drop[u] >> k) & 1u) == 0u;
+          o[k] = kept ? (1.f - W.prob(w[u][k])) * gv : 0.f;
+        }
+    }
+    const vu4 out = W.pack_vec(o);
+    if (i < Gm.nvec) __builtin_nontemporal_store(out, yv + i);
+  }
+  if (hv) y[tid] = W.grad_at(yh, tid, yh > vc || keepH);
+  if (tv) y[tail0 + tid] = W.grad_at(ytl, tail0 + tid, ytl > vc || keepTl);
+}
+
+// Per row with a rank-form cut and rcut > 0 (one wave each): the pieces'
+// tie counts scanned in order, and the listed ties of rank < rcut written as
+// zeros (a piece whose list overflowed is read again, its ties ranked by
+// ballot).  Measured on the top-p backward of bf16 [4, 4096, 151936] rows
+// (about 75 zeros per row): 0.17 ms, the cost of that many scattered 2-byte
+// writes into lines already written back.  A decoupled look-back in the piece
+// kernel (each piece adding up the counts its row's earlier pieces publish,
+// so that every tie is written once) measured 2.9 ms for the piece kernel
+// alone: pieces waiting on pieces of other XCDs hold their slots.
+template <class E, int CONV>
+__global__ __launch_bounds__(256) void filter_bwd_piece_fixup_kernel(FilterBwdParams P, PieceGeom Gm,
+                                                                     int64_t nrows) {
+  using raw = typename E::raw;
+  constexpr int VEC = E::kVec;
+  const int lane = threadIdx.x & 63;
+  const int64_t srow = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (srow >= nrows) return;
+  const int64_t b = srow / P.R, r = srow - b * P.R;
+  const float gv = P.g[b * P.gsb + r * P.gsr];
+  if (gv == 0.f) return;
+  const RowInfo ri = P.info[srow];
+  if (ri.i_cut >= -1) return;  // index form, or every tie kept
+  const uint32_t rcut = (uint32_t)(-1 - ri.i_cut);
+  raw* y = static_cast<raw*>(P.gin) + b * P.gisb + r * P.gisr;
+  const raw* x = static_cast<const raw*>(P.logits) + b * P.sb + r * P.sr;
+  const raw zr = E::from_float(0.f);
+  const WalkMath<E, CONV> W(P, ri, gv, -1);
+  const uint32_t* cnt = Gm.tie_cnt + srow * Gm.ppr;
+  const uint16_t* pos = Gm.tie_pos + srow * Gm.ppr * kPieceTieCap;
+  const uint64_t below = (1ull << lane) - 1ull;
+  uint32_t seen = 0u;
+  for (int c0 = 0; c0 < Gm.ppr && seen < rcut; c0 += 64) {
+    const int pc = c0 + lane;
+    const uint32_t n = pc < Gm.ppr ? cnt[pc] : 0u;
+    const uint32_t inc = wave_scan_dpp(n);
+    const uint32_t start = seen + inc - n;
+    const bool need = n > 0u && start < rcut;
+    if (need && n <= (uint32_t)kPieceTieCap) {
+      // the piece's list read whole (independent loads), then the zeros stored
+      const int j0 = piece_j0(Gm, pc, VEC);
+      const uint32_t m = min(n, rcut - start);
+      const uint32_t* pw = reinterpret_cast<const uint32_t*>(pos + pc * kPieceTieCap);
+      uint32_t wv[kPieceTieCap / 2];
+#pragma unroll
+      for (int a = 0; a < kPieceTieCap / 2; ++a) wv[a] = 2u * a < m ? pw[a] : 0u;
+#pragma unroll
+      for (int a = 0; a < kPieceTieCap; ++a)
+        if ((uint32_t)a < m) y[j0 + ((wv[a >> 1] >> (16 * (a & 1))) & 0xffffu)] = zr;
+    }
+    for (uint64_t ov = __ballot(need && n > (uint32_t)kPieceTieCap); ov != 0ull; ov &= ov - 1ull) {
+      const int l = __ffsll((unsigned long long)ov) - 1;
+      const int pv = c0 + l;
+      uint32_t rk = (uint32_t)__shfl((int)start, l, 64);
+      const int64_t j0 = piece_j0(Gm, pv, VEC);
+      const int64_t j1 = pv == Gm.ppr - 1 ? P.V : (int64_t)Gm.head + (int64_t)(pv + 1) * kPcVectors * VEC;
+      for (int64_t jj = j0; jj < j1 && rk < rcut; jj += 64) {
+        const int64_t j = jj + lane;
+        const bool tie = j < j1 && W.yval(E::load(x + j)) == W.vc;
+        const uint64_t bal = __ballot(tie);
+        if (tie && rk + (uint32_t)__popcll(bal & below) < rcut) y[j] = zr;
+        rk += (uint32_t)__popcll(bal);
+      }
+    }
+    seen += (uint32_t)__shfl((int)inc, 63, 64);
+  }
+}
+
 // Phase 2, one wave per row with a non-zero upstream gradient: with the saved
 // kept list each kept entry is stored on its own (phase 1 zeroed the rest);
 // otherwise the row is re-read and rewritten whole.
@@ -1535,11 +1855,65 @@ int launch_topk_export(const FilterParams& P, int64_t rows, hipStream_t st) {
   return check_launch("topk_export_general_kernel");
 }
 
+// Pieces per row bound (16-byte vectors of V elements, 4 KB pieces), for the workspace size.
+int64_t piece_ppr_bound(int64_t V, int64_t esz) {
+  const int64_t nv = V * esz / 16;
+  return nv > 0 ? (nv + kPcVectors - 1) / kPcVectors : 1;
+}
+
+// The piece schedule's geometry when the layout allows it (logits and gradient
+// co-aligned, every row at the same 16-byte offset, rows whole in 32-bit
+// indexing), else ppr = 0.
 template <class E>
-int launch_bwd(const FilterBwdParams& P, int64_t B, int64_t rows, hipStream_t st) {
+PieceGeom piece_geom(const FilterBwdParams& P, int64_t B, int64_t rows, void* ws) {
+  PieceGeom Gm{};
+  constexpr int64_t esz = sizeof(typename E::raw);
+  const uintptr_t ax = reinterpret_cast<uintptr_t>(P.logits), ay = reinterpret_cast<uintptr_t>(P.gin);
+  auto row_step_ok = [&](int64_t stride, int64_t extent) { return extent <= 1 || (stride * esz) % 16 == 0; };
+  if (ws == nullptr || ax % esz != 0 || ay % esz != 0 || ax % 16 != ay % 16) return Gm;
+  if (!row_step_ok(P.sb, B) || !row_step_ok(P.sr, P.R) || !row_step_ok(P.gisb, B) || !row_step_ok(P.gisr, P.Rt))
+    return Gm;
+  int64_t head = (int64_t)(((16u - (ay & 15u)) & 15u) / esz);
+  if (head > P.V) head = P.V;
+  const int64_t nvec = (P.V - head) / E::kVec;
+  const int64_t ppr = nvec > 0 ? (nvec + kPcVectors - 1) / kPcVectors : 1;
+  if (rows * ppr * kPcThreads >= (int64_t(1) << 32)) return Gm;
+  // workspace: the tie counts, then the tie lists
+  const int64_t slots = B * P.R * piece_ppr_bound(P.V, esz);
+  Gm.ppr = (int)ppr;
+  Gm.nvec = (int)nvec;
+  Gm.head = (int)head;
+  Gm.tie_cnt = static_cast<uint32_t*>(ws);
+  Gm.tie_pos = reinterpret_cast<uint16_t*>(Gm.tie_cnt + slots);
+  return Gm;
+}
+
+template <class E>
+int launch_bwd(const FilterBwdParams& P, int64_t B, int64_t rows, void* ws, hipStream_t st) {
   if (P.zero_rows) {
-    // rows without kept lists: each row written once, by a workgroup of its own
+    // rows without kept lists: each row written once
     if (rows == 0) return MIRL_OK;
+    const PieceGeom Gm = piece_geom<E>(P, B, rows, ws);
+    if (Gm.ppr > 0) {
+      // 4 KB pieces in address order, then the per-row fix-up of rank-form ties
+      const int64_t srows = B * P.R;
+      auto launch = [&](auto conv) {
+        constexpr int CONV = decltype(conv)::value;
+        hipLaunchKernelGGL((filter_bwd_piece_kernel<E, CONV>), dim3((unsigned)(rows * Gm.ppr)),
+                           dim3(kPcThreads), 0, st, P, Gm);
+        if (srows > 0)
+          hipLaunchKernelGGL((filter_bwd_piece_fixup_kernel<E, CONV>), dim3((unsigned)((srows + 3) / 4)),
+                             dim3(256), 0, st, P, Gm, srows);
+      };
+      switch (grad_conv(P.has_t, P.has_gt)) {
+        case kConvPlain: launch(std::integral_constant<int, kConvPlain>{}); break;
+        case kConvGT: launch(std::integral_constant<int, kConvGT>{}); break;
+        case kConvT: launch(std::integral_constant<int, kConvT>{}); break;
+        default: launch(std::integral_constant<int, kConvTwo>{}); break;
+      }
+      return check_launch("filter_bwd_piece_kernel");
+    }
+    // other layouts: a workgroup walks each row
     auto launch = [&](auto conv) {
       constexpr int CONV = decltype(conv)::value;
       hipLaunchKernelGGL((filter_bwd_row_kernel<E, CONV>), dim3((unsigned)rows), dim3(kRowThreads), 0,
@@ -1682,7 +2056,8 @@ extern "C" int mirl_filtered_logprob_bwd(const void* logits, int dtype, int64_t 
                                          const void* row_info, const int32_t* kept_idx,
                                          const float* kept_p, const float* grad_out,
                                          int64_t g_stride_b, int64_t g_stride_r, void* grad_in,
-                                         int64_t gi_stride_b, int64_t gi_stride_r, void* stream) {
+                                         int64_t gi_stride_b, int64_t gi_stride_r, void* workspace,
+                                         void* stream) {
   clear_error();
   if (dtype != MIRL_DTYPE_F32 && dtype != MIRL_DTYPE_BF16 && dtype != MIRL_DTYPE_F16) {
     set_error("unsupported logits dtype code %d", dtype);
@@ -1724,9 +2099,23 @@ extern "C" int mirl_filtered_logprob_bwd(const void* logits, int dtype, int64_t 
   // rewritten whole and each row is written once
   P.zero_rows = !(top_k >= 1 && top_k <= kCandCap);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (dtype == MIRL_DTYPE_F32) return launch_bwd<F32>(P, B, rows, st);
-  if (dtype == MIRL_DTYPE_BF16) return launch_bwd<BF16>(P, B, rows, st);
-  return launch_bwd<F16>(P, B, rows, st);
+  if (dtype == MIRL_DTYPE_F32) return launch_bwd<F32>(P, B, rows, workspace, st);
+  if (dtype == MIRL_DTYPE_BF16) return launch_bwd<BF16>(P, B, rows, workspace, st);
+  return launch_bwd<F16>(P, B, rows, workspace, st);
+}
+
+extern "C" int64_t mirl_filtered_logprob_bwd_workspace_bytes(int dtype, int64_t B, int64_t R, int64_t V) {
+  clear_error();
+  const int64_t esz = dtype == MIRL_DTYPE_F32 ? 4 : (dtype == MIRL_DTYPE_BF16 || dtype == MIRL_DTYPE_F16) ? 2 : 0;
+  if (esz == 0) {
+    set_error("unsupported logits dtype code %d", dtype);
+    return -1;
+  }
+  if (B < 0 || R < 0 || V <= 0) {
+    set_error("invalid shape B=%lld R=%lld V=%lld", (long long)B, (long long)R, (long long)V);
+    return -1;
+  }
+  return B * R * piece_ppr_bound(V, esz) * (int64_t)(4 + 2 * kPieceTieCap);
 }
 
 extern "C" int mirl_top_k_top_p_mask(const void* logits, int dtype, int64_t N, int64_t V,

@@ -107,10 +107,10 @@ def _temperature_node(logits: torch.Tensor):
 
 
 def _filtered_grad(ctx: Any, logits, target, temperature, info, kidx, kp, g):
-    top_k = getattr(ctx, "top_k", 0)
     """The logits gradient of a filtered op: folded into the in-place temperature
     node ahead of it when that node has no gradient from another filtered op yet
     (then None is returned for autograd), else returned as usual."""
+    top_k = getattr(ctx, "top_k", 0)
     node = getattr(ctx, "temperature_node", None)
     ref = getattr(ctx, "logits_ref", None)
     scaled = ref() if ref is not None else None
