@@ -102,7 +102,9 @@ int mirl_logprob_bwd(const void* logits, int dtype, int64_t B, int64_t R,
  * returns at once otherwise.  The recomputation leaves the rows whose
  * grad_out equals grad_used (and the rows past R) as the earlier call wrote
  * them, so grad_in must still hold that call's output there.  Arguments as
- * for mirl_logprob_bwd.
+ * for mirl_logprob_bwd.  row_list (or NULL): B * R int32 of scratch; with it
+ * the check also lists the rows that differ (each flag is then its
+ * workgroup's count) and the recomputation visits those rows only.
  *
  * Replaces: nothing in the reference (an ordering device: it lets the
  * backward start before the host has synchronised on the loss's metrics).
@@ -117,7 +119,7 @@ int mirl_logprob_bwd_recheck(const void* logits, int dtype, int64_t B, int64_t R
                              int64_t g_stride_b, int64_t g_stride_r,
                              const float* grad_used, void* grad_in,
                              int64_t gi_stride_b, int64_t gi_stride_r, int* flag,
-                             void* stream);
+                             int32_t* row_list, void* stream);
 
 /*
  * Log-probabilities at K given vocabulary ids per row:

@@ -140,7 +140,7 @@ SIGNATURES = {
     "mirl_logprob_bwd_recheck": (
         _I,
         [_P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I64, _I64, _I64, _I64, _P, _P, _I64,
-         _I64, _P, _P, _I64, _I64, _P, _P],
+         _I64, _P, _P, _I64, _I64, _P, _P, _P],
     ),
     "mirl_clipped_pg_workspace_elems": (_I64, [_I64, _I64, _I]),
     "mirl_clipped_pg": (
@@ -543,11 +543,13 @@ def logprob_bwd_recheck(
     grad_out: torch.Tensor,
     grad_used: torch.Tensor,
     grad_in: torch.Tensor,
+    listed: bool = True,
 ) -> torch.Tensor:
     """grad_in was written by logprob_bwd for grad_used; make it right for grad_out (device-side check).
 
     Returns the check's flags ([64] int32 on the device, all zero when grad_out
-    equals grad_used bit for bit): one flag per check workgroup."""
+    equals grad_used bit for bit): one flag per check workgroup (with ``listed``,
+    the number of its rows that differ; the redo then visits only those rows)."""
     dev = _require_gpu(logits, target, stats, grad_out, grad_used, grad_in)
     B, R = target.shape
     Rt = grad_in.shape[1]
@@ -555,13 +557,14 @@ def logprob_bwd_recheck(
     _require(grad_used.is_contiguous() and tuple(grad_used.shape) == (B, R), "grad_used.is_contiguous() and tuple(grad_used.shape) == (B, R)")
     _require(grad_out.dtype == torch.float32 and grad_used.dtype == torch.float32, "grad_out.dtype == torch.float32 and grad_used.dtype == torch.float32")
     flag = torch.empty(64, dtype=torch.int32, device=dev)  # MIRL_RECHECK_FLAGS
+    rows_ws = torch.empty(max(1, B * R), dtype=torch.int32, device=dev) if listed else None
     st = _launch(
         "mirl_logprob_bwd_recheck", dev,
         logits.data_ptr(), _dtype_code(logits), B, R, Rt, V, logits.stride(0), logits.stride(1),
         target.data_ptr(), target.stride(0), target.stride(1), int(vocab_start), int(vocab_end),
         stats.data_ptr(), grad_out.data_ptr(), grad_out.stride(0), grad_out.stride(1),
         grad_used.data_ptr(), grad_in.data_ptr(), grad_in.stride(0), grad_in.stride(1),
-        flag.data_ptr(), _stream(dev),
+        flag.data_ptr(), _ptr(rows_ws), _stream(dev),
     )
     _check(st, "mirl_logprob_bwd_recheck")
     return flag[: min(B * R, 64)]  # one flag per check workgroup
