@@ -999,14 +999,24 @@ __global__ __launch_bounds__(G::NT, 2048 / G::NT) void filter_compact_kernel(Fil
       count_key(k2 & 0xffffu);
       count_key(k2 >> 16);
     } else {
-      // word min(|x| bits, kWords), the sign choosing the half
+      // word min(|x| bits, kWords), the sign choosing the half.  Eight VALU
+      // instructions for the two values (the compiler's form took eleven):
+      // each half's byte address by one shift that reads the half directly
+      // (SDWA operand select), each increment 1 + sign * 0xffff by a bit
+      // extract and one 24-bit multiply-add.
       const u16x2 mag = __builtin_bit_cast(u16x2, w & 0x7fff7fffu);
       const uint32_t c =
           __builtin_bit_cast(uint32_t, __builtin_elementwise_min(mag, (u16x2)(uint16_t)G::kWords));
+      uint32_t alo, ahi, ilo, ihi;
+      asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:WORD_0"
+          : "=v"(alo) : "v"(c));
+      asm("v_lshlrev_b32_sdwa %0, 2, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:WORD_1"
+          : "=v"(ahi) : "v"(c));
+      asm("v_bfe_u32 %0, %1, 15, 1\n\tv_mad_u32_u24 %0, %0, %2, 1" : "=&v"(ilo) : "v"(w), "s"(0xffffu));
+      asm("v_lshrrev_b32 %0, 31, %1\n\tv_mad_u32_u24 %0, %0, %2, 1" : "=&v"(ihi) : "v"(w), "s"(0xffffu));
       char* base = reinterpret_cast<char*>(sh.u.hist);
-      atomicAdd(reinterpret_cast<uint32_t*>(base + ((c & 0xffffu) << 2)),
-                1u + ((w >> 15) & 1u) * 0xffffu);
-      atomicAdd(reinterpret_cast<uint32_t*>(base + ((c >> 16) << 2)), 1u + (w >> 31) * 0xffffu);
+      atomicAdd(reinterpret_cast<uint32_t*>(base + alo), ilo);
+      atomicAdd(reinterpret_cast<uint32_t*>(base + ahi), ihi);
     }
   };
   // one value (a row's unaligned head and tail), in the table's layout
@@ -1161,17 +1171,25 @@ __global__ __launch_bounds__(G::NT, 2048 / G::NT) void filter_compact_kernel(Fil
   for (int w = 0; w < kWPT; ++w) wd[w] = sh.u.hist[phys(L0 + (uint32_t)w)];
   __syncthreads();  // every table word is in registers: the entries overwrite the table
   if constexpr (G::kWindow) {
+    // Branch-free: a half with no values writes to this thread's own slot past
+    // the entry list (kc[kEntCap + tid], inside the y array, which is written
+    // after the next barrier and read only below N), so that no lane waits on
+    // the others' branches.
+    static_assert(kEntCap + NT <= 3 * kEntCap, "the spare slots lie inside the entry arrays");
+    const uint32_t spare = (uint32_t)kEntCap + (uint32_t)tid;
     uint32_t j = off_n;
 #pragma unroll
     for (int w = kWPT - 1; w >= 0; --w) {
       const uint32_t hi = wd[w] >> 16;
-      if (hi != 0u) sh.u.ent.kc[j++] = (0x7fffu - (L0 + (uint32_t)w)) | (hi << 16);
+      sh.u.ent.kc[hi != 0u ? j : spare] = (0x7fffu - (L0 + (uint32_t)w)) | (hi << 16);
+      j += hi != 0u ? 1u : 0u;
     }
     j = off_p;
 #pragma unroll
     for (int w = 0; w < kWPT; ++w) {
       const uint32_t lo = wd[w] & 0xffffu;
-      if (lo != 0u) sh.u.ent.kc[j++] = (0x8000u | (L0 + (uint32_t)w)) | (lo << 16);
+      sh.u.ent.kc[lo != 0u ? j : spare] = (0x8000u | (L0 + (uint32_t)w)) | (lo << 16);
+      j += lo != 0u ? 1u : 0u;
     }
   } else {
     uint32_t j = off_p;
