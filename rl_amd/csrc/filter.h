@@ -130,6 +130,28 @@ __device__ int block_sum_i(int v, int* red) {
   return r;
 }
 
+// The lowest thread of the workgroup whose flag is set goes into *slot (which
+// holds a larger value beforehand) by an LDS minimum.  LDS atomics that many
+// lanes aim at one address are serialised (a whole flagged wave costs
+// microseconds), so each wave sends one, from its lowest flagged lane.  Every
+// thread of the wave calls it.
+__device__ __forceinline__ void block_first_flagged(bool f, int* slot) {
+  const uint64_t m = __ballot(f);
+  if (m != 0u && (int)(threadIdx.x & 63u) == __ffsll((long long)m) - 1)
+    atomicMin(slot, (int)threadIdx.x);
+}
+// Unsigned maximum and minimum over the 64 lanes of a wave.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, off, 64));
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = min(v, (uint32_t)__shfl_xor((int)v, off, 64));
+  return v;
+}
+
 // Cross-lane moves by DPP (no LDS traffic): row_shr:n shifts within rows of 16
 // lanes, row_bcast:15 / row_bcast:31 pass a row's last lane on to the next
 // row(s).  Lanes with no source, and rows outside ROWMASK, read 0, the

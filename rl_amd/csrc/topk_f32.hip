@@ -608,8 +608,13 @@ __global__ __launch_bounds__(kFT, 4) void filter_f32_kernel(FilterParams P) {
       ah += (double)c * ehi;
       if (my2 == 0xffffffffu && al > cutp * (al + fmax(Zhi - ah, 0.0))) my2 = k16;
     }
-    if (my1 != 0u) atomicMax(&sh.b1, my1);
-    if (my2 != 0xffffffffu) atomicMin(&sh.b2, my2);
+    // one LDS atomic per wave (same-address LDS atomics are serialised)
+    my1 = wave_max_u32(my1);
+    my2 = wave_min_u32(my2);
+    if ((tid & 63) == 0) {
+      if (my1 != 0u) atomicMax(&sh.b1, my1);
+      if (my2 != 0xffffffffu) atomicMin(&sh.b2, my2);
+    }
     __syncthreads();
     B1 = sh.b1;
     B2 = sh.b2 == 0xffffffffu ? top16 : sh.b2;

@@ -580,7 +580,7 @@ __global__ __launch_bounds__(kHT) void filter_hist_kernel(FilterParams P, int al
         }
         X += (double)n * p;
       });
-      if (found) atomicMin(&sh.first_lo, tid);
+      block_first_flagged(found, &sh.first_lo);
       __syncthreads();
       if (sh.first_lo == tid) {
         sh.key_lo = fk;
@@ -636,8 +636,8 @@ __global__ __launch_bounds__(kHT) void filter_hist_kernel(FilterParams P, int al
           X = X1;
           D = Db;
         });
-        if (flo) atomicMin(&sh.first_lo, tid);
-        if (fhi) atomicMin(&sh.first_hi, tid);
+        block_first_flagged(flo, &sh.first_lo);
+        block_first_flagged(fhi, &sh.first_hi);
         if (!slack_ok) sh.walk_hit = -1;
         __syncthreads();
         if (sh.first_lo == tid) {
@@ -1335,7 +1335,7 @@ __global__ __launch_bounds__(G::NT, 2048 / G::NT) void filter_compact_kernel(Fil
           X += (double)n * p;
         }
       }
-      if (found) atomicMin(&sh.first_lo, tid);
+      block_first_flagged(found, &sh.first_lo);
       __syncthreads();
       if (sh.first_lo == tid) {
         sh.ent_lo = fk;
@@ -1398,8 +1398,8 @@ __global__ __launch_bounds__(G::NT, 2048 / G::NT) void filter_compact_kernel(Fil
           }
         }
       }
-      if (flo) atomicMin(&sh.first_lo, tid);
-      if (fhi) atomicMin(&sh.first_hi, tid);
+      block_first_flagged(flo, &sh.first_lo);
+      block_first_flagged(fhi, &sh.first_hi);
       if (!slack_ok) sh.fail = 1;
       __syncthreads();
       if (sh.first_lo == tid) {
