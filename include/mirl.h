@@ -273,7 +273,11 @@ int mirl_divergence_bwd(int kind, const void* student, const void* teacher,
 
 /* Per-row result of the filtered forward.  The kept set is
  * { j : y_j > v_cut || (y_j == v_cut && j >= i_cut) }, y = the (temperature
- * scaled) fp32 value; m is its maximum and logsum = log(sum_kept exp(y - m)). */
+ * scaled) fp32 value; m is its maximum and logsum = log(sum_kept exp(y - m)).
+ * flags: bit 2 set when the row has no kept list (the backward re-reads the
+ * row); bit 3 set when a top-p cut decided in the 16-bit dtype was found by
+ * the exact one-element-at-a-time sum because the error bounds of the
+ * parallel sum did not settle it (informational); other bits internal. */
 typedef struct mirl_filter_row_info {
   float m;
   float logsum;

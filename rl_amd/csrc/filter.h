@@ -24,10 +24,12 @@ struct RowInfo {
   float v_cut;    // kept <=> y > v_cut || (y == v_cut && j >= i_cut)
   int32_t i_cut;  // < 0: rank form, kept among y == v_cut <=> rank in index order >= -1 - i_cut
   int32_t n_kept;
-  int32_t flags;  // bit 0: row must be (re)done by a general path; bit 2: no kept list
+  int32_t flags;  // bit 0: row must be (re)done by a general path; bit 2: no kept list;
+                  // bit 3: a 16-bit top-p cut decided by the exact sequential sum
 };
 constexpr int kFlagRedo = 1;
 constexpr int kFlagNoKeptList = 4;
+constexpr int kFlagWalked = 8;
 static_assert(sizeof(RowInfo) == sizeof(mirl_filter_row_info), "row info layout");
 
 struct FilterParams {

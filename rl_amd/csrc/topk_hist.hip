@@ -541,7 +541,7 @@ __global__ __launch_bounds__(kHT) void filter_hist_kernel(FilterParams P, int al
   // ---- top-p cut -----------------------------------------------------------
   // (cut_key, cut_pos): the cut is the cut_pos-th element (1-based) of key
   // cut_key in the ascending order; no cut keeps the maximum only
-  bool have_cut = false;
+  bool have_cut = false, walked = false;
   uint32_t cut_key = 0, cut_pos = 0;
   if (P.has_p) {
     const float inv = 1.0f / Z;
@@ -669,6 +669,7 @@ __global__ __launch_bounds__(kHT) void filter_hist_kernel(FilterParams P, int al
       } else {
         // the exact sequence, one wave: ranges whose additions are all exact
         // and stay inside S's binade below the threshold are added at once
+        walked = true;
         __syncthreads();
         if (tid < 64) {
           float S = 0.f;
@@ -846,7 +847,7 @@ __global__ __launch_bounds__(kHT) void filter_hist_kernel(FilterParams P, int al
     ri.v_cut = v_cut;
     ri.i_cut = i_cut;
     ri.n_kept = (int32_t)n_kept;
-    ri.flags = 0;
+    ri.flags = walked ? kFlagWalked : 0;
     P.info[row] = ri;
     if (P.out != nullptr) {
       const int64_t t = P.target[b * P.tsb + r * P.tsr];
@@ -1290,7 +1291,7 @@ __global__ __launch_bounds__(G::NT, 2048 / G::NT) void filter_compact_kernel(Fil
   const float Z = (float)zs[0];
 
   // ---- top-p cut: (entry, 1-based position inside it) -----------------------
-  bool have_cut = false;
+  bool have_cut = false, walked = false;
   uint32_t cut_ent = 0, cut_pos = 0;
   if (P.has_p) {
     const float inv = 1.0f / Z;
@@ -1352,25 +1353,34 @@ __global__ __launch_bounds__(G::NT, 2048 / G::NT) void filter_compact_kernel(Fil
       const float mid = 0.5f * (t16 + nxt);
       const float Bthr = round_trip<E>(mid) > t16 ? mid : nextafterf(mid, INFINITY);
       const double Bd = (double)Bthr;
-      double bt = 0.0;
-      {
-        double X = X0;
+      // the share's bound bt, its end Xe, and for the tests below without
+      // the other threads' bound D0: smin = min over entries of
+      // (kSlack / 2) X1 - (bound so far), hmax = max of X1 - (bound so far)
+      double bt = 0.0, Xe = X0, smin = INFINITY, hmax = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < CMAX; ++i) {
-          if (in_k(i)) {
-            const double p = (double)rp[i];
-            const uint32_t n = rn[i];
-            const double X1 = X + (double)n * p;
-            bt += run_error_bound(n, p, X, X1);
-            X = X1;
-          }
+      for (int i = 0; i < CMAX; ++i) {
+        if (in_k(i)) {
+          const double p = (double)rp[i];
+          const uint32_t n = rn[i];
+          const double X1 = Xe + (double)n * p;
+          bt += run_error_bound(n, p, Xe, X1);
+          smin = fmin(smin, 0.5 * kSlack * X1 - bt);
+          hmax = fmax(hmax, X1 - bt);
+          Xe = X1;
         }
       }
       double btot;
       const double D0 = block_excl_scan1<double, NW>(bt, sh.red_d + 2 * NW, &btot);
       bool flo = false, fhi = false, slack_ok = true;
       uint32_t klo = 0, plo = 0, khi = 0, phi = 0;
-      {
+      // The search below runs in the shares that may hold the lower or upper
+      // crossing (a margin of 2^-40 over the differently associated sums);
+      // every other share checks each entry's slack, D0 + bound <= (kSlack /
+      // 2) X1, at once.
+      const double Bm = Bd * (1.0 - 0x1p-40);
+      const bool search = Xe + D0 + bt >= Bm || hmax - D0 >= Bm;
+      if (!search) slack_ok = D0 <= smin;
+      if (search) {
         double X = X0, D = D0;
 #pragma unroll
         for (int i = 0; i < CMAX; ++i) {
@@ -1420,6 +1430,7 @@ __global__ __launch_bounds__(G::NT, 2048 / G::NT) void filter_compact_kernel(Fil
         cut_ent = sh.ent_hi;
         cut_pos = sh.pos_hi;
       } else {
+        walked = true;
         // the exact sequence, one wave, 64 entries at a time: a group whose
         // additions are all exact and stay inside S's binade below the
         // threshold is added at once, the others entry by entry (a run of one
@@ -1584,7 +1595,7 @@ __global__ __launch_bounds__(G::NT, 2048 / G::NT) void filter_compact_kernel(Fil
     ri.v_cut = v_cut;
     ri.i_cut = rcut > 0u ? -1 - (int32_t)rcut : 0;
     ri.n_kept = (int32_t)n_kept;
-    ri.flags = 4;
+    ri.flags = kFlagNoKeptList | (walked ? kFlagWalked : 0);
     P.info[row] = ri;
     if (P.out != nullptr) P.out[row] = lp;
   }

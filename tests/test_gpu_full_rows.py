@@ -15,6 +15,8 @@ asserted unused here), keep sets bit-exact.
       the rows whose keep set moves when the normaliser
       moves by one fp32 ulp, and the rows with ties at the cut, are counted and
       printed;
+  the same shape's top-p 0.9 decided in bf16: keep sets of the rows the exact
+      sequential sum decided and of 1024 sampled rows;
   64 packed sequences, V = 256000: logprobs and the logits gradient of the
       GRPO + KL loss, every row.
 """
@@ -195,6 +197,39 @@ def test_filtered_every_row_keep_sets_exact():
     assert n_bad == 0
     assert gr[:, -1].abs().max().item() == 0
     del xl, gr
+
+
+def test_bf16_decided_topp_rows_keep_sets_exact():
+    """Top-p 0.9 decided in bf16 (the reference's rule on the 16-bit tensor) at T = 0.7
+    on the [4, 4096, 151936] top-p workload: the keep sets of the rows whose cut the
+    exact one-element-at-a-time sum decided (row flags bit 3: the error bounds of the
+    parallel sum did not settle them) and of 1024 sampled rows, decoded from the row
+    records, bit-exact against the oracle with an exactly rounded normaliser."""
+    say("bf16-decided top-p rows of [4, 4096, 151936], T=0.7, p=0.9")
+    d = workloads.general_filter_bf16(top_k=None, top_p=0.9, device=DEV)
+    x, ids = d["logits"], d["input_ids"]
+    T, p = d["temperature"], d["top_p"]
+    B, S, V = x.shape
+    R = B * (S - 1)
+    info, _, _ = _C.filtered_fwd(x, ids[:, 1:], T, 0, p, None, None)
+    rec = info.view(torch.int32).view(-1, 6)[:R]
+    walked = ((rec[:, 5].cpu() & 8) != 0).nonzero().flatten()
+    sample = torch.randperm(R, generator=torch.Generator().manual_seed(3))[:1024]
+    rows = torch.unique(torch.cat([walked[:512], sample]))
+    say("rows decided by the exact sum:", walked.numel(), "of", R, "; rows checked:", rows.numel())
+    assert walked.numel() > 0, "no row of the workload exercised the exact sum"
+    n_walked_checked = 0
+    for a in range(0, rows.numel(), 256):
+        rr = rows[a : a + 256]
+        rd = rr.to(DEV)
+        y_dev = x[rd // (S - 1), rd % (S - 1)].div_(T)  # a copy, divided in place as the reference does
+        yc = y_dev.cpu()
+        _, keep_o = top_k_top_p(yc, None, p, exact_normaliser=True)
+        keep = keep_from_row_info(yc.float(), rec[rd])
+        bad = (keep != keep_o).any(-1).nonzero().flatten()
+        assert bad.numel() == 0, f"keep sets differ in rows {rr[bad].tolist()}"
+        n_walked_checked += int(torch.isin(rr, walked).sum())
+    assert n_walked_checked == min(walked.numel(), 512)
 
 
 def test_packed_grpo_kl_every_row(single_rank_group):
