@@ -1098,30 +1098,46 @@ __global__ __launch_bounds__(G::NT, 2048 / G::NT) void filter_compact_kernel(Fil
   // order), then the positive ones by ascending m.
   const uint32_t L0 = (uint32_t)tid * (uint32_t)kWPT;
   const uint32_t key0 = G::kBase + 2u * L0;
+  // The thread's words are read once, into registers, for the counts here and
+  // the entries below; the entries may then overwrite the table after the one
+  // barrier of the offsets.
+  uint32_t wd[kWPT];
+#pragma unroll
+  for (int w = 0; w < kWPT; ++w) wd[w] = sh.u.hist[phys(L0 + (uint32_t)w)];
+  const uint32_t outside = sh.u.hist[phys((uint32_t)G::kWords)];
   uint32_t ct = 0, nzp = 0, nzn = 0, kloc = 0;
-  {
-    uint32_t kpos = 0, kneg = 0;
-    bool seen_neg = false;
+  if constexpr (G::kWindow) {
+    // per word: the count of both halves by one sum of absolute differences,
+    // the occupied halves as (lo != 0) | (hi != 0) << 16 by one packed minimum,
+    // the last occupied positive and the first occupied negative word as
+    // maxima of (w + 1) and (kWPT - w) over the occupied words
+    typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+    uint32_t occ = 0, wpos = 0, wneg = 0;
+#pragma unroll
+    for (int w = 0; w < kWPT; ++w) {
+      ct = __builtin_amdgcn_sad_u16(wd[w], 0u, ct);
+      const uint32_t o = __builtin_bit_cast(
+          uint32_t, __builtin_elementwise_min(__builtin_bit_cast(u16x2, wd[w]), (u16x2)(uint16_t)1));
+      occ += o;
+      wpos = max(wpos, (o & 1u) * (uint32_t)(w + 1));
+      wneg = max(wneg, (o >> 16) * (uint32_t)(kWPT - w));
+    }
+    nzp = occ & 0xffffu;
+    nzn = occ >> 16;
+    const uint32_t kpos = wpos != 0u ? 0x8000u | (L0 + wpos - 1u) : 0u;
+    const uint32_t kneg = wneg != 0u ? 0x7fffu - (L0 + (uint32_t)kWPT - wneg) : 0u;
+    kloc = kpos != 0u ? kpos : kneg;  // key 0 (the largest NaN) orders below every other
+  } else {
+    uint32_t kpos = 0;
 #pragma unroll 8
     for (int w = 0; w < kWPT; ++w) {
-      const uint32_t word = sh.u.hist[phys(L0 + (uint32_t)w)];
-      const uint32_t lo = word & 0xffffu, hi = word >> 16;
+      const uint32_t lo = wd[w] & 0xffffu, hi = wd[w] >> 16;
       ct += lo + hi;
-      if constexpr (G::kWindow) {
-        nzp += lo != 0u ? 1u : 0u;
-        nzn += hi != 0u ? 1u : 0u;
-        if (lo != 0u) kpos = 0x8000u | (L0 + (uint32_t)w);
-        if (hi != 0u && !seen_neg) {
-          kneg = 0x7fffu - (L0 + (uint32_t)w);
-          seen_neg = true;
-        }
-      } else {
-        nzp += (lo != 0u ? 1u : 0u) + (hi != 0u ? 1u : 0u);
-        if (lo != 0u) kpos = key0 + 2u * (uint32_t)w;
-        if (hi != 0u) kpos = key0 + 2u * (uint32_t)w + 1u;
-      }
+      nzp += (lo != 0u ? 1u : 0u) + (hi != 0u ? 1u : 0u);
+      if (lo != 0u) kpos = key0 + 2u * (uint32_t)w;
+      if (hi != 0u) kpos = key0 + 2u * (uint32_t)w + 1u;
     }
-    kloc = kpos != 0u ? kpos : kneg;  // key 0 (the largest NaN) orders below every other
+    kloc = kpos;
   }
   // one barrier for the entry offsets, the numbers of entries, the total
   // count and the largest occupied key
@@ -1159,7 +1175,7 @@ __global__ __launch_bounds__(G::NT, 2048 / G::NT) void filter_compact_kernel(Fil
     off_n = Nn - (bn + in_);     // the negative entries of later threads come first
   }
   // a 16-bit count that wrapped loses a multiple of 65536 from the total
-  if (tot != (uint32_t)V || sh.u.hist[phys((uint32_t)G::kWords)] != 0u || N > (uint32_t)kEntCap) {
+  if (tot != (uint32_t)V || outside != 0u || N > (uint32_t)kEntCap) {
     if (tid == 0) {
       RowInfo ri{};
       ri.flags = 1;
@@ -1167,10 +1183,7 @@ __global__ __launch_bounds__(G::NT, 2048 / G::NT) void filter_compact_kernel(Fil
     }
     return;
   }
-  uint32_t wd[kWPT];
-#pragma unroll
-  for (int w = 0; w < kWPT; ++w) wd[w] = sh.u.hist[phys(L0 + (uint32_t)w)];
-  __syncthreads();  // every table word is in registers: the entries overwrite the table
+  // (every table word was read before the offsets' barrier)
   if constexpr (G::kWindow) {
     // Branch-free: a half with no values writes to this thread's own slot past
     // the entry list (kc[kEntCap + tid], inside the y array, which is written
@@ -1178,19 +1191,24 @@ __global__ __launch_bounds__(G::NT, 2048 / G::NT) void filter_compact_kernel(Fil
     // the others' branches.
     static_assert(kEntCap + NT <= 3 * kEntCap, "the spare slots lie inside the entry arrays");
     const uint32_t spare = (uint32_t)kEntCap + (uint32_t)tid;
-    uint32_t j = off_n;
+    // (a wave whose words are all empty, most of the table, skips both loops)
+    if (nzn != 0u) {
+      uint32_t j = off_n;
 #pragma unroll
-    for (int w = kWPT - 1; w >= 0; --w) {
-      const uint32_t hi = wd[w] >> 16;
-      sh.u.ent.kc[hi != 0u ? j : spare] = (0x7fffu - (L0 + (uint32_t)w)) | (hi << 16);
-      j += hi != 0u ? 1u : 0u;
+      for (int w = kWPT - 1; w >= 0; --w) {
+        const uint32_t hi = wd[w] >> 16;
+        sh.u.ent.kc[hi != 0u ? j : spare] = (0x7fffu - (L0 + (uint32_t)w)) | (hi << 16);
+        j += hi != 0u ? 1u : 0u;
+      }
     }
-    j = off_p;
+    if (nzp != 0u) {
+      uint32_t j = off_p;
 #pragma unroll
-    for (int w = 0; w < kWPT; ++w) {
-      const uint32_t lo = wd[w] & 0xffffu;
-      sh.u.ent.kc[lo != 0u ? j : spare] = (0x8000u | (L0 + (uint32_t)w)) | (lo << 16);
-      j += lo != 0u ? 1u : 0u;
+      for (int w = 0; w < kWPT; ++w) {
+        const uint32_t lo = wd[w] & 0xffffu;
+        sh.u.ent.kc[lo != 0u ? j : spare] = (0x8000u | (L0 + (uint32_t)w)) | (lo << 16);
+        j += lo != 0u ? 1u : 0u;
+      }
     }
   } else {
     uint32_t j = off_p;
@@ -1277,7 +1295,7 @@ __global__ __launch_bounds__(G::NT, 2048 / G::NT) void filter_compact_kernel(Fil
     __syncthreads();
     const uint32_t jk = sh.sel[0];
     y_thr = ey[jk];
-    thr = first_ge(0u, jk, y_thr);
+    thr = (jk == 0u || ey[jk - 1u] < y_thr) ? jk : first_ge(0u, jk, y_thr);
   }
   // entry i of the share is inside the kept-k values
   auto in_k = [&](int i) { return rn[i] != 0u && j0 + (uint32_t)i >= thr; };
@@ -1508,15 +1526,18 @@ __global__ __launch_bounds__(G::NT, 2048 / G::NT) void filter_compact_kernel(Fil
   // ---- the cut's value group, kept count and log-sum-exp --------------------
   uint32_t g_lo, g_hi;
   float v_cut;
-  if (!P.has_p) {
+  // (entries hold distinct keys: equal values only where the temperature
+  // merges keys, so the group is usually the one entry, seen from its
+  // neighbours without a search)
+  if (!P.has_p && P.top_k <= 0) {
     v_cut = y_thr;
     g_lo = thr;
     g_hi = last_le(thr, N - 1u, y_thr);
   } else {
-    const uint32_t ck = have_cut ? cut_ent : N - 1u;
-    v_cut = ey[ck];
-    g_lo = first_ge(thr, ck, v_cut);
-    g_hi = last_le(ck, N - 1u, v_cut);
+    const uint32_t ck = !P.has_p ? thr : have_cut ? cut_ent : N - 1u;
+    v_cut = ey[ck];  // (y_thr when there is no top-p)
+    g_lo = (ck == thr || ey[ck - 1u] < v_cut) ? ck : first_ge(thr, ck, v_cut);
+    g_hi = (ck == N - 1u || ey[ck + 1u] > v_cut) ? ck : last_le(ck, N - 1u, v_cut);
   }
   double ksum_above = 0.0;  // kept mass above the group
   uint32_t cnts[3] = {0u, 0u, 0u};  // elements above the group, in it, in it before the cut entry
