@@ -1327,8 +1327,23 @@ __global__ __launch_bounds__(G::NT, 2048 / G::NT) void filter_compact_kernel(Fil
       if (in_k(i)) mt += (double)rn[i] * (double)rp[i];
     double mtot;
     const double X0 = block_excl_scan1<double, NW>(mt, sh.red_d + NW, &mtot);
-    auto first_in_run = [&](double X, double p, uint32_t n, auto&& hit) {
-      uint32_t a = 1u, c = n;
+    // first addition t in [1, n] of a run X + t p for which hit() holds
+    // (hit(X + n p) holds, and hit is monotone in t), where v is about the
+    // least value hit() accepts: t = ceil((v - X) / p) is checked with its
+    // neighbour, and a binary search finishes only when that misses
+    auto first_in_run = [&](double X, double p, uint32_t n, double v, auto&& hit) {
+      uint32_t a = 1u, c = n;  // the answer lies in [a, c]
+      const double te = ceil((v - X) / p);
+      if (te > 1.0 && te < (double)n) {  // (false for NaN)
+        const uint32_t t = (uint32_t)te;
+        if (hit(X + (double)t * p)) {
+          c = t;
+          if (hit(X + (double)(t - 1u) * p)) c = t - 1u; else a = t;
+        } else {
+          a = t + 1u;
+          if (hit(X + (double)(t + 1u) * p)) c = t + 1u; else a = t + 2u;
+        }
+      }
       while (a < c) {
         const uint32_t mid = a + ((c - a) >> 1);
         if (hit(X + (double)mid * p)) c = mid; else a = mid + 1u;
@@ -1338,6 +1353,8 @@ __global__ __launch_bounds__(G::NT, 2048 / G::NT) void filter_compact_kernel(Fil
     if constexpr (!DEC16) {
       const float cut = P.cut;
       auto hit = [&](double X) { return (float)X > cut; };
+      // the midpoint above cut, about where the fp32 rounding passes it
+      const double vcut = 0.5 * ((double)cut + (double)nextafterf(cut, INFINITY));
       double X = X0;
       bool found = false;
       uint32_t fk = 0, fp = 0;
@@ -1349,7 +1366,7 @@ __global__ __launch_bounds__(G::NT, 2048 / G::NT) void filter_compact_kernel(Fil
           if (hit(X + (double)n * p)) {
             found = true;
             fk = j0 + (uint32_t)i;
-            fp = hit(X) ? 1u : first_in_run(X, p, n, hit);
+            fp = hit(X) ? 1u : first_in_run(X, p, n, vcut, hit);
           }
           X += (double)n * p;
         }
@@ -1414,12 +1431,12 @@ __global__ __launch_bounds__(G::NT, 2048 / G::NT) void filter_compact_kernel(Fil
             if (!flo && hlo(X1)) {
               flo = true;
               klo = j;
-              plo = hlo(X) ? 1u : first_in_run(X, p, n, hlo);
+              plo = hlo(X) ? 1u : first_in_run(X, p, n, Bd - Db, hlo);
             }
             if (!fhi && hhi(X1)) {
               fhi = true;
               khi = j;
-              phi = hhi(X) ? 1u : first_in_run(X, p, n, hhi);
+              phi = hhi(X) ? 1u : first_in_run(X, p, n, Bd + Db, hhi);
             }
             X = X1;
             D = Db;
