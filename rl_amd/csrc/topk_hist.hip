@@ -1466,10 +1466,9 @@ __global__ __launch_bounds__(G::NT, 2048 / G::NT) void filter_compact_kernel(Fil
         cut_pos = sh.pos_hi;
       } else {
         walked = true;
-        // the exact sequence, one wave, 64 entries at a time: a group whose
-        // additions are all exact and stay inside S's binade below the
-        // threshold is added at once, the others entry by entry (a run of one
-        // value in closed form)
+        // the exact sequence, one wave, 64 entries at a time: the lanes whose
+        // additions stay inside S's binade below the threshold are added at
+        // once, the others entry by entry (a run of one value in closed form)
         __syncthreads();  // every thread has read the certification's results
         if (tid < 64) {
           const int lane = tid;
@@ -1483,38 +1482,72 @@ __global__ __launch_bounds__(G::NT, 2048 / G::NT) void filter_compact_kernel(Fil
             int l0 = 0;  // first lane of the group not added yet
             while (l0 < 64 && !hit) {
               if (S > 0.f) {
-                // inside S's binade (ulp u) every addition adds p rounded to
-                // a multiple of u, the same for every S there unless p / u
-                // ends in exactly one half (then the rounding depends on S's
-                // parity): lanes l0.. up to the first such tie, the first
-                // that would leave the binade or reach the threshold, are
-                // added at once
+                // Inside S's binade (ulp u), with S = s u, an addition of p
+                // = P u rounds s + P to an integer: s + round(P), except that
+                // a P ending in exactly one half goes to the even neighbour,
+                // so the step depends on s's parity.  Every run of n equal
+                // additions is then a map s -> s + d[s & 1] (its pair d,
+                // closed form below), the maps compose (f then g: d[b] =
+                // f.d[b] + g.d[(b + f.d[b]) & 1]), and a scan over the lanes
+                // gives s after each lane's run.  Lanes l0.. up to the first
+                // that would leave the binade or reach the threshold are added
+                // at once.  A step of 2^25 or more leaves the binade (s < 2^24)
+                // and is held at 2^25, so that 64 of them fit 32 bits.
                 int eS = ilogbf(S);
                 if (eS < -126) eS = -126;
                 const int eu = eS - 23;
+                const uint32_t s0 = (uint32_t)ldexp((double)S, -eu);  // < 2^24
                 const double q = ldexp((double)p, -eu);
-                const double fq = floor(q);
                 const bool mine = lane >= l0;
-                const bool tie = mine && n != 0u && q - fq == 0.5;
-                const double units = mine ? (double)n * ((q - fq) < 0.5 ? fq : fq + 1.0) : 0.0;
-                double incl = units;
-#pragma unroll
-                for (int o = 1; o < 64; o <<= 1) {
-                  const double v = __shfl_up(incl, o, 64);
-                  if (lane >= o) incl += v;
+                constexpr double kBig = 33554432.0;  // 2^25
+                uint32_t d0 = 0u, d1 = 0u;  // identity for the lanes before l0 and past N
+                if (mine && n != 0u) {
+                  const double fq = floor(q), nd = (double)n;
+                  if (q - fq == 0.5) {
+                    // from an even s every step ends even; from an odd s the
+                    // first step does
+                    const bool odd_a = fq < kBig && (((uint32_t)fq) & 1u) != 0u;
+                    const double e0 = nd * (odd_a ? fq + 1.0 : fq);
+                    const double e1 = odd_a ? e0 - 1.0 : e0 + 1.0;
+                    d0 = e0 >= kBig ? (uint32_t)kBig : (uint32_t)e0;
+                    d1 = e1 >= kBig ? (uint32_t)kBig : (uint32_t)e1;
+                  } else {
+                    const double e = nd * (q - fq < 0.5 ? fq : fq + 1.0);
+                    d0 = d1 = e >= kBig ? (uint32_t)kBig : (uint32_t)e;
+                  }
                 }
-                const double Su = ldexp((double)S, -eu) + incl;  // in units of u
-                const bool bad = mine && (tie || Su >= 16777216.0 || ldexp(Su, eu) >= Bd);
-                const uint64_t badm = __ballot(bad);
-                const int lb = badm ? __ffsll((long long)badm) - 1 : 64;
-                if (lb > l0) {
-                  const double s_at = __shfl(Su, lb - 1, 64);
-                  S = (float)ldexp(s_at, eu);
+                auto past = [&](uint32_t sv) {
+                  return sv >= 16777216u || ldexp((double)sv, eu) >= Bd;
+                };
+                // lane l0 alone already leaves the binade or reaches the
+                // threshold: no scan
+                const uint32_t own0 =
+                    (uint32_t)__builtin_amdgcn_readlane((int)((s0 & 1u) ? d1 : d0), l0);
+                if (!past(s0 + own0)) {
+                  // the scan by DPP moves (the lanes with no source read the
+                  // identity map 0): the earlier lanes' map, then this one's
+                  auto after = [&](uint32_t f0, uint32_t f1) {
+                    const uint32_t g0 = f0 + ((f0 & 1u) ? d1 : d0);
+                    const uint32_t g1 = f1 + ((f1 & 1u) ? d0 : d1);
+                    d0 = g0;
+                    d1 = g1;
+                  };
+                  after(dpp_u32<0x111>(d0), dpp_u32<0x111>(d1));
+                  after(dpp_u32<0x112>(d0), dpp_u32<0x112>(d1));
+                  after(dpp_u32<0x114>(d0), dpp_u32<0x114>(d1));
+                  after(dpp_u32<0x118>(d0), dpp_u32<0x118>(d1));
+                  after(dpp_u32<0x142, 0xa>(d0), dpp_u32<0x142, 0xa>(d1));
+                  after(dpp_u32<0x143, 0xc>(d0), dpp_u32<0x143, 0xc>(d1));
+                  const uint32_t sl = s0 + ((s0 & 1u) ? d1 : d0);
+                  const uint64_t badm = __ballot(mine && past(sl));
+                  const int lb = badm ? __ffsll((long long)badm) - 1 : 64;
+                  // (lb > l0: lane l0 itself stays inside)
+                  S = (float)ldexp((double)(uint32_t)__builtin_amdgcn_readlane((int)sl, lb - 1), eu);
                   l0 = lb;
                   continue;
                 }
               }
-              // lane l0 alone: a tie, a binade crossing, the threshold, or S == 0
+              // lane l0 alone: a binade crossing, the threshold, or S == 0
               const uint32_t nl = (uint32_t)__builtin_amdgcn_readlane((int)n, l0);
               const float pl = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), l0));
               uint32_t at = 0;
