@@ -307,18 +307,20 @@ __device__ bool seq_add_run(float& S, float p, uint32_t n, float B, uint32_t* at
   return false;
 }
 
-// WALK = false: rows whose 16-bit cut the bound leaves undecided are flagged
-// (info.flags bit 0) and left to the WALK = true launch, which decides them by
-// the exact sequence.
+// One row of filter_hist_kernel.  WALK = false: a row whose 16-bit cut the
+// bound leaves undecided is flagged again (info.flags bit 0) and left to the
+// WALK = true launch, which decides it by the exact sequence.
 template <class E, int NV, bool WALK>
-__global__ __launch_bounds__(kHT) void filter_hist_kernel(FilterParams P, int all_rows) {
+__device__ __forceinline__ void hist_row(const FilterParams& P, const int64_t row) {
   using raw = typename E::raw;
   __shared__ HistShared sh;
-  const int64_t row = blockIdx.x;
-  if (!all_rows && (P.info[row].flags & 1) == 0) return;
   const int64_t b = row / P.R, r = row - b * P.R;
   const raw* x = static_cast<const raw*>(P.logits) + b * P.sb + r * P.sr;
-  const int tid = threadIdx.x, lane = tid & 63;
+  // (the thread index passes an empty asm once per row, so that nothing
+  // derived from it is kept across the rows of filter_hist_kernel's loop)
+  int tid_ = threadIdx.x;
+  asm volatile("" : "+v"(tid_));
+  const int tid = tid_, lane = tid & 63;
   const int64_t V = P.V;
   const RowSpan<E> sp(x, V);
   const vu4* xv = reinterpret_cast<const vu4*>(x + sp.head);
@@ -858,6 +860,34 @@ __global__ __launch_bounds__(kHT) void filter_hist_kernel(FilterParams P, int al
       }
       P.out[row] = lp;
     }
+  }
+}
+
+// The rows flagged (info.flags bit 0) among this workgroup's share, rows
+// blockIdx.x + k gridDim.x for k < per (<= kHT): their flags are read at once,
+// the flagged rows listed in LDS and decided one after another, so that a
+// launch over rows of which few or none are flagged costs a few microseconds.
+template <class E, int NV, bool WALK>
+__global__ __launch_bounds__(kHT) void filter_hist_kernel(FilterParams P, int64_t rows, int per) {
+  __shared__ int s_n;
+  __shared__ int64_t s_rows[kHT];
+  const int tid = threadIdx.x;
+  if (tid == 0) s_n = 0;
+  __syncthreads();
+  if (tid < per) {
+    const int64_t row = (int64_t)blockIdx.x + (int64_t)tid * gridDim.x;
+    if (row < rows && (P.info[row].flags & 1) != 0) s_rows[atomicAdd(&s_n, 1)] = row;
+  }
+  __syncthreads();
+  // (the count and the rows are uniform: in scalar registers, as blockIdx.x
+  // would be, so that the loop is not taken for a divergent one)
+  const int n = __builtin_amdgcn_readfirstlane(s_n);
+  for (int i = 0; i < n; ++i) {
+    const uint64_t rw = (uint64_t)s_rows[i];
+    const int64_t row = (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(rw >> 32)) << 32) |
+                                  (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)rw));
+    hist_row<E, NV, WALK>(P, row);
+    __syncthreads();  // the row's last reads of the table before the next row clears it
   }
 }
 
@@ -1748,13 +1778,16 @@ int launch_hist(const FilterParams& P, int64_t rows, int all_rows, hipStream_t s
     hipLaunchKernelGGL((filter_compact_kernel<E, G, false>), dim3((unsigned)rows), dim3(G::NT), 0,
                        st, P, all_rows);
   if (int e = check_launch("filter_compact_kernel")) return e;
-  hipLaunchKernelGGL((filter_hist_kernel<E, 0, false>), dim3((unsigned)rows), dim3(kHT), 0, st, P,
-                     0);
+  // the flagged rows, each workgroup over a share of at most kHT rows
+  const int64_t grid = std::min<int64_t>(rows, std::max<int64_t>(256, (rows + kHT - 1) / kHT));
+  const int per = (int)((rows + grid - 1) / grid);
+  hipLaunchKernelGGL((filter_hist_kernel<E, 0, false>), dim3((unsigned)grid), dim3(kHT), 0, st, P,
+                     rows, per);
   if (int e = check_launch("filter_hist_kernel")) return e;
   if (!P.dec16) return MIRL_OK;
   // rows the rounding bound left undecided
-  hipLaunchKernelGGL((filter_hist_kernel<E, 0, true>), dim3((unsigned)rows), dim3(kHT), 0, st, P,
-                     0);
+  hipLaunchKernelGGL((filter_hist_kernel<E, 0, true>), dim3((unsigned)grid), dim3(kHT), 0, st, P,
+                     rows, per);
   return check_launch("filter_hist_kernel(walk)");
 }
 
