@@ -975,13 +975,12 @@ __device__ __forceinline__ uint32_t okey16x2(uint32_t w) {
 // waves (two 512-thread rows per CU for the window table; one 1024-thread row for
 // the full one).
 template <class E, class G, bool DEC16>
-__global__ __launch_bounds__(G::NT, 2048 / G::NT) void filter_compact_kernel(FilterParams P, int all_rows) {
+__global__ __launch_bounds__(G::NT, 2048 / G::NT) void filter_compact_kernel(FilterParams P) {
   using raw = typename E::raw;
   using SH = CompactShared<G>;
   constexpr int NT = G::NT, NW = SH::NW, kWPT = SH::kWPT, kEntCap = SH::kEntCap;
   __shared__ SH sh;
   const int64_t row = blockIdx.x;
-  if (!all_rows && (P.info[row].flags & 1) == 0) return;
   const int64_t b = row / P.R, r = row - b * P.R;
   const raw* x = static_cast<const raw*>(P.logits) + b * P.sb + r * P.sr;
   const int tid = threadIdx.x;
@@ -1771,13 +1770,18 @@ int launch_hist(const FilterParams& P, int64_t rows, int all_rows, hipStream_t s
   // the compact kernel first; the rows it flags go to filter_hist_kernel
   using G = typename std::conditional<std::is_same<E, BF16>::value, CompactWindow,
                                       CompactFull>::type;
-  if (P.dec16)
-    hipLaunchKernelGGL((filter_compact_kernel<E, G, true>), dim3((unsigned)rows), dim3(G::NT), 0, st,
-                       P, all_rows);
-  else
-    hipLaunchKernelGGL((filter_compact_kernel<E, G, false>), dim3((unsigned)rows), dim3(G::NT), 0,
-                       st, P, all_rows);
-  if (int e = check_launch("filter_compact_kernel")) return e;
+  // (after the fast kernel, all_rows == 0, the few rows it flagged, if any, go
+  // straight to filter_hist_kernel: a compact launch over every row to find
+  // them would cost more than it saves)
+  if (all_rows) {
+    if (P.dec16)
+      hipLaunchKernelGGL((filter_compact_kernel<E, G, true>), dim3((unsigned)rows), dim3(G::NT), 0,
+                         st, P);
+    else
+      hipLaunchKernelGGL((filter_compact_kernel<E, G, false>), dim3((unsigned)rows), dim3(G::NT), 0,
+                         st, P);
+    if (int e = check_launch("filter_compact_kernel")) return e;
+  }
   // the flagged rows, each workgroup over a share of at most kHT rows
   const int64_t grid = std::min<int64_t>(rows, std::max<int64_t>(256, (rows + kHT - 1) / kHT));
   const int per = (int)((rows + grid - 1) / grid);
