@@ -332,6 +332,39 @@ def test_full_size_workload_sampled_rows():
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("k,p", [(None, 0.9), (10, 0.9), (None, 0.5)])
+def test_many_flagged_rows_share_fallback_workgroups(dtype, k, p):
+    """800 rows of which many go to the full-table kernel: a value of 600 in every third
+    row (outside the bf16 count window) and all-equal rows (every element ties with the
+    k-th value, so the fast top-k kernel hands them on).  That kernel runs on 256
+    workgroups here, each reading the flags of its share of rows at once and deciding up
+    to four flagged rows in turn.  Keep sets against the oracle with an exactly rounded
+    normaliser (the kernels' rule: with CPU torch's fp32 normaliser one row of the
+    (None, 0.5) bf16 case keeps one more element, a probability at the cut that the
+    normaliser's last bit moves), logprobs against the oracle on the other rows."""
+    print("[case] many flagged rows", dtype, k, p, flush=True)
+    V = 3001
+    g = torch.Generator().manual_seed(41)
+    x = torch.randn(2, 400, V, generator=g)
+    x[:, ::3, 7] = 600.0
+    x[:, 1::5] = 0.0
+    x[:, 1::5, 11] = 1.0
+    x = x.to(dtype)
+    ids = torch.randint(0, V, (2, 400), generator=g)
+    lp_o, keep_t = filtered_logprobs(x, ids, k, p)
+    keep_x = top_k_top_p(x, k, p, exact_normaliser=True)[1] if p < 1.0 else keep_t
+    same = (keep_t == keep_x).all(-1)
+    assert int((~same).sum()) <= 2
+    lp = DistributedLogprobWithSampling.apply(x.to(DEV), ids.to(DEV), None, k, p, True)
+    lp_c = lp.cpu()
+    assert torch.equal(torch.isinf(lp_c[same]), torch.isinf(lp_o[same]))
+    fin = torch.isfinite(lp_o) & same
+    torch.testing.assert_close(lp_c[fin], lp_o[fin], rtol=0, atol=2e-3)
+    _, keep = apply_top_k_top_p(x.to(DEV), k, p)
+    assert torch.equal(keep.cpu(), keep_x)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("k,p", [(None, 0.9), (None, 0.5), (3000, 0.9)])
 def test_values_outside_the_bf16_count_window(dtype, k, p):
     """Rows holding values of magnitude 512 and beyond (and -inf, +-0) next to ordinary ones.
