@@ -28,6 +28,7 @@ roofline (the default line above is the headline measurement):
   topp_only    as topk_filter with top-p 0.9 alone (no top-k): the histogram path
   topk2000     as topk_filter with k = 2000, p = 0.9: the histogram path
   topp_only_f32 as topp_only with fp32 logits: the fp32 two-pass path
+  topp_only_f16 as topp_only with fp16 logits: the histogram path over the full 65536-key table
   filtered16_fwd  forward-only filtered logprobs decided in bf16 (the Megatron logprob
                post-processor's call on the scaled bf16 logits), T=0.7, p=0.9
   packed_kl    packed GRPO step with k3 KL, 64 sequences in bf16 [1, ~34.8k, 256000],
@@ -65,7 +66,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--workload", default="grpo",
                     choices=["grpo", "fwd_f32", "long_context", "topk_filter", "topk_filter_fused",
-                             "topp_only", "topk2000", "topp_only_f32", "filtered16_fwd", "packed_kl",
+                             "topp_only", "topk2000", "topp_only_f32", "topp_only_f16", "filtered16_fwd", "packed_kl",
                              "linear_ce",
                              "distill_rkl", "score_centering", "topk_export"])
     ap.add_argument("--dtype", default="bf16", choices=["bf16", "fp16", "fp32"],
@@ -588,7 +589,7 @@ def bench_workload(args) -> None:
 
             return _cpu_timed(run, n_s, f"the first {n_s} of the {rows} next-token rows (V={V}, bf16, "
                               "chunk 4096): forward + backward", secs)
-    elif w in ("topk_filter", "topp_only", "topk2000", "topp_only_f32", "filtered16_fwd"):
+    elif w in ("topk_filter", "topp_only", "topk2000", "topp_only_f32", "topp_only_f16", "filtered16_fwd"):
         from rl_amd.algorithms.logits_sampling_utils import TrainingSamplingParams, apply_temperature_scaling
         from rl_amd.distributed.model_utils import get_next_token_logprobs_from_logits
 
@@ -598,6 +599,8 @@ def bench_workload(args) -> None:
             d = workloads.general_filter_bf16(top_k=2000, top_p=0.9, device=dev)
         elif w == "topp_only_f32":
             d = workloads.general_filter_bf16(top_k=None, top_p=0.9, device=dev, dtype=torch.float32)
+        elif w == "topp_only_f16":
+            d = workloads.general_filter_bf16(top_k=None, top_p=0.9, device=dev, dtype=torch.float16)
         else:
             d = workloads.general_filter_bf16(top_k=None, top_p=0.9, device=dev)
         raw = d["logits"]
@@ -670,7 +673,8 @@ def bench_workload(args) -> None:
             cfg = {"workload": {"topk_filter": "topk_topp_temperature_filtered_logprob_fwd_bwd",
                                 "topp_only": "topp_temperature_filtered_logprob_fwd_bwd",
                                 "topk2000": "topk2000_topp_temperature_filtered_logprob_fwd_bwd",
-                                "topp_only_f32": "fp32_topp_temperature_filtered_logprob_fwd_bwd"}[w],
+                                "topp_only_f32": "fp32_topp_temperature_filtered_logprob_fwd_bwd",
+                                "topp_only_f16": "fp16_topp_temperature_filtered_logprob_fwd_bwd"}[w],
                    "logits": [B, S, V], "temperature": T, "top_k": k, "top_p": p, "next_token_rows": rows,
                    "call": "apply_temperature_scaling in place, get_next_token_logprobs_from_logits("
                            "sampling_params), backward to the raw logits (the division's backward "
@@ -682,7 +686,7 @@ def bench_workload(args) -> None:
         extra["filtered_fwd_gbps"] = fwd_bytes / (fwd_ms * 1e-3) / 1e9 if fwd_ms > 0 else None
         extra["filtered_bwd_gbps"] = bwd_bytes / (bwd_ms * 1e-3) / 1e9 if bwd_ms > 0 else None
         extra["temperature_scale_gbps"] = scale_bytes / (sc_ms * 1e-3) / 1e9 if sc_ms > 0 else None
-        dtype = "fp32" if esz == 4 else "bf16"
+        dtype = "fp32" if esz == 4 else ("fp16" if raw.dtype == torch.float16 else "bf16")
     elif w == "topk_filter_fused":
         from rl_amd.distributed.sampling import filtered_next_token_logprobs
 

@@ -187,7 +187,7 @@ def general_filter_bf16(
     boost per row) for filters that keep large sets (top-p alone, k = 2000);
     targets 90% uniform over each row's kept set (found with a descending sort
     in chunks of 512 rows), 10% uniform over the vocabulary.  `dtype` is the
-    logits dtype (bf16 or fp32)."""
+    logits dtype (bf16, fp16 or fp32)."""
     g = _gen(seed)
     dev = torch.device(device) if device is not None else torch.device("cpu")
     logits = _randn_bf16((B, S, V), 1.0, g, device, dtype)

@@ -1,4 +1,5 @@
-"""fp32 rows filtered with top-p alone or k > 1024 (the two-pass kernel) against the oracle (GPU).
+"""fp32 rows, and fp16 rows decided in fp32, filtered with top-p alone or k > 1024 (the
+two-pass kernel) against the oracle (GPU).
 
 The oracle is the fp32 rule of ``top_k_top_p(..., exact_normaliser=True)``
 (reference nemo_rl/algorithms/logits_sampling_utils.py:111-212 on the fp32
@@ -26,9 +27,9 @@ DEV = torch.device("cuda", 0)
 CASES = [(None, 0.9), (None, 0.5), (None, 0.99), (None, 0.05), (2000, 0.9), (5000, 0.3), (1100, 1.0)]
 
 
-def _rows(S: int, seed: int) -> torch.Tensor:
-    """fp32 rows shaped like the filtered workload: N(0, 1) plus a Zipf-ranked +8 boost."""
-    d = workloads.general_filter_bf16(B=1, S=S, top_k=None, top_p=0.9, seed=seed, dtype=torch.float32)
+def _rows(S: int, seed: int, dtype=torch.float32) -> torch.Tensor:
+    """Rows shaped like the filtered workload: N(0, 1) plus a Zipf-ranked +8 boost."""
+    d = workloads.general_filter_bf16(B=1, S=S, top_k=None, top_p=0.9, seed=seed, dtype=dtype)
     return d["logits"]
 
 
@@ -49,11 +50,12 @@ def _expected(y: torch.Tensor, keep: torch.Tensor, tgt: torch.Tensor, gout=None,
 
 
 def _check_rows(x: torch.Tensor, k, p, T: float, expect_two_pass: bool):
-    """x [1, S, V] fp32 on the CPU: forward records, keep sets and logprobs against the oracle."""
+    """x [1, S, V] (fp32 or fp16) on the CPU: forward records, keep sets and logprobs
+    against the oracle on y = dtype(x * fl32(1 / T)) upcast to fp32."""
     S, V = x.shape[1], x.shape[2]
     g = torch.Generator().manual_seed(5)
     ids = torch.randint(0, V, (1, S), generator=g)
-    y = apply_temperature(x, T)[0, :-1]
+    y = apply_temperature(x, T)[0, :-1].float()
     # half the targets on the row maximum (kept), the rest uniform
     ids[0, 1::2] = y[::2].argmax(-1)
     xd = x.to(DEV)
@@ -78,19 +80,21 @@ def _check_rows(x: torch.Tensor, k, p, T: float, expect_two_pass: bool):
 
 @pytest.mark.parametrize("k,p", CASES)
 @pytest.mark.parametrize("T", [1.0, 0.7])
-def test_workload_rows_keep_sets_exact(k, p, T):
-    print("[case] f32 two-pass", k, p, T, flush=True)
-    x = _rows(65, seed=31 + (k or 0))
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_workload_rows_keep_sets_exact(k, p, T, dtype):
+    print("[case] two-pass", dtype, k, p, T, flush=True)
+    x = _rows(65, seed=31 + (k or 0), dtype=dtype)
     _check_rows(x, k, p, T, expect_two_pass=True)
 
 
 @pytest.mark.parametrize("k,p", [(None, 0.9), (2000, 0.9), (None, 0.5)])
-def test_exact_third_pass(k, p, monkeypatch):
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_exact_third_pass(k, p, dtype, monkeypatch):
     """Every row's mass below the bracket summed exactly (the pass an undecided
     bound falls back to): same keep sets."""
-    print("[case] f32 third pass", k, p, flush=True)
+    print("[case] third pass", dtype, k, p, flush=True)
     monkeypatch.setenv("MIRL_F32_FILTER_EXACT_BELOW", "1")
-    x = _rows(33, seed=77)
+    x = _rows(33, seed=77, dtype=dtype)
     _check_rows(x, k, p, 0.7, expect_two_pass=True)
 
 
@@ -119,15 +123,18 @@ def test_rows_outside_the_table_take_the_radix_kernel():
 
 
 @pytest.mark.parametrize("k,p", [(None, 0.9), (3000, 0.8)])
-def test_backward_against_oracle(k, p):
-    """The row backward with the two-pass kernel's index cut: gradient within 1e-3."""
-    print("[case] f32 backward", k, p, flush=True)
-    x = _rows(17, seed=41)
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_backward_against_oracle(k, p, dtype):
+    """The row backward with the two-pass kernel's index cut: gradient within 1e-3 for
+    fp32 rows, 2e-3 for fp16 rows (the fp16 gradient and the division's backward round
+    twice, half an fp16 ulp each)."""
+    print("[case] backward", dtype, k, p, flush=True)
+    x = _rows(17, seed=41, dtype=dtype)
     S, V = x.shape[1], x.shape[2]
     T = 0.7
     g = torch.Generator().manual_seed(8)
     ids = torch.randint(0, V, (1, S), generator=g)
-    y = apply_temperature(x, T)[0, :-1]
+    y = apply_temperature(x, T)[0, :-1].float()
     ids[0, 1::2] = y[::2].argmax(-1)
     gout = torch.randn(1, S - 1, generator=g)
     _, keep_exp = top_k_top_p(y, k, p, exact_normaliser=True)
@@ -137,15 +144,17 @@ def test_backward_against_oracle(k, p):
     (gr,) = torch.autograd.grad(lp, [xd], gout.to(DEV))
     fin = torch.isfinite(lp_o)
     torch.testing.assert_close(lp.detach().cpu()[0][fin], lp_o[fin], rtol=0, atol=1e-5)
-    grc = gr.cpu()[0]
-    torch.testing.assert_close(grc[:-1], gy, rtol=0, atol=1e-3)
+    grc = gr.cpu()[0].float()
+    torch.testing.assert_close(grc[:-1], gy, rtol=0, atol=1e-3 if dtype == torch.float32 else 2e-3)
     assert grc[-1].abs().max().item() == 0
 
 
-def test_mask_entry_point():
-    """mirl_top_k_top_p_mask on fp32 rows (top-p alone): the oracle's keep mask."""
-    print("[case] f32 mask", flush=True)
-    x = _rows(17, seed=50)[0]
-    keep_exp = top_k_top_p(x, None, 0.9, exact_normaliser=True)[1]
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_mask_entry_point(dtype):
+    """mirl_top_k_top_p_mask on fp32 rows, and on fp16 rows decided in fp32 (top-p
+    alone): the oracle's keep mask."""
+    print("[case] mask", dtype, flush=True)
+    x = _rows(17, seed=50, dtype=dtype)[0]
+    keep_exp = top_k_top_p(x.float(), None, 0.9, exact_normaliser=True)[1]
     _, keep = _C.top_k_top_p_mask(x.to(DEV), 0, 0.9, decision_dtype=torch.float32)
     assert torch.equal(keep.cpu(), keep_exp)
