@@ -212,13 +212,6 @@ int launch_resolve_rows(const FilterParams& P, int dtype, int64_t rows, hipStrea
 // cannot finish are flagged (info.flags bit 0) for filter_general_kernel.
 int launch_f32_rows(const FilterParams& P, int64_t rows, hipStream_t st);
 
-// The same two passes over fp16 rows decided in fp32 (every row; the rows it
-// cannot finish are flagged, info.flags bit 0, for filter_hist_kernel).  An
-// fp16 row of the vocabulary holds about 20000 distinct values, more than the
-// compact kernel's entry list takes, while the two-pass kernel's bins are the
-// bf16 truncations of the values.
-int launch_f16_two_pass_rows(const FilterParams& P, int64_t rows, hipStream_t st);
-
 // Largest vocabulary the histogram kernel accepts (its exact-count table
 // covers at most 8 values repeated 65536 times or more).
 constexpr int64_t kHistMaxV = 9 * 65536 - 1;

@@ -1,7 +1,5 @@
 // Top-k / top-p filtered forward for fp32 rows whose filter keeps large sets
-// (top-p without top-k, or k > 1024): two passes over each row.  The same
-// kernel body takes fp16 rows decided in fp32 (filter_f16_two_pass_kernel):
-// y = fp16(fl32(x * fl32(1 / T))), everything after it as below.
+// (top-p without top-k, or k > 1024): two passes over each row.
 //
 // Semantics (those of topk_filter.hip with fp32 decisions; reference
 // nemo_rl/algorithms/logits_sampling_utils.py:111-212 on the fp32 tensor of
@@ -78,12 +76,11 @@ struct F32Shared {
 // -0.0 becomes +0.0 (the order key treats them as one value, and so must the table)
 __device__ __forceinline__ float canon(float y) { return y + 0.0f; }
 
-// The filtered value y = dtype(fl32(x * fl32(1 / T))) (the in-place
-// division's output); -0.0 is left as it is (the float comparisons and the
-// order key treat it as +0.0).
-template <class E, bool HAS_T>
+// The filtered value y = fl32(x * fl32(1 / T)); -0.0 is left as it is (the
+// float comparisons and the order key treat it as +0.0).
+template <bool HAS_T>
 __device__ __forceinline__ float y_of(float x, float rT) {
-  if constexpr (HAS_T) return round_trip<E>(mul_rn(x, rT));
+  if constexpr (HAS_T) return mul_rn(x, rT);
   else return x;
 }
 // Calls f(std::integral_constant<bool, has_t>): the streaming loops are
@@ -150,16 +147,15 @@ __device__ __forceinline__ void bin_bounds(uint32_t k16, float M, double& elo, d
 // where an element is, so that a wave's ballots and the counts kept from them
 // stay the same in all its lanes), the body as 16-byte vectors in batches of
 // UB per lane with the next batch in flight while the current one is visited.
-template <class E, int UB, bool HAS_T, class F>
-__device__ __forceinline__ void stream_row(const typename E::raw* x, int64_t V, float rT, F&& f) {
-  constexpr int VEC = E::kVec;
+template <int UB, bool HAS_T, class F>
+__device__ __forceinline__ void stream_row(const float* x, int64_t V, float rT, F&& f) {
   const int tid = threadIdx.x;
-  const RowSpan<E> sp(x, V);
+  const RowSpan<F32> sp(x, V);
   if (tid < kWave) {  // the whole of wave 0
     const bool hv = tid < sp.head;
-    f(hv ? y_of<E, HAS_T>(E::load(x + tid), rT) : 0.f, (uint32_t)tid, hv);
+    f(hv ? y_of<HAS_T>(x[tid], rT) : 0.f, (uint32_t)tid, hv);
     const bool tv = sp.tail0 + tid < V;
-    f(tv ? y_of<E, HAS_T>(E::load(x + sp.tail0 + tid), rT) : 0.f, (uint32_t)(sp.tail0 + tid), tv);
+    f(tv ? y_of<HAS_T>(x[sp.tail0 + tid], rT) : 0.f, (uint32_t)(sp.tail0 + tid), tv);
   }
   const vu4* xv = reinterpret_cast<const vu4*>(x + sp.head);
   const int nv = (int)sp.nvec;  // < 2^29: V < 2^31
@@ -174,22 +170,12 @@ __device__ __forceinline__ void stream_row(const typename E::raw* x, int64_t V, 
   auto visit = [&](const vu4(&q)[UB], int bi) {
 #pragma unroll
     for (int u = 0; u < UB; ++u) {
-      const uint32_t j0 = head + (uint32_t)VEC * (uint32_t)(bi * kStep + tid + u * kFT);
-      if constexpr (VEC == 4) {
-        f(y_of<E, HAS_T>(__uint_as_float(q[u].x), rT), j0, true);
-        f(y_of<E, HAS_T>(__uint_as_float(q[u].y), rT), j0 + 1u, true);
-        f(y_of<E, HAS_T>(__uint_as_float(q[u].z), rT), j0 + 2u, true);
-        f(y_of<E, HAS_T>(__uint_as_float(q[u].w), rT), j0 + 3u, true);
-        __builtin_amdgcn_sched_barrier(0);  // one vector at a time (register budget)
-      } else {
-        float w[VEC];
-        E::unpack(q[u], w);
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-          f(y_of<E, HAS_T>(w[e], rT), j0 + (uint32_t)e, true);
-          if ((e & 3) == 3) __builtin_amdgcn_sched_barrier(0);  // four values at a time
-        }
-      }
+      const uint32_t j0 = head + 4u * (uint32_t)(bi * kStep + tid + u * kFT);
+      f(y_of<HAS_T>(__uint_as_float(q[u].x), rT), j0, true);
+      f(y_of<HAS_T>(__uint_as_float(q[u].y), rT), j0 + 1u, true);
+      f(y_of<HAS_T>(__uint_as_float(q[u].z), rT), j0 + 2u, true);
+      f(y_of<HAS_T>(__uint_as_float(q[u].w), rT), j0 + 3u, true);
+      __builtin_amdgcn_sched_barrier(0);  // one vector at a time (register budget)
     }
   };
   if (nfull > 0) issue(qa, 0);
@@ -207,14 +193,11 @@ __device__ __forceinline__ void stream_row(const typename E::raw* x, int64_t V, 
     // the remaining vectors: every lane of a wave visits them, valid where one is
     const bool vv = v < nv;
     const vu4 q = vv ? __builtin_nontemporal_load(xv + v) : vu4{0u, 0u, 0u, 0u};
-    const uint32_t j0 = head + (uint32_t)VEC * (uint32_t)v;
-    float w[VEC];
-    E::unpack(q, w);
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) {
-      f(y_of<E, HAS_T>(w[e], rT), j0 + (uint32_t)e, vv);
-      if ((e & 3) == 3) __builtin_amdgcn_sched_barrier(0);  // four values at a time
-    }
+    const uint32_t j0 = head + 4u * (uint32_t)v;
+    f(y_of<HAS_T>(__uint_as_float(q.x), rT), j0, vv);
+    f(y_of<HAS_T>(__uint_as_float(q.y), rT), j0 + 1u, vv);
+    f(y_of<HAS_T>(__uint_as_float(q.z), rT), j0 + 2u, vv);
+    f(y_of<HAS_T>(__uint_as_float(q.w), rT), j0 + 3u, vv);
   }
 }
 
@@ -437,14 +420,14 @@ __device__ __forceinline__ void flag_row(const FilterParams& P, int64_t row) {
 // vb1), and the collection of the bracket [vb1, vb2e) and of the k-th largest
 // value's bin [vlo, vloe) into LDS.  TOPK: some values fall below the k-th
 // largest value's bin (otherwise every value is kept-k and the tests drop).
-template <class E, bool TOPK, bool HAS_T>
-__device__ __forceinline__ void pass2(const typename E::raw* x, int64_t V, const FilterParams& P,
+template <bool TOPK, bool HAS_T>
+__device__ __forceinline__ void pass2(const float* x, int64_t V, const FilterParams& P,
                                       F32Shared& sh, float M, float vinc, float vb1, float vb2e,
                                       float vlo, float vloe, double& zall, double& db) {
   // each wave appends to its own segment at a wave-uniform count: no atomics
   uint64_t* seg = sh.u.cand + (threadIdx.x >> 6) * kWaveCap;
   uint32_t wc = 0u;
-  stream_row<E, kUB, HAS_T>(x, V, P.rT, [&](float y, uint32_t j, bool valid) {
+  stream_row<kUB, HAS_T>(x, V, P.rT, [&](float y, uint32_t j, bool valid) {
     const double de = valid ? (double)exp_le0(y - M) : 0.0;
     const bool below = y < vb1;
     bool coll = valid && !below && y < vb2e;
@@ -470,13 +453,11 @@ __device__ __forceinline__ void pass2(const typename E::raw* x, int64_t V, const
   if ((threadIdx.x & 63) == 0) sh.wcnt[threadIdx.x >> 6] = wc;
 }
 
-// One row (blockIdx.x) of fp32 or fp16 logits, decided in fp32.
-template <class E>
-__device__ __forceinline__ void two_pass_row(FilterParams P) {
+__global__ __launch_bounds__(kFT, 4) void filter_f32_kernel(FilterParams P) {
   __shared__ F32Shared sh;
   const int64_t row = blockIdx.x;
   const int64_t b = row / P.R, r = row - b * P.R;
-  const typename E::raw* x = static_cast<const typename E::raw*>(P.logits) + b * P.sb + r * P.sr;
+  const float* x = static_cast<const float*>(P.logits) + b * P.sb + r * P.sr;
   const int tid = threadIdx.x;
   const int64_t V = P.V;
 
@@ -496,7 +477,7 @@ __device__ __forceinline__ void two_pass_row(FilterParams P) {
   float yt = 0.f;
   if (tid == 0 && P.out != nullptr) {
     t = P.target[b * P.tsb + r * P.tsr];
-    if (t >= 0 && t < V) yt = canon(scaled<E>(E::load(x + t), P));
+    if (t >= 0 && t < V) yt = canon(P.has_t ? mul_rn(x[t], P.rT) : x[t]);
   }
 
   // ---- pass 1: the maximum and the 16-bit prefix counts ----
@@ -504,7 +485,7 @@ __device__ __forceinline__ void two_pass_row(FilterParams P) {
   {
     char* hb = reinterpret_cast<char*>(sh.u.hist);
     with_t(P.has_t, [&](auto ht) {
-      stream_row<E, kUB, decltype(ht)::value>(x, V, P.rT, [&](float y, uint32_t, bool valid) {
+      stream_row<kUB, decltype(ht)::value>(x, V, P.rT, [&](float y, uint32_t, bool valid) {
         if (!valid) return;
         y = canon(y);  // -0.0 counted with +0.0, as the order key has it
         mloc = fmaxf(mloc, y);
@@ -664,8 +645,8 @@ __device__ __forceinline__ void two_pass_row(FilterParams P) {
   __builtin_amdgcn_s_setprio(0);
   with_t(P.has_t, [&](auto ht) {
     constexpr bool HT = decltype(ht)::value;
-    if (topk) pass2<E, true, HT>(x, V, P, sh, M, vinc, vb1, vb2e, vlo, vloe, zall, db);
-    else pass2<E, false, HT>(x, V, P, sh, M, vinc, vb1, vb2e, vlo, vloe, zall, db);
+    if (topk) pass2<true, HT>(x, V, P, sh, M, vinc, vb1, vb2e, vlo, vloe, zall, db);
+    else pass2<false, HT>(x, V, P, sh, M, vinc, vb1, vb2e, vlo, vloe, zall, db);
   });
   __builtin_amdgcn_s_setprio(2);
   double zd[2] = {zall, db};
@@ -790,7 +771,7 @@ __device__ __forceinline__ void two_pass_row(FilterParams P) {
       double dx = 0.0;
       __builtin_amdgcn_s_setprio(0);
       with_t(P.has_t, [&](auto ht) {
-        stream_row<E, kUB, decltype(ht)::value>(x, V, P.rT, [&](float y, uint32_t, bool valid) {
+        stream_row<kUB, decltype(ht)::value>(x, V, P.rT, [&](float y, uint32_t, bool valid) {
           const bool below_b1 = valid && y >= vinc && y < vb1;
           dx += below_b1 ? (double)(exp_le0(y - M) * inv) : 0.0;
         });
@@ -871,21 +852,11 @@ __device__ __forceinline__ void two_pass_row(FilterParams P) {
   }
 }
 
-__global__ __launch_bounds__(kFT, 4) void filter_f32_kernel(FilterParams P) { two_pass_row<F32>(P); }
-__global__ __launch_bounds__(kFT, 4) void filter_f16_two_pass_kernel(FilterParams P) {
-  two_pass_row<F16>(P);
-}
-
 }  // namespace
 
 int launch_f32_rows(const FilterParams& P, int64_t rows, hipStream_t st) {
   hipLaunchKernelGGL(filter_f32_kernel, dim3((unsigned)rows), dim3(kFT), 0, st, P);
   return check_launch("filter_f32_kernel");
-}
-
-int launch_f16_two_pass_rows(const FilterParams& P, int64_t rows, hipStream_t st) {
-  hipLaunchKernelGGL(filter_f16_two_pass_kernel, dim3((unsigned)rows), dim3(kFT), 0, st, P);
-  return check_launch("filter_f16_two_pass_kernel");
 }
 
 }  // namespace mirl

@@ -1820,11 +1820,6 @@ int launch_fwd(const FilterParams& P, int64_t rows, hipStream_t st) {
     if (int e = check_launch("filter_fast_kernel")) return e;
   }
   // the rows left to a general path: all of them, or those the fast kernel flagged
-  if (std::is_same<E, F16>::value && !fast && !P.dec16 && P.V <= kHistMaxV) {
-    // fp16 rows decided in fp32: two passes, the rows it flags to the histogram kernel
-    if (int e = launch_f16_two_pass_rows(P, rows, st)) return e;
-    return launch_hist_rows(P, dtype_code<E>(), rows, 0, st);
-  }
   if (sizeof(typename E::raw) == 2 && P.V <= kHistMaxV)
     return launch_hist_rows(P, dtype_code<E>(), rows, fast ? 0 : 1, st);
   bool all = !fast;

@@ -926,6 +926,12 @@ struct CompactFull {
   static constexpr int kWords = 32768;      // logical words (2 keys each)
   static constexpr bool kWindow = false;
   static constexpr bool kPad = true;        // one pad word per 32 (strided reads of 32 words)
+  // Lean entries: the key and count only (y and exp(y - m) are formed again
+  // from the key where an entry other than the thread's own is read), so that
+  // an fp16 row's distinct values fit (about 14000-16000 on N(0, 1) rows of
+  // 151936): at most 18 per thread.
+  static constexpr bool kLean = true;
+  static constexpr int kLeanCap = 18 * NT;
 };
 struct CompactWindow {
   static constexpr int NT = 512;
@@ -933,6 +939,8 @@ struct CompactWindow {
   static constexpr int kWords = 0x4400;     // magnitudes below bf16 512.0
   static constexpr bool kWindow = true;
   static constexpr bool kPad = false;       // strided reads of 34 words: 2-way bank conflicts
+  static constexpr bool kLean = false;      // 12-byte entries: key and count, y, exp(y - m)
+  static constexpr int kLeanCap = 0;
 };
 
 template <class G>
@@ -940,15 +948,18 @@ struct CompactShared {
   static constexpr int kWPT = G::kWords / G::NT;          // logical words per thread
   // the table's physical words, then one word counting the values outside it
   static constexpr int kPadWords = G::kWords + (G::kPad ? G::kWords / 32 : 0) + 1;
-  static constexpr int kEntCap = kPadWords / 3;          // 12-byte entries over the same bytes
+  // entries over the same bytes: 12 bytes each, or 4 (lean)
+  static constexpr int kEntCap = G::kLean ? G::kLeanCap : kPadWords / 3;
+  static constexpr int kYE = G::kLean ? 1 : kEntCap;  // (unused in the lean layout)
   static constexpr int NW = G::NT / 64;
   static_assert(kWPT * G::NT == G::kWords, "table words split evenly over the threads");
+  static_assert(!G::kLean || kEntCap <= kPadWords, "lean entries over the table's bytes");
   union {
     uint32_t hist[kPadWords];  // logical word L at L (+ L / 32 with padding)
     struct {
       uint32_t kc[kEntCap];
-      float y[kEntCap];
-      float e[kEntCap];
+      float y[kYE];
+      float e[kYE];
     } ent;
   } u;
   // one slot of NW entries per reduction of a row (each written once)
@@ -1269,23 +1280,32 @@ __global__ __launch_bounds__(G::NT, 2048 / G::NT) void filter_compact_kernel(Fil
       const uint32_t kcj = sh.u.ent.kc[j];
       const float y = yk(kcj & 0xffffu);
       const float e = expf(y - m);
-      sh.u.ent.y[j] = y;
-      sh.u.ent.e[j] = e;
+      if constexpr (!G::kLean) {
+        sh.u.ent.y[j] = y;
+        sh.u.ent.e[j] = e;
+      }
       rn[i] = kcj >> 16;
       re[i] = e;
     }
   }
   __syncthreads();
   const uint32_t* kc = sh.u.ent.kc;
-  const float* ey = sh.u.ent.y;
-  const float* ee = sh.u.ent.e;
+  // entry j's y and exp(y - m): from LDS, or formed again from its key (lean)
+  auto yat = [&](uint32_t j) -> float {
+    if constexpr (G::kLean) return yk(kc[j] & 0xffffu);
+    else return sh.u.ent.y[j];
+  };
+  auto eat = [&](uint32_t j) -> float {
+    if constexpr (G::kLean) return expf(yat(j) - m);
+    else return sh.u.ent.e[j];
+  };
   auto cnt = [&](uint32_t j) { return kc[j] >> 16; };
   // first entry in [lo, hi] whose y >= v (hi + 1 if none); last entry whose y <= v (lo - 1 if none)
   auto first_ge = [&](uint32_t lo, uint32_t hi, float v) {
     uint32_t a = lo, c = hi + 1u;
     while (a < c) {
       const uint32_t mid = (a + c) >> 1;
-      if (ey[mid] >= v) c = mid; else a = mid + 1u;
+      if (yat(mid) >= v) c = mid; else a = mid + 1u;
     }
     return a;
   };
@@ -1293,7 +1313,7 @@ __global__ __launch_bounds__(G::NT, 2048 / G::NT) void filter_compact_kernel(Fil
     uint32_t a = lo, c = hi + 1u;
     while (a < c) {
       const uint32_t mid = (a + c) >> 1;
-      if (ey[mid] <= v) a = mid + 1u; else c = mid;
+      if (yat(mid) <= v) a = mid + 1u; else c = mid;
     }
     return a - 1u;
   };
@@ -1323,8 +1343,8 @@ __global__ __launch_bounds__(G::NT, 2048 / G::NT) void filter_compact_kernel(Fil
     }
     __syncthreads();
     const uint32_t jk = sh.sel[0];
-    y_thr = ey[jk];
-    thr = (jk == 0u || ey[jk - 1u] < y_thr) ? jk : first_ge(0u, jk, y_thr);
+    y_thr = yat(jk);
+    thr = (jk == 0u || yat(jk - 1u) < y_thr) ? jk : first_ge(0u, jk, y_thr);
   }
   // entry i of the share is inside the kept-k values
   auto in_k = [&](int i) { return rn[i] != 0u && j0 + (uint32_t)i >= thr; };
@@ -1343,7 +1363,7 @@ __global__ __launch_bounds__(G::NT, 2048 / G::NT) void filter_compact_kernel(Fil
   if (P.has_p) {
     const float inv = 1.0f / Z;
     auto pmass = [&](uint32_t j) -> double {
-      return DEC16 ? (double)round_trip<E>(ee[j] / Z) : (double)(ee[j] * inv);
+      return DEC16 ? (double)round_trip<E>(eat(j) / Z) : (double)(eat(j) * inv);
     };
     // the share's probabilities (in place of the exponentials, which the
     // group phase reads from LDS)
@@ -1614,9 +1634,9 @@ __global__ __launch_bounds__(G::NT, 2048 / G::NT) void filter_compact_kernel(Fil
     g_hi = last_le(thr, N - 1u, y_thr);
   } else {
     const uint32_t ck = !P.has_p ? thr : have_cut ? cut_ent : N - 1u;
-    v_cut = ey[ck];  // (y_thr when there is no top-p)
-    g_lo = (ck == thr || ey[ck - 1u] < v_cut) ? ck : first_ge(thr, ck, v_cut);
-    g_hi = (ck == N - 1u || ey[ck + 1u] > v_cut) ? ck : last_le(ck, N - 1u, v_cut);
+    v_cut = yat(ck);  // (y_thr when there is no top-p)
+    g_lo = (ck == thr || yat(ck - 1u) < v_cut) ? ck : first_ge(thr, ck, v_cut);
+    g_hi = (ck == N - 1u || yat(ck + 1u) > v_cut) ? ck : last_le(ck, N - 1u, v_cut);
   }
   double ksum_above = 0.0;  // kept mass above the group
   uint32_t cnts[3] = {0u, 0u, 0u};  // elements above the group, in it, in it before the cut entry
@@ -1627,7 +1647,7 @@ __global__ __launch_bounds__(G::NT, 2048 / G::NT) void filter_compact_kernel(Fil
     if (n == 0u) continue;
     if (j > g_hi) {
       cnts[0] += n;
-      ksum_above += (double)n * (double)ee[j];
+      ksum_above += (double)n * (double)eat(j);
     } else if (j >= g_lo) {
       cnts[1] += n;
       if (have_cut && j < cut_ent) cnts[2] += n;
@@ -1661,7 +1681,7 @@ __global__ __launch_bounds__(G::NT, 2048 / G::NT) void filter_compact_kernel(Fil
   uint32_t rcut = 0;  // group elements (in index order) before the cut
   if (P.has_p) rcut = have_cut ? cnts[2] + cut_pos - 1u : n_group - 1u;
   const uint32_t n_kept = cnts[0] + (n_group - rcut);
-  const double ksum = sums[0] + (double)(n_group - rcut) * (double)ee[g_lo];
+  const double ksum = sums[0] + (double)(n_group - rcut) * (double)eat(g_lo);
   const float logsum = logf((float)ksum);
   const uint32_t gk_lo = kc[g_lo] & 0xffffu, gk_hi = kc[g_hi] & 0xffffu;
 

@@ -1,5 +1,6 @@
-"""fp32 rows, and fp16 rows decided in fp32, filtered with top-p alone or k > 1024 (the
-two-pass kernel) against the oracle (GPU).
+"""fp32 rows (the two-pass kernel), and fp16 rows decided in fp32 (the compact kernel
+over the full 65536-key table, entries holding key and count only), filtered with top-p
+alone or k > 1024, against the oracle (GPU).
 
 The oracle is the fp32 rule of ``top_k_top_p(..., exact_normaliser=True)``
 (reference nemo_rl/algorithms/logits_sampling_utils.py:111-212 on the fp32
@@ -7,9 +8,9 @@ tensor that get_next_token_logprobs_from_logits filters, model_utils.py:1660-166
 Keep sets are compared bit-exactly, decoded from the forward's row records;
 logprobs within 1e-5 abs (-inf exactly where the target is dropped); gradients
 within 1e-3 abs.  Row records tell which kernel finished a row: the two-pass
-kernel writes no kept list (flags bit 2), the radix kernel it hands rows over
-to does (flags 0), so the tests also check that ordinary rows stay on the
-two-pass kernel and that rows outside its table reach the radix kernel.
+and compact kernels write no kept list (flags bit 2), the kernels they hand rows
+over to do (flags 0), so the tests also check that ordinary rows stay on the
+first kernel and that fp32 rows outside its table reach the radix kernel.
 """
 
 import pytest

@@ -16,7 +16,8 @@ asserted unused here), keep sets bit-exact.
       moves by one fp32 ulp, and the rows with ties at the cut, are counted and
       printed;
   the same shape's top-p 0.9 decided in bf16: keep sets of the rows the exact
-      sequential sum decided and of 1024 sampled rows;
+      sequential sum decided and of 1024 sampled rows; and with fp16 logits, decided in
+      fp32 and in fp16;
   64 packed sequences, V = 256000: logprobs and the logits gradient of the
       GRPO + KL loss, every row.
 """
@@ -230,6 +231,55 @@ def test_bf16_decided_topp_rows_keep_sets_exact():
         assert bad.numel() == 0, f"keep sets differ in rows {rr[bad].tolist()}"
         n_walked_checked += int(torch.isin(rr, walked).sum())
     assert n_walked_checked == min(walked.numel(), 512)
+
+
+@pytest.mark.parametrize("decision", ["fp32", "fp16"])
+def test_fp16_topp_rows_keep_sets_exact(decision, monkeypatch):
+    """fp16 logits [4, 4096, 151936], T = 0.7, top-p 0.9, decided in fp32 (the
+    get_next_token upcast) or in fp16 (the reference on the 16-bit tensor): the compact
+    kernel over the full 65536-key table (about 14000 distinct values per row).  Keep sets
+    of 768 sampled rows and of up to 256 rows whose cut the exact sequential sum decided
+    (flags bit 3), decoded from the row records, bit-exact against the oracle with an
+    exactly rounded normaliser and the exponential evaluated on the GPU, as the
+    reference's softmax evaluates it (CPU torch's exp differs from it by one ulp on about
+    6% of these rows' values, which moves the cut of about one row in a thousand; those
+    rows are counted and printed); no row may leave the compact kernel."""
+    import oracle.sampling as osp
+
+    say("fp16 top-p rows of [4, 4096, 151936], decided in", decision)
+    d = workloads.general_filter_bf16(top_k=None, top_p=0.9, device=DEV, dtype=torch.float16)
+    x, ids = d["logits"], d["input_ids"]
+    T, p = d["temperature"], d["top_p"]
+    B, S, V = x.shape
+    R = B * (S - 1)
+    dec = torch.float32 if decision == "fp32" else None
+    info, _, _ = _C.filtered_fwd(x, ids[:, 1:], T, 0, p, None, dec)
+    rec = info.view(torch.int32).view(-1, 6)[:R]
+    flags = rec[:, 5].cpu()
+    assert bool(((flags & 4) != 0).all()), "rows left the compact kernel"
+    walked = ((flags & 8) != 0).nonzero().flatten()
+    sample = torch.randperm(R, generator=torch.Generator().manual_seed(5))[:768]
+    rows = torch.unique(torch.cat([walked[:256], sample]))
+    say("rows decided by the exact sum:", walked.numel(), "of", R, "; rows checked:", rows.numel())
+    if decision == "fp16":
+        assert walked.numel() > 0, "no row of the workload exercised the exact sum"
+    cpu_exp = torch.exp
+    n_cpu_exp_differs = 0
+    for a in range(0, rows.numel(), 256):
+        rr = rows[a : a + 256]
+        rd = rr.to(DEV)
+        y16 = x[rd // (S - 1), rd % (S - 1)].div_(T).cpu()  # a copy, divided in place
+        yo = y16.float() if decision == "fp32" else y16
+        keep = keep_from_row_info(y16.float(), rec[rd])
+        _, keep_c = top_k_top_p(yo, None, p, exact_normaliser=True)
+        with monkeypatch.context() as m:
+            m.setattr(osp.torch, "exp", lambda t: cpu_exp(t.to(DEV)).cpu())
+            _, keep_o = top_k_top_p(yo, None, p, exact_normaliser=True)
+        bad = (keep != keep_o).any(-1).nonzero().flatten()
+        assert bad.numel() == 0, f"keep sets differ in rows {rr[bad].tolist()}"
+        n_cpu_exp_differs += int((keep_c != keep_o).any(-1).sum())
+    say("rows whose cut CPU torch's exp moves:", n_cpu_exp_differs)
+    assert n_cpu_exp_differs <= rows.numel() // 100
 
 
 def test_packed_grpo_kl_every_row(single_rank_group):
