@@ -454,23 +454,31 @@ void lce_tile_kernel(LceParams P) {
     // a bf16 output over an fp32 running sum: the sum is completed in C first,
     // then each thread rounds the elements it wrote
     const bool via_c = to_bf16 && P.accumulate && P.C != nullptr;
+    // every accumulator inside the output, one loop per kind of store: a
+    // single loop choosing its store per element grew past what the compiler
+    // unrolls and put the 256 accumulators on the stack (1088 bytes per lane)
+    auto each = [&](auto&& put) {
 #pragma unroll
-    for (int i = 0; i < kTM; ++i)
+      for (int i = 0; i < kTM; ++i)
 #pragma unroll
-      for (int j = 0; j < kTN; ++j)
+        for (int j = 0; j < kTN; ++j)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int64_t row = m0 + wm * kWM + i * 32 + (v >> 2) * 8 + half_g * 4 + (v & 3);
-          const int64_t col = n0 + wn * kWN + j * 32 + col_g;
-          if (row >= row_end || col >= P.V) continue;
-          if (to_bf16 && !via_c) {
-            const float o = acc[i][j][v];
-            P.Cb[row * P.ldcb + col] = P.cb_f16 ? bits_of<F16>(o) : bits_of<BF16>(o);
-          } else {
-            float* c = P.C + (ks * P.nrows + row) * P.ldc + col;
-            *c = P.accumulate ? *c + acc[i][j][v] : acc[i][j][v];
+          for (int v = 0; v < 16; ++v) {
+            const int64_t row = m0 + wm * kWM + i * 32 + (v >> 2) * 8 + half_g * 4 + (v & 3);
+            const int64_t col = n0 + wn * kWN + j * 32 + col_g;
+            if (row < row_end && col < P.V) put(row, col, acc[i][j][v]);
           }
-        }
+    };
+    if (to_bf16 && !via_c) {
+      if (P.cb_f16)
+        each([&](int64_t row, int64_t col, float o) { P.Cb[row * P.ldcb + col] = bits_of<F16>(o); });
+      else
+        each([&](int64_t row, int64_t col, float o) { P.Cb[row * P.ldcb + col] = bits_of<BF16>(o); });
+    } else if (P.accumulate) {
+      each([&](int64_t row, int64_t col, float o) { P.C[(ks * P.nrows + row) * P.ldc + col] += o; });
+    } else {
+      each([&](int64_t row, int64_t col, float o) { P.C[(ks * P.nrows + row) * P.ldc + col] = o; });
+    }
     if (via_c) {
 #pragma unroll
       for (int i = 0; i < kTM; ++i)
