@@ -632,7 +632,9 @@ void lce_tile_kernel(LceParams P) {
 
 // dst[c][r] = bf16(src[r][c]) for r < R, c < C, and dst[c][r] = 0 for
 // R <= r < Rp (src of dtype ES, bf16 or fp16; dst rows of stride ldd >= Rp),
-// R = min(R, *count) when count is given.  64 x 64 tiles through LDS.
+// R = min(R, *count) when count is given.  64 x 64 tiles through LDS, moved
+// as 16-byte pieces (eight elements of a row in, eight of a column out) where
+// the pointers, strides and tile edges allow, element by element elsewhere.
 template <class ES>
 __global__ __launch_bounds__(256) void transpose_bf16_kernel(const uint16_t* __restrict__ src,
                                                              int64_t R, int64_t C, int64_t lds,
@@ -640,23 +642,60 @@ __global__ __launch_bounds__(256) void transpose_bf16_kernel(const uint16_t* __r
                                                              int64_t ldd, int64_t Rp,
                                                              int64_t n_ct,
                                                              const int64_t* __restrict__ count) {
-  __shared__ uint16_t tile[64][66];
+  // row pitch 66 elements (33 words): the eight rows 8 apart that a wave's
+  // column reads touch start in different LDS banks
+  constexpr int kP = 66;
+  __shared__ uint16_t tile[64 * kP];
   if (count != nullptr && *count < R) R = *count;
   const int64_t tr = blockIdx.x / n_ct, tc = blockIdx.x - tr * n_ct;
   const int64_t r0 = tr * 64, c0 = tc * 64;
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-#pragma unroll 4
-  for (int k = 0; k < 16; ++k) {
-    const int64_t r = r0 + ty + 4 * k, c = c0 + tx;
-    uint16_t v = (r < R && c < C) ? src[r * lds + c] : (uint16_t)0;
-    if constexpr (std::is_same<ES, F16>::value) v = bits_of<BF16>(value_of<F16>(v));
-    tile[ty + 4 * k][tx] = v;
+  const bool vin = ((lds & 7) | (reinterpret_cast<uintptr_t>(src) & 15)) == 0;
+  const bool vout = ((ldd & 7) | (reinterpret_cast<uintptr_t>(dst) & 15)) == 0;
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int idx = (int)threadIdx.x + 256 * k, lr = idx >> 3, cg = (idx & 7) * 8;
+    const int64_t r = r0 + lr, c = c0 + cg;
+    uint32_t w[4];
+    if (vin && r < R && c + 8 <= C) {
+      const vu4 q = *reinterpret_cast<const vu4*>(src + r * lds + c);
+      w[0] = q.x; w[1] = q.y; w[2] = q.z; w[3] = q.w;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t lo = (r < R && c + 2 * j < C) ? src[r * lds + c + 2 * j] : 0u;
+        const uint32_t hi = (r < R && c + 2 * j + 1 < C) ? src[r * lds + c + 2 * j + 1] : 0u;
+        w[j] = lo | (hi << 16);
+      }
+    }
+    if constexpr (std::is_same<ES, F16>::value) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        w[j] = (uint32_t)bits_of<BF16>(value_of<F16>((uint16_t)(w[j] & 0xffffu))) |
+               ((uint32_t)bits_of<BF16>(value_of<F16>((uint16_t)(w[j] >> 16))) << 16);
+    }
+    // (lr * 66 + cg) elements = a whole number of 4-byte words
+    uint32_t* t32 = reinterpret_cast<uint32_t*>(tile + lr * kP + cg);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) t32[j] = w[j];
   }
   __syncthreads();
-#pragma unroll 4
-  for (int k = 0; k < 16; ++k) {
-    const int64_t c = c0 + ty + 4 * k, r = r0 + tx;
-    if (c < C && r < Rp) dst[c * ldd + r] = tile[tx][ty + 4 * k];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int idx = (int)threadIdx.x + 256 * k, lc = idx >> 3, rg = (idx & 7) * 8;
+    const int64_t c = c0 + lc, r = r0 + rg;
+    if (c >= C) continue;
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      w[j] = (uint32_t)tile[(rg + 2 * j) * kP + lc] | ((uint32_t)tile[(rg + 2 * j + 1) * kP + lc] << 16);
+    uint16_t* d = dst + c * ldd + r;
+    if (vout && r + 8 <= Rp) {
+      *reinterpret_cast<vu4*>(d) = vu4{w[0], w[1], w[2], w[3]};
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (r + i < Rp) d[i] = (uint16_t)(w[i >> 1] >> (16 * (i & 1)));
+    }
   }
 }
 

@@ -273,6 +273,34 @@ def test_gradient_blocks_with_device_count(active):
     assert not dh.cpu()[(g == 0).t()].any()
 
 
+@pytest.mark.parametrize("R,C,lds,off,Rp,ldd,dtype", [
+    (130, 77, 77, 0, 136, 136, torch.bfloat16),     # columns not a multiple of 8: element loads
+    (200, 128, 136, 3, 203, 208, torch.bfloat16),   # source 6 bytes past alignment, Rp not a multiple of 8
+    (64, 256, 256, 0, 64, 64, torch.float16),       # whole tiles, fp16 rounded to bf16
+    (1000, 520, 520, 0, 1024, 1030, torch.bfloat16),  # destination stride not a multiple of 8
+    (0, 64, 64, 0, 64, 64, torch.bfloat16),         # no rows: zeros
+])
+def test_transpose_shapes_and_alignments(R, C, lds, off, Rp, ldd, dtype):
+    """mirl_transpose_bf16 gives dst[c, r] = bf16(src[r, c]) for r < R and 0 for
+    R <= r < Rp, with the columns past Rp of each destination row left alone, for
+    16-byte and element-wise pieces alike."""
+    from rl_amd import _C
+
+    say("transpose", R, C, lds, off, Rp, ldd, dtype)
+    gen = torch.Generator().manual_seed(R * 7 + C)
+    rows = max(R, 1)
+    flat = torch.randn(rows * lds + off, generator=gen).to(dtype)
+    src = flat[off:].view(rows, lds)[:, :C]
+    dst_full = torch.full((C, ldd), 9.0, dtype=torch.bfloat16)
+    dst = dst_full.to(DEV)
+    src_d = flat.to(DEV)[off:].view(rows, lds)[:, :C]
+    _C.transpose_bf16(src_d, R, dst[:, :Rp])
+    ref = dst_full.clone()
+    ref[:, :Rp] = 0
+    ref[:, :R] = src[:R].t().to(torch.bfloat16)
+    assert torch.equal(dst.cpu(), ref)
+
+
 def test_gemm_primitives_with_device_counts():
     """The GEMM, split sum and transpose with a device count equal the same calls on the
     host-trimmed operands, bit for bit."""
