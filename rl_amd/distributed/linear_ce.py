@@ -170,7 +170,7 @@ class ChunkedDistributedHiddenStatesToLogprobs(torch.autograd.Function):
         if need_w:
             hT = torch.empty((H, _padded_width(T)), dtype=torch.bfloat16, device=dev)
             _C.transpose_bf16(h_a, T, hT, count=count)
-        wT = _weight_transposed(weight, Vp) if need_h else None
+        wT, wT_ready = _weight_transposed(weight, Vp) if need_h else (None, None)
         # dH is written row by row at each permuted row's own position
         dH = torch.empty((T, H), dtype=hidden.dtype, device=dev) if need_h else None
         hk_a, wk = _kernel_operand(h_a), _kernel_operand(weight)
@@ -189,6 +189,9 @@ class ChunkedDistributedHiddenStatesToLogprobs(torch.autograd.Function):
                 # the count are written as zeros
                 splits = _dh_splits(n, H, Vp, count_known=False)
                 part = torch.empty((splits, n, H), dtype=torch.float32, device=dev)
+                if wT_ready is not None:
+                    torch.cuda.current_stream(dev).wait_event(wT_ready)
+                    wT_ready = None
                 _C.gemm_bf16_abt(Gc, wT, Vp, part, k_splits=splits, count=count, count_off=r0,
                                  count_axis=_C.COUNT_ROWS)
                 _C.sum_splits_bf16(part, dH, count=count, count_off=r0, out_rows=perm[r0 : r0 + n])
@@ -202,6 +205,8 @@ class ChunkedDistributedHiddenStatesToLogprobs(torch.autograd.Function):
                 else:
                     _C.gemm_bf16_abt(Gt, hb, nk, dW32, accumulate=r0 > 0, count=count, count_off=r0,
                                      count_axis=_C.COUNT_K, out_bf16=dW, final_at=r0 + n)
+        if wT_ready is not None:  # no block ran: W^T still waits to be released after its writer
+            torch.cuda.current_stream(dev).wait_event(wT_ready)
         grad_h = dH.view(S, B, H) if need_h else None
         grad_w = (dW if dW.dtype == weight.dtype else dW.to(weight.dtype)) if need_w else None
         return grad_h, None, grad_w, None, None, None, None, None
@@ -451,17 +456,36 @@ def _dh_splits(n: int, H: int, K: int, count_known: bool = True) -> int:
     return best
 
 
-def _weight_transposed(weight: torch.Tensor, Vp: int) -> torch.Tensor:
+_transpose_streams: dict = {}
+
+
+def _weight_transposed(weight: torch.Tensor, Vp: int):
     """W^T [H, Vp] bf16 (columns past V zero; an fp16 weight rounded), formed from the weight's current contents
-    in every backward (one read and one write of W, about 0.5 ms at [151936, 4096]).
+    in every backward (one read and one write of W, about 0.5 ms at [151936, 4096]), and the event
+    that marks it written.
+
+    The transpose runs on a side stream (default priority) behind everything already
+    enqueued on the current stream, so it overlaps the gradient kernel, which is bound by
+    the MFMA units; the caller waits for the event on the current stream before the first
+    product that reads W^T.  The buffer is allocated on the current stream, which frees
+    it only after that product, itself ordered after the transpose.
 
     Nothing is kept across calls: a weight can change without its version counter
     moving (``p.data.copy_``, collectives writing into parameter storage), so a copy
     reused by key could silently give dH from an old weight."""
     V, H = weight.shape
-    wT = torch.empty((H, Vp), dtype=torch.bfloat16, device=weight.device)
-    _C.transpose_bf16(weight, V, wT)
-    return wT
+    dev = weight.device
+    wT = torch.empty((H, Vp), dtype=torch.bfloat16, device=dev)
+    side = _transpose_streams.get(dev)
+    if side is None:
+        side = torch.cuda.Stream(dev)
+        _transpose_streams[dev] = side
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        _C.transpose_bf16(weight, V, wT)
+        ready = torch.cuda.Event()
+        ready.record(side)
+    return wT, ready
 
 
 def from_parallel_hidden_states_to_logprobs(
