@@ -701,31 +701,59 @@ __global__ __launch_bounds__(256) void transpose_bf16_kernel(const uint16_t* __r
 
 // dst[c][r] = src[r][c] for r < R, c < C, and dst[c][r] = 0 for R <= r < Rp
 // (fp32; dst rows of stride ldd >= Rp), R = min(R, *count - count_off) when
-// count is given.  64 x 64 tiles through LDS.
+// count is given.  64 x 64 tiles through LDS, moved as 16-byte pieces (four
+// elements of a row in, four of a column out) where the pointers, strides and
+// tile edges allow, element by element elsewhere.
 __global__ __launch_bounds__(256) void transpose_f32_kernel(const float* __restrict__ src, int64_t R,
                                                             int64_t C, int64_t lds,
                                                             float* __restrict__ dst, int64_t ldd,
                                                             int64_t Rp, int64_t n_ct,
                                                             const int64_t* __restrict__ count,
                                                             int64_t count_off) {
-  __shared__ float tile[64][65];
+  // row pitch 65 words: a wave's row pieces and column reads each fall in
+  // distinct LDS banks
+  constexpr int kP = 65;
+  __shared__ float tile[64 * kP];
   if (count != nullptr) {
     const int64_t c = *count - count_off;
     if (c < R) R = c < 0 ? 0 : c;
   }
   const int64_t tr = blockIdx.x / n_ct, tc = blockIdx.x - tr * n_ct;
   const int64_t r0 = tr * 64, c0 = tc * 64;
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-#pragma unroll 4
-  for (int k = 0; k < 16; ++k) {
-    const int64_t r = r0 + ty + 4 * k, c = c0 + tx;
-    tile[ty + 4 * k][tx] = (r < R && c < C) ? src[r * lds + c] : 0.f;
+  const bool vin = ((lds & 3) | (reinterpret_cast<uintptr_t>(src) & 15)) == 0;
+  const bool vout = ((ldd & 3) | (reinterpret_cast<uintptr_t>(dst) & 15)) == 0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int idx = (int)threadIdx.x + 256 * k, lr = idx >> 4, cg = (idx & 15) * 4;
+    const int64_t r = r0 + lr, c = c0 + cg;
+    float w[4];
+    if (vin && r < R && c + 4 <= C) {
+      const float4 q = *reinterpret_cast<const float4*>(src + r * lds + c);
+      w[0] = q.x; w[1] = q.y; w[2] = q.z; w[3] = q.w;
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) w[j] = (r < R && c + j < C) ? src[r * lds + c + j] : 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) tile[lr * kP + cg + j] = w[j];
   }
   __syncthreads();
-#pragma unroll 4
-  for (int k = 0; k < 16; ++k) {
-    const int64_t c = c0 + ty + 4 * k, r = r0 + tx;
-    if (c < C && r < Rp) dst[c * ldd + r] = tile[tx][ty + 4 * k];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int idx = (int)threadIdx.x + 256 * k, lc = idx >> 4, rg = (idx & 15) * 4;
+    const int64_t c = c0 + lc, r = r0 + rg;
+    if (c >= C) continue;
+    float w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = tile[(rg + i) * kP + lc];
+    float* d = dst + c * ldd + r;
+    if (vout && r + 4 <= Rp) {
+      *reinterpret_cast<float4*>(d) = make_float4(w[0], w[1], w[2], w[3]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (r + i < Rp) d[i] = w[i];
+    }
   }
 }
 

@@ -301,6 +301,36 @@ def test_transpose_shapes_and_alignments(R, C, lds, off, Rp, ldd, dtype):
     assert torch.equal(dst.cpu(), ref)
 
 
+@pytest.mark.parametrize("R,C,lds,off,Rp,ldd", [
+    (130, 77, 77, 0, 136, 136),     # columns not a multiple of 4: element loads
+    (200, 128, 132, 1, 203, 208),   # source 4 bytes past alignment, Rp not a multiple of 4
+    (64, 256, 256, 0, 64, 64),      # whole tiles
+    (1000, 520, 520, 0, 1024, 1030),  # destination stride not a multiple of 4
+    (0, 64, 64, 0, 64, 64),         # no rows: zeros
+])
+def test_transpose_f32_shapes_and_alignments(R, C, lds, off, Rp, ldd):
+    """mirl_transpose_f32 gives dst[c, r] = src[r, c] for r < min(R, count - count_off) and
+    0 up to Rp, with the columns past Rp of each destination row left alone."""
+    from rl_amd import _C
+
+    say("transpose f32", R, C, lds, off, Rp, ldd)
+    gen = torch.Generator().manual_seed(R * 5 + C)
+    rows = max(R, 1)
+    flat = torch.randn(rows * lds + off, generator=gen)
+    src = flat[off:].view(rows, lds)[:, :C]
+    src_d = flat.to(DEV)[off:].view(rows, lds)[:, :C]
+    for cnt in (None, R // 2 + 10):
+        dst_full = torch.full((C, ldd), 9.0)
+        dst = dst_full.to(DEV)
+        count = None if cnt is None else torch.tensor([cnt], dtype=torch.int64, device=DEV)
+        _C.transpose_f32(src_d, R, dst[:, :Rp], count=count, count_off=10 if cnt is not None else 0)
+        n = R if cnt is None else min(R, cnt - 10)
+        ref = dst_full.clone()
+        ref[:, :Rp] = 0
+        ref[:, :n] = src[:n].t()
+        assert torch.equal(dst.cpu(), ref), cnt
+
+
 def test_gemm_primitives_with_device_counts():
     """The GEMM, split sum and transpose with a device count equal the same calls on the
     host-trimmed operands, bit for bit."""
